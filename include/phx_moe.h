@@ -1,0 +1,175 @@
+/*
+ * phx_moe.h -- C ABI of libphxmoe.so, the MI355X (gfx950) mixture-of-experts FFN layer of
+ * phoenix-lai's Gemma 4 26B-A4B path.
+ *
+ * The library replaces, for this path only, the Vulkan device layer that GemmaGpu's three MoE call
+ * sites record into (src/Gpu.cs:566 CreateKernel, src/Gpu.cs:848-867 Record):
+ *   GemmaGpu.RecordMoe      (src/GemmaGpu.cs:656-669)  -> phx_moe_ffn, T = 1, shared given
+ *   GemmaGpu.RecordFfnMoe   (src/GemmaGpu.cs:683-704)  -> phx_moe_ffn, T = 1, shared FFN computed
+ *   GemmaGpu.RecordMoeRows  (src/GemmaGpu.cs:850-882)  -> phx_moe_ffn, T rows
+ * and computes what GemmaCpu.MoeFfn (src/GemmaCpu.cs:376-422) defines, with the same rounding:
+ * router ids and per-expert lists are bit-exact, outputs match the CPU reference to the last bit
+ * except where the reference's libm (exp) rounds differently.
+ *
+ * Plain pointers and sizes only.  One context is used by one thread at a time (the C# host keeps
+ * GpuGate.Lock, src/Vulkan.cs:210-215).  Host buffers are borrowed for the duration of a call.
+ */
+#ifndef PHX_MOE_H
+#define PHX_MOE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Return codes.  The C# side maps PHX_ERR_DEVICE_LOST to GpuDeviceLostException
+ * (src/Vulkan.cs:194-208), PHX_ERR_ARG to ArgumentException (src/Gpu.cs:851-852) and
+ * PHX_ERR_UNSUPPORTED to NotSupportedException (src/GemmaGpu.cs:189-190, src/GemmaCpu.cs:72-73). */
+#define PHX_OK 0
+#define PHX_ERR_ARG (-1)
+#define PHX_ERR_OOM (-2)
+#define PHX_ERR_UNSUPPORTED (-3)
+#define PHX_ERR_DEVICE_LOST (-4)
+#define PHX_ERR_HIP (-5)
+
+/* GgmlType codes of the supported tensors (src/Gguf.cs:18-24). */
+#define PHX_F32 0
+#define PHX_Q4_0 2
+#define PHX_Q8_0 8
+#define PHX_Q4_K 12
+#define PHX_Q6_K 14
+
+/* Layout limits of the reference (src/KernelsMoe.cs:43, checked at src/GemmaCpu.cs:72-73). */
+#define PHX_MAX_EXPERTS 256
+#define PHX_MAX_USED 16
+
+/* Router weight rule.  PHX_WEIGHTS_SOFTMAX: renormalised softmax over the k selected logits
+ * (src/KernelsMoe.cs:80-98; llama.cpp build_moe_ffn), evaluated with GemmaCpu's double exp/sum.
+ * PHX_WEIGHTS_CPUREF: GemmaCpu.cs:406-407 as written, whose in-place update of sel[0] turns every
+ * later term into exp(l_j - 1). */
+#define PHX_WEIGHTS_SOFTMAX 0
+#define PHX_WEIGHTS_CPUREF 1
+
+/* phx_moe_ffn flags */
+#define PHX_FLAG_DEVICE_PTRS 1u /* x, shared, out are device pointers (no PCIe copies) */
+#define PHX_FLAG_ASYNC 2u       /* return after enqueueing; phx_moe_sync waits */
+#define PHX_FLAG_RESIDUAL 4u    /* also x += rmsnorm(out) * post_ffw_norm (src/GemmaCpu.cs:355-356); x is updated in place */
+
+typedef struct phx_moe_ctx phx_moe_ctx;
+
+/* One MoE layer as the GGUF file holds it (tensor names from src/GemmaCpu.cs:180-188; GGUF dims
+ * list ne[0] first, src/Gguf.cs:77-90):
+ *   gate_inp        ffn_gate_inp.weight     f32  [d, E]          -> E rows of d
+ *   gate_inp_scale  ffn_gate_inp.scale      f32  [d]
+ *   down_scale      ffn_down_exps.scale     f32  [E]
+ *   pre_ffw_norm_2, post_ffw_norm_1, post_ffw_norm_2   f32 [d]
+ *   gate_up_exps    ffn_gate_up_exps.weight quant [d, 2nf, E]   -> per expert 2nf rows (gate, then up)
+ *   down_exps       ffn_down_exps.weight    quant [down_cols, d, E]
+ * down_cols is n_ff for Q4_0/Q8_0 and n_ff rounded up to 256 for K-quants: the rows are
+ * zero-padded, an extension (the reference refuses such rows, src/Gguf.cs:202-203).
+ * Optional dense shared FFN (n_ff_shared > 0; src/GemmaCpu.cs:348-353): ffn_norm [d],
+ * ffn_gate/ffn_up [d, n_ff_shared], ffn_down [n_ff_shared, d], all of shared_type.
+ * post_ffw_norm [d] is the layer's post-FFN norm, needed only with PHX_FLAG_RESIDUAL. */
+typedef struct phx_moe_layer_desc {
+    int32_t d;
+    int32_t n_expert;
+    int32_t n_used;
+    int32_t n_ff;
+    int32_t down_cols;
+    float eps;
+    int32_t gate_up_type;
+    int32_t down_type;
+    int32_t weight_rule;
+    int32_t n_ff_shared;
+    int32_t shared_type;
+    int32_t reserved;
+    const float* gate_inp;
+    const float* gate_inp_scale;
+    const float* down_scale;
+    const float* pre_ffw_norm_2;
+    const float* post_ffw_norm_1;
+    const float* post_ffw_norm_2;
+    const void* gate_up_exps;
+    const void* down_exps;
+    const float* ffn_norm;
+    const void* ffn_gate;
+    const void* ffn_up;
+    const void* ffn_down;
+    const float* post_ffw_norm;
+} phx_moe_layer_desc;
+
+/* Context: device, stream, all device memory.  Replaces GpuDevice.Create (src/Gpu.cs:255). */
+int phx_moe_create(int hip_device, phx_moe_ctx** out);
+void phx_moe_destroy(phx_moe_ctx* ctx);
+const char* phx_moe_last_error(const phx_moe_ctx* ctx);
+
+/* Shape and type validation of a descriptor, without touching the GPU (the checks of
+ * src/GemmaCpu.cs:72-73 and src/GemmaGpu.cs:189-190 generalised to the supported types). */
+int phx_moe_check_desc(const phx_moe_layer_desc* desc);
+
+/* Upload (and repack) one layer's tensors from host memory; replaces GemmaGpu's MoE uploads
+ * (src/GemmaGpu.cs:178-192 UploadF32/UploadW, repack src/GemmaGpu.cs:340-436).  Layers are indexed
+ * from 0; uploading an index again replaces it. */
+int phx_moe_layer_upload(phx_moe_ctx* ctx, int layer, const phx_moe_layer_desc* desc);
+
+/* One MoE FFN block for T token rows (src/GemmaGpu.cs:656-704 for T = 1, :850-882 for T rows):
+ *   out[t] = rmsnorm(shared[t]) * post_ffw_norm_1 + rmsnorm(sum_j w_tj * down_e(gelu(gate_e(n)) * up_e(n))) * post_ffw_norm_2
+ * with n = rmsnorm(x[t]) * pre_ffw_norm_2 and (e, w) the router's top-k.  shared == NULL: the
+ * layer's shared FFN is computed from x when it has one, else the shared branch is zero.
+ * x, shared: [T][d] f32; out: [T][d] f32. */
+int phx_moe_ffn(phx_moe_ctx* ctx, int layer, int T, float* x, const float* shared, float* out, unsigned flags);
+
+/* Routing of the last phx_moe_ffn call (any pointer may be NULL): ids [T][k] best first,
+ * weights [T][k] (with ffn_down_exps.scale folded in, src/GemmaCpu.cs:417), offsets [E+1] and
+ * perm [T*k] (expert e's assignments a = t*k + j in ascending order: perm[offsets[e]..offsets[e+1]),
+ * the lists of src/KernelsMoe.cs:281-330), logits [T][E]. */
+int phx_moe_get_routing(phx_moe_ctx* ctx, int32_t* ids, float* weights, int32_t* offsets, int32_t* perm, float* logits);
+
+/* Expert intermediates of the last call (debug; NULL skips): g, u [T*k][n_ff] gate/up products
+ * and yd [T*k][d] the down products, in assignment order a = t*k + j. */
+int phx_moe_get_intermediates(phx_moe_ctx* ctx, float* g, float* u, float* yd);
+
+/* Consecutive layers as one HIP graph (batched decode): each layer does phx_moe_ffn with
+ * PHX_FLAG_RESIDUAL on a device-resident x of T rows.  capture once, then run many times. */
+int phx_moe_stack_capture(phx_moe_ctx* ctx, int first_layer, int n_layers, int T);
+int phx_moe_stack_run(phx_moe_ctx* ctx, float* x_inout, int T, unsigned flags);
+
+int phx_moe_sync(phx_moe_ctx* ctx);
+
+/* Device memory for callers without their own allocator (test harness, benchmark). */
+int phx_moe_dev_alloc(phx_moe_ctx* ctx, uint64_t bytes, void** ptr);
+int phx_moe_dev_free(phx_moe_ctx* ctx, void* ptr);
+int phx_moe_memcpy_h2d(phx_moe_ctx* ctx, void* dst, const void* src, uint64_t bytes);
+int phx_moe_memcpy_d2h(phx_moe_ctx* ctx, void* dst, const void* src, uint64_t bytes);
+
+/* Per-kernel timing with HIP events on the library's stream (the Gpu.cs:163-171 profiling
+ * counterpart).  Kinds: */
+#define PHX_K_PROLOGUE 0
+#define PHX_K_ROUTER 1
+#define PHX_K_TOPK 2
+#define PHX_K_DISPATCH 3
+#define PHX_K_GATE_UP 4
+#define PHX_K_REQUANT 5
+#define PHX_K_DOWN 6
+#define PHX_K_COMBINE 7
+#define PHX_K_SHARED 8
+#define PHX_K_COUNT 9
+int phx_moe_profile(phx_moe_ctx* ctx, int enable);
+int phx_moe_profile_read(phx_moe_ctx* ctx, double* total_ms, int64_t* launches);
+
+/* Arithmetic self-test: runs the library's device primitives on n host inputs so a test can check
+ * them bit for bit against IEEE results.  op: 0 f32 division a/b, 1 rms scale 1/(float)sqrt(a+b)
+ * as the reference writes it, 2 double->float of (double)a/(double)b, 3 roundf(a), 4 fp16 bits of a
+ * (round to nearest even), 5 nearest-even int of a (1.5*2^23 trick), 6 GELU(a).  out is float
+ * (int results as their value). */
+int phx_moe_selftest(phx_moe_ctx* ctx, int op, int n, const float* a, const float* b, float* out);
+
+/* Number of row norms, since the context was created, whose double sum of squares could not be
+ * certified to round like the reference's sequential sum and were re-summed sequentially. */
+int phx_moe_fallback_count(phx_moe_ctx* ctx, int* count);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

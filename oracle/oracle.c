@@ -1,0 +1,543 @@
+/*
+ * oracle.c -- CPU restatement of phoenix-lai's MoE FFN reference path (see oracle.h).
+ *
+ * TEST INFRASTRUCTURE ONLY: loaded by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
+ * leg as the checker.  Never linked into or called by the product library.
+ *
+ * Build: gcc -O2 -ffp-contract=off -fno-fast-math -fopenmp (oracle/Makefile).  Every float
+ * expression keeps the reference's evaluation order; comments cite the C# line it restates.
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define QK8_0 32
+#define QK_K 256
+
+static uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+/* ---------------------------------------------------------------- fp16: src/Half.cs */
+
+/* Half.FromFloat (Half.cs:26-54): round to nearest even, subnormals, NaN keeps a quiet bit. */
+uint16_t orc_half_from_float(float value)
+{
+    uint32_t f = f2u(value);
+    uint32_t sign = (f >> 16) & 0x8000u;
+    int e = (int)((f >> 23) & 0xFF);
+    uint32_t m = f & 0x7FFFFFu;
+    if (e == 255) return (uint16_t)(sign | 0x7C00u | (m != 0 ? 0x200u : 0u));
+    int ne = e - 127 + 15;
+    if (ne >= 31) return (uint16_t)(sign | 0x7C00u);
+    if (ne <= 0) {
+        if (ne < -10) return (uint16_t)sign;
+        m |= 0x800000u;
+        int shift = 14 - ne;
+        uint32_t hm = m >> shift;
+        uint32_t rem = m & ((1u << shift) - 1);
+        uint32_t halfway = 1u << (shift - 1);
+        if (rem > halfway || (rem == halfway && (hm & 1) != 0)) hm++;
+        return (uint16_t)(sign | hm);
+    }
+    uint32_t h = sign | ((uint32_t)ne << 10) | (m >> 13);
+    uint32_t r = m & 0x1FFFu;
+    if (r > 0x1000u || (r == 0x1000u && (h & 1) != 0)) h++;
+    return (uint16_t)h;
+}
+
+/* Half.Decode (Half.cs:56-86): exact half -> float. */
+float orc_half_to_float(uint16_t h)
+{
+    uint32_t sign = (uint32_t)(h >> 15) << 31;
+    int exp = (h >> 10) & 0x1F;
+    uint32_t mant = (uint32_t)(h & 0x3FF);
+    uint32_t bits;
+    if (exp == 0) {
+        if (mant == 0) {
+            bits = sign;
+        } else {
+            int e = -1;
+            do { e++; mant <<= 1; } while ((mant & 0x400) == 0);
+            mant &= 0x3FF;
+            bits = sign | (uint32_t)(127 - 15 - e) << 23 | mant << 13;
+        }
+    } else if (exp == 31) {
+        bits = sign | 0x7F800000u | mant << 13;
+    } else {
+        bits = sign | (uint32_t)(exp - 15 + 127) << 23 | mant << 13;
+    }
+    return u2f(bits);
+}
+
+/* Half.Round (Half.cs:21-24) */
+float orc_half_round(float f) { return orc_half_to_float(orc_half_from_float(f)); }
+
+void orc_half_from_float_n(const float* x, uint16_t* h, int64_t n)
+{
+    for (int64_t i = 0; i < n; i++) h[i] = orc_half_from_float(x[i]);
+}
+
+void orc_half_to_float_n(const uint16_t* h, float* x, int64_t n)
+{
+    for (int64_t i = 0; i < n; i++) x[i] = orc_half_to_float(h[i]);
+}
+
+/* ---------------------------------------------------------------- activation quantizers */
+
+/* CpuRef.QuantizeQ8_0 + RoundAway (CpuRef.cs:49-67): per 32, d = amax/127, q = roundf(x * (1/d)). */
+void orc_quantize_q8_0(const float* x, int n, uint16_t* dq, int8_t* qs)
+{
+    int nb = n / QK8_0;
+    for (int b = 0; b < nb; b++) {
+        int o = b * QK8_0;
+        float amax = 0;
+        for (int j = 0; j < QK8_0; j++) { float a = fabsf(x[o + j]); if (a > amax) amax = a; }
+        float d = amax / 127.0f;
+        float id = d != 0 ? 1.0f / d : 0.0f;
+        dq[b] = orc_half_from_float(d);
+        for (int j = 0; j < QK8_0; j++) qs[o + j] = (int8_t)roundf(x[o + j] * id);
+    }
+}
+
+/* CpuRef.NearestInt (CpuRefKQuants.cs:45-51): round half to even through 1.5*2^23. */
+int orc_nearest_int(float f)
+{
+    float val = f + 12582912.0f;
+    int32_t i;
+    memcpy(&i, &val, 4);
+    return (i & 0x007fffff) - 0x00400000;
+}
+
+/* CpuRef.QuantizeQ8_K (CpuRefKQuants.cs:53-86): the signed value of largest |x| (first index on
+ * ties) sets iscale = -127/max; q = min(127, nearest(iscale*x)); d = 1/iscale; bsums per 16. */
+void orc_quantize_q8_k(const float* x, int n, float* kd, int8_t* kq, int16_t* kbs)
+{
+    int nb = n / QK_K;
+    for (int b = 0; b < nb; b++) {
+        int o = b * QK_K;
+        float max = 0, amax = 0;
+        for (int j = 0; j < QK_K; j++) {
+            float ax = fabsf(x[o + j]);
+            if (ax > amax) { amax = ax; max = x[o + j]; }
+        }
+        if (amax == 0) {
+            kd[b] = 0;
+            for (int j = 0; j < QK_K; j++) kq[o + j] = 0;
+            for (int j = 0; j < QK_K / 16; j++) kbs[b * 16 + j] = 0;
+            continue;
+        }
+        float iscale = -127.0f / max;
+        for (int j = 0; j < QK_K; j++) {
+            int v = orc_nearest_int(iscale * x[o + j]);
+            kq[o + j] = (int8_t)(v < 127 ? v : 127);
+        }
+        for (int j = 0; j < QK_K / 16; j++) {
+            int sum = 0;
+            for (int ii = 0; ii < 16; ii++) sum += kq[o + j * 16 + ii];
+            kbs[b * 16 + j] = (int16_t)sum;
+        }
+        kd[b] = 1.0f / iscale;
+    }
+}
+
+/* ---------------------------------------------------------------- block layouts: src/Gguf.cs:29-59 */
+
+int64_t orc_row_bytes(int type, int cols)
+{
+    switch (type) {
+    case ORC_F32: return (int64_t)cols * 4;
+    case ORC_Q4_0: return (int64_t)(cols / 32) * 18;
+    case ORC_Q8_0: return (int64_t)(cols / 32) * 34;
+    case ORC_Q4_K: return (int64_t)(cols / 256) * 144;
+    case ORC_Q6_K: return (int64_t)(cols / 256) * 210;
+    }
+    return -1;
+}
+
+static uint16_t rd16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+
+/* get_scale_min_k4 (CpuRefKQuants.cs:32-43) */
+static void scale_min_k4(int j, const uint8_t* q, int* sc, int* m)
+{
+    if (j < 4) {
+        *sc = q[j] & 63; *m = q[j + 4] & 63;
+    } else {
+        *sc = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
+        *m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+    }
+}
+
+/* UnpackK (CpuRefKQuants.cs:90-147), Q4_K and Q6_K: 256 small integers, scales, mins. */
+static void unpack_k(int t, const uint8_t* blk, int8_t* a, int* scales, int* mins, float* d, float* dmin)
+{
+    if (t == ORC_Q6_K) {
+        const uint8_t* ql = blk; const uint8_t* qh = blk + 128; const int8_t* sc = (const int8_t*)(blk + 192);
+        for (int n = 0; n < QK_K / 128; n++) {
+            for (int l = 0; l < 32; l++) {
+                a[l + 0] = (int8_t)(((ql[l + 0] & 0xF) | (((qh[l] >> 0) & 3) << 4)) - 32);
+                a[l + 32] = (int8_t)(((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32);
+                a[l + 64] = (int8_t)(((ql[l + 0] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32);
+                a[l + 96] = (int8_t)(((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32);
+            }
+            a += 128; ql += 64; qh += 32;
+        }
+        for (int j = 0; j < 16; j++) scales[j] = sc[j];
+        *d = orc_half_to_float(rd16(blk + 208));
+        *dmin = 0;
+        return;
+    }
+    /* Q4_K */
+    *d = orc_half_to_float(rd16(blk));
+    *dmin = orc_half_to_float(rd16(blk + 2));
+    const uint8_t* sc8 = blk + 4;
+    for (int j = 0; j < 8; j++) scale_min_k4(j, sc8, &scales[j], &mins[j]);
+    const uint8_t* q4 = blk + 16;
+    for (int j = 0; j < QK_K / 64; j++) {
+        for (int l = 0; l < 32; l++) a[l] = (int8_t)(q4[l] & 0xF);
+        a += 32;
+        for (int l = 0; l < 32; l++) a[l] = (int8_t)(q4[l] >> 4);
+        a += 32; q4 += 32;
+    }
+}
+
+/* GetRow (CpuRef.cs:148-181), DequantizeRowQ4_0 (CpuRefGemma.cs:42-55), DequantizeRowK
+ * (CpuRefKQuants.cs:149-174) */
+int orc_dequantize_row(int type, const uint8_t* row, int cols, float* dst)
+{
+    if (type == ORC_F32) { memcpy(dst, row, (size_t)cols * 4); return 0; }
+    if (type == ORC_Q8_0) {
+        for (int b = 0; b < cols / QK8_0; b++) {
+            const uint8_t* blk = row + b * 34;
+            float d = orc_half_to_float(rd16(blk));
+            const int8_t* q = (const int8_t*)(blk + 2);
+            for (int j = 0; j < QK8_0; j++) dst[b * QK8_0 + j] = q[j] * d;
+        }
+        return 0;
+    }
+    if (type == ORC_Q4_0) {
+        for (int b = 0; b < cols / QK8_0; b++) {
+            const uint8_t* blk = row + b * 18;
+            float d = orc_half_to_float(rd16(blk));
+            const uint8_t* qs = blk + 2;
+            for (int j = 0; j < 16; j++) {
+                dst[b * QK8_0 + j] = ((qs[j] & 0x0F) - 8) * d;
+                dst[b * QK8_0 + j + 16] = ((qs[j] >> 4) - 8) * d;
+            }
+        }
+        return 0;
+    }
+    if (type == ORC_Q4_K || type == ORC_Q6_K) {
+        int nb = cols / QK_K, bytes = type == ORC_Q4_K ? 144 : 210;
+        int8_t a[QK_K]; int scales[16]; int mins[8];
+        for (int b = 0; b < nb; b++) {
+            float d, dmin;
+            unpack_k(type, row + (int64_t)b * bytes, a, scales, mins, &d, &dmin);
+            int o = b * QK_K;
+            if (type == ORC_Q6_K) {
+                for (int e = 0; e < QK_K; e++) dst[o + e] = d * scales[e / 16] * a[e];
+            } else {
+                for (int e = 0; e < QK_K; e++) { int sb = e / 32; dst[o + e] = d * scales[sb] * a[e] - dmin * mins[sb]; }
+            }
+        }
+        return 0;
+    }
+    return -3;
+}
+
+/* MatVecQ4_0 row body (CpuRefGemma.cs:23-38): per block integer sum, then
+ * sum += isum * (d_w * d_x), a float sum in block order. */
+float orc_dot_q4_0(const uint8_t* row, int nb, const uint16_t* xd, const int8_t* xq)
+{
+    float sum = 0;
+    for (int b = 0; b < nb; b++) {
+        const uint8_t* blk = row + b * 18;
+        const uint8_t* qs = blk + 2;
+        const int8_t* qx = xq + b * QK8_0;
+        int isum = 0;
+        for (int j = 0; j < 16; j++) isum += ((qs[j] & 0x0F) - 8) * qx[j] + ((qs[j] >> 4) - 8) * qx[j + 16];
+        sum += (float)isum * (orc_half_to_float(rd16(blk)) * orc_half_to_float(xd[b]));
+    }
+    return sum;
+}
+
+/* MatVecQ8_0 row body (CpuRef.cs:102-117) */
+float orc_dot_q8_0(const uint8_t* row, int nb, const uint16_t* xd, const int8_t* xq)
+{
+    float sum = 0;
+    for (int b = 0; b < nb; b++) {
+        const uint8_t* blk = row + b * 34;
+        const int8_t* qw = (const int8_t*)(blk + 2);
+        const int8_t* qx = xq + b * QK8_0;
+        int isum = 0;
+        for (int j = 0; j < QK8_0; j += 4)
+            isum += qw[j] * qx[j] + qw[j + 1] * qx[j + 1] + qw[j + 2] * qx[j + 2] + qw[j + 3] * qx[j + 3];
+        sum += (float)isum * (orc_half_to_float(rd16(blk)) * orc_half_to_float(xd[b]));
+    }
+    return sum;
+}
+
+/* DotK (CpuRefKQuants.cs:177-212): eight integer lanes aux32[l] per super-block, float lanes
+ * sums[l] += (d*yd) * aux32[l], the Q4_K min term sumf -= (dmin*yd) * sumi, then sumf += sums[l]. */
+float orc_dot_k(int t, const uint8_t* row, int nb, const float* kd, const int8_t* kq, const int16_t* kbs)
+{
+    float sums[8];
+    int aux32[8];
+    int8_t a[QK_K]; int scales[16]; int mins[8];
+    for (int l = 0; l < 8; l++) sums[l] = 0;
+    float sumf = 0;
+    int sixteen = t == ORC_Q6_K;
+    int sub = sixteen ? 16 : 32;
+    int bytes = t == ORC_Q4_K ? 144 : 210;
+    for (int i = 0; i < nb; i++) {
+        float d, dmin;
+        unpack_k(t, row + (int64_t)i * bytes, a, scales, mins, &d, &dmin);
+        for (int l = 0; l < 8; l++) aux32[l] = 0;
+        int o = i * QK_K;
+        for (int e = 0; e < QK_K; e += 8) {
+            int scale = scales[e / sub];
+            for (int l = 0; l < 8; l++) aux32[l] += scale * (int16_t)(kq[o + e + l] * a[e + l]);
+        }
+        float yd = kd[i];
+        float dd = d * yd;
+        for (int l = 0; l < 8; l++) sums[l] += dd * (float)aux32[l];
+        if (!sixteen) {
+            int sumi = 0;
+            for (int j = 0; j < QK_K / 16; j++) sumi += kbs[i * 16 + j] * mins[j / 2];
+            float dm = dmin * yd;
+            sumf -= dm * (float)sumi;
+        }
+    }
+    for (int l = 0; l < 8; l++) sumf += sums[l];
+    return sumf;
+}
+
+static int set_threads(int nthreads)
+{
+#ifdef _OPENMP
+    return nthreads > 0 ? nthreads : omp_get_max_threads();
+#else
+    (void)nthreads;
+    return 1;
+#endif
+}
+
+/* CpuRef.MatVec (CpuRef.cs:70-89) for F32/Q4_0/Q8_0/Q4_K/Q6_K: the activation quantization, then
+ * one independent dot per row (Parallel.For in the reference; rows never interact).  F32 follows
+ * MatVecF32 (CpuRef.cs:121-132): a double sum cast to float. */
+int orc_matvec(int type, const uint8_t* w, int rows, int cols, const float* x, float* y, int nthreads)
+{
+    int64_t rb = orc_row_bytes(type, cols);
+    if (rb < 0) return -3;
+    int nt = set_threads(nthreads);
+    (void)nt;
+    if (type == ORC_F32) {
+#pragma omp parallel for num_threads(nt) schedule(static)
+        for (int r = 0; r < rows; r++) {
+            const float* row = (const float*)(w + (int64_t)r * rb);
+            double sum = 0;
+            for (int j = 0; j < cols; j++) sum += row[j] * x[j];
+            y[r] = (float)sum;
+        }
+        return 0;
+    }
+    if (type == ORC_Q4_0 || type == ORC_Q8_0) {
+        if (cols % QK8_0) return -1;
+        int nb = cols / QK8_0;
+        uint16_t* xd = (uint16_t*)malloc(sizeof(uint16_t) * nb);
+        int8_t* xq = (int8_t*)malloc((size_t)cols);
+        orc_quantize_q8_0(x, cols, xd, xq);
+#pragma omp parallel for num_threads(nt) schedule(static)
+        for (int r = 0; r < rows; r++)
+            y[r] = type == ORC_Q4_0 ? orc_dot_q4_0(w + (int64_t)r * rb, nb, xd, xq)
+                                    : orc_dot_q8_0(w + (int64_t)r * rb, nb, xd, xq);
+        free(xd); free(xq);
+        return 0;
+    }
+    /* MatVecK (CpuRefKQuants.cs:214-232): rows must be whole super-blocks */
+    if (cols % QK_K) return -1;
+    int nb = cols / QK_K;
+    float* kd = (float*)malloc(sizeof(float) * nb);
+    int8_t* kq = (int8_t*)malloc((size_t)cols);
+    int16_t* kbs = (int16_t*)malloc(sizeof(int16_t) * (cols / 16));
+    orc_quantize_q8_k(x, cols, kd, kq, kbs);
+#pragma omp parallel for num_threads(nt) schedule(static)
+    for (int r = 0; r < rows; r++) y[r] = orc_dot_k(type, w + (int64_t)r * rb, nb, kd, kq, kbs);
+    free(kd); free(kq); free(kbs);
+    return 0;
+}
+
+/* ---------------------------------------------------------------- elementwise */
+
+/* CpuRef.Gelu (CpuRefGemma.cs:85-92): fp16(0.5 h (1 + tanh(c h (1 + 0.044715 h h)))) with
+ * h = fp16(x); tanh in double, every other operation in float, left to right. */
+float orc_gelu(float x)
+{
+    if (x <= -10.0f) return 0.0f;
+    if (x >= 10.0f) return x;
+    float h = orc_half_round(x);
+    float inner = 0.79788456080286535587989211986876f * h * (1.0f + 0.044715f * h * h);
+    float g = 0.5f * h * (1.0f + (float)tanh((double)inner));
+    return orc_half_round(g);
+}
+
+void orc_gelu_n(const float* x, float* y, int64_t n)
+{
+    for (int64_t i = 0; i < n; i++) y[i] = orc_gelu(x[i]);
+}
+
+/* The scale of CpuRef.RmsNorm (CpuRef.cs:186-189): double sum of squares in index order,
+ * mean = (float)(sum/n), scale = 1f / (float)sqrt(mean + eps). */
+float orc_rms_scale(const float* x, int n, float eps)
+{
+    double sum = 0;
+    for (int i = 0; i < n; i++) sum += (double)x[i] * x[i];
+    float mean = (float)(sum / n);
+    return 1.0f / (float)sqrt((double)(mean + eps));
+}
+
+/* CpuRef.RmsNorm (CpuRef.cs:184-191): y = x * scale * w */
+void orc_rmsnorm(const float* x, int n, const float* w, float eps, float* y)
+{
+    float scale = orc_rms_scale(x, n, eps);
+    for (int i = 0; i < n; i++) y[i] = x[i] * scale * w[i];
+}
+
+/* ---------------------------------------------------------------- MoE layer: src/GemmaCpu.cs */
+
+/* Router, top-k and weights (GemmaCpu.cs:385-407, weight fold :417). */
+void orc_router(const orc_layer* L, const float* x, float* logits, int32_t* ids, float* w)
+{
+    int d = L->d, ne = L->n_expert, k = L->n_used;
+    float* in = (float*)malloc(sizeof(float) * d);
+    double ss = 0;
+    for (int i = 0; i < d; i++) ss += (double)x[i] * x[i];
+    float rinv = 1.0f / (float)sqrt((double)((float)(ss / d) + L->eps));
+    float sc = 1.0f / (float)sqrt((double)d);
+    for (int i = 0; i < d; i++) in[i] = x[i] * rinv * sc * L->gate_inp_scale[i];
+    for (int e = 0; e < ne; e++) {
+        const float* wr = L->gate_inp + (int64_t)e * d;
+        float s = 0;
+        for (int i = 0; i < d; i++) s += wr[i] * in[i];
+        logits[e] = s;
+    }
+    /* k rounds of argmax, strict '>' so the lower index wins ties (GemmaCpu.cs:400-405) */
+    float sel[64];
+    char taken[1024];
+    memset(taken, 0, sizeof(taken));
+    for (int j = 0; j < k; j++) {
+        int bi = -1;
+        for (int e = 0; e < ne; e++) if (!taken[e] && (bi < 0 || logits[e] > logits[bi])) bi = e;
+        taken[bi] = 1; ids[j] = bi; sel[j] = logits[bi];
+    }
+    double sum = 0;
+    if (L->weight_rule == ORC_W_CPUREF) {
+        /* GemmaCpu.cs:407 as written: sel[0] is replaced by exp(0) = 1 before later terms read it */
+        for (int j = 0; j < k; j++) { sel[j] = (float)exp((double)(sel[j] - sel[0])); sum += sel[j]; }
+    } else {
+        float top = sel[0];
+        for (int j = 0; j < k; j++) { sel[j] = (float)exp((double)(sel[j] - top)); sum += sel[j]; }
+    }
+    /* GemmaCpu.cs:417: we = (float)(sel[j] / sum) * DownScale[e] */
+    for (int j = 0; j < k; j++) w[j] = (float)(sel[j] / sum) * L->down_scale[ids[j]];
+    free(in);
+}
+
+static int64_t exp_rows_bytes(int type, int rows, int cols) { return (int64_t)rows * orc_row_bytes(type, cols); }
+
+/* GemmaCpu.MoeFfn (GemmaCpu.cs:376-422) for one token. */
+void orc_moe_token(const orc_layer* L, const float* x, const float* shared, float* out, int32_t* ids,
+                   float* wout, float* gdbg, float* udbg, float* yddbg, int nthreads)
+{
+    int d = L->d, nf = L->n_ff, k = L->n_used, dc = L->down_cols;
+    float* mlp = (float*)calloc((size_t)d, sizeof(float));
+    float* logits = (float*)malloc(sizeof(float) * L->n_expert);
+    float* moe_in = (float*)malloc(sizeof(float) * d);
+    float* acc = (float*)calloc((size_t)d, sizeof(float));
+    float* gu = (float*)malloc(sizeof(float) * 2 * nf);
+    float* eg = (float*)calloc((size_t)dc, sizeof(float));
+    float* ed = (float*)malloc(sizeof(float) * d);
+    float* acc2 = (float*)malloc(sizeof(float) * d);
+    float w[64];
+    int32_t id[64];
+    /* _mlp = rmsnorm(shared) * post_ffw_norm_1 (GemmaCpu.cs:384); zero shared gives zero */
+    if (shared) orc_rmsnorm(shared, d, L->post_ffw_norm_1, L->eps, mlp);
+    orc_router(L, x, logits, id, w);
+    orc_rmsnorm(x, d, L->pre_ffw_norm_2, L->eps, moe_in);            /* GemmaCpu.cs:409 */
+    int64_t gu_bytes = exp_rows_bytes(L->gate_up_type, 2 * nf, d);
+    int64_t dn_bytes = exp_rows_bytes(L->down_type, d, dc);
+    for (int j = 0; j < k; j++) {                                     /* GemmaCpu.cs:411-419 */
+        int e = id[j];
+        orc_matvec(L->gate_up_type, L->gate_up_exps + (int64_t)e * gu_bytes, 2 * nf, d, moe_in, gu, nthreads);
+        for (int i = 0; i < nf; i++) eg[i] = orc_gelu(gu[i]) * gu[nf + i];
+        orc_matvec(L->down_type, L->down_exps + (int64_t)e * dn_bytes, d, dc, eg, ed, nthreads);
+        for (int i = 0; i < d; i++) acc[i] += ed[i] * w[j];
+        if (gdbg) memcpy(gdbg + (int64_t)j * nf, gu, sizeof(float) * nf);
+        if (udbg) memcpy(udbg + (int64_t)j * nf, gu + nf, sizeof(float) * nf);
+        if (yddbg) memcpy(yddbg + (int64_t)j * d, ed, sizeof(float) * d);
+    }
+    orc_rmsnorm(acc, d, L->post_ffw_norm_2, L->eps, acc2);           /* GemmaCpu.cs:420 */
+    for (int i = 0; i < d; i++) out[i] = mlp[i] + acc2[i];            /* GemmaCpu.cs:421 */
+    if (ids) memcpy(ids, id, sizeof(int32_t) * k);
+    if (wout) memcpy(wout, w, sizeof(float) * k);
+    free(mlp); free(logits); free(moe_in); free(acc); free(gu); free(eg); free(ed); free(acc2);
+}
+
+/* PostAndFfn's dense FFN (GemmaCpu.cs:348-353) */
+void orc_shared_ffn_token(const orc_layer* L, const float* x, float* out, int nthreads)
+{
+    int d = L->d, nff = L->n_ff_shared;
+    float* n = (float*)malloc(sizeof(float) * d);
+    float* gate = (float*)malloc(sizeof(float) * nff);
+    float* up = (float*)malloc(sizeof(float) * nff);
+    orc_rmsnorm(x, d, L->ffn_norm, L->eps, n);
+    orc_matvec(L->shared_type, L->ffn_gate, nff, d, n, gate, nthreads);
+    orc_matvec(L->shared_type, L->ffn_up, nff, d, n, up, nthreads);
+    for (int i = 0; i < nff; i++) gate[i] = orc_gelu(gate[i]) * up[i];
+    orc_matvec(L->shared_type, L->ffn_down, d, nff, gate, out, nthreads);
+    free(n); free(gate); free(up);
+}
+
+void orc_moe_block(const orc_layer* L, int T, const float* x, const float* shared, float* out, int32_t* ids,
+                   float* w, int nthreads)
+{
+    int d = L->d, k = L->n_used;
+    float* sh = NULL;
+    if (!shared && L->n_ff_shared > 0) sh = (float*)malloc(sizeof(float) * d);
+    for (int t = 0; t < T; t++) {
+        const float* s = shared ? shared + (int64_t)t * d : NULL;
+        if (sh) { orc_shared_ffn_token(L, x + (int64_t)t * d, sh, nthreads); s = sh; }
+        orc_moe_token(L, x + (int64_t)t * d, s, out + (int64_t)t * d, ids ? ids + (int64_t)t * k : NULL,
+                      w ? w + (int64_t)t * k : NULL, NULL, NULL, NULL, nthreads);
+    }
+    free(sh);
+}
+
+/* GemmaCpu.cs:355-356: x += rmsnorm(out) * post_ffw_norm */
+void orc_residual(const orc_layer* L, int T, float* x, const float* out)
+{
+    int d = L->d;
+    float* y = (float*)malloc(sizeof(float) * d);
+    for (int t = 0; t < T; t++) {
+        orc_rmsnorm(out + (int64_t)t * d, d, L->post_ffw_norm, L->eps, y);
+        for (int i = 0; i < d; i++) x[(int64_t)t * d + i] += y[i];
+    }
+    free(y);
+}
+
+/* KernelsMoe.Bucket list semantics (KernelsMoe.cs:281-330): expert e's list holds every assignment
+ * a = t*k + j routed to e, in ascending a; here as one compact permutation with offsets. */
+void orc_bucket(const int32_t* ids, int T, int k, int E, int32_t* offsets, int32_t* perm)
+{
+    for (int e = 0; e <= E; e++) offsets[e] = 0;
+    for (int a = 0; a < T * k; a++) offsets[ids[a] + 1]++;
+    for (int e = 0; e < E; e++) offsets[e + 1] += offsets[e];
+    int32_t* fill = (int32_t*)malloc(sizeof(int32_t) * (E > 0 ? E : 1));
+    for (int e = 0; e < E; e++) fill[e] = offsets[e];
+    for (int a = 0; a < T * k; a++) perm[fill[ids[a]]++] = a;
+    free(fill);
+}

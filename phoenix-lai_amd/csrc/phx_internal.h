@@ -1,0 +1,76 @@
+// Internal types shared by the runtime (runtime.hip) and the gfx950 kernels (kernels.hip).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "phx_moe.h"
+
+#define PHX_Q4_0_DEV 2
+#define PHX_Q8_0_DEV 8
+#define PHX_Q4_K_DEV 12
+#define PHX_Q6_K_DEV 14
+#define PHX_MAX_USED_DEV 16
+#define PHX_MAX_EXPERTS_DEV 256
+
+namespace phx {
+
+constexpr int kRowGroup = 64;  // rows per interleaved row group: one wave64, lane = row
+
+// Activation formats produced for each weight type.
+enum ActFmt { ACT_Q8_0 = 0, ACT_K4 = 1, ACT_K6 = 2 };
+
+// One stack of quantized matrices (experts, or one dense matrix), repacked at upload into row
+// groups of 64 rows: payload[m][rg][b][lane][pay] and scale[m][rg][b][lane][sbytes], so the 64
+// lanes of a wave read block b of 64 consecutive rows as one contiguous span.
+//   Q4_0: pay 16 (nibbles, low = element j, high = j+16), scale fp16 d
+//   Q8_0: pay 32 (int8), scale fp16 d
+//   Q4_K: pay 144 = 128 nibbles in (sub-block, l, m) order + sc[8] + m[8]; scale fp16 d | fp16 dmin << 16
+//   Q6_K: pay 208 = 128 low-nibble plane + 64 high-bit plane + int8 sc[16]; scale fp16 d
+struct QMat {
+    int type = -1;
+    int n_mat = 0, rows = 0, cols = 0;  // cols includes any zero padding of K
+    int rg = 0, nb = 0;                 // row groups, blocks (32 or 256 elements) per row
+    int pay = 0, sbytes = 0;
+    uint8_t* payload = nullptr;
+    uint8_t* scale = nullptr;
+    int64_t mat_pay_stride() const { return (int64_t)rg * nb * kRowGroup * pay; }
+    int64_t mat_sc_stride() const { return (int64_t)rg * nb * kRowGroup * sbytes; }
+};
+
+// Quantized activation rows for one weight type.
+//   ACT_Q8_0: q int8 [cols], d f32 [cols/32] (value of the fp16 scale), s int32 [cols/32] block sums
+//   ACT_K4:   q int8 [cols] permuted per 32-sub-block as dwords (l, m) = x[32s + l + 8m],
+//             d f32 [cols/256], s int32 [cols/16] (the Q8_K bsums)
+//   ACT_K6:   q int32 [cols/256][8 P][8 l][2] masked pair dwords, d f32 [cols/256],
+//             s int32 [cols/256][16 sub][8 l] offset terms -32*(x_l + x_{l+8})
+struct Act {
+    int fmt = ACT_Q8_0;
+    int cols = 0;
+    int8_t* q = nullptr;
+    int64_t qstride = 0;  // bytes per row
+    float* d = nullptr;
+    int dstride = 0;      // floats per row
+    int* s = nullptr;
+    int sstride = 0;      // ints per row
+};
+
+struct Tile { int e, start, cnt; };
+
+// kernels.hip launchers (all enqueue on `st`)
+void launch_prologue(hipStream_t st, int T, int d, float eps, const float* x, const float* gate_inp_scale,
+                     const float* pre2, const float* ffn_norm, float* router_in, float* xscale, Act act_gu,
+                     Act act_sh, int* flags);
+void launch_router_exact(hipStream_t st, int T, int d, int E, const float* wt4, const float* router_in, float* logits);
+void launch_topk(hipStream_t st, int T, int E, int k, int rule, const float* logits, const float* down_scale,
+                 int* ids, float* w);
+void launch_dispatch(hipStream_t st, int n_assign, int E, int A, const int* ids, int* offsets, int* perm,
+                     Tile* tiles, int* ntiles);
+void launch_grouped(hipStream_t st, const QMat& w, Act act, const Tile* tiles, const int* ntiles, int max_tiles,
+                    int A, const int* perm, int act_div, float* out0, float* out1, int split, int out_stride);
+void launch_requant(hipStream_t st, int rows, int nf, const float* g, const float* u, const float* gelu_tab, Act act);
+void launch_combine(hipStream_t st, int T, int d, int k, float eps, const float* yd, const float* w,
+                    const float* shared, const float* post1, const float* post2, float* out, float* x_resid,
+                    const float* post_ffw, int* flags);
+void launch_selftest(hipStream_t st, int op, int n, const float* a, const float* b, float* out, const float* gelu_tab);
+
+}  // namespace phx

@@ -1,0 +1,890 @@
+// libphxmoe.so host runtime: the C ABI of include/phx_moe.h.  Owns the HIP device, one stream, all
+// device memory, the per-layer repacked weights and the workspace; enqueues the kernels of
+// kernels.hip for one MoE FFN block (the sequence GemmaGpu records at src/GemmaGpu.cs:683-704 and
+// :850-882, with the CPU reference's arithmetic), and captures consecutive layers into a HIP graph.
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "phx_internal.h"
+
+using namespace phx;
+
+namespace {
+
+// ------------------------------------------------------------------------------ host fp16 (RNE)
+uint16_t half_bits(float value)
+{
+    uint32_t f;
+    memcpy(&f, &value, 4);
+    uint32_t sign = (f >> 16) & 0x8000u;
+    int e = (int)((f >> 23) & 0xFF);
+    uint32_t m = f & 0x7FFFFFu;
+    if (e == 255) return (uint16_t)(sign | 0x7C00u | (m ? 0x200u : 0u));
+    int ne = e - 112;
+    if (ne >= 31) return (uint16_t)(sign | 0x7C00u);
+    if (ne <= 0) {
+        if (ne < -10) return (uint16_t)sign;
+        m |= 0x800000u;
+        int sh = 14 - ne;
+        uint32_t hm = m >> sh, rem = m & ((1u << sh) - 1), half = 1u << (sh - 1);
+        if (rem > half || (rem == half && (hm & 1))) hm++;
+        return (uint16_t)(sign | hm);
+    }
+    uint32_t h = sign | ((uint32_t)ne << 10) | (m >> 13), r = m & 0x1FFFu;
+    if (r > 0x1000u || (r == 0x1000u && (h & 1))) h++;
+    return (uint16_t)h;
+}
+
+float half_value(uint16_t h)
+{
+    uint32_t s = (uint32_t)(h >> 15) << 31, e = (h >> 10) & 0x1F, m = h & 0x3FF, bits;
+    if (e == 0) {
+        if (!m) bits = s;
+        else {
+            int k = -1;
+            do { k++; m <<= 1; } while (!(m & 0x400));
+            bits = s | (uint32_t)(112 - k) << 23 | (m & 0x3FF) << 13;
+        }
+    } else if (e == 31) bits = s | 0x7F800000u | m << 13;
+    else bits = s | (e + 112) << 23 | m << 13;
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+// GELU over the 65,536 fp16 inputs, the reference formula (src/CpuRefGemma.cs:85-92) evaluated in
+// binary32 with a binary64 tanh: the table the kernels read for |x| < 10.
+void build_gelu_table(std::vector<float>& tab)
+{
+    tab.resize(65536);
+    for (int i = 0; i < 65536; i++) {
+        float h = half_value((uint16_t)i);
+        float g;
+        if (!(h == h) || h <= -10.0f) g = 0.0f;
+        else if (h >= 10.0f) g = h;
+        else {
+            float inner = 0.79788456080286535587989211986876f * h * (1.0f + 0.044715f * h * h);
+            float v = 0.5f * h * (1.0f + (float)tanh((double)inner));
+            g = half_value(half_bits(v));
+        }
+        tab[i] = g;
+    }
+}
+
+int64_t row_bytes(int type, int cols)
+{
+    switch (type) {
+    case PHX_F32: return (int64_t)cols * 4;
+    case PHX_Q4_0: return (int64_t)(cols / 32) * 18;
+    case PHX_Q8_0: return (int64_t)(cols / 32) * 34;
+    case PHX_Q4_K: return (int64_t)(cols / 256) * 144;
+    case PHX_Q6_K: return (int64_t)(cols / 256) * 210;
+    }
+    return -1;
+}
+
+bool quant_type(int t) { return t == PHX_Q4_0 || t == PHX_Q8_0 || t == PHX_Q4_K || t == PHX_Q6_K; }
+int block_elems(int t) { return (t == PHX_Q4_K || t == PHX_Q6_K) ? 256 : 32; }
+int act_fmt(int t) { return t == PHX_Q4_K ? ACT_K4 : t == PHX_Q6_K ? ACT_K6 : ACT_Q8_0; }
+int round_up(int v, int m) { return (v + m - 1) / m * m; }
+
+// ------------------------------------------------------------------------------ repack
+// GGUF rows [n_mat][rows][row_bytes] -> row groups of 64 (see QMat).
+struct HostQ {
+    std::vector<uint8_t> payload, scale;
+};
+
+void decode_q4k_natural(const uint8_t* blk, uint8_t* q, int* sc, int* mn)
+{
+    // UnpackK's element order for Q4_K (src/CpuRefKQuants.cs:118-133)
+    const uint8_t* s8 = blk + 4;
+    for (int j = 0; j < 8; j++) {
+        if (j < 4) { sc[j] = s8[j] & 63; mn[j] = s8[j + 4] & 63; }
+        else { sc[j] = (s8[j + 4] & 0xF) | ((s8[j - 4] >> 6) << 4); mn[j] = (s8[j + 4] >> 4) | ((s8[j] >> 6) << 4); }
+    }
+    const uint8_t* q4 = blk + 16;
+    for (int c = 0; c < 4; c++)
+        for (int l = 0; l < 32; l++) {
+            q[64 * c + l] = q4[32 * c + l] & 0xF;
+            q[64 * c + 32 + l] = q4[32 * c + l] >> 4;
+        }
+}
+
+void decode_q6k_natural(const uint8_t* blk, uint8_t* v)
+{
+    // UnpackK's element order for Q6_K (src/CpuRefKQuants.cs:98-111), kept unsigned (q + 32)
+    const uint8_t* ql = blk;
+    const uint8_t* qh = blk + 128;
+    for (int n = 0; n < 2; n++) {
+        uint8_t* a = v + 128 * n;
+        for (int l = 0; l < 32; l++) {
+            a[l] = (uint8_t)((ql[l] & 0xF) | (((qh[l] >> 0) & 3) << 4));
+            a[l + 32] = (uint8_t)((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4));
+            a[l + 64] = (uint8_t)((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4));
+            a[l + 96] = (uint8_t)((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4));
+        }
+        ql += 64;
+        qh += 32;
+    }
+}
+
+void repack_block(int type, const uint8_t* blk, uint8_t* pay, uint8_t* sc)
+{
+    switch (type) {
+    case PHX_Q4_0:
+        memcpy(sc, blk, 2);
+        memcpy(pay, blk + 2, 16);
+        break;
+    case PHX_Q8_0:
+        memcpy(sc, blk, 2);
+        memcpy(pay, blk + 2, 32);
+        break;
+    case PHX_Q4_K: {
+        uint8_t q[256];
+        int s[8], m[8];
+        decode_q4k_natural(blk, q, s, m);
+        for (int w = 0; w < 32; w++) {
+            int sb = w / 4, p = w % 4;
+            for (int mm = 0; mm < 4; mm++)
+                pay[4 * w + mm] = (uint8_t)(q[32 * sb + 2 * p + 8 * mm] | (q[32 * sb + 2 * p + 1 + 8 * mm] << 4));
+        }
+        for (int j = 0; j < 8; j++) { pay[128 + j] = (uint8_t)s[j]; pay[136 + j] = (uint8_t)m[j]; }
+        memcpy(sc, blk, 4);  // d | dmin << 16
+        break;
+    }
+    case PHX_Q6_K: {
+        uint8_t v[256], out[256];
+        decode_q6k_natural(blk, v);
+        for (int P = 0; P < 8; P++)
+            for (int l = 0; l < 8; l++) {
+                uint8_t* o = out + 4 * (P * 8 + l);
+                o[0] = v[32 * P + l];
+                o[1] = v[32 * P + l + 8];
+                o[2] = v[32 * P + 16 + l];
+                o[3] = v[32 * P + 16 + l + 8];
+            }
+        for (int w = 0; w < 32; w++)
+            for (int mm = 0; mm < 4; mm++)
+                pay[4 * w + mm] = (uint8_t)((out[4 * (2 * w) + mm] & 0xF) | ((out[4 * (2 * w + 1) + mm] & 0xF) << 4));
+        for (int h = 0; h < 16; h++)
+            for (int mm = 0; mm < 4; mm++) {
+                uint8_t b = 0;
+                for (int i = 0; i < 4; i++) b |= (uint8_t)(((out[4 * (4 * h + i) + mm] >> 4) & 3) << (2 * i));
+                pay[128 + 4 * h + mm] = b;
+            }
+        memcpy(pay + 192, blk + 192, 16);
+        memcpy(sc, blk + 208, 2);
+        break;
+    }
+    }
+}
+
+void repack(int type, const uint8_t* src, int n_mat, int rows, int cols, QMat& q, HostQ& h)
+{
+    q.type = type;
+    q.n_mat = n_mat;
+    q.rows = rows;
+    q.cols = cols;
+    q.rg = (rows + kRowGroup - 1) / kRowGroup;
+    q.nb = cols / block_elems(type);
+    q.pay = type == PHX_Q4_0 ? 16 : type == PHX_Q8_0 ? 32 : type == PHX_Q4_K ? 144 : 208;
+    q.sbytes = type == PHX_Q4_K ? 4 : 2;
+    const int64_t rb = row_bytes(type, cols), bb = rb / q.nb;
+    h.payload.assign((size_t)q.mat_pay_stride() * n_mat, 0);
+    h.scale.assign((size_t)q.mat_sc_stride() * n_mat, 0);
+    const int64_t total_rows = (int64_t)n_mat * rows;
+    unsigned nt = std::max(1u, std::min(16u, std::thread::hardware_concurrency()));
+    std::vector<std::thread> th;
+    for (unsigned w = 0; w < nt; w++) {
+        th.emplace_back([&, w]() {
+            for (int64_t gr = w; gr < total_rows; gr += nt) {
+                int m = (int)(gr / rows), r = (int)(gr % rows);
+                int rg = r / kRowGroup, lane = r % kRowGroup;
+                const uint8_t* row = src + gr * rb;
+                for (int b = 0; b < q.nb; b++) {
+                    int64_t idx = (((int64_t)m * q.rg + rg) * q.nb + b) * kRowGroup + lane;
+                    repack_block(type, row + b * bb, h.payload.data() + idx * q.pay, h.scale.data() + idx * q.sbytes);
+                }
+            }
+        });
+    }
+    for (auto& t : th) t.join();
+}
+
+struct Layer {
+    bool present = false;
+    phx_moe_layer_desc desc{};
+    float *wt4 = nullptr, *gis = nullptr, *ds = nullptr, *pre2 = nullptr, *post1 = nullptr, *post2 = nullptr;
+    float *ffn_norm = nullptr, *post_ffw = nullptr;
+    QMat gu, dn, sgu, sdn;
+};
+
+struct Buf {
+    void* p = nullptr;
+    size_t bytes = 0;
+};
+
+}  // namespace
+
+struct phx_moe_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::string err;
+    float* gelu_tab = nullptr;
+    std::vector<Layer> layers;
+    std::vector<Buf> ws;
+    int* flags = nullptr;  // [0] count of certified-sum fallbacks
+    int last_T = 0, last_layer = -1;
+    // profiling
+    bool profiling = false;
+    struct Pending { int kind; hipEvent_t a, b; };
+    std::vector<Pending> pending;
+    std::vector<hipEvent_t> pool;
+    double prof_ms[PHX_K_COUNT] = {};
+    int64_t prof_n[PHX_K_COUNT] = {};
+    // stack graph
+    hipGraphExec_t graph_exec = nullptr;
+    hipGraph_t graph = nullptr;
+    int graph_T = 0, graph_first = 0, graph_n = 0;
+};
+
+namespace {
+
+int set_err(phx_moe_ctx* c, int code, const char* fmt, ...)
+{
+    if (c) {
+        char buf[512];
+        va_list ap;
+        va_start(ap, fmt);
+        vsnprintf(buf, sizeof buf, fmt, ap);
+        va_end(ap);
+        c->err = buf;
+    }
+    return code;
+}
+
+int hip_code(hipError_t e)
+{
+    switch (e) {
+    case hipSuccess: return PHX_OK;
+    case hipErrorOutOfMemory: return PHX_ERR_OOM;
+    case hipErrorIllegalAddress:
+    case hipErrorLaunchFailure:
+    case hipErrorNoDevice: return PHX_ERR_DEVICE_LOST;
+    default: return PHX_ERR_HIP;
+    }
+}
+
+#define HIPCHK(c, expr)                                                                                       \
+    do {                                                                                                      \
+        hipError_t e_ = (expr);                                                                               \
+        if (e_ != hipSuccess) return set_err(c, hip_code(e_), "%s: %s", #expr, hipGetErrorString(e_));        \
+    } while (0)
+
+enum WsId {
+    W_X, W_SHARED, W_OUT, W_RIN, W_XSCALE, W_AGU_Q, W_AGU_D, W_AGU_S, W_ASH_Q, W_ASH_D, W_ASH_S, W_LOGITS, W_IDS, W_W,
+    W_OFF, W_PERM, W_TILES, W_NTILES, W_G, W_U, W_ADN_Q, W_ADN_D, W_ADN_S, W_YD, W_SHG, W_SHU, W_ASD_Q, W_ASD_D,
+    W_ASD_S, W_SHOUT, W_ZERO, W_STILES, W_SNTILES, W_SOFF, W_SPERM, W_COUNT
+};
+
+int ensure(phx_moe_ctx* c, int id, size_t bytes)
+{
+    if ((int)c->ws.size() < W_COUNT) c->ws.resize(W_COUNT);
+    Buf& b = c->ws[id];
+    if (b.bytes >= bytes && b.p) return PHX_OK;
+    if (b.p) HIPCHK(c, hipFree(b.p));
+    b.p = nullptr;
+    b.bytes = 0;
+    size_t n = std::max<size_t>(bytes, 256);
+    HIPCHK(c, hipMalloc(&b.p, n));
+    b.bytes = n;
+    if (id == W_ZERO) HIPCHK(c, hipMemset(b.p, 0, n));
+    return PHX_OK;
+}
+
+template <class T> T* wp(phx_moe_ctx* c, int id) { return (T*)c->ws[id].p; }
+
+// sizes of an activation buffer of `rows` rows of `cols` elements in format fmt
+void act_sizes(int fmt, int64_t rows, int cols, size_t& qb, size_t& db, size_t& sb)
+{
+    if (fmt == ACT_Q8_0) { qb = rows * cols; db = rows * (cols / 32) * 4; sb = rows * (cols / 32) * 4; }
+    else if (fmt == ACT_K4) { qb = rows * cols; db = rows * (cols / 256) * 4; sb = rows * (cols / 16) * 4; }
+    else { qb = rows * (cols / 256) * 512; db = rows * (cols / 256) * 4; sb = rows * (cols / 256) * 128 * 4; }
+}
+
+Act make_act(phx_moe_ctx* c, int fmt, int cols, int qid, int did, int sid)
+{
+    Act a;
+    a.fmt = fmt;
+    a.cols = cols;
+    a.q = wp<int8_t>(c, qid);
+    a.d = wp<float>(c, did);
+    a.s = wp<int>(c, sid);
+    if (fmt == ACT_Q8_0) { a.qstride = cols; a.dstride = cols / 32; a.sstride = cols / 32; }
+    else if (fmt == ACT_K4) { a.qstride = cols; a.dstride = cols / 256; a.sstride = cols / 16; }
+    else { a.qstride = (int64_t)(cols / 256) * 512; a.dstride = cols / 256; a.sstride = (cols / 256) * 128; }
+    return a;
+}
+
+int ensure_act(phx_moe_ctx* c, int fmt, int64_t rows, int cols, int qid, int did, int sid)
+{
+    size_t qb, db, sb;
+    act_sizes(fmt, rows, cols, qb, db, sb);
+    int rc;
+    if ((rc = ensure(c, qid, qb)) || (rc = ensure(c, did, db)) || (rc = ensure(c, sid, sb))) return rc;
+    return PHX_OK;
+}
+
+constexpr int kTileA = 4;  // assignments per grouped tile
+
+int ensure_workspace(phx_moe_ctx* c, const Layer& L, int T)
+{
+    const phx_moe_layer_desc& D = L.desc;
+    const int64_t n = (int64_t)T * D.n_used;
+    int rc;
+#define ENS(id, bytes) \
+    if ((rc = ensure(c, id, (size_t)(bytes)))) return rc
+    ENS(W_X, (size_t)T * D.d * 4);
+    ENS(W_SHARED, (size_t)T * D.d * 4);
+    ENS(W_OUT, (size_t)T * D.d * 4);
+    ENS(W_RIN, (size_t)T * D.d * 4);
+    ENS(W_XSCALE, (size_t)T * 4);
+    ENS(W_LOGITS, (size_t)T * D.n_expert * 4);
+    ENS(W_IDS, n * 4);
+    ENS(W_W, n * 4);
+    ENS(W_OFF, (size_t)(D.n_expert + 1) * 4);
+    ENS(W_PERM, n * 4);
+    ENS(W_TILES, (size_t)((n + kTileA - 1) / kTileA + D.n_expert) * sizeof(Tile));
+    ENS(W_NTILES, 4);
+    ENS(W_G, n * D.n_ff * 4);
+    ENS(W_U, n * D.n_ff * 4);
+    ENS(W_YD, n * D.d * 4);
+    if ((rc = ensure_act(c, act_fmt(D.gate_up_type), T, D.d, W_AGU_Q, W_AGU_D, W_AGU_S))) return rc;
+    if ((rc = ensure_act(c, act_fmt(D.down_type), n, D.down_cols, W_ADN_Q, W_ADN_D, W_ADN_S))) return rc;
+    if (D.n_ff_shared > 0) {
+        int scols = round_up(D.n_ff_shared, block_elems(D.shared_type));
+        if ((rc = ensure_act(c, act_fmt(D.shared_type), T, D.d, W_ASH_Q, W_ASH_D, W_ASH_S))) return rc;
+        if ((rc = ensure_act(c, act_fmt(D.shared_type), T, scols, W_ASD_Q, W_ASD_D, W_ASD_S))) return rc;
+        ENS(W_SHG, (size_t)T * D.n_ff_shared * 4);
+        ENS(W_SHU, (size_t)T * D.n_ff_shared * 4);
+        ENS(W_SHOUT, (size_t)T * D.d * 4);
+        ENS(W_ZERO, (size_t)T * 4);
+        ENS(W_STILES, (size_t)((T + kTileA - 1) / kTileA + 1) * sizeof(Tile));
+        ENS(W_SNTILES, 4);
+        ENS(W_SOFF, 8);
+        ENS(W_SPERM, (size_t)T * 4);
+    }
+#undef ENS
+    return PHX_OK;
+}
+
+hipEvent_t get_event(phx_moe_ctx* c)
+{
+    if (!c->pool.empty()) {
+        hipEvent_t e = c->pool.back();
+        c->pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    (void)hipEventCreate(&e);
+    return e;
+}
+
+struct ProfScope {
+    phx_moe_ctx* c;
+    int kind;
+    hipEvent_t a = nullptr;
+    ProfScope(phx_moe_ctx* c_, int k) : c(c_), kind(k)
+    {
+        if (c->profiling) {
+            a = get_event(c);
+            (void)hipEventRecord(a, c->stream);
+        }
+    }
+    ~ProfScope()
+    {
+        if (a) {
+            hipEvent_t b = get_event(c);
+            (void)hipEventRecord(b, c->stream);
+            c->pending.push_back({kind, a, b});
+        }
+    }
+};
+
+// Enqueue one MoE FFN block on the context stream.
+int run_layer(phx_moe_ctx* c, const Layer& L, int T, const float* x, const float* shared, float* out, float* xres)
+{
+    const phx_moe_layer_desc& D = L.desc;
+    hipStream_t st = c->stream;
+    const int d = D.d, E = D.n_expert, k = D.n_used, nf = D.n_ff;
+    const int n = T * k;
+    const bool shared_ffn = shared == nullptr && D.n_ff_shared > 0;
+    Act agu = make_act(c, act_fmt(D.gate_up_type), d, W_AGU_Q, W_AGU_D, W_AGU_S);
+    Act ash;
+    if (shared_ffn) ash = make_act(c, act_fmt(D.shared_type), d, W_ASH_Q, W_ASH_D, W_ASH_S);
+    ash.cols = shared_ffn ? ash.cols : 0;
+    {
+        ProfScope p(c, PHX_K_PROLOGUE);
+        launch_prologue(st, T, d, D.eps, x, L.gis, L.pre2, shared_ffn ? L.ffn_norm : nullptr, wp<float>(c, W_RIN),
+                        wp<float>(c, W_XSCALE), agu, ash, c->flags);
+    }
+    {
+        ProfScope p(c, PHX_K_ROUTER);
+        launch_router_exact(st, T, d, E, L.wt4, wp<float>(c, W_RIN), wp<float>(c, W_LOGITS));
+    }
+    {
+        ProfScope p(c, PHX_K_TOPK);
+        launch_topk(st, T, E, k, D.weight_rule, wp<float>(c, W_LOGITS), L.ds, wp<int>(c, W_IDS), wp<float>(c, W_W));
+    }
+    const int max_tiles = (n + kTileA - 1) / kTileA + E;
+    {
+        ProfScope p(c, PHX_K_DISPATCH);
+        launch_dispatch(st, n, E, kTileA, wp<int>(c, W_IDS), wp<int>(c, W_OFF), wp<int>(c, W_PERM), wp<Tile>(c, W_TILES),
+                        wp<int>(c, W_NTILES));
+    }
+    {
+        ProfScope p(c, PHX_K_GATE_UP);
+        launch_grouped(st, L.gu, agu, wp<Tile>(c, W_TILES), wp<int>(c, W_NTILES), max_tiles, kTileA, wp<int>(c, W_PERM), k,
+                       wp<float>(c, W_G), wp<float>(c, W_U), nf, nf);
+    }
+    Act adn = make_act(c, act_fmt(D.down_type), D.down_cols, W_ADN_Q, W_ADN_D, W_ADN_S);
+    {
+        ProfScope p(c, PHX_K_REQUANT);
+        launch_requant(st, n, nf, wp<float>(c, W_G), wp<float>(c, W_U), c->gelu_tab, adn);
+    }
+    {
+        ProfScope p(c, PHX_K_DOWN);
+        launch_grouped(st, L.dn, adn, wp<Tile>(c, W_TILES), wp<int>(c, W_NTILES), max_tiles, kTileA, wp<int>(c, W_PERM), 1,
+                       wp<float>(c, W_YD), wp<float>(c, W_YD), d, d);
+    }
+    const float* sh = shared;
+    if (shared_ffn) {
+        ProfScope p(c, PHX_K_SHARED);
+        const int nff = D.n_ff_shared;
+        const int smax = (T + kTileA - 1) / kTileA + 1;
+        launch_dispatch(st, T, 1, kTileA, wp<int>(c, W_ZERO), wp<int>(c, W_SOFF), wp<int>(c, W_SPERM),
+                        wp<Tile>(c, W_STILES), wp<int>(c, W_SNTILES));
+        launch_grouped(st, L.sgu, ash, wp<Tile>(c, W_STILES), wp<int>(c, W_SNTILES), smax, kTileA, wp<int>(c, W_SPERM), 1,
+                       wp<float>(c, W_SHG), wp<float>(c, W_SHU), nff, nff);
+        Act asd = make_act(c, act_fmt(D.shared_type), round_up(nff, block_elems(D.shared_type)), W_ASD_Q, W_ASD_D,
+                           W_ASD_S);
+        launch_requant(st, T, nff, wp<float>(c, W_SHG), wp<float>(c, W_SHU), c->gelu_tab, asd);
+        launch_grouped(st, L.sdn, asd, wp<Tile>(c, W_STILES), wp<int>(c, W_SNTILES), smax, kTileA, wp<int>(c, W_SPERM), 1,
+                       wp<float>(c, W_SHOUT), wp<float>(c, W_SHOUT), d, d);
+        sh = wp<float>(c, W_SHOUT);
+    }
+    {
+        ProfScope p(c, PHX_K_COMBINE);
+        launch_combine(st, T, d, k, D.eps, wp<float>(c, W_YD), wp<float>(c, W_W), sh, L.post1, L.post2, out, xres,
+                       L.post_ffw, c->flags);
+    }
+    HIPCHK(c, hipGetLastError());
+    return PHX_OK;
+}
+
+int upload_f32(phx_moe_ctx* c, const float* src, size_t n, float** dst)
+{
+    if (*dst) HIPCHK(c, hipFree(*dst));
+    *dst = nullptr;
+    HIPCHK(c, hipMalloc((void**)dst, std::max<size_t>(n, 1) * 4));
+    HIPCHK(c, hipMemcpy(*dst, src, n * 4, hipMemcpyHostToDevice));
+    return PHX_OK;
+}
+
+void free_qmat(QMat& q)
+{
+    if (q.payload) (void)hipFree(q.payload);
+    if (q.scale) (void)hipFree(q.scale);
+    q.payload = nullptr;
+    q.scale = nullptr;
+}
+
+int upload_q(phx_moe_ctx* c, int type, const void* src, int n_mat, int rows, int cols, QMat& q)
+{
+    free_qmat(q);
+    HostQ h;
+    repack(type, (const uint8_t*)src, n_mat, rows, cols, q, h);
+    HIPCHK(c, hipMalloc((void**)&q.payload, h.payload.size()));
+    HIPCHK(c, hipMalloc((void**)&q.scale, h.scale.size()));
+    HIPCHK(c, hipMemcpy(q.payload, h.payload.data(), h.payload.size(), hipMemcpyHostToDevice));
+    HIPCHK(c, hipMemcpy(q.scale, h.scale.data(), h.scale.size(), hipMemcpyHostToDevice));
+    return PHX_OK;
+}
+
+void free_layer(Layer& L)
+{
+    float** fs[] = {&L.wt4, &L.gis, &L.ds, &L.pre2, &L.post1, &L.post2, &L.ffn_norm, &L.post_ffw};
+    for (float** f : fs) {
+        if (*f) (void)hipFree(*f);
+        *f = nullptr;
+    }
+    free_qmat(L.gu);
+    free_qmat(L.dn);
+    free_qmat(L.sgu);
+    free_qmat(L.sdn);
+    L.present = false;
+}
+
+int drain_profile(phx_moe_ctx* c)
+{
+    if (c->pending.empty()) return PHX_OK;
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    for (auto& p : c->pending) {
+        float ms = 0.0f;
+        if (hipEventElapsedTime(&ms, p.a, p.b) == hipSuccess) {
+            c->prof_ms[p.kind] += ms;
+            c->prof_n[p.kind] += 1;
+        }
+        c->pool.push_back(p.a);
+        c->pool.push_back(p.b);
+    }
+    c->pending.clear();
+    return PHX_OK;
+}
+
+}  // namespace
+
+// ================================================================================ C ABI
+
+extern "C" {
+
+int phx_moe_check_desc(const phx_moe_layer_desc* D)
+{
+    if (!D) return PHX_ERR_ARG;
+    if (D->d <= 0 || D->n_expert <= 0 || D->n_used <= 0 || D->n_ff <= 0) return PHX_ERR_ARG;
+    if (D->n_expert > PHX_MAX_EXPERTS || D->n_used > PHX_MAX_USED || D->n_used > D->n_expert) return PHX_ERR_UNSUPPORTED;
+    if (D->n_ff % 32 != 0 || D->d % 32 != 0) return PHX_ERR_UNSUPPORTED;
+    if (!quant_type(D->gate_up_type) || !quant_type(D->down_type)) return PHX_ERR_UNSUPPORTED;
+    if (D->d % block_elems(D->gate_up_type) != 0) return PHX_ERR_UNSUPPORTED;
+    if (D->down_cols != round_up(D->n_ff, block_elems(D->down_type))) return PHX_ERR_ARG;
+    if (D->weight_rule != PHX_WEIGHTS_SOFTMAX && D->weight_rule != PHX_WEIGHTS_CPUREF) return PHX_ERR_ARG;
+    if (!D->gate_inp || !D->gate_inp_scale || !D->down_scale || !D->pre_ffw_norm_2 || !D->post_ffw_norm_1 ||
+        !D->post_ffw_norm_2 || !D->gate_up_exps || !D->down_exps)
+        return PHX_ERR_ARG;
+    if (!(D->eps >= 0.0f)) return PHX_ERR_ARG;
+    if (D->n_ff_shared < 0) return PHX_ERR_ARG;
+    if (D->n_ff_shared > 0) {
+        if (!quant_type(D->shared_type)) return PHX_ERR_UNSUPPORTED;
+        if (D->d % block_elems(D->shared_type) != 0 || D->n_ff_shared % 32 != 0) return PHX_ERR_UNSUPPORTED;
+        if (block_elems(D->shared_type) == 256 && D->n_ff_shared % 256 != 0) return PHX_ERR_UNSUPPORTED;
+        if (!D->ffn_norm || !D->ffn_gate || !D->ffn_up || !D->ffn_down) return PHX_ERR_ARG;
+    }
+    return PHX_OK;
+}
+
+int phx_moe_create(int hip_device, phx_moe_ctx** out)
+{
+    if (!out) return PHX_ERR_ARG;
+    *out = nullptr;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n <= 0) return PHX_ERR_DEVICE_LOST;
+    if (hip_device < 0 || hip_device >= n) return PHX_ERR_ARG;
+    phx_moe_ctx* c = new phx_moe_ctx();
+    c->device = hip_device;
+    int rc = PHX_OK;
+    do {
+        hipError_t h;
+        if ((h = hipSetDevice(hip_device)) != hipSuccess) { rc = set_err(c, hip_code(h), "hipSetDevice failed"); break; }
+        if ((h = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking)) != hipSuccess) {
+            rc = set_err(c, hip_code(h), "hipStreamCreate failed");
+            break;
+        }
+        std::vector<float> tab;
+        build_gelu_table(tab);
+        if ((h = hipMalloc((void**)&c->gelu_tab, tab.size() * 4)) != hipSuccess) { rc = set_err(c, hip_code(h), "OOM"); break; }
+        if ((h = hipMemcpy(c->gelu_tab, tab.data(), tab.size() * 4, hipMemcpyHostToDevice)) != hipSuccess) {
+            rc = set_err(c, hip_code(h), "gelu table upload failed");
+            break;
+        }
+        if ((h = hipMalloc((void**)&c->flags, 64)) != hipSuccess) { rc = set_err(c, hip_code(h), "OOM"); break; }
+        if ((h = hipMemset(c->flags, 0, 64)) != hipSuccess) { rc = set_err(c, hip_code(h), "memset failed"); break; }
+    } while (0);
+    if (rc != PHX_OK) {
+        phx_moe_destroy(c);
+        return rc;
+    }
+    *out = c;
+    return PHX_OK;
+}
+
+void phx_moe_destroy(phx_moe_ctx* c)
+{
+    if (!c) return;
+    (void)hipSetDevice(c->device);
+    if (c->stream) (void)hipStreamSynchronize(c->stream);
+    if (c->graph_exec) (void)hipGraphExecDestroy(c->graph_exec);
+    if (c->graph) (void)hipGraphDestroy(c->graph);
+    for (auto& L : c->layers) free_layer(L);
+    for (auto& b : c->ws)
+        if (b.p) (void)hipFree(b.p);
+    for (auto& p : c->pending) {
+        (void)hipEventDestroy(p.a);
+        (void)hipEventDestroy(p.b);
+    }
+    for (auto e : c->pool) (void)hipEventDestroy(e);
+    if (c->gelu_tab) (void)hipFree(c->gelu_tab);
+    if (c->flags) (void)hipFree(c->flags);
+    if (c->stream) (void)hipStreamDestroy(c->stream);
+    delete c;
+}
+
+const char* phx_moe_last_error(const phx_moe_ctx* c) { return c ? c->err.c_str() : "null context"; }
+
+int phx_moe_layer_upload(phx_moe_ctx* c, int layer, const phx_moe_layer_desc* D)
+{
+    if (!c) return PHX_ERR_ARG;
+    int rc = phx_moe_check_desc(D);
+    if (rc) return set_err(c, rc, "layer %d: invalid or unsupported descriptor (%d)", layer, rc);
+    if (layer < 0 || layer > 4096) return set_err(c, PHX_ERR_ARG, "layer index %d out of range", layer);
+    HIPCHK(c, hipSetDevice(c->device));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    if ((int)c->layers.size() <= layer) c->layers.resize(layer + 1);
+    Layer& L = c->layers[layer];
+    free_layer(L);
+    L.desc = *D;
+    const int d = D->d, E = D->n_expert, nf = D->n_ff;
+    // router transposed to [d/4][E][4] (consecutive experts are consecutive lanes)
+    std::vector<float> wt((size_t)d * E);
+    for (int e = 0; e < E; e++)
+        for (int i = 0; i < d; i++) wt[((size_t)(i / 4) * E + e) * 4 + (i % 4)] = D->gate_inp[(size_t)e * d + i];
+    if ((rc = upload_f32(c, wt.data(), wt.size(), &L.wt4))) return rc;
+    if ((rc = upload_f32(c, D->gate_inp_scale, d, &L.gis))) return rc;
+    if ((rc = upload_f32(c, D->down_scale, E, &L.ds))) return rc;
+    if ((rc = upload_f32(c, D->pre_ffw_norm_2, d, &L.pre2))) return rc;
+    if ((rc = upload_f32(c, D->post_ffw_norm_1, d, &L.post1))) return rc;
+    if ((rc = upload_f32(c, D->post_ffw_norm_2, d, &L.post2))) return rc;
+    if (D->post_ffw_norm && (rc = upload_f32(c, D->post_ffw_norm, d, &L.post_ffw))) return rc;
+    if ((rc = upload_q(c, D->gate_up_type, D->gate_up_exps, E, 2 * nf, d, L.gu))) return rc;
+    if ((rc = upload_q(c, D->down_type, D->down_exps, E, d, D->down_cols, L.dn))) return rc;
+    if (D->n_ff_shared > 0) {
+        const int nff = D->n_ff_shared;
+        const int64_t rb = row_bytes(D->shared_type, d);
+        std::vector<uint8_t> fused((size_t)2 * nff * rb);
+        memcpy(fused.data(), D->ffn_gate, (size_t)nff * rb);
+        memcpy(fused.data() + (size_t)nff * rb, D->ffn_up, (size_t)nff * rb);
+        if ((rc = upload_f32(c, D->ffn_norm, d, &L.ffn_norm))) return rc;
+        if ((rc = upload_q(c, D->shared_type, fused.data(), 1, 2 * nff, d, L.sgu))) return rc;
+        if ((rc = upload_q(c, D->shared_type, D->ffn_down, 1, d, round_up(nff, block_elems(D->shared_type)), L.sdn)))
+            return rc;
+    }
+    L.present = true;
+    return PHX_OK;
+}
+
+int phx_moe_ffn(phx_moe_ctx* c, int layer, int T, float* x, const float* shared, float* out, unsigned flags)
+{
+    if (!c) return PHX_ERR_ARG;
+    if (layer < 0 || layer >= (int)c->layers.size() || !c->layers[layer].present)
+        return set_err(c, PHX_ERR_ARG, "layer %d not uploaded", layer);
+    const Layer& L = c->layers[layer];
+    if (T <= 0 || (int64_t)T * L.desc.n_used > 65535) return set_err(c, PHX_ERR_ARG, "T=%d out of range", T);
+    if (!x || !out) return set_err(c, PHX_ERR_ARG, "null x/out");
+    if ((flags & PHX_FLAG_RESIDUAL) && !L.post_ffw) return set_err(c, PHX_ERR_ARG, "residual needs post_ffw_norm");
+    HIPCHK(c, hipSetDevice(c->device));
+    int rc = ensure_workspace(c, L, T);
+    if (rc) return rc;
+    const size_t bytes = (size_t)T * L.desc.d * 4;
+    const bool dev = flags & PHX_FLAG_DEVICE_PTRS;
+    float* xin = x;
+    const float* shin = shared;
+    float* o = out;
+    if (!dev) {
+        xin = wp<float>(c, W_X);
+        o = wp<float>(c, W_OUT);
+        HIPCHK(c, hipMemcpyAsync(xin, x, bytes, hipMemcpyHostToDevice, c->stream));
+        if (shared) {
+            HIPCHK(c, hipMemcpyAsync(wp<float>(c, W_SHARED), shared, bytes, hipMemcpyHostToDevice, c->stream));
+            shin = wp<float>(c, W_SHARED);
+        }
+    }
+    rc = run_layer(c, L, T, xin, shin, o, (flags & PHX_FLAG_RESIDUAL) ? xin : nullptr);
+    if (rc) return rc;
+    c->last_T = T;
+    c->last_layer = layer;
+    if (!dev) {
+        HIPCHK(c, hipMemcpyAsync(out, o, bytes, hipMemcpyDeviceToHost, c->stream));
+        if (flags & PHX_FLAG_RESIDUAL) HIPCHK(c, hipMemcpyAsync(x, xin, bytes, hipMemcpyDeviceToHost, c->stream));
+    }
+    if (!(flags & PHX_FLAG_ASYNC) || !dev) HIPCHK(c, hipStreamSynchronize(c->stream));
+    return PHX_OK;
+}
+
+int phx_moe_get_routing(phx_moe_ctx* c, int32_t* ids, float* weights, int32_t* offsets, int32_t* perm, float* logits)
+{
+    if (!c || c->last_layer < 0) return PHX_ERR_ARG;
+    const phx_moe_layer_desc& D = c->layers[c->last_layer].desc;
+    const size_t n = (size_t)c->last_T * D.n_used;
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    if (ids) HIPCHK(c, hipMemcpy(ids, c->ws[W_IDS].p, n * 4, hipMemcpyDeviceToHost));
+    if (weights) HIPCHK(c, hipMemcpy(weights, c->ws[W_W].p, n * 4, hipMemcpyDeviceToHost));
+    if (offsets) HIPCHK(c, hipMemcpy(offsets, c->ws[W_OFF].p, (size_t)(D.n_expert + 1) * 4, hipMemcpyDeviceToHost));
+    if (perm) HIPCHK(c, hipMemcpy(perm, c->ws[W_PERM].p, n * 4, hipMemcpyDeviceToHost));
+    if (logits)
+        HIPCHK(c, hipMemcpy(logits, c->ws[W_LOGITS].p, (size_t)c->last_T * D.n_expert * 4, hipMemcpyDeviceToHost));
+    return PHX_OK;
+}
+
+int phx_moe_get_intermediates(phx_moe_ctx* c, float* g, float* u, float* yd)
+{
+    if (!c || c->last_layer < 0) return PHX_ERR_ARG;
+    const phx_moe_layer_desc& D = c->layers[c->last_layer].desc;
+    const size_t n = (size_t)c->last_T * D.n_used;
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    if (g) HIPCHK(c, hipMemcpy(g, c->ws[W_G].p, n * D.n_ff * 4, hipMemcpyDeviceToHost));
+    if (u) HIPCHK(c, hipMemcpy(u, c->ws[W_U].p, n * D.n_ff * 4, hipMemcpyDeviceToHost));
+    if (yd) HIPCHK(c, hipMemcpy(yd, c->ws[W_YD].p, n * D.d * 4, hipMemcpyDeviceToHost));
+    return PHX_OK;
+}
+
+int phx_moe_stack_capture(phx_moe_ctx* c, int first, int n_layers, int T)
+{
+    if (!c || n_layers <= 0 || first < 0 || first + n_layers > (int)c->layers.size() || T <= 0)
+        return set_err(c, PHX_ERR_ARG, "bad stack range");
+    HIPCHK(c, hipSetDevice(c->device));
+    int d = c->layers[first].desc.d;
+    for (int l = first; l < first + n_layers; l++) {
+        const Layer& L = c->layers[l];
+        if (!L.present || !L.post_ffw || L.desc.d != d) return set_err(c, PHX_ERR_ARG, "layer %d unusable in a stack", l);
+        if ((int64_t)T * L.desc.n_used > 65535) return set_err(c, PHX_ERR_ARG, "T too large");
+        int rc = ensure_workspace(c, L, T);
+        if (rc) return rc;
+    }
+    if (c->graph_exec) { (void)hipGraphExecDestroy(c->graph_exec); c->graph_exec = nullptr; }
+    if (c->graph) { (void)hipGraphDestroy(c->graph); c->graph = nullptr; }
+    bool prof = c->profiling;
+    c->profiling = false;
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    HIPCHK(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+    int rc = PHX_OK;
+    for (int l = first; l < first + n_layers && rc == PHX_OK; l++)
+        rc = run_layer(c, c->layers[l], T, wp<float>(c, W_X), nullptr, wp<float>(c, W_OUT), wp<float>(c, W_X));
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(c->stream, &g);
+    c->profiling = prof;
+    if (rc) { if (g) (void)hipGraphDestroy(g); return rc; }
+    if (e != hipSuccess) return set_err(c, hip_code(e), "stream capture failed: %s", hipGetErrorString(e));
+    c->graph = g;
+    HIPCHK(c, hipGraphInstantiate(&c->graph_exec, g, nullptr, nullptr, 0));
+    c->graph_T = T;
+    c->graph_first = first;
+    c->graph_n = n_layers;
+    return PHX_OK;
+}
+
+int phx_moe_stack_run(phx_moe_ctx* c, float* x, int T, unsigned flags)
+{
+    if (!c || !c->graph_exec) return set_err(c, PHX_ERR_ARG, "no captured stack");
+    if (T != c->graph_T || !x) return set_err(c, PHX_ERR_ARG, "T=%d differs from the captured %d", T, c->graph_T);
+    HIPCHK(c, hipSetDevice(c->device));
+    const size_t bytes = (size_t)T * c->layers[c->graph_first].desc.d * 4;
+    const bool dev = flags & PHX_FLAG_DEVICE_PTRS;
+    float* xs = wp<float>(c, W_X);
+    HIPCHK(c, hipMemcpyAsync(xs, x, bytes, dev ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, c->stream));
+    HIPCHK(c, hipGraphLaunch(c->graph_exec, c->stream));
+    HIPCHK(c, hipMemcpyAsync(x, xs, bytes, dev ? hipMemcpyDeviceToDevice : hipMemcpyDeviceToHost, c->stream));
+    c->last_T = T;
+    c->last_layer = c->graph_first + c->graph_n - 1;
+    if (!(flags & PHX_FLAG_ASYNC) || !dev) HIPCHK(c, hipStreamSynchronize(c->stream));
+    return PHX_OK;
+}
+
+int phx_moe_sync(phx_moe_ctx* c)
+{
+    if (!c) return PHX_ERR_ARG;
+    HIPCHK(c, hipSetDevice(c->device));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    return PHX_OK;
+}
+
+int phx_moe_dev_alloc(phx_moe_ctx* c, uint64_t bytes, void** ptr)
+{
+    if (!c || !ptr) return PHX_ERR_ARG;
+    HIPCHK(c, hipSetDevice(c->device));
+    HIPCHK(c, hipMalloc(ptr, std::max<uint64_t>(bytes, 1)));
+    return PHX_OK;
+}
+
+int phx_moe_dev_free(phx_moe_ctx* c, void* ptr)
+{
+    if (!c) return PHX_ERR_ARG;
+    HIPCHK(c, hipSetDevice(c->device));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    if (ptr) HIPCHK(c, hipFree(ptr));
+    return PHX_OK;
+}
+
+int phx_moe_memcpy_h2d(phx_moe_ctx* c, void* dst, const void* src, uint64_t bytes)
+{
+    if (!c) return PHX_ERR_ARG;
+    HIPCHK(c, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    return PHX_OK;
+}
+
+int phx_moe_memcpy_d2h(phx_moe_ctx* c, void* dst, const void* src, uint64_t bytes)
+{
+    if (!c) return PHX_ERR_ARG;
+    HIPCHK(c, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, c->stream));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    return PHX_OK;
+}
+
+int phx_moe_profile(phx_moe_ctx* c, int enable)
+{
+    if (!c) return PHX_ERR_ARG;
+    int rc = drain_profile(c);
+    if (rc) return rc;
+    c->profiling = enable != 0;
+    for (int i = 0; i < PHX_K_COUNT; i++) { c->prof_ms[i] = 0; c->prof_n[i] = 0; }
+    return PHX_OK;
+}
+
+int phx_moe_profile_read(phx_moe_ctx* c, double* total_ms, int64_t* launches)
+{
+    if (!c) return PHX_ERR_ARG;
+    int rc = drain_profile(c);
+    if (rc) return rc;
+    for (int i = 0; i < PHX_K_COUNT; i++) {
+        if (total_ms) total_ms[i] = c->prof_ms[i];
+        if (launches) launches[i] = c->prof_n[i];
+    }
+    return PHX_OK;
+}
+
+int phx_moe_selftest(phx_moe_ctx* c, int op, int n, const float* a, const float* b, float* out)
+{
+    if (!c || n <= 0 || !a || !b || !out || op < 0 || op > 7) return PHX_ERR_ARG;
+    HIPCHK(c, hipSetDevice(c->device));
+    float *da = nullptr, *db = nullptr, *dout = nullptr;
+    size_t bytes = (size_t)n * 4;
+    HIPCHK(c, hipMalloc((void**)&da, bytes));
+    HIPCHK(c, hipMalloc((void**)&db, bytes));
+    HIPCHK(c, hipMalloc((void**)&dout, bytes));
+    HIPCHK(c, hipMemcpy(da, a, bytes, hipMemcpyHostToDevice));
+    HIPCHK(c, hipMemcpy(db, b, bytes, hipMemcpyHostToDevice));
+    launch_selftest(c->stream, op, n, da, db, dout, c->gelu_tab);
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    HIPCHK(c, hipMemcpy(out, dout, bytes, hipMemcpyDeviceToHost));
+    (void)hipFree(da);
+    (void)hipFree(db);
+    (void)hipFree(dout);
+    return PHX_OK;
+}
+
+int phx_moe_fallback_count(phx_moe_ctx* c, int* count)
+{
+    if (!c || !count) return PHX_ERR_ARG;
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    HIPCHK(c, hipMemcpy(count, c->flags, 4, hipMemcpyDeviceToHost));
+    return PHX_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,291 @@
+"""ctypes binding of libphxmoe.so (include/phx_moe.h).
+
+Error behaviour follows the reference host: a nonzero status raises the exception the C# side
+maps it to (src/Vulkan.cs:194-208 device lost, src/Gpu.cs:851-852 bad arguments,
+src/GemmaGpu.cs:189-190 unsupported layouts).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+import numpy as np
+
+_HERE = Path(__file__).resolve().parent
+
+
+class PHX:
+    OK, ERR_ARG, ERR_OOM, ERR_UNSUPPORTED, ERR_DEVICE_LOST, ERR_HIP = 0, -1, -2, -3, -4, -5
+    F32, Q4_0, Q8_0, Q4_K, Q6_K = 0, 2, 8, 12, 14
+    WEIGHTS_SOFTMAX, WEIGHTS_CPUREF = 0, 1
+    FLAG_DEVICE_PTRS, FLAG_ASYNC, FLAG_RESIDUAL = 1, 2, 4
+    KINDS = ["prologue", "router", "topk", "dispatch", "gate_up", "requant", "down", "combine", "shared"]
+    MAX_EXPERTS, MAX_USED = 256, 16
+
+
+class MoeError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"phx_moe error {code}: {msg}")
+        self.code = code
+
+
+class ArgumentError(MoeError, ValueError):
+    pass
+
+
+class NotSupportedError(MoeError):
+    pass
+
+
+class GpuDeviceLostError(MoeError):
+    pass
+
+
+def _raise(code: int, msg: str):
+    if code == PHX.ERR_ARG:
+        raise ArgumentError(code, msg)
+    if code == PHX.ERR_UNSUPPORTED:
+        raise NotSupportedError(code, msg)
+    if code == PHX.ERR_DEVICE_LOST:
+        raise GpuDeviceLostError(code, msg)
+    raise MoeError(code, msg)
+
+
+class LayerDesc(C.Structure):
+    """phx_moe_layer_desc (include/phx_moe.h)."""
+
+    _fields_ = [
+        ("d", C.c_int32), ("n_expert", C.c_int32), ("n_used", C.c_int32), ("n_ff", C.c_int32),
+        ("down_cols", C.c_int32), ("eps", C.c_float), ("gate_up_type", C.c_int32), ("down_type", C.c_int32),
+        ("weight_rule", C.c_int32), ("n_ff_shared", C.c_int32), ("shared_type", C.c_int32), ("reserved", C.c_int32),
+        ("gate_inp", C.c_void_p), ("gate_inp_scale", C.c_void_p), ("down_scale", C.c_void_p),
+        ("pre_ffw_norm_2", C.c_void_p), ("post_ffw_norm_1", C.c_void_p), ("post_ffw_norm_2", C.c_void_p),
+        ("gate_up_exps", C.c_void_p), ("down_exps", C.c_void_p), ("ffn_norm", C.c_void_p),
+        ("ffn_gate", C.c_void_p), ("ffn_up", C.c_void_p), ("ffn_down", C.c_void_p), ("post_ffw_norm", C.c_void_p),
+    ]
+
+    @classmethod
+    def from_layer(cls, L: dict) -> "LayerDesc":
+        """Descriptor over the numpy arrays of a layer dict (see synth.make_layer); the dict must
+        outlive every call that uses the descriptor."""
+        def p(name):
+            a = L.get(name)
+            return None if a is None else a.ctypes.data
+        d = cls()
+        d.d, d.n_expert, d.n_used, d.n_ff = L["d"], L["n_expert"], L["n_used"], L["n_ff"]
+        d.down_cols, d.eps = L["down_cols"], L["eps"]
+        d.gate_up_type, d.down_type, d.weight_rule = L["gate_up_type"], L["down_type"], L.get("weight_rule", 0)
+        d.n_ff_shared, d.shared_type = L.get("n_ff_shared", 0), L.get("shared_type", 0)
+        for f in ("gate_inp", "gate_inp_scale", "down_scale", "pre_ffw_norm_2", "post_ffw_norm_1", "post_ffw_norm_2",
+                  "gate_up_exps", "down_exps", "ffn_norm", "ffn_gate", "ffn_up", "ffn_down", "post_ffw_norm"):
+            setattr(d, f, p(f))
+        return d
+
+
+def lib_path() -> Path:
+    return _HERE / "libphxmoe.so"
+
+
+_LIB = None
+
+
+def load_lib():
+    """Load libphxmoe.so (built by __graft_entry__.build()); raise if it is missing."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    path = lib_path()
+    if not path.exists():
+        raise FileNotFoundError(f"{path} is not built: run __graft_entry__.build() (hipcc, gfx950)")
+    lib = C.CDLL(str(path))
+    vp, i32, u32, f32p, i32p = C.c_void_p, C.c_int, C.c_uint, C.POINTER(C.c_float), C.POINTER(C.c_int32)
+    sig = {
+        "phx_moe_create": (i32, [i32, C.POINTER(vp)]),
+        "phx_moe_destroy": (None, [vp]),
+        "phx_moe_last_error": (C.c_char_p, [vp]),
+        "phx_moe_check_desc": (i32, [C.POINTER(LayerDesc)]),
+        "phx_moe_layer_upload": (i32, [vp, i32, C.POINTER(LayerDesc)]),
+        "phx_moe_ffn": (i32, [vp, i32, i32, vp, vp, vp, u32]),
+        "phx_moe_get_routing": (i32, [vp, vp, vp, vp, vp, vp]),
+        "phx_moe_get_intermediates": (i32, [vp, vp, vp, vp]),
+        "phx_moe_stack_capture": (i32, [vp, i32, i32, i32]),
+        "phx_moe_stack_run": (i32, [vp, vp, i32, u32]),
+        "phx_moe_sync": (i32, [vp]),
+        "phx_moe_dev_alloc": (i32, [vp, C.c_uint64, C.POINTER(vp)]),
+        "phx_moe_dev_free": (i32, [vp, vp]),
+        "phx_moe_memcpy_h2d": (i32, [vp, vp, vp, C.c_uint64]),
+        "phx_moe_memcpy_d2h": (i32, [vp, vp, vp, C.c_uint64]),
+        "phx_moe_profile": (i32, [vp, i32]),
+        "phx_moe_profile_read": (i32, [vp, C.POINTER(C.c_double), C.POINTER(C.c_int64)]),
+        "phx_moe_selftest": (i32, [vp, i32, i32, f32p, f32p, f32p]),
+        "phx_moe_fallback_count": (i32, [vp, i32p]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _LIB = lib
+    return lib
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+class DeviceBuffer:
+    def __init__(self, ctx: "MoeContext", nbytes: int):
+        self.ctx, self.nbytes = ctx, nbytes
+        p = C.c_void_p()
+        ctx._check(ctx.lib.phx_moe_dev_alloc(ctx.h, nbytes, C.byref(p)))
+        self.ptr = p.value
+
+    def upload(self, arr: np.ndarray):
+        arr = np.ascontiguousarray(arr)
+        assert arr.nbytes <= self.nbytes
+        self.ctx._check(self.ctx.lib.phx_moe_memcpy_h2d(self.ctx.h, self.ptr, arr.ctypes.data, arr.nbytes))
+
+    def download(self, shape, dtype=np.float32) -> np.ndarray:
+        out = np.empty(shape, dtype=dtype)
+        assert out.nbytes <= self.nbytes
+        self.ctx._check(self.ctx.lib.phx_moe_memcpy_d2h(self.ctx.h, out.ctypes.data, self.ptr, out.nbytes))
+        return out
+
+    def free(self):
+        if self.ptr:
+            self.ctx._check(self.ctx.lib.phx_moe_dev_free(self.ctx.h, self.ptr))
+            self.ptr = None
+
+
+class MoeContext:
+    """A libphxmoe context on one HIP device (GpuDevice + the MoE parts of GemmaGpu)."""
+
+    def __init__(self, device: int = 0):
+        self.lib = load_lib()
+        h = C.c_void_p()
+        rc = self.lib.phx_moe_create(device, C.byref(h))
+        if rc:
+            _raise(rc, f"phx_moe_create({device}) failed")
+        self.h = h.value
+        self.layers: dict[int, dict] = {}
+
+    def close(self):
+        if self.h:
+            self.lib.phx_moe_destroy(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def _check(self, rc: int):
+        if rc:
+            msg = self.lib.phx_moe_last_error(self.h).decode(errors="replace") if self.h else ""
+            _raise(rc, msg)
+
+    # ------------------------------------------------------------------ layers
+    def upload(self, layer: int, L: dict):
+        desc = LayerDesc.from_layer(L)
+        self._check(self.lib.phx_moe_layer_upload(self.h, layer, C.byref(desc)))
+        self.layers[layer] = {k: L[k] for k in ("d", "n_expert", "n_used", "n_ff")}
+
+    def ffn(self, layer: int, x: np.ndarray, shared: np.ndarray | None = None, residual: bool = False) -> np.ndarray:
+        """out[T][d] of one MoE FFN block on host arrays (x is updated in place when residual)."""
+        x = _f32(x)
+        T, d = x.shape
+        out = np.empty_like(x)
+        sh = None if shared is None else _f32(shared)
+        flags = PHX.FLAG_RESIDUAL if residual else 0
+        self._last_layer, self._last_T = layer, T
+        self._check(self.lib.phx_moe_ffn(self.h, layer, T, x.ctypes.data, None if sh is None else sh.ctypes.data,
+                                         out.ctypes.data, flags))
+        return (out, x) if residual else out
+
+    def ffn_device(self, layer: int, T: int, x_ptr: int, shared_ptr, out_ptr: int, flags: int = 0):
+        self._last_layer, self._last_T = layer, T
+        self._check(self.lib.phx_moe_ffn(self.h, layer, T, x_ptr, shared_ptr, out_ptr, flags | PHX.FLAG_DEVICE_PTRS))
+
+    # the reference's three call sites
+    def RecordMoe(self, layer: int, x: np.ndarray, shared: np.ndarray) -> np.ndarray:
+        """src/GemmaGpu.cs:656-669: one decode token, the shared MLP's output given."""
+        return self.ffn(layer, np.reshape(x, (1, -1)), np.reshape(shared, (1, -1)))[0]
+
+    def RecordFfnMoe(self, layer: int, x: np.ndarray) -> np.ndarray:
+        """src/GemmaGpu.cs:683-704: one decode token, the layer's dense shared FFN computed too."""
+        return self.ffn(layer, np.reshape(x, (1, -1)))[0]
+
+    def RecordMoeRows(self, layer: int, x: np.ndarray, shared: np.ndarray | None) -> np.ndarray:
+        """src/GemmaGpu.cs:850-882: T prompt rows (shared: the shared MLP's down outputs)."""
+        return self.ffn(layer, x, shared)
+
+    def routing(self):
+        """(ids [T][k], weights [T][k], offsets [E+1], perm [T*k], logits [T][E]) of the last call."""
+        lay = self._last_dims()
+        T, k, E = self._last_T, lay["n_used"], lay["n_expert"]
+        ids = np.empty((T, k), np.int32)
+        w = np.empty((T, k), np.float32)
+        off = np.empty(E + 1, np.int32)
+        perm = np.empty(T * k, np.int32)
+        logits = np.empty((T, E), np.float32)
+        self._check(self.lib.phx_moe_get_routing(self.h, ids.ctypes.data, w.ctypes.data, off.ctypes.data,
+                                                 perm.ctypes.data, logits.ctypes.data))
+        return ids, w, off, perm, logits
+
+    def intermediates(self):
+        lay = self._last_dims()
+        n = self._last_T * lay["n_used"]
+        g = np.empty((n, lay["n_ff"]), np.float32)
+        u = np.empty_like(g)
+        yd = np.empty((n, lay["d"]), np.float32)
+        self._check(self.lib.phx_moe_get_intermediates(self.h, g.ctypes.data, u.ctypes.data, yd.ctypes.data))
+        return g, u, yd
+
+    def _last_dims(self):
+        return self.layers[self._last_layer]
+
+    # the last call, for routing()/intermediates()
+    _last_T = 0
+    _last_layer = 0
+
+    # ------------------------------------------------------------------ stack (HIP graph)
+    def stack_capture(self, first: int, n_layers: int, T: int):
+        self._check(self.lib.phx_moe_stack_capture(self.h, first, n_layers, T))
+        self._stack_last = first + n_layers - 1
+
+    def stack_run(self, x: np.ndarray) -> np.ndarray:
+        x = _f32(x).copy()
+        self._last_layer, self._last_T = self._stack_last, x.shape[0]
+        self._check(self.lib.phx_moe_stack_run(self.h, x.ctypes.data, x.shape[0], 0))
+        return x
+
+    # ------------------------------------------------------------------ misc
+    def sync(self):
+        self._check(self.lib.phx_moe_sync(self.h))
+
+    def alloc(self, nbytes: int) -> DeviceBuffer:
+        return DeviceBuffer(self, nbytes)
+
+    def profile(self, enable: bool):
+        self._check(self.lib.phx_moe_profile(self.h, 1 if enable else 0))
+
+    def profile_read(self) -> dict:
+        ms = (C.c_double * len(PHX.KINDS))()
+        n = (C.c_int64 * len(PHX.KINDS))()
+        self._check(self.lib.phx_moe_profile_read(self.h, ms, n))
+        return {k: (ms[i], n[i]) for i, k in enumerate(PHX.KINDS)}
+
+    def selftest(self, op: int, a: np.ndarray, b: np.ndarray | None = None) -> np.ndarray:
+        a = _f32(a).ravel()
+        b = np.zeros_like(a) if b is None else _f32(b).ravel()
+        out = np.empty_like(a)
+        fp = C.POINTER(C.c_float)
+        self._check(self.lib.phx_moe_selftest(self.h, op, a.size, a.ctypes.data_as(fp), b.ctypes.data_as(fp),
+                                              out.ctypes.data_as(fp)))
+        return out
+
+    def fallback_count(self) -> int:
+        c = C.c_int32()
+        self._check(self.lib.phx_moe_fallback_count(self.h, C.byref(c)))
+        return c.value
