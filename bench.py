@@ -1,0 +1,214 @@
+#!/usr/bin/env python3
+"""Benchmark of the MoE FFN layer on one MI355X (libphxmoe.so through its C ABI).
+
+Default workload: decode, T=1 token, d=2816, E=128 experts, top-8,
+expert ffn 704, Q4_0 experts plus the dense shared FFN (ffn 2112, Q4_0), synthetic N(0,0.02)
+weights.  One step = one MoE FFN layer applied to the T tokens.  The layer is placed in 8 distinct
+layer slots and the 8 layers are captured as one HIP graph (the reference replays one recorded
+command buffer per decode pass, src/GemmaGpu.cs:544-554); every replay starts from a different
+input, so the experts touched change from replay to replay and the 256 MB MALL cannot serve them.
+
+Prints one JSON line: value = tokens/s through the layer (inputs resident in HBM), a roofline
+object for the dominant kernel (the grouped gate|up product, HIP-event durations from an
+instrumented eager pass of the same workload) and the CPU baseline (the C restatement of the
+reference CPU path timed on this host's cores over a bounded sample).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0  # dense int8 MFMA, MI355X
+
+METRIC = "MoE layer tokens/s; decode HBM GB/s vs peak; prefill MFMA util"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def expert_bytes(L) -> tuple[int, int]:
+    """(gate|up bytes, down bytes) of one expert in GGUF block sizes."""
+    from phoenix_lai_amd import synth as S  # noqa
+    gu = 2 * L["n_ff"] * S.row_bytes(L["gate_up_type"], L["d"])
+    dn = L["d"] * S.row_bytes(L["down_type"], L["n_ff"] if L["down_cols"] == L["n_ff"] else L["down_cols"])
+    if L["down_cols"] != L["n_ff"]:
+        # algorithmic bytes count the unpadded K (the padding is a layout extension)
+        dn = int(dn * L["n_ff"] / L["down_cols"])
+    return gu, dn
+
+
+def cpu_baseline(pkg, L, cfg_name, T, budget_s=12.0):
+    """The oracle (C restatement of GemmaCpu.MoeFfn, row-parallel like Parallel.For) on this host."""
+    from oracle import oracle as orc
+    threads = min(16, os.cpu_count() or 1)
+    S = pkg.synth
+    x = S.make_input(cfg_name, T=max(T, 64), seed=4242, name="cpu.x")
+    orc.moe_block(L, x[:1], nthreads=threads)  # warm-up
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < budget_s and n < x.shape[0]:
+        orc.moe_block(L, x[n:n + 1], nthreads=threads)
+        n += 1
+    dt = time.perf_counter() - t0
+    return {"value": round(n / dt, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{n} tokens of {cfg_name} one at a time (as GemmaCpu.Prefill does), shared FFN included, "
+                      f"{dt:.1f} s, OpenMP over rows with {threads} threads"}
+
+
+def run_decode(args, pkg):
+    S = pkg.synth
+    cfg_name = args.config
+    cfg = S.CONFIGS[cfg_name]
+    T = args.T or cfg["T"]
+    n_slots = args.layers
+    log(f"[bench] generating {cfg_name} layer ...")
+    L = S.make_layer(cfg_name)
+    ctx = pkg.MoeContext(0)
+    log(f"[bench] uploading {n_slots} layer slots ...")
+    for i in range(n_slots):
+        ctx.upload(i, L)
+    d = L["d"]
+    NX = 64
+    xs = S.normal(cfg["idx"] + 7000, "bench.x", (NX, T, d))
+    if L.get("biased"):
+        xs[:, :, -1] = S.BIAS_X
+    xbuf = ctx.alloc(xs.nbytes)
+    xbuf.upload(xs)
+    obuf = ctx.alloc(T * d * 4)
+    xstride = T * d * 4
+
+    # ---- timed region: K layer steps = K / n_slots replays of the n_slots-layer graph
+    ctx.stack_capture(0, n_slots, T)
+    reps = max(1, (args.steps + n_slots - 1) // n_slots)
+    wreps = max(1, (args.warmup + n_slots - 1) // n_slots)
+    for r in range(wreps):
+        ctx.stack_run_device(xbuf.ptr + (r % NX) * xstride, T)
+    ctx.sync()
+    t0 = time.perf_counter()
+    for r in range(reps):
+        ctx.stack_run_device(xbuf.ptr + (r % NX) * xstride, T)
+    ctx.sync()
+    dt = time.perf_counter() - t0
+    steps = reps * n_slots
+    ms_per_step = dt * 1e3 / steps
+    tokens_s = T * steps / dt
+
+    # ---- instrumented eager pass: per-kernel HIP-event durations and touched experts
+    gu_b, dn_b = expert_bytes(L)
+    prof_steps = min(steps, args.prof_steps)
+    ctx.profile(True)
+    distinct = 0
+    for s in range(prof_steps):
+        ctx.ffn_device(s % n_slots, T, xbuf.ptr + (s % NX) * xstride, None, obuf.ptr, pkg.PHX.FLAG_ASYNC)
+        ids = ctx.routing()[0]
+        distinct += len(np.unique(ids))
+    prof = ctx.profile_read()
+    ctx.profile(False)
+    avg_experts = distinct / prof_steps
+    gu_ms = prof["gate_up"][0] / max(1, prof["gate_up"][1])
+    dn_ms = prof["down"][0] / max(1, prof["down"][1])
+    gu_bytes = avg_experts * gu_b
+    achieved = gu_bytes / (gu_ms * 1e-3) / 1e9
+    layer_expert_bytes = avg_experts * (gu_b + dn_b)
+    sh_bytes = 0
+    if L.get("n_ff_shared"):
+        sh_bytes = 3 * L["n_ff_shared"] * S.row_bytes(L["shared_type"], d)
+    router_bytes = L["n_expert"] * d * 4
+
+    # ---- measured streaming-read rate of this box (2 GiB, coalesced 128-bit loads)
+    sbuf = ctx.alloc(2 << 30)
+    sread_ms = ctx.stream_read_ms(sbuf, 10)
+    stream_gbs = (2 << 30) / (sread_ms * 1e-3) / 1e9
+    sbuf.free()
+
+    kernels = {k: {"avg_us": round(v[0] / max(1, v[1]) * 1e3, 2), "launches": v[1]} for k, v in prof.items() if v[1]}
+    line = {
+        "metric": METRIC,
+        "value": round(tokens_s, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": wreps * n_slots,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {
+            "workload": f"{cfg_name}: MoE FFN layer, T={T}, d={d}, E={L['n_expert']}, top-{L['n_used']}, "
+                        f"expert ffn {L['n_ff']}, {qname(L['gate_up_type'])}/{qname(L['down_type'])} experts"
+                        + (f", shared FFN {L['n_ff_shared']} {qname(L['shared_type'])}" if sh_bytes else "")
+                        + f"; {n_slots} layer slots replayed as one HIP graph, x varied per replay",
+            "global_batch": T,
+            "parallelism": "none (1 GPU)",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "gate_up (grouped Q4_0 x Q8_0 row products)" if L["gate_up_type"] == 2 else "gate_up",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "bytes_per_launch": int(gu_bytes),
+            "avg_launch_us": round(gu_ms * 1e3, 3),
+            "per_unit": f"{gu_b} B of gate|up weights per touched expert x {avg_experts:.2f} experts per launch",
+        },
+        "layer": {
+            "expert_bytes_per_step": int(layer_expert_bytes),
+            "expert_gbs": round(layer_expert_bytes / (ms_per_step * 1e-3) / 1e9, 1),
+            "all_bytes_gbs": round((layer_expert_bytes + sh_bytes + router_bytes) / (ms_per_step * 1e-3) / 1e9, 1),
+            "expert_gbs_frac_of_peak": round(layer_expert_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "down_avg_us": round(dn_ms * 1e3, 3),
+            "kernels": kernels,
+            "stream_read_gbs_measured": round(stream_gbs, 1),
+        },
+    }
+    if not args.no_cpu:
+        log("[bench] CPU baseline ...")
+        line["cpu_baseline"] = cpu_baseline(pkg, L, cfg_name, T, args.cpu_seconds)
+    ctx.close()
+    return line
+
+
+def qname(t):
+    return {0: "F32", 2: "Q4_0", 8: "Q8_0", 12: "Q4_K", 14: "Q6_K"}.get(t, str(t))
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=4000, help="layer steps timed (rounded up to whole graph replays)")
+    ap.add_argument("--warmup", type=int, default=400)
+    ap.add_argument("--config", default="c2_decode")
+    ap.add_argument("--T", type=int, default=0)
+    ap.add_argument("--layers", type=int, default=8, help="distinct layer slots in the replayed graph")
+    ap.add_argument("--prof-steps", type=int, default=200)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print(f"bench.py: this build runs on one GPU only (the MoE path shards by experts across GPUs by design, "
+              f"see DESIGN.md); --gpus {args.gpus} is not supported", file=sys.stderr)
+        sys.exit(2)
+    import __graft_entry__ as ge
+    if not ge._built():
+        ge.build()
+    pkg = ge.load_package()
+    line = run_decode(args, pkg)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

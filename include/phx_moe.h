@@ -55,6 +55,8 @@ extern "C" {
 #define PHX_FLAG_DEVICE_PTRS 1u /* x, shared, out are device pointers (no PCIe copies) */
 #define PHX_FLAG_ASYNC 2u       /* return after enqueueing; phx_moe_sync waits */
 #define PHX_FLAG_RESIDUAL 4u    /* also x += rmsnorm(out) * post_ffw_norm (src/GemmaCpu.cs:355-356); x is updated in place */
+#define PHX_FLAG_EXACT_ROUTER 8u /* replay the reference's float router sums for every token (outputs bit-exact
+                                    to the CPU reference) instead of the certified decode router */
 
 typedef struct phx_moe_ctx phx_moe_ctx;
 
@@ -133,6 +135,8 @@ int phx_moe_get_intermediates(phx_moe_ctx* ctx, float* g, float* u, float* yd);
 /* Consecutive layers as one HIP graph (batched decode): each layer does phx_moe_ffn with
  * PHX_FLAG_RESIDUAL on a device-resident x of T rows.  capture once, then run many times. */
 int phx_moe_stack_capture(phx_moe_ctx* ctx, int first_layer, int n_layers, int T);
+/* The same with phx_moe_ffn flags applied to every layer (PHX_FLAG_EXACT_ROUTER). */
+int phx_moe_stack_capture2(phx_moe_ctx* ctx, int first_layer, int n_layers, int T, unsigned flags);
 int phx_moe_stack_run(phx_moe_ctx* ctx, float* x_inout, int T, unsigned flags);
 
 int phx_moe_sync(phx_moe_ctx* ctx);
@@ -165,9 +169,15 @@ int phx_moe_profile_read(phx_moe_ctx* ctx, double* total_ms, int64_t* launches);
  * (int results as their value). */
 int phx_moe_selftest(phx_moe_ctx* ctx, int op, int n, const float* a, const float* b, float* out);
 
-/* Number of row norms, since the context was created, whose double sum of squares could not be
- * certified to round like the reference's sequential sum and were re-summed sequentially. */
-int phx_moe_fallback_count(phx_moe_ctx* ctx, int* count);
+/* Average time (ms) of `iters` coalesced streaming reads of a device buffer: the achievable HBM
+ * read rate that the roofline figures are compared with (no counterpart in the reference). */
+int phx_moe_stream_read(phx_moe_ctx* ctx, const void* buf, uint64_t bytes, int iters, double* ms);
+
+/* Fallbacks since the context was created (counts[2]): [0] row norms whose double sum of squares
+ * could not be certified to round like the reference's sequential sum (re-summed sequentially),
+ * [1] decode-path tokens whose top-k order could not be certified (router re-run as the
+ * reference's float chains). */
+int phx_moe_fallback_count(phx_moe_ctx* ctx, int* counts);
 
 #ifdef __cplusplus
 }

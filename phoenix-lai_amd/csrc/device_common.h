@@ -1,0 +1,241 @@
+// Device helpers shared by the kernels: exact conversions and roundings of the reference CPU path,
+// wave reductions, and the certified double-precision mean of squares of RmsNorm.
+#pragma once
+#include <hip/hip_fp16.h>
+
+#include <type_traits>
+
+#include "phx_internal.h"
+
+namespace phx {
+
+// ------------------------------------------------------------------------------ scalar helpers
+
+// fp16 bits -> float (exact: every binary16 value is a binary32 value; f16 denormals are kept)
+__device__ __forceinline__ float h2f(uint32_t h) { return __half2float(__ushort_as_half((unsigned short)h)); }
+
+// float -> fp16 bits, round to nearest even with subnormals: the rounding rule of Half.FromFloat
+// (src/Half.cs:26-54), written for the device.
+__device__ __forceinline__ uint32_t f2h_bits(float value)
+{
+    uint32_t f = __float_as_uint(value);
+    uint32_t sign = (f >> 16) & 0x8000u;
+    int e = (int)((f >> 23) & 0xFF);
+    uint32_t m = f & 0x7FFFFFu;
+    if (e == 255) return sign | 0x7C00u | (m != 0 ? 0x200u : 0u);
+    int ne = e - 112;
+    if (ne >= 31) return sign | 0x7C00u;
+    if (ne <= 0) {
+        if (ne < -10) return sign;
+        m |= 0x800000u;
+        int sh = 14 - ne;
+        uint32_t hm = m >> sh, rem = m & ((1u << sh) - 1), half = 1u << (sh - 1);
+        if (rem > half || (rem == half && (hm & 1))) hm++;
+        return sign | hm;
+    }
+    uint32_t h = sign | ((uint32_t)ne << 10) | (m >> 13), r = m & 0x1FFFu;
+    if (r > 0x1000u || (r == 0x1000u && (h & 1))) h++;
+    return h;
+}
+
+// C's nearest_int through 1.5*2^23 (src/CpuRefKQuants.cs:45-51)
+__device__ __forceinline__ int nearest_int(float f)
+{
+    float val = f + 12582912.0f;
+    int i = __float_as_int(val);
+    return (i & 0x007fffff) - 0x00400000;
+}
+
+// 1f / (float)sqrt((double)(mean + eps)), the scale expression of CpuRef.RmsNorm (src/CpuRef.cs:188-189)
+__device__ __forceinline__ float rms_scale_from_mean(float mean, float eps)
+{
+    float me = mean + eps;
+    return 1.0f / (float)__dsqrt_rn((double)me);
+}
+
+// GELU of the reference (src/CpuRefGemma.cs:85-92): 0 at or below -10, x at or above 10, otherwise
+// a function of fp16(x) only, read from the 65,536-entry table the runtime builds at context creation.
+__device__ __forceinline__ float gelu_ref(float x, const float* __restrict__ tab)
+{
+    if (x <= -10.0f) return 0.0f;
+    if (x >= 10.0f) return x;
+    return tab[f2h_bits(x)];
+}
+
+// Selection key of a logit: a total order in which NaN ranks below every number, so a parallel
+// argmax agrees on every lane and never loses track of the available experts.  For non-NaN values
+// the order (and the lower-index tie-break applied with it) is the reference's strict '>' scan.
+__device__ __forceinline__ float sel_key(float v) { return v != v ? -INFINITY : v; }
+__device__ __forceinline__ double sel_key(double v) { return v != v ? -INFINITY : v; }
+
+// (key, index) pair `o` beats `b`: higher key, or equal key and lower index; index < 0 is empty.
+template <class F>
+__device__ __forceinline__ bool sel_beats(F ov, int oi, F bv, int bi)
+{
+    return oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi));
+}
+
+// An expert id outside [0, E) can only come from a bug upstream; it is mapped into range so no list
+// write leaves its buffer.
+__device__ __forceinline__ int clamp_id(int e, int E) { return e < 0 ? 0 : (e >= E ? E - 1 : e); }
+
+// ---- DPP reductions (VALU-latency lane exchanges; gfx9 row_bcast for the cross-row steps)
+template <int CTRL, int ROWMASK = 0xf>
+__device__ __forceinline__ int dpp_i(int old, int v)
+{
+    return __builtin_amdgcn_update_dpp(old, v, CTRL, ROWMASK, 0xf, false);
+}
+template <int CTRL, int ROWMASK = 0xf>
+__device__ __forceinline__ float dpp_f(float old, float v)
+{
+    return __int_as_float(dpp_i<CTRL, ROWMASK>(__float_as_int(old), __float_as_int(v)));
+}
+template <int CTRL, int ROWMASK = 0xf>
+__device__ __forceinline__ double dpp_d(double old, double v)
+{
+    const long long o = __double_as_longlong(old), x = __double_as_longlong(v);
+    const int lo = dpp_i<CTRL, ROWMASK>((int)o, (int)x);
+    const int hi = dpp_i<CTRL, ROWMASK>((int)(o >> 32), (int)(x >> 32));
+    return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
+
+// Sum of a 16-lane row, in every lane of the row (quad swaps, half mirror, mirror).
+template <class F>
+__device__ __forceinline__ F row_sum(F v)
+{
+    if constexpr (sizeof(F) == 8) {
+        v += dpp_d<0xb1>(0.0, v);
+        v += dpp_d<0x4e>(0.0, v);
+        v += dpp_d<0x141>(0.0, v);
+        v += dpp_d<0x140>(0.0, v);
+    } else if constexpr (std::is_same<F, float>::value) {
+        v += dpp_f<0xb1>(0.0f, v);
+        v += dpp_f<0x4e>(0.0f, v);
+        v += dpp_f<0x141>(0.0f, v);
+        v += dpp_f<0x140>(0.0f, v);
+    } else {
+        v += dpp_i<0xb1>(0, v);
+        v += dpp_i<0x4e>(0, v);
+        v += dpp_i<0x141>(0, v);
+        v += dpp_i<0x140>(0, v);
+    }
+    return v;
+}
+
+__device__ __forceinline__ float row_max(float v)
+{
+    v = fmaxf(v, dpp_f<0xb1>(v, v));
+    v = fmaxf(v, dpp_f<0x4e>(v, v));
+    v = fmaxf(v, dpp_f<0x141>(v, v));
+    v = fmaxf(v, dpp_f<0x140>(v, v));
+    return v;
+}
+
+// Sum over the 64 lanes, the same value returned to every lane: rows are summed, rows 0+1 and 2+3
+// combined through row_bcast15, then row_bcast31; lane 63 holds the total.
+__device__ __forceinline__ double wave_sum_dpp(double v)
+{
+    v = row_sum(v);
+    v += dpp_d<0x142, 0xa>(0.0, v);
+    v += dpp_d<0x143, 0xc>(0.0, v);
+    const long long t = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_readlane((int)t, 63), hi = __builtin_amdgcn_readlane((int)(t >> 32), 63);
+    return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
+
+// Sum / max over each 32-lane half (lanes 0-31 and 32-63), returned to the lanes of that half.
+__device__ __forceinline__ int half_sum_i(int v)
+{
+    v = row_sum(v);
+    v += dpp_i<0x142, 0xa>(0, v);
+    const int a = __builtin_amdgcn_readlane(v, 31), b = __builtin_amdgcn_readlane(v, 63);
+    return (threadIdx.x & 32) ? b : a;
+}
+
+__device__ __forceinline__ float half_max_f(float v)
+{
+    v = row_max(v);
+    v = fmaxf(v, dpp_f<0x142, 0xa>(v, v));
+    const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 31));
+    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+    return (threadIdx.x & 32) ? b : a;
+}
+
+// sum over the 64 lanes of a wave (butterfly: every lane ends with the same value)
+__device__ __forceinline__ double wave_sum_d(double v)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ __forceinline__ double wave_max_d(double v)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmax(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// Mean of squares of one row as CpuRef.RmsNorm rounds it: (float)(sum / n) with sum the double sum of
+// x_i^2 in index order (src/CpuRef.cs:186-188).  A parallel double sum differs from the sequential
+// one by at most (n + per + depth) * 2^-53 * sum (all terms are non-negative); when both ends of
+// that interval give the same float the result is certain, otherwise one thread re-sums
+// sequentially (rare; counted in fallbacks[0]).  Block-level: NT threads, red >= NT/64 + 1 doubles.
+template <int NT>
+__device__ float mean_sq_cert(const float* x, int n, double* red, int* fallbacks)
+{
+    constexpr int NW = NT / 64;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    double s = 0.0;
+    for (int i = tid; i < n; i += NT) {
+        double v = (double)x[i];
+        s += v * v;
+    }
+    s = wave_sum_dpp(s);
+    if (lane == 0) red[wave] = s;
+    __syncthreads();
+    double S = 0.0;
+    for (int w = 0; w < NW; w++) S += red[w];
+    const int per = (n + NT - 1) / NT;
+    const double B = ((double)n + per + 64.0) * 0x1p-53 * S * 2.0;
+    const float lo = (float)((S - B) / (double)n), hi = (float)((S + B) / (double)n);
+    float mean = lo;
+    if (lo != hi) {
+        __syncthreads();
+        if (tid == 0) {
+            double q = 0.0;
+            for (int i = 0; i < n; i++) q += (double)x[i] * (double)x[i];
+            red[NW] = q;
+            if (fallbacks) atomicAdd(fallbacks, 1);
+        }
+        __syncthreads();
+        mean = (float)(red[NW] / (double)n);
+    }
+    __syncthreads();
+    return mean;
+}
+
+// The same for one wave over contiguous per-lane chunks (no barriers).
+__device__ __forceinline__ float mean_sq_cert_wave(const float* x, int n, int* fallbacks)
+{
+    const int lane = threadIdx.x & 63;
+    const int per = (n + 63) / 64, c0 = min(n, lane * per), c1 = min(n, c0 + per);
+    double s = 0.0;
+    for (int i = c0; i < c1; i++) {
+        double v = (double)x[i];
+        s += v * v;
+    }
+    const double S = wave_sum_dpp(s);
+    const double B = ((double)n + per + 64.0) * 0x1p-53 * S * 2.0;
+    const float lo = (float)((S - B) / (double)n), hi = (float)((S + B) / (double)n);
+    if (lo == hi) return lo;
+    double q = 0.0;
+    if (lane == 0) {
+        for (int i = 0; i < n; i++) q += (double)x[i] * (double)x[i];
+        if (fallbacks) atomicAdd(fallbacks, 1);
+    }
+    q = __shfl(q, 0, 64);
+    return (float)(q / (double)n);
+}
+
+}  // namespace phx

@@ -4,101 +4,9 @@
 // in that order (per-row block chains, the router's dot chain, the rank-ordered combine), and the
 // double-precision sums of squares of RmsNorm are reproduced through a certified error bound with
 // an exact sequential fallback.
-#include "phx_internal.h"
-
-#include <hip/hip_fp16.h>
+#include "device_common.h"
 
 namespace phx {
-
-// ------------------------------------------------------------------------------ scalar helpers
-
-// fp16 bits -> float (exact: every binary16 value is a binary32 value; f16 denormals are kept)
-__device__ __forceinline__ float h2f(uint32_t h) { return __half2float(__ushort_as_half((unsigned short)h)); }
-
-// float -> fp16 bits, round to nearest even with subnormals: the rounding rule of Half.FromFloat
-// (src/Half.cs:26-54), written for the device.
-__device__ __forceinline__ uint32_t f2h_bits(float value)
-{
-    uint32_t f = __float_as_uint(value);
-    uint32_t sign = (f >> 16) & 0x8000u;
-    int e = (int)((f >> 23) & 0xFF);
-    uint32_t m = f & 0x7FFFFFu;
-    if (e == 255) return sign | 0x7C00u | (m != 0 ? 0x200u : 0u);
-    int ne = e - 112;
-    if (ne >= 31) return sign | 0x7C00u;
-    if (ne <= 0) {
-        if (ne < -10) return sign;
-        m |= 0x800000u;
-        int sh = 14 - ne;
-        uint32_t hm = m >> sh, rem = m & ((1u << sh) - 1), half = 1u << (sh - 1);
-        if (rem > half || (rem == half && (hm & 1))) hm++;
-        return sign | hm;
-    }
-    uint32_t h = sign | ((uint32_t)ne << 10) | (m >> 13), r = m & 0x1FFFu;
-    if (r > 0x1000u || (r == 0x1000u && (h & 1))) h++;
-    return h;
-}
-
-// C's nearest_int through 1.5*2^23 (src/CpuRefKQuants.cs:45-51)
-__device__ __forceinline__ int nearest_int(float f)
-{
-    float val = f + 12582912.0f;
-    int i = __float_as_int(val);
-    return (i & 0x007fffff) - 0x00400000;
-}
-
-// 1f / (float)sqrt((double)(mean + eps)), the scale expression of CpuRef.RmsNorm (src/CpuRef.cs:188-189)
-__device__ __forceinline__ float rms_scale_from_mean(float mean, float eps)
-{
-    float me = mean + eps;
-    return 1.0f / (float)__dsqrt_rn((double)me);
-}
-
-// GELU of the reference (src/CpuRefGemma.cs:85-92): 0 at or below -10, x at or above 10, otherwise
-// a function of fp16(x) only, read from the 65,536-entry table the runtime builds at context creation.
-__device__ __forceinline__ float gelu_ref(float x, const float* __restrict__ tab)
-{
-    if (x <= -10.0f) return 0.0f;
-    if (x >= 10.0f) return x;
-    return tab[f2h_bits(x)];
-}
-
-// Mean of squares of one row as CpuRef.RmsNorm rounds it: (float)(sum / n) with sum the double sum of
-// x_i^2 in index order.  A parallel double sum differs from the sequential one by at most
-// (n + per + depth) * 2^-53 * sum (all terms are non-negative); when both ends of that interval give
-// the same float the result is certain, otherwise thread 0 re-sums sequentially (rare, counted).
-template <int NT>
-__device__ float mean_sq_cert(const float* x, int n, double* red, int* fallbacks)
-{
-    const int tid = threadIdx.x;
-    double s = 0.0;
-    for (int i = tid; i < n; i += NT) {
-        double v = (double)x[i];
-        s += v * v;
-    }
-    red[tid] = s;
-    __syncthreads();
-    for (int w = NT / 2; w > 0; w >>= 1) {
-        if (tid < w) red[tid] += red[tid + w];
-        __syncthreads();
-    }
-    double S = red[0];
-    __syncthreads();
-    int per = (n + NT - 1) / NT;
-    double B = ((double)n + per + 64.0) * 0x1p-53 * S * 2.0;
-    float lo = (float)((S - B) / (double)n), hi = (float)((S + B) / (double)n);
-    if (lo == hi) return lo;
-    if (tid == 0) {
-        double q = 0.0;
-        for (int i = 0; i < n; i++) q += (double)x[i] * (double)x[i];
-        red[0] = q;
-        if (fallbacks) atomicAdd(fallbacks, 1);
-    }
-    __syncthreads();
-    float mean = (float)(red[0] / (double)n);
-    __syncthreads();
-    return mean;
-}
 
 // ------------------------------------------------------------------------------ activation quantizers
 
@@ -271,20 +179,23 @@ __global__ __launch_bounds__(64) void k_topk(int E, int k, int rule, const float
         avail[q] = e < E;
         v[q] = avail[q] ? logits[(int64_t)t * E + e] : 0.0f;
     }
+    float key[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) key[q] = sel_key(v[q]);
     for (int j = 0; j < k; j++) {
-        float bv = 0.0f;
+        float bk = 0.0f, bv = 0.0f;
         int bi = -1;
 #pragma unroll
         for (int q = 0; q < 4; q++)
-            if (avail[q] && (bi < 0 || v[q] > bv)) { bv = v[q]; bi = lane + 64 * q; }
+            if (avail[q] && sel_beats(key[q], lane + 64 * q, bk, bi)) { bk = key[q]; bv = v[q]; bi = lane + 64 * q; }
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) {
-            float ov = __shfl_xor(bv, off, 64);
+            float ok = __shfl_xor(bk, off, 64), ov = __shfl_xor(bv, off, 64);
             int oi = __shfl_xor(bi, off, 64);
-            if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) { bv = ov; bi = oi; }
+            if (sel_beats(ok, oi, bk, bi)) { bk = ok; bv = ov; bi = oi; }
         }
         if (bi >= 0 && lane == (bi & 63)) avail[bi >> 6] = false;
-        if (lane == 0) { sel[j] = bv; sid[j] = bi; }
+        if (lane == 0) { sel[j] = bv; sid[j] = bi < 0 ? 0 : bi; }
     }
     __syncthreads();
     if (lane == 0) {
@@ -336,7 +247,7 @@ __global__ __launch_bounds__(256) void k_dispatch(int n, int E, int A, const int
     __syncthreads();
     const int a0 = tid * cs, a1 = min(n, a0 + cs);
     if (tid < nch)
-        for (int a = a0; a < a1; a++) hist[ids[a] * nch + tid]++;
+        for (int a = a0; a < a1; a++) hist[clamp_id(ids[a], E) * nch + tid]++;
     __syncthreads();
     if (tid < E) {
         int run = 0;
@@ -364,7 +275,7 @@ __global__ __launch_bounds__(256) void k_dispatch(int n, int E, int A, const int
     for (int e = tid; e <= E; e += 256) offsets[e] = toff[e];
     if (tid < nch)
         for (int a = a0; a < a1; a++) {
-            int e = ids[a];
+            int e = clamp_id(ids[a], E);
             int pos = toff[e] + hist[e * nch + tid];
             hist[e * nch + tid]++;
             perm[pos] = a;
@@ -408,7 +319,24 @@ struct GroupArgs {
     float* out0;
     float* out1;
     int split, out_stride;
+    bool paired;
 };
+
+// Output of lane `lane` of row group rgi for assignment row a: natural row order, or for a paired
+// gate|up matrix lanes 0-31 = gate output 32 rgi + lane, lanes 32-63 = the matching up output.
+__device__ __forceinline__ void store_row(const GroupArgs& g, int rgi, int lane, int64_t a, float v)
+{
+    if (g.paired) {
+        const int j = rgi * 32 + (lane & 31);
+        if (j < g.split) (lane < 32 ? g.out0 : g.out1)[a * g.out_stride + j] = v;
+    } else {
+        const int row = rgi * 64 + lane;
+        if (row < g.rows) {
+            if (row < g.split) g.out0[a * g.out_stride + row] = v;
+            else g.out1[a * g.out_stride + row - g.split] = v;
+        }
+    }
+}
 
 template <int TYPE, int A>
 __global__ __launch_bounds__(256) void k_grouped_q(GroupArgs g)
@@ -462,17 +390,9 @@ __global__ __launch_bounds__(256) void k_grouped_q(GroupArgs g)
             }
         }
     }
-    const int row = rgi * 64 + lane;
-    if (row < g.rows) {
 #pragma unroll
-        for (int i = 0; i < A; i++) {
-            if (i < tl.cnt) {
-                const int64_t a = g.perm[tl.start + i];
-                if (row < g.split) g.out0[a * g.out_stride + row] = acc[i];
-                else g.out1[a * g.out_stride + row - g.split] = acc[i];
-            }
-        }
-    }
+    for (int i = 0; i < A; i++)
+        if (i < tl.cnt) store_row(g, rgi, lane, g.perm[tl.start + i], acc[i]);
 }
 
 // K-quant rows: DotK (src/CpuRefKQuants.cs:177-212) per (row, assignment): per super-block the eight
@@ -588,18 +508,13 @@ __global__ __launch_bounds__(256) void k_grouped_k(GroupArgs g)
             }
         }
     }
-    const int row = rgi * 64 + lane;
-    if (row < g.rows) {
 #pragma unroll
-        for (int i = 0; i < A; i++) {
-            if (i < tl.cnt) {
-                float s = sumf[i];
+    for (int i = 0; i < A; i++) {
+        if (i < tl.cnt) {
+            float s = sumf[i];
 #pragma unroll
-                for (int l = 0; l < 8; l++) s += sums[i][l];
-                const int64_t a = g.perm[tl.start + i];
-                if (row < g.split) g.out0[a * g.out_stride + row] = s;
-                else g.out1[a * g.out_stride + row - g.split] = s;
-            }
+            for (int l = 0; l < 8; l++) s += sums[i][l];
+            store_row(g, rgi, lane, g.perm[tl.start + i], s);
         }
     }
 }
@@ -624,6 +539,7 @@ void launch_grouped(hipStream_t st, const QMat& w, Act act, const Tile* tiles, c
     g.out1 = out1;
     g.split = split;
     g.out_stride = out_stride;
+    g.paired = w.paired;
     dim3 grid(max_tiles, (w.rg + 3) / 4);
     if (A != 4) A = 4;  // the tile size the dispatch used; one instantiation for now
     switch (w.type) {
@@ -697,6 +613,26 @@ void launch_combine(hipStream_t st, int T, int d, int k, float eps, const float*
 {
     hipLaunchKernelGGL(k_combine, dim3(T), dim3(256), (size_t)2 * d * sizeof(float), st, d, k, eps, yd, w, shared, post1,
                        post2, out, xres, post_ffw, flags);
+}
+
+// ------------------------------------------------------------------------------ streaming read
+// Reads `n16` 16-byte words with coalesced 128-bit loads and folds them into one word per thread
+// (written only when it equals a sentinel, so the loads cannot be elided): the achievable HBM read
+// rate of the box, the denominator check of the roofline.
+__global__ __launch_bounds__(256) void k_stream_read(const uint4* __restrict__ src, int64_t n16, uint32_t* sink)
+{
+    uint32_t acc = 0;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride) {
+        uint4 v = src[i];
+        acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+    if (acc == 0x9E3779B9u) sink[0] = acc;
+}
+
+void launch_stream_read(hipStream_t st, const void* src, int64_t bytes, uint32_t* sink)
+{
+    hipLaunchKernelGGL(k_stream_read, dim3(256 * 8), dim3(256), 0, st, (const uint4*)src, bytes / 16, sink);
 }
 
 // ------------------------------------------------------------------------------ arithmetic self-test

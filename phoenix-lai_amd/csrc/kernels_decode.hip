@@ -1,0 +1,677 @@
+// Decode-shaped MoE FFN kernels (a few tokens, T <= 16): four launches per layer.
+//   k_route_dec    router logits (certified), the quantized expert / shared-FFN inputs, then in the
+//                  last workgroup: top-k, weights and the expert lists
+//   k_dec_mm<0>    gate|up of the routed experts and of the shared FFN; epilogue: gelu(g) * u and
+//                  its Q8_0 quantization (the down input)
+//   k_dec_mm<1>    down of the routed experts and of the shared FFN
+//   k_combine_dec  rank-ordered combine, branch norms, optional residual
+// Arithmetic follows the reference CPU path (src/GemmaCpu.cs:376-422) as in kernels.hip; the router
+// logits are the one quantity certified rather than replayed (see k_route_dec).
+#include <algorithm>
+
+#include "device_common.h"
+
+namespace phx {
+
+// Q8_0 of 32 values held one per lane of a 32-lane half (CpuRef.QuantizeQ8_0, src/CpuRef.cs:49-62):
+// returns q; *dval and *sum (fp16 scale value and block sum) are valid in every lane of the half.
+__device__ __forceinline__ int q8_0_half(float x, float* dval, int* sum)
+{
+    const float amax = half_max_f(fabsf(x));
+    const float dd = amax / 127.0f;
+    const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
+    const int q = (int)roundf(x * id);
+    *dval = h2f(f2h_bits(dd));
+    *sum = half_sum_i(q);
+    return q;
+}
+
+// ------------------------------------------------------------------------------ router (decode)
+// One wave per (token, expert).  The reference logit is the sequential float sum of the rounded
+// products p_i = fl(W[e][i] * m_i) (src/GemmaCpu.cs:390-395).  The wave forms the same p_i, sums
+// them in double (L), and bounds the reference's accumulated rounding:
+//   |S_ref - L| <= 2^-24 * sum_k |S_k| / (1 - n 2^-24)  (+ slack for the double arithmetic),
+// S_k the exact prefix sums (a wave scan).  The last workgroup ranks the experts by L and accepts
+// the order if every chosen expert's interval lies strictly above every later expert's; otherwise
+// the experts whose intervals reach the chosen ones are recomputed as the reference's float chains
+// and ranked exactly.  Ids are therefore always the reference's; weights use (float)L for certified
+// tokens (within ~1e-6 of the reference's logit) and the exact logits otherwise.
+// The same launch also writes the Q8_0 expert input n = x * scale * pre_ffw_norm_2 (and the shared
+// FFN input with ffn_norm): workgroup (bx, t) quantizes every (8 * gridDim.x)-th 32-block of token t.
+struct RouteDecArgs {
+    int T, d, E, k, rule, A, max_tiles;
+    float eps;
+    const float* x;
+    const float* W;       // [E][d] row-major (ffn_gate_inp.weight)
+    const float* gis;     // ffn_gate_inp.scale
+    const float* ds;      // ffn_down_exps.scale
+    const float* pre2;    // pre_ffw_norm_2
+    const float* fnorm;   // ffn_norm (shared FFN input) or null
+    Act act_gu, act_sh;
+    double* Lb;           // [T][E]
+    double* Bb;           // [T][E]
+    int* counter;         // zero between launches
+    int* ids;
+    float* w;
+    float* logits;
+    int* offsets;
+    int* perm;
+    Tile* tiles;
+    int* ntiles;
+    int* flags;           // [0] norm fallbacks, [1] router fallbacks
+};
+
+constexpr int RT_PER = 64;        // elements per lane (d <= 4096)
+
+__device__ __forceinline__ double ld_agent(const double* p)
+{
+    unsigned long long v = __hip_atomic_load((const unsigned long long*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return __longlong_as_double((long long)v);
+}
+
+__device__ __forceinline__ void st_agent(double* p, double v)
+{
+    __hip_atomic_store((unsigned long long*)p, (unsigned long long)__double_as_longlong(v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// exact reference logit of expert e for token t (src/GemmaCpu.cs:389-395)
+__device__ float exact_logit(const RouteDecArgs& a, int t, int e, float rinv, float sc)
+{
+    const float* xr = a.x + (int64_t)t * a.d;
+    const float* wr = a.W + (int64_t)e * a.d;
+    float s = 0.0f;
+    for (int i = 0; i < a.d; i += 4) {
+        const float4 xv = *(const float4*)(xr + i), gv = *(const float4*)(a.gis + i), wv = *(const float4*)(wr + i);
+        s += wv.x * (xv.x * rinv * sc * gv.x);
+        s += wv.y * (xv.y * rinv * sc * gv.y);
+        s += wv.z * (xv.z * rinv * sc * gv.z);
+        s += wv.w * (xv.w * rinv * sc * gv.w);
+    }
+    return s;
+}
+
+__global__ __launch_bounds__(256) void k_route_dec(RouteDecArgs a)
+{
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, tid = threadIdx.x;
+    const int e = blockIdx.x * 4 + wave, t = blockIdx.y;
+    extern __shared__ __align__(16) unsigned char rsm[];
+    __shared__ int s_last, s_bad[16];
+    __shared__ double red[8];
+    __shared__ int s_ids[256];
+    __shared__ int s_cnt[PHX_MAX_EXPERTS_DEV + 1], s_off[PHX_MAX_EXPERTS_DEV + 1], s_tb[PHX_MAX_EXPERTS_DEV + 1];
+    const float sc = 1.0f / (float)__dsqrt_rn((double)a.d);
+    const float* xr = a.x + (int64_t)t * a.d;
+    const int d = a.d;
+
+    // ---- x, the router scale and this workgroup's 4 router rows into LDS (coalesced 128-bit loads)
+    float* sx = (float*)rsm;
+    float* sg = sx + d;
+    float* sw = sg + d;  // [4][d]
+    {
+        const float4* x4 = (const float4*)xr;
+        const float4* g4 = (const float4*)a.gis;
+        for (int i = tid; i < d / 4; i += 256) {
+            ((float4*)sx)[i] = x4[i];
+            ((float4*)sg)[i] = g4[i];
+        }
+        for (int w = 0; w < 4; w++) {
+            const int ew = min(blockIdx.x * 4 + w, a.E - 1);
+            const float4* w4 = (const float4*)(a.W + (int64_t)ew * d);
+            for (int i = tid; i < d / 4; i += 256) ((float4*)(sw + w * d))[i] = w4[i];
+        }
+    }
+    __syncthreads();
+    // ---- the lane's contiguous chunk (d % 256 == 0: per = d / 64, a multiple of 4)
+    const int per = d / 64, c0 = lane * per;
+    float xv[RT_PER], gv[RT_PER], wv[RT_PER];
+#pragma unroll
+    for (int j = 0; j < RT_PER; j += 4) {
+        if (j < per) {
+            const float4 a4 = *(const float4*)(sx + c0 + j), b4 = *(const float4*)(sg + c0 + j),
+                         c4 = *(const float4*)(sw + wave * d + c0 + j);
+            xv[j] = a4.x; xv[j + 1] = a4.y; xv[j + 2] = a4.z; xv[j + 3] = a4.w;
+            gv[j] = b4.x; gv[j + 1] = b4.y; gv[j + 2] = b4.z; gv[j + 3] = b4.w;
+            wv[j] = c4.x; wv[j + 1] = c4.y; wv[j + 2] = c4.z; wv[j + 3] = c4.w;
+        } else {
+            xv[j] = xv[j + 1] = xv[j + 2] = xv[j + 3] = 0.0f;
+            gv[j] = gv[j + 1] = gv[j + 2] = gv[j + 3] = 0.0f;
+            wv[j] = wv[j + 1] = wv[j + 2] = wv[j + 3] = 0.0f;
+        }
+    }
+    const int c1 = c0 + per;
+    // certified mean of squares of x (every wave of the token computes the same value)
+    double s = 0.0;
+#pragma unroll
+    for (int j = 0; j < RT_PER; j++) {
+        const double v = (double)xv[j];
+        s += v * v;
+    }
+    const double S = wave_sum_dpp(s);
+    const double Bs = ((double)a.d + per + 64.0) * 0x1p-53 * S * 2.0;
+    float mean = (float)((S - Bs) / (double)a.d);
+    if (mean != (float)((S + Bs) / (double)a.d)) {
+        double q = 0.0;
+        if (lane == 0) {
+            for (int i = 0; i < a.d; i++) q += (double)sx[i] * (double)sx[i];
+            if (a.flags) atomicAdd(a.flags, 1);
+        }
+        mean = (float)(__shfl(q, 0, 64) / (double)a.d);
+    }
+    const float rinv = rms_scale_from_mean(mean, a.eps);  // also the RmsNorm scale of x
+    if (e < a.E) {
+        double loc = 0.0, P = 0.0;
+#pragma unroll
+        for (int j = 0; j < RT_PER; j++) {
+            const float m = xv[j] * rinv * sc * gv[j];
+            const float p = wv[j] * m;
+            xv[j] = p;
+            loc += (double)p;
+            P += fabs((double)p);
+        }
+        double inc = loc;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const double y = __shfl_up(inc, o, 64);
+            if (lane >= o) inc += y;
+        }
+        double acc = __shfl_up(inc, 1, 64);
+        if (lane == 0) acc = 0.0;
+        double A = 0.0;
+#pragma unroll
+        for (int j = 0; j < RT_PER; j++) {
+            if (c0 + j < c1) {
+                acc += (double)xv[j];
+                A += fabs(acc);
+            }
+        }
+        A = wave_sum_dpp(A);
+        P = wave_sum_dpp(P);
+        const double L = __shfl(inc, 63, 64);
+        if (lane == 0) {
+            st_agent(&a.Lb[(int64_t)t * a.E + e], L);
+            st_agent(&a.Bb[(int64_t)t * a.E + e], 0x1p-24 * A * 1.001 + 0x1p-45 * P);
+        }
+    }
+
+    // ---- quantized expert input (and shared FFN input): one 32-lane half per 32-block
+    {
+        const int nbK = a.d / 32, half = tid >> 5, l32 = tid & 31;
+        for (int b = blockIdx.x * 8 + half; b < nbK; b += gridDim.x * 8) {
+            const int i = b * 32 + l32;
+            for (int which = 0; which < 2; which++) {
+                const float* nw = which ? a.fnorm : a.pre2;
+                if (!nw) continue;
+                const Act& act = which ? a.act_sh : a.act_gu;
+                float dval;
+                int sum;
+                const int q = q8_0_half(sx[i] * rinv * nw[i], &dval, &sum);
+                act.q[(int64_t)t * act.qstride + i] = (int8_t)q;
+                if (l32 == 0) {
+                    act.d[(int64_t)t * act.dstride + b] = dval;
+                    act.s[(int64_t)t * act.sstride + b] = sum;
+                }
+            }
+        }
+    }
+
+    // ---- hand-off to the last workgroup
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) {
+        const int total = gridDim.x * gridDim.y;
+        const int prev = __hip_atomic_fetch_add(a.counter, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = prev == total - 1;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+
+    const int TE = a.T * a.E;
+    double* sL = (double*)rsm;
+    double* sB = sL + kRouteMaxTE;
+    short* s_rank = (short*)(sB + kRouteMaxTE);
+    char* s_amb = (char*)(s_rank + kRouteMaxTE);
+    for (int i = tid; i < TE; i += 256) {
+        sL[i] = ld_agent(&a.Lb[i]);
+        sB[i] = ld_agent(&a.Bb[i]);
+    }
+    if (tid < 16) s_bad[tid] = 0;
+    __syncthreads();
+    // rank of every (token, expert) under (L desc, index asc); NaN ranks last
+    for (int i = tid; i < TE; i += 256) {
+        const int tt = i / a.E, ex = i - tt * a.E;
+        const double my = sel_key(sL[i]);
+        int r = 0;
+        const double* row = sL + tt * a.E;
+#pragma unroll 16
+        for (int b = 0; b < a.E; b++) r += sel_beats(sel_key(row[b]), b, my, ex);
+        s_rank[i] = (short)r;
+        if (!(isfinite(sL[i]) && isfinite(sB[i]))) s_bad[tt] = 1;
+    }
+    __syncthreads();
+    // certification: each chosen expert's lower end above every later-ranked expert's upper end
+    for (int i = tid; i < TE; i += 256) {
+        const int tt = i / a.E;
+        const int r = s_rank[i];
+        if (r < a.k) {
+            const double lo = sL[i] - sB[i];
+            bool ok = true;
+#pragma unroll 16
+            for (int b = 0; b < a.E; b++) {
+                const int j = tt * a.E + b;
+                ok &= !(s_rank[j] > r) || lo > sL[j] + sB[j];
+            }
+            if (!ok) s_bad[tt] = 1;
+        }
+    }
+    __syncthreads();
+    // uncertified tokens: exact chains for every expert that can reach the chosen ones
+    for (int tt = 0; tt < a.T; tt++) {
+        if (!s_bad[tt]) continue;  // uniform: an LDS value read after a barrier
+        if (tid == 0) atomicAdd(&a.flags[1], 1);
+        const float rinv_t = rms_scale_from_mean(mean_sq_cert<256>(a.x + (int64_t)tt * a.d, a.d, red, a.flags), a.eps);
+        double minlo = INFINITY;
+        bool nonfinite = false;
+        for (int b = 0; b < a.E; b++) {
+            const int j = tt * a.E + b;
+            if (!(isfinite(sL[j]) && isfinite(sB[j]))) nonfinite = true;
+            if (s_rank[j] < a.k) minlo = fmin(minlo, sL[j] - sB[j]);
+        }
+        __syncthreads();
+        for (int b = tid; b < a.E; b += 256) {
+            const int j = tt * a.E + b;
+            const bool amb = nonfinite || s_rank[j] < a.k || sL[j] + sB[j] >= minlo;
+            s_amb[j] = amb;
+            if (amb) sL[j] = (double)exact_logit(a, tt, b, rinv_t, sc);  // the others cannot be chosen
+        }
+        __syncthreads();
+        for (int b = tid; b < a.E; b += 256) {
+            const int j = tt * a.E + b;
+            const double my = s_amb[j] ? sel_key(sL[j]) : -INFINITY;
+            int r = 0;
+            for (int c = 0; c < a.E; c++) {
+                const int jc = tt * a.E + c;
+                r += sel_beats(s_amb[jc] ? sel_key(sL[jc]) : -INFINITY, c, my, b);
+            }
+            s_rank[j] = (short)r;
+        }
+        __syncthreads();
+    }
+    // ids, logits (debug: certified L rounded, or exact), weights (src/GemmaCpu.cs:406-407,417)
+    for (int i = tid; i < TE; i += 256) {
+        const int tt = i / a.E, ex = i - tt * a.E;
+        const int r = s_rank[i];
+        if (r < a.k) s_ids[tt * a.k + r] = ex;
+        a.logits[i] = (float)sL[i];
+    }
+    __syncthreads();
+    // one lane per (token, rank j); wave w takes tokens w, w+4, ...
+    for (int tt = wave; tt < a.T; tt += 4) {
+        const int j = lane;
+        const bool act = j < a.k;
+        const int id = act ? s_ids[tt * a.k + j] : 0;
+        const float selj = act ? (float)sL[tt * a.E + id] : 0.0f;
+        const float sel0 = __shfl(selj, 0, 64);
+        // p_0 = exp(0) = 1 exactly, so the CPU's in-place rule uses 1 for every later term
+        const float top = (a.rule == 1 && j > 0) ? 1.0f : sel0;
+        const float pj = act ? (float)exp((double)(selj - top)) : 0.0f;
+        double sum = 0.0;
+        for (int q = 0; q < a.k; q++) sum += (double)__shfl(pj, q, 64);  // in rank order
+        if (act) {
+            a.ids[(int64_t)tt * a.k + j] = id;
+            a.w[(int64_t)tt * a.k + j] = (float)((double)pj / sum) * a.ds[id];
+        }
+    }
+
+    // ---- expert lists (ascending assignment order) and tiles of <= A assignments
+    const int n = a.T * a.k;
+    for (int x = tid; x <= a.E; x += 256) s_cnt[x] = 0;
+    __syncthreads();
+    int my_e = 0, my_rank = 0;
+    if (tid < n) {
+        my_e = clamp_id(s_ids[tid], a.E);
+        for (int b = 0; b < tid; b++) my_rank += clamp_id(s_ids[b], a.E) == my_e;
+        atomicAdd(&s_cnt[my_e], 1);
+    }
+    __syncthreads();
+    // exclusive scans of the counts and of the tile counts (E <= 256: one expert per thread)
+    {
+        const int c = tid < a.E ? s_cnt[tid] : 0;
+        const int tcount = (c + a.A - 1) / a.A;
+        int v1 = c, v2 = tcount;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int y1 = __shfl_up(v1, o, 64), y2 = __shfl_up(v2, o, 64);
+            if (lane >= o) { v1 += y1; v2 += y2; }
+        }
+        __shared__ int wtot1[4], wtot2[4];
+        if (lane == 63) { wtot1[wave] = v1; wtot2[wave] = v2; }
+        __syncthreads();
+        int b1 = 0, b2 = 0;
+        for (int w = 0; w < wave; w++) { b1 += wtot1[w]; b2 += wtot2[w]; }
+        if (tid < a.E) { s_off[tid] = b1 + v1 - c; s_tb[tid] = b2 + v2 - tcount; }
+        if (tid == 0) {
+            s_off[a.E] = wtot1[0] + wtot1[1] + wtot1[2] + wtot1[3];
+            *a.ntiles = wtot2[0] + wtot2[1] + wtot2[2] + wtot2[3];
+        }
+        __syncthreads();
+    }
+    for (int x = tid; x <= a.E; x += 256) a.offsets[x] = s_off[x];
+    if (tid < n) a.perm[s_off[my_e] + my_rank] = tid;
+    if (tid < a.E) {
+        const int c = s_cnt[tid], base = s_tb[tid];
+        for (int q = 0; q * a.A < c; q++) {
+            Tile tl;
+            tl.e = tid;
+            tl.start = s_off[tid] + q * a.A;
+            tl.cnt = min(a.A, c - q * a.A);
+            a.tiles[base + q] = tl;
+        }
+    }
+    {
+        // slots past the last tile carry e = -1: a grouped workgroup reads one slot and stops
+        const int used = s_tb[a.E - 1] + (s_cnt[a.E - 1] + a.A - 1) / a.A;
+        for (int q = used + tid; q < a.max_tiles; q += 256) a.tiles[q] = Tile{-1, 0, 0};
+    }
+    if (tid == 0) __hip_atomic_store(a.counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+void launch_route_dec(hipStream_t st, const RouteDecArgsH& h)
+{
+    RouteDecArgs a{h.T, h.d, h.E, h.k, h.rule, h.A, h.max_tiles, h.eps, h.x, h.W, h.gis, h.ds, h.pre2, h.fnorm, h.act_gu,
+                   h.act_sh, h.Lb, h.Bb, h.counter, h.ids, h.w, h.logits, h.offsets, h.perm, h.tiles, h.ntiles, h.flags};
+    const size_t lds = std::max((size_t)6 * h.d * sizeof(float), (size_t)kRouteMaxTE * 19);
+    static bool attr = false;
+    if (!attr) {
+        (void)hipFuncSetAttribute((const void*)k_route_dec, hipFuncAttributeMaxDynamicSharedMemorySize, 6 * 4096 * 4);
+        attr = true;
+    }
+    hipLaunchKernelGGL(k_route_dec, dim3((h.E + 3) / 4, h.T), dim3(256), lds, st, a);
+}
+
+// ------------------------------------------------------------------------------ grouped products (decode)
+// Work items: (tile of <= DEC_A assignments of one expert, row group of 64 rows) for the experts,
+// then (tile of <= DEC_A tokens, row group) for the dense shared FFN.  The 8 waves each take a
+// contiguous slice of the row's blocks with all their weight loads issued at once (lane = row),
+// read the activation blocks (wave-uniform) from the Q8_0 buffers, and store the per-block terms
+// (float)isum * (d_w * d_x) in LDS; one wave per assignment adds them in block order: the
+// reference's float chain (src/CpuRefGemma.cs:27-36, src/CpuRef.cs:106-115).
+// Gate|up matrices are repacked in paired row groups (lanes 0-31 gate rows 32g.., lanes 32-63 the
+// matching up rows), so the epilogue forms e = gelu(g) * u (src/GemmaCpu.cs:415) for 32 consecutive
+// outputs and writes their Q8_0 block, the down input (src/CpuRef.cs:49-62).
+
+constexpr int DEC_A = kDecA;
+constexpr int DEC_NW = 8;
+constexpr int DEC_NT = DEC_NW * 64;
+constexpr int DEC_MAXB = 16;  // blocks per wave (nb <= 128)
+
+struct DecMat {
+    const uint8_t* pay;
+    const uint8_t* sc;
+    int64_t mat_pay, mat_sc;
+    int rg, nb, rows;
+    Act in;               // activations (rows: token for gate|up, assignment for down)
+    float* out0;          // gate|up: g rows [r][split]; down: y rows [r][rows]
+    float* out1;          // gate|up: u rows
+    int split;            // gate|up: n_ff (valid outputs per row of g/u)
+    Act out_act;          // gate|up: Q8_0 of gelu(g) * u
+};
+
+struct DecArgs {
+    DecMat m0, m1;        // experts, shared FFN (m1.rg == 0: none)
+    const Tile* tiles;
+    const int* ntiles;
+    int max_tiles;
+    const int* perm;
+    int act_div;          // expert activation row = perm entry / act_div
+    int T;
+    const float* gelu_tab;
+};
+
+template <int MODE, int TYPE>
+__global__ __launch_bounds__(DEC_NT) void k_dec_mm(DecArgs a)
+{
+    __shared__ float terms[DEC_A][DEC_MAXB * DEC_NW][64];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    constexpr int PAY = TYPE == PHX_Q4_0_DEV ? 16 : 32;
+
+    int which, rgi, e, cnt;
+    int orow[DEC_A], arow[DEC_A];
+    const int nexp = a.max_tiles * a.m0.rg;
+    if ((int)blockIdx.x < nexp) {
+        which = 0;
+        const int tile = blockIdx.x / a.m0.rg;
+        rgi = blockIdx.x % a.m0.rg;
+        const Tile tl = a.tiles[tile];
+        if (tl.e < 0) return;  // slot past the last tile
+        e = tl.e;
+        cnt = min(tl.cnt, DEC_A);
+#pragma unroll
+        for (int i = 0; i < DEC_A; i++) {
+            orow[i] = i < cnt ? a.perm[tl.start + i] : 0;
+            arow[i] = orow[i] / a.act_div;
+        }
+    } else {
+        which = 1;
+        const int sid = blockIdx.x - nexp;
+        const int tile = sid / a.m1.rg;
+        rgi = sid % a.m1.rg;
+        e = 0;
+        const int t0 = tile * DEC_A;
+        cnt = min(DEC_A, a.T - t0);
+#pragma unroll
+        for (int i = 0; i < DEC_A; i++) orow[i] = arow[i] = t0 + i;
+    }
+    const DecMat M = which ? a.m1 : a.m0;
+    const int nb = M.nb;
+
+    // ---- weights: this wave's blocks of the lane's row, all loads issued at once
+    const int bpw = (nb + DEC_NW - 1) / DEC_NW;
+    const int b0 = wave * bpw, b1 = min(nb, b0 + bpw);
+    const uint8_t* wp = M.pay + e * M.mat_pay + ((int64_t)rgi * nb * 64 + lane) * PAY;
+    const uint16_t* ws = (const uint16_t*)(M.sc + e * M.mat_sc) + (int64_t)rgi * nb * 64 + lane;
+    uint4 wv[DEC_MAXB][PAY / 16];
+    uint16_t dwh[DEC_MAXB];
+#pragma unroll
+    for (int j = 0; j < DEC_MAXB; j++) {
+        if (b0 + j < b1) {
+            const uint4* src = (const uint4*)(wp + (int64_t)(b0 + j) * 64 * PAY);
+#pragma unroll
+            for (int c = 0; c < PAY / 16; c++) wv[j][c] = src[c];
+            dwh[j] = ws[(int64_t)(b0 + j) * 64];
+        }
+    }
+    // ---- per-block terms of every assignment
+    for (int i = 0; i < cnt; i++) {
+        const int64_t r = arow[i];
+        const uint32_t* xq = (const uint32_t*)(M.in.q + r * M.in.qstride);
+        const float* xd = M.in.d + r * M.in.dstride;
+        const int* xs = M.in.s + r * M.in.sstride;
+#pragma unroll
+        for (int j = 0; j < DEC_MAXB; j++) {
+            const int b = b0 + j;
+            if (b < b1) {
+                const uint32_t* xb = xq + b * 8;
+                int isum = 0;
+                if (TYPE == PHX_Q4_0_DEV) {
+                    const uint32_t w4[4] = {wv[j][0].x, wv[j][0].y, wv[j][0].z, wv[j][0].w};
+#pragma unroll
+                    for (int w = 0; w < 4; w++) {
+                        isum = __builtin_amdgcn_sdot4((int)(w4[w] & 0x0F0F0F0Fu), (int)xb[w], isum, false);
+                        isum = __builtin_amdgcn_sdot4((int)((w4[w] >> 4) & 0x0F0F0F0Fu), (int)xb[4 + w], isum, false);
+                    }
+                    isum -= 8 * xs[b];
+                } else {
+                    const uint32_t w8[8] = {wv[j][0].x, wv[j][0].y, wv[j][0].z, wv[j][0].w,
+                                            wv[j][PAY / 16 - 1].x, wv[j][PAY / 16 - 1].y, wv[j][PAY / 16 - 1].z,
+                                            wv[j][PAY / 16 - 1].w};
+#pragma unroll
+                    for (int w = 0; w < 8; w++) isum = __builtin_amdgcn_sdot4((int)w8[w], (int)xb[w], isum, false);
+                }
+                const float dd = h2f(dwh[j]) * xd[b];
+                terms[i][b][lane] = (float)isum * dd;
+            }
+        }
+    }
+    __syncthreads();
+    // ---- the float chain in block order (wave i for assignment i), then the epilogue
+    if (wave < cnt) {
+        const int i = wave;
+        float S = 0.0f;
+#pragma unroll 8
+        for (int b = 0; b < nb; b++) S += terms[i][b][lane];
+        const int64_t orr = orow[i];
+        if (MODE == 0) {
+            // paired row group: lanes 0-31 gate j, lanes 32-63 up j, j = 32 rgi + lane % 32
+            const int jj = rgi * 32 + (lane & 31);
+            const float u = __shfl_down(S, 32, 64);
+            if (jj < M.split) {
+                if (lane < 32) M.out0[orr * M.split + jj] = S;
+                else M.out1[orr * M.split + jj] = S;
+            }
+            const float ev = lane < 32 ? gelu_ref(S, a.gelu_tab) * u : 0.0f;
+            float dval;
+            int sum;
+            const int q = q8_0_half(ev, &dval, &sum);
+            if (lane < 32) {
+                const Act& o = M.out_act;
+                o.q[orr * o.qstride + jj] = (int8_t)q;
+                if (lane == 0) {
+                    o.d[orr * o.dstride + rgi] = dval;
+                    o.s[orr * o.sstride + rgi] = sum;
+                }
+            }
+        } else {
+            const int row = rgi * 64 + lane;
+            if (row < M.rows) M.out0[orr * M.rows + row] = S;
+        }
+    }
+}
+
+static DecMat to_dev(const DecMatH& h)
+{
+    DecMat m{};
+    if (!h.q) return m;
+    m.pay = h.q->payload;
+    m.sc = h.q->scale;
+    m.mat_pay = h.q->mat_pay_stride();
+    m.mat_sc = h.q->mat_sc_stride();
+    m.rg = h.q->rg;
+    m.nb = h.q->nb;
+    m.rows = h.q->rows;
+    m.in = h.in;
+    m.out0 = h.out0;
+    m.out1 = h.out1;
+    m.split = h.split;
+    m.out_act = h.out_act;
+    return m;
+}
+
+void launch_dec(hipStream_t st, int mode, const DecMatH& m0, const DecMatH& m1, const Tile* tiles, const int* ntiles,
+                int max_tiles, const int* perm, int act_div, int T, const float* gelu_tab)
+{
+    DecArgs a{};
+    a.m0 = to_dev(m0);
+    a.m1 = to_dev(m1);
+    a.tiles = tiles;
+    a.ntiles = ntiles;
+    a.max_tiles = max_tiles;
+    a.perm = perm;
+    a.act_div = act_div;
+    a.T = T;
+    a.gelu_tab = gelu_tab;
+    const int items = max_tiles * a.m0.rg + (a.m1.rg > 0 ? (T + DEC_A - 1) / DEC_A * a.m1.rg : 0);
+    const bool q4 = m0.q->type == PHX_Q4_0_DEV;
+    if (mode == 0) {
+        if (q4) hipLaunchKernelGGL((k_dec_mm<0, PHX_Q4_0_DEV>), dim3(items), dim3(DEC_NT), 0, st, a);
+        else hipLaunchKernelGGL((k_dec_mm<0, PHX_Q8_0_DEV>), dim3(items), dim3(DEC_NT), 0, st, a);
+    } else {
+        if (q4) hipLaunchKernelGGL((k_dec_mm<1, PHX_Q4_0_DEV>), dim3(items), dim3(DEC_NT), 0, st, a);
+        else hipLaunchKernelGGL((k_dec_mm<1, PHX_Q8_0_DEV>), dim3(items), dim3(DEC_NT), 0, st, a);
+    }
+}
+
+// ------------------------------------------------------------------------------ combine (decode)
+// k_combine's arithmetic (rank-ordered sum of w_j * yd_j, the two branch norms, optional residual;
+// src/GemmaCpu.cs:384,418-421,355-356) with 1024 threads per token and every global load of the
+// token issued in one round (d <= 4096, k <= 16).
+constexpr int CB_NT = 1024, CB_MAXE = 4;
+
+__global__ __launch_bounds__(CB_NT) void k_combine_dec(int d, int k, float eps, const float* __restrict__ yd,
+                                                       const float* __restrict__ w, const float* __restrict__ shared,
+                                                       const float* __restrict__ post1, const float* __restrict__ post2,
+                                                       float* __restrict__ out, float* __restrict__ xres,
+                                                       const float* __restrict__ post_ffw, int* flags)
+{
+    extern __shared__ float cb[];  // acc [d], shared [d], out [d]
+    __shared__ double red[CB_NT / 64 + 1];
+    const int t = blockIdx.x, tid = threadIdx.x;
+    float* sacc = cb;
+    float* ssh = cb + d;
+    float* so = cb + 2 * d;
+    const float* sh = shared ? shared + (int64_t)t * d : nullptr;
+    float wj[PHX_MAX_USED_DEV];
+#pragma unroll
+    for (int j = 0; j < PHX_MAX_USED_DEV; j++) wj[j] = j < k ? w[(int64_t)t * k + j] : 0.0f;
+    float yv[CB_MAXE][PHX_MAX_USED_DEV], shv[CB_MAXE], p1[CB_MAXE], p2[CB_MAXE], pf[CB_MAXE], xv[CB_MAXE];
+#pragma unroll
+    for (int q = 0; q < CB_MAXE; q++) {
+        const int i = tid + q * CB_NT;
+        const bool in = i < d;
+#pragma unroll
+        for (int j = 0; j < PHX_MAX_USED_DEV; j++) yv[q][j] = (in && j < k) ? yd[((int64_t)t * k + j) * d + i] : 0.0f;
+        shv[q] = (in && sh) ? sh[i] : 0.0f;
+        p1[q] = (in && sh) ? post1[i] : 0.0f;
+        p2[q] = in ? post2[i] : 0.0f;
+        pf[q] = (in && xres) ? post_ffw[i] : 0.0f;
+        xv[q] = (in && xres) ? xres[(int64_t)t * d + i] : 0.0f;
+    }
+    float accv[CB_MAXE];
+#pragma unroll
+    for (int q = 0; q < CB_MAXE; q++) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < PHX_MAX_USED_DEV; j++)
+            if (j < k) acc += yv[q][j] * wj[j];
+        accv[q] = acc;
+        const int i = tid + q * CB_NT;
+        if (i < d) {
+            sacc[i] = acc;
+            ssh[i] = shv[q];
+        }
+    }
+    __syncthreads();
+    const float s2 = rms_scale_from_mean(mean_sq_cert<CB_NT>(sacc, d, red, flags), eps);
+    const float s1 = sh ? rms_scale_from_mean(mean_sq_cert<CB_NT>(ssh, d, red, flags), eps) : 0.0f;
+    float ov[CB_MAXE];
+#pragma unroll
+    for (int q = 0; q < CB_MAXE; q++) {
+        const int i = tid + q * CB_NT;
+        const float mlp = sh ? shv[q] * s1 * p1[q] : 0.0f;
+        ov[q] = mlp + accv[q] * s2 * p2[q];
+        if (i < d) {
+            out[(int64_t)t * d + i] = ov[q];
+            so[i] = ov[q];
+        }
+    }
+    if (xres) {
+        __syncthreads();
+        const float s3 = rms_scale_from_mean(mean_sq_cert<CB_NT>(so, d, red, flags), eps);
+#pragma unroll
+        for (int q = 0; q < CB_MAXE; q++) {
+            const int i = tid + q * CB_NT;
+            if (i < d) xres[(int64_t)t * d + i] = xv[q] + ov[q] * s3 * pf[q];
+        }
+    }
+}
+
+void launch_combine_dec(hipStream_t st, int T, int d, int k, float eps, const float* yd, const float* w,
+                        const float* shared, const float* post1, const float* post2, float* out, float* xres,
+                        const float* post_ffw, int* flags)
+{
+    hipLaunchKernelGGL(k_combine_dec, dim3(T), dim3(CB_NT), (size_t)3 * d * sizeof(float), st, d, k, eps, yd, w, shared,
+                       post1, post2, out, xres, post_ffw, flags);
+}
+
+}  // namespace phx

@@ -31,6 +31,7 @@ struct QMat {
     int n_mat = 0, rows = 0, cols = 0;  // cols includes any zero padding of K
     int rg = 0, nb = 0;                 // row groups, blocks (32 or 256 elements) per row
     int pay = 0, sbytes = 0;
+    bool paired = false;                // gate|up: row group g = gate rows 32g..32g+31 and the matching up rows
     uint8_t* payload = nullptr;
     uint8_t* scale = nullptr;
     int64_t mat_pay_stride() const { return (int64_t)rg * nb * kRowGroup * pay; }
@@ -71,6 +72,46 @@ void launch_requant(hipStream_t st, int rows, int nf, const float* g, const floa
 void launch_combine(hipStream_t st, int T, int d, int k, float eps, const float* yd, const float* w,
                     const float* shared, const float* post1, const float* post2, float* out, float* x_resid,
                     const float* post_ffw, int* flags);
+// decode path (kernels_decode.hip)
+constexpr int kDecA = 2;          // assignments per decode tile
+constexpr int kRouteMaxTE = 2048; // T * E the decode router's last workgroup holds
+struct RouteDecArgsH {
+    int T, d, E, k, rule, A, max_tiles;
+    float eps;
+    const float* x;
+    const float* W;
+    const float* gis;
+    const float* ds;
+    const float* pre2;
+    const float* fnorm;
+    Act act_gu, act_sh;
+    double* Lb;
+    double* Bb;
+    int* counter;
+    int* ids;
+    float* w;
+    float* logits;
+    int* offsets;
+    int* perm;
+    Tile* tiles;
+    int* ntiles;
+    int* flags;
+};
+void launch_route_dec(hipStream_t st, const RouteDecArgsH& h);
+struct DecMatH {  // host-side description of one matrix of a decode grouped launch
+    const QMat* q = nullptr;
+    Act in;
+    float* out0 = nullptr;
+    float* out1 = nullptr;
+    int split = 0;
+    Act out_act;
+};
+void launch_dec(hipStream_t st, int mode, const DecMatH& m0, const DecMatH& m1, const Tile* tiles, const int* ntiles,
+                int max_tiles, const int* perm, int act_div, int T, const float* gelu_tab);
+void launch_combine_dec(hipStream_t st, int T, int d, int k, float eps, const float* yd, const float* w,
+                        const float* shared, const float* post1, const float* post2, float* out, float* xres,
+                        const float* post_ffw, int* flags);
+void launch_stream_read(hipStream_t st, const void* src, int64_t bytes, uint32_t* sink);
 void launch_selftest(hipStream_t st, int op, int n, const float* a, const float* b, float* out, const float* gelu_tab);
 
 }  // namespace phx

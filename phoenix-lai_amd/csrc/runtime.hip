@@ -186,13 +186,16 @@ void repack_block(int type, const uint8_t* blk, uint8_t* pay, uint8_t* sc)
     }
 }
 
-void repack(int type, const uint8_t* src, int n_mat, int rows, int cols, QMat& q, HostQ& h)
+// paired: rows are [gate (rows/2) | up (rows/2)]; row group g holds gate rows 32g..32g+31 in lanes 0-31
+// and up rows rows/2 + 32g.. in lanes 32-63.
+void repack(int type, const uint8_t* src, int n_mat, int rows, int cols, QMat& q, HostQ& h, bool paired = false)
 {
     q.type = type;
     q.n_mat = n_mat;
     q.rows = rows;
     q.cols = cols;
-    q.rg = (rows + kRowGroup - 1) / kRowGroup;
+    q.paired = paired;
+    q.rg = paired ? (rows / 2 + 31) / 32 : (rows + kRowGroup - 1) / kRowGroup;
     q.nb = cols / block_elems(type);
     q.pay = type == PHX_Q4_0 ? 16 : type == PHX_Q8_0 ? 32 : type == PHX_Q4_K ? 144 : 208;
     q.sbytes = type == PHX_Q4_K ? 4 : 2;
@@ -207,6 +210,11 @@ void repack(int type, const uint8_t* src, int n_mat, int rows, int cols, QMat& q
             for (int64_t gr = w; gr < total_rows; gr += nt) {
                 int m = (int)(gr / rows), r = (int)(gr % rows);
                 int rg = r / kRowGroup, lane = r % kRowGroup;
+                if (paired) {
+                    const int half = rows / 2, up = r >= half, j = up ? r - half : r;
+                    rg = j / 32;
+                    lane = (j % 32) + (up ? 32 : 0);
+                }
                 const uint8_t* row = src + gr * rb;
                 for (int b = 0; b < q.nb; b++) {
                     int64_t idx = (((int64_t)m * q.rg + rg) * q.nb + b) * kRowGroup + lane;
@@ -221,7 +229,7 @@ void repack(int type, const uint8_t* src, int n_mat, int rows, int cols, QMat& q
 struct Layer {
     bool present = false;
     phx_moe_layer_desc desc{};
-    float *wt4 = nullptr, *gis = nullptr, *ds = nullptr, *pre2 = nullptr, *post1 = nullptr, *post2 = nullptr;
+    float *wt4 = nullptr, *wrow = nullptr, *gis = nullptr, *ds = nullptr, *pre2 = nullptr, *post1 = nullptr, *post2 = nullptr;
     float *ffn_norm = nullptr, *post_ffw = nullptr;
     QMat gu, dn, sgu, sdn;
 };
@@ -291,7 +299,7 @@ int hip_code(hipError_t e)
 enum WsId {
     W_X, W_SHARED, W_OUT, W_RIN, W_XSCALE, W_AGU_Q, W_AGU_D, W_AGU_S, W_ASH_Q, W_ASH_D, W_ASH_S, W_LOGITS, W_IDS, W_W,
     W_OFF, W_PERM, W_TILES, W_NTILES, W_G, W_U, W_ADN_Q, W_ADN_D, W_ADN_S, W_YD, W_SHG, W_SHU, W_ASD_Q, W_ASD_D,
-    W_ASD_S, W_SHOUT, W_ZERO, W_STILES, W_SNTILES, W_SOFF, W_SPERM, W_COUNT
+    W_ASD_S, W_SHOUT, W_ZERO, W_STILES, W_SNTILES, W_SOFF, W_SPERM, W_LB, W_BB, W_COUNTER, W_COUNT
 };
 
 int ensure(phx_moe_ctx* c, int id, size_t bytes)
@@ -305,7 +313,7 @@ int ensure(phx_moe_ctx* c, int id, size_t bytes)
     size_t n = std::max<size_t>(bytes, 256);
     HIPCHK(c, hipMalloc(&b.p, n));
     b.bytes = n;
-    if (id == W_ZERO) HIPCHK(c, hipMemset(b.p, 0, n));
+    if (id == W_ZERO || id == W_COUNTER) HIPCHK(c, hipMemset(b.p, 0, n));
     return PHX_OK;
 }
 
@@ -364,6 +372,9 @@ int ensure_workspace(phx_moe_ctx* c, const Layer& L, int T)
     ENS(W_TILES, (size_t)((n + kTileA - 1) / kTileA + D.n_expert) * sizeof(Tile));
     ENS(W_NTILES, 4);
     ENS(W_G, n * D.n_ff * 4);
+    ENS(W_LB, (size_t)T * D.n_expert * 8);
+    ENS(W_BB, (size_t)T * D.n_expert * 8);
+    ENS(W_COUNTER, 64);
     ENS(W_U, n * D.n_ff * 4);
     ENS(W_YD, n * D.d * 4);
     if ((rc = ensure_act(c, act_fmt(D.gate_up_type), T, D.d, W_AGU_Q, W_AGU_D, W_AGU_S))) return rc;
@@ -381,6 +392,7 @@ int ensure_workspace(phx_moe_ctx* c, const Layer& L, int T)
         ENS(W_SOFF, 8);
         ENS(W_SPERM, (size_t)T * 4);
     }
+    ENS(W_TILES, (size_t)((n + kDecA - 1) / kDecA + D.n_expert) * sizeof(Tile));
 #undef ENS
     return PHX_OK;
 }
@@ -418,8 +430,113 @@ struct ProfScope {
     }
 };
 
-// Enqueue one MoE FFN block on the context stream.
-int run_layer(phx_moe_ctx* c, const Layer& L, int T, const float* x, const float* shared, float* out, float* xres)
+bool dec_type(int t) { return t == PHX_Q4_0 || t == PHX_Q8_0; }
+
+// The decode path: few tokens, Q4_0/Q8_0 weights, K <= 4096 (kernels_decode.hip).
+bool use_decode(const Layer& L, int T, unsigned flags)
+{
+    const phx_moe_layer_desc& D = L.desc;
+    if (flags & PHX_FLAG_EXACT_ROUTER) return false;
+    if (T > 16 || T * D.n_used > 256 || T * D.n_expert > kRouteMaxTE || D.d > 4096 || D.d % 256 != 0) return false;
+    if (!dec_type(D.gate_up_type) || !dec_type(D.down_type) || D.down_cols > 4096) return false;
+    if (D.n_ff_shared > 0 && (D.shared_type != D.gate_up_type || D.shared_type != D.down_type || D.n_ff_shared > 4096))
+        return false;
+    return true;
+}
+
+int run_layer_decode(phx_moe_ctx* c, const Layer& L, int T, const float* x, const float* shared, float* out, float* xres)
+{
+    const phx_moe_layer_desc& D = L.desc;
+    hipStream_t st = c->stream;
+    const int d = D.d, E = D.n_expert, k = D.n_used, nf = D.n_ff;
+    const int n = T * k;
+    const bool shared_ffn = shared == nullptr && D.n_ff_shared > 0;
+    // every tile holds at least one assignment: at most n tiles, and at most ceil(n/A) + E
+    const int max_tiles = std::min(n, (n + kDecA - 1) / kDecA + E);
+    Act agu = make_act(c, ACT_Q8_0, d, W_AGU_Q, W_AGU_D, W_AGU_S);
+    Act adn = make_act(c, ACT_Q8_0, D.down_cols, W_ADN_Q, W_ADN_D, W_ADN_S);
+    Act ash, asd;
+    if (shared_ffn) {
+        ash = make_act(c, ACT_Q8_0, d, W_ASH_Q, W_ASH_D, W_ASH_S);
+        asd = make_act(c, ACT_Q8_0, D.n_ff_shared, W_ASD_Q, W_ASD_D, W_ASD_S);
+    }
+    {
+        ProfScope p(c, PHX_K_ROUTER);
+        RouteDecArgsH r{};
+        r.T = T;
+        r.d = d;
+        r.E = E;
+        r.k = k;
+        r.rule = D.weight_rule;
+        r.A = kDecA;
+        r.max_tiles = max_tiles;
+        r.eps = D.eps;
+        r.x = x;
+        r.W = L.wrow;
+        r.gis = L.gis;
+        r.ds = L.ds;
+        r.pre2 = L.pre2;
+        r.fnorm = shared_ffn ? L.ffn_norm : nullptr;
+        r.act_gu = agu;
+        r.act_sh = ash;
+        r.Lb = wp<double>(c, W_LB);
+        r.Bb = wp<double>(c, W_BB);
+        r.counter = wp<int>(c, W_COUNTER);
+        r.ids = wp<int>(c, W_IDS);
+        r.w = wp<float>(c, W_W);
+        r.logits = wp<float>(c, W_LOGITS);
+        r.offsets = wp<int>(c, W_OFF);
+        r.perm = wp<int>(c, W_PERM);
+        r.tiles = wp<Tile>(c, W_TILES);
+        r.ntiles = wp<int>(c, W_NTILES);
+        r.flags = c->flags;
+        launch_route_dec(st, r);
+    }
+    {
+        ProfScope p(c, PHX_K_GATE_UP);
+        DecMatH m0, m1;
+        m0.q = &L.gu;
+        m0.in = agu;
+        m0.out0 = wp<float>(c, W_G);
+        m0.out1 = wp<float>(c, W_U);
+        m0.split = nf;
+        m0.out_act = adn;
+        if (shared_ffn) {
+            m1.q = &L.sgu;
+            m1.in = ash;
+            m1.out0 = wp<float>(c, W_SHG);
+            m1.out1 = wp<float>(c, W_SHU);
+            m1.split = D.n_ff_shared;
+            m1.out_act = asd;
+        }
+        launch_dec(st, 0, m0, m1, wp<Tile>(c, W_TILES), wp<int>(c, W_NTILES), max_tiles, wp<int>(c, W_PERM), k, T,
+                   c->gelu_tab);
+    }
+    {
+        ProfScope p(c, PHX_K_DOWN);
+        DecMatH m0, m1;
+        m0.q = &L.dn;
+        m0.in = adn;
+        m0.out0 = wp<float>(c, W_YD);
+        if (shared_ffn) {
+            m1.q = &L.sdn;
+            m1.in = asd;
+            m1.out0 = wp<float>(c, W_SHOUT);
+        }
+        launch_dec(st, 1, m0, m1, wp<Tile>(c, W_TILES), wp<int>(c, W_NTILES), max_tiles, wp<int>(c, W_PERM), 1, T,
+                   c->gelu_tab);
+    }
+    {
+        ProfScope p(c, PHX_K_COMBINE);
+        launch_combine_dec(st, T, d, k, D.eps, wp<float>(c, W_YD), wp<float>(c, W_W),
+                           shared_ffn ? wp<float>(c, W_SHOUT) : shared, L.post1, L.post2, out, xres, L.post_ffw, c->flags);
+    }
+    HIPCHK(c, hipGetLastError());
+    return PHX_OK;
+}
+
+// Enqueue one MoE FFN block on the context stream (any T; exact router chains).
+int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, const float* shared, float* out, float* xres)
 {
     const phx_moe_layer_desc& D = L.desc;
     hipStream_t st = c->stream;
@@ -443,7 +560,7 @@ int run_layer(phx_moe_ctx* c, const Layer& L, int T, const float* x, const float
         ProfScope p(c, PHX_K_TOPK);
         launch_topk(st, T, E, k, D.weight_rule, wp<float>(c, W_LOGITS), L.ds, wp<int>(c, W_IDS), wp<float>(c, W_W));
     }
-    const int max_tiles = (n + kTileA - 1) / kTileA + E;
+    const int max_tiles = std::min(n, (n + kTileA - 1) / kTileA + E);
     {
         ProfScope p(c, PHX_K_DISPATCH);
         launch_dispatch(st, n, E, kTileA, wp<int>(c, W_IDS), wp<int>(c, W_OFF), wp<int>(c, W_PERM), wp<Tile>(c, W_TILES),
@@ -489,6 +606,13 @@ int run_layer(phx_moe_ctx* c, const Layer& L, int T, const float* x, const float
     return PHX_OK;
 }
 
+int run_layer(phx_moe_ctx* c, const Layer& L, int T, const float* x, const float* shared, float* out, float* xres,
+              unsigned flags)
+{
+    if (use_decode(L, T, flags)) return run_layer_decode(c, L, T, x, shared, out, xres);
+    return run_layer_general(c, L, T, x, shared, out, xres);
+}
+
 int upload_f32(phx_moe_ctx* c, const float* src, size_t n, float** dst)
 {
     if (*dst) HIPCHK(c, hipFree(*dst));
@@ -506,11 +630,11 @@ void free_qmat(QMat& q)
     q.scale = nullptr;
 }
 
-int upload_q(phx_moe_ctx* c, int type, const void* src, int n_mat, int rows, int cols, QMat& q)
+int upload_q(phx_moe_ctx* c, int type, const void* src, int n_mat, int rows, int cols, QMat& q, bool paired = false)
 {
     free_qmat(q);
     HostQ h;
-    repack(type, (const uint8_t*)src, n_mat, rows, cols, q, h);
+    repack(type, (const uint8_t*)src, n_mat, rows, cols, q, h, paired);
     HIPCHK(c, hipMalloc((void**)&q.payload, h.payload.size()));
     HIPCHK(c, hipMalloc((void**)&q.scale, h.scale.size()));
     HIPCHK(c, hipMemcpy(q.payload, h.payload.data(), h.payload.size(), hipMemcpyHostToDevice));
@@ -520,7 +644,7 @@ int upload_q(phx_moe_ctx* c, int type, const void* src, int n_mat, int rows, int
 
 void free_layer(Layer& L)
 {
-    float** fs[] = {&L.wt4, &L.gis, &L.ds, &L.pre2, &L.post1, &L.post2, &L.ffn_norm, &L.post_ffw};
+    float** fs[] = {&L.wt4, &L.wrow, &L.gis, &L.ds, &L.pre2, &L.post1, &L.post2, &L.ffn_norm, &L.post_ffw};
     for (float** f : fs) {
         if (*f) (void)hipFree(*f);
         *f = nullptr;
@@ -656,13 +780,14 @@ int phx_moe_layer_upload(phx_moe_ctx* c, int layer, const phx_moe_layer_desc* D)
     for (int e = 0; e < E; e++)
         for (int i = 0; i < d; i++) wt[((size_t)(i / 4) * E + e) * 4 + (i % 4)] = D->gate_inp[(size_t)e * d + i];
     if ((rc = upload_f32(c, wt.data(), wt.size(), &L.wt4))) return rc;
+    if ((rc = upload_f32(c, D->gate_inp, (size_t)d * E, &L.wrow))) return rc;
     if ((rc = upload_f32(c, D->gate_inp_scale, d, &L.gis))) return rc;
     if ((rc = upload_f32(c, D->down_scale, E, &L.ds))) return rc;
     if ((rc = upload_f32(c, D->pre_ffw_norm_2, d, &L.pre2))) return rc;
     if ((rc = upload_f32(c, D->post_ffw_norm_1, d, &L.post1))) return rc;
     if ((rc = upload_f32(c, D->post_ffw_norm_2, d, &L.post2))) return rc;
     if (D->post_ffw_norm && (rc = upload_f32(c, D->post_ffw_norm, d, &L.post_ffw))) return rc;
-    if ((rc = upload_q(c, D->gate_up_type, D->gate_up_exps, E, 2 * nf, d, L.gu))) return rc;
+    if ((rc = upload_q(c, D->gate_up_type, D->gate_up_exps, E, 2 * nf, d, L.gu, true))) return rc;
     if ((rc = upload_q(c, D->down_type, D->down_exps, E, d, D->down_cols, L.dn))) return rc;
     if (D->n_ff_shared > 0) {
         const int nff = D->n_ff_shared;
@@ -671,7 +796,7 @@ int phx_moe_layer_upload(phx_moe_ctx* c, int layer, const phx_moe_layer_desc* D)
         memcpy(fused.data(), D->ffn_gate, (size_t)nff * rb);
         memcpy(fused.data() + (size_t)nff * rb, D->ffn_up, (size_t)nff * rb);
         if ((rc = upload_f32(c, D->ffn_norm, d, &L.ffn_norm))) return rc;
-        if ((rc = upload_q(c, D->shared_type, fused.data(), 1, 2 * nff, d, L.sgu))) return rc;
+        if ((rc = upload_q(c, D->shared_type, fused.data(), 1, 2 * nff, d, L.sgu, true))) return rc;
         if ((rc = upload_q(c, D->shared_type, D->ffn_down, 1, d, round_up(nff, block_elems(D->shared_type)), L.sdn)))
             return rc;
     }
@@ -705,7 +830,7 @@ int phx_moe_ffn(phx_moe_ctx* c, int layer, int T, float* x, const float* shared,
             shin = wp<float>(c, W_SHARED);
         }
     }
-    rc = run_layer(c, L, T, xin, shin, o, (flags & PHX_FLAG_RESIDUAL) ? xin : nullptr);
+    rc = run_layer(c, L, T, xin, shin, o, (flags & PHX_FLAG_RESIDUAL) ? xin : nullptr, flags);
     if (rc) return rc;
     c->last_T = T;
     c->last_layer = layer;
@@ -746,6 +871,11 @@ int phx_moe_get_intermediates(phx_moe_ctx* c, float* g, float* u, float* yd)
 
 int phx_moe_stack_capture(phx_moe_ctx* c, int first, int n_layers, int T)
 {
+    return phx_moe_stack_capture2(c, first, n_layers, T, 0);
+}
+
+int phx_moe_stack_capture2(phx_moe_ctx* c, int first, int n_layers, int T, unsigned flags)
+{
     if (!c || n_layers <= 0 || first < 0 || first + n_layers > (int)c->layers.size() || T <= 0)
         return set_err(c, PHX_ERR_ARG, "bad stack range");
     HIPCHK(c, hipSetDevice(c->device));
@@ -765,7 +895,7 @@ int phx_moe_stack_capture(phx_moe_ctx* c, int first, int n_layers, int T)
     HIPCHK(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
     int rc = PHX_OK;
     for (int l = first; l < first + n_layers && rc == PHX_OK; l++)
-        rc = run_layer(c, c->layers[l], T, wp<float>(c, W_X), nullptr, wp<float>(c, W_OUT), wp<float>(c, W_X));
+        rc = run_layer(c, c->layers[l], T, wp<float>(c, W_X), nullptr, wp<float>(c, W_OUT), wp<float>(c, W_X), flags);
     hipGraph_t g = nullptr;
     hipError_t e = hipStreamEndCapture(c->stream, &g);
     c->profiling = prof;
@@ -879,11 +1009,34 @@ int phx_moe_selftest(phx_moe_ctx* c, int op, int n, const float* a, const float*
     return PHX_OK;
 }
 
-int phx_moe_fallback_count(phx_moe_ctx* c, int* count)
+int phx_moe_stream_read(phx_moe_ctx* c, const void* buf, uint64_t bytes, int iters, double* ms)
 {
-    if (!c || !count) return PHX_ERR_ARG;
+    if (!c || !buf || bytes < 16 || iters <= 0 || !ms) return PHX_ERR_ARG;
+    HIPCHK(c, hipSetDevice(c->device));
+    uint32_t* sink = nullptr;
+    HIPCHK(c, hipMalloc((void**)&sink, 256));
+    hipEvent_t a, b;
+    HIPCHK(c, hipEventCreate(&a));
+    HIPCHK(c, hipEventCreate(&b));
+    launch_stream_read(c->stream, buf, (int64_t)bytes, sink);
+    HIPCHK(c, hipEventRecord(a, c->stream));
+    for (int i = 0; i < iters; i++) launch_stream_read(c->stream, buf, (int64_t)bytes, sink);
+    HIPCHK(c, hipEventRecord(b, c->stream));
+    HIPCHK(c, hipEventSynchronize(b));
+    float t = 0.0f;
+    HIPCHK(c, hipEventElapsedTime(&t, a, b));
+    *ms = t / iters;
+    (void)hipEventDestroy(a);
+    (void)hipEventDestroy(b);
+    (void)hipFree(sink);
+    return PHX_OK;
+}
+
+int phx_moe_fallback_count(phx_moe_ctx* c, int* counts)
+{
+    if (!c || !counts) return PHX_ERR_ARG;
     HIPCHK(c, hipStreamSynchronize(c->stream));
-    HIPCHK(c, hipMemcpy(count, c->flags, 4, hipMemcpyDeviceToHost));
+    HIPCHK(c, hipMemcpy(counts, c->flags, 8, hipMemcpyDeviceToHost));
     return PHX_OK;
 }
 

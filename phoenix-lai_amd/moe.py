@@ -19,7 +19,7 @@ class PHX:
     OK, ERR_ARG, ERR_OOM, ERR_UNSUPPORTED, ERR_DEVICE_LOST, ERR_HIP = 0, -1, -2, -3, -4, -5
     F32, Q4_0, Q8_0, Q4_K, Q6_K = 0, 2, 8, 12, 14
     WEIGHTS_SOFTMAX, WEIGHTS_CPUREF = 0, 1
-    FLAG_DEVICE_PTRS, FLAG_ASYNC, FLAG_RESIDUAL = 1, 2, 4
+    FLAG_DEVICE_PTRS, FLAG_ASYNC, FLAG_RESIDUAL, FLAG_EXACT_ROUTER = 1, 2, 4, 8
     KINDS = ["prologue", "router", "topk", "dispatch", "gate_up", "requant", "down", "combine", "shared"]
     MAX_EXPERTS, MAX_USED = 256, 16
 
@@ -110,6 +110,7 @@ def load_lib():
         "phx_moe_get_routing": (i32, [vp, vp, vp, vp, vp, vp]),
         "phx_moe_get_intermediates": (i32, [vp, vp, vp, vp]),
         "phx_moe_stack_capture": (i32, [vp, i32, i32, i32]),
+        "phx_moe_stack_capture2": (i32, [vp, i32, i32, i32, u32]),
         "phx_moe_stack_run": (i32, [vp, vp, i32, u32]),
         "phx_moe_sync": (i32, [vp]),
         "phx_moe_dev_alloc": (i32, [vp, C.c_uint64, C.POINTER(vp)]),
@@ -120,6 +121,7 @@ def load_lib():
         "phx_moe_profile_read": (i32, [vp, C.POINTER(C.c_double), C.POINTER(C.c_int64)]),
         "phx_moe_selftest": (i32, [vp, i32, i32, f32p, f32p, f32p]),
         "phx_moe_fallback_count": (i32, [vp, i32p]),
+        "phx_moe_stream_read": (i32, [vp, vp, C.c_uint64, i32, C.POINTER(C.c_double)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -191,13 +193,16 @@ class MoeContext:
         self._check(self.lib.phx_moe_layer_upload(self.h, layer, C.byref(desc)))
         self.layers[layer] = {k: L[k] for k in ("d", "n_expert", "n_used", "n_ff")}
 
-    def ffn(self, layer: int, x: np.ndarray, shared: np.ndarray | None = None, residual: bool = False) -> np.ndarray:
-        """out[T][d] of one MoE FFN block on host arrays (x is updated in place when residual)."""
+    def ffn(self, layer: int, x: np.ndarray, shared: np.ndarray | None = None, residual: bool = False,
+            exact_router: bool = False) -> np.ndarray:
+        """out[T][d] of one MoE FFN block on host arrays; with residual, returns (out, x + rmsnorm(out) * post)."""
         x = _f32(x)
+        if residual:
+            x = x.copy()
         T, d = x.shape
         out = np.empty_like(x)
         sh = None if shared is None else _f32(shared)
-        flags = PHX.FLAG_RESIDUAL if residual else 0
+        flags = (PHX.FLAG_RESIDUAL if residual else 0) | (PHX.FLAG_EXACT_ROUTER if exact_router else 0)
         self._last_layer, self._last_T = layer, T
         self._check(self.lib.phx_moe_ffn(self.h, layer, T, x.ctypes.data, None if sh is None else sh.ctypes.data,
                                          out.ctypes.data, flags))
@@ -250,8 +255,9 @@ class MoeContext:
     _last_layer = 0
 
     # ------------------------------------------------------------------ stack (HIP graph)
-    def stack_capture(self, first: int, n_layers: int, T: int):
-        self._check(self.lib.phx_moe_stack_capture(self.h, first, n_layers, T))
+    def stack_capture(self, first: int, n_layers: int, T: int, exact_router: bool = False):
+        self._check(self.lib.phx_moe_stack_capture2(self.h, first, n_layers, T,
+                                                    PHX.FLAG_EXACT_ROUTER if exact_router else 0))
         self._stack_last = first + n_layers - 1
 
     def stack_run(self, x: np.ndarray) -> np.ndarray:
@@ -285,7 +291,17 @@ class MoeContext:
                                               out.ctypes.data_as(fp)))
         return out
 
-    def fallback_count(self) -> int:
-        c = C.c_int32()
-        self._check(self.lib.phx_moe_fallback_count(self.h, C.byref(c)))
-        return c.value
+    def stream_read_ms(self, buf: "DeviceBuffer", iters: int = 20) -> float:
+        ms = C.c_double()
+        self._check(self.lib.phx_moe_stream_read(self.h, buf.ptr, buf.nbytes, iters, C.byref(ms)))
+        return ms.value
+
+    def stack_run_device(self, x_ptr: int, T: int):
+        """Replay the captured stack on a device-resident x (async; sync() waits)."""
+        self._check(self.lib.phx_moe_stack_run(self.h, x_ptr, T, PHX.FLAG_DEVICE_PTRS | PHX.FLAG_ASYNC))
+
+    def fallback_counts(self) -> tuple[int, int]:
+        """(norm sums re-summed sequentially, decode tokens routed through the exact router)"""
+        c = (C.c_int32 * 2)()
+        self._check(self.lib.phx_moe_fallback_count(self.h, c))
+        return c[0], c[1]
