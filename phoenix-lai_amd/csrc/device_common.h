@@ -161,6 +161,78 @@ __device__ __forceinline__ float half_max_f(float v)
     return (threadIdx.x & 32) ? b : a;
 }
 
+// Maximum over the 64 lanes of an unsigned 64-bit key (returned to every lane).
+__device__ __forceinline__ bool u64_gt(unsigned hi_a, unsigned lo_a, unsigned hi_b, unsigned lo_b)
+{
+    return hi_a > hi_b || (hi_a == hi_b && lo_a > lo_b);
+}
+template <int CTRL, int ROWMASK = 0xf>
+__device__ __forceinline__ void u64_max_step(unsigned& hi, unsigned& lo)
+{
+    const unsigned ohi = (unsigned)dpp_i<CTRL, ROWMASK>((int)hi, (int)hi);
+    const unsigned olo = (unsigned)dpp_i<CTRL, ROWMASK>((int)lo, (int)lo);
+    if (u64_gt(ohi, olo, hi, lo)) { hi = ohi; lo = olo; }
+}
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v)
+{
+    unsigned hi = (unsigned)(v >> 32), lo = (unsigned)v;
+    u64_max_step<0xb1>(hi, lo);
+    u64_max_step<0x4e>(hi, lo);
+    u64_max_step<0x141>(hi, lo);
+    u64_max_step<0x140>(hi, lo);
+    u64_max_step<0x142, 0xa>(hi, lo);
+    u64_max_step<0x143, 0xc>(hi, lo);
+    hi = (unsigned)__builtin_amdgcn_readlane((int)hi, 63);
+    lo = (unsigned)__builtin_amdgcn_readlane((int)lo, 63);
+    return ((unsigned long long)hi << 32) | lo;
+}
+
+// Maximum over the 64 lanes of an unsigned 32-bit value, returned to every lane.
+__device__ __forceinline__ unsigned wave_max_u32(unsigned v)
+{
+    v = max(v, (unsigned)dpp_i<0xb1>((int)v, (int)v));
+    v = max(v, (unsigned)dpp_i<0x4e>((int)v, (int)v));
+    v = max(v, (unsigned)dpp_i<0x141>((int)v, (int)v));
+    v = max(v, (unsigned)dpp_i<0x140>((int)v, (int)v));
+    v = max(v, (unsigned)dpp_i<0x142, 0xa>((int)v, (int)v));
+    v = max(v, (unsigned)dpp_i<0x143, 0xc>((int)v, (int)v));
+    return (unsigned)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+// Maximum over the 64 lanes of a double (NaN-free inputs), returned to every lane.
+__device__ __forceinline__ double wave_max_dpp(double v)
+{
+    v = fmax(v, dpp_d<0xb1>(v, v));
+    v = fmax(v, dpp_d<0x4e>(v, v));
+    v = fmax(v, dpp_d<0x141>(v, v));
+    v = fmax(v, dpp_d<0x140>(v, v));
+    v = fmax(v, dpp_d<0x142, 0xa>(v, v));
+    v = fmax(v, dpp_d<0x143, 0xc>(v, v));
+    const long long t = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_readlane((int)t, 63), hi = __builtin_amdgcn_readlane((int)(t >> 32), 63);
+    return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
+
+// Inclusive prefix sum over the 64 lanes (row shifts within 16-lane rows, then row broadcasts).
+__device__ __forceinline__ double wave_incl_scan_dpp(double v)
+{
+    v += dpp_d<0x111>(0.0, v);  // row_shr:1
+    v += dpp_d<0x112>(0.0, v);  // row_shr:2
+    v += dpp_d<0x114>(0.0, v);  // row_shr:4
+    v += dpp_d<0x118>(0.0, v);  // row_shr:8
+    v += dpp_d<0x142, 0xa>(0.0, v);  // row_bcast:15 into rows 1 and 3
+    v += dpp_d<0x143, 0xc>(0.0, v);  // row_bcast:31 into rows 2 and 3
+    return v;
+}
+
+// Order-preserving map of a float to uint32 (NaN to 0, below every number).
+__device__ __forceinline__ unsigned sortable_f32(float f)
+{
+    if (f != f) return 0u;
+    const unsigned b = __float_as_uint(f);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
 // sum over the 64 lanes of a wave (butterfly: every lane ends with the same value)
 __device__ __forceinline__ double wave_sum_d(double v)
 {

@@ -62,6 +62,8 @@ struct RouteDecArgs {
 };
 
 constexpr int RT_PER = 64;        // elements per lane (d <= 4096)
+typedef __attribute__((address_space(3))) void* lds_void_t;
+typedef __attribute__((address_space(1))) void* glb_void_t;
 
 __device__ __forceinline__ double ld_agent(const double* p)
 {
@@ -76,13 +78,13 @@ __device__ __forceinline__ void st_agent(double* p, double v)
 }
 
 // exact reference logit of expert e for token t (src/GemmaCpu.cs:389-395)
-__device__ float exact_logit(const RouteDecArgs& a, int t, int e, float rinv, float sc)
+__device__ float exact_logit(const float* x, const float* W, const float* gis, int d, int t, int e, float rinv, float sc)
 {
-    const float* xr = a.x + (int64_t)t * a.d;
-    const float* wr = a.W + (int64_t)e * a.d;
+    const float* xr = x + (int64_t)t * d;
+    const float* wr = W + (int64_t)e * d;
     float s = 0.0f;
-    for (int i = 0; i < a.d; i += 4) {
-        const float4 xv = *(const float4*)(xr + i), gv = *(const float4*)(a.gis + i), wv = *(const float4*)(wr + i);
+    for (int i = 0; i < d; i += 4) {
+        const float4 xv = *(const float4*)(xr + i), gv = *(const float4*)(gis + i), wv = *(const float4*)(wr + i);
         s += wv.x * (xv.x * rinv * sc * gv.x);
         s += wv.y * (xv.y * rinv * sc * gv.y);
         s += wv.z * (xv.z * rinv * sc * gv.z);
@@ -108,44 +110,44 @@ __global__ __launch_bounds__(256) void k_route_dec(RouteDecArgs a)
     float* sx = (float*)rsm;
     float* sg = sx + d;
     float* sw = sg + d;  // [4][d]
+    const float* spre2 = sw + 4 * d;
+    const float* sfnorm = spre2 + d;
     {
-        const float4* x4 = (const float4*)xr;
-        const float4* g4 = (const float4*)a.gis;
-        for (int i = tid; i < d / 4; i += 256) {
-            ((float4*)sx)[i] = x4[i];
-            ((float4*)sg)[i] = g4[i];
+        // direct global -> LDS loads (global_load_lds_dwordx4): every load in flight at once, no
+        // registers; each wave fills 64 consecutive float4 of an array per instruction
+        const int n4 = d / 4;
+        const float4* srcs[8] = {(const float4*)xr, (const float4*)a.gis,
+                                 (const float4*)(a.W + (int64_t)min(blockIdx.x * 4 + 0, a.E - 1) * d),
+                                 (const float4*)(a.W + (int64_t)min(blockIdx.x * 4 + 1, a.E - 1) * d),
+                                 (const float4*)(a.W + (int64_t)min(blockIdx.x * 4 + 2, a.E - 1) * d),
+                                 (const float4*)(a.W + (int64_t)min(blockIdx.x * 4 + 3, a.E - 1) * d),
+                                 (const float4*)a.pre2, (const float4*)(a.fnorm ? a.fnorm : a.pre2)};
+#pragma unroll
+        for (int r = 0; r < 8; r++) {
+            float4* dst = (float4*)(sx + r * d);
+            for (int q = 0; q * 256 < n4; q++) {
+                const int i = q * 256 + tid;
+                if (i < n4)
+                    __builtin_amdgcn_global_load_lds((glb_void_t)(srcs[r] + i), (lds_void_t)(dst + q * 256 + wave * 64), 16, 0,
+                                                     0);
+            }
         }
-        for (int w = 0; w < 4; w++) {
-            const int ew = min(blockIdx.x * 4 + w, a.E - 1);
-            const float4* w4 = (const float4*)(a.W + (int64_t)ew * d);
-            for (int i = tid; i < d / 4; i += 256) ((float4*)(sw + w * d))[i] = w4[i];
-        }
+        __builtin_amdgcn_s_waitcnt(0);
     }
     __syncthreads();
-    // ---- the lane's contiguous chunk (d % 256 == 0: per = d / 64, a multiple of 4)
+    // ---- the lane's contiguous chunk (d % 256 == 0: per = d / 64, a multiple of 4), read from LDS
     const int per = d / 64, c0 = lane * per;
-    float xv[RT_PER], gv[RT_PER], wv[RT_PER];
-#pragma unroll
-    for (int j = 0; j < RT_PER; j += 4) {
-        if (j < per) {
-            const float4 a4 = *(const float4*)(sx + c0 + j), b4 = *(const float4*)(sg + c0 + j),
-                         c4 = *(const float4*)(sw + wave * d + c0 + j);
-            xv[j] = a4.x; xv[j + 1] = a4.y; xv[j + 2] = a4.z; xv[j + 3] = a4.w;
-            gv[j] = b4.x; gv[j + 1] = b4.y; gv[j + 2] = b4.z; gv[j + 3] = b4.w;
-            wv[j] = c4.x; wv[j + 1] = c4.y; wv[j + 2] = c4.z; wv[j + 3] = c4.w;
-        } else {
-            xv[j] = xv[j + 1] = xv[j + 2] = xv[j + 3] = 0.0f;
-            gv[j] = gv[j + 1] = gv[j + 2] = gv[j + 3] = 0.0f;
-            wv[j] = wv[j + 1] = wv[j + 2] = wv[j + 3] = 0.0f;
-        }
-    }
-    const int c1 = c0 + per;
     // certified mean of squares of x (every wave of the token computes the same value)
     double s = 0.0;
 #pragma unroll
-    for (int j = 0; j < RT_PER; j++) {
-        const double v = (double)xv[j];
-        s += v * v;
+    for (int j = 0; j < RT_PER; j += 4) {
+        if (j < per) {
+            const float4 a4 = *(const float4*)(sx + c0 + j);
+            s += (double)a4.x * (double)a4.x;
+            s += (double)a4.y * (double)a4.y;
+            s += (double)a4.z * (double)a4.z;
+            s += (double)a4.w * (double)a4.w;
+        }
     }
     const double S = wave_sum_dpp(s);
     const double Bs = ((double)a.d + per + 64.0) * 0x1p-53 * S * 2.0;
@@ -160,28 +162,34 @@ __global__ __launch_bounds__(256) void k_route_dec(RouteDecArgs a)
     }
     const float rinv = rms_scale_from_mean(mean, a.eps);  // also the RmsNorm scale of x
     if (e < a.E) {
+        // p_i = fl(W[e][i] * m_i), m_i = ((x_i * rinv) * sc) * s_i (src/GemmaCpu.cs:389,394)
+        float pv[RT_PER];
         double loc = 0.0, P = 0.0;
 #pragma unroll
-        for (int j = 0; j < RT_PER; j++) {
-            const float m = xv[j] * rinv * sc * gv[j];
-            const float p = wv[j] * m;
-            xv[j] = p;
-            loc += (double)p;
-            P += fabs((double)p);
-        }
-        double inc = loc;
+        for (int j = 0; j < RT_PER; j += 4) {
+            if (j < per) {
+                const float4 a4 = *(const float4*)(sx + c0 + j), b4 = *(const float4*)(sg + c0 + j),
+                             c4 = *(const float4*)(sw + wave * d + c0 + j);
+                pv[j] = c4.x * (a4.x * rinv * sc * b4.x);
+                pv[j + 1] = c4.y * (a4.y * rinv * sc * b4.y);
+                pv[j + 2] = c4.z * (a4.z * rinv * sc * b4.z);
+                pv[j + 3] = c4.w * (a4.w * rinv * sc * b4.w);
 #pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const double y = __shfl_up(inc, o, 64);
-            if (lane >= o) inc += y;
+                for (int u = 0; u < 4; u++) {
+                    loc += (double)pv[j + u];
+                    P += fabs((double)pv[j + u]);
+                }
+            } else {
+                pv[j] = pv[j + 1] = pv[j + 2] = pv[j + 3] = 0.0f;
+            }
         }
-        double acc = __shfl_up(inc, 1, 64);
-        if (lane == 0) acc = 0.0;
+        const double inc = wave_incl_scan_dpp(loc);
+        double acc = inc - loc;  // exclusive prefix (exact up to the double rounding the bound allows for)
         double A = 0.0;
 #pragma unroll
         for (int j = 0; j < RT_PER; j++) {
-            if (c0 + j < c1) {
-                acc += (double)xv[j];
+            if (j < per) {
+                acc += (double)pv[j];
                 A += fabs(acc);
             }
         }
@@ -200,16 +208,21 @@ __global__ __launch_bounds__(256) void k_route_dec(RouteDecArgs a)
         for (int b = blockIdx.x * 8 + half; b < nbK; b += gridDim.x * 8) {
             const int i = b * 32 + l32;
             for (int which = 0; which < 2; which++) {
-                const float* nw = which ? a.fnorm : a.pre2;
-                if (!nw) continue;
-                const Act& act = which ? a.act_sh : a.act_gu;
+                if (which && !a.fnorm) continue;
+                const float* nw = which ? sfnorm : spre2;
+                int8_t* aq = which ? a.act_sh.q : a.act_gu.q;
+                float* ad = which ? a.act_sh.d : a.act_gu.d;
+                int* as = which ? a.act_sh.s : a.act_gu.s;
+                const int64_t qs = which ? a.act_sh.qstride : a.act_gu.qstride;
+                const int dstr = which ? a.act_sh.dstride : a.act_gu.dstride;
+                const int sstr = which ? a.act_sh.sstride : a.act_gu.sstride;
                 float dval;
                 int sum;
                 const int q = q8_0_half(sx[i] * rinv * nw[i], &dval, &sum);
-                act.q[(int64_t)t * act.qstride + i] = (int8_t)q;
+                aq[(int64_t)t * qs + i] = (int8_t)q;
                 if (l32 == 0) {
-                    act.d[(int64_t)t * act.dstride + b] = dval;
-                    act.s[(int64_t)t * act.sstride + b] = sum;
+                    ad[(int64_t)t * dstr + b] = dval;
+                    as[(int64_t)t * sstr + b] = sum;
                 }
             }
         }
@@ -238,32 +251,72 @@ __global__ __launch_bounds__(256) void k_route_dec(RouteDecArgs a)
     }
     if (tid < 16) s_bad[tid] = 0;
     __syncthreads();
-    // rank of every (token, expert) under (L desc, index asc); NaN ranks last
-    for (int i = tid; i < TE; i += 256) {
-        const int tt = i / a.E, ex = i - tt * a.E;
-        const double my = sel_key(sL[i]);
-        int r = 0;
-        const double* row = sL + tt * a.E;
-#pragma unroll 16
-        for (int b = 0; b < a.E; b++) r += sel_beats(sel_key(row[b]), b, my, ex);
-        s_rank[i] = (short)r;
-        if (!(isfinite(sL[i]) && isfinite(sB[i]))) s_bad[tt] = 1;
-    }
-    __syncthreads();
-    // certification: each chosen expert's lower end above every later-ranked expert's upper end
-    for (int i = tid; i < TE; i += 256) {
-        const int tt = i / a.E;
-        const int r = s_rank[i];
-        if (r < a.k) {
-            const double lo = sL[i] - sB[i];
-            bool ok = true;
-#pragma unroll 16
-            for (int b = 0; b < a.E; b++) {
-                const int j = tt * a.E + b;
-                ok &= !(s_rank[j] > r) || lo > sL[j] + sB[j];
-            }
-            if (!ok) s_bad[tt] = 1;
+    // selection per token (wave w: tokens w, w+4, ...): k rounds of a wave maximum of the sortable
+    // (float)L, the lowest index among equal keys (ballot); then the order is certified if each
+    // chosen expert's lower end lies above the upper ends of every expert ranked after it.  Ranking
+    // by (float)L is safe: logits that round alike have overlapping intervals, so such an order is
+    // never certified and goes to the exact path below.
+    for (int tt = wave; tt < a.T; tt += 4) {
+        const double* Lr = sL + tt * a.E;
+        const double* Br = sB + tt * a.E;
+        unsigned key[4];
+        double lo[4], hi[4];
+        bool valid[4], fin = true;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int ex = lane + 64 * q;
+            valid[q] = ex < a.E;
+            const double Lq = valid[q] ? Lr[ex] : 0.0, Bq = valid[q] ? Br[ex] : 0.0;
+            if (valid[q] && !(isfinite(Lq) && isfinite(Bq))) fin = false;
+            key[q] = valid[q] ? sortable_f32((float)Lq) + 1u : 0u;  // +1: every valid key beats "taken" (0)
+            lo[q] = Lq - Bq;
+            hi[q] = Lq + Bq;
         }
+        int chosen[PHX_MAX_USED_DEV];
+        for (int j = 0; j < a.k; j++) {
+            unsigned mk = 0u;
+#pragma unroll
+            for (int q = 0; q < 4; q++) mk = max(mk, key[q]);
+            mk = wave_max_u32(mk);
+            int ej = -1;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const unsigned long long m = __ballot(key[q] == mk && mk != 0u);
+                if (ej < 0 && m) ej = (__ffsll((long long)m) - 1) + 64 * q;  // lowest index first
+            }
+            if (ej < 0) ej = 0;
+            chosen[j] = ej;
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                if (lane + 64 * q == ej) key[q] = 0u;
+        }
+        // certification
+        double hmax = -INFINITY;
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            if (valid[q] && key[q] != 0u) hmax = fmax(hmax, hi[q]);
+        hmax = wave_max_dpp(hmax);
+        bool cert = __all(fin);
+        double suffix = hmax;
+        for (int j = a.k - 1; j >= 0; j--) {
+            const int ej = chosen[j], ln = ej & 63, q = ej >> 6;
+            const double lq = q == 0 ? lo[0] : q == 1 ? lo[1] : q == 2 ? lo[2] : lo[3];
+            const double hq = q == 0 ? hi[0] : q == 1 ? hi[1] : q == 2 ? hi[2] : hi[3];
+            const long long lb = __double_as_longlong(lq), hb = __double_as_longlong(hq);
+            const double lo_j = __longlong_as_double(((long long)__builtin_amdgcn_readlane((int)(lb >> 32), ln) << 32) |
+                                                     (unsigned)__builtin_amdgcn_readlane((int)lb, ln));
+            const double hi_j = __longlong_as_double(((long long)__builtin_amdgcn_readlane((int)(hb >> 32), ln) << 32) |
+                                                     (unsigned)__builtin_amdgcn_readlane((int)hb, ln));
+            if (!(lo_j > suffix)) cert = false;
+            suffix = fmax(suffix, hi_j);
+        }
+        // ranks for the code below: chosen j -> j, the others k + 1
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            if (valid[q]) s_rank[tt * a.E + lane + 64 * q] = (short)(a.k + 1);
+        for (int j = 0; j < a.k; j++)
+            if (lane == 0) s_rank[tt * a.E + chosen[j]] = (short)j;
+        if (lane == 0) s_bad[tt] = !cert;
     }
     __syncthreads();
     // uncertified tokens: exact chains for every expert that can reach the chosen ones
@@ -283,7 +336,7 @@ __global__ __launch_bounds__(256) void k_route_dec(RouteDecArgs a)
             const int j = tt * a.E + b;
             const bool amb = nonfinite || s_rank[j] < a.k || sL[j] + sB[j] >= minlo;
             s_amb[j] = amb;
-            if (amb) sL[j] = (double)exact_logit(a, tt, b, rinv_t, sc);  // the others cannot be chosen
+            if (amb) sL[j] = (double)exact_logit(a.x, a.W, a.gis, a.d, tt, b, rinv_t, sc);  // the others cannot be chosen
         }
         __syncthreads();
         for (int b = tid; b < a.E; b += 256) {
@@ -381,10 +434,10 @@ void launch_route_dec(hipStream_t st, const RouteDecArgsH& h)
 {
     RouteDecArgs a{h.T, h.d, h.E, h.k, h.rule, h.A, h.max_tiles, h.eps, h.x, h.W, h.gis, h.ds, h.pre2, h.fnorm, h.act_gu,
                    h.act_sh, h.Lb, h.Bb, h.counter, h.ids, h.w, h.logits, h.offsets, h.perm, h.tiles, h.ntiles, h.flags};
-    const size_t lds = std::max((size_t)6 * h.d * sizeof(float), (size_t)kRouteMaxTE * 19);
+    const size_t lds = std::max((size_t)8 * h.d * sizeof(float), (size_t)kRouteMaxTE * 19);
     static bool attr = false;
     if (!attr) {
-        (void)hipFuncSetAttribute((const void*)k_route_dec, hipFuncAttributeMaxDynamicSharedMemorySize, 6 * 4096 * 4);
+        (void)hipFuncSetAttribute((const void*)k_route_dec, hipFuncAttributeMaxDynamicSharedMemorySize, 8 * 4096 * 4);
         attr = true;
     }
     hipLaunchKernelGGL(k_route_dec, dim3((h.E + 3) / 4, h.T), dim3(256), lds, st, a);
@@ -436,7 +489,7 @@ __global__ __launch_bounds__(DEC_NT) void k_dec_mm(DecArgs a)
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     constexpr int PAY = TYPE == PHX_Q4_0_DEV ? 16 : 32;
 
-    int which, rgi, e, cnt;
+    int which, rgi, e, cnt, start = -1;
     int orow[DEC_A], arow[DEC_A];
     const int nexp = a.max_tiles * a.m0.rg;
     if ((int)blockIdx.x < nexp) {
@@ -447,11 +500,7 @@ __global__ __launch_bounds__(DEC_NT) void k_dec_mm(DecArgs a)
         if (tl.e < 0) return;  // slot past the last tile
         e = tl.e;
         cnt = min(tl.cnt, DEC_A);
-#pragma unroll
-        for (int i = 0; i < DEC_A; i++) {
-            orow[i] = i < cnt ? a.perm[tl.start + i] : 0;
-            arow[i] = orow[i] / a.act_div;
-        }
+        start = tl.start;
     } else {
         which = 1;
         const int sid = blockIdx.x - nexp;
@@ -480,6 +529,14 @@ __global__ __launch_bounds__(DEC_NT) void k_dec_mm(DecArgs a)
 #pragma unroll
             for (int c = 0; c < PAY / 16; c++) wv[j][c] = src[c];
             dwh[j] = ws[(int64_t)(b0 + j) * 64];
+        }
+    }
+    // the tile's assignment rows (expert tiles), read while the weights are in flight
+    if (start >= 0) {
+#pragma unroll
+        for (int i = 0; i < DEC_A; i++) {
+            orow[i] = i < cnt ? a.perm[start + i] : 0;
+            arow[i] = orow[i] / a.act_div;
         }
     }
     // ---- per-block terms of every assignment
