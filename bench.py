@@ -9,9 +9,10 @@ command buffer per decode pass, src/GemmaGpu.cs:544-554); every replay starts fr
 input, so the experts touched change from replay to replay and the 256 MB MALL cannot serve them.
 
 Prints one JSON line: value = tokens/s through the layer (inputs resident in HBM), a roofline
-object for the dominant kernel (the grouped gate|up product, HIP-event durations from an
-instrumented eager pass of the same workload) and the CPU baseline (the C restatement of the
-reference CPU path timed on this host's cores over a bounded sample).
+object for the dominant kernel (the grouped gate|up product; its average execution interval from
+HIP events that the runtime stamps at kernel start and end, over an instrumented eager pass of the
+same workload) and the CPU baseline (the C restatement of the reference CPU path timed on this
+host's cores over a bounded sample).
 """
 from __future__ import annotations
 
@@ -53,11 +54,12 @@ def cpu_baseline(pkg, L, cfg_name, T, budget_s=12.0):
     from oracle import oracle as orc
     threads = min(16, os.cpu_count() or 1)
     S = pkg.synth
-    x = S.make_input(cfg_name, T=max(T, 64), seed=4242, name="cpu.x")
+    pool = 1024  # distinct tokens; the sample cycles through them until the time budget is spent
+    x = S.make_input(cfg_name, T=pool, seed=4242, name="cpu.x")
     orc.moe_block(L, x[:1], nthreads=threads)  # warm-up
     n, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < budget_s and n < x.shape[0]:
-        orc.moe_block(L, x[n:n + 1], nthreads=threads)
+    while time.perf_counter() - t0 < budget_s:
+        orc.moe_block(L, x[n % pool:n % pool + 1], nthreads=threads)
         n += 1
     dt = time.perf_counter() - t0
     return {"value": round(n / dt, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
@@ -117,12 +119,17 @@ def run_decode(args, pkg):
     avg_experts = distinct / prof_steps
     gu_ms = prof["gate_up"][0] / max(1, prof["gate_up"][1])
     dn_ms = prof["down"][0] / max(1, prof["down"][1])
-    gu_bytes = avg_experts * gu_b
-    achieved = gu_bytes / (gu_ms * 1e-3) / 1e9
-    layer_expert_bytes = avg_experts * (gu_b + dn_b)
-    sh_bytes = 0
+    # the decode path's gate|up launch also computes the dense shared FFN's gate and up rows, and its
+    # down launch the shared down rows: their weights are part of those launches' algorithmic bytes
+    sh_gu_b = sh_dn_b = 0
     if L.get("n_ff_shared"):
-        sh_bytes = 3 * L["n_ff_shared"] * S.row_bytes(L["shared_type"], d)
+        sh_gu_b = 2 * L["n_ff_shared"] * S.row_bytes(L["shared_type"], d)
+        sh_dn_b = d * S.row_bytes(L["shared_type"], L["n_ff_shared"])
+    sh_bytes = sh_gu_b + sh_dn_b
+    gu_bytes = avg_experts * gu_b + sh_gu_b
+    achieved = gu_bytes / (gu_ms * 1e-3) / 1e9
+    dn_bytes = avg_experts * dn_b + sh_dn_b
+    layer_expert_bytes = avg_experts * (gu_b + dn_b)
     router_bytes = L["n_expert"] * d * 4
 
     # ---- measured streaming-read rate of this box (2 GiB, coalesced 128-bit loads)
@@ -163,7 +170,8 @@ def run_decode(args, pkg):
             "traffic": None,
             "bytes_per_launch": int(gu_bytes),
             "avg_launch_us": round(gu_ms * 1e3, 3),
-            "per_unit": f"{gu_b} B of gate|up weights per touched expert x {avg_experts:.2f} experts per launch",
+            "per_unit": f"{gu_b} B of gate|up weights per touched expert x {avg_experts:.2f} experts per launch"
+                        + (f" + {sh_gu_b} B of shared-FFN gate and up weights" if sh_gu_b else ""),
         },
         "layer": {
             "expert_bytes_per_step": int(layer_expert_bytes),
@@ -171,15 +179,37 @@ def run_decode(args, pkg):
             "all_bytes_gbs": round((layer_expert_bytes + sh_bytes + router_bytes) / (ms_per_step * 1e-3) / 1e9, 1),
             "expert_gbs_frac_of_peak": round(layer_expert_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "down_avg_us": round(dn_ms * 1e3, 3),
+            "down_gbs": round(dn_bytes / (dn_ms * 1e-3) / 1e9, 1),
             "kernels": kernels,
             "stream_read_gbs_measured": round(stream_gbs, 1),
         },
     }
+    if args.calibrate:
+        line["calibration"] = calibration_kernels(ctx)
     if not args.no_cpu:
         log("[bench] CPU baseline ...")
         line["cpu_baseline"] = cpu_baseline(pkg, L, cfg_name, T, args.cpu_seconds)
     ctx.close()
     return line
+
+
+def calibration_kernels(ctx, mib=1024):
+    """Kernels of known traffic for scaling the PMC byte counters (FETCH_SIZE, WRITE_SIZE): one
+    streaming read of `mib` MiB through the library, and one device copy of `mib` MiB (torch's copy
+    kernel: `mib` MiB read and `mib` MiB written)."""
+    import torch
+    n = mib << 20
+    buf = ctx.alloc(n)
+    ctx.stream_read_ms(buf, 2)
+    buf.free()
+    src = torch.ones(n // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    return {"stream_read_bytes": n, "copy_read_bytes": n, "copy_write_bytes": n,
+            "kernels": ["phx::k_stream_read", "torch elementwise copy"]}
 
 
 def qname(t):
@@ -197,6 +227,7 @@ def main():
     ap.add_argument("--prof-steps", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--calibrate", action="store_true", help="also run the PMC calibration kernels")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(f"bench.py: this build runs on one GPU only (the MoE path shards by experts across GPUs by design, "

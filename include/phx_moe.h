@@ -147,8 +147,10 @@ int phx_moe_dev_free(phx_moe_ctx* ctx, void* ptr);
 int phx_moe_memcpy_h2d(phx_moe_ctx* ctx, void* dst, const void* src, uint64_t bytes);
 int phx_moe_memcpy_d2h(phx_moe_ctx* ctx, void* dst, const void* src, uint64_t bytes);
 
-/* Per-kernel timing with HIP events on the library's stream (the Gpu.cs:163-171 profiling
- * counterpart).  Kinds: */
+/* Per-kernel timing on the library's stream (the Gpu.cs:163-171 profiling counterpart).  While
+ * enabled, every kernel is launched with start/stop events stamped with its own execution interval
+ * (hipExtLaunchKernel), the interval a kernel-trace profiler reports.  profile_read returns, per kind,
+ * the summed kernel time (ms) and the number of calls that launched that kind.  Kinds: */
 #define PHX_K_PROLOGUE 0
 #define PHX_K_ROUTER 1
 #define PHX_K_TOPK 2

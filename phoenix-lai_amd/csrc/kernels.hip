@@ -126,7 +126,7 @@ void launch_prologue(hipStream_t st, int T, int d, float eps, const float* x, co
 {
     int cols = act_gu.cols > act_sh.cols ? act_gu.cols : act_sh.cols;
     if (cols < d) cols = d;
-    hipLaunchKernelGGL(k_prologue<256>, dim3(T), dim3(256), (size_t)cols * sizeof(float), st, d, eps, x, gis, pre2,
+    launch(k_prologue<256>, dim3(T), dim3(256), (size_t)cols * sizeof(float), st, d, eps, x, gis, pre2,
                        ffn_norm, router_in, xscale, act_gu, act_sh, flags);
 }
 
@@ -157,7 +157,7 @@ __global__ __launch_bounds__(64) void k_router_exact(int d, int E, const float4*
 
 void launch_router_exact(hipStream_t st, int T, int d, int E, const float* wt4, const float* rin, float* logits)
 {
-    hipLaunchKernelGGL(k_router_exact, dim3((E + 63) / 64, T), dim3(64), 0, st, d, E, (const float4*)wt4, rin, logits);
+    launch(k_router_exact, dim3((E + 63) / 64, T), dim3(64), 0, st, d, E, (const float4*)wt4, rin, logits);
 }
 
 // ------------------------------------------------------------------------------ top-k and weights
@@ -217,7 +217,7 @@ __global__ __launch_bounds__(64) void k_topk(int E, int k, int rule, const float
 
 void launch_topk(hipStream_t st, int T, int E, int k, int rule, const float* logits, const float* ds, int* ids, float* w)
 {
-    hipLaunchKernelGGL(k_topk, dim3(T), dim3(64), 0, st, E, k, rule, logits, ds, ids, w);
+    launch(k_topk, dim3(T), dim3(64), 0, st, E, k, rule, logits, ds, ids, w);
 }
 
 // ------------------------------------------------------------------------------ dispatch
@@ -296,7 +296,7 @@ void launch_dispatch(hipStream_t st, int n, int E, int A, const int* ids, int* o
                      int* ntiles)
 {
     int nch = dispatch_chunks(n, E);
-    hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(256), (size_t)E * nch * sizeof(uint16_t), st, n, E, A, ids, offsets,
+    launch(k_dispatch, dim3(1), dim3(256), (size_t)E * nch * sizeof(uint16_t), st, n, E, A, ids, offsets,
                        perm, tiles, ntiles);
 }
 
@@ -543,10 +543,10 @@ void launch_grouped(hipStream_t st, const QMat& w, Act act, const Tile* tiles, c
     dim3 grid(max_tiles, (w.rg + 3) / 4);
     if (A != 4) A = 4;  // the tile size the dispatch used; one instantiation for now
     switch (w.type) {
-    case PHX_Q4_0_DEV: hipLaunchKernelGGL((k_grouped_q<PHX_Q4_0_DEV, 4>), grid, dim3(256), 0, st, g); break;
-    case PHX_Q8_0_DEV: hipLaunchKernelGGL((k_grouped_q<PHX_Q8_0_DEV, 4>), grid, dim3(256), 0, st, g); break;
-    case PHX_Q4_K_DEV: hipLaunchKernelGGL((k_grouped_k<PHX_Q4_K_DEV, 4>), grid, dim3(256), 0, st, g); break;
-    case PHX_Q6_K_DEV: hipLaunchKernelGGL((k_grouped_k<PHX_Q6_K_DEV, 4>), grid, dim3(256), 0, st, g); break;
+    case PHX_Q4_0_DEV: launch((k_grouped_q<PHX_Q4_0_DEV, 4>), grid, dim3(256), 0, st, g); break;
+    case PHX_Q8_0_DEV: launch((k_grouped_q<PHX_Q8_0_DEV, 4>), grid, dim3(256), 0, st, g); break;
+    case PHX_Q4_K_DEV: launch((k_grouped_k<PHX_Q4_K_DEV, 4>), grid, dim3(256), 0, st, g); break;
+    case PHX_Q6_K_DEV: launch((k_grouped_k<PHX_Q6_K_DEV, 4>), grid, dim3(256), 0, st, g); break;
     }
 }
 
@@ -567,7 +567,7 @@ __global__ __launch_bounds__(256) void k_requant(int nf, const float* __restrict
 
 void launch_requant(hipStream_t st, int rows, int nf, const float* g, const float* u, const float* tab, Act act)
 {
-    hipLaunchKernelGGL(k_requant, dim3(rows), dim3(256), (size_t)act.cols * sizeof(float), st, nf, g, u, tab, act);
+    launch(k_requant, dim3(rows), dim3(256), (size_t)act.cols * sizeof(float), st, nf, g, u, tab, act);
 }
 
 // ------------------------------------------------------------------------------ combine, norms, residual
@@ -611,7 +611,7 @@ __global__ __launch_bounds__(256) void k_combine(int d, int k, float eps, const 
 void launch_combine(hipStream_t st, int T, int d, int k, float eps, const float* yd, const float* w, const float* shared,
                     const float* post1, const float* post2, float* out, float* xres, const float* post_ffw, int* flags)
 {
-    hipLaunchKernelGGL(k_combine, dim3(T), dim3(256), (size_t)2 * d * sizeof(float), st, d, k, eps, yd, w, shared, post1,
+    launch(k_combine, dim3(T), dim3(256), (size_t)2 * d * sizeof(float), st, d, k, eps, yd, w, shared, post1,
                        post2, out, xres, post_ffw, flags);
 }
 
@@ -632,7 +632,7 @@ __global__ __launch_bounds__(256) void k_stream_read(const uint4* __restrict__ s
 
 void launch_stream_read(hipStream_t st, const void* src, int64_t bytes, uint32_t* sink)
 {
-    hipLaunchKernelGGL(k_stream_read, dim3(256 * 8), dim3(256), 0, st, (const uint4*)src, bytes / 16, sink);
+    launch(k_stream_read, dim3(256 * 8), dim3(256), 0, st, (const uint4*)src, bytes / 16, sink);
 }
 
 // ------------------------------------------------------------------------------ arithmetic self-test
@@ -657,7 +657,7 @@ __global__ void k_selftest(int op, int n, const float* __restrict__ a, const flo
 
 void launch_selftest(hipStream_t st, int op, int n, const float* a, const float* b, float* out, const float* tab)
 {
-    hipLaunchKernelGGL(k_selftest, dim3((n + 255) / 256), dim3(256), 0, st, op, n, a, b, out, tab);
+    launch(k_selftest, dim3((n + 255) / 256), dim3(256), 0, st, op, n, a, b, out, tab);
 }
 
 }  // namespace phx

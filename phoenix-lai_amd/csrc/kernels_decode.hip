@@ -440,7 +440,7 @@ void launch_route_dec(hipStream_t st, const RouteDecArgsH& h)
         (void)hipFuncSetAttribute((const void*)k_route_dec, hipFuncAttributeMaxDynamicSharedMemorySize, 8 * 4096 * 4);
         attr = true;
     }
-    hipLaunchKernelGGL(k_route_dec, dim3((h.E + 3) / 4, h.T), dim3(256), lds, st, a);
+    launch(k_route_dec, dim3((h.E + 3) / 4, h.T), dim3(256), lds, st, a);
 }
 
 // ------------------------------------------------------------------------------ grouped products (decode)
@@ -641,11 +641,11 @@ void launch_dec(hipStream_t st, int mode, const DecMatH& m0, const DecMatH& m1, 
     const int items = max_tiles * a.m0.rg + (a.m1.rg > 0 ? (T + DEC_A - 1) / DEC_A * a.m1.rg : 0);
     const bool q4 = m0.q->type == PHX_Q4_0_DEV;
     if (mode == 0) {
-        if (q4) hipLaunchKernelGGL((k_dec_mm<0, PHX_Q4_0_DEV>), dim3(items), dim3(DEC_NT), 0, st, a);
-        else hipLaunchKernelGGL((k_dec_mm<0, PHX_Q8_0_DEV>), dim3(items), dim3(DEC_NT), 0, st, a);
+        if (q4) launch((k_dec_mm<0, PHX_Q4_0_DEV>), dim3(items), dim3(DEC_NT), 0, st, a);
+        else launch((k_dec_mm<0, PHX_Q8_0_DEV>), dim3(items), dim3(DEC_NT), 0, st, a);
     } else {
-        if (q4) hipLaunchKernelGGL((k_dec_mm<1, PHX_Q4_0_DEV>), dim3(items), dim3(DEC_NT), 0, st, a);
-        else hipLaunchKernelGGL((k_dec_mm<1, PHX_Q8_0_DEV>), dim3(items), dim3(DEC_NT), 0, st, a);
+        if (q4) launch((k_dec_mm<1, PHX_Q4_0_DEV>), dim3(items), dim3(DEC_NT), 0, st, a);
+        else launch((k_dec_mm<1, PHX_Q8_0_DEV>), dim3(items), dim3(DEC_NT), 0, st, a);
     }
 }
 
@@ -727,7 +727,7 @@ void launch_combine_dec(hipStream_t st, int T, int d, int k, float eps, const fl
                         const float* shared, const float* post1, const float* post2, float* out, float* xres,
                         const float* post_ffw, int* flags)
 {
-    hipLaunchKernelGGL(k_combine_dec, dim3(T), dim3(CB_NT), (size_t)3 * d * sizeof(float), st, d, k, eps, yd, w, shared,
+    launch(k_combine_dec, dim3(T), dim3(CB_NT), (size_t)3 * d * sizeof(float), st, d, k, eps, yd, w, shared,
                        post1, post2, out, xres, post_ffw, flags);
 }
 

@@ -1,5 +1,6 @@
 // Internal types shared by the runtime (runtime.hip) and the gfx950 kernels (kernels.hip).
 #pragma once
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -13,6 +14,27 @@
 #define PHX_MAX_EXPERTS_DEV 256
 
 namespace phx {
+
+// Kernel timing hook.  While a context profiles, every launch carries a start and a stop event that
+// the runtime stamps with the kernel's own execution interval (hipExtLaunchKernel), the interval a
+// kernel-trace profiler reports, so dispatch latency is not counted; otherwise a plain launch.
+struct LaunchTimer {
+    virtual hipEvent_t event() = 0;
+    virtual void done(hipEvent_t start, hipEvent_t stop) = 0;
+};
+extern thread_local LaunchTimer* g_launch_timer;
+
+template <typename... KArgs, typename... Args>
+inline void launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, uint32_t lds, hipStream_t st, Args... args)
+{
+    if (LaunchTimer* t = g_launch_timer) {
+        hipEvent_t a = t->event(), b = t->event();
+        hipExtLaunchKernelGGL(kernel, grid, block, lds, st, a, b, 0u, args...);
+        t->done(a, b);
+    } else {
+        hipLaunchKernelGGL(kernel, grid, block, lds, st, args...);
+    }
+}
 
 constexpr int kRowGroup = 64;  // rows per interleaved row group: one wave64, lane = row
 

@@ -16,6 +16,10 @@
 
 using namespace phx;
 
+namespace phx {
+thread_local LaunchTimer* g_launch_timer = nullptr;
+}
+
 namespace {
 
 // ------------------------------------------------------------------------------ host fp16 (RNE)
@@ -256,7 +260,7 @@ struct phx_moe_ctx {
     std::vector<Pending> pending;
     std::vector<hipEvent_t> pool;
     double prof_ms[PHX_K_COUNT] = {};
-    int64_t prof_n[PHX_K_COUNT] = {};
+    int64_t prof_calls[PHX_K_COUNT] = {};
     // stack graph
     hipGraphExec_t graph_exec = nullptr;
     hipGraph_t graph = nullptr;
@@ -409,24 +413,27 @@ hipEvent_t get_event(phx_moe_ctx* c)
     return e;
 }
 
-struct ProfScope {
+// While profiling, the kernels launched inside a scope are timed one by one (their own execution
+// intervals, see LaunchTimer); a kind's time per call is the sum over its kernels.
+struct ProfScope : LaunchTimer {
     phx_moe_ctx* c;
     int kind;
-    hipEvent_t a = nullptr;
+    LaunchTimer* prev = nullptr;
+    bool on = false;
     ProfScope(phx_moe_ctx* c_, int k) : c(c_), kind(k)
     {
         if (c->profiling) {
-            a = get_event(c);
-            (void)hipEventRecord(a, c->stream);
+            on = true;
+            c->prof_calls[kind] += 1;
+            prev = g_launch_timer;
+            g_launch_timer = this;
         }
     }
+    hipEvent_t event() override { return get_event(c); }
+    void done(hipEvent_t a, hipEvent_t b) override { c->pending.push_back({kind, a, b}); }
     ~ProfScope()
     {
-        if (a) {
-            hipEvent_t b = get_event(c);
-            (void)hipEventRecord(b, c->stream);
-            c->pending.push_back({kind, a, b});
-        }
+        if (on) g_launch_timer = prev;
     }
 };
 
@@ -662,10 +669,7 @@ int drain_profile(phx_moe_ctx* c)
     HIPCHK(c, hipStreamSynchronize(c->stream));
     for (auto& p : c->pending) {
         float ms = 0.0f;
-        if (hipEventElapsedTime(&ms, p.a, p.b) == hipSuccess) {
-            c->prof_ms[p.kind] += ms;
-            c->prof_n[p.kind] += 1;
-        }
+        if (hipEventElapsedTime(&ms, p.a, p.b) == hipSuccess) c->prof_ms[p.kind] += ms;
         c->pool.push_back(p.a);
         c->pool.push_back(p.b);
     }
@@ -973,7 +977,7 @@ int phx_moe_profile(phx_moe_ctx* c, int enable)
     int rc = drain_profile(c);
     if (rc) return rc;
     c->profiling = enable != 0;
-    for (int i = 0; i < PHX_K_COUNT; i++) { c->prof_ms[i] = 0; c->prof_n[i] = 0; }
+    for (int i = 0; i < PHX_K_COUNT; i++) { c->prof_ms[i] = 0; c->prof_calls[i] = 0; }
     return PHX_OK;
 }
 
@@ -984,7 +988,7 @@ int phx_moe_profile_read(phx_moe_ctx* c, double* total_ms, int64_t* launches)
     if (rc) return rc;
     for (int i = 0; i < PHX_K_COUNT; i++) {
         if (total_ms) total_ms[i] = c->prof_ms[i];
-        if (launches) launches[i] = c->prof_n[i];
+        if (launches) launches[i] = c->prof_calls[i];
     }
     return PHX_OK;
 }

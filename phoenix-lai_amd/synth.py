@@ -133,8 +133,9 @@ def calibrated_bias(seed: int, E: int, k: int, kind: str, param: float) -> np.nd
 
 
 def make_layer(cfg: dict | str, layer: int = 0, weight_rule: int = 0, norms: str = "unit", seed: int | None = None,
-               with_post: bool = True) -> dict:
-    """One MoE layer (numpy arrays in GGUF byte layout) of a configuration."""
+               with_post: bool = True, experts: bool = True) -> dict:
+    """One MoE layer (numpy arrays in GGUF byte layout) of a configuration.  experts=False leaves out
+    the expert and shared-FFN weights (router-only uses); every other tensor is unchanged."""
     if isinstance(cfg, str):
         cfg = CONFIGS[cfg]
     seed = 1000 + cfg["idx"] if seed is None else seed
@@ -158,9 +159,10 @@ def make_layer(cfg: dict | str, layer: int = 0, weight_rule: int = 0, norms: str
     L["post_ffw_norm_2"] = vec("post_ffw_norm_2.weight", d)
     if with_post:
         L["post_ffw_norm"] = vec("post_ffw_norm.weight", d)
-    L["gate_up_exps"] = quantized_normal(seed, p + "ffn_gate_up_exps.weight", gu, E * 2 * nf, d, d)
-    L["down_exps"] = quantized_normal(seed, p + "ffn_down_exps.weight", dn, E * d, nf, dc)
-    if cfg.get("nff"):
+    if experts:
+        L["gate_up_exps"] = quantized_normal(seed, p + "ffn_gate_up_exps.weight", gu, E * 2 * nf, d, d)
+        L["down_exps"] = quantized_normal(seed, p + "ffn_down_exps.weight", dn, E * d, nf, dc)
+    if cfg.get("nff") and experts:
         nff, st = cfg["nff"], cfg["sh"]
         L["n_ff_shared"], L["shared_type"] = nff, st
         L["ffn_norm"] = vec("ffn_norm.weight", d)

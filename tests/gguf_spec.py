@@ -1,0 +1,118 @@
+"""Independent numpy decoders of the GGUF block layouts (the layout table of src/Gguf.cs:29-59 and
+the ggml block structs): Q4_0, Q8_0, Q4_K, Q6_K.  Written from the format, not from the oracle's
+code, so the oracle's bit-level decoding is checked against a second reading of the spec."""
+import numpy as np
+
+QK = 256
+
+
+def f16(u16):
+    return np.asarray(u16, np.uint16).view(np.float16).astype(np.float32)
+
+
+def dequant_q4_0(row: np.ndarray, cols: int) -> np.ndarray:
+    """block: fp16 d, 16 bytes; low nibble of byte j is element j, high nibble element j+16; (q-8)*d"""
+    b = row.reshape(cols // 32, 18)
+    d = f16(b[:, 0].astype(np.uint16) | (b[:, 1].astype(np.uint16) << 8))
+    qs = b[:, 2:]
+    q = np.concatenate([qs & 0x0F, qs >> 4], axis=1).astype(np.int32) - 8
+    return (q.astype(np.float32) * d[:, None]).reshape(-1)
+
+
+def dequant_q8_0(row: np.ndarray, cols: int) -> np.ndarray:
+    b = row.reshape(cols // 32, 34)
+    d = f16(b[:, 0].astype(np.uint16) | (b[:, 1].astype(np.uint16) << 8))
+    q = b[:, 2:].view(np.int8).astype(np.float32)
+    return (q * d[:, None]).reshape(-1)
+
+
+def q4_k_parts(blk: np.ndarray):
+    """(d, dmin, sc[8], m[8], q[256]) of one 144-byte Q4_K super-block.
+    scales: 12 bytes; sub-block j<4: sc = s[j] & 63, m = s[j+4] & 63; j>=4: sc = (s[j+4] & 15) | (s[j-4] >> 6) << 4,
+    m = (s[j+4] >> 4) | (s[j] >> 6) << 4.  qs: 4 chunks of 32 bytes, chunk c holds sub-blocks 2c (low nibbles)
+    and 2c+1 (high nibbles)."""
+    d = f16(int(blk[0]) | (int(blk[1]) << 8))
+    dmin = f16(int(blk[2]) | (int(blk[3]) << 8))
+    s = blk[4:16].astype(np.int32)
+    sc = np.zeros(8, np.int32)
+    m = np.zeros(8, np.int32)
+    for j in range(8):
+        if j < 4:
+            sc[j], m[j] = s[j] & 63, s[j + 4] & 63
+        else:
+            sc[j] = (s[j + 4] & 15) | ((s[j - 4] >> 6) << 4)
+            m[j] = (s[j + 4] >> 4) | ((s[j] >> 6) << 4)
+    qs = blk[16:144].reshape(4, 32).astype(np.int32)
+    q = np.empty(256, np.int32)
+    for c in range(4):
+        q[64 * c:64 * c + 32] = qs[c] & 15
+        q[64 * c + 32:64 * c + 64] = qs[c] >> 4
+    return d, dmin, sc, m, q
+
+
+def q6_k_parts(blk: np.ndarray):
+    """(d, sc[16], q[256] in -32..31) of one 210-byte Q6_K super-block: ql[128], qh[64], int8 scales[16],
+    fp16 d.  Per 128-element half (64 ql bytes L, 32 qh bytes H), element l of the four 32-runs is:
+    run 0 low nibble of L[l], run 1 low nibble of L[l+32], run 2 high nibble of L[l], run 3 high nibble
+    of L[l+32]; bits 4-5 come from H[l] at shifts 0, 2, 4, 6 for runs 0-3; the value is offset by -32."""
+    ql = blk[0:128].astype(np.int32)
+    qh = blk[128:192].astype(np.int32)
+    sc = blk[192:208].view(np.int8).astype(np.int32)
+    d = f16(int(blk[208]) | (int(blk[209]) << 8))
+    q = np.empty(256, np.int32)
+    for h in range(2):
+        L = ql[64 * h:64 * h + 64]
+        H = qh[32 * h:32 * h + 32]
+        for l in range(32):
+            q[128 * h + l] = (L[l] & 15) | (((H[l] >> 0) & 3) << 4)
+            q[128 * h + l + 32] = (L[l + 32] & 15) | (((H[l] >> 2) & 3) << 4)
+            q[128 * h + l + 64] = (L[l] >> 4) | (((H[l] >> 4) & 3) << 4)
+            q[128 * h + l + 96] = (L[l + 32] >> 4) | (((H[l] >> 6) & 3) << 4)
+    return d, sc, q - 32
+
+
+def dequant_q4_k(row: np.ndarray, cols: int) -> np.ndarray:
+    out = np.empty(cols, np.float32)
+    for b in range(cols // QK):
+        d, dmin, sc, m, q = q4_k_parts(row[144 * b:144 * b + 144])
+        sb = np.arange(256) // 32
+        out[QK * b:QK * b + QK] = (np.float32(d) * sc[sb].astype(np.float32) * q.astype(np.float32)
+                                   - np.float32(dmin) * m[sb].astype(np.float32))
+    return out
+
+
+def dequant_q6_k(row: np.ndarray, cols: int) -> np.ndarray:
+    out = np.empty(cols, np.float32)
+    for b in range(cols // QK):
+        d, sc, q = q6_k_parts(row[210 * b:210 * b + 210])
+        out[QK * b:QK * b + QK] = np.float32(d) * sc[np.arange(256) // 16].astype(np.float32) * q.astype(np.float32)
+    return out
+
+
+DEQUANT = {2: dequant_q4_0, 8: dequant_q8_0, 12: dequant_q4_k, 14: dequant_q6_k}
+BLOCK = {2: (32, 18), 8: (32, 34), 12: (256, 144), 14: (256, 210)}
+
+
+def random_blocks(rng: np.random.Generator, t: int, nblocks: int) -> np.ndarray:
+    """Random valid blocks: random payload bytes, finite normal fp16 scales of either sign."""
+    elems, size = BLOCK[t]
+    b = rng.integers(0, 256, (nblocks, size), dtype=np.uint8)
+
+    def h16(n, lo=-12, hi=-4):
+        v = (rng.uniform(0.5, 1.0, n) * 2.0 ** rng.integers(lo, hi, n)).astype(np.float16)
+        return v.view(np.uint16)
+
+    if t in (2, 8):
+        d = h16(nblocks)
+        b[:, 0] = d & 0xFF
+        b[:, 1] = d >> 8
+    elif t == 12:
+        for off in (0, 2):
+            d = h16(nblocks)
+            b[:, off] = d & 0xFF
+            b[:, off + 1] = d >> 8
+    else:
+        d = h16(nblocks)
+        b[:, 208] = d & 0xFF
+        b[:, 209] = d >> 8
+    return b.reshape(-1)

@@ -241,3 +241,52 @@ def test_nonfinite_inputs_route_safely(ctx, pkg, orc, exact):
         rout, _, _, _, _, _ = orc.moe_token(L, x[t], orc.shared_ffn(L, x[t]))
         ok, emax = within(out[t], rout)
         assert ok, f"t={t}: {emax}"
+
+
+# ---------------------------------------------------------------------------------------- fixtures
+def _golden():
+    from pathlib import Path
+    gold = Path(__file__).resolve().parent / "golden"
+    if str(gold) not in sys.path:
+        sys.path.insert(0, str(gold))
+    import make_golden
+    return gold, make_golden
+
+
+@pytest.mark.parametrize("exact", [False, True])
+@pytest.mark.parametrize("rule", [0, 1])
+def test_golden_c1_fixture(ctx, pkg, rule, exact):
+    """configs[0] at full size against tests/golden/c1_tiny.npz (noisy norms, shared input given)."""
+    say(f"golden c1 rule={rule} exact={exact}")
+    gold, MG = _golden()
+    f = np.load(gold / "c1_tiny.npz")
+    L, x, shared = MG.c1_inputs(pkg.synth)
+    assert MG.layer_digest(L) == str(f["layer_sha256"]), "synthetic generator drifted from the fixture"
+    L["weight_rule"] = rule
+    ctx.upload(0, L)
+    out = ctx.ffn(0, f["x"], f["shared"], exact_router=exact)
+    ids, w, off, perm, logits = ctx.routing()
+    np.testing.assert_array_equal(ids, f[f"ids_r{rule}"])
+    np.testing.assert_array_equal(off, f["offsets"])
+    np.testing.assert_array_equal(perm, f["perm"])
+    ok, emax = within(out, f[f"out_r{rule}"])
+    assert ok, f"max abs err {emax}"
+    if exact:
+        np.testing.assert_array_equal(logits, f["logits"])
+        np.testing.assert_array_equal(w, f[f"w_r{rule}"])
+        np.testing.assert_array_equal(out, f[f"out_r{rule}"])
+    say(f"golden c1: bit-exact {int((out == f[f'out_r{rule}']).sum())}/{out.size}, max abs err {emax:.3g}")
+
+
+def test_golden_kquant_fixture(ctx, pkg):
+    """Q4_K gate|up and a padded Q6_K down (288 -> 512) against tests/golden/kquant_tiny.npz."""
+    say("golden kquant T=4")
+    gold, MG = _golden()
+    f = np.load(gold / "kquant_tiny.npz")
+    L, x = MG.kq_inputs(pkg.synth)
+    assert MG.layer_digest(L) == str(f["layer_sha256"])
+    ctx.upload(0, L)
+    out = ctx.ffn(0, f["x"], exact_router=True)
+    ids = ctx.routing()[0]
+    np.testing.assert_array_equal(ids, f["ids"])
+    np.testing.assert_array_equal(out, f["out"])
