@@ -33,6 +33,14 @@ INT8_PEAK_TOPS = 5000.0  # dense int8 MFMA, MI355X
 
 METRIC = "MoE layer tokens/s; decode HBM GB/s vs peak; prefill MFMA util"
 
+# HBM bytes per launch of the roofline kernel, from two rocprofv3 counter runs (FETCH_SIZE, then
+# WRITE_SIZE) of this file with --calibrate, each scaled by what the counter reads for the library's
+# streaming read and copy kernels of known size (fetch factor 2.000, write factor 1.000).  Keyed by
+# (config, T, kernel); re-measured whenever that kernel changes.
+PMC_TRAFFIC = {
+    ("c2_decode", 1, "gate_up"): (25182625, "profiles/c2_decode_pmc_traffic.md"),
+}
+
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
@@ -132,6 +140,17 @@ def run_decode(args, pkg):
     layer_expert_bytes = avg_experts * (gu_b + dn_b)
     router_bytes = L["n_expert"] * d * 4
 
+    # ---- the same layer called with host buffers (the C# host's boundary: x and the output cross PCIe
+    # inside every call, which also waits for completion); a side figure, never `value`
+    n_host = 200
+    ctx.ffn(0, xs[0])
+    th = time.perf_counter()
+    for s in range(n_host):
+        ctx.ffn(s % n_slots, xs[s % NX])
+    host_dt = time.perf_counter() - th
+    pcie = {"tokens_s": round(T * n_host / host_dt, 1), "us_per_call": round(host_dt / n_host * 1e6, 2),
+            "note": "phx_moe_ffn on host x/out (H2D + layer + D2H + sync per call), eager launches"}
+
     # ---- measured streaming-read rate of this box (2 GiB, coalesced 128-bit loads)
     sbuf = ctx.alloc(2 << 30)
     sread_ms = ctx.stream_read_ms(sbuf, 10)
@@ -167,7 +186,8 @@ def run_decode(args, pkg):
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": PMC_TRAFFIC.get((cfg_name, T, "gate_up"), (None, None))[0],
+            "traffic_source": PMC_TRAFFIC.get((cfg_name, T, "gate_up"), (None, None))[1],
             "bytes_per_launch": int(gu_bytes),
             "avg_launch_us": round(gu_ms * 1e3, 3),
             "per_unit": f"{gu_b} B of gate|up weights per touched expert x {avg_experts:.2f} experts per launch"
@@ -182,6 +202,7 @@ def run_decode(args, pkg):
             "down_gbs": round(dn_bytes / (dn_ms * 1e-3) / 1e9, 1),
             "kernels": kernels,
             "stream_read_gbs_measured": round(stream_gbs, 1),
+            "pcie_inclusive": pcie,
         },
     }
     if args.calibrate:
@@ -194,22 +215,17 @@ def run_decode(args, pkg):
 
 
 def calibration_kernels(ctx, mib=1024):
-    """Kernels of known traffic for scaling the PMC byte counters (FETCH_SIZE, WRITE_SIZE): one
-    streaming read of `mib` MiB through the library, and one device copy of `mib` MiB (torch's copy
-    kernel: `mib` MiB read and `mib` MiB written)."""
-    import torch
+    """Kernels of known traffic for scaling the PMC byte counters (FETCH_SIZE, WRITE_SIZE): streaming
+    reads of `mib` MiB (phx::k_stream_read) and streaming copies of `mib` MiB (phx::k_stream_copy:
+    `mib` MiB read and `mib` MiB written), 3 launches each."""
     n = mib << 20
-    buf = ctx.alloc(n)
-    ctx.stream_read_ms(buf, 2)
-    buf.free()
-    src = torch.ones(n // 4, dtype=torch.float32, device="cuda")
-    dst = torch.empty_like(src)
-    for _ in range(2):
-        dst.copy_(src)
-    torch.cuda.synchronize()
-    del src, dst
+    src, dst = ctx.alloc(n), ctx.alloc(n)
+    ctx.stream_read_ms(src, 2)
+    ctx.stream_copy_ms(dst, src, n, 2)
+    src.free()
+    dst.free()
     return {"stream_read_bytes": n, "copy_read_bytes": n, "copy_write_bytes": n,
-            "kernels": ["phx::k_stream_read", "torch elementwise copy"]}
+            "kernels": ["phx::k_stream_read", "phx::k_stream_copy"]}
 
 
 def qname(t):

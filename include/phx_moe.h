@@ -175,6 +175,11 @@ int phx_moe_selftest(phx_moe_ctx* ctx, int op, int n, const float* a, const floa
  * read rate that the roofline figures are compared with (no counterpart in the reference). */
 int phx_moe_stream_read(phx_moe_ctx* ctx, const void* buf, uint64_t bytes, int iters, double* ms);
 
+/* Average time (ms) of `iters` streaming copies of `bytes` (a multiple of 16) between two device
+ * buffers: a kernel of known traffic for scaling a profiler's memory counters (no counterpart in the
+ * reference). */
+int phx_moe_stream_copy(phx_moe_ctx* ctx, void* dst, const void* src, uint64_t bytes, int iters, double* ms);
+
 /* Fallbacks since the context was created (counts[2]): [0] row norms whose double sum of squares
  * could not be certified to round like the reference's sequential sum (re-summed sequentially),
  * [1] decode-path tokens whose top-k order could not be certified (router re-run as the

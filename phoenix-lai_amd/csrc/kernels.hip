@@ -635,6 +635,19 @@ void launch_stream_read(hipStream_t st, const void* src, int64_t bytes, uint32_t
     launch(k_stream_read, dim3(256 * 8), dim3(256), 0, st, (const uint4*)src, bytes / 16, sink);
 }
 
+// Streaming copy of n16 16-byte words: a kernel of known traffic (bytes read = bytes written) for
+// scaling the memory counters of a profiler.
+__global__ __launch_bounds__(256) void k_stream_copy(uint4* __restrict__ dst, const uint4* __restrict__ src, int64_t n16)
+{
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride) dst[i] = src[i];
+}
+
+void launch_stream_copy(hipStream_t st, void* dst, const void* src, int64_t bytes)
+{
+    launch(k_stream_copy, dim3(256 * 8), dim3(256), 0, st, (uint4*)dst, (const uint4*)src, bytes / 16);
+}
+
 // ------------------------------------------------------------------------------ arithmetic self-test
 __global__ void k_selftest(int op, int n, const float* __restrict__ a, const float* __restrict__ b, float* __restrict__ out,
                            const float* __restrict__ tab)

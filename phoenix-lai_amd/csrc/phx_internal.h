@@ -134,6 +134,7 @@ void launch_combine_dec(hipStream_t st, int T, int d, int k, float eps, const fl
                         const float* shared, const float* post1, const float* post2, float* out, float* xres,
                         const float* post_ffw, int* flags);
 void launch_stream_read(hipStream_t st, const void* src, int64_t bytes, uint32_t* sink);
+void launch_stream_copy(hipStream_t st, void* dst, const void* src, int64_t bytes);
 void launch_selftest(hipStream_t st, int op, int n, const float* a, const float* b, float* out, const float* gelu_tab);
 
 }  // namespace phx

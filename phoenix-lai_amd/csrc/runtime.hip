@@ -1036,6 +1036,27 @@ int phx_moe_stream_read(phx_moe_ctx* c, const void* buf, uint64_t bytes, int ite
     return PHX_OK;
 }
 
+int phx_moe_stream_copy(phx_moe_ctx* c, void* dst, const void* src, uint64_t bytes, int iters, double* ms)
+{
+    if (!c || !dst || !src || bytes < 16 || bytes % 16 || iters <= 0 || !ms) return PHX_ERR_ARG;
+    HIPCHK(c, hipSetDevice(c->device));
+    hipEvent_t a = nullptr, b = nullptr;
+    HIPCHK(c, hipEventCreate(&a));
+    HIPCHK(c, hipEventCreate(&b));
+    launch_stream_copy(c->stream, dst, src, (int64_t)bytes);
+    (void)hipEventRecord(a, c->stream);
+    for (int i = 0; i < iters; i++) launch_stream_copy(c->stream, dst, src, (int64_t)bytes);
+    (void)hipEventRecord(b, c->stream);
+    hipError_t e = hipEventSynchronize(b);
+    float t = 0.0f;
+    if (e == hipSuccess) e = hipEventElapsedTime(&t, a, b);
+    (void)hipEventDestroy(a);
+    (void)hipEventDestroy(b);
+    HIPCHK(c, e);
+    *ms = t / iters;
+    return PHX_OK;
+}
+
 int phx_moe_fallback_count(phx_moe_ctx* c, int* counts)
 {
     if (!c || !counts) return PHX_ERR_ARG;

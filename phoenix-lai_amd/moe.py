@@ -122,6 +122,7 @@ def load_lib():
         "phx_moe_selftest": (i32, [vp, i32, i32, f32p, f32p, f32p]),
         "phx_moe_fallback_count": (i32, [vp, i32p]),
         "phx_moe_stream_read": (i32, [vp, vp, C.c_uint64, i32, C.POINTER(C.c_double)]),
+        "phx_moe_stream_copy": (i32, [vp, vp, vp, C.c_uint64, i32, C.POINTER(C.c_double)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -294,6 +295,11 @@ class MoeContext:
     def stream_read_ms(self, buf: "DeviceBuffer", iters: int = 20) -> float:
         ms = C.c_double()
         self._check(self.lib.phx_moe_stream_read(self.h, buf.ptr, buf.nbytes, iters, C.byref(ms)))
+        return ms.value
+
+    def stream_copy_ms(self, dst: "DeviceBuffer", src: "DeviceBuffer", nbytes: int, iters: int = 2) -> float:
+        ms = C.c_double()
+        self._check(self.lib.phx_moe_stream_copy(self.h, dst.ptr, src.ptr, nbytes, iters, C.byref(ms)))
         return ms.value
 
     def stack_run_device(self, x_ptr: int, T: int):
