@@ -56,12 +56,12 @@ struct RouteDecArgs {
     float* logits;
     int* offsets;
     int* perm;
-    Tile* tiles;
+    DecTile* tiles;
     int* ntiles;
     int* flags;           // [0] norm fallbacks, [1] router fallbacks
 };
 
-constexpr int RT_PER = 64;        // elements per lane (d <= 4096)
+constexpr int RT_PER = 16;        // elements per lane (d <= 4096, 256 lanes)
 typedef __attribute__((address_space(3))) void* lds_void_t;
 typedef __attribute__((address_space(1))) void* glb_void_t;
 
@@ -93,37 +93,39 @@ __device__ float exact_logit(const float* x, const float* W, const float* gis, i
     return s;
 }
 
+// One workgroup per (expert e, token t): x_t, the router scale and W[e] staged in LDS, then each of
+// the 256 lanes takes d / 256 consecutive indices; the double sum, its prefix sums (a wave scan
+// plus the four wave totals) and the bound terms follow the layout above.
 __global__ __launch_bounds__(256) void k_route_dec(RouteDecArgs a)
 {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, tid = threadIdx.x;
-    const int e = blockIdx.x * 4 + wave, t = blockIdx.y;
+    const int e = blockIdx.x, t = blockIdx.y;
     extern __shared__ __align__(16) unsigned char rsm[];
     __shared__ int s_last, s_bad[16];
-    __shared__ double red[8];
-    __shared__ int s_ids[256];
+    __shared__ double red[8], wsum[4], wA[4], wP[4], s_seq;
+    __shared__ int s_ids[256], s_perm[256];
     __shared__ int s_cnt[PHX_MAX_EXPERTS_DEV + 1], s_off[PHX_MAX_EXPERTS_DEV + 1], s_tb[PHX_MAX_EXPERTS_DEV + 1];
     const float sc = 1.0f / (float)__dsqrt_rn((double)a.d);
     const float* xr = a.x + (int64_t)t * a.d;
     const int d = a.d;
 
-    // ---- x, the router scale and this workgroup's 4 router rows into LDS (coalesced 128-bit loads)
+    // ---- x_t, the router scale and W[e] into LDS (direct global -> LDS loads, 16 B per lane,
+    // every load in flight at once; each wave fills 64 consecutive float4 per instruction)
     float* sx = (float*)rsm;
     float* sg = sx + d;
-    float* sw = sg + d;  // [4][d]
-    const float* spre2 = sw + 4 * d;
-    const float* sfnorm = spre2 + d;
+    float* sw = sg + d;
+    // the norm weight of this thread's first quantization slot (see below), loaded beside the staging
+    const int nin = a.fnorm ? 2 : 1, q_p0 = e * 8 + (tid >> 5);
+    float nw0 = 0.0f;
+    if (q_p0 < (d / 32) * nin) {
+        const int b = q_p0 / nin;
+        nw0 = (q_p0 - b * nin ? a.fnorm : a.pre2)[b * 32 + (tid & 31)];
+    }
     {
-        // direct global -> LDS loads (global_load_lds_dwordx4): every load in flight at once, no
-        // registers; each wave fills 64 consecutive float4 of an array per instruction
         const int n4 = d / 4;
-        const float4* srcs[8] = {(const float4*)xr, (const float4*)a.gis,
-                                 (const float4*)(a.W + (int64_t)min(blockIdx.x * 4 + 0, a.E - 1) * d),
-                                 (const float4*)(a.W + (int64_t)min(blockIdx.x * 4 + 1, a.E - 1) * d),
-                                 (const float4*)(a.W + (int64_t)min(blockIdx.x * 4 + 2, a.E - 1) * d),
-                                 (const float4*)(a.W + (int64_t)min(blockIdx.x * 4 + 3, a.E - 1) * d),
-                                 (const float4*)a.pre2, (const float4*)(a.fnorm ? a.fnorm : a.pre2)};
+        const float4* srcs[3] = {(const float4*)xr, (const float4*)a.gis, (const float4*)(a.W + (int64_t)e * d)};
 #pragma unroll
-        for (int r = 0; r < 8; r++) {
+        for (int r = 0; r < 3; r++) {
             float4* dst = (float4*)(sx + r * d);
             for (int q = 0; q * 256 < n4; q++) {
                 const int i = q * 256 + tid;
@@ -135,187 +137,178 @@ __global__ __launch_bounds__(256) void k_route_dec(RouteDecArgs a)
         __builtin_amdgcn_s_waitcnt(0);
     }
     __syncthreads();
-    // ---- the lane's contiguous chunk (d % 256 == 0: per = d / 64, a multiple of 4), read from LDS
-    const int per = d / 64, c0 = lane * per;
-    // certified mean of squares of x (every wave of the token computes the same value)
+    // ---- the lane's contiguous chunk of d / 256 indices (d % 256 == 0)
+    const int per = d / 256, c0 = tid * per;
+    // certified mean of squares of x_t: every workgroup of the token forms the same sum in the same order
     double s = 0.0;
 #pragma unroll
-    for (int j = 0; j < RT_PER; j += 4) {
+    for (int j = 0; j < RT_PER; j++)
         if (j < per) {
-            const float4 a4 = *(const float4*)(sx + c0 + j);
-            s += (double)a4.x * (double)a4.x;
-            s += (double)a4.y * (double)a4.y;
-            s += (double)a4.z * (double)a4.z;
-            s += (double)a4.w * (double)a4.w;
+            const double v = (double)sx[c0 + j];
+            s += v * v;
         }
-    }
-    const double S = wave_sum_dpp(s);
-    const double Bs = ((double)a.d + per + 64.0) * 0x1p-53 * S * 2.0;
-    float mean = (float)((S - Bs) / (double)a.d);
-    if (mean != (float)((S + Bs) / (double)a.d)) {
-        double q = 0.0;
-        if (lane == 0) {
-            for (int i = 0; i < a.d; i++) q += (double)sx[i] * (double)sx[i];
-            if (a.flags) atomicAdd(a.flags, 1);
+    s = wave_sum_dpp(s);
+    if (lane == 0) red[wave] = s;
+    __syncthreads();
+    const double S = (red[0] + red[1]) + (red[2] + red[3]);
+    const double Bs = ((double)d + per + 256.0) * 0x1p-53 * S * 2.0;
+    float mean = (float)((S - Bs) / (double)d);
+    if (mean != (float)((S + Bs) / (double)d)) {  // uniform: S is the same in every thread
+        if (tid == 0) {
+            double q = 0.0;
+            for (int i = 0; i < d; i++) q += (double)sx[i] * (double)sx[i];
+            s_seq = q;
+            if (a.flags && e == 0) atomicAdd(a.flags, 1);
         }
-        mean = (float)(__shfl(q, 0, 64) / (double)a.d);
+        __syncthreads();
+        mean = (float)(s_seq / (double)d);
     }
-    const float rinv = rms_scale_from_mean(mean, a.eps);  // also the RmsNorm scale of x
-    if (e < a.E) {
+    const float rinv = rms_scale_from_mean(mean, a.eps);  // also the RmsNorm scale of x_t
+    {
         // p_i = fl(W[e][i] * m_i), m_i = ((x_i * rinv) * sc) * s_i (src/GemmaCpu.cs:389,394)
         float pv[RT_PER];
         double loc = 0.0, P = 0.0;
 #pragma unroll
-        for (int j = 0; j < RT_PER; j += 4) {
+        for (int j = 0; j < RT_PER; j++) {
             if (j < per) {
-                const float4 a4 = *(const float4*)(sx + c0 + j), b4 = *(const float4*)(sg + c0 + j),
-                             c4 = *(const float4*)(sw + wave * d + c0 + j);
-                pv[j] = c4.x * (a4.x * rinv * sc * b4.x);
-                pv[j + 1] = c4.y * (a4.y * rinv * sc * b4.y);
-                pv[j + 2] = c4.z * (a4.z * rinv * sc * b4.z);
-                pv[j + 3] = c4.w * (a4.w * rinv * sc * b4.w);
-#pragma unroll
-                for (int u = 0; u < 4; u++) {
-                    loc += (double)pv[j + u];
-                    P += fabs((double)pv[j + u]);
-                }
+                pv[j] = sw[c0 + j] * (sx[c0 + j] * rinv * sc * sg[c0 + j]);
+                loc += (double)pv[j];
+                P += fabs((double)pv[j]);
             } else {
-                pv[j] = pv[j + 1] = pv[j + 2] = pv[j + 3] = 0.0f;
+                pv[j] = 0.0f;
             }
         }
         const double inc = wave_incl_scan_dpp(loc);
-        double acc = inc - loc;  // exclusive prefix (exact up to the double rounding the bound allows for)
+        if (lane == 63) wsum[wave] = inc;
+        __syncthreads();
+        double base = 0.0;
+        for (int w = 0; w < wave; w++) base += wsum[w];
+        double acc = base + (inc - loc);  // exclusive prefix (within the double slack of the bound)
         double A = 0.0;
 #pragma unroll
-        for (int j = 0; j < RT_PER; j++) {
+        for (int j = 0; j < RT_PER; j++)
             if (j < per) {
                 acc += (double)pv[j];
                 A += fabs(acc);
             }
-        }
         A = wave_sum_dpp(A);
         P = wave_sum_dpp(P);
-        const double L = __shfl(inc, 63, 64);
         if (lane == 0) {
+            wA[wave] = A;
+            wP[wave] = P;
+        }
+        __syncthreads();
+        if (tid == 0) {
+            const double L = ((wsum[0] + wsum[1]) + wsum[2]) + wsum[3];
+            const double As = (wA[0] + wA[1]) + (wA[2] + wA[3]), Ps = (wP[0] + wP[1]) + (wP[2] + wP[3]);
             st_agent(&a.Lb[(int64_t)t * a.E + e], L);
-            st_agent(&a.Bb[(int64_t)t * a.E + e], 0x1p-24 * A * 1.001 + 0x1p-45 * P);
+            st_agent(&a.Bb[(int64_t)t * a.E + e], 0x1p-24 * As * 1.001 + 0x1p-45 * Ps);
         }
     }
 
-    // ---- quantized expert input (and shared FFN input): one 32-lane half per 32-block
+    // ---- quantized expert input (and shared FFN input) of token t: one 32-lane half per (block, input),
+    // spread over the E workgroups of the token
     {
-        const int nbK = a.d / 32, half = tid >> 5, l32 = tid & 31;
-        for (int b = blockIdx.x * 8 + half; b < nbK; b += gridDim.x * 8) {
+        const int nbK = d / 32, l32 = tid & 31;
+        for (int p = q_p0; p < nbK * nin; p += a.E * 8) {
+            const int b = p / nin, which = p - b * nin;
             const int i = b * 32 + l32;
-            for (int which = 0; which < 2; which++) {
-                if (which && !a.fnorm) continue;
-                const float* nw = which ? sfnorm : spre2;
-                int8_t* aq = which ? a.act_sh.q : a.act_gu.q;
-                float* ad = which ? a.act_sh.d : a.act_gu.d;
-                int* as = which ? a.act_sh.s : a.act_gu.s;
-                const int64_t qs = which ? a.act_sh.qstride : a.act_gu.qstride;
-                const int dstr = which ? a.act_sh.dstride : a.act_gu.dstride;
-                const int sstr = which ? a.act_sh.sstride : a.act_gu.sstride;
-                float dval;
-                int sum;
-                const int q = q8_0_half(sx[i] * rinv * nw[i], &dval, &sum);
-                aq[(int64_t)t * qs + i] = (int8_t)q;
-                if (l32 == 0) {
-                    ad[(int64_t)t * dstr + b] = dval;
-                    as[(int64_t)t * sstr + b] = sum;
-                }
+            const float nwv = p == q_p0 ? nw0 : (which ? a.fnorm : a.pre2)[i];
+            const Act& o = which ? a.act_sh : a.act_gu;
+            float dval;
+            int sum;
+            const int q = q8_0_half(sx[i] * rinv * nwv, &dval, &sum);
+            o.q[(int64_t)t * o.qstride + i] = (int8_t)q;
+            if (l32 == 0) {
+                o.d[(int64_t)t * o.dstride + b] = dval;
+                o.s[(int64_t)t * o.sstride + b] = sum;
             }
         }
     }
 
-    // ---- hand-off to the last workgroup
-    __threadfence();
+    // ---- hand-off to the last workgroup: the barrier orders every wave's stores before thread 0's
+    // agent-scope release increment; the workgroup that completes the count acquires.
     __syncthreads();
     if (tid == 0) {
         const int total = gridDim.x * gridDim.y;
-        const int prev = __hip_atomic_fetch_add(a.counter, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        const int prev = __hip_atomic_fetch_add(a.counter, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
         s_last = prev == total - 1;
     }
     __syncthreads();
     if (!s_last) return;
-    __threadfence();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
 
     const int TE = a.T * a.E;
     double* sL = (double*)rsm;
-    double* sB = sL + kRouteMaxTE;
-    short* s_rank = (short*)(sB + kRouteMaxTE);
-    char* s_amb = (char*)(s_rank + kRouteMaxTE);
+    double* sB = sL + TE;
+    unsigned* s_key = (unsigned*)(sB + TE);
+    short* s_rank = (short*)(s_key + TE);
+    char* s_amb = (char*)(s_rank + TE);
     for (int i = tid; i < TE; i += 256) {
         sL[i] = ld_agent(&a.Lb[i]);
         sB[i] = ld_agent(&a.Bb[i]);
     }
     if (tid < 16) s_bad[tid] = 0;
     __syncthreads();
-    // selection per token (wave w: tokens w, w+4, ...): k rounds of a wave maximum of the sortable
-    // (float)L, the lowest index among equal keys (ballot); then the order is certified if each
-    // chosen expert's lower end lies above the upper ends of every expert ranked after it.  Ranking
-    // by (float)L is safe: logits that round alike have overlapping intervals, so such an order is
-    // never certified and goes to the exact path below.
+    // selection: the rank of every (token, expert) from all pairs in LDS (one to two threads per
+    // pair) by a 32-bit key: the order-preserving bits of (float)L with the low 8 bits replaced by
+    // 255 - expert, so keys are distinct and ties go to the lower index.  The order is then certified
+    // per token if each chosen expert's lower end lies above the upper ends of every expert ranked
+    // after it.  An order the key gets wrong (logits within 256 float ulps) is never certified, since
+    // certification compares the intervals themselves; such tokens take the exact path below.
+    for (int i = tid; i < TE; i += 256) {
+        const int ex = i % a.E;
+        s_key[i] = (sortable_f32((float)sL[i]) & ~0xFFu) | (unsigned)(255 - ex);
+    }
+    __syncthreads();
+    {
+        int split = 1;  // threads per pair: a power of two, split * TE <= 256
+        while (split < 64 && split * 2 * TE <= 256) split *= 2;
+        const int part = tid % split, chunk = (a.E + split - 1) / split;
+        for (int i = tid / split; i < TE; i += 256 / split) {
+            const int tt = i / a.E;
+            const unsigned my = s_key[i];
+            const unsigned* kr = s_key + tt * a.E;
+            const int c0 = part * chunk, c1 = min(a.E, c0 + chunk);
+            int r = 0, c = c0;
+            for (; c + 8 <= c1; c += 8) {  // eight keys in flight per step
+                const unsigned k0 = kr[c], k1 = kr[c + 1], k2 = kr[c + 2], k3 = kr[c + 3], k4 = kr[c + 4], k5 = kr[c + 5],
+                               k6 = kr[c + 6], k7 = kr[c + 7];
+                r += (int)(k0 > my) + (int)(k1 > my) + (int)(k2 > my) + (int)(k3 > my) + (int)(k4 > my) + (int)(k5 > my) +
+                     (int)(k6 > my) + (int)(k7 > my);
+            }
+            for (; c < c1; c++) r += kr[c] > my;
+            for (int o = 1; o < split; o <<= 1) r += __shfl_xor(r, o, 64);
+            if (part == 0) s_rank[i] = (short)min(r, a.k + 1);
+        }
+    }
+    __syncthreads();
+    for (int i = tid; i < TE; i += 256)
+        if (s_rank[i] < a.k) s_ids[(i / a.E) * a.k + s_rank[i]] = i % a.E;
+    __syncthreads();
     for (int tt = wave; tt < a.T; tt += 4) {
         const double* Lr = sL + tt * a.E;
         const double* Br = sB + tt * a.E;
-        unsigned key[4];
-        double lo[4], hi[4];
-        bool valid[4], fin = true;
-#pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const int ex = lane + 64 * q;
-            valid[q] = ex < a.E;
-            const double Lq = valid[q] ? Lr[ex] : 0.0, Bq = valid[q] ? Br[ex] : 0.0;
-            if (valid[q] && !(isfinite(Lq) && isfinite(Bq))) fin = false;
-            key[q] = valid[q] ? sortable_f32((float)Lq) + 1u : 0u;  // +1: every valid key beats "taken" (0)
-            lo[q] = Lq - Bq;
-            hi[q] = Lq + Bq;
+        const short* Rr = s_rank + tt * a.E;
+        double hun = -INFINITY;
+        bool fin = true;
+        for (int ex = lane; ex < a.E; ex += 64) {
+            const double Lq = Lr[ex], Bq = Br[ex];
+            if (!(isfinite(Lq) && isfinite(Bq))) fin = false;
+            if (Rr[ex] >= a.k) hun = fmax(hun, Lq + Bq);
         }
-        int chosen[PHX_MAX_USED_DEV];
-        for (int j = 0; j < a.k; j++) {
-            unsigned mk = 0u;
-#pragma unroll
-            for (int q = 0; q < 4; q++) mk = max(mk, key[q]);
-            mk = wave_max_u32(mk);
-            int ej = -1;
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const unsigned long long m = __ballot(key[q] == mk && mk != 0u);
-                if (ej < 0 && m) ej = (__ffsll((long long)m) - 1) + 64 * q;  // lowest index first
-            }
-            if (ej < 0) ej = 0;
-            chosen[j] = ej;
-#pragma unroll
-            for (int q = 0; q < 4; q++)
-                if (lane + 64 * q == ej) key[q] = 0u;
+        hun = wave_max_dpp(hun);
+        const bool act = lane < a.k;
+        const int ej = act ? s_ids[tt * a.k + lane] : 0;
+        const double lo_j = act ? Lr[ej] - Br[ej] : INFINITY, hi_j = act ? Lr[ej] + Br[ej] : -INFINITY;
+        // suffix maximum over the later ranks (lanes above), then the unchosen experts
+        double suf = hi_j;
+        for (int o = 1; o < 16; o <<= 1) {
+            const double up = __shfl_down(suf, o, 64);
+            if (lane + o < 16) suf = fmax(suf, up);
         }
-        // certification
-        double hmax = -INFINITY;
-#pragma unroll
-        for (int q = 0; q < 4; q++)
-            if (valid[q] && key[q] != 0u) hmax = fmax(hmax, hi[q]);
-        hmax = wave_max_dpp(hmax);
-        bool cert = __all(fin);
-        double suffix = hmax;
-        for (int j = a.k - 1; j >= 0; j--) {
-            const int ej = chosen[j], ln = ej & 63, q = ej >> 6;
-            const double lq = q == 0 ? lo[0] : q == 1 ? lo[1] : q == 2 ? lo[2] : lo[3];
-            const double hq = q == 0 ? hi[0] : q == 1 ? hi[1] : q == 2 ? hi[2] : hi[3];
-            const long long lb = __double_as_longlong(lq), hb = __double_as_longlong(hq);
-            const double lo_j = __longlong_as_double(((long long)__builtin_amdgcn_readlane((int)(lb >> 32), ln) << 32) |
-                                                     (unsigned)__builtin_amdgcn_readlane((int)lb, ln));
-            const double hi_j = __longlong_as_double(((long long)__builtin_amdgcn_readlane((int)(hb >> 32), ln) << 32) |
-                                                     (unsigned)__builtin_amdgcn_readlane((int)hb, ln));
-            if (!(lo_j > suffix)) cert = false;
-            suffix = fmax(suffix, hi_j);
-        }
-        // ranks for the code below: chosen j -> j, the others k + 1
-#pragma unroll
-        for (int q = 0; q < 4; q++)
-            if (valid[q]) s_rank[tt * a.E + lane + 64 * q] = (short)(a.k + 1);
-        for (int j = 0; j < a.k; j++)
-            if (lane == 0) s_rank[tt * a.E + chosen[j]] = (short)j;
+        const double later = fmax(hun, lane + 1 < 16 ? __shfl_down(suf, 1, 64) : -INFINITY);
+        const bool cert = __all(fin && (!act || lo_j > later));
         if (lane == 0) s_bad[tt] = !cert;
     }
     __syncthreads();
@@ -359,26 +352,93 @@ __global__ __launch_bounds__(256) void k_route_dec(RouteDecArgs a)
         a.logits[i] = (float)sL[i];
     }
     __syncthreads();
-    // one lane per (token, rank j); wave w takes tokens w, w+4, ...
-    for (int tt = wave; tt < a.T; tt += 4) {
-        const int j = lane;
-        const bool act = j < a.k;
-        const int id = act ? s_ids[tt * a.k + j] : 0;
-        const float selj = act ? (float)sL[tt * a.E + id] : 0.0f;
-        const float sel0 = __shfl(selj, 0, 64);
-        // p_0 = exp(0) = 1 exactly, so the CPU's in-place rule uses 1 for every later term
-        const float top = (a.rule == 1 && j > 0) ? 1.0f : sel0;
-        const float pj = act ? (float)exp((double)(selj - top)) : 0.0f;
-        double sum = 0.0;
-        for (int q = 0; q < a.k; q++) sum += (double)__shfl(pj, q, 64);  // in rank order
-        if (act) {
-            a.ids[(int64_t)tt * a.k + j] = id;
-            a.w[(int64_t)tt * a.k + j] = (float)((double)pj / sum) * a.ds[id];
+    const int n = a.T * a.k;
+    const bool fast_lists = n <= 64;  // one wave builds the lists while the others form the weights
+    // weights: one lane per (token, rank j); waves take tokens in turn (waves 0-2 beside the list wave)
+    {
+        const int nw = fast_lists ? 3 : 4;
+        for (int tt = wave; wave < nw && tt < a.T; tt += nw) {
+            const int j = lane;
+            const bool act = j < a.k;
+            const int id = act ? s_ids[tt * a.k + j] : 0;
+            const float selj = act ? (float)sL[tt * a.E + id] : 0.0f;
+            const float sel0 = __shfl(selj, 0, 64);
+            // p_0 = exp(0) = 1 exactly, so the CPU's in-place rule uses 1 for every later term
+            const float top = (a.rule == 1 && j > 0) ? 1.0f : sel0;
+            const float pj = act ? (float)exp((double)(selj - top)) : 0.0f;
+            double sum = 0.0;
+            for (int q = 0; q < a.k; q++) sum += (double)__shfl(pj, q, 64);  // in rank order
+            if (act) {
+                a.ids[(int64_t)tt * a.k + j] = id;
+                a.w[(int64_t)tt * a.k + j] = (float)((double)pj / sum) * a.ds[id];
+            }
         }
+    }
+    if (fast_lists) {
+        if (wave == 3) {
+            // lane i = assignment i (token i / k, rank i % k): its place in the stable order by
+            // (expert, assignment) is the number of assignments before it in that order
+            const bool act = lane < n;
+            const int ei = act ? clamp_id(s_ids[lane], a.E) : 0;
+            int rank = 0;
+            for (int j = 0; j < n; j++) {
+                const int ej = clamp_id(s_ids[j], a.E);
+                rank += (ej < ei) || (ej == ei && j < lane);
+            }
+            if (act) {
+                a.perm[rank] = lane;
+                s_perm[rank] = lane;
+            }
+            // counts per expert, then exclusive scans of counts and tile counts (4 experts per lane)
+            for (int x = lane; x <= a.E; x += 64) s_cnt[x] = 0;
+            __builtin_amdgcn_wave_barrier();
+            if (act) atomicAdd(&s_cnt[ei], 1);
+            __builtin_amdgcn_wave_barrier();
+            int c[4], tc[4], sc1 = 0, sc2 = 0;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int ex = lane * 4 + q;
+                c[q] = ex < a.E ? s_cnt[ex] : 0;
+                tc[q] = (c[q] + a.A - 1) / a.A;
+                sc1 += c[q];
+                sc2 += tc[q];
+            }
+            int v1 = sc1, v2 = sc2;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const int y1 = __shfl_up(v1, o, 64), y2 = __shfl_up(v2, o, 64);
+                if (lane >= o) {
+                    v1 += y1;
+                    v2 += y2;
+                }
+            }
+            int off = v1 - sc1, tb = v2 - sc2;
+            const int used = __shfl(v2, 63, 64);
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int ex = lane * 4 + q;
+                if (ex < a.E) {
+                    a.offsets[ex] = off;
+                    for (int r = 0; r * a.A < c[q]; r++) {
+                        const int st0 = off + r * a.A, m = min(a.A, c[q] - r * a.A);
+                        a.tiles[tb + r] = DecTile{ex, m, {s_perm[st0], m > 1 ? s_perm[st0 + 1] : 0}};
+                    }
+                }
+                off += c[q];
+                tb += tc[q];
+            }
+            if (lane == 0) {
+                a.offsets[a.E] = n;
+                *a.ntiles = used;
+            }
+            // slots past the last tile carry e = -1: a grouped workgroup reads one slot and stops
+            for (int q = used + lane; q < a.max_tiles; q += 64) a.tiles[q] = DecTile{-1, 0, {0, 0}};
+        }
+        if (tid == 0) __hip_atomic_store(a.counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
     }
 
     // ---- expert lists (ascending assignment order) and tiles of <= A assignments
-    const int n = a.T * a.k;
     for (int x = tid; x <= a.E; x += 256) s_cnt[x] = 0;
     __syncthreads();
     int my_e = 0, my_rank = 0;
@@ -411,21 +471,22 @@ __global__ __launch_bounds__(256) void k_route_dec(RouteDecArgs a)
         __syncthreads();
     }
     for (int x = tid; x <= a.E; x += 256) a.offsets[x] = s_off[x];
-    if (tid < n) a.perm[s_off[my_e] + my_rank] = tid;
+    if (tid < n) {
+        a.perm[s_off[my_e] + my_rank] = tid;
+        s_perm[s_off[my_e] + my_rank] = tid;
+    }
+    __syncthreads();
     if (tid < a.E) {
         const int c = s_cnt[tid], base = s_tb[tid];
         for (int q = 0; q * a.A < c; q++) {
-            Tile tl;
-            tl.e = tid;
-            tl.start = s_off[tid] + q * a.A;
-            tl.cnt = min(a.A, c - q * a.A);
-            a.tiles[base + q] = tl;
+            const int st0 = s_off[tid] + q * a.A, m = min(a.A, c - q * a.A);
+            a.tiles[base + q] = DecTile{tid, m, {s_perm[st0], m > 1 ? s_perm[st0 + 1] : 0}};
         }
     }
     {
         // slots past the last tile carry e = -1: a grouped workgroup reads one slot and stops
         const int used = s_tb[a.E - 1] + (s_cnt[a.E - 1] + a.A - 1) / a.A;
-        for (int q = used + tid; q < a.max_tiles; q += 256) a.tiles[q] = Tile{-1, 0, 0};
+        for (int q = used + tid; q < a.max_tiles; q += 256) a.tiles[q] = DecTile{-1, 0, {0, 0}};
     }
     if (tid == 0) __hip_atomic_store(a.counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -434,13 +495,14 @@ void launch_route_dec(hipStream_t st, const RouteDecArgsH& h)
 {
     RouteDecArgs a{h.T, h.d, h.E, h.k, h.rule, h.A, h.max_tiles, h.eps, h.x, h.W, h.gis, h.ds, h.pre2, h.fnorm, h.act_gu,
                    h.act_sh, h.Lb, h.Bb, h.counter, h.ids, h.w, h.logits, h.offsets, h.perm, h.tiles, h.ntiles, h.flags};
-    const size_t lds = std::max((size_t)8 * h.d * sizeof(float), (size_t)kRouteMaxTE * 19);
+    // staging [3][d] floats, or for the last workgroup L, B (8 B each), key (4 B), rank (2 B), flag (1 B) per (token, expert)
+    const size_t lds = std::max((size_t)3 * h.d * sizeof(float), (size_t)h.T * h.E * 23);
     static bool attr = false;
     if (!attr) {
-        (void)hipFuncSetAttribute((const void*)k_route_dec, hipFuncAttributeMaxDynamicSharedMemorySize, 8 * 4096 * 4);
+        (void)hipFuncSetAttribute((const void*)k_route_dec, hipFuncAttributeMaxDynamicSharedMemorySize, 3 * 4096 * 4);
         attr = true;
     }
-    launch(k_route_dec, dim3((h.E + 3) / 4, h.T), dim3(256), lds, st, a);
+    launch(k_route_dec, dim3(h.E, h.T), dim3(256), lds, st, a);
 }
 
 // ------------------------------------------------------------------------------ grouped products (decode)
@@ -455,9 +517,7 @@ void launch_route_dec(hipStream_t st, const RouteDecArgsH& h)
 // outputs and writes their Q8_0 block, the down input (src/CpuRef.cs:49-62).
 
 constexpr int DEC_A = kDecA;
-constexpr int DEC_NW = 8;
-constexpr int DEC_NT = DEC_NW * 64;
-constexpr int DEC_MAXB = 16;  // blocks per wave (nb <= 128)
+static_assert(DEC_A == 2, "DecTile holds two assignment rows");
 
 struct DecMat {
     const uint8_t* pay;
@@ -473,34 +533,38 @@ struct DecMat {
 
 struct DecArgs {
     DecMat m0, m1;        // experts, shared FFN (m1.rg == 0: none)
-    const Tile* tiles;
-    const int* ntiles;
+    const DecTile* tiles;
     int max_tiles;
-    const int* perm;
-    int act_div;          // expert activation row = perm entry / act_div
+    int act_div;          // expert activation row = assignment row / act_div
     int T;
     const float* gelu_tab;
 };
 
-template <int MODE, int TYPE>
-__global__ __launch_bounds__(DEC_NT) void k_dec_mm(DecArgs a)
+// NW waves per workgroup, each holding up to MAXB blocks of its lane's row (nb <= NW * MAXB)
+template <int MODE, int TYPE, int NW, int MAXB>
+__global__ __launch_bounds__(NW * 64) void k_dec_mm(DecArgs a)
 {
+    constexpr int DEC_NW = NW, DEC_MAXB = MAXB;
     __shared__ float terms[DEC_A][DEC_MAXB * DEC_NW][64];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     constexpr int PAY = TYPE == PHX_Q4_0_DEV ? 16 : 32;
 
-    int which, rgi, e, cnt, start = -1;
+    int which, rgi, e, cnt;
     int orow[DEC_A], arow[DEC_A];
     const int nexp = a.max_tiles * a.m0.rg;
     if ((int)blockIdx.x < nexp) {
         which = 0;
         const int tile = blockIdx.x / a.m0.rg;
         rgi = blockIdx.x % a.m0.rg;
-        const Tile tl = a.tiles[tile];
-        if (tl.e < 0) return;  // slot past the last tile
-        e = tl.e;
-        cnt = min(tl.cnt, DEC_A);
-        start = tl.start;
+        const int4 tl = *(const int4*)(a.tiles + tile);  // {e, cnt, row0, row1}
+        // wave-uniform values: scalar registers, so the activation rows are read with scalar loads
+        e = __builtin_amdgcn_readfirstlane(tl.x);
+        if (e < 0) return;  // slot past the last tile
+        cnt = min(__builtin_amdgcn_readfirstlane(tl.y), DEC_A);
+        orow[0] = __builtin_amdgcn_readfirstlane(tl.z);
+        orow[1] = __builtin_amdgcn_readfirstlane(tl.w);
+        arow[0] = orow[0] / a.act_div;
+        arow[1] = orow[1] / a.act_div;
     } else {
         which = 1;
         const int sid = blockIdx.x - nexp;
@@ -531,16 +595,10 @@ __global__ __launch_bounds__(DEC_NT) void k_dec_mm(DecArgs a)
             dwh[j] = ws[(int64_t)(b0 + j) * 64];
         }
     }
-    // the tile's assignment rows (expert tiles), read while the weights are in flight
-    if (start >= 0) {
+    // ---- per-block terms of every assignment (unrolled: the rows stay in scalar registers)
 #pragma unroll
-        for (int i = 0; i < DEC_A; i++) {
-            orow[i] = i < cnt ? a.perm[start + i] : 0;
-            arow[i] = orow[i] / a.act_div;
-        }
-    }
-    // ---- per-block terms of every assignment
-    for (int i = 0; i < cnt; i++) {
+    for (int i = 0; i < DEC_A; i++) {
+        if (i >= cnt) break;
         const int64_t r = arow[i];
         const uint32_t* xq = (const uint32_t*)(M.in.q + r * M.in.qstride);
         const float* xd = M.in.d + r * M.in.dstride;
@@ -625,27 +683,26 @@ static DecMat to_dev(const DecMatH& h)
     return m;
 }
 
-void launch_dec(hipStream_t st, int mode, const DecMatH& m0, const DecMatH& m1, const Tile* tiles, const int* ntiles,
-                int max_tiles, const int* perm, int act_div, int T, const float* gelu_tab)
+void launch_dec(hipStream_t st, int mode, const DecMatH& m0, const DecMatH& m1, const DecTile* tiles, int max_tiles,
+                int act_div, int T, const float* gelu_tab)
 {
     DecArgs a{};
     a.m0 = to_dev(m0);
     a.m1 = to_dev(m1);
     a.tiles = tiles;
-    a.ntiles = ntiles;
     a.max_tiles = max_tiles;
-    a.perm = perm;
     a.act_div = act_div;
     a.T = T;
     a.gelu_tab = gelu_tab;
     const int items = max_tiles * a.m0.rg + (a.m1.rg > 0 ? (T + DEC_A - 1) / DEC_A * a.m1.rg : 0);
     const bool q4 = m0.q->type == PHX_Q4_0_DEV;
+    // 8 waves share a row's blocks (nb <= 128)
     if (mode == 0) {
-        if (q4) launch((k_dec_mm<0, PHX_Q4_0_DEV>), dim3(items), dim3(DEC_NT), 0, st, a);
-        else launch((k_dec_mm<0, PHX_Q8_0_DEV>), dim3(items), dim3(DEC_NT), 0, st, a);
+        if (q4) launch((k_dec_mm<0, PHX_Q4_0_DEV, 8, 16>), dim3(items), dim3(512), 0, st, a);
+        else launch((k_dec_mm<0, PHX_Q8_0_DEV, 8, 16>), dim3(items), dim3(512), 0, st, a);
     } else {
-        if (q4) launch((k_dec_mm<1, PHX_Q4_0_DEV>), dim3(items), dim3(DEC_NT), 0, st, a);
-        else launch((k_dec_mm<1, PHX_Q8_0_DEV>), dim3(items), dim3(DEC_NT), 0, st, a);
+        if (q4) launch((k_dec_mm<1, PHX_Q4_0_DEV, 8, 16>), dim3(items), dim3(512), 0, st, a);
+        else launch((k_dec_mm<1, PHX_Q8_0_DEV, 8, 16>), dim3(items), dim3(512), 0, st, a);
     }
 }
 

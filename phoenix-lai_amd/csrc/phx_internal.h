@@ -78,6 +78,9 @@ struct Act {
 };
 
 struct Tile { int e, start, cnt; };
+// decode-path tile: expert, assignment count (<= kDecA) and the assignment rows themselves, so a
+// grouped workgroup learns everything it needs from one 16-byte read
+struct DecTile { int e, cnt, row[2]; };
 
 // kernels.hip launchers (all enqueue on `st`)
 void launch_prologue(hipStream_t st, int T, int d, float eps, const float* x, const float* gate_inp_scale,
@@ -115,7 +118,7 @@ struct RouteDecArgsH {
     float* logits;
     int* offsets;
     int* perm;
-    Tile* tiles;
+    DecTile* tiles;
     int* ntiles;
     int* flags;
 };
@@ -128,8 +131,8 @@ struct DecMatH {  // host-side description of one matrix of a decode grouped lau
     int split = 0;
     Act out_act;
 };
-void launch_dec(hipStream_t st, int mode, const DecMatH& m0, const DecMatH& m1, const Tile* tiles, const int* ntiles,
-                int max_tiles, const int* perm, int act_div, int T, const float* gelu_tab);
+void launch_dec(hipStream_t st, int mode, const DecMatH& m0, const DecMatH& m1, const DecTile* tiles, int max_tiles,
+                int act_div, int T, const float* gelu_tab);
 void launch_combine_dec(hipStream_t st, int T, int d, int k, float eps, const float* yd, const float* w,
                         const float* shared, const float* post1, const float* post2, float* out, float* xres,
                         const float* post_ffw, int* flags);

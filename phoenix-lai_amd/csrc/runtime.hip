@@ -396,7 +396,7 @@ int ensure_workspace(phx_moe_ctx* c, const Layer& L, int T)
         ENS(W_SOFF, 8);
         ENS(W_SPERM, (size_t)T * 4);
     }
-    ENS(W_TILES, (size_t)((n + kDecA - 1) / kDecA + D.n_expert) * sizeof(Tile));
+    ENS(W_TILES, (size_t)((n + kDecA - 1) / kDecA + D.n_expert) * sizeof(DecTile));
 #undef ENS
     return PHX_OK;
 }
@@ -494,7 +494,7 @@ int run_layer_decode(phx_moe_ctx* c, const Layer& L, int T, const float* x, cons
         r.logits = wp<float>(c, W_LOGITS);
         r.offsets = wp<int>(c, W_OFF);
         r.perm = wp<int>(c, W_PERM);
-        r.tiles = wp<Tile>(c, W_TILES);
+        r.tiles = wp<DecTile>(c, W_TILES);
         r.ntiles = wp<int>(c, W_NTILES);
         r.flags = c->flags;
         launch_route_dec(st, r);
@@ -516,8 +516,7 @@ int run_layer_decode(phx_moe_ctx* c, const Layer& L, int T, const float* x, cons
             m1.split = D.n_ff_shared;
             m1.out_act = asd;
         }
-        launch_dec(st, 0, m0, m1, wp<Tile>(c, W_TILES), wp<int>(c, W_NTILES), max_tiles, wp<int>(c, W_PERM), k, T,
-                   c->gelu_tab);
+        launch_dec(st, 0, m0, m1, wp<DecTile>(c, W_TILES), max_tiles, k, T, c->gelu_tab);
     }
     {
         ProfScope p(c, PHX_K_DOWN);
@@ -530,8 +529,7 @@ int run_layer_decode(phx_moe_ctx* c, const Layer& L, int T, const float* x, cons
             m1.in = asd;
             m1.out0 = wp<float>(c, W_SHOUT);
         }
-        launch_dec(st, 1, m0, m1, wp<Tile>(c, W_TILES), wp<int>(c, W_NTILES), max_tiles, wp<int>(c, W_PERM), 1, T,
-                   c->gelu_tab);
+        launch_dec(st, 1, m0, m1, wp<DecTile>(c, W_TILES), max_tiles, 1, T, c->gelu_tab);
     }
     {
         ProfScope p(c, PHX_K_COMBINE);
