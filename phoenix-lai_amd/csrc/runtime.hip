@@ -438,6 +438,7 @@ struct ProfScope : LaunchTimer {
 };
 
 bool dec_type(int t) { return t == PHX_Q4_0 || t == PHX_Q8_0; }
+bool mfma_type(int t) { return t == PHX_Q4_0 || t == PHX_Q8_0; }
 
 // The decode path: few tokens, Q4_0/Q8_0 weights, K <= 4096 (kernels_decode.hip).
 bool use_decode(const Layer& L, int T, unsigned flags)
@@ -565,16 +566,23 @@ int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, con
         ProfScope p(c, PHX_K_TOPK);
         launch_topk(st, T, E, k, D.weight_rule, wp<float>(c, W_LOGITS), L.ds, wp<int>(c, W_IDS), wp<float>(c, W_W));
     }
-    const int max_tiles = std::min(n, (n + kTileA - 1) / kTileA + E);
+    // prefill-sized expert work (several assignments per expert on average) runs on the matrix cores
+    const bool mma = mfma_type(D.gate_up_type) && mfma_type(D.down_type) && n >= 8 * E;
+    const int tileA = mma ? kMmaTile : kTileA;
+    const int max_tiles = std::min(n, (n + tileA - 1) / tileA + E);
     {
         ProfScope p(c, PHX_K_DISPATCH);
-        launch_dispatch(st, n, E, kTileA, wp<int>(c, W_IDS), wp<int>(c, W_OFF), wp<int>(c, W_PERM), wp<Tile>(c, W_TILES),
+        launch_dispatch(st, n, E, tileA, wp<int>(c, W_IDS), wp<int>(c, W_OFF), wp<int>(c, W_PERM), wp<Tile>(c, W_TILES),
                         wp<int>(c, W_NTILES));
     }
     {
         ProfScope p(c, PHX_K_GATE_UP);
-        launch_grouped(st, L.gu, agu, wp<Tile>(c, W_TILES), wp<int>(c, W_NTILES), max_tiles, kTileA, wp<int>(c, W_PERM), k,
-                       wp<float>(c, W_G), wp<float>(c, W_U), nf, nf);
+        if (mma)
+            launch_grouped_mfma(st, L.gu, agu, wp<Tile>(c, W_TILES), wp<int>(c, W_NTILES), max_tiles, wp<int>(c, W_PERM), k,
+                                wp<float>(c, W_G), wp<float>(c, W_U), nf, nf);
+        else
+            launch_grouped(st, L.gu, agu, wp<Tile>(c, W_TILES), wp<int>(c, W_NTILES), max_tiles, kTileA, wp<int>(c, W_PERM),
+                           k, wp<float>(c, W_G), wp<float>(c, W_U), nf, nf);
     }
     Act adn = make_act(c, act_fmt(D.down_type), D.down_cols, W_ADN_Q, W_ADN_D, W_ADN_S);
     {
@@ -583,23 +591,37 @@ int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, con
     }
     {
         ProfScope p(c, PHX_K_DOWN);
-        launch_grouped(st, L.dn, adn, wp<Tile>(c, W_TILES), wp<int>(c, W_NTILES), max_tiles, kTileA, wp<int>(c, W_PERM), 1,
-                       wp<float>(c, W_YD), wp<float>(c, W_YD), d, d);
+        if (mma)
+            launch_grouped_mfma(st, L.dn, adn, wp<Tile>(c, W_TILES), wp<int>(c, W_NTILES), max_tiles, wp<int>(c, W_PERM), 1,
+                                wp<float>(c, W_YD), wp<float>(c, W_YD), d, d);
+        else
+            launch_grouped(st, L.dn, adn, wp<Tile>(c, W_TILES), wp<int>(c, W_NTILES), max_tiles, kTileA, wp<int>(c, W_PERM),
+                           1, wp<float>(c, W_YD), wp<float>(c, W_YD), d, d);
     }
     const float* sh = shared;
     if (shared_ffn) {
         ProfScope p(c, PHX_K_SHARED);
         const int nff = D.n_ff_shared;
-        const int smax = (T + kTileA - 1) / kTileA + 1;
-        launch_dispatch(st, T, 1, kTileA, wp<int>(c, W_ZERO), wp<int>(c, W_SOFF), wp<int>(c, W_SPERM),
-                        wp<Tile>(c, W_STILES), wp<int>(c, W_SNTILES));
-        launch_grouped(st, L.sgu, ash, wp<Tile>(c, W_STILES), wp<int>(c, W_SNTILES), smax, kTileA, wp<int>(c, W_SPERM), 1,
-                       wp<float>(c, W_SHG), wp<float>(c, W_SHU), nff, nff);
+        const bool smma = mfma_type(D.shared_type) && T >= 32;
+        const int sA = smma ? kMmaTile : kTileA;
+        const int smax = (T + sA - 1) / sA + 1;
+        launch_dispatch(st, T, 1, sA, wp<int>(c, W_ZERO), wp<int>(c, W_SOFF), wp<int>(c, W_SPERM), wp<Tile>(c, W_STILES),
+                        wp<int>(c, W_SNTILES));
+        if (smma)
+            launch_grouped_mfma(st, L.sgu, ash, wp<Tile>(c, W_STILES), wp<int>(c, W_SNTILES), smax, wp<int>(c, W_SPERM), 1,
+                                wp<float>(c, W_SHG), wp<float>(c, W_SHU), nff, nff);
+        else
+            launch_grouped(st, L.sgu, ash, wp<Tile>(c, W_STILES), wp<int>(c, W_SNTILES), smax, kTileA, wp<int>(c, W_SPERM),
+                           1, wp<float>(c, W_SHG), wp<float>(c, W_SHU), nff, nff);
         Act asd = make_act(c, act_fmt(D.shared_type), round_up(nff, block_elems(D.shared_type)), W_ASD_Q, W_ASD_D,
                            W_ASD_S);
         launch_requant(st, T, nff, wp<float>(c, W_SHG), wp<float>(c, W_SHU), c->gelu_tab, asd);
-        launch_grouped(st, L.sdn, asd, wp<Tile>(c, W_STILES), wp<int>(c, W_SNTILES), smax, kTileA, wp<int>(c, W_SPERM), 1,
-                       wp<float>(c, W_SHOUT), wp<float>(c, W_SHOUT), d, d);
+        if (smma)
+            launch_grouped_mfma(st, L.sdn, asd, wp<Tile>(c, W_STILES), wp<int>(c, W_SNTILES), smax, wp<int>(c, W_SPERM), 1,
+                                wp<float>(c, W_SHOUT), wp<float>(c, W_SHOUT), d, d);
+        else
+            launch_grouped(st, L.sdn, asd, wp<Tile>(c, W_STILES), wp<int>(c, W_SNTILES), smax, kTileA, wp<int>(c, W_SPERM),
+                           1, wp<float>(c, W_SHOUT), wp<float>(c, W_SHOUT), d, d);
         sh = wp<float>(c, W_SHOUT);
     }
     {

@@ -290,3 +290,27 @@ def test_golden_kquant_fixture(ctx, pkg):
     ids = ctx.routing()[0]
     np.testing.assert_array_equal(ids, f["ids"])
     np.testing.assert_array_equal(out, f["out"])
+
+
+# ---------------------------------------------------------------------------------------- matrix cores
+MFMA_CASES = {
+    # (layer config, T, shared input given): n = T * k >= 8 * E puts the experts on the MFMA kernel,
+    # T >= 32 the shared FFN
+    "c1_T64_q4_0": ("c1_tiny", 64, True),
+    "q8_0_shared_T64": (dict(idx=12, T=64, d=512, E=8, k=2, nf=256, gu=8, dn=8, nff=256, sh=8), 64, False),
+    "c2_T64_shared_only": ("c2_decode", 64, False),
+    "c3_T128": ("c3_prefill", 128, False),
+}
+
+
+@pytest.mark.parametrize("case", list(MFMA_CASES))
+def test_mfma_grouped_products_bit_exact(ctx, pkg, orc, case):
+    """The MFMA grouped kernel keeps the reference's per-block float chain: gate/up/down rows and the
+    outputs equal the CPU reference bit for bit (the general path's router is the exact one)."""
+    cfg, T, with_shared = MFMA_CASES[case]
+    say(f"mfma {case}: T={T}")
+    L = pkg.synth.make_layer(cfg, norms="noisy")
+    x = pkg.synth.make_input(cfg, T=T)
+    shared = pkg.synth.normal(1234, "mfma.shared", x.shape) if with_shared else None
+    ctx.upload(0, L)
+    check_layer(ctx, orc, L, x, shared, tag=f"mfma {case}", exact=True)
