@@ -75,20 +75,20 @@ def cpu_baseline(pkg, L, cfg_name, T, budget_s=12.0):
                       f"{dt:.1f} s, OpenMP over rows with {threads} threads"}
 
 
-def run_decode(args, pkg):
+def run_layer(args, pkg):
     S = pkg.synth
     cfg_name = args.config
     cfg = S.CONFIGS[cfg_name]
     T = args.T or cfg["T"]
-    n_slots = args.layers
+    n_slots = args.layers or cfg.get("layers", 8)
     log(f"[bench] generating {cfg_name} layer ...")
     L = S.make_layer(cfg_name)
     ctx = pkg.MoeContext(0)
     log(f"[bench] uploading {n_slots} layer slots ...")
     for i in range(n_slots):
         ctx.upload(i, L)
-    d = L["d"]
-    NX = 64
+    d, E, k = L["d"], L["n_expert"], L["n_used"]
+    NX = int(min(64, max(4, (512 << 20) // (T * d * 4))))  # distinct inputs, cycled through the replays
     xs = S.normal(cfg["idx"] + 7000, "bench.x", (NX, T, d))
     if L.get("biased"):
         xs[:, :, -1] = S.BIAS_X
@@ -113,9 +113,9 @@ def run_decode(args, pkg):
     ms_per_step = dt * 1e3 / steps
     tokens_s = T * steps / dt
 
-    # ---- instrumented eager pass: per-kernel HIP-event durations and touched experts
+    # ---- instrumented eager pass: per-kernel execution intervals and touched experts
     gu_b, dn_b = expert_bytes(L)
-    prof_steps = min(steps, args.prof_steps)
+    prof_steps = max(1, min(steps, args.prof_steps))
     ctx.profile(True)
     distinct = 0
     for s in range(prof_steps):
@@ -127,6 +127,10 @@ def run_decode(args, pkg):
     avg_experts = distinct / prof_steps
     gu_ms = prof["gate_up"][0] / max(1, prof["gate_up"][1])
     dn_ms = prof["down"][0] / max(1, prof["down"][1])
+    decode = prof["dispatch"][1] == 0  # the decode path has no separate dispatch launch
+    n = T * k
+    mfma = (not decode and L["gate_up_type"] in (pkg.PHX.Q4_0, pkg.PHX.Q8_0)
+            and L["down_type"] in (pkg.PHX.Q4_0, pkg.PHX.Q8_0) and n >= 8 * E)
     # the decode path's gate|up launch also computes the dense shared FFN's gate and up rows, and its
     # down launch the shared down rows: their weights are part of those launches' algorithmic bytes
     sh_gu_b = sh_dn_b = 0
@@ -134,15 +138,50 @@ def run_decode(args, pkg):
         sh_gu_b = 2 * L["n_ff_shared"] * S.row_bytes(L["shared_type"], d)
         sh_dn_b = d * S.row_bytes(L["shared_type"], L["n_ff_shared"])
     sh_bytes = sh_gu_b + sh_dn_b
-    gu_bytes = avg_experts * gu_b + sh_gu_b
-    achieved = gu_bytes / (gu_ms * 1e-3) / 1e9
-    dn_bytes = avg_experts * dn_b + sh_dn_b
     layer_expert_bytes = avg_experts * (gu_b + dn_b)
-    router_bytes = L["n_expert"] * d * 4
+    router_bytes = E * d * 4
+    if decode:
+        gu_bytes = avg_experts * gu_b + sh_gu_b
+        dn_bytes = avg_experts * dn_b + sh_dn_b
+        achieved = gu_bytes / (gu_ms * 1e-3) / 1e9
+        roofline = {
+            "bound": "hbm",
+            "kernel": "gate_up (grouped Q4_0 x Q8_0 row products, decode)" if L["gate_up_type"] == 2 else "gate_up (decode)",
+            "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": PMC_TRAFFIC.get((cfg_name, T, "gate_up"), (None, None))[0],
+            "traffic_source": PMC_TRAFFIC.get((cfg_name, T, "gate_up"), (None, None))[1],
+            "bytes_per_launch": int(gu_bytes), "avg_launch_us": round(gu_ms * 1e3, 3),
+            "per_unit": f"{gu_b} B of gate|up weights per touched expert x {avg_experts:.2f} experts per launch"
+                        + (f" + {sh_gu_b} B of shared-FFN gate and up weights" if sh_gu_b else ""),
+        }
+        down_rate = {"down_gbs": round(dn_bytes / (dn_ms * 1e-3) / 1e9, 1)}
+    elif mfma:
+        # int8 operations of the routed experts' gate|up products (2 per multiply-add)
+        ops = 2.0 * n * 2 * L["n_ff"] * d
+        achieved = ops / (gu_ms * 1e-3) / 1e12
+        roofline = {
+            "bound": "mfma", "kernel": "gate_up (grouped int8 MFMA, exact block sums + reference float chain)",
+            "achieved": round(achieved, 2), "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
+            "frac": round(achieved / INT8_PEAK_TOPS, 4), "traffic": None,
+            "ops_per_launch": int(ops), "avg_launch_us": round(gu_ms * 1e3, 3),
+            "per_unit": f"2 x {2 * L['n_ff']} x {d} int8 ops per assignment x {n} assignments per launch",
+        }
+        dn_ops = 2.0 * n * d * L["n_ff"]
+        down_rate = {"down_tops": round(dn_ops / (dn_ms * 1e-3) / 1e12, 2)}
+    else:
+        gu_bytes = avg_experts * gu_b
+        achieved = gu_bytes / (gu_ms * 1e-3) / 1e9
+        roofline = {
+            "bound": "hbm", "kernel": f"gate_up (grouped {qname(L['gate_up_type'])} row products, VALU)",
+            "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None, "bytes_per_launch": int(gu_bytes), "avg_launch_us": round(gu_ms * 1e3, 3),
+            "per_unit": f"{gu_b} B of gate|up weights per touched expert x {avg_experts:.2f} experts per launch",
+        }
+        down_rate = {"down_gbs": round(avg_experts * dn_b / (dn_ms * 1e-3) / 1e9, 1)}
 
     # ---- the same layer called with host buffers (the C# host's boundary: x and the output cross PCIe
     # inside every call, which also waits for completion); a side figure, never `value`
-    n_host = 200
+    n_host = max(5, min(200, int(0.5 / max(ms_per_step * 1e-3, 1e-6))))
     ctx.ffn(0, xs[0])
     th = time.perf_counter()
     for s in range(n_host):
@@ -157,7 +196,7 @@ def run_decode(args, pkg):
     stream_gbs = (2 << 30) / (sread_ms * 1e-3) / 1e9
     sbuf.free()
 
-    kernels = {k: {"avg_us": round(v[0] / max(1, v[1]) * 1e3, 2), "launches": v[1]} for k, v in prof.items() if v[1]}
+    kernels = {k_: {"avg_us": round(v[0] / max(1, v[1]) * 1e3, 2), "launches": v[1]} for k_, v in prof.items() if v[1]}
     line = {
         "metric": METRIC,
         "value": round(tokens_s, 2),
@@ -172,34 +211,25 @@ def run_decode(args, pkg):
         "dtype": "int8",
         "data": "synthetic",
         "config": {
-            "workload": f"{cfg_name}: MoE FFN layer, T={T}, d={d}, E={L['n_expert']}, top-{L['n_used']}, "
+            "workload": f"{cfg_name}: MoE FFN layer, T={T}, d={d}, E={E}, top-{k}, "
                         f"expert ffn {L['n_ff']}, {qname(L['gate_up_type'])}/{qname(L['down_type'])} experts"
                         + (f", shared FFN {L['n_ff_shared']} {qname(L['shared_type'])}" if sh_bytes else "")
+                        + (", Zipf(1.1) router bias" if cfg.get("zipf") else "")
+                        + (f", hot expert {cfg['hot']:.0%} of tokens" if cfg.get("hot") else "")
                         + f"; {n_slots} layer slots replayed as one HIP graph, x varied per replay",
             "global_batch": T,
             "parallelism": "none (1 GPU)",
+            "path": "decode" if decode else ("mfma" if mfma else "valu"),
         },
-        "roofline": {
-            "bound": "hbm",
-            "kernel": "gate_up (grouped Q4_0 x Q8_0 row products)" if L["gate_up_type"] == 2 else "gate_up",
-            "achieved": round(achieved, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": PMC_TRAFFIC.get((cfg_name, T, "gate_up"), (None, None))[0],
-            "traffic_source": PMC_TRAFFIC.get((cfg_name, T, "gate_up"), (None, None))[1],
-            "bytes_per_launch": int(gu_bytes),
-            "avg_launch_us": round(gu_ms * 1e3, 3),
-            "per_unit": f"{gu_b} B of gate|up weights per touched expert x {avg_experts:.2f} experts per launch"
-                        + (f" + {sh_gu_b} B of shared-FFN gate and up weights" if sh_gu_b else ""),
-        },
+        "roofline": roofline,
         "layer": {
             "expert_bytes_per_step": int(layer_expert_bytes),
             "expert_gbs": round(layer_expert_bytes / (ms_per_step * 1e-3) / 1e9, 1),
             "all_bytes_gbs": round((layer_expert_bytes + sh_bytes + router_bytes) / (ms_per_step * 1e-3) / 1e9, 1),
             "expert_gbs_frac_of_peak": round(layer_expert_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "distinct_experts_per_step": round(avg_experts, 2),
             "down_avg_us": round(dn_ms * 1e3, 3),
-            "down_gbs": round(dn_bytes / (dn_ms * 1e-3) / 1e9, 1),
+            **down_rate,
             "kernels": kernels,
             "stream_read_gbs_measured": round(stream_gbs, 1),
             "pcie_inclusive": pcie,
@@ -239,7 +269,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=400)
     ap.add_argument("--config", default="c2_decode")
     ap.add_argument("--T", type=int, default=0)
-    ap.add_argument("--layers", type=int, default=8, help="distinct layer slots in the replayed graph")
+    ap.add_argument("--layers", type=int, default=0,
+                    help="layer slots in the replayed graph (default 8, or the config's stack depth)")
     ap.add_argument("--prof-steps", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -253,7 +284,7 @@ def main():
     if not ge._built():
         ge.build()
     pkg = ge.load_package()
-    line = run_decode(args, pkg)
+    line = run_layer(args, pkg)
     print(json.dumps(line), flush=True)
 
 
