@@ -1,20 +1,117 @@
-// Decode-shaped MoE FFN kernels (a few tokens, T <= 16): four launches per layer.
-//   k_route_dec    router logits (certified), the quantized expert / shared-FFN inputs, then in the
-//                  last workgroup: top-k, weights and the expert lists
-//   k_dec_mm<0>    gate|up of the routed experts and of the shared FFN; epilogue: gelu(g) * u and
-//                  its Q8_0 quantization (the down input)
-//   k_dec_mm<1>    down of the routed experts and of the shared FFN
-//   k_combine_dec  rank-ordered combine, branch norms, optional residual
-// Arithmetic follows the reference CPU path (src/GemmaCpu.cs:376-422) as in kernels.hip; the router
-// logits are the one quantity certified rather than replayed (see k_route_dec).
+// Decode-shaped MoE FFN kernels (a few tokens, T <= 16; Q4_0 / Q8_0 weights): four launches per layer.
+//   k_dec_route    router logits with certified error bounds, one workgroup per (token, expert); beside
+//                  them, the dense shared FFN's gate|up product with its gelu(g) * u Q8_0 epilogue
+//   k_dec_gu       every workgroup selects the top-k from the router's bounds (exact fallback when the
+//                  order cannot be certified) and forms the expert tiles, then computes one (tile, row
+//                  group) of the routed experts' gate|up products with the same epilogue; beside them,
+//                  the shared FFN's down product
+//   k_dec_down     one (tile, row group) of the routed experts' down products
+//   k_dec_combine  per token: the rank-ordered combine, the two branch norms, the optional residual
+// Arithmetic follows the reference CPU path (src/GemmaCpu.cs:376-422): integer block sums, the float
+// block chain sum += (float)isum * (d_w * d_x) in block order (src/CpuRefGemma.cs:27-36,
+// src/CpuRef.cs:106-115), the rank-ordered combine (GemmaCpu.cs:417-418) and RmsNorm's double sums of
+// squares (src/CpuRef.cs:183-191) reproduced through certified bounds.  The router logits are the one
+// quantity certified rather than replayed (k_dec_route).
+//
+// Work layout: a row group (64 rows, lane = row) is one workgroup of ceil(nb / 8) waves, wave w
+// holding blocks 8w..8w+7 of its lane's row.  Every wave issues its 8 payload loads (16 B per lane, a
+// 1 KB contiguous span per instruction) and one 16 B load of the 8 blocks' fp16 scales before it
+// waits on any of them; the small activation loads are issued before the weights, so the first wait
+// is for them alone.  Block indices past the row end are clamped, never branched around.
 #include <algorithm>
 
 #include "device_common.h"
 
 namespace phx {
 
-// Q8_0 of 32 values held one per lane of a 32-lane half (CpuRef.QuantizeQ8_0, src/CpuRef.cs:49-62):
-// returns q; *dval and *sum (fp16 scale value and block sum) are valid in every lane of the half.
+constexpr int DMAXNB = 128;  // blocks of 32 per row: K <= 4096
+constexpr int DROWS = 2;     // assignments (expert tiles) or tokens (shared FFN) per workgroup
+constexpr int DBPW = 8;      // blocks per wave
+constexpr int RPER = 16;     // router elements per thread (d <= 4096 over >= 256 threads)
+
+template <int TYPE>
+struct DecCfg {
+    static constexpr int PAY = TYPE == PHX_Q4_0_DEV ? 16 : 32;  // payload bytes per block
+    static constexpr int NC = PAY / 16;                         // 16 B loads per block
+};
+
+// decode-layout view of one matrix stack (QMat): payload [m][rg][b][64][PAY], scales [m][rg][b/8][64][8]
+struct MatD {
+    const uint8_t* pay;
+    const uint4* sc8;
+    int64_t mat_pay;  // bytes per matrix
+    int64_t mat_sc8;  // uint4 per matrix
+    int rg, nb, nb8, rows;
+};
+
+// Q8_0 activation rows in LDS: q as 8 dwords per block, the fp16 scale value, the block sum
+struct ActL {
+    int q[DMAXNB * 8];
+    float d[DMAXNB];
+    int s[DMAXNB];
+};
+
+struct DecArgs {
+    int T, d, E, k, nf, nff, rule, max_tiles;
+    float eps;
+    const float* x;       // [T][d]
+    const float* W;       // [E][d] router (ffn_gate_inp.weight)
+    const float* gis;     // ffn_gate_inp.scale
+    const float* ds;      // ffn_down_exps.scale
+    const float* pre2;    // pre_ffw_norm_2
+    const float* post1;   // post_ffw_norm_1
+    const float* post2;   // post_ffw_norm_2
+    const float* fnorm;   // ffn_norm (shared FFN input)
+    const float* post_ffw;
+    MatD gu, dn, sgu, sdn;  // sgu.rg == 0: no shared FFN computed
+    double* Lb;           // [T][E] certified logits (double sums)
+    double* Bb;           // [T][E] their error bounds
+    int* ids;             // [T][k]
+    float* w;             // [T][k]
+    float* logits;        // [T][E]
+    int* offsets;         // [E + 1]
+    int* perm;            // [T * k]
+    DecTile* tiles;       // [max_tiles] (e = -1 past the last tile)
+    float* g;             // [T*k][nf] gate products
+    float* u;             // [T*k][nf] up products
+    Act adn;              // Q8_0 of gelu(g) * u: the down input, [T*k][nf]
+    float* yd;            // [T*k][d] down products
+    float* shg;           // [T][nff]
+    float* shu;
+    Act asd;              // Q8_0 of the shared gelu(g) * u, [T][nff]
+    float* shout;         // [T][d] shared branch (the shared FFN's output, or the given one), or null
+    float* out;           // [T][d]
+    float* xres;          // x updated in place with the residual, or null
+    const float* gelu_tab;
+    int* flags;           // [0] norm fallbacks, [1] router fallbacks
+};
+
+// ------------------------------------------------------------------------------ helpers
+
+// Q8_0 of one 32-block held as 4 consecutive values per lane by an 8-lane group (lane l of the group:
+// elements 4l..4l+3), CpuRef.QuantizeQ8_0 (src/CpuRef.cs:49-62): amax, d = amax / 127, id = 1 / d,
+// q = roundf(x * id) (half away from zero), fp16 d.  Returns the lane's 4 q bytes as one dword (the
+// LDS activation layout); *dval and *sum (the block's q sum) are valid in all 8 lanes.
+__device__ __forceinline__ int q8_0_oct(float4 v, float* dval, int* sum)
+{
+    float am = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    am = fmaxf(am, __shfl_xor(am, 1, 64));
+    am = fmaxf(am, __shfl_xor(am, 2, 64));
+    am = fmaxf(am, __shfl_xor(am, 4, 64));
+    const float dd = am / 127.0f;
+    const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
+    const int q0 = (int)roundf(v.x * id), q1 = (int)roundf(v.y * id), q2 = (int)roundf(v.z * id),
+              q3 = (int)roundf(v.w * id);
+    int sm = q0 + q1 + q2 + q3;
+    sm += __shfl_xor(sm, 1, 64);
+    sm += __shfl_xor(sm, 2, 64);
+    sm += __shfl_xor(sm, 4, 64);
+    *dval = h2f(f2h_bits(dd));
+    *sum = sm;
+    return (q0 & 0xFF) | ((q1 & 0xFF) << 8) | ((q2 & 0xFF) << 16) | (int)((unsigned)q3 << 24);
+}
+
+// The same for 32 values held one per lane of a 32-lane half; returns q.
 __device__ __forceinline__ int q8_0_half(float x, float* dval, int* sum)
 {
     const float amax = half_max_f(fabsf(x));
@@ -26,58 +123,257 @@ __device__ __forceinline__ int q8_0_half(float x, float* dval, int* sum)
     return q;
 }
 
-// ------------------------------------------------------------------------------ router (decode)
-// One wave per (token, expert).  The reference logit is the sequential float sum of the rounded
-// products p_i = fl(W[e][i] * m_i) (src/GemmaCpu.cs:390-395).  The wave forms the same p_i, sums
-// them in double (L), and bounds the reference's accumulated rounding:
-//   |S_ref - L| <= 2^-24 * sum_k |S_k| / (1 - n 2^-24)  (+ slack for the double arithmetic),
-// S_k the exact prefix sums (a wave scan).  The last workgroup ranks the experts by L and accepts
-// the order if every chosen expert's interval lies strictly above every later expert's; otherwise
-// the experts whose intervals reach the chosen ones are recomputed as the reference's float chains
-// and ranked exactly.  Ids are therefore always the reference's; weights use (float)L for certified
-// tokens (within ~1e-6 of the reference's logit) and the exact logits otherwise.
-// The same launch also writes the Q8_0 expert input n = x * scale * pre_ffw_norm_2 (and the shared
-// FFN input with ffn_norm): workgroup (bx, t) quantizes every (8 * gridDim.x)-th 32-block of token t.
-struct RouteDecArgs {
-    int T, d, E, k, rule, A, max_tiles;
-    float eps;
-    const float* x;
-    const float* W;       // [E][d] row-major (ffn_gate_inp.weight)
-    const float* gis;     // ffn_gate_inp.scale
-    const float* ds;      // ffn_down_exps.scale
-    const float* pre2;    // pre_ffw_norm_2
-    const float* fnorm;   // ffn_norm (shared FFN input) or null
-    Act act_gu, act_sh;
-    double* Lb;           // [T][E]
-    double* Bb;           // [T][E]
-    int* counter;         // zero between launches
-    int* ids;
-    float* w;
-    float* logits;
-    int* offsets;
-    int* perm;
-    DecTile* tiles;
-    int* ntiles;
-    int* flags;           // [0] norm fallbacks, [1] router fallbacks
+// Mean of squares of a row (RmsNorm's (float)(sum / n), sum the sequential double sum of x_i^2,
+// src/CpuRef.cs:186-188) from per-thread partial double sums `s` over disjoint elements.  Any order of
+// summing n non-negative terms is within (n + 64) * 2^-52 * sum of the sequential sum (the summation
+// depth here is far below 64); when both ends of that interval give the same float the result is the
+// reference's, otherwise thread 0 re-sums sequentially (rare; counted in *fallbacks when non-null).
+// Workgroup-level: every thread calls it; red holds blockDim.x / 64 + 1 doubles.
+__device__ float wg_mean_sq(double s, const float* xr, int n, double* red, int* fallbacks)
+{
+    const int tid = threadIdx.x, nw = blockDim.x >> 6;
+    s = wave_sum_dpp(s);
+    if ((tid & 63) == 0) red[tid >> 6] = s;
+    __syncthreads();
+    double S = 0.0;
+    for (int w = 0; w < nw; w++) S += red[w];
+    const double B = ((double)n + 64.0) * 0x1p-52 * S;
+    const float lo = (float)((S - B) / (double)n), hi = (float)((S + B) / (double)n);
+    float mean = lo;
+    if (lo != hi) {  // uniform: every thread formed the same S
+        if (tid == 0) {
+            double q = 0.0;
+            for (int i = 0; i < n; i++) q += (double)xr[i] * (double)xr[i];
+            red[nw] = q;
+            if (fallbacks) atomicAdd(fallbacks, 1);
+        }
+        __syncthreads();
+        mean = (float)(red[nw] / (double)n);
+    }
+    __syncthreads();  // red is reused by the next call
+    return mean;
+}
+
+// The Q8_0 input rows of a gate|up workgroup: n_i = (x_i * rinv) * nw_i (src/GemmaCpu.cs:409 with
+// CpuRef.RmsNorm, src/CpuRef.cs:183-191; the shared FFN: ffn_norm, :349), rinv the token's RmsNorm
+// scale, quantized per 32-block into act[r].  8-lane group g takes block g (the workgroup has at least
+// 8 * nb threads).  quant_issue loads the values (before the weight loads); quant_finish forms the rows.
+struct QIn {
+    float4 x0, x1, nw;
 };
 
-constexpr int RT_PER = 16;        // elements per lane (d <= 4096, 256 lanes)
-typedef __attribute__((address_space(3))) void* lds_void_t;
-typedef __attribute__((address_space(1))) void* glb_void_t;
-
-__device__ __forceinline__ double ld_agent(const double* p)
+__device__ __forceinline__ void quant_issue(QIn& in, const float* x, int tok0, int tok1, const float* nw, int d)
 {
-    unsigned long long v = __hip_atomic_load((const unsigned long long*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return __longlong_as_double((long long)v);
+    const int tid = threadIdx.x, nb = d / 32;
+    const int i = min(tid >> 3, nb - 1) * 8 + (tid & 7);
+    in.nw = ((const float4*)nw)[i];
+    in.x0 = ((const float4*)(x + (int64_t)tok0 * d))[i];
+    in.x1 = ((const float4*)(x + (int64_t)tok1 * d))[i];  // tok1 == tok0 for one row: no branch
 }
 
-__device__ __forceinline__ void st_agent(double* p, double v)
+__device__ __forceinline__ void quant_row(float4 xv, float4 nwv, const float* xr, int d, float eps, ActL& act,
+                                          double* red, int* fallbacks)
 {
-    __hip_atomic_store((unsigned long long*)p, (unsigned long long)__double_as_longlong(v), __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
+    const int tid = threadIdx.x, b = tid >> 3, l8 = tid & 7, nb = d / 32;
+    double s = 0.0;
+    if (b < nb)
+        s = ((double)xv.x * (double)xv.x + (double)xv.y * (double)xv.y) +
+            ((double)xv.z * (double)xv.z + (double)xv.w * (double)xv.w);
+    const float rinv = rms_scale_from_mean(wg_mean_sq(s, xr, d, red, fallbacks), eps);
+    const float4 v = make_float4((xv.x * rinv) * nwv.x, (xv.y * rinv) * nwv.y, (xv.z * rinv) * nwv.z,
+                                 (xv.w * rinv) * nwv.w);
+    float dval;
+    int sum;
+    const int qw = q8_0_oct(v, &dval, &sum);
+    if (b < nb) {
+        act.q[b * 8 + l8] = qw;
+        if (l8 == 0) {
+            act.d[b] = dval;
+            act.s[b] = sum;
+        }
+    }
 }
 
-// exact reference logit of expert e for token t (src/GemmaCpu.cs:389-395)
+__device__ __forceinline__ void quant_finish(const QIn& in, const float* x, int tok0, int tok1, int cnt, int d, float eps,
+                                             ActL* act, double* red, int* fallbacks)
+{
+    quant_row(in.x0, in.nw, x + (int64_t)tok0 * d, d, eps, act[0], red, fallbacks);
+    if (cnt > 1) quant_row(in.x1, in.nw, x + (int64_t)tok1 * d, d, eps, act[1], red, fallbacks);
+}
+
+// Q8_0 rows of a packed global activation buffer into LDS (nb blocks each): act_issue loads them into
+// registers (before the weight loads), act_store writes them to LDS.  A packed global row is 10 * nb
+// contiguous dwords: q (8 nb), d (nb), s (nb) (the decode path's Act buffers, see the runtime); an ActL
+// row holds the same at fixed offsets.  The workgroup has at least 8 * nb threads, so two dwords per
+// thread and row cover 10 * nb.
+struct ActIn {
+    int v[DROWS][2];
+};
+
+__device__ __forceinline__ const int* act_src(const Act& src, int64_t row, int nb, int i)
+{
+    return (const int*)(src.q + row * src.qstride) + min(i, 10 * nb - 1);
+}
+
+__device__ __forceinline__ int act_dst(int nb, int i)  // dword index in an ActL row
+{
+    return i < 8 * nb ? i : i < 9 * nb ? 8 * DMAXNB + (i - 8 * nb) : 9 * DMAXNB + (i - 9 * nb);
+}
+
+__device__ __forceinline__ void act_issue(ActIn& in, const Act& src, int64_t row0, int64_t row1, int cnt, int nb)
+{
+    const int tid = threadIdx.x, nt = blockDim.x;
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+        const int i = min(tid + nt * c, 10 * nb - 1);
+        in.v[0][c] = *act_src(src, row0, nb, i);
+        in.v[1][c] = *act_src(src, row1, nb, i);  // row1 == row0 for one row: no branch
+    }
+}
+
+__device__ __forceinline__ void act_store(const ActIn& in, int cnt, int nb, ActL* act)
+{
+    const int tid = threadIdx.x, nt = blockDim.x;
+#pragma unroll
+    for (int r = 0; r < DROWS; r++) {
+        if (r < cnt) {
+#pragma unroll
+            for (int c = 0; c < 2; c++) {
+                const int i = tid + nt * c;
+                if (i < 10 * nb) ((int*)&act[r])[act_dst(nb, i)] = in.v[r][c];
+            }
+        }
+    }
+}
+
+// Weight registers of one wave: blocks 8w..8w+7 of the lane's row (indices clamped to the row) and
+// their 8 fp16 scales.
+template <int TYPE>
+struct WRegs {
+    uint4 p[DBPW][DecCfg<TYPE>::NC];
+    uint4 s;
+};
+
+template <int TYPE>
+__device__ __forceinline__ void load_w(const MatD& M, int e, int rgi, int wave, int lane, WRegs<TYPE>& W)
+{
+    constexpr int PAY = DecCfg<TYPE>::PAY, NC = DecCfg<TYPE>::NC;
+    const int b0 = min(wave * DBPW, (M.nb8 - 1) * DBPW);  // waves past the row reload its last blocks
+    const uint8_t* p = M.pay + (int64_t)e * M.mat_pay + ((int64_t)rgi * M.nb * 64 + lane) * PAY;
+#pragma unroll
+    for (int j = 0; j < DBPW; j++) {
+        const int b = min(b0 + j, M.nb - 1);
+#pragma unroll
+        for (int c = 0; c < NC; c++) W.p[j][c] = *(const uint4*)(p + (int64_t)b * 64 * PAY + 16 * c);
+    }
+    W.s = M.sc8[(int64_t)e * M.mat_sc8 + ((int64_t)rgi * M.nb8 + b0 / DBPW) * 64 + lane];
+}
+
+// fp16 scale bits of block j of a WRegs
+template <int TYPE>
+__device__ __forceinline__ uint32_t w_scale(const WRegs<TYPE>& W, int j)
+{
+    const int h = j / 2;
+    const uint32_t wd = h == 0 ? W.s.x : h == 1 ? W.s.y : h == 2 ? W.s.z : W.s.w;
+    return (j & 1) ? wd >> 16 : wd & 0xFFFFu;
+}
+
+// The reference block term (float)isum * (d_w * d_x) of block j of W against activation block b.
+template <int TYPE>
+__device__ __forceinline__ float blk_term(const WRegs<TYPE>& W, int j, const ActL& a, int b)
+{
+    const int4 xa = *(const int4*)&a.q[b * 8];
+    const int4 xb = *(const int4*)&a.q[b * 8 + 4];
+    int isum = 0;
+    if (TYPE == PHX_Q4_0_DEV) {
+        const uint4 w = W.p[j][0];
+        // low nibbles: elements 0..15 (x words 0..3); high nibbles: elements 16..31 (x words 4..7)
+        isum = __builtin_amdgcn_sdot4((int)(w.x & 0x0F0F0F0Fu), xa.x, isum, false);
+        isum = __builtin_amdgcn_sdot4((int)(w.y & 0x0F0F0F0Fu), xa.y, isum, false);
+        isum = __builtin_amdgcn_sdot4((int)(w.z & 0x0F0F0F0Fu), xa.z, isum, false);
+        isum = __builtin_amdgcn_sdot4((int)(w.w & 0x0F0F0F0Fu), xa.w, isum, false);
+        isum = __builtin_amdgcn_sdot4((int)((w.x >> 4) & 0x0F0F0F0Fu), xb.x, isum, false);
+        isum = __builtin_amdgcn_sdot4((int)((w.y >> 4) & 0x0F0F0F0Fu), xb.y, isum, false);
+        isum = __builtin_amdgcn_sdot4((int)((w.z >> 4) & 0x0F0F0F0Fu), xb.z, isum, false);
+        isum = __builtin_amdgcn_sdot4((int)((w.w >> 4) & 0x0F0F0F0Fu), xb.w, isum, false);
+        isum -= 8 * a.s[b];
+    } else {
+        const uint4 w0 = W.p[j][0], w1 = W.p[j][DecCfg<TYPE>::NC - 1];
+        isum = __builtin_amdgcn_sdot4((int)w0.x, xa.x, isum, false);
+        isum = __builtin_amdgcn_sdot4((int)w0.y, xa.y, isum, false);
+        isum = __builtin_amdgcn_sdot4((int)w0.z, xa.z, isum, false);
+        isum = __builtin_amdgcn_sdot4((int)w0.w, xa.w, isum, false);
+        isum = __builtin_amdgcn_sdot4((int)w1.x, xb.x, isum, false);
+        isum = __builtin_amdgcn_sdot4((int)w1.y, xb.y, isum, false);
+        isum = __builtin_amdgcn_sdot4((int)w1.z, xb.z, isum, false);
+        isum = __builtin_amdgcn_sdot4((int)w1.w, xb.w, isum, false);
+    }
+    const float dd = h2f(w_scale(W, j)) * a.d[b];
+    return (float)isum * dd;
+}
+
+// One row group for cnt <= DROWS activation rows: every wave's block terms into LDS
+// (terms[r][b][lane], row stride nb), then wave r adds row r's terms in block order.  Returns the chain
+// value in waves r < cnt (0 elsewhere).
+template <int TYPE>
+__device__ float rowgroup_chain(const WRegs<TYPE>& W, int nb, const ActL* act, int cnt, float* terms)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, b0 = wave * DBPW;
+    if (b0 < nb) {  // uniform per wave
+        for (int r = 0; r < cnt; r++) {
+#pragma unroll
+            for (int j = 0; j < DBPW; j++) {
+                const int b = min(b0 + j, nb - 1);
+                const float t = blk_term(W, j, act[r], b);
+                if (b0 + j < nb) terms[(r * nb + b0 + j) * 64 + lane] = t;
+            }
+        }
+    }
+    __syncthreads();
+    float S = 0.0f;
+    if (wave < cnt) {
+        const float* tr = terms + wave * nb * 64 + lane;
+        int b = 0;
+        for (; b + 8 <= nb; b += 8) {
+            float t[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) t[i] = tr[(b + i) * 64];
+#pragma unroll
+            for (int i = 0; i < 8; i++) S += t[i];
+        }
+        for (; b < nb; b++) S += tr[b * 64];
+    }
+    return S;
+}
+
+// gate|up epilogue of a paired row group (lanes 0-31 gate rows 32 rgi + l, lanes 32-63 the matching
+// up rows): g and u to the debug outputs, e = gelu(g) * u (src/GemmaCpu.cs:415) quantized to the
+// Q8_0 block rgi of the down input row (src/CpuRef.cs:49-62).
+__device__ __forceinline__ void gu_epilogue(float S, int rgi, int split, int64_t orow, float* g, float* u, const Act& o,
+                                            const float* gelu_tab)
+{
+    const int lane = threadIdx.x & 63;
+    const int jj = rgi * 32 + (lane & 31);
+    const float uv = __shfl_down(S, 32, 64);
+    if (jj < split) {
+        if (lane < 32) g[orow * split + jj] = S;
+        else u[orow * split + jj] = S;
+    }
+    const float ev = lane < 32 ? gelu_ref(S, gelu_tab) * uv : 0.0f;
+    float dval;
+    int sum;
+    const int q = q8_0_half(ev, &dval, &sum);
+    if (lane < 32) {
+        o.q[orow * o.qstride + jj] = (int8_t)q;
+        if (lane == 0) {
+            o.d[orow * o.dstride + rgi] = dval;
+            o.s[orow * o.sstride + rgi] = sum;
+        }
+    }
+}
+
+// exact reference logit of expert e for token t (src/GemmaCpu.cs:389-395): the products rounded,
+// added in index order
 __device__ float exact_logit(const float* x, const float* W, const float* gis, int d, int t, int e, float rinv, float sc)
 {
     const float* xr = x + (int64_t)t * d;
@@ -93,353 +389,268 @@ __device__ float exact_logit(const float* x, const float* W, const float* gis, i
     return s;
 }
 
-// One workgroup per (expert e, token t): x_t, the router scale and W[e] staged in LDS, then each of
-// the 256 lanes takes d / 256 consecutive indices; the double sum, its prefix sums (a wave scan
-// plus the four wave totals) and the bound terms follow the layout above.
-__global__ __launch_bounds__(256) void k_route_dec(RouteDecArgs a)
-{
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, tid = threadIdx.x;
-    const int e = blockIdx.x, t = blockIdx.y;
-    extern __shared__ __align__(16) unsigned char rsm[];
-    __shared__ int s_last, s_bad[16];
-    __shared__ double red[8], wsum[4], wA[4], wP[4], s_seq;
-    __shared__ int s_ids[256], s_perm[256];
-    __shared__ int s_cnt[PHX_MAX_EXPERTS_DEV + 1], s_off[PHX_MAX_EXPERTS_DEV + 1], s_tb[PHX_MAX_EXPERTS_DEV + 1];
-    const float sc = 1.0f / (float)__dsqrt_rn((double)a.d);
-    const float* xr = a.x + (int64_t)t * a.d;
-    const int d = a.d;
+typedef __attribute__((address_space(3))) void* lds_void_t;
+typedef __attribute__((address_space(1))) void* glb_void_t;
 
-    // ---- x_t, the router scale and W[e] into LDS (direct global -> LDS loads, 16 B per lane,
-    // every load in flight at once; each wave fills 64 consecutive float4 per instruction)
-    float* sx = (float*)rsm;
-    float* sg = sx + d;
-    float* sw = sg + d;
-    // the norm weight of this thread's first quantization slot (see below), loaded beside the staging
-    const int nin = a.fnorm ? 2 : 1, q_p0 = e * 8 + (tid >> 5);
-    float nw0 = 0.0f;
-    if (q_p0 < (d / 32) * nin) {
-        const int b = q_p0 / nin;
-        nw0 = (q_p0 - b * nin ? a.fnorm : a.pre2)[b * 32 + (tid & 31)];
-    }
+// ------------------------------------------------------------------------------ k_dec_route
+// Router part: one workgroup per (token t, expert e).  The reference logit is the sequential float
+// sum of the rounded products p_i = fl(W[e][i] * m_i), m_i = ((x_i * rinv) * sc) * s_i
+// (src/GemmaCpu.cs:389-395).  The workgroup forms the same p_i (each thread a contiguous chunk of i),
+// sums them in double (L), and bounds the reference's accumulated rounding by
+//   |S_ref - L| <= 2^-24 * sum_k |S_k| * 1.001 + 2^-45 * sum_i |p_i|,
+// S_k the prefix sums (a scan over the chunks), the second term covering the double arithmetic.
+// k_dec_gu ranks the experts by L and certifies the order from these intervals.
+__device__ void route_wg(const DecArgs& a, int t, int e, unsigned char* smem)
+{
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, d = a.d, NT = blockDim.x, NWV = NT >> 6;
+    float* sx = (float*)smem;
+    float* sg = sx + d + RPER;
+    float* sw = sg + d + RPER;
+    double* red = (double*)(sw + d + RPER);  // 17
+    double* wsum = red + 17;                 // 16
+    double* wA = wsum + 16;
+    double* wP = wA + 16;
     {
+        // x_t, the router scale and W[e] into LDS with direct global -> LDS loads (16 B per lane)
         const int n4 = d / 4;
-        const float4* srcs[3] = {(const float4*)xr, (const float4*)a.gis, (const float4*)(a.W + (int64_t)e * d)};
-#pragma unroll
-        for (int r = 0; r < 3; r++) {
-            float4* dst = (float4*)(sx + r * d);
-            for (int q = 0; q * 256 < n4; q++) {
-                const int i = q * 256 + tid;
+        auto stage = [&](const float* src, float* dst) {
+            for (int q = 0; q * NT < n4; q++) {
+                const int i = q * NT + tid;
                 if (i < n4)
-                    __builtin_amdgcn_global_load_lds((glb_void_t)(srcs[r] + i), (lds_void_t)(dst + q * 256 + wave * 64), 16, 0,
-                                                     0);
+                    __builtin_amdgcn_global_load_lds((glb_void_t)((const float4*)src + i),
+                                                     (lds_void_t)((float4*)dst + q * NT + wave * 64), 16, 0, 0);
             }
-        }
+        };
+        stage(a.x + (int64_t)t * d, sx);
+        stage(a.gis, sg);
+        stage(a.W + (int64_t)e * d, sw);
         __builtin_amdgcn_s_waitcnt(0);
     }
     __syncthreads();
-    // ---- the lane's contiguous chunk of d / 256 indices (d % 256 == 0)
-    const int per = d / 256, c0 = tid * per;
-    // certified mean of squares of x_t: every workgroup of the token forms the same sum in the same order
-    double s = 0.0;
+    const int per = (d + NT - 1) / NT, c0 = min(tid * per, d), cnt = min(per, d - c0);
+    float xv[RPER], gv[RPER], wv[RPER];
 #pragma unroll
-    for (int j = 0; j < RT_PER; j++)
-        if (j < per) {
-            const double v = (double)sx[c0 + j];
-            s += v * v;
-        }
-    s = wave_sum_dpp(s);
-    if (lane == 0) red[wave] = s;
+    for (int j = 0; j < RPER; j++) {
+        xv[j] = sx[c0 + j];
+        gv[j] = sg[c0 + j];
+        wv[j] = sw[c0 + j];
+    }
+    double s2 = 0.0;
+#pragma unroll
+    for (int j = 0; j < RPER; j++)
+        if (j < cnt) s2 += (double)xv[j] * (double)xv[j];
+    int* flags0 = (t == 0 && e == 0) ? a.flags : nullptr;
+    const float rinv = rms_scale_from_mean(wg_mean_sq(s2, sx, d, red, flags0), a.eps);
+    const float sc = 1.0f / (float)__dsqrt_rn((double)d);
+    float pv[RPER];
+    double loc = 0.0, P = 0.0;
+#pragma unroll
+    for (int j = 0; j < RPER; j++) {
+        const float p = wv[j] * (xv[j] * rinv * sc * gv[j]);
+        pv[j] = j < cnt ? p : 0.0f;
+        loc += (double)pv[j];
+        P += fabs((double)pv[j]);
+    }
+    const double inc = wave_incl_scan_dpp(loc);
+    if (lane == 63) wsum[wave] = inc;
     __syncthreads();
-    const double S = (red[0] + red[1]) + (red[2] + red[3]);
-    const double Bs = ((double)d + per + 256.0) * 0x1p-53 * S * 2.0;
-    float mean = (float)((S - Bs) / (double)d);
-    if (mean != (float)((S + Bs) / (double)d)) {  // uniform: S is the same in every thread
-        if (tid == 0) {
-            double q = 0.0;
-            for (int i = 0; i < d; i++) q += (double)sx[i] * (double)sx[i];
-            s_seq = q;
-            if (a.flags && e == 0) atomicAdd(a.flags, 1);
-        }
-        __syncthreads();
-        mean = (float)(s_seq / (double)d);
-    }
-    const float rinv = rms_scale_from_mean(mean, a.eps);  // also the RmsNorm scale of x_t
-    {
-        // p_i = fl(W[e][i] * m_i), m_i = ((x_i * rinv) * sc) * s_i (src/GemmaCpu.cs:389,394)
-        float pv[RT_PER];
-        double loc = 0.0, P = 0.0;
+    double base = 0.0;
+    for (int w = 0; w < wave; w++) base += wsum[w];
+    double acc = base + (inc - loc);  // exclusive prefix (within the double slack of the bound)
+    double A = 0.0;
 #pragma unroll
-        for (int j = 0; j < RT_PER; j++) {
-            if (j < per) {
-                pv[j] = sw[c0 + j] * (sx[c0 + j] * rinv * sc * sg[c0 + j]);
-                loc += (double)pv[j];
-                P += fabs((double)pv[j]);
-            } else {
-                pv[j] = 0.0f;
-            }
-        }
-        const double inc = wave_incl_scan_dpp(loc);
-        if (lane == 63) wsum[wave] = inc;
-        __syncthreads();
-        double base = 0.0;
-        for (int w = 0; w < wave; w++) base += wsum[w];
-        double acc = base + (inc - loc);  // exclusive prefix (within the double slack of the bound)
-        double A = 0.0;
-#pragma unroll
-        for (int j = 0; j < RT_PER; j++)
-            if (j < per) {
-                acc += (double)pv[j];
-                A += fabs(acc);
-            }
-        A = wave_sum_dpp(A);
-        P = wave_sum_dpp(P);
-        if (lane == 0) {
-            wA[wave] = A;
-            wP[wave] = P;
-        }
-        __syncthreads();
-        if (tid == 0) {
-            const double L = ((wsum[0] + wsum[1]) + wsum[2]) + wsum[3];
-            const double As = (wA[0] + wA[1]) + (wA[2] + wA[3]), Ps = (wP[0] + wP[1]) + (wP[2] + wP[3]);
-            st_agent(&a.Lb[(int64_t)t * a.E + e], L);
-            st_agent(&a.Bb[(int64_t)t * a.E + e], 0x1p-24 * As * 1.001 + 0x1p-45 * Ps);
-        }
+    for (int j = 0; j < RPER; j++) {
+        acc += (double)pv[j];
+        if (j < cnt) A += fabs(acc);
     }
-
-    // ---- quantized expert input (and shared FFN input) of token t: one 32-lane half per (block, input),
-    // spread over the E workgroups of the token
-    {
-        const int nbK = d / 32, l32 = tid & 31;
-        for (int p = q_p0; p < nbK * nin; p += a.E * 8) {
-            const int b = p / nin, which = p - b * nin;
-            const int i = b * 32 + l32;
-            const float nwv = p == q_p0 ? nw0 : (which ? a.fnorm : a.pre2)[i];
-            const Act& o = which ? a.act_sh : a.act_gu;
-            float dval;
-            int sum;
-            const int q = q8_0_half(sx[i] * rinv * nwv, &dval, &sum);
-            o.q[(int64_t)t * o.qstride + i] = (int8_t)q;
-            if (l32 == 0) {
-                o.d[(int64_t)t * o.dstride + b] = dval;
-                o.s[(int64_t)t * o.sstride + b] = sum;
-            }
-        }
+    A = wave_sum_dpp(A);
+    P = wave_sum_dpp(P);
+    if (lane == 0) {
+        wA[wave] = A;
+        wP[wave] = P;
     }
-
-    // ---- hand-off to the last workgroup: the barrier orders every wave's stores before thread 0's
-    // agent-scope release increment; the workgroup that completes the count acquires.
     __syncthreads();
     if (tid == 0) {
-        const int total = gridDim.x * gridDim.y;
-        const int prev = __hip_atomic_fetch_add(a.counter, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = prev == total - 1;
+        double L = 0.0, As = 0.0, Ps = 0.0;
+        for (int w = 0; w < NWV; w++) {
+            L += wsum[w];
+            As += wA[w];
+            Ps += wP[w];
+        }
+        a.Lb[(int64_t)t * a.E + e] = L;
+        a.Bb[(int64_t)t * a.E + e] = 0x1p-24 * As * 1.001 + 0x1p-45 * Ps;
     }
-    __syncthreads();
-    if (!s_last) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+}
 
-    const int TE = a.T * a.E;
-    double* sL = (double*)rsm;
-    double* sB = sL + TE;
-    unsigned* s_key = (unsigned*)(sB + TE);
-    short* s_rank = (short*)(s_key + TE);
-    char* s_amb = (char*)(s_rank + TE);
-    for (int i = tid; i < TE; i += 256) {
-        sL[i] = ld_agent(&a.Lb[i]);
-        sB[i] = ld_agent(&a.Bb[i]);
-    }
-    if (tid < 16) s_bad[tid] = 0;
+// Shared FFN gate|up part: one workgroup per (pair of tokens, paired row group).
+template <int TYPE>
+__device__ void shared_gu_wg(const DecArgs& a, int tile, int rgi, unsigned char* smem)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    ActL* act = (ActL*)smem;
+    double* red = (double*)(act + DROWS);
+    float* terms = (float*)(red + 32);
+    const int t0 = tile * DROWS, cnt = min(DROWS, a.T - t0), t1 = min(t0 + 1, a.T - 1);
+    QIn qin;
+    quant_issue(qin, a.x, t0, t1, a.fnorm, a.d);
+    __builtin_amdgcn_sched_barrier(0);  // keep the activation loads ahead of the weight loads
+    WRegs<TYPE> W;
+    load_w<TYPE>(a.sgu, 0, rgi, wave, lane, W);  // unconditional: a wave past the row reloads its last block
+    quant_finish(qin, a.x, t0, t1, cnt, a.d, a.eps, act, red, nullptr);
     __syncthreads();
-    // selection: the rank of every (token, expert) from all pairs in LDS (one to two threads per
-    // pair) by a 32-bit key: the order-preserving bits of (float)L with the low 8 bits replaced by
-    // 255 - expert, so keys are distinct and ties go to the lower index.  The order is then certified
-    // per token if each chosen expert's lower end lies above the upper ends of every expert ranked
-    // after it.  An order the key gets wrong (logits within 256 float ulps) is never certified, since
-    // certification compares the intervals themselves; such tokens take the exact path below.
-    for (int i = tid; i < TE; i += 256) {
-        const int ex = i % a.E;
-        s_key[i] = (sortable_f32((float)sL[i]) & ~0xFFu) | (unsigned)(255 - ex);
+    const float S = rowgroup_chain<TYPE>(W, a.sgu.nb, act, cnt, terms);
+    if (wave < cnt) gu_epilogue(S, rgi, a.nff, t0 + wave, a.shg, a.shu, a.asd, a.gelu_tab);
+}
+
+template <int TYPE>
+__global__ __launch_bounds__(1024) void k_dec_route(DecArgs a)
+{
+    extern __shared__ __align__(16) unsigned char dsm[];
+    const int nr = a.T * a.E;
+    if ((int)blockIdx.x < nr) {
+        route_wg(a, blockIdx.x / a.E, blockIdx.x % a.E, dsm);
+    } else {
+        const int s = blockIdx.x - nr;
+        shared_gu_wg<TYPE>(a, s / a.sgu.rg, s % a.sgu.rg, dsm);
     }
-    __syncthreads();
-    {
-        int split = 1;  // threads per pair: a power of two, split * TE <= 256
-        while (split < 64 && split * 2 * TE <= 256) split *= 2;
-        const int part = tid % split, chunk = (a.E + split - 1) / split;
-        for (int i = tid / split; i < TE; i += 256 / split) {
-            const int tt = i / a.E;
-            const unsigned my = s_key[i];
-            const unsigned* kr = s_key + tt * a.E;
-            const int c0 = part * chunk, c1 = min(a.E, c0 + chunk);
-            int r = 0, c = c0;
-            for (; c + 8 <= c1; c += 8) {  // eight keys in flight per step
-                const unsigned k0 = kr[c], k1 = kr[c + 1], k2 = kr[c + 2], k3 = kr[c + 3], k4 = kr[c + 4], k5 = kr[c + 5],
-                               k6 = kr[c + 6], k7 = kr[c + 7];
-                r += (int)(k0 > my) + (int)(k1 > my) + (int)(k2 > my) + (int)(k3 > my) + (int)(k4 > my) + (int)(k5 > my) +
-                     (int)(k6 > my) + (int)(k7 > my);
+}
+
+// ------------------------------------------------------------------------------ k_dec_gu
+// Selection, in every expert workgroup.  Fast path, one wave per token: the experts' 32-bit keys (the
+// order-preserving bits of (float)L with the low 8 bits replaced by 255 - expert, so keys are
+// distinct and ties go to the lower index) and k rounds of a wave maximum give the top-k.  The order
+// is certified if each chosen expert's lower end L - B lies above the upper ends L + B of every expert
+// ranked after it; an order the key gets wrong (logits within 256 float ulps) is never certified,
+// since certification compares the intervals themselves.  When a token is not certified, the whole
+// workgroup takes select_exact.
+__device__ bool wave_topk(const DecArgs& a, int t, int* s_ids)
+{
+    const int lane = threadIdx.x & 63;
+    const double* Lr = a.Lb + (int64_t)t * a.E;
+    const double* Br = a.Bb + (int64_t)t * a.E;
+    double L[4], B[4];
+    unsigned key[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const int ex = min(lane + 64 * q, a.E - 1);
+        L[q] = Lr[ex];
+        B[q] = Br[ex];
+    }
+    bool fin = true;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const int ex = lane + 64 * q;
+        key[q] = ex < a.E ? (sortable_f32((float)L[q]) & ~0xFFu) | (unsigned)(255 - ex) : 0u;
+        if (ex < a.E && !(isfinite(L[q]) && isfinite(B[q]))) fin = false;
+    }
+    // k rounds of the wave maximum; chosen[q] marks this lane's chosen slots
+    bool chosen[4] = {false, false, false, false};
+    double lo_mine = INFINITY, hi_mine = -INFINITY;  // lane j: the rank-j expert's interval
+    int id_mine = 0;
+    for (int j = 0; j < a.k; j++) {
+        unsigned m = max(max(key[0], key[1]), max(key[2], key[3]));
+        m = wave_max_u32(m);
+        const int ex = 255 - (int)(m & 0xFFu);
+        // the slot owning the key leaves the candidates; its interval goes to lane j
+        double lo = INFINITY, hi = -INFINITY;
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            if (key[q] == m && lane + 64 * q == ex) {
+                key[q] = 0u;
+                chosen[q] = true;
+                lo = L[q] - B[q];
+                hi = L[q] + B[q];
             }
-            for (; c < c1; c++) r += kr[c] > my;
-            for (int o = 1; o < split; o <<= 1) r += __shfl_xor(r, o, 64);
-            if (part == 0) s_rank[i] = (short)min(r, a.k + 1);
+        const int owner = ex & 63;
+        lo = __shfl(lo, owner, 64);
+        hi = __shfl(hi, owner, 64);
+        if (lane == j) {
+            lo_mine = lo;
+            hi_mine = hi;
+            id_mine = ex;
         }
     }
-    __syncthreads();
-    for (int i = tid; i < TE; i += 256)
-        if (s_rank[i] < a.k) s_ids[(i / a.E) * a.k + s_rank[i]] = i % a.E;
-    __syncthreads();
-    for (int tt = wave; tt < a.T; tt += 4) {
-        const double* Lr = sL + tt * a.E;
-        const double* Br = sB + tt * a.E;
-        const short* Rr = s_rank + tt * a.E;
-        double hun = -INFINITY;
-        bool fin = true;
-        for (int ex = lane; ex < a.E; ex += 64) {
-            const double Lq = Lr[ex], Bq = Br[ex];
-            if (!(isfinite(Lq) && isfinite(Bq))) fin = false;
-            if (Rr[ex] >= a.k) hun = fmax(hun, Lq + Bq);
-        }
-        hun = wave_max_dpp(hun);
-        const bool act = lane < a.k;
-        const int ej = act ? s_ids[tt * a.k + lane] : 0;
-        const double lo_j = act ? Lr[ej] - Br[ej] : INFINITY, hi_j = act ? Lr[ej] + Br[ej] : -INFINITY;
-        // suffix maximum over the later ranks (lanes above), then the unchosen experts
-        double suf = hi_j;
-        for (int o = 1; o < 16; o <<= 1) {
-            const double up = __shfl_down(suf, o, 64);
-            if (lane + o < 16) suf = fmax(suf, up);
-        }
-        const double later = fmax(hun, lane + 1 < 16 ? __shfl_down(suf, 1, 64) : -INFINITY);
-        const bool cert = __all(fin && (!act || lo_j > later));
-        if (lane == 0) s_bad[tt] = !cert;
+    double hun = -INFINITY;
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+        if (lane + 64 * q < a.E && !chosen[q]) hun = fmax(hun, L[q] + B[q]);
+    hun = wave_max_dpp(hun);
+    // suffix maximum over the later ranks (lanes above), then the unchosen experts
+    double suf = hi_mine;
+    for (int o = 1; o < 16; o <<= 1) {
+        const double up = __shfl_down(suf, o, 64);
+        if (lane + o < 16) suf = fmax(suf, up);
     }
-    __syncthreads();
-    // uncertified tokens: exact chains for every expert that can reach the chosen ones
+    const double later = fmax(hun, lane + 1 < 16 ? __shfl_down(suf, 1, 64) : -INFINITY);
+    const bool act = lane < a.k;
+    const bool cert = __all(fin && (!act || lo_mine > later));
+    if (act) s_ids[t * a.k + lane] = id_mine;
+    return cert;
+}
+
+// Exact selection for the tokens marked in s_bad (rare): the experts that can reach the chosen ones
+// are recomputed as the reference's float chains (src/GemmaCpu.cs:389-395) and all are ranked exactly:
+// ties to the lower index, NaN below every number (the strict '>' scan of GemmaCpu.cs:400-405).
+// sL, samb, srank: LDS [T*E]; sL ends holding the logits the routing reports for those tokens.
+__device__ void select_exact(const DecArgs& a, double* sL, char* samb, short* srank, int* s_ids, const int* s_bad,
+                             double* red, bool count)
+{
+    const int tid = threadIdx.x, NT = blockDim.x;
+    const float sc = 1.0f / (float)__dsqrt_rn((double)a.d);
     for (int tt = 0; tt < a.T; tt++) {
         if (!s_bad[tt]) continue;  // uniform: an LDS value read after a barrier
-        if (tid == 0) atomicAdd(&a.flags[1], 1);
-        const float rinv_t = rms_scale_from_mean(mean_sq_cert<256>(a.x + (int64_t)tt * a.d, a.d, red, a.flags), a.eps);
+        if (count && tid == 0) atomicAdd(&a.flags[1], 1);
+        const float* xr = a.x + (int64_t)tt * a.d;
+        double s = 0.0;
+        for (int i = tid; i < a.d; i += NT) s += (double)xr[i] * (double)xr[i];
+        const float rinv_t = rms_scale_from_mean(wg_mean_sq(s, xr, a.d, red, nullptr), a.eps);
+        const double* Lr = a.Lb + (int64_t)tt * a.E;
+        const double* Br = a.Bb + (int64_t)tt * a.E;
+        // the lowest lower end among the fast path's chosen experts: an expert whose upper end does not
+        // reach it ranks below every chosen one in exact arithmetic too
         double minlo = INFINITY;
         bool nonfinite = false;
-        for (int b = 0; b < a.E; b++) {
+        for (int j = 0; j < a.k; j++) {
+            const int ex = s_ids[tt * a.k + j];
+            minlo = fmin(minlo, Lr[ex] - Br[ex]);
+        }
+        for (int b = 0; b < a.E; b++)
+            if (!(isfinite(Lr[b]) && isfinite(Br[b]))) nonfinite = true;
+        for (int b = tid; b < a.E; b += NT) {
             const int j = tt * a.E + b;
-            if (!(isfinite(sL[j]) && isfinite(sB[j]))) nonfinite = true;
-            if (s_rank[j] < a.k) minlo = fmin(minlo, sL[j] - sB[j]);
+            const bool amb = nonfinite || !(Lr[b] + Br[b] < minlo);
+            samb[j] = amb;
+            sL[j] = amb ? (double)exact_logit(a.x, a.W, a.gis, a.d, tt, b, rinv_t, sc) : Lr[b];
         }
         __syncthreads();
-        for (int b = tid; b < a.E; b += 256) {
+        for (int b = tid; b < a.E; b += NT) {
             const int j = tt * a.E + b;
-            const bool amb = nonfinite || s_rank[j] < a.k || sL[j] + sB[j] >= minlo;
-            s_amb[j] = amb;
-            if (amb) sL[j] = (double)exact_logit(a.x, a.W, a.gis, a.d, tt, b, rinv_t, sc);  // the others cannot be chosen
-        }
-        __syncthreads();
-        for (int b = tid; b < a.E; b += 256) {
-            const int j = tt * a.E + b;
-            const double my = s_amb[j] ? sel_key(sL[j]) : -INFINITY;
+            const double my = samb[j] ? sel_key(sL[j]) : -INFINITY;
             int r = 0;
             for (int c = 0; c < a.E; c++) {
                 const int jc = tt * a.E + c;
-                r += sel_beats(s_amb[jc] ? sel_key(sL[jc]) : -INFINITY, c, my, b);
+                r += sel_beats(samb[jc] ? sel_key(sL[jc]) : -INFINITY, c, my, b);
             }
-            s_rank[j] = (short)r;
+            srank[j] = (short)r;
+        }
+        __syncthreads();
+        for (int b = tid; b < a.E; b += NT) {
+            const int r = srank[tt * a.E + b];
+            if (r < a.k) s_ids[tt * a.k + r] = b;
         }
         __syncthreads();
     }
-    // ids, logits (debug: certified L rounded, or exact), weights (src/GemmaCpu.cs:406-407,417)
-    for (int i = tid; i < TE; i += 256) {
-        const int tt = i / a.E, ex = i - tt * a.E;
-        const int r = s_rank[i];
-        if (r < a.k) s_ids[tt * a.k + r] = ex;
-        a.logits[i] = (float)sL[i];
-    }
-    __syncthreads();
-    const int n = a.T * a.k;
-    const bool fast_lists = n <= 64;  // one wave builds the lists while the others form the weights
-    // weights: one lane per (token, rank j); waves take tokens in turn (waves 0-2 beside the list wave)
-    {
-        const int nw = fast_lists ? 3 : 4;
-        for (int tt = wave; wave < nw && tt < a.T; tt += nw) {
-            const int j = lane;
-            const bool act = j < a.k;
-            const int id = act ? s_ids[tt * a.k + j] : 0;
-            const float selj = act ? (float)sL[tt * a.E + id] : 0.0f;
-            const float sel0 = __shfl(selj, 0, 64);
-            // p_0 = exp(0) = 1 exactly, so the CPU's in-place rule uses 1 for every later term
-            const float top = (a.rule == 1 && j > 0) ? 1.0f : sel0;
-            const float pj = act ? (float)exp((double)(selj - top)) : 0.0f;
-            double sum = 0.0;
-            for (int q = 0; q < a.k; q++) sum += (double)__shfl(pj, q, 64);  // in rank order
-            if (act) {
-                a.ids[(int64_t)tt * a.k + j] = id;
-                a.w[(int64_t)tt * a.k + j] = (float)((double)pj / sum) * a.ds[id];
-            }
-        }
-    }
-    if (fast_lists) {
-        if (wave == 3) {
-            // lane i = assignment i (token i / k, rank i % k): its place in the stable order by
-            // (expert, assignment) is the number of assignments before it in that order
-            const bool act = lane < n;
-            const int ei = act ? clamp_id(s_ids[lane], a.E) : 0;
-            int rank = 0;
-            for (int j = 0; j < n; j++) {
-                const int ej = clamp_id(s_ids[j], a.E);
-                rank += (ej < ei) || (ej == ei && j < lane);
-            }
-            if (act) {
-                a.perm[rank] = lane;
-                s_perm[rank] = lane;
-            }
-            // counts per expert, then exclusive scans of counts and tile counts (4 experts per lane)
-            for (int x = lane; x <= a.E; x += 64) s_cnt[x] = 0;
-            __builtin_amdgcn_wave_barrier();
-            if (act) atomicAdd(&s_cnt[ei], 1);
-            __builtin_amdgcn_wave_barrier();
-            int c[4], tc[4], sc1 = 0, sc2 = 0;
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const int ex = lane * 4 + q;
-                c[q] = ex < a.E ? s_cnt[ex] : 0;
-                tc[q] = (c[q] + a.A - 1) / a.A;
-                sc1 += c[q];
-                sc2 += tc[q];
-            }
-            int v1 = sc1, v2 = sc2;
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) {
-                const int y1 = __shfl_up(v1, o, 64), y2 = __shfl_up(v2, o, 64);
-                if (lane >= o) {
-                    v1 += y1;
-                    v2 += y2;
-                }
-            }
-            int off = v1 - sc1, tb = v2 - sc2;
-            const int used = __shfl(v2, 63, 64);
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const int ex = lane * 4 + q;
-                if (ex < a.E) {
-                    a.offsets[ex] = off;
-                    for (int r = 0; r * a.A < c[q]; r++) {
-                        const int st0 = off + r * a.A, m = min(a.A, c[q] - r * a.A);
-                        a.tiles[tb + r] = DecTile{ex, m, {s_perm[st0], m > 1 ? s_perm[st0 + 1] : 0}};
-                    }
-                }
-                off += c[q];
-                tb += tc[q];
-            }
-            if (lane == 0) {
-                a.offsets[a.E] = n;
-                *a.ntiles = used;
-            }
-            // slots past the last tile carry e = -1: a grouped workgroup reads one slot and stops
-            for (int q = used + lane; q < a.max_tiles; q += 64) a.tiles[q] = DecTile{-1, 0, {0, 0}};
-        }
-        if (tid == 0) __hip_atomic_store(a.counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        return;
-    }
+}
 
-    // ---- expert lists (ascending assignment order) and tiles of <= A assignments
-    for (int x = tid; x <= a.E; x += 256) s_cnt[x] = 0;
+// Expert lists (ascending assignment order within each expert, the lists of KernelsMoe.Bucket,
+// src/KernelsMoe.cs:281-330) and tiles of <= DROWS assignments, from s_ids into LDS.  The
+// workgroup has at least max(E, T * k) threads.
+__device__ void build_tiles(const DecArgs& a, const int* s_ids, int* s_cnt, int* s_off, int* s_tb, int* s_perm,
+                            DecTile* s_tiles, int* s_nt, int* wtot)
+{
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, NT = blockDim.x;
+    const int n = a.T * a.k;
+    for (int x = tid; x <= a.E; x += NT) s_cnt[x] = 0;
     __syncthreads();
     int my_e = 0, my_rank = 0;
     if (tid < n) {
@@ -448,344 +659,476 @@ __global__ __launch_bounds__(256) void k_route_dec(RouteDecArgs a)
         atomicAdd(&s_cnt[my_e], 1);
     }
     __syncthreads();
-    // exclusive scans of the counts and of the tile counts (E <= 256: one expert per thread)
+    // exclusive scans of the counts and of the tile counts (one expert per thread)
     {
         const int c = tid < a.E ? s_cnt[tid] : 0;
-        const int tcount = (c + a.A - 1) / a.A;
+        const int tcount = (c + DROWS - 1) / DROWS;
         int v1 = c, v2 = tcount;
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
             const int y1 = __shfl_up(v1, o, 64), y2 = __shfl_up(v2, o, 64);
-            if (lane >= o) { v1 += y1; v2 += y2; }
+            if (lane >= o) {
+                v1 += y1;
+                v2 += y2;
+            }
         }
-        __shared__ int wtot1[4], wtot2[4];
-        if (lane == 63) { wtot1[wave] = v1; wtot2[wave] = v2; }
+        if (lane == 63) {
+            wtot[wave] = v1;
+            wtot[16 + wave] = v2;
+        }
         __syncthreads();
         int b1 = 0, b2 = 0;
-        for (int w = 0; w < wave; w++) { b1 += wtot1[w]; b2 += wtot2[w]; }
-        if (tid < a.E) { s_off[tid] = b1 + v1 - c; s_tb[tid] = b2 + v2 - tcount; }
+        for (int w = 0; w < wave; w++) {
+            b1 += wtot[w];
+            b2 += wtot[16 + w];
+        }
+        if (tid < a.E) {
+            s_off[tid] = b1 + v1 - c;
+            s_tb[tid] = b2 + v2 - tcount;
+        }
         if (tid == 0) {
-            s_off[a.E] = wtot1[0] + wtot1[1] + wtot1[2] + wtot1[3];
-            *a.ntiles = wtot2[0] + wtot2[1] + wtot2[2] + wtot2[3];
+            int t1 = 0, t2 = 0;
+            for (int w = 0; w < NT / 64; w++) {
+                t1 += wtot[w];
+                t2 += wtot[16 + w];
+            }
+            s_off[a.E] = t1;
+            *s_nt = t2;
         }
         __syncthreads();
     }
-    for (int x = tid; x <= a.E; x += 256) a.offsets[x] = s_off[x];
-    if (tid < n) {
-        a.perm[s_off[my_e] + my_rank] = tid;
-        s_perm[s_off[my_e] + my_rank] = tid;
-    }
+    if (tid < n) s_perm[s_off[my_e] + my_rank] = tid;
     __syncthreads();
     if (tid < a.E) {
         const int c = s_cnt[tid], base = s_tb[tid];
-        for (int q = 0; q * a.A < c; q++) {
-            const int st0 = s_off[tid] + q * a.A, m = min(a.A, c - q * a.A);
-            a.tiles[base + q] = DecTile{tid, m, {s_perm[st0], m > 1 ? s_perm[st0 + 1] : 0}};
-        }
-    }
-    {
-        // slots past the last tile carry e = -1: a grouped workgroup reads one slot and stops
-        const int used = s_tb[a.E - 1] + (s_cnt[a.E - 1] + a.A - 1) / a.A;
-        for (int q = used + tid; q < a.max_tiles; q += 256) a.tiles[q] = DecTile{-1, 0, {0, 0}};
-    }
-    if (tid == 0) __hip_atomic_store(a.counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-void launch_route_dec(hipStream_t st, const RouteDecArgsH& h)
-{
-    RouteDecArgs a{h.T, h.d, h.E, h.k, h.rule, h.A, h.max_tiles, h.eps, h.x, h.W, h.gis, h.ds, h.pre2, h.fnorm, h.act_gu,
-                   h.act_sh, h.Lb, h.Bb, h.counter, h.ids, h.w, h.logits, h.offsets, h.perm, h.tiles, h.ntiles, h.flags};
-    // staging [3][d] floats, or for the last workgroup L, B (8 B each), key (4 B), rank (2 B), flag (1 B) per (token, expert)
-    const size_t lds = std::max((size_t)3 * h.d * sizeof(float), (size_t)h.T * h.E * 23);
-    static bool attr = false;
-    if (!attr) {
-        (void)hipFuncSetAttribute((const void*)k_route_dec, hipFuncAttributeMaxDynamicSharedMemorySize, 3 * 4096 * 4);
-        attr = true;
-    }
-    launch(k_route_dec, dim3(h.E, h.T), dim3(256), lds, st, a);
-}
-
-// ------------------------------------------------------------------------------ grouped products (decode)
-// Work items: (tile of <= DEC_A assignments of one expert, row group of 64 rows) for the experts,
-// then (tile of <= DEC_A tokens, row group) for the dense shared FFN.  The 8 waves each take a
-// contiguous slice of the row's blocks with all their weight loads issued at once (lane = row),
-// read the activation blocks (wave-uniform) from the Q8_0 buffers, and store the per-block terms
-// (float)isum * (d_w * d_x) in LDS; one wave per assignment adds them in block order: the
-// reference's float chain (src/CpuRefGemma.cs:27-36, src/CpuRef.cs:106-115).
-// Gate|up matrices are repacked in paired row groups (lanes 0-31 gate rows 32g.., lanes 32-63 the
-// matching up rows), so the epilogue forms e = gelu(g) * u (src/GemmaCpu.cs:415) for 32 consecutive
-// outputs and writes their Q8_0 block, the down input (src/CpuRef.cs:49-62).
-
-constexpr int DEC_A = kDecA;
-static_assert(DEC_A == 2, "DecTile holds two assignment rows");
-
-struct DecMat {
-    const uint8_t* pay;
-    const uint8_t* sc;
-    int64_t mat_pay, mat_sc;
-    int rg, nb, rows;
-    Act in;               // activations (rows: token for gate|up, assignment for down)
-    float* out0;          // gate|up: g rows [r][split]; down: y rows [r][rows]
-    float* out1;          // gate|up: u rows
-    int split;            // gate|up: n_ff (valid outputs per row of g/u)
-    Act out_act;          // gate|up: Q8_0 of gelu(g) * u
-};
-
-struct DecArgs {
-    DecMat m0, m1;        // experts, shared FFN (m1.rg == 0: none)
-    const DecTile* tiles;
-    int max_tiles;
-    int act_div;          // expert activation row = assignment row / act_div
-    int T;
-    const float* gelu_tab;
-};
-
-// NW waves per workgroup, each holding up to MAXB blocks of its lane's row (nb <= NW * MAXB)
-template <int MODE, int TYPE, int NW, int MAXB>
-__global__ __launch_bounds__(NW * 64) void k_dec_mm(DecArgs a)
-{
-    constexpr int DEC_NW = NW, DEC_MAXB = MAXB;
-    __shared__ float terms[DEC_A][DEC_MAXB * DEC_NW][64];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    constexpr int PAY = TYPE == PHX_Q4_0_DEV ? 16 : 32;
-
-    int which, rgi, e, cnt;
-    int orow[DEC_A], arow[DEC_A];
-    const int nexp = a.max_tiles * a.m0.rg;
-    if ((int)blockIdx.x < nexp) {
-        which = 0;
-        const int tile = blockIdx.x / a.m0.rg;
-        rgi = blockIdx.x % a.m0.rg;
-        const int4 tl = *(const int4*)(a.tiles + tile);  // {e, cnt, row0, row1}
-        // wave-uniform values: scalar registers, so the activation rows are read with scalar loads
-        e = __builtin_amdgcn_readfirstlane(tl.x);
-        if (e < 0) return;  // slot past the last tile
-        cnt = min(__builtin_amdgcn_readfirstlane(tl.y), DEC_A);
-        orow[0] = __builtin_amdgcn_readfirstlane(tl.z);
-        orow[1] = __builtin_amdgcn_readfirstlane(tl.w);
-        arow[0] = orow[0] / a.act_div;
-        arow[1] = orow[1] / a.act_div;
-    } else {
-        which = 1;
-        const int sid = blockIdx.x - nexp;
-        const int tile = sid / a.m1.rg;
-        rgi = sid % a.m1.rg;
-        e = 0;
-        const int t0 = tile * DEC_A;
-        cnt = min(DEC_A, a.T - t0);
-#pragma unroll
-        for (int i = 0; i < DEC_A; i++) orow[i] = arow[i] = t0 + i;
-    }
-    const DecMat M = which ? a.m1 : a.m0;
-    const int nb = M.nb;
-
-    // ---- weights: this wave's blocks of the lane's row, all loads issued at once
-    const int bpw = (nb + DEC_NW - 1) / DEC_NW;
-    const int b0 = wave * bpw, b1 = min(nb, b0 + bpw);
-    const uint8_t* wp = M.pay + e * M.mat_pay + ((int64_t)rgi * nb * 64 + lane) * PAY;
-    const uint16_t* ws = (const uint16_t*)(M.sc + e * M.mat_sc) + (int64_t)rgi * nb * 64 + lane;
-    uint4 wv[DEC_MAXB][PAY / 16];
-    uint16_t dwh[DEC_MAXB];
-#pragma unroll
-    for (int j = 0; j < DEC_MAXB; j++) {
-        if (b0 + j < b1) {
-            const uint4* src = (const uint4*)(wp + (int64_t)(b0 + j) * 64 * PAY);
-#pragma unroll
-            for (int c = 0; c < PAY / 16; c++) wv[j][c] = src[c];
-            dwh[j] = ws[(int64_t)(b0 + j) * 64];
-        }
-    }
-    // ---- per-block terms of every assignment (unrolled: the rows stay in scalar registers)
-#pragma unroll
-    for (int i = 0; i < DEC_A; i++) {
-        if (i >= cnt) break;
-        const int64_t r = arow[i];
-        const uint32_t* xq = (const uint32_t*)(M.in.q + r * M.in.qstride);
-        const float* xd = M.in.d + r * M.in.dstride;
-        const int* xs = M.in.s + r * M.in.sstride;
-#pragma unroll
-        for (int j = 0; j < DEC_MAXB; j++) {
-            const int b = b0 + j;
-            if (b < b1) {
-                const uint32_t* xb = xq + b * 8;
-                int isum = 0;
-                if (TYPE == PHX_Q4_0_DEV) {
-                    const uint32_t w4[4] = {wv[j][0].x, wv[j][0].y, wv[j][0].z, wv[j][0].w};
-#pragma unroll
-                    for (int w = 0; w < 4; w++) {
-                        isum = __builtin_amdgcn_sdot4((int)(w4[w] & 0x0F0F0F0Fu), (int)xb[w], isum, false);
-                        isum = __builtin_amdgcn_sdot4((int)((w4[w] >> 4) & 0x0F0F0F0Fu), (int)xb[4 + w], isum, false);
-                    }
-                    isum -= 8 * xs[b];
-                } else {
-                    const uint32_t w8[8] = {wv[j][0].x, wv[j][0].y, wv[j][0].z, wv[j][0].w,
-                                            wv[j][PAY / 16 - 1].x, wv[j][PAY / 16 - 1].y, wv[j][PAY / 16 - 1].z,
-                                            wv[j][PAY / 16 - 1].w};
-#pragma unroll
-                    for (int w = 0; w < 8; w++) isum = __builtin_amdgcn_sdot4((int)w8[w], (int)xb[w], isum, false);
-                }
-                const float dd = h2f(dwh[j]) * xd[b];
-                terms[i][b][lane] = (float)isum * dd;
-            }
+        for (int q = 0; q * DROWS < c; q++) {
+            const int st0 = s_off[tid] + q * DROWS, m = min(DROWS, c - q * DROWS);
+            s_tiles[base + q] = DecTile{tid, m, {s_perm[st0], m > 1 ? s_perm[st0 + 1] : 0}};
         }
     }
     __syncthreads();
-    // ---- the float chain in block order (wave i for assignment i), then the epilogue
-    if (wave < cnt) {
-        const int i = wave;
-        float S = 0.0f;
-#pragma unroll 8
-        for (int b = 0; b < nb; b++) S += terms[i][b][lane];
-        const int64_t orr = orow[i];
-        if (MODE == 0) {
-            // paired row group: lanes 0-31 gate j, lanes 32-63 up j, j = 32 rgi + lane % 32
-            const int jj = rgi * 32 + (lane & 31);
-            const float u = __shfl_down(S, 32, 64);
-            if (jj < M.split) {
-                if (lane < 32) M.out0[orr * M.split + jj] = S;
-                else M.out1[orr * M.split + jj] = S;
-            }
-            const float ev = lane < 32 ? gelu_ref(S, a.gelu_tab) * u : 0.0f;
-            float dval;
-            int sum;
-            const int q = q8_0_half(ev, &dval, &sum);
-            if (lane < 32) {
-                const Act& o = M.out_act;
-                o.q[orr * o.qstride + jj] = (int8_t)q;
-                if (lane == 0) {
-                    o.d[orr * o.dstride + rgi] = dval;
-                    o.s[orr * o.sstride + rgi] = sum;
-                }
-            }
-        } else {
-            const int row = rgi * 64 + lane;
-            if (row < M.rows) M.out0[orr * M.rows + row] = S;
+}
+
+// Routing outputs (workgroup 0): ids, logits, weights (src/GemmaCpu.cs:406-407,417: p_j = exp in
+// double, sum in double, w_j = (float)(p_j / sum) * down_scale), offsets, lists and the tile list of
+// k_dec_down.  Lr(t, e) gives the logit the routing used.
+template <class LF>
+__device__ void write_routing(const DecArgs& a, LF Lr, const int* s_ids, const int* s_off, const int* s_perm,
+                              const DecTile* s_tiles, int ntiles)
+{
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, NT = blockDim.x;
+    const int TE = a.T * a.E, n = a.T * a.k;
+    for (int i = tid; i < TE; i += NT) a.logits[i] = (float)Lr(i / a.E, i % a.E);
+    for (int x = tid; x <= a.E; x += NT) a.offsets[x] = s_off[x];
+    for (int i = tid; i < n; i += NT) a.perm[i] = s_perm[i];
+    for (int q = tid; q < a.max_tiles; q += NT) a.tiles[q] = q < ntiles ? s_tiles[q] : DecTile{-1, 0, {0, 0}};
+    for (int tt = wave; tt < a.T; tt += NT / 64) {
+        const int j = lane;
+        const bool act = j < a.k;
+        const int id = act ? s_ids[tt * a.k + j] : 0;
+        const float selj = act ? (float)Lr(tt, id) : 0.0f;
+        const float sel0 = __shfl(selj, 0, 64);
+        // p_0 = exp(0) = 1 exactly, so the CPU's in-place rule uses 1 for every later term
+        const float top = (a.rule == 1 && j > 0) ? 1.0f : sel0;
+        const float pj = act ? (float)exp((double)(selj - top)) : 0.0f;
+        double sum = 0.0;
+        for (int q = 0; q < a.k; q++) sum += (double)__shfl(pj, q, 64);  // in rank order
+        if (act) {
+            a.ids[(int64_t)tt * a.k + j] = id;
+            a.w[(int64_t)tt * a.k + j] = (float)((double)pj / sum) * a.ds[id];
         }
     }
 }
 
-static DecMat to_dev(const DecMatH& h)
+template <int TYPE>
+__device__ void expert_gu_wg(const DecArgs& a, unsigned char* smem)
 {
-    DecMat m{};
-    if (!h.q) return m;
-    m.pay = h.q->payload;
-    m.sc = h.q->scale;
-    m.mat_pay = h.q->mat_pay_stride();
-    m.mat_sc = h.q->mat_sc_stride();
-    m.rg = h.q->rg;
-    m.nb = h.q->nb;
-    m.rows = h.q->rows;
-    m.in = h.in;
-    m.out0 = h.out0;
-    m.out1 = h.out1;
-    m.split = h.split;
-    m.out_act = h.out_act;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, NT = blockDim.x, NWV = NT >> 6;
+    const int TE = a.T * a.E, nb = a.gu.nb;
+    // LDS: [terms | exact-selection arrays] [act rows] [ids, perm, lists, tiles] [scratch]
+    const size_t terms_bytes = (size_t)DROWS * nb * 64 * 4, sel_bytes = (size_t)TE * 11;
+    unsigned char* un = smem;
+    ActL* act = (ActL*)(un + ((std::max(terms_bytes, sel_bytes) + 15) & ~(size_t)15));
+    int* s_ids = (int*)(act + DROWS);   // 256
+    int* s_perm = s_ids + 256;          // 256
+    int* s_cnt = s_perm + 256;          // 260
+    int* s_off = s_cnt + 260;           // 260
+    int* s_tb = s_off + 260;            // 260
+    DecTile* s_tiles = (DecTile*)(s_tb + 260);  // 272
+    int* s_misc = (int*)(s_tiles + 272);        // [0] ntiles, [1] any uncertified, [2..17] bad per token
+    int* wtot = s_misc + 20;                    // 32
+    double* red = (double*)(wtot + 32);         // 17
+    if (tid == 0) s_misc[1] = 0;
+    __syncthreads();
+    for (int t = wave; t < a.T; t += NWV) {
+        const bool cert = wave_topk(a, t, s_ids);
+        if (lane == 0) {
+            s_misc[2 + t] = !cert;
+            if (!cert) s_misc[1] = 1;
+        }
+    }
+    __syncthreads();
+    const bool exact = s_misc[1] != 0;
+    double* sL = (double*)un;
+    if (exact) {
+        char* samb = (char*)(sL + TE);
+        short* srank = (short*)(samb + TE);
+        select_exact(a, sL, samb, srank, s_ids, s_misc + 2, red, blockIdx.x == 0);
+    }
+    int ntiles;
+    if (a.T == 1) {
+        // one token: tile j is assignment j (the k experts are distinct)
+        if (tid < a.k) s_tiles[tid] = DecTile{s_ids[tid], 1, {tid, 0}};
+        if (blockIdx.x == 0) {
+            // expert lists: rank of assignment tid in ascending expert order; offsets by counting
+            if (tid < a.k) {
+                const int e = s_ids[tid];
+                int r = 0;
+                for (int j = 0; j < a.k; j++) r += s_ids[j] < e;
+                s_perm[r] = tid;
+            }
+            for (int x = tid; x <= a.E; x += NT) {
+                int c = 0;
+                for (int j = 0; j < a.k; j++) c += s_ids[j] < x;
+                s_off[x] = c;
+            }
+        }
+        ntiles = a.k;
+        __syncthreads();
+    } else {
+        build_tiles(a, s_ids, s_cnt, s_off, s_tb, s_perm, s_tiles, s_misc, wtot);
+        ntiles = s_misc[0];
+    }
+    if (blockIdx.x == 0) {
+        const double* Lg = a.Lb;
+        const int* bad = s_misc + 2;
+        const int E = a.E;
+        write_routing(
+            a, [&](int t, int e) { return (exact && bad[t]) ? sL[t * E + e] : Lg[(int64_t)t * E + e]; }, s_ids, s_off,
+            s_perm, s_tiles, ntiles);
+    }
+    const int tile = blockIdx.x / a.gu.rg, rgi = blockIdx.x % a.gu.rg;
+    if (tile >= ntiles) return;  // uniform: no barriers follow for this workgroup
+    const DecTile tl = s_tiles[tile];
+    const int e = tl.e, cnt = min(tl.cnt, DROWS);
+    const int tok0 = tl.row[0] / a.k, tok1 = tl.row[cnt > 1 ? 1 : 0] / a.k;
+    QIn qin;
+    quant_issue(qin, a.x, tok0, tok1, a.pre2, a.d);
+    __builtin_amdgcn_sched_barrier(0);  // keep the activation loads ahead of the weight loads
+    WRegs<TYPE> W;
+    load_w<TYPE>(a.gu, clamp_id(e, a.E), rgi, wave, lane, W);  // unconditional (see shared_gu_wg)
+    __syncthreads();  // the exact-selection arrays are about to become terms
+    quant_finish(qin, a.x, tok0, tok1, cnt, a.d, a.eps, act, red, nullptr);
+    __syncthreads();
+    const float S = rowgroup_chain<TYPE>(W, nb, act, cnt, (float*)un);
+    if (wave < cnt) gu_epilogue(S, rgi, a.nf, wave == 0 ? tl.row[0] : tl.row[1], a.g, a.u, a.adn, a.gelu_tab);
+}
+
+template <int TYPE>
+__device__ void shared_dn_wg(const DecArgs& a, int tile, int rgi, unsigned char* smem)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    ActL* act = (ActL*)smem;
+    float* terms = (float*)(act + DROWS);
+    const int t0 = tile * DROWS, cnt = min(DROWS, a.T - t0);
+    ActIn ain;
+    act_issue(ain, a.asd, t0, min(t0 + 1, a.T - 1), cnt, a.sdn.nb);
+    __builtin_amdgcn_sched_barrier(0);  // keep the activation loads ahead of the weight loads
+    WRegs<TYPE> W;
+    load_w<TYPE>(a.sdn, 0, rgi, wave, lane, W);  // unconditional (see shared_gu_wg)
+    act_store(ain, cnt, a.sdn.nb, act);
+    __syncthreads();
+    const float S = rowgroup_chain<TYPE>(W, a.sdn.nb, act, cnt, terms);
+    const int row = rgi * 64 + lane;
+    if (wave < cnt && row < a.sdn.rows) a.shout[(int64_t)(t0 + wave) * a.d + row] = S;
+}
+
+template <int TYPE>
+__global__ __launch_bounds__(1024) void k_dec_gu(DecArgs a)
+{
+    extern __shared__ __align__(16) unsigned char dsm[];
+    const int ne = a.max_tiles * a.gu.rg;
+    if ((int)blockIdx.x < ne) {
+        expert_gu_wg<TYPE>(a, dsm);
+    } else {
+        const int s = blockIdx.x - ne;
+        shared_dn_wg<TYPE>(a, s / a.sdn.rg, s % a.sdn.rg, dsm);
+    }
+}
+
+// ------------------------------------------------------------------------------ k_dec_down
+// One (tile, row group) of the routed experts' down products, the tile list from k_dec_gu's
+// workgroup 0: yd[a][row] = down_e(gelu(g) * u)[row] for the tile's assignments.
+template <int TYPE>
+__global__ __launch_bounds__(1024) void k_dec_down(DecArgs a)
+{
+    extern __shared__ __align__(16) unsigned char dsm[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int tile = blockIdx.x / a.dn.rg, rgi = blockIdx.x % a.dn.rg;
+    const int4 tl = *(const int4*)(a.tiles + tile);  // {e, cnt, row0, row1}
+    if (tl.x < 0) return;                            // slot past the last tile
+    const int e = tl.x, cnt = min(tl.y, DROWS), nb = a.dn.nb;
+    ActL* act = (ActL*)dsm;
+    float* terms = (float*)(act + DROWS);
+    ActIn ain;
+    act_issue(ain, a.adn, tl.z, cnt > 1 ? tl.w : tl.z, cnt, nb);
+    __builtin_amdgcn_sched_barrier(0);  // keep the activation loads ahead of the weight loads
+    WRegs<TYPE> W;
+    load_w<TYPE>(a.dn, clamp_id(e, a.E), rgi, wave, lane, W);  // unconditional (see shared_gu_wg)
+    act_store(ain, cnt, nb, act);
+    __syncthreads();
+    const float S = rowgroup_chain<TYPE>(W, nb, act, cnt, terms);
+    const int row = rgi * 64 + lane;
+    if (wave < cnt && row < a.d) a.yd[(int64_t)(wave == 0 ? tl.z : tl.w) * a.d + row] = S;
+}
+
+// ------------------------------------------------------------------------------ k_dec_combine
+// Per token (1024 threads): acc = sum_j w_j * yd_j in rank order (src/GemmaCpu.cs:417-418, each term
+// rounded then added), out = rmsnorm(shared) * post1 + rmsnorm(acc) * post2 (src/GemmaCpu.cs:384,
+// 420-421), and with a residual x += rmsnorm(out) * post_ffw_norm (src/GemmaCpu.cs:355-356).  Every
+// load of the token is issued in one round (d <= 4096: four elements per thread; ranks in groups of 8).
+constexpr int CB_NT = 1024, CB_E = 4;
+
+__global__ __launch_bounds__(CB_NT) void k_dec_combine(DecArgs a)
+{
+    extern __shared__ __align__(16) float cb[];  // acc [d], out [d]
+    __shared__ double red[CB_NT / 64 + 1];
+    const int t = blockIdx.x, tid = threadIdx.x, d = a.d, k = a.k;
+    float* sacc = cb;
+    float* so = cb + d;
+    const float* sh = a.shout ? a.shout + (int64_t)t * d : nullptr;
+    int ix[CB_E];
+    float accv[CB_E], shv[CB_E], p1[CB_E], p2[CB_E];
+#pragma unroll
+    for (int q = 0; q < CB_E; q++) {
+        ix[q] = min(tid + q * CB_NT, d - 1);
+        accv[q] = 0.0f;
+    }
+    // ranks in groups of 8, every load of a group issued before its first use
+    for (int j0 = 0; j0 < k; j0 += 8) {
+        float yv[CB_E][8], wj[8];
+#pragma unroll
+        for (int jj = 0; jj < 8; jj++) wj[jj] = a.w[(int64_t)t * k + min(j0 + jj, k - 1)];
+#pragma unroll
+        for (int q = 0; q < CB_E; q++)
+#pragma unroll
+            for (int jj = 0; jj < 8; jj++) yv[q][jj] = a.yd[((int64_t)t * k + min(j0 + jj, k - 1)) * d + ix[q]];
+        if (j0 == 0) {
+#pragma unroll
+            for (int q = 0; q < CB_E; q++) {
+                shv[q] = sh ? sh[ix[q]] : 0.0f;
+                p1[q] = a.post1[ix[q]];
+                p2[q] = a.post2[ix[q]];
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < CB_E; q++)
+#pragma unroll
+            for (int jj = 0; jj < 8; jj++)
+                if (j0 + jj < k) accv[q] += yv[q][jj] * wj[jj];
+    }
+    double s2 = 0.0, s1 = 0.0;
+#pragma unroll
+    for (int q = 0; q < CB_E; q++) {
+        const int i = tid + q * CB_NT;
+        if (i < d) {
+            sacc[i] = accv[q];
+            s2 += (double)accv[q] * (double)accv[q];
+            s1 += (double)shv[q] * (double)shv[q];
+        }
+    }
+    __syncthreads();
+    const float sc2 = rms_scale_from_mean(wg_mean_sq(s2, sacc, d, red, a.flags), a.eps);
+    const float sc1 = sh ? rms_scale_from_mean(wg_mean_sq(s1, sh, d, red, a.flags), a.eps) : 0.0f;
+    float ov[CB_E];
+    double s3 = 0.0;
+#pragma unroll
+    for (int q = 0; q < CB_E; q++) {
+        const int i = tid + q * CB_NT;
+        const float mlp = sh ? shv[q] * sc1 * p1[q] : 0.0f;
+        ov[q] = mlp + accv[q] * sc2 * p2[q];
+        if (i < d) {
+            a.out[(int64_t)t * d + i] = ov[q];
+            so[i] = ov[q];
+            s3 += (double)ov[q] * (double)ov[q];
+        }
+    }
+    if (a.xres) {
+        float xv[CB_E], pf[CB_E];
+#pragma unroll
+        for (int q = 0; q < CB_E; q++) {
+            xv[q] = a.xres[(int64_t)t * d + ix[q]];
+            pf[q] = a.post_ffw[ix[q]];
+        }
+        __syncthreads();
+        const float sc3 = rms_scale_from_mean(wg_mean_sq(s3, so, d, red, a.flags), a.eps);
+#pragma unroll
+        for (int q = 0; q < CB_E; q++) {
+            const int i = tid + q * CB_NT;
+            if (i < d) a.xres[(int64_t)t * d + i] = xv[q] + ov[q] * sc3 * pf[q];
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------ launchers
+
+static MatD mat_d(const QMat* q)
+{
+    MatD m{};
+    if (!q || !q->payload) return m;
+    m.pay = q->payload;
+    m.sc8 = (const uint4*)q->scale8;
+    m.mat_pay = q->mat_pay_stride();
+    m.mat_sc8 = q->mat_sc8_stride();
+    m.rg = q->rg;
+    m.nb = q->nb;
+    m.nb8 = (q->nb + 7) / 8;
+    m.rows = q->rows;
     return m;
 }
 
-void launch_dec(hipStream_t st, int mode, const DecMatH& m0, const DecMatH& m1, const DecTile* tiles, int max_tiles,
-                int act_div, int T, const float* gelu_tab)
+static DecArgs dec_args(const DecLayerH& h)
 {
     DecArgs a{};
-    a.m0 = to_dev(m0);
-    a.m1 = to_dev(m1);
-    a.tiles = tiles;
-    a.max_tiles = max_tiles;
-    a.act_div = act_div;
-    a.T = T;
-    a.gelu_tab = gelu_tab;
-    const int items = max_tiles * a.m0.rg + (a.m1.rg > 0 ? (T + DEC_A - 1) / DEC_A * a.m1.rg : 0);
-    const bool q4 = m0.q->type == PHX_Q4_0_DEV;
-    // 8 waves share a row's blocks (nb <= 128)
-    if (mode == 0) {
-        if (q4) launch((k_dec_mm<0, PHX_Q4_0_DEV, 8, 16>), dim3(items), dim3(512), 0, st, a);
-        else launch((k_dec_mm<0, PHX_Q8_0_DEV, 8, 16>), dim3(items), dim3(512), 0, st, a);
+    a.T = h.T;
+    a.d = h.d;
+    a.E = h.E;
+    a.k = h.k;
+    a.nf = h.nf;
+    a.nff = h.sgu ? h.nff : 0;
+    a.rule = h.rule;
+    a.max_tiles = h.max_tiles;
+    a.eps = h.eps;
+    a.x = h.x;
+    a.W = h.W;
+    a.gis = h.gis;
+    a.ds = h.ds;
+    a.pre2 = h.pre2;
+    a.post1 = h.post1;
+    a.post2 = h.post2;
+    a.fnorm = h.fnorm;
+    a.post_ffw = h.post_ffw;
+    a.gu = mat_d(h.gu);
+    a.dn = mat_d(h.dn);
+    a.sgu = mat_d(h.sgu);
+    a.sdn = mat_d(h.sdn);
+    a.Lb = h.Lb;
+    a.Bb = h.Bb;
+    a.ids = h.ids;
+    a.w = h.w;
+    a.logits = h.logits;
+    a.offsets = h.offsets;
+    a.perm = h.perm;
+    a.tiles = h.tiles;
+    a.g = h.g;
+    a.u = h.u;
+    a.adn = h.adn;
+    a.yd = h.yd;
+    a.shg = h.shg;
+    a.shu = h.shu;
+    a.asd = h.asd;
+    a.shout = h.sgu ? h.shout : const_cast<float*>(h.shared_in);
+    a.out = h.out;
+    a.xres = h.xres;
+    a.gelu_tab = h.gelu_tab;
+    a.flags = h.flags;
+    return a;
+}
+
+static int waves_for(int nb) { return (nb + DBPW - 1) / DBPW; }
+
+// block sizes: every row-group workgroup has one wave per 8 blocks (and at least 4 waves where the
+// selection, the lists or the router run)
+static int nt_route(const DecLayerH& h) { return 64 * std::max(4, waves_for(h.gu->nb)); }
+
+static int nt_gu(const DecLayerH& h)
+{
+    int nw = std::max(4, waves_for(h.gu->nb));
+    if (h.sdn) nw = std::max(nw, waves_for(h.sdn->nb));
+    return 64 * nw;
+}
+
+static size_t route_lds(const DecLayerH& h)
+{
+    const size_t router = (size_t)3 * (h.d + RPER) * 4 + (size_t)(17 + 48) * 8;
+    const size_t sh = h.sgu ? sizeof(ActL) * DROWS + 32 * 8 + (size_t)DROWS * h.sgu->nb * 64 * 4 : 0;
+    return std::max(router, sh);
+}
+
+static size_t gu_lds(const DecLayerH& h)
+{
+    const size_t TE = (size_t)h.T * h.E;
+    const size_t un = (std::max((size_t)DROWS * h.gu->nb * 64 * 4, TE * 11) + 15) & ~(size_t)15;
+    const size_t ex = un + sizeof(ActL) * DROWS + (256 * 2 + 260 * 3) * 4 + 272 * sizeof(DecTile) + (20 + 32) * 4 +
+                      17 * 8;
+    const size_t sh = h.sdn ? sizeof(ActL) * DROWS + (size_t)DROWS * h.sdn->nb * 64 * 4 : 0;
+    return std::max(ex, sh);
+}
+
+static size_t down_lds(const DecLayerH& h) { return sizeof(ActL) * DROWS + (size_t)DROWS * h.dn->nb * 64 * 4; }
+
+template <class K>
+static void raise_lds(K kernel, size_t bytes)
+{
+    (void)hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+}
+
+bool dec_supported(const DecLayerH& h)
+{
+    if (h.d > 4096 || h.d % 256 || h.gu->nb > DMAXNB || h.dn->nb > DMAXNB || h.E > 256 || h.T * h.k > 256) return false;
+    if (h.sgu && (h.sgu->nb > DMAXNB || h.sdn->nb > DMAXNB)) return false;
+    if (nt_gu(h) < std::max(h.E, h.T * h.k)) return false;  // build_tiles: a thread per expert and assignment
+    return gu_lds(h) <= 160 * 1024 && route_lds(h) <= 160 * 1024;
+}
+
+void launch_dec_route(hipStream_t st, const DecLayerH& h)
+{
+    const DecArgs a = dec_args(h);
+    const int nsh = h.sgu ? (h.T + DROWS - 1) / DROWS * a.sgu.rg : 0;
+    const dim3 grid(h.T * h.E + nsh), block(nt_route(h));
+    const size_t lds = route_lds(h);
+    if (h.gu->type == PHX_Q4_0_DEV) {
+        raise_lds(k_dec_route<PHX_Q4_0_DEV>, lds);
+        launch(k_dec_route<PHX_Q4_0_DEV>, grid, block, (uint32_t)lds, st, a);
     } else {
-        if (q4) launch((k_dec_mm<1, PHX_Q4_0_DEV, 8, 16>), dim3(items), dim3(512), 0, st, a);
-        else launch((k_dec_mm<1, PHX_Q8_0_DEV, 8, 16>), dim3(items), dim3(512), 0, st, a);
+        raise_lds(k_dec_route<PHX_Q8_0_DEV>, lds);
+        launch(k_dec_route<PHX_Q8_0_DEV>, grid, block, (uint32_t)lds, st, a);
     }
 }
 
-// ------------------------------------------------------------------------------ combine (decode)
-// k_combine's arithmetic (rank-ordered sum of w_j * yd_j, the two branch norms, optional residual;
-// src/GemmaCpu.cs:384,418-421,355-356) with 1024 threads per token and every global load of the
-// token issued in one round (d <= 4096, k <= 16).
-constexpr int CB_NT = 1024, CB_MAXE = 4;
-
-__global__ __launch_bounds__(CB_NT) void k_combine_dec(int d, int k, float eps, const float* __restrict__ yd,
-                                                       const float* __restrict__ w, const float* __restrict__ shared,
-                                                       const float* __restrict__ post1, const float* __restrict__ post2,
-                                                       float* __restrict__ out, float* __restrict__ xres,
-                                                       const float* __restrict__ post_ffw, int* flags)
+void launch_dec_gu(hipStream_t st, const DecLayerH& h)
 {
-    extern __shared__ float cb[];  // acc [d], shared [d], out [d]
-    __shared__ double red[CB_NT / 64 + 1];
-    const int t = blockIdx.x, tid = threadIdx.x;
-    float* sacc = cb;
-    float* ssh = cb + d;
-    float* so = cb + 2 * d;
-    const float* sh = shared ? shared + (int64_t)t * d : nullptr;
-    float wj[PHX_MAX_USED_DEV];
-#pragma unroll
-    for (int j = 0; j < PHX_MAX_USED_DEV; j++) wj[j] = j < k ? w[(int64_t)t * k + j] : 0.0f;
-    float yv[CB_MAXE][PHX_MAX_USED_DEV], shv[CB_MAXE], p1[CB_MAXE], p2[CB_MAXE], pf[CB_MAXE], xv[CB_MAXE];
-#pragma unroll
-    for (int q = 0; q < CB_MAXE; q++) {
-        const int i = tid + q * CB_NT;
-        const bool in = i < d;
-#pragma unroll
-        for (int j = 0; j < PHX_MAX_USED_DEV; j++) yv[q][j] = (in && j < k) ? yd[((int64_t)t * k + j) * d + i] : 0.0f;
-        shv[q] = (in && sh) ? sh[i] : 0.0f;
-        p1[q] = (in && sh) ? post1[i] : 0.0f;
-        p2[q] = in ? post2[i] : 0.0f;
-        pf[q] = (in && xres) ? post_ffw[i] : 0.0f;
-        xv[q] = (in && xres) ? xres[(int64_t)t * d + i] : 0.0f;
-    }
-    float accv[CB_MAXE];
-#pragma unroll
-    for (int q = 0; q < CB_MAXE; q++) {
-        float acc = 0.0f;
-#pragma unroll
-        for (int j = 0; j < PHX_MAX_USED_DEV; j++)
-            if (j < k) acc += yv[q][j] * wj[j];
-        accv[q] = acc;
-        const int i = tid + q * CB_NT;
-        if (i < d) {
-            sacc[i] = acc;
-            ssh[i] = shv[q];
-        }
-    }
-    __syncthreads();
-    const float s2 = rms_scale_from_mean(mean_sq_cert<CB_NT>(sacc, d, red, flags), eps);
-    const float s1 = sh ? rms_scale_from_mean(mean_sq_cert<CB_NT>(ssh, d, red, flags), eps) : 0.0f;
-    float ov[CB_MAXE];
-#pragma unroll
-    for (int q = 0; q < CB_MAXE; q++) {
-        const int i = tid + q * CB_NT;
-        const float mlp = sh ? shv[q] * s1 * p1[q] : 0.0f;
-        ov[q] = mlp + accv[q] * s2 * p2[q];
-        if (i < d) {
-            out[(int64_t)t * d + i] = ov[q];
-            so[i] = ov[q];
-        }
-    }
-    if (xres) {
-        __syncthreads();
-        const float s3 = rms_scale_from_mean(mean_sq_cert<CB_NT>(so, d, red, flags), eps);
-#pragma unroll
-        for (int q = 0; q < CB_MAXE; q++) {
-            const int i = tid + q * CB_NT;
-            if (i < d) xres[(int64_t)t * d + i] = xv[q] + ov[q] * s3 * pf[q];
-        }
+    const DecArgs a = dec_args(h);
+    const int nsh = h.sdn ? (h.T + DROWS - 1) / DROWS * a.sdn.rg : 0;
+    const dim3 grid(h.max_tiles * a.gu.rg + nsh), block(nt_gu(h));
+    const size_t lds = gu_lds(h);
+    if (h.gu->type == PHX_Q4_0_DEV) {
+        raise_lds(k_dec_gu<PHX_Q4_0_DEV>, lds);
+        launch(k_dec_gu<PHX_Q4_0_DEV>, grid, block, (uint32_t)lds, st, a);
+    } else {
+        raise_lds(k_dec_gu<PHX_Q8_0_DEV>, lds);
+        launch(k_dec_gu<PHX_Q8_0_DEV>, grid, block, (uint32_t)lds, st, a);
     }
 }
 
-void launch_combine_dec(hipStream_t st, int T, int d, int k, float eps, const float* yd, const float* w,
-                        const float* shared, const float* post1, const float* post2, float* out, float* xres,
-                        const float* post_ffw, int* flags)
+void launch_dec_down(hipStream_t st, const DecLayerH& h)
 {
-    launch(k_combine_dec, dim3(T), dim3(CB_NT), (size_t)3 * d * sizeof(float), st, d, k, eps, yd, w, shared,
-                       post1, post2, out, xres, post_ffw, flags);
+    const DecArgs a = dec_args(h);
+    const dim3 grid(h.max_tiles * a.dn.rg), block(64 * waves_for(h.dn->nb));
+    const size_t lds = down_lds(h);
+    if (h.gu->type == PHX_Q4_0_DEV) {
+        raise_lds(k_dec_down<PHX_Q4_0_DEV>, lds);
+        launch(k_dec_down<PHX_Q4_0_DEV>, grid, block, (uint32_t)lds, st, a);
+    } else {
+        raise_lds(k_dec_down<PHX_Q8_0_DEV>, lds);
+        launch(k_dec_down<PHX_Q8_0_DEV>, grid, block, (uint32_t)lds, st, a);
+    }
+}
+
+void launch_dec_combine(hipStream_t st, const DecLayerH& h)
+{
+    const DecArgs a = dec_args(h);
+    launch(k_dec_combine, dim3(h.T), dim3(CB_NT), (uint32_t)((size_t)2 * h.d * 4), st, a);
 }
 
 }  // namespace phx

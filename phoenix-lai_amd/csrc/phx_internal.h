@@ -56,8 +56,12 @@ struct QMat {
     bool paired = false;                // gate|up: row group g = gate rows 32g..32g+31 and the matching up rows
     uint8_t* payload = nullptr;
     uint8_t* scale = nullptr;
+    // Q4_0 / Q8_0 only: the same fp16 scales grouped per lane by 8 blocks, [m][rg][nb/8][lane][8], so
+    // one 16 B load gives a row the scales of 8 consecutive blocks (the decode kernels' layout)
+    uint8_t* scale8 = nullptr;
     int64_t mat_pay_stride() const { return (int64_t)rg * nb * kRowGroup * pay; }
     int64_t mat_sc_stride() const { return (int64_t)rg * nb * kRowGroup * sbytes; }
+    int64_t mat_sc8_stride() const { return (int64_t)rg * ((nb + 7) / 8) * kRowGroup; }  // 16 B units
 };
 
 // Quantized activation rows for one weight type.
@@ -78,8 +82,7 @@ struct Act {
 };
 
 struct Tile { int e, start, cnt; };
-// decode-path tile: expert, assignment count (<= kDecA) and the assignment rows themselves, so a
-// grouped workgroup learns everything it needs from one 16-byte read
+// decode-path tile: expert, assignment count (<= 2) and the assignment rows themselves
 struct DecTile { int e, cnt, row[2]; };
 
 // kernels.hip launchers (all enqueue on `st`)
@@ -102,45 +105,24 @@ void launch_grouped_mfma(hipStream_t st, const QMat& w, Act act, const Tile* til
 void launch_combine(hipStream_t st, int T, int d, int k, float eps, const float* yd, const float* w,
                     const float* shared, const float* post1, const float* post2, float* out, float* x_resid,
                     const float* post_ffw, int* flags);
-// decode path (kernels_decode.hip)
-constexpr int kDecA = 2;          // assignments per decode tile
-constexpr int kRouteMaxTE = 2048; // T * E the decode router's last workgroup holds
-struct RouteDecArgsH {
-    int T, d, E, k, rule, A, max_tiles;
+// decode path (kernels_decode.hip): four launches per layer for T <= 16 tokens, Q4_0 / Q8_0
+struct DecLayerH {
+    int T, d, E, k, nf, nff, rule, max_tiles;
     float eps;
-    const float* x;
-    const float* W;
-    const float* gis;
-    const float* ds;
-    const float* pre2;
-    const float* fnorm;
-    Act act_gu, act_sh;
-    double* Lb;
-    double* Bb;
-    int* counter;
-    int* ids;
-    float* w;
-    float* logits;
-    int* offsets;
-    int* perm;
+    const float *x, *W, *gis, *ds, *pre2, *post1, *post2, *fnorm, *post_ffw, *shared_in;
+    const QMat *gu, *dn, *sgu, *sdn;  // sgu / sdn null: no shared FFN computed in the call
+    double *Lb, *Bb;
+    int *ids, *offsets, *perm, *flags;
+    float *w, *logits, *g, *u, *yd, *shg, *shu, *shout, *out, *xres;
     DecTile* tiles;
-    int* ntiles;
-    int* flags;
+    Act adn, asd;
+    const float* gelu_tab;
 };
-void launch_route_dec(hipStream_t st, const RouteDecArgsH& h);
-struct DecMatH {  // host-side description of one matrix of a decode grouped launch
-    const QMat* q = nullptr;
-    Act in;
-    float* out0 = nullptr;
-    float* out1 = nullptr;
-    int split = 0;
-    Act out_act;
-};
-void launch_dec(hipStream_t st, int mode, const DecMatH& m0, const DecMatH& m1, const DecTile* tiles, int max_tiles,
-                int act_div, int T, const float* gelu_tab);
-void launch_combine_dec(hipStream_t st, int T, int d, int k, float eps, const float* yd, const float* w,
-                        const float* shared, const float* post1, const float* post2, float* out, float* xres,
-                        const float* post_ffw, int* flags);
+bool dec_supported(const DecLayerH& h);
+void launch_dec_route(hipStream_t st, const DecLayerH& h);
+void launch_dec_gu(hipStream_t st, const DecLayerH& h);
+void launch_dec_down(hipStream_t st, const DecLayerH& h);
+void launch_dec_combine(hipStream_t st, const DecLayerH& h);
 void launch_stream_read(hipStream_t st, const void* src, int64_t bytes, uint32_t* sink);
 void launch_stream_copy(hipStream_t st, void* dst, const void* src, int64_t bytes);
 void launch_selftest(hipStream_t st, int op, int n, const float* a, const float* b, float* out, const float* gelu_tab);

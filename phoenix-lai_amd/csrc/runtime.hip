@@ -102,7 +102,7 @@ int round_up(int v, int m) { return (v + m - 1) / m * m; }
 // ------------------------------------------------------------------------------ repack
 // GGUF rows [n_mat][rows][row_bytes] -> row groups of 64 (see QMat).
 struct HostQ {
-    std::vector<uint8_t> payload, scale;
+    std::vector<uint8_t> payload, scale, scale8;
 };
 
 void decode_q4k_natural(const uint8_t* blk, uint8_t* q, int* sc, int* mn)
@@ -228,6 +228,17 @@ void repack(int type, const uint8_t* src, int n_mat, int rows, int cols, QMat& q
         });
     }
     for (auto& t : th) t.join();
+    if (type == PHX_Q4_0 || type == PHX_Q8_0) {
+        // scale8: [m][rg][b / 8][lane][8] fp16, the scales of 8 consecutive blocks of a row together
+        const int nb8 = (q.nb + 7) / 8;
+        h.scale8.assign((size_t)q.mat_sc8_stride() * 16 * n_mat, 0);
+        uint16_t* s8 = (uint16_t*)h.scale8.data();
+        const uint16_t* s1 = (const uint16_t*)h.scale.data();
+        for (int64_t mr = 0; mr < (int64_t)n_mat * q.rg; mr++)
+            for (int b = 0; b < q.nb; b++)
+                for (int lane = 0; lane < kRowGroup; lane++)
+                    s8[((mr * nb8 + b / 8) * kRowGroup + lane) * 8 + b % 8] = s1[(mr * q.nb + b) * kRowGroup + lane];
+    }
 }
 
 struct Layer {
@@ -303,7 +314,7 @@ int hip_code(hipError_t e)
 enum WsId {
     W_X, W_SHARED, W_OUT, W_RIN, W_XSCALE, W_AGU_Q, W_AGU_D, W_AGU_S, W_ASH_Q, W_ASH_D, W_ASH_S, W_LOGITS, W_IDS, W_W,
     W_OFF, W_PERM, W_TILES, W_NTILES, W_G, W_U, W_ADN_Q, W_ADN_D, W_ADN_S, W_YD, W_SHG, W_SHU, W_ASD_Q, W_ASD_D,
-    W_ASD_S, W_SHOUT, W_ZERO, W_STILES, W_SNTILES, W_SOFF, W_SPERM, W_LB, W_BB, W_COUNTER, W_COUNT
+    W_ASD_S, W_SHOUT, W_ZERO, W_STILES, W_SNTILES, W_SOFF, W_SPERM, W_LB, W_BB, W_ADEC, W_SDEC, W_COUNT
 };
 
 int ensure(phx_moe_ctx* c, int id, size_t bytes)
@@ -317,7 +328,7 @@ int ensure(phx_moe_ctx* c, int id, size_t bytes)
     size_t n = std::max<size_t>(bytes, 256);
     HIPCHK(c, hipMalloc(&b.p, n));
     b.bytes = n;
-    if (id == W_ZERO || id == W_COUNTER) HIPCHK(c, hipMemset(b.p, 0, n));
+    if (id == W_ZERO) HIPCHK(c, hipMemset(b.p, 0, n));
     return PHX_OK;
 }
 
@@ -342,6 +353,24 @@ Act make_act(phx_moe_ctx* c, int fmt, int cols, int qid, int did, int sid)
     if (fmt == ACT_Q8_0) { a.qstride = cols; a.dstride = cols / 32; a.sstride = cols / 32; }
     else if (fmt == ACT_K4) { a.qstride = cols; a.dstride = cols / 256; a.sstride = cols / 16; }
     else { a.qstride = (int64_t)(cols / 256) * 512; a.dstride = cols / 256; a.sstride = (cols / 256) * 128; }
+    return a;
+}
+
+// Q8_0 rows packed one row after another, each row q (cols bytes), d (cols/32 floats), s (cols/32
+// ints) contiguous: the decode kernels copy a row with one run of dword loads.
+Act make_act_packed(phx_moe_ctx* c, int cols, int id)
+{
+    Act a;
+    a.fmt = ACT_Q8_0;
+    a.cols = cols;
+    const int nb = cols / 32;
+    uint8_t* base = wp<uint8_t>(c, id);
+    a.q = (int8_t*)base;
+    a.qstride = (int64_t)nb * 40;
+    a.d = (float*)(base + cols);
+    a.dstride = nb * 10;
+    a.s = (int*)(base + cols + nb * 4);
+    a.sstride = nb * 10;
     return a;
 }
 
@@ -378,7 +407,6 @@ int ensure_workspace(phx_moe_ctx* c, const Layer& L, int T)
     ENS(W_G, n * D.n_ff * 4);
     ENS(W_LB, (size_t)T * D.n_expert * 8);
     ENS(W_BB, (size_t)T * D.n_expert * 8);
-    ENS(W_COUNTER, 64);
     ENS(W_U, n * D.n_ff * 4);
     ENS(W_YD, n * D.d * 4);
     if ((rc = ensure_act(c, act_fmt(D.gate_up_type), T, D.d, W_AGU_Q, W_AGU_D, W_AGU_S))) return rc;
@@ -396,7 +424,9 @@ int ensure_workspace(phx_moe_ctx* c, const Layer& L, int T)
         ENS(W_SOFF, 8);
         ENS(W_SPERM, (size_t)T * 4);
     }
-    ENS(W_TILES, (size_t)((n + kDecA - 1) / kDecA + D.n_expert) * sizeof(DecTile));
+    ENS(W_TILES, (size_t)((n + 1) / 2 + D.n_expert) * sizeof(DecTile));
+    ENS(W_ADEC, (size_t)n * (D.down_cols / 32) * 40);
+    if (D.n_ff_shared > 0) ENS(W_SDEC, (size_t)T * (D.n_ff_shared / 32) * 40);
 #undef ENS
     return PHX_OK;
 }
@@ -440,102 +470,92 @@ struct ProfScope : LaunchTimer {
 bool dec_type(int t) { return t == PHX_Q4_0 || t == PHX_Q8_0; }
 bool mfma_type(int t) { return t == PHX_Q4_0 || t == PHX_Q8_0; }
 
-// The decode path: few tokens, Q4_0/Q8_0 weights, K <= 4096 (kernels_decode.hip).
-bool use_decode(const Layer& L, int T, unsigned flags)
+// The decode path (kernels_decode.hip): few tokens, Q4_0/Q8_0 weights, K <= 4096.
+DecLayerH dec_layer(phx_moe_ctx* c, const Layer& L, int T, const float* x, const float* shared, float* out, float* xres)
+{
+    const phx_moe_layer_desc& D = L.desc;
+    const int n = T * D.n_used;
+    const bool shared_ffn = shared == nullptr && D.n_ff_shared > 0;
+    DecLayerH h{};
+    h.T = T;
+    h.d = D.d;
+    h.E = D.n_expert;
+    h.k = D.n_used;
+    h.nf = D.n_ff;
+    h.nff = D.n_ff_shared;
+    h.rule = D.weight_rule;
+    h.max_tiles = std::min(n, (n + 1) / 2 + D.n_expert);  // every tile holds one or two assignments
+    h.eps = D.eps;
+    h.x = x;
+    h.W = L.wrow;
+    h.gis = L.gis;
+    h.ds = L.ds;
+    h.pre2 = L.pre2;
+    h.post1 = L.post1;
+    h.post2 = L.post2;
+    h.fnorm = L.ffn_norm;
+    h.post_ffw = L.post_ffw;
+    h.shared_in = shared;
+    h.gu = &L.gu;
+    h.dn = &L.dn;
+    h.sgu = shared_ffn ? &L.sgu : nullptr;
+    h.sdn = shared_ffn ? &L.sdn : nullptr;
+    h.out = out;
+    h.xres = xres;
+    h.gelu_tab = c->gelu_tab;
+    h.flags = c->flags;
+    if (c->ws.size() >= (size_t)W_COUNT && c->ws[W_LB].p) {
+        h.Lb = wp<double>(c, W_LB);
+        h.Bb = wp<double>(c, W_BB);
+        h.ids = wp<int>(c, W_IDS);
+        h.offsets = wp<int>(c, W_OFF);
+        h.perm = wp<int>(c, W_PERM);
+        h.w = wp<float>(c, W_W);
+        h.logits = wp<float>(c, W_LOGITS);
+        h.g = wp<float>(c, W_G);
+        h.u = wp<float>(c, W_U);
+        h.yd = wp<float>(c, W_YD);
+        h.tiles = wp<DecTile>(c, W_TILES);
+        h.adn = make_act_packed(c, D.down_cols, W_ADEC);
+        if (shared_ffn) {
+            h.shg = wp<float>(c, W_SHG);
+            h.shu = wp<float>(c, W_SHU);
+            h.shout = wp<float>(c, W_SHOUT);
+            h.asd = make_act_packed(c, D.n_ff_shared, W_SDEC);
+        }
+    }
+    return h;
+}
+
+bool use_decode(phx_moe_ctx* c, const Layer& L, int T, unsigned flags)
 {
     const phx_moe_layer_desc& D = L.desc;
     if (flags & PHX_FLAG_EXACT_ROUTER) return false;
-    if (T > 16 || T * D.n_used > 256 || T * D.n_expert > kRouteMaxTE || D.d > 4096 || D.d % 256 != 0) return false;
-    if (!dec_type(D.gate_up_type) || !dec_type(D.down_type) || D.down_cols > 4096) return false;
-    if (D.n_ff_shared > 0 && (D.shared_type != D.gate_up_type || D.shared_type != D.down_type || D.n_ff_shared > 4096))
-        return false;
-    return true;
+    if (T > 16 || T * D.n_used > 256 || T * D.n_expert > 2048 || D.d > 4096 || D.d % 256 != 0) return false;
+    if (!dec_type(D.gate_up_type) || D.down_type != D.gate_up_type) return false;
+    if (D.n_ff_shared > 0 && D.shared_type != D.gate_up_type) return false;
+    return dec_supported(dec_layer(c, L, T, nullptr, nullptr, nullptr, nullptr));
 }
 
 int run_layer_decode(phx_moe_ctx* c, const Layer& L, int T, const float* x, const float* shared, float* out, float* xres)
 {
-    const phx_moe_layer_desc& D = L.desc;
     hipStream_t st = c->stream;
-    const int d = D.d, E = D.n_expert, k = D.n_used, nf = D.n_ff;
-    const int n = T * k;
-    const bool shared_ffn = shared == nullptr && D.n_ff_shared > 0;
-    // every tile holds at least one assignment: at most n tiles, and at most ceil(n/A) + E
-    const int max_tiles = std::min(n, (n + kDecA - 1) / kDecA + E);
-    Act agu = make_act(c, ACT_Q8_0, d, W_AGU_Q, W_AGU_D, W_AGU_S);
-    Act adn = make_act(c, ACT_Q8_0, D.down_cols, W_ADN_Q, W_ADN_D, W_ADN_S);
-    Act ash, asd;
-    if (shared_ffn) {
-        ash = make_act(c, ACT_Q8_0, d, W_ASH_Q, W_ASH_D, W_ASH_S);
-        asd = make_act(c, ACT_Q8_0, D.n_ff_shared, W_ASD_Q, W_ASD_D, W_ASD_S);
-    }
+    const DecLayerH h = dec_layer(c, L, T, x, shared, out, xres);
     {
         ProfScope p(c, PHX_K_ROUTER);
-        RouteDecArgsH r{};
-        r.T = T;
-        r.d = d;
-        r.E = E;
-        r.k = k;
-        r.rule = D.weight_rule;
-        r.A = kDecA;
-        r.max_tiles = max_tiles;
-        r.eps = D.eps;
-        r.x = x;
-        r.W = L.wrow;
-        r.gis = L.gis;
-        r.ds = L.ds;
-        r.pre2 = L.pre2;
-        r.fnorm = shared_ffn ? L.ffn_norm : nullptr;
-        r.act_gu = agu;
-        r.act_sh = ash;
-        r.Lb = wp<double>(c, W_LB);
-        r.Bb = wp<double>(c, W_BB);
-        r.counter = wp<int>(c, W_COUNTER);
-        r.ids = wp<int>(c, W_IDS);
-        r.w = wp<float>(c, W_W);
-        r.logits = wp<float>(c, W_LOGITS);
-        r.offsets = wp<int>(c, W_OFF);
-        r.perm = wp<int>(c, W_PERM);
-        r.tiles = wp<DecTile>(c, W_TILES);
-        r.ntiles = wp<int>(c, W_NTILES);
-        r.flags = c->flags;
-        launch_route_dec(st, r);
+        launch_dec_route(st, h);
     }
     {
         ProfScope p(c, PHX_K_GATE_UP);
-        DecMatH m0, m1;
-        m0.q = &L.gu;
-        m0.in = agu;
-        m0.out0 = wp<float>(c, W_G);
-        m0.out1 = wp<float>(c, W_U);
-        m0.split = nf;
-        m0.out_act = adn;
-        if (shared_ffn) {
-            m1.q = &L.sgu;
-            m1.in = ash;
-            m1.out0 = wp<float>(c, W_SHG);
-            m1.out1 = wp<float>(c, W_SHU);
-            m1.split = D.n_ff_shared;
-            m1.out_act = asd;
-        }
-        launch_dec(st, 0, m0, m1, wp<DecTile>(c, W_TILES), max_tiles, k, T, c->gelu_tab);
+        launch_dec_gu(st, h);
     }
     {
         ProfScope p(c, PHX_K_DOWN);
-        DecMatH m0, m1;
-        m0.q = &L.dn;
-        m0.in = adn;
-        m0.out0 = wp<float>(c, W_YD);
-        if (shared_ffn) {
-            m1.q = &L.sdn;
-            m1.in = asd;
-            m1.out0 = wp<float>(c, W_SHOUT);
-        }
-        launch_dec(st, 1, m0, m1, wp<DecTile>(c, W_TILES), max_tiles, 1, T, c->gelu_tab);
+        launch_dec_down(st, h);
     }
     {
         ProfScope p(c, PHX_K_COMBINE);
-        launch_combine_dec(st, T, d, k, D.eps, wp<float>(c, W_YD), wp<float>(c, W_W),
-                           shared_ffn ? wp<float>(c, W_SHOUT) : shared, L.post1, L.post2, out, xres, L.post_ffw, c->flags);
+        launch_dec_combine(st, h);
     }
     HIPCHK(c, hipGetLastError());
     return PHX_OK;
@@ -636,7 +656,7 @@ int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, con
 int run_layer(phx_moe_ctx* c, const Layer& L, int T, const float* x, const float* shared, float* out, float* xres,
               unsigned flags)
 {
-    if (use_decode(L, T, flags)) return run_layer_decode(c, L, T, x, shared, out, xres);
+    if (use_decode(c, L, T, flags)) return run_layer_decode(c, L, T, x, shared, out, xres);
     return run_layer_general(c, L, T, x, shared, out, xres);
 }
 
@@ -653,8 +673,10 @@ void free_qmat(QMat& q)
 {
     if (q.payload) (void)hipFree(q.payload);
     if (q.scale) (void)hipFree(q.scale);
+    if (q.scale8) (void)hipFree(q.scale8);
     q.payload = nullptr;
     q.scale = nullptr;
+    q.scale8 = nullptr;
 }
 
 int upload_q(phx_moe_ctx* c, int type, const void* src, int n_mat, int rows, int cols, QMat& q, bool paired = false)
@@ -666,6 +688,10 @@ int upload_q(phx_moe_ctx* c, int type, const void* src, int n_mat, int rows, int
     HIPCHK(c, hipMalloc((void**)&q.scale, h.scale.size()));
     HIPCHK(c, hipMemcpy(q.payload, h.payload.data(), h.payload.size(), hipMemcpyHostToDevice));
     HIPCHK(c, hipMemcpy(q.scale, h.scale.data(), h.scale.size(), hipMemcpyHostToDevice));
+    if (!h.scale8.empty()) {
+        HIPCHK(c, hipMalloc((void**)&q.scale8, h.scale8.size()));
+        HIPCHK(c, hipMemcpy(q.scale8, h.scale8.data(), h.scale8.size(), hipMemcpyHostToDevice));
+    }
     return PHX_OK;
 }
 
