@@ -129,8 +129,8 @@ def run_layer(args, pkg):
     n = T * k
     mfma = (not decode and L["gate_up_type"] in (pkg.PHX.Q4_0, pkg.PHX.Q8_0)
             and L["down_type"] in (pkg.PHX.Q4_0, pkg.PHX.Q8_0) and n >= 8 * E)
-    # the decode path's router launch also computes the dense shared FFN's gate and up rows, and its
-    # gate|up launch the shared down rows: their weights are part of those launches' algorithmic bytes
+    # the decode path's gate|up launch also computes the dense shared FFN's gate and up rows, and its
+    # down launch the shared down rows: their weights are part of those launches' algorithmic bytes
     sh_gu_b = sh_dn_b = 0
     if L.get("n_ff_shared"):
         sh_gu_b = 2 * L["n_ff_shared"] * S.row_bytes(L["shared_type"], d)
@@ -139,8 +139,8 @@ def run_layer(args, pkg):
     layer_expert_bytes = avg_experts * (gu_b + dn_b)
     router_bytes = E * d * 4
     if decode:
-        gu_bytes = avg_experts * gu_b + sh_dn_b
-        dn_bytes = avg_experts * dn_b
+        gu_bytes = avg_experts * gu_b + sh_gu_b
+        dn_bytes = avg_experts * dn_b + sh_dn_b
         achieved = gu_bytes / (gu_ms * 1e-3) / 1e9
         roofline = {
             "bound": "hbm",
@@ -150,7 +150,7 @@ def run_layer(args, pkg):
             "traffic_source": PMC_TRAFFIC.get((cfg_name, T, "gate_up"), (None, None))[1],
             "bytes_per_launch": int(gu_bytes), "avg_launch_us": round(gu_ms * 1e3, 3),
             "per_unit": f"{gu_b} B of gate|up weights per touched expert x {avg_experts:.2f} experts per launch"
-                        + (f" + {sh_dn_b} B of shared-FFN down weights" if sh_dn_b else ""),
+                        + (f" + {sh_gu_b} B of shared-FFN gate and up weights" if sh_gu_b else ""),
         }
         down_rate = {"down_gbs": round(dn_bytes / (dn_ms * 1e-3) / 1e9, 1)}
     elif mfma:

@@ -1,11 +1,13 @@
 // Decode-shaped MoE FFN kernels (a few tokens, T <= 16; Q4_0 / Q8_0 weights): four launches per layer.
-//   k_dec_route    router logits with certified error bounds, one workgroup per (token, expert); beside
-//                  them, the dense shared FFN's gate|up product with its gelu(g) * u Q8_0 epilogue
-//   k_dec_gu       every workgroup selects the top-k from the router's bounds (exact fallback when the
-//                  order cannot be certified) and forms the expert tiles, then computes one (tile, row
-//                  group) of the routed experts' gate|up products with the same epilogue; beside them,
-//                  the shared FFN's down product
-//   k_dec_down     one (tile, row group) of the routed experts' down products
+//   k_dec_route    router logits with certified error bounds, one workgroup per (token, expert), and the
+//                  Q8_0 expert and shared-FFN inputs (each workgroup quantizes its share of the
+//                  token's 32-blocks)
+//   k_dec_gu       every expert workgroup selects the top-k from the router's bounds (exact fallback
+//                  when the order cannot be certified) and forms the expert tiles, then computes one
+//                  (tile, row group) of the routed experts' gate|up products with the gelu(g) * u Q8_0
+//                  epilogue; beside them, the dense shared FFN's gate|up product
+//   k_dec_down     (tile, row groups) of the routed experts' down products; beside them, the shared
+//                  FFN's down product
 //   k_dec_combine  per token: the rank-ordered combine, the two branch norms, the optional residual
 // Arithmetic follows the reference CPU path (src/GemmaCpu.cs:376-422): integer block sums, the float
 // block chain sum += (float)isum * (d_w * d_x) in block order (src/CpuRefGemma.cs:27-36,
@@ -17,7 +19,9 @@
 // holding blocks 8w..8w+7 of its lane's row.  Every wave issues its 8 payload loads (16 B per lane, a
 // 1 KB contiguous span per instruction) and one 16 B load of the 8 blocks' fp16 scales before it
 // waits on any of them; the small activation loads are issued before the weights, so the first wait
-// is for them alone.  Block indices past the row end are clamped, never branched around.
+// is for them alone.  Block indices past the row end are clamped, never branched around.  These
+// kernels are bound by latency and by the CU's issue rate, so per-thread work is sized at compile time
+// (no masked slots) and reductions use DPP.
 #include <algorithm>
 
 #include "device_common.h"
@@ -27,7 +31,6 @@ namespace phx {
 constexpr int DMAXNB = 128;  // blocks of 32 per row: K <= 4096
 constexpr int DROWS = 2;     // assignments (expert tiles) or tokens (shared FFN) per workgroup
 constexpr int DBPW = 8;      // blocks per wave
-constexpr int RPER = 16;     // router elements per thread (d <= 4096 over >= 256 threads)
 
 template <int TYPE>
 struct DecCfg {
@@ -64,6 +67,9 @@ struct DecArgs {
     const float* fnorm;   // ffn_norm (shared FFN input)
     const float* post_ffw;
     MatD gu, dn, sgu, sdn;  // sgu.rg == 0: no shared FFN computed
+    Act agu;              // packed Q8_0 expert input rows [T] (k_dec_route writes, k_dec_gu reads)
+    Act ash;              // packed Q8_0 shared-FFN input rows [T]
+    int rpw;              // k_dec_down: expert row groups per workgroup
     double* Lb;           // [T][E] certified logits (double sums)
     double* Bb;           // [T][E] their error bounds
     int* ids;             // [T][k]
@@ -131,12 +137,11 @@ __device__ __forceinline__ int q8_0_half(float x, float* dval, int* sum)
 // Workgroup-level: every thread calls it; red holds blockDim.x / 64 + 1 doubles.
 __device__ float wg_mean_sq(double s, const float* xr, int n, double* red, int* fallbacks)
 {
-    const int tid = threadIdx.x, nw = blockDim.x >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, nw = blockDim.x >> 6;
     s = wave_sum_dpp(s);
-    if ((tid & 63) == 0) red[tid >> 6] = s;
+    if (lane == 0) red[tid >> 6] = s;
     __syncthreads();
-    double S = 0.0;
-    for (int w = 0; w < nw; w++) S += red[w];
+    const double S = wave_sum_dpp(lane < nw ? red[lane] : 0.0);  // the wave totals in a fixed tree order
     const double B = ((double)n + 64.0) * 0x1p-52 * S;
     const float lo = (float)((S - B) / (double)n), hi = (float)((S + B) / (double)n);
     float mean = lo;
@@ -258,7 +263,9 @@ template <int TYPE>
 __device__ __forceinline__ void load_w(const MatD& M, int e, int rgi, int wave, int lane, WRegs<TYPE>& W)
 {
     constexpr int PAY = DecCfg<TYPE>::PAY, NC = DecCfg<TYPE>::NC;
-    const int b0 = min(wave * DBPW, (M.nb8 - 1) * DBPW);  // waves past the row reload its last blocks
+    // unconditional: a wave past the row reloads the row's last blocks (no branch around the loads, so
+    // the compiler's wait counts stay exact)
+    const int b0 = min(wave * DBPW, (M.nb8 - 1) * DBPW);
     const uint8_t* p = M.pay + (int64_t)e * M.mat_pay + ((int64_t)rgi * M.nb * 64 + lane) * PAY;
 #pragma unroll
     for (int j = 0; j < DBPW; j++) {
@@ -312,13 +319,14 @@ __device__ __forceinline__ float blk_term(const WRegs<TYPE>& W, int j, const Act
     return (float)isum * dd;
 }
 
-// One row group for cnt <= DROWS activation rows: every wave's block terms into LDS
-// (terms[r][b][lane], row stride nb), then wave r adds row r's terms in block order.  Returns the chain
-// value in waves r < cnt (0 elsewhere).
+// One row group for cnt <= DROWS activation rows, computed by the waves wl = 0, 1, ... of the group
+// (wave wl holds blocks 8 wl..8 wl+7): every wave's block terms into LDS (terms[r][b][lane], row stride
+// nb), a workgroup barrier, then wave wl = r adds row r's terms in block order.  Returns the chain value
+// in waves wl < cnt (0 elsewhere).  Every wave of the workgroup calls it once (one barrier).
 template <int TYPE>
-__device__ float rowgroup_chain(const WRegs<TYPE>& W, int nb, const ActL* act, int cnt, float* terms)
+__device__ float rowgroup_chain(const WRegs<TYPE>& W, int wl, int nb, const ActL* act, int cnt, float* terms)
 {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, b0 = wave * DBPW;
+    const int lane = threadIdx.x & 63, b0 = wl * DBPW;
     if (b0 < nb) {  // uniform per wave
         for (int r = 0; r < cnt; r++) {
 #pragma unroll
@@ -331,8 +339,8 @@ __device__ float rowgroup_chain(const WRegs<TYPE>& W, int nb, const ActL* act, i
     }
     __syncthreads();
     float S = 0.0f;
-    if (wave < cnt) {
-        const float* tr = terms + wave * nb * 64 + lane;
+    if (wl < cnt) {
+        const float* tr = terms + wl * nb * 64 + lane;
         int b = 0;
         for (; b + 8 <= nb; b += 8) {
             float t[8];
@@ -393,126 +401,131 @@ typedef __attribute__((address_space(3))) void* lds_void_t;
 typedef __attribute__((address_space(1))) void* glb_void_t;
 
 // ------------------------------------------------------------------------------ k_dec_route
-// Router part: one workgroup per (token t, expert e).  The reference logit is the sequential float
-// sum of the rounded products p_i = fl(W[e][i] * m_i), m_i = ((x_i * rinv) * sc) * s_i
-// (src/GemmaCpu.cs:389-395).  The workgroup forms the same p_i (each thread a contiguous chunk of i),
-// sums them in double (L), and bounds the reference's accumulated rounding by
+// One workgroup per (token t, expert e), d / 4 threads: thread i holds elements 4i..4i+3.  The
+// reference logit is the sequential float sum of the rounded products p_i = fl(W[e][i] * m_i),
+// m_i = ((x_i * rinv) * sc) * s_i (src/GemmaCpu.cs:389-395).  The workgroup forms the same p_i, sums
+// them in double (L), and bounds the reference's accumulated rounding by
 //   |S_ref - L| <= 2^-24 * sum_k |S_k| * 1.001 + 2^-45 * sum_i |p_i|,
-// S_k the prefix sums (a scan over the chunks), the second term covering the double arithmetic.
-// k_dec_gu ranks the experts by L and certifies the order from these intervals.
-__device__ void route_wg(const DecArgs& a, int t, int e, unsigned char* smem)
+// S_k the prefix sums (a scan over the threads), the second term covering the double arithmetic.
+// k_dec_gu ranks the experts by L and certifies the order from these intervals.  The workgroup also
+// writes the Q8_0 expert input n = (x * rinv) * pre_ffw_norm_2 (src/GemmaCpu.cs:409) of the 32-blocks b
+// with b % E == e: the 8 threads of block b hold its 32 values.
+__global__ __launch_bounds__(1024) void k_dec_route(DecArgs a)
 {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, d = a.d, NT = blockDim.x, NWV = NT >> 6;
-    float* sx = (float*)smem;
-    float* sg = sx + d + RPER;
-    float* sw = sg + d + RPER;
-    double* red = (double*)(sw + d + RPER);  // 17
-    double* wsum = red + 17;                 // 16
-    double* wA = wsum + 16;
-    double* wP = wA + 16;
-    {
-        // x_t, the router scale and W[e] into LDS with direct global -> LDS loads (16 B per lane)
-        const int n4 = d / 4;
-        auto stage = [&](const float* src, float* dst) {
-            for (int q = 0; q * NT < n4; q++) {
-                const int i = q * NT + tid;
-                if (i < n4)
-                    __builtin_amdgcn_global_load_lds((glb_void_t)((const float4*)src + i),
-                                                     (lds_void_t)((float4*)dst + q * NT + wave * 64), 16, 0, 0);
-            }
-        };
-        stage(a.x + (int64_t)t * d, sx);
-        stage(a.gis, sg);
-        stage(a.W + (int64_t)e * d, sw);
-        __builtin_amdgcn_s_waitcnt(0);
-    }
-    __syncthreads();
-    const int per = (d + NT - 1) / NT, c0 = min(tid * per, d), cnt = min(per, d - c0);
-    float xv[RPER], gv[RPER], wv[RPER];
-#pragma unroll
-    for (int j = 0; j < RPER; j++) {
-        xv[j] = sx[c0 + j];
-        gv[j] = sg[c0 + j];
-        wv[j] = sw[c0 + j];
-    }
-    double s2 = 0.0;
-#pragma unroll
-    for (int j = 0; j < RPER; j++)
-        if (j < cnt) s2 += (double)xv[j] * (double)xv[j];
-    int* flags0 = (t == 0 && e == 0) ? a.flags : nullptr;
-    const float rinv = rms_scale_from_mean(wg_mean_sq(s2, sx, d, red, flags0), a.eps);
+    __shared__ double red[17], wsum[16], wA[16], wP[16];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, NWV = blockDim.x >> 6, d = a.d;
+    const int t = blockIdx.x / a.E, e = blockIdx.x % a.E;
+    const float* xr = a.x + (int64_t)t * d;
+    const float4 xv = ((const float4*)xr)[tid];
+    const float4 gv = ((const float4*)a.gis)[tid];
+    const float4 wv = ((const float4*)(a.W + (int64_t)e * d))[tid];
+    const float4 nv = ((const float4*)a.pre2)[tid];
+    const float4 fv = a.ash.q ? ((const float4*)a.fnorm)[tid] : nv;
+    const double s2 = ((double)xv.x * (double)xv.x + (double)xv.y * (double)xv.y) +
+                      ((double)xv.z * (double)xv.z + (double)xv.w * (double)xv.w);
+    const float rinv = rms_scale_from_mean(wg_mean_sq(s2, xr, d, red, (t == 0 && e == 0) ? a.flags : nullptr), a.eps);
     const float sc = 1.0f / (float)__dsqrt_rn((double)d);
-    float pv[RPER];
-    double loc = 0.0, P = 0.0;
-#pragma unroll
-    for (int j = 0; j < RPER; j++) {
-        const float p = wv[j] * (xv[j] * rinv * sc * gv[j]);
-        pv[j] = j < cnt ? p : 0.0f;
-        loc += (double)pv[j];
-        P += fabs((double)pv[j]);
-    }
+    const float p0 = wv.x * (xv.x * rinv * sc * gv.x), p1 = wv.y * (xv.y * rinv * sc * gv.y),
+                p2 = wv.z * (xv.z * rinv * sc * gv.z), p3 = wv.w * (xv.w * rinv * sc * gv.w);
+    const double q0 = p0, q1 = p1, q2 = p2, q3 = p3;
+    const double loc = ((q0 + q1) + q2) + q3;
+    double P = (fabs(q0) + fabs(q1)) + (fabs(q2) + fabs(q3));
     const double inc = wave_incl_scan_dpp(loc);
     if (lane == 63) wsum[wave] = inc;
     __syncthreads();
-    double base = 0.0;
-    for (int w = 0; w < wave; w++) base += wsum[w];
+    const double base = wave_sum_dpp(lane < wave ? wsum[lane] : 0.0);  // the earlier waves' totals
     double acc = base + (inc - loc);  // exclusive prefix (within the double slack of the bound)
-    double A = 0.0;
-#pragma unroll
-    for (int j = 0; j < RPER; j++) {
-        acc += (double)pv[j];
-        if (j < cnt) A += fabs(acc);
-    }
+    double A;
+    acc += q0;
+    A = fabs(acc);
+    acc += q1;
+    A += fabs(acc);
+    acc += q2;
+    A += fabs(acc);
+    acc += q3;
+    A += fabs(acc);
     A = wave_sum_dpp(A);
     P = wave_sum_dpp(P);
     if (lane == 0) {
         wA[wave] = A;
         wP[wave] = P;
     }
-    __syncthreads();
-    if (tid == 0) {
-        double L = 0.0, As = 0.0, Ps = 0.0;
-        for (int w = 0; w < NWV; w++) {
-            L += wsum[w];
-            As += wA[w];
-            Ps += wP[w];
+    // the expert input blocks of this workgroup (uniform per 8-lane group)
+    const int b = tid >> 3;
+    if (b % a.E == e) {
+        const float4 v = make_float4((xv.x * rinv) * nv.x, (xv.y * rinv) * nv.y, (xv.z * rinv) * nv.z,
+                                     (xv.w * rinv) * nv.w);
+        float dval;
+        int sum;
+        const int qw = q8_0_oct(v, &dval, &sum);
+        ((int*)(a.agu.q + (int64_t)t * a.agu.qstride))[tid] = qw;
+        if ((tid & 7) == 0) {
+            a.agu.d[(int64_t)t * a.agu.dstride + b] = dval;
+            a.agu.s[(int64_t)t * a.agu.sstride + b] = sum;
         }
-        a.Lb[(int64_t)t * a.E + e] = L;
-        a.Bb[(int64_t)t * a.E + e] = 0x1p-24 * As * 1.001 + 0x1p-45 * Ps;
+        if (a.ash.q) {  // the shared FFN input (x * rinv) * ffn_norm (src/GemmaCpu.cs:349)
+            const float4 u = make_float4((xv.x * rinv) * fv.x, (xv.y * rinv) * fv.y, (xv.z * rinv) * fv.z,
+                                         (xv.w * rinv) * fv.w);
+            const int qs = q8_0_oct(u, &dval, &sum);
+            ((int*)(a.ash.q + (int64_t)t * a.ash.qstride))[tid] = qs;
+            if ((tid & 7) == 0) {
+                a.ash.d[(int64_t)t * a.ash.dstride + b] = dval;
+                a.ash.s[(int64_t)t * a.ash.sstride + b] = sum;
+            }
+        }
+    }
+    __syncthreads();
+    if (wave == 0) {
+        const bool in = lane < NWV;
+        const double L = wave_sum_dpp(in ? wsum[lane] : 0.0);
+        const double As = wave_sum_dpp(in ? wA[lane] : 0.0);
+        const double Ps = wave_sum_dpp(in ? wP[lane] : 0.0);
+        if (lane == 0) {
+            a.Lb[(int64_t)t * a.E + e] = L;
+            a.Bb[(int64_t)t * a.E + e] = 0x1p-24 * As * 1.001 + 0x1p-45 * Ps;
+        }
     }
 }
 
-// Shared FFN gate|up part: one workgroup per (pair of tokens, paired row group).
+// ------------------------------------------------------------------------------ shared FFN workgroups
+// Shared gate|up (in k_dec_gu): one workgroup per (pair of tokens, paired row group), input from
+// k_dec_route's packed Q8_0 rows.
 template <int TYPE>
 __device__ void shared_gu_wg(const DecArgs& a, int tile, int rgi, unsigned char* smem)
 {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     ActL* act = (ActL*)smem;
-    double* red = (double*)(act + DROWS);
-    float* terms = (float*)(red + 32);
-    const int t0 = tile * DROWS, cnt = min(DROWS, a.T - t0), t1 = min(t0 + 1, a.T - 1);
-    QIn qin;
-    quant_issue(qin, a.x, t0, t1, a.fnorm, a.d);
+    float* terms = (float*)(act + DROWS);
+    const int t0 = tile * DROWS, cnt = min(DROWS, a.T - t0);
+    ActIn ain;
+    act_issue(ain, a.ash, t0, min(t0 + 1, a.T - 1), cnt, a.sgu.nb);
     __builtin_amdgcn_sched_barrier(0);  // keep the activation loads ahead of the weight loads
     WRegs<TYPE> W;
-    load_w<TYPE>(a.sgu, 0, rgi, wave, lane, W);  // unconditional: a wave past the row reloads its last block
-    quant_finish(qin, a.x, t0, t1, cnt, a.d, a.eps, act, red, nullptr);
+    load_w<TYPE>(a.sgu, 0, rgi, wave, lane, W);
+    act_store(ain, cnt, a.sgu.nb, act);
     __syncthreads();
-    const float S = rowgroup_chain<TYPE>(W, a.sgu.nb, act, cnt, terms);
+    const float S = rowgroup_chain<TYPE>(W, wave, a.sgu.nb, act, cnt, terms);
     if (wave < cnt) gu_epilogue(S, rgi, a.nff, t0 + wave, a.shg, a.shu, a.asd, a.gelu_tab);
 }
 
+// Shared down (in k_dec_down): one workgroup per (pair of tokens, row group).
 template <int TYPE>
-__global__ __launch_bounds__(1024) void k_dec_route(DecArgs a)
+__device__ void shared_dn_wg(const DecArgs& a, int tile, int rgi, unsigned char* smem)
 {
-    extern __shared__ __align__(16) unsigned char dsm[];
-    const int nr = a.T * a.E;
-    if ((int)blockIdx.x < nr) {
-        route_wg(a, blockIdx.x / a.E, blockIdx.x % a.E, dsm);
-    } else {
-        const int s = blockIdx.x - nr;
-        shared_gu_wg<TYPE>(a, s / a.sgu.rg, s % a.sgu.rg, dsm);
-    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    ActL* act = (ActL*)smem;
+    float* terms = (float*)(act + DROWS);
+    const int t0 = tile * DROWS, cnt = min(DROWS, a.T - t0);
+    ActIn ain;
+    act_issue(ain, a.asd, t0, min(t0 + 1, a.T - 1), cnt, a.sdn.nb);
+    __builtin_amdgcn_sched_barrier(0);  // keep the activation loads ahead of the weight loads
+    WRegs<TYPE> W;
+    load_w<TYPE>(a.sdn, 0, rgi, wave, lane, W);
+    act_store(ain, cnt, a.sdn.nb, act);
+    __syncthreads();
+    const float S = rowgroup_chain<TYPE>(W, wave, a.sdn.nb, act, cnt, terms);
+    const int row = rgi * 64 + lane;
+    if (wave < cnt && row < a.sdn.rows) a.shout[(int64_t)(t0 + wave) * a.d + row] = S;
 }
 
 // ------------------------------------------------------------------------------ k_dec_gu
@@ -523,6 +536,13 @@ __global__ __launch_bounds__(1024) void k_dec_route(DecArgs a)
 // ranked after it; an order the key gets wrong (logits within 256 float ulps) is never certified,
 // since certification compares the intervals themselves.  When a token is not certified, the whole
 // workgroup takes select_exact.
+__device__ __forceinline__ double readlane_d(double v, int l)
+{
+    const long long b = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_readlane((int)b, l), hi = __builtin_amdgcn_readlane((int)(b >> 32), l);
+    return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
+
 __device__ bool wave_topk(const DecArgs& a, int t, int* s_ids)
 {
     const int lane = threadIdx.x & 63;
@@ -543,48 +563,42 @@ __device__ bool wave_topk(const DecArgs& a, int t, int* s_ids)
         key[q] = ex < a.E ? (sortable_f32((float)L[q]) & ~0xFFu) | (unsigned)(255 - ex) : 0u;
         if (ex < a.E && !(isfinite(L[q]) && isfinite(B[q]))) fin = false;
     }
-    // k rounds of the wave maximum; chosen[q] marks this lane's chosen slots
-    bool chosen[4] = {false, false, false, false};
-    double lo_mine = INFINITY, hi_mine = -INFINITY;  // lane j: the rank-j expert's interval
+    // k rounds of the wave maximum: the winner's slot leaves the candidates; rank j's interval is read
+    // from the owning lane (a uniform index) and kept in lane j
+    double lo_mine = INFINITY, hi_mine = -INFINITY;
     int id_mine = 0;
     for (int j = 0; j < a.k; j++) {
-        unsigned m = max(max(key[0], key[1]), max(key[2], key[3]));
-        m = wave_max_u32(m);
-        const int ex = 255 - (int)(m & 0xFFu);
-        // the slot owning the key leaves the candidates; its interval goes to lane j
-        double lo = INFINITY, hi = -INFINITY;
+        const unsigned m = wave_max_u32(max(max(key[0], key[1]), max(key[2], key[3])));
+        const int ex = 255 - (int)(m & 0xFFu), owner = ex & 63, qo = ex >> 6;
+        double lo = 0.0, hi = 0.0;
 #pragma unroll
         for (int q = 0; q < 4; q++)
-            if (key[q] == m && lane + 64 * q == ex) {
-                key[q] = 0u;
-                chosen[q] = true;
-                lo = L[q] - B[q];
-                hi = L[q] + B[q];
+            if (q == qo) {
+                if (lane == owner) key[q] = 0u;
+                lo = readlane_d(L[q] - B[q], owner);
+                hi = readlane_d(L[q] + B[q], owner);
             }
-        const int owner = ex & 63;
-        lo = __shfl(lo, owner, 64);
-        hi = __shfl(hi, owner, 64);
         if (lane == j) {
             lo_mine = lo;
             hi_mine = hi;
             id_mine = ex;
         }
     }
+    // the unchosen experts' highest upper end (chosen slots hold key 0)
     double hun = -INFINITY;
 #pragma unroll
     for (int q = 0; q < 4; q++)
-        if (lane + 64 * q < a.E && !chosen[q]) hun = fmax(hun, L[q] + B[q]);
+        if (lane + 64 * q < a.E && key[q] != 0u) hun = fmax(hun, L[q] + B[q]);
     hun = wave_max_dpp(hun);
-    // suffix maximum over the later ranks (lanes above), then the unchosen experts
-    double suf = hi_mine;
-    for (int o = 1; o < 16; o <<= 1) {
-        const double up = __shfl_down(suf, o, 64);
-        if (lane + o < 16) suf = fmax(suf, up);
+    // certified iff, from the last rank down, each lower end exceeds every later upper end
+    bool cert = __all(fin);
+    double later = hun;
+    for (int j = a.k - 1; j >= 0; j--) {
+        const double loj = readlane_d(lo_mine, j), hij = readlane_d(hi_mine, j);
+        cert = cert && loj > later;
+        later = fmax(later, hij);
     }
-    const double later = fmax(hun, lane + 1 < 16 ? __shfl_down(suf, 1, 64) : -INFINITY);
-    const bool act = lane < a.k;
-    const bool cert = __all(fin && (!act || lo_mine > later));
-    if (act) s_ids[t * a.k + lane] = id_mine;
+    if (lane < a.k) s_ids[t * a.k + lane] = id_mine;
     return cert;
 }
 
@@ -812,35 +826,16 @@ __device__ void expert_gu_wg(const DecArgs& a, unsigned char* smem)
     const DecTile tl = s_tiles[tile];
     const int e = tl.e, cnt = min(tl.cnt, DROWS);
     const int tok0 = tl.row[0] / a.k, tok1 = tl.row[cnt > 1 ? 1 : 0] / a.k;
-    QIn qin;
-    quant_issue(qin, a.x, tok0, tok1, a.pre2, a.d);
-    __builtin_amdgcn_sched_barrier(0);  // keep the activation loads ahead of the weight loads
-    WRegs<TYPE> W;
-    load_w<TYPE>(a.gu, clamp_id(e, a.E), rgi, wave, lane, W);  // unconditional (see shared_gu_wg)
-    __syncthreads();  // the exact-selection arrays are about to become terms
-    quant_finish(qin, a.x, tok0, tok1, cnt, a.d, a.eps, act, red, nullptr);
-    __syncthreads();
-    const float S = rowgroup_chain<TYPE>(W, nb, act, cnt, (float*)un);
-    if (wave < cnt) gu_epilogue(S, rgi, a.nf, wave == 0 ? tl.row[0] : tl.row[1], a.g, a.u, a.adn, a.gelu_tab);
-}
-
-template <int TYPE>
-__device__ void shared_dn_wg(const DecArgs& a, int tile, int rgi, unsigned char* smem)
-{
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    ActL* act = (ActL*)smem;
-    float* terms = (float*)(act + DROWS);
-    const int t0 = tile * DROWS, cnt = min(DROWS, a.T - t0);
     ActIn ain;
-    act_issue(ain, a.asd, t0, min(t0 + 1, a.T - 1), cnt, a.sdn.nb);
+    act_issue(ain, a.agu, tok0, tok1, cnt, nb);
     __builtin_amdgcn_sched_barrier(0);  // keep the activation loads ahead of the weight loads
     WRegs<TYPE> W;
-    load_w<TYPE>(a.sdn, 0, rgi, wave, lane, W);  // unconditional (see shared_gu_wg)
-    act_store(ain, cnt, a.sdn.nb, act);
+    load_w<TYPE>(a.gu, clamp_id(e, a.E), rgi, wave, lane, W);  // unconditional (see load_w)
+    __syncthreads();  // the exact-selection arrays are about to become terms
+    act_store(ain, cnt, nb, act);
     __syncthreads();
-    const float S = rowgroup_chain<TYPE>(W, a.sdn.nb, act, cnt, terms);
-    const int row = rgi * 64 + lane;
-    if (wave < cnt && row < a.sdn.rows) a.shout[(int64_t)(t0 + wave) * a.d + row] = S;
+    const float S = rowgroup_chain<TYPE>(W, wave, nb, act, cnt, (float*)un);
+    if (wave < cnt) gu_epilogue(S, rgi, a.nf, wave == 0 ? tl.row[0] : tl.row[1], a.g, a.u, a.adn, a.gelu_tab);
 }
 
 template <int TYPE>
@@ -852,34 +847,44 @@ __global__ __launch_bounds__(1024) void k_dec_gu(DecArgs a)
         expert_gu_wg<TYPE>(a, dsm);
     } else {
         const int s = blockIdx.x - ne;
-        shared_dn_wg<TYPE>(a, s / a.sdn.rg, s % a.sdn.rg, dsm);
+        shared_gu_wg<TYPE>(a, s / a.sgu.rg, s % a.sgu.rg, dsm);
     }
 }
 
 // ------------------------------------------------------------------------------ k_dec_down
-// One (tile, row group) of the routed experts' down products, the tile list from k_dec_gu's
-// workgroup 0: yd[a][row] = down_e(gelu(g) * u)[row] for the tile's assignments.
+// Expert workgroups: a tile (from k_dec_gu's workgroup 0) and rpw consecutive row groups, wpr =
+// ceil(nb / 8) waves each: yd[a][row] = down_e(gelu(g) * u)[row] for the tile's assignments.  Shared
+// workgroups (after the expert ones): the shared FFN's down product.
 template <int TYPE>
 __global__ __launch_bounds__(1024) void k_dec_down(DecArgs a)
 {
     extern __shared__ __align__(16) unsigned char dsm[];
+    const int nb = a.dn.nb, wpr = (nb + DBPW - 1) / DBPW, nrgb = (a.dn.rg + a.rpw - 1) / a.rpw;
+    const int ne = a.max_tiles * nrgb;
+    if ((int)blockIdx.x >= ne) {
+        const int s = blockIdx.x - ne;
+        shared_dn_wg<TYPE>(a, s / a.sdn.rg, s % a.sdn.rg, dsm);
+        return;
+    }
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int tile = blockIdx.x / a.dn.rg, rgi = blockIdx.x % a.dn.rg;
+    const int tile = blockIdx.x / nrgb, g = wave / wpr, wl = wave % wpr;
+    const int rgi = (blockIdx.x % nrgb) * a.rpw + g;
+    const bool live = g < a.rpw && rgi < a.dn.rg;  // spare waves compute a clamped row group, store nothing
     const int4 tl = *(const int4*)(a.tiles + tile);  // {e, cnt, row0, row1}
-    if (tl.x < 0) return;                            // slot past the last tile
-    const int e = tl.x, cnt = min(tl.y, DROWS), nb = a.dn.nb;
+    if (tl.x < 0) return;                            // slot past the last tile (uniform)
+    const int e = tl.x, cnt = min(tl.y, DROWS);
     ActL* act = (ActL*)dsm;
-    float* terms = (float*)(act + DROWS);
+    float* terms = (float*)(act + DROWS) + (size_t)min(g, a.rpw - 1) * DROWS * nb * 64;
     ActIn ain;
     act_issue(ain, a.adn, tl.z, cnt > 1 ? tl.w : tl.z, cnt, nb);
     __builtin_amdgcn_sched_barrier(0);  // keep the activation loads ahead of the weight loads
     WRegs<TYPE> W;
-    load_w<TYPE>(a.dn, clamp_id(e, a.E), rgi, wave, lane, W);  // unconditional (see shared_gu_wg)
+    load_w<TYPE>(a.dn, clamp_id(e, a.E), min(rgi, a.dn.rg - 1), wl, lane, W);  // unconditional (see load_w)
     act_store(ain, cnt, nb, act);
     __syncthreads();
-    const float S = rowgroup_chain<TYPE>(W, nb, act, cnt, terms);
+    const float S = rowgroup_chain<TYPE>(W, live ? wl : wpr, nb, act, cnt, terms);
     const int row = rgi * 64 + lane;
-    if (wave < cnt && row < a.d) a.yd[(int64_t)(wave == 0 ? tl.z : tl.w) * a.d + row] = S;
+    if (live && wl < cnt && row < a.d) a.yd[(int64_t)(wl == 0 ? tl.z : tl.w) * a.d + row] = S;
 }
 
 // ------------------------------------------------------------------------------ k_dec_combine
@@ -987,6 +992,21 @@ static MatD mat_d(const QMat* q)
     return m;
 }
 
+static int waves_for(int nb) { return (nb + DBPW - 1) / DBPW; }
+
+// block sizes: a row-group workgroup has one wave per 8 blocks (at least 4 where the selection and the
+// lists run); the router has d / 4 threads; a down workgroup holds rpw expert row groups, as many as
+// fit the shared down's workgroup size
+static int nt_gu(const DecLayerH& h)
+{
+    int nw = std::max(4, waves_for(h.gu->nb));
+    if (h.sgu) nw = std::max(nw, waves_for(h.sgu->nb));
+    return 64 * nw;
+}
+
+static int nw_down(const DecLayerH& h) { return std::max(waves_for(h.dn->nb), h.sdn ? waves_for(h.sdn->nb) : 0); }
+static int rpw_down(const DecLayerH& h) { return nw_down(h) / waves_for(h.dn->nb); }
+
 static DecArgs dec_args(const DecLayerH& h)
 {
     DecArgs a{};
@@ -1012,6 +1032,9 @@ static DecArgs dec_args(const DecLayerH& h)
     a.dn = mat_d(h.dn);
     a.sgu = mat_d(h.sgu);
     a.sdn = mat_d(h.sdn);
+    a.agu = h.agu;
+    a.ash = h.sgu ? h.ash : Act{};
+    a.rpw = rpw_down(h);
     a.Lb = h.Lb;
     a.Bb = h.Bb;
     a.ids = h.ids;
@@ -1035,37 +1058,21 @@ static DecArgs dec_args(const DecLayerH& h)
     return a;
 }
 
-static int waves_for(int nb) { return (nb + DBPW - 1) / DBPW; }
-
-// block sizes: every row-group workgroup has one wave per 8 blocks (and at least 4 waves where the
-// selection, the lists or the router run)
-static int nt_route(const DecLayerH& h) { return 64 * std::max(4, waves_for(h.gu->nb)); }
-
-static int nt_gu(const DecLayerH& h)
-{
-    int nw = std::max(4, waves_for(h.gu->nb));
-    if (h.sdn) nw = std::max(nw, waves_for(h.sdn->nb));
-    return 64 * nw;
-}
-
-static size_t route_lds(const DecLayerH& h)
-{
-    const size_t router = (size_t)3 * (h.d + RPER) * 4 + (size_t)(17 + 48) * 8;
-    const size_t sh = h.sgu ? sizeof(ActL) * DROWS + 32 * 8 + (size_t)DROWS * h.sgu->nb * 64 * 4 : 0;
-    return std::max(router, sh);
-}
-
 static size_t gu_lds(const DecLayerH& h)
 {
     const size_t TE = (size_t)h.T * h.E;
     const size_t un = (std::max((size_t)DROWS * h.gu->nb * 64 * 4, TE * 11) + 15) & ~(size_t)15;
-    const size_t ex = un + sizeof(ActL) * DROWS + (256 * 2 + 260 * 3) * 4 + 272 * sizeof(DecTile) + (20 + 32) * 4 +
-                      17 * 8;
-    const size_t sh = h.sdn ? sizeof(ActL) * DROWS + (size_t)DROWS * h.sdn->nb * 64 * 4 : 0;
+    const size_t ex = un + sizeof(ActL) * DROWS + (256 * 2 + 260 * 3) * 4 + 272 * sizeof(DecTile) + (20 + 32) * 4 + 17 * 8;
+    const size_t sh = h.sgu ? sizeof(ActL) * DROWS + (size_t)DROWS * h.sgu->nb * 64 * 4 : 0;
     return std::max(ex, sh);
 }
 
-static size_t down_lds(const DecLayerH& h) { return sizeof(ActL) * DROWS + (size_t)DROWS * h.dn->nb * 64 * 4; }
+static size_t down_lds(const DecLayerH& h)
+{
+    const size_t ex = sizeof(ActL) * DROWS + (size_t)rpw_down(h) * DROWS * h.dn->nb * 64 * 4;
+    const size_t sh = h.sdn ? sizeof(ActL) * DROWS + (size_t)DROWS * h.sdn->nb * 64 * 4 : 0;
+    return std::max(ex, sh);
+}
 
 template <class K>
 static void raise_lds(K kernel, size_t bytes)
@@ -1078,57 +1085,44 @@ bool dec_supported(const DecLayerH& h)
     if (h.d > 4096 || h.d % 256 || h.gu->nb > DMAXNB || h.dn->nb > DMAXNB || h.E > 256 || h.T * h.k > 256) return false;
     if (h.sgu && (h.sgu->nb > DMAXNB || h.sdn->nb > DMAXNB)) return false;
     if (nt_gu(h) < std::max(h.E, h.T * h.k)) return false;  // build_tiles: a thread per expert and assignment
-    return gu_lds(h) <= 160 * 1024 && route_lds(h) <= 160 * 1024;
+    return gu_lds(h) <= 160 * 1024 && down_lds(h) <= 160 * 1024;
 }
+
+template <template <int> class KT>
+static void launch_typed(const DecLayerH& h, dim3 grid, dim3 block, size_t lds, hipStream_t st, const DecArgs& a)
+{
+    if (h.gu->type == PHX_Q4_0_DEV) {
+        raise_lds(KT<PHX_Q4_0_DEV>::fn, lds);
+        launch(KT<PHX_Q4_0_DEV>::fn, grid, block, (uint32_t)lds, st, a);
+    } else {
+        raise_lds(KT<PHX_Q8_0_DEV>::fn, lds);
+        launch(KT<PHX_Q8_0_DEV>::fn, grid, block, (uint32_t)lds, st, a);
+    }
+}
+template <int T> struct KGu { static constexpr auto fn = k_dec_gu<T>; };
+template <int T> struct KDown { static constexpr auto fn = k_dec_down<T>; };
 
 void launch_dec_route(hipStream_t st, const DecLayerH& h)
 {
-    const DecArgs a = dec_args(h);
-    const int nsh = h.sgu ? (h.T + DROWS - 1) / DROWS * a.sgu.rg : 0;
-    const dim3 grid(h.T * h.E + nsh), block(nt_route(h));
-    const size_t lds = route_lds(h);
-    if (h.gu->type == PHX_Q4_0_DEV) {
-        raise_lds(k_dec_route<PHX_Q4_0_DEV>, lds);
-        launch(k_dec_route<PHX_Q4_0_DEV>, grid, block, (uint32_t)lds, st, a);
-    } else {
-        raise_lds(k_dec_route<PHX_Q8_0_DEV>, lds);
-        launch(k_dec_route<PHX_Q8_0_DEV>, grid, block, (uint32_t)lds, st, a);
-    }
+    launch(k_dec_route, dim3(h.T * h.E), dim3(h.d / 4), 0, st, dec_args(h));
 }
 
 void launch_dec_gu(hipStream_t st, const DecLayerH& h)
 {
-    const DecArgs a = dec_args(h);
-    const int nsh = h.sdn ? (h.T + DROWS - 1) / DROWS * a.sdn.rg : 0;
-    const dim3 grid(h.max_tiles * a.gu.rg + nsh), block(nt_gu(h));
-    const size_t lds = gu_lds(h);
-    if (h.gu->type == PHX_Q4_0_DEV) {
-        raise_lds(k_dec_gu<PHX_Q4_0_DEV>, lds);
-        launch(k_dec_gu<PHX_Q4_0_DEV>, grid, block, (uint32_t)lds, st, a);
-    } else {
-        raise_lds(k_dec_gu<PHX_Q8_0_DEV>, lds);
-        launch(k_dec_gu<PHX_Q8_0_DEV>, grid, block, (uint32_t)lds, st, a);
-    }
+    const int nsh = h.sgu ? (h.T + DROWS - 1) / DROWS * h.sgu->rg : 0;
+    launch_typed<KGu>(h, dim3(h.max_tiles * h.gu->rg + nsh), dim3(nt_gu(h)), gu_lds(h), st, dec_args(h));
 }
 
 void launch_dec_down(hipStream_t st, const DecLayerH& h)
 {
-    const DecArgs a = dec_args(h);
-    const dim3 grid(h.max_tiles * a.dn.rg), block(64 * waves_for(h.dn->nb));
-    const size_t lds = down_lds(h);
-    if (h.gu->type == PHX_Q4_0_DEV) {
-        raise_lds(k_dec_down<PHX_Q4_0_DEV>, lds);
-        launch(k_dec_down<PHX_Q4_0_DEV>, grid, block, (uint32_t)lds, st, a);
-    } else {
-        raise_lds(k_dec_down<PHX_Q8_0_DEV>, lds);
-        launch(k_dec_down<PHX_Q8_0_DEV>, grid, block, (uint32_t)lds, st, a);
-    }
+    const int rpw = rpw_down(h), nrgb = (h.dn->rg + rpw - 1) / rpw;
+    const int nsh = h.sdn ? (h.T + DROWS - 1) / DROWS * h.sdn->rg : 0;
+    launch_typed<KDown>(h, dim3(h.max_tiles * nrgb + nsh), dim3(64 * nw_down(h)), down_lds(h), st, dec_args(h));
 }
 
 void launch_dec_combine(hipStream_t st, const DecLayerH& h)
 {
-    const DecArgs a = dec_args(h);
-    launch(k_dec_combine, dim3(h.T), dim3(CB_NT), (uint32_t)((size_t)2 * h.d * 4), st, a);
+    launch(k_dec_combine, dim3(h.T), dim3(CB_NT), (uint32_t)((size_t)2 * h.d * 4), st, dec_args(h));
 }
 
 }  // namespace phx

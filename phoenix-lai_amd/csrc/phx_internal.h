@@ -115,7 +115,7 @@ struct DecLayerH {
     int *ids, *offsets, *perm, *flags;
     float *w, *logits, *g, *u, *yd, *shg, *shu, *shout, *out, *xres;
     DecTile* tiles;
-    Act adn, asd;
+    Act agu, ash, adn, asd;  // packed Q8_0 rows: expert and shared inputs [T], down inputs [T*k], [T]
     const float* gelu_tab;
 };
 bool dec_supported(const DecLayerH& h);

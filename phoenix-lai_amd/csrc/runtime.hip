@@ -314,7 +314,7 @@ int hip_code(hipError_t e)
 enum WsId {
     W_X, W_SHARED, W_OUT, W_RIN, W_XSCALE, W_AGU_Q, W_AGU_D, W_AGU_S, W_ASH_Q, W_ASH_D, W_ASH_S, W_LOGITS, W_IDS, W_W,
     W_OFF, W_PERM, W_TILES, W_NTILES, W_G, W_U, W_ADN_Q, W_ADN_D, W_ADN_S, W_YD, W_SHG, W_SHU, W_ASD_Q, W_ASD_D,
-    W_ASD_S, W_SHOUT, W_ZERO, W_STILES, W_SNTILES, W_SOFF, W_SPERM, W_LB, W_BB, W_ADEC, W_SDEC, W_COUNT
+    W_ASD_S, W_SHOUT, W_ZERO, W_STILES, W_SNTILES, W_SOFF, W_SPERM, W_LB, W_BB, W_ADEC, W_SDEC, W_AGUP, W_ASHP, W_COUNT
 };
 
 int ensure(phx_moe_ctx* c, int id, size_t bytes)
@@ -426,6 +426,8 @@ int ensure_workspace(phx_moe_ctx* c, const Layer& L, int T)
     }
     ENS(W_TILES, (size_t)((n + 1) / 2 + D.n_expert) * sizeof(DecTile));
     ENS(W_ADEC, (size_t)n * (D.down_cols / 32) * 40);
+    ENS(W_AGUP, (size_t)T * (D.d / 32) * 40);
+    if (D.n_ff_shared > 0) ENS(W_ASHP, (size_t)T * (D.d / 32) * 40);
     if (D.n_ff_shared > 0) ENS(W_SDEC, (size_t)T * (D.n_ff_shared / 32) * 40);
 #undef ENS
     return PHX_OK;
@@ -517,11 +519,13 @@ DecLayerH dec_layer(phx_moe_ctx* c, const Layer& L, int T, const float* x, const
         h.yd = wp<float>(c, W_YD);
         h.tiles = wp<DecTile>(c, W_TILES);
         h.adn = make_act_packed(c, D.down_cols, W_ADEC);
+        h.agu = make_act_packed(c, D.d, W_AGUP);
         if (shared_ffn) {
             h.shg = wp<float>(c, W_SHG);
             h.shu = wp<float>(c, W_SHU);
             h.shout = wp<float>(c, W_SHOUT);
             h.asd = make_act_packed(c, D.n_ff_shared, W_SDEC);
+            h.ash = make_act_packed(c, D.d, W_ASHP);
         }
     }
     return h;
