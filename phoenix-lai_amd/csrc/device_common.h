@@ -143,6 +143,15 @@ __device__ __forceinline__ double wave_sum_dpp(double v)
     return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
 }
 
+// Float sum over the 64 lanes (the same tree as wave_sum_dpp), returned to every lane.
+__device__ __forceinline__ float wave_sum_f(float v)
+{
+    v = row_sum(v);
+    v += dpp_f<0x142, 0xa>(0.0f, v);
+    v += dpp_f<0x143, 0xc>(0.0f, v);
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 // Sum / max over each 32-lane half (lanes 0-31 and 32-63), returned to the lanes of that half.
 __device__ __forceinline__ int half_sum_i(int v)
 {

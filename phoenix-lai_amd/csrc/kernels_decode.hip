@@ -401,89 +401,159 @@ typedef __attribute__((address_space(3))) void* lds_void_t;
 typedef __attribute__((address_space(1))) void* glb_void_t;
 
 // ------------------------------------------------------------------------------ k_dec_route
-// One workgroup per (token t, expert e), d / 4 threads: thread i holds elements 4i..4i+3.  The
-// reference logit is the sequential float sum of the rounded products p_i = fl(W[e][i] * m_i),
-// m_i = ((x_i * rinv) * sc) * s_i (src/GemmaCpu.cs:389-395).  The workgroup forms the same p_i, sums
-// them in double (L), and bounds the reference's accumulated rounding by
+// One workgroup of 256 threads per (token t, expert e); thread i holds the PER = d / 256 consecutive
+// elements PER*i..PER*i+PER-1 (x_t, the router scale and W[e] staged in LDS by direct global -> LDS
+// loads; an odd PER reads LDS without bank conflicts).  The reference logit is the sequential float sum
+// of the rounded products p_i = fl(W[e][i] * m_i), m_i = ((x_i * rinv) * sc) * s_i
+// (src/GemmaCpu.cs:389-395).  The workgroup forms the same p_i, sums them in double (L, from a scan of
+// the chunk sums), and bounds the reference's accumulated rounding by
 //   |S_ref - L| <= 2^-24 * sum_k |S_k| * 1.001 + 2^-45 * sum_i |p_i|,
-// S_k the prefix sums (a scan over the threads), the second term covering the double arithmetic.
-// k_dec_gu ranks the experts by L and certifies the order from these intervals.  The workgroup also
-// writes the Q8_0 expert input n = (x * rinv) * pre_ffw_norm_2 (src/GemmaCpu.cs:409) of the 32-blocks b
-// with b % E == e: the 8 threads of block b hold its 32 values.
-__global__ __launch_bounds__(1024) void k_dec_route(DecArgs a)
+// S_k the prefix sums; sum_k |S_k| and sum_i |p_i| are accumulated in float and enlarged by 2^-10 (far
+// above their float rounding, so the bound still holds).  k_dec_gu ranks the experts by L and
+// certifies the order from these intervals.  The workgroup also writes the Q8_0 expert input
+// n = (x * rinv) * pre_ffw_norm_2 (src/GemmaCpu.cs:409) and the shared-FFN input (x * rinv) * ffn_norm
+// (:349) of the 32-blocks b with b % E == e, one 8-lane group per block.
+constexpr int RT_NT = 256;
+
+template <int PER>
+__device__ void route_wg(const DecArgs& a, int t, int e, float* sx, float* sg, float* sw)
 {
-    __shared__ double red[17], wsum[16], wA[16], wP[16];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, NWV = blockDim.x >> 6, d = a.d;
-    const int t = blockIdx.x / a.E, e = blockIdx.x % a.E;
+    __shared__ double red[5], wsum[4];
+    __shared__ float wA[4], wP[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, d = a.d;
     const float* xr = a.x + (int64_t)t * d;
-    const float4 xv = ((const float4*)xr)[tid];
-    const float4 gv = ((const float4*)a.gis)[tid];
-    const float4 wv = ((const float4*)(a.W + (int64_t)e * d))[tid];
-    const float4 nv = ((const float4*)a.pre2)[tid];
-    const float4 fv = a.ash.q ? ((const float4*)a.fnorm)[tid] : nv;
-    const double s2 = ((double)xv.x * (double)xv.x + (double)xv.y * (double)xv.y) +
-                      ((double)xv.z * (double)xv.z + (double)xv.w * (double)xv.w);
-    const float rinv = rms_scale_from_mean(wg_mean_sq(s2, xr, d, red, (t == 0 && e == 0) ? a.flags : nullptr), a.eps);
+    {
+        const int n4 = d / 4;
+        auto stage = [&](const float* src, float* dst) {
+            for (int q = 0; q * RT_NT < n4; q++) {
+                const int i = q * RT_NT + tid;
+                if (i < n4)
+                    __builtin_amdgcn_global_load_lds((glb_void_t)((const float4*)src + i),
+                                                     (lds_void_t)((float4*)dst + q * RT_NT + wave * 64), 16, 0, 0);
+            }
+        };
+        stage(xr, sx);
+        stage(a.gis, sg);
+        stage(a.W + (int64_t)e * d, sw);
+        __builtin_amdgcn_s_waitcnt(0);
+    }
+    __syncthreads();
+    const int c0 = tid * PER;
+    float xv[PER], pv[PER];
+    double s2 = 0.0;
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        xv[j] = sx[c0 + j];
+        s2 += (double)xv[j] * (double)xv[j];
+    }
+    // the RmsNorm scale: wave sums, then the four wave totals in a fixed order
+    s2 = wave_sum_dpp(s2);
+    if (lane == 0) red[wave] = s2;
+    __syncthreads();
+    const double S = (red[0] + red[1]) + (red[2] + red[3]);
+    const double Bs = ((double)d + 64.0) * 0x1p-52 * S;
+    float mean = (float)((S - Bs) / (double)d);
+    if (mean != (float)((S + Bs) / (double)d)) {  // uniform: S is the same in every thread
+        if (tid == 0) {
+            double q = 0.0;
+            for (int i = 0; i < d; i++) q += (double)sx[i] * (double)sx[i];
+            red[4] = q;
+            if (t == 0 && e == 0) atomicAdd(&a.flags[0], 1);
+        }
+        __syncthreads();
+        mean = (float)(red[4] / (double)d);
+    }
+    const float rinv = rms_scale_from_mean(mean, a.eps);
     const float sc = 1.0f / (float)__dsqrt_rn((double)d);
-    const float p0 = wv.x * (xv.x * rinv * sc * gv.x), p1 = wv.y * (xv.y * rinv * sc * gv.y),
-                p2 = wv.z * (xv.z * rinv * sc * gv.z), p3 = wv.w * (xv.w * rinv * sc * gv.w);
-    const double q0 = p0, q1 = p1, q2 = p2, q3 = p3;
-    const double loc = ((q0 + q1) + q2) + q3;
-    double P = (fabs(q0) + fabs(q1)) + (fabs(q2) + fabs(q3));
+    double loc = 0.0;
+    float Pf = 0.0f;
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        pv[j] = sw[c0 + j] * (xv[j] * rinv * sc * sg[c0 + j]);
+        loc += (double)pv[j];
+        Pf += fabsf(pv[j]);
+    }
     const double inc = wave_incl_scan_dpp(loc);
     if (lane == 63) wsum[wave] = inc;
     __syncthreads();
-    const double base = wave_sum_dpp(lane < wave ? wsum[lane] : 0.0);  // the earlier waves' totals
+    double base = 0.0;
+    if (wave > 0) base += wsum[0];
+    if (wave > 1) base += wsum[1];
+    if (wave > 2) base += wsum[2];
     double acc = base + (inc - loc);  // exclusive prefix (within the double slack of the bound)
-    double A;
-    acc += q0;
-    A = fabs(acc);
-    acc += q1;
-    A += fabs(acc);
-    acc += q2;
-    A += fabs(acc);
-    acc += q3;
-    A += fabs(acc);
-    A = wave_sum_dpp(A);
-    P = wave_sum_dpp(P);
-    if (lane == 0) {
-        wA[wave] = A;
-        wP[wave] = P;
+    float Af = 0.0f;
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        acc += (double)pv[j];
+        Af += fabsf((float)acc);
     }
-    // the expert input blocks of this workgroup (uniform per 8-lane group)
-    const int b = tid >> 3;
-    if (b % a.E == e) {
-        const float4 v = make_float4((xv.x * rinv) * nv.x, (xv.y * rinv) * nv.y, (xv.z * rinv) * nv.z,
-                                     (xv.w * rinv) * nv.w);
+    Af = wave_sum_f(Af);
+    Pf = wave_sum_f(Pf);
+    if (lane == 0) {
+        wA[wave] = Af;
+        wP[wave] = Pf;
+    }
+    // the expert and shared-FFN input blocks of this workgroup (8 threads per block)
+    const int nb = d / 32, g = tid >> 3, l8 = tid & 7, b = e + g * a.E;
+    if (b < nb) {
+        const float4 xq = *(const float4*)(sx + 32 * b + 4 * l8);
+        const float4 nv = ((const float4*)a.pre2)[8 * b + l8];
         float dval;
         int sum;
-        const int qw = q8_0_oct(v, &dval, &sum);
-        ((int*)(a.agu.q + (int64_t)t * a.agu.qstride))[tid] = qw;
-        if ((tid & 7) == 0) {
+        const int qw = q8_0_oct(make_float4((xq.x * rinv) * nv.x, (xq.y * rinv) * nv.y, (xq.z * rinv) * nv.z,
+                                            (xq.w * rinv) * nv.w),
+                                &dval, &sum);
+        ((int*)(a.agu.q + (int64_t)t * a.agu.qstride))[8 * b + l8] = qw;
+        if (l8 == 0) {
             a.agu.d[(int64_t)t * a.agu.dstride + b] = dval;
             a.agu.s[(int64_t)t * a.agu.sstride + b] = sum;
         }
-        if (a.ash.q) {  // the shared FFN input (x * rinv) * ffn_norm (src/GemmaCpu.cs:349)
-            const float4 u = make_float4((xv.x * rinv) * fv.x, (xv.y * rinv) * fv.y, (xv.z * rinv) * fv.z,
-                                         (xv.w * rinv) * fv.w);
-            const int qs = q8_0_oct(u, &dval, &sum);
-            ((int*)(a.ash.q + (int64_t)t * a.ash.qstride))[tid] = qs;
-            if ((tid & 7) == 0) {
+        if (a.ash.q) {
+            const float4 fv = ((const float4*)a.fnorm)[8 * b + l8];
+            const int qs = q8_0_oct(make_float4((xq.x * rinv) * fv.x, (xq.y * rinv) * fv.y, (xq.z * rinv) * fv.z,
+                                                (xq.w * rinv) * fv.w),
+                                    &dval, &sum);
+            ((int*)(a.ash.q + (int64_t)t * a.ash.qstride))[8 * b + l8] = qs;
+            if (l8 == 0) {
                 a.ash.d[(int64_t)t * a.ash.dstride + b] = dval;
                 a.ash.s[(int64_t)t * a.ash.sstride + b] = sum;
             }
         }
     }
     __syncthreads();
-    if (wave == 0) {
-        const bool in = lane < NWV;
-        const double L = wave_sum_dpp(in ? wsum[lane] : 0.0);
-        const double As = wave_sum_dpp(in ? wA[lane] : 0.0);
-        const double Ps = wave_sum_dpp(in ? wP[lane] : 0.0);
-        if (lane == 0) {
-            a.Lb[(int64_t)t * a.E + e] = L;
-            a.Bb[(int64_t)t * a.E + e] = 0x1p-24 * As * 1.001 + 0x1p-45 * Ps;
-        }
+    if (tid == 0) {
+        const double L = ((wsum[0] + wsum[1]) + wsum[2]) + wsum[3];
+        const double As = (double)((wA[0] + wA[1]) + (wA[2] + wA[3])) * (1.0 + 0x1p-10);
+        const double Ps = (double)((wP[0] + wP[1]) + (wP[2] + wP[3])) * (1.0 + 0x1p-10);
+        a.Lb[(int64_t)t * a.E + e] = L;
+        a.Bb[(int64_t)t * a.E + e] = 0x1p-24 * As * 1.001 + 0x1p-45 * Ps;
+    }
+}
+
+__global__ __launch_bounds__(RT_NT) void k_dec_route(DecArgs a)
+{
+    extern __shared__ __align__(16) float rsm[];  // x, router scale, W row: 3 * (d + 4) floats
+    const int t = blockIdx.x / a.E, e = blockIdx.x % a.E, d = a.d;
+    float* sx = rsm;
+    float* sg = sx + d + 4;
+    float* sw = sg + d + 4;
+    switch (d / RT_NT) {
+    case 1: route_wg<1>(a, t, e, sx, sg, sw); break;
+    case 2: route_wg<2>(a, t, e, sx, sg, sw); break;
+    case 3: route_wg<3>(a, t, e, sx, sg, sw); break;
+    case 4: route_wg<4>(a, t, e, sx, sg, sw); break;
+    case 5: route_wg<5>(a, t, e, sx, sg, sw); break;
+    case 6: route_wg<6>(a, t, e, sx, sg, sw); break;
+    case 7: route_wg<7>(a, t, e, sx, sg, sw); break;
+    case 8: route_wg<8>(a, t, e, sx, sg, sw); break;
+    case 9: route_wg<9>(a, t, e, sx, sg, sw); break;
+    case 10: route_wg<10>(a, t, e, sx, sg, sw); break;
+    case 11: route_wg<11>(a, t, e, sx, sg, sw); break;
+    case 12: route_wg<12>(a, t, e, sx, sg, sw); break;
+    case 13: route_wg<13>(a, t, e, sx, sg, sw); break;
+    case 14: route_wg<14>(a, t, e, sx, sg, sw); break;
+    case 15: route_wg<15>(a, t, e, sx, sg, sw); break;
+    default: route_wg<16>(a, t, e, sx, sg, sw); break;
     }
 }
 
@@ -529,77 +599,96 @@ __device__ void shared_dn_wg(const DecArgs& a, int tile, int rgi, unsigned char*
 }
 
 // ------------------------------------------------------------------------------ k_dec_gu
-// Selection, in every expert workgroup.  Fast path, one wave per token: the experts' 32-bit keys (the
-// order-preserving bits of (float)L with the low 8 bits replaced by 255 - expert, so keys are
-// distinct and ties go to the lower index) and k rounds of a wave maximum give the top-k.  The order
-// is certified if each chosen expert's lower end L - B lies above the upper ends L + B of every expert
-// ranked after it; an order the key gets wrong (logits within 256 float ulps) is never certified,
-// since certification compares the intervals themselves.  When a token is not certified, the whole
-// workgroup takes select_exact.
-__device__ __forceinline__ double readlane_d(double v, int l)
+// Selection, in every expert workgroup and in the routing workgroup.  Fast path, one wave per token:
+// the experts' 32-bit keys (the order-preserving bits of (float)L with the low 8 bits replaced by
+// 255 - expert, so keys are distinct and ties go to the lower index) and k rounds of a wave maximum
+// give the top-k.  The order is certified if each chosen expert's lower end L - B lies above the
+// upper ends L + B of every expert ranked after it, compared as floats rounded outward (so a float
+// comparison that holds implies the exact one); an order the key gets wrong (logits within 256 float
+// ulps) is never certified, since certification compares the intervals themselves.  When a token is
+// not certified, the whole workgroup takes select_exact.
+__device__ __forceinline__ float f32_down(double v)  // the largest float <= v
 {
-    const long long b = __double_as_longlong(v);
-    const int lo = __builtin_amdgcn_readlane((int)b, l), hi = __builtin_amdgcn_readlane((int)(b >> 32), l);
-    return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+    const float f = (float)v;
+    if (!((double)f > v)) return f;
+    if (f == 0.0f) return -__uint_as_float(1u);  // below zero: minus the smallest subnormal
+    const unsigned b = __float_as_uint(f);
+    return __uint_as_float(f > 0.0f ? b - 1u : b + 1u);
 }
 
-__device__ bool wave_topk(const DecArgs& a, int t, int* s_ids)
+__device__ __forceinline__ float f32_up(double v)  // the smallest float >= v
+{
+    const float f = (float)v;
+    if (!((double)f < v)) return f;
+    if (f == 0.0f) return __uint_as_float(1u);
+    const unsigned b = __float_as_uint(f);
+    return __uint_as_float(f > 0.0f ? b + 1u : b - 1u);
+}
+
+__device__ bool wave_topk(const DecArgs& a, int t, int* s_ids, unsigned* s_klo, unsigned* s_khi)
 {
     const int lane = threadIdx.x & 63;
     const double* Lr = a.Lb + (int64_t)t * a.E;
     const double* Br = a.Bb + (int64_t)t * a.E;
     double L[4], B[4];
-    unsigned key[4];
 #pragma unroll
     for (int q = 0; q < 4; q++) {
         const int ex = min(lane + 64 * q, a.E - 1);
         L[q] = Lr[ex];
         B[q] = Br[ex];
     }
+    unsigned key[4], klo[4], khi[4];
+    int rank[4];
     bool fin = true;
 #pragma unroll
     for (int q = 0; q < 4; q++) {
         const int ex = lane + 64 * q;
-        key[q] = ex < a.E ? (sortable_f32((float)L[q]) & ~0xFFu) | (unsigned)(255 - ex) : 0u;
-        if (ex < a.E && !(isfinite(L[q]) && isfinite(B[q]))) fin = false;
+        const bool valid = ex < a.E;
+        const bool f = isfinite(L[q]) && isfinite(B[q]);
+        if (valid && !f) fin = false;
+        key[q] = valid ? (sortable_f32((float)L[q]) & ~0xFFu) | (unsigned)(255 - ex) : 0u;
+        klo[q] = f ? sortable_f32(f32_down(L[q] - B[q])) : 0u;
+        khi[q] = f ? sortable_f32(f32_up(L[q] + B[q])) : 0xFFFFFFFFu;
+        rank[q] = 64;
     }
-    // k rounds of the wave maximum: the winner's slot leaves the candidates; rank j's interval is read
-    // from the owning lane (a uniform index) and kept in lane j
-    double lo_mine = INFINITY, hi_mine = -INFINITY;
-    int id_mine = 0;
+    const int nq = (a.E + 63) / 64;
     for (int j = 0; j < a.k; j++) {
-        const unsigned m = wave_max_u32(max(max(key[0], key[1]), max(key[2], key[3])));
-        const int ex = 255 - (int)(m & 0xFFu), owner = ex & 63, qo = ex >> 6;
-        double lo = 0.0, hi = 0.0;
+        unsigned m = key[0];
+        if (nq > 1) m = max(m, key[1]);
+        if (nq > 2) m = max(m, max(key[2], key[3]));
+        m = wave_max_u32(m);
 #pragma unroll
         for (int q = 0; q < 4; q++)
-            if (q == qo) {
-                if (lane == owner) key[q] = 0u;
-                lo = readlane_d(L[q] - B[q], owner);
-                hi = readlane_d(L[q] + B[q], owner);
+            if (key[q] == m) {  // the keys are distinct and nonzero: one slot of one lane
+                key[q] = 0u;
+                rank[q] = j;
             }
-        if (lane == j) {
-            lo_mine = lo;
-            hi_mine = hi;
-            id_mine = ex;
+    }
+    unsigned hun = 0u;  // the unchosen experts' highest upper end
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const int ex = lane + 64 * q;
+        if (rank[q] < 64) {
+            s_klo[rank[q]] = klo[q];
+            s_khi[rank[q]] = khi[q];
+            s_ids[t * a.k + rank[q]] = ex;
+        } else if (ex < a.E) {
+            hun = max(hun, khi[q]);
         }
     }
-    // the unchosen experts' highest upper end (chosen slots hold key 0)
-    double hun = -INFINITY;
+    hun = wave_max_u32(hun);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // lane j < k: its lower end must lie above every later rank's upper end and the unchosen ones'
+    unsigned later = hun;
 #pragma unroll
-    for (int q = 0; q < 4; q++)
-        if (lane + 64 * q < a.E && key[q] != 0u) hun = fmax(hun, L[q] + B[q]);
-    hun = wave_max_dpp(hun);
-    // certified iff, from the last rank down, each lower end exceeds every later upper end
-    bool cert = __all(fin);
-    double later = hun;
-    for (int j = a.k - 1; j >= 0; j--) {
-        const double loj = readlane_d(lo_mine, j), hij = readlane_d(hi_mine, j);
-        cert = cert && loj > later;
-        later = fmax(later, hij);
+    for (int r = 0; r < PHX_MAX_USED_DEV; r++) {
+        const unsigned h = s_khi[r];
+        if (r > lane && r < a.k) later = max(later, h);
     }
-    if (lane < a.k) s_ids[t * a.k + lane] = id_mine;
-    return cert;
+    const bool ok = lane >= a.k || s_klo[lane] > later;
+    return __all(fin && ok);
 }
 
 // Exact selection for the tokens marked in s_bad (rare): the experts that can reach the chosen ones
@@ -772,10 +861,12 @@ __device__ void expert_gu_wg(const DecArgs& a, unsigned char* smem)
     int* s_misc = (int*)(s_tiles + 272);        // [0] ntiles, [1] any uncertified, [2..17] bad per token
     int* wtot = s_misc + 20;                    // 32
     double* red = (double*)(wtot + 32);         // 17
+    unsigned* s_kb = (unsigned*)(red + 17);     // [waves][2][16] selection bounds
+    const bool routing = blockIdx.x == gridDim.x - 1;  // the routing workgroup: outputs, no tile
     if (tid == 0) s_misc[1] = 0;
     __syncthreads();
     for (int t = wave; t < a.T; t += NWV) {
-        const bool cert = wave_topk(a, t, s_ids);
+        const bool cert = wave_topk(a, t, s_ids, s_kb + wave * 32, s_kb + wave * 32 + 16);
         if (lane == 0) {
             s_misc[2 + t] = !cert;
             if (!cert) s_misc[1] = 1;
@@ -787,13 +878,13 @@ __device__ void expert_gu_wg(const DecArgs& a, unsigned char* smem)
     if (exact) {
         char* samb = (char*)(sL + TE);
         short* srank = (short*)(samb + TE);
-        select_exact(a, sL, samb, srank, s_ids, s_misc + 2, red, blockIdx.x == 0);
+        select_exact(a, sL, samb, srank, s_ids, s_misc + 2, red, routing);
     }
     int ntiles;
     if (a.T == 1) {
         // one token: tile j is assignment j (the k experts are distinct)
         if (tid < a.k) s_tiles[tid] = DecTile{s_ids[tid], 1, {tid, 0}};
-        if (blockIdx.x == 0) {
+        if (routing) {
             // expert lists: rank of assignment tid in ascending expert order; offsets by counting
             if (tid < a.k) {
                 const int e = s_ids[tid];
@@ -813,13 +904,14 @@ __device__ void expert_gu_wg(const DecArgs& a, unsigned char* smem)
         build_tiles(a, s_ids, s_cnt, s_off, s_tb, s_perm, s_tiles, s_misc, wtot);
         ntiles = s_misc[0];
     }
-    if (blockIdx.x == 0) {
+    if (routing) {
         const double* Lg = a.Lb;
         const int* bad = s_misc + 2;
         const int E = a.E;
         write_routing(
             a, [&](int t, int e) { return (exact && bad[t]) ? sL[t * E + e] : Lg[(int64_t)t * E + e]; }, s_ids, s_off,
             s_perm, s_tiles, ntiles);
+        return;
     }
     const int tile = blockIdx.x / a.gu.rg, rgi = blockIdx.x % a.gu.rg;
     if (tile >= ntiles) return;  // uniform: no barriers follow for this workgroup
@@ -843,8 +935,8 @@ __global__ __launch_bounds__(1024) void k_dec_gu(DecArgs a)
 {
     extern __shared__ __align__(16) unsigned char dsm[];
     const int ne = a.max_tiles * a.gu.rg;
-    if ((int)blockIdx.x < ne) {
-        expert_gu_wg<TYPE>(a, dsm);
+    if ((int)blockIdx.x < ne || (int)blockIdx.x == (int)gridDim.x - 1) {
+        expert_gu_wg<TYPE>(a, dsm);  // an expert tile, or (the last workgroup) the routing outputs
     } else {
         const int s = blockIdx.x - ne;
         shared_gu_wg<TYPE>(a, s / a.sgu.rg, s % a.sgu.rg, dsm);
@@ -1062,7 +1154,8 @@ static size_t gu_lds(const DecLayerH& h)
 {
     const size_t TE = (size_t)h.T * h.E;
     const size_t un = (std::max((size_t)DROWS * h.gu->nb * 64 * 4, TE * 11) + 15) & ~(size_t)15;
-    const size_t ex = un + sizeof(ActL) * DROWS + (256 * 2 + 260 * 3) * 4 + 272 * sizeof(DecTile) + (20 + 32) * 4 + 17 * 8;
+    const size_t ex = un + sizeof(ActL) * DROWS + (256 * 2 + 260 * 3) * 4 + 272 * sizeof(DecTile) + (20 + 32) * 4 + 17 * 8 +
+                      16 * 32 * 4;
     const size_t sh = h.sgu ? sizeof(ActL) * DROWS + (size_t)DROWS * h.sgu->nb * 64 * 4 : 0;
     return std::max(ex, sh);
 }
@@ -1082,7 +1175,7 @@ static void raise_lds(K kernel, size_t bytes)
 
 bool dec_supported(const DecLayerH& h)
 {
-    if (h.d > 4096 || h.d % 256 || h.gu->nb > DMAXNB || h.dn->nb > DMAXNB || h.E > 256 || h.T * h.k > 256) return false;
+    if (h.d > 4096 || h.d % 256 || h.gu->nb > DMAXNB || h.gu->nb > 32 * h.E || h.dn->nb > DMAXNB || h.E > 256 || h.T * h.k > 256) return false;
     if (h.sgu && (h.sgu->nb > DMAXNB || h.sdn->nb > DMAXNB)) return false;
     if (nt_gu(h) < std::max(h.E, h.T * h.k)) return false;  // build_tiles: a thread per expert and assignment
     return gu_lds(h) <= 160 * 1024 && down_lds(h) <= 160 * 1024;
@@ -1104,13 +1197,13 @@ template <int T> struct KDown { static constexpr auto fn = k_dec_down<T>; };
 
 void launch_dec_route(hipStream_t st, const DecLayerH& h)
 {
-    launch(k_dec_route, dim3(h.T * h.E), dim3(h.d / 4), 0, st, dec_args(h));
+    launch(k_dec_route, dim3(h.T * h.E), dim3(RT_NT), (uint32_t)((size_t)3 * (h.d + 4) * 4), st, dec_args(h));
 }
 
 void launch_dec_gu(hipStream_t st, const DecLayerH& h)
 {
     const int nsh = h.sgu ? (h.T + DROWS - 1) / DROWS * h.sgu->rg : 0;
-    launch_typed<KGu>(h, dim3(h.max_tiles * h.gu->rg + nsh), dim3(nt_gu(h)), gu_lds(h), st, dec_args(h));
+    launch_typed<KGu>(h, dim3(h.max_tiles * h.gu->rg + nsh + 1), dim3(nt_gu(h)), gu_lds(h), st, dec_args(h));
 }
 
 void launch_dec_down(hipStream_t st, const DecLayerH& h)
