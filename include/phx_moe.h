@@ -54,7 +54,8 @@ extern "C" {
 /* phx_moe_ffn flags */
 #define PHX_FLAG_DEVICE_PTRS 1u /* x, shared, out are device pointers (no PCIe copies) */
 #define PHX_FLAG_ASYNC 2u       /* return after enqueueing; phx_moe_sync waits */
-#define PHX_FLAG_RESIDUAL 4u    /* also x += rmsnorm(out) * post_ffw_norm (src/GemmaCpu.cs:355-356); x is updated in place */
+#define PHX_FLAG_RESIDUAL 4u    /* also x += rmsnorm(out) * post_ffw_norm (src/GemmaCpu.cs:355-356); x is updated in place
+                                   and out must not be x */
 #define PHX_FLAG_EXACT_ROUTER 8u /* replay the reference's float router sums for every token (outputs bit-exact
                                     to the CPU reference) instead of the certified decode router */
 

@@ -309,7 +309,7 @@ void launch_dispatch(hipStream_t st, int n, int E, int A, const int* ids, int* o
 struct GroupArgs {
     const uint8_t* payload;
     const uint8_t* scale;
-    int64_t mat_pay, mat_sc;
+    int64_t mat_pay, mat_sc, rg_pay;
     int rg, nb, rows;
     Act act;
     const Tile* tiles;
@@ -348,7 +348,7 @@ __global__ __launch_bounds__(256) void k_grouped_q(GroupArgs g)
     const int rgi = blockIdx.y * 4 + wave;
     if (rgi >= g.rg) return;
     constexpr int PAY = TYPE == PHX_Q4_0_DEV ? 16 : 32;
-    const uint8_t* wp = g.payload + tl.e * g.mat_pay + ((int64_t)rgi * g.nb * 64 + lane) * PAY;
+    const uint8_t* wp = g.payload + tl.e * g.mat_pay + rgi * g.rg_pay + lane * PAY;
     const uint16_t* ws = (const uint16_t*)(g.scale + tl.e * g.mat_sc) + (int64_t)rgi * g.nb * 64 + lane;
     int arow[A];
     float acc[A];
@@ -409,7 +409,7 @@ __global__ __launch_bounds__(256) void k_grouped_k(GroupArgs g)
     if (rgi >= g.rg) return;
     constexpr bool Q4K = TYPE == PHX_Q4_K_DEV;
     constexpr int PAY = Q4K ? 144 : 208;
-    const uint8_t* wp = g.payload + tl.e * g.mat_pay + ((int64_t)rgi * g.nb * 64 + lane) * PAY;
+    const uint8_t* wp = g.payload + tl.e * g.mat_pay + rgi * g.rg_pay + lane * PAY;
     const uint8_t* wsb = g.scale + tl.e * g.mat_sc + ((int64_t)rgi * g.nb * 64 + lane) * (Q4K ? 4 : 2);
     int arow[A];
     float sums[A][8], sumf[A];
@@ -526,6 +526,7 @@ void launch_grouped(hipStream_t st, const QMat& w, Act act, const Tile* tiles, c
     g.payload = w.payload;
     g.scale = w.scale;
     g.mat_pay = w.mat_pay_stride();
+    g.rg_pay = w.rg_pay;
     g.mat_sc = w.mat_sc_stride();
     g.rg = w.rg;
     g.nb = w.nb;

@@ -38,12 +38,13 @@ struct DecCfg {
     static constexpr int NC = PAY / 16;                         // 16 B loads per block
 };
 
-// decode-layout view of one matrix stack (QMat): payload [m][rg][b][64][PAY], scales [m][rg][b/8][64][8]
+// decode-layout view of one matrix stack (QMat): row group rg of matrix m at pay + m * mat_pay +
+// rg * rg_pay holds the blocks [b][64][PAY], then at sc_off the scale groups [b/8][64][8] fp16
 struct MatD {
     const uint8_t* pay;
-    const uint4* sc8;
     int64_t mat_pay;  // bytes per matrix
-    int64_t mat_sc8;  // uint4 per matrix
+    int64_t rg_pay;   // bytes per row group
+    int64_t sc_off;   // scale groups within a row group
     int rg, nb, nb8, rows;
 };
 
@@ -159,6 +160,49 @@ __device__ float wg_mean_sq(double s, const float* xr, int n, double* red, int* 
     return mean;
 }
 
+// The means of squares of two rows in one reduction pass, each by the rule of wg_mean_sq (x1 may be
+// null when s1 is zero everywhere).  red holds 2 * (blockDim.x / 64 + 1) doubles.
+__device__ void wg_mean_sq2(double s0, double s1, const float* x0, const float* x1, int n, double* red,
+                            int* fallbacks, float* m0, float* m1)
+{
+    const int tid = threadIdx.x, lane = tid & 63, nw = blockDim.x >> 6;
+    double* red1 = red + nw + 1;
+    s0 = wave_sum_dpp(s0);
+    s1 = wave_sum_dpp(s1);
+    if (lane == 0) {
+        red[tid >> 6] = s0;
+        red1[tid >> 6] = s1;
+    }
+    __syncthreads();
+    const double S0 = wave_sum_dpp(lane < nw ? red[lane] : 0.0);
+    const double S1 = wave_sum_dpp(lane < nw ? red1[lane] : 0.0);
+    const double B0 = ((double)n + 64.0) * 0x1p-52 * S0, B1 = ((double)n + 64.0) * 0x1p-52 * S1;
+    float lo0 = (float)((S0 - B0) / (double)n), hi0 = (float)((S0 + B0) / (double)n);
+    float lo1 = (float)((S1 - B1) / (double)n), hi1 = (float)((S1 + B1) / (double)n);
+    if (lo0 != hi0 || lo1 != hi1) {  // uniform: every thread formed the same sums
+        if (tid == 0) {
+            if (lo0 != hi0) {
+                double q = 0.0;
+                for (int i = 0; i < n; i++) q += (double)x0[i] * (double)x0[i];
+                red[nw] = q;
+                if (fallbacks) atomicAdd(fallbacks, 1);
+            }
+            if (lo1 != hi1 && x1) {
+                double q = 0.0;
+                for (int i = 0; i < n; i++) q += (double)x1[i] * (double)x1[i];
+                red1[nw] = q;
+                if (fallbacks) atomicAdd(fallbacks, 1);
+            }
+        }
+        __syncthreads();
+        if (lo0 != hi0) lo0 = (float)(red[nw] / (double)n);
+        if (lo1 != hi1 && x1) lo1 = (float)(red1[nw] / (double)n);
+    }
+    *m0 = lo0;
+    *m1 = lo1;
+    __syncthreads();  // red is reused by the next call
+}
+
 // The Q8_0 input rows of a gate|up workgroup: n_i = (x_i * rinv) * nw_i (src/GemmaCpu.cs:409 with
 // CpuRef.RmsNorm, src/CpuRef.cs:183-191; the shared FFN: ffn_norm, :349), rinv the token's RmsNorm
 // scale, quantized per 32-block into act[r].  8-lane group g takes block g (the workgroup has at least
@@ -266,14 +310,15 @@ __device__ __forceinline__ void load_w(const MatD& M, int e, int rgi, int wave, 
     // unconditional: a wave past the row reloads the row's last blocks (no branch around the loads, so
     // the compiler's wait counts stay exact)
     const int b0 = min(wave * DBPW, (M.nb8 - 1) * DBPW);
-    const uint8_t* p = M.pay + (int64_t)e * M.mat_pay + ((int64_t)rgi * M.nb * 64 + lane) * PAY;
+    const uint8_t* rgp = M.pay + (int64_t)e * M.mat_pay + (int64_t)rgi * M.rg_pay;
+    const uint8_t* p = rgp + lane * PAY;
 #pragma unroll
     for (int j = 0; j < DBPW; j++) {
         const int b = min(b0 + j, M.nb - 1);
 #pragma unroll
         for (int c = 0; c < NC; c++) W.p[j][c] = *(const uint4*)(p + (int64_t)b * 64 * PAY + 16 * c);
     }
-    W.s = M.sc8[(int64_t)e * M.mat_sc8 + ((int64_t)rgi * M.nb8 + b0 / DBPW) * 64 + lane];
+    W.s = *(const uint4*)(rgp + M.sc_off + ((b0 / DBPW) * 64 + lane) * 16);
 }
 
 // fp16 scale bits of block j of a WRegs
@@ -422,6 +467,10 @@ __device__ void route_wg(const DecArgs& a, int t, int e, float* sx, float* sg, f
     __shared__ float wA[4], wP[4];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, d = a.d;
     const float* xr = a.x + (int64_t)t * d;
+    // the input blocks of this workgroup (8 threads per block): their norm weights, loaded now
+    const int nb = d / 32, g = tid >> 3, l8 = tid & 7, b = e + g * a.E, bc = min(b, nb - 1);
+    const float4 nv = ((const float4*)a.pre2)[8 * bc + l8];
+    const float4 fv = a.ash.q ? ((const float4*)a.fnorm)[8 * bc + l8] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     {
         const int n4 = d / 4;
         auto stage = [&](const float* src, float* dst) {
@@ -458,7 +507,7 @@ __device__ void route_wg(const DecArgs& a, int t, int e, float* sx, float* sg, f
             double q = 0.0;
             for (int i = 0; i < d; i++) q += (double)sx[i] * (double)sx[i];
             red[4] = q;
-            if (t == 0 && e == 0) atomicAdd(&a.flags[0], 1);
+            if (e == 0) atomicAdd(&a.flags[0], 1);
         }
         __syncthreads();
         mean = (float)(red[4] / (double)d);
@@ -493,11 +542,9 @@ __device__ void route_wg(const DecArgs& a, int t, int e, float* sx, float* sg, f
         wA[wave] = Af;
         wP[wave] = Pf;
     }
-    // the expert and shared-FFN input blocks of this workgroup (8 threads per block)
-    const int nb = d / 32, g = tid >> 3, l8 = tid & 7, b = e + g * a.E;
+    // the expert and shared-FFN input blocks of this workgroup
     if (b < nb) {
         const float4 xq = *(const float4*)(sx + 32 * b + 4 * l8);
-        const float4 nv = ((const float4*)a.pre2)[8 * b + l8];
         float dval;
         int sum;
         const int qw = q8_0_oct(make_float4((xq.x * rinv) * nv.x, (xq.y * rinv) * nv.y, (xq.z * rinv) * nv.z,
@@ -509,7 +556,6 @@ __device__ void route_wg(const DecArgs& a, int t, int e, float* sx, float* sg, f
             a.agu.s[(int64_t)t * a.agu.sstride + b] = sum;
         }
         if (a.ash.q) {
-            const float4 fv = ((const float4*)a.fnorm)[8 * b + l8];
             const int qs = q8_0_oct(make_float4((xq.x * rinv) * fv.x, (xq.y * rinv) * fv.y, (xq.z * rinv) * fv.z,
                                                 (xq.w * rinv) * fv.w),
                                     &dval, &sum);
@@ -863,6 +909,10 @@ __device__ void expert_gu_wg(const DecArgs& a, unsigned char* smem)
     double* red = (double*)(wtot + 32);         // 17
     unsigned* s_kb = (unsigned*)(red + 17);     // [waves][2][16] selection bounds
     const bool routing = blockIdx.x == gridDim.x - 1;  // the routing workgroup: outputs, no tile
+    // one token: every tile's input row is row 0, so its loads go out now, beside the selection's (the
+    // router launch wrote it: a cold read that would otherwise start only once the tile is known)
+    ActIn ain;
+    if (a.T == 1) act_issue(ain, a.agu, 0, 0, 1, nb);
     if (tid == 0) s_misc[1] = 0;
     __syncthreads();
     for (int t = wave; t < a.T; t += NWV) {
@@ -918,8 +968,7 @@ __device__ void expert_gu_wg(const DecArgs& a, unsigned char* smem)
     const DecTile tl = s_tiles[tile];
     const int e = tl.e, cnt = min(tl.cnt, DROWS);
     const int tok0 = tl.row[0] / a.k, tok1 = tl.row[cnt > 1 ? 1 : 0] / a.k;
-    ActIn ain;
-    act_issue(ain, a.agu, tok0, tok1, cnt, nb);
+    if (a.T != 1) act_issue(ain, a.agu, tok0, tok1, cnt, nb);
     __builtin_amdgcn_sched_barrier(0);  // keep the activation loads ahead of the weight loads
     WRegs<TYPE> W;
     load_w<TYPE>(a.gu, clamp_id(e, a.E), rgi, wave, lane, W);  // unconditional (see load_w)
@@ -962,13 +1011,15 @@ __global__ __launch_bounds__(1024) void k_dec_down(DecArgs a)
     const int tile = blockIdx.x / nrgb, g = wave / wpr, wl = wave % wpr;
     const int rgi = (blockIdx.x % nrgb) * a.rpw + g;
     const bool live = g < a.rpw && rgi < a.dn.rg;  // spare waves compute a clamped row group, store nothing
+    // one token: tile j is assignment j, so its input row is known before the (cold) tile load
+    ActIn ain;
+    if (a.T == 1) act_issue(ain, a.adn, min(tile, a.k - 1), min(tile, a.k - 1), 1, nb);
     const int4 tl = *(const int4*)(a.tiles + tile);  // {e, cnt, row0, row1}
     if (tl.x < 0) return;                            // slot past the last tile (uniform)
     const int e = tl.x, cnt = min(tl.y, DROWS);
     ActL* act = (ActL*)dsm;
     float* terms = (float*)(act + DROWS) + (size_t)min(g, a.rpw - 1) * DROWS * nb * 64;
-    ActIn ain;
-    act_issue(ain, a.adn, tl.z, cnt > 1 ? tl.w : tl.z, cnt, nb);
+    if (a.T != 1) act_issue(ain, a.adn, tl.z, cnt > 1 ? tl.w : tl.z, cnt, nb);
     __builtin_amdgcn_sched_barrier(0);  // keep the activation loads ahead of the weight loads
     WRegs<TYPE> W;
     load_w<TYPE>(a.dn, clamp_id(e, a.E), min(rgi, a.dn.rg - 1), wl, lane, W);  // unconditional (see load_w)
@@ -983,19 +1034,21 @@ __global__ __launch_bounds__(1024) void k_dec_down(DecArgs a)
 // Per token (1024 threads): acc = sum_j w_j * yd_j in rank order (src/GemmaCpu.cs:417-418, each term
 // rounded then added), out = rmsnorm(shared) * post1 + rmsnorm(acc) * post2 (src/GemmaCpu.cs:384,
 // 420-421), and with a residual x += rmsnorm(out) * post_ffw_norm (src/GemmaCpu.cs:355-356).  Every
-// load of the token is issued in one round (d <= 4096: four elements per thread; ranks in groups of 8).
+// load of the token, the residual row included, is issued in one round before the first use (d <= 4096:
+// four elements per thread; ranks in groups of 8), and the two branch norms share one reduction.
 constexpr int CB_NT = 1024, CB_E = 4;
 
 __global__ __launch_bounds__(CB_NT) void k_dec_combine(DecArgs a)
 {
     extern __shared__ __align__(16) float cb[];  // acc [d], out [d]
-    __shared__ double red[CB_NT / 64 + 1];
+    __shared__ double red[2 * (CB_NT / 64 + 1)];
     const int t = blockIdx.x, tid = threadIdx.x, d = a.d, k = a.k;
     float* sacc = cb;
     float* so = cb + d;
     const float* sh = a.shout ? a.shout + (int64_t)t * d : nullptr;
+    float* xr = a.xres ? a.xres + (int64_t)t * d : nullptr;
     int ix[CB_E];
-    float accv[CB_E], shv[CB_E], p1[CB_E], p2[CB_E];
+    float accv[CB_E], shv[CB_E], p1[CB_E], p2[CB_E], xv[CB_E], pf[CB_E];
 #pragma unroll
     for (int q = 0; q < CB_E; q++) {
         ix[q] = min(tid + q * CB_NT, d - 1);
@@ -1016,6 +1069,8 @@ __global__ __launch_bounds__(CB_NT) void k_dec_combine(DecArgs a)
                 shv[q] = sh ? sh[ix[q]] : 0.0f;
                 p1[q] = a.post1[ix[q]];
                 p2[q] = a.post2[ix[q]];
+                xv[q] = xr ? xr[ix[q]] : 0.0f;
+                pf[q] = xr ? a.post_ffw[ix[q]] : 0.0f;
             }
         }
 #pragma unroll
@@ -1035,8 +1090,10 @@ __global__ __launch_bounds__(CB_NT) void k_dec_combine(DecArgs a)
         }
     }
     __syncthreads();
-    const float sc2 = rms_scale_from_mean(wg_mean_sq(s2, sacc, d, red, a.flags), a.eps);
-    const float sc1 = sh ? rms_scale_from_mean(wg_mean_sq(s1, sh, d, red, a.flags), a.eps) : 0.0f;
+    float m2, m1;
+    wg_mean_sq2(s2, s1, sacc, sh, d, red, a.flags, &m2, &m1);
+    const float sc2 = rms_scale_from_mean(m2, a.eps);
+    const float sc1 = sh ? rms_scale_from_mean(m1, a.eps) : 0.0f;
     float ov[CB_E];
     double s3 = 0.0;
 #pragma unroll
@@ -1050,19 +1107,13 @@ __global__ __launch_bounds__(CB_NT) void k_dec_combine(DecArgs a)
             s3 += (double)ov[q] * (double)ov[q];
         }
     }
-    if (a.xres) {
-        float xv[CB_E], pf[CB_E];
-#pragma unroll
-        for (int q = 0; q < CB_E; q++) {
-            xv[q] = a.xres[(int64_t)t * d + ix[q]];
-            pf[q] = a.post_ffw[ix[q]];
-        }
+    if (xr) {
         __syncthreads();
         const float sc3 = rms_scale_from_mean(wg_mean_sq(s3, so, d, red, a.flags), a.eps);
 #pragma unroll
         for (int q = 0; q < CB_E; q++) {
             const int i = tid + q * CB_NT;
-            if (i < d) a.xres[(int64_t)t * d + i] = xv[q] + ov[q] * sc3 * pf[q];
+            if (i < d) xr[i] = xv[q] + ov[q] * sc3 * pf[q];
         }
     }
 }
@@ -1074,9 +1125,9 @@ static MatD mat_d(const QMat* q)
     MatD m{};
     if (!q || !q->payload) return m;
     m.pay = q->payload;
-    m.sc8 = (const uint4*)q->scale8;
     m.mat_pay = q->mat_pay_stride();
-    m.mat_sc8 = q->mat_sc8_stride();
+    m.rg_pay = q->rg_pay;
+    m.sc_off = q->sc8_off();
     m.rg = q->rg;
     m.nb = q->nb;
     m.nb8 = (q->nb + 7) / 8;

@@ -21,7 +21,7 @@ typedef int mv16i __attribute__((ext_vector_type(16)));
 struct MmaArgs {
     const uint8_t* payload;
     const uint8_t* scale;
-    int64_t mat_pay, mat_sc;
+    int64_t mat_pay, mat_sc, rg_pay;
     int rg, nb, rows;
     Act act;
     const Tile* tiles;
@@ -61,7 +61,7 @@ __global__ __launch_bounds__(256) void k_grouped_mfma(MmaArgs g)
         orow[j] = valid[j] ? g.perm[tl.start + s] : 0;
         arow[j] = orow[j] / g.act_div;
     }
-    const uint8_t* pay = g.payload + tl.e * g.mat_pay + ((int64_t)gI * nb * 64 + half * 32 + r32) * PAY;
+    const uint8_t* pay = g.payload + tl.e * g.mat_pay + gI * g.rg_pay + (half * 32 + r32) * PAY;
     const uint16_t* scl = (const uint16_t*)(g.scale + tl.e * g.mat_sc) + (int64_t)gI * nb * 64 + half * 32 + 4 * h;
     const mv4i neg8 = {(int)0xF8F8F8F8u, (int)0xF8F8F8F8u, (int)0xF8F8F8F8u, (int)0xF8F8F8F8u};
     const mv16i zero = {};
@@ -165,6 +165,7 @@ void launch_grouped_mfma(hipStream_t st, const QMat& w, Act act, const Tile* til
     g.payload = w.payload;
     g.scale = w.scale;
     g.mat_pay = w.mat_pay_stride();
+    g.rg_pay = w.rg_pay;
     g.mat_sc = w.mat_sc_stride();
     g.rg = w.rg;
     g.nb = w.nb;

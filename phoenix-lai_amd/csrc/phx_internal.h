@@ -43,7 +43,10 @@ enum ActFmt { ACT_Q8_0 = 0, ACT_K4 = 1, ACT_K6 = 2 };
 
 // One stack of quantized matrices (experts, or one dense matrix), repacked at upload into row
 // groups of 64 rows: payload[m][rg][b][lane][pay] and scale[m][rg][b][lane][sbytes], so the 64
-// lanes of a wave read block b of 64 consecutive rows as one contiguous span.
+// lanes of a wave read block b of 64 consecutive rows as one contiguous span.  A row group's payload
+// is rg_pay bytes: for Q4_0 / Q8_0 its nb * 64 payload blocks are followed by the same fp16 scales
+// grouped per lane by 8 blocks, [nb/8][lane][8] (one 16 B load gives a row the scales of 8
+// consecutive blocks: the decode kernels' layout), so a row group's weights and scales share pages.
 //   Q4_0: pay 16 (nibbles, low = element j, high = j+16), scale fp16 d
 //   Q8_0: pay 32 (int8), scale fp16 d
 //   Q4_K: pay 144 = 128 nibbles in (sub-block, l, m) order + sc[8] + m[8]; scale fp16 d | fp16 dmin << 16
@@ -54,14 +57,13 @@ struct QMat {
     int rg = 0, nb = 0;                 // row groups, blocks (32 or 256 elements) per row
     int pay = 0, sbytes = 0;
     bool paired = false;                // gate|up: row group g = gate rows 32g..32g+31 and the matching up rows
+    int64_t rg_pay = 0;                 // payload bytes per row group (blocks, then Q4_0 / Q8_0 scale groups)
     uint8_t* payload = nullptr;
     uint8_t* scale = nullptr;
-    // Q4_0 / Q8_0 only: the same fp16 scales grouped per lane by 8 blocks, [m][rg][nb/8][lane][8], so
-    // one 16 B load gives a row the scales of 8 consecutive blocks (the decode kernels' layout)
-    uint8_t* scale8 = nullptr;
-    int64_t mat_pay_stride() const { return (int64_t)rg * nb * kRowGroup * pay; }
+    bool has_sc8() const { return type == PHX_Q4_0_DEV || type == PHX_Q8_0_DEV; }
+    int64_t sc8_off() const { return (int64_t)nb * kRowGroup * pay; }  // scale groups within a row group
+    int64_t mat_pay_stride() const { return (int64_t)rg * rg_pay; }
     int64_t mat_sc_stride() const { return (int64_t)rg * nb * kRowGroup * sbytes; }
-    int64_t mat_sc8_stride() const { return (int64_t)rg * ((nb + 7) / 8) * kRowGroup; }  // 16 B units
 };
 
 // Quantized activation rows for one weight type.

@@ -102,7 +102,7 @@ int round_up(int v, int m) { return (v + m - 1) / m * m; }
 // ------------------------------------------------------------------------------ repack
 // GGUF rows [n_mat][rows][row_bytes] -> row groups of 64 (see QMat).
 struct HostQ {
-    std::vector<uint8_t> payload, scale, scale8;
+    std::vector<uint8_t> payload, scale;
 };
 
 void decode_q4k_natural(const uint8_t* blk, uint8_t* q, int* sc, int* mn)
@@ -204,6 +204,8 @@ void repack(int type, const uint8_t* src, int n_mat, int rows, int cols, QMat& q
     q.pay = type == PHX_Q4_0 ? 16 : type == PHX_Q8_0 ? 32 : type == PHX_Q4_K ? 144 : 208;
     q.sbytes = type == PHX_Q4_K ? 4 : 2;
     const int64_t rb = row_bytes(type, cols), bb = rb / q.nb;
+    const int nb8 = (q.nb + 7) / 8;
+    q.rg_pay = (int64_t)q.nb * kRowGroup * q.pay + (q.has_sc8() ? (int64_t)nb8 * kRowGroup * 16 : 0);
     h.payload.assign((size_t)q.mat_pay_stride() * n_mat, 0);
     h.scale.assign((size_t)q.mat_sc_stride() * n_mat, 0);
     const int64_t total_rows = (int64_t)n_mat * rows;
@@ -220,24 +222,25 @@ void repack(int type, const uint8_t* src, int n_mat, int rows, int cols, QMat& q
                     lane = (j % 32) + (up ? 32 : 0);
                 }
                 const uint8_t* row = src + gr * rb;
+                uint8_t* rgp = h.payload.data() + ((int64_t)m * q.rg + rg) * q.rg_pay;
                 for (int b = 0; b < q.nb; b++) {
                     int64_t idx = (((int64_t)m * q.rg + rg) * q.nb + b) * kRowGroup + lane;
-                    repack_block(type, row + b * bb, h.payload.data() + idx * q.pay, h.scale.data() + idx * q.sbytes);
+                    repack_block(type, row + b * bb, rgp + ((int64_t)b * kRowGroup + lane) * q.pay,
+                                 h.scale.data() + idx * q.sbytes);
                 }
             }
         });
     }
     for (auto& t : th) t.join();
-    if (type == PHX_Q4_0 || type == PHX_Q8_0) {
-        // scale8: [m][rg][b / 8][lane][8] fp16, the scales of 8 consecutive blocks of a row together
-        const int nb8 = (q.nb + 7) / 8;
-        h.scale8.assign((size_t)q.mat_sc8_stride() * 16 * n_mat, 0);
-        uint16_t* s8 = (uint16_t*)h.scale8.data();
+    if (q.has_sc8()) {
+        // each row group's scale groups [b / 8][lane][8] fp16 after its payload blocks
         const uint16_t* s1 = (const uint16_t*)h.scale.data();
-        for (int64_t mr = 0; mr < (int64_t)n_mat * q.rg; mr++)
+        for (int64_t mr = 0; mr < (int64_t)n_mat * q.rg; mr++) {
+            uint16_t* s8 = (uint16_t*)(h.payload.data() + mr * q.rg_pay + q.sc8_off());
             for (int b = 0; b < q.nb; b++)
                 for (int lane = 0; lane < kRowGroup; lane++)
-                    s8[((mr * nb8 + b / 8) * kRowGroup + lane) * 8 + b % 8] = s1[(mr * q.nb + b) * kRowGroup + lane];
+                    s8[((b / 8) * kRowGroup + lane) * 8 + b % 8] = s1[(mr * q.nb + b) * kRowGroup + lane];
+        }
     }
 }
 
@@ -677,10 +680,8 @@ void free_qmat(QMat& q)
 {
     if (q.payload) (void)hipFree(q.payload);
     if (q.scale) (void)hipFree(q.scale);
-    if (q.scale8) (void)hipFree(q.scale8);
     q.payload = nullptr;
     q.scale = nullptr;
-    q.scale8 = nullptr;
 }
 
 int upload_q(phx_moe_ctx* c, int type, const void* src, int n_mat, int rows, int cols, QMat& q, bool paired = false)
@@ -692,10 +693,6 @@ int upload_q(phx_moe_ctx* c, int type, const void* src, int n_mat, int rows, int
     HIPCHK(c, hipMalloc((void**)&q.scale, h.scale.size()));
     HIPCHK(c, hipMemcpy(q.payload, h.payload.data(), h.payload.size(), hipMemcpyHostToDevice));
     HIPCHK(c, hipMemcpy(q.scale, h.scale.data(), h.scale.size(), hipMemcpyHostToDevice));
-    if (!h.scale8.empty()) {
-        HIPCHK(c, hipMalloc((void**)&q.scale8, h.scale8.size()));
-        HIPCHK(c, hipMemcpy(q.scale8, h.scale8.data(), h.scale8.size(), hipMemcpyHostToDevice));
-    }
     return PHX_OK;
 }
 
@@ -867,6 +864,7 @@ int phx_moe_ffn(phx_moe_ctx* c, int layer, int T, float* x, const float* shared,
     if (T <= 0 || (int64_t)T * L.desc.n_used > 65535) return set_err(c, PHX_ERR_ARG, "T=%d out of range", T);
     if (!x || !out) return set_err(c, PHX_ERR_ARG, "null x/out");
     if ((flags & PHX_FLAG_RESIDUAL) && !L.post_ffw) return set_err(c, PHX_ERR_ARG, "residual needs post_ffw_norm");
+    if ((flags & PHX_FLAG_RESIDUAL) && out == x) return set_err(c, PHX_ERR_ARG, "residual needs out distinct from x");
     HIPCHK(c, hipSetDevice(c->device));
     int rc = ensure_workspace(c, L, T);
     if (rc) return rc;
