@@ -9,9 +9,9 @@ command buffer per decode pass, src/GemmaGpu.cs:544-554); every replay starts fr
 input, so the experts touched change from replay to replay and the 256 MB MALL cannot serve them.
 
 Prints one JSON line: value = tokens/s through the layer (inputs resident in HBM), a roofline
-object for the dominant kernel (the grouped gate|up product; its average execution interval from
-HIP events that the runtime stamps at kernel start and end, over an instrumented eager pass of the
-same workload) and the CPU baseline (the C restatement of the reference CPU path timed on this
+object for the dominant kernel (the grouped gate|up product; its average duration from HIP timing
+events recorded around it in the same captured stack, replayed like the timed region) and the CPU
+baseline (the C restatement of the reference CPU path timed on this
 host's cores over a bounded sample).
 """
 from __future__ import annotations
@@ -37,7 +37,10 @@ METRIC = "MoE layer tokens/s; decode HBM GB/s vs peak; prefill MFMA util"
 # WRITE_SIZE) of this file with --calibrate, each scaled by what the counter reads for the library's
 # streaming read and copy kernels of known size (fetch factor 2.000, write factor 1.000).  Keyed by
 # (config, T, kernel); re-measured whenever that kernel changes.
-PMC_TRAFFIC = {}
+PMC_TRAFFIC = {
+    # FETCH_SIZE 12,381.8 KiB x 2.000 + WRITE_SIZE 86.6 KiB x 1.000 per launch of phx::k_dec_gu<2>
+    ("c2_decode", 1, "gate_up"): (25_446_605, "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, 305 launches each"),
+}
 
 
 def log(*a):
@@ -111,18 +114,24 @@ def run_layer(args, pkg):
     ms_per_step = dt * 1e3 / steps
     tokens_s = T * steps / dt
 
-    # ---- instrumented eager pass: per-kernel execution intervals and touched experts
+    # ---- per-kernel durations: the same stack captured again with HIP timing events recorded as graph
+    # nodes around each kernel (each interval runs from the previous node's end to the kernel's end,
+    # as a kernel-trace profiler reports graph kernels), read back after every replay
     gu_b, dn_b = expert_bytes(L)
     prof_steps = max(1, min(steps, args.prof_steps))
     ctx.profile(True)
-    distinct = 0
-    for s in range(prof_steps):
-        ctx.ffn_device(s % n_slots, T, xbuf.ptr + (s % NX) * xstride, None, obuf.ptr, pkg.PHX.FLAG_ASYNC)
-        ids = ctx.routing()[0]
-        distinct += len(np.unique(ids))
+    ctx.stack_capture(0, n_slots, T)
+    for r in range(max(1, prof_steps // n_slots)):
+        ctx.stack_run_device(xbuf.ptr + (r % NX) * xstride, T)
     prof = ctx.profile_read()
     ctx.profile(False)
-    avg_experts = distinct / prof_steps
+    # experts touched per step (the routing of each step read back)
+    distinct = 0
+    n_route = min(prof_steps, 64)
+    for s in range(n_route):
+        ctx.ffn_device(s % n_slots, T, xbuf.ptr + (s % NX) * xstride, None, obuf.ptr, pkg.PHX.FLAG_ASYNC)
+        distinct += len(np.unique(ctx.routing()[0]))
+    avg_experts = distinct / n_route
     gu_ms = prof["gate_up"][0] / max(1, prof["gate_up"][1])
     dn_ms = prof["down"][0] / max(1, prof["down"][1])
     decode = prof["dispatch"][1] == 0  # the decode path has no separate dispatch launch

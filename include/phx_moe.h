@@ -150,8 +150,11 @@ int phx_moe_memcpy_d2h(phx_moe_ctx* ctx, void* dst, const void* src, uint64_t by
 
 /* Per-kernel timing on the library's stream (the Gpu.cs:163-171 profiling counterpart).  While
  * enabled, every kernel is launched with start/stop events stamped with its own execution interval
- * (hipExtLaunchKernel), the interval a kernel-trace profiler reports.  profile_read returns, per kind,
- * the summed kernel time (ms) and the number of calls that launched that kind.  Kinds: */
+ * (hipExtLaunchKernel), the interval a kernel-trace profiler reports.  A stack captured while
+ * profiling holds the events as graph nodes around each kernel (the interval from the previous node's
+ * end to the kernel's end); each phx_moe_stack_run of it then waits for the replay and adds them up.
+ * profile_read returns, per kind, the summed kernel time (ms) and the number of launches of that
+ * kind.  Kinds: */
 #define PHX_K_PROLOGUE 0
 #define PHX_K_ROUTER 1
 #define PHX_K_TOPK 2

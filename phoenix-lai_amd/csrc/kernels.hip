@@ -134,8 +134,54 @@ void launch_prologue(hipStream_t st, int T, int d, float eps, const float* x, co
 // logits[t][e] = sum_i W[e][i] * m[t][i] as the sequential float sum of GemmaCpu.cs:393-394: one lane
 // per (t, e), the products rounded, then added in index order.  W is stored [d/4][E][4] so the 64
 // lanes (experts) of a wave read 1 KB contiguous; m is wave-uniform.
-__global__ __launch_bounds__(64) void k_router_exact(int d, int E, const float4* __restrict__ wt4,
+template <int TB>
+__global__ __launch_bounds__(64) void k_router_exact(int T, int d, int E, const float4* __restrict__ wt4,
                                                      const float* __restrict__ rin, float* __restrict__ logits)
+{
+    extern __shared__ float4 srin[];  // [TB][d / 4]: the wave's token rows of m
+    const int lane = threadIdx.x, e = blockIdx.x * 64 + lane, t0 = blockIdx.y * TB;
+    const int ee = e < E ? e : E - 1;
+    const float4* w = wt4 + ee;
+    const int n4 = d / 4;  // d % 32 == 0
+    for (int j = 0; j < TB; j++) {
+        const float4* m = (const float4*)(rin + (int64_t)min(t0 + j, T - 1) * d);
+        for (int i = lane; i < n4; i += 64) srin[j * n4 + i] = m[i];
+    }
+    float4 wv[8];
+#pragma unroll
+    for (int q = 0; q < 8; q++) wv[q] = w[(int64_t)q * E];
+    __syncthreads();
+    float s[TB];
+#pragma unroll
+    for (int j = 0; j < TB; j++) s[j] = 0.0f;
+    for (int i = 0; i < n4; i += 8) {
+        float4 wn[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++) wn[q] = w[(int64_t)min(i + 8 + q, n4 - 1) * E];  // the next chunk (clamped)
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+#pragma unroll
+            for (int j = 0; j < TB; j++) {
+                const float4 mv = srin[j * n4 + i + q];  // one LDS broadcast for the wave
+                s[j] += wv[q].x * mv.x;
+                s[j] += wv[q].y * mv.y;
+                s[j] += wv[q].z * mv.z;
+                s[j] += wv[q].w * mv.w;
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < 8; q++) wv[q] = wn[q];
+    }
+    if (e < E) {
+#pragma unroll
+        for (int j = 0; j < TB; j++)
+            if (t0 + j < T) logits[(int64_t)(t0 + j) * E + e] = s[j];
+    }
+}
+
+// Many tokens: one wave per (64 experts, token) and no LDS, so the occupancy hides the load latency.
+__global__ __launch_bounds__(64) void k_router_exact_wide(int d, int E, const float4* __restrict__ wt4,
+                                                          const float* __restrict__ rin, float* __restrict__ logits)
 {
     const int e = blockIdx.x * 64 + threadIdx.x, t = blockIdx.y;
     const int ee = e < E ? e : E - 1;
@@ -145,8 +191,8 @@ __global__ __launch_bounds__(64) void k_router_exact(int d, int E, const float4*
     const int n4 = d / 4;
 #pragma unroll 4
     for (int i = 0; i < n4; i++) {
-        float4 wv = w[(int64_t)i * E];
-        float4 mv = m[i];
+        const float4 wv = w[(int64_t)i * E];
+        const float4 mv = m[i];
         s += wv.x * mv.x;
         s += wv.y * mv.y;
         s += wv.z * mv.z;
@@ -155,9 +201,20 @@ __global__ __launch_bounds__(64) void k_router_exact(int d, int E, const float4*
     if (e < E) logits[(int64_t)t * E + e] = s;
 }
 
+// Fewer tokens: each lane carries TB tokens' sequential chains (each in index order, as the
+// reference): one read of W serves TB tokens and the independent chains fill the add latency.  The
+// token rows of m sit in LDS; W streams in 32-element chunks, the next chunk's loads issued before the
+// current chunk's adds.
 void launch_router_exact(hipStream_t st, int T, int d, int E, const float* wt4, const float* rin, float* logits)
 {
-    launch(k_router_exact, dim3((E + 63) / 64, T), dim3(64), 0, st, d, E, (const float4*)wt4, rin, logits);
+    const int gx = (E + 63) / 64;
+    const float4* w = (const float4*)wt4;
+    if (T >= 1024)
+        launch(k_router_exact_wide, dim3(gx, T), dim3(64), 0, st, d, E, w, rin, logits);
+    else if (T >= 128)
+        launch(k_router_exact<2>, dim3(gx, (T + 1) / 2), dim3(64), (uint32_t)(2 * d * 4), st, T, d, E, w, rin, logits);
+    else
+        launch(k_router_exact<1>, dim3(gx, T), dim3(64), (uint32_t)(d * 4), st, T, d, E, w, rin, logits);
 }
 
 // ------------------------------------------------------------------------------ top-k and weights

@@ -2,10 +2,12 @@
 //   k_dec_route    router logits with certified error bounds, one workgroup per (token, expert), and the
 //                  Q8_0 expert and shared-FFN inputs (each workgroup quantizes its share of the
 //                  token's 32-blocks)
-//   k_dec_gu       every expert workgroup selects the top-k from the router's bounds (exact fallback
-//                  when the order cannot be certified) and forms the expert tiles, then computes one
-//                  (tile, row group) of the routed experts' gate|up products with the gelu(g) * u Q8_0
-//                  epilogue; beside them, the dense shared FFN's gate|up product
+//   k_dec_gu       at most one workgroup per CU, each over a strided share of the units: first the
+//                  dense shared FFN's (token pair, row group) gate|up units, then the routed experts'
+//                  (tile, row group) units with the gelu(g) * u Q8_0 epilogue.  Before its first expert
+//                  unit a workgroup selects the top-k from the router's bounds (exact fallback when the
+//                  order cannot be certified) and forms the expert tiles; the last workgroup writes
+//                  the routing outputs
 //   k_dec_down     (tile, row groups) of the routed experts' down products; beside them, the shared
 //                  FFN's down product
 //   k_dec_combine  per token: the rank-ordered combine, the two branch norms, the optional residual
@@ -425,19 +427,33 @@ __device__ __forceinline__ void gu_epilogue(float S, int rgi, int split, int64_t
     }
 }
 
-// exact reference logit of expert e for token t (src/GemmaCpu.cs:389-395): the products rounded,
-// added in index order
-__device__ float exact_logit(const float* x, const float* W, const float* gis, int d, int t, int e, float rinv, float sc)
+// Exact reference logit (src/GemmaCpu.cs:389-395): the products p_i = W[e][i] * m_i rounded, added
+// in index order, with m = ((x * rinv) * sc) * s the token's router input (in LDS, d floats).  The W
+// row streams in 32-element chunks, the next chunk's loads issued before the current chunk's adds, so
+// the chain waits on memory once per chunk at most (d % 32 == 0).
+__device__ float exact_logit(const float* sm, const float* wrow, int d)
 {
-    const float* xr = x + (int64_t)t * d;
-    const float* wr = W + (int64_t)e * d;
+    const float4* w4 = (const float4*)wrow;
+    const float4* m4 = (const float4*)sm;
+    const int n4 = d / 4;
+    float4 w[8];
+#pragma unroll
+    for (int q = 0; q < 8; q++) w[q] = w4[q];
     float s = 0.0f;
-    for (int i = 0; i < d; i += 4) {
-        const float4 xv = *(const float4*)(xr + i), gv = *(const float4*)(gis + i), wv = *(const float4*)(wr + i);
-        s += wv.x * (xv.x * rinv * sc * gv.x);
-        s += wv.y * (xv.y * rinv * sc * gv.y);
-        s += wv.z * (xv.z * rinv * sc * gv.z);
-        s += wv.w * (xv.w * rinv * sc * gv.w);
+    for (int c = 0; c < n4; c += 8) {
+        float4 wn[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++) wn[q] = w4[min(c + 8 + q, n4 - 1)];  // the next chunk (clamped)
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            const float4 m = m4[c + q];
+            s += w[q].x * m.x;
+            s += w[q].y * m.y;
+            s += w[q].z * m.z;
+            s += w[q].w * m.w;
+        }
+#pragma unroll
+        for (int q = 0; q < 8; q++) w[q] = wn[q];
     }
     return s;
 }
@@ -604,8 +620,8 @@ __global__ __launch_bounds__(RT_NT) void k_dec_route(DecArgs a)
 }
 
 // ------------------------------------------------------------------------------ shared FFN workgroups
-// Shared gate|up (in k_dec_gu): one workgroup per (pair of tokens, paired row group), input from
-// k_dec_route's packed Q8_0 rows.
+// Shared gate|up unit (in k_dec_gu): one (pair of tokens, paired row group), input from k_dec_route's
+// packed Q8_0 rows.
 template <int TYPE>
 __device__ void shared_gu_wg(const DecArgs& a, int tile, int rgi, unsigned char* smem)
 {
@@ -740,9 +756,10 @@ __device__ bool wave_topk(const DecArgs& a, int t, int* s_ids, unsigned* s_klo, 
 // Exact selection for the tokens marked in s_bad (rare): the experts that can reach the chosen ones
 // are recomputed as the reference's float chains (src/GemmaCpu.cs:389-395) and all are ranked exactly:
 // ties to the lower index, NaN below every number (the strict '>' scan of GemmaCpu.cs:400-405).
-// sL, samb, srank: LDS [T*E]; sL ends holding the logits the routing reports for those tokens.
-__device__ void select_exact(const DecArgs& a, double* sL, char* samb, short* srank, int* s_ids, const int* s_bad,
-                             double* red, bool count)
+// sL, samb, srank: LDS [T*E]; sm: LDS [d], the router input of the token being ranked; sL ends
+// holding the logits the routing reports for those tokens.
+__device__ void select_exact(const DecArgs& a, double* sL, char* samb, short* srank, float* sm, int* s_ids,
+                             const int* s_bad, double* red, bool count)
 {
     const int tid = threadIdx.x, NT = blockDim.x;
     const float sc = 1.0f / (float)__dsqrt_rn((double)a.d);
@@ -753,6 +770,8 @@ __device__ void select_exact(const DecArgs& a, double* sL, char* samb, short* sr
         double s = 0.0;
         for (int i = tid; i < a.d; i += NT) s += (double)xr[i] * (double)xr[i];
         const float rinv_t = rms_scale_from_mean(wg_mean_sq(s, xr, a.d, red, nullptr), a.eps);
+        for (int i = tid; i < a.d; i += NT) sm[i] = ((xr[i] * rinv_t) * sc) * a.gis[i];
+        __syncthreads();
         const double* Lr = a.Lb + (int64_t)tt * a.E;
         const double* Br = a.Bb + (int64_t)tt * a.E;
         // the lowest lower end among the fast path's chosen experts: an expert whose upper end does not
@@ -769,7 +788,7 @@ __device__ void select_exact(const DecArgs& a, double* sL, char* samb, short* sr
             const int j = tt * a.E + b;
             const bool amb = nonfinite || !(Lr[b] + Br[b] < minlo);
             samb[j] = amb;
-            sL[j] = amb ? (double)exact_logit(a.x, a.W, a.gis, a.d, tt, b, rinv_t, sc) : Lr[b];
+            sL[j] = amb ? (double)exact_logit(sm, a.W + (int64_t)b * a.d, a.d) : Lr[b];
         }
         __syncthreads();
         for (int b = tid; b < a.E; b += NT) {
@@ -890,12 +909,12 @@ __device__ void write_routing(const DecArgs& a, LF Lr, const int* s_ids, const i
 }
 
 template <int TYPE>
-__device__ void expert_gu_wg(const DecArgs& a, unsigned char* smem)
+__device__ void gu_wg(const DecArgs& a, unsigned char* smem)
 {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, NT = blockDim.x, NWV = NT >> 6;
     const int TE = a.T * a.E, nb = a.gu.nb;
-    // LDS: [terms | exact-selection arrays] [act rows] [ids, perm, lists, tiles] [scratch]
-    const size_t terms_bytes = (size_t)DROWS * nb * 64 * 4, sel_bytes = (size_t)TE * 11;
+    // LDS: [terms | exact-selection arrays and router input] [act rows] [ids, perm, lists, tiles] [scratch]
+    const size_t terms_bytes = (size_t)DROWS * nb * 64 * 4, sel_bytes = (size_t)TE * 11 + 16 + (size_t)a.d * 4;
     unsigned char* un = smem;
     ActL* act = (ActL*)(un + ((std::max(terms_bytes, sel_bytes) + 15) & ~(size_t)15));
     int* s_ids = (int*)(act + DROWS);   // 256
@@ -908,11 +927,23 @@ __device__ void expert_gu_wg(const DecArgs& a, unsigned char* smem)
     int* wtot = s_misc + 20;                    // 32
     double* red = (double*)(wtot + 32);         // 17
     unsigned* s_kb = (unsigned*)(red + 17);     // [waves][2][16] selection bounds
-    const bool routing = blockIdx.x == gridDim.x - 1;  // the routing workgroup: outputs, no tile
+    const bool routing = blockIdx.x == gridDim.x - 1;  // the routing workgroup: outputs, no units
+    // units: the shared FFN's (token pair, row group) units first, then the expert (tile, row group)
+    // units; unit workgroup b takes units b, b + G, b + 2G, ... (G = gridDim.x - 1)
+    const int G = gridDim.x - 1;
+    const int nsh = a.sgu.rg ? (a.T + DROWS - 1) / DROWS * a.sgu.rg : 0;
+    const int total = nsh + a.max_tiles * a.gu.rg;
+    int u = routing ? total : (int)blockIdx.x;
+    if (u < nsh) {
+        for (; u < nsh; u += G) shared_gu_wg<TYPE>(a, u / a.sgu.rg, u % a.sgu.rg, smem);
+        if (u >= total) return;  // uniform: no barriers follow
+        __syncthreads();         // the shared units' LDS becomes the selection's
+    }
     // one token: every tile's input row is row 0, so its loads go out now, beside the selection's (the
     // router launch wrote it: a cold read that would otherwise start only once the tile is known)
+    const bool pre = a.T == 1 && !routing;
     ActIn ain;
-    if (a.T == 1) act_issue(ain, a.agu, 0, 0, 1, nb);
+    if (pre) act_issue(ain, a.agu, 0, 0, 1, nb);
     if (tid == 0) s_misc[1] = 0;
     __syncthreads();
     for (int t = wave; t < a.T; t += NWV) {
@@ -928,7 +959,8 @@ __device__ void expert_gu_wg(const DecArgs& a, unsigned char* smem)
     if (exact) {
         char* samb = (char*)(sL + TE);
         short* srank = (short*)(samb + TE);
-        select_exact(a, sL, samb, srank, s_ids, s_misc + 2, red, routing);
+        float* sm = (float*)(((uintptr_t)(srank + TE) + 15) & ~(uintptr_t)15);
+        select_exact(a, sL, samb, srank, sm, s_ids, s_misc + 2, red, routing);
     }
     int ntiles;
     if (a.T == 1) {
@@ -963,33 +995,31 @@ __device__ void expert_gu_wg(const DecArgs& a, unsigned char* smem)
             s_perm, s_tiles, ntiles);
         return;
     }
-    const int tile = blockIdx.x / a.gu.rg, rgi = blockIdx.x % a.gu.rg;
-    if (tile >= ntiles) return;  // uniform: no barriers follow for this workgroup
-    const DecTile tl = s_tiles[tile];
-    const int e = tl.e, cnt = min(tl.cnt, DROWS);
-    const int tok0 = tl.row[0] / a.k, tok1 = tl.row[cnt > 1 ? 1 : 0] / a.k;
-    if (a.T != 1) act_issue(ain, a.agu, tok0, tok1, cnt, nb);
-    __builtin_amdgcn_sched_barrier(0);  // keep the activation loads ahead of the weight loads
-    WRegs<TYPE> W;
-    load_w<TYPE>(a.gu, clamp_id(e, a.E), rgi, wave, lane, W);  // unconditional (see load_w)
-    __syncthreads();  // the exact-selection arrays are about to become terms
-    act_store(ain, cnt, nb, act);
-    __syncthreads();
-    const float S = rowgroup_chain<TYPE>(W, wave, nb, act, cnt, (float*)un);
-    if (wave < cnt) gu_epilogue(S, rgi, a.nf, wave == 0 ? tl.row[0] : tl.row[1], a.g, a.u, a.adn, a.gelu_tab);
+    for (; u < total; u += G) {
+        const int x = u - nsh, tile = x / a.gu.rg, rgi = x % a.gu.rg;
+        if (tile >= ntiles) return;  // uniform; the later units of this workgroup lie past the tiles too
+        const DecTile tl = s_tiles[tile];
+        const int e = tl.e, cnt = min(tl.cnt, DROWS);
+        const int tok0 = tl.row[0] / a.k, tok1 = tl.row[cnt > 1 ? 1 : 0] / a.k;
+        if (!pre) act_issue(ain, a.agu, tok0, tok1, cnt, nb);  // one token: ain holds row 0 throughout
+        __builtin_amdgcn_sched_barrier(0);  // keep the activation loads ahead of the weight loads
+        WRegs<TYPE> W;
+        load_w<TYPE>(a.gu, clamp_id(e, a.E), rgi, wave, lane, W);  // unconditional (see load_w)
+        __syncthreads();  // the exact-selection arrays (first unit) or the last unit's rows are done with
+        act_store(ain, cnt, nb, act);
+        __syncthreads();
+        const float S = rowgroup_chain<TYPE>(W, wave, nb, act, cnt, (float*)un);
+        if (wave < cnt) gu_epilogue(S, rgi, a.nf, wave == 0 ? tl.row[0] : tl.row[1], a.g, a.u, a.adn, a.gelu_tab);
+    }
 }
 
-template <int TYPE>
-__global__ __launch_bounds__(1024) void k_dec_gu(DecArgs a)
+// NTMAX: the workgroup-size bound the compiler allocates registers for (768 gives the unit loop the
+// registers it needs without scratch; 1024 for the widest rows)
+template <int TYPE, int NTMAX>
+__global__ __launch_bounds__(NTMAX) void k_dec_gu(DecArgs a)
 {
     extern __shared__ __align__(16) unsigned char dsm[];
-    const int ne = a.max_tiles * a.gu.rg;
-    if ((int)blockIdx.x < ne || (int)blockIdx.x == (int)gridDim.x - 1) {
-        expert_gu_wg<TYPE>(a, dsm);  // an expert tile, or (the last workgroup) the routing outputs
-    } else {
-        const int s = blockIdx.x - ne;
-        shared_gu_wg<TYPE>(a, s / a.sgu.rg, s % a.sgu.rg, dsm);
-    }
+    gu_wg<TYPE>(a, dsm);  // shared and expert units, or (the last workgroup) the routing outputs
 }
 
 // ------------------------------------------------------------------------------ k_dec_down
@@ -1204,7 +1234,7 @@ static DecArgs dec_args(const DecLayerH& h)
 static size_t gu_lds(const DecLayerH& h)
 {
     const size_t TE = (size_t)h.T * h.E;
-    const size_t un = (std::max((size_t)DROWS * h.gu->nb * 64 * 4, TE * 11) + 15) & ~(size_t)15;
+    const size_t un = (std::max((size_t)DROWS * h.gu->nb * 64 * 4, TE * 11 + 16 + (size_t)h.d * 4) + 15) & ~(size_t)15;
     const size_t ex = un + sizeof(ActL) * DROWS + (256 * 2 + 260 * 3) * 4 + 272 * sizeof(DecTile) + (20 + 32) * 4 + 17 * 8 +
                       16 * 32 * 4;
     const size_t sh = h.sgu ? sizeof(ActL) * DROWS + (size_t)DROWS * h.sgu->nb * 64 * 4 : 0;
@@ -1243,7 +1273,8 @@ static void launch_typed(const DecLayerH& h, dim3 grid, dim3 block, size_t lds, 
         launch(KT<PHX_Q8_0_DEV>::fn, grid, block, (uint32_t)lds, st, a);
     }
 }
-template <int T> struct KGu { static constexpr auto fn = k_dec_gu<T>; };
+template <int T> struct KGu { static constexpr auto fn = k_dec_gu<T, 768>; };
+template <int T> struct KGuW { static constexpr auto fn = k_dec_gu<T, 1024>; };
 template <int T> struct KDown { static constexpr auto fn = k_dec_down<T>; };
 
 void launch_dec_route(hipStream_t st, const DecLayerH& h)
@@ -1254,7 +1285,10 @@ void launch_dec_route(hipStream_t st, const DecLayerH& h)
 void launch_dec_gu(hipStream_t st, const DecLayerH& h)
 {
     const int nsh = h.sgu ? (h.T + DROWS - 1) / DROWS * h.sgu->rg : 0;
-    launch_typed<KGu>(h, dim3(h.max_tiles * h.gu->rg + nsh + 1), dim3(nt_gu(h)), gu_lds(h), st, dec_args(h));
+    const int units = nsh + h.max_tiles * h.gu->rg;
+    const dim3 grid(std::min(units, std::max(1, h.ncu)) + 1);
+    if (nt_gu(h) <= 768) launch_typed<KGu>(h, grid, dim3(nt_gu(h)), gu_lds(h), st, dec_args(h));
+    else launch_typed<KGuW>(h, grid, dim3(nt_gu(h)), gu_lds(h), st, dec_args(h));
 }
 
 void launch_dec_down(hipStream_t st, const DecLayerH& h)

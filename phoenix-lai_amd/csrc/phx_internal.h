@@ -17,10 +17,15 @@ namespace phx {
 
 // Kernel timing hook.  While a context profiles, every launch carries a start and a stop event that
 // the runtime stamps with the kernel's own execution interval (hipExtLaunchKernel), the interval a
-// kernel-trace profiler reports, so dispatch latency is not counted; otherwise a plain launch.
+// kernel-trace profiler reports, so dispatch latency is not counted; inside a stream capture the two
+// events become graph nodes around the launch; otherwise a plain launch.
 struct LaunchTimer {
     virtual hipEvent_t event() = 0;
     virtual void done(hipEvent_t start, hipEvent_t stop) = 0;
+    // inside a stream capture: the events become event-record nodes of the capture graph around a
+    // plain launch (mark adds one after the stream's current capture dependencies)
+    virtual bool capturing() const { return false; }
+    virtual void mark(hipStream_t, hipEvent_t) {}
 };
 extern thread_local LaunchTimer* g_launch_timer;
 
@@ -29,7 +34,13 @@ inline void launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, uint32_t lds
 {
     if (LaunchTimer* t = g_launch_timer) {
         hipEvent_t a = t->event(), b = t->event();
-        hipExtLaunchKernelGGL(kernel, grid, block, lds, st, a, b, 0u, args...);
+        if (t->capturing()) {
+            t->mark(st, a);
+            hipLaunchKernelGGL(kernel, grid, block, lds, st, args...);
+            t->mark(st, b);
+        } else {
+            hipExtLaunchKernelGGL(kernel, grid, block, lds, st, a, b, 0u, args...);
+        }
         t->done(a, b);
     } else {
         hipLaunchKernelGGL(kernel, grid, block, lds, st, args...);
@@ -110,6 +121,7 @@ void launch_combine(hipStream_t st, int T, int d, int k, float eps, const float*
 // decode path (kernels_decode.hip): four launches per layer for T <= 16 tokens, Q4_0 / Q8_0
 struct DecLayerH {
     int T, d, E, k, nf, nff, rule, max_tiles;
+    int ncu;  // compute units: the gate|up launch has at most one unit workgroup per CU
     float eps;
     const float *x, *W, *gis, *ds, *pre2, *post1, *post2, *fnorm, *post_ffw, *shared_in;
     const QMat *gu, *dn, *sgu, *sdn;  // sgu / sdn null: no shared FFN computed in the call

@@ -261,6 +261,7 @@ struct Buf {
 
 struct phx_moe_ctx {
     int device = 0;
+    int ncu = 256;  // compute units of the device
     hipStream_t stream = nullptr;
     std::string err;
     float* gelu_tab = nullptr;
@@ -270,8 +271,10 @@ struct phx_moe_ctx {
     int last_T = 0, last_layer = -1;
     // profiling
     bool profiling = false;
-    struct Pending { int kind; hipEvent_t a, b; };
+    struct Pending { int kind; hipEvent_t a, b; bool first = true; };  // first: the call's first kernel
     std::vector<Pending> pending;
+    std::vector<Pending> graph_timing;  // event pairs recorded inside the captured stack
+    bool capturing = false;
     std::vector<hipEvent_t> pool;
     double prof_ms[PHX_K_COUNT] = {};
     int64_t prof_calls[PHX_K_COUNT] = {};
@@ -454,18 +457,45 @@ struct ProfScope : LaunchTimer {
     phx_moe_ctx* c;
     int kind;
     LaunchTimer* prev = nullptr;
-    bool on = false;
+    bool on = false, any = false;
     ProfScope(phx_moe_ctx* c_, int k) : c(c_), kind(k)
     {
         if (c->profiling) {
             on = true;
-            c->prof_calls[kind] += 1;
+            if (!c->capturing) c->prof_calls[kind] += 1;
             prev = g_launch_timer;
             g_launch_timer = this;
         }
     }
-    hipEvent_t event() override { return get_event(c); }
-    void done(hipEvent_t a, hipEvent_t b) override { c->pending.push_back({kind, a, b}); }
+    hipEvent_t event() override
+    {
+        if (!c->capturing) return get_event(c);
+        hipEvent_t e = nullptr;  // owned by the captured graph's timing list
+        (void)hipEventCreate(&e);
+        return e;
+    }
+    void done(hipEvent_t a, hipEvent_t b) override
+    {
+        (c->capturing ? c->graph_timing : c->pending).push_back({kind, a, b, !any});
+        any = true;
+    }
+    bool capturing() const override { return c->capturing; }
+    // an event-record node after the capture's current dependencies, which then move past it (events
+    // recorded through hipEventRecord inside a capture cannot be timed on this runtime)
+    void mark(hipStream_t st, hipEvent_t e) override
+    {
+        hipStreamCaptureStatus status;
+        unsigned long long id;
+        hipGraph_t g;
+        const hipGraphNode_t* deps;
+        size_t nd;
+        if (hipStreamGetCaptureInfo_v2(st, &status, &id, &g, &deps, &nd) != hipSuccess ||
+            status != hipStreamCaptureStatusActive)
+            return;
+        hipGraphNode_t n;
+        if (hipGraphAddEventRecordNode(&n, g, deps, nd, e) != hipSuccess) return;
+        (void)hipStreamUpdateCaptureDependencies(st, &n, 1, hipStreamSetCaptureDependencies);
+    }
     ~ProfScope()
     {
         if (on) g_launch_timer = prev;
@@ -490,6 +520,7 @@ DecLayerH dec_layer(phx_moe_ctx* c, const Layer& L, int T, const float* x, const
     h.nff = D.n_ff_shared;
     h.rule = D.weight_rule;
     h.max_tiles = std::min(n, (n + 1) / 2 + D.n_expert);  // every tile holds one or two assignments
+    h.ncu = c->ncu;
     h.eps = D.eps;
     h.x = x;
     h.W = L.wrow;
@@ -710,6 +741,15 @@ void free_layer(Layer& L)
     L.present = false;
 }
 
+void drop_graph_timing(phx_moe_ctx* c)
+{
+    for (auto& p : c->graph_timing) {
+        (void)hipEventDestroy(p.a);
+        (void)hipEventDestroy(p.b);
+    }
+    c->graph_timing.clear();
+}
+
 int drain_profile(phx_moe_ctx* c)
 {
     if (c->pending.empty()) return PHX_OK;
@@ -768,6 +808,10 @@ int phx_moe_create(int hip_device, phx_moe_ctx** out)
     do {
         hipError_t h;
         if ((h = hipSetDevice(hip_device)) != hipSuccess) { rc = set_err(c, hip_code(h), "hipSetDevice failed"); break; }
+        if ((h = hipDeviceGetAttribute(&c->ncu, hipDeviceAttributeMultiprocessorCount, hip_device)) != hipSuccess) {
+            rc = set_err(c, hip_code(h), "hipDeviceGetAttribute failed");
+            break;
+        }
         if ((h = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking)) != hipSuccess) {
             rc = set_err(c, hip_code(h), "hipStreamCreate failed");
             break;
@@ -805,6 +849,7 @@ void phx_moe_destroy(phx_moe_ctx* c)
         (void)hipEventDestroy(p.b);
     }
     for (auto e : c->pool) (void)hipEventDestroy(e);
+    drop_graph_timing(c);
     if (c->gelu_tab) (void)hipFree(c->gelu_tab);
     if (c->flags) (void)hipFree(c->flags);
     if (c->stream) (void)hipStreamDestroy(c->stream);
@@ -941,16 +986,17 @@ int phx_moe_stack_capture2(phx_moe_ctx* c, int first, int n_layers, int T, unsig
     }
     if (c->graph_exec) { (void)hipGraphExecDestroy(c->graph_exec); c->graph_exec = nullptr; }
     if (c->graph) { (void)hipGraphDestroy(c->graph); c->graph = nullptr; }
-    bool prof = c->profiling;
-    c->profiling = false;
+    drop_graph_timing(c);
     HIPCHK(c, hipStreamSynchronize(c->stream));
     HIPCHK(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+    c->capturing = true;  // while profiling: timing events become graph nodes around each kernel
     int rc = PHX_OK;
     for (int l = first; l < first + n_layers && rc == PHX_OK; l++)
         rc = run_layer(c, c->layers[l], T, wp<float>(c, W_X), nullptr, wp<float>(c, W_OUT), wp<float>(c, W_X), flags);
+    c->capturing = false;
     hipGraph_t g = nullptr;
     hipError_t e = hipStreamEndCapture(c->stream, &g);
-    c->profiling = prof;
+    if (rc || e != hipSuccess) drop_graph_timing(c);
     if (rc) { if (g) (void)hipGraphDestroy(g); return rc; }
     if (e != hipSuccess) return set_err(c, hip_code(e), "stream capture failed: %s", hipGetErrorString(e));
     c->graph = g;
@@ -974,6 +1020,15 @@ int phx_moe_stack_run(phx_moe_ctx* c, float* x, int T, unsigned flags)
     HIPCHK(c, hipMemcpyAsync(x, xs, bytes, dev ? hipMemcpyDeviceToDevice : hipMemcpyDeviceToHost, c->stream));
     c->last_T = T;
     c->last_layer = c->graph_first + c->graph_n - 1;
+    if (c->profiling && !c->graph_timing.empty()) {
+        // a stack captured while profiling: this replay's kernel intervals, read before the next one
+        HIPCHK(c, hipStreamSynchronize(c->stream));
+        for (auto& p : c->graph_timing) {
+            float ms = 0.0f;
+            if (hipEventElapsedTime(&ms, p.a, p.b) == hipSuccess) c->prof_ms[p.kind] += ms;
+            c->prof_calls[p.kind] += p.first;
+        }
+    }
     if (!(flags & PHX_FLAG_ASYNC) || !dev) HIPCHK(c, hipStreamSynchronize(c->stream));
     return PHX_OK;
 }

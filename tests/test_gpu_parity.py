@@ -215,6 +215,37 @@ def test_c5_stack_graph(ctx, pkg, orc, exact):
         assert np.isfinite(eager).all()
 
 
+def test_stack_profiled_replays(ctx, pkg, orc):
+    """A stack captured while profiling carries timing nodes around its kernels: its replays still give
+    the oracle's results, every decode kernel kind reports one timed launch per layer and replay, and
+    later calls run cleanly."""
+    say("c5 stack: 2 layers, T=4, captured while profiling, replayed 3 times")
+    cfg = dict(pkg.synth.CONFIGS["c5_stack"])
+    layers = [layer(pkg, "c5_stack", layer=i) for i in range(2)]
+    for i, L in enumerate(layers):
+        ctx.upload(i, L)
+    x0 = pkg.synth.make_input(cfg, T=4)
+    ref = x0.copy()
+    for L in layers:
+        out, _, _ = orc.moe_block(L, ref)
+        ref = orc.residual(L, ref, out)
+    ctx.profile(True)
+    ctx.stack_capture(0, 2, 4)
+    for rep in range(3):
+        got = ctx.stack_run(x0)
+        ok, emax = within(got, ref)
+        assert ok, f"replay {rep}: max abs err {emax}"
+    prof = ctx.profile_read()
+    ctx.profile(False)
+    say({k: v for k, v in prof.items() if v[1]})
+    for kind in ("router", "gate_up", "down", "combine"):
+        ms, n = prof[kind]
+        assert n == 6 and ms > 0, (kind, ms, n)
+    ctx.stack_capture(0, 2, 4)  # a plain capture again
+    assert within(ctx.stack_run(x0), ref)[0]
+    assert np.isfinite(ctx.ffn(1, x0)).all()
+
+
 @pytest.mark.parametrize("exact", [False, True])
 def test_nonfinite_inputs_route_safely(ctx, pkg, orc, exact):
     """A token with a NaN or an Inf activation has all-NaN router logits; the reference's strict '>'
