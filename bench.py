@@ -29,7 +29,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
-INT8_PEAK_TOPS = 5000.0  # dense int8 MFMA, MI355X
+FP16_PEAK_TFLOPS = 2500.0  # dense fp16 / bf16 MFMA, MI355X
 
 METRIC = "MoE layer tokens/s; decode HBM GB/s vs peak; prefill MFMA util"
 
@@ -163,18 +163,20 @@ def run_layer(args, pkg):
         }
         down_rate = {"down_gbs": round(dn_bytes / (dn_ms * 1e-3) / 1e9, 1)}
     elif mfma:
-        # int8 operations of the routed experts' gate|up products (2 per multiply-add)
+        # multiply-adds of the routed experts' gate|up products (2 flops each), on fp16 MFMA: the
+        # weight and activation integers enter exactly as fp16, so the block sums are exact
         ops = 2.0 * n * 2 * L["n_ff"] * d
         achieved = ops / (gu_ms * 1e-3) / 1e12
         roofline = {
-            "bound": "mfma", "kernel": "gate_up (grouped int8 MFMA, exact block sums + reference float chain)",
-            "achieved": round(achieved, 2), "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
-            "frac": round(achieved / INT8_PEAK_TOPS, 4), "traffic": None,
+            "bound": "mfma", "kernel": "gate_up (grouped fp16 MFMA on exact integer operands: block sums, "
+                                       "scale products, reference float chain)",
+            "achieved": round(achieved, 2), "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(achieved / FP16_PEAK_TFLOPS, 4), "traffic": None,
             "ops_per_launch": int(ops), "avg_launch_us": round(gu_ms * 1e3, 3),
-            "per_unit": f"2 x {2 * L['n_ff']} x {d} int8 ops per assignment x {n} assignments per launch",
+            "per_unit": f"2 x {2 * L['n_ff']} x {d} flops per assignment x {n} assignments per launch",
         }
         dn_ops = 2.0 * n * d * L["n_ff"]
-        down_rate = {"down_tops": round(dn_ops / (dn_ms * 1e-3) / 1e12, 2)}
+        down_rate = {"down_tflops": round(dn_ops / (dn_ms * 1e-3) / 1e12, 2)}
     else:
         gu_bytes = avg_experts * gu_b
         achieved = gu_bytes / (gu_ms * 1e-3) / 1e9
@@ -215,7 +217,7 @@ def run_layer(args, pkg):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8",
+        "dtype": "fp16" if mfma else "int8",  # the products' arithmetic: fp16 MFMA, or int8 dot4 on VALU
         "data": "synthetic",
         "config": {
             "workload": f"{cfg_name}: MoE FFN layer, T={T}, d={d}, E={E}, top-{k}, "

@@ -1,27 +1,36 @@
 // Prefill-shaped grouped products on the matrix cores (gfx950 MFMA), Q4_0 and Q8_0 weights.
 //
 // The reference row dot is, per 32-element block b, sum += (float)isum_b * (d_w * d_x) in block
-// order (src/CpuRefGemma.cs:27-36, src/CpuRef.cs:106-115).  Here the integer block sums of a
-// 32-row x 32-token tile come from one v_mfma_i32_32x32x32_i8 per block (exact int32), and the
-// float chain runs on VALU in block order for every (row, token), so results equal the CPU
-// reference bit for bit.  Q4_0 nibbles enter the MFMA as 0..15; a second MFMA with a constant -8
-// operand adds -8 * sum_k q_x, giving the signed block sums without per-element work.
+// order (src/CpuRefGemma.cs:27-36, src/CpuRef.cs:106-115).  Per block and 32 x 32 (row, token) tile:
+//   - two v_mfma_f32_32x32x16_f16 give isum_b exactly as floats: the weights enter as the integers
+//     q_w - 8 (Q4_0) or q_w (Q8_0) and the activations as their Q8_0 integers, all exact in fp16, and
+//     every partial sum is an integer below 2^24, so the fp32 accumulation is exact in any order;
+//   - one more v_mfma_f32_32x32x16_f16 with a single nonzero k forms d_w * d_x for the whole tile:
+//     both scales are fp16 values, so the products are exact in fp32;
+//   - the float chain runs on VALU, one multiply and one add per (row, token, block), in block order,
+//     so results equal the CPU reference bit for bit.
 //
-// Operand layout (verified on gfx950): A lane l holds row l % 32 and 16 of the block's 32 k values
-// (lanes 0-31 one set, 32-63 the other); B lane l holds token l % 32 and the same k set; the
-// 32 x 32 result C[i][j] sits in lane j + 32 * ((i / 4) % 2), register (i % 4) + 4 * (i / 8).  Q4_0
-// lanes 0-31 take the low nibbles (elements 0-15) and 32-63 the high nibbles (16-31).
+// Operand layout of v_mfma_f32_32x32x16_f16 (verified on gfx950): A lane l holds row l % 32 and the
+// eight k values 8 (l / 32) + e, e = 0..7; B lane l holds column l % 32 and the same k; the 32 x 32
+// result C[i][j] sits in lane j + 32 * ((i / 4) % 2), register (i % 4) + 4 * (i / 8).
+//
+// Work layout: a workgroup of four waves covers two row groups (128 rows; wave w: 32 rows) and one
+// tile of up to 128 assignments (four 32-token column tiles; the empty ones are skipped).  Per block,
+// the tile's activation bytes are staged in LDS once for the four waves, converted to fp16 (token
+// rows of 40 halves, an 80-byte stride that keeps the 16-byte reads free of bank conflicts); the
+// weights stream two blocks ahead in registers, the activations one block ahead.
 #include "device_common.h"
 
 namespace phx {
 
-typedef int mv4i __attribute__((ext_vector_type(4)));
-typedef int mv16i __attribute__((ext_vector_type(16)));
+typedef _Float16 mh8 __attribute__((ext_vector_type(8)));
+typedef _Float16 mh2 __attribute__((ext_vector_type(2)));
+typedef float mf16 __attribute__((ext_vector_type(16)));
 
 struct MmaArgs {
     const uint8_t* payload;
     const uint8_t* scale;
-    int64_t mat_pay, mat_sc, rg_pay;
+    int64_t mat_pay, mat_sc, rg_pay, sc_off;
     int rg, nb, rows;
     Act act;
     const Tile* tiles;
@@ -34,113 +43,150 @@ struct MmaArgs {
     bool paired;
 };
 
-constexpr int MMA_NTOK = 2;  // 32-token column tiles per wave: tiles of up to 64 assignments
+constexpr int MMA_NT = 4;                 // 32-token column tiles per workgroup
+constexpr int MMA_TOK = 32 * MMA_NT;      // tile capacity (kMmaTile)
+constexpr int MMA_LDS_TOK = 40;           // halves per staged token row
+static_assert(MMA_TOK == kMmaTile, "tile capacity");
 
-template <int TYPE>
-__global__ __launch_bounds__(256) void k_grouped_mfma(MmaArgs g)
+// Bytes to exact fp16 pairs by the 1024-bias: the half with bits 0x64XX is 1024 + XX.  Returns the
+// pair (byte 2p, byte 2p + 1) of w minus `bias` (1152 gives a signed int8 from w ^ 0x80808080,
+// 1032 gives q - 8 from a nibble).
+__device__ __forceinline__ uint32_t bias_pair(uint32_t w, int p, float bias)
 {
-    const int tile = blockIdx.y;
-    if (tile >= *g.ntiles) return;
-    const Tile tl = g.tiles[tile];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int r32 = lane & 31, h = lane >> 5;
-    const int R0 = blockIdx.x * 128 + wave * 32;  // first (repacked) row of this wave's slice
-    const int gI = R0 >> 6, half = (R0 >> 5) & 1;
-    if (gI >= g.rg) return;  // no barriers below: a wave past the last row group just stops
+    const uint32_t b = __builtin_amdgcn_perm(0x64646464u, w, p ? 0x04030402u : 0x04010400u);
+    mh2 v = __builtin_bit_cast(mh2, b);
+    v = v - mh2{(_Float16)bias, (_Float16)bias};
+    return __builtin_bit_cast(uint32_t, v);
+}
+
+// eight values of two dwords as an mh8 operand
+__device__ __forceinline__ mh8 bias8(uint32_t w0, uint32_t w1, float bias)
+{
+    const uint4 u = make_uint4(bias_pair(w0, 0, bias), bias_pair(w0, 1, bias), bias_pair(w1, 0, bias),
+                               bias_pair(w1, 1, bias));
+    return __builtin_bit_cast(mh8, u);
+}
+
+// One workgroup's tile: NJ active 32-token column tiles (1..4), every block's MFMAs issued before the
+// chain's VALU work.  sx / sdx: the workgroup's LDS staging buffers.
+template <int TYPE, int NJ>
+__device__ __forceinline__ void mma_tile(const MmaArgs& g, const Tile& tl, int cnt, uint32_t* sx, unsigned short* sdx)
+{
     constexpr int PAY = TYPE == PHX_Q4_0_DEV ? 16 : 32;
+    constexpr int XW = MMA_TOK * MMA_LDS_TOK / 2;  // dwords per staging buffer
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, r32 = lane & 31, h = lane >> 5;
+    const int gI = blockIdx.x * 2 + (wave >> 1), half = wave & 1;
+    const bool live = gI < g.rg;  // a wave past the last row group computes a clamped one, stores nothing
     const int nb = g.nb;
 
-    // the tile's tokens: column r32 of each 32-token column tile
-    int orow[MMA_NTOK];
-    int64_t arow[MMA_NTOK];
-    bool valid[MMA_NTOK];
-#pragma unroll
-    for (int j = 0; j < MMA_NTOK; j++) {
-        const int s = 32 * j + r32;
-        valid[j] = s < tl.cnt;
-        orow[j] = valid[j] ? g.perm[tl.start + s] : 0;
-        arow[j] = orow[j] / g.act_div;
-    }
-    const uint8_t* pay = g.payload + tl.e * g.mat_pay + gI * g.rg_pay + (half * 32 + r32) * PAY;
-    const uint16_t* scl = (const uint16_t*)(g.scale + tl.e * g.mat_sc) + (int64_t)gI * nb * 64 + half * 32 + 4 * h;
-    const mv4i neg8 = {(int)0xF8F8F8F8u, (int)0xF8F8F8F8u, (int)0xF8F8F8F8u, (int)0xF8F8F8F8u};
-    const mv16i zero = {};
+    // staging: thread tid brings token tid / 2, bytes 16 (tid % 2) .. + 15 of each block
+    const int st_tok = tid >> 1, st_part = tid & 1;
+    const bool st_valid = st_tok < cnt;
+    const int64_t st_row = st_valid ? (int64_t)(g.perm[tl.start + st_tok] / g.act_div) : 0;
+    const uint8_t* st_q = (const uint8_t*)g.act.q + st_row * g.act.qstride + 16 * st_part;
+    const float* st_d = g.act.d + st_row * g.act.dstride;
+    uint4 xq;
+    float xd;
+    auto load_x = [&](int b) {
+        xq = *(const uint4*)(st_q + (int64_t)b * 32);
+        xd = st_d[b];
+    };
+    const uint32_t st_mask = st_valid ? ~0u : 0u;  // invalid tokens: zero bytes (0x80 after the flip -> 0)
+    // unconditional in every thread (both threads of a token write the same scale), so the compiler
+    // keeps the loads where they are issued instead of sinking them to a conditional use
+    auto store_x = [&](int buf) {
+        const uint4 u = make_uint4((xq.x & st_mask) ^ 0x80808080u, (xq.y & st_mask) ^ 0x80808080u,
+                                   (xq.z & st_mask) ^ 0x80808080u, (xq.w & st_mask) ^ 0x80808080u);
+        uint32_t* dst = sx + buf * XW + st_tok * (MMA_LDS_TOK / 2) + 8 * st_part;
+        *(uint4*)dst = make_uint4(bias_pair(u.x, 0, 1152.0f), bias_pair(u.x, 1, 1152.0f), bias_pair(u.y, 0, 1152.0f),
+                                  bias_pair(u.y, 1, 1152.0f));
+        *(uint4*)(dst + 4) = make_uint4(bias_pair(u.z, 0, 1152.0f), bias_pair(u.z, 1, 1152.0f),
+                                        bias_pair(u.w, 0, 1152.0f), bias_pair(u.w, 1, 1152.0f));
+        sdx[buf * MMA_TOK + st_tok] = (unsigned short)(f2h_bits(xd) & st_mask);  // xd is an fp16 value
+    };
 
-    float S[MMA_NTOK][16];
+    // weights: lane (row 32 half + r32, h) reads the payload bytes of its k values and its row's fp16
+    // scale from the row group's scale groups
+    const int gIc = min(gI, g.rg - 1);
+    const uint8_t* rgp = g.payload + tl.e * g.mat_pay + gIc * g.rg_pay;
+    const int wrow = half * 32 + r32;
+    struct WB {
+        uint2 q0, q1;  // Q4_0: q0 = bytes 8h..8h+7; Q8_0: q0 = bytes 8h.., q1 = bytes 16 + 8h..
+        uint32_t sc;   // fp16 scale bits of the block (row wrow)
+    };
+    auto load_w = [&](int b, WB& w) {
+        const uint8_t* pb = rgp + ((int64_t)b * 64 + wrow) * PAY + 8 * h;
+        w.q0 = *(const uint2*)pb;
+        w.q1 = TYPE == PHX_Q4_0_DEV ? w.q0 : *(const uint2*)(pb + 16);
+        w.sc = *(const uint16_t*)(rgp + g.sc_off + ((int64_t)(b >> 3) * 64 + wrow) * 16 + (b & 7) * 2);
+    };
+
+    mf16 S[NJ];
 #pragma unroll
-    for (int j = 0; j < MMA_NTOK; j++)
+    for (int j = 0; j < NJ; j++)
 #pragma unroll
         for (int q = 0; q < 16; q++) S[j][q] = 0.0f;
+    const mf16 zero = {};
+    const uint32_t hmask = h == 0 ? 0xFFFFu : 0u;  // the scale MFMA's single k sits in lanes 0-31, element 0
 
-    // operands of one block, loaded one block ahead of their use (software pipelining)
-    struct Stage {
-        uint4 w;               // Q4_0: the row's 16 payload bytes; Q8_0: this lane's 16 of 32
-        uint2 sc[4];           // fp16 scales of the 16 result rows
-        mv4i B[MMA_NTOK];
-        float dx[MMA_NTOK];
-    };
-    auto load = [&](int b, Stage& st) {
-        st.w = *(const uint4*)(pay + (int64_t)b * 64 * PAY + (TYPE == PHX_Q4_0_DEV ? 0 : 16 * h));
-#pragma unroll
-        for (int qq = 0; qq < 4; qq++) st.sc[qq] = *(const uint2*)(scl + (int64_t)b * 64 + 8 * qq);
-#pragma unroll
-        for (int j = 0; j < MMA_NTOK; j++) {
-            if (valid[j]) {
-                st.B[j] = *(const mv4i*)(g.act.q + arow[j] * g.act.qstride + b * 32 + 16 * h);
-                st.dx[j] = g.act.d[arow[j] * g.act.dstride + b];
-            } else {
-                st.B[j] = mv4i{0, 0, 0, 0};
-                st.dx[j] = 0.0f;
-            }
-        }
-    };
-    auto compute = [&](const Stage& st) {
-        mv4i A;
+    // one block: block b + 1's loads first, then block b from the weights in w and the staged rows;
+    // tile j + 1's products go out before tile j's chain, so the matrix cores overlap the VALU work
+    WB w, wn;
+    load_x(0);
+    load_w(0, w);
+    store_x(0);
+    __syncthreads();
+    for (int b = 0; b < nb; b++) {
+        const int buf = b & 1;
+        load_x(min(b + 1, nb - 1));
+        load_w(min(b + 1, nb - 1), wn);
+        mh8 A0, A1;
         if (TYPE == PHX_Q4_0_DEV) {
-            const unsigned sh = h ? 4u : 0u;
-            A.x = (int)((st.w.x >> sh) & 0x0F0F0F0Fu);
-            A.y = (int)((st.w.y >> sh) & 0x0F0F0F0Fu);
-            A.z = (int)((st.w.z >> sh) & 0x0F0F0F0Fu);
-            A.w = (int)((st.w.w >> sh) & 0x0F0F0F0Fu);
+            A0 = bias8(w.q0.x & 0x0F0F0F0Fu, w.q0.y & 0x0F0F0F0Fu, 1032.0f);
+            A1 = bias8((w.q0.x >> 4) & 0x0F0F0F0Fu, (w.q0.y >> 4) & 0x0F0F0F0Fu, 1032.0f);
         } else {
-            A = mv4i{(int)st.w.x, (int)st.w.y, (int)st.w.z, (int)st.w.w};
+            A0 = bias8(w.q0.x ^ 0x80808080u, w.q0.y ^ 0x80808080u, 1152.0f);
+            A1 = bias8(w.q1.x ^ 0x80808080u, w.q1.y ^ 0x80808080u, 1152.0f);
         }
-        float dw[16];
+        const mh8 Ad = __builtin_bit_cast(mh8, make_uint4(w.sc & hmask, 0u, 0u, 0u));
+        const uint32_t* xb = sx + buf * XW;
+        auto products = [&](int j, mf16& C, mf16& D) {
+            const uint32_t* row = xb + (32 * j + r32) * (MMA_LDS_TOK / 2);
+            const mh8 B0 = __builtin_bit_cast(mh8, *(const uint4*)(row + 4 * h));
+            const mh8 B1 = __builtin_bit_cast(mh8, *(const uint4*)(row + 8 + 4 * h));
+            const uint32_t dxb = sdx[buf * MMA_TOK + 32 * j + r32];
+            const mh8 Bd = __builtin_bit_cast(mh8, make_uint4(dxb & hmask, 0u, 0u, 0u));
+            C = __builtin_amdgcn_mfma_f32_32x32x16_f16(A0, B0, zero, 0, 0, 0);
+            C = __builtin_amdgcn_mfma_f32_32x32x16_f16(A1, B1, C, 0, 0, 0);
+            D = __builtin_amdgcn_mfma_f32_32x32x16_f16(Ad, Bd, zero, 0, 0, 0);
+        };
+        mf16 C, D;
+        products(0, C, D);
 #pragma unroll
-        for (int qq = 0; qq < 4; qq++) {
-            dw[4 * qq + 0] = h2f(st.sc[qq].x & 0xFFFFu);
-            dw[4 * qq + 1] = h2f(st.sc[qq].x >> 16);
-            dw[4 * qq + 2] = h2f(st.sc[qq].y & 0xFFFFu);
-            dw[4 * qq + 3] = h2f(st.sc[qq].y >> 16);
-        }
-#pragma unroll
-        for (int j = 0; j < MMA_NTOK; j++) {
-            mv16i C = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, st.B[j], zero, 0, 0, 0);
-            if (TYPE == PHX_Q4_0_DEV) C = __builtin_amdgcn_mfma_i32_32x32x32_i8(neg8, st.B[j], C, 0, 0, 0);
+        for (int j = 0; j < NJ; j++) {
+            mf16 Cn, Dn;
+            if (j + 1 < NJ) products(j + 1, Cn, Dn);
             // the reference chain: sum += (float)isum * (d_w * d_x), in block order
 #pragma unroll
-            for (int q = 0; q < 16; q++) {
-                const float dd = dw[q] * st.dx[j];
-                S[j][q] = S[j][q] + (float)C[q] * dd;
+            for (int q = 0; q < 16; q++) S[j][q] = S[j][q] + C[q] * D[q];
+            if (j + 1 < NJ) {
+                C = Cn;
+                D = Dn;
             }
         }
-    };
-    Stage s0, s1;
-    load(0, s0);
-    int b = 0;
-    for (; b + 2 <= nb; b += 2) {
-        load(b + 1, s1);
-        compute(s0);
-        if (b + 2 < nb) load(b + 2, s0);
-        compute(s1);
+        store_x(buf ^ 1);  // that buffer was last read before the previous barrier (after the last block:
+                           // a harmless write of a buffer nobody reads again)
+        w = wn;
+        __syncthreads();
     }
-    if (b < nb) compute(s0);  // odd block count: the last block is in s0
 
-    // results: lane holds rows i_q = 8 (q / 4) + 4 h + (q % 4) of the slice, token column r32
+    // results: lane holds rows i_q = 8 (q / 4) + 4 h + (q % 4) of the wave's 32, token column r32
+    if (!live) return;
 #pragma unroll
-    for (int j = 0; j < MMA_NTOK; j++) {
-        if (!valid[j]) continue;
-        const int64_t a = orow[j];
+    for (int j = 0; j < NJ; j++) {
+        const int sidx = 32 * j + r32;
+        if (sidx >= cnt) continue;
+        const int64_t a = g.perm[tl.start + sidx];
 #pragma unroll
         for (int q = 0; q < 16; q++) {
             const int lg = half * 32 + 8 * (q >> 2) + 4 * h + (q & 3);  // lane within the row group
@@ -158,6 +204,23 @@ __global__ __launch_bounds__(256) void k_grouped_mfma(MmaArgs g)
     }
 }
 
+template <int TYPE>
+__global__ __launch_bounds__(256) void k_grouped_mfma(MmaArgs g)
+{
+    __shared__ __align__(16) uint32_t sx[2 * MMA_TOK * MMA_LDS_TOK / 2];  // fp16 token rows of one block
+    __shared__ unsigned short sdx[2 * MMA_TOK];                            // their scales' fp16 bits
+    const int tile = blockIdx.y;
+    if (tile >= *g.ntiles) return;  // uniform over the workgroup
+    const Tile tl = g.tiles[tile];
+    const int cnt = min(tl.cnt, MMA_TOK);
+    switch ((cnt + 31) / 32) {  // active 32-token column tiles
+    case 1: mma_tile<TYPE, 1>(g, tl, cnt, sx, sdx); break;
+    case 2: mma_tile<TYPE, 2>(g, tl, cnt, sx, sdx); break;
+    case 3: mma_tile<TYPE, 3>(g, tl, cnt, sx, sdx); break;
+    default: mma_tile<TYPE, 4>(g, tl, cnt, sx, sdx); break;
+    }
+}
+
 void launch_grouped_mfma(hipStream_t st, const QMat& w, Act act, const Tile* tiles, const int* ntiles, int max_tiles,
                          const int* perm, int act_div, float* out0, float* out1, int split, int out_stride)
 {
@@ -166,6 +229,7 @@ void launch_grouped_mfma(hipStream_t st, const QMat& w, Act act, const Tile* til
     g.scale = w.scale;
     g.mat_pay = w.mat_pay_stride();
     g.rg_pay = w.rg_pay;
+    g.sc_off = w.sc8_off();
     g.mat_sc = w.mat_sc_stride();
     g.rg = w.rg;
     g.nb = w.nb;

@@ -112,7 +112,7 @@ void launch_grouped(hipStream_t st, const QMat& w, Act act, const Tile* tiles, c
 void launch_requant(hipStream_t st, int rows, int nf, const float* g, const float* u, const float* gelu_tab, Act act);
 // prefill path (kernels_prefill.hip): Q4_0 / Q8_0 grouped products on MFMA, tiles of up to kMmaTile
 // assignments; same arguments and outputs as launch_grouped
-constexpr int kMmaTile = 64;
+constexpr int kMmaTile = 128;
 void launch_grouped_mfma(hipStream_t st, const QMat& w, Act act, const Tile* tiles, const int* ntiles, int max_tiles,
                          const int* perm, int act_div, float* out0, float* out1, int split, int out_stride);
 void launch_combine(hipStream_t st, int T, int d, int k, float eps, const float* yd, const float* w,

@@ -331,6 +331,10 @@ MFMA_CASES = {
     "q8_0_shared_T64": (dict(idx=12, T=64, d=512, E=8, k=2, nf=256, gu=8, dn=8, nff=256, sh=8), 64, False),
     "c2_T64_shared_only": ("c2_decode", 64, False),
     "c3_T128": ("c3_prefill", 128, False),
+    # about 128 assignments per expert: full and partial 128-token tiles; 9 paired row groups (an odd
+    # count leaves a workgroup with a spare wave pair), 608 down rows, odd block counts (19 and 9)
+    "q4_0_T256_full_tiles": (dict(idx=13, T=256, d=608, E=4, k=2, nf=288, gu=2, dn=2), 256, False),
+    "q8_0_T256_full_tiles": (dict(idx=14, T=256, d=512, E=4, k=2, nf=256, gu=8, dn=8), 256, False),
 }
 
 
