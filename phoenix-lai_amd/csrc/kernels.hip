@@ -18,30 +18,22 @@ __device__ void quantize_row(const float* v, Act act, int64_t row)
 {
     const int tid = threadIdx.x;
     if (act.fmt == ACT_Q8_0) {
-        int nb = act.cols / 32;
-        for (int b = tid; b < nb; b += NT) {
-            const float* x = v + b * 32;
-            float amax = 0.0f;
-            for (int j = 0; j < 32; j++) { float a = fabsf(x[j]); if (a > amax) amax = a; }
-            float d = amax / 127.0f;
-            float id = d != 0.0f ? 1.0f / d : 0.0f;
-            uint32_t dh = f2h_bits(d);
-            uint32_t w[8];
-            int sum = 0;
-            for (int j = 0; j < 32; j += 4) {
-                uint32_t pk = 0;
-                for (int m = 0; m < 4; m++) {
-                    int q = (int)roundf(x[j + m] * id);
-                    sum += q;
-                    pk |= (uint32_t)(q & 0xFF) << (8 * m);
+        // eight lanes per 32-block, four values each (q8_0_oct); every thread runs the same number of
+        // rounds (the shuffles need whole 8-lane groups), rounds past the last block store nothing
+        const int nb = act.cols / 32, g = tid >> 3, l8 = tid & 7;
+        for (int b0 = 0; b0 < nb; b0 += NT / 8) {
+            const int b = b0 + g, bc = min(b, nb - 1);
+            const float4 xv = *(const float4*)(v + bc * 32 + 4 * l8);
+            float dval;
+            int sum;
+            const int qw = q8_0_oct(xv, &dval, &sum);
+            if (b < nb) {
+                ((int*)(act.q + row * act.qstride))[8 * b + l8] = qw;
+                if (l8 == 0) {
+                    act.d[row * act.dstride + b] = dval;
+                    act.s[row * act.sstride + b] = sum;
                 }
-                w[j / 4] = pk;
             }
-            uint4* dst = (uint4*)(act.q + row * act.qstride + b * 32);
-            dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
-            dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
-            act.d[row * act.dstride + b] = h2f(dh);
-            act.s[row * act.sstride + b] = sum;
         }
         return;
     }
@@ -100,21 +92,36 @@ __global__ __launch_bounds__(NT) void k_prologue(int d, float eps, const float* 
                                                  const float* __restrict__ ffn_norm, float* __restrict__ router_in,
                                                  float* __restrict__ xscale, Act act_gu, Act act_sh, int* flags)
 {
-    extern __shared__ float sbuf[];
+    extern __shared__ __align__(16) float sbuf[];
     __shared__ double red[NT];
     const int t = blockIdx.x, tid = threadIdx.x;
     const float* xr = x + (int64_t)t * d;
     float scale = rms_scale_from_mean(mean_sq_cert<NT>(xr, d, red, flags), eps);
     float sc = 1.0f / (float)__dsqrt_rn((double)d);
     float* ri = router_in + (int64_t)t * d;
-    for (int i = tid; i < d; i += NT) ri[i] = xr[i] * scale * sc * gis[i];
-    int cols = act_gu.cols;
-    for (int i = tid; i < cols; i += NT) sbuf[i] = i < d ? xr[i] * scale * pre2[i] : 0.0f;
+    // four values per thread and round (d and the activation widths are multiples of 32)
+    const float4* x4 = (const float4*)xr;
+    auto fill = [&](const float* nw, int cols) {
+        for (int i4 = tid; i4 < cols / 4; i4 += NT) {
+            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (4 * i4 < d) {
+                const float4 xv = x4[i4], nv = ((const float4*)nw)[i4];
+                v = make_float4(xv.x * scale * nv.x, xv.y * scale * nv.y, xv.z * scale * nv.z, xv.w * scale * nv.w);
+            }
+            ((float4*)sbuf)[i4] = v;
+        }
+    };
+    for (int i4 = tid; i4 < d / 4; i4 += NT) {
+        const float4 xv = x4[i4], gv = ((const float4*)gis)[i4];
+        ((float4*)ri)[i4] = make_float4(xv.x * scale * sc * gv.x, xv.y * scale * sc * gv.y, xv.z * scale * sc * gv.z,
+                                        xv.w * scale * sc * gv.w);
+    }
+    fill(pre2, act_gu.cols);
     __syncthreads();
     quantize_row<NT>(sbuf, act_gu, t);
     if (ffn_norm) {
         __syncthreads();
-        for (int i = tid; i < act_sh.cols; i += NT) sbuf[i] = i < d ? xr[i] * scale * ffn_norm[i] : 0.0f;
+        fill(ffn_norm, act_sh.cols);
         __syncthreads();
         quantize_row<NT>(sbuf, act_sh, t);
     }
@@ -284,67 +291,118 @@ void launch_topk(hipStream_t st, int T, int E, int k, int rule, const float* log
 // (expert, first list position, count <= A) tiles for the grouped kernels.
 // chunks of the stable counting sort: at most 256 (one per thread) and at most 16,384 / E so the
 // u16 histogram stays within 32 KB of LDS
-__host__ __device__ inline int dispatch_chunks(int n, int E)
+// One workgroup of 16 waves; wave w owns the contiguous segment w of the assignments and walks it 64
+// at a time.  In a batch, eight ballots over the expert-id bits give each lane the mask of the lanes
+// holding the same expert: its rank among them (a popcount of the lower lanes) and their count, so no
+// lane waits on another.  Pass 1 counts each segment's experts, a prefix over (expert, segment) gives
+// the list offsets and every segment's start in every list, pass 2 places the assignments: the lists
+// come out in ascending assignment order (a stable counting sort, the lists of KernelsMoe.Bucket).
+constexpr int DSP_NT = 1024, DSP_SEG = DSP_NT / 64;
+
+__device__ __forceinline__ uint64_t same_expert_mask(int e, bool valid, int nbits)
 {
-    int c = n < 256 ? (n > 0 ? n : 1) : 256;
-    int cap = 16384 / (E > 0 ? E : 1);
-    return c < cap ? c : (cap > 0 ? cap : 1);
+    uint64_t m = __ballot(valid);
+    for (int b = 0; b < nbits; b++) {
+        const bool bit = (e >> b) & 1;
+        const uint64_t v = __ballot(bit);
+        m &= bit ? v : ~v;
+    }
+    return valid ? m : 0ull;
 }
 
-__global__ __launch_bounds__(256) void k_dispatch(int n, int E, int A, const int* __restrict__ ids,
-                                                  int* __restrict__ offsets, int* __restrict__ perm,
-                                                  Tile* __restrict__ tiles, int* __restrict__ ntiles)
+__global__ __launch_bounds__(DSP_NT) void k_dispatch(int n, int E, int A, const int* __restrict__ ids,
+                                                     int* __restrict__ offsets, int* __restrict__ perm,
+                                                     Tile* __restrict__ tiles, int* __restrict__ ntiles)
 {
-    extern __shared__ uint16_t hist[];  // [E][nch]
-    __shared__ int tot[PHX_MAX_EXPERTS_DEV + 1], toff[PHX_MAX_EXPERTS_DEV + 1], tb[PHX_MAX_EXPERTS_DEV + 1];
-    const int tid = threadIdx.x;
-    const int nch = dispatch_chunks(n, E);
-    const int cs = (n + nch - 1) / nch;
-    for (int i = tid; i < E * nch; i += 256) hist[i] = 0;
+    __shared__ int cnt[DSP_SEG][PHX_MAX_EXPERTS_DEV];
+    __shared__ int toff[PHX_MAX_EXPERTS_DEV + 1], tb[PHX_MAX_EXPERTS_DEV + 1];
+    __shared__ int wsum[2][DSP_SEG];
+    extern __shared__ uint8_t sid[];  // the expert ids as bytes [n]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int nbits = 0;
+    while ((1 << nbits) < E) nbits++;
+    for (int i = tid; i < DSP_SEG * PHX_MAX_EXPERTS_DEV; i += DSP_NT) (&cnt[0][0])[i] = 0;
+    // the ids (written by the previous launch: cold reads) in batches of 16 loads per thread
+    for (int i0 = tid; i0 < n; i0 += DSP_NT * 16) {
+        int v[16];
+#pragma unroll
+        for (int u = 0; u < 16; u++) v[u] = ids[min(i0 + DSP_NT * u, n - 1)];
+#pragma unroll
+        for (int u = 0; u < 16; u++)
+            if (i0 + DSP_NT * u < n) sid[i0 + DSP_NT * u] = (uint8_t)clamp_id(v[u], E);
+    }
+    const int seg = (n + DSP_SEG - 1) / DSP_SEG, s0 = min(n, wave * seg), s1 = min(n, s0 + seg);
+    const uint64_t lower = (1ull << lane) - 1ull;
     __syncthreads();
-    const int a0 = tid * cs, a1 = min(n, a0 + cs);
-    if (tid < nch)
-        for (int a = a0; a < a1; a++) hist[clamp_id(ids[a], E) * nch + tid]++;
-    __syncthreads();
-    if (tid < E) {
-        int run = 0;
-        for (int c = 0; c < nch; c++) {
-            int h = hist[tid * nch + c];
-            hist[tid * nch + c] = (uint16_t)run;
-            run += h;
-        }
-        tot[tid] = run;
+    // pass 1: per segment and expert, the count (the lowest lane of each expert adds its batch count)
+    for (int a0 = s0; a0 < s1; a0 += 64) {
+        const int a = a0 + lane;
+        const bool valid = a < s1;
+        const int e = valid ? sid[a] : 0;
+        const uint64_t m = same_expert_mask(e, valid, nbits);
+        if (valid && (m & lower) == 0) cnt[wave][e] += __popcll(m);
     }
     __syncthreads();
-    if (tid == 0) {
-        int r = 0, tr = 0;
-        for (int e = 0; e < E; e++) {
-            toff[e] = r;
-            r += tot[e];
-            tb[e] = tr;
-            tr += (tot[e] + A - 1) / A;
+    // per expert: total, tile count, and each segment's start within the expert's list
+    int c = 0, tcount = 0;
+    if (tid < E) {
+        for (int w = 0; w < DSP_SEG; w++) {
+            const int h = cnt[w][tid];
+            cnt[w][tid] = c;
+            c += h;
         }
-        toff[E] = r;
-        tb[E] = tr;
-        *ntiles = tr;
+        tcount = (c + A - 1) / A;
+    }
+    // exclusive scans of c and tcount over the experts (E <= 256: threads 0-255)
+    int v1 = c, v2 = tcount;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y1 = __shfl_up(v1, o, 64), y2 = __shfl_up(v2, o, 64);
+        if (lane >= o) {
+            v1 += y1;
+            v2 += y2;
+        }
+    }
+    if (lane == 63) {
+        wsum[0][wave] = v1;
+        wsum[1][wave] = v2;
     }
     __syncthreads();
-    for (int e = tid; e <= E; e += 256) offsets[e] = toff[e];
-    if (tid < nch)
-        for (int a = a0; a < a1; a++) {
-            int e = clamp_id(ids[a], E);
-            int pos = toff[e] + hist[e * nch + tid];
-            hist[e * nch + tid]++;
-            perm[pos] = a;
-        }
+    int b1 = 0, b2 = 0;
+    for (int w = 0; w < wave; w++) {
+        b1 += wsum[0][w];
+        b2 += wsum[1][w];
+    }
     if (tid < E) {
-        int c = tot[tid], base = tb[tid];
-        for (int s = 0; s * A < c; s++) {
+        toff[tid] = b1 + v1 - c;
+        tb[tid] = b2 + v2 - tcount;
+    }
+    if (tid == PHX_MAX_EXPERTS_DEV - 1) {  // the scans' totals: experts past E hold zeros
+        toff[E] = b1 + v1;
+        tb[E] = b2 + v2;
+        *ntiles = b2 + v2;
+    }
+    __syncthreads();
+    for (int e = tid; e <= E; e += DSP_NT) offsets[e] = toff[e];
+    // pass 2: placement in assignment order
+    for (int a0 = s0; a0 < s1; a0 += 64) {
+        const int a = a0 + lane;
+        const bool valid = a < s1;
+        const int e = valid ? sid[a] : 0;
+        const uint64_t m = same_expert_mask(e, valid, nbits);
+        const int base = valid ? toff[e] + cnt[wave][e] : 0;
+        if (valid) perm[base + __popcll(m & lower)] = a;
+        __builtin_amdgcn_wave_barrier();  // every lane has read cnt before the batch's leaders advance it
+        if (valid && (m & lower) == 0) cnt[wave][e] += __popcll(m);
+    }
+    if (tid < E) {
+        const int base = tb[tid];
+        for (int q = 0; q * A < c; q++) {
             Tile tl;
             tl.e = tid;
-            tl.start = toff[tid] + s * A;
-            tl.cnt = min(A, c - s * A);
-            tiles[base + s] = tl;
+            tl.start = toff[tid] + q * A;
+            tl.cnt = min(A, c - q * A);
+            tiles[base + q] = tl;
         }
     }
 }
@@ -352,9 +410,8 @@ __global__ __launch_bounds__(256) void k_dispatch(int n, int E, int A, const int
 void launch_dispatch(hipStream_t st, int n, int E, int A, const int* ids, int* offsets, int* perm, Tile* tiles,
                      int* ntiles)
 {
-    int nch = dispatch_chunks(n, E);
-    launch(k_dispatch, dim3(1), dim3(256), (size_t)E * nch * sizeof(uint16_t), st, n, E, A, ids, offsets,
-                       perm, tiles, ntiles);
+    (void)hipFuncSetAttribute((const void*)k_dispatch, hipFuncAttributeMaxDynamicSharedMemorySize, n);
+    launch(k_dispatch, dim3(1), dim3(DSP_NT), (uint32_t)n, st, n, E, A, ids, offsets, perm, tiles, ntiles);
 }
 
 // ------------------------------------------------------------------------------ grouped row products
@@ -614,11 +671,21 @@ void launch_grouped(hipStream_t st, const QMat& w, Act act, const Tile* tiles, c
 __global__ __launch_bounds__(256) void k_requant(int nf, const float* __restrict__ g, const float* __restrict__ u,
                                                  const float* __restrict__ tab, Act act)
 {
-    extern __shared__ float sbuf[];
+    extern __shared__ __align__(16) float sbuf[];
     const int64_t r = blockIdx.x;
     const int tid = threadIdx.x;
-    for (int i = tid; i < act.cols; i += 256)
-        sbuf[i] = i < nf ? gelu_ref(g[r * nf + i], tab) * u[r * nf + i] : 0.0f;
+    // four values per thread and round (nf and cols are multiples of 32)
+    const float4* g4 = (const float4*)(g + r * nf);
+    const float4* u4 = (const float4*)(u + r * nf);
+    for (int i4 = tid; i4 < act.cols / 4; i4 += 256) {
+        float4 e = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (4 * i4 < nf) {
+            const float4 gv = g4[i4], uv = u4[i4];
+            e = make_float4(gelu_ref(gv.x, tab) * uv.x, gelu_ref(gv.y, tab) * uv.y, gelu_ref(gv.z, tab) * uv.z,
+                            gelu_ref(gv.w, tab) * uv.w);
+        }
+        ((float4*)sbuf)[i4] = e;
+    }
     __syncthreads();
     quantize_row<256>(sbuf, act, r);
 }
@@ -640,13 +707,35 @@ __global__ __launch_bounds__(256) void k_combine(int d, int k, float eps, const 
 {
     extern __shared__ float sbuf[];  // [2][d]
     __shared__ double red[256];
-    const int t = blockIdx.x, tid = threadIdx.x;
+    const int t = blockIdx.x, tid = threadIdx.x, d4 = d / 4;  // d % 32 == 0
     float* acc = sbuf;
     float* o = sbuf + d;
-    for (int i = tid; i < d; i += 256) {
-        float a = 0.0f;
-        for (int j = 0; j < k; j++) a += yd[((int64_t)t * k + j) * d + i] * w[(int64_t)t * k + j];
-        acc[i] = a;
+    const float4* y4 = (const float4*)yd + (int64_t)t * k * d4;
+    const float* wt = w + (int64_t)t * k;
+    // acc = sum_j w_j * yd_j in rank order (each term rounded, then added); four elements per thread,
+    // the loads of eight ranks issued before their use
+    for (int i4 = tid; i4 < d4; i4 += 256) {
+        float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (int j0 = 0; j0 < k; j0 += 8) {
+            float4 yv[8];
+            float wj[8];
+#pragma unroll
+            for (int jj = 0; jj < 8; jj++) {
+                const int j = min(j0 + jj, k - 1);
+                yv[jj] = y4[(int64_t)j * d4 + i4];
+                wj[jj] = wt[j];
+            }
+#pragma unroll
+            for (int jj = 0; jj < 8; jj++) {
+                if (j0 + jj < k) {
+                    a.x += yv[jj].x * wj[jj];
+                    a.y += yv[jj].y * wj[jj];
+                    a.z += yv[jj].z * wj[jj];
+                    a.w += yv[jj].w * wj[jj];
+                }
+            }
+        }
+        ((float4*)acc)[i4] = a;
     }
     __syncthreads();
     const float s2 = rms_scale_from_mean(mean_sq_cert<256>(acc, d, red, flags), eps);

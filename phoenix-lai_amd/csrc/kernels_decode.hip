@@ -97,29 +97,6 @@ struct DecArgs {
 
 // ------------------------------------------------------------------------------ helpers
 
-// Q8_0 of one 32-block held as 4 consecutive values per lane by an 8-lane group (lane l of the group:
-// elements 4l..4l+3), CpuRef.QuantizeQ8_0 (src/CpuRef.cs:49-62): amax, d = amax / 127, id = 1 / d,
-// q = roundf(x * id) (half away from zero), fp16 d.  Returns the lane's 4 q bytes as one dword (the
-// LDS activation layout); *dval and *sum (the block's q sum) are valid in all 8 lanes.
-__device__ __forceinline__ int q8_0_oct(float4 v, float* dval, int* sum)
-{
-    float am = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-    am = fmaxf(am, __shfl_xor(am, 1, 64));
-    am = fmaxf(am, __shfl_xor(am, 2, 64));
-    am = fmaxf(am, __shfl_xor(am, 4, 64));
-    const float dd = am / 127.0f;
-    const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
-    const int q0 = (int)roundf(v.x * id), q1 = (int)roundf(v.y * id), q2 = (int)roundf(v.z * id),
-              q3 = (int)roundf(v.w * id);
-    int sm = q0 + q1 + q2 + q3;
-    sm += __shfl_xor(sm, 1, 64);
-    sm += __shfl_xor(sm, 2, 64);
-    sm += __shfl_xor(sm, 4, 64);
-    *dval = h2f(f2h_bits(dd));
-    *sum = sm;
-    return (q0 & 0xFF) | ((q1 & 0xFF) << 8) | ((q2 & 0xFF) << 16) | (int)((unsigned)q3 << 24);
-}
-
 // The same for 32 values held one per lane of a 32-lane half; returns q.
 __device__ __forceinline__ int q8_0_half(float x, float* dval, int* sum)
 {
