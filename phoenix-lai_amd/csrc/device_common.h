@@ -170,6 +170,19 @@ __device__ __forceinline__ float half_max_f(float v)
     return (threadIdx.x & 32) ? b : a;
 }
 
+typedef _Float16 mh2 __attribute__((ext_vector_type(2)));
+
+// Bytes to exact fp16 pairs by the 1024-bias: the half with bits 0x64XX is 1024 + XX.  Returns the
+// pair (byte 2p, byte 2p + 1) of w minus `bias` (1152 gives a signed int8 from w ^ 0x80808080,
+// 1032 gives q - 8 from a nibble).
+__device__ __forceinline__ uint32_t bias_pair(uint32_t w, int p, float bias)
+{
+    const uint32_t b = __builtin_amdgcn_perm(0x64646464u, w, p ? 0x04030402u : 0x04010400u);
+    mh2 v = __builtin_bit_cast(mh2, b);
+    v = v - mh2{(_Float16)bias, (_Float16)bias};
+    return __builtin_bit_cast(uint32_t, v);
+}
+
 // Q8_0 of one 32-block held as 4 consecutive values per lane by an 8-lane group (lane l of the group:
 // elements 4l..4l+3), CpuRef.QuantizeQ8_0 (src/CpuRef.cs:49-62): amax, d = amax / 127, id = 1 / d,
 // q = roundf(x * id) (half away from zero), fp16 d.  Returns the lane's 4 q bytes as one dword (the

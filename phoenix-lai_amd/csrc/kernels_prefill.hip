@@ -16,15 +16,15 @@
 //
 // Work layout: a workgroup of four waves covers two row groups (128 rows; wave w: 32 rows) and one
 // tile of up to 128 assignments (four 32-token column tiles; the empty ones are skipped).  Per block,
-// the tile's activation bytes are staged in LDS once for the four waves, converted to fp16 (token
-// rows of 40 halves, an 80-byte stride that keeps the 16-byte reads free of bank conflicts); the
-// weights stream two blocks ahead in registers, the activations one block ahead.
+// the tile's activations (the fp16 copy of their Q8_0 integers that the quantizer writes) are staged
+// in LDS once for the four waves (token rows of 40 halves, an 80-byte stride that keeps the 16-byte
+// reads free of bank conflicts), with each token's scale as a ready operand entry; the weights and the
+// activations stream one block ahead.
 #include "device_common.h"
 
 namespace phx {
 
 typedef _Float16 mh8 __attribute__((ext_vector_type(8)));
-typedef _Float16 mh2 __attribute__((ext_vector_type(2)));
 typedef float mf16 __attribute__((ext_vector_type(16)));
 
 struct MmaArgs {
@@ -48,17 +48,6 @@ constexpr int MMA_TOK = 32 * MMA_NT;      // tile capacity (kMmaTile)
 constexpr int MMA_LDS_TOK = 40;           // halves per staged token row
 static_assert(MMA_TOK == kMmaTile, "tile capacity");
 
-// Bytes to exact fp16 pairs by the 1024-bias: the half with bits 0x64XX is 1024 + XX.  Returns the
-// pair (byte 2p, byte 2p + 1) of w minus `bias` (1152 gives a signed int8 from w ^ 0x80808080,
-// 1032 gives q - 8 from a nibble).
-__device__ __forceinline__ uint32_t bias_pair(uint32_t w, int p, float bias)
-{
-    const uint32_t b = __builtin_amdgcn_perm(0x64646464u, w, p ? 0x04030402u : 0x04010400u);
-    mh2 v = __builtin_bit_cast(mh2, b);
-    v = v - mh2{(_Float16)bias, (_Float16)bias};
-    return __builtin_bit_cast(uint32_t, v);
-}
-
 // eight values of two dwords as an mh8 operand
 __device__ __forceinline__ mh8 bias8(uint32_t w0, uint32_t w1, float bias)
 {
@@ -70,7 +59,8 @@ __device__ __forceinline__ mh8 bias8(uint32_t w0, uint32_t w1, float bias)
 // One workgroup's tile: NJ active 32-token column tiles (1..4), every block's MFMAs issued before the
 // chain's VALU work.  sx / sdx: the workgroup's LDS staging buffers.
 template <int TYPE, int NJ>
-__device__ __forceinline__ void mma_tile(const MmaArgs& g, const Tile& tl, int cnt, uint32_t* sx, unsigned short* sdx)
+__device__ __forceinline__ void mma_tile(const MmaArgs& g, const Tile& tl, int cnt, uint32_t* sx, uint4* sdx,
+                                         const uint4& szero)
 {
     constexpr int PAY = TYPE == PHX_Q4_0_DEV ? 16 : 32;
     constexpr int XW = MMA_TOK * MMA_LDS_TOK / 2;  // dwords per staging buffer
@@ -79,30 +69,28 @@ __device__ __forceinline__ void mma_tile(const MmaArgs& g, const Tile& tl, int c
     const bool live = gI < g.rg;  // a wave past the last row group computes a clamped one, stores nothing
     const int nb = g.nb;
 
-    // staging: thread tid brings token tid / 2, bytes 16 (tid % 2) .. + 15 of each block
+    // staging: thread tid brings token tid / 2, halves 16 (tid % 2) .. + 15 of each block of the
+    // activations' fp16 copy, and the block's scale as a ready scale-product operand entry
     const int st_tok = tid >> 1, st_part = tid & 1;
     const bool st_valid = st_tok < cnt;
     const int64_t st_row = st_valid ? (int64_t)(g.perm[tl.start + st_tok] / g.act_div) : 0;
-    const uint8_t* st_q = (const uint8_t*)g.act.q + st_row * g.act.qstride + 16 * st_part;
+    const uint16_t* st_q = g.act.qh + st_row * g.act.qhstride + 16 * st_part;
     const float* st_d = g.act.d + st_row * g.act.dstride;
-    uint4 xq;
+    uint4 xq0, xq1;
     float xd;
     auto load_x = [&](int b) {
-        xq = *(const uint4*)(st_q + (int64_t)b * 32);
+        xq0 = *(const uint4*)(st_q + (int64_t)b * 32);
+        xq1 = *(const uint4*)(st_q + (int64_t)b * 32 + 8);
         xd = st_d[b];
     };
-    const uint32_t st_mask = st_valid ? ~0u : 0u;  // invalid tokens: zero bytes (0x80 after the flip -> 0)
-    // unconditional in every thread (both threads of a token write the same scale), so the compiler
-    // keeps the loads where they are issued instead of sinking them to a conditional use
+    const uint32_t st_mask = st_valid ? ~0u : 0u;  // invalid tokens: zeros
+    // unconditional in every thread (both threads of a token write the same scale entry), so the
+    // compiler keeps the loads where they are issued instead of sinking them to a conditional use
     auto store_x = [&](int buf) {
-        const uint4 u = make_uint4((xq.x & st_mask) ^ 0x80808080u, (xq.y & st_mask) ^ 0x80808080u,
-                                   (xq.z & st_mask) ^ 0x80808080u, (xq.w & st_mask) ^ 0x80808080u);
         uint32_t* dst = sx + buf * XW + st_tok * (MMA_LDS_TOK / 2) + 8 * st_part;
-        *(uint4*)dst = make_uint4(bias_pair(u.x, 0, 1152.0f), bias_pair(u.x, 1, 1152.0f), bias_pair(u.y, 0, 1152.0f),
-                                  bias_pair(u.y, 1, 1152.0f));
-        *(uint4*)(dst + 4) = make_uint4(bias_pair(u.z, 0, 1152.0f), bias_pair(u.z, 1, 1152.0f),
-                                        bias_pair(u.w, 0, 1152.0f), bias_pair(u.w, 1, 1152.0f));
-        sdx[buf * MMA_TOK + st_tok] = (unsigned short)(f2h_bits(xd) & st_mask);  // xd is an fp16 value
+        *(uint4*)dst = make_uint4(xq0.x & st_mask, xq0.y & st_mask, xq0.z & st_mask, xq0.w & st_mask);
+        *(uint4*)(dst + 4) = make_uint4(xq1.x & st_mask, xq1.y & st_mask, xq1.z & st_mask, xq1.w & st_mask);
+        sdx[buf * MMA_TOK + st_tok] = make_uint4(f2h_bits(xd) & st_mask, 0u, 0u, 0u);  // xd is an fp16 value
     };
 
     // weights: lane (row 32 half + r32, h) reads the payload bytes of its k values and its row's fp16
@@ -154,25 +142,19 @@ __device__ __forceinline__ void mma_tile(const MmaArgs& g, const Tile& tl, int c
             const uint32_t* row = xb + (32 * j + r32) * (MMA_LDS_TOK / 2);
             const mh8 B0 = __builtin_bit_cast(mh8, *(const uint4*)(row + 4 * h));
             const mh8 B1 = __builtin_bit_cast(mh8, *(const uint4*)(row + 8 + 4 * h));
-            const uint32_t dxb = sdx[buf * MMA_TOK + 32 * j + r32];
-            const mh8 Bd = __builtin_bit_cast(mh8, make_uint4(dxb & hmask, 0u, 0u, 0u));
+            const mh8 Bd = __builtin_bit_cast(mh8, *(h == 0 ? &sdx[buf * MMA_TOK + 32 * j + r32] : &szero));
             C = __builtin_amdgcn_mfma_f32_32x32x16_f16(A0, B0, zero, 0, 0, 0);
             C = __builtin_amdgcn_mfma_f32_32x32x16_f16(A1, B1, C, 0, 0, 0);
             D = __builtin_amdgcn_mfma_f32_32x32x16_f16(Ad, Bd, zero, 0, 0, 0);
         };
-        mf16 C, D;
-        products(0, C, D);
+        mf16 C[2], D[2];  // slots j % 2: compile-time after unrolling, so no copies
+        products(0, C[0], D[0]);
 #pragma unroll
         for (int j = 0; j < NJ; j++) {
-            mf16 Cn, Dn;
-            if (j + 1 < NJ) products(j + 1, Cn, Dn);
+            if (j + 1 < NJ) products(j + 1, C[(j + 1) & 1], D[(j + 1) & 1]);
             // the reference chain: sum += (float)isum * (d_w * d_x), in block order
 #pragma unroll
-            for (int q = 0; q < 16; q++) S[j][q] = S[j][q] + C[q] * D[q];
-            if (j + 1 < NJ) {
-                C = Cn;
-                D = Dn;
-            }
+            for (int q = 0; q < 16; q++) S[j][q] = S[j][q] + C[j & 1][q] * D[j & 1][q];
         }
         store_x(buf ^ 1);  // that buffer was last read before the previous barrier (after the last block:
                            // a harmless write of a buffer nobody reads again)
@@ -208,16 +190,18 @@ template <int TYPE>
 __global__ __launch_bounds__(256) void k_grouped_mfma(MmaArgs g)
 {
     __shared__ __align__(16) uint32_t sx[2 * MMA_TOK * MMA_LDS_TOK / 2];  // fp16 token rows of one block
-    __shared__ unsigned short sdx[2 * MMA_TOK];                            // their scales' fp16 bits
+    __shared__ __align__(16) uint4 sdx[2 * MMA_TOK];  // their scales: (fp16 bits, 0, 0, 0) operand entries
+    __shared__ __align__(16) uint4 szero;             // the upper lanes' scale operand
     const int tile = blockIdx.y;
     if (tile >= *g.ntiles) return;  // uniform over the workgroup
+    if (threadIdx.x == 0) szero = make_uint4(0u, 0u, 0u, 0u);  // visible after mma_tile's first barrier
     const Tile tl = g.tiles[tile];
     const int cnt = min(tl.cnt, MMA_TOK);
     switch ((cnt + 31) / 32) {  // active 32-token column tiles
-    case 1: mma_tile<TYPE, 1>(g, tl, cnt, sx, sdx); break;
-    case 2: mma_tile<TYPE, 2>(g, tl, cnt, sx, sdx); break;
-    case 3: mma_tile<TYPE, 3>(g, tl, cnt, sx, sdx); break;
-    default: mma_tile<TYPE, 4>(g, tl, cnt, sx, sdx); break;
+    case 1: mma_tile<TYPE, 1>(g, tl, cnt, sx, sdx, szero); break;
+    case 2: mma_tile<TYPE, 2>(g, tl, cnt, sx, sdx, szero); break;
+    case 3: mma_tile<TYPE, 3>(g, tl, cnt, sx, sdx, szero); break;
+    default: mma_tile<TYPE, 4>(g, tl, cnt, sx, sdx, szero); break;
     }
 }
 

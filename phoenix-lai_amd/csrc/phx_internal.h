@@ -92,6 +92,8 @@ struct Act {
     int dstride = 0;      // floats per row
     int* s = nullptr;
     int sstride = 0;      // ints per row
+    uint16_t* qh = nullptr;  // ACT_Q8_0, optional: the same integers as fp16 bits [row][cols] (for MFMA)
+    int64_t qhstride = 0;    // halves per row
 };
 
 struct Tile { int e, start, cnt; };

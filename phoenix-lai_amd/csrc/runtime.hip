@@ -320,7 +320,7 @@ int hip_code(hipError_t e)
 enum WsId {
     W_X, W_SHARED, W_OUT, W_RIN, W_XSCALE, W_AGU_Q, W_AGU_D, W_AGU_S, W_ASH_Q, W_ASH_D, W_ASH_S, W_LOGITS, W_IDS, W_W,
     W_OFF, W_PERM, W_TILES, W_NTILES, W_G, W_U, W_ADN_Q, W_ADN_D, W_ADN_S, W_YD, W_SHG, W_SHU, W_ASD_Q, W_ASD_D,
-    W_ASD_S, W_SHOUT, W_ZERO, W_STILES, W_SNTILES, W_SOFF, W_SPERM, W_LB, W_BB, W_ADEC, W_SDEC, W_AGUP, W_ASHP, W_COUNT
+    W_ASD_S, W_SHOUT, W_ZERO, W_STILES, W_SNTILES, W_SOFF, W_SPERM, W_LB, W_BB, W_ADEC, W_SDEC, W_AGUP, W_ASHP, W_AGU_H, W_ADN_H, W_ASH_H, W_ASD_H, W_COUNT
 };
 
 int ensure(phx_moe_ctx* c, int id, size_t bytes)
@@ -391,6 +391,8 @@ int ensure_act(phx_moe_ctx* c, int fmt, int64_t rows, int cols, int qid, int did
 
 constexpr int kTileA = 4;  // assignments per grouped tile
 
+bool mfma_type(int t);
+
 int ensure_workspace(phx_moe_ctx* c, const Layer& L, int T)
 {
     const phx_moe_layer_desc& D = L.desc;
@@ -417,10 +419,18 @@ int ensure_workspace(phx_moe_ctx* c, const Layer& L, int T)
     ENS(W_YD, n * D.d * 4);
     if ((rc = ensure_act(c, act_fmt(D.gate_up_type), T, D.d, W_AGU_Q, W_AGU_D, W_AGU_S))) return rc;
     if ((rc = ensure_act(c, act_fmt(D.down_type), n, D.down_cols, W_ADN_Q, W_ADN_D, W_ADN_S))) return rc;
+    if (mfma_type(D.gate_up_type) && mfma_type(D.down_type)) {  // the MFMA path's fp16 activation copies
+        ENS(W_AGU_H, (size_t)T * D.d * 2);
+        ENS(W_ADN_H, (size_t)n * D.down_cols * 2);
+    }
     if (D.n_ff_shared > 0) {
         int scols = round_up(D.n_ff_shared, block_elems(D.shared_type));
         if ((rc = ensure_act(c, act_fmt(D.shared_type), T, D.d, W_ASH_Q, W_ASH_D, W_ASH_S))) return rc;
         if ((rc = ensure_act(c, act_fmt(D.shared_type), T, scols, W_ASD_Q, W_ASD_D, W_ASD_S))) return rc;
+        if (mfma_type(D.shared_type)) {
+            ENS(W_ASH_H, (size_t)T * D.d * 2);
+            ENS(W_ASD_H, (size_t)T * scols * 2);
+        }
         ENS(W_SHG, (size_t)T * D.n_ff_shared * 4);
         ENS(W_SHU, (size_t)T * D.n_ff_shared * 4);
         ENS(W_SHOUT, (size_t)T * D.d * 4);
@@ -607,10 +617,22 @@ int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, con
     const int d = D.d, E = D.n_expert, k = D.n_used, nf = D.n_ff;
     const int n = T * k;
     const bool shared_ffn = shared == nullptr && D.n_ff_shared > 0;
+    // prefill-sized expert work (several assignments per expert on average) runs on the matrix cores,
+    // whose kernels read the activations' fp16 copies
+    const bool mma = mfma_type(D.gate_up_type) && mfma_type(D.down_type) && n >= 8 * E;
+    const bool smma = shared_ffn && mfma_type(D.shared_type) && T >= 32;
     Act agu = make_act(c, act_fmt(D.gate_up_type), d, W_AGU_Q, W_AGU_D, W_AGU_S);
+    if (mma) {
+        agu.qh = wp<uint16_t>(c, W_AGU_H);
+        agu.qhstride = d;
+    }
     Act ash;
     if (shared_ffn) ash = make_act(c, act_fmt(D.shared_type), d, W_ASH_Q, W_ASH_D, W_ASH_S);
     ash.cols = shared_ffn ? ash.cols : 0;
+    if (smma) {
+        ash.qh = wp<uint16_t>(c, W_ASH_H);
+        ash.qhstride = d;
+    }
     {
         ProfScope p(c, PHX_K_PROLOGUE);
         launch_prologue(st, T, d, D.eps, x, L.gis, L.pre2, shared_ffn ? L.ffn_norm : nullptr, wp<float>(c, W_RIN),
@@ -624,8 +646,6 @@ int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, con
         ProfScope p(c, PHX_K_TOPK);
         launch_topk(st, T, E, k, D.weight_rule, wp<float>(c, W_LOGITS), L.ds, wp<int>(c, W_IDS), wp<float>(c, W_W));
     }
-    // prefill-sized expert work (several assignments per expert on average) runs on the matrix cores
-    const bool mma = mfma_type(D.gate_up_type) && mfma_type(D.down_type) && n >= 8 * E;
     const int tileA = mma ? kMmaTile : kTileA;
     const int max_tiles = std::min(n, (n + tileA - 1) / tileA + E);
     {
@@ -643,6 +663,10 @@ int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, con
                            k, wp<float>(c, W_G), wp<float>(c, W_U), nf, nf);
     }
     Act adn = make_act(c, act_fmt(D.down_type), D.down_cols, W_ADN_Q, W_ADN_D, W_ADN_S);
+    if (mma) {
+        adn.qh = wp<uint16_t>(c, W_ADN_H);
+        adn.qhstride = D.down_cols;
+    }
     {
         ProfScope p(c, PHX_K_REQUANT);
         launch_requant(st, n, nf, wp<float>(c, W_G), wp<float>(c, W_U), c->gelu_tab, adn);
@@ -660,7 +684,6 @@ int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, con
     if (shared_ffn) {
         ProfScope p(c, PHX_K_SHARED);
         const int nff = D.n_ff_shared;
-        const bool smma = mfma_type(D.shared_type) && T >= 32;
         const int sA = smma ? kMmaTile : kTileA;
         const int smax = (T + sA - 1) / sA + 1;
         launch_dispatch(st, T, 1, sA, wp<int>(c, W_ZERO), wp<int>(c, W_SOFF), wp<int>(c, W_SPERM), wp<Tile>(c, W_STILES),
@@ -673,6 +696,10 @@ int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, con
                            1, wp<float>(c, W_SHG), wp<float>(c, W_SHU), nff, nff);
         Act asd = make_act(c, act_fmt(D.shared_type), round_up(nff, block_elems(D.shared_type)), W_ASD_Q, W_ASD_D,
                            W_ASD_S);
+        if (smma) {
+            asd.qh = wp<uint16_t>(c, W_ASD_H);
+            asd.qhstride = asd.cols;
+        }
         launch_requant(st, T, nff, wp<float>(c, W_SHG), wp<float>(c, W_SHU), c->gelu_tab, asd);
         if (smma)
             launch_grouped_mfma(st, L.sdn, asd, wp<Tile>(c, W_STILES), wp<int>(c, W_SNTILES), smax, wp<int>(c, W_SPERM), 1,
