@@ -661,7 +661,7 @@ void launch_grouped(hipStream_t st, const QMat& w, Act act, const Tile* tiles, c
     g.out_stride = out_stride;
     g.paired = w.paired;
     dim3 grid(max_tiles, (w.rg + 3) / 4);
-    if (A != 4) A = 4;  // the tile size the dispatch used; one instantiation for now
+    (void)A;  // the tile size the dispatch used: 4, the one instantiation
     switch (w.type) {
     case PHX_Q4_0_DEV: launch((k_grouped_q<PHX_Q4_0_DEV, 4>), grid, dim3(256), 0, st, g); break;
     case PHX_Q8_0_DEV: launch((k_grouped_q<PHX_Q8_0_DEV, 4>), grid, dim3(256), 0, st, g); break;

@@ -646,6 +646,8 @@ int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, con
         ProfScope p(c, PHX_K_TOPK);
         launch_topk(st, T, E, k, D.weight_rule, wp<float>(c, W_LOGITS), L.ds, wp<int>(c, W_IDS), wp<float>(c, W_W));
     }
+    // tile sizes: the MFMA kernel's 128, the VALU kernels' 4 (their row walk is VALU-bound: larger
+    // tiles cost occupancy and measured slower)
     const int tileA = mma ? kMmaTile : kTileA;
     const int max_tiles = std::min(n, (n + tileA - 1) / tileA + E);
     {
@@ -659,7 +661,7 @@ int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, con
             launch_grouped_mfma(st, L.gu, agu, wp<Tile>(c, W_TILES), wp<int>(c, W_NTILES), max_tiles, wp<int>(c, W_PERM), k,
                                 wp<float>(c, W_G), wp<float>(c, W_U), nf, nf);
         else
-            launch_grouped(st, L.gu, agu, wp<Tile>(c, W_TILES), wp<int>(c, W_NTILES), max_tiles, kTileA, wp<int>(c, W_PERM),
+            launch_grouped(st, L.gu, agu, wp<Tile>(c, W_TILES), wp<int>(c, W_NTILES), max_tiles, tileA, wp<int>(c, W_PERM),
                            k, wp<float>(c, W_G), wp<float>(c, W_U), nf, nf);
     }
     Act adn = make_act(c, act_fmt(D.down_type), D.down_cols, W_ADN_Q, W_ADN_D, W_ADN_S);
@@ -677,7 +679,7 @@ int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, con
             launch_grouped_mfma(st, L.dn, adn, wp<Tile>(c, W_TILES), wp<int>(c, W_NTILES), max_tiles, wp<int>(c, W_PERM), 1,
                                 wp<float>(c, W_YD), wp<float>(c, W_YD), d, d);
         else
-            launch_grouped(st, L.dn, adn, wp<Tile>(c, W_TILES), wp<int>(c, W_NTILES), max_tiles, kTileA, wp<int>(c, W_PERM),
+            launch_grouped(st, L.dn, adn, wp<Tile>(c, W_TILES), wp<int>(c, W_NTILES), max_tiles, tileA, wp<int>(c, W_PERM),
                            1, wp<float>(c, W_YD), wp<float>(c, W_YD), d, d);
     }
     const float* sh = shared;

@@ -189,6 +189,17 @@ def test_c4_kquant_reduced(ctx, pkg, orc):
     check_layer(ctx, orc, L, x, tag="c4 T=12")
 
 
+def test_kquant_full_tiles(ctx, pkg, orc):
+    """About 32 assignments per expert: the K-quant grouped kernel's full tiles (Q4_K gate|up, Q6_K
+    down with its rows padded to whole super-blocks), bit-exact through the exact router."""
+    say("k-quant T=64, E=4, k=2: full tiles")
+    cfg = dict(idx=15, T=64, d=512, E=4, k=2, nf=384, gu=12, dn=14)
+    L = pkg.synth.make_layer(cfg, norms="noisy")
+    x = pkg.synth.make_input(cfg, T=64)
+    ctx.upload(0, L)
+    check_layer(ctx, orc, L, x, tag="kquant full tiles", exact=True)
+
+
 @pytest.mark.parametrize("exact", [False, True])
 def test_c5_stack_graph(ctx, pkg, orc, exact):
     say(f"c5 stack: 3 layers, T=8, HIP graph replayed 3 times, exact={exact}")
