@@ -404,37 +404,6 @@ __device__ __forceinline__ void gu_epilogue(float S, int rgi, int split, int64_t
     }
 }
 
-// Exact reference logit (src/GemmaCpu.cs:389-395): the products p_i = W[e][i] * m_i rounded, added
-// in index order, with m = ((x * rinv) * sc) * s the token's router input (in LDS, d floats).  The W
-// row streams in 32-element chunks, the next chunk's loads issued before the current chunk's adds, so
-// the chain waits on memory once per chunk at most (d % 32 == 0).
-__device__ float exact_logit(const float* sm, const float* wrow, int d)
-{
-    const float4* w4 = (const float4*)wrow;
-    const float4* m4 = (const float4*)sm;
-    const int n4 = d / 4;
-    float4 w[8];
-#pragma unroll
-    for (int q = 0; q < 8; q++) w[q] = w4[q];
-    float s = 0.0f;
-    for (int c = 0; c < n4; c += 8) {
-        float4 wn[8];
-#pragma unroll
-        for (int q = 0; q < 8; q++) wn[q] = w4[min(c + 8 + q, n4 - 1)];  // the next chunk (clamped)
-#pragma unroll
-        for (int q = 0; q < 8; q++) {
-            const float4 m = m4[c + q];
-            s += w[q].x * m.x;
-            s += w[q].y * m.y;
-            s += w[q].z * m.z;
-            s += w[q].w * m.w;
-        }
-#pragma unroll
-        for (int q = 0; q < 8; q++) w[q] = wn[q];
-    }
-    return s;
-}
-
 typedef __attribute__((address_space(3))) void* lds_void_t;
 typedef __attribute__((address_space(1))) void* glb_void_t;
 
@@ -730,58 +699,192 @@ __device__ bool wave_topk(const DecArgs& a, int t, int* s_ids, unsigned* s_klo, 
     return __all(fin && ok);
 }
 
-// Exact selection for the tokens marked in s_bad (rare): the experts that can reach the chosen ones
-// are recomputed as the reference's float chains (src/GemmaCpu.cs:389-395) and all are ranked exactly:
-// ties to the lower index, NaN below every number (the strict '>' scan of GemmaCpu.cs:400-405).
-// sL, samb, srank: LDS [T*E]; sm: LDS [d], the router input of the token being ranked; sL ends
-// holding the logits the routing reports for those tokens.
-__device__ void select_exact(const DecArgs& a, double* sL, char* samb, short* srank, float* sm, int* s_ids,
-                             const int* s_bad, double* red, bool count)
+// LDS of the exact selection, from the start of the workgroup's union region: sL [T*E] doubles, the
+// token's router input m [d] floats, the ambiguous experts' list [E] and
+// four wave counts, the chosen experts' lower ends [16] and the ambiguous experts' exact keys [E]
+// (doubles), and two product buffers of sel_buf_floats(NT) floats.  The host sizes the region with
+// the same function.
+__host__ __device__ inline size_t sel_buf_floats(int NT) { return (size_t)4 * (NT - 64) + 256; }
+
+struct SelLds {
+    size_t m, list, lo, key, buf, total;
+};
+
+__host__ __device__ inline SelLds sel_lds(int T, int E, int d, int NT)
 {
-    const int tid = threadIdx.x, NT = blockDim.x;
+    SelLds o;
+    const size_t TE = (size_t)T * E;
+    o.m = (TE * 8 + 15) & ~(size_t)15;
+    o.list = o.m + (size_t)d * 4;
+    o.lo = (o.list + (size_t)(E + 4) * 4 + 7) & ~(size_t)7;
+    o.key = o.lo + PHX_MAX_USED_DEV * 8;
+    o.buf = (o.key + (size_t)E * 8 + 15) & ~(size_t)15;
+    o.total = o.buf + 2 * sel_buf_floats(NT) * 4;
+    return o;
+}
+
+// Exact logits of ng <= 64 experts (list[0..ng-1]) for one token: the reference's float chains
+// s = fl(s + fl(W[e][i] * m_i)), i = 0..d-1 in order, from s = 0 (src/GemmaCpu.cs:389-395).  Waves
+// 1..NWV-1 form the products of one segment of seg = 4 * segq elements of every chain per step (one
+// float4 each, its W loads issued PD steps ahead) into one of two LDS buffers; lane j of wave 0 adds
+// chain j's previous segment from the other buffer in index order, its LDS reads eight float4 ahead of
+// the adds.  One barrier per step.  The chains' sums go to out[list[j]] as doubles.
+constexpr int SEL_PD = 4;
+
+__device__ void exact_chains(const float* W, int d, const float* sm, const int* list, int ng, float* sbuf,
+                             size_t bufn, double* out)
+{
+    ng = __builtin_amdgcn_readfirstlane(ng);  // uniform (an LDS count): scalar loop control
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), NPT = blockDim.x - 64;
+    const int sq = NPT / ng, segq = min(sq >= 16 ? sq & ~15 : sq, d / 4), seg = 4 * segq, stride = seg + 4;
+    const int nseg = (d + seg - 1) / seg;
+    // producer q = tid - 64: chain jq, float4 slot oq of the segment (idle when jq >= ng).  Every thread
+    // issues the loads (wave 0 and idle producers at clamped, valid addresses), so no branch separates
+    // a load from its use and the loads of later steps stay in flight.
+    const int q = tid >= 64 ? tid - 64 : tid, jq = q / segq, oq = q - jq * segq;
+    const bool prod = wave > 0 && jq < ng;
+    const float4* wrow = (const float4*)(W + (int64_t)list[min(jq, ng - 1)] * d);
+    const int n4 = d / 4;
+    float4 r[SEL_PD];
+#pragma unroll
+    for (int k = 0; k < SEL_PD; k++) {
+        r[k] = wrow[min(k * segq + oq, n4 - 1)];
+        __builtin_amdgcn_sched_barrier(0);  // in step order, as the loop issues them: a step waits on its own
+    }
+    float s = 0.0f;
+    for (int s0 = 0; s0 <= nseg; s0 += SEL_PD) {  // steps 0..nseg, padded to whole groups of PD
+#pragma unroll
+        for (int k = 0; k < SEL_PD; k++) {
+            const int st = s0 + k;
+            const int i4 = st * segq + oq;
+            if (prod && st < nseg && i4 < n4) {
+                const float4 m = ((const float4*)sm)[i4];
+                float4 p;
+                p.x = r[k].x * m.x;
+                p.y = r[k].y * m.y;
+                p.z = r[k].z * m.z;
+                p.w = r[k].w * m.w;
+                *(float4*)(sbuf + (st & 1) * bufn + jq * stride + 4 * oq) = p;
+            }
+            r[k] = wrow[min((st + SEL_PD) * segq + oq, n4 - 1)];  // the step PD ahead (clamped)
+            if (wave == 0 && st >= 1 && st <= nseg && tid < ng) {
+                const int sp = st - 1, c4 = min(segq, n4 - sp * segq);
+                const float4* b4 = (const float4*)(sbuf + (sp & 1) * bufn + tid * stride);
+                // batches of sixteen float4: the batch's reads go out together and the adds of its first
+                // float4 wait for one LDS round trip, the rest arrive while the earlier ones are added
+                const int c8 = c4 & ~15;
+                for (int c = 0; c < c8; c += 16) {
+                    float4 v[16];
+#pragma unroll
+                    for (int u = 0; u < 16; u++) v[u] = b4[c + u];
+#pragma unroll
+                    for (int u = 0; u < 16; u++) {
+                        s += v[u].x;
+                        s += v[u].y;
+                        s += v[u].z;
+                        s += v[u].w;
+                    }
+                }
+                for (int c = c8; c < c4; c++) {
+                    const float4 t = b4[c];
+                    s += t.x;
+                    s += t.y;
+                    s += t.z;
+                    s += t.w;
+                }
+            }
+            __syncthreads();
+        }
+    }
+    if (wave == 0 && tid < ng) out[list[tid]] = (double)s;
+    __syncthreads();
+}
+
+// Exact selection for the tokens marked in s_bad (rare): the experts that can reach the chosen ones
+// (the ambiguous ones) are recomputed as the reference's float chains (src/GemmaCpu.cs:389-395) and
+// ranked exactly: ties to the lower index, NaN below every number (the strict '>' scan of
+// GemmaCpu.cs:400-405).  Every other expert's upper end lies below every chosen expert's lower end,
+// so the top-k lies among the ambiguous ones, unless a chain ends non-finite: then every expert of
+// the token is recomputed and ranked.  un: the LDS of sel_lds; sL (at un) ends holding the logits
+// the routing reports for those tokens.
+__device__ void select_exact(const DecArgs& a, unsigned char* un, int* s_ids, const int* s_bad, double* red,
+                             bool count)
+{
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, NT = blockDim.x;
+    const SelLds lds = sel_lds(a.T, a.E, a.d, NT);
+    double* sL = (double*)un;
+    float* sm = (float*)(un + lds.m);
+    int* slist = (int*)(un + lds.list);
+    int* swc = slist + a.E;
+    double* slo = (double*)(un + lds.lo);
+    double* skey = (double*)(un + lds.key);
+    float* sbuf = (float*)(un + lds.buf);
     const float sc = 1.0f / (float)__dsqrt_rn((double)a.d);
+    const int E = a.E, k = a.k, nwe = (E + 63) / 64;
     for (int tt = 0; tt < a.T; tt++) {
         if (!s_bad[tt]) continue;  // uniform: an LDS value read after a barrier
         if (count && tid == 0) atomicAdd(&a.flags[1], 1);
         const float* xr = a.x + (int64_t)tt * a.d;
+        const double* Lr = a.Lb + (int64_t)tt * E;
+        const double* Br = a.Bb + (int64_t)tt * E;
+        // the bounds (thread b: expert b) and the chosen experts' lower ends, loaded beside x
+        double lb = 0.0, bb = 0.0;
+        if (tid < E) {
+            lb = Lr[tid];
+            bb = Br[tid];
+        }
+        if (tid < k) {
+            const int ex = s_ids[tt * k + tid];
+            slo[tid] = Lr[ex] - Br[ex];
+        }
         double s = 0.0;
         for (int i = tid; i < a.d; i += NT) s += (double)xr[i] * (double)xr[i];
         const float rinv_t = rms_scale_from_mean(wg_mean_sq(s, xr, a.d, red, nullptr), a.eps);
         for (int i = tid; i < a.d; i += NT) sm[i] = ((xr[i] * rinv_t) * sc) * a.gis[i];
-        __syncthreads();
-        const double* Lr = a.Lb + (int64_t)tt * a.E;
-        const double* Br = a.Bb + (int64_t)tt * a.E;
+        const bool nonfinite = __syncthreads_or(tid < E && !(isfinite(lb) && isfinite(bb)));  // publishes sm, slo
         // the lowest lower end among the fast path's chosen experts: an expert whose upper end does not
         // reach it ranks below every chosen one in exact arithmetic too
         double minlo = INFINITY;
-        bool nonfinite = false;
-        for (int j = 0; j < a.k; j++) {
-            const int ex = s_ids[tt * a.k + j];
-            minlo = fmin(minlo, Lr[ex] - Br[ex]);
-        }
-        for (int b = 0; b < a.E; b++)
-            if (!(isfinite(Lr[b]) && isfinite(Br[b]))) nonfinite = true;
-        for (int b = tid; b < a.E; b += NT) {
-            const int j = tt * a.E + b;
-            const bool amb = nonfinite || !(Lr[b] + Br[b] < minlo);
-            samb[j] = amb;
-            sL[j] = amb ? (double)exact_logit(sm, a.W + (int64_t)b * a.d, a.d) : Lr[b];
-        }
-        __syncthreads();
-        for (int b = tid; b < a.E; b += NT) {
-            const int j = tt * a.E + b;
-            const double my = samb[j] ? sel_key(sL[j]) : -INFINITY;
-            int r = 0;
-            for (int c = 0; c < a.E; c++) {
-                const int jc = tt * a.E + c;
-                r += sel_beats(samb[jc] ? sel_key(sL[jc]) : -INFINITY, c, my, b);
+        for (int j = 0; j < k; j++) minlo = fmin(minlo, slo[j]);
+        int na = 0;
+        for (int all = nonfinite; all < 2; all++) {
+            // the ambiguous experts in index order: one per lane of waves 0..nwe-1
+            bool amb = false;
+            uint64_t m = 0;
+            if (wave < nwe) {
+                if (tid < E) {
+                    amb = all || !(lb + bb < minlo);
+                    sL[tt * E + tid] = lb;
+                }
+                m = __ballot(amb);
+                if (lane == 0) swc[wave] = __popcll(m);
             }
-            srank[j] = (short)r;
+            __syncthreads();
+            int off = 0;
+            na = 0;
+            for (int w = 0; w < nwe; w++) {
+                const int c = swc[w];
+                if (w < wave) off += c;
+                na += c;
+            }
+            if (amb) slist[off + __popcll(m & ((1ull << lane) - 1))] = tid;
+            __syncthreads();
+            for (int g0 = 0; g0 < na; g0 += 64)
+                exact_chains(a.W, a.d, sm, slist + g0, min(64, na - g0), sbuf, sel_buf_floats(NT), sL + tt * E);
+            if (all) break;
+            // a non-finite chain (overflow) voids the bounds' argument: recompute every expert
+            const bool nfc = tid < na && !isfinite(sL[tt * E + slist[tid]]);
+            if (!__syncthreads_or(nfc)) break;
         }
+        // exact ranks among the ambiguous experts
+        if (tid < na) skey[tid] = sel_key(sL[tt * E + slist[tid]]);
         __syncthreads();
-        for (int b = tid; b < a.E; b += NT) {
-            const int r = srank[tt * a.E + b];
-            if (r < a.k) s_ids[tt * a.k + r] = b;
+        if (tid < na) {
+            const double my = skey[tid];
+            const int b = slist[tid];
+            int r = 0;
+            for (int c = 0; c < na; c++) r += sel_beats(skey[c], slist[c], my, b);
+            if (r < k) s_ids[tt * k + r] = b;
         }
         __syncthreads();
     }
@@ -889,9 +992,9 @@ template <int TYPE>
 __device__ void gu_wg(const DecArgs& a, unsigned char* smem)
 {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, NT = blockDim.x, NWV = NT >> 6;
-    const int TE = a.T * a.E, nb = a.gu.nb;
+    const int nb = a.gu.nb;
     // LDS: [terms | exact-selection arrays and router input] [act rows] [ids, perm, lists, tiles] [scratch]
-    const size_t terms_bytes = (size_t)DROWS * nb * 64 * 4, sel_bytes = (size_t)TE * 11 + 16 + (size_t)a.d * 4;
+    const size_t terms_bytes = (size_t)DROWS * nb * 64 * 4, sel_bytes = sel_lds(a.T, a.E, a.d, NT).total;
     unsigned char* un = smem;
     ActL* act = (ActL*)(un + ((std::max(terms_bytes, sel_bytes) + 15) & ~(size_t)15));
     int* s_ids = (int*)(act + DROWS);   // 256
@@ -933,12 +1036,7 @@ __device__ void gu_wg(const DecArgs& a, unsigned char* smem)
     __syncthreads();
     const bool exact = s_misc[1] != 0;
     double* sL = (double*)un;
-    if (exact) {
-        char* samb = (char*)(sL + TE);
-        short* srank = (short*)(samb + TE);
-        float* sm = (float*)(((uintptr_t)(srank + TE) + 15) & ~(uintptr_t)15);
-        select_exact(a, sL, samb, srank, sm, s_ids, s_misc + 2, red, routing);
-    }
+    if (exact) select_exact(a, un, s_ids, s_misc + 2, red, routing);
     int ntiles;
     if (a.T == 1) {
         // one token: tile j is assignment j (the k experts are distinct)
@@ -1210,8 +1308,7 @@ static DecArgs dec_args(const DecLayerH& h)
 
 static size_t gu_lds(const DecLayerH& h)
 {
-    const size_t TE = (size_t)h.T * h.E;
-    const size_t un = (std::max((size_t)DROWS * h.gu->nb * 64 * 4, TE * 11 + 16 + (size_t)h.d * 4) + 15) & ~(size_t)15;
+    const size_t un = (std::max((size_t)DROWS * h.gu->nb * 64 * 4, sel_lds(h.T, h.E, h.d, nt_gu(h)).total) + 15) & ~(size_t)15;
     const size_t ex = un + sizeof(ActL) * DROWS + (256 * 2 + 260 * 3) * 4 + 272 * sizeof(DecTile) + (20 + 32) * 4 + 17 * 8 +
                       16 * 32 * 4;
     const size_t sh = h.sgu ? sizeof(ActL) * DROWS + (size_t)DROWS * h.sgu->nb * 64 * 4 : 0;

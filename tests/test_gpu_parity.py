@@ -59,10 +59,14 @@ def check_layer(ctx, orc, L, x, shared=None, tag="", exact=False):
             bad_ids += 1
             continue
         if exact:
-            assert np.array_equal(logits[t], rlog), f"{tag} t={t}: router logits differ"
+            # NaN logits (a NaN router weight) compare equal to NaN
+            np.testing.assert_array_equal(logits[t], rlog, err_msg=f"{tag} t={t}: router logits differ")
             np.testing.assert_array_equal(w[t], rw, err_msg=f"{tag} t={t} weights")
         else:
-            assert np.abs(logits[t].astype(np.float64) - rlog).max() <= 1e-5, f"{tag} t={t}: logits beyond bound"
+            fin = np.isfinite(rlog)
+            np.testing.assert_array_equal(logits[t][~fin], rlog[~fin], err_msg=f"{tag} t={t}: nonfinite logits")
+            err = np.abs(logits[t][fin].astype(np.float64) - rlog[fin])
+            assert err.max(initial=0.0) <= 1e-5, f"{tag} t={t}: logits beyond bound"
             np.testing.assert_allclose(w[t], rw, rtol=1e-4, atol=1e-7, err_msg=f"{tag} t={t} weights")
         np.testing.assert_array_equal(g[t * k:(t + 1) * k], rg, err_msg=f"{tag} t={t} gate")
         np.testing.assert_array_equal(u[t * k:(t + 1) * k], ru, err_msg=f"{tag} t={t} up")
@@ -171,6 +175,51 @@ def test_router_tie_forces_fallback(ctx, pkg, orc):
     say(f"tokens with both tied experts: {len(both)}; router fallbacks {after - before}")
     assert len(both) >= x.shape[0] // 2, "the planted tie should reach the top-k of most tokens"
     assert after - before >= len(both)
+
+
+def test_router_ties_decode_T8(ctx, pkg, orc):
+    """The exact fallback at the decode path's full width (d=2816, 128 experts) for several tokens of one
+    call: three planted pairs of identical router rows along the tokens' mean reach most tokens' top-k,
+    so most tokens are ranked by the reference's float chains (ties to the lower index)."""
+    say("router ties: duplicate router rows in c2 T=8")
+    L = dict(layer(pkg, "c2_decode"))
+    W = L["gate_inp"].copy()
+    x = pkg.synth.make_input("c2_decode", T=8)
+    xbar = x.mean(0)
+    for a, b, scale in [(3, 90, 0.9), (17, 40, 0.7), (64, 65, 0.5)]:
+        W[a] = (scale * xbar / np.linalg.norm(xbar)).astype(np.float32)
+        W[b] = W[a]
+    L["gate_inp"] = W
+    before = ctx.fallback_counts()[1]
+    ctx.upload(0, L)
+    check_layer(ctx, orc, L, x, tag="c2 T=8 ties")
+    ids = ctx.routing()[0]
+    for a, b, _ in [(3, 90, 0), (17, 40, 0), (64, 65, 0)]:
+        both = [list(r) for r in ids if a in r and b in r]
+        assert all(r.index(a) < r.index(b) for r in both)
+    fb = ctx.fallback_counts()[1] - before
+    say(f"router fallbacks {fb}")
+    assert fb >= 4, "the planted ties should send most tokens to the exact fallback"
+
+
+@pytest.mark.parametrize("exact", [False, True])
+def test_router_nan_row_decode_T8(ctx, pkg, orc, exact):
+    """A NaN router weight makes one expert's logit NaN for every token: no order is certified, every
+    expert of every token goes to the exact chains (two groups of 64 in the fallback), and NaN ranks
+    below every number (the strict '>' scan of src/GemmaCpu.cs:400-405)."""
+    say(f"router NaN row in c2 T=8 exact={exact}")
+    L = dict(layer(pkg, "c2_decode"))
+    W = L["gate_inp"].copy()
+    W[11, 5] = np.nan
+    L["gate_inp"] = W
+    x = pkg.synth.make_input("c2_decode", T=8)
+    before = ctx.fallback_counts()[1]
+    ctx.upload(0, L)
+    check_layer(ctx, orc, L, x, tag=f"c2 T=8 NaN row exact={exact}", exact=exact)
+    ids, _, _, _, logits = ctx.routing()
+    assert np.isnan(logits[:, 11]).all() and not (ids == 11).any()
+    if not exact:
+        assert ctx.fallback_counts()[1] - before == 8
 
 
 def test_c3_prefill_reduced(ctx, pkg, orc):
