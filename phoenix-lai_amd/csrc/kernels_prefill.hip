@@ -15,11 +15,17 @@
 // result C[i][j] sits in lane j + 32 * ((i / 4) % 2), register (i % 4) + 4 * (i / 8).
 //
 // Work layout: a workgroup of four waves covers two row groups (128 rows; wave w: 32 rows) and one
-// tile of up to 128 assignments (four 32-token column tiles; the empty ones are skipped).  Per block,
-// the tile's activations (the fp16 copy of their Q8_0 integers that the quantizer writes) are staged
-// in LDS once for the four waves (token rows of 40 halves, an 80-byte stride that keeps the 16-byte
-// reads free of bank conflicts), with each token's scale as a ready operand entry; the weights and the
-// activations stream one block ahead.
+// tile of up to 128 assignments (four 32-token column tiles; the empty ones are skipped).  Every
+// block's operands reach LDS by direct global -> LDS loads (no registers, no staging code) into a ring
+// of MMA_RING slots, MMA_RING - 1 blocks ahead of the block being multiplied: the tile's activation
+// rows (the fp16 copy of their Q8_0 integers that the quantizer writes) and their scales, the 128
+// weight rows' payload and their fp16 scales.  Each wave issues the same five loads per block, so
+// its own count of outstanding loads tells when a block has landed; one barrier per block then
+// publishes it.  The operands are read from LDS with explicit ds_read instructions whose completion
+// the code waits for itself (the compiler would otherwise wait for every outstanding direct load
+// before any LDS read).  Activation rows sit in 16-token groups of 1 KB with the four 16-byte parts
+// of token t at slot 4 (t % 16) + (part ^ ((t % 16) / 4)), so the 32 lanes of an operand read hit
+// 32 distinct bank groups.
 #include "device_common.h"
 
 namespace phx {
@@ -45,7 +51,6 @@ struct MmaArgs {
 
 constexpr int MMA_NT = 4;                 // 32-token column tiles per workgroup
 constexpr int MMA_TOK = 32 * MMA_NT;      // tile capacity (kMmaTile)
-constexpr int MMA_LDS_TOK = 40;           // halves per staged token row
 static_assert(MMA_TOK == kMmaTile, "tile capacity");
 
 // eight values of two dwords as an mh8 operand
@@ -56,57 +61,126 @@ __device__ __forceinline__ mh8 bias8(uint32_t w0, uint32_t w1, float bias)
     return __builtin_bit_cast(mh8, u);
 }
 
-// One workgroup's tile: NJ active 32-token column tiles (1..4), every block's MFMAs issued before the
-// chain's VALU work.  sx / sdx: the workgroup's LDS staging buffers.
-template <int TYPE, int NJ>
-__device__ __forceinline__ void mma_tile(const MmaArgs& g, const Tile& tl, int cnt, uint32_t* sx, uint4* sdx,
-                                         const uint4& szero)
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) void* lds_void_t;
+typedef __attribute__((address_space(1))) void* glb_void_t;
+
+constexpr int MMA_RING = 4;  // LDS ring slots: blocks in flight ahead of the one being multiplied
+constexpr int MMA_DMA = 5;   // direct loads per wave per block
+
+// LDS ring slot layout (bytes).  A direct load of 1, 2 or 4 bytes writes lane l's value at 4 l from
+// the wave's LDS base (16 l for 16-byte loads).
+template <int TYPE>
+struct MmaSlot {
+    static constexpr int PAY = TYPE == PHX_Q4_0_DEV ? 16 : 32;
+    static constexpr int ACT = 0;                    // 128 tokens x 64 B, swizzled 16-token groups
+    static constexpr int ADX = ACT + MMA_TOK * 64;   // 128 token scales (float)
+    static constexpr int WQ = ADX + MMA_TOK * 4;     // 128 weight rows x PAY
+    static constexpr int WD = WQ + 128 * PAY;        // 128 weight scales (fp16 in the low half of a dword)
+    static constexpr int BYTES = WD + 128 * 4;
+};
+
+// explicit LDS reads at address a + OFF (asynchronous: the value is valid after lds_wait)
+template <int OFF = 0>
+__device__ __forceinline__ u32x4 ds_r128(uint32_t a)
 {
-    constexpr int PAY = TYPE == PHX_Q4_0_DEV ? 16 : 32;
-    constexpr int XW = MMA_TOK * MMA_LDS_TOK / 2;  // dwords per staging buffer
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, r32 = lane & 31, h = lane >> 5;
+    u32x4 v;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(a), "i"(OFF));
+    return v;
+}
+template <int OFF = 0>
+__device__ __forceinline__ u32x2 ds_r64(uint32_t a)
+{
+    u32x2 v;
+    asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(v) : "v"(a), "i"(OFF));
+    return v;
+}
+template <int OFF = 0>
+__device__ __forceinline__ uint32_t ds_r32(uint32_t a)
+{
+    uint32_t v;
+    asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v) : "v"(a), "i"(OFF));
+    return v;
+}
+__device__ __forceinline__ uint32_t ds_ru16(uint32_t a)
+{
+    uint32_t v;
+    asm volatile("ds_read_u16 %0, %1" : "=v"(v) : "v"(a));
+    return v;
+}
+// waits for every LDS read of the wave; the registers passed are the reads' results, tied to the wait
+// so that no use of them is scheduled above it.  A read's result must have no other use before its
+// wait, and the read and its wait must sit in one basic block: the compiler takes an asm result as
+// ready at once, so a copy it placed in between (to split a value, or at a branch join) would copy
+// the register before the data lands.
+__device__ __forceinline__ void lds_wait(u32x4& a, u32x4& b, uint32_t& c)
+{
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c)::"memory");
+}
+__device__ __forceinline__ void lds_wait(u32x4& a, u32x4& b, uint32_t& c, u32x2& d, uint32_t& f)
+{
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d), "+v"(f)::"memory");
+}
+__device__ __forceinline__ void lds_wait(u32x4& a, u32x4& b, uint32_t& c, u32x2& d, u32x2& e, uint32_t& f)
+{
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d), "+v"(e), "+v"(f)::"memory");
+}
+
+// byte offset of (token t, 16-byte part q) in a slot's activation rows
+__device__ __forceinline__ uint32_t act_off(int t, int q)
+{
+    const int tl = t & 15;
+    return (uint32_t)((t >> 4) * 1024 + (tl * 4 + (q ^ (tl >> 2))) * 16);
+}
+
+// One workgroup's tile: NJ active 32-token column tiles (1..4).  ring: the workgroup's LDS ring.
+template <int TYPE, int NJ>
+__device__ __forceinline__ void mma_tile(const MmaArgs& g, const Tile& tl, int cnt, unsigned char* ring)
+{
+    using SL = MmaSlot<TYPE>;
+    constexpr int PAY = SL::PAY;
+    const int tid = threadIdx.x, lane = tid & 63, r32 = lane & 31, h = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int gI = blockIdx.x * 2 + (wave >> 1), half = wave & 1;
     const bool live = gI < g.rg;  // a wave past the last row group computes a clamped one, stores nothing
     const int nb = g.nb;
+    const uint32_t ring0 = (uint32_t)(uintptr_t)(lds_void_t)ring;
 
-    // staging: thread tid brings token tid / 2, halves 16 (tid % 2) .. + 15 of each block of the
-    // activations' fp16 copy, and the block's scale as a ready scale-product operand entry
-    const int st_tok = tid >> 1, st_part = tid & 1;
-    const bool st_valid = st_tok < cnt;
-    const int64_t st_row = st_valid ? (int64_t)(g.perm[tl.start + st_tok] / g.act_div) : 0;
-    const uint16_t* st_q = g.act.qh + st_row * g.act.qhstride + 16 * st_part;
-    const float* st_d = g.act.d + st_row * g.act.dstride;
-    uint4 xq0, xq1;
-    float xd;
-    auto load_x = [&](int b) {
-        xq0 = *(const uint4*)(st_q + (int64_t)b * 32);
-        xq1 = *(const uint4*)(st_q + (int64_t)b * 32 + 8);
-        xd = st_d[b];
-    };
-    const uint32_t st_mask = st_valid ? ~0u : 0u;  // invalid tokens: zeros
-    // unconditional in every thread (both threads of a token write the same scale entry), so the
-    // compiler keeps the loads where they are issued instead of sinking them to a conditional use
-    auto store_x = [&](int buf) {
-        uint32_t* dst = sx + buf * XW + st_tok * (MMA_LDS_TOK / 2) + 8 * st_part;
-        *(uint4*)dst = make_uint4(xq0.x & st_mask, xq0.y & st_mask, xq0.z & st_mask, xq0.w & st_mask);
-        *(uint4*)(dst + 4) = make_uint4(xq1.x & st_mask, xq1.y & st_mask, xq1.z & st_mask, xq1.w & st_mask);
-        sdx[buf * MMA_TOK + st_tok] = make_uint4(f2h_bits(xd) & st_mask, 0u, 0u, 0u);  // xd is an fp16 value
-    };
-
-    // weights: lane (row 32 half + r32, h) reads the payload bytes of its k values and its row's fp16
-    // scale from the row group's scale groups
+    // this wave's five direct loads per block: lane addresses at block 0 and their per-block steps
+    // (1) (2) activation rows of tokens 32 w + 16 i + lane / 4, part (lane % 4) ^ (lane / 16)
+    const uint16_t* xs[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int t = min(32 * wave + 16 * i + (lane >> 2), cnt - 1);  // past cnt: a valid row, never stored
+        const int q = (lane & 3) ^ ((lane >> 4) & 3);
+        const int64_t row = g.perm[tl.start + t] / g.act_div;
+        xs[i] = g.act.qh + row * g.act.qhstride + 8 * q;
+    }
+    // (3) token scales of tokens 32 w + lane (lanes 0-31)
+    const float* ds = g.act.d + (int64_t)(g.perm[tl.start + min(32 * wave + r32, cnt - 1)] / g.act_div) * g.act.dstride;
+    // (4) weight payload: Q4_0 rows 32 half + lane (lanes 0-31), Q8_0 row 32 half + lane / 2, half lane % 2
     const int gIc = min(gI, g.rg - 1);
     const uint8_t* rgp = g.payload + tl.e * g.mat_pay + gIc * g.rg_pay;
-    const int wrow = half * 32 + r32;
-    struct WB {
-        uint2 q0, q1;  // Q4_0: q0 = bytes 8h..8h+7; Q8_0: q0 = bytes 8h.., q1 = bytes 16 + 8h..
-        uint32_t sc;   // fp16 scale bits of the block (row wrow)
-    };
-    auto load_w = [&](int b, WB& w) {
-        const uint8_t* pb = rgp + ((int64_t)b * 64 + wrow) * PAY + 8 * h;
-        w.q0 = *(const uint2*)pb;
-        w.q1 = TYPE == PHX_Q4_0_DEV ? w.q0 : *(const uint2*)(pb + 16);
-        w.sc = *(const uint16_t*)(rgp + g.sc_off + ((int64_t)(b >> 3) * 64 + wrow) * 16 + (b & 7) * 2);
+    const uint8_t* wq = PAY == 16 ? rgp + (32 * half + r32) * 16 : rgp + (32 * half + (lane >> 1)) * 32 + 16 * (lane & 1);
+    // (5) weight scales of rows 32 half + lane (lanes 0-31): fp16 at (b / 8, row) * 16 + (b % 8) * 2
+    const uint8_t* wd = rgp + g.sc_off + (32 * half + r32) * 16;
+
+    auto issue = [&](int b) {  // block b (clamped: past the end a harmless reload) into its ring slot
+        const int bc = min(b, nb - 1);
+        unsigned char* slot = ring + (b % MMA_RING) * SL::BYTES;
+        __builtin_amdgcn_global_load_lds((glb_void_t)(xs[0] + (int64_t)bc * 32),
+                                         (lds_void_t)(slot + SL::ACT + (2 * wave) * 1024), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((glb_void_t)(xs[1] + (int64_t)bc * 32),
+                                         (lds_void_t)(slot + SL::ACT + (2 * wave + 1) * 1024), 16, 0, 0);
+        if (h == 0) {
+            __builtin_amdgcn_global_load_lds((glb_void_t)(ds + bc), (lds_void_t)(slot + SL::ADX + 128 * wave), 4, 0, 0);
+            __builtin_amdgcn_global_load_lds((glb_void_t)(wd + (int64_t)(bc >> 3) * 1024 + (bc & 7) * 2),
+                                             (lds_void_t)(slot + SL::WD + 128 * wave), 2, 0, 0);
+        }
+        if (PAY == 32 || h == 0)
+            __builtin_amdgcn_global_load_lds((glb_void_t)(wq + (int64_t)bc * 64 * PAY),
+                                             (lds_void_t)(slot + SL::WQ + 32 * PAY * wave), 16, 0, 0);
     };
 
     mf16 S[NJ];
@@ -117,50 +191,105 @@ __device__ __forceinline__ void mma_tile(const MmaArgs& g, const Tile& tl, int c
     const mf16 zero = {};
     const uint32_t hmask = h == 0 ? 0xFFFFu : 0u;  // the scale MFMA's single k sits in lanes 0-31, element 0
 
-    // one block: block b + 1's loads first, then block b from the weights in w and the staged rows;
-    // tile j + 1's products go out before tile j's chain, so the matrix cores overlap the VALU work
-    WB w, wn;
-    load_x(0);
-    load_w(0, w);
-    store_x(0);
-    __syncthreads();
+    // the lane's LDS read offsets within a slot
+    const uint32_t o_b0 = SL::ACT + act_off(r32, h), o_b1 = SL::ACT + act_off(r32, 2 + h);
+    const uint32_t o_dx = SL::ADX + 4 * r32;
+    const uint32_t o_wq = SL::WQ + 32 * PAY * wave + PAY * r32 + 8 * h;
+    const uint32_t o_wd = SL::WD + 128 * wave + 4 * r32;
+
+    // block b has landed once at most the two later blocks' loads are outstanding; the barrier then
+    // publishes it to every wave, and ends every wave's reads of the slot that issue(b + RING - 1)
+    // refills (the slot of block b - 1)
+    auto land = [&](int b) {
+        __builtin_amdgcn_s_waitcnt((MMA_DMA * (MMA_RING - 2)) | (0x7 << 4) | (0xF << 8));
+        __builtin_amdgcn_s_barrier();
+        issue(b + MMA_RING - 1);
+    };
+    u32x2 wq0, wq1;
+    uint32_t wdv;
+    u32x4 B0[2], B1[2];
+    uint32_t dx[2];
+    uint32_t a_b0, a_b1, a_dx;  // this block's read addresses (tile offsets go in the immediates)
+    // the block's first reads: weights, weight scale and tile 0's operands
+    auto start_reads = [&](int b) {
+        const uint32_t sb = ring0 + (b % MMA_RING) * SL::BYTES;
+        a_b0 = sb + o_b0;
+        a_b1 = sb + o_b1;
+        a_dx = sb + o_dx;
+        wq0 = ds_r64(sb + o_wq);
+        if (PAY == 32) wq1 = ds_r64<16>(sb + o_wq);
+        wdv = ds_ru16(sb + o_wd);
+        B0[0] = ds_r128(a_b0);
+        B1[0] = ds_r128(a_b1);
+        dx[0] = ds_r32(a_dx);
+    };
+    auto start_wait = [&]() {
+        if (PAY == 32) lds_wait(B0[0], B1[0], dx[0], wq0, wq1, wdv);
+        else lds_wait(B0[0], B1[0], dx[0], wq0, wdv);
+    };
+    auto reads = [&](int j) {  // tile j's operands (j: compile-time)
+        const int s = j & 1;
+        switch (j) {
+        case 1: B0[s] = ds_r128<2048>(a_b0); B1[s] = ds_r128<2048>(a_b1); dx[s] = ds_r32<128>(a_dx); break;
+        case 2: B0[s] = ds_r128<4096>(a_b0); B1[s] = ds_r128<4096>(a_b1); dx[s] = ds_r32<256>(a_dx); break;
+        default: B0[s] = ds_r128<6144>(a_b0); B1[s] = ds_r128<6144>(a_b1); dx[s] = ds_r32<384>(a_dx); break;
+        }
+    };
+    u32x4 bd = {0u, 0u, 0u, 0u}, ad = {0u, 0u, 0u, 0u};  // scale operands: one nonzero element
+
+#pragma unroll
+    for (int b = 0; b < MMA_RING - 1; b++) issue(b);
+    land(0);
+    start_reads(0);
+    start_wait();
     for (int b = 0; b < nb; b++) {
-        const int buf = b & 1;
-        load_x(min(b + 1, nb - 1));
-        load_w(min(b + 1, nb - 1), wn);
         mh8 A0, A1;
         if (TYPE == PHX_Q4_0_DEV) {
-            A0 = bias8(w.q0.x & 0x0F0F0F0Fu, w.q0.y & 0x0F0F0F0Fu, 1032.0f);
-            A1 = bias8((w.q0.x >> 4) & 0x0F0F0F0Fu, (w.q0.y >> 4) & 0x0F0F0F0Fu, 1032.0f);
+            A0 = bias8(wq0.x & 0x0F0F0F0Fu, wq0.y & 0x0F0F0F0Fu, 1032.0f);
+            A1 = bias8((wq0.x >> 4) & 0x0F0F0F0Fu, (wq0.y >> 4) & 0x0F0F0F0Fu, 1032.0f);
         } else {
-            A0 = bias8(w.q0.x ^ 0x80808080u, w.q0.y ^ 0x80808080u, 1152.0f);
-            A1 = bias8(w.q1.x ^ 0x80808080u, w.q1.y ^ 0x80808080u, 1152.0f);
+            A0 = bias8(wq0.x ^ 0x80808080u, wq0.y ^ 0x80808080u, 1152.0f);
+            A1 = bias8(wq1.x ^ 0x80808080u, wq1.y ^ 0x80808080u, 1152.0f);
         }
-        const mh8 Ad = __builtin_bit_cast(mh8, make_uint4(w.sc & hmask, 0u, 0u, 0u));
-        const uint32_t* xb = sx + buf * XW;
-        auto products = [&](int j, mf16& C, mf16& D) {
-            const uint32_t* row = xb + (32 * j + r32) * (MMA_LDS_TOK / 2);
-            const mh8 B0 = __builtin_bit_cast(mh8, *(const uint4*)(row + 4 * h));
-            const mh8 B1 = __builtin_bit_cast(mh8, *(const uint4*)(row + 8 + 4 * h));
-            const mh8 Bd = __builtin_bit_cast(mh8, *(h == 0 ? &sdx[buf * MMA_TOK + 32 * j + r32] : &szero));
-            C = __builtin_amdgcn_mfma_f32_32x32x16_f16(A0, B0, zero, 0, 0, 0);
-            C = __builtin_amdgcn_mfma_f32_32x32x16_f16(A1, B1, C, 0, 0, 0);
-            D = __builtin_amdgcn_mfma_f32_32x32x16_f16(Ad, Bd, zero, 0, 0, 0);
-        };
+        ad.x = wdv & hmask;
+        const mh8 Ad = __builtin_bit_cast(mh8, ad);
         mf16 C[2], D[2];  // slots j % 2: compile-time after unrolling, so no copies
-        products(0, C[0], D[0]);
+        auto products = [&](int j) {
+            const int s = j & 1;
+            // the token scale is an fp16 value: the conversion is exact
+            bd.x = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)__uint_as_float(dx[s])) & hmask;
+            C[s] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A0, __builtin_bit_cast(mh8, B0[s]), zero, 0, 0, 0);
+            C[s] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A1, __builtin_bit_cast(mh8, B1[s]), C[s], 0, 0, 0);
+            D[s] = __builtin_amdgcn_mfma_f32_32x32x16_f16(Ad, __builtin_bit_cast(mh8, bd), zero, 0, 0, 0);
+        };
+        products(0);
+        if (NJ > 1) reads(1);
 #pragma unroll
         for (int j = 0; j < NJ; j++) {
-            if (j + 1 < NJ) products(j + 1, C[(j + 1) & 1], D[(j + 1) & 1]);
+            if (j + 1 < NJ) {
+                const int s = (j + 1) & 1;
+                lds_wait(B0[s], B1[s], dx[s]);
+                products(j + 1);
+                if (j + 2 < NJ) reads(j + 2);
+            } else {
+                // the next block lands and its first reads go out behind this block's last chain (after
+                // the last block: a harmless extra barrier and reads of a slot nobody uses)
+                land(b + 1);
+                start_reads(b + 1);
+            }
+            // keep the program order: tile j + 1's products and the reads ahead of tile j's chain, each
+            // tile's chain between its neighbours' matrix products (two C / D slots, no more)
+            __builtin_amdgcn_sched_barrier(0);
             // the reference chain: sum += (float)isum * (d_w * d_x), in block order
 #pragma unroll
             for (int q = 0; q < 16; q++) S[j][q] = S[j][q] + C[j & 1][q] * D[j & 1][q];
+            asm volatile("" : "+v"(S[j]));  // the chain stays here, not sunk towards its next use
+            __builtin_amdgcn_sched_barrier(0);
+            if (j == NJ - 1) start_wait();  // in the reads' basic block: the loop carries landed values
         }
-        store_x(buf ^ 1);  // that buffer was last read before the previous barrier (after the last block:
-                           // a harmless write of a buffer nobody reads again)
-        w = wn;
-        __syncthreads();
     }
+    // the loads issued past the last block land in this workgroup's LDS: let them finish before it ends
+    __builtin_amdgcn_s_waitcnt(0);
 
     // results: lane holds rows i_q = 8 (q / 4) + 4 h + (q % 4) of the wave's 32, token column r32
     if (!live) return;
@@ -189,19 +318,16 @@ __device__ __forceinline__ void mma_tile(const MmaArgs& g, const Tile& tl, int c
 template <int TYPE>
 __global__ __launch_bounds__(256) void k_grouped_mfma(MmaArgs g)
 {
-    __shared__ __align__(16) uint32_t sx[2 * MMA_TOK * MMA_LDS_TOK / 2];  // fp16 token rows of one block
-    __shared__ __align__(16) uint4 sdx[2 * MMA_TOK];  // their scales: (fp16 bits, 0, 0, 0) operand entries
-    __shared__ __align__(16) uint4 szero;             // the upper lanes' scale operand
+    __shared__ __align__(16) unsigned char ring[MMA_RING * MmaSlot<TYPE>::BYTES];
     const int tile = blockIdx.y;
     if (tile >= *g.ntiles) return;  // uniform over the workgroup
-    if (threadIdx.x == 0) szero = make_uint4(0u, 0u, 0u, 0u);  // visible after mma_tile's first barrier
     const Tile tl = g.tiles[tile];
     const int cnt = min(tl.cnt, MMA_TOK);
     switch ((cnt + 31) / 32) {  // active 32-token column tiles
-    case 1: mma_tile<TYPE, 1>(g, tl, cnt, sx, sdx, szero); break;
-    case 2: mma_tile<TYPE, 2>(g, tl, cnt, sx, sdx, szero); break;
-    case 3: mma_tile<TYPE, 3>(g, tl, cnt, sx, sdx, szero); break;
-    default: mma_tile<TYPE, 4>(g, tl, cnt, sx, sdx, szero); break;
+    case 1: mma_tile<TYPE, 1>(g, tl, cnt, ring); break;
+    case 2: mma_tile<TYPE, 2>(g, tl, cnt, ring); break;
+    case 3: mma_tile<TYPE, 3>(g, tl, cnt, ring); break;
+    default: mma_tile<TYPE, 4>(g, tl, cnt, ring); break;
     }
 }
 
