@@ -15,27 +15,13 @@ namespace phx {
 __device__ __forceinline__ float h2f(uint32_t h) { return __half2float(__ushort_as_half((unsigned short)h)); }
 
 // float -> fp16 bits, round to nearest even with subnormals: the rounding rule of Half.FromFloat
-// (src/Half.cs:26-54), written for the device.
+// (src/Half.cs:26-54), which is IEEE binary16 conversion except that every NaN becomes the quiet NaN
+// sign | 0x7E00.  The hardware conversion (round to nearest even; fp16 denormals are not flushed in
+// the default mode) gives the same bits for every non-NaN value; the NaN case is fixed up here.
 __device__ __forceinline__ uint32_t f2h_bits(float value)
 {
-    uint32_t f = __float_as_uint(value);
-    uint32_t sign = (f >> 16) & 0x8000u;
-    int e = (int)((f >> 23) & 0xFF);
-    uint32_t m = f & 0x7FFFFFu;
-    if (e == 255) return sign | 0x7C00u | (m != 0 ? 0x200u : 0u);
-    int ne = e - 112;
-    if (ne >= 31) return sign | 0x7C00u;
-    if (ne <= 0) {
-        if (ne < -10) return sign;
-        m |= 0x800000u;
-        int sh = 14 - ne;
-        uint32_t hm = m >> sh, rem = m & ((1u << sh) - 1), half = 1u << (sh - 1);
-        if (rem > half || (rem == half && (hm & 1))) hm++;
-        return sign | hm;
-    }
-    uint32_t h = sign | ((uint32_t)ne << 10) | (m >> 13), r = m & 0x1FFFu;
-    if (r > 0x1000u || (r == 0x1000u && (h & 1))) h++;
-    return h;
+    const uint32_t h = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)value);
+    return value != value ? (h & 0x8000u) | 0x7E00u : h;
 }
 
 // C's nearest_int through 1.5*2^23 (src/CpuRefKQuants.cs:45-51)

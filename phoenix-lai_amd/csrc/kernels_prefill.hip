@@ -47,6 +47,17 @@ struct MmaArgs {
     float* out1;
     int split, out_stride;
     bool paired;
+    // npos > 0: the activations are in expert-list order, block-major: the fp16 integers of (block b,
+    // list position p) at act.qh + (b * npos + p) * 32 and its scale at act.d[b * npos + p] (token t
+    // of a tile is position tiles.start + t; no perm indirection on the input side)
+    int64_t npos;
+    // paired gate|up only, when qout.qh is set: e = gelu(g) * u quantized to Q8_0 into qout (the down
+    // product's input, one 32-column block per row group) in that list-order layout over qnpos
+    // positions, in place of a separate requant pass; only the fp16 integers and the scales are
+    // written (what the matrix-core down product reads)
+    Act qout;
+    int64_t qnpos;
+    const float* gelu_tab;
 };
 
 constexpr int MMA_NT = 4;                 // 32-token column tiles per workgroup
@@ -150,15 +161,18 @@ __device__ __forceinline__ void mma_tile(const MmaArgs& g, const Tile& tl, int c
     // this wave's five direct loads per block: lane addresses at block 0 and their per-block steps
     // (1) (2) activation rows of tokens 32 w + 16 i + lane / 4, part (lane % 4) ^ (lane / 16)
     const uint16_t* xs[2];
+    const bool lst = g.npos > 0;
+    const int64_t xstep = lst ? g.npos * 32 : 32, dstep = lst ? g.npos : 1;  // per block
 #pragma unroll
     for (int i = 0; i < 2; i++) {
         const int t = min(32 * wave + 16 * i + (lane >> 2), cnt - 1);  // past cnt: a valid row, never stored
         const int q = (lane & 3) ^ ((lane >> 4) & 3);
-        const int64_t row = g.perm[tl.start + t] / g.act_div;
-        xs[i] = g.act.qh + row * g.act.qhstride + 8 * q;
+        xs[i] = lst ? g.act.qh + (int64_t)(tl.start + t) * 32 + 8 * q
+                    : g.act.qh + (int64_t)(g.perm[tl.start + t] / g.act_div) * g.act.qhstride + 8 * q;
     }
     // (3) token scales of tokens 32 w + lane (lanes 0-31)
-    const float* ds = g.act.d + (int64_t)(g.perm[tl.start + min(32 * wave + r32, cnt - 1)] / g.act_div) * g.act.dstride;
+    const int td = min(32 * wave + r32, cnt - 1);
+    const float* ds = lst ? g.act.d + tl.start + td : g.act.d + (int64_t)(g.perm[tl.start + td] / g.act_div) * g.act.dstride;
     // (4) weight payload: Q4_0 rows 32 half + lane (lanes 0-31), Q8_0 row 32 half + lane / 2, half lane % 2
     const int gIc = min(gI, g.rg - 1);
     const uint8_t* rgp = g.payload + tl.e * g.mat_pay + gIc * g.rg_pay;
@@ -169,12 +183,13 @@ __device__ __forceinline__ void mma_tile(const MmaArgs& g, const Tile& tl, int c
     auto issue = [&](int b) {  // block b (clamped: past the end a harmless reload) into its ring slot
         const int bc = min(b, nb - 1);
         unsigned char* slot = ring + (b % MMA_RING) * SL::BYTES;
-        __builtin_amdgcn_global_load_lds((glb_void_t)(xs[0] + (int64_t)bc * 32),
+        __builtin_amdgcn_global_load_lds((glb_void_t)(xs[0] + bc * xstep),
                                          (lds_void_t)(slot + SL::ACT + (2 * wave) * 1024), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds((glb_void_t)(xs[1] + (int64_t)bc * 32),
+        __builtin_amdgcn_global_load_lds((glb_void_t)(xs[1] + bc * xstep),
                                          (lds_void_t)(slot + SL::ACT + (2 * wave + 1) * 1024), 16, 0, 0);
         if (h == 0) {
-            __builtin_amdgcn_global_load_lds((glb_void_t)(ds + bc), (lds_void_t)(slot + SL::ADX + 128 * wave), 4, 0, 0);
+            __builtin_amdgcn_global_load_lds((glb_void_t)(ds + bc * dstep), (lds_void_t)(slot + SL::ADX + 128 * wave), 4,
+                                             0, 0);
             __builtin_amdgcn_global_load_lds((glb_void_t)(wd + (int64_t)(bc >> 3) * 1024 + (bc & 7) * 2),
                                              (lds_void_t)(slot + SL::WD + 128 * wave), 2, 0, 0);
         }
@@ -291,6 +306,63 @@ __device__ __forceinline__ void mma_tile(const MmaArgs& g, const Tile& tl, int c
     // the loads issued past the last block land in this workgroup's LDS: let them finish before it ends
     __builtin_amdgcn_s_waitcnt(0);
 
+    if (g.qout.qh) {  // uniform: the requant epilogue (src/GemmaCpu.cs:415, src/CpuRef.cs:49-62)
+        // the gate wave of each pair (half 0) hands its g values to the up wave through the ring
+        __syncthreads();  // every wave is done with the ring
+        float* xg = (float*)ring + (wave >> 1) * (MMA_NT * 16 * 64);
+        if (half == 0) {
+#pragma unroll
+            for (int j = 0; j < NJ; j++)
+#pragma unroll
+                for (int q = 0; q < 16; q++) xg[(j * 16 + q) * 64 + lane] = S[j][q];
+        }
+        __syncthreads();
+        if (half == 1 && live) {
+            const Act& o = g.qout;
+#pragma unroll
+            for (int j = 0; j < NJ; j++) {
+                // lane (r32, h): token column r32 of tile j, block columns 8 (q / 4) + 4 h + q % 4
+                float e[16], am = 0.0f;
+#pragma unroll
+                for (int q = 0; q < 16; q++) {
+                    const int col = gI * 32 + 8 * (q >> 2) + 4 * h + (q & 3);
+                    e[q] = col < g.split ? gelu_ref(xg[(j * 16 + q) * 64 + lane], g.gelu_tab) * S[j][q] : 0.0f;
+                    am = fmaxf(am, fabsf(e[q]));
+                }
+                am = fmaxf(am, __shfl_xor(am, 32, 64));  // the other 16 columns: lane r32 + 32 (1 - 2 h)
+                const float dd = am / 127.0f;
+                const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
+                // the integers as exact fp16 (signed bytes through the 1152 bias), four per column group
+                uint32_t w[4][2];
+#pragma unroll
+                for (int g4 = 0; g4 < 4; g4++) {
+                    const int q0 = (int)roundf(e[4 * g4] * id), q1 = (int)roundf(e[4 * g4 + 1] * id),
+                              q2 = (int)roundf(e[4 * g4 + 2] * id), q3 = (int)roundf(e[4 * g4 + 3] * id);
+                    const uint32_t u = (uint32_t)((q0 & 0xFF) | ((q1 & 0xFF) << 8) | ((q2 & 0xFF) << 16) |
+                                                  ((unsigned)q3 << 24)) ^ 0x80808080u;
+                    w[g4][0] = bias_pair(u, 0, 1152.0f);
+                    w[g4][1] = bias_pair(u, 1, 1152.0f);
+                }
+                // this lane writes columns 16 h .. 16 h + 15: groups 2 h and 2 h + 1 of both halves (the
+                // partner lane's half from it)
+                const uint32_t s0 = h ? w[0][0] : w[2][0], s1 = h ? w[0][1] : w[2][1];
+                const uint32_t s2 = h ? w[1][0] : w[3][0], s3 = h ? w[1][1] : w[3][1];
+                const uint32_t p0 = (uint32_t)__shfl_xor((int)s0, 32, 64), p1 = (uint32_t)__shfl_xor((int)s1, 32, 64);
+                const uint32_t p2 = (uint32_t)__shfl_xor((int)s2, 32, 64), p3 = (uint32_t)__shfl_xor((int)s3, 32, 64);
+                const uint4 lo = h ? make_uint4(p0, p1, w[2][0], w[2][1]) : make_uint4(w[0][0], w[0][1], p0, p1);
+                const uint4 hi = h ? make_uint4(p2, p3, w[3][0], w[3][1]) : make_uint4(w[1][0], w[1][1], p2, p3);
+                const int sidx = 32 * j + r32;
+                if (sidx < cnt) {
+                    const int64_t pos = (int64_t)gI * g.qnpos + tl.start + sidx;
+                    uint16_t* hq = o.qh + pos * 32 + 16 * h;
+                    *(uint4*)hq = lo;
+                    *(uint4*)(hq + 8) = hi;
+                    if (h == 0) o.d[pos] = h2f(f2h_bits(dd));
+                }
+            }
+        }
+    }
+
     // results: lane holds rows i_q = 8 (q / 4) + 4 h + (q % 4) of the wave's 32, token column r32
     if (!live) return;
 #pragma unroll
@@ -332,7 +404,8 @@ __global__ __launch_bounds__(256) void k_grouped_mfma(MmaArgs g)
 }
 
 void launch_grouped_mfma(hipStream_t st, const QMat& w, Act act, const Tile* tiles, const int* ntiles, int max_tiles,
-                         const int* perm, int act_div, float* out0, float* out1, int split, int out_stride)
+                         const int* perm, int act_div, float* out0, float* out1, int split, int out_stride,
+                         int64_t npos, const Act* qout, int64_t qnpos, const float* gelu_tab)
 {
     MmaArgs g;
     g.payload = w.payload;
@@ -354,6 +427,10 @@ void launch_grouped_mfma(hipStream_t st, const QMat& w, Act act, const Tile* til
     g.split = split;
     g.out_stride = out_stride;
     g.paired = w.paired;
+    g.npos = npos;
+    g.qout = qout && w.paired ? *qout : Act{};
+    g.qnpos = qnpos;
+    g.gelu_tab = gelu_tab;
     const dim3 grid((w.rg + 1) / 2, max_tiles);
     if (w.type == PHX_Q4_0_DEV) launch(k_grouped_mfma<PHX_Q4_0_DEV>, grid, dim3(256), 0, st, g);
     else launch(k_grouped_mfma<PHX_Q8_0_DEV>, grid, dim3(256), 0, st, g);

@@ -113,10 +113,15 @@ void launch_grouped(hipStream_t st, const QMat& w, Act act, const Tile* tiles, c
                     int A, const int* perm, int act_div, float* out0, float* out1, int split, int out_stride);
 void launch_requant(hipStream_t st, int rows, int nf, const float* g, const float* u, const float* gelu_tab, Act act);
 // prefill path (kernels_prefill.hip): Q4_0 / Q8_0 grouped products on MFMA, tiles of up to kMmaTile
-// assignments; same arguments and outputs as launch_grouped
+// assignments; same arguments and outputs as launch_grouped.  npos > 0 reads the activations in
+// expert-list order, block-major (fp16 integers of block b, list position p at qh + (b * npos + p) * 32,
+// scales at d[b * npos + p]).  For a paired gate|up matrix with qout set, the kernel also does the
+// GELU-gated requant into qout in that layout over qnpos positions (its qh and d only).
 constexpr int kMmaTile = 128;
 void launch_grouped_mfma(hipStream_t st, const QMat& w, Act act, const Tile* tiles, const int* ntiles, int max_tiles,
-                         const int* perm, int act_div, float* out0, float* out1, int split, int out_stride);
+                         const int* perm, int act_div, float* out0, float* out1, int split, int out_stride,
+                         int64_t npos = 0, const Act* qout = nullptr, int64_t qnpos = 0,
+                         const float* gelu_tab = nullptr);
 void launch_combine(hipStream_t st, int T, int d, int k, float eps, const float* yd, const float* w,
                     const float* shared, const float* post1, const float* post2, float* out, float* x_resid,
                     const float* post_ffw, int* flags);

@@ -655,21 +655,21 @@ int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, con
         launch_dispatch(st, n, E, tileA, wp<int>(c, W_IDS), wp<int>(c, W_OFF), wp<int>(c, W_PERM), wp<Tile>(c, W_TILES),
                         wp<int>(c, W_NTILES));
     }
-    {
-        ProfScope p(c, PHX_K_GATE_UP);
-        if (mma)
-            launch_grouped_mfma(st, L.gu, agu, wp<Tile>(c, W_TILES), wp<int>(c, W_NTILES), max_tiles, wp<int>(c, W_PERM), k,
-                                wp<float>(c, W_G), wp<float>(c, W_U), nf, nf);
-        else
-            launch_grouped(st, L.gu, agu, wp<Tile>(c, W_TILES), wp<int>(c, W_NTILES), max_tiles, tileA, wp<int>(c, W_PERM),
-                           k, wp<float>(c, W_G), wp<float>(c, W_U), nf, nf);
-    }
     Act adn = make_act(c, act_fmt(D.down_type), D.down_cols, W_ADN_Q, W_ADN_D, W_ADN_S);
     if (mma) {
         adn.qh = wp<uint16_t>(c, W_ADN_H);
         adn.qhstride = D.down_cols;
     }
     {
+        ProfScope p(c, PHX_K_GATE_UP);
+        if (mma)  // the matrix-core gate|up also writes the down input (GELU-gated Q8_0, list order)
+            launch_grouped_mfma(st, L.gu, agu, wp<Tile>(c, W_TILES), wp<int>(c, W_NTILES), max_tiles, wp<int>(c, W_PERM), k,
+                                wp<float>(c, W_G), wp<float>(c, W_U), nf, nf, 0, &adn, n, c->gelu_tab);
+        else
+            launch_grouped(st, L.gu, agu, wp<Tile>(c, W_TILES), wp<int>(c, W_NTILES), max_tiles, tileA, wp<int>(c, W_PERM),
+                           k, wp<float>(c, W_G), wp<float>(c, W_U), nf, nf);
+    }
+    if (!mma) {
         ProfScope p(c, PHX_K_REQUANT);
         launch_requant(st, n, nf, wp<float>(c, W_G), wp<float>(c, W_U), c->gelu_tab, adn);
     }
@@ -677,7 +677,7 @@ int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, con
         ProfScope p(c, PHX_K_DOWN);
         if (mma)
             launch_grouped_mfma(st, L.dn, adn, wp<Tile>(c, W_TILES), wp<int>(c, W_NTILES), max_tiles, wp<int>(c, W_PERM), 1,
-                                wp<float>(c, W_YD), wp<float>(c, W_YD), d, d);
+                                wp<float>(c, W_YD), wp<float>(c, W_YD), d, d, n);
         else
             launch_grouped(st, L.dn, adn, wp<Tile>(c, W_TILES), wp<int>(c, W_NTILES), max_tiles, tileA, wp<int>(c, W_PERM),
                            1, wp<float>(c, W_YD), wp<float>(c, W_YD), d, d);
@@ -690,22 +690,22 @@ int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, con
         const int smax = (T + sA - 1) / sA + 1;
         launch_dispatch(st, T, 1, sA, wp<int>(c, W_ZERO), wp<int>(c, W_SOFF), wp<int>(c, W_SPERM), wp<Tile>(c, W_STILES),
                         wp<int>(c, W_SNTILES));
-        if (smma)
-            launch_grouped_mfma(st, L.sgu, ash, wp<Tile>(c, W_STILES), wp<int>(c, W_SNTILES), smax, wp<int>(c, W_SPERM), 1,
-                                wp<float>(c, W_SHG), wp<float>(c, W_SHU), nff, nff);
-        else
-            launch_grouped(st, L.sgu, ash, wp<Tile>(c, W_STILES), wp<int>(c, W_SNTILES), smax, kTileA, wp<int>(c, W_SPERM),
-                           1, wp<float>(c, W_SHG), wp<float>(c, W_SHU), nff, nff);
         Act asd = make_act(c, act_fmt(D.shared_type), round_up(nff, block_elems(D.shared_type)), W_ASD_Q, W_ASD_D,
                            W_ASD_S);
         if (smma) {
             asd.qh = wp<uint16_t>(c, W_ASD_H);
             asd.qhstride = asd.cols;
         }
-        launch_requant(st, T, nff, wp<float>(c, W_SHG), wp<float>(c, W_SHU), c->gelu_tab, asd);
+        if (smma)
+            launch_grouped_mfma(st, L.sgu, ash, wp<Tile>(c, W_STILES), wp<int>(c, W_SNTILES), smax, wp<int>(c, W_SPERM), 1,
+                                wp<float>(c, W_SHG), wp<float>(c, W_SHU), nff, nff, 0, &asd, T, c->gelu_tab);
+        else
+            launch_grouped(st, L.sgu, ash, wp<Tile>(c, W_STILES), wp<int>(c, W_SNTILES), smax, kTileA, wp<int>(c, W_SPERM),
+                           1, wp<float>(c, W_SHG), wp<float>(c, W_SHU), nff, nff);
+        if (!smma) launch_requant(st, T, nff, wp<float>(c, W_SHG), wp<float>(c, W_SHU), c->gelu_tab, asd);
         if (smma)
             launch_grouped_mfma(st, L.sdn, asd, wp<Tile>(c, W_STILES), wp<int>(c, W_SNTILES), smax, wp<int>(c, W_SPERM), 1,
-                                wp<float>(c, W_SHOUT), wp<float>(c, W_SHOUT), d, d);
+                                wp<float>(c, W_SHOUT), wp<float>(c, W_SHOUT), d, d, T);
         else
             launch_grouped(st, L.sdn, asd, wp<Tile>(c, W_STILES), wp<int>(c, W_SNTILES), smax, kTileA, wp<int>(c, W_SPERM),
                            1, wp<float>(c, W_SHOUT), wp<float>(c, W_SHOUT), d, d);

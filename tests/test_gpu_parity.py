@@ -106,6 +106,15 @@ def test_selftest_arith(ctx, orc):
     np.testing.assert_array_equal(ctx.selftest(3, r), rr)
     # fp16 bits (round to nearest even) against the oracle's Half.FromFloat
     np.testing.assert_array_equal(ctx.selftest(4, a).astype(np.uint32), orc.half_from_float(a).astype(np.uint32))
+    # and its edge cases: NaNs of both signs and any payload, infinities, signed zeros, overflow and
+    # the 65520 boundary, ties to even among normals and subnormals, the 2^-25 underflow boundary
+    edge = np.array([0.0, -0.0, np.inf, -np.inf, 65504.0, 65519.996, 65520.0, -65520.0, 1e30,
+                     1.0 + 2.0 ** -11, 1.0 + 3 * 2.0 ** -11, 2.0 ** -14, 2.0 ** -14 * (1 - 2.0 ** -11),
+                     2.0 ** -24, 2.0 ** -25, 1.5 * 2.0 ** -25, 2.0 ** -25 * (1 + 2.0 ** -20), 2.0 ** -26,
+                     -2.0 ** -25, 3 * 2.0 ** -25, 5 * 2.0 ** -25, 2.0 ** -30], dtype=np.float32)
+    nans = np.array([0x7FC00000, 0xFFC00000, 0x7F800001, 0xFF812345, 0x7FFFFFFF], dtype=np.uint32).view(np.float32)
+    edge = np.concatenate([edge, nans])
+    np.testing.assert_array_equal(ctx.selftest(4, edge).astype(np.uint32), orc.half_from_float(edge).astype(np.uint32))
     # nearest_int (1.5*2^23) on |x| < 2^22
     z = (rng.uniform(-4e6, 4e6, 4096)).astype(np.float32)
     z = np.concatenate([z, np.arange(-200, 200, dtype=np.float32) + 0.5])
