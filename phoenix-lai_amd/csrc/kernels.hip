@@ -191,26 +191,44 @@ __global__ __launch_bounds__(64) void k_router_exact(int T, int d, int E, const 
     }
 }
 
-// Many tokens: one wave per (64 experts, token) and no LDS, so the occupancy hides the load latency.
-__global__ __launch_bounds__(64) void k_router_exact_wide(int d, int E, const float4* __restrict__ wt4,
+// Many tokens: one wave per (64 experts, RXW_TB tokens) and no LDS, so the occupancy hides the load
+// latency.  Lane e carries the RXW_TB tokens' chains (each in index order): one column load serves
+// them all, which is what bounds this kernel (the per-CU vector load bandwidth), and the independent
+// chains fill the add latency; the token rows of m are wave-uniform (scalar loads).  Eight column
+// loads per lane in flight.
+constexpr int RXW_TB = 2;
+__global__ __launch_bounds__(64) void k_router_exact_wide(int T, int d, int E, const float4* __restrict__ wt4,
                                                           const float* __restrict__ rin, float* __restrict__ logits)
 {
-    const int e = blockIdx.x * 64 + threadIdx.x, t = blockIdx.y;
-    const int ee = e < E ? e : E - 1;
+    const int e = blockIdx.x * 64 + threadIdx.x, t0 = blockIdx.y * RXW_TB;
+    const int ee = min(e, E - 1);
     const float4* w = wt4 + ee;
-    const float4* m = (const float4*)(rin + (int64_t)t * d);
-    float s = 0.0f;
-    const int n4 = d / 4;
-#pragma unroll 4
-    for (int i = 0; i < n4; i++) {
-        const float4 wv = w[(int64_t)i * E];
-        const float4 mv = m[i];
-        s += wv.x * mv.x;
-        s += wv.y * mv.y;
-        s += wv.z * mv.z;
-        s += wv.w * mv.w;
+    const float4* m[RXW_TB];
+#pragma unroll
+    for (int b = 0; b < RXW_TB; b++) m[b] = (const float4*)(rin + (int64_t)min(t0 + b, T - 1) * d);
+    float s[RXW_TB];
+#pragma unroll
+    for (int b = 0; b < RXW_TB; b++) s[b] = 0.0f;
+    const int n4 = d / 4;  // d % 32 == 0: whole groups of eight
+    for (int i = 0; i < n4; i += 8) {
+        float4 wv[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) wv[u] = w[(int64_t)(i + u) * E];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+#pragma unroll
+            for (int b = 0; b < RXW_TB; b++) {
+                const float4 mv = m[b][i + u];
+                s[b] += wv[u].x * mv.x;
+                s[b] += wv[u].y * mv.y;
+                s[b] += wv[u].z * mv.z;
+                s[b] += wv[u].w * mv.w;
+            }
+        }
     }
-    if (e < E) logits[(int64_t)t * E + e] = s;
+#pragma unroll
+    for (int b = 0; b < RXW_TB; b++)
+        if (e < E && t0 + b < T) logits[(int64_t)(t0 + b) * E + e] = s[b];
 }
 
 // Fewer tokens: each lane carries TB tokens' sequential chains (each in index order, as the
@@ -222,7 +240,7 @@ void launch_router_exact(hipStream_t st, int T, int d, int E, const float* wt4, 
     const int gx = (E + 63) / 64;
     const float4* w = (const float4*)wt4;
     if (T >= 1024)
-        launch(k_router_exact_wide, dim3(gx, T), dim3(64), 0, st, d, E, w, rin, logits);
+        launch(k_router_exact_wide, dim3(gx, (T + RXW_TB - 1) / RXW_TB), dim3(64), 0, st, T, d, E, w, rin, logits);
     else if (T >= 128)
         launch(k_router_exact<2>, dim3(gx, (T + 1) / 2), dim3(64), (uint32_t)(2 * d * 4), st, T, d, E, w, rin, logits);
     else

@@ -239,6 +239,33 @@ def test_c3_prefill_reduced(ctx, pkg, orc):
     check_layer(ctx, orc, L, x, tag="c3 T=48")
 
 
+def test_c3_prefill_wide_router(ctx, pkg, orc):
+    """T = 1030 (past the size where the exact router switches to its many-token kernel, and not a
+    multiple of its four-token workgroups): router logits bit-exact for every token through the exact
+    router, ids and expert lists bit-exact, and the layer output of 40 sampled tokens bit-exact."""
+    T = 1030
+    say(f"c3_prefill T={T} (zipf router, exact)")
+    L = pkg.synth.make_layer("c3_prefill")
+    x = pkg.synth.make_input("c3_prefill", T=T)
+    ctx.upload(0, L)
+    out = ctx.ffn(0, x, exact_router=True)
+    ids, w, off, perm, logits = ctx.routing()
+    k = L["n_used"]
+    for t in range(T):
+        rlog, rids, rw = orc.router(L, x[t])
+        np.testing.assert_array_equal(logits[t], rlog, err_msg=f"t={t} logits")
+        np.testing.assert_array_equal(ids[t], rids, err_msg=f"t={t} ids")
+    roff, rperm = orc.bucket(ids, L["n_expert"])
+    np.testing.assert_array_equal(off, roff)
+    np.testing.assert_array_equal(perm, rperm)
+    rng = np.random.default_rng(5)
+    sample = sorted(set([0, 1, T - 2, T - 1] + rng.choice(T, 36, replace=False).tolist()))
+    for t in sample:
+        rout = orc.moe_token(L, x[t], orc.shared_ffn(L, x[t]) if L.get("n_ff_shared", 0) > 0 else None)[0]
+        np.testing.assert_array_equal(out[t], rout, err_msg=f"t={t} output")
+    say(f"c3 T={T}: logits, ids, lists bit-exact; {len(sample)} sampled outputs bit-exact")
+
+
 def test_c4_kquant_reduced(ctx, pkg, orc):
     say("c4_kquant T=12")
     L = pkg.synth.make_layer("c4_kquant")
