@@ -38,8 +38,8 @@ METRIC = "MoE layer tokens/s; decode HBM GB/s vs peak; prefill MFMA util"
 # streaming read and copy kernels of known size (fetch factor 2.000, write factor 1.000).  Keyed by
 # (config, T, kernel); re-measured whenever that kernel changes.
 PMC_TRAFFIC = {
-    # FETCH_SIZE 12,381.8 KiB x 2.000 + WRITE_SIZE 86.6 KiB x 1.000 per launch of phx::k_dec_gu<2>
-    ("c2_decode", 1, "gate_up"): (25_446_605, "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, 305 launches each"),
+    # FETCH_SIZE 12,377.4 KiB x 2.000 + WRITE_SIZE 86.6 KiB x 1.000 per launch of phx::k_dec_gu<2>
+    ("c2_decode", 1, "gate_up"): (25_437_594, "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, 337 launches each"),
 }
 
 
