@@ -25,7 +25,9 @@
 // the code waits for itself (the compiler would otherwise wait for every outstanding direct load
 // before any LDS read).  Activation rows sit in 16-token groups of 1 KB with the four 16-byte parts
 // of token t at slot 4 (t % 16) + (part ^ ((t % 16) / 4)), so the 32 lanes of an operand read hit
-// 32 distinct bank groups.
+// 32 distinct bank groups.  A wave keeps one block-sum / scale-product pair (each column's chain
+// follows its own products), which holds it to 163 VGPRs: three workgroups per CU (three waves per
+// SIMD, 3 x 44 KB of LDS for Q4_0) fill each other's waits.
 #include "device_common.h"
 
 namespace phx {
@@ -268,36 +270,36 @@ __device__ __forceinline__ void mma_tile(const MmaArgs& g, const Tile& tl, int c
         }
         ad.x = wdv & hmask;
         const mh8 Ad = __builtin_bit_cast(mh8, ad);
-        mf16 C[2], D[2];  // slots j % 2: compile-time after unrolling, so no copies
+        mf16 C, D;  // one slot: each column's chain follows its own products (three waves per SIMD
+                    // fill the wait; a second slot would cost the third wave's registers)
         auto products = [&](int j) {
             const int s = j & 1;
             // the token scale is an fp16 value: the conversion is exact
             bd.x = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)__uint_as_float(dx[s])) & hmask;
-            C[s] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A0, __builtin_bit_cast(mh8, B0[s]), zero, 0, 0, 0);
-            C[s] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A1, __builtin_bit_cast(mh8, B1[s]), C[s], 0, 0, 0);
-            D[s] = __builtin_amdgcn_mfma_f32_32x32x16_f16(Ad, __builtin_bit_cast(mh8, bd), zero, 0, 0, 0);
+            C = __builtin_amdgcn_mfma_f32_32x32x16_f16(A0, __builtin_bit_cast(mh8, B0[s]), zero, 0, 0, 0);
+            C = __builtin_amdgcn_mfma_f32_32x32x16_f16(A1, __builtin_bit_cast(mh8, B1[s]), C, 0, 0, 0);
+            D = __builtin_amdgcn_mfma_f32_32x32x16_f16(Ad, __builtin_bit_cast(mh8, bd), zero, 0, 0, 0);
         };
-        products(0);
         if (NJ > 1) reads(1);
 #pragma unroll
         for (int j = 0; j < NJ; j++) {
-            if (j + 1 < NJ) {
-                const int s = (j + 1) & 1;
+            if (j > 0) {
+                const int s = j & 1;
                 lds_wait(B0[s], B1[s], dx[s]);
-                products(j + 1);
-                if (j + 2 < NJ) reads(j + 2);
-            } else {
+            }
+            products(j);
+            if (j + 2 < NJ) reads(j + 2);
+            if (j == NJ - 1) {
                 // the next block lands and its first reads go out behind this block's last chain (after
                 // the last block: a harmless extra barrier and reads of a slot nobody uses)
                 land(b + 1);
                 start_reads(b + 1);
             }
-            // keep the program order: tile j + 1's products and the reads ahead of tile j's chain, each
-            // tile's chain between its neighbours' matrix products (two C / D slots, no more)
+            // keep the program order: the reads ahead of the chain, the chain before the next column
             __builtin_amdgcn_sched_barrier(0);
             // the reference chain: sum += (float)isum * (d_w * d_x), in block order
 #pragma unroll
-            for (int q = 0; q < 16; q++) S[j][q] = S[j][q] + C[j & 1][q] * D[j & 1][q];
+            for (int q = 0; q < 16; q++) S[j][q] = S[j][q] + C[q] * D[q];
             asm volatile("" : "+v"(S[j]));  // the chain stays here, not sunk towards its next use
             __builtin_amdgcn_sched_barrier(0);
             if (j == NJ - 1) start_wait();  // in the reads' basic block: the loop carries landed values
@@ -307,14 +309,23 @@ __device__ __forceinline__ void mma_tile(const MmaArgs& g, const Tile& tl, int c
     __builtin_amdgcn_s_waitcnt(0);
 
     if (g.qout.qh) {  // uniform: the requant epilogue (src/GemmaCpu.cs:415, src/CpuRef.cs:49-62)
-        // the gate wave of each pair (half 0) hands its g values to the up wave through the ring
+        // the gate wave of each pair (half 0) forms gelu(g) (src/CpuRefGemma.cs:85-92: the table lookups
+        // of all its values issued together) and hands it to the up wave through the ring
         __syncthreads();  // every wave is done with the ring
         float* xg = (float*)ring + (wave >> 1) * (MMA_NT * 16 * 64);
         if (half == 0) {
+            float tv[NJ][16];
 #pragma unroll
             for (int j = 0; j < NJ; j++)
 #pragma unroll
-                for (int q = 0; q < 16; q++) xg[(j * 16 + q) * 64 + lane] = S[j][q];
+                for (int q = 0; q < 16; q++) tv[j][q] = g.gelu_tab[f2h_bits(S[j][q])];
+#pragma unroll
+            for (int j = 0; j < NJ; j++)
+#pragma unroll
+                for (int q = 0; q < 16; q++) {
+                    const float v = S[j][q];
+                    xg[(j * 16 + q) * 64 + lane] = v <= -10.0f ? 0.0f : (v >= 10.0f ? v : tv[j][q]);
+                }
         }
         __syncthreads();
         if (half == 1 && live) {
@@ -326,7 +337,7 @@ __device__ __forceinline__ void mma_tile(const MmaArgs& g, const Tile& tl, int c
 #pragma unroll
                 for (int q = 0; q < 16; q++) {
                     const int col = gI * 32 + 8 * (q >> 2) + 4 * h + (q & 3);
-                    e[q] = col < g.split ? gelu_ref(xg[(j * 16 + q) * 64 + lane], g.gelu_tab) * S[j][q] : 0.0f;
+                    e[q] = col < g.split ? xg[(j * 16 + q) * 64 + lane] * S[j][q] : 0.0f;
                     am = fmaxf(am, fabsf(e[q]));
                 }
                 am = fmaxf(am, __shfl_xor(am, 32, 64));  // the other 16 columns: lane r32 + 32 (1 - 2 h)
@@ -388,7 +399,7 @@ __device__ __forceinline__ void mma_tile(const MmaArgs& g, const Tile& tl, int c
 }
 
 template <int TYPE>
-__global__ __launch_bounds__(256) void k_grouped_mfma(MmaArgs g)
+__global__ __launch_bounds__(256, 3) void k_grouped_mfma(MmaArgs g)
 {
     __shared__ __align__(16) unsigned char ring[MMA_RING * MmaSlot<TYPE>::BYTES];
     const int tile = blockIdx.y;
