@@ -381,18 +381,33 @@ __device__ __forceinline__ void mma_tile(const MmaArgs& g, const Tile& tl, int c
         const int sidx = 32 * j + r32;
         if (sidx >= cnt) continue;
         const int64_t a = g.perm[tl.start + sidx];
+        // four consecutive rows (columns of the output row a) per q4: one 16-byte store where the four
+        // lie inside the output and the row stride keeps them aligned, else element by element
+        const bool vec = (g.out_stride & 3) == 0;
 #pragma unroll
-        for (int q = 0; q < 16; q++) {
-            const int lg = half * 32 + 8 * (q >> 2) + 4 * h + (q & 3);  // lane within the row group
+        for (int q4 = 0; q4 < 4; q4++) {
+            const int lg0 = half * 32 + 8 * q4 + 4 * h;  // lane within the row group of the first of four
+            const float4 v = make_float4(S[j][4 * q4], S[j][4 * q4 + 1], S[j][4 * q4 + 2], S[j][4 * q4 + 3]);
             if (g.paired) {
-                const int col = gI * 32 + (lg & 31);
-                if (col < g.split) (lg < 32 ? g.out0 : g.out1)[a * g.out_stride + col] = S[j][q];
+                const int col = gI * 32 + (lg0 & 31);
+                float* dst = (half ? g.out1 : g.out0) + a * g.out_stride + col;
+                if (vec && col + 3 < g.split) *(float4*)dst = v;
+                else
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        if (col + i < g.split) dst[i] = S[j][4 * q4 + i];
             } else {
-                const int row = gI * 64 + lg;
-                if (row < g.rows) {
-                    if (row < g.split) g.out0[a * g.out_stride + row] = S[j][q];
-                    else g.out1[a * g.out_stride + row - g.split] = S[j][q];
-                }
+                const int row = gI * 64 + lg0;
+                if (vec && row + 3 < min(g.rows, g.split)) *(float4*)(g.out0 + a * g.out_stride + row) = v;
+                else
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const int r = row + i;
+                        if (r < g.rows) {
+                            if (r < g.split) g.out0[a * g.out_stride + r] = S[j][4 * q4 + i];
+                            else g.out1[a * g.out_stride + r - g.split] = S[j][4 * q4 + i];
+                        }
+                    }
             }
         }
     }
