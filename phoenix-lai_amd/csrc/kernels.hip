@@ -191,44 +191,70 @@ __global__ __launch_bounds__(64) void k_router_exact(int T, int d, int E, const 
     }
 }
 
-// Many tokens: one wave per (64 experts, RXW_TB tokens) and no LDS, so the occupancy hides the load
-// latency.  Lane e carries the RXW_TB tokens' chains (each in index order): one column load serves
-// them all, which is what bounds this kernel (the per-CU vector load bandwidth), and the independent
-// chains fill the add latency; the token rows of m are wave-uniform (scalar loads).  Eight column
-// loads per lane in flight.
-constexpr int RXW_TB = 2;
-__global__ __launch_bounds__(64) void k_router_exact_wide(int T, int d, int E, const float4* __restrict__ wt4,
-                                                          const float* __restrict__ rin, float* __restrict__ logits)
+// Many tokens: a workgroup of four waves takes 64 experts and 8 tokens; wave w carries tokens 2w and
+// 2w + 1, lane e expert e, each chain in index order (the reference's sequential sum).  The router
+// columns of the 64 experts and the 8 token rows of m stream through LDS in 128-element chunks (36 KB,
+// two buffers): every thread loads its share of the next chunk into registers before the current
+// chunk's adds and stores it after, one barrier per chunk.  W leaves L2 once per eight tokens and
+// reaches the lanes at the LDS rate, and with every operand read from LDS the reads of the next eight
+// columns can go out ahead of the current eight's adds (LDS reads complete in order).
+constexpr int RXW_TOK = 8, RXW_CH4 = 32;  // tokens per workgroup; float4 columns per chunk
+__global__ __launch_bounds__(256, 2) void k_router_exact_wide(int T, int d, int E, const float4* __restrict__ wt4,
+                                                              const float* __restrict__ rin,
+                                                              float* __restrict__ logits)
 {
-    const int e = blockIdx.x * 64 + threadIdx.x, t0 = blockIdx.y * RXW_TB;
-    const int ee = min(e, E - 1);
-    const float4* w = wt4 + ee;
-    const float4* m[RXW_TB];
+    __shared__ float4 wbuf[2][RXW_CH4][64];
+    __shared__ float4 mbuf[2][RXW_TOK][RXW_CH4];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int e0 = blockIdx.x * 64, e = e0 + lane;
+    const int tb = blockIdx.y * RXW_TOK, t0 = tb + 2 * wave;
+    const int n4 = d / 4, nch = (n4 + RXW_CH4 - 1) / RXW_CH4;
+    // this thread's share of a chunk: W columns (tid / 64) + 4 k, k = 0..7, of expert e0 + lane, and
+    // column tid % 32 of token row tid / 32
+    const int er = min(e, E - 1), cr = tid >> 6, mt = tid >> 5, mc = tid & 31;
+    const float4* mrow = (const float4*)(rin + (int64_t)min(tb + mt, T - 1) * d);
+    float4 st[8], sm;
 #pragma unroll
-    for (int b = 0; b < RXW_TB; b++) m[b] = (const float4*)(rin + (int64_t)min(t0 + b, T - 1) * d);
-    float s[RXW_TB];
+    for (int k = 0; k < 8; k++) st[k] = wt4[(int64_t)min(cr + 4 * k, n4 - 1) * E + er];
+    sm = mrow[min(mc, n4 - 1)];
 #pragma unroll
-    for (int b = 0; b < RXW_TB; b++) s[b] = 0.0f;
-    const int n4 = d / 4;  // d % 32 == 0: whole groups of eight
-    for (int i = 0; i < n4; i += 8) {
-        float4 wv[8];
+    for (int k = 0; k < 8; k++) wbuf[0][cr + 4 * k][lane] = st[k];
+    mbuf[0][mt][mc] = sm;
+    __syncthreads();
+    float s0 = 0.0f, s1 = 0.0f;
+    for (int c = 0; c < nch; c++) {
+        const int buf = c & 1;
+        // the next chunk's loads (past the last chunk: a clamped reload nobody reads)
+        const int cn = min(c + 1, nch - 1) * RXW_CH4;
 #pragma unroll
-        for (int u = 0; u < 8; u++) wv[u] = w[(int64_t)(i + u) * E];
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-#pragma unroll
-            for (int b = 0; b < RXW_TB; b++) {
-                const float4 mv = m[b][i + u];
-                s[b] += wv[u].x * mv.x;
-                s[b] += wv[u].y * mv.y;
-                s[b] += wv[u].z * mv.z;
-                s[b] += wv[u].w * mv.w;
-            }
+        for (int k = 0; k < 8; k++) st[k] = wt4[(int64_t)min(cn + cr + 4 * k, n4 - 1) * E + er];
+        sm = mrow[min(cn + mc, n4 - 1)];
+        const int ni = min(RXW_CH4, n4 - c * RXW_CH4);  // d % 32 == 0: ni % 8 == 0
+        const float4* m0 = mbuf[buf][2 * wave];
+        const float4* m1 = mbuf[buf][2 * wave + 1];
+#pragma unroll 8
+        for (int i = 0; i < ni; i++) {
+            const float4 w = wbuf[buf][i][lane];
+            const float4 a = m0[i], b = m1[i];
+            s0 += w.x * a.x;
+            s1 += w.x * b.x;
+            s0 += w.y * a.y;
+            s1 += w.y * b.y;
+            s0 += w.z * a.z;
+            s1 += w.z * b.z;
+            s0 += w.w * a.w;
+            s1 += w.w * b.w;
         }
-    }
 #pragma unroll
-    for (int b = 0; b < RXW_TB; b++)
-        if (e < E && t0 + b < T) logits[(int64_t)(t0 + b) * E + e] = s[b];
+        for (int k = 0; k < 8; k++) wbuf[buf ^ 1][cr + 4 * k][lane] = st[k];  // read before the last barrier
+        mbuf[buf ^ 1][mt][mc] = sm;
+        __syncthreads();
+    }
+    if (e < E) {
+        if (t0 < T) logits[(int64_t)t0 * E + e] = s0;
+        if (t0 + 1 < T) logits[(int64_t)(t0 + 1) * E + e] = s1;
+    }
 }
 
 // Fewer tokens: each lane carries TB tokens' sequential chains (each in index order, as the
@@ -240,7 +266,7 @@ void launch_router_exact(hipStream_t st, int T, int d, int E, const float* wt4, 
     const int gx = (E + 63) / 64;
     const float4* w = (const float4*)wt4;
     if (T >= 1024)
-        launch(k_router_exact_wide, dim3(gx, (T + RXW_TB - 1) / RXW_TB), dim3(64), 0, st, T, d, E, w, rin, logits);
+        launch(k_router_exact_wide, dim3(gx, (T + RXW_TOK - 1) / RXW_TOK), dim3(256), 0, st, T, d, E, w, rin, logits);
     else if (T >= 128)
         launch(k_router_exact<2>, dim3(gx, (T + 1) / 2), dim3(64), (uint32_t)(2 * d * 4), st, T, d, E, w, rin, logits);
     else
