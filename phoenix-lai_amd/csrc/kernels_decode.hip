@@ -91,6 +91,7 @@ struct DecArgs {
     float* shout;         // [T][d] shared branch (the shared FFN's output, or the given one), or null
     float* out;           // [T][d]
     float* xres;          // x updated in place with the residual, or null
+    const float* xin;     // with xres: the residual's source rows when not xres itself (or null)
     const float* gelu_tab;
     int* flags;           // [0] norm fallbacks, [1] router fallbacks
 };
@@ -407,6 +408,118 @@ __device__ __forceinline__ void gu_epilogue(float S, int rgi, int split, int64_t
 typedef __attribute__((address_space(3))) void* lds_void_t;
 typedef __attribute__((address_space(1))) void* glb_void_t;
 
+// ------------------------------------------------------------------------------ combine of a token
+// The layer's output for token t by a whole workgroup whose threads hold CQ float4 columns each
+// (CQ * 4 * blockDim.x >= d): acc = sum_j w_j * yd_j in rank order (src/GemmaCpu.cs:417-418, each
+// term rounded then added), out = rmsnorm(shared) * post1 + rmsnorm(acc) * post2 (src/GemmaCpu.cs:384,
+// 420-421), x_new = x + rmsnorm(out) * post_ffw_norm (src/GemmaCpu.cs:355-356), the same expressions
+// as k_dec_combine.  Every load is issued in one round into registers (the caller's occupancy is set
+// by its LDS, so the registers are free); x_new lands in sx (LDS, [d]); with leader, out and x_new
+// also go to p.out and p.xres (x read from p.xin).  sacc and so: LDS [d] each.
+// What the combine of a layer reads and writes (a small kernel argument of the fused router)
+struct CombArgs {
+    int d, k;
+    float eps;
+    const float *w, *yd, *shout, *post1, *post2, *post_ffw, *xin;
+    float *out, *xres;
+    int* flags;
+};
+
+template <int CQ>
+__device__ __forceinline__ void combine_into(const CombArgs& p, int t, float* sx, float* sacc, float* so, double* red,
+                                             bool leader)
+{
+    constexpr int RG = CQ <= 3 ? 8 : 4;  // ranks per load round (register budget)
+    const int tid = threadIdx.x, NT = blockDim.x, d = p.d, k = p.k, n4 = d / 4;
+    const float4* sh4 = p.shout ? (const float4*)(p.shout + (int64_t)t * d) : nullptr;
+    const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    int ix[CQ];
+    float4 acc[CQ], shv[CQ], p1[CQ], p2[CQ], xv[CQ], pf[CQ];
+#pragma unroll
+    for (int q = 0; q < CQ; q++) {
+        ix[q] = min(tid + q * NT, n4 - 1);
+        acc[q] = z4;
+    }
+    // pass 1: every load of the token in one round (ranks RG at a time), acc in rank order
+    for (int j0 = 0; j0 < k; j0 += RG) {
+        float4 yv[CQ][RG];
+        float wj[RG];
+#pragma unroll
+        for (int jj = 0; jj < RG; jj++) wj[jj] = p.w[(int64_t)t * k + min(j0 + jj, k - 1)];
+#pragma unroll
+        for (int q = 0; q < CQ; q++)
+#pragma unroll
+            for (int jj = 0; jj < RG; jj++)
+                yv[q][jj] = ((const float4*)(p.yd + ((int64_t)t * k + min(j0 + jj, k - 1)) * d))[ix[q]];
+        if (j0 == 0) {
+#pragma unroll
+            for (int q = 0; q < CQ; q++) {
+                shv[q] = sh4 ? sh4[ix[q]] : z4;
+                p1[q] = ((const float4*)p.post1)[ix[q]];
+                p2[q] = ((const float4*)p.post2)[ix[q]];
+                xv[q] = ((const float4*)(p.xin + (int64_t)t * d))[ix[q]];
+                pf[q] = ((const float4*)p.post_ffw)[ix[q]];
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < CQ; q++)
+#pragma unroll
+            for (int jj = 0; jj < RG; jj++)
+                if (j0 + jj < k) {
+                    acc[q].x += yv[q][jj].x * wj[jj];
+                    acc[q].y += yv[q][jj].y * wj[jj];
+                    acc[q].z += yv[q][jj].z * wj[jj];
+                    acc[q].w += yv[q][jj].w * wj[jj];
+                }
+    }
+    double s2 = 0.0, s1 = 0.0;
+#pragma unroll
+    for (int q = 0; q < CQ; q++)
+        if (tid + q * NT < n4) {
+            ((float4*)sacc)[tid + q * NT] = acc[q];
+            s2 += (double)acc[q].x * (double)acc[q].x + (double)acc[q].y * (double)acc[q].y;
+            s2 += (double)acc[q].z * (double)acc[q].z + (double)acc[q].w * (double)acc[q].w;
+            s1 += (double)shv[q].x * (double)shv[q].x + (double)shv[q].y * (double)shv[q].y;
+            s1 += (double)shv[q].z * (double)shv[q].z + (double)shv[q].w * (double)shv[q].w;
+        }
+    __syncthreads();
+    float m2, m1;
+    wg_mean_sq2(s2, s1, sacc, sh4 ? (const float*)sh4 : nullptr, d, red, leader ? p.flags : nullptr, &m2, &m1);
+    const float sc2 = rms_scale_from_mean(m2, p.eps);
+    const float sc1 = sh4 ? rms_scale_from_mean(m1, p.eps) : 0.0f;
+    // pass 2: out = rmsnorm(shared) * post1 + rmsnorm(acc) * post2 and its sum of squares
+    float4 ov[CQ];
+    double s3 = 0.0;
+#pragma unroll
+    for (int q = 0; q < CQ; q++) {
+        ov[q].x = (sh4 ? shv[q].x * sc1 * p1[q].x : 0.0f) + acc[q].x * sc2 * p2[q].x;
+        ov[q].y = (sh4 ? shv[q].y * sc1 * p1[q].y : 0.0f) + acc[q].y * sc2 * p2[q].y;
+        ov[q].z = (sh4 ? shv[q].z * sc1 * p1[q].z : 0.0f) + acc[q].z * sc2 * p2[q].z;
+        ov[q].w = (sh4 ? shv[q].w * sc1 * p1[q].w : 0.0f) + acc[q].w * sc2 * p2[q].w;
+        const int i4 = tid + q * NT;
+        if (i4 < n4) {
+            ((float4*)so)[i4] = ov[q];
+            if (leader) ((float4*)(p.out + (int64_t)t * d))[i4] = ov[q];
+            s3 += (double)ov[q].x * (double)ov[q].x + (double)ov[q].y * (double)ov[q].y;
+            s3 += (double)ov[q].z * (double)ov[q].z + (double)ov[q].w * (double)ov[q].w;
+        }
+    }
+    __syncthreads();
+    const float sc3 = rms_scale_from_mean(wg_mean_sq(s3, so, d, red, leader ? p.flags : nullptr), p.eps);
+    // pass 3: x_new = x + rmsnorm(out) * post_ffw_norm
+#pragma unroll
+    for (int q = 0; q < CQ; q++) {
+        const int i4 = tid + q * NT;
+        const float4 xn = make_float4(xv[q].x + ov[q].x * sc3 * pf[q].x, xv[q].y + ov[q].y * sc3 * pf[q].y,
+                                      xv[q].z + ov[q].z * sc3 * pf[q].z, xv[q].w + ov[q].w * sc3 * pf[q].w);
+        if (i4 < n4) {
+            ((float4*)sx)[i4] = xn;
+            if (leader) ((float4*)(p.xres + (int64_t)t * d))[i4] = xn;
+        }
+    }
+    __syncthreads();
+}
+
 // ------------------------------------------------------------------------------ k_dec_route
 // One workgroup of 256 threads per (token t, expert e); thread i holds the PER = d / 256 consecutive
 // elements PER*i..PER*i+PER-1 (x_t, the router scale and W[e] staged in LDS by direct global -> LDS
@@ -422,10 +535,11 @@ typedef __attribute__((address_space(1))) void* glb_void_t;
 // (:349) of the 32-blocks b with b % E == e, one 8-lane group per block.
 constexpr int RT_NT = 256;
 
-template <int PER>
-__device__ void route_wg(const DecArgs& a, int t, int e, float* sx, float* sg, float* sw)
+template <int PER, bool FUSED>
+__device__ __forceinline__ void route_wg(const DecArgs& a, int t, int e, float* sx, float* sg, float* sw,
+                                         const CombArgs& prev, float* scb)
 {
-    __shared__ double red[5], wsum[4];
+    __shared__ double red[5], wsum[4], red5[2 * (RT_NT / 64 + 1)];
     __shared__ float wA[4], wP[4];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, d = a.d;
     const float* xr = a.x + (int64_t)t * d;
@@ -443,9 +557,11 @@ __device__ void route_wg(const DecArgs& a, int t, int e, float* sx, float* sg, f
                                                      (lds_void_t)((float4*)dst + q * RT_NT + wave * 64), 16, 0, 0);
             }
         };
-        stage(xr, sx);
+        if (!FUSED) stage(xr, sx);
         stage(a.gis, sg);
         stage(a.W + (int64_t)e * d, sw);
+        // fused: this token's x is the previous layer's combine, formed here (scb: its two LDS rows)
+        if (FUSED) combine_into<(PER + 3) / 4>(prev, t, sx, scb, scb + d, red5, e == 0);
         __builtin_amdgcn_s_waitcnt(0);
     }
     __syncthreads();
@@ -538,31 +654,38 @@ __device__ void route_wg(const DecArgs& a, int t, int e, float* sx, float* sg, f
     }
 }
 
-__global__ __launch_bounds__(RT_NT) void k_dec_route(DecArgs a)
+template <bool FUSED>
+__device__ __forceinline__ void route_dispatch(const DecArgs& a, const CombArgs& prev, float* rsm)
 {
-    extern __shared__ __align__(16) float rsm[];  // x, router scale, W row: 3 * (d + 4) floats
     const int t = blockIdx.x / a.E, e = blockIdx.x % a.E, d = a.d;
     float* sx = rsm;
     float* sg = sx + d + 4;
     float* sw = sg + d + 4;
+    float* scb = sw + d + 4;  // fused: the combine's two rows
+#define RT_CASE(n) \
+    case n: route_wg<n, FUSED>(a, t, e, sx, sg, sw, prev, scb); break;
     switch (d / RT_NT) {
-    case 1: route_wg<1>(a, t, e, sx, sg, sw); break;
-    case 2: route_wg<2>(a, t, e, sx, sg, sw); break;
-    case 3: route_wg<3>(a, t, e, sx, sg, sw); break;
-    case 4: route_wg<4>(a, t, e, sx, sg, sw); break;
-    case 5: route_wg<5>(a, t, e, sx, sg, sw); break;
-    case 6: route_wg<6>(a, t, e, sx, sg, sw); break;
-    case 7: route_wg<7>(a, t, e, sx, sg, sw); break;
-    case 8: route_wg<8>(a, t, e, sx, sg, sw); break;
-    case 9: route_wg<9>(a, t, e, sx, sg, sw); break;
-    case 10: route_wg<10>(a, t, e, sx, sg, sw); break;
-    case 11: route_wg<11>(a, t, e, sx, sg, sw); break;
-    case 12: route_wg<12>(a, t, e, sx, sg, sw); break;
-    case 13: route_wg<13>(a, t, e, sx, sg, sw); break;
-    case 14: route_wg<14>(a, t, e, sx, sg, sw); break;
-    case 15: route_wg<15>(a, t, e, sx, sg, sw); break;
-    default: route_wg<16>(a, t, e, sx, sg, sw); break;
+        RT_CASE(1) RT_CASE(2) RT_CASE(3) RT_CASE(4) RT_CASE(5) RT_CASE(6) RT_CASE(7) RT_CASE(8) RT_CASE(9)
+        RT_CASE(10) RT_CASE(11) RT_CASE(12) RT_CASE(13) RT_CASE(14) RT_CASE(15)
+    default: route_wg<16, FUSED>(a, t, e, sx, sg, sw, prev, scb); break;
     }
+#undef RT_CASE
+}
+
+__global__ __launch_bounds__(RT_NT) void k_dec_route(DecArgs a)
+{
+    extern __shared__ __align__(16) float rsm[];  // x, router scale, W row: 3 * (d + 4) floats
+    route_dispatch<false>(a, CombArgs{}, rsm);
+}
+
+// A layer of a stack whose previous layer's combine is folded in: every (token, expert) workgroup forms
+// the token's x from the previous layer's outputs (combine_into, identical in every workgroup), the
+// expert-0 workgroup of each token also writes that layer's out and the new x, then the router as
+// k_dec_route.  One launch fewer per layer than route + combine.
+__global__ __launch_bounds__(RT_NT) void k_dec_route_fused(CombArgs prev, DecArgs a)
+{
+    extern __shared__ __align__(16) float rsm[];  // x, router scale, W row, combine rows: 5 * (d + 4)
+    route_dispatch<true>(a, prev, rsm);
 }
 
 // ------------------------------------------------------------------------------ shared FFN workgroups
@@ -1152,6 +1275,7 @@ __global__ __launch_bounds__(CB_NT) void k_dec_combine(DecArgs a)
     float* so = cb + d;
     const float* sh = a.shout ? a.shout + (int64_t)t * d : nullptr;
     float* xr = a.xres ? a.xres + (int64_t)t * d : nullptr;
+    const float* xi = a.xin ? a.xin + (int64_t)t * d : xr;  // the residual's source row
     int ix[CB_E];
     float accv[CB_E], shv[CB_E], p1[CB_E], p2[CB_E], xv[CB_E], pf[CB_E];
 #pragma unroll
@@ -1174,7 +1298,7 @@ __global__ __launch_bounds__(CB_NT) void k_dec_combine(DecArgs a)
                 shv[q] = sh ? sh[ix[q]] : 0.0f;
                 p1[q] = a.post1[ix[q]];
                 p2[q] = a.post2[ix[q]];
-                xv[q] = xr ? xr[ix[q]] : 0.0f;
+                xv[q] = xr ? xi[ix[q]] : 0.0f;
                 pf[q] = xr ? a.post_ffw[ix[q]] : 0.0f;
             }
         }
@@ -1301,6 +1425,7 @@ static DecArgs dec_args(const DecLayerH& h)
     a.shout = h.sgu ? h.shout : const_cast<float*>(h.shared_in);
     a.out = h.out;
     a.xres = h.xres;
+    a.xin = h.xin;
     a.gelu_tab = h.gelu_tab;
     a.flags = h.flags;
     return a;
@@ -1354,6 +1479,27 @@ template <int T> struct KDown { static constexpr auto fn = k_dec_down<T>; };
 void launch_dec_route(hipStream_t st, const DecLayerH& h)
 {
     launch(k_dec_route, dim3(h.T * h.E), dim3(RT_NT), (uint32_t)((size_t)3 * (h.d + 4) * 4), st, dec_args(h));
+}
+
+void launch_dec_route_fused(hipStream_t st, const DecLayerH& prev, const DecLayerH& h)
+{
+    const size_t lds = (size_t)5 * (h.d + 4) * 4;
+    raise_lds(k_dec_route_fused, lds);
+    CombArgs cb;
+    cb.d = prev.d;
+    cb.k = prev.k;
+    cb.eps = prev.eps;
+    cb.w = prev.w;
+    cb.yd = prev.yd;
+    cb.shout = prev.sgu ? prev.shout : prev.shared_in;
+    cb.post1 = prev.post1;
+    cb.post2 = prev.post2;
+    cb.post_ffw = prev.post_ffw;
+    cb.xin = prev.xin;
+    cb.out = prev.out;
+    cb.xres = prev.xres;
+    cb.flags = prev.flags;
+    launch(k_dec_route_fused, dim3(h.T * h.E), dim3(RT_NT), (uint32_t)lds, st, cb, dec_args(h));
 }
 
 void launch_dec_gu(hipStream_t st, const DecLayerH& h)

@@ -135,12 +135,16 @@ struct DecLayerH {
     double *Lb, *Bb;
     int *ids, *offsets, *perm, *flags;
     float *w, *logits, *g, *u, *yd, *shg, *shu, *shout, *out, *xres;
+    const float* xin = nullptr;  // the residual's source rows when not xres itself
     DecTile* tiles;
     Act agu, ash, adn, asd;  // packed Q8_0 rows: expert and shared inputs [T], down inputs [T*k], [T]
     const float* gelu_tab;
 };
 bool dec_supported(const DecLayerH& h);
 void launch_dec_route(hipStream_t st, const DecLayerH& h);
+// a stack layer's router with the previous layer's combine folded in (prev: that layer, its xin the
+// rows it reads, its xres where the new x goes; h.x must be prev.xres)
+void launch_dec_route_fused(hipStream_t st, const DecLayerH& prev, const DecLayerH& h);
 void launch_dec_gu(hipStream_t st, const DecLayerH& h);
 void launch_dec_down(hipStream_t st, const DecLayerH& h);
 void launch_dec_combine(hipStream_t st, const DecLayerH& h);
