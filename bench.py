@@ -253,6 +253,85 @@ def run_layer(args, pkg):
     return line
 
 
+QUANT_MODES = {"plain": 0, "silu_mul": 1, "rms_norm": 2, "gelu_mul": 3}
+
+
+def run_quant(args, pkg):
+    """The standalone activation quantizers (phx_quant_q8_0 / phx_quant_q8_k, KernelsQuant.Q80 / Q8K)
+    at the C3 prefill shapes: gelu(g) * u of 2048 x 8 assignment rows of 704 into Q8_0 (the
+    down input; the line's value), and every mode and format over 2048 token rows of 2816 (Q8_K:
+    3072).  HBM-bound: algorithmic bytes = the float inputs read once + the quants, scales and block
+    sums written, per launch; the time of a launch is the wall clock over `iters` back-to-back
+    launches on the library's stream, inputs resident in HBM."""
+    ctx = pkg.MoeContext(0)
+    rng = np.random.default_rng(11)
+    iters = max(20, args.steps // 20)
+
+    def one(k_quant, mode, rows, n):
+        x = (rng.standard_normal((rows, n)) * 2).astype(np.float32)
+        aux = rng.standard_normal(n if mode == 2 else (rows, n)).astype(np.float32) if mode else None
+        nd = rows * n // (256 if k_quant else 32)
+        bufs = [ctx.alloc(x.nbytes), ctx.alloc(rows * n), ctx.alloc(nd * (4 if k_quant else 2))]
+        bufs[0].upload(x)
+        aux_ptr = bs_ptr = None
+        if aux is not None:
+            bufs.append(ctx.alloc(aux.nbytes))
+            bufs[-1].upload(aux)
+            aux_ptr = bufs[-1].ptr
+        if k_quant:
+            bufs.append(ctx.alloc(rows * n // 16 * 2))
+            bs_ptr = bufs[-1].ptr
+        run = lambda: ctx.quant_device(k_quant, mode, bufs[0].ptr, aux_ptr, rows, n, 1e-6, bufs[1].ptr, bufs[2].ptr,
+                                       bs_ptr)
+        for _ in range(max(3, args.warmup // 100)):
+            run()
+        ctx.sync()
+        t0 = time.perf_counter()
+        for _ in range(iters):
+            run()
+        ctx.sync()
+        us = (time.perf_counter() - t0) / iters * 1e6
+        nbytes = x.nbytes + (aux.nbytes if aux is not None and mode != 2 else 0) + rows * n + nd * (4 if k_quant else 2)
+        nbytes += rows * n // 16 * 2 if k_quant else 0
+        for b in bufs:
+            b.free()
+        return us, nbytes
+
+    us, nbytes = one(False, 3, 2048 * 8, 704)
+    gbs = nbytes / us / 1e3
+    modes = {}
+    for name, m in QUANT_MODES.items():
+        for k_quant, n in ((False, 2816), (True, 3072)):
+            u, b = one(k_quant, m, 2048, n)
+            modes[f"{'q8_k' if k_quant else 'q8_0'}_{name}"] = {"us": round(u, 2), "gbs": round(b / u / 1e3, 1)}
+    line = {"metric": "activation quantizer GB/s (algorithmic bytes) vs HBM peak", "value": round(gbs, 1),
+            "unit": "GB/s", "n_gpus": 1, "steps": iters, "warmup": max(3, args.warmup // 100),
+            "ms_per_step": round(us / 1e3, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "f32->int8", "data": "synthetic",
+            "config": {"workload": "quant: phx_quant_q8_0 GELU_MUL, 16384 rows x 704 (C3's 2048 tokens x top-8 "
+                                   "down inputs)", "parallelism": "none (1 GPU)"},
+            "roofline": {"bound": "hbm", "kernel": "k_quant<GELU_MUL, Q8_0>", "achieved": round(gbs, 1),
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                         "bytes_per_launch": nbytes, "avg_launch_us": round(us, 3),
+                         "per_unit": "704 x (4 B g + 4 B u read, 1 B quant + 2/32 B fp16 scale written) per row"},
+            "modes_2048_rows": modes}
+    ctx.close()
+    if not args.no_cpu:
+        from oracle import oracle as orc
+        g = (rng.standard_normal((256, 704)) * 2).astype(np.float32)
+        u = rng.standard_normal((256, 704)).astype(np.float32)
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < min(args.cpu_seconds, 5.0):
+            r = n % 256
+            orc.quantize_q8_0((orc.gelu(g[r]) * u[r]).astype(np.float32))
+            n += 1
+        dt = time.perf_counter() - t0
+        line["cpu_baseline"] = {"value": round(n * 704 * 9.0625 / dt / 1e9, 4), "unit": "GB/s", "cores": 1,
+                                "kind": "port", "sample": f"{n} rows of 704 through the oracle's gelu and "
+                                                         f"quantize_q8_0, one at a time, {dt:.1f} s"}
+    return line
+
+
 def calibration_kernels(ctx, mib=1024):
     """Kernels of known traffic for scaling the PMC byte counters (FETCH_SIZE, WRITE_SIZE): streaming
     reads of `mib` MiB (phx::k_stream_read) and streaming copies of `mib` MiB (phx::k_stream_copy:
@@ -293,7 +372,7 @@ def main():
     if not ge._built():
         ge.build()
     pkg = ge.load_package()
-    line = run_layer(args, pkg)
+    line = run_quant(args, pkg) if args.config == "quant" else run_layer(args, pkg)
     print(json.dumps(line), flush=True)
 
 

@@ -190,6 +190,28 @@ int phx_moe_stream_copy(phx_moe_ctx* ctx, void* dst, const void* src, uint64_t b
  * reference's float chains). */
 int phx_moe_fallback_count(phx_moe_ctx* ctx, int* counts);
 
+/* Activation quantizers, the standalone form of KernelsQuant.Q80 / KernelsQuant.Q8K
+ * (src/KernelsQuant.cs:57-172) as GemmaGpu.Quant / Q80To record them (src/GemmaGpu.cs:442-461,
+ * 670-677).  Each of `rows` rows of n floats at x is quantized like CpuRef.QuantizeQ8_0
+ * (src/CpuRef.cs:49-62) or CpuRef.QuantizeQ8_K (src/CpuRefKQuants.cs:53-86) applied to
+ *   PHX_QUANT_PLAIN     x
+ *   PHX_QUANT_SILU_MUL  silu(x) * aux        (CpuRef.Silu, src/CpuRef.cs:225-228; aux rows x n)
+ *   PHX_QUANT_RMS_NORM  CpuRef.RmsNorm(x, aux, eps) per row (src/CpuRef.cs:183-191; aux [n])
+ *   PHX_QUANT_GELU_MUL  gelu(x) * aux        (src/CpuRefGemma.cs:85-92; aux rows x n)
+ * into CpuRef.Q8Activations' planar layout (src/CpuRef.cs:34-46): qs int8 [rows][n]; Q8_0 d fp16 bits
+ * [rows][n/32]; Q8_K d float [rows][n/256] and bsums int16 [rows][n/16] (bsums may be null).
+ * Device pointers (x and aux 16-byte aligned, qs 4-byte aligned); n a multiple of 32 (Q8_K: 256);
+ * asynchronous on the context's stream (phx_moe_sync waits).  No counterpart takes several rows in
+ * the reference; one row is its case. */
+#define PHX_QUANT_PLAIN 0
+#define PHX_QUANT_SILU_MUL 1
+#define PHX_QUANT_RMS_NORM 2
+#define PHX_QUANT_GELU_MUL 3
+int phx_quant_q8_0(phx_moe_ctx* ctx, int mode, const float* x, const float* aux, int rows, int n, float eps,
+                   int8_t* qs, uint16_t* d);
+int phx_quant_q8_k(phx_moe_ctx* ctx, int mode, const float* x, const float* aux, int rows, int n, float eps,
+                   int8_t* qs, float* d, int16_t* bsums);
+
 #ifdef __cplusplus
 }
 #endif

@@ -390,6 +390,18 @@ void orc_gelu_n(const float* x, float* y, int64_t n)
     for (int64_t i = 0; i < n; i++) y[i] = orc_gelu(x[i]);
 }
 
+/* CpuRef.Silu (CpuRef.cs:225-228): v / (1 + (float)Math.Exp(-v)), the exponential in double (glibc's
+ * exp, the C runtime function .NET's Math.Exp calls on Linux). */
+float orc_silu(float v)
+{
+    return v / (1.0f + (float)exp(-(double)v));
+}
+
+void orc_silu_n(const float* x, float* y, int64_t n)
+{
+    for (int64_t i = 0; i < n; i++) y[i] = orc_silu(x[i]);
+}
+
 /* The scale of CpuRef.RmsNorm (CpuRef.cs:186-189): double sum of squares in index order,
  * mean = (float)(sum/n), scale = 1f / (float)sqrt(mean + eps). */
 float orc_rms_scale(const float* x, int n, float eps)

@@ -52,6 +52,8 @@ int orc_matvec(int type, const uint8_t* w, int rows, int cols, const float* x, f
 /* elementwise */
 float orc_gelu(float x);
 void orc_gelu_n(const float* x, float* y, int64_t n);
+float orc_silu(float v);
+void orc_silu_n(const float* x, float* y, int64_t n);
 void orc_rmsnorm(const float* x, int n, const float* w, float eps, float* y);
 float orc_rms_scale(const float* x, int n, float eps);
 

@@ -69,6 +69,9 @@ def lib():
         L.orc_gelu.argtypes = [f32]
         L.orc_gelu.restype = f32
         L.orc_gelu_n.argtypes = [vp, vp, i64]
+        L.orc_silu.argtypes = [f32]
+        L.orc_silu.restype = f32
+        L.orc_silu_n.argtypes = [vp, vp, i64]
         L.orc_rmsnorm.argtypes = [vp, i32, vp, f32, vp]
         L.orc_rms_scale.argtypes = [vp, i32, f32]
         L.orc_rms_scale.restype = f32
@@ -167,6 +170,13 @@ def gelu(x):
     x = f32(x)
     y = np.empty_like(x)
     lib().orc_gelu_n(x.ctypes.data, y.ctypes.data, x.size)
+    return y
+
+
+def silu(x):
+    x = f32(x)
+    y = np.empty_like(x)
+    lib().orc_silu_n(x.ctypes.data, y.ctypes.data, x.size)
     return y
 
 

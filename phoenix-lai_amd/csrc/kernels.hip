@@ -744,6 +744,131 @@ void launch_requant(hipStream_t st, int rows, int nf, const float* g, const floa
     launch(k_requant, dim3(rows), dim3(256), (size_t)act.cols * sizeof(float), st, nf, g, u, tab, act);
 }
 
+// ------------------------------------------------------------------------------ standalone quantizers
+// KernelsQuant.Q80 / Q8K as an op of their own (src/KernelsQuant.cs:57-172, recorded by GemmaGpu.Quant,
+// src/GemmaGpu.cs:442-461): rows x n inputs, each row quantized like CpuRef.QuantizeQ8_0
+// (src/CpuRef.cs:49-62) or CpuRef.QuantizeQ8_K (src/CpuRefKQuants.cs:53-86) applied to
+//   QZ_PLAIN x;  QZ_SILU silu(x) * u (CpuRef.Silu, src/CpuRef.cs:225-228: the exponential in double);
+//   QZ_RMS   CpuRef.RmsNorm(x, w) (src/CpuRef.cs:183-191: (x * scale) * w, the row's certified mean);
+//   QZ_GELU  gelu(x) * u (src/CpuRefGemma.cs:85-92).
+// Outputs in CpuRef.Q8Activations' planar layout (src/CpuRef.cs:34-46): qs int8 [n] per row; Q8_0 d as
+// fp16 bits [n/32]; Q8_K d float [n/256] and bsums int16 [n/16].  A workgroup takes QZ_CH elements of
+// one row (in QZ_RMS every workgroup forms its row's mean, as the reference's do).
+enum QzMode { QZ_PLAIN = 0, QZ_SILU = 1, QZ_RMS = 2, QZ_GELU = 3 };
+constexpr int QZ_NT = 256, QZ_CH = 2048;
+
+template <int MODE>
+__device__ __forceinline__ float qz_in(float v, float a, float scale, const float* __restrict__ tab)
+{
+    if (MODE == QZ_SILU) return v / (1.0f + (float)exp(-(double)v)) * a;
+    if (MODE == QZ_RMS) return v * scale * a;
+    if (MODE == QZ_GELU) return gelu_ref(v, tab) * a;
+    return v;
+}
+
+template <int MODE, bool K>
+__global__ __launch_bounds__(QZ_NT) void k_quant(int n, float eps, const float* __restrict__ x,
+                                                 const float* __restrict__ aux, const float* __restrict__ tab,
+                                                 int8_t* __restrict__ qs, uint16_t* __restrict__ d16,
+                                                 float* __restrict__ dk, int16_t* __restrict__ bsums, int* flags)
+{
+    const int64_t row = blockIdx.y;
+    const int tid = threadIdx.x, c0 = blockIdx.x * QZ_CH, c1 = min(n, c0 + QZ_CH);
+    const float* xr = x + row * n;
+    const float* ar = MODE == QZ_RMS ? aux : aux + row * n;  // the norm weight is shared by the rows
+    float scale = 0.0f;
+    if (MODE == QZ_RMS) {
+        __shared__ double red[QZ_NT / 64 + 1];
+        scale = rms_scale_from_mean(mean_sq_cert<QZ_NT>(xr, n, red, flags), eps);
+    }
+    auto in4 = [&](int i) {
+        const float4 v = *(const float4*)(xr + i);
+        float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (MODE != QZ_PLAIN) a = *(const float4*)(ar + i);
+        return make_float4(qz_in<MODE>(v.x, a.x, scale, tab), qz_in<MODE>(v.y, a.y, scale, tab),
+                           qz_in<MODE>(v.z, a.z, scale, tab), qz_in<MODE>(v.w, a.w, scale, tab));
+    };
+    if (!K) {
+        // eight lanes per 32-block, four values each; whole 8-lane groups run every round (shuffles)
+        const int g = tid >> 3, l8 = tid & 7;
+        for (int b0 = c0 / 32; b0 < c1 / 32; b0 += QZ_NT / 8) {
+            const int b = b0 + g, bc = min(b, c1 / 32 - 1);
+            float dval;
+            int sum;
+            const int qw = q8_0_oct(in4(bc * 32 + 4 * l8), &dval, &sum);
+            if (b < c1 / 32) {
+                *(int*)(qs + row * n + bc * 32 + 4 * l8) = qw;
+                if (l8 == 0) d16[row * (n / 32) + bc] = (uint16_t)f2h_bits(dval);
+            }
+        }
+        return;
+    }
+    // Q8_K: one wave per 256-block, lane l holds elements 4l..4l+3
+    const int lane = tid & 63, wave = tid >> 6;
+    for (int b = c0 / 256 + wave; b < c1 / 256; b += QZ_NT / 64) {
+        const float4 v4 = in4(b * 256 + 4 * lane);
+        const float v[4] = {v4.x, v4.y, v4.z, v4.w};
+        // the reference's scan: the first element of largest |x| (strict '>', from 0)
+        float amax = 0.0f, vmax = 0.0f;
+        int imax = 1 << 30;
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            if (fabsf(v[j]) > amax) {
+                amax = fabsf(v[j]);
+                vmax = v[j];
+                imax = 4 * lane + j;
+            }
+#pragma unroll
+        for (int m = 1; m < 64; m <<= 1) {
+            const float oa = __shfl_xor(amax, m, 64), ov = __shfl_xor(vmax, m, 64);
+            const int oi = __shfl_xor(imax, m, 64);
+            if (oa > amax || (oa == amax && oi < imax)) {
+                amax = oa;
+                vmax = ov;
+                imax = oi;
+            }
+        }
+        const float iscale = amax == 0.0f ? 0.0f : -127.0f / vmax;
+        int q[4], sm = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            q[j] = amax == 0.0f ? 0 : min(nearest_int(iscale * v[j]), 127);
+            sm += q[j];
+        }
+        *(int*)(qs + row * n + b * 256 + 4 * lane) =
+            (q[0] & 0xFF) | ((q[1] & 0xFF) << 8) | ((q[2] & 0xFF) << 16) | (int)((unsigned)q[3] << 24);
+        sm += __shfl_xor(sm, 1, 64);
+        sm += __shfl_xor(sm, 2, 64);
+        if (bsums && (lane & 3) == 0) bsums[row * (n / 16) + b * 16 + (lane >> 2)] = (int16_t)sm;
+        if (lane == 0) dk[row * (n / 256) + b] = amax == 0.0f ? 0.0f : 1.0f / iscale;
+    }
+}
+
+int launch_quant(hipStream_t st, int fmt_k, int mode, int rows, int n, float eps, const float* x, const float* aux,
+                 const float* tab, int8_t* qs, uint16_t* d16, float* dk, int16_t* bsums, int* flags)
+{
+    // rows are independent outside QZ_RMS and the outputs are row-major: quantize them as one row
+    if (mode != QZ_RMS && (int64_t)rows * n <= (int64_t)1 << 30) {
+        n *= rows;
+        rows = 1;
+    }
+    const dim3 grid((n + QZ_CH - 1) / QZ_CH, rows), blk(QZ_NT);
+#define QZ_L(M, K) launch((k_quant<M, K>), grid, blk, 0, st, n, eps, x, aux, tab, qs, d16, dk, bsums, flags)
+    switch (mode * 2 + (fmt_k ? 1 : 0)) {
+    case 0: QZ_L(QZ_PLAIN, false); break;
+    case 1: QZ_L(QZ_PLAIN, true); break;
+    case 2: QZ_L(QZ_SILU, false); break;
+    case 3: QZ_L(QZ_SILU, true); break;
+    case 4: QZ_L(QZ_RMS, false); break;
+    case 5: QZ_L(QZ_RMS, true); break;
+    case 6: QZ_L(QZ_GELU, false); break;
+    case 7: QZ_L(QZ_GELU, true); break;
+    default: return -1;
+    }
+#undef QZ_L
+    return 0;
+}
+
 // ------------------------------------------------------------------------------ combine, norms, residual
 // Per token: acc = sum_j yd[t*k+j] * w_j in rank order (src/GemmaCpu.cs:418, each term rounded then
 // added), out = rmsnorm(shared) * post1 + rmsnorm(acc) * post2 (src/GemmaCpu.cs:384,420-421), and

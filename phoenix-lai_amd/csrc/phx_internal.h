@@ -112,6 +112,9 @@ void launch_dispatch(hipStream_t st, int n_assign, int E, int A, const int* ids,
 void launch_grouped(hipStream_t st, const QMat& w, Act act, const Tile* tiles, const int* ntiles, int max_tiles,
                     int A, const int* perm, int act_div, float* out0, float* out1, int split, int out_stride);
 void launch_requant(hipStream_t st, int rows, int nf, const float* g, const float* u, const float* gelu_tab, Act act);
+// standalone Q8_0 (fmt_k 0) / Q8_K (fmt_k 1) quantizer of rows x n inputs; mode as PHX_QUANT_*; -1 on a bad mode
+int launch_quant(hipStream_t st, int fmt_k, int mode, int rows, int n, float eps, const float* x, const float* aux,
+                 const float* tab, int8_t* qs, uint16_t* d16, float* dk, int16_t* bsums, int* flags);
 // prefill path (kernels_prefill.hip): Q4_0 / Q8_0 grouped products on MFMA, tiles of up to kMmaTile
 // assignments; same arguments and outputs as launch_grouped.  npos > 0 reads the activations in
 // expert-list order, block-major (fp16 integers of block b, list position p at qh + (b * npos + p) * 32,

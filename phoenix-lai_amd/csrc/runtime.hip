@@ -1249,4 +1249,42 @@ int phx_moe_fallback_count(phx_moe_ctx* c, int* counts)
     return PHX_OK;
 }
 
+static int quant_check(phx_moe_ctx* c, int mode, const float* x, const float* aux, int rows, int n, int blk,
+                       const void* qs)
+{
+    if (mode < PHX_QUANT_PLAIN || mode > PHX_QUANT_GELU_MUL) return set_err(c, PHX_ERR_ARG, "quant mode %d", mode);
+    if (rows <= 0 || rows > 65535 || n <= 0 || n % blk)
+        return set_err(c, PHX_ERR_ARG, "quant shape %d x %d (n a positive multiple of %d)", rows, n, blk);
+    if (!x || !qs || (mode != PHX_QUANT_PLAIN && !aux)) return set_err(c, PHX_ERR_ARG, "quant: null buffer");
+    if ((uintptr_t)x % 16 || (uintptr_t)aux % 16 || (uintptr_t)qs % 4)
+        return set_err(c, PHX_ERR_ARG, "quant: x and aux need 16-byte, qs 4-byte alignment");
+    return PHX_OK;
+}
+
+int phx_quant_q8_0(phx_moe_ctx* c, int mode, const float* x, const float* aux, int rows, int n, float eps, int8_t* qs,
+                   uint16_t* d)
+{
+    if (!c) return PHX_ERR_ARG;
+    int rc = quant_check(c, mode, x, aux, rows, n, 32, qs);
+    if (rc) return rc;
+    if (!d) return set_err(c, PHX_ERR_ARG, "quant: null buffer");
+    HIPCHK(c, hipSetDevice(c->device));
+    launch_quant(c->stream, 0, mode, rows, n, eps, x, aux, c->gelu_tab, qs, d, nullptr, nullptr, c->flags);
+    HIPCHK(c, hipGetLastError());
+    return PHX_OK;
+}
+
+int phx_quant_q8_k(phx_moe_ctx* c, int mode, const float* x, const float* aux, int rows, int n, float eps, int8_t* qs,
+                   float* d, int16_t* bsums)
+{
+    if (!c) return PHX_ERR_ARG;
+    int rc = quant_check(c, mode, x, aux, rows, n, 256, qs);
+    if (rc) return rc;
+    if (!d) return set_err(c, PHX_ERR_ARG, "quant: null buffer");
+    HIPCHK(c, hipSetDevice(c->device));
+    launch_quant(c->stream, 1, mode, rows, n, eps, x, aux, c->gelu_tab, qs, nullptr, d, bsums, c->flags);
+    HIPCHK(c, hipGetLastError());
+    return PHX_OK;
+}
+
 }  // extern "C"

@@ -22,6 +22,8 @@ class PHX:
     FLAG_DEVICE_PTRS, FLAG_ASYNC, FLAG_RESIDUAL, FLAG_EXACT_ROUTER = 1, 2, 4, 8
     KINDS = ["prologue", "router", "topk", "dispatch", "gate_up", "requant", "down", "combine", "shared"]
     MAX_EXPERTS, MAX_USED = 256, 16
+    # activation quantizer modes (KernelsQuant.Mode, src/KernelsQuant.cs:13)
+    QUANT_PLAIN, QUANT_SILU_MUL, QUANT_RMS_NORM, QUANT_GELU_MUL = 0, 1, 2, 3
 
 
 class MoeError(RuntimeError):
@@ -123,6 +125,8 @@ def load_lib():
         "phx_moe_fallback_count": (i32, [vp, i32p]),
         "phx_moe_stream_read": (i32, [vp, vp, C.c_uint64, i32, C.POINTER(C.c_double)]),
         "phx_moe_stream_copy": (i32, [vp, vp, vp, C.c_uint64, i32, C.POINTER(C.c_double)]),
+        "phx_quant_q8_0": (i32, [vp, i32, vp, vp, i32, i32, C.c_float, vp, vp]),
+        "phx_quant_q8_k": (i32, [vp, i32, vp, vp, i32, i32, C.c_float, vp, vp, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -301,6 +305,53 @@ class MoeContext:
         ms = C.c_double()
         self._check(self.lib.phx_moe_stream_copy(self.h, dst.ptr, src.ptr, nbytes, iters, C.byref(ms)))
         return ms.value
+
+    def quant_device(self, k_quant: bool, mode: int, x_ptr: int, aux_ptr, rows: int, n: int, eps: float,
+                     qs_ptr: int, d_ptr: int, bsums_ptr=None):
+        """Enqueue phx_quant_q8_0 (k_quant False) or phx_quant_q8_k on device buffers (sync() waits)."""
+        if k_quant:
+            rc = self.lib.phx_quant_q8_k(self.h, mode, x_ptr, aux_ptr, rows, n, eps, qs_ptr, d_ptr, bsums_ptr)
+        else:
+            rc = self.lib.phx_quant_q8_0(self.h, mode, x_ptr, aux_ptr, rows, n, eps, qs_ptr, d_ptr)
+        self._check(rc)
+
+    def _quant(self, k_quant: bool, mode: int, x: np.ndarray, aux, eps: float):
+        x = _f32(x)
+        x2 = x.reshape(1, -1) if x.ndim == 1 else x
+        rows, n = x2.shape
+        bufs = [self.alloc(max(x2.nbytes, 16))]
+        bufs[0].upload(x2)
+        aux_ptr = None
+        if aux is not None:
+            a = _f32(aux)
+            bufs.append(self.alloc(max(a.nbytes, 16)))
+            bufs[-1].upload(a)
+            aux_ptr = bufs[-1].ptr
+        nd = rows * n // (256 if k_quant else 32)
+        qs, d = self.alloc(rows * n), self.alloc(nd * (4 if k_quant else 2))
+        bs = self.alloc(rows * n // 16 * 2) if k_quant else None
+        bufs += [qs, d] + ([bs] if bs else [])
+        try:
+            self.quant_device(k_quant, mode, bufs[0].ptr, aux_ptr, rows, n, eps, qs.ptr, d.ptr, bs.ptr if bs else None)
+            self.sync()
+            out = [qs.download((rows, n), np.int8),
+                   d.download((rows, n // (256 if k_quant else 32)), np.float32 if k_quant else np.uint16)]
+            if k_quant:
+                out.append(bs.download((rows, n // 16), np.int16))
+        finally:
+            for b in bufs:
+                b.free()
+        if x.ndim == 1:
+            out = [o[0] for o in out]
+        return tuple(out)
+
+    def Q80(self, mode: int, x: np.ndarray, aux: np.ndarray | None = None, eps: float = 1e-6):
+        """KernelsQuant.Q80 (src/KernelsQuant.cs:133-170) on host arrays: (qs int8, d fp16 bits) per row."""
+        return self._quant(False, mode, x, aux, eps)
+
+    def Q8K(self, mode: int, x: np.ndarray, aux: np.ndarray | None = None, eps: float = 1e-6):
+        """KernelsQuant.Q8K (src/KernelsQuant.cs:60-128) on host arrays: (qs int8, d f32, bsums int16) per row."""
+        return self._quant(True, mode, x, aux, eps)
 
     def stack_run_device(self, x_ptr: int, T: int):
         """Replay the captured stack on a device-resident x (async; sync() waits)."""

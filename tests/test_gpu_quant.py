@@ -1,0 +1,87 @@
+"""GPU parity of the standalone activation quantizers (phx_quant_q8_0 / phx_quant_q8_k, the
+KernelsQuant.Q80 / Q8K ops of src/KernelsQuant.cs:57-172) through the C ABI: every mode's quantized
+integers, scales and block sums equal the oracle's CpuRef.QuantizeQ8_0 / QuantizeQ8_K of the
+transformed input (CpuRef.RmsNorm, gelu(x) * u, silu(x) * u), bit for bit."""
+import sys
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+EPS = 1e-6
+MODES = {"plain": 0, "silu_mul": 1, "rms_norm": 2, "gelu_mul": 3}
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def transformed(orc, mode, x, aux):
+    """The reference's input to the quantizer, row by row (float32 products as the C# code rounds them)."""
+    if mode == "plain":
+        return x
+    if mode == "rms_norm":
+        return np.stack([orc.rmsnorm(r, aux, EPS) for r in x])
+    f = orc.gelu(x) if mode == "gelu_mul" else orc.silu(x)
+    return (f * aux).astype(np.float32)
+
+
+def inputs(rows, n, seed):
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal((rows, n)) * 3.0).astype(np.float32)
+    u = rng.standard_normal((rows, n)).astype(np.float32)
+    w = (1.0 + 0.2 * rng.standard_normal(n)).astype(np.float32)
+    # edge rows: an all-zero row; ties of |x| of both signs (the first index wins in Q8_K) and
+    # halfway products (Q8_0 rounds them away from zero, Q8_K to even)
+    x[1] = 0.0
+    x[2, :64] = np.tile(np.float32([127.0, -127.0, 2.5, -2.5, 0.5, -0.5, 1.5, 126.5]), 8)
+    if n >= 512:
+        x[2, 256:264] = np.float32([-127.0, 127.0, 2.5, -2.5, 3.5, -3.5, 0.0, -0.0])
+    return x, u, w
+
+
+@pytest.mark.parametrize("mode", list(MODES))
+@pytest.mark.parametrize("n", [256, 2816, 4352])
+def test_q8_0_matches_oracle(ctx, orc, mode, n):
+    say(f"quant q8_0: mode={mode} rows=4 n={n}")
+    x, u, w = inputs(4, n, seed=n + MODES[mode])
+    aux = None if mode == "plain" else (w if mode == "rms_norm" else u)
+    qs, d = ctx.Q80(MODES[mode], x, aux, EPS)
+    v = transformed(orc, mode, x, aux)
+    for r in range(4):
+        rd, rq = orc.quantize_q8_0(v[r])
+        np.testing.assert_array_equal(d[r], rd, err_msg=f"row {r}: fp16 scales")
+        np.testing.assert_array_equal(qs[r], rq, err_msg=f"row {r}: quants")
+
+
+@pytest.mark.parametrize("mode", list(MODES))
+@pytest.mark.parametrize("n", [256, 3072, 4608])
+def test_q8_k_matches_oracle(ctx, orc, mode, n):
+    say(f"quant q8_k: mode={mode} rows=4 n={n}")
+    x, u, w = inputs(4, n, seed=7 * n + MODES[mode])
+    aux = None if mode == "plain" else (w if mode == "rms_norm" else u)
+    qs, d, bs = ctx.Q8K(MODES[mode], x, aux, EPS)
+    v = transformed(orc, mode, x, aux)
+    for r in range(4):
+        rd, rq, rb = orc.quantize_q8_k(v[r])
+        np.testing.assert_array_equal(d[r].view(np.uint32), rd.view(np.uint32), err_msg=f"row {r}: scales")
+        np.testing.assert_array_equal(qs[r], rq, err_msg=f"row {r}: quants")
+        np.testing.assert_array_equal(bs[r], rb, err_msg=f"row {r}: block sums")
+
+
+def test_quant_rejects_bad_arguments(ctx, pkg, orc):
+    say("quant: argument checks")
+    x = np.ones((2, 64), np.float32)
+    with pytest.raises(pkg.moe.ArgumentError):
+        ctx.Q80(7, x)  # no such mode
+    with pytest.raises(pkg.moe.ArgumentError):
+        ctx.Q80(0, np.ones((2, 48), np.float32))  # n not a multiple of 32
+    with pytest.raises(pkg.moe.ArgumentError):
+        ctx.Q8K(0, x)  # n not a multiple of 256
+    with pytest.raises(pkg.moe.ArgumentError):
+        ctx.Q80(3, x)  # gelu_mul without u
+    qs, d = ctx.Q80(0, x)  # the context still works
+    rd, rq = orc.quantize_q8_0(x[0])
+    assert (qs == rq).all() and (d == rd).all()

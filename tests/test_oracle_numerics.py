@@ -256,6 +256,23 @@ def test_gelu_rounds_input_to_fp16_and_cutoffs(orc):
     assert g[5] == TB.gelu(edge[5:6])[0]
 
 
+# ---------------------------------------------------------------------------------------- SiLU
+def test_silu_against_the_logistic_function(orc):
+    """silu(x) = x * sigmoid(x) (scipy's expit in float64) to within the three float roundings of the
+    reference expression, with the limits fixed exactly: 0 at 0, x where exp(-x) vanishes against 1,
+    -0 where exp(-x) overflows float."""
+    from scipy.special import expit
+    rng = np.random.default_rng(75)
+    x = np.concatenate([rng.standard_normal(20000) * 6, rng.uniform(-80, 80, 2000)]).astype(np.float32)
+    y = orc.silu(x).astype(np.float64)
+    want = x.astype(np.float64) * expit(x.astype(np.float64))
+    assert np.all(np.abs(y - want) <= 4 * 2.0 ** -24 * np.abs(want) + 1e-38)
+    edge = orc.silu(np.array([0.0, 40.0, 100.0, -100.0, -1.0], np.float32))
+    assert edge[0] == 0 and edge[1] == 40.0 and edge[2] == 100.0
+    assert edge[3] == 0 and np.signbit(edge[3])
+    assert edge[4] == np.float32(-1.0) / (np.float32(1.0) + np.float32(np.e))
+
+
 # ---------------------------------------------------------------------------------------- RMSNorm
 def test_rmsnorm_closed_form(orc):
     rng = np.random.default_rng(70)
