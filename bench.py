@@ -304,6 +304,31 @@ def run_quant(args, pkg):
         for k_quant, n in ((False, 2816), (True, 3072)):
             u, b = one(k_quant, m, 2048, n)
             modes[f"{'q8_k' if k_quant else 'q8_0'}_{name}"] = {"us": round(u, 2), "gbs": round(b / u / 1e3, 1)}
+    for rows in (1, 2048):  # NormAddQuant: the decode step's single row, and a prefill batch
+        n = 2816
+        x = ctx.alloc(rows * n * 4)
+        y = ctx.alloc(rows * n * 4)
+        w = ctx.alloc(n * 4)
+        w2 = ctx.alloc(n * 4)
+        qs, dq = ctx.alloc(rows * n), ctx.alloc(rows * n // 16)
+        x.upload((rng.standard_normal((rows, n))).astype(np.float32))
+        y.upload((rng.standard_normal((rows, n))).astype(np.float32))
+        w.upload(np.ones(n, np.float32))
+        w2.upload(np.ones(n, np.float32))
+        run = lambda: ctx._check(ctx.lib.phx_norm_add(ctx.h, x.ptr, y.ptr, w.ptr, rows, n, 1e-6, 1.0, w2.ptr, qs.ptr,
+                                                      dq.ptr))
+        for _ in range(3):
+            run()
+        ctx.sync()
+        t0 = time.perf_counter()
+        for _ in range(iters):
+            run()
+        ctx.sync()
+        u = (time.perf_counter() - t0) / iters * 1e6
+        b = rows * n * (4 + 4 + 4 + 1) + rows * n // 16 + 2 * n * 4
+        modes[f"norm_add_quant_{rows}_rows"] = {"us": round(u, 2), "gbs": round(b / u / 1e3, 1)}
+        for buf in (x, y, w, w2, qs, dq):
+            buf.free()
     line = {"metric": "activation quantizer GB/s (algorithmic bytes) vs HBM peak", "value": round(gbs, 1),
             "unit": "GB/s", "n_gpus": 1, "steps": iters, "warmup": max(3, args.warmup // 100),
             "ms_per_step": round(us / 1e3, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,

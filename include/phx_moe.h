@@ -212,6 +212,16 @@ int phx_quant_q8_0(phx_moe_ctx* ctx, int mode, const float* x, const float* aux,
 int phx_quant_q8_k(phx_moe_ctx* ctx, int mode, const float* x, const float* aux, int rows, int n, float eps,
                    int8_t* qs, float* d, int16_t* bsums);
 
+/* Residual norm-add with the next norm's quantized input: KernelsGemma.NormAdd (w2 null) and
+ * NormAddQuant (src/KernelsGemma.cs:126-226), recorded at src/GemmaGpu.cs:614 and 644 (the router's
+ * and the next layer's input producers).  Per row of n: x = x + CpuRef.RmsNorm(y, w, eps), then
+ * x *= s when s != 1 (GemmaCpu.PostAndFfn, src/GemmaCpu.cs:353-356, 367); with w2, qs / d get the
+ * Q8_0 quantization of CpuRef.RmsNorm(x, w2, eps) (src/CpuRef.cs:49-62, 183-191) in the layout of
+ * phx_quant_q8_0.  Device pointers (x, y, w, w2 16-byte aligned); n <= 16384, a multiple of 4 (32
+ * with w2); asynchronous on the context's stream. */
+int phx_norm_add(phx_moe_ctx* ctx, float* x, const float* y, const float* w, int rows, int n, float eps, float s,
+                 const float* w2, int8_t* qs, uint16_t* d);
+
 #ifdef __cplusplus
 }
 #endif

@@ -869,6 +869,60 @@ int launch_quant(hipStream_t st, int fmt_k, int mode, int rows, int n, float eps
     return 0;
 }
 
+// ------------------------------------------------------------------------------ norm + residual (+ quant)
+// KernelsGemma.NormAdd / NormAddQuant (src/KernelsGemma.cs:126-226) with the CPU path's rounding
+// (GemmaCpu.PostAndFfn, src/GemmaCpu.cs:353-356 and 367; then the next RmsNorm and MatVec's Q8_0 input,
+// src/CpuRef.cs:49-62, 183-191), one workgroup per row: x = x + rmsnorm(y, w) (the term rounded as
+// CpuRef.RmsNorm forms it), times s when s != 1; with w2, the Q8_0 quantization of rmsnorm(x_new, w2)
+// into qs / d16 (fp16 bits).  Both means of squares are certified (mean_sq_cert).
+constexpr int NA_NT = 512;
+
+__global__ __launch_bounds__(NA_NT) void k_norm_add(int n, float eps, float s, float* __restrict__ x,
+                                                    const float* __restrict__ y, const float* __restrict__ w,
+                                                    const float* __restrict__ w2, int8_t* __restrict__ qs,
+                                                    uint16_t* __restrict__ d16, int* flags)
+{
+    extern __shared__ __align__(16) float sx[];  // the new x row
+    __shared__ double red[NA_NT / 64 + 1];
+    const int64_t row = blockIdx.x;
+    const int tid = threadIdx.x, n4 = n / 4;
+    float* xr = x + row * n;
+    const float* yr = y + row * n;
+    const float sc1 = rms_scale_from_mean(mean_sq_cert<NA_NT>(yr, n, red, flags), eps);
+    for (int i4 = tid; i4 < n4; i4 += NA_NT) {
+        const float4 xv = ((const float4*)xr)[i4], yv = ((const float4*)yr)[i4], wv = ((const float4*)w)[i4];
+        float4 v = make_float4(xv.x + yv.x * sc1 * wv.x, xv.y + yv.y * sc1 * wv.y, xv.z + yv.z * sc1 * wv.z,
+                               xv.w + yv.w * sc1 * wv.w);
+        if (s != 1.0f) v = make_float4(v.x * s, v.y * s, v.z * s, v.w * s);
+        ((float4*)xr)[i4] = v;
+        ((float4*)sx)[i4] = v;
+    }
+    if (!w2) return;  // uniform
+    __syncthreads();
+    const float sc2 = rms_scale_from_mean(mean_sq_cert<NA_NT>(sx, n, red, flags), eps);
+    // eight lanes per 32-block; whole 8-lane groups run every round (shuffles)
+    const int g = tid >> 3, l8 = tid & 7, nb = n / 32;
+    for (int b0 = 0; b0 < nb; b0 += NA_NT / 8) {
+        const int b = b0 + g, bc = min(b, nb - 1);
+        const float4 xv = *(const float4*)(sx + bc * 32 + 4 * l8), wv = *(const float4*)(w2 + bc * 32 + 4 * l8);
+        float dval;
+        int sum;
+        const int qw = q8_0_oct(make_float4(xv.x * sc2 * wv.x, xv.y * sc2 * wv.y, xv.z * sc2 * wv.z,
+                                            xv.w * sc2 * wv.w),
+                                &dval, &sum);
+        if (b < nb) {
+            *(int*)(qs + row * n + bc * 32 + 4 * l8) = qw;
+            if (l8 == 0) d16[row * nb + bc] = (uint16_t)f2h_bits(dval);
+        }
+    }
+}
+
+void launch_norm_add(hipStream_t st, int rows, int n, float eps, float s, float* x, const float* y, const float* w,
+                     const float* w2, int8_t* qs, uint16_t* d16, int* flags)
+{
+    launch(k_norm_add, dim3(rows), dim3(NA_NT), (size_t)n * sizeof(float), st, n, eps, s, x, y, w, w2, qs, d16, flags);
+}
+
 // ------------------------------------------------------------------------------ combine, norms, residual
 // Per token: acc = sum_j yd[t*k+j] * w_j in rank order (src/GemmaCpu.cs:418, each term rounded then
 // added), out = rmsnorm(shared) * post1 + rmsnorm(acc) * post2 (src/GemmaCpu.cs:384,420-421), and

@@ -115,6 +115,9 @@ void launch_requant(hipStream_t st, int rows, int nf, const float* g, const floa
 // standalone Q8_0 (fmt_k 0) / Q8_K (fmt_k 1) quantizer of rows x n inputs; mode as PHX_QUANT_*; -1 on a bad mode
 int launch_quant(hipStream_t st, int fmt_k, int mode, int rows, int n, float eps, const float* x, const float* aux,
                  const float* tab, int8_t* qs, uint16_t* d16, float* dk, int16_t* bsums, int* flags);
+// per row: x = (x + rmsnorm(y) * w) * s (s != 1), then with w2 the Q8_0 of rmsnorm(x) * w2 (n <= 16384)
+void launch_norm_add(hipStream_t st, int rows, int n, float eps, float s, float* x, const float* y, const float* w,
+                     const float* w2, int8_t* qs, uint16_t* d16, int* flags);
 // prefill path (kernels_prefill.hip): Q4_0 / Q8_0 grouped products on MFMA, tiles of up to kMmaTile
 // assignments; same arguments and outputs as launch_grouped.  npos > 0 reads the activations in
 // expert-list order, block-major (fp16 integers of block b, list position p at qh + (b * npos + p) * 32,

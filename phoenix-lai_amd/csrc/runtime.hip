@@ -1287,4 +1287,19 @@ int phx_quant_q8_k(phx_moe_ctx* c, int mode, const float* x, const float* aux, i
     return PHX_OK;
 }
 
+int phx_norm_add(phx_moe_ctx* c, float* x, const float* y, const float* w, int rows, int n, float eps, float s,
+                 const float* w2, int8_t* qs, uint16_t* d)
+{
+    if (!c) return PHX_ERR_ARG;
+    if (rows <= 0 || rows > 65535 || n <= 0 || n > 16384 || n % (w2 ? 32 : 4))
+        return set_err(c, PHX_ERR_ARG, "norm_add shape %d x %d (n <= 16384, a multiple of %d)", rows, n, w2 ? 32 : 4);
+    if (!x || !y || !w || (w2 && (!qs || !d))) return set_err(c, PHX_ERR_ARG, "norm_add: null buffer");
+    if ((uintptr_t)x % 16 || (uintptr_t)y % 16 || (uintptr_t)w % 16 || (uintptr_t)w2 % 16 || (uintptr_t)qs % 4)
+        return set_err(c, PHX_ERR_ARG, "norm_add: x, y, w, w2 need 16-byte, qs 4-byte alignment");
+    HIPCHK(c, hipSetDevice(c->device));
+    launch_norm_add(c->stream, rows, n, eps, s, x, y, w, w2, w2 ? qs : nullptr, w2 ? d : nullptr, c->flags);
+    HIPCHK(c, hipGetLastError());
+    return PHX_OK;
+}
+
 }  // extern "C"

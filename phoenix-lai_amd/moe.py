@@ -127,6 +127,7 @@ def load_lib():
         "phx_moe_stream_copy": (i32, [vp, vp, vp, C.c_uint64, i32, C.POINTER(C.c_double)]),
         "phx_quant_q8_0": (i32, [vp, i32, vp, vp, i32, i32, C.c_float, vp, vp]),
         "phx_quant_q8_k": (i32, [vp, i32, vp, vp, i32, i32, C.c_float, vp, vp, vp]),
+        "phx_norm_add": (i32, [vp, vp, vp, vp, i32, i32, C.c_float, C.c_float, vp, vp, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -352,6 +353,35 @@ class MoeContext:
     def Q8K(self, mode: int, x: np.ndarray, aux: np.ndarray | None = None, eps: float = 1e-6):
         """KernelsQuant.Q8K (src/KernelsQuant.cs:60-128) on host arrays: (qs int8, d f32, bsums int16) per row."""
         return self._quant(True, mode, x, aux, eps)
+
+    def NormAdd(self, x: np.ndarray, y: np.ndarray, w: np.ndarray, eps: float = 1e-6, s: float = 1.0,
+                w2: np.ndarray | None = None):
+        """KernelsGemma.NormAdd / NormAddQuant (src/KernelsGemma.cs:126-226) on host arrays: returns the new
+        x, and with w2 also (qs int8, d fp16 bits) of rmsnorm(x_new, w2)."""
+        x = _f32(x)
+        x2 = x.reshape(1, -1) if x.ndim == 1 else x
+        rows, n = x2.shape
+        bufs = [self.alloc(x2.nbytes), self.alloc(x2.nbytes), self.alloc(n * 4)]
+        for b, a in zip(bufs, (x2, _f32(y), _f32(w))):
+            b.upload(a)
+        if w2 is not None:
+            bufs += [self.alloc(n * 4), self.alloc(rows * n), self.alloc(rows * n // 32 * 2)]
+            bufs[3].upload(_f32(w2))
+        try:
+            self._check(self.lib.phx_norm_add(self.h, bufs[0].ptr, bufs[1].ptr, bufs[2].ptr, rows, n, eps, s,
+                                              bufs[3].ptr if w2 is not None else None,
+                                              bufs[4].ptr if w2 is not None else None,
+                                              bufs[5].ptr if w2 is not None else None))
+            self.sync()
+            out = [bufs[0].download((rows, n))]
+            if w2 is not None:
+                out += [bufs[4].download((rows, n), np.int8), bufs[5].download((rows, n // 32), np.uint16)]
+        finally:
+            for b in bufs:
+                b.free()
+        if x.ndim == 1:
+            out = [o[0] for o in out]
+        return out[0] if w2 is None else tuple(out)
 
     def stack_run_device(self, x_ptr: int, T: int):
         """Replay the captured stack on a device-resident x (async; sync() waits)."""

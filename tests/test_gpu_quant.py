@@ -1,7 +1,9 @@
 """GPU parity of the standalone activation quantizers (phx_quant_q8_0 / phx_quant_q8_k, the
-KernelsQuant.Q80 / Q8K ops of src/KernelsQuant.cs:57-172) through the C ABI: every mode's quantized
-integers, scales and block sums equal the oracle's CpuRef.QuantizeQ8_0 / QuantizeQ8_K of the
-transformed input (CpuRef.RmsNorm, gelu(x) * u, silu(x) * u), bit for bit."""
+KernelsQuant.Q80 / Q8K ops of src/KernelsQuant.cs:57-172) and of the residual norm-add with the next
+norm's quantized input (phx_norm_add, KernelsGemma.NormAdd / NormAddQuant, src/KernelsGemma.cs:126-226)
+through the C ABI: every mode's quantized integers, scales and block sums equal the oracle's
+CpuRef.QuantizeQ8_0 / QuantizeQ8_K of the transformed input (CpuRef.RmsNorm, gelu(x) * u, silu(x) * u),
+and the new residual rows the oracle's, bit for bit."""
 import sys
 
 import numpy as np
@@ -85,3 +87,48 @@ def test_quant_rejects_bad_arguments(ctx, pkg, orc):
     qs, d = ctx.Q80(0, x)  # the context still works
     rd, rq = orc.quantize_q8_0(x[0])
     assert (qs == rq).all() and (d == rd).all()
+
+
+# ---------------------------------------------------------------------------------------- norm + residual
+def norm_add_ref(orc, x, y, w, s, w2):
+    """GemmaCpu.PostAndFfn's residual (src/GemmaCpu.cs:353-356, 367) and the next layer's quantized
+    RmsNorm input (src/CpuRef.cs:49-62, 183-191), row by row through the oracle."""
+    xn = np.stack([(x[r] + orc.rmsnorm(y[r], w, EPS)).astype(np.float32) for r in range(x.shape[0])])
+    if s != 1.0:
+        xn = (xn * np.float32(s)).astype(np.float32)
+    if w2 is None:
+        return xn, None, None
+    q = [orc.quantize_q8_0(orc.rmsnorm(xn[r], w2, EPS)) for r in range(x.shape[0])]
+    return xn, np.stack([a[1] for a in q]), np.stack([a[0] for a in q])
+
+
+@pytest.mark.parametrize("s", [1.0, 0.75])
+@pytest.mark.parametrize("quant", [False, True])
+@pytest.mark.parametrize("n", [2816, 16384])
+def test_norm_add_matches_oracle(ctx, orc, s, quant, n):
+    say(f"norm_add: rows=3 n={n} s={s} quant={quant}")
+    rng = np.random.default_rng(n + int(4 * s) + quant)
+    x = (rng.standard_normal((3, n)) * 4).astype(np.float32)
+    y = (rng.standard_normal((3, n)) * 40).astype(np.float32)
+    y[1] = 0.0  # rmsnorm of zeros adds zeros
+    w = (1 + 0.3 * rng.standard_normal(n)).astype(np.float32)
+    w2 = (1 + 0.3 * rng.standard_normal(n)).astype(np.float32) if quant else None
+    got = ctx.NormAdd(x, y, w, EPS, s, w2)
+    want = norm_add_ref(orc, x, y, w, s, w2)
+    if not quant:
+        np.testing.assert_array_equal(got, want[0])
+        return
+    np.testing.assert_array_equal(got[0], want[0], err_msg="new x")
+    np.testing.assert_array_equal(got[1], want[1], err_msg="quants")
+    np.testing.assert_array_equal(got[2], want[2], err_msg="fp16 scales")
+
+
+def test_norm_add_rejects_bad_arguments(ctx, pkg):
+    say("norm_add: argument checks")
+    x = np.ones((2, 64), np.float32)
+    with pytest.raises(pkg.moe.ArgumentError):
+        ctx.NormAdd(np.ones((1, 16392), np.float32), np.ones((1, 16392), np.float32), np.ones(16392, np.float32))
+    with pytest.raises(pkg.moe.ArgumentError):
+        ctx.NormAdd(np.ones((1, 36), np.float32), np.ones((1, 36), np.float32), np.ones(36, np.float32),
+                    w2=np.ones(36, np.float32))  # n not a multiple of 32 with the quantized output
+    np.testing.assert_array_equal(ctx.NormAdd(x, np.zeros_like(x), np.ones(64, np.float32)), x)
