@@ -329,6 +329,27 @@ def run_quant(args, pkg):
         modes[f"norm_add_quant_{rows}_rows"] = {"us": round(u, 2), "gbs": round(b / u / 1e3, 1)}
         for buf in (x, y, w, w2, qs, dq):
             buf.free()
+    for wtype, rows, cols in ((2, 2112, 2816), (2, 2816, 2112), (8, 2112, 2816)):  # the shared FFN's matvecs
+        bb = 18 if wtype == 2 else 34
+        wb = ctx.alloc(rows * cols // 32 * bb)
+        blocks = rng.integers(0, 256, (rows * cols // 32, bb), dtype=np.uint8)
+        blocks[:, :2] = (rng.standard_normal(rows * cols // 32) * 0.01).astype(np.float16).view(np.uint8).reshape(-1, 2)
+        wb.upload(blocks)
+        xq, xd, y = ctx.alloc(cols), ctx.alloc(cols // 16), ctx.alloc(rows * 4)
+        xq.upload(np.ones(cols, np.int8))
+        xd.upload(np.full(cols // 32, 0x3C00, np.uint16))
+        run = lambda: ctx._check(ctx.lib.phx_matvec(ctx.h, wtype, wb.ptr, rows, cols, 1, xq.ptr, xd.ptr, y.ptr))
+        for _ in range(3):
+            run()
+        ctx.sync()
+        t0 = time.perf_counter()
+        for _ in range(iters):
+            run()
+        ctx.sync()
+        u = (time.perf_counter() - t0) / iters * 1e6
+        modes[f"matvec_{qname(wtype)}_{rows}x{cols}"] = {"us": round(u, 2), "gbs": round(wb.nbytes / u / 1e3, 1)}
+        for buf in (wb, xq, xd, y):
+            buf.free()
     line = {"metric": "activation quantizer GB/s (algorithmic bytes) vs HBM peak", "value": round(gbs, 1),
             "unit": "GB/s", "n_gpus": 1, "steps": iters, "warmup": max(3, args.warmup // 100),
             "ms_per_step": round(us / 1e3, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,

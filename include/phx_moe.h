@@ -222,6 +222,17 @@ int phx_quant_q8_k(phx_moe_ctx* ctx, int mode, const float* x, const float* aux,
 int phx_norm_add(phx_moe_ctx* ctx, float* x, const float* y, const float* w, int rows, int n, float eps, float s,
                  const float* w2, int8_t* qs, uint16_t* d);
 
+/* Dense matvec of quantized weights: KernelsGemma.MatVecQ4_0 and the Q8_0 matvec as GemmaGpu.MatVec
+ * records them (src/KernelsGemma.cs:244-306, src/GemmaGpu.cs:463-476); the shared FFN's projections
+ * are its callers.  w: `rows` GGUF rows of `cols` (type PHX_Q4_0 or PHX_Q8_0, row r at r * row bytes,
+ * as the file holds them).  xq / xd: T Q8_0 input rows in the layout of phx_quant_q8_0.  y[t][r] is
+ * CpuRef.MatVec's value (src/CpuRef.cs:91-119, src/CpuRefGemma.cs:12-40: the block terms
+ * (float)isum * (d_w * d_x) added in block order).  Device pointers (xq 16-byte aligned); cols a
+ * multiple of 32, at most
+ * 16384 (Q8_0: 13,792); other weight types return PHX_ERR_UNSUPPORTED. */
+int phx_matvec(phx_moe_ctx* ctx, int type, const void* w, int rows, int cols, int T, const int8_t* xq,
+               const uint16_t* xd, float* y);
+
 #ifdef __cplusplus
 }
 #endif

@@ -923,6 +923,92 @@ void launch_norm_add(hipStream_t st, int rows, int n, float eps, float s, float*
     launch(k_norm_add, dim3(rows), dim3(NA_NT), (size_t)n * sizeof(float), st, n, eps, s, x, y, w, w2, qs, d16, flags);
 }
 
+// ------------------------------------------------------------------------------ dense matvec
+// KernelsGemma.MatVecQ4_0 / the Q8_0 matvec as GemmaGpu.MatVec records them (src/KernelsGemma.cs:244-306,
+// src/GemmaGpu.cs:463-476), with CpuRef's rounding (MatVecQ4_0, src/CpuRefGemma.cs:12-40; MatVecQ8_0,
+// src/CpuRef.cs:91-119): y[t][r] = the float sum, in block order from 0, of (float)isum_b * (d_w * d_x),
+// isum_b the integer dot of weight block b of row r with input block b of token t (planar Q8_0 input as
+// phx_quant_q8_0 writes it).  Rows as the GGUF file holds them (row r at r * row_bytes).  One wave per
+// row: the row staged in LDS by coalesced 2-byte loads, one block per lane and round, the terms added in
+// block order by lane 0.
+constexpr int MV_NT = 256, MV_ROWS = MV_NT / 64;
+
+template <int TYPE>  // PHX_Q4_0_DEV or PHX_Q8_0_DEV
+__global__ __launch_bounds__(MV_NT) void k_matvec(int rows, int nb, const uint8_t* __restrict__ w,
+                                                  const int8_t* __restrict__ xq, const uint16_t* __restrict__ xd,
+                                                  float* __restrict__ y)
+{
+    constexpr int BB = TYPE == PHX_Q4_0_DEV ? 18 : 34;
+    extern __shared__ __align__(16) uint8_t mv[];  // [MV_ROWS][terms nb floats], then [MV_ROWS][row bytes]
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, rb = nb * BB;
+    const int r = blockIdx.x * MV_ROWS + wave;  // wave-uniform
+    const int64_t t = blockIdx.y;
+    float* terms = (float*)mv + wave * nb;
+    uint16_t* srow = (uint16_t*)((float*)mv + MV_ROWS * nb) + wave * (rb / 2);
+    // the lane's first activation block, loaded beside the row (it does not depend on the weights)
+    const int4* qx0 = (const int4*)(xq + (t * nb + min(lane, nb - 1)) * 32);
+    const int4 xa0 = qx0[0], xb0 = qx0[1];
+    if (r < rows) {
+        const uint16_t* src = (const uint16_t*)(w + (int64_t)r * rb);
+        for (int i = lane; i < rb / 2; i += 64) srow[i] = src[i];
+    }
+    __syncthreads();
+    if (r < rows) {
+        for (int b = lane; b < nb; b += 64) {
+            const uint16_t* blk = srow + b * (BB / 2);  // d, then the payload as 2-byte halves
+            const int4* qx4 = (const int4*)(xq + (t * nb + b) * 32);
+            const int4 xa = b == lane ? xa0 : qx4[0], xb = b == lane ? xb0 : qx4[1];
+            const int x[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+            int isum = 0;
+            if (TYPE == PHX_Q4_0_DEV) {
+                // word k holds the nibbles of elements 4k..4k+3 (low) and 4k+16..4k+19 (high); each
+                // nibble n becomes the signed byte n - 8 (bias through the top bit)
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const uint32_t q = (uint32_t)blk[1 + 2 * k] | ((uint32_t)blk[2 + 2 * k] << 16);
+                    const int lo = (int)((((q & 0x0F0F0F0Fu) | 0x80808080u) - 0x08080808u) ^ 0x80808080u);
+                    const int hi = (int)(((((q >> 4) & 0x0F0F0F0Fu) | 0x80808080u) - 0x08080808u) ^ 0x80808080u);
+                    isum = __builtin_amdgcn_sdot4(lo, x[k], isum, false);
+                    isum = __builtin_amdgcn_sdot4(hi, x[k + 4], isum, false);
+                }
+            } else {
+#pragma unroll
+                for (int k = 0; k < 8; k++)
+                    isum = __builtin_amdgcn_sdot4((int)((uint32_t)blk[1 + 2 * k] | ((uint32_t)blk[2 + 2 * k] << 16)),
+                                                  x[k], isum, false);
+            }
+            terms[b] = (float)isum * (h2f(blk[0]) * h2f(xd[t * nb + b]));
+        }
+    }
+    __syncthreads();
+    if (r < rows && lane == 0) {
+        // sixteen terms read at a time (every read issued before the first add), added in order
+        float sum = 0.0f;
+        int b = 0;
+        for (; b + 16 <= nb; b += 16) {
+            float v[16];
+#pragma unroll
+            for (int j = 0; j < 16; j++) v[j] = terms[b + j];
+#pragma unroll
+            for (int j = 0; j < 16; j++) sum += v[j];
+        }
+        for (; b < nb; b++) sum += terms[b];
+        y[t * rows + r] = sum;
+    }
+}
+
+size_t matvec_lds(int type, int nb) { return (size_t)MV_ROWS * nb * (4 + (type == PHX_Q4_0_DEV ? 18 : 34)); }
+
+void launch_matvec(hipStream_t st, int type, int rows, int nb, int T, const uint8_t* w, const int8_t* xq,
+                   const uint16_t* xd, float* y)
+{
+    const dim3 grid((rows + MV_ROWS - 1) / MV_ROWS, T);
+    if (type == PHX_Q4_0_DEV)
+        launch(k_matvec<PHX_Q4_0_DEV>, grid, dim3(MV_NT), matvec_lds(type, nb), st, rows, nb, w, xq, xd, y);
+    else
+        launch(k_matvec<PHX_Q8_0_DEV>, grid, dim3(MV_NT), matvec_lds(type, nb), st, rows, nb, w, xq, xd, y);
+}
+
 // ------------------------------------------------------------------------------ combine, norms, residual
 // Per token: acc = sum_j yd[t*k+j] * w_j in rank order (src/GemmaCpu.cs:418, each term rounded then
 // added), out = rmsnorm(shared) * post1 + rmsnorm(acc) * post2 (src/GemmaCpu.cs:384,420-421), and

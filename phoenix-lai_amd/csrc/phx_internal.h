@@ -118,6 +118,10 @@ int launch_quant(hipStream_t st, int fmt_k, int mode, int rows, int n, float eps
 // per row: x = (x + rmsnorm(y) * w) * s (s != 1), then with w2 the Q8_0 of rmsnorm(x) * w2 (n <= 16384)
 void launch_norm_add(hipStream_t st, int rows, int n, float eps, float s, float* x, const float* y, const float* w,
                      const float* w2, int8_t* qs, uint16_t* d16, int* flags);
+// dense Q4_0 / Q8_0 matvec of GGUF rows with planar Q8_0 input, T input rows; LDS bytes per launch
+size_t matvec_lds(int type, int nb);
+void launch_matvec(hipStream_t st, int type, int rows, int nb, int T, const uint8_t* w, const int8_t* xq,
+                   const uint16_t* xd, float* y);
 // prefill path (kernels_prefill.hip): Q4_0 / Q8_0 grouped products on MFMA, tiles of up to kMmaTile
 // assignments; same arguments and outputs as launch_grouped.  npos > 0 reads the activations in
 // expert-list order, block-major (fp16 integers of block b, list position p at qh + (b * npos + p) * 32,

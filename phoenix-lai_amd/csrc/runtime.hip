@@ -1302,4 +1302,23 @@ int phx_norm_add(phx_moe_ctx* c, float* x, const float* y, const float* w, int r
     return PHX_OK;
 }
 
+int phx_matvec(phx_moe_ctx* c, int type, const void* w, int rows, int cols, int T, const int8_t* xq, const uint16_t* xd,
+               float* y)
+{
+    if (!c) return PHX_ERR_ARG;
+    if (type != PHX_Q4_0 && type != PHX_Q8_0)
+        return set_err(c, PHX_ERR_UNSUPPORTED, "matvec: weight type %d (Q4_0 and Q8_0 only)", type);
+    if (rows <= 0 || T <= 0 || T > 65535 || cols <= 0 || cols % 32 || cols > 16384)
+        return set_err(c, PHX_ERR_ARG, "matvec shape %d x %d, T=%d (cols a multiple of 32, <= 16384)", rows, cols, T);
+    if (!w || !xq || !xd || !y) return set_err(c, PHX_ERR_ARG, "matvec: null buffer");
+    if ((uintptr_t)w % 2 || (uintptr_t)xq % 16 || (uintptr_t)xd % 2 || (uintptr_t)y % 4)
+        return set_err(c, PHX_ERR_ARG, "matvec: w and xd need 2-byte, xq 16-byte, y 4-byte alignment");
+    const int dev = type == PHX_Q4_0 ? PHX_Q4_0_DEV : PHX_Q8_0_DEV;
+    HIPCHK(c, hipSetDevice(c->device));
+    if (matvec_lds(dev, cols / 32) > 65536) return set_err(c, PHX_ERR_ARG, "matvec: cols %d too large", cols);
+    launch_matvec(c->stream, dev, rows, cols / 32, T, (const uint8_t*)w, xq, xd, y);
+    HIPCHK(c, hipGetLastError());
+    return PHX_OK;
+}
+
 }  // extern "C"

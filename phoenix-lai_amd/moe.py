@@ -128,6 +128,7 @@ def load_lib():
         "phx_quant_q8_0": (i32, [vp, i32, vp, vp, i32, i32, C.c_float, vp, vp]),
         "phx_quant_q8_k": (i32, [vp, i32, vp, vp, i32, i32, C.c_float, vp, vp, vp]),
         "phx_norm_add": (i32, [vp, vp, vp, vp, i32, i32, C.c_float, C.c_float, vp, vp, vp]),
+        "phx_matvec": (i32, [vp, i32, vp, i32, i32, i32, vp, vp, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -382,6 +383,25 @@ class MoeContext:
         if x.ndim == 1:
             out = [o[0] for o in out]
         return out[0] if w2 is None else tuple(out)
+
+    def MatVec(self, wtype: int, w: np.ndarray, rows: int, cols: int, xq: np.ndarray, xd: np.ndarray) -> np.ndarray:
+        """GemmaGpu.MatVec for Q4_0 / Q8_0 weights (src/GemmaGpu.cs:463-476) on host arrays: w the GGUF rows
+        (bytes), xq / xd the Q8_0 input rows as Q80 returns them; y [T][rows] f32."""
+        w = np.ascontiguousarray(w, dtype=np.uint8)
+        xq = np.ascontiguousarray(xq, dtype=np.int8).reshape(-1, cols)
+        xd = np.ascontiguousarray(xd, dtype=np.uint16).reshape(xq.shape[0], cols // 32)
+        T = xq.shape[0]
+        bufs = [self.alloc(w.nbytes), self.alloc(xq.nbytes), self.alloc(xd.nbytes), self.alloc(T * rows * 4)]
+        for b, a in zip(bufs, (w, xq, xd)):
+            b.upload(a)
+        try:
+            self._check(self.lib.phx_matvec(self.h, wtype, bufs[0].ptr, rows, cols, T, bufs[1].ptr, bufs[2].ptr,
+                                            bufs[3].ptr))
+            self.sync()
+            return bufs[3].download((T, rows))
+        finally:
+            for b in bufs:
+                b.free()
 
     def stack_run_device(self, x_ptr: int, T: int):
         """Replay the captured stack on a device-resident x (async; sync() waits)."""

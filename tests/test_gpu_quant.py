@@ -132,3 +132,37 @@ def test_norm_add_rejects_bad_arguments(ctx, pkg):
         ctx.NormAdd(np.ones((1, 36), np.float32), np.ones((1, 36), np.float32), np.ones(36, np.float32),
                     w2=np.ones(36, np.float32))  # n not a multiple of 32 with the quantized output
     np.testing.assert_array_equal(ctx.NormAdd(x, np.zeros_like(x), np.ones(64, np.float32)), x)
+
+
+# ---------------------------------------------------------------------------------------- dense matvec
+def gguf_rows(rng, wtype, rows, cols):
+    """Random GGUF rows of Q4_0 (18-byte blocks) or Q8_0 (34-byte): random quants, finite fp16 scales."""
+    bb = 18 if wtype == 2 else 34
+    blocks = rng.integers(0, 256, (rows * cols // 32, bb), dtype=np.uint8)
+    d = (rng.standard_normal(rows * cols // 32) * 0.01).astype(np.float16)
+    blocks[:, :2] = d.view(np.uint8).reshape(-1, 2)
+    return blocks.reshape(-1)
+
+
+@pytest.mark.parametrize("wtype", [2, 8])
+@pytest.mark.parametrize("T,rows,cols", [(1, 2112, 2816), (3, 301, 2816), (2, 64, 12288)])
+def test_matvec_matches_oracle(ctx, orc, wtype, T, rows, cols):
+    """phx_quant_q8_0 then phx_matvec equals CpuRef.MatVec (the oracle's matvec: Q8_0 input, block terms
+    added in order), bit for bit; rows not a multiple of the workgroup's four."""
+    say(f"matvec: type={wtype} T={T} rows={rows} cols={cols}")
+    rng = np.random.default_rng(rows + cols + wtype)
+    w = gguf_rows(rng, wtype, rows, cols)
+    x = rng.standard_normal((T, cols)).astype(np.float32)
+    qs, d = ctx.Q80(0, x)
+    y = ctx.MatVec(wtype, w, rows, cols, qs, d)
+    for t in range(T):
+        np.testing.assert_array_equal(y[t], orc.matvec(wtype, w, rows, cols, x[t]), err_msg=f"token {t}")
+
+
+def test_matvec_rejects_other_types(ctx, pkg):
+    say("matvec: argument checks")
+    q, d = np.zeros(64, np.int8), np.zeros(2, np.uint16)
+    with pytest.raises(pkg.moe.NotSupportedError):
+        ctx.MatVec(12, np.zeros(144, np.uint8), 1, 64, q, d)  # Q4_K
+    with pytest.raises(pkg.moe.ArgumentError):
+        ctx.MatVec(2, np.zeros(18, np.uint8), 1, 48, np.zeros(48, np.int8), np.zeros(1, np.uint16))
