@@ -13,6 +13,11 @@ object for the dominant kernel (the grouped gate|up product; its average duratio
 events recorded around it in the same captured stack, replayed like the timed region) and the CPU
 baseline (the C restatement of the reference CPU path timed on this
 host's cores over a bounded sample).
+
+`--config quant` measures the ops either side of the layer instead (the activation quantizers, the
+residual norm-add with the quantized next input and the dense matvec): one JSON line of the same form
+whose value is the GELU-gated Q8_0 quantizer's GB/s at C3's down-input shape, with every other mode
+and op under "modes_2048_rows".
 """
 from __future__ import annotations
 
