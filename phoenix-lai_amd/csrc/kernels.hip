@@ -752,8 +752,8 @@ void launch_requant(hipStream_t st, int rows, int nf, const float* g, const floa
 //   QZ_RMS   CpuRef.RmsNorm(x, w) (src/CpuRef.cs:183-191: (x * scale) * w, the row's certified mean);
 //   QZ_GELU  gelu(x) * u (src/CpuRefGemma.cs:85-92).
 // Outputs in CpuRef.Q8Activations' planar layout (src/CpuRef.cs:34-46): qs int8 [n] per row; Q8_0 d as
-// fp16 bits [n/32]; Q8_K d float [n/256] and bsums int16 [n/16].  A workgroup takes QZ_CH elements of
-// one row (in QZ_RMS every workgroup forms its row's mean, as the reference's do).
+// fp16 bits [n/32]; Q8_K d float [n/256] and bsums int16 [n/16].  A workgroup takes ch elements of
+// one row: QZ_CH, or in QZ_RMS the whole row up to 8192 (every workgroup forms its row's mean).
 enum QzMode { QZ_PLAIN = 0, QZ_SILU = 1, QZ_RMS = 2, QZ_GELU = 3 };
 constexpr int QZ_NT = 256, QZ_CH = 2048;
 
@@ -767,13 +767,13 @@ __device__ __forceinline__ float qz_in(float v, float a, float scale, const floa
 }
 
 template <int MODE, bool K>
-__global__ __launch_bounds__(QZ_NT) void k_quant(int n, float eps, const float* __restrict__ x,
+__global__ __launch_bounds__(QZ_NT) void k_quant(int n, int ch, float eps, const float* __restrict__ x,
                                                  const float* __restrict__ aux, const float* __restrict__ tab,
                                                  int8_t* __restrict__ qs, uint16_t* __restrict__ d16,
                                                  float* __restrict__ dk, int16_t* __restrict__ bsums, int* flags)
 {
     const int64_t row = blockIdx.y;
-    const int tid = threadIdx.x, c0 = blockIdx.x * QZ_CH, c1 = min(n, c0 + QZ_CH);
+    const int tid = threadIdx.x, c0 = blockIdx.x * ch, c1 = min(n, c0 + ch);
     const float* xr = x + row * n;
     const float* ar = MODE == QZ_RMS ? aux : aux + row * n;  // the norm weight is shared by the rows
     float scale = 0.0f;
@@ -852,8 +852,9 @@ int launch_quant(hipStream_t st, int fmt_k, int mode, int rows, int n, float eps
         n *= rows;
         rows = 1;
     }
-    const dim3 grid((n + QZ_CH - 1) / QZ_CH, rows), blk(QZ_NT);
-#define QZ_L(M, K) launch((k_quant<M, K>), grid, blk, 0, st, n, eps, x, aux, tab, qs, d16, dk, bsums, flags)
+    const int ch = mode == QZ_RMS && n <= 8192 ? n : QZ_CH;  // a multiple of 256 or of 32 as the format needs
+    const dim3 grid((n + ch - 1) / ch, rows), blk(QZ_NT);
+#define QZ_L(M, K) launch((k_quant<M, K>), grid, blk, 0, st, n, ch, eps, x, aux, tab, qs, d16, dk, bsums, flags)
     switch (mode * 2 + (fmt_k ? 1 : 0)) {
     case 0: QZ_L(QZ_PLAIN, false); break;
     case 1: QZ_L(QZ_PLAIN, true); break;
