@@ -48,17 +48,37 @@ __device__ __forceinline__ float gelu_ref(float x, const float* __restrict__ tab
     return tab[f2h_bits(x)];
 }
 
-// Selection key of a logit: a total order in which NaN ranks below every number, so a parallel
-// argmax agrees on every lane and never loses track of the available experts.  For non-NaN values
-// the order (and the lower-index tie-break applied with it) is the reference's strict '>' scan.
-__device__ __forceinline__ float sel_key(float v) { return v != v ? -INFINITY : v; }
-__device__ __forceinline__ double sel_key(double v) { return v != v ? -INFINITY : v; }
-
 // (key, index) pair `o` beats `b`: higher key, or equal key and lower index; index < 0 is empty.
+// Keys compared with it are never NaN.
 template <class F>
 __device__ __forceinline__ bool sel_beats(F ov, int oi, F bv, int bi)
 {
     return oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi));
+}
+
+// Top-k rounds of the reference (src/GemmaCpu.cs:400-405): a round starts from the lowest-index
+// untaken expert e0 and replaces the current one only by a strictly greater logit.  Nothing compares
+// greater than NaN and NaN compares greater than nothing, so a round takes e0 when its logit is NaN,
+// and otherwise the largest non-NaN logit among the untaken experts, the lower index on ties.
+// scan_start finds e0 over a wave holding expert lane + 64 q in slot q: its index (-1 when no expert
+// is left, in every lane) and whether its logit is NaN.
+template <class F>
+__device__ __forceinline__ int scan_start(const bool (&avail)[4], const F (&v)[4], bool* e0_nan)
+{
+    int e0 = -1;
+    bool nan0 = false;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const uint64_t m = __ballot(avail[q]);
+        const uint64_t n = __ballot(avail[q] && v[q] != v[q]);
+        if (e0 < 0 && m != 0ull) {
+            const int l = __builtin_ctzll(m);
+            e0 = 64 * q + l;
+            nan0 = (n >> l) & 1ull;
+        }
+    }
+    *e0_nan = nan0;
+    return e0;
 }
 
 // An expert id outside [0, E) can only come from a bug upstream; it is mapped into range so no list
@@ -257,7 +277,8 @@ __device__ __forceinline__ double wave_incl_scan_dpp(double v)
     return v;
 }
 
-// Order-preserving map of a float to uint32 (NaN to 0, below every number).
+// Order-preserving map of a float to uint32 (NaN to 0, below every number; the certified selection
+// never accepts an order with a NaN logit, see wave_topk).
 __device__ __forceinline__ unsigned sortable_f32(float f)
 {
     if (f != f) return 0u;

@@ -274,8 +274,10 @@ void launch_router_exact(hipStream_t st, int T, int d, int E, const float* wt4, 
 }
 
 // ------------------------------------------------------------------------------ top-k and weights
-// One wave per token.  k rounds of argmax with the lower expert index winning ties, the order of
-// GemmaCpu.cs:400-405 (and the rank rule of KernelsMoe.RouterSelect, src/KernelsMoe.cs:64-78).
+// One wave per token.  k rounds of the reference's scan (GemmaCpu.cs:400-405, see scan_start): the
+// lowest-index untaken expert when its logit is NaN, else the argmax of the untaken non-NaN logits
+// with the lower expert index winning ties (the rank rule of KernelsMoe.RouterSelect,
+// src/KernelsMoe.cs:64-78, for NaN-free logits).
 // Weights as GemmaCpu.cs:406-407,417: p_j = (float)exp((double)(l_j - l_0)), sum in double,
 // w_j = (float)(p_j / sum) * down_scale[e_j]; rule 1 keeps the CPU's in-place sel[0] update.
 __global__ __launch_bounds__(64) void k_topk(int E, int k, int rule, const float* __restrict__ logits,
@@ -292,20 +294,26 @@ __global__ __launch_bounds__(64) void k_topk(int E, int k, int rule, const float
         avail[q] = e < E;
         v[q] = avail[q] ? logits[(int64_t)t * E + e] : 0.0f;
     }
-    float key[4];
-#pragma unroll
-    for (int q = 0; q < 4; q++) key[q] = sel_key(v[q]);
     for (int j = 0; j < k; j++) {
-        float bk = 0.0f, bv = 0.0f;
+        bool e0_nan;
+        const int e0 = scan_start(avail, v, &e0_nan);
+        float bv = 0.0f;
         int bi = -1;
+        if (e0_nan) {  // uniform: the scan keeps e0
+            bi = e0;
+            const int q0 = e0 >> 6;
+            const float vq = q0 == 0 ? v[0] : q0 == 1 ? v[1] : q0 == 2 ? v[2] : v[3];
+            bv = __shfl(vq, e0 & 63, 64);
+        } else {
 #pragma unroll
-        for (int q = 0; q < 4; q++)
-            if (avail[q] && sel_beats(key[q], lane + 64 * q, bk, bi)) { bk = key[q]; bv = v[q]; bi = lane + 64 * q; }
+            for (int q = 0; q < 4; q++)
+                if (avail[q] && v[q] == v[q] && sel_beats(v[q], lane + 64 * q, bv, bi)) { bv = v[q]; bi = lane + 64 * q; }
 #pragma unroll
-        for (int off = 32; off > 0; off >>= 1) {
-            float ok = __shfl_xor(bk, off, 64), ov = __shfl_xor(bv, off, 64);
-            int oi = __shfl_xor(bi, off, 64);
-            if (sel_beats(ok, oi, bk, bi)) { bk = ok; bv = ov; bi = oi; }
+            for (int off = 32; off > 0; off >>= 1) {
+                float ov = __shfl_xor(bv, off, 64);
+                int oi = __shfl_xor(bi, off, 64);
+                if (sel_beats(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+            }
         }
         if (bi >= 0 && lane == (bi & 63)) avail[bi >> 6] = false;
         if (lane == 0) { sel[j] = bv; sid[j] = bi < 0 ? 0 : bi; }

@@ -925,10 +925,10 @@ __device__ void exact_chains(const float* W, int d, const float* sm, const int* 
 
 // Exact selection for the tokens marked in s_bad (rare): the experts that can reach the chosen ones
 // (the ambiguous ones) are recomputed as the reference's float chains (src/GemmaCpu.cs:389-395) and
-// ranked exactly: ties to the lower index, NaN below every number (the strict '>' scan of
-// GemmaCpu.cs:400-405).  Every other expert's upper end lies below every chosen expert's lower end,
-// so the top-k lies among the ambiguous ones, unless a chain ends non-finite: then every expert of
-// the token is recomputed and ranked.  un: the LDS of sel_lds; sL (at un) ends holding the logits
+// ranked exactly by the strict '>' scan of GemmaCpu.cs:400-405 (ties to the lower index; a NaN
+// logit is taken once every lower-index expert is).  Every other expert's upper end lies below every
+// chosen expert's lower end, so the top-k lies among the ambiguous ones, unless a chain ends
+// non-finite: then every expert of the token is recomputed and ranked.  un: the LDS of sel_lds; sL (at un) ends holding the logits
 // the routing reports for those tokens.
 __device__ void select_exact(const DecArgs& a, unsigned char* un, int* s_ids, const int* s_bad, double* red,
                              bool count)
@@ -999,16 +999,46 @@ __device__ void select_exact(const DecArgs& a, unsigned char* un, int* s_ids, co
             const bool nfc = tid < na && !isfinite(sL[tt * E + slist[tid]]);
             if (!__syncthreads_or(nfc)) break;
         }
-        // exact ranks among the ambiguous experts
-        if (tid < na) skey[tid] = sel_key(sL[tt * E + slist[tid]]);
+        // exact ranks among the ambiguous experts (slist holds them in index order, so list position
+        // order is expert order).  A non-NaN expert's rank r among the non-NaN ones is the count of
+        // those that beat it.  A NaN logit appears only with every expert in the list, and the
+        // reference's scan (see scan_start) takes a NaN expert as soon as every lower-index expert is
+        // taken: right after the last-ranked non-NaN expert below it (rank P, -1 when there is none),
+        // behind the NaN experts below it.  So a NaN expert's position is P + 1 + (NaN experts below
+        // it) and a non-NaN expert's is r + (NaN experts whose P lies below r).
+        if (tid < na) skey[tid] = sL[tt * E + slist[tid]];
         __syncthreads();
-        if (tid < na) {
-            const double my = skey[tid];
-            const int b = slist[tid];
-            int r = 0;
-            for (int c = 0; c < na; c++) r += sel_beats(skey[c], slist[c], my, b);
-            if (r < k) s_ids[tt * k + r] = b;
+        const double my = tid < na ? skey[tid] : 0.0;
+        const bool my_nan = tid < na && my != my;
+        int r = 0;
+        if (tid < na && !my_nan)
+            for (int c = 0; c < na; c++) {
+                const double o = skey[c];
+                r += o == o && sel_beats(o, c, my, tid);
+            }
+        if (__syncthreads_or(my_nan)) {  // uniform; sbuf is free once the chains are done
+            int* srank = (int*)sbuf;     // [na] ranks of the non-NaN experts
+            int* sprev = srank + E;      // [na] P of the NaN experts, INT_MAX for the others
+            if (tid < na) srank[tid] = r;
+            __syncthreads();
+            int P = -1, below = 0;
+            if (my_nan)
+                for (int c = 0; c < tid; c++) {
+                    const double o = skey[c];
+                    if (o != o) below++;
+                    else P = max(P, srank[c]);
+                }
+            if (tid < na) sprev[tid] = my_nan ? P : INT_MAX;
+            __syncthreads();
+            if (my_nan) {
+                r = P + 1 + below;
+            } else if (tid < na) {
+                int ahead = 0;
+                for (int c = 0; c < na; c++) ahead += sprev[c] < r;
+                r += ahead;
+            }
         }
+        if (tid < na && r < k) s_ids[tt * k + r] = slist[tid];
         __syncthreads();
     }
 }

@@ -30,8 +30,13 @@ def layer(pkg, name, **kw):
 
 
 def within(gpu, ref):
-    err = np.abs(gpu.astype(np.float64) - ref.astype(np.float64))
-    return bool((err <= np.maximum(RTOL * np.abs(ref), ATOL)).all()), float(err.max())
+    """Tolerance check; a NaN matches only a NaN (a NaN logit selected by the scan makes every weight
+    and output of its token NaN)."""
+    gpu, ref = gpu.astype(np.float64), ref.astype(np.float64)
+    both_nan = np.isnan(gpu) & np.isnan(ref)
+    err = np.where(both_nan, 0.0, np.abs(gpu - ref))
+    ok = both_nan | (err <= np.maximum(RTOL * np.abs(ref), ATOL))
+    return bool(ok.all()), float(np.max(np.where(np.isnan(err), np.inf, err), initial=0.0))
 
 
 def check_layer(ctx, orc, L, x, shared=None, tag="", exact=False):
@@ -74,7 +79,7 @@ def check_layer(ctx, orc, L, x, shared=None, tag="", exact=False):
         ok, emax = within(out[t], rout)
         assert ok, f"{tag} t={t}: output beyond tolerance, max abs err {emax}"
         worst = max(worst, emax)
-        same = bool(np.array_equal(out[t], rout))
+        same = bool(np.array_equal(out[t], rout, equal_nan=True))
         exact_out += int(same)
         if exact:
             assert same, f"{tag} t={t}: exact-router output not bit-exact (max abs err {emax})"
@@ -229,6 +234,60 @@ def test_router_nan_row_decode_T8(ctx, pkg, orc, exact):
     assert np.isnan(logits[:, 11]).all() and not (ids == 11).any()
     if not exact:
         assert ctx.fallback_counts()[1] - before == 8
+
+
+# NaN router rows that the reference's scan does select (src/GemmaCpu.cs:400-405): a round starts at the
+# lowest untaken expert and keeps it when its logit is NaN, so a NaN expert is taken as soon as every
+# lower-index expert is.  (NaN expert, experts boosted to the top so that happens early.)
+NAN_PICKS = {"nan0": (0, ()), "nan1_after0": (1, (0,)), "nan3_after012": (3, (0, 1, 2))}
+
+
+@pytest.mark.parametrize("T,exact", [(1, False), (1, True), (8, False), (8, True), (40, False)])
+@pytest.mark.parametrize("case", list(NAN_PICKS))
+def test_router_nan_taken_by_scan(ctx, pkg, orc, case, T, exact):
+    """Decode T=1 and T=8 (certified with the exact fallback, and the exact router), and the general
+    path at T=40: ids, lists and logits match the oracle's scan; tokens that select the NaN expert have
+    all-NaN weights and outputs, as the reference computes them."""
+    nan_e, boost = NAN_PICKS[case]
+    say(f"router NaN pick {case} T={T} exact={exact}")
+    L = dict(layer(pkg, "c2_decode"))
+    W = L["gate_inp"].copy()
+    x = pkg.synth.make_input("c2_decode", T=T)
+    xbar = x.mean(0)
+    for j, e in enumerate(boost):
+        W[e] = ((0.9 - 0.1 * j) * xbar / np.linalg.norm(xbar)).astype(np.float32)
+    W[nan_e, 5] = np.nan
+    L["gate_inp"] = W
+    ctx.upload(0, L)
+    check_layer(ctx, orc, L, x, tag=f"NaN {case} T={T} exact={exact}", exact=exact)
+    ids, w, _, _, logits = ctx.routing()
+    assert np.isnan(logits[:, nan_e]).all()
+    picked = (ids == nan_e).any(1)
+    if not boost:
+        assert (ids[:, 0] == nan_e).all()
+    else:
+        # the boosted experts rank first for most tokens, and then the NaN expert comes next
+        top = [set(r[:len(boost)]) == set(boost) for r in ids]
+        assert sum(top) >= T // 2
+        assert all(r[len(boost)] == nan_e for r, tp in zip(ids, top) if tp)
+    assert np.isnan(w[picked]).all()
+    say(f"tokens taking the NaN expert: {int(picked.sum())}/{T}")
+
+
+def test_router_nan_row0_c1(ctx, pkg, orc):
+    """configs[0] with NaN in router row 0: every token takes expert 0 first (the reference's scan),
+    then its best expert."""
+    say("router NaN row 0 in c1")
+    L = dict(layer(pkg, "c1_tiny"))
+    W = L["gate_inp"].copy()
+    W[0, 0] = np.nan
+    L["gate_inp"] = W
+    x = pkg.synth.make_input("c1_tiny")
+    for exact in (False, True):
+        ctx.upload(0, L)
+        check_layer(ctx, orc, L, x, tag=f"c1 NaN row 0 exact={exact}", exact=exact)
+        ids = ctx.routing()[0]
+        assert (ids[:, 0] == 0).all()
 
 
 def test_c3_prefill_reduced(ctx, pkg, orc):

@@ -58,6 +58,80 @@ def test_router_ties_pick_lower_index(orc, synth):
     assert list(ids) == [0, 1] and w[0] == w[1] == np.float32(0.5)
 
 
+def _planted_logits_layer(synth, vals):
+    """A layer whose router logits are exactly fl(vals[e] * m_0): W[e] is vals[e] at element 0 and zero
+    elsewhere, so every other product is a zero and the reference's chain adds only zeros to it."""
+    E = len(vals)
+    L = synth.make_layer(_cfg(E=E, k=E))
+    W = np.zeros_like(L["gate_inp"])
+    W[:, 0] = np.asarray(vals, np.float32)
+    L["gate_inp"] = W
+    x = np.ones(L["d"], np.float32)  # m_0 = 1/sqrt(d) > 0, so the logits keep the order of vals
+    return L, x
+
+
+# Known answers of the reference's scan (GemmaCpu.cs:400-405) with NaN logits, derived by hand: a round
+# starts at the lowest untaken expert and moves only to a strictly greater logit, so it stays on a NaN
+# start and never moves to a NaN.
+NAN_SCAN_CASES = [
+    ([np.nan, 1.0, 2.0], [0, 2, 1]),
+    ([1.0, np.nan, 2.0], [2, 0, 1]),
+    ([3.0, np.nan, 5.0, 1.0, np.nan, np.nan, 7.0, 2.0], [6, 2, 0, 1, 7, 3, 4, 5]),
+    ([np.nan] * 4, [0, 1, 2, 3]),
+    ([2.0, 2.0, np.nan, -np.inf, np.nan, 2.0], [0, 1, 2, 5, 3, 4]),
+    ([-np.inf, np.nan, -np.inf, 4.0], [3, 0, 1, 2]),
+]
+
+
+@pytest.mark.parametrize("case", range(len(NAN_SCAN_CASES)))
+def test_router_nan_scan_known_answers(orc, synth, case):
+    vals, want = NAN_SCAN_CASES[case]
+    L, x = _planted_logits_layer(synth, vals)
+    logits, ids, w = orc.router(L, x)
+    assert np.array_equal(np.isnan(logits), np.isnan(np.asarray(vals)))
+    assert list(ids) == want
+
+
+def nan_scan_positions(logits):
+    """The positions the decode path's exact fallback assigns in parallel (kernels_decode.hip,
+    select_exact): a non-NaN expert at its rank r among the non-NaN ones plus the NaN experts whose P
+    lies below r; a NaN expert at P + 1 + the NaN experts below it, P being the largest rank among the
+    non-NaN experts below it (-1 if none).  Checked here against the oracle's sequential scan."""
+    E = len(logits)
+    isn = np.isnan(logits)
+    r = np.zeros(E, np.int64)
+    for e in range(E):
+        if not isn[e]:
+            r[e] = sum(1 for c in range(E) if not isn[c] and (logits[c] > logits[e] or (logits[c] == logits[e] and c < e)))
+    P = np.full(E, np.iinfo(np.int64).max)
+    pos = r.copy()
+    for n in range(E):
+        if isn[n]:
+            P[n] = max([r[c] for c in range(n) if not isn[c]], default=-1)
+            pos[n] = P[n] + 1 + int(isn[:n].sum())
+    for e in range(E):
+        if not isn[e]:
+            pos[e] = r[e] + int((P < r[e]).sum())
+    order = np.empty(E, np.int64)
+    order[pos] = np.arange(E)
+    return order
+
+
+def test_router_nan_parallel_positions_equal_scan(orc, synth):
+    rng = np.random.default_rng(11)
+    for trial in range(300):
+        E = int(rng.integers(2, 20))
+        vals = rng.integers(-3, 4, E).astype(np.float64)  # small integers: many exact ties
+        vals[rng.random(E) < rng.uniform(0, 0.7)] = np.nan
+        if trial % 7 == 0:
+            vals[rng.random(E) < 0.2] = -np.inf
+        L, x = _planted_logits_layer(synth, vals)
+        logits, ids, _ = orc.router(L, x)
+        assert list(nan_scan_positions(logits)) == list(ids), (vals, list(ids))
+    for c, (vals, want) in enumerate(NAN_SCAN_CASES):
+        assert list(nan_scan_positions(np.asarray(vals, np.float32))) == want
+
+
 def test_router_cpuref_weight_quirk(orc, synth):
     """weight_rule 1 keeps the reference CPU's in-place update: w_0 = 1/S, w_j = exp(l_j - 1)/S."""
     L = synth.make_layer(_cfg(E=8, k=4), weight_rule=1)
