@@ -6,13 +6,15 @@ leg, as the checker (or the timed CPU baseline).  The product never imports it.
 from __future__ import annotations
 
 import ctypes as C
+import os
 import subprocess
 from pathlib import Path
 
 import numpy as np
 
 HERE = Path(__file__).resolve().parent
-LIB = HERE / "_build" / "liboracle.so"
+# PHX_ORACLE_LIB names another build of oracle.c (tests/mutation_check.py loads planted-mistake copies)
+LIB = Path(os.environ.get("PHX_ORACLE_LIB", HERE / "_build" / "liboracle.so"))
 
 
 def build():

@@ -116,3 +116,47 @@ def random_blocks(rng: np.random.Generator, t: int, nblocks: int) -> np.ndarray:
         b[:, 208] = d & 0xFF
         b[:, 209] = d >> 8
     return b.reshape(-1)
+
+
+def h16_bits(v) -> int:
+    return int(np.float16(v).view(np.uint16))
+
+
+def pack_q4_k(d_bits: int, dmin_bits: int, sc, m, q) -> np.ndarray:
+    """One 144-byte Q4_K super-block from its parts (the inverse of q4_k_parts): sc, m in 0..63, q in 0..15."""
+    blk = np.zeros(144, np.uint8)
+    blk[0], blk[1] = d_bits & 0xFF, d_bits >> 8
+    blk[2], blk[3] = dmin_bits & 0xFF, dmin_bits >> 8
+    s = np.zeros(12, np.int32)
+    for j in range(8):
+        if j < 4:
+            s[j] |= sc[j] & 63
+            s[j + 4] |= m[j] & 63
+        else:
+            s[j + 4] |= (sc[j] & 15) | ((m[j] & 15) << 4)
+            s[j - 4] |= (sc[j] >> 4) << 6
+            s[j] |= (m[j] >> 4) << 6
+    blk[4:16] = s.astype(np.uint8)
+    q = np.asarray(q, np.int32)
+    for c in range(4):
+        blk[16 + 32 * c:16 + 32 * c + 32] = (q[64 * c:64 * c + 32] | (q[64 * c + 32:64 * c + 64] << 4)).astype(np.uint8)
+    return blk
+
+
+def pack_q6_k(d_bits: int, sc, q) -> np.ndarray:
+    """One 210-byte Q6_K super-block from its parts (the inverse of q6_k_parts): int8 sc[16], q in -32..31."""
+    blk = np.zeros(210, np.uint8)
+    u = np.asarray(q, np.int32) + 32
+    for h in range(2):
+        L = np.zeros(64, np.int32)
+        H = np.zeros(32, np.int32)
+        for l in range(32):
+            v0, v1, v2, v3 = (u[128 * h + l + 32 * r] for r in range(4))
+            L[l] = (v0 & 15) | ((v2 & 15) << 4)
+            L[l + 32] = (v1 & 15) | ((v3 & 15) << 4)
+            H[l] = (v0 >> 4) | ((v1 >> 4) << 2) | ((v2 >> 4) << 4) | ((v3 >> 4) << 6)
+        blk[64 * h:64 * h + 64] = L.astype(np.uint8)
+        blk[128 + 32 * h:128 + 32 * h + 32] = H.astype(np.uint8)
+    blk[192:208] = np.asarray(sc, np.int8).view(np.uint8)
+    blk[208], blk[209] = d_bits & 0xFF, d_bits >> 8
+    return blk

@@ -1,0 +1,115 @@
+"""Mutation check of the oracle's pins (run by hand: `python tests/mutation_check.py`; not collected).
+
+Each mutation plants one plausible mistake into a copy of oracle/oracle.c, builds it into a temporary
+library with the oracle's own flags, and runs the pin tests (tests/test_oracle_numerics.py,
+test_oracle_layer.py, test_oracle_chain_order.py) against it through PHX_ORACLE_LIB.  A mutation that
+every pin test passes means the pins miss that mistake; the script reports it and exits nonzero.  The
+golden fixtures are left out on purpose: they were written by the oracle, so they would flag every
+change without pinning anything.
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+import tempfile
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent.parent
+ORACLE = ROOT / "oracle"
+PINS = ["tests/test_oracle_numerics.py", "tests/test_oracle_layer.py", "tests/test_oracle_chain_order.py"]
+CFLAGS = ["-O2", "-std=c11", "-fPIC", "-ffp-contract=off", "-fno-fast-math", "-fexcess-precision=standard",
+          "-fopenmp", "-shared"]
+
+# name: [(text in oracle.c, replacement), ...]; every text must occur exactly once
+MUTATIONS = {
+    "q4_0 nibbles swapped": [("((qs[j] & 0x0F) - 8) * qx[j] + ((qs[j] >> 4) - 8) * qx[j + 16]",
+                              "((qs[j] >> 4) - 8) * qx[j] + ((qs[j] & 0x0F) - 8) * qx[j + 16]")],
+    "router 1/sqrt(d) dropped": [("float sc = 1.0f / (float)sqrt((double)d);", "float sc = 1.0f;")],
+    "q8_0 half-even rounding": [("qs[o + j] = (int8_t)roundf(x[o + j] * id);", "qs[o + j] = (int8_t)rintf(x[o + j] * id);")],
+    "q4_k min sign": [("sumf -= dm * (float)sumi;", "sumf += dm * (float)sumi;")],
+    "gelu constant": [("0.044715f", "0.04472f")],
+    "post norm missing": [("orc_rmsnorm(acc, d, L->post_ffw_norm_2, L->eps, acc2);", "memcpy(acc2, acc, sizeof(float) * d);")],
+    "q6_k high-bit shift": [("(((qh[l] >> 2) & 3) << 4)", "(((qh[l] >> 4) & 3) << 4)")],
+    "q8_k last index on ties": [("if (ax > amax) { amax = ax; max = x[o + j]; }", "if (ax >= amax) { amax = ax; max = x[o + j]; }")],
+    "down scale missing": [("w[j] = (float)(sel[j] / sum) * L->down_scale[ids[j]];", "w[j] = (float)(sel[j] / sum);")],
+    "top-k ties to the higher index": [("(bi < 0 || logits[e] > logits[bi])", "(bi < 0 || logits[e] >= logits[bi])")],
+    "fp16 truncates": [("if (r > 0x1000u || (r == 0x1000u && (h & 1) != 0)) h++;", "")],
+    "weight rules swapped": [("if (L->weight_rule == ORC_W_CPUREF) {", "if (L->weight_rule != ORC_W_CPUREF) {")],
+    "lists unstable": [("for (int a = 0; a < T * k; a++) perm[fill[ids[a]]++] = a;",
+                        "for (int a = T * k - 1; a >= 0; a--) perm[fill[ids[a]]++] = a;")],
+    "top-k ranks NaN lowest": [("(bi < 0 || logits[e] > logits[bi])",
+                                "(bi < 0 || logits[e] > logits[bi] || (logits[bi] != logits[bi] && logits[e] == logits[e]))")],
+    # chain orders
+    "router chain reversed": [("for (int i = 0; i < d; i++) s += wr[i] * in[i];",
+                               "for (int i = d - 1; i >= 0; i--) s += wr[i] * in[i];")],
+    "router chain in double": [("        float s = 0;\n        for (int i = 0; i < d; i++) s += wr[i] * in[i];",
+                                "        double s = 0;\n        for (int i = 0; i < d; i++) s += wr[i] * in[i];")],
+    "router chain two lanes": [("for (int i = 0; i < d; i++) s += wr[i] * in[i];",
+                                "{ float ev = 0, od = 0; for (int i = 0; i < d; i += 2) { ev += wr[i] * in[i]; "
+                                "if (i + 1 < d) od += wr[i + 1] * in[i + 1]; } s = ev + od; }")],
+    "q4_0 block chain reversed": [("for (int b = 0; b < nb; b++) {\n        const uint8_t* blk = row + b * 18;\n        const uint8_t* qs",
+                                   "for (int b = nb - 1; b >= 0; b--) {\n        const uint8_t* blk = row + b * 18;\n        const uint8_t* qs")],
+    "q4_0 block chain two lanes": [
+        ("const int8_t* xq)\n{\n    float sum = 0;\n    for (int b = 0; b < nb; b++) {\n        const uint8_t* blk = row + b * 18;",
+         "const int8_t* xq)\n{\n    float sum = 0, sum2 = 0;\n    for (int b = 0; b < nb; b++) {\n        const uint8_t* blk = row + b * 18;"),
+        ("        sum += (float)isum * (orc_half_to_float(rd16(blk)) * orc_half_to_float(xd[b]));\n    }\n    return sum;\n}\n\n/* MatVecQ8_0",
+         "        if (b & 1) sum2 += (float)isum * (orc_half_to_float(rd16(blk)) * orc_half_to_float(xd[b]));\n"
+         "        else sum += (float)isum * (orc_half_to_float(rd16(blk)) * orc_half_to_float(xd[b]));\n    }\n"
+         "    return sum + sum2;\n}\n\n/* MatVecQ8_0")],
+    "q8_0 block chain in double": [("{\n    float sum = 0;\n    for (int b = 0; b < nb; b++) {\n        const uint8_t* blk = row + b * 34;",
+                                    "{\n    double sum = 0;\n    for (int b = 0; b < nb; b++) {\n        const uint8_t* blk = row + b * 34;")],
+    "q8_0 block chain reversed": [("for (int b = 0; b < nb; b++) {\n        const uint8_t* blk = row + b * 34;\n        const int8_t* qw",
+                                   "for (int b = nb - 1; b >= 0; b--) {\n        const uint8_t* blk = row + b * 34;\n        const int8_t* qw")],
+    "dotk lanes merged": [("for (int l = 0; l < 8; l++) sums[l] += dd * (float)aux32[l];",
+                           "for (int l = 0; l < 8; l++) sumf += dd * (float)aux32[l];")],
+    "dotk fold reversed": [("for (int l = 0; l < 8; l++) sumf += sums[l];", "for (int l = 7; l >= 0; l--) sumf += sums[l];")],
+    "dotk fold in double": [("    float sumf = 0;\n    int sixteen", "    double sumf = 0;\n    int sixteen")],
+    "dotk min term last": [("    float sumf = 0;\n    int sixteen", "    float sumf = 0, summin = 0;\n    int sixteen"),
+                           ("sumf -= dm * (float)sumi;", "summin += dm * (float)sumi;"),
+                           ("for (int l = 0; l < 8; l++) sumf += sums[l];\n    return sumf;",
+                            "for (int l = 0; l < 8; l++) sumf += sums[l];\n    sumf -= summin;\n    return sumf;")],
+}
+
+
+def build(src: str, out: Path) -> None:
+    c = out.with_suffix(".c")
+    c.write_text(src)
+    subprocess.run(["gcc", *CFLAGS, f"-I{ORACLE}", "-o", str(out), str(c), "-lm"], check=True)
+
+
+def run_pins(lib: Path) -> tuple[bool, str]:
+    env = dict(os.environ, PHX_ORACLE_LIB=str(lib))
+    r = subprocess.run([sys.executable, "-m", "pytest", *PINS, "-x", "-q", "-m", "not gpu", "-p", "no:cacheprovider"],
+                       cwd=ROOT, env=env, capture_output=True, text=True)
+    failed = [ln for ln in r.stdout.splitlines() if ln.startswith("FAILED")]
+    return r.returncode == 0, failed[0][7:] if failed else r.stdout.strip().splitlines()[-1]
+
+
+def main() -> int:
+    base = (ORACLE / "oracle.c").read_text()
+    missed = []
+    with tempfile.TemporaryDirectory() as td:
+        lib = Path(td) / "lib_clean.so"
+        build(base, lib)
+        ok, msg = run_pins(lib)
+        print(f"{'clean oracle':34s} {'passes' if ok else 'FAILS: ' + msg}", flush=True)
+        if not ok:
+            return 2
+        for i, (name, subs) in enumerate(MUTATIONS.items()):
+            src = base
+            for old, new in subs:
+                assert src.count(old) == 1, f"{name}: pattern occurs {src.count(old)} times"
+                src = src.replace(old, new)
+            lib = Path(td) / f"lib_m{i}.so"
+            build(src, lib)
+            ok, msg = run_pins(lib)
+            print(f"{name:34s} {'MISSED' if ok else 'caught by ' + msg}", flush=True)
+            if ok:
+                missed.append(name)
+    print(f"{len(MUTATIONS) - len(missed)}/{len(MUTATIONS)} mutations caught")
+    return 1 if missed else 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
