@@ -123,6 +123,19 @@ int phx_moe_layer_upload(phx_moe_ctx* ctx, int layer, const phx_moe_layer_desc* 
  * x, shared: [T][d] f32; out: [T][d] f32. */
 int phx_moe_ffn(phx_moe_ctx* ctx, int layer, int T, float* x, const float* shared, float* out, unsigned flags);
 
+/* phx_moe_ffn without allocating: no counterpart in the reference.  For callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * The same computation and kernels as phx_moe_ffn with PHX_FLAG_DEVICE_PTRS (x, shared, out are device
+ * pointers; PHX_FLAG_RESIDUAL, PHX_FLAG_EXACT_ROUTER and PHX_FLAG_ASYNC apply), but the call's workspace
+ * (activations, routing, lists, intermediates) lives in a fixed array of PHX_NOALLOC_SCRATCH_BYTES per
+ * device instead of the context's arena, and the call makes no hipMalloc / hipFree.  A call whose
+ * workspace would not fit returns PHX_ERR_ARG (at C2's shapes every T up to 64 fits).  Every noalloc
+ * call on one device shares that array and leaves its contents behind: calls that overlap on one
+ * device (several contexts or threads) race.  Profiling timers are not applied. */
+#define PHX_NOALLOC_SCRATCH_BYTES (32u << 20)
+int phx_moe_ffn_noalloc(phx_moe_ctx* ctx, int layer, int T, float* x, const float* shared, float* out,
+                        unsigned flags);
+
 /* Routing of the last phx_moe_ffn call (any pointer may be NULL): ids [T][k] best first,
  * weights [T][k] (with ffn_down_exps.scale folded in, src/GemmaCpu.cs:417), offsets [E+1] and
  * perm [T*k] (expert e's assignments a = t*k + j in ascending order: perm[offsets[e]..offsets[e+1]),

@@ -4,6 +4,8 @@
 // in that order (per-row block chains, the router's dot chain, the rank-ordered combine), and the
 // double-precision sums of squares of RmsNorm are reproduced through a certified error bound with
 // an exact sequential fallback.
+#include <algorithm>
+
 #include "device_common.h"
 
 namespace phx {
@@ -1116,6 +1118,20 @@ __global__ __launch_bounds__(256) void k_stream_copy(uint4* __restrict__ dst, co
 void launch_stream_copy(hipStream_t st, void* dst, const void* src, int64_t bytes)
 {
     launch(k_stream_copy, dim3(256 * 8), dim3(256), 0, st, (uint4*)dst, (const uint4*)src, bytes / 16);
+}
+
+// Fill n 32-bit words with v: clears workspace that must start at zero with a kernel rather than a
+// memset node, so the enqueued work stays a plain kernel when a caller captures it into a graph.
+__global__ __launch_bounds__(256) void k_fill_u32(uint32_t* __restrict__ p, int64_t n, uint32_t v)
+{
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) p[i] = v;
+}
+
+void launch_fill_u32(hipStream_t st, uint32_t* p, int64_t n, uint32_t v)
+{
+    const int64_t blocks = std::min<int64_t>((n + 255) / 256, 1024);
+    launch(k_fill_u32, dim3((unsigned)std::max<int64_t>(blocks, 1)), dim3(256), 0, st, p, n, v);
 }
 
 // ------------------------------------------------------------------------------ arithmetic self-test

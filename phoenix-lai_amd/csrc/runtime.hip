@@ -8,6 +8,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 #include <string>
 #include <thread>
 #include <vector>
@@ -282,6 +283,14 @@ struct phx_moe_ctx {
     hipGraphExec_t graph_exec = nullptr;
     hipGraph_t graph = nullptr;
     int graph_T = 0, graph_first = 0, graph_n = 0;
+    // phx_moe_ffn_noalloc: this device's address of the scratch array, the workspace table laid out
+    // inside it (sized at creation, swapped with ws during a call), whether the last call used it, and
+    // the bump allocation ensure() does while it lays the table out
+    unsigned char* scratch = nullptr;
+    std::vector<Buf> ws_scratch;
+    bool last_scratch = false;
+    unsigned char* bump_base = nullptr;
+    size_t bump_off = 0, bump_cap = 0;
 };
 
 namespace {
@@ -328,6 +337,15 @@ int ensure(phx_moe_ctx* c, int id, size_t bytes)
     if ((int)c->ws.size() < W_COUNT) c->ws.resize(W_COUNT);
     Buf& b = c->ws[id];
     if (b.bytes >= bytes && b.p) return PHX_OK;
+    if (c->bump_base) {  // laying out phx_moe_ffn_noalloc's table inside the scratch array
+        const size_t off = (c->bump_off + 255) & ~(size_t)255, n = std::max<size_t>(bytes, 256);
+        if (off + n > c->bump_cap)
+            return set_err(c, PHX_ERR_ARG, "the call's workspace exceeds the %zu-byte scratch array", c->bump_cap);
+        b.p = c->bump_base + off;
+        b.bytes = n;
+        c->bump_off = off + n;
+        return PHX_OK;
+    }
     if (b.p) HIPCHK(c, hipFree(b.p));
     b.p = nullptr;
     b.bytes = 0;
@@ -796,6 +814,53 @@ int drain_profile(phx_moe_ctx* c)
 
 }  // namespace
 
+// Workspace of phx_moe_ffn_noalloc: one array per device, which each GPU the library runs on holds
+// until the process ends.  In host code the name is only a stand-in, never a device address: the
+// address comes from hipGetSymbolAddress, once per device with that device current (at context
+// creation), and only that address is used.  Every noalloc call on a device shares the array and
+// leaves its contents behind; calls that overlap on one device race.
+static __device__ __align__(256) unsigned char scratch[PHX_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+unsigned char* g_scratch_addr[kMaxDevices] = {};
+
+// The scratch array's address on c's device (current), looked up on the device's first context.
+int scratch_address(phx_moe_ctx* c)
+{
+    if (c->device >= kMaxDevices) return set_err(c, PHX_ERR_UNSUPPORTED, "device index %d too large", c->device);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_addr[c->device]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return set_err(c, e == hipSuccess ? PHX_ERR_HIP : hip_code(e), "hipGetSymbolAddress(scratch): %s",
+                           hipGetErrorString(e));
+        g_scratch_addr[c->device] = (unsigned char*)p;
+    }
+    c->scratch = g_scratch_addr[c->device];
+    return PHX_OK;
+}
+
+int check_ffn_args(phx_moe_ctx* c, int layer, int T, const float* x, float* out, unsigned flags)
+{
+    if (layer < 0 || layer >= (int)c->layers.size() || !c->layers[layer].present)
+        return set_err(c, PHX_ERR_ARG, "layer %d not uploaded", layer);
+    const Layer& L = c->layers[layer];
+    if (T <= 0 || (int64_t)T * L.desc.n_used > 65535) return set_err(c, PHX_ERR_ARG, "T=%d out of range", T);
+    if (!x || !out) return set_err(c, PHX_ERR_ARG, "null x/out");
+    if ((flags & PHX_FLAG_RESIDUAL) && !L.post_ffw) return set_err(c, PHX_ERR_ARG, "residual needs post_ffw_norm");
+    if ((flags & PHX_FLAG_RESIDUAL) && out == x) return set_err(c, PHX_ERR_ARG, "residual needs out distinct from x");
+    return PHX_OK;
+}
+
+// the workspace table the last call used (routing and intermediates are read from it)
+const std::vector<Buf>& last_ws(const phx_moe_ctx* c) { return c->last_scratch ? c->ws_scratch : c->ws; }
+
+}  // namespace
+
 // ================================================================================ C ABI
 
 extern "C" {
@@ -855,6 +920,8 @@ int phx_moe_create(int hip_device, phx_moe_ctx** out)
         }
         if ((h = hipMalloc((void**)&c->flags, 64)) != hipSuccess) { rc = set_err(c, hip_code(h), "OOM"); break; }
         if ((h = hipMemset(c->flags, 0, 64)) != hipSuccess) { rc = set_err(c, hip_code(h), "memset failed"); break; }
+        if ((rc = scratch_address(c)) != PHX_OK) break;
+        c->ws_scratch.resize(W_COUNT);
     } while (0);
     if (rc != PHX_OK) {
         phx_moe_destroy(c);
@@ -933,16 +1000,13 @@ int phx_moe_layer_upload(phx_moe_ctx* c, int layer, const phx_moe_layer_desc* D)
 int phx_moe_ffn(phx_moe_ctx* c, int layer, int T, float* x, const float* shared, float* out, unsigned flags)
 {
     if (!c) return PHX_ERR_ARG;
-    if (layer < 0 || layer >= (int)c->layers.size() || !c->layers[layer].present)
-        return set_err(c, PHX_ERR_ARG, "layer %d not uploaded", layer);
-    const Layer& L = c->layers[layer];
-    if (T <= 0 || (int64_t)T * L.desc.n_used > 65535) return set_err(c, PHX_ERR_ARG, "T=%d out of range", T);
-    if (!x || !out) return set_err(c, PHX_ERR_ARG, "null x/out");
-    if ((flags & PHX_FLAG_RESIDUAL) && !L.post_ffw) return set_err(c, PHX_ERR_ARG, "residual needs post_ffw_norm");
-    if ((flags & PHX_FLAG_RESIDUAL) && out == x) return set_err(c, PHX_ERR_ARG, "residual needs out distinct from x");
-    HIPCHK(c, hipSetDevice(c->device));
-    int rc = ensure_workspace(c, L, T);
+    int rc = check_ffn_args(c, layer, T, x, out, flags);
     if (rc) return rc;
+    const Layer& L = c->layers[layer];
+    HIPCHK(c, hipSetDevice(c->device));
+    rc = ensure_workspace(c, L, T);
+    if (rc) return rc;
+    c->last_scratch = false;
     const size_t bytes = (size_t)T * L.desc.d * 4;
     const bool dev = flags & PHX_FLAG_DEVICE_PTRS;
     float* xin = x;
@@ -969,18 +1033,53 @@ int phx_moe_ffn(phx_moe_ctx* c, int layer, int T, float* x, const float* shared,
     return PHX_OK;
 }
 
+int phx_moe_ffn_noalloc(phx_moe_ctx* c, int layer, int T, float* x, const float* shared, float* out, unsigned flags)
+{
+    if (!c) return PHX_ERR_ARG;
+    int rc = check_ffn_args(c, layer, T, x, out, flags);
+    if (rc) return rc;
+    if (!c->scratch || (int)c->ws_scratch.size() != W_COUNT) return set_err(c, PHX_ERR_HIP, "no scratch array");
+    const Layer& L = c->layers[layer];
+    HIPCHK(c, hipSetDevice(c->device));
+    // this call's workspace table, laid out afresh inside the scratch array (no allocation: the table
+    // was sized at creation and the vectors only swap)
+    std::swap(c->ws, c->ws_scratch);
+    for (Buf& b : c->ws) b = Buf{};
+    c->bump_base = c->scratch;
+    c->bump_off = 0;
+    c->bump_cap = PHX_NOALLOC_SCRATCH_BYTES;
+    rc = ensure_workspace(c, L, T);
+    c->bump_base = nullptr;
+    const bool prof = c->profiling;  // the timers would create events
+    c->profiling = false;
+    if (rc == PHX_OK) {
+        // the shared FFN's one-expert ids must read zero; the array keeps the previous call's bytes
+        if (c->ws[W_ZERO].p) launch_fill_u32(c->stream, (uint32_t*)c->ws[W_ZERO].p, (int64_t)T, 0u);
+        rc = run_layer(c, L, T, x, shared, out, (flags & PHX_FLAG_RESIDUAL) ? x : nullptr, flags);
+    }
+    c->profiling = prof;
+    std::swap(c->ws, c->ws_scratch);
+    if (rc) return rc;
+    HIPCHK(c, hipGetLastError());
+    c->last_T = T;
+    c->last_layer = layer;
+    c->last_scratch = true;
+    if (!(flags & PHX_FLAG_ASYNC)) HIPCHK(c, hipStreamSynchronize(c->stream));
+    return PHX_OK;
+}
+
 int phx_moe_get_routing(phx_moe_ctx* c, int32_t* ids, float* weights, int32_t* offsets, int32_t* perm, float* logits)
 {
     if (!c || c->last_layer < 0) return PHX_ERR_ARG;
     const phx_moe_layer_desc& D = c->layers[c->last_layer].desc;
     const size_t n = (size_t)c->last_T * D.n_used;
     HIPCHK(c, hipStreamSynchronize(c->stream));
-    if (ids) HIPCHK(c, hipMemcpy(ids, c->ws[W_IDS].p, n * 4, hipMemcpyDeviceToHost));
-    if (weights) HIPCHK(c, hipMemcpy(weights, c->ws[W_W].p, n * 4, hipMemcpyDeviceToHost));
-    if (offsets) HIPCHK(c, hipMemcpy(offsets, c->ws[W_OFF].p, (size_t)(D.n_expert + 1) * 4, hipMemcpyDeviceToHost));
-    if (perm) HIPCHK(c, hipMemcpy(perm, c->ws[W_PERM].p, n * 4, hipMemcpyDeviceToHost));
-    if (logits)
-        HIPCHK(c, hipMemcpy(logits, c->ws[W_LOGITS].p, (size_t)c->last_T * D.n_expert * 4, hipMemcpyDeviceToHost));
+    const std::vector<Buf>& ws = last_ws(c);
+    if (ids) HIPCHK(c, hipMemcpy(ids, ws[W_IDS].p, n * 4, hipMemcpyDeviceToHost));
+    if (weights) HIPCHK(c, hipMemcpy(weights, ws[W_W].p, n * 4, hipMemcpyDeviceToHost));
+    if (offsets) HIPCHK(c, hipMemcpy(offsets, ws[W_OFF].p, (size_t)(D.n_expert + 1) * 4, hipMemcpyDeviceToHost));
+    if (perm) HIPCHK(c, hipMemcpy(perm, ws[W_PERM].p, n * 4, hipMemcpyDeviceToHost));
+    if (logits) HIPCHK(c, hipMemcpy(logits, ws[W_LOGITS].p, (size_t)c->last_T * D.n_expert * 4, hipMemcpyDeviceToHost));
     return PHX_OK;
 }
 
@@ -990,9 +1089,10 @@ int phx_moe_get_intermediates(phx_moe_ctx* c, float* g, float* u, float* yd)
     const phx_moe_layer_desc& D = c->layers[c->last_layer].desc;
     const size_t n = (size_t)c->last_T * D.n_used;
     HIPCHK(c, hipStreamSynchronize(c->stream));
-    if (g) HIPCHK(c, hipMemcpy(g, c->ws[W_G].p, n * D.n_ff * 4, hipMemcpyDeviceToHost));
-    if (u) HIPCHK(c, hipMemcpy(u, c->ws[W_U].p, n * D.n_ff * 4, hipMemcpyDeviceToHost));
-    if (yd) HIPCHK(c, hipMemcpy(yd, c->ws[W_YD].p, n * D.d * 4, hipMemcpyDeviceToHost));
+    const std::vector<Buf>& ws = last_ws(c);
+    if (g) HIPCHK(c, hipMemcpy(g, ws[W_G].p, n * D.n_ff * 4, hipMemcpyDeviceToHost));
+    if (u) HIPCHK(c, hipMemcpy(u, ws[W_U].p, n * D.n_ff * 4, hipMemcpyDeviceToHost));
+    if (yd) HIPCHK(c, hipMemcpy(yd, ws[W_YD].p, n * D.d * 4, hipMemcpyDeviceToHost));
     return PHX_OK;
 }
 
@@ -1101,6 +1201,7 @@ int phx_moe_stack_run(phx_moe_ctx* c, float* x, int T, unsigned flags)
     HIPCHK(c, hipMemcpyAsync(x, xs, bytes, dev ? hipMemcpyDeviceToDevice : hipMemcpyDeviceToHost, c->stream));
     c->last_T = T;
     c->last_layer = c->graph_first + c->graph_n - 1;
+    c->last_scratch = false;
     if (c->profiling && !c->graph_timing.empty()) {
         // a stack captured while profiling: this replay's kernel intervals, read before the next one
         HIPCHK(c, hipStreamSynchronize(c->stream));

@@ -109,6 +109,7 @@ def load_lib():
         "phx_moe_check_desc": (i32, [C.POINTER(LayerDesc)]),
         "phx_moe_layer_upload": (i32, [vp, i32, C.POINTER(LayerDesc)]),
         "phx_moe_ffn": (i32, [vp, i32, i32, vp, vp, vp, u32]),
+        "phx_moe_ffn_noalloc": (i32, [vp, i32, i32, vp, vp, vp, u32]),
         "phx_moe_get_routing": (i32, [vp, vp, vp, vp, vp, vp]),
         "phx_moe_get_intermediates": (i32, [vp, vp, vp, vp]),
         "phx_moe_stack_capture": (i32, [vp, i32, i32, i32]),
@@ -218,6 +219,11 @@ class MoeContext:
     def ffn_device(self, layer: int, T: int, x_ptr: int, shared_ptr, out_ptr: int, flags: int = 0):
         self._last_layer, self._last_T = layer, T
         self._check(self.lib.phx_moe_ffn(self.h, layer, T, x_ptr, shared_ptr, out_ptr, flags | PHX.FLAG_DEVICE_PTRS))
+
+    def ffn_noalloc_device(self, layer: int, T: int, x_ptr: int, shared_ptr, out_ptr: int, flags: int = 0):
+        """phx_moe_ffn_noalloc: ffn_device with the workspace in the library's fixed scratch array."""
+        self._last_layer, self._last_T = layer, T
+        self._check(self.lib.phx_moe_ffn_noalloc(self.h, layer, T, x_ptr, shared_ptr, out_ptr, flags))
 
     # the reference's three call sites
     def RecordMoe(self, layer: int, x: np.ndarray, shared: np.ndarray) -> np.ndarray:
