@@ -3,16 +3,19 @@
 
 Default workload: decode, T=1 token, d=2816, E=128 experts, top-8,
 expert ffn 704, Q4_0 experts plus the dense shared FFN (ffn 2112, Q4_0), synthetic N(0,0.02)
-weights.  One step = one MoE FFN layer applied to the T tokens.  The layer is placed in 8 distinct
-layer slots and the 8 layers are captured as one HIP graph (the reference replays one recorded
-command buffer per decode pass, src/GemmaGpu.cs:544-554); every replay starts from a different
-input, so the experts touched change from replay to replay and the 256 MB MALL cannot serve them.
+weights.  One step = one MoE FFN layer applied to the T tokens.  The layer is placed in up to 32
+distinct layer slots (as many as divide --steps, so exactly --steps layer steps are timed) and the
+slots are captured as one HIP graph (the reference replays one recorded command buffer per decode
+pass, src/GemmaGpu.cs:544-554); every replay starts from a different input, so the experts touched
+change from replay to replay and the 256 MB MALL cannot serve them.
 
 Prints one JSON line: value = tokens/s through the layer (inputs resident in HBM), a roofline
-object for the dominant kernel (the grouped gate|up product; its average duration from HIP timing
-events recorded around it in the same captured stack, replayed like the timed region) and the CPU
-baseline (the C restatement of the reference CPU path timed on this
-host's cores over a bounded sample).
+object for the dominant kernel (the grouped gate|up product: algorithmic bytes per launch over its
+average duration, each launch's execution interval stamped by HIP events on the library's stream,
+the interval a kernel-trace profiler reports), the CPU baseline (the C restatement of the reference
+CPU path timed on this host's cores over a bounded sample), and a `prefill` object for configs[2]
+(T=2048, Zipf routing) measured in the same run: tokens/s and the matrix-core utilisation of the
+grouped gate|up and down products.
 
 `--config quant` measures the ops either side of the layer instead (the activation quantizers, the
 residual norm-add with the quantized next input and the dense matvec): one JSON line of the same form
@@ -63,10 +66,31 @@ def expert_bytes(L) -> tuple[int, int]:
     return gu, dn
 
 
-def cpu_baseline(pkg, L, cfg_name, T, budget_s=12.0):
-    """The oracle (C restatement of GemmaCpu.MoeFfn, row-parallel like Parallel.For) on this host."""
+def host_cpu():
+    """(threads to use, description): every core this process may run on, capped by OMP_NUM_THREADS when
+    the environment sets it (the GPU boxes give a job a fixed share of the host)."""
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:
+        affinity = os.cpu_count() or 1
+    omp = os.environ.get("OMP_NUM_THREADS")
+    threads = min(affinity, int(omp)) if omp and omp.isdigit() and int(omp) > 0 else affinity
+    model = "unknown"
+    try:
+        for ln in Path("/proc/cpuinfo").read_text().splitlines():
+            if ln.startswith("model name"):
+                model = ln.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return threads, {"nproc": os.cpu_count(), "affinity_cores": affinity, "omp_num_threads": omp, "cpu_model": model}
+
+
+def cpu_baseline(pkg, L, cfg_name, budget_s=12.0):
+    """The oracle (C restatement of GemmaCpu.MoeFfn, row-parallel like Parallel.For) on this host, one token
+    at a time as the reference's CPU path runs (GemmaCpu.Prefill), over a bounded sample of the workload."""
     from oracle import oracle as orc
-    threads = min(16, os.cpu_count() or 1)
+    threads, host = host_cpu()
     S = pkg.synth
     pool = 1024  # distinct tokens; the sample cycles through them until the time budget is spent
     x = S.make_input(cfg_name, T=pool, seed=4242, name="cpu.x")
@@ -77,8 +101,61 @@ def cpu_baseline(pkg, L, cfg_name, T, budget_s=12.0):
         n += 1
     dt = time.perf_counter() - t0
     return {"value": round(n / dt, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"{n} tokens of {cfg_name} one at a time (as GemmaCpu.Prefill does), shared FFN included, "
-                      f"{dt:.1f} s, OpenMP over rows with {threads} threads"}
+            "sample": f"{n} tokens of {cfg_name} one at a time (as GemmaCpu.Prefill does)"
+                      + (", shared FFN included" if L.get("n_ff_shared") else "")
+                      + f", {dt:.1f} s, OpenMP over rows with {threads} threads", **host}
+
+
+def graph_slots(steps: int, max_slots: int) -> int:
+    """Layer slots of the replayed graph: the largest count <= max_slots that divides steps, so the timed
+    region is exactly `steps` layer steps of whole replays; if that is below 4, max_slots (the remainder
+    then runs as eager layer calls inside the timed region)."""
+    best = max(s for s in range(1, max_slots + 1) if steps % s == 0)
+    return best if best >= 4 else max_slots
+
+
+def decode_roofline(pkg, L, cfg_name, T, avg_experts, gu_ms):
+    S = pkg.synth
+    gu_b, _ = expert_bytes(L)
+    sh_gu_b = 2 * L["n_ff_shared"] * S.row_bytes(L["shared_type"], L["d"]) if L.get("n_ff_shared") else 0
+    gu_bytes = avg_experts * gu_b + sh_gu_b
+    achieved = gu_bytes / (gu_ms * 1e-3) / 1e9
+    tr = PMC_TRAFFIC.get((cfg_name, T, "gate_up"), (None, None))
+    return {
+        "bound": "hbm",
+        "kernel": "phx::k_dec_gu (grouped Q4_0 x Q8_0 gate|up row products, decode)" if L["gate_up_type"] == 2
+        else "phx::k_dec_gu (decode gate|up)",
+        "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+        "traffic": tr[0], "traffic_source": tr[1],
+        "bytes_per_launch": int(gu_bytes), "avg_launch_us": round(gu_ms * 1e3, 3),
+        "per_unit": f"{gu_b} B of gate|up weights per touched expert x {avg_experts:.2f} experts per launch"
+                    + (f" + {sh_gu_b} B of shared-FFN gate and up weights" if sh_gu_b else ""),
+    }
+
+
+def mfma_rates(L, T, gu_ms, dn_ms):
+    """Matrix-core rates of the grouped products: 2 flops per multiply-add of the routed experts' gate|up
+    (2 nf x d per assignment) and down (d x nf) products, against the dense fp16 peak (the operands are
+    exact integers in fp16)."""
+    n = T * L["n_used"]
+    gu_ops = 2.0 * n * 2 * L["n_ff"] * L["d"]
+    dn_ops = 2.0 * n * L["d"] * L["n_ff"]
+    gu_t, dn_t = gu_ops / (gu_ms * 1e-3) / 1e12, dn_ops / (dn_ms * 1e-3) / 1e12
+    return {"gate_up_tflops": round(gu_t, 2), "gate_up_frac_fp16_peak": round(gu_t / FP16_PEAK_TFLOPS, 4),
+            "gate_up_avg_us": round(gu_ms * 1e3, 2), "gate_up_flops_per_launch": int(gu_ops),
+            "down_tflops": round(dn_t, 2), "down_frac_fp16_peak": round(dn_t / FP16_PEAK_TFLOPS, 4),
+            "down_avg_us": round(dn_ms * 1e3, 2), "down_flops_per_launch": int(dn_ops)}
+
+
+def kernel_times(ctx, calls):
+    """Run `calls` (eager layer calls) with profiling on: every kernel's own execution interval, summed
+    per kind; returns {kind: (avg ms per launch, launches)}."""
+    ctx.profile(True)
+    calls()
+    ctx.sync()
+    prof = ctx.profile_read()
+    ctx.profile(False)
+    return {k: (v[0] / v[1], v[1]) for k, v in prof.items() if v[1]}
 
 
 def run_layer(args, pkg):
@@ -86,7 +163,8 @@ def run_layer(args, pkg):
     cfg_name = args.config
     cfg = S.CONFIGS[cfg_name]
     T = args.T or cfg["T"]
-    n_slots = args.layers or cfg.get("layers", 8)
+    steps = args.steps
+    n_slots = args.layers or graph_slots(steps, cfg.get("layers", 32))
     log(f"[bench] generating {cfg_name} layer ...")
     L = S.make_layer(cfg_name)
     ctx = pkg.MoeContext(0)
@@ -102,10 +180,12 @@ def run_layer(args, pkg):
     xbuf.upload(xs)
     obuf = ctx.alloc(T * d * 4)
     xstride = T * d * 4
+    RES_ASYNC = pkg.PHX.FLAG_RESIDUAL | pkg.PHX.FLAG_ASYNC
 
-    # ---- timed region: K layer steps = K / n_slots replays of the n_slots-layer graph
+    # ---- timed region: exactly `steps` layer steps: whole replays of the n_slots-layer graph, then any
+    # remainder as eager layer calls (each with the residual update the graph's layers apply)
     ctx.stack_capture(0, n_slots, T)
-    reps = max(1, (args.steps + n_slots - 1) // n_slots)
+    reps, rem = divmod(steps, n_slots)
     wreps = max(1, (args.warmup + n_slots - 1) // n_slots)
     for r in range(wreps):
         ctx.stack_run_device(xbuf.ptr + (r % NX) * xstride, T)
@@ -113,23 +193,22 @@ def run_layer(args, pkg):
     t0 = time.perf_counter()
     for r in range(reps):
         ctx.stack_run_device(xbuf.ptr + (r % NX) * xstride, T)
+    for s in range(rem):
+        ctx.ffn_device(s, T, xbuf.ptr + ((reps + s) % NX) * xstride, None, obuf.ptr, RES_ASYNC)
     ctx.sync()
     dt = time.perf_counter() - t0
-    steps = reps * n_slots
     ms_per_step = dt * 1e3 / steps
     tokens_s = T * steps / dt
 
-    # ---- per-kernel durations: the same stack captured again with HIP timing events recorded as graph
-    # nodes around each kernel (each interval runs from the previous node's end to the kernel's end,
-    # as a kernel-trace profiler reports graph kernels), read back after every replay
-    gu_b, dn_b = expert_bytes(L)
+    # ---- per-kernel durations: eager layer calls over the slots and inputs, every launch stamped with
+    # its own execution interval (hipExtLaunchKernel events on the library's stream)
     prof_steps = max(1, min(steps, args.prof_steps))
-    ctx.profile(True)
-    ctx.stack_capture(0, n_slots, T)
-    for r in range(max(1, prof_steps // n_slots)):
-        ctx.stack_run_device(xbuf.ptr + (r % NX) * xstride, T)
-    prof = ctx.profile_read()
-    ctx.profile(False)
+
+    def prof_calls():
+        for s in range(prof_steps):
+            ctx.ffn_device(s % n_slots, T, xbuf.ptr + (s % NX) * xstride, None, obuf.ptr, RES_ASYNC)
+
+    prof = kernel_times(ctx, prof_calls)
     # experts touched per step (the routing of each step read back)
     distinct = 0
     n_route = min(prof_steps, 64)
@@ -137,61 +216,35 @@ def run_layer(args, pkg):
         ctx.ffn_device(s % n_slots, T, xbuf.ptr + (s % NX) * xstride, None, obuf.ptr, pkg.PHX.FLAG_ASYNC)
         distinct += len(np.unique(ctx.routing()[0]))
     avg_experts = distinct / n_route
-    gu_ms = prof["gate_up"][0] / max(1, prof["gate_up"][1])
-    dn_ms = prof["down"][0] / max(1, prof["down"][1])
-    decode = prof["dispatch"][1] == 0  # the decode path has no separate dispatch launch
-    n = T * k
+    gu_ms, dn_ms = prof["gate_up"][0], prof["down"][0]
+    decode = "dispatch" not in prof  # the decode path has no separate dispatch launch
     mfma = (not decode and L["gate_up_type"] in (pkg.PHX.Q4_0, pkg.PHX.Q8_0)
-            and L["down_type"] in (pkg.PHX.Q4_0, pkg.PHX.Q8_0) and n >= 8 * E)
-    # the decode path's gate|up launch also computes the dense shared FFN's gate and up rows, and its
-    # down launch the shared down rows: their weights are part of those launches' algorithmic bytes
-    sh_gu_b = sh_dn_b = 0
+            and L["down_type"] in (pkg.PHX.Q4_0, pkg.PHX.Q8_0) and T * k >= 8 * E)
+    gu_b, dn_b = expert_bytes(L)
+    sh_bytes = 0
     if L.get("n_ff_shared"):
-        sh_gu_b = 2 * L["n_ff_shared"] * S.row_bytes(L["shared_type"], d)
-        sh_dn_b = d * S.row_bytes(L["shared_type"], L["n_ff_shared"])
-    sh_bytes = sh_gu_b + sh_dn_b
+        sh_bytes = 3 * L["n_ff_shared"] * S.row_bytes(L["shared_type"], d)
     layer_expert_bytes = avg_experts * (gu_b + dn_b)
     router_bytes = E * d * 4
-    if decode:
-        gu_bytes = avg_experts * gu_b + sh_gu_b
-        dn_bytes = avg_experts * dn_b + sh_dn_b
-        achieved = gu_bytes / (gu_ms * 1e-3) / 1e9
-        roofline = {
-            "bound": "hbm",
-            "kernel": "gate_up (grouped Q4_0 x Q8_0 row products, decode)" if L["gate_up_type"] == 2 else "gate_up (decode)",
-            "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": PMC_TRAFFIC.get((cfg_name, T, "gate_up"), (None, None))[0],
-            "traffic_source": PMC_TRAFFIC.get((cfg_name, T, "gate_up"), (None, None))[1],
-            "bytes_per_launch": int(gu_bytes), "avg_launch_us": round(gu_ms * 1e3, 3),
-            "per_unit": f"{gu_b} B of gate|up weights per touched expert x {avg_experts:.2f} experts per launch"
-                        + (f" + {sh_gu_b} B of shared-FFN gate and up weights" if sh_gu_b else ""),
-        }
-        down_rate = {"down_gbs": round(dn_bytes / (dn_ms * 1e-3) / 1e9, 1)}
-    elif mfma:
-        # multiply-adds of the routed experts' gate|up products (2 flops each), on fp16 MFMA: the
-        # weight and activation integers enter exactly as fp16, so the block sums are exact
-        ops = 2.0 * n * 2 * L["n_ff"] * d
-        achieved = ops / (gu_ms * 1e-3) / 1e12
-        roofline = {
-            "bound": "mfma", "kernel": "gate_up (grouped fp16 MFMA on exact integer operands: block sums, "
-                                       "scale products, reference float chain)",
-            "achieved": round(achieved, 2), "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(achieved / FP16_PEAK_TFLOPS, 4), "traffic": None,
-            "ops_per_launch": int(ops), "avg_launch_us": round(gu_ms * 1e3, 3),
-            "per_unit": f"2 x {2 * L['n_ff']} x {d} flops per assignment x {n} assignments per launch",
-        }
-        dn_ops = 2.0 * n * d * L["n_ff"]
-        down_rate = {"down_tflops": round(dn_ops / (dn_ms * 1e-3) / 1e12, 2)}
+    if mfma:
+        rates = mfma_rates(L, T, gu_ms, dn_ms)
+        roofline = {"bound": "mfma", "kernel": "phx::k_grouped_mfma gate|up (fp16 MFMA on exact integer operands: "
+                                               "block sums, scale products, reference float chain)",
+                    "achieved": rates["gate_up_tflops"], "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                    "frac": rates["gate_up_frac_fp16_peak"], "traffic": None,
+                    "ops_per_launch": rates["gate_up_flops_per_launch"], "avg_launch_us": rates["gate_up_avg_us"],
+                    "per_unit": f"2 x {2 * L['n_ff']} x {d} flops per assignment x {T * k} assignments per launch"}
+        down_rate = {"down_tflops": rates["down_tflops"]}
     else:
-        gu_bytes = avg_experts * gu_b
-        achieved = gu_bytes / (gu_ms * 1e-3) / 1e9
-        roofline = {
+        roofline = decode_roofline(pkg, L, cfg_name, T, avg_experts, gu_ms) if decode else {
             "bound": "hbm", "kernel": f"gate_up (grouped {qname(L['gate_up_type'])} row products, VALU)",
-            "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None, "bytes_per_launch": int(gu_bytes), "avg_launch_us": round(gu_ms * 1e3, 3),
-            "per_unit": f"{gu_b} B of gate|up weights per touched expert x {avg_experts:.2f} experts per launch",
-        }
-        down_rate = {"down_gbs": round(avg_experts * dn_b / (dn_ms * 1e-3) / 1e9, 1)}
+            "achieved": round(avg_experts * gu_b / (gu_ms * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(avg_experts * gu_b / (gu_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
+            "bytes_per_launch": int(avg_experts * gu_b), "avg_launch_us": round(gu_ms * 1e3, 3),
+            "per_unit": f"{gu_b} B of gate|up weights per touched expert x {avg_experts:.2f} experts per launch"}
+        dn_bytes = avg_experts * dn_b + (L["d"] * S.row_bytes(L["shared_type"], L["n_ff_shared"])
+                                         if decode and L.get("n_ff_shared") else 0)
+        down_rate = {"down_gbs": round(dn_bytes / (dn_ms * 1e-3) / 1e9, 1)}
 
     # ---- the same layer called with host buffers (the C# host's boundary: x and the output cross PCIe
     # inside every call, which also waits for completion); a side figure, never `value`
@@ -210,7 +263,7 @@ def run_layer(args, pkg):
     stream_gbs = (2 << 30) / (sread_ms * 1e-3) / 1e9
     sbuf.free()
 
-    kernels = {k_: {"avg_us": round(v[0] / max(1, v[1]) * 1e3, 2), "launches": v[1]} for k_, v in prof.items() if v[1]}
+    kernels = {k_: {"avg_us": round(v[0] * 1e3, 2), "launches": v[1]} for k_, v in prof.items()}
     line = {
         "metric": METRIC,
         "value": round(tokens_s, 2),
@@ -230,7 +283,8 @@ def run_layer(args, pkg):
                         + (f", shared FFN {L['n_ff_shared']} {qname(L['shared_type'])}" if sh_bytes else "")
                         + (", Zipf(1.1) router bias" if cfg.get("zipf") else "")
                         + (f", hot expert {cfg['hot']:.0%} of tokens" if cfg.get("hot") else "")
-                        + f"; {n_slots} layer slots replayed as one HIP graph, x varied per replay",
+                        + f"; {n_slots} layer slots replayed as one HIP graph ({reps} replays"
+                        + (f" + {rem} eager layer calls" if rem else "") + "), x varied per replay",
             "global_batch": T,
             "parallelism": "none (1 GPU)",
             "path": "decode" if decode else ("mfma" if mfma else "valu"),
@@ -245,20 +299,69 @@ def run_layer(args, pkg):
             "down_avg_us": round(dn_ms * 1e3, 3),
             **down_rate,
             "kernels": kernels,
+            "kernel_timing": f"{prof_steps} eager layer calls, each kernel's execution interval",
             "stream_read_gbs_measured": round(stream_gbs, 1),
             "pcie_inclusive": pcie,
         },
     }
     if args.calibrate:
         line["calibration"] = calibration_kernels(ctx)
+    ctx.close()
     if not args.no_cpu:
         log("[bench] CPU baseline ...")
-        line["cpu_baseline"] = cpu_baseline(pkg, L, cfg_name, T, args.cpu_seconds)
-    ctx.close()
+        line["cpu_baseline"] = cpu_baseline(pkg, L, cfg_name, args.cpu_seconds)
+    del L
+    if cfg_name == "c2_decode" and not args.no_prefill:
+        log("[bench] prefill (configs[2], T=2048) ...")
+        line["prefill"] = run_prefill(args, pkg)
     return line
 
 
-QUANT_MODES = {"plain": 0, "silu_mul": 1, "rms_norm": 2, "gelu_mul": 3}
+def run_prefill(args, pkg, cfg_name="c3_prefill"):
+    """configs[2] in the same run: T = 2048 tokens with Zipf(1.1) expert popularity through one layer,
+    eager (one call per step, inputs resident in HBM), the grouped products on the matrix cores."""
+    S = pkg.synth
+    cfg = S.CONFIGS[cfg_name]
+    T = cfg["T"]
+    L = S.make_layer(cfg_name)
+    ctx = pkg.MoeContext(0)
+    ctx.upload(0, L)
+    NX = 4
+    xs = S.normal(cfg["idx"] + 7000, "bench.x", (NX, T, L["d"]))
+    xs[:, :, -1] = S.BIAS_X
+    xbuf = ctx.alloc(xs.nbytes)
+    xbuf.upload(xs)
+    obuf = ctx.alloc(T * L["d"] * 4)
+    xstride = T * L["d"] * 4
+    steps = args.prefill_steps
+    for s in range(3):
+        ctx.ffn_device(0, T, xbuf.ptr + (s % NX) * xstride, None, obuf.ptr, pkg.PHX.FLAG_ASYNC)
+    ctx.sync()
+    t0 = time.perf_counter()
+    for s in range(steps):
+        ctx.ffn_device(0, T, xbuf.ptr + (s % NX) * xstride, None, obuf.ptr, pkg.PHX.FLAG_ASYNC)
+    ctx.sync()
+    dt = time.perf_counter() - t0
+
+    def calls():
+        for s in range(steps):
+            ctx.ffn_device(0, T, xbuf.ptr + (s % NX) * xstride, None, obuf.ptr, pkg.PHX.FLAG_ASYNC)
+
+    prof = kernel_times(ctx, calls)
+    ids = ctx.routing()[0]
+    cnt = np.bincount(ids.ravel(), minlength=L["n_expert"])
+    ctx.close()
+    out = {"workload": f"{cfg_name}: T={T}, d={L['d']}, E={L['n_expert']}, top-{L['n_used']}, expert ffn {L['n_ff']}, "
+                       f"Q4_0, Zipf(1.1) router bias; {steps} eager layer calls, inputs in HBM",
+           "tokens_s": round(T * steps / dt, 1), "ms_per_step": round(dt * 1e3 / steps, 4), "steps": steps,
+           **mfma_rates(L, T, prof["gate_up"][0], prof["down"][0]),
+           "kernels": {k_: {"avg_us": round(v[0] * 1e3, 2), "launches": v[1]} for k_, v in prof.items()},
+           "kernel_timing": f"{steps} eager layer calls, each kernel's execution interval",
+           "assignments_per_expert": {"max": int(cnt.max()), "empty_experts": int((cnt == 0).sum())}}
+    if not args.no_cpu:
+        log("[bench] prefill CPU baseline ...")
+        out["cpu_baseline"] = cpu_baseline(pkg, L, cfg_name, min(args.cpu_seconds, 6.0))
+    return out
 
 
 def run_quant(args, pkg):
@@ -404,16 +507,19 @@ def qname(t):
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=4000, help="layer steps timed (rounded up to whole graph replays)")
+    ap.add_argument("--steps", type=int, default=4000, help="layer steps timed (exactly this many)")
     ap.add_argument("--warmup", type=int, default=400)
     ap.add_argument("--config", default="c2_decode")
     ap.add_argument("--T", type=int, default=0)
     ap.add_argument("--layers", type=int, default=0,
-                    help="layer slots in the replayed graph (default 8, or the config's stack depth)")
+                    help="layer slots in the replayed graph (default: the largest count <= 32, or <= the "
+                         "config's stack depth, that divides --steps)")
     ap.add_argument("--prof-steps", type=int, default=200)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--calibrate", action="store_true", help="also run the PMC calibration kernels")
+    ap.add_argument("--no-prefill", action="store_true", help="leave out the prefill object of the default run")
+    ap.add_argument("--prefill-steps", type=int, default=40, help="timed C3 layer calls of the prefill object")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(f"bench.py: this build runs on one GPU only (the MoE path shards by experts across GPUs by design, "
