@@ -8,11 +8,14 @@ mirroring the three MoE call sites of the reference's ``GemmaGpu``:
 * ``RecordFfnMoe``   (src/GemmaGpu.cs:683-704): one token, dense shared FFN computed on the GPU
 * ``RecordMoeRows``  (src/GemmaGpu.cs:850-882): T prompt rows
 
+``gguf`` reads real models (GgufFile.Open and the MoE part of GemmaConfig.FromGguf).
+
 There is no CPU fallback: loading fails loudly when the HIP library is missing.
 """
 from .moe import (  # noqa: F401
     ArgumentError,
     GpuDeviceLostError,
+    InvalidDataError,
     MoeContext,
     MoeError,
     NotSupportedError,
@@ -21,4 +24,4 @@ from .moe import (  # noqa: F401
     lib_path,
     load_lib,
 )
-from . import synth  # noqa: F401
+from . import gguf, synth  # noqa: F401

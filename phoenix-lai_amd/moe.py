@@ -16,7 +16,7 @@ _HERE = Path(__file__).resolve().parent
 
 
 class PHX:
-    OK, ERR_ARG, ERR_OOM, ERR_UNSUPPORTED, ERR_DEVICE_LOST, ERR_HIP = 0, -1, -2, -3, -4, -5
+    OK, ERR_ARG, ERR_OOM, ERR_UNSUPPORTED, ERR_DEVICE_LOST, ERR_HIP, ERR_FORMAT = 0, -1, -2, -3, -4, -5, -6
     F32, Q4_0, Q8_0, Q4_K, Q6_K = 0, 2, 8, 12, 14
     WEIGHTS_SOFTMAX, WEIGHTS_CPUREF = 0, 1
     FLAG_DEVICE_PTRS, FLAG_ASYNC, FLAG_RESIDUAL, FLAG_EXACT_ROUTER = 1, 2, 4, 8
@@ -44,6 +44,10 @@ class GpuDeviceLostError(MoeError):
     pass
 
 
+class InvalidDataError(MoeError, ValueError):
+    """A malformed GGUF file (InvalidDataException in the reference, src/Gguf.cs:116-210)."""
+
+
 def _raise(code: int, msg: str):
     if code == PHX.ERR_ARG:
         raise ArgumentError(code, msg)
@@ -51,6 +55,8 @@ def _raise(code: int, msg: str):
         raise NotSupportedError(code, msg)
     if code == PHX.ERR_DEVICE_LOST:
         raise GpuDeviceLostError(code, msg)
+    if code == PHX.ERR_FORMAT:
+        raise InvalidDataError(code, msg)
     raise MoeError(code, msg)
 
 

@@ -12,6 +12,7 @@ import pytest
 
 ROOT = Path(__file__).resolve().parent.parent
 HEADER = ROOT / "include" / "phx_moe.h"
+HEADERS = sorted((ROOT / "include").glob("*.h"))
 
 
 def _strip_comments(src: str) -> str:
@@ -20,14 +21,17 @@ def _strip_comments(src: str) -> str:
 
 
 def declared_functions() -> list[str]:
-    src = _strip_comments(HEADER.read_text())
-    return sorted(set(re.findall(r"\b(phx_\w+)\s*\(", src)))
+    names = set()
+    for h in HEADERS:
+        names |= set(re.findall(r"\b(phx_\w+)\s*\(", _strip_comments(h.read_text())))
+    return sorted(names)
 
 
 def header_defines() -> dict[str, int]:
     out = {}
-    for name, val in re.findall(r"#define\s+(PHX_\w+)\s+\(?(-?\d+)u?\)?", HEADER.read_text()):
-        out[name] = int(val)
+    for h in HEADERS:
+        for name, val in re.findall(r"#define\s+(PHX_\w+)\s+\(?(-?\d+)u?\)?", h.read_text()):
+            out[name] = int(val)
     return out
 
 
@@ -45,17 +49,34 @@ def test_every_declared_function_is_exported(pkg):
 
 def test_python_binding_covers_the_header(pkg):
     import inspect
-    src = inspect.getsource(pkg.moe.load_lib)
+    src = inspect.getsource(pkg.moe.load_lib) + inspect.getsource(pkg.gguf._lib)
     for n in declared_functions():
-        assert f'"{n}"' in src, f"{n} has no ctypes signature in moe.load_lib"
+        assert f'"{n}"' in src, f"{n} has no ctypes signature in moe.load_lib or gguf._lib"
 
 
+@pytest.mark.parametrize("header", [h.name for h in HEADERS])
 @pytest.mark.parametrize("compiler,std", [("gcc", "-std=c99"), ("g++", "-std=c++11")])
-def test_header_compiles_standalone(tmp_path, compiler, std):
+def test_header_compiles_standalone(tmp_path, compiler, std, header):
     src = tmp_path / ("t.c" if compiler == "gcc" else "t.cc")
-    src.write_text('#include "phx_moe.h"\nint main(void) { return PHX_OK; }\n')
+    src.write_text(f'#include "{header}"\nint main(void) {{ return PHX_OK; }}\n')
     subprocess.run([compiler, std, "-Wall", "-Werror", "-pedantic", "-fsyntax-only", f"-I{HEADER.parent}", str(src)],
                    check=True)
+
+
+@pytest.mark.parametrize("struct,cname", [("TensorInfo", "phx_gguf_tensor"), ("ModelConfig", "phx_moe_model_config")])
+def test_gguf_struct_layouts_match_c(tmp_path, pkg, struct, cname):
+    S = getattr(pkg.gguf, struct)
+    fields = [f for f, _ in S._fields_]
+    prog = ['#include <stdio.h>', '#include <stddef.h>', '#include "phx_gguf.h"', "int main(void) {",
+            f'  printf("%zu\\n", sizeof({cname}));']
+    prog += [f'  printf("%zu\\n", offsetof({cname}, {f}));' for f in fields]
+    prog += ["  return 0;", "}"]
+    (tmp_path / "g.c").write_text("\n".join(prog))
+    exe = tmp_path / "g"
+    subprocess.run(["gcc", "-std=c99", f"-I{HEADER.parent}", "-o", str(exe), str(tmp_path / "g.c")], check=True)
+    vals = [int(v) for v in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    assert vals[0] == C.sizeof(S)
+    assert vals[1:] == [getattr(S, f).offset for f in fields]
 
 
 def test_descriptor_layout_matches_c(tmp_path, pkg):
@@ -77,7 +98,8 @@ def test_constants_match_python_mirror(pkg):
     P = pkg.PHX
     d = header_defines()
     assert (d["PHX_OK"], d["PHX_ERR_ARG"], d["PHX_ERR_OOM"], d["PHX_ERR_UNSUPPORTED"], d["PHX_ERR_DEVICE_LOST"],
-            d["PHX_ERR_HIP"]) == (P.OK, P.ERR_ARG, P.ERR_OOM, P.ERR_UNSUPPORTED, P.ERR_DEVICE_LOST, P.ERR_HIP)
+            d["PHX_ERR_HIP"], d["PHX_ERR_FORMAT"]) == (P.OK, P.ERR_ARG, P.ERR_OOM, P.ERR_UNSUPPORTED, P.ERR_DEVICE_LOST,
+                                                   P.ERR_HIP, P.ERR_FORMAT)
     assert (d["PHX_F32"], d["PHX_Q4_0"], d["PHX_Q8_0"], d["PHX_Q4_K"], d["PHX_Q6_K"]) == (P.F32, P.Q4_0, P.Q8_0,
                                                                                        P.Q4_K, P.Q6_K)
     assert (d["PHX_MAX_EXPERTS"], d["PHX_MAX_USED"]) == (P.MAX_EXPERTS, P.MAX_USED)

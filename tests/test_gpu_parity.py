@@ -39,15 +39,15 @@ def within(gpu, ref):
     return bool(ok.all()), float(np.max(np.where(np.isnan(err), np.inf, err), initial=0.0))
 
 
-def check_layer(ctx, orc, L, x, shared=None, tag="", exact=False):
+def check_layer(ctx, orc, L, x, shared=None, tag="", exact=False, layer=0):
     """Run one layer on the GPU and compare every stage with the oracle.
 
-    exact=True forces the router that replays the reference's float sums: then logits, weights and
-    outputs are compared bit for bit too.  Otherwise (the decode path's certified router for T <= 16)
+    layer: the uploaded slot that holds L.  exact=True forces the router that replays the reference's
+    float sums: then logits, weights and outputs are compared bit for bit too.  Otherwise (the decode path's certified router for T <= 16)
     ids and lists are bit-exact, logits agree within the router's error bound and weights/outputs
     within the tolerance; gate/up/down products are bit-exact on both paths."""
     T = x.shape[0]
-    out = ctx.ffn(0, x, shared, exact_router=exact)
+    out = ctx.ffn(layer, x, shared, exact_router=exact)
     ids, w, off, perm, logits = ctx.routing()
     g, u, yd = ctx.intermediates()
     k = L["n_used"]
