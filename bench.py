@@ -364,6 +364,9 @@ def run_prefill(args, pkg, cfg_name="c3_prefill"):
     return out
 
 
+QUANT_MODES = {"plain": 0, "silu_mul": 1, "rms_norm": 2, "gelu_mul": 3}
+
+
 def run_quant(args, pkg):
     """The standalone activation quantizers (phx_quant_q8_0 / phx_quant_q8_k, KernelsQuant.Q80 / Q8K)
     at the C3 prefill shapes: gelu(g) * u of 2048 x 8 assignment rows of 704 into Q8_0 (the
@@ -458,6 +461,30 @@ def run_quant(args, pkg):
         modes[f"matvec_{qname(wtype)}_{rows}x{cols}"] = {"us": round(u, 2), "gbs": round(wb.nbytes / u / 1e3, 1)}
         for buf in (wb, xq, xd, y):
             buf.free()
+    for wtype, rows, cols in ((2, 2112, 2816), (2, 2816, 2112), (8, 2112, 2816)):  # prefill dense matmul, T = 2048
+        T = 2048
+        bb = 18 if wtype == 2 else 34
+        blocks = rng.integers(0, 256, (rows * cols // 32, bb), dtype=np.uint8)
+        blocks[:, :2] = (rng.standard_normal(rows * cols // 32) * 0.01).astype(np.float16).view(np.uint8).reshape(-1, 2)
+        h = ctx.weight_upload(wtype, blocks.reshape(-1), rows, cols)
+        xq, xd, y = ctx.alloc(T * cols), ctx.alloc(T * cols // 16), ctx.alloc(T * rows * 4)
+        xq.upload(rng.integers(-127, 128, T * cols, dtype=np.int8))
+        xd.upload(np.full(T * cols // 32, 0x2C00, np.uint16))
+        run = lambda: ctx.matmul_device(h, T, xq.ptr, xd.ptr, y.ptr)
+        for _ in range(3):
+            run()
+        ctx.sync()
+        t0 = time.perf_counter()
+        for _ in range(max(10, iters // 4)):
+            run()
+        ctx.sync()
+        u = (time.perf_counter() - t0) / max(10, iters // 4) * 1e6
+        tflops = 2.0 * T * rows * cols / (u * 1e-6) / 1e12
+        modes[f"matmul_{qname(wtype)}_{rows}x{cols}_T{T}"] = {
+            "us": round(u, 2), "tflops": round(tflops, 1), "frac_fp16_peak": round(tflops / FP16_PEAK_TFLOPS, 4)}
+        for buf in (xq, xd, y):
+            buf.free()
+        ctx.weight_free(h)
     line = {"metric": "activation quantizer GB/s (algorithmic bytes) vs HBM peak", "value": round(gbs, 1),
             "unit": "GB/s", "n_gpus": 1, "steps": iters, "warmup": max(3, args.warmup // 100),
             "ms_per_step": round(us / 1e3, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,

@@ -246,6 +246,20 @@ int phx_norm_add(phx_moe_ctx* ctx, float* x, const float* y, const float* w, int
 int phx_matvec(phx_moe_ctx* ctx, int type, const void* w, int rows, int cols, int T, const int8_t* xq,
                const uint16_t* xd, float* y);
 
+/* Prefill matmul of a dense quantized matrix over T token rows: KernelsPrefill.MatMulQ4Q8Tile as
+ * GemmaGpu.Mm records it (src/KernelsPrefill.cs:143-260, src/GemmaGpu.cs:907-923) for the shared FFN
+ * and every other dense projection of a prompt chunk.  phx_weight_upload repacks `rows` GGUF rows of
+ * `cols` (PHX_Q4_0 or PHX_Q8_0, host memory, as the file holds them) into the device's row groups once
+ * (GemmaGpu.UploadW, src/GemmaGpu.cs:344-352); phx_weight_free releases them.  phx_matmul: xq / xd are
+ * T Q8_0 rows in the layout of phx_quant_q8_0 (device pointers, xq 4-byte aligned) and
+ * y[t][r] = CpuRef.MatVec's value for token t (src/CpuRef.cs:91-119, src/CpuRefGemma.cs:12-40: the block
+ * terms (float)isum * (d_w * d_x) added in block order), on the matrix cores for T >= 32;
+ * asynchronous on the context's stream.  cols a multiple of 32, at most 16384. */
+typedef struct phx_weight phx_weight;
+int phx_weight_upload(phx_moe_ctx* ctx, int type, int rows, int cols, const void* gguf_rows, phx_weight** out);
+void phx_weight_free(phx_moe_ctx* ctx, phx_weight* w);
+int phx_matmul(phx_moe_ctx* ctx, const phx_weight* w, int T, const int8_t* xq, const uint16_t* xd, float* y);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1120,6 +1120,46 @@ void launch_stream_copy(hipStream_t st, void* dst, const void* src, int64_t byte
     launch(k_stream_copy, dim3(256 * 8), dim3(256), 0, st, (uint4*)dst, (const uint4*)src, bytes / 16);
 }
 
+// Planar Q8_0 rows (qs int8 [rows][n] and fp16 scale bits [rows][n/32], the layout phx_quant_q8_0
+// writes) into the grouped kernels' activation arrays: each block's scale as a float, the sum of its
+// integers (the Q4_0 offset term of the VALU kernels) and, when a.qh is set, the integers as exact
+// fp16 (the matrix-core operands).  An 8-lane group per block, four integers per lane.
+__global__ __launch_bounds__(256) void k_planar_act(int64_t nblk, int nb, const int8_t* __restrict__ qs,
+                                                    const uint16_t* __restrict__ d, Act a)
+{
+    const int64_t g = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 3;
+    const int l8 = threadIdx.x & 7;
+    const bool ok = g < nblk;
+    const int64_t gc = ok ? g : nblk - 1;  // every lane takes part in the group's shuffles
+    const uint32_t w = ((const uint32_t*)qs)[gc * 8 + l8];
+    const int q0 = (int8_t)(w & 0xFF), q1 = (int8_t)((w >> 8) & 0xFF), q2 = (int8_t)((w >> 16) & 0xFF),
+              q3 = (int8_t)(w >> 24);
+    int sm = q0 + q1 + q2 + q3;
+    sm += __shfl_xor(sm, 1, 64);
+    sm += __shfl_xor(sm, 2, 64);
+    sm += __shfl_xor(sm, 4, 64);
+    if (!ok) return;
+    const int64_t t = g / nb;
+    const int b = (int)(g - t * nb);
+    if (l8 == 0) {
+        a.d[t * a.dstride + b] = h2f(d[g]);
+        a.s[t * a.sstride + b] = sm;
+    }
+    if (a.qh) {
+        const uint32_t h01 = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)q0) |
+                             ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)q1) << 16);
+        const uint32_t h23 = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)q2) |
+                             ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)q3) << 16);
+        *(uint2*)(a.qh + t * a.qhstride + b * 32 + 4 * l8) = make_uint2(h01, h23);
+    }
+}
+
+void launch_planar_act(hipStream_t st, int rows, int n, const int8_t* qs, const uint16_t* d, Act a)
+{
+    const int64_t nblk = (int64_t)rows * (n / 32);
+    launch(k_planar_act, dim3((unsigned)((nblk * 8 + 255) / 256)), dim3(256), 0, st, nblk, n / 32, qs, d, a);
+}
+
 // Fill n 32-bit words with v: clears workspace that must start at zero with a kernel rather than a
 // memset node, so the enqueued work stays a plain kernel when a caller captures it into a graph.
 __global__ __launch_bounds__(256) void k_fill_u32(uint32_t* __restrict__ p, int64_t n, uint32_t v)

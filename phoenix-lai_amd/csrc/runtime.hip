@@ -329,7 +329,8 @@ int hip_code(hipError_t e)
 enum WsId {
     W_X, W_SHARED, W_OUT, W_RIN, W_XSCALE, W_AGU_Q, W_AGU_D, W_AGU_S, W_ASH_Q, W_ASH_D, W_ASH_S, W_LOGITS, W_IDS, W_W,
     W_OFF, W_PERM, W_TILES, W_NTILES, W_G, W_U, W_ADN_Q, W_ADN_D, W_ADN_S, W_YD, W_SHG, W_SHU, W_ASD_Q, W_ASD_D,
-    W_ASD_S, W_SHOUT, W_ZERO, W_STILES, W_SNTILES, W_SOFF, W_SPERM, W_LB, W_BB, W_ADEC, W_SDEC, W_AGUP, W_ASHP, W_AGU_H, W_ADN_H, W_ASH_H, W_ASD_H, W_X2, W_COUNT
+    W_ASD_S, W_SHOUT, W_ZERO, W_STILES, W_SNTILES, W_SOFF, W_SPERM, W_LB, W_BB, W_ADEC, W_SDEC, W_AGUP, W_ASHP, W_AGU_H, W_ADN_H, W_ASH_H, W_ASD_H, W_X2,
+    W_MM_IDS, W_MM_OFF, W_MM_PERM, W_MM_TILES, W_MM_NT, W_MM_D, W_MM_S, W_MM_H, W_COUNT
 };
 
 int ensure(phx_moe_ctx* c, int id, size_t bytes)
@@ -813,6 +814,13 @@ int drain_profile(phx_moe_ctx* c)
 }
 
 }  // namespace
+
+// One dense quantized matrix on the device (GemmaGpu's GW, src/GemmaGpu.cs:344-352), repacked into row
+// groups like the experts, for phx_matmul.
+struct phx_weight {
+    QMat q;
+    int type = 0, rows = 0, cols = 0;
+};
 
 // Workspace of phx_moe_ffn_noalloc: one array per device, which each GPU the library runs on holds
 // until the process ends.  In host code the name is only a stand-in, never a device address: the
@@ -1399,6 +1407,95 @@ int phx_norm_add(phx_moe_ctx* c, float* x, const float* y, const float* w, int r
         return set_err(c, PHX_ERR_ARG, "norm_add: x, y, w, w2 need 16-byte, qs 4-byte alignment");
     HIPCHK(c, hipSetDevice(c->device));
     launch_norm_add(c->stream, rows, n, eps, s, x, y, w, w2, w2 ? qs : nullptr, w2 ? d : nullptr, c->flags);
+    HIPCHK(c, hipGetLastError());
+    return PHX_OK;
+}
+
+int phx_weight_upload(phx_moe_ctx* c, int type, int rows, int cols, const void* src, phx_weight** out)
+{
+    if (!c || !out) return PHX_ERR_ARG;
+    *out = nullptr;
+    if (type != PHX_Q4_0 && type != PHX_Q8_0)
+        return set_err(c, PHX_ERR_UNSUPPORTED, "weight upload: type %d (Q4_0 and Q8_0 only)", type);
+    if (rows <= 0 || cols <= 0 || cols % 32 || cols > 16384 || !src)
+        return set_err(c, PHX_ERR_ARG, "weight upload: shape %d x %d (cols a multiple of 32, <= 16384)", rows, cols);
+    HIPCHK(c, hipSetDevice(c->device));
+    HIPCHK(c, hipStreamSynchronize(c->stream));
+    phx_weight* w = new phx_weight();
+    w->type = type;
+    w->rows = rows;
+    w->cols = cols;
+    const int rc = upload_q(c, type, src, 1, rows, cols, w->q, false);
+    if (rc) {
+        free_qmat(w->q);
+        delete w;
+        return rc;
+    }
+    *out = w;
+    return PHX_OK;
+}
+
+void phx_weight_free(phx_moe_ctx* c, phx_weight* w)
+{
+    if (!w) return;
+    if (c) {
+        (void)hipSetDevice(c->device);
+        (void)hipStreamSynchronize(c->stream);
+    }
+    free_qmat(w->q);
+    delete w;
+}
+
+int phx_matmul(phx_moe_ctx* c, const phx_weight* w, int T, const int8_t* xq, const uint16_t* xd, float* y)
+{
+    if (!c) return PHX_ERR_ARG;
+    if (!w || !xq || !xd || !y) return set_err(c, PHX_ERR_ARG, "matmul: null argument");
+    if (T <= 0 || T > 65535) return set_err(c, PHX_ERR_ARG, "matmul: T=%d out of range", T);
+    if ((uintptr_t)xq % 4 || (uintptr_t)xd % 2 || (uintptr_t)y % 4)
+        return set_err(c, PHX_ERR_ARG, "matmul: xq needs 4-byte, xd 2-byte, y 4-byte alignment");
+    HIPCHK(c, hipSetDevice(c->device));
+    const int nb = w->cols / 32;
+    // many tokens: the matrix cores on the integers as exact fp16; a few: the VALU row walk
+    const bool mma = T >= 32;
+    const int A = mma ? kMmaTile : kTileA;
+    const int max_tiles = (T + A - 1) / A;
+    int rc;
+#define ENS(id, bytes) \
+    if ((rc = ensure(c, id, (size_t)(bytes)))) return rc
+    ENS(W_MM_IDS, (size_t)T * 4);
+    ENS(W_MM_OFF, 8);
+    ENS(W_MM_PERM, (size_t)T * 4);
+    ENS(W_MM_TILES, (size_t)max_tiles * sizeof(Tile));
+    ENS(W_MM_NT, 4);
+    ENS(W_MM_D, (size_t)T * nb * 4);
+    ENS(W_MM_S, (size_t)T * nb * 4);
+    if (mma) ENS(W_MM_H, (size_t)T * w->cols * 2);
+#undef ENS
+    hipStream_t st = c->stream;
+    Act a;
+    a.fmt = ACT_Q8_0;
+    a.cols = w->cols;
+    a.q = (int8_t*)xq;
+    a.qstride = w->cols;
+    a.d = wp<float>(c, W_MM_D);
+    a.dstride = nb;
+    a.s = wp<int>(c, W_MM_S);
+    a.sstride = nb;
+    if (mma) {
+        a.qh = wp<uint16_t>(c, W_MM_H);
+        a.qhstride = w->cols;
+    }
+    launch_planar_act(st, T, w->cols, xq, xd, a);
+    // every token is an assignment of the one matrix: the stable dispatch gives the identity list
+    launch_fill_u32(st, (uint32_t*)wp<int>(c, W_MM_IDS), T, 0u);
+    launch_dispatch(st, T, 1, A, wp<int>(c, W_MM_IDS), wp<int>(c, W_MM_OFF), wp<int>(c, W_MM_PERM),
+                    wp<Tile>(c, W_MM_TILES), wp<int>(c, W_MM_NT));
+    if (mma)
+        launch_grouped_mfma(st, w->q, a, wp<Tile>(c, W_MM_TILES), wp<int>(c, W_MM_NT), max_tiles, wp<int>(c, W_MM_PERM), 1,
+                            y, y, w->rows, w->rows, 0, nullptr, 0, nullptr);
+    else
+        launch_grouped(st, w->q, a, wp<Tile>(c, W_MM_TILES), wp<int>(c, W_MM_NT), max_tiles, A, wp<int>(c, W_MM_PERM), 1,
+                       y, y, w->rows, w->rows);
     HIPCHK(c, hipGetLastError());
     return PHX_OK;
 }

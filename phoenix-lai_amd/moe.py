@@ -136,6 +136,9 @@ def load_lib():
         "phx_quant_q8_k": (i32, [vp, i32, vp, vp, i32, i32, C.c_float, vp, vp, vp]),
         "phx_norm_add": (i32, [vp, vp, vp, vp, i32, i32, C.c_float, C.c_float, vp, vp, vp]),
         "phx_matvec": (i32, [vp, i32, vp, i32, i32, i32, vp, vp, vp]),
+        "phx_weight_upload": (i32, [vp, i32, i32, i32, vp, C.POINTER(vp)]),
+        "phx_weight_free": (None, [vp, vp]),
+        "phx_matmul": (i32, [vp, vp, i32, vp, vp, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -158,12 +161,14 @@ class DeviceBuffer:
 
     def upload(self, arr: np.ndarray):
         arr = np.ascontiguousarray(arr)
-        assert arr.nbytes <= self.nbytes
+        if arr.nbytes > self.nbytes:
+            raise ArgumentError(PHX.ERR_ARG, f"upload of {arr.nbytes} bytes into a {self.nbytes}-byte buffer")
         self.ctx._check(self.ctx.lib.phx_moe_memcpy_h2d(self.ctx.h, self.ptr, arr.ctypes.data, arr.nbytes))
 
     def download(self, shape, dtype=np.float32) -> np.ndarray:
         out = np.empty(shape, dtype=dtype)
-        assert out.nbytes <= self.nbytes
+        if out.nbytes > self.nbytes:
+            raise ArgumentError(PHX.ERR_ARG, f"download of {out.nbytes} bytes from a {self.nbytes}-byte buffer")
         self.ctx._check(self.ctx.lib.phx_moe_memcpy_d2h(self.ctx.h, out.ctypes.data, self.ptr, out.nbytes))
         return out
 
@@ -374,8 +379,11 @@ class MoeContext:
         x = _f32(x)
         x2 = x.reshape(1, -1) if x.ndim == 1 else x
         rows, n = x2.shape
+        y, w = _f32(y), _f32(w)
+        if y.size != x2.size or w.size != n or (w2 is not None and _f32(w2).size != n):
+            raise ArgumentError(PHX.ERR_ARG, f"norm_add: y has {y.size}, w {w.size} values for {rows} rows of {n}")
         bufs = [self.alloc(x2.nbytes), self.alloc(x2.nbytes), self.alloc(n * 4)]
-        for b, a in zip(bufs, (x2, _f32(y), _f32(w))):
+        for b, a in zip(bufs, (x2, y, w)):
             b.upload(a)
         if w2 is not None:
             bufs += [self.alloc(n * 4), self.alloc(rows * n), self.alloc(rows * n // 32 * 2)]
@@ -400,8 +408,15 @@ class MoeContext:
         """GemmaGpu.MatVec for Q4_0 / Q8_0 weights (src/GemmaGpu.cs:463-476) on host arrays: w the GGUF rows
         (bytes), xq / xd the Q8_0 input rows as Q80 returns them; y [T][rows] f32."""
         w = np.ascontiguousarray(w, dtype=np.uint8)
-        xq = np.ascontiguousarray(xq, dtype=np.int8).reshape(-1, cols)
-        xd = np.ascontiguousarray(xd, dtype=np.uint16).reshape(xq.shape[0], cols // 32)
+        bb = {PHX.Q4_0: 18, PHX.Q8_0: 34}.get(wtype)
+        if bb is not None and (cols % 32 or w.size != rows * (cols // 32) * bb):
+            raise ArgumentError(PHX.ERR_ARG, f"weight bytes {w.size} != {rows} rows x {cols // 32} blocks x {bb}")
+        xq = np.ascontiguousarray(xq, dtype=np.int8)
+        xd = np.ascontiguousarray(xd, dtype=np.uint16)
+        if cols <= 0 or xq.size % cols or xd.size * 32 != xq.size:
+            raise ArgumentError(PHX.ERR_ARG, f"input of {xq.size} quants and {xd.size} scales for {cols} columns")
+        xq = xq.reshape(-1, cols)
+        xd = xd.reshape(xq.shape[0], cols // 32)
         T = xq.shape[0]
         bufs = [self.alloc(w.nbytes), self.alloc(xq.nbytes), self.alloc(xd.nbytes), self.alloc(T * rows * 4)]
         for b, a in zip(bufs, (w, xq, xd)):
@@ -411,6 +426,40 @@ class MoeContext:
                                             bufs[3].ptr))
             self.sync()
             return bufs[3].download((T, rows))
+        finally:
+            for b in bufs:
+                b.free()
+
+    def weight_upload(self, wtype: int, w: np.ndarray, rows: int, cols: int) -> int:
+        """phx_weight_upload (GemmaGpu.UploadW): GGUF rows from host memory, repacked on the device once;
+        returns the handle for matmul_device / weight_free."""
+        w = np.ascontiguousarray(w, dtype=np.uint8)
+        bb = 18 if wtype == PHX.Q4_0 else 34
+        if w.size != rows * (cols // 32) * bb:
+            raise ArgumentError(PHX.ERR_ARG, f"weight bytes {w.size} != {rows} rows x {cols // 32} blocks x {bb}")
+        h = C.c_void_p()
+        self._check(self.lib.phx_weight_upload(self.h, wtype, rows, cols, w.ctypes.data, C.byref(h)))
+        return h.value
+
+    def weight_free(self, handle: int):
+        self.lib.phx_weight_free(self.h, handle)
+
+    def matmul_device(self, handle: int, T: int, xq_ptr: int, xd_ptr: int, y_ptr: int):
+        """phx_matmul (KernelsPrefill.MatMulQ4Q8Tile as GemmaGpu.Mm records it), asynchronous."""
+        self._check(self.lib.phx_matmul(self.h, handle, T, xq_ptr, xd_ptr, y_ptr))
+
+    def MatMul(self, handle: int, rows: int, cols: int, xq: np.ndarray, xd: np.ndarray) -> np.ndarray:
+        """GemmaGpu.Mm on host arrays: y [T][rows] f32 from T Q8_0 rows (as Q80 returns them)."""
+        xq = np.ascontiguousarray(xq, dtype=np.int8).reshape(-1, cols)
+        xd = np.ascontiguousarray(xd, dtype=np.uint16).reshape(xq.shape[0], cols // 32)
+        T = xq.shape[0]
+        bufs = [self.alloc(xq.nbytes), self.alloc(xd.nbytes), self.alloc(T * rows * 4)]
+        try:
+            bufs[0].upload(xq)
+            bufs[1].upload(xd)
+            self.matmul_device(handle, T, bufs[0].ptr, bufs[1].ptr, bufs[2].ptr)
+            self.sync()
+            return bufs[2].download((T, rows))
         finally:
             for b in bufs:
                 b.free()

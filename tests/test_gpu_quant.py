@@ -4,6 +4,7 @@ norm's quantized input (phx_norm_add, KernelsGemma.NormAdd / NormAddQuant, src/K
 through the C ABI: every mode's quantized integers, scales and block sums equal the oracle's
 CpuRef.QuantizeQ8_0 / QuantizeQ8_K of the transformed input (CpuRef.RmsNorm, gelu(x) * u, silu(x) * u),
 and the new residual rows the oracle's, bit for bit."""
+import ctypes as C
 import sys
 
 import numpy as np
@@ -44,8 +45,10 @@ def inputs(rows, n, seed):
     return x, u, w
 
 
+# n above 8192 (RmsNorm mode): several 2048-element workgroups per row, each forming the row mean, with a
+# partial last chunk at 9216 and 8448
 @pytest.mark.parametrize("mode", list(MODES))
-@pytest.mark.parametrize("n", [256, 2816, 4352])
+@pytest.mark.parametrize("n", [256, 2816, 4352, 9216, 12288])
 def test_q8_0_matches_oracle(ctx, orc, mode, n):
     say(f"quant q8_0: mode={mode} rows=4 n={n}")
     x, u, w = inputs(4, n, seed=n + MODES[mode])
@@ -59,7 +62,7 @@ def test_q8_0_matches_oracle(ctx, orc, mode, n):
 
 
 @pytest.mark.parametrize("mode", list(MODES))
-@pytest.mark.parametrize("n", [256, 3072, 4608])
+@pytest.mark.parametrize("n", [256, 3072, 4608, 8448, 12288])
 def test_q8_k_matches_oracle(ctx, orc, mode, n):
     say(f"quant q8_k: mode={mode} rows=4 n={n}")
     x, u, w = inputs(4, n, seed=7 * n + MODES[mode])
@@ -157,6 +160,40 @@ def test_matvec_matches_oracle(ctx, orc, wtype, T, rows, cols):
     y = ctx.MatVec(wtype, w, rows, cols, qs, d)
     for t in range(T):
         np.testing.assert_array_equal(y[t], orc.matvec(wtype, w, rows, cols, x[t]), err_msg=f"token {t}")
+
+
+@pytest.mark.parametrize("wtype", [2, 8])
+@pytest.mark.parametrize("T,rows,cols", [(1, 301, 512), (5, 2112, 2816), (31, 64, 12288), (32, 301, 2816),
+                                         (200, 2112, 2816), (2048, 2816, 2112)])
+def test_matmul_matches_oracle(ctx, orc, wtype, T, rows, cols):
+    """phx_weight_upload + phx_matmul (KernelsPrefill.MatMulQ4Q8Tile as GemmaGpu.Mm records it) equal
+    CpuRef.MatVec per token, bit for bit: the VALU row walk below 32 tokens, the matrix cores from 32 (one
+    partial 128-token tile, several, and C3's 2048 prompt rows through the shared FFN's down shape); row
+    counts not a multiple of the 64-row group."""
+    say(f"matmul: type={wtype} T={T} rows={rows} cols={cols}")
+    rng = np.random.default_rng(rows + cols + wtype + T)
+    w = gguf_rows(rng, wtype, rows, cols)
+    h = ctx.weight_upload(wtype, w, rows, cols)
+    try:
+        x = rng.standard_normal((T, cols)).astype(np.float32)
+        qs, d = ctx.Q80(0, x)
+        y = ctx.MatMul(h, rows, cols, qs, d)
+    finally:
+        ctx.weight_free(h)
+    toks = range(T) if T <= 200 else sorted(set([0, 1, T - 1] + rng.choice(T, 45, replace=False).tolist()))
+    for t in toks:
+        np.testing.assert_array_equal(y[t], orc.matvec(wtype, w, rows, cols, x[t]), err_msg=f"token {t}")
+
+
+def test_matmul_rejects_bad_arguments(ctx, pkg):
+    say("matmul: argument checks")
+    with pytest.raises(pkg.moe.NotSupportedError):
+        ctx._check(ctx.lib.phx_weight_upload(ctx.h, 12, 1, 256, np.zeros(144, np.uint8).ctypes.data,
+                                             C.byref(C.c_void_p())))
+    with pytest.raises(pkg.moe.ArgumentError):
+        ctx.weight_upload(2, np.zeros(17, np.uint8), 1, 32)  # short rows
+    with pytest.raises(pkg.moe.ArgumentError):
+        ctx.weight_upload(2, np.zeros(18 * 2, np.uint8), 1, 48)  # cols not a multiple of 32
 
 
 def test_matvec_rejects_other_types(ctx, pkg):
