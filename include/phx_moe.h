@@ -39,6 +39,12 @@ extern "C" {
 #define PHX_Q8_0 8
 #define PHX_Q4_K 12
 #define PHX_Q6_K 14
+/* IQ expert formats (CpuRefIQuants.cs:9-12: 256-element super-blocks of 66, 82 and 110 bytes), dotted
+ * against Q8_K activations by the reference's DotIQ2XXS / DotIQ2S / DotIQ3S (src/CpuRefIQuants.cs:45-167)
+ * with the codebooks of src/IqTables.cs. */
+#define PHX_IQ2_XXS 16
+#define PHX_IQ3_S 21
+#define PHX_IQ2_S 22
 
 /* Layout limits of the reference (src/KernelsMoe.cs:43, checked at src/GemmaCpu.cs:72-73). */
 #define PHX_MAX_EXPERTS 256

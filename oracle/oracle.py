@@ -66,6 +66,8 @@ def lib():
         L.orc_dot_q8_0.restype = f32
         L.orc_dot_k.argtypes = [i32, vp, i32, vp, vp, vp]
         L.orc_dot_k.restype = f32
+        L.orc_dot_iq.argtypes = [i32, vp, i32, vp, vp]
+        L.orc_dot_iq.restype = f32
         L.orc_matvec.argtypes = [i32, vp, i32, i32, vp, vp, i32]
         L.orc_matvec.restype = i32
         L.orc_gelu.argtypes = [f32]

@@ -73,6 +73,9 @@ __device__ void quantize_row(const float* v, Act act, int64_t row)
                 for (int i = 0; i < 16; i++) sum += qv(16 * j + i);
                 act.s[row * act.sstride + b * 16 + j] = sum;
             }
+        } else if (act.fmt == ACT_Q8K) {
+            int8_t* dst = act.q + row * act.qstride + (int64_t)b * 256;
+            for (int j = 0; j < 256; j++) dst[j] = (int8_t)qv(j);
         } else {
             uint32_t* dst = (uint32_t*)(act.q + row * act.qstride + (int64_t)b * 512);
             int* c = act.s + row * act.sstride + b * 128;
@@ -493,6 +496,7 @@ struct GroupArgs {
     float* out1;
     int split, out_stride;
     bool paired;
+    const void* grid;  // IQ types: the expanded codebook (64-bit words for IQ2_XXS / IQ2_S, 32-bit for IQ3_S)
 };
 
 // Output of lane `lane` of row group rgi for assignment row a: natural row order, or for a paired
@@ -692,6 +696,122 @@ __global__ __launch_bounds__(256) void k_grouped_k(GroupArgs g)
     }
 }
 
+// Signs applied to four codebook bytes: bit j of nib set negates byte j.  The bit spread gives 0x01 in
+// the negated bytes, times 0xFF the byte masks; (w ^ m) + (m & 0x01010101) negates those bytes without a
+// carry between them, as every codebook byte is at least 1.
+__device__ __forceinline__ uint32_t iq_signed(uint32_t w, uint32_t nib)
+{
+    const uint32_t m = ((nib * 0x00204081u) & 0x01010101u) * 0xFFu;
+    return (w ^ m) + (m & 0x01010101u);
+}
+
+// ksigns of the IQ2_XXS format: seven stored sign bits and the eighth making the count even
+__device__ __forceinline__ uint32_t iq_ksigns(uint32_t i) { return i | ((__builtin_popcount(i) & 1u) << 7); }
+
+// IQ rows: DotIQ2XXS / DotIQ2S / DotIQ3S (src/CpuRefIQuants.cs:45-146) per (row, assignment).  Per
+// super-block: the codebook points with their signs applied become 64 signed-byte dwords in element order
+// (once per row), every assignment's integer sum bsum adds the 32-element (IQ2_S: 16-element) dot
+// products times their odd scales, and sumf += (d * yd) * (float)bsum in super-block order; the IQ2 types
+// return 0.125 * sumf.  The codebook sits in LDS (lanes look up different entries).
+template <int TYPE, int A>
+__global__ __launch_bounds__(256) void k_grouped_iq(GroupArgs g)
+{
+    constexpr bool IQ3 = TYPE == PHX_IQ3_S_DEV, IQ2S = TYPE == PHX_IQ2_S_DEV;
+    constexpr int PAY = TYPE == PHX_IQ2_XXS_DEV ? 64 : IQ2S ? 80 : 112;
+    constexpr int NW = TYPE == PHX_IQ2_XXS_DEV ? 512 : IQ2S ? 2048 : 512;  // codebook dwords
+    __shared__ uint32_t cb[NW];
+    for (int i = threadIdx.x; i < NW; i += 256) cb[i] = ((const uint32_t*)g.grid)[i];
+    __syncthreads();
+    const int tile = blockIdx.x;
+    if (tile >= *g.ntiles) return;
+    const Tile tl = g.tiles[tile];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int rgi = blockIdx.y * 4 + wave;
+    if (rgi >= g.rg) return;
+    const uint8_t* wp = g.payload + tl.e * g.mat_pay + rgi * g.rg_pay + lane * PAY;
+    const uint8_t* wsb = g.scale + tl.e * g.mat_sc + ((int64_t)rgi * g.nb * 64 + lane) * 2;
+    int arow[A];
+    float sumf[A];
+#pragma unroll
+    for (int i = 0; i < A; i++) {
+        arow[i] = i < tl.cnt ? g.perm[tl.start + i] / g.act_div : 0;
+        sumf[i] = 0.0f;
+    }
+    for (int b = 0; b < g.nb; b++) {
+        uint32_t wv[PAY / 4];
+        {
+            const uint4* src = (const uint4*)(wp + (int64_t)b * 64 * PAY);
+#pragma unroll
+            for (int c = 0; c < PAY / 16; c++) {
+                const uint4 t4 = src[c];
+                wv[4 * c] = t4.x;
+                wv[4 * c + 1] = t4.y;
+                wv[4 * c + 2] = t4.z;
+                wv[4 * c + 3] = t4.w;
+            }
+        }
+        const float d = h2f(*(const uint16_t*)(wsb + (int64_t)b * 64 * 2));
+        auto byte_at = [&](int o) -> uint32_t { return (wv[o >> 2] >> (8 * (o & 3))) & 0xFFu; };
+        uint32_t v[64];
+        int sc[16];  // scale per 16 elements
+#pragma unroll
+        for (int ib = 0; ib < 8; ib++) {
+            if (TYPE == PHX_IQ2_XXS_DEV) {
+                const uint32_t a0 = wv[2 * ib], a1 = wv[2 * ib + 1];
+                sc[2 * ib] = sc[2 * ib + 1] = (int)(2 * (a1 >> 28) + 1);
+#pragma unroll
+                for (int l = 0; l < 4; l++) {
+                    const uint32_t gi = (a0 >> (8 * l)) & 0xFFu, sg = iq_ksigns((a1 >> (7 * l)) & 127u);
+                    v[8 * ib + 2 * l] = iq_signed(cb[2 * gi], sg & 15u);
+                    v[8 * ib + 2 * l + 1] = iq_signed(cb[2 * gi + 1], sg >> 4);
+                }
+            } else if (IQ2S) {
+                const uint32_t qh = byte_at(64 + ib), s8 = byte_at(72 + ib);
+                sc[2 * ib] = 1 + 2 * (int)(s8 & 0xFu);
+                sc[2 * ib + 1] = 1 + 2 * (int)(s8 >> 4);
+#pragma unroll
+                for (int l = 0; l < 4; l++) {
+                    const uint32_t gi = byte_at(4 * ib + l) | ((qh << (8 - 2 * l)) & 0x300u);
+                    const uint32_t sg = byte_at(32 + 4 * ib + l);
+                    v[8 * ib + 2 * l] = iq_signed(cb[2 * gi], sg & 15u);
+                    v[8 * ib + 2 * l + 1] = iq_signed(cb[2 * gi + 1], sg >> 4);
+                }
+            } else {
+                const uint32_t h = byte_at(64 + ib), s8 = byte_at(104 + ib / 2);
+                sc[2 * ib] = sc[2 * ib + 1] = 2 * (int)((ib & 1) ? s8 >> 4 : s8 & 0xFu) + 1;
+#pragma unroll
+                for (int l = 0; l < 4; l++) {
+                    const uint32_t g1 = cb[byte_at(8 * ib + 2 * l) | ((h << (8 - 2 * l)) & 256u)];
+                    const uint32_t g2 = cb[byte_at(8 * ib + 2 * l + 1) | ((h << (7 - 2 * l)) & 256u)];
+                    const uint32_t sg = byte_at(72 + 4 * ib + l);
+                    v[8 * ib + 2 * l] = iq_signed(g1, sg & 15u);
+                    v[8 * ib + 2 * l + 1] = iq_signed(g2, sg >> 4);
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < A; i++) {
+            if (i < tl.cnt) {
+                const int64_t r = arow[i];
+                const uint32_t* xq = (const uint32_t*)(g.act.q + r * g.act.qstride + (int64_t)b * 256);
+                int bsum = 0;
+#pragma unroll
+                for (int h16 = 0; h16 < 16; h16++) {
+                    int s16 = 0;
+#pragma unroll
+                    for (int k = 0; k < 4; k++) s16 = __builtin_amdgcn_sdot4((int)v[4 * h16 + k], (int)xq[4 * h16 + k], s16, false);
+                    bsum += sc[h16] * s16;
+                }
+                const float dd = d * g.act.d[r * g.act.dstride + b];
+                sumf[i] += dd * (float)bsum;
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < A; i++)
+        if (i < tl.cnt) store_row(g, rgi, lane, g.perm[tl.start + i], IQ3 ? sumf[i] : 0.125f * sumf[i]);
+}
+
 void launch_grouped(hipStream_t st, const QMat& w, Act act, const Tile* tiles, const int* ntiles, int max_tiles, int A,
                     const int* perm, int act_div, float* out0, float* out1, int split, int out_stride)
 {
@@ -714,6 +834,7 @@ void launch_grouped(hipStream_t st, const QMat& w, Act act, const Tile* tiles, c
     g.split = split;
     g.out_stride = out_stride;
     g.paired = w.paired;
+    g.grid = w.grid;
     dim3 grid(max_tiles, (w.rg + 3) / 4);
     (void)A;  // the tile size the dispatch used: 4, the one instantiation
     switch (w.type) {
@@ -721,6 +842,9 @@ void launch_grouped(hipStream_t st, const QMat& w, Act act, const Tile* tiles, c
     case PHX_Q8_0_DEV: launch((k_grouped_q<PHX_Q8_0_DEV, 4>), grid, dim3(256), 0, st, g); break;
     case PHX_Q4_K_DEV: launch((k_grouped_k<PHX_Q4_K_DEV, 4>), grid, dim3(256), 0, st, g); break;
     case PHX_Q6_K_DEV: launch((k_grouped_k<PHX_Q6_K_DEV, 4>), grid, dim3(256), 0, st, g); break;
+    case PHX_IQ2_XXS_DEV: launch((k_grouped_iq<PHX_IQ2_XXS_DEV, 4>), grid, dim3(256), 0, st, g); break;
+    case PHX_IQ2_S_DEV: launch((k_grouped_iq<PHX_IQ2_S_DEV, 4>), grid, dim3(256), 0, st, g); break;
+    case PHX_IQ3_S_DEV: launch((k_grouped_iq<PHX_IQ3_S_DEV, 4>), grid, dim3(256), 0, st, g); break;
     }
 }
 

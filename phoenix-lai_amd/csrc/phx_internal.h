@@ -10,6 +10,9 @@
 #define PHX_Q8_0_DEV 8
 #define PHX_Q4_K_DEV 12
 #define PHX_Q6_K_DEV 14
+#define PHX_IQ2_XXS_DEV 16
+#define PHX_IQ3_S_DEV 21
+#define PHX_IQ2_S_DEV 22
 #define PHX_MAX_USED_DEV 16
 #define PHX_MAX_EXPERTS_DEV 256
 
@@ -50,7 +53,7 @@ inline void launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, uint32_t lds
 constexpr int kRowGroup = 64;  // rows per interleaved row group: one wave64, lane = row
 
 // Activation formats produced for each weight type.
-enum ActFmt { ACT_Q8_0 = 0, ACT_K4 = 1, ACT_K6 = 2 };
+enum ActFmt { ACT_Q8_0 = 0, ACT_K4 = 1, ACT_K6 = 2, ACT_Q8K = 3 };
 
 // One stack of quantized matrices (experts, or one dense matrix), repacked at upload into row
 // groups of 64 rows: payload[m][rg][b][lane][pay] and scale[m][rg][b][lane][sbytes], so the 64
@@ -62,6 +65,8 @@ enum ActFmt { ACT_Q8_0 = 0, ACT_K4 = 1, ACT_K6 = 2 };
 //   Q8_0: pay 32 (int8), scale fp16 d
 //   Q4_K: pay 144 = 128 nibbles in (sub-block, l, m) order + sc[8] + m[8]; scale fp16 d | fp16 dmin << 16
 //   Q6_K: pay 208 = 128 low-nibble plane + 64 high-bit plane + int8 sc[16]; scale fp16 d
+//   IQ2_XXS / IQ2_S / IQ3_S: pay 64 / 80 / 112 = the block's bytes after d, unchanged (IQ3_S padded by 4);
+//             scale fp16 d; grid points at the codebooks (iq_grids.h) expanded on the device
 struct QMat {
     int type = -1;
     int n_mat = 0, rows = 0, cols = 0;  // cols includes any zero padding of K
@@ -71,6 +76,7 @@ struct QMat {
     int64_t rg_pay = 0;                 // payload bytes per row group (blocks, then Q4_0 / Q8_0 scale groups)
     uint8_t* payload = nullptr;
     uint8_t* scale = nullptr;
+    const void* grid = nullptr;         // IQ types: the context's expanded codebook of this type
     bool has_sc8() const { return type == PHX_Q4_0_DEV || type == PHX_Q8_0_DEV; }
     int64_t sc8_off() const { return (int64_t)nb * kRowGroup * pay; }  // scale groups within a row group
     int64_t mat_pay_stride() const { return (int64_t)rg * rg_pay; }
@@ -83,6 +89,7 @@ struct QMat {
 //             d f32 [cols/256], s int32 [cols/16] (the Q8_K bsums)
 //   ACT_K6:   q int32 [cols/256][8 P][8 l][2] masked pair dwords, d f32 [cols/256],
 //             s int32 [cols/256][16 sub][8 l] offset terms -32*(x_l + x_{l+8})
+//   ACT_Q8K:  q int8 [cols] in element order, d f32 [cols/256] (the IQ types' Q8_K input)
 struct Act {
     int fmt = ACT_Q8_0;
     int cols = 0;

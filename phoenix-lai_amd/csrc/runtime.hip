@@ -13,6 +13,7 @@
 #include <thread>
 #include <vector>
 
+#include "iq_grids.h"
 #include "phx_internal.h"
 
 using namespace phx;
@@ -91,13 +92,18 @@ int64_t row_bytes(int type, int cols)
     case PHX_Q8_0: return (int64_t)(cols / 32) * 34;
     case PHX_Q4_K: return (int64_t)(cols / 256) * 144;
     case PHX_Q6_K: return (int64_t)(cols / 256) * 210;
+    case PHX_IQ2_XXS: return (int64_t)(cols / 256) * 66;
+    case PHX_IQ2_S: return (int64_t)(cols / 256) * 82;
+    case PHX_IQ3_S: return (int64_t)(cols / 256) * 110;
     }
     return -1;
 }
 
-bool quant_type(int t) { return t == PHX_Q4_0 || t == PHX_Q8_0 || t == PHX_Q4_K || t == PHX_Q6_K; }
-int block_elems(int t) { return (t == PHX_Q4_K || t == PHX_Q6_K) ? 256 : 32; }
-int act_fmt(int t) { return t == PHX_Q4_K ? ACT_K4 : t == PHX_Q6_K ? ACT_K6 : ACT_Q8_0; }
+bool iq_type(int t) { return t == PHX_IQ2_XXS || t == PHX_IQ2_S || t == PHX_IQ3_S; }
+bool quant_type(int t) { return t == PHX_Q4_0 || t == PHX_Q8_0 || t == PHX_Q4_K || t == PHX_Q6_K || iq_type(t); }
+int block_elems(int t) { return (t == PHX_Q4_0 || t == PHX_Q8_0) ? 32 : 256; }
+int act_fmt(int t) { return t == PHX_Q4_K ? ACT_K4 : t == PHX_Q6_K ? ACT_K6 : iq_type(t) ? ACT_Q8K : ACT_Q8_0; }
+int iq_pay(int t) { return t == PHX_IQ2_XXS ? 64 : t == PHX_IQ2_S ? 80 : 112; }
 int round_up(int v, int m) { return (v + m - 1) / m * m; }
 
 // ------------------------------------------------------------------------------ repack
@@ -188,6 +194,12 @@ void repack_block(int type, const uint8_t* blk, uint8_t* pay, uint8_t* sc)
         memcpy(sc, blk + 208, 2);
         break;
     }
+    case PHX_IQ2_XXS:
+    case PHX_IQ2_S:
+    case PHX_IQ3_S:  // the bytes after d unchanged (IQ3_S's 108 padded to 112 by the zeroed buffer)
+        memcpy(sc, blk, 2);
+        memcpy(pay, blk + 2, (size_t)(row_bytes(type, 256) - 2));
+        break;
     }
 }
 
@@ -202,7 +214,7 @@ void repack(int type, const uint8_t* src, int n_mat, int rows, int cols, QMat& q
     q.paired = paired;
     q.rg = paired ? (rows / 2 + 31) / 32 : (rows + kRowGroup - 1) / kRowGroup;
     q.nb = cols / block_elems(type);
-    q.pay = type == PHX_Q4_0 ? 16 : type == PHX_Q8_0 ? 32 : type == PHX_Q4_K ? 144 : 208;
+    q.pay = type == PHX_Q4_0 ? 16 : type == PHX_Q8_0 ? 32 : type == PHX_Q4_K ? 144 : iq_type(type) ? iq_pay(type) : 208;
     q.sbytes = type == PHX_Q4_K ? 4 : 2;
     const int64_t rb = row_bytes(type, cols), bb = rb / q.nb;
     const int nb8 = (q.nb + 7) / 8;
@@ -288,6 +300,8 @@ struct phx_moe_ctx {
     // the bump allocation ensure() does while it lays the table out
     unsigned char* scratch = nullptr;
     std::vector<Buf> ws_scratch;
+    // the IQ codebooks expanded (iq_grids.h): IQ2_XXS 256 and IQ2_S 1024 64-bit words, IQ3_S 512 32-bit
+    uint8_t* iq_grid = nullptr;
     bool last_scratch = false;
     unsigned char* bump_base = nullptr;
     size_t bump_off = 0, bump_cap = 0;
@@ -364,6 +378,7 @@ void act_sizes(int fmt, int64_t rows, int cols, size_t& qb, size_t& db, size_t& 
 {
     if (fmt == ACT_Q8_0) { qb = rows * cols; db = rows * (cols / 32) * 4; sb = rows * (cols / 32) * 4; }
     else if (fmt == ACT_K4) { qb = rows * cols; db = rows * (cols / 256) * 4; sb = rows * (cols / 16) * 4; }
+    else if (fmt == ACT_Q8K) { qb = rows * cols; db = rows * (cols / 256) * 4; sb = 4; }
     else { qb = rows * (cols / 256) * 512; db = rows * (cols / 256) * 4; sb = rows * (cols / 256) * 128 * 4; }
 }
 
@@ -377,6 +392,7 @@ Act make_act(phx_moe_ctx* c, int fmt, int cols, int qid, int did, int sid)
     a.s = wp<int>(c, sid);
     if (fmt == ACT_Q8_0) { a.qstride = cols; a.dstride = cols / 32; a.sstride = cols / 32; }
     else if (fmt == ACT_K4) { a.qstride = cols; a.dstride = cols / 256; a.sstride = cols / 16; }
+    else if (fmt == ACT_Q8K) { a.qstride = cols; a.dstride = cols / 256; a.sstride = 0; }
     else { a.qstride = (int64_t)(cols / 256) * 512; a.dstride = cols / 256; a.sstride = (cols / 256) * 128; }
     return a;
 }
@@ -764,11 +780,34 @@ void free_qmat(QMat& q)
     q.scale = nullptr;
 }
 
+constexpr size_t kIqGridBytes = 256 * 8 + 1024 * 8 + 512 * 4;
+
+const void* iq_grid_of(const phx_moe_ctx* c, int type)
+{
+    if (!c->iq_grid) return nullptr;
+    return type == PHX_IQ2_XXS ? c->iq_grid : type == PHX_IQ2_S ? c->iq_grid + 256 * 8 : c->iq_grid + 1280 * 8;
+}
+
+int upload_iq_grids(phx_moe_ctx* c)
+{
+    std::vector<uint8_t> h(kIqGridBytes);
+    uint64_t* g2xxs = (uint64_t*)h.data();
+    uint64_t* g2s = g2xxs + 256;
+    uint32_t* g3s = (uint32_t*)(g2s + 1024);
+    for (int i = 0; i < 256; i++) g2xxs[i] = phx_iq2_grid_word(phx_iq2xxs_codes[i]);
+    for (int i = 0; i < 1024; i++) g2s[i] = phx_iq2_grid_word(phx_iq2s_codes[i]);
+    for (int i = 0; i < 512; i++) g3s[i] = phx_iq3s_grid_word(phx_iq3s_codes[i]);
+    HIPCHK(c, hipMalloc((void**)&c->iq_grid, kIqGridBytes));
+    HIPCHK(c, hipMemcpy(c->iq_grid, h.data(), kIqGridBytes, hipMemcpyHostToDevice));
+    return PHX_OK;
+}
+
 int upload_q(phx_moe_ctx* c, int type, const void* src, int n_mat, int rows, int cols, QMat& q, bool paired = false)
 {
     free_qmat(q);
     HostQ h;
     repack(type, (const uint8_t*)src, n_mat, rows, cols, q, h, paired);
+    q.grid = iq_type(type) ? iq_grid_of(c, type) : nullptr;
     HIPCHK(c, hipMalloc((void**)&q.payload, h.payload.size()));
     HIPCHK(c, hipMalloc((void**)&q.scale, h.scale.size()));
     HIPCHK(c, hipMemcpy(q.payload, h.payload.data(), h.payload.size(), hipMemcpyHostToDevice));
@@ -930,6 +969,7 @@ int phx_moe_create(int hip_device, phx_moe_ctx** out)
         if ((h = hipMemset(c->flags, 0, 64)) != hipSuccess) { rc = set_err(c, hip_code(h), "memset failed"); break; }
         if ((rc = scratch_address(c)) != PHX_OK) break;
         c->ws_scratch.resize(W_COUNT);
+        if ((rc = upload_iq_grids(c)) != PHX_OK) break;
     } while (0);
     if (rc != PHX_OK) {
         phx_moe_destroy(c);
@@ -957,6 +997,7 @@ void phx_moe_destroy(phx_moe_ctx* c)
     drop_graph_timing(c);
     if (c->gelu_tab) (void)hipFree(c->gelu_tab);
     if (c->flags) (void)hipFree(c->flags);
+    if (c->iq_grid) (void)hipFree(c->iq_grid);
     if (c->stream) (void)hipStreamDestroy(c->stream);
     delete c;
 }

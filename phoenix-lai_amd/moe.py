@@ -17,7 +17,7 @@ _HERE = Path(__file__).resolve().parent
 
 class PHX:
     OK, ERR_ARG, ERR_OOM, ERR_UNSUPPORTED, ERR_DEVICE_LOST, ERR_HIP, ERR_FORMAT = 0, -1, -2, -3, -4, -5, -6
-    F32, Q4_0, Q8_0, Q4_K, Q6_K = 0, 2, 8, 12, 14
+    F32, Q4_0, Q8_0, Q4_K, Q6_K, IQ2_XXS, IQ3_S, IQ2_S = 0, 2, 8, 12, 14, 16, 21, 22
     WEIGHTS_SOFTMAX, WEIGHTS_CPUREF = 0, 1
     FLAG_DEVICE_PTRS, FLAG_ASYNC, FLAG_RESIDUAL, FLAG_EXACT_ROUTER = 1, 2, 4, 8
     KINDS = ["prologue", "router", "topk", "dispatch", "gate_up", "requant", "down", "combine", "shared"]

@@ -60,12 +60,17 @@ def lib():
     return _L
 
 
+_IQ_BYTES = {PHX.IQ2_XXS: 66, PHX.IQ2_S: 82, PHX.IQ3_S: 110}
+
+
 def row_bytes(t: int, cols: int) -> int:
+    if t in _IQ_BYTES:
+        return cols // 256 * _IQ_BYTES[t]
     return int(lib().phx_synth_row_bytes(t, cols))
 
 
 def block_elems(t: int) -> int:
-    return 256 if t in (PHX.Q4_K, PHX.Q6_K) else (1 if t == PHX.F32 else 32)
+    return 256 if t in (PHX.Q4_K, PHX.Q6_K) or t in _IQ_BYTES else (1 if t == PHX.F32 else 32)
 
 
 def normal(seed: int, name: str, shape, mean=0.0, std=1.0, offset=0) -> np.ndarray:
@@ -90,7 +95,24 @@ def quantize(t: int, x: np.ndarray) -> np.ndarray:
     return out
 
 
+IQ_TYPES = (PHX.IQ2_XXS, PHX.IQ2_S, PHX.IQ3_S)
+
+
+def iq_blocks(seed: int, name: str, t: int, rows: int, cols: int, std=0.02) -> np.ndarray:
+    """Seeded IQ2_XXS / IQ2_S / IQ3_S rows.  Every bit pattern of an IQ super-block is a valid encoding
+    (grid indices, signs and scales all decode), so the payload is seeded random bytes and only the fp16
+    d is chosen: |N(0, 1)| * std over the format's typical |grid * scale| (about 50 for the IQ2 types with
+    their 1/8, 128 for IQ3_S), so the decoded weights have roughly the given spread."""
+    bb = row_bytes(t, 256)
+    blocks = random_bytes(seed, name, rows * (cols // 256) * bb).reshape(-1, bb)
+    d = np.abs(normal(seed, name + ".d", (blocks.shape[0],))) * (std / (128.0 if t == PHX.IQ3_S else 50.0))
+    blocks[:, :2] = d.astype(np.float16).view(np.uint8).reshape(-1, 2)
+    return blocks.reshape(-1)
+
+
 def quantized_normal(seed: int, name: str, t: int, rows: int, logical_cols: int, cols: int, std=0.02) -> np.ndarray:
+    if t in IQ_TYPES:
+        return iq_blocks(seed, name, t, rows, cols, std)
     out = np.empty(rows * row_bytes(t, cols), np.uint8)
     rc = lib().phx_synth_quantized_normal(seed, name.encode(), 0.0, std, t, rows, logical_cols, cols, out.ctypes.data)
     if rc:

@@ -17,7 +17,8 @@ from pathlib import Path
 
 ROOT = Path(__file__).resolve().parent.parent
 ORACLE = ROOT / "oracle"
-PINS = ["tests/test_oracle_numerics.py", "tests/test_oracle_layer.py", "tests/test_oracle_chain_order.py"]
+PINS = ["tests/test_oracle_numerics.py", "tests/test_oracle_layer.py", "tests/test_oracle_chain_order.py",
+        "tests/test_oracle_iq.py"]
 CFLAGS = ["-O2", "-std=c11", "-fPIC", "-ffp-contract=off", "-fno-fast-math", "-fexcess-precision=standard",
           "-fopenmp", "-shared"]
 
@@ -69,13 +70,23 @@ MUTATIONS = {
                            ("sumf -= dm * (float)sumi;", "summin += dm * (float)sumi;"),
                            ("for (int l = 0; l < 8; l++) sumf += sums[l];\n    return sumf;",
                             "for (int l = 0; l < 8; l++) sumf += sums[l];\n    sumf -= summin;\n    return sumf;")],
+    # IQ formats
+    "iq2_xxs super-blocks reversed": [("    for (int i = 0; i < nb; i++) {\n        const uint8_t* blk = row + (int64_t)i * 66;",
+                                       "    for (int i = nb - 1; i >= 0; i--) {\n        const uint8_t* blk = row + (int64_t)i * 66;")],
+    "iq2_xxs scale without the +1": [("int ls = (int)(2 * (a1 >> 28) + 1);", "int ls = (int)(2 * (a1 >> 28));")],
+    "iq2_s high bits shifted": [("((qh[ib32] << (8 - 2 * l)) & 0x300)", "((qh[ib32] << (6 - 2 * l)) & 0x300)")],
+    "iq2_s scales of the halves swapped": [("if (l < 2) sumi1 += s;", "if (l >= 2) sumi1 += s;")],
+    "iq3_s second point's high bit": [("((h << (7 - 2 * l)) & 256)", "((h << (8 - 2 * l)) & 256)")],
+    "iq3_s half scales swapped": [("bsum += sumi * (half == 0 ? ls1 : ls2);", "bsum += sumi * (half == 0 ? ls2 : ls1);")],
+    "iq2 final 1/8 dropped": [("    return 0.125f * sumf;\n}\n\n/* DotIQ2S", "    return sumf;\n}\n\n/* DotIQ2S")],
 }
 
 
 def build(src: str, out: Path) -> None:
     c = out.with_suffix(".c")
     c.write_text(src)
-    subprocess.run(["gcc", *CFLAGS, f"-I{ORACLE}", "-o", str(out), str(c), "-lm"], check=True)
+    subprocess.run(["gcc", *CFLAGS, f"-I{ORACLE}", f"-I{ROOT / 'phoenix-lai_amd' / 'csrc'}", "-o", str(out), str(c), "-lm"],
+                   check=True)
 
 
 def run_pins(lib: Path) -> tuple[bool, str]:

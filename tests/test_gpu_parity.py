@@ -534,3 +534,25 @@ def test_mfma_grouped_products_bit_exact(ctx, pkg, orc, case):
     shared = pkg.synth.normal(1234, "mfma.shared", x.shape) if with_shared else None
     ctx.upload(0, L)
     check_layer(ctx, orc, L, x, shared, tag=f"mfma {case}", exact=True)
+
+
+# ---------------------------------------------------------------------------------------- IQ formats
+IQ_CASES = {
+    # gate|up, down (and the shared FFN) in the IQ formats (CpuRefIQuants.cs); n_ff 384 pads the down rows
+    # to 512 (zero activations in the tail), 512 does not
+    "iq2xxs_gu_iq2s_dn": (dict(idx=41, T=12, d=512, E=8, k=2, nf=384, gu=16, dn=22), 12),
+    "iq3s_both_shared": (dict(idx=42, T=12, d=768, E=8, k=2, nf=512, gu=21, dn=21, nff=512, sh=21), 12),
+    "iq2s_gu_iq2xxs_dn_full_tiles": (dict(idx=43, T=64, d=512, E=4, k=2, nf=512, gu=22, dn=16), 64),
+}
+
+
+@pytest.mark.parametrize("case", list(IQ_CASES))
+def test_iq_layers_bit_exact(ctx, pkg, orc, case):
+    """IQ2_XXS / IQ2_S / IQ3_S experts on the VALU grouped kernel, codebooks in LDS: gate, up and down
+    products and outputs equal the oracle's DotIQ chains bit for bit (exact router)."""
+    cfg, T = IQ_CASES[case]
+    say(f"iq {case}: T={T}")
+    L = pkg.synth.make_layer(cfg, norms="noisy")
+    x = pkg.synth.make_input(cfg, T=T)
+    ctx.upload(0, L)
+    check_layer(ctx, orc, L, x, tag=f"iq {case}", exact=True)

@@ -184,3 +184,26 @@ def test_dotk_min_term_precedes_the_fold(orc):
     terms = [-LANE_BIG] + [LANE_SMALL] * 8
     assert _seq(terms[1:] + terms[:1]) != want  # min term added after the lanes
     _assert_discriminates(want, terms)
+
+
+def test_iq_superblock_chain_is_left_to_right(orc):
+    """DotIQ2XXS's sumf += d * bsum over super-blocks (src/CpuRefIQuants.cs:51-75), then 0.125 * sumf.
+    Every super-block uses grid entry 0 (all eights), no signs and scale 1, so bsum = 8 * (sum of its
+    quants): 800 in super-block 0 (d = 1), 600 in super-blocks 1..7 (d = 2^-24: 600 * 2^-24 is between
+    half an ulp and an ulp of 800).  The chain ends at 800 + 7 * 2^-14, scaled exactly by 0.125."""
+    nsb = 8
+    row = np.zeros((nsb, 66), np.uint8)
+    row[0, 0], row[0, 1] = D1 & 0xFF, D1 >> 8
+    row[1:, 0] = DTINY
+    x = np.zeros(256 * nsb, F32)
+    x[::256] = -127.0
+    x[1::256] = 127.0
+    x[2] = 100.0
+    x[256 + 2::256] = 75.0
+    got = orc.matvec(16, row.reshape(-1), 1, 256 * nsb, x)[0]
+    small = 600 * 2.0 ** -24
+    assert ulp(800.0) / 2 < small < ulp(800.0)
+    want = F32(F32(800.0 + (nsb - 1) * ulp(800.0)) * F32(0.125))
+    assert got == want, (float(got), float(want))
+    for alt in (_rev, _pairwise, _double):
+        assert F32(alt([800.0] + [small] * (nsb - 1)) * F32(0.125)) != want
