@@ -425,9 +425,9 @@ struct CombArgs {
     int* flags;
 };
 
-template <int CQ>
+template <int CQ, class F>
 __device__ __forceinline__ void combine_into(const CombArgs& p, int t, float* sx, float* sacc, float* so, double* red,
-                                             bool leader)
+                                             bool leader, F&& after_issue)
 {
     constexpr int RG = CQ <= 3 ? 8 : 4;  // ranks per load round (register budget)
     const int tid = threadIdx.x, NT = blockDim.x, d = p.d, k = p.k, n4 = d / 4;
@@ -460,6 +460,10 @@ __device__ __forceinline__ void combine_into(const CombArgs& p, int t, float* sx
                 xv[q] = ((const float4*)(p.xin + (int64_t)t * d))[ix[q]];
                 pf[q] = ((const float4*)p.post_ffw)[ix[q]];
             }
+            // the caller's own loads go out behind these (the first use waits for these alone)
+            __builtin_amdgcn_sched_barrier(0);
+            after_issue();
+            __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
         for (int q = 0; q < CQ; q++)
@@ -549,19 +553,27 @@ __device__ __forceinline__ void route_wg(const DecArgs& a, int t, int e, float* 
     const float4 fv = a.ash.q ? ((const float4*)a.fnorm)[8 * bc + l8] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     {
         const int n4 = d / 4;
+        // every lane issues every load (the last ones clamped to the row's end, landing in the padding of
+        // the LDS row), so no branch makes the compiler's wait counts conservative
         auto stage = [&](const float* src, float* dst) {
             for (int q = 0; q * RT_NT < n4; q++) {
-                const int i = q * RT_NT + tid;
-                if (i < n4)
-                    __builtin_amdgcn_global_load_lds((glb_void_t)((const float4*)src + i),
-                                                     (lds_void_t)((float4*)dst + q * RT_NT + wave * 64), 16, 0, 0);
+                const int i = min(q * RT_NT + tid, n4 - 1);
+                __builtin_amdgcn_global_load_lds((glb_void_t)((const float4*)src + i),
+                                                 (lds_void_t)((float4*)dst + q * RT_NT + wave * 64), 16, 0, 0);
             }
         };
-        if (!FUSED) stage(xr, sx);
-        stage(a.gis, sg);
-        stage(a.W + (int64_t)e * d, sw);
-        // fused: this token's x is the previous layer's combine, formed here (scb: its two LDS rows)
-        if (FUSED) combine_into<(PER + 3) / 4>(prev, t, sx, scb, scb + d, red5, e == 0);
+        if (FUSED) {
+            // this token's x is the previous layer's combine, formed here (scb: its two LDS rows); its loads
+            // go out first, the router scale and W row behind them
+            combine_into<(PER + 3) / 4>(prev, t, sx, scb, scb + d, red5, e == 0, [&] {
+                stage(a.gis, sg);
+                stage(a.W + (int64_t)e * d, sw);
+            });
+        } else {
+            stage(xr, sx);
+            stage(a.gis, sg);
+            stage(a.W + (int64_t)e * d, sw);
+        }
         __builtin_amdgcn_s_waitcnt(0);
     }
     __syncthreads();
@@ -654,14 +666,18 @@ __device__ __forceinline__ void route_wg(const DecArgs& a, int t, int e, float* 
     }
 }
 
+// floats of one staged router row in LDS: d rounded up to whole rounds of RT_NT float4 (the staging's
+// clamped last loads land in the padding)
+__host__ __device__ inline int route_row_floats(int d) { return (d / 4 + RT_NT - 1) / RT_NT * RT_NT * 4; }
+
 template <bool FUSED>
 __device__ __forceinline__ void route_dispatch(const DecArgs& a, const CombArgs& prev, float* rsm)
 {
-    const int t = blockIdx.x / a.E, e = blockIdx.x % a.E, d = a.d;
+    const int t = blockIdx.x / a.E, e = blockIdx.x % a.E, d = a.d, dp = route_row_floats(d);
     float* sx = rsm;
-    float* sg = sx + d + 4;
-    float* sw = sg + d + 4;
-    float* scb = sw + d + 4;  // fused: the combine's two rows
+    float* sg = sx + dp;
+    float* sw = sg + dp;
+    float* scb = sw + dp;  // fused: the combine's two rows
 #define RT_CASE(n) \
     case n: route_wg<n, FUSED>(a, t, e, sx, sg, sw, prev, scb); break;
     switch (d / RT_NT) {
@@ -674,7 +690,7 @@ __device__ __forceinline__ void route_dispatch(const DecArgs& a, const CombArgs&
 
 __global__ __launch_bounds__(RT_NT) void k_dec_route(DecArgs a)
 {
-    extern __shared__ __align__(16) float rsm[];  // x, router scale, W row: 3 * (d + 4) floats
+    extern __shared__ __align__(16) float rsm[];  // x, router scale, W row: route_row_floats(d) each
     route_dispatch<false>(a, CombArgs{}, rsm);
 }
 
@@ -684,7 +700,7 @@ __global__ __launch_bounds__(RT_NT) void k_dec_route(DecArgs a)
 // k_dec_route.  One launch fewer per layer than route + combine.
 __global__ __launch_bounds__(RT_NT) void k_dec_route_fused(CombArgs prev, DecArgs a)
 {
-    extern __shared__ __align__(16) float rsm[];  // x, router scale, W row, combine rows: 5 * (d + 4)
+    extern __shared__ __align__(16) float rsm[];  // x, router scale, W row, then the combine's two rows
     route_dispatch<true>(a, prev, rsm);
 }
 
@@ -756,17 +772,33 @@ __device__ __forceinline__ float f32_up(double v)  // the smallest float >= v
     return __uint_as_float(f > 0.0f ? b + 1u : b - 1u);
 }
 
-__device__ bool wave_topk(const DecArgs& a, int t, int* s_ids, unsigned* s_klo, unsigned* s_khi)
+// The router's logits and bounds of token t for one wave (lane + 64 q in slot q): cold reads (the router
+// launch wrote them), issued at workgroup start so they travel beside the shared units' weights.
+struct SelIn {
+    double L[4], B[4];
+};
+
+__device__ __forceinline__ void sel_issue(const DecArgs& a, int t, SelIn& in)
 {
     const int lane = threadIdx.x & 63;
     const double* Lr = a.Lb + (int64_t)t * a.E;
     const double* Br = a.Bb + (int64_t)t * a.E;
-    double L[4], B[4];
 #pragma unroll
     for (int q = 0; q < 4; q++) {
         const int ex = min(lane + 64 * q, a.E - 1);
-        L[q] = Lr[ex];
-        B[q] = Br[ex];
+        in.L[q] = Lr[ex];
+        in.B[q] = Br[ex];
+    }
+}
+
+__device__ bool wave_topk(const DecArgs& a, int t, const SelIn& in, int* s_ids, unsigned* s_klo, unsigned* s_khi)
+{
+    const int lane = threadIdx.x & 63;
+    double L[4], B[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        L[q] = in.L[q];
+        B[q] = in.B[q];
     }
     unsigned key[4], klo[4], khi[4];
     int rank[4];
@@ -1141,7 +1173,9 @@ __device__ void write_routing(const DecArgs& a, LF Lr, const int* s_ids, const i
     }
 }
 
-template <int TYPE>
+// PRESEL: the selection's inputs are loaded at entry and held in registers through the shared units
+// (left out where the register budget is tight)
+template <int TYPE, bool PRESEL>
 __device__ void gu_wg(const DecArgs& a, unsigned char* smem)
 {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, NT = blockDim.x, NWV = NT >> 6;
@@ -1167,6 +1201,9 @@ __device__ void gu_wg(const DecArgs& a, unsigned char* smem)
     const int nsh = a.sgu.rg ? (a.T + DROWS - 1) / DROWS * a.sgu.rg : 0;
     const int total = nsh + a.max_tiles * a.gu.rg;
     int u = routing ? total : (int)blockIdx.x;
+    // this wave's token's selection inputs (tokens past the waves load theirs at the selection)
+    SelIn sin;
+    if (PRESEL && wave < a.T) sel_issue(a, wave, sin);
     if (u < nsh) {
         for (; u < nsh; u += G) shared_gu_wg<TYPE>(a, u / a.sgu.rg, u % a.sgu.rg, smem);
         if (u >= total) return;  // uniform: no barriers follow
@@ -1180,7 +1217,8 @@ __device__ void gu_wg(const DecArgs& a, unsigned char* smem)
     if (tid == 0) s_misc[1] = 0;
     __syncthreads();
     for (int t = wave; t < a.T; t += NWV) {
-        const bool cert = wave_topk(a, t, s_ids, s_kb + wave * 32, s_kb + wave * 32 + 16);
+        if (!PRESEL || t != wave) sel_issue(a, t, sin);
+        const bool cert = wave_topk(a, t, sin, s_ids, s_kb + wave * 32, s_kb + wave * 32 + 16);
         if (lane == 0) {
             s_misc[2 + t] = !cert;
             if (!cert) s_misc[1] = 1;
@@ -1242,12 +1280,12 @@ __device__ void gu_wg(const DecArgs& a, unsigned char* smem)
 }
 
 // NTMAX: the workgroup-size bound the compiler allocates registers for (768 gives the unit loop the
-// registers it needs without scratch; 1024 for the widest rows)
+// registers it needs without scratch, and room for the early selection loads; 1024 for the widest rows)
 template <int TYPE, int NTMAX>
 __global__ __launch_bounds__(NTMAX) void k_dec_gu(DecArgs a)
 {
     extern __shared__ __align__(16) unsigned char dsm[];
-    gu_wg<TYPE>(a, dsm);  // shared and expert units, or (the last workgroup) the routing outputs
+    gu_wg<TYPE, (NTMAX <= 768)>(a, dsm);  // shared and expert units, or (the last workgroup) the routing outputs
 }
 
 // ------------------------------------------------------------------------------ k_dec_down
@@ -1508,12 +1546,13 @@ template <int T> struct KDown { static constexpr auto fn = k_dec_down<T>; };
 
 void launch_dec_route(hipStream_t st, const DecLayerH& h)
 {
-    launch(k_dec_route, dim3(h.T * h.E), dim3(RT_NT), (uint32_t)((size_t)3 * (h.d + 4) * 4), st, dec_args(h));
+    launch(k_dec_route, dim3(h.T * h.E), dim3(RT_NT), (uint32_t)((size_t)3 * route_row_floats(h.d) * 4), st,
+           dec_args(h));
 }
 
 void launch_dec_route_fused(hipStream_t st, const DecLayerH& prev, const DecLayerH& h)
 {
-    const size_t lds = (size_t)5 * (h.d + 4) * 4;
+    const size_t lds = ((size_t)3 * route_row_floats(h.d) + 2 * (h.d + 4)) * 4;
     raise_lds(k_dec_route_fused, lds);
     CombArgs cb;
     cb.d = prev.d;
