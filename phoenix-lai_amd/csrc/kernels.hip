@@ -14,7 +14,8 @@ namespace phx {
 
 // Quantize one row (in LDS, `cols` floats) into format act, row index `row`.  Block-level (NT threads).
 //  Q8_0: CpuRef.QuantizeQ8_0 (src/CpuRef.cs:49-62), plus the block sum of q for the Q4_0 offset.
-//  K4/K6: CpuRef.QuantizeQ8_K (src/CpuRefKQuants.cs:53-86), stored in the dot-product orders.
+//  K4/K6/Q8K: CpuRef.QuantizeQ8_K (src/CpuRefKQuants.cs:53-86), stored in the dot-product orders (and,
+//  with qh / bh set, the matrix cores' fp16 copies).
 template <int NT>
 __device__ void quantize_row(const float* v, Act act, int64_t row)
 {
@@ -60,6 +61,21 @@ __device__ void quantize_row(const float* v, Act act, int64_t row)
             return t < 127 ? t : 127;
         };
         act.d[row * act.dstride + b] = amax == 0.0f ? 0.0f : 1.0f / iscale;
+        if (act.qh) {  // the matrix cores' copy: exact fp16 integers, halves [l][s][mm'] of the super-block
+            uint32_t* hq = (uint32_t*)(act.qh + row * act.qhstride + (int64_t)b * 256);
+            for (int l = 0; l < 8; l++)
+                for (int s = 0; s < 8; s++) {
+                    const int e = 32 * s + l;
+                    hq[l * 16 + s * 2] = f2h_bits((float)qv(e)) | (f2h_bits((float)qv(e + 16)) << 16);
+                    hq[l * 16 + s * 2 + 1] = f2h_bits((float)qv(e + 8)) | (f2h_bits((float)qv(e + 24)) << 16);
+                }
+        }
+        if (act.bh)  // block sums of 16 (|sum| <= 2048: exact in fp16)
+            for (int j = 0; j < 16; j++) {
+                int sum = 0;
+                for (int i = 0; i < 16; i++) sum += qv(16 * j + i);
+                act.bh[row * act.bhstride + b * 16 + j] = (uint16_t)f2h_bits((float)sum);
+            }
         if (act.fmt == ACT_K4) {
             uint32_t* dst = (uint32_t*)(act.q + row * act.qstride + b * 256);
             for (int s = 0; s < 8; s++)

@@ -1,4 +1,5 @@
-// Prefill-shaped grouped products on the matrix cores (gfx950 MFMA), Q4_0 and Q8_0 weights.
+// Prefill-shaped grouped products on the matrix cores (gfx950 MFMA): Q4_0 and Q8_0 weights
+// (k_grouped_mfma), Q4_K and Q6_K weights (k_grouped_kmma, further down).
 //
 // The reference row dot is, per 32-element block b, sum += (float)isum_b * (d_w * d_x) in block
 // order (src/CpuRefGemma.cs:27-36, src/CpuRef.cs:106-115).  Per block and 32 x 32 (row, token) tile:
@@ -460,6 +461,390 @@ void launch_grouped_mfma(hipStream_t st, const QMat& w, Act act, const Tile* til
     const dim3 grid((w.rg + 1) / 2, max_tiles);
     if (w.type == PHX_Q4_0_DEV) launch(k_grouped_mfma<PHX_Q4_0_DEV>, grid, dim3(256), 0, st, g);
     else launch(k_grouped_mfma<PHX_Q8_0_DEV>, grid, dim3(256), 0, st, g);
+}
+
+// ============================================================================ K-quant products
+// DotK (src/CpuRefKQuants.cs:177-212) per (row, assignment): per 256-element super-block the eight
+// integer lanes aux32[l] = sum over the 32 elements e = 8 i + l of scale(e) * a(e) * x(e), the float
+// lanes sums[l] += (d * yd) * aux32[l], for Q4_K the min term sumf -= (dmin * yd) * sumi with
+// sumi = sum_j bsum_j * min(j / 2); after the last super-block sumf += sums[l] in l order.
+// Per super-block and 16 x 16 (row, assignment) tile on the matrix cores:
+//   - aux32[l] is one v_mfma_f32_16x16x32_f16 over lane l's 32 elements: the weights enter as
+//     scale * a, the activations as their Q8_K integers, all exact in fp16 (Q4_K: scale * a <= 945),
+//     and every partial sum is an integer of magnitude at most 2^24, exact in fp32 in any order.
+//     Q6_K's scale * a reaches 4096, past fp16's exact odd integers: with scale = 32 hi + lo
+//     (lo = 0..31) it enters as lo * a (|.| <= 992) and 32 hi * a (a multiple of 32, |.| <= 4096),
+//     two products into one accumulator;
+//   - sumi is one v_mfma_f32_16x16x16_f16 of the mins against the fp16 block sums (|bsum| <= 2048);
+//   - the float chain runs on VALU in the reference's order, so results equal DotK bit for bit.
+// Operand layouts (gfx950): v_mfma_f32_16x16x32_f16 A lane l holds row l % 16 and k = 8 (l / 16) + e,
+// e = 0..7, B lane l column l % 16 and the same k, and the 16 x 16 result D[i][j] sits in lane
+// j + 16 (i / 4), register i % 4; v_mfma_f32_16x16x16_f16 the same with k = 4 (l / 16) + e, e = 0..3.
+// Lane quarter q's k = 8 q + e is element 32 s + l + 8 mm of the super-block with s = 2 q + e / 4 and
+// mm = {0, 2, 1, 3}[e % 4]: the activations' fp16 copy holds, per row and super-block, the halves
+// [l][s][mm'] (x(32 s + l + 8 {0, 2, 1, 3}[mm'])), so a quarter's eight values are the 16-byte chunk
+// 4 l + q, and the repacked weights (bytes (s, l / 2, mm): low nibble l even, high nibble l odd) give
+// the pairs (mm 0, 2) and (mm 1, 3) of a byte-lane dword by one mask each.
+//
+// Work layout: a workgroup of eight waves covers two row groups (wave w: rows 16 (w % 4) .. + 15 of
+// row group 2 x + w / 4) and one tile of up to 32 assignments (two 16-assignment column tiles).  Per
+// super-block its operands reach LDS by direct loads into a ring slot, RING - 1 super-blocks ahead: the
+// activation chunks chunk-major ([chunk][assignment][16 B]: the 16 lanes of an operand read one
+// 256-byte run), Q4_K block sums and token scales, each wave's 16 weight rows and their scales.  Each
+// wave issues the same KM_DMA loads per super-block (some with lanes masked off), so its own count of
+// outstanding loads tells when a super-block has landed.
+constexpr int KM_TOK = 32;  // assignments per tile (kKmmaTile)
+static_assert(KM_TOK == kKmmaTile, "tile capacity");
+constexpr int KM_NW = 8;    // waves per workgroup
+constexpr int KM_DMA = 8;   // direct loads per wave per super-block
+
+template <int TYPE>
+struct KmSlot {
+    static constexpr bool Q4K = TYPE == PHX_Q4_K_DEV;
+    static constexpr int PAY = Q4K ? 144 : 208;
+    static constexpr int ACT = 0;                                // [32 chunks][32 assignments][16 B]
+    static constexpr int BSM = ACT + 32 * KM_TOK * 16;           // Q4_K: [4 quarters][32][4 fp16 bsums]
+    static constexpr int YD = BSM + (Q4K ? 4 * KM_TOK * 8 : 0);  // [32] token scales
+    static constexpr int W = YD + KM_TOK * 4;                    // [8 waves][16 rows][PAY]
+    static constexpr int WS = W + KM_NW * 16 * PAY;              // [8 waves][16 rows] 4-byte slots
+    static constexpr int BYTES = WS + KM_NW * 16 * 4;
+    static constexpr int RING = Q4K ? 4 : 3;
+};
+
+typedef _Float16 mh4 __attribute__((ext_vector_type(4)));
+typedef float mf4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint32_t pk_fma(uint32_t a, mh2 b, mh2 c)
+{
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(mh2, a), b, c));
+}
+__device__ __forceinline__ uint32_t pk_mul(uint32_t a, mh2 b)
+{
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(mh2, a) * b);
+}
+__device__ __forceinline__ uint32_t pk_add(uint32_t a, mh2 b)
+{
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(mh2, a) + b);
+}
+__device__ __forceinline__ mh2 hpair(_Float16 a, _Float16 b) { return mh2{a, b}; }
+// s_waitcnt vmcnt(n) alone (gfx9 encoding: vmcnt bits 3:0 and 15:14)
+constexpr int vm_wait(int n) { return (n & 15) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
+__device__ __forceinline__ void tie(u32x4& v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void tie(u32x2& v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void tie(uint32_t& v) { asm volatile("" : "+v"(v)); }
+
+template <int TYPE, int NJ>
+__device__ __forceinline__ void kmma_tile(const MmaArgs& g, const Tile& tl, int cnt, unsigned char* ring)
+{
+    using SL = KmSlot<TYPE>;
+    constexpr bool Q4K = SL::Q4K;
+    constexpr int PAY = SL::PAY, RING = SL::RING, SBY = Q4K ? 4 : 2;
+    const int tid = threadIdx.x, lane = tid & 63, r16 = lane & 15, q = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int gI = blockIdx.x * 2 + (wave >> 2), ws = wave & 3;
+    const bool live = gI < g.rg;  // a wave past the last row group computes a clamped one, stores nothing
+    const int nb = g.nb;
+    const uint32_t ring0 = (uint32_t)(uintptr_t)(lds_void_t)ring;
+
+    // the direct loads' lane sources at super-block 0 (assignments past cnt: a valid row, never stored)
+    auto arow = [&](int t) -> int64_t { return g.perm[tl.start + min(t, cnt - 1)] / g.act_div; };
+    // (1)(2) chunks 4 wave + 2 i + lane / 32 of assignment lane % 32
+    const uint16_t* xs = g.act.qh + arow(lane & 31) * g.act.qhstride + 8 * (4 * wave + (lane >> 5));
+    // (3) Q4_K: dword 32 wave + lane (lanes 0-31) of the block sums' [quarter][assignment][2 dwords]
+    const uint16_t* bsrc = nullptr;
+    if (Q4K) bsrc = g.act.bh + arow(16 * (wave & 1) + ((lane & 31) >> 1)) * g.act.bhstride + 4 * (wave >> 1) + 2 * (lane & 1);
+    // (4) token scales of assignments 4 wave + lane (lanes 0-3)
+    const float* ysrc = g.act.d + arow(4 * wave + (lane & 3)) * g.act.dstride;
+    // (5) the wave's 16 weight rows, 1 KB per load; (6) their scales (lanes 0-15)
+    const int gIc = min(gI, g.rg - 1);
+    const uint8_t* wsrc = g.payload + tl.e * g.mat_pay + gIc * g.rg_pay + 16 * ws * PAY + 16 * lane;
+    const uint8_t* ssrc = g.scale + tl.e * g.mat_sc + ((int64_t)gIc * nb * 64 + 16 * ws + r16) * SBY;
+
+#define KM_DMA_LOAD(src, lds_off, size) \
+    __builtin_amdgcn_global_load_lds((glb_void_t)(src), (lds_void_t)(ring + (lds_off)), size, 0, 0)
+    auto dma16 = [&](const void* src, uint32_t lds_off) { KM_DMA_LOAD(src, lds_off, 16); };
+    auto dma4 = [&](const void* src, uint32_t lds_off) { KM_DMA_LOAD(src, lds_off, 4); };
+    auto dma2 = [&](const void* src, uint32_t lds_off) { KM_DMA_LOAD(src, lds_off, 2); };
+#undef KM_DMA_LOAD
+    auto issue = [&](int b) {  // super-block b (clamped: past the end a harmless reload) into its slot
+        const int bc = min(b, nb - 1);
+        const uint32_t slot = (uint32_t)(b % RING) * SL::BYTES;
+        const uint8_t* wb = wsrc + (int64_t)bc * 64 * PAY;
+        const uint32_t wl = slot + SL::W + wave * 16 * PAY;
+        dma16(xs + (int64_t)bc * 256, slot + SL::ACT + (4 * wave) * 512);
+        dma16(xs + (int64_t)bc * 256 + 16, slot + SL::ACT + (4 * wave + 2) * 512);
+        if (Q4K) {
+            if (lane < 32) dma4(bsrc + (int64_t)bc * 16, slot + SL::BSM + 128 * wave);
+        } else {
+            if (lane < 16) dma16(wb + 3072, wl + 3072);  // Q6_K rows: 3328 bytes
+        }
+        if (lane < 4) dma4(ysrc + bc, slot + SL::YD + 16 * wave);
+        dma16(wb, wl);
+        dma16(wb + 1024, wl + 1024);
+        if (Q4K) {
+            if (lane < 16) dma16(wb + 2048, wl + 2048);  // Q4_K rows: 2304 bytes
+        } else {
+            dma16(wb + 2048, wl + 2048);
+        }
+        if (lane < 16) {
+            if (Q4K) dma4(ssrc + (int64_t)bc * 64 * SBY, slot + SL::WS + 64 * wave);
+            else dma2(ssrc + (int64_t)bc * 64 * SBY, slot + SL::WS + 64 * wave);
+        }
+    };
+    // super-block b has landed once at most the later ones' loads are outstanding; the barrier then
+    // publishes it and ends every wave's reads of the slot that issue(b + RING - 1) refills
+    auto land = [&](int b) {
+        __builtin_amdgcn_s_waitcnt(vm_wait(KM_DMA * (RING - 2)));
+        __builtin_amdgcn_s_barrier();
+        issue(b + RING - 1);
+    };
+
+    float sums[8][NJ][4], sumf[NJ][4];
+#pragma unroll
+    for (int c = 0; c < NJ; c++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            sumf[c][v] = 0.0f;
+#pragma unroll
+            for (int l = 0; l < 8; l++) sums[l][c][v] = 0.0f;
+        }
+    const mf4 zero4 = {};
+    // the lane's LDS read offsets within a slot
+    const uint32_t o_act = SL::ACT + q * 512 + r16 * 16;
+    const uint32_t o_bs = SL::BSM + q * 256 + r16 * 8;
+    const uint32_t o_yd = SL::YD + r16 * 4;
+    const uint32_t o_row = SL::W + (wave * 16 + r16) * PAY;
+    const uint32_t o_ws = SL::WS + (wave * 16 + 4 * q) * 4;
+
+#pragma unroll
+    for (int b = 0; b < RING - 1; b++) issue(b);
+    for (int b = 0; b < nb; b++) {
+        land(b);
+        const uint32_t sb = ring0 + (uint32_t)(b % RING) * SL::BYTES;
+        // the super-block's weights, row scales, token scales, block sums and the first operands
+        u32x4 D0 = ds_r128(sb + o_row + 32 * q), D1 = ds_r128<16>(sb + o_row + 32 * q);
+        // Q4_K: X.x the dword of sc[2 q], sc[2 q + 1], Y that of mins[2 q], mins[2 q + 1];
+        // Q6_K: X the high-bit dwords (s = 2 q: lq 0, 1; s = 2 q + 1: lq 0, 1), Y sc[4 q .. 4 q + 3]
+        // (a read's result is used only after its wait, never first composed into another value)
+        u32x4 X;
+        uint32_t X0;
+        if (Q4K) X0 = ds_r32(sb + o_row + 128 + 4 * (q >> 1));
+        else X = ds_r128(sb + o_row + 128 + 16 * q);
+        uint32_t Y = Q4K ? ds_r32<8>(sb + o_row + 128 + 4 * (q >> 1)) : ds_r32(sb + o_row + 192 + 4 * q);
+        u32x4 WSV = ds_r128(sb + o_ws);
+        uint32_t YD[NJ];
+        u32x2 BS[NJ];
+        u32x4 B[2][NJ];
+        const uint32_t a_act = sb + o_act;
+#pragma unroll
+        for (int c = 0; c < NJ; c++) {
+            YD[c] = c == 0 ? ds_r32(sb + o_yd) : ds_r32<64>(sb + o_yd);
+            if (Q4K) BS[c] = c == 0 ? ds_r64(sb + o_bs) : ds_r64<128>(sb + o_bs);
+            B[0][c] = c == 0 ? ds_r128(a_act) : ds_r128<256>(a_act);
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        tie(D0);
+        tie(D1);
+        if (Q4K) tie(X0);
+        else tie(X);
+        tie(Y);
+        tie(WSV);
+#pragma unroll
+        for (int c = 0; c < NJ; c++) {
+            tie(YD[c]);
+            if (Q4K) tie(BS[c]);
+            tie(B[0][c]);
+        }
+        // d * yd (and dmin * yd) per (row 4 q + v, assignment)
+        float dd[NJ][4], dm[NJ][4];
+#pragma unroll
+        for (int c = 0; c < NJ; c++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const float yd = __uint_as_float(YD[c]);
+                dd[c][v] = h2f(WSV[v] & 0xFFFFu) * yd;
+                if (Q4K) dm[c][v] = h2f(WSV[v] >> 16) * yd;
+            }
+        // per-s constants of the A operands (s = 2 q, 2 q + 1)
+        mh2 K0[2], M0[2], K1[2], M1[2];  // Q4_K: even l (K0, M0), odd l (K1, M1); Q6_K: lo, -1056 lo, 32 hi
+        if (Q4K) {
+            const uint32_t sw = X0 >> (16 * (q & 1));  // sc[2 q], sc[2 q + 1]
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const _Float16 f = (_Float16)(int)((sw >> (8 * j)) & 0xFFu);
+                K0[j] = hpair(f, f);
+                M0[j] = hpair(f * (_Float16)-1024.0f, f * (_Float16)-1024.0f);
+                K1[j] = hpair(f * (_Float16)0.0625f, f * (_Float16)0.0625f);
+                M1[j] = hpair(f * (_Float16)-64.0f, f * (_Float16)-64.0f);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 2; j++) {  // sc[4 q + 2 j], sc[4 q + 2 j + 1]
+                const int s0 = (int)(int8_t)(Y >> (16 * j)), s1 = (int)(int8_t)(Y >> (16 * j + 8));
+                const _Float16 lo0 = (_Float16)(s0 & 31), lo1 = (_Float16)(s1 & 31);
+                K0[j] = hpair(lo0, lo1);
+                M0[j] = hpair(lo0 * (_Float16)-1056.0f, lo1 * (_Float16)-1056.0f);
+                K1[j] = hpair((_Float16)(32 * (s0 >> 5)), (_Float16)(32 * (s1 >> 5)));
+            }
+        }
+        const mh2 m1056 = hpair((_Float16)-1056.0f, (_Float16)-1056.0f);
+        // lane l's A operand(s): pairs (s = 2 q: mm 0, 2), (mm 1, 3), then s = 2 q + 1
+        auto a_op = [&](int l, mh8& A, mh8& A2) {
+            const int p = l >> 1;
+            const uint32_t x0 = D0[p], x1 = D1[p];
+            uint32_t w[4];
+            if (Q4K) {
+                const uint32_t m = (l & 1) ? 0x00F000F0u : 0x000F000Fu;
+                const mh2 k0 = (l & 1) ? K1[0] : K0[0], c0 = (l & 1) ? M1[0] : M0[0];
+                const mh2 k1 = (l & 1) ? K1[1] : K0[1], c1 = (l & 1) ? M1[1] : M0[1];
+                w[0] = pk_fma((x0 & m) | 0x64006400u, k0, c0);
+                w[1] = pk_fma(((x0 >> 8) & m) | 0x64006400u, k0, c0);
+                w[2] = pk_fma((x1 & m) | 0x64006400u, k1, c1);
+                w[3] = pk_fma(((x1 >> 8) & m) | 0x64006400u, k1, c1);
+                A = __builtin_bit_cast(mh8, make_uint4(w[0], w[1], w[2], w[3]));
+            } else {
+                const int i = l & 3, lq = l >> 2;
+                const uint32_t h0 = X[lq], h1 = X[2 + lq];
+                auto lo = [&](uint32_t x, int pr) { return (l & 1) ? x >> (4 + 8 * pr) : x >> (8 * pr); };
+                auto hi = [&](uint32_t h, int pr) {
+                    return pr ? h >> (4 + 2 * i) : (i == 3 ? h >> 2 : h << (4 - 2 * i));
+                };
+                uint32_t v[4];
+                v[0] = (hi(h0, 0) & 0x00300030u) | ((lo(x0, 0) & 0x000F000Fu) | 0x64006400u);
+                v[1] = (hi(h0, 1) & 0x00300030u) | ((lo(x0, 1) & 0x000F000Fu) | 0x64006400u);
+                v[2] = (hi(h1, 0) & 0x00300030u) | ((lo(x1, 0) & 0x000F000Fu) | 0x64006400u);
+                v[3] = (hi(h1, 1) & 0x00300030u) | ((lo(x1, 1) & 0x000F000Fu) | 0x64006400u);
+                uint32_t u[4];
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    w[j] = pk_fma(v[j], K0[j >> 1], M0[j >> 1]);       // lo * (q6 - 32)
+                    u[j] = pk_mul(pk_add(v[j], m1056), K1[j >> 1]);  // 32 hi * (q6 - 32)
+                }
+                A = __builtin_bit_cast(mh8, make_uint4(w[0], w[1], w[2], w[3]));
+                A2 = __builtin_bit_cast(mh8, make_uint4(u[0], u[1], u[2], u[3]));
+            }
+        };
+#pragma unroll
+        for (int l = 0; l < 8; l++) {
+            const int cur = l & 1;
+            if (l + 1 < 8)  // the next lane's operands behind this one's products
+#pragma unroll
+                for (int c = 0; c < NJ; c++) B[cur ^ 1][c] = ds_r128(a_act + (l + 1) * 2048 + c * 256);
+            mh8 A, A2;
+            a_op(l, A, A2);
+#pragma unroll
+            for (int c = 0; c < NJ; c++) {
+                mf4 C = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, __builtin_bit_cast(mh8, B[cur][c]), zero4, 0, 0, 0);
+                if (!Q4K) C = __builtin_amdgcn_mfma_f32_16x16x32_f16(A2, __builtin_bit_cast(mh8, B[cur][c]), C, 0, 0, 0);
+                // the reference chain: sums[l] += (d * yd) * aux32[l]
+#pragma unroll
+                for (int v = 0; v < 4; v++) sums[l][c][v] = sums[l][c][v] + dd[c][v] * C[v];
+            }
+            if (l + 1 < 8) {
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+                for (int c = 0; c < NJ; c++) tie(B[cur ^ 1][c]);
+            }
+        }
+        if (Q4K) {  // the min term: sumf -= (dmin * yd) * sumi
+            const uint32_t mw = Y >> (16 * (q & 1));  // mins[2 q], mins[2 q + 1]
+            const _Float16 m0 = (_Float16)(int)(mw & 0xFFu), m1 = (_Float16)(int)((mw >> 8) & 0xFFu);
+            const mh4 Am = {m0, m0, m1, m1};
+#pragma unroll
+            for (int c = 0; c < NJ; c++) {
+                const mf4 Cm = __builtin_amdgcn_mfma_f32_16x16x16f16(Am, __builtin_bit_cast(mh4, BS[c]), zero4, 0, 0, 0);
+#pragma unroll
+                for (int v = 0; v < 4; v++) sumf[c][v] = sumf[c][v] - dm[c][v] * Cm[v];
+            }
+        }
+    }
+    // the loads issued past the last super-block land in this workgroup's LDS: let them finish
+    __builtin_amdgcn_s_waitcnt(0);
+    if (!live) return;
+    // lane (r16, q): assignment 16 c + r16, rows 4 q .. 4 q + 3 of the wave's 16
+#pragma unroll
+    for (int c = 0; c < NJ; c++) {
+        const int t = 16 * c + r16;
+        if (t >= cnt) continue;
+        float o[4];
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            float s = sumf[c][v];
+#pragma unroll
+            for (int l = 0; l < 8; l++) s += sums[l][c][v];
+            o[v] = s;
+        }
+        const int64_t a = g.perm[tl.start + t];
+        const int lg0 = 16 * ws + 4 * q;  // lane within the row group of the first of four
+        const bool vec = (g.out_stride & 3) == 0;
+        if (g.paired) {
+            const int col = gI * 32 + (lg0 & 31);
+            float* dst = (lg0 < 32 ? g.out0 : g.out1) + a * g.out_stride + col;
+            if (vec && col + 3 < g.split) *(float4*)dst = make_float4(o[0], o[1], o[2], o[3]);
+            else
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    if (col + i < g.split) dst[i] = o[i];
+        } else {
+            const int row = gI * 64 + lg0;
+            if (vec && row + 3 < min(g.rows, g.split)) *(float4*)(g.out0 + a * g.out_stride + row) = make_float4(o[0], o[1], o[2], o[3]);
+            else
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int r = row + i;
+                    if (r < g.rows) {
+                        if (r < g.split) g.out0[a * g.out_stride + r] = o[i];
+                        else g.out1[a * g.out_stride + r - g.split] = o[i];
+                    }
+                }
+        }
+    }
+}
+
+template <int TYPE>
+__global__ __launch_bounds__(KM_NW * 64, 1) void k_grouped_kmma(MmaArgs g)
+{
+    extern __shared__ __align__(16) unsigned char kring[];
+    const int tile = blockIdx.y;
+    if (tile >= *g.ntiles) return;  // uniform over the workgroup
+    const Tile tl = g.tiles[tile];
+    const int cnt = min(tl.cnt, KM_TOK);
+    if (cnt > 16) kmma_tile<TYPE, 2>(g, tl, cnt, kring);
+    else kmma_tile<TYPE, 1>(g, tl, cnt, kring);
+}
+
+void launch_grouped_kmma(hipStream_t st, const QMat& w, Act act, const Tile* tiles, const int* ntiles, int max_tiles,
+                         const int* perm, int act_div, float* out0, float* out1, int split, int out_stride)
+{
+    MmaArgs g{};
+    g.payload = w.payload;
+    g.scale = w.scale;
+    g.mat_pay = w.mat_pay_stride();
+    g.rg_pay = w.rg_pay;
+    g.mat_sc = w.mat_sc_stride();
+    g.rg = w.rg;
+    g.nb = w.nb;
+    g.rows = w.rows;
+    g.act = act;
+    g.tiles = tiles;
+    g.ntiles = ntiles;
+    g.perm = perm;
+    g.act_div = act_div;
+    g.out0 = out0;
+    g.out1 = out1;
+    g.split = split;
+    g.out_stride = out_stride;
+    g.paired = w.paired;
+    const dim3 grid((w.rg + 1) / 2, max_tiles);
+    if (w.type == PHX_Q4_K_DEV) {
+        constexpr size_t lds = (size_t)KmSlot<PHX_Q4_K_DEV>::RING * KmSlot<PHX_Q4_K_DEV>::BYTES;
+        (void)hipFuncSetAttribute((const void*)k_grouped_kmma<PHX_Q4_K_DEV>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        launch(k_grouped_kmma<PHX_Q4_K_DEV>, grid, dim3(KM_NW * 64), (uint32_t)lds, st, g);
+    } else {
+        constexpr size_t lds = (size_t)KmSlot<PHX_Q6_K_DEV>::RING * KmSlot<PHX_Q6_K_DEV>::BYTES;
+        (void)hipFuncSetAttribute((const void*)k_grouped_kmma<PHX_Q6_K_DEV>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        launch(k_grouped_kmma<PHX_Q6_K_DEV>, grid, dim3(KM_NW * 64), (uint32_t)lds, st, g);
+    }
 }
 
 }  // namespace phx

@@ -99,8 +99,12 @@ struct Act {
     int dstride = 0;      // floats per row
     int* s = nullptr;
     int sstride = 0;      // ints per row
-    uint16_t* qh = nullptr;  // ACT_Q8_0, optional: the same integers as fp16 bits [row][cols] (for MFMA)
+    uint16_t* qh = nullptr;  // optional: the same integers as fp16 bits [row][cols] (for MFMA); ACT_Q8_0 in
+                             // element order, the K formats per super-block in the order [l][s][mm']:
+                             // x(32 s + l + 8 {0, 2, 1, 3}[mm'])
     int64_t qhstride = 0;    // halves per row
+    uint16_t* bh = nullptr;  // optional, K formats: the Q8_K block sums as fp16 [row][cols / 16]
+    int64_t bhstride = 0;    // halves per row
 };
 
 struct Tile { int e, start, cnt; };
@@ -139,6 +143,12 @@ void launch_grouped_mfma(hipStream_t st, const QMat& w, Act act, const Tile* til
                          const int* perm, int act_div, float* out0, float* out1, int split, int out_stride,
                          int64_t npos = 0, const Act* qout = nullptr, int64_t qnpos = 0,
                          const float* gelu_tab = nullptr);
+// K-quant prefill path (kernels_prefill.hip): Q4_K / Q6_K grouped products on MFMA, tiles of up to
+// kKmmaTile assignments, activations' fp16 copies (qh; Q4_K also bh) in row order; arguments and outputs
+// as launch_grouped
+constexpr int kKmmaTile = 32;
+void launch_grouped_kmma(hipStream_t st, const QMat& w, Act act, const Tile* tiles, const int* ntiles, int max_tiles,
+                         const int* perm, int act_div, float* out0, float* out1, int split, int out_stride);
 void launch_combine(hipStream_t st, int T, int d, int k, float eps, const float* yd, const float* w,
                     const float* shared, const float* post1, const float* post2, float* out, float* x_resid,
                     const float* post_ffw, int* flags);

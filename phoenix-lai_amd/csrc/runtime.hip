@@ -344,7 +344,7 @@ enum WsId {
     W_X, W_SHARED, W_OUT, W_RIN, W_XSCALE, W_AGU_Q, W_AGU_D, W_AGU_S, W_ASH_Q, W_ASH_D, W_ASH_S, W_LOGITS, W_IDS, W_W,
     W_OFF, W_PERM, W_TILES, W_NTILES, W_G, W_U, W_ADN_Q, W_ADN_D, W_ADN_S, W_YD, W_SHG, W_SHU, W_ASD_Q, W_ASD_D,
     W_ASD_S, W_SHOUT, W_ZERO, W_STILES, W_SNTILES, W_SOFF, W_SPERM, W_LB, W_BB, W_ADEC, W_SDEC, W_AGUP, W_ASHP, W_AGU_H, W_ADN_H, W_ASH_H, W_ASD_H, W_X2,
-    W_MM_IDS, W_MM_OFF, W_MM_PERM, W_MM_TILES, W_MM_NT, W_MM_D, W_MM_S, W_MM_H, W_COUNT
+    W_MM_IDS, W_MM_OFF, W_MM_PERM, W_MM_TILES, W_MM_NT, W_MM_D, W_MM_S, W_MM_H, W_AGU_BH, W_ADN_BH, W_COUNT
 };
 
 int ensure(phx_moe_ctx* c, int id, size_t bytes)
@@ -427,6 +427,7 @@ int ensure_act(phx_moe_ctx* c, int fmt, int64_t rows, int cols, int qid, int did
 constexpr int kTileA = 4;  // assignments per grouped tile
 
 bool mfma_type(int t);
+bool kmma_type(int t) { return t == PHX_Q4_K || t == PHX_Q6_K; }
 
 int ensure_workspace(phx_moe_ctx* c, const Layer& L, int T)
 {
@@ -455,9 +456,14 @@ int ensure_workspace(phx_moe_ctx* c, const Layer& L, int T)
     ENS(W_YD, n * D.d * 4);
     if ((rc = ensure_act(c, act_fmt(D.gate_up_type), T, D.d, W_AGU_Q, W_AGU_D, W_AGU_S))) return rc;
     if ((rc = ensure_act(c, act_fmt(D.down_type), n, D.down_cols, W_ADN_Q, W_ADN_D, W_ADN_S))) return rc;
-    if (mfma_type(D.gate_up_type) && mfma_type(D.down_type)) {  // the MFMA path's fp16 activation copies
+    if ((mfma_type(D.gate_up_type) && mfma_type(D.down_type)) || (kmma_type(D.gate_up_type) && kmma_type(D.down_type))) {
+        // the matrix-core paths' fp16 activation copies (and the K path's fp16 block sums)
         ENS(W_AGU_H, (size_t)T * D.d * 2);
         ENS(W_ADN_H, (size_t)n * D.down_cols * 2);
+        if (kmma_type(D.gate_up_type)) {
+            ENS(W_AGU_BH, (size_t)T * (D.d / 16) * 2);
+            ENS(W_ADN_BH, (size_t)n * (D.down_cols / 16) * 2);
+        }
     }
     if (D.n_ff_shared > 0) {
         int scols = round_up(D.n_ff_shared, block_elems(D.shared_type));
@@ -656,11 +662,16 @@ int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, con
     // prefill-sized expert work (several assignments per expert on average) runs on the matrix cores,
     // whose kernels read the activations' fp16 copies
     const bool mma = mfma_type(D.gate_up_type) && mfma_type(D.down_type) && n >= 8 * E;
+    const bool kmma = kmma_type(D.gate_up_type) && kmma_type(D.down_type) && n >= 8 * E;
     const bool smma = shared_ffn && mfma_type(D.shared_type) && T >= 32;
     Act agu = make_act(c, act_fmt(D.gate_up_type), d, W_AGU_Q, W_AGU_D, W_AGU_S);
-    if (mma) {
+    if (mma || kmma) {
         agu.qh = wp<uint16_t>(c, W_AGU_H);
         agu.qhstride = d;
+    }
+    if (kmma && D.gate_up_type == PHX_Q4_K) {
+        agu.bh = wp<uint16_t>(c, W_AGU_BH);
+        agu.bhstride = d / 16;
     }
     Act ash;
     if (shared_ffn) ash = make_act(c, act_fmt(D.shared_type), d, W_ASH_Q, W_ASH_D, W_ASH_S);
@@ -682,9 +693,9 @@ int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, con
         ProfScope p(c, PHX_K_TOPK);
         launch_topk(st, T, E, k, D.weight_rule, wp<float>(c, W_LOGITS), L.ds, wp<int>(c, W_IDS), wp<float>(c, W_W));
     }
-    // tile sizes: the MFMA kernel's 128, the VALU kernels' 4 (their row walk is VALU-bound: larger
-    // tiles cost occupancy and measured slower)
-    const int tileA = mma ? kMmaTile : kTileA;
+    // tile sizes: the MFMA kernels' 128 (Q4_0 / Q8_0) and 32 (K-quants), the VALU kernels' 4 (their row
+    // walk is VALU-bound: larger tiles cost occupancy and measured slower)
+    const int tileA = mma ? kMmaTile : kmma ? kKmmaTile : kTileA;
     const int max_tiles = std::min(n, (n + tileA - 1) / tileA + E);
     {
         ProfScope p(c, PHX_K_DISPATCH);
@@ -692,15 +703,22 @@ int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, con
                         wp<int>(c, W_NTILES));
     }
     Act adn = make_act(c, act_fmt(D.down_type), D.down_cols, W_ADN_Q, W_ADN_D, W_ADN_S);
-    if (mma) {
+    if (mma || kmma) {
         adn.qh = wp<uint16_t>(c, W_ADN_H);
         adn.qhstride = D.down_cols;
+    }
+    if (kmma && D.down_type == PHX_Q4_K) {
+        adn.bh = wp<uint16_t>(c, W_ADN_BH);
+        adn.bhstride = D.down_cols / 16;
     }
     {
         ProfScope p(c, PHX_K_GATE_UP);
         if (mma)  // the matrix-core gate|up also writes the down input (GELU-gated Q8_0, list order)
             launch_grouped_mfma(st, L.gu, agu, wp<Tile>(c, W_TILES), wp<int>(c, W_NTILES), max_tiles, wp<int>(c, W_PERM), k,
                                 wp<float>(c, W_G), wp<float>(c, W_U), nf, nf, 0, &adn, n, c->gelu_tab);
+        else if (kmma)
+            launch_grouped_kmma(st, L.gu, agu, wp<Tile>(c, W_TILES), wp<int>(c, W_NTILES), max_tiles, wp<int>(c, W_PERM), k,
+                                wp<float>(c, W_G), wp<float>(c, W_U), nf, nf);
         else
             launch_grouped(st, L.gu, agu, wp<Tile>(c, W_TILES), wp<int>(c, W_NTILES), max_tiles, tileA, wp<int>(c, W_PERM),
                            k, wp<float>(c, W_G), wp<float>(c, W_U), nf, nf);
@@ -714,6 +732,9 @@ int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, con
         if (mma)
             launch_grouped_mfma(st, L.dn, adn, wp<Tile>(c, W_TILES), wp<int>(c, W_NTILES), max_tiles, wp<int>(c, W_PERM), 1,
                                 wp<float>(c, W_YD), wp<float>(c, W_YD), d, d, n);
+        else if (kmma)
+            launch_grouped_kmma(st, L.dn, adn, wp<Tile>(c, W_TILES), wp<int>(c, W_NTILES), max_tiles, wp<int>(c, W_PERM), 1,
+                                wp<float>(c, W_YD), wp<float>(c, W_YD), d, d);
         else
             launch_grouped(st, L.dn, adn, wp<Tile>(c, W_TILES), wp<int>(c, W_NTILES), max_tiles, tileA, wp<int>(c, W_PERM),
                            1, wp<float>(c, W_YD), wp<float>(c, W_YD), d, d);

@@ -536,6 +536,29 @@ def test_mfma_grouped_products_bit_exact(ctx, pkg, orc, case):
     check_layer(ctx, orc, L, x, shared, tag=f"mfma {case}", exact=True)
 
 
+# K-quants on the matrix cores: n = T * k >= 8 * E; tiles of up to 32 assignments (one or two 16-wide
+# column tiles), Q4_K with its min term, Q6_K's split scales, either type on either product
+KMMA_CASES = {
+    "q4k_gu_q6k_dn_T96": (dict(idx=51, T=96, d=1024, E=8, k=2, nf=512, gu=12, dn=14), 96),
+    "q6k_gu_q4k_dn_T64": (dict(idx=52, T=64, d=768, E=4, k=2, nf=256, gu=14, dn=12), 64),
+    # nine paired row groups (a spare wave quartet) and down rows padded 288 -> 512
+    "q4k_q6k_odd_rows_T80": (dict(idx=53, T=80, d=1280, E=4, k=2, nf=288, gu=12, dn=14), 80),
+    "q4k_both_T40": (dict(idx=54, T=40, d=512, E=4, k=4, nf=512, gu=12, dn=12), 40),
+}
+
+
+@pytest.mark.parametrize("case", list(KMMA_CASES))
+def test_kmma_grouped_products_bit_exact(ctx, pkg, orc, case):
+    """The K-quant MFMA kernel keeps DotK's lane chains: gate/up/down rows and the outputs equal the CPU
+    reference bit for bit (exact router)."""
+    cfg, T = KMMA_CASES[case]
+    say(f"kmma {case}: T={T}")
+    L = pkg.synth.make_layer(cfg, norms="noisy")
+    x = pkg.synth.make_input(cfg, T=T)
+    ctx.upload(0, L)
+    check_layer(ctx, orc, L, x, tag=f"kmma {case}", exact=True)
+
+
 # ---------------------------------------------------------------------------------------- IQ formats
 IQ_CASES = {
     # gate|up, down (and the shared FFN) in the IQ formats (CpuRefIQuants.cs); n_ff 384 pads the down rows
