@@ -45,65 +45,83 @@ __device__ void quantize_row(const float* v, Act act, int64_t row)
         }
         return;
     }
-    int nb = act.cols / 256;
-    for (int b = tid; b < nb; b += NT) {
-        const float* x = v + b * 256;
-        float max = 0.0f, amax = 0.0f;
-        for (int j = 0; j < 256; j++) {
-            float ax = fabsf(x[j]);
-            if (ax > amax) { amax = ax; max = x[j]; }
-        }
-        // q(j) recomputed where it is needed: no private array
-        const float iscale = amax == 0.0f ? 0.0f : -127.0f / max;
-        auto qv = [&](int j) -> int {
-            if (amax == 0.0f) return 0;
-            int t = nearest_int(iscale * x[j]);
-            return t < 127 ? t : 127;
-        };
-        act.d[row * act.dstride + b] = amax == 0.0f ? 0.0f : 1.0f / iscale;
-        if (act.qh) {  // the matrix cores' copy: exact fp16 integers, halves [l][s][mm'] of the super-block
-            uint32_t* hq = (uint32_t*)(act.qh + row * act.qhstride + (int64_t)b * 256);
-            for (int l = 0; l < 8; l++)
-                for (int s = 0; s < 8; s++) {
-                    const int e = 32 * s + l;
-                    hq[l * 16 + s * 2] = f2h_bits((float)qv(e)) | (f2h_bits((float)qv(e + 16)) << 16);
-                    hq[l * 16 + s * 2 + 1] = f2h_bits((float)qv(e + 8)) | (f2h_bits((float)qv(e + 24)) << 16);
-                }
-        }
-        if (act.bh)  // block sums of 16 (|sum| <= 2048: exact in fp16)
-            for (int j = 0; j < 16; j++) {
-                int sum = 0;
-                for (int i = 0; i < 16; i++) sum += qv(16 * j + i);
-                act.bh[row * act.bhstride + b * 16 + j] = (uint16_t)f2h_bits((float)sum);
+    // Q8_K: one wave per 256-block, lane l holds elements 4l..4l+3; the block's integers pass through
+    // the wave's LDS row to reach the packed orders
+    __shared__ uint32_t qsm[NT / 64][64];
+    const int nb = act.cols / 256, lane = tid & 63, wave = tid >> 6;
+    const uint8_t* qb = (const uint8_t*)qsm[wave];
+    for (int b = wave; b < nb; b += NT / 64) {
+        const float4 v4 = ((const float4*)(v + b * 256))[lane];
+        const float x[4] = {v4.x, v4.y, v4.z, v4.w};
+        // the reference's scan: the first element of largest |x| (strict '>', from 0)
+        float amax = 0.0f, vmax = 0.0f;
+        int imax = 1 << 30;
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            if (fabsf(x[j]) > amax) {
+                amax = fabsf(x[j]);
+                vmax = x[j];
+                imax = 4 * lane + j;
             }
-        if (act.fmt == ACT_K4) {
-            uint32_t* dst = (uint32_t*)(act.q + row * act.qstride + b * 256);
-            for (int s = 0; s < 8; s++)
-                for (int l = 0; l < 8; l++) {
-                    uint32_t pk = 0;
-                    for (int m = 0; m < 4; m++) pk |= (uint32_t)(qv(32 * s + l + 8 * m) & 0xFF) << (8 * m);
-                    dst[s * 8 + l] = pk;
-                }
-            for (int j = 0; j < 16; j++) {
-                int sum = 0;
-                for (int i = 0; i < 16; i++) sum += qv(16 * j + i);
-                act.s[row * act.sstride + b * 16 + j] = sum;
+#pragma unroll
+        for (int m = 1; m < 64; m <<= 1) {
+            const float oa = __shfl_xor(amax, m, 64), ov = __shfl_xor(vmax, m, 64);
+            const int oi = __shfl_xor(imax, m, 64);
+            if (oa > amax || (oa == amax && oi < imax)) {
+                amax = oa;
+                vmax = ov;
+                imax = oi;
             }
-        } else if (act.fmt == ACT_Q8K) {
-            int8_t* dst = act.q + row * act.qstride + (int64_t)b * 256;
-            for (int j = 0; j < 256; j++) dst[j] = (int8_t)qv(j);
-        } else {
+        }
+        const float iscale = amax == 0.0f ? 0.0f : -127.0f / vmax;
+        int q[4], sm = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            q[j] = amax == 0.0f ? 0 : min(nearest_int(iscale * x[j]), 127);
+            sm += q[j];
+        }
+        const uint32_t pk = (uint32_t)(q[0] & 0xFF) | ((uint32_t)(q[1] & 0xFF) << 8) | ((uint32_t)(q[2] & 0xFF) << 16) |
+                            ((uint32_t)q[3] << 24);
+        if (lane == 0) act.d[row * act.dstride + b] = amax == 0.0f ? 0.0f : 1.0f / iscale;
+        // block sums of 16: lanes 4j .. 4j + 3
+        sm += __shfl_xor(sm, 1, 64);
+        sm += __shfl_xor(sm, 2, 64);
+        if ((lane & 3) == 0) {
+            if (act.fmt == ACT_K4) act.s[row * act.sstride + b * 16 + (lane >> 2)] = sm;
+            if (act.bh) act.bh[row * act.bhstride + b * 16 + (lane >> 2)] = (uint16_t)f2h_bits((float)sm);  // exact
+        }
+        if (act.fmt == ACT_Q8K) {
+            ((uint32_t*)(act.q + row * act.qstride + (int64_t)b * 256))[lane] = pk;
+            if (!act.qh) continue;  // uniform
+        }
+        qsm[wave][lane] = pk;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        auto qv = [&](int e) { return (int)(int8_t)qb[e]; };
+        if (act.fmt == ACT_K4) {  // dword (s, l) = x[32 s + l + 8 m], m = 0..3: lane = 8 s + l
+            const int s8 = lane >> 3, l = lane & 7, e = 32 * s8 + l;
+            ((uint32_t*)(act.q + row * act.qstride + (int64_t)b * 256))[lane] =
+                (uint32_t)qb[e] | ((uint32_t)qb[e + 8] << 8) | ((uint32_t)qb[e + 16] << 16) | ((uint32_t)qb[e + 24] << 24);
+        } else if (act.fmt == ACT_K6) {  // (P, l): lane = 8 P + l
+            const int P = lane >> 3, l = lane & 7, e = 32 * P + l;
             uint32_t* dst = (uint32_t*)(act.q + row * act.qstride + (int64_t)b * 512);
             int* c = act.s + row * act.sstride + b * 128;
-            for (int P = 0; P < 8; P++)
-                for (int l = 0; l < 8; l++) {
-                    int x0 = qv(32 * P + l), x1 = qv(32 * P + l + 8), x2 = qv(32 * P + 16 + l), x3 = qv(32 * P + 16 + l + 8);
-                    dst[(P * 8 + l) * 2 + 0] = (uint32_t)(x0 & 0xFF) | ((uint32_t)(x1 & 0xFF) << 8);
-                    dst[(P * 8 + l) * 2 + 1] = ((uint32_t)(x2 & 0xFF) << 16) | ((uint32_t)(x3 & 0xFF) << 24);
-                    c[(2 * P) * 8 + l] = -32 * (x0 + x1);
-                    c[(2 * P + 1) * 8 + l] = -32 * (x2 + x3);
-                }
+            dst[lane * 2 + 0] = (uint32_t)qb[e] | ((uint32_t)qb[e + 8] << 8);
+            dst[lane * 2 + 1] = ((uint32_t)qb[e + 16] << 16) | ((uint32_t)qb[e + 24] << 24);
+            c[(2 * P) * 8 + l] = -32 * (qv(e) + qv(e + 8));
+            c[(2 * P + 1) * 8 + l] = -32 * (qv(e + 16) + qv(e + 24));
         }
+        if (act.qh) {  // the matrix cores' copy: exact fp16 integers, halves [l][s][mm']: lane = 8 l + s
+            const int l = lane >> 3, s8 = lane & 7, e = 32 * s8 + l;
+            uint32_t* hq = (uint32_t*)(act.qh + row * act.qhstride + (int64_t)b * 256) + l * 16 + s8 * 2;
+            hq[0] = f2h_bits((float)qv(e)) | (f2h_bits((float)qv(e + 16)) << 16);
+            hq[1] = f2h_bits((float)qv(e + 8)) | (f2h_bits((float)qv(e + 24)) << 16);
+        }
+        // the row is rewritten by the next block's wave only after every lane's reads above
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
 }
 
@@ -212,28 +230,32 @@ __global__ __launch_bounds__(64) void k_router_exact(int T, int d, int E, const 
     }
 }
 
-// Many tokens: a workgroup of four waves takes 64 experts and 8 tokens; wave w carries tokens 2w and
-// 2w + 1, lane e expert e, each chain in index order (the reference's sequential sum).  The router
-// columns of the 64 experts and the 8 token rows of m stream through LDS in 128-element chunks (36 KB,
-// two buffers): every thread loads its share of the next chunk into registers before the current
-// chunk's adds and stores it after, one barrier per chunk.  W leaves L2 once per eight tokens and
-// reaches the lanes at the LDS rate, and with every operand read from LDS the reads of the next eight
-// columns can go out ahead of the current eight's adds (LDS reads complete in order).
-constexpr int RXW_TOK = 8, RXW_CH4 = 32;  // tokens per workgroup; float4 columns per chunk
+// Many tokens: a workgroup of four waves takes 64 experts and 4 TPW tokens; wave w carries tokens
+// TPW w .. TPW w + TPW - 1, lane e expert e, each chain in index order (the reference's sequential
+// sum).  The router columns of the 64 experts and the token rows of m stream through LDS in
+// 128-element chunks (two buffers): every thread loads its share of the next chunk into registers
+// before the current chunk's adds and stores it after, one barrier per chunk.  W leaves L2 once per
+// 4 TPW tokens and reaches the lanes at the LDS rate, and with every operand read from LDS the reads
+// of the next eight columns can go out ahead of the current eight's adds (LDS reads complete in
+// order).  TPW 2 halves W's traffic, TPW 1 doubles the waves (for fewer tokens).
+constexpr int RXW_CH4 = 32;  // float4 columns per chunk
+template <int TPW>
 __global__ __launch_bounds__(256, 2) void k_router_exact_wide(int T, int d, int E, const float4* __restrict__ wt4,
                                                               const float* __restrict__ rin,
                                                               float* __restrict__ logits)
 {
+    constexpr int TOK = 4 * TPW;
     __shared__ float4 wbuf[2][RXW_CH4][64];
-    __shared__ float4 mbuf[2][RXW_TOK][RXW_CH4];
+    __shared__ float4 mbuf[2][TOK][RXW_CH4];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int e0 = blockIdx.x * 64, e = e0 + lane;
-    const int tb = blockIdx.y * RXW_TOK, t0 = tb + 2 * wave;
+    const int tb = blockIdx.y * TOK, t0 = tb + TPW * wave;
     const int n4 = d / 4, nch = (n4 + RXW_CH4 - 1) / RXW_CH4;
     // this thread's share of a chunk: W columns (tid / 64) + 4 k, k = 0..7, of expert e0 + lane, and
-    // column tid % 32 of token row tid / 32
-    const int er = min(e, E - 1), cr = tid >> 6, mt = tid >> 5, mc = tid & 31;
+    // (threads below 32 TOK) column tid % 32 of token row tid / 32
+    const int er = min(e, E - 1), cr = tid >> 6, mt = min(tid >> 5, TOK - 1), mc = tid & 31;
+    const bool mld = tid < 32 * TOK;
     const float4* mrow = (const float4*)(rin + (int64_t)min(tb + mt, T - 1) * d);
     float4 st[8], sm;
 #pragma unroll
@@ -241,9 +263,11 @@ __global__ __launch_bounds__(256, 2) void k_router_exact_wide(int T, int d, int 
     sm = mrow[min(mc, n4 - 1)];
 #pragma unroll
     for (int k = 0; k < 8; k++) wbuf[0][cr + 4 * k][lane] = st[k];
-    mbuf[0][mt][mc] = sm;
+    if (mld) mbuf[0][mt][mc] = sm;
     __syncthreads();
-    float s0 = 0.0f, s1 = 0.0f;
+    float s[TPW];
+#pragma unroll
+    for (int j = 0; j < TPW; j++) s[j] = 0.0f;
     for (int c = 0; c < nch; c++) {
         const int buf = c & 1;
         // the next chunk's loads (past the last chunk: a clamped reload nobody reads)
@@ -252,44 +276,43 @@ __global__ __launch_bounds__(256, 2) void k_router_exact_wide(int T, int d, int 
         for (int k = 0; k < 8; k++) st[k] = wt4[(int64_t)min(cn + cr + 4 * k, n4 - 1) * E + er];
         sm = mrow[min(cn + mc, n4 - 1)];
         const int ni = min(RXW_CH4, n4 - c * RXW_CH4);  // d % 32 == 0: ni % 8 == 0
-        const float4* m0 = mbuf[buf][2 * wave];
-        const float4* m1 = mbuf[buf][2 * wave + 1];
 #pragma unroll 8
         for (int i = 0; i < ni; i++) {
             const float4 w = wbuf[buf][i][lane];
-            const float4 a = m0[i], b = m1[i];
-            s0 += w.x * a.x;
-            s1 += w.x * b.x;
-            s0 += w.y * a.y;
-            s1 += w.y * b.y;
-            s0 += w.z * a.z;
-            s1 += w.z * b.z;
-            s0 += w.w * a.w;
-            s1 += w.w * b.w;
+            float4 a[TPW];
+#pragma unroll
+            for (int j = 0; j < TPW; j++) a[j] = mbuf[buf][TPW * wave + j][i];
+#pragma unroll
+            for (int j = 0; j < TPW; j++) s[j] += w.x * a[j].x;
+#pragma unroll
+            for (int j = 0; j < TPW; j++) s[j] += w.y * a[j].y;
+#pragma unroll
+            for (int j = 0; j < TPW; j++) s[j] += w.z * a[j].z;
+#pragma unroll
+            for (int j = 0; j < TPW; j++) s[j] += w.w * a[j].w;
         }
 #pragma unroll
         for (int k = 0; k < 8; k++) wbuf[buf ^ 1][cr + 4 * k][lane] = st[k];  // read before the last barrier
-        mbuf[buf ^ 1][mt][mc] = sm;
+        if (mld) mbuf[buf ^ 1][mt][mc] = sm;
         __syncthreads();
     }
     if (e < E) {
-        if (t0 < T) logits[(int64_t)t0 * E + e] = s0;
-        if (t0 + 1 < T) logits[(int64_t)(t0 + 1) * E + e] = s1;
+#pragma unroll
+        for (int j = 0; j < TPW; j++)
+            if (t0 + j < T) logits[(int64_t)(t0 + j) * E + e] = s[j];
     }
 }
 
-// Fewer tokens: each lane carries TB tokens' sequential chains (each in index order, as the
-// reference): one read of W serves TB tokens and the independent chains fill the add latency.  The
-// token rows of m sit in LDS; W streams in 32-element chunks, the next chunk's loads issued before the
-// current chunk's adds.
+// Eight tokens per workgroup where that still makes 1024 workgroups, four from 64 tokens, below that
+// one wave per (64 experts, token) with the token's row of m in LDS.
 void launch_router_exact(hipStream_t st, int T, int d, int E, const float* wt4, const float* rin, float* logits)
 {
     const int gx = (E + 63) / 64;
     const float4* w = (const float4*)wt4;
-    if (T >= 1024)
-        launch(k_router_exact_wide, dim3(gx, (T + RXW_TOK - 1) / RXW_TOK), dim3(256), 0, st, T, d, E, w, rin, logits);
-    else if (T >= 128)
-        launch(k_router_exact<2>, dim3(gx, (T + 1) / 2), dim3(64), (uint32_t)(2 * d * 4), st, T, d, E, w, rin, logits);
+    if (T * gx >= 1024)  // enough workgroups at eight tokens each
+        launch(k_router_exact_wide<2>, dim3(gx, (T + 7) / 8), dim3(256), 0, st, T, d, E, w, rin, logits);
+    else if (T >= 64)
+        launch(k_router_exact_wide<1>, dim3(gx, (T + 3) / 4), dim3(256), 0, st, T, d, E, w, rin, logits);
     else
         launch(k_router_exact<1>, dim3(gx, T), dim3(64), (uint32_t)(d * 4), st, T, d, E, w, rin, logits);
 }

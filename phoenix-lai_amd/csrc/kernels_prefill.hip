@@ -487,28 +487,28 @@ void launch_grouped_mfma(hipStream_t st, const QMat& w, Act act, const Tile* til
 // the pairs (mm 0, 2) and (mm 1, 3) of a byte-lane dword by one mask each.
 //
 // Work layout: a workgroup of eight waves covers two row groups (wave w: rows 16 (w % 4) .. + 15 of
-// row group 2 x + w / 4) and one tile of up to 32 assignments (two 16-assignment column tiles).  Per
+// row group 2 x + w / 4) and one tile of up to 48 assignments (three 16-assignment column tiles).  Per
 // super-block its operands reach LDS by direct loads into a ring slot, RING - 1 super-blocks ahead: the
 // activation chunks chunk-major ([chunk][assignment][16 B]: the 16 lanes of an operand read one
 // 256-byte run), Q4_K block sums and token scales, each wave's 16 weight rows and their scales.  Each
 // wave issues the same KM_DMA loads per super-block (some with lanes masked off), so its own count of
 // outstanding loads tells when a super-block has landed.
-constexpr int KM_TOK = 32;  // assignments per tile (kKmmaTile)
+constexpr int KM_TOK = 48;  // assignments per tile (kKmmaTile)
 static_assert(KM_TOK == kKmmaTile, "tile capacity");
 constexpr int KM_NW = 8;    // waves per workgroup
-constexpr int KM_DMA = 8;   // direct loads per wave per super-block
+constexpr int KM_DMA = 9;   // direct loads per wave per super-block
+constexpr int KM_RING = 3;  // ring slots
 
 template <int TYPE>
 struct KmSlot {
     static constexpr bool Q4K = TYPE == PHX_Q4_K_DEV;
     static constexpr int PAY = Q4K ? 144 : 208;
-    static constexpr int ACT = 0;                                // [32 chunks][32 assignments][16 B]
-    static constexpr int BSM = ACT + 32 * KM_TOK * 16;           // Q4_K: [4 quarters][32][4 fp16 bsums]
-    static constexpr int YD = BSM + (Q4K ? 4 * KM_TOK * 8 : 0);  // [32] token scales
+    static constexpr int ACT = 0;                                // [32 chunks][48 assignments][16 B]
+    static constexpr int BSM = ACT + 32 * KM_TOK * 16;           // Q4_K: [4 quarters][48][4 fp16 bsums]
+    static constexpr int YD = BSM + (Q4K ? 4 * KM_TOK * 8 : 0);  // [48] token scales
     static constexpr int W = YD + KM_TOK * 4;                    // [8 waves][16 rows][PAY]
     static constexpr int WS = W + KM_NW * 16 * PAY;              // [8 waves][16 rows] 4-byte slots
     static constexpr int BYTES = WS + KM_NW * 16 * 4;
-    static constexpr int RING = Q4K ? 4 : 3;
 };
 
 typedef _Float16 mh4 __attribute__((ext_vector_type(4)));
@@ -518,27 +518,27 @@ __device__ __forceinline__ uint32_t pk_fma(uint32_t a, mh2 b, mh2 c)
 {
     return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(mh2, a), b, c));
 }
-__device__ __forceinline__ uint32_t pk_mul(uint32_t a, mh2 b)
-{
-    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(mh2, a) * b);
-}
-__device__ __forceinline__ uint32_t pk_add(uint32_t a, mh2 b)
-{
-    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(mh2, a) + b);
-}
 __device__ __forceinline__ mh2 hpair(_Float16 a, _Float16 b) { return mh2{a, b}; }
+// (x & m) | c in one instruction (the compiler splits it to keep the constants out of SGPRs)
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t c)
+{
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "s"(m), "v"(c));  // one SGPR operand (gfx9)
+    return r;
+}
 // s_waitcnt vmcnt(n) alone (gfx9 encoding: vmcnt bits 3:0 and 15:14)
 constexpr int vm_wait(int n) { return (n & 15) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
 __device__ __forceinline__ void tie(u32x4& v) { asm volatile("" : "+v"(v)); }
 __device__ __forceinline__ void tie(u32x2& v) { asm volatile("" : "+v"(v)); }
 __device__ __forceinline__ void tie(uint32_t& v) { asm volatile("" : "+v"(v)); }
+template <int N> using ic = std::integral_constant<int, N>;
 
 template <int TYPE, int NJ>
 __device__ __forceinline__ void kmma_tile(const MmaArgs& g, const Tile& tl, int cnt, unsigned char* ring)
 {
     using SL = KmSlot<TYPE>;
     constexpr bool Q4K = SL::Q4K;
-    constexpr int PAY = SL::PAY, RING = SL::RING, SBY = Q4K ? 4 : 2;
+    constexpr int PAY = SL::PAY, RING = KM_RING, SBY = Q4K ? 4 : 2;
     const int tid = threadIdx.x, lane = tid & 63, r16 = lane & 15, q = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int gI = blockIdx.x * 2 + (wave >> 2), ws = wave & 3;
@@ -548,49 +548,55 @@ __device__ __forceinline__ void kmma_tile(const MmaArgs& g, const Tile& tl, int 
 
     // the direct loads' lane sources at super-block 0 (assignments past cnt: a valid row, never stored)
     auto arow = [&](int t) -> int64_t { return g.perm[tl.start + min(t, cnt - 1)] / g.act_div; };
-    // (1)(2) chunks 4 wave + 2 i + lane / 32 of assignment lane % 32
-    const uint16_t* xs = g.act.qh + arow(lane & 31) * g.act.qhstride + 8 * (4 * wave + (lane >> 5));
-    // (3) Q4_K: dword 32 wave + lane (lanes 0-31) of the block sums' [quarter][assignment][2 dwords]
+    // (1)-(3) activation chunks: load i of wave w fills positions 64 (3 w + i) + lane of the
+    // [chunk][assignment] array: chunk p / 48 of assignment p % 48
+    const uint16_t* xs[3];
+#pragma unroll
+    for (int i = 0; i < 3; i++) {
+        const int p = 64 * (3 * wave + i) + lane;
+        xs[i] = g.act.qh + arow(p % KM_TOK) * g.act.qhstride + 8 * (p / KM_TOK);
+    }
+    // (4) Q4_K: dword 48 w + lane (lanes 0-47) of the block sums' [quarter][assignment][2 dwords]
     const uint16_t* bsrc = nullptr;
-    if (Q4K) bsrc = g.act.bh + arow(16 * (wave & 1) + ((lane & 31) >> 1)) * g.act.bhstride + 4 * (wave >> 1) + 2 * (lane & 1);
-    // (4) token scales of assignments 4 wave + lane (lanes 0-3)
-    const float* ysrc = g.act.d + arow(4 * wave + (lane & 3)) * g.act.dstride;
-    // (5) the wave's 16 weight rows, 1 KB per load; (6) their scales (lanes 0-15)
+    if (Q4K) {
+        const int dw = 48 * wave + min(lane, 47);
+        bsrc = g.act.bh + arow((dw % 96) >> 1) * g.act.bhstride + 4 * (dw / 96) + 2 * (dw & 1);
+    }
+    // (5) token scales of assignments 6 w + lane (lanes 0-5)
+    const float* ysrc = g.act.d + arow(6 * wave + min(lane, 5)) * g.act.dstride;
+    // (6)-(8) the wave's 16 weight rows, 1 KB per load; (9) their scales (lanes 0-15)
     const int gIc = min(gI, g.rg - 1);
     const uint8_t* wsrc = g.payload + tl.e * g.mat_pay + gIc * g.rg_pay + 16 * ws * PAY + 16 * lane;
     const uint8_t* ssrc = g.scale + tl.e * g.mat_sc + ((int64_t)gIc * nb * 64 + 16 * ws + r16) * SBY;
 
 #define KM_DMA_LOAD(src, lds_off, size) \
     __builtin_amdgcn_global_load_lds((glb_void_t)(src), (lds_void_t)(ring + (lds_off)), size, 0, 0)
-    auto dma16 = [&](const void* src, uint32_t lds_off) { KM_DMA_LOAD(src, lds_off, 16); };
-    auto dma4 = [&](const void* src, uint32_t lds_off) { KM_DMA_LOAD(src, lds_off, 4); };
-    auto dma2 = [&](const void* src, uint32_t lds_off) { KM_DMA_LOAD(src, lds_off, 2); };
-#undef KM_DMA_LOAD
     auto issue = [&](int b) {  // super-block b (clamped: past the end a harmless reload) into its slot
         const int bc = min(b, nb - 1);
         const uint32_t slot = (uint32_t)(b % RING) * SL::BYTES;
         const uint8_t* wb = wsrc + (int64_t)bc * 64 * PAY;
         const uint32_t wl = slot + SL::W + wave * 16 * PAY;
-        dma16(xs + (int64_t)bc * 256, slot + SL::ACT + (4 * wave) * 512);
-        dma16(xs + (int64_t)bc * 256 + 16, slot + SL::ACT + (4 * wave + 2) * 512);
+#pragma unroll
+        for (int i = 0; i < 3; i++) KM_DMA_LOAD(xs[i] + (int64_t)bc * 256, slot + SL::ACT + (3 * wave + i) * 1024, 16);
         if (Q4K) {
-            if (lane < 32) dma4(bsrc + (int64_t)bc * 16, slot + SL::BSM + 128 * wave);
+            if (lane < 48) KM_DMA_LOAD(bsrc + (int64_t)bc * 16, slot + SL::BSM + 192 * wave, 4);
         } else {
-            if (lane < 16) dma16(wb + 3072, wl + 3072);  // Q6_K rows: 3328 bytes
+            if (lane < 16) KM_DMA_LOAD(wb + 3072, wl + 3072, 16);  // Q6_K rows: 3328 bytes
         }
-        if (lane < 4) dma4(ysrc + bc, slot + SL::YD + 16 * wave);
-        dma16(wb, wl);
-        dma16(wb + 1024, wl + 1024);
+        if (lane < 6) KM_DMA_LOAD(ysrc + bc, slot + SL::YD + 24 * wave, 4);
+        KM_DMA_LOAD(wb, wl, 16);
+        KM_DMA_LOAD(wb + 1024, wl + 1024, 16);
         if (Q4K) {
-            if (lane < 16) dma16(wb + 2048, wl + 2048);  // Q4_K rows: 2304 bytes
+            if (lane < 16) KM_DMA_LOAD(wb + 2048, wl + 2048, 16);  // Q4_K rows: 2304 bytes
         } else {
-            dma16(wb + 2048, wl + 2048);
+            KM_DMA_LOAD(wb + 2048, wl + 2048, 16);
         }
         if (lane < 16) {
-            if (Q4K) dma4(ssrc + (int64_t)bc * 64 * SBY, slot + SL::WS + 64 * wave);
-            else dma2(ssrc + (int64_t)bc * 64 * SBY, slot + SL::WS + 64 * wave);
+            if (Q4K) KM_DMA_LOAD(ssrc + (int64_t)bc * 64 * SBY, slot + SL::WS + 64 * wave, 4);
+            else KM_DMA_LOAD(ssrc + (int64_t)bc * 64 * SBY, slot + SL::WS + 64 * wave, 2);
         }
     };
+#undef KM_DMA_LOAD
     // super-block b has landed once at most the later ones' loads are outstanding; the barrier then
     // publishes it and ends every wave's reads of the slot that issue(b + RING - 1) refills
     auto land = [&](int b) {
@@ -610,10 +616,12 @@ __device__ __forceinline__ void kmma_tile(const MmaArgs& g, const Tile& tl, int 
         }
     const mf4 zero4 = {};
     // the lane's LDS read offsets within a slot
-    const uint32_t o_act = SL::ACT + q * 512 + r16 * 16;
-    const uint32_t o_bs = SL::BSM + q * 256 + r16 * 8;
+    const uint32_t o_act = SL::ACT + q * (KM_TOK * 16) + r16 * 16;
+    const uint32_t o_bs = SL::BSM + q * (KM_TOK * 8) + r16 * 8;
     const uint32_t o_yd = SL::YD + r16 * 4;
-    const uint32_t o_row = SL::W + (wave * 16 + r16) * PAY;
+    const uint32_t o_row = SL::W + (wave * 16 + r16) * PAY + 32 * q;
+    const uint32_t o_sc = SL::W + (wave * 16 + r16) * PAY + (Q4K ? 128 + 4 * (q >> 1) : 128 + 16 * q);
+    const uint32_t o_y = Q4K ? o_sc + 8 : SL::W + (wave * 16 + r16) * PAY + 192 + 4 * q;
     const uint32_t o_ws = SL::WS + (wave * 16 + 4 * q) * 4;
 
 #pragma unroll
@@ -621,26 +629,34 @@ __device__ __forceinline__ void kmma_tile(const MmaArgs& g, const Tile& tl, int 
     for (int b = 0; b < nb; b++) {
         land(b);
         const uint32_t sb = ring0 + (uint32_t)(b % RING) * SL::BYTES;
-        // the super-block's weights, row scales, token scales, block sums and the first operands
-        u32x4 D0 = ds_r128(sb + o_row + 32 * q), D1 = ds_r128<16>(sb + o_row + 32 * q);
-        // Q4_K: X.x the dword of sc[2 q], sc[2 q + 1], Y that of mins[2 q], mins[2 q + 1];
+        // the super-block's weights, row scales, token scales, block sums and the first operands (a read's
+        // result is used only after its wait, never first composed into another value)
+        const uint32_t a_row = sb + o_row, a_sc = sb + o_sc, a_act = sb + o_act, a_yd = sb + o_yd;
+        u32x4 D0 = ds_r128(a_row), D1 = ds_r128<16>(a_row);
+        // Q4_K: X0 the dword of sc[2 q], sc[2 q + 1], Y that of mins[2 q], mins[2 q + 1];
         // Q6_K: X the high-bit dwords (s = 2 q: lq 0, 1; s = 2 q + 1: lq 0, 1), Y sc[4 q .. 4 q + 3]
-        // (a read's result is used only after its wait, never first composed into another value)
         u32x4 X;
         uint32_t X0;
-        if (Q4K) X0 = ds_r32(sb + o_row + 128 + 4 * (q >> 1));
-        else X = ds_r128(sb + o_row + 128 + 16 * q);
-        uint32_t Y = Q4K ? ds_r32<8>(sb + o_row + 128 + 4 * (q >> 1)) : ds_r32(sb + o_row + 192 + 4 * q);
+        if (Q4K) X0 = ds_r32(a_sc);
+        else X = ds_r128(a_sc);
+        uint32_t Y = ds_r32(sb + o_y);
         u32x4 WSV = ds_r128(sb + o_ws);
         uint32_t YD[NJ];
         u32x2 BS[NJ];
         u32x4 B[2][NJ];
-        const uint32_t a_act = sb + o_act;
-#pragma unroll
-        for (int c = 0; c < NJ; c++) {
-            YD[c] = c == 0 ? ds_r32(sb + o_yd) : ds_r32<64>(sb + o_yd);
-            if (Q4K) BS[c] = c == 0 ? ds_r64(sb + o_bs) : ds_r64<128>(sb + o_bs);
-            B[0][c] = c == 0 ? ds_r128(a_act) : ds_r128<256>(a_act);
+        const uint32_t a_bs = sb + o_bs;
+        YD[0] = ds_r32(a_yd);
+        if (Q4K) BS[0] = ds_r64(a_bs);
+        B[0][0] = ds_r128(a_act);
+        if (NJ > 1) {
+            YD[1 % NJ] = ds_r32<64>(a_yd);
+            if (Q4K) BS[1 % NJ] = ds_r64<128>(a_bs);
+            B[0][1 % NJ] = ds_r128<256>(a_act);
+        }
+        if (NJ > 2) {
+            YD[2 % NJ] = ds_r32<128>(a_yd);
+            if (Q4K) BS[2 % NJ] = ds_r64<256>(a_bs);
+            B[0][2 % NJ] = ds_r128<512>(a_act);
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         tie(D0);
@@ -665,8 +681,12 @@ __device__ __forceinline__ void kmma_tile(const MmaArgs& g, const Tile& tl, int 
                 dd[c][v] = h2f(WSV[v] & 0xFFFFu) * yd;
                 if (Q4K) dm[c][v] = h2f(WSV[v] >> 16) * yd;
             }
-        // per-s constants of the A operands (s = 2 q, 2 q + 1)
-        mh2 K0[2], M0[2], K1[2], M1[2];  // Q4_K: even l (K0, M0), odd l (K1, M1); Q6_K: lo, -1056 lo, 32 hi
+        // per-s constants of the A operands (s = 2 q, 2 q + 1).  Q4_K: the nibble n enters as the half
+        // 1024 + n (l even) or 1024 + 16 n (l odd), so sc * n = fma(., sc, -1024 sc) or
+        // fma(., sc / 16, -64 sc).  Q6_K: the 6-bit value v enters as 1024 + 4 v, q = v - 32, and with
+        // sc = 32 hi + lo: lo * q = fma(., lo / 4, -288 lo), 32 hi * q = fma(., 8 hi, -9216 hi) (every
+        // constant and result exact in fp16, each fma rounding once to an exact value)
+        mh2 K0[2], M0[2], K1[2], M1[2];
         if (Q4K) {
             const uint32_t sw = X0 >> (16 * (q & 1));  // sc[2 q], sc[2 q + 1]
 #pragma unroll
@@ -682,12 +702,13 @@ __device__ __forceinline__ void kmma_tile(const MmaArgs& g, const Tile& tl, int 
             for (int j = 0; j < 2; j++) {  // sc[4 q + 2 j], sc[4 q + 2 j + 1]
                 const int s0 = (int)(int8_t)(Y >> (16 * j)), s1 = (int)(int8_t)(Y >> (16 * j + 8));
                 const _Float16 lo0 = (_Float16)(s0 & 31), lo1 = (_Float16)(s1 & 31);
-                K0[j] = hpair(lo0, lo1);
-                M0[j] = hpair(lo0 * (_Float16)-1056.0f, lo1 * (_Float16)-1056.0f);
-                K1[j] = hpair((_Float16)(32 * (s0 >> 5)), (_Float16)(32 * (s1 >> 5)));
+                const _Float16 hi0 = (_Float16)(s0 >> 5), hi1 = (_Float16)(s1 >> 5);
+                K0[j] = hpair(lo0 * (_Float16)0.25f, lo1 * (_Float16)0.25f);
+                M0[j] = hpair(lo0 * (_Float16)-288.0f, lo1 * (_Float16)-288.0f);
+                K1[j] = hpair(hi0 * (_Float16)8.0f, hi1 * (_Float16)8.0f);
+                M1[j] = hpair(hi0 * (_Float16)-9216.0f, hi1 * (_Float16)-9216.0f);
             }
         }
-        const mh2 m1056 = hpair((_Float16)-1056.0f, (_Float16)-1056.0f);
         // lane l's A operand(s): pairs (s = 2 q: mm 0, 2), (mm 1, 3), then s = 2 q + 1
         auto a_op = [&](int l, mh8& A, mh8& A2) {
             const int p = l >> 1;
@@ -697,39 +718,47 @@ __device__ __forceinline__ void kmma_tile(const MmaArgs& g, const Tile& tl, int 
                 const uint32_t m = (l & 1) ? 0x00F000F0u : 0x000F000Fu;
                 const mh2 k0 = (l & 1) ? K1[0] : K0[0], c0 = (l & 1) ? M1[0] : M0[0];
                 const mh2 k1 = (l & 1) ? K1[1] : K0[1], c1 = (l & 1) ? M1[1] : M0[1];
-                w[0] = pk_fma((x0 & m) | 0x64006400u, k0, c0);
-                w[1] = pk_fma(((x0 >> 8) & m) | 0x64006400u, k0, c0);
-                w[2] = pk_fma((x1 & m) | 0x64006400u, k1, c1);
-                w[3] = pk_fma(((x1 >> 8) & m) | 0x64006400u, k1, c1);
+                w[0] = pk_fma(and_or(x0, m, 0x64006400u), k0, c0);
+                w[1] = pk_fma(and_or(x0 >> 8, m, 0x64006400u), k0, c0);
+                w[2] = pk_fma(and_or(x1, m, 0x64006400u), k1, c1);
+                w[3] = pk_fma(and_or(x1 >> 8, m, 0x64006400u), k1, c1);
                 A = __builtin_bit_cast(mh8, make_uint4(w[0], w[1], w[2], w[3]));
             } else {
+                // the low nibble to bits 2-5 of each half, the two high bits (bits 2 i of the byte,
+                // i = l % 4) to bits 6-7
                 const int i = l & 3, lq = l >> 2;
                 const uint32_t h0 = X[lq], h1 = X[2 + lq];
-                auto lo = [&](uint32_t x, int pr) { return (l & 1) ? x >> (4 + 8 * pr) : x >> (8 * pr); };
+                auto lo = [&](uint32_t x, int pr) {
+                    const int sh = ((l & 1) ? 4 : 0) + 8 * pr - 2;  // from bit sh + 2 to bit 2
+                    return sh >= 0 ? x >> sh : x << -sh;
+                };
                 auto hi = [&](uint32_t h, int pr) {
-                    return pr ? h >> (4 + 2 * i) : (i == 3 ? h >> 2 : h << (4 - 2 * i));
+                    const int sh = 2 * i + 8 * pr - 6;  // from bit sh + 6 to bit 6
+                    return sh >= 0 ? h >> sh : h << -sh;
                 };
                 uint32_t v[4];
-                v[0] = (hi(h0, 0) & 0x00300030u) | ((lo(x0, 0) & 0x000F000Fu) | 0x64006400u);
-                v[1] = (hi(h0, 1) & 0x00300030u) | ((lo(x0, 1) & 0x000F000Fu) | 0x64006400u);
-                v[2] = (hi(h1, 0) & 0x00300030u) | ((lo(x1, 0) & 0x000F000Fu) | 0x64006400u);
-                v[3] = (hi(h1, 1) & 0x00300030u) | ((lo(x1, 1) & 0x000F000Fu) | 0x64006400u);
+                v[0] = and_or(hi(h0, 0), 0x00C000C0u, and_or(lo(x0, 0), 0x003C003Cu, 0x64006400u));
+                v[1] = and_or(hi(h0, 1), 0x00C000C0u, and_or(lo(x0, 1), 0x003C003Cu, 0x64006400u));
+                v[2] = and_or(hi(h1, 0), 0x00C000C0u, and_or(lo(x1, 0), 0x003C003Cu, 0x64006400u));
+                v[3] = and_or(hi(h1, 1), 0x00C000C0u, and_or(lo(x1, 1), 0x003C003Cu, 0x64006400u));
                 uint32_t u[4];
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    w[j] = pk_fma(v[j], K0[j >> 1], M0[j >> 1]);       // lo * (q6 - 32)
-                    u[j] = pk_mul(pk_add(v[j], m1056), K1[j >> 1]);  // 32 hi * (q6 - 32)
+                    w[j] = pk_fma(v[j], K0[j >> 1], M0[j >> 1]);  // lo * (v - 32)
+                    u[j] = pk_fma(v[j], K1[j >> 1], M1[j >> 1]);  // 32 hi * (v - 32)
                 }
                 A = __builtin_bit_cast(mh8, make_uint4(w[0], w[1], w[2], w[3]));
                 A2 = __builtin_bit_cast(mh8, make_uint4(u[0], u[1], u[2], u[3]));
             }
         };
-#pragma unroll
-        for (int l = 0; l < 8; l++) {
-            const int cur = l & 1;
-            if (l + 1 < 8)  // the next lane's operands behind this one's products
-#pragma unroll
-                for (int c = 0; c < NJ; c++) B[cur ^ 1][c] = ds_r128(a_act + (l + 1) * 2048 + c * 256);
+        // lane l: operands of lane l + 1 read behind its products (immediate offsets: l compile-time)
+        auto step = [&](auto LC) {
+            constexpr int l = decltype(LC)::value, cur = l & 1;
+            if (l + 1 < 8) {
+                B[cur ^ 1][0] = ds_r128<(l + 1) * KM_TOK * 64>(a_act);
+                if (NJ > 1) B[cur ^ 1][1 % NJ] = ds_r128<(l + 1) * KM_TOK * 64 + 256>(a_act);
+                if (NJ > 2) B[cur ^ 1][2 % NJ] = ds_r128<(l + 1) * KM_TOK * 64 + 512>(a_act);
+            }
             mh8 A, A2;
             a_op(l, A, A2);
 #pragma unroll
@@ -745,7 +774,15 @@ __device__ __forceinline__ void kmma_tile(const MmaArgs& g, const Tile& tl, int 
 #pragma unroll
                 for (int c = 0; c < NJ; c++) tie(B[cur ^ 1][c]);
             }
-        }
+        };
+        step(ic<0>{});
+        step(ic<1>{});
+        step(ic<2>{});
+        step(ic<3>{});
+        step(ic<4>{});
+        step(ic<5>{});
+        step(ic<6>{});
+        step(ic<7>{});
         if (Q4K) {  // the min term: sumf -= (dmin * yd) * sumi
             const uint32_t mw = Y >> (16 * (q & 1));  // mins[2 q], mins[2 q + 1]
             const _Float16 m0 = (_Float16)(int)(mw & 0xFFu), m1 = (_Float16)(int)((mw >> 8) & 0xFFu);
@@ -809,7 +846,8 @@ __global__ __launch_bounds__(KM_NW * 64, 1) void k_grouped_kmma(MmaArgs g)
     if (tile >= *g.ntiles) return;  // uniform over the workgroup
     const Tile tl = g.tiles[tile];
     const int cnt = min(tl.cnt, KM_TOK);
-    if (cnt > 16) kmma_tile<TYPE, 2>(g, tl, cnt, kring);
+    if (cnt > 32) kmma_tile<TYPE, 3>(g, tl, cnt, kring);
+    else if (cnt > 16) kmma_tile<TYPE, 2>(g, tl, cnt, kring);
     else kmma_tile<TYPE, 1>(g, tl, cnt, kring);
 }
 
@@ -837,11 +875,11 @@ void launch_grouped_kmma(hipStream_t st, const QMat& w, Act act, const Tile* til
     g.paired = w.paired;
     const dim3 grid((w.rg + 1) / 2, max_tiles);
     if (w.type == PHX_Q4_K_DEV) {
-        constexpr size_t lds = (size_t)KmSlot<PHX_Q4_K_DEV>::RING * KmSlot<PHX_Q4_K_DEV>::BYTES;
+        constexpr size_t lds = (size_t)KM_RING * KmSlot<PHX_Q4_K_DEV>::BYTES;
         (void)hipFuncSetAttribute((const void*)k_grouped_kmma<PHX_Q4_K_DEV>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         launch(k_grouped_kmma<PHX_Q4_K_DEV>, grid, dim3(KM_NW * 64), (uint32_t)lds, st, g);
     } else {
-        constexpr size_t lds = (size_t)KmSlot<PHX_Q6_K_DEV>::RING * KmSlot<PHX_Q6_K_DEV>::BYTES;
+        constexpr size_t lds = (size_t)KM_RING * KmSlot<PHX_Q6_K_DEV>::BYTES;
         (void)hipFuncSetAttribute((const void*)k_grouped_kmma<PHX_Q6_K_DEV>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         launch(k_grouped_kmma<PHX_Q6_K_DEV>, grid, dim3(KM_NW * 64), (uint32_t)lds, st, g);
     }

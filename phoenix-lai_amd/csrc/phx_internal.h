@@ -146,7 +146,7 @@ void launch_grouped_mfma(hipStream_t st, const QMat& w, Act act, const Tile* til
 // K-quant prefill path (kernels_prefill.hip): Q4_K / Q6_K grouped products on MFMA, tiles of up to
 // kKmmaTile assignments, activations' fp16 copies (qh; Q4_K also bh) in row order; arguments and outputs
 // as launch_grouped
-constexpr int kKmmaTile = 32;
+constexpr int kKmmaTile = 48;
 void launch_grouped_kmma(hipStream_t st, const QMat& w, Act act, const Tile* tiles, const int* ntiles, int max_tiles,
                          const int* perm, int act_div, float* out0, float* out1, int split, int out_stride);
 void launch_combine(hipStream_t st, int T, int d, int k, float eps, const float* yd, const float* w,
