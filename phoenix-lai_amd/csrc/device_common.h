@@ -363,4 +363,64 @@ __device__ __forceinline__ float mean_sq_cert_wave(const float* x, int n, int* f
     return (float)(q / (double)n);
 }
 
+// ------------------------------------------------------------------------------ explicit LDS reads
+// Kernels that fill LDS with direct global -> LDS loads read it back with these: the compiler would
+// otherwise wait for every outstanding direct load before any LDS read it emits.
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) void* lds_void_t;
+typedef __attribute__((address_space(1))) void* glb_void_t;
+
+// explicit LDS reads at address a + OFF (asynchronous: the value is valid after lds_wait)
+template <int OFF = 0>
+__device__ __forceinline__ u32x4 ds_r128(uint32_t a)
+{
+    u32x4 v;
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(a), "i"(OFF));
+    return v;
+}
+template <int OFF = 0>
+__device__ __forceinline__ u32x2 ds_r64(uint32_t a)
+{
+    u32x2 v;
+    asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(v) : "v"(a), "i"(OFF));
+    return v;
+}
+template <int OFF = 0>
+__device__ __forceinline__ uint32_t ds_r32(uint32_t a)
+{
+    uint32_t v;
+    asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v) : "v"(a), "i"(OFF));
+    return v;
+}
+__device__ __forceinline__ uint32_t ds_ru16(uint32_t a)
+{
+    uint32_t v;
+    asm volatile("ds_read_u16 %0, %1" : "=v"(v) : "v"(a));
+    return v;
+}
+// waits for every LDS read of the wave; the registers passed are the reads' results, tied to the wait
+// so that no use of them is scheduled above it.  A read's result must have no other use before its
+// wait, and the read and its wait must sit in one basic block: the compiler takes an asm result as
+// ready at once, so a copy it placed in between (to split a value, or at a branch join) would copy
+// the register before the data lands.
+__device__ __forceinline__ void lds_wait(u32x4& a, u32x4& b, uint32_t& c)
+{
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c)::"memory");
+}
+__device__ __forceinline__ void lds_wait(u32x4& a, u32x4& b, uint32_t& c, u32x2& d, uint32_t& f)
+{
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d), "+v"(f)::"memory");
+}
+__device__ __forceinline__ void lds_wait(u32x4& a, u32x4& b, uint32_t& c, u32x2& d, u32x2& e, uint32_t& f)
+{
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d), "+v"(e), "+v"(f)::"memory");
+}
+// compile-time index for unrolled steps with immediate offsets
+template <int N> using ic = std::integral_constant<int, N>;
+// after an explicit `s_waitcnt lgkmcnt(0)`: the read's result is defined here (no use moves above it)
+__device__ __forceinline__ void tie(u32x4& v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void tie(u32x2& v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void tie(uint32_t& v) { asm volatile("" : "+v"(v)); }
+
 }  // namespace phx

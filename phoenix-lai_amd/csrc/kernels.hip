@@ -303,16 +303,105 @@ __global__ __launch_bounds__(256, 2) void k_router_exact_wide(int T, int d, int 
     }
 }
 
-// Eight tokens per workgroup where that still makes 1024 workgroups, four from 64 tokens, below that
-// one wave per (64 experts, token) with the token's row of m in LDS.
+// Fewer tokens (latency-bound: too few chains to hide the loads): the same four-wave workgroup of 64
+// experts and four tokens (one per wave), with the router columns streamed through a ring of RR_RING
+// LDS slots by direct global -> LDS loads, RR_RING - 1 chunks of 64 elements ahead: a wave issues
+// four 1-KB column loads (the 64 experts of one float4 column are contiguous) and its token's 16
+// float4 of m per chunk, so its own count of outstanding loads tells when a chunk has landed.
+constexpr int RR_CH4 = 16, RR_RING = 4, RR_DMA = 5;
+__global__ __launch_bounds__(256) void k_router_ring(int T, int d, int E, const float4* __restrict__ wt4,
+                                                     const float* __restrict__ rin, float* __restrict__ logits)
+{
+    __shared__ float4 wring[RR_RING][RR_CH4][64];
+    __shared__ float4 mring[RR_RING][4][RR_CH4];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int e = blockIdx.x * 64 + lane, t = blockIdx.y * 4 + wave;
+    const int n4 = d / 4, nch = (n4 + RR_CH4 - 1) / RR_CH4;  // d % 64 == 0: whole chunks
+    const float4* wsrc = wt4 + min(e, E - 1);                      // column c: + c * E
+    const float4* msrc = (const float4*)(rin + (int64_t)min(t, T - 1) * d) + min(lane, RR_CH4 - 1);
+    auto issue = [&](int c) {  // chunk c (clamped: past the end a harmless reload) into its slot
+        const int cc = min(c, nch - 1), slot = c % RR_RING;
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            __builtin_amdgcn_global_load_lds((glb_void_t)(wsrc + (int64_t)(cc * RR_CH4 + 4 * wave + j) * E),
+                                             (lds_void_t)&wring[slot][4 * wave + j][0], 16, 0, 0);
+        if (lane < RR_CH4)
+            __builtin_amdgcn_global_load_lds((glb_void_t)(msrc + cc * RR_CH4), (lds_void_t)&mring[slot][wave][0], 16, 0, 0);
+    };
+#pragma unroll
+    for (int c = 0; c < RR_RING - 1; c++) issue(c);
+    float s = 0.0f;
+    const uint32_t w0 = (uint32_t)(uintptr_t)(lds_void_t)&wring[0][0][lane];
+    const uint32_t m0 = (uint32_t)(uintptr_t)(lds_void_t)&mring[0][wave][0];
+    for (int c = 0; c < nch; c++) {
+        // chunk c has landed once at most the two later chunks' loads are outstanding; the barrier then
+        // publishes it and ends every wave's reads of the slot that issue(c + RING - 1) refills
+        __builtin_amdgcn_s_waitcnt((RR_DMA * (RR_RING - 2)) | (0x7 << 4) | (0xF << 8));
+        __builtin_amdgcn_s_barrier();
+        issue(c + RR_RING - 1);
+        const int slot = c % RR_RING;
+        // explicit reads (see device_common.h), four columns per batch, the next batch's reads issued
+        // before this batch's adds
+        const uint32_t wa = w0 + slot * (RR_CH4 * 64 * 16), ma = m0 + slot * (4 * RR_CH4 * 16);
+        u32x4 W[2][4], M[2][4];
+        auto reads = [&](auto GC) {
+            constexpr int g = decltype(GC)::value, b = g & 1;
+            W[b][0] = ds_r128<(4 * g + 0) * 1024>(wa);
+            W[b][1] = ds_r128<(4 * g + 1) * 1024>(wa);
+            W[b][2] = ds_r128<(4 * g + 2) * 1024>(wa);
+            W[b][3] = ds_r128<(4 * g + 3) * 1024>(wa);
+            M[b][0] = ds_r128<(4 * g + 0) * 16>(ma);  // one LDS broadcast for the wave
+            M[b][1] = ds_r128<(4 * g + 1) * 16>(ma);
+            M[b][2] = ds_r128<(4 * g + 2) * 16>(ma);
+            M[b][3] = ds_r128<(4 * g + 3) * 16>(ma);
+        };
+        auto landed = [&](int b) {
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                tie(W[b][j]);
+                tie(M[b][j]);
+            }
+        };
+        auto adds = [&](int b) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float4 w = __builtin_bit_cast(float4, W[b][j]), m = __builtin_bit_cast(float4, M[b][j]);
+                s += w.x * m.x;
+                s += w.y * m.y;
+                s += w.z * m.z;
+                s += w.w * m.w;
+            }
+        };
+        reads(ic<0>{});
+        landed(0);
+        reads(ic<1>{});
+        adds(0);
+        landed(1);
+        reads(ic<2>{});
+        adds(1);
+        landed(0);
+        reads(ic<3>{});
+        adds(0);
+        landed(1);
+        adds(1);
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // the reloads past the last chunk land before the workgroup ends
+    if (e < E && t < T) logits[(int64_t)t * E + e] = s;
+}
+
+// Eight tokens per workgroup where that still makes 1024 workgroups (enough chains to keep the SIMDs
+// busy: compute-bound), else four with the deeper load ring (d % 64 == 0), else one wave per (64
+// experts, token) with the token's row of m in LDS.
 void launch_router_exact(hipStream_t st, int T, int d, int E, const float* wt4, const float* rin, float* logits)
 {
     const int gx = (E + 63) / 64;
     const float4* w = (const float4*)wt4;
-    if (T * gx >= 1024)  // enough workgroups at eight tokens each
+    if (T * gx >= 1024)
         launch(k_router_exact_wide<2>, dim3(gx, (T + 7) / 8), dim3(256), 0, st, T, d, E, w, rin, logits);
-    else if (T >= 64)
-        launch(k_router_exact_wide<1>, dim3(gx, (T + 3) / 4), dim3(256), 0, st, T, d, E, w, rin, logits);
+    else if (d % 64 == 0)
+        launch(k_router_ring, dim3(gx, (T + 3) / 4), dim3(256), 0, st, T, d, E, w, rin, logits);
     else
         launch(k_router_exact<1>, dim3(gx, T), dim3(64), (uint32_t)(d * 4), st, T, d, E, w, rin, logits);
 }

@@ -405,9 +405,6 @@ __device__ __forceinline__ void gu_epilogue(float S, int rgi, int split, int64_t
     }
 }
 
-typedef __attribute__((address_space(3))) void* lds_void_t;
-typedef __attribute__((address_space(1))) void* glb_void_t;
-
 // ------------------------------------------------------------------------------ combine of a token
 // The layer's output for token t by a whole workgroup whose threads hold CQ float4 columns each
 // (CQ * 4 * blockDim.x >= d): acc = sum_j w_j * yd_j in rank order (src/GemmaCpu.cs:417-418, each

@@ -75,11 +75,6 @@ __device__ __forceinline__ mh8 bias8(uint32_t w0, uint32_t w1, float bias)
     return __builtin_bit_cast(mh8, u);
 }
 
-typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
-typedef __attribute__((address_space(3))) void* lds_void_t;
-typedef __attribute__((address_space(1))) void* glb_void_t;
-
 constexpr int MMA_RING = 4;  // LDS ring slots: blocks in flight ahead of the one being multiplied
 constexpr int MMA_DMA = 5;   // direct loads per wave per block
 
@@ -94,52 +89,6 @@ struct MmaSlot {
     static constexpr int WD = WQ + 128 * PAY;        // 128 weight scales (fp16 in the low half of a dword)
     static constexpr int BYTES = WD + 128 * 4;
 };
-
-// explicit LDS reads at address a + OFF (asynchronous: the value is valid after lds_wait)
-template <int OFF = 0>
-__device__ __forceinline__ u32x4 ds_r128(uint32_t a)
-{
-    u32x4 v;
-    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(a), "i"(OFF));
-    return v;
-}
-template <int OFF = 0>
-__device__ __forceinline__ u32x2 ds_r64(uint32_t a)
-{
-    u32x2 v;
-    asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(v) : "v"(a), "i"(OFF));
-    return v;
-}
-template <int OFF = 0>
-__device__ __forceinline__ uint32_t ds_r32(uint32_t a)
-{
-    uint32_t v;
-    asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v) : "v"(a), "i"(OFF));
-    return v;
-}
-__device__ __forceinline__ uint32_t ds_ru16(uint32_t a)
-{
-    uint32_t v;
-    asm volatile("ds_read_u16 %0, %1" : "=v"(v) : "v"(a));
-    return v;
-}
-// waits for every LDS read of the wave; the registers passed are the reads' results, tied to the wait
-// so that no use of them is scheduled above it.  A read's result must have no other use before its
-// wait, and the read and its wait must sit in one basic block: the compiler takes an asm result as
-// ready at once, so a copy it placed in between (to split a value, or at a branch join) would copy
-// the register before the data lands.
-__device__ __forceinline__ void lds_wait(u32x4& a, u32x4& b, uint32_t& c)
-{
-    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c)::"memory");
-}
-__device__ __forceinline__ void lds_wait(u32x4& a, u32x4& b, uint32_t& c, u32x2& d, uint32_t& f)
-{
-    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d), "+v"(f)::"memory");
-}
-__device__ __forceinline__ void lds_wait(u32x4& a, u32x4& b, uint32_t& c, u32x2& d, u32x2& e, uint32_t& f)
-{
-    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d), "+v"(e), "+v"(f)::"memory");
-}
 
 // byte offset of (token t, 16-byte part q) in a slot's activation rows
 __device__ __forceinline__ uint32_t act_off(int t, int q)
@@ -528,10 +477,6 @@ __device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t c)
 }
 // s_waitcnt vmcnt(n) alone (gfx9 encoding: vmcnt bits 3:0 and 15:14)
 constexpr int vm_wait(int n) { return (n & 15) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
-__device__ __forceinline__ void tie(u32x4& v) { asm volatile("" : "+v"(v)); }
-__device__ __forceinline__ void tie(u32x2& v) { asm volatile("" : "+v"(v)); }
-__device__ __forceinline__ void tie(uint32_t& v) { asm volatile("" : "+v"(v)); }
-template <int N> using ic = std::integral_constant<int, N>;
 
 template <int TYPE, int NJ>
 __device__ __forceinline__ void kmma_tile(const MmaArgs& g, const Tile& tl, int cnt, unsigned char* ring)
