@@ -220,6 +220,8 @@ def run_layer(args, pkg):
     decode = "dispatch" not in prof  # the decode path has no separate dispatch launch
     mfma = (not decode and L["gate_up_type"] in (pkg.PHX.Q4_0, pkg.PHX.Q8_0)
             and L["down_type"] in (pkg.PHX.Q4_0, pkg.PHX.Q8_0) and T * k >= 8 * E)
+    kmma = (not decode and L["gate_up_type"] in (pkg.PHX.Q4_K, pkg.PHX.Q6_K)
+            and L["down_type"] in (pkg.PHX.Q4_K, pkg.PHX.Q6_K) and T * k >= 8 * E)
     gu_b, dn_b = expert_bytes(L)
     sh_bytes = 0
     if L.get("n_ff_shared"):
@@ -234,6 +236,20 @@ def run_layer(args, pkg):
                     "frac": rates["gate_up_frac_fp16_peak"], "traffic": None,
                     "ops_per_launch": rates["gate_up_flops_per_launch"], "avg_launch_us": rates["gate_up_avg_us"],
                     "per_unit": f"2 x {2 * L['n_ff']} x {d} flops per assignment x {T * k} assignments per launch"}
+        down_rate = {"down_tflops": rates["down_tflops"]}
+    elif kmma:
+        rates = mfma_rates(L, T, gu_ms, dn_ms)
+        gu_gbs = avg_experts * gu_b / (gu_ms * 1e-3) / 1e9
+        roofline = {"bound": "mfma", "kernel": "phx::k_grouped_kmma gate|up (K-quant integer lanes on fp16 MFMA, "
+                                               "DotK's float lane chains on VALU)",
+                    "achieved": rates["gate_up_tflops"], "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                    "frac": rates["gate_up_frac_fp16_peak"], "traffic": None,
+                    "ops_per_launch": rates["gate_up_flops_per_launch"], "avg_launch_us": rates["gate_up_avg_us"],
+                    "per_unit": f"2 x {2 * L['n_ff']} x {d} flops per assignment x {T * k} assignments per launch",
+                    "hbm": {"achieved_gbs": round(gu_gbs, 1), "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
+                            "bytes_per_launch": int(avg_experts * gu_b)},
+                    "note": "the reference's per-lane float chain (2 rounded VALU operations per row, assignment, "
+                            "lane and super-block) bounds this kernel, not the matrix cores"}
         down_rate = {"down_tflops": rates["down_tflops"]}
     else:
         roofline = decode_roofline(pkg, L, cfg_name, T, avg_experts, gu_ms) if decode else {
@@ -275,7 +291,7 @@ def run_layer(args, pkg):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp16" if mfma else "int8",  # the products' arithmetic: fp16 MFMA, or int8 dot4 on VALU
+        "dtype": "fp16" if mfma or kmma else "int8",  # the products' arithmetic: fp16 MFMA, or int8 dot4 on VALU
         "data": "synthetic",
         "config": {
             "workload": f"{cfg_name}: MoE FFN layer, T={T}, d={d}, E={E}, top-{k}, "
@@ -287,7 +303,7 @@ def run_layer(args, pkg):
                         + (f" + {rem} eager layer calls" if rem else "") + "), x varied per replay",
             "global_batch": T,
             "parallelism": "none (1 GPU)",
-            "path": "decode" if decode else ("mfma" if mfma else "valu"),
+            "path": "decode" if decode else ("mfma" if mfma or kmma else "valu"),
         },
         "roofline": roofline,
         "layer": {
