@@ -19,6 +19,7 @@ from .moe import (  # noqa: F401
     MoeContext,
     MoeError,
     NotSupportedError,
+    OutOfDeviceMemoryError,
     LayerDesc,
     PHX,
     lib_path,

@@ -32,9 +32,29 @@ struct LaunchTimer {
 };
 extern thread_local LaunchTimer* g_launch_timer;
 
+// Fault injection for tests of the error paths: PHX_FAULT="malloc:n" or "launch:n", read when a context
+// is created, fails that context's n-th device allocation with hipErrorOutOfMemory, or skips its n-th
+// kernel launch and every later one of the same call and reports hipErrorLaunchFailure at the call's
+// launch check (as a lost device would); one fault per context.
+struct FaultPlan {
+    enum Site { NONE = 0, MALLOC = 1, LAUNCH = 2 };
+    int site = NONE;
+    int64_t n = 0, count = 0;
+    hipError_t pending = hipSuccess;
+    bool fire(int s) { return site == s && n > 0 && ++count == n; }
+};
+extern thread_local FaultPlan* g_fault;  // the plan of the context whose call is running
+
 template <typename... KArgs, typename... Args>
 inline void launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, uint32_t lds, hipStream_t st, Args... args)
 {
+    if (FaultPlan* f = g_fault) {
+        if (f->pending != hipSuccess) return;  // after a fault nothing more runs in the call
+        if (f->fire(FaultPlan::LAUNCH)) {
+            f->pending = hipErrorLaunchFailure;
+            return;
+        }
+    }
     if (LaunchTimer* t = g_launch_timer) {
         hipEvent_t a = t->event(), b = t->event();
         if (t->capturing()) {

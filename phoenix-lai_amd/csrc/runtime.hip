@@ -5,6 +5,7 @@
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <algorithm>
@@ -20,6 +21,7 @@ using namespace phx;
 
 namespace phx {
 thread_local LaunchTimer* g_launch_timer = nullptr;
+thread_local FaultPlan* g_fault = nullptr;
 }
 
 namespace {
@@ -305,6 +307,7 @@ struct phx_moe_ctx {
     bool last_scratch = false;
     unsigned char* bump_base = nullptr;
     size_t bump_off = 0, bump_cap = 0;
+    FaultPlan fault;  // PHX_FAULT, see phx_internal.h
 };
 
 namespace {
@@ -340,6 +343,42 @@ int hip_code(hipError_t e)
         if (e_ != hipSuccess) return set_err(c, hip_code(e_), "%s: %s", #expr, hipGetErrorString(e_));        \
     } while (0)
 
+// every device allocation of a context (the fault plan may fail it)
+hipError_t dev_malloc(phx_moe_ctx* c, void** p, size_t n)
+{
+    if (c && c->fault.fire(FaultPlan::MALLOC)) {
+        *p = nullptr;
+        return hipErrorOutOfMemory;
+    }
+    return hipMalloc(p, n);  // the one allocation site
+}
+
+// the launches' status: an injected launch fault, else the runtime's last error
+hipError_t launch_status(phx_moe_ctx* c)
+{
+    if (c && c->fault.pending != hipSuccess) {
+        const hipError_t e = c->fault.pending;
+        c->fault.pending = hipSuccess;
+        (void)hipGetLastError();
+        return e;
+    }
+    return hipGetLastError();
+}
+
+// an API call on context c: its device current and its fault plan visible to the launches
+struct CtxScope {
+    FaultPlan* prev;
+    explicit CtxScope(phx_moe_ctx* c) : prev(g_fault)
+    {
+        c->fault.pending = hipSuccess;  // a fault is reported by the call it happened in
+        g_fault = &c->fault;
+    }
+    ~CtxScope() { g_fault = prev; }
+};
+#define ENTER(c)               \
+    CtxScope ctx_scope_(c);    \
+    HIPCHK(c, hipSetDevice((c)->device))
+
 enum WsId {
     W_X, W_SHARED, W_OUT, W_RIN, W_XSCALE, W_AGU_Q, W_AGU_D, W_AGU_S, W_ASH_Q, W_ASH_D, W_ASH_S, W_LOGITS, W_IDS, W_W,
     W_OFF, W_PERM, W_TILES, W_NTILES, W_G, W_U, W_ADN_Q, W_ADN_D, W_ADN_S, W_YD, W_SHG, W_SHU, W_ASD_Q, W_ASD_D,
@@ -365,7 +404,7 @@ int ensure(phx_moe_ctx* c, int id, size_t bytes)
     b.p = nullptr;
     b.bytes = 0;
     size_t n = std::max<size_t>(bytes, 256);
-    HIPCHK(c, hipMalloc(&b.p, n));
+    HIPCHK(c, dev_malloc(c, &b.p, n));
     b.bytes = n;
     if (id == W_ZERO) HIPCHK(c, hipMemset(b.p, 0, n));
     return PHX_OK;
@@ -647,7 +686,7 @@ int run_layer_decode(phx_moe_ctx* c, const Layer& L, int T, const float* x, cons
         ProfScope p(c, PHX_K_COMBINE);
         launch_dec_combine(st, h);
     }
-    HIPCHK(c, hipGetLastError());
+    HIPCHK(c, launch_status(c));
     return PHX_OK;
 }
 
@@ -773,7 +812,7 @@ int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, con
         launch_combine(st, T, d, k, D.eps, wp<float>(c, W_YD), wp<float>(c, W_W), sh, L.post1, L.post2, out, xres,
                        L.post_ffw, c->flags);
     }
-    HIPCHK(c, hipGetLastError());
+    HIPCHK(c, launch_status(c));
     return PHX_OK;
 }
 
@@ -788,7 +827,7 @@ int upload_f32(phx_moe_ctx* c, const float* src, size_t n, float** dst)
 {
     if (*dst) HIPCHK(c, hipFree(*dst));
     *dst = nullptr;
-    HIPCHK(c, hipMalloc((void**)dst, std::max<size_t>(n, 1) * 4));
+    HIPCHK(c, dev_malloc(c, (void**)dst, std::max<size_t>(n, 1) * 4));
     HIPCHK(c, hipMemcpy(*dst, src, n * 4, hipMemcpyHostToDevice));
     return PHX_OK;
 }
@@ -818,7 +857,7 @@ int upload_iq_grids(phx_moe_ctx* c)
     for (int i = 0; i < 256; i++) g2xxs[i] = phx_iq2_grid_word(phx_iq2xxs_codes[i]);
     for (int i = 0; i < 1024; i++) g2s[i] = phx_iq2_grid_word(phx_iq2s_codes[i]);
     for (int i = 0; i < 512; i++) g3s[i] = phx_iq3s_grid_word(phx_iq3s_codes[i]);
-    HIPCHK(c, hipMalloc((void**)&c->iq_grid, kIqGridBytes));
+    HIPCHK(c, dev_malloc(c, (void**)&c->iq_grid, kIqGridBytes));
     HIPCHK(c, hipMemcpy(c->iq_grid, h.data(), kIqGridBytes, hipMemcpyHostToDevice));
     return PHX_OK;
 }
@@ -829,8 +868,8 @@ int upload_q(phx_moe_ctx* c, int type, const void* src, int n_mat, int rows, int
     HostQ h;
     repack(type, (const uint8_t*)src, n_mat, rows, cols, q, h, paired);
     q.grid = iq_type(type) ? iq_grid_of(c, type) : nullptr;
-    HIPCHK(c, hipMalloc((void**)&q.payload, h.payload.size()));
-    HIPCHK(c, hipMalloc((void**)&q.scale, h.scale.size()));
+    HIPCHK(c, dev_malloc(c, (void**)&q.payload, h.payload.size()));
+    HIPCHK(c, dev_malloc(c, (void**)&q.scale, h.scale.size()));
     HIPCHK(c, hipMemcpy(q.payload, h.payload.data(), h.payload.size(), hipMemcpyHostToDevice));
     HIPCHK(c, hipMemcpy(q.scale, h.scale.data(), h.scale.size(), hipMemcpyHostToDevice));
     return PHX_OK;
@@ -967,6 +1006,12 @@ int phx_moe_create(int hip_device, phx_moe_ctx** out)
     if (hip_device < 0 || hip_device >= n) return PHX_ERR_ARG;
     phx_moe_ctx* c = new phx_moe_ctx();
     c->device = hip_device;
+    if (const char* f = getenv("PHX_FAULT")) {  // "malloc:n" | "launch:n" (tests of the error paths)
+        long long n = 0;
+        if (sscanf(f, "malloc:%lld", &n) == 1) c->fault.site = FaultPlan::MALLOC;
+        else if (sscanf(f, "launch:%lld", &n) == 1) c->fault.site = FaultPlan::LAUNCH;
+        c->fault.n = n;
+    }
     int rc = PHX_OK;
     do {
         hipError_t h;
@@ -981,12 +1026,12 @@ int phx_moe_create(int hip_device, phx_moe_ctx** out)
         }
         std::vector<float> tab;
         build_gelu_table(tab);
-        if ((h = hipMalloc((void**)&c->gelu_tab, tab.size() * 4)) != hipSuccess) { rc = set_err(c, hip_code(h), "OOM"); break; }
+        if ((h = dev_malloc(c, (void**)&c->gelu_tab, tab.size() * 4)) != hipSuccess) { rc = set_err(c, hip_code(h), "OOM"); break; }
         if ((h = hipMemcpy(c->gelu_tab, tab.data(), tab.size() * 4, hipMemcpyHostToDevice)) != hipSuccess) {
             rc = set_err(c, hip_code(h), "gelu table upload failed");
             break;
         }
-        if ((h = hipMalloc((void**)&c->flags, 64)) != hipSuccess) { rc = set_err(c, hip_code(h), "OOM"); break; }
+        if ((h = dev_malloc(c, (void**)&c->flags, 64)) != hipSuccess) { rc = set_err(c, hip_code(h), "OOM"); break; }
         if ((h = hipMemset(c->flags, 0, 64)) != hipSuccess) { rc = set_err(c, hip_code(h), "memset failed"); break; }
         if ((rc = scratch_address(c)) != PHX_OK) break;
         c->ws_scratch.resize(W_COUNT);
@@ -1031,7 +1076,7 @@ int phx_moe_layer_upload(phx_moe_ctx* c, int layer, const phx_moe_layer_desc* D)
     int rc = phx_moe_check_desc(D);
     if (rc) return set_err(c, rc, "layer %d: invalid or unsupported descriptor (%d)", layer, rc);
     if (layer < 0 || layer > 4096) return set_err(c, PHX_ERR_ARG, "layer index %d out of range", layer);
-    HIPCHK(c, hipSetDevice(c->device));
+    ENTER(c);
     HIPCHK(c, hipStreamSynchronize(c->stream));
     if ((int)c->layers.size() <= layer) c->layers.resize(layer + 1);
     Layer& L = c->layers[layer];
@@ -1073,7 +1118,7 @@ int phx_moe_ffn(phx_moe_ctx* c, int layer, int T, float* x, const float* shared,
     int rc = check_ffn_args(c, layer, T, x, out, flags);
     if (rc) return rc;
     const Layer& L = c->layers[layer];
-    HIPCHK(c, hipSetDevice(c->device));
+    ENTER(c);
     rc = ensure_workspace(c, L, T);
     if (rc) return rc;
     c->last_scratch = false;
@@ -1110,7 +1155,7 @@ int phx_moe_ffn_noalloc(phx_moe_ctx* c, int layer, int T, float* x, const float*
     if (rc) return rc;
     if (!c->scratch || (int)c->ws_scratch.size() != W_COUNT) return set_err(c, PHX_ERR_HIP, "no scratch array");
     const Layer& L = c->layers[layer];
-    HIPCHK(c, hipSetDevice(c->device));
+    ENTER(c);
     // this call's workspace table, laid out afresh inside the scratch array (no allocation: the table
     // was sized at creation and the vectors only swap)
     std::swap(c->ws, c->ws_scratch);
@@ -1130,7 +1175,7 @@ int phx_moe_ffn_noalloc(phx_moe_ctx* c, int layer, int T, float* x, const float*
     c->profiling = prof;
     std::swap(c->ws, c->ws_scratch);
     if (rc) return rc;
-    HIPCHK(c, hipGetLastError());
+    HIPCHK(c, launch_status(c));
     c->last_T = T;
     c->last_layer = layer;
     c->last_scratch = true;
@@ -1206,7 +1251,7 @@ static int capture_decode_stack(phx_moe_ctx* c, int first, int n_layers, int T)
         ProfScope p(c, PHX_K_COMBINE);
         launch_dec_combine(st, prev);
     }
-    HIPCHK(c, hipGetLastError());
+    HIPCHK(c, launch_status(c));
     return PHX_OK;
 }
 
@@ -1219,7 +1264,7 @@ int phx_moe_stack_capture2(phx_moe_ctx* c, int first, int n_layers, int T, unsig
 {
     if (!c || n_layers <= 0 || first < 0 || first + n_layers > (int)c->layers.size() || T <= 0)
         return set_err(c, PHX_ERR_ARG, "bad stack range");
-    HIPCHK(c, hipSetDevice(c->device));
+    ENTER(c);
     int d = c->layers[first].desc.d;
     for (int l = first; l < first + n_layers; l++) {
         const Layer& L = c->layers[l];
@@ -1262,7 +1307,7 @@ int phx_moe_stack_run(phx_moe_ctx* c, float* x, int T, unsigned flags)
 {
     if (!c || !c->graph_exec) return set_err(c, PHX_ERR_ARG, "no captured stack");
     if (T != c->graph_T || !x) return set_err(c, PHX_ERR_ARG, "T=%d differs from the captured %d", T, c->graph_T);
-    HIPCHK(c, hipSetDevice(c->device));
+    ENTER(c);
     const size_t bytes = (size_t)T * c->layers[c->graph_first].desc.d * 4;
     const bool dev = flags & PHX_FLAG_DEVICE_PTRS;
     float* xs = wp<float>(c, W_X);
@@ -1288,7 +1333,7 @@ int phx_moe_stack_run(phx_moe_ctx* c, float* x, int T, unsigned flags)
 int phx_moe_sync(phx_moe_ctx* c)
 {
     if (!c) return PHX_ERR_ARG;
-    HIPCHK(c, hipSetDevice(c->device));
+    ENTER(c);
     HIPCHK(c, hipStreamSynchronize(c->stream));
     return PHX_OK;
 }
@@ -1296,15 +1341,15 @@ int phx_moe_sync(phx_moe_ctx* c)
 int phx_moe_dev_alloc(phx_moe_ctx* c, uint64_t bytes, void** ptr)
 {
     if (!c || !ptr) return PHX_ERR_ARG;
-    HIPCHK(c, hipSetDevice(c->device));
-    HIPCHK(c, hipMalloc(ptr, std::max<uint64_t>(bytes, 1)));
+    ENTER(c);
+    HIPCHK(c, dev_malloc(c, ptr, std::max<uint64_t>(bytes, 1)));
     return PHX_OK;
 }
 
 int phx_moe_dev_free(phx_moe_ctx* c, void* ptr)
 {
     if (!c) return PHX_ERR_ARG;
-    HIPCHK(c, hipSetDevice(c->device));
+    ENTER(c);
     HIPCHK(c, hipStreamSynchronize(c->stream));
     if (ptr) HIPCHK(c, hipFree(ptr));
     return PHX_OK;
@@ -1351,12 +1396,12 @@ int phx_moe_profile_read(phx_moe_ctx* c, double* total_ms, int64_t* launches)
 int phx_moe_selftest(phx_moe_ctx* c, int op, int n, const float* a, const float* b, float* out)
 {
     if (!c || n <= 0 || !a || !b || !out || op < 0 || op > 7) return PHX_ERR_ARG;
-    HIPCHK(c, hipSetDevice(c->device));
+    ENTER(c);
     float *da = nullptr, *db = nullptr, *dout = nullptr;
     size_t bytes = (size_t)n * 4;
-    HIPCHK(c, hipMalloc((void**)&da, bytes));
-    HIPCHK(c, hipMalloc((void**)&db, bytes));
-    HIPCHK(c, hipMalloc((void**)&dout, bytes));
+    HIPCHK(c, dev_malloc(c, (void**)&da, bytes));
+    HIPCHK(c, dev_malloc(c, (void**)&db, bytes));
+    HIPCHK(c, dev_malloc(c, (void**)&dout, bytes));
     HIPCHK(c, hipMemcpy(da, a, bytes, hipMemcpyHostToDevice));
     HIPCHK(c, hipMemcpy(db, b, bytes, hipMemcpyHostToDevice));
     launch_selftest(c->stream, op, n, da, db, dout, c->gelu_tab);
@@ -1371,9 +1416,9 @@ int phx_moe_selftest(phx_moe_ctx* c, int op, int n, const float* a, const float*
 int phx_moe_stream_read(phx_moe_ctx* c, const void* buf, uint64_t bytes, int iters, double* ms)
 {
     if (!c || !buf || bytes < 16 || iters <= 0 || !ms) return PHX_ERR_ARG;
-    HIPCHK(c, hipSetDevice(c->device));
+    ENTER(c);
     uint32_t* sink = nullptr;
-    HIPCHK(c, hipMalloc((void**)&sink, 256));
+    HIPCHK(c, dev_malloc(c, (void**)&sink, 256));
     hipEvent_t a, b;
     HIPCHK(c, hipEventCreate(&a));
     HIPCHK(c, hipEventCreate(&b));
@@ -1394,7 +1439,7 @@ int phx_moe_stream_read(phx_moe_ctx* c, const void* buf, uint64_t bytes, int ite
 int phx_moe_stream_copy(phx_moe_ctx* c, void* dst, const void* src, uint64_t bytes, int iters, double* ms)
 {
     if (!c || !dst || !src || bytes < 16 || bytes % 16 || iters <= 0 || !ms) return PHX_ERR_ARG;
-    HIPCHK(c, hipSetDevice(c->device));
+    ENTER(c);
     hipEvent_t a = nullptr, b = nullptr;
     HIPCHK(c, hipEventCreate(&a));
     HIPCHK(c, hipEventCreate(&b));
@@ -1439,9 +1484,9 @@ int phx_quant_q8_0(phx_moe_ctx* c, int mode, const float* x, const float* aux, i
     int rc = quant_check(c, mode, x, aux, rows, n, 32, qs);
     if (rc) return rc;
     if (!d) return set_err(c, PHX_ERR_ARG, "quant: null buffer");
-    HIPCHK(c, hipSetDevice(c->device));
+    ENTER(c);
     launch_quant(c->stream, 0, mode, rows, n, eps, x, aux, c->gelu_tab, qs, d, nullptr, nullptr, c->flags);
-    HIPCHK(c, hipGetLastError());
+    HIPCHK(c, launch_status(c));
     return PHX_OK;
 }
 
@@ -1452,9 +1497,9 @@ int phx_quant_q8_k(phx_moe_ctx* c, int mode, const float* x, const float* aux, i
     int rc = quant_check(c, mode, x, aux, rows, n, 256, qs);
     if (rc) return rc;
     if (!d) return set_err(c, PHX_ERR_ARG, "quant: null buffer");
-    HIPCHK(c, hipSetDevice(c->device));
+    ENTER(c);
     launch_quant(c->stream, 1, mode, rows, n, eps, x, aux, c->gelu_tab, qs, nullptr, d, bsums, c->flags);
-    HIPCHK(c, hipGetLastError());
+    HIPCHK(c, launch_status(c));
     return PHX_OK;
 }
 
@@ -1467,9 +1512,9 @@ int phx_norm_add(phx_moe_ctx* c, float* x, const float* y, const float* w, int r
     if (!x || !y || !w || (w2 && (!qs || !d))) return set_err(c, PHX_ERR_ARG, "norm_add: null buffer");
     if ((uintptr_t)x % 16 || (uintptr_t)y % 16 || (uintptr_t)w % 16 || (uintptr_t)w2 % 16 || (uintptr_t)qs % 4)
         return set_err(c, PHX_ERR_ARG, "norm_add: x, y, w, w2 need 16-byte, qs 4-byte alignment");
-    HIPCHK(c, hipSetDevice(c->device));
+    ENTER(c);
     launch_norm_add(c->stream, rows, n, eps, s, x, y, w, w2, w2 ? qs : nullptr, w2 ? d : nullptr, c->flags);
-    HIPCHK(c, hipGetLastError());
+    HIPCHK(c, launch_status(c));
     return PHX_OK;
 }
 
@@ -1481,7 +1526,7 @@ int phx_weight_upload(phx_moe_ctx* c, int type, int rows, int cols, const void* 
         return set_err(c, PHX_ERR_UNSUPPORTED, "weight upload: type %d (Q4_0 and Q8_0 only)", type);
     if (rows <= 0 || cols <= 0 || cols % 32 || cols > 16384 || !src)
         return set_err(c, PHX_ERR_ARG, "weight upload: shape %d x %d (cols a multiple of 32, <= 16384)", rows, cols);
-    HIPCHK(c, hipSetDevice(c->device));
+    ENTER(c);
     HIPCHK(c, hipStreamSynchronize(c->stream));
     phx_weight* w = new phx_weight();
     w->type = type;
@@ -1515,7 +1560,7 @@ int phx_matmul(phx_moe_ctx* c, const phx_weight* w, int T, const int8_t* xq, con
     if (T <= 0 || T > 65535) return set_err(c, PHX_ERR_ARG, "matmul: T=%d out of range", T);
     if ((uintptr_t)xq % 4 || (uintptr_t)xd % 2 || (uintptr_t)y % 4)
         return set_err(c, PHX_ERR_ARG, "matmul: xq needs 4-byte, xd 2-byte, y 4-byte alignment");
-    HIPCHK(c, hipSetDevice(c->device));
+    ENTER(c);
     const int nb = w->cols / 32;
     // many tokens: the matrix cores on the integers as exact fp16; a few: the VALU row walk
     const bool mma = T >= 32;
@@ -1558,7 +1603,7 @@ int phx_matmul(phx_moe_ctx* c, const phx_weight* w, int T, const int8_t* xq, con
     else
         launch_grouped(st, w->q, a, wp<Tile>(c, W_MM_TILES), wp<int>(c, W_MM_NT), max_tiles, A, wp<int>(c, W_MM_PERM), 1,
                        y, y, w->rows, w->rows);
-    HIPCHK(c, hipGetLastError());
+    HIPCHK(c, launch_status(c));
     return PHX_OK;
 }
 
@@ -1574,10 +1619,10 @@ int phx_matvec(phx_moe_ctx* c, int type, const void* w, int rows, int cols, int 
     if ((uintptr_t)w % 2 || (uintptr_t)xq % 16 || (uintptr_t)xd % 2 || (uintptr_t)y % 4)
         return set_err(c, PHX_ERR_ARG, "matvec: w and xd need 2-byte, xq 16-byte, y 4-byte alignment");
     const int dev = type == PHX_Q4_0 ? PHX_Q4_0_DEV : PHX_Q8_0_DEV;
-    HIPCHK(c, hipSetDevice(c->device));
+    ENTER(c);
     if (matvec_lds(dev, cols / 32) > 65536) return set_err(c, PHX_ERR_ARG, "matvec: cols %d too large", cols);
     launch_matvec(c->stream, dev, rows, cols / 32, T, (const uint8_t*)w, xq, xd, y);
-    HIPCHK(c, hipGetLastError());
+    HIPCHK(c, launch_status(c));
     return PHX_OK;
 }
 

@@ -44,6 +44,10 @@ class GpuDeviceLostError(MoeError):
     pass
 
 
+class OutOfDeviceMemoryError(MoeError, MemoryError):
+    """PHX_ERR_OOM: a device allocation failed (the context stays usable)."""
+
+
 class InvalidDataError(MoeError, ValueError):
     """A malformed GGUF file (InvalidDataException in the reference, src/Gguf.cs:116-210)."""
 
@@ -55,6 +59,8 @@ def _raise(code: int, msg: str):
         raise NotSupportedError(code, msg)
     if code == PHX.ERR_DEVICE_LOST:
         raise GpuDeviceLostError(code, msg)
+    if code == PHX.ERR_OOM:
+        raise OutOfDeviceMemoryError(code, msg)
     if code == PHX.ERR_FORMAT:
         raise InvalidDataError(code, msg)
     raise MoeError(code, msg)
