@@ -536,6 +536,15 @@ __device__ __forceinline__ void combine_into(const CombArgs& p, int t, float* sx
 // (:349) of the 32-blocks b with b % E == e, one 8-lane group per block.
 constexpr int RT_NT = 256;
 
+// the matrix-core kernels' copy of a Q8_0 activation dword (four integers as exact fp16, signed bytes
+// through the 1152 bias), for the general path's rows when it routes through this kernel
+__device__ __forceinline__ void store_qh(const Act& act, int t, int b, int l8, int qw)
+{
+    const uint32_t u = (uint32_t)qw ^ 0x80808080u;
+    *(uint2*)(act.qh + (int64_t)t * act.qhstride + 32 * b + 4 * l8) =
+        make_uint2(bias_pair(u, 0, 1152.0f), bias_pair(u, 1, 1152.0f));
+}
+
 template <int PER, bool FUSED>
 __device__ __forceinline__ void route_wg(const DecArgs& a, int t, int e, float* sx, float* sg, float* sw,
                                          const CombArgs& prev, float* scb)
@@ -638,6 +647,7 @@ __device__ __forceinline__ void route_wg(const DecArgs& a, int t, int e, float* 
                                             (xq.w * rinv) * nv.w),
                                 &dval, &sum);
         ((int*)(a.agu.q + (int64_t)t * a.agu.qstride))[8 * b + l8] = qw;
+        if (a.agu.qh) store_qh(a.agu, t, b, l8, qw);
         if (l8 == 0) {
             a.agu.d[(int64_t)t * a.agu.dstride + b] = dval;
             a.agu.s[(int64_t)t * a.agu.sstride + b] = sum;
@@ -647,6 +657,7 @@ __device__ __forceinline__ void route_wg(const DecArgs& a, int t, int e, float* 
                                                 (xq.w * rinv) * fv.w),
                                     &dval, &sum);
             ((int*)(a.ash.q + (int64_t)t * a.ash.qstride))[8 * b + l8] = qs;
+            if (a.ash.qh) store_qh(a.ash, t, b, l8, qs);
             if (l8 == 0) {
                 a.ash.d[(int64_t)t * a.ash.dstride + b] = dval;
                 a.ash.s[(int64_t)t * a.ash.sstride + b] = sum;
@@ -1170,6 +1181,51 @@ __device__ void write_routing(const DecArgs& a, LF Lr, const int* s_ids, const i
     }
 }
 
+// The general path's selection from the certified router (k_dec_route's sums and bounds), one
+// workgroup of CS_NT threads per token: the fast path of wave_topk, else select_exact (counted as a
+// router fallback); then the token's ids and weights (as write_routing) and the logits it used.
+constexpr int CS_NT = 256;
+__global__ __launch_bounds__(CS_NT) void k_cert_select(DecArgs a)
+{
+    extern __shared__ __align__(16) unsigned char csm[];  // sel_lds(1, E, d, CS_NT)
+    __shared__ int s_ids[PHX_MAX_USED_DEV];
+    __shared__ unsigned s_kb[2 * PHX_MAX_USED_DEV];
+    __shared__ double red[CS_NT / 64 + 1];
+    __shared__ int s_bad;
+    const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    DecArgs b = a;  // the token's own view: one token
+    b.T = 1;
+    b.x = a.x + (int64_t)t * a.d;
+    b.Lb = a.Lb + (int64_t)t * a.E;
+    b.Bb = a.Bb + (int64_t)t * a.E;
+    if (wave == 0) {
+        SelIn in;
+        sel_issue(b, 0, in);
+        const bool cert = wave_topk(b, 0, in, s_ids, s_kb, s_kb + PHX_MAX_USED_DEV);
+        if (lane == 0) s_bad = !cert;
+    }
+    __syncthreads();
+    const bool exact = s_bad != 0;  // uniform
+    if (exact) select_exact(b, csm, s_ids, &s_bad, red, true);
+    const double* sL = (const double*)csm;
+    for (int e = tid; e < a.E; e += CS_NT) a.logits[(int64_t)t * a.E + e] = (float)(exact ? sL[e] : b.Lb[e]);
+    if (wave == 0) {  // weights (src/GemmaCpu.cs:406-407,417), as write_routing
+        const int j = lane;
+        const bool act = j < a.k;
+        const int id = act ? s_ids[j] : 0;
+        const float selj = act ? (float)(exact ? sL[id] : b.Lb[id]) : 0.0f;
+        const float sel0 = __shfl(selj, 0, 64);
+        const float top = (a.rule == 1 && j > 0) ? 1.0f : sel0;
+        const float pj = act ? (float)exp((double)(selj - top)) : 0.0f;
+        double sum = 0.0;
+        for (int q = 0; q < a.k; q++) sum += (double)__shfl(pj, q, 64);  // in rank order
+        if (act) {
+            a.ids[(int64_t)t * a.k + j] = id;
+            a.w[(int64_t)t * a.k + j] = (float)((double)pj / sum) * a.ds[id];
+        }
+    }
+}
+
 // PRESEL: the selection's inputs are loaded at entry and held in registers through the shared units
 // (left out where the register budget is tight)
 template <int TYPE, bool PRESEL>
@@ -1545,6 +1601,13 @@ void launch_dec_route(hipStream_t st, const DecLayerH& h)
 {
     launch(k_dec_route, dim3(h.T * h.E), dim3(RT_NT), (uint32_t)((size_t)3 * route_row_floats(h.d) * 4), st,
            dec_args(h));
+}
+
+void launch_cert_select(hipStream_t st, const DecLayerH& h)
+{
+    const size_t lds = sel_lds(1, h.E, h.d, CS_NT).total;
+    raise_lds(k_cert_select, lds);
+    launch(k_cert_select, dim3(h.T), dim3(CS_NT), (uint32_t)lds, st, dec_args(h));
 }
 
 void launch_dec_route_fused(hipStream_t st, const DecLayerH& prev, const DecLayerH& h)

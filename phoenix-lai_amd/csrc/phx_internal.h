@@ -189,6 +189,8 @@ struct DecLayerH {
 };
 bool dec_supported(const DecLayerH& h);
 void launch_dec_route(hipStream_t st, const DecLayerH& h);
+// the general path's selection from k_dec_route's certified sums: ids, weights and logits per token
+void launch_cert_select(hipStream_t st, const DecLayerH& h);
 // a stack layer's router with the previous layer's combine folded in (prev: that layer, its xin the
 // rows it reads, its xres where the new x goes; h.x must be prev.xres)
 void launch_dec_route_fused(hipStream_t st, const DecLayerH& prev, const DecLayerH& h);

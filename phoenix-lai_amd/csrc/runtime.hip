@@ -691,7 +691,22 @@ int run_layer_decode(phx_moe_ctx* c, const Layer& L, int T, const float* x, cons
 }
 
 // Enqueue one MoE FFN block on the context stream (any T; exact router chains).
-int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, const float* shared, float* out, float* xres)
+// The general path routes through the certified router (k_dec_route's double sums and bounds, then
+// k_cert_select: the decode path's selection, exact chains for a token it cannot certify) where the
+// router launch has few enough workgroups (T * E of them, each reading a router row) and the expert
+// input is Q8_0 (k_dec_route writes it, with the matrix cores' fp16 copy where the rows carry one);
+// otherwise, and always under PHX_FLAG_EXACT_ROUTER, through the exact float chains.
+constexpr int CERT_MAX_TE = 8192;
+bool cert_route(const Layer& L, int T, bool shared_ffn)
+{
+    const phx_moe_layer_desc& D = L.desc;
+    if ((int64_t)T * D.n_expert > CERT_MAX_TE || D.d > 4096 || D.d % 256 != 0 || D.n_expert > 256) return false;
+    if (!dec_type(D.gate_up_type) || (shared_ffn && !dec_type(D.shared_type))) return false;
+    return true;
+}
+
+int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, const float* shared, float* out, float* xres,
+                      bool exact)
 {
     const phx_moe_layer_desc& D = L.desc;
     hipStream_t st = c->stream;
@@ -719,18 +734,34 @@ int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, con
         ash.qh = wp<uint16_t>(c, W_ASH_H);
         ash.qhstride = d;
     }
-    {
-        ProfScope p(c, PHX_K_PROLOGUE);
-        launch_prologue(st, T, d, D.eps, x, L.gis, L.pre2, shared_ffn ? L.ffn_norm : nullptr, wp<float>(c, W_RIN),
-                        wp<float>(c, W_XSCALE), agu, ash, c->flags);
-    }
-    {
-        ProfScope p(c, PHX_K_ROUTER);
-        launch_router_exact(st, T, d, E, L.wt4, wp<float>(c, W_RIN), wp<float>(c, W_LOGITS));
-    }
-    {
-        ProfScope p(c, PHX_K_TOPK);
-        launch_topk(st, T, E, k, D.weight_rule, wp<float>(c, W_LOGITS), L.ds, wp<int>(c, W_IDS), wp<float>(c, W_W));
+    if (!exact && cert_route(L, T, shared_ffn)) {
+        // the router's certified sums with the expert (and shared) inputs quantized beside them, then
+        // the selection
+        DecLayerH h = dec_layer(c, L, T, x, shared, out, xres);
+        h.agu = agu;
+        h.ash = ash;
+        {
+            ProfScope p(c, PHX_K_ROUTER);
+            launch_dec_route(st, h);
+        }
+        {
+            ProfScope p(c, PHX_K_TOPK);
+            launch_cert_select(st, h);
+        }
+    } else {
+        {
+            ProfScope p(c, PHX_K_PROLOGUE);
+            launch_prologue(st, T, d, D.eps, x, L.gis, L.pre2, shared_ffn ? L.ffn_norm : nullptr, wp<float>(c, W_RIN),
+                            wp<float>(c, W_XSCALE), agu, ash, c->flags);
+        }
+        {
+            ProfScope p(c, PHX_K_ROUTER);
+            launch_router_exact(st, T, d, E, L.wt4, wp<float>(c, W_RIN), wp<float>(c, W_LOGITS));
+        }
+        {
+            ProfScope p(c, PHX_K_TOPK);
+            launch_topk(st, T, E, k, D.weight_rule, wp<float>(c, W_LOGITS), L.ds, wp<int>(c, W_IDS), wp<float>(c, W_W));
+        }
     }
     // tile sizes: the MFMA kernels' 128 (Q4_0 / Q8_0) and 32 (K-quants), the VALU kernels' 4 (their row
     // walk is VALU-bound: larger tiles cost occupancy and measured slower)
@@ -820,7 +851,7 @@ int run_layer(phx_moe_ctx* c, const Layer& L, int T, const float* x, const float
               unsigned flags)
 {
     if (use_decode(c, L, T, flags)) return run_layer_decode(c, L, T, x, shared, out, xres);
-    return run_layer_general(c, L, T, x, shared, out, xres);
+    return run_layer_general(c, L, T, x, shared, out, xres, (flags & PHX_FLAG_EXACT_ROUTER) != 0);
 }
 
 int upload_f32(phx_moe_ctx* c, const float* src, size_t n, float** dst)

@@ -2,9 +2,10 @@
 
 configs[2] (C3): prefill, T = 2048 with Zipf(1.1) routing, on the matrix-core path; configs[3] (C4):
 K-quants at T = 512 with the Q6_K down padded 1408 -> 1536; configs[4] (C5): the 30-layer batched
-decode stack at T = 32 with one hot expert, captured as one HIP graph.  T > 16 runs the general path,
-whose router replays the reference's float chains, so logits, ids, lists, weights and outputs are all
-compared bit for bit.
+decode stack at T = 32 with one hot expert, captured as one HIP graph.  T > 16 runs the general path;
+under PHX_FLAG_EXACT_ROUTER its router replays the reference's float chains, so logits, ids, lists,
+weights and outputs are all compared bit for bit.  Without the flag a C5 layer routes through the
+certified router (ids and lists bit-exact, outputs within the tolerance), checked layer by layer.
 """
 import sys
 import time
@@ -101,9 +102,17 @@ def test_c5_stack_30_layers(ctx, pkg, orc):
     # the bias channel x[t][d-1] carries the hot expert into layer 0; every residual add then moves it,
     # so later layers see the bias only partly
     assert hot[0] > 0.3
-    ctx.stack_capture(0, n, T)
+    ctx.stack_capture(0, n, T, exact_router=True)
     for rep in range(2):
         got = ctx.stack_run(x0)
         np.testing.assert_array_equal(got, ref, err_msg=f"replay {rep}: 30-layer stack differs from the oracle")
         say(f"c5 replay {rep}: 30 layers bit-exact")
+    # the default routing (certified router): each distinct layer on the oracle's own input for it
+    from test_gpu_parity import check_layer
+    xin = x0.copy()
+    for i in range(3):
+        L = distinct[i]
+        check_layer(ctx, orc, L, xin, tag=f"c5 certified layer {i}", layer=i)
+        out, _, _ = orc.moe_block(L, xin)
+        xin = orc.residual(L, xin, out)
     del distinct
