@@ -255,8 +255,9 @@ int phx_matvec(phx_moe_ctx* ctx, int type, const void* w, int rows, int cols, in
 /* Prefill matmul of a dense quantized matrix over T token rows: KernelsPrefill.MatMulQ4Q8Tile as
  * GemmaGpu.Mm records it (src/KernelsPrefill.cs:143-260, src/GemmaGpu.cs:907-923) for the shared FFN
  * and every other dense projection of a prompt chunk.  phx_weight_upload repacks `rows` GGUF rows of
- * `cols` (PHX_Q4_0 or PHX_Q8_0, host memory, as the file holds them) into the device's row groups once
- * (GemmaGpu.UploadW, src/GemmaGpu.cs:344-352); phx_weight_free releases them.  phx_matmul: xq / xd are
+ * `cols` (PHX_Q4_0 or PHX_Q8_0; PHX_Q4_K or PHX_Q6_K for phx_matmul_k, cols a multiple of 256; host
+ * memory, as the file holds them) into the device's row groups once (GemmaGpu.UploadW / UploadK,
+ * src/GemmaGpu.cs:344-352, 402-436); phx_weight_free releases them.  phx_matmul: xq / xd are
  * T Q8_0 rows in the layout of phx_quant_q8_0 (device pointers, xq 4-byte aligned) and
  * y[t][r] = CpuRef.MatVec's value for token t (src/CpuRef.cs:91-119, src/CpuRefGemma.cs:12-40: the block
  * terms (float)isum * (d_w * d_x) added in block order), on the matrix cores for T >= 32;
@@ -265,6 +266,17 @@ typedef struct phx_weight phx_weight;
 int phx_weight_upload(phx_moe_ctx* ctx, int type, int rows, int cols, const void* gguf_rows, phx_weight** out);
 void phx_weight_free(phx_moe_ctx* ctx, phx_weight* w);
 int phx_matmul(phx_moe_ctx* ctx, const phx_weight* w, int T, const int8_t* xq, const uint16_t* xd, float* y);
+
+/* Dense K-quant matvec over T token rows: KernelsK.MatVec for Q4_K / Q6_K weights as GemmaGpu.MatVec
+ * records it (src/KernelsKQuants.cs:65-108, src/GemmaGpu.cs:471-473, bindings w, kq, kd, y), for any
+ * K-quant dense projection (the shared FFN and attention of a K-quant model).  w: a phx_weight_upload
+ * handle of type PHX_Q4_K or PHX_Q6_K (cols a multiple of 256; Q4_0 / Q8_0 handles return
+ * PHX_ERR_UNSUPPORTED).  xq / xd: T Q8_K input rows in the layout of phx_quant_q8_k (qs int8 [T][cols],
+ * d float [T][cols/256]; device pointers, 4-byte aligned); the block sums are formed from xq.
+ * y[t][r] = CpuRefKQuants.MatVecK's value for token t (src/CpuRefKQuants.cs:176-232: DotK's integer lane
+ * sums, the eight float lanes and their fold); on the matrix cores from 8 rows, the VALU row walk below;
+ * asynchronous on the context's stream. */
+int phx_matmul_k(phx_moe_ctx* ctx, const phx_weight* w, int T, const int8_t* xq, const float* xd, float* y);
 
 #ifdef __cplusplus
 }

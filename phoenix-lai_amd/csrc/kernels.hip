@@ -12,6 +12,57 @@ namespace phx {
 
 // ------------------------------------------------------------------------------ activation quantizers
 
+// The integers of Q8_K super-block b of row `row` (lane l holds elements 4l..4l+3 packed in pk) stored in
+// act's dot-product order (K4 / K6 / Q8K), with the sums of 16 (K4's s, and bh when set) and, with qh
+// set, the matrix cores' fp16 copies; the block's scale is the caller's.  qrow is the wave's 64-dword
+// LDS row through which the integers reach the packed orders.  Wave-level: all 64 lanes call it.
+__device__ __forceinline__ void store_q8k_block(const Act& act, int64_t row, int b, int lane, uint32_t pk,
+                                                uint32_t* qrow)
+{
+    int sm = (int)(int8_t)(pk & 0xFF) + (int)(int8_t)((pk >> 8) & 0xFF) + (int)(int8_t)((pk >> 16) & 0xFF) +
+             (int)(int8_t)(pk >> 24);
+    // block sums of 16: lanes 4j .. 4j + 3
+    sm += __shfl_xor(sm, 1, 64);
+    sm += __shfl_xor(sm, 2, 64);
+    if ((lane & 3) == 0) {
+        if (act.fmt == ACT_K4) act.s[row * act.sstride + b * 16 + (lane >> 2)] = sm;
+        if (act.bh) act.bh[row * act.bhstride + b * 16 + (lane >> 2)] = (uint16_t)f2h_bits((float)sm);  // exact
+    }
+    if (act.fmt == ACT_Q8K) {
+        ((uint32_t*)(act.q + row * act.qstride + (int64_t)b * 256))[lane] = pk;
+        if (!act.qh) return;  // uniform
+    }
+    const uint8_t* qb = (const uint8_t*)qrow;
+    qrow[lane] = pk;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    auto qv = [&](int e) { return (int)(int8_t)qb[e]; };
+    if (act.fmt == ACT_K4) {  // dword (s, l) = x[32 s + l + 8 m], m = 0..3: lane = 8 s + l
+        const int s8 = lane >> 3, l = lane & 7, e = 32 * s8 + l;
+        ((uint32_t*)(act.q + row * act.qstride + (int64_t)b * 256))[lane] =
+            (uint32_t)qb[e] | ((uint32_t)qb[e + 8] << 8) | ((uint32_t)qb[e + 16] << 16) | ((uint32_t)qb[e + 24] << 24);
+    } else if (act.fmt == ACT_K6) {  // (P, l): lane = 8 P + l
+        const int P = lane >> 3, l = lane & 7, e = 32 * P + l;
+        uint32_t* dst = (uint32_t*)(act.q + row * act.qstride + (int64_t)b * 512);
+        int* c = act.s + row * act.sstride + b * 128;
+        dst[lane * 2 + 0] = (uint32_t)qb[e] | ((uint32_t)qb[e + 8] << 8);
+        dst[lane * 2 + 1] = ((uint32_t)qb[e + 16] << 16) | ((uint32_t)qb[e + 24] << 24);
+        c[(2 * P) * 8 + l] = -32 * (qv(e) + qv(e + 8));
+        c[(2 * P + 1) * 8 + l] = -32 * (qv(e + 16) + qv(e + 24));
+    }
+    if (act.qh) {  // the matrix cores' copy: exact fp16 integers, halves [l][s][mm']: lane = 8 l + s
+        const int l = lane >> 3, s8 = lane & 7, e = 32 * s8 + l;
+        uint32_t* hq = (uint32_t*)(act.qh + row * act.qhstride + (int64_t)b * 256) + l * 16 + s8 * 2;
+        hq[0] = f2h_bits((float)qv(e)) | (f2h_bits((float)qv(e + 16)) << 16);
+        hq[1] = f2h_bits((float)qv(e + 8)) | (f2h_bits((float)qv(e + 24)) << 16);
+    }
+    // the row is rewritten by the wave's next block only after every lane's reads above
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // Quantize one row (in LDS, `cols` floats) into format act, row index `row`.  Block-level (NT threads).
 //  Q8_0: CpuRef.QuantizeQ8_0 (src/CpuRef.cs:49-62), plus the block sum of q for the Q4_0 offset.
 //  K4/K6/Q8K: CpuRef.QuantizeQ8_K (src/CpuRefKQuants.cs:53-86), stored in the dot-product orders (and,
@@ -49,7 +100,6 @@ __device__ void quantize_row(const float* v, Act act, int64_t row)
     // the wave's LDS row to reach the packed orders
     __shared__ uint32_t qsm[NT / 64][64];
     const int nb = act.cols / 256, lane = tid & 63, wave = tid >> 6;
-    const uint8_t* qb = (const uint8_t*)qsm[wave];
     for (int b = wave; b < nb; b += NT / 64) {
         const float4 v4 = ((const float4*)(v + b * 256))[lane];
         const float x[4] = {v4.x, v4.y, v4.z, v4.w};
@@ -74,54 +124,13 @@ __device__ void quantize_row(const float* v, Act act, int64_t row)
             }
         }
         const float iscale = amax == 0.0f ? 0.0f : -127.0f / vmax;
-        int q[4], sm = 0;
+        int q[4];
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            q[j] = amax == 0.0f ? 0 : min(nearest_int(iscale * x[j]), 127);
-            sm += q[j];
-        }
+        for (int j = 0; j < 4; j++) q[j] = amax == 0.0f ? 0 : min(nearest_int(iscale * x[j]), 127);
         const uint32_t pk = (uint32_t)(q[0] & 0xFF) | ((uint32_t)(q[1] & 0xFF) << 8) | ((uint32_t)(q[2] & 0xFF) << 16) |
                             ((uint32_t)q[3] << 24);
         if (lane == 0) act.d[row * act.dstride + b] = amax == 0.0f ? 0.0f : 1.0f / iscale;
-        // block sums of 16: lanes 4j .. 4j + 3
-        sm += __shfl_xor(sm, 1, 64);
-        sm += __shfl_xor(sm, 2, 64);
-        if ((lane & 3) == 0) {
-            if (act.fmt == ACT_K4) act.s[row * act.sstride + b * 16 + (lane >> 2)] = sm;
-            if (act.bh) act.bh[row * act.bhstride + b * 16 + (lane >> 2)] = (uint16_t)f2h_bits((float)sm);  // exact
-        }
-        if (act.fmt == ACT_Q8K) {
-            ((uint32_t*)(act.q + row * act.qstride + (int64_t)b * 256))[lane] = pk;
-            if (!act.qh) continue;  // uniform
-        }
-        qsm[wave][lane] = pk;
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        auto qv = [&](int e) { return (int)(int8_t)qb[e]; };
-        if (act.fmt == ACT_K4) {  // dword (s, l) = x[32 s + l + 8 m], m = 0..3: lane = 8 s + l
-            const int s8 = lane >> 3, l = lane & 7, e = 32 * s8 + l;
-            ((uint32_t*)(act.q + row * act.qstride + (int64_t)b * 256))[lane] =
-                (uint32_t)qb[e] | ((uint32_t)qb[e + 8] << 8) | ((uint32_t)qb[e + 16] << 16) | ((uint32_t)qb[e + 24] << 24);
-        } else if (act.fmt == ACT_K6) {  // (P, l): lane = 8 P + l
-            const int P = lane >> 3, l = lane & 7, e = 32 * P + l;
-            uint32_t* dst = (uint32_t*)(act.q + row * act.qstride + (int64_t)b * 512);
-            int* c = act.s + row * act.sstride + b * 128;
-            dst[lane * 2 + 0] = (uint32_t)qb[e] | ((uint32_t)qb[e + 8] << 8);
-            dst[lane * 2 + 1] = ((uint32_t)qb[e + 16] << 16) | ((uint32_t)qb[e + 24] << 24);
-            c[(2 * P) * 8 + l] = -32 * (qv(e) + qv(e + 8));
-            c[(2 * P + 1) * 8 + l] = -32 * (qv(e + 16) + qv(e + 24));
-        }
-        if (act.qh) {  // the matrix cores' copy: exact fp16 integers, halves [l][s][mm']: lane = 8 l + s
-            const int l = lane >> 3, s8 = lane & 7, e = 32 * s8 + l;
-            uint32_t* hq = (uint32_t*)(act.qh + row * act.qhstride + (int64_t)b * 256) + l * 16 + s8 * 2;
-            hq[0] = f2h_bits((float)qv(e)) | (f2h_bits((float)qv(e + 16)) << 16);
-            hq[1] = f2h_bits((float)qv(e + 8)) | (f2h_bits((float)qv(e + 24)) << 16);
-        }
-        // the row is rewritten by the next block's wave only after every lane's reads above
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        store_q8k_block(act, row, b, lane, pk, qsm[wave]);
     }
 }
 
@@ -1410,6 +1419,29 @@ void launch_planar_act(hipStream_t st, int rows, int n, const int8_t* qs, const 
 {
     const int64_t nblk = (int64_t)rows * (n / 32);
     launch(k_planar_act, dim3((unsigned)((nblk * 8 + 255) / 256)), dim3(256), 0, st, nblk, n / 32, qs, d, a);
+}
+
+// Planar Q8_K rows (qs int8 [rows][n] in element order and the float scale [rows][n/256], the layout
+// phx_quant_q8_k writes) into the K-quant kernels' activation arrays (ACT_K4 / ACT_K6 orders, the sums
+// of 16, and with a.qh / a.bh set the matrix cores' fp16 copies).  One wave per 256-block.
+__global__ __launch_bounds__(256) void k_planar_act_k(int64_t nblk, int nb, const int8_t* __restrict__ qs,
+                                                      const float* __restrict__ d, Act a)
+{
+    __shared__ uint32_t qsm[4][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t g = (int64_t)blockIdx.x * 4 + wave;
+    if (g >= nblk) return;  // wave-uniform; the block store synchronises within the wave only
+    const int64_t t = g / nb;
+    const int b = (int)(g - t * nb);
+    const uint32_t pk = ((const uint32_t*)qs)[g * 64 + lane];
+    if (lane == 0) a.d[t * a.dstride + b] = d[g];
+    store_q8k_block(a, t, b, lane, pk, qsm[wave]);
+}
+
+void launch_planar_act_k(hipStream_t st, int rows, int n, const int8_t* qs, const float* d, Act a)
+{
+    const int64_t nblk = (int64_t)rows * (n / 256);
+    launch(k_planar_act_k, dim3((unsigned)((nblk + 3) / 4)), dim3(256), 0, st, nblk, n / 256, qs, d, a);
 }
 
 // Fill n 32-bit words with v: clears workspace that must start at zero with a kernel rather than a

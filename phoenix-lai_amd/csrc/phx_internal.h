@@ -201,6 +201,8 @@ void launch_stream_read(hipStream_t st, const void* src, int64_t bytes, uint32_t
 void launch_stream_copy(hipStream_t st, void* dst, const void* src, int64_t bytes);
 void launch_fill_u32(hipStream_t st, uint32_t* p, int64_t n, uint32_t v);
 void launch_planar_act(hipStream_t st, int rows, int n, const int8_t* qs, const uint16_t* d, Act a);
+// planar Q8_K rows (qs [rows][n], d [rows][n/256]) into a's K-quant orders (ACT_K4 / ACT_K6, qh / bh when set)
+void launch_planar_act_k(hipStream_t st, int rows, int n, const int8_t* qs, const float* d, Act a);
 void launch_selftest(hipStream_t st, int op, int n, const float* a, const float* b, float* out, const float* gelu_tab);
 
 }  // namespace phx

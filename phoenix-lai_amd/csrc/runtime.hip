@@ -383,7 +383,8 @@ enum WsId {
     W_X, W_SHARED, W_OUT, W_RIN, W_XSCALE, W_AGU_Q, W_AGU_D, W_AGU_S, W_ASH_Q, W_ASH_D, W_ASH_S, W_LOGITS, W_IDS, W_W,
     W_OFF, W_PERM, W_TILES, W_NTILES, W_G, W_U, W_ADN_Q, W_ADN_D, W_ADN_S, W_YD, W_SHG, W_SHU, W_ASD_Q, W_ASD_D,
     W_ASD_S, W_SHOUT, W_ZERO, W_STILES, W_SNTILES, W_SOFF, W_SPERM, W_LB, W_BB, W_ADEC, W_SDEC, W_AGUP, W_ASHP, W_AGU_H, W_ADN_H, W_ASH_H, W_ASD_H, W_X2,
-    W_MM_IDS, W_MM_OFF, W_MM_PERM, W_MM_TILES, W_MM_NT, W_MM_D, W_MM_S, W_MM_H, W_AGU_BH, W_ADN_BH, W_COUNT
+    W_MM_IDS, W_MM_OFF, W_MM_PERM, W_MM_TILES, W_MM_NT, W_MM_D, W_MM_S, W_MM_H, W_AGU_BH, W_ADN_BH, W_MK_Q, W_MK_BH,
+    W_COUNT
 };
 
 int ensure(phx_moe_ctx* c, int id, size_t bytes)
@@ -1553,10 +1554,11 @@ int phx_weight_upload(phx_moe_ctx* c, int type, int rows, int cols, const void* 
 {
     if (!c || !out) return PHX_ERR_ARG;
     *out = nullptr;
-    if (type != PHX_Q4_0 && type != PHX_Q8_0)
-        return set_err(c, PHX_ERR_UNSUPPORTED, "weight upload: type %d (Q4_0 and Q8_0 only)", type);
-    if (rows <= 0 || cols <= 0 || cols % 32 || cols > 16384 || !src)
-        return set_err(c, PHX_ERR_ARG, "weight upload: shape %d x %d (cols a multiple of 32, <= 16384)", rows, cols);
+    if (type != PHX_Q4_0 && type != PHX_Q8_0 && type != PHX_Q4_K && type != PHX_Q6_K)
+        return set_err(c, PHX_ERR_UNSUPPORTED, "weight upload: type %d (Q4_0, Q8_0, Q4_K and Q6_K only)", type);
+    const int be = block_elems(type);
+    if (rows <= 0 || cols <= 0 || cols % be || cols > 16384 || !src)
+        return set_err(c, PHX_ERR_ARG, "weight upload: shape %d x %d (cols a multiple of %d, <= 16384)", rows, cols, be);
     ENTER(c);
     HIPCHK(c, hipStreamSynchronize(c->stream));
     phx_weight* w = new phx_weight();
@@ -1589,6 +1591,8 @@ int phx_matmul(phx_moe_ctx* c, const phx_weight* w, int T, const int8_t* xq, con
     if (!c) return PHX_ERR_ARG;
     if (!w || !xq || !xd || !y) return set_err(c, PHX_ERR_ARG, "matmul: null argument");
     if (T <= 0 || T > 65535) return set_err(c, PHX_ERR_ARG, "matmul: T=%d out of range", T);
+    if (w->type != PHX_Q4_0 && w->type != PHX_Q8_0)
+        return set_err(c, PHX_ERR_UNSUPPORTED, "matmul: weight type %d takes Q8_K input (phx_matmul_k)", w->type);
     if ((uintptr_t)xq % 4 || (uintptr_t)xd % 2 || (uintptr_t)y % 4)
         return set_err(c, PHX_ERR_ARG, "matmul: xq needs 4-byte, xd 2-byte, y 4-byte alignment");
     ENTER(c);
@@ -1631,6 +1635,62 @@ int phx_matmul(phx_moe_ctx* c, const phx_weight* w, int T, const int8_t* xq, con
     if (mma)
         launch_grouped_mfma(st, w->q, a, wp<Tile>(c, W_MM_TILES), wp<int>(c, W_MM_NT), max_tiles, wp<int>(c, W_MM_PERM), 1,
                             y, y, w->rows, w->rows, 0, nullptr, 0, nullptr);
+    else
+        launch_grouped(st, w->q, a, wp<Tile>(c, W_MM_TILES), wp<int>(c, W_MM_NT), max_tiles, A, wp<int>(c, W_MM_PERM), 1,
+                       y, y, w->rows, w->rows);
+    HIPCHK(c, launch_status(c));
+    return PHX_OK;
+}
+
+int phx_matmul_k(phx_moe_ctx* c, const phx_weight* w, int T, const int8_t* xq, const float* xd, float* y)
+{
+    if (!c) return PHX_ERR_ARG;
+    if (!w || !xq || !xd || !y) return set_err(c, PHX_ERR_ARG, "matmul_k: null argument");
+    if (T <= 0 || T > 65535) return set_err(c, PHX_ERR_ARG, "matmul_k: T=%d out of range", T);
+    if (w->type != PHX_Q4_K && w->type != PHX_Q6_K)
+        return set_err(c, PHX_ERR_UNSUPPORTED, "matmul_k: weight type %d (Q4_K and Q6_K only)", w->type);
+    if ((uintptr_t)xq % 4 || (uintptr_t)xd % 4 || (uintptr_t)y % 4)
+        return set_err(c, PHX_ERR_ARG, "matmul_k: xq, xd and y need 4-byte alignment");
+    ENTER(c);
+    const int fmt = act_fmt(w->type), cols = w->cols;
+    // the general path's rule with one matrix (at least 8 rows per matrix): the matrix cores, else the
+    // VALU row walk
+    const bool kmma = T >= 8;
+    const int A = kmma ? kKmmaTile : kTileA;
+    const int max_tiles = (T + A - 1) / A;
+    size_t qb, db, sb;
+    act_sizes(fmt, T, cols, qb, db, sb);
+    int rc;
+#define ENS(id, bytes) \
+    if ((rc = ensure(c, id, (size_t)(bytes)))) return rc
+    ENS(W_MM_IDS, (size_t)T * 4);
+    ENS(W_MM_OFF, 8);
+    ENS(W_MM_PERM, (size_t)T * 4);
+    ENS(W_MM_TILES, (size_t)max_tiles * sizeof(Tile));
+    ENS(W_MM_NT, 4);
+    ENS(W_MK_Q, qb);
+    ENS(W_MM_D, db);
+    ENS(W_MM_S, sb);
+    if (kmma) ENS(W_MM_H, (size_t)T * cols * 2);
+    if (kmma && fmt == ACT_K4) ENS(W_MK_BH, (size_t)T * (cols / 16) * 2);
+#undef ENS
+    hipStream_t st = c->stream;
+    Act a = make_act(c, fmt, cols, W_MK_Q, W_MM_D, W_MM_S);
+    if (kmma) {
+        a.qh = wp<uint16_t>(c, W_MM_H);
+        a.qhstride = cols;
+        if (fmt == ACT_K4) {
+            a.bh = wp<uint16_t>(c, W_MK_BH);
+            a.bhstride = cols / 16;
+        }
+    }
+    launch_planar_act_k(st, T, cols, xq, xd, a);
+    launch_fill_u32(st, (uint32_t*)wp<int>(c, W_MM_IDS), T, 0u);
+    launch_dispatch(st, T, 1, A, wp<int>(c, W_MM_IDS), wp<int>(c, W_MM_OFF), wp<int>(c, W_MM_PERM),
+                    wp<Tile>(c, W_MM_TILES), wp<int>(c, W_MM_NT));
+    if (kmma)
+        launch_grouped_kmma(st, w->q, a, wp<Tile>(c, W_MM_TILES), wp<int>(c, W_MM_NT), max_tiles, wp<int>(c, W_MM_PERM), 1,
+                            y, y, w->rows, w->rows);
     else
         launch_grouped(st, w->q, a, wp<Tile>(c, W_MM_TILES), wp<int>(c, W_MM_NT), max_tiles, A, wp<int>(c, W_MM_PERM), 1,
                        y, y, w->rows, w->rows);

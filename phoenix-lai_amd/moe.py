@@ -145,6 +145,7 @@ def load_lib():
         "phx_weight_upload": (i32, [vp, i32, i32, i32, vp, C.POINTER(vp)]),
         "phx_weight_free": (None, [vp, vp]),
         "phx_matmul": (i32, [vp, vp, i32, vp, vp, vp]),
+        "phx_matmul_k": (i32, [vp, vp, i32, vp, vp, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -440,9 +441,9 @@ class MoeContext:
         """phx_weight_upload (GemmaGpu.UploadW): GGUF rows from host memory, repacked on the device once;
         returns the handle for matmul_device / weight_free."""
         w = np.ascontiguousarray(w, dtype=np.uint8)
-        bb = 18 if wtype == PHX.Q4_0 else 34
-        if w.size != rows * (cols // 32) * bb:
-            raise ArgumentError(PHX.ERR_ARG, f"weight bytes {w.size} != {rows} rows x {cols // 32} blocks x {bb}")
+        be, bb = {PHX.Q4_0: (32, 18), PHX.Q8_0: (32, 34), PHX.Q4_K: (256, 144), PHX.Q6_K: (256, 210)}.get(wtype, (32, 0))
+        if cols <= 0 or cols % be or w.size != rows * (cols // be) * bb:
+            raise ArgumentError(PHX.ERR_ARG, f"weight bytes {w.size} != {rows} rows x {cols // be} blocks x {bb}")
         h = C.c_void_p()
         self._check(self.lib.phx_weight_upload(self.h, wtype, rows, cols, w.ctypes.data, C.byref(h)))
         return h.value
@@ -464,6 +465,32 @@ class MoeContext:
             bufs[0].upload(xq)
             bufs[1].upload(xd)
             self.matmul_device(handle, T, bufs[0].ptr, bufs[1].ptr, bufs[2].ptr)
+            self.sync()
+            return bufs[2].download((T, rows))
+        finally:
+            for b in bufs:
+                b.free()
+
+    def matmul_k_device(self, handle: int, T: int, xq_ptr: int, xd_ptr: int, y_ptr: int):
+        """phx_matmul_k (KernelsK.MatVec as GemmaGpu.MatVec records it for K-quant weights), asynchronous."""
+        self._check(self.lib.phx_matmul_k(self.h, handle, T, xq_ptr, xd_ptr, y_ptr))
+
+    def MatMulK(self, handle: int, rows: int, cols: int, xq: np.ndarray, xd: np.ndarray) -> np.ndarray:
+        """GemmaGpu.MatVec for a Q4_K / Q6_K weight on host arrays: y [T][rows] f32 from T Q8_K rows (qs and
+        d as Q8K returns them; the block sums are formed on the device)."""
+        if cols <= 0 or cols % 256:
+            raise ArgumentError(PHX.ERR_ARG, f"cols {cols} is not a multiple of 256")
+        xq = np.ascontiguousarray(xq, dtype=np.int8)
+        xd = np.ascontiguousarray(xd, dtype=np.float32)
+        if xq.size % cols or xd.size * 256 != xq.size:
+            raise ArgumentError(PHX.ERR_ARG, f"input of {xq.size} quants and {xd.size} scales for {cols} columns")
+        xq = xq.reshape(-1, cols)
+        T = xq.shape[0]
+        bufs = [self.alloc(xq.nbytes), self.alloc(xd.nbytes), self.alloc(T * rows * 4)]
+        try:
+            bufs[0].upload(xq)
+            bufs[1].upload(xd)
+            self.matmul_k_device(handle, T, bufs[0].ptr, bufs[1].ptr, bufs[2].ptr)
             self.sync()
             return bufs[2].download((T, rows))
         finally:

@@ -185,11 +185,65 @@ def test_matmul_matches_oracle(ctx, orc, wtype, T, rows, cols):
         np.testing.assert_array_equal(y[t], orc.matvec(wtype, w, rows, cols, x[t]), err_msg=f"token {t}")
 
 
+def gguf_k_rows(rng, wtype, rows, cols):
+    """Random GGUF rows of Q4_K (144-byte super-blocks) or Q6_K (210-byte): every quant, 6-bit scale and
+    min, and int8 sub-block scale value, with finite fp16 super-block scales (d, dmin)."""
+    bb = 144 if wtype == 12 else 210
+    n = rows * cols // 256
+    blocks = rng.integers(0, 256, (n, bb), dtype=np.uint8)
+    d = (rng.standard_normal(n) * 0.002).astype(np.float16)
+    if wtype == 12:
+        blocks[:, 0:2] = d.view(np.uint8).reshape(-1, 2)
+        dmin = (np.abs(rng.standard_normal(n)) * 0.001).astype(np.float16)
+        blocks[:, 2:4] = dmin.view(np.uint8).reshape(-1, 2)
+    else:
+        blocks[:, 208:210] = d.view(np.uint8).reshape(-1, 2)
+    return blocks.reshape(-1)
+
+
+@pytest.mark.parametrize("wtype", [12, 14])
+@pytest.mark.parametrize("T,rows,cols", [(1, 1408, 4096), (3, 301, 2816), (7, 64, 12288), (8, 301, 2816),
+                                         (48, 4096, 1536), (200, 2112, 4096), (512, 4096, 1536)])
+def test_matmul_k_matches_oracle(ctx, orc, wtype, T, rows, cols):
+    """phx_quant_q8_k, phx_weight_upload and phx_matmul_k (KernelsK.MatVec as GemmaGpu.MatVec records it for
+    Q4_K / Q6_K weights) equal CpuRefKQuants.MatVecK per token, bit for bit: the VALU row walk below 8
+    tokens, the matrix cores from 8 (one partial tile, whole tiles, and C4's 512 rows through its down
+    shape); row counts not a multiple of the 64-row group."""
+    say(f"matmul_k: type={wtype} T={T} rows={rows} cols={cols}")
+    rng = np.random.default_rng(rows + cols + wtype + T)
+    w = gguf_k_rows(rng, wtype, rows, cols)
+    h = ctx.weight_upload(wtype, w, rows, cols)
+    try:
+        x = rng.standard_normal((T, cols)).astype(np.float32)
+        x[0, :256] = 0.0  # an all-zero super-block (d = 0)
+        qs, d, _ = ctx.Q8K(0, x)
+        y = ctx.MatMulK(h, rows, cols, qs, d)
+    finally:
+        ctx.weight_free(h)
+    toks = range(T) if T <= 64 else sorted(set([0, 1, T - 1] + rng.choice(T, 45, replace=False).tolist()))
+    for t in toks:
+        np.testing.assert_array_equal(y[t], orc.matvec(wtype, w, rows, cols, x[t]), err_msg=f"token {t}")
+
+
 def test_matmul_rejects_bad_arguments(ctx, pkg):
     say("matmul: argument checks")
-    with pytest.raises(pkg.moe.NotSupportedError):
-        ctx._check(ctx.lib.phx_weight_upload(ctx.h, 12, 1, 256, np.zeros(144, np.uint8).ctypes.data,
+    with pytest.raises(pkg.moe.NotSupportedError):  # IQ2_XXS: no dense upload
+        ctx._check(ctx.lib.phx_weight_upload(ctx.h, 16, 1, 256, np.zeros(66, np.uint8).ctypes.data,
                                              C.byref(C.c_void_p())))
+    with pytest.raises(pkg.moe.ArgumentError):
+        ctx.weight_upload(12, np.zeros(144, np.uint8), 1, 128)  # K-quant cols not a multiple of 256
+    hk = ctx.weight_upload(12, np.zeros(144, np.uint8), 1, 256)
+    h0 = ctx.weight_upload(2, np.zeros(18 * 8, np.uint8), 1, 256)
+    try:
+        q, dk, d0 = np.zeros((1, 256), np.int8), np.zeros((1, 1), np.float32), np.zeros((1, 8), np.uint16)
+        with pytest.raises(pkg.moe.NotSupportedError):  # a K-quant weight takes Q8_K input
+            ctx.MatMul(hk, 1, 256, q, d0)
+        with pytest.raises(pkg.moe.NotSupportedError):  # and a Q4_0 weight Q8_0 input
+            ctx.MatMulK(h0, 1, 256, q, dk)
+        np.testing.assert_array_equal(ctx.MatMulK(hk, 1, 256, q, dk), np.zeros((1, 1), np.float32))
+    finally:
+        ctx.weight_free(hk)
+        ctx.weight_free(h0)
     with pytest.raises(pkg.moe.ArgumentError):
         ctx.weight_upload(2, np.zeros(17, np.uint8), 1, 32)  # short rows
     with pytest.raises(pkg.moe.ArgumentError):
