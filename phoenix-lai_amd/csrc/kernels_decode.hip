@@ -30,6 +30,23 @@
 
 namespace phx {
 
+// Clock stamps of kernel phases, compiled only into an instrumented build (-DPHX_TIMELINE): thread 0 of
+// workgroup b (< TL_WG) writes the 100 MHz wall clock at phase `slot` of launch kind `kind` of stack
+// layer `seq` (modulo TL_SEQ); phxdbg_timeline copies the table to the host.  Without the macro the
+// stamps compile to nothing.
+#ifdef PHX_TIMELINE
+constexpr int TL_SEQ = 64, TL_KIND = 4, TL_SLOT = 8, TL_WG = 512;
+__device__ unsigned long long phx_tl[TL_SEQ * TL_KIND * TL_SLOT * TL_WG];
+#define TL_STAMP(seq, kind, slot)                                                                   \
+    do {                                                                                            \
+        if (threadIdx.x == 0 && blockIdx.x < TL_WG)                                                 \
+            phx_tl[((((seq) % TL_SEQ) * TL_KIND + (kind)) * TL_SLOT + (slot)) * TL_WG + blockIdx.x] = \
+                wall_clock64();                                                                     \
+    } while (0)
+#else
+#define TL_STAMP(seq, kind, slot) ((void)0)
+#endif
+
 constexpr int DMAXNB = 128;  // blocks of 32 per row: K <= 4096
 constexpr int DROWS = 2;     // assignments (expert tiles) or tokens (shared FFN) per workgroup
 constexpr int DBPW = 8;      // blocks per wave
@@ -59,6 +76,7 @@ struct ActL {
 
 struct DecArgs {
     int T, d, E, k, nf, nff, rule, max_tiles;
+    int seq;              // position in a captured stack (clock-stamp slot of the instrumented build)
     float eps;
     const float* x;       // [T][d]
     const float* W;       // [E][d] router (ffn_gate_inp.weight)
@@ -552,6 +570,7 @@ __device__ __forceinline__ void route_wg(const DecArgs& a, int t, int e, float* 
     __shared__ double red[5], wsum[4], red5[2 * (RT_NT / 64 + 1)];
     __shared__ float wA[4], wP[4];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, d = a.d;
+    TL_STAMP(a.seq, 0, 0);
     const float* xr = a.x + (int64_t)t * d;
     // the input blocks of this workgroup (8 threads per block): their norm weights, loaded now
     const int nb = d / 32, g = tid >> 3, l8 = tid & 7, b = e + g * a.E, bc = min(b, nb - 1);
@@ -583,6 +602,7 @@ __device__ __forceinline__ void route_wg(const DecArgs& a, int t, int e, float* 
         __builtin_amdgcn_s_waitcnt(0);
     }
     __syncthreads();
+    TL_STAMP(a.seq, 0, 1);
     const int c0 = tid * PER;
     float xv[PER], pv[PER];
     double s2 = 0.0;
@@ -609,6 +629,7 @@ __device__ __forceinline__ void route_wg(const DecArgs& a, int t, int e, float* 
         mean = (float)(red[4] / (double)d);
     }
     const float rinv = rms_scale_from_mean(mean, a.eps);
+    TL_STAMP(a.seq, 0, 2);
     const float sc = 1.0f / (float)__dsqrt_rn((double)d);
     double loc = 0.0;
     float Pf = 0.0f;
@@ -672,6 +693,7 @@ __device__ __forceinline__ void route_wg(const DecArgs& a, int t, int e, float* 
         a.Lb[(int64_t)t * a.E + e] = L;
         a.Bb[(int64_t)t * a.E + e] = 0x1p-24 * As * 1.001 + 0x1p-45 * Ps;
     }
+    TL_STAMP(a.seq, 0, 3);
 }
 
 // floats of one staged router row in LDS: d rounded up to whole rounds of RT_NT float4 (the staging's
@@ -1254,11 +1276,13 @@ __device__ void gu_wg(const DecArgs& a, unsigned char* smem)
     const int nsh = a.sgu.rg ? (a.T + DROWS - 1) / DROWS * a.sgu.rg : 0;
     const int total = nsh + a.max_tiles * a.gu.rg;
     int u = routing ? total : (int)blockIdx.x;
+    TL_STAMP(a.seq, 1, 0);
     // this wave's token's selection inputs (tokens past the waves load theirs at the selection)
     SelIn sin;
     if (PRESEL && wave < a.T) sel_issue(a, wave, sin);
     if (u < nsh) {
         for (; u < nsh; u += G) shared_gu_wg<TYPE>(a, u / a.sgu.rg, u % a.sgu.rg, smem);
+        TL_STAMP(a.seq, 1, 1);
         if (u >= total) return;  // uniform: no barriers follow
         __syncthreads();         // the shared units' LDS becomes the selection's
     }
@@ -1305,6 +1329,7 @@ __device__ void gu_wg(const DecArgs& a, unsigned char* smem)
         build_tiles(a, s_ids, s_cnt, s_off, s_tb, s_perm, s_tiles, s_misc, wtot);
         ntiles = s_misc[0];
     }
+    TL_STAMP(a.seq, 1, 2);
     if (routing) {
         const double* Lg = a.Lb;
         const int* bad = s_misc + 2;
@@ -1324,12 +1349,17 @@ __device__ void gu_wg(const DecArgs& a, unsigned char* smem)
         __builtin_amdgcn_sched_barrier(0);  // keep the activation loads ahead of the weight loads
         WRegs<TYPE> W;
         load_w<TYPE>(a.gu, clamp_id(e, a.E), rgi, wave, lane, W);  // unconditional (see load_w)
+        TL_STAMP(a.seq, 1, 6);
         __syncthreads();  // the exact-selection arrays (first unit) or the last unit's rows are done with
         act_store(ain, cnt, nb, act);
+        TL_STAMP(a.seq, 1, 7);
         __syncthreads();
+        TL_STAMP(a.seq, 1, 3);
         const float S = rowgroup_chain<TYPE>(W, wave, nb, act, cnt, (float*)un);
+        TL_STAMP(a.seq, 1, 4);
         if (wave < cnt) gu_epilogue(S, rgi, a.nf, wave == 0 ? tl.row[0] : tl.row[1], a.g, a.u, a.adn, a.gelu_tab);
     }
+    TL_STAMP(a.seq, 1, 5);
 }
 
 // NTMAX: the workgroup-size bound the compiler allocates registers for (768 gives the unit loop the
@@ -1351,9 +1381,11 @@ __global__ __launch_bounds__(1024) void k_dec_down(DecArgs a)
     extern __shared__ __align__(16) unsigned char dsm[];
     const int nb = a.dn.nb, wpr = (nb + DBPW - 1) / DBPW, nrgb = (a.dn.rg + a.rpw - 1) / a.rpw;
     const int ne = a.max_tiles * nrgb;
+    TL_STAMP(a.seq, 2, 0);
     if ((int)blockIdx.x >= ne) {
         const int s = blockIdx.x - ne;
         shared_dn_wg<TYPE>(a, s / a.sdn.rg, s % a.sdn.rg, dsm);
+        TL_STAMP(a.seq, 2, 3);
         return;
     }
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -1374,9 +1406,12 @@ __global__ __launch_bounds__(1024) void k_dec_down(DecArgs a)
     load_w<TYPE>(a.dn, clamp_id(e, a.E), min(rgi, a.dn.rg - 1), wl, lane, W);  // unconditional (see load_w)
     act_store(ain, cnt, nb, act);
     __syncthreads();
+    TL_STAMP(a.seq, 2, 1);
     const float S = rowgroup_chain<TYPE>(W, live ? wl : wpr, nb, act, cnt, terms);
+    TL_STAMP(a.seq, 2, 2);
     const int row = rgi * 64 + lane;
     if (live && wl < cnt && row < a.d) a.yd[(int64_t)(wl == 0 ? tl.z : tl.w) * a.d + row] = S;
+    TL_STAMP(a.seq, 2, 3);
 }
 
 // ------------------------------------------------------------------------------ k_dec_combine
@@ -1511,6 +1546,7 @@ static DecArgs dec_args(const DecLayerH& h)
     a.nff = h.sgu ? h.nff : 0;
     a.rule = h.rule;
     a.max_tiles = h.max_tiles;
+    a.seq = h.seq;
     a.eps = h.eps;
     a.x = h.x;
     a.W = h.W;
@@ -1653,3 +1689,19 @@ void launch_dec_combine(hipStream_t st, const DecLayerH& h)
 }
 
 }  // namespace phx
+
+#ifdef PHX_TIMELINE
+// the instrumented build's clock-stamp table [seq][kind][slot][workgroup], 100 MHz ticks (0: no stamp)
+extern "C" __attribute__((visibility("default"))) int phxdbg_timeline(unsigned long long* host, size_t n, int clear)
+{
+    const size_t all = sizeof(phx::phx_tl) / sizeof(phx::phx_tl[0]);
+    if (host && hipMemcpyFromSymbol(host, HIP_SYMBOL(phx::phx_tl), std::min(n, all) * 8, 0, hipMemcpyDeviceToHost) != hipSuccess)
+        return -1;
+    if (clear) {
+        static unsigned long long* zero = nullptr;
+        if (!zero) zero = (unsigned long long*)calloc(all, 8);
+        if (hipMemcpyToSymbol(HIP_SYMBOL(phx::phx_tl), zero, all * 8, 0, hipMemcpyHostToDevice) != hipSuccess) return -1;
+    }
+    return (int)all;
+}
+#endif

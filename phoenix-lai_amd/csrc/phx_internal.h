@@ -175,6 +175,7 @@ void launch_combine(hipStream_t st, int T, int d, int k, float eps, const float*
 // decode path (kernels_decode.hip): four launches per layer for T <= 16 tokens, Q4_0 / Q8_0
 struct DecLayerH {
     int T, d, E, k, nf, nff, rule, max_tiles;
+    int seq = 0;  // position in a captured stack (the instrumented build's clock-stamp slot)
     int ncu;  // compute units: the gate|up launch has at most one unit workgroup per CU
     float eps;
     const float *x, *W, *gis, *ds, *pre2, *post1, *post2, *fnorm, *post_ffw, *shared_in;

@@ -1258,6 +1258,7 @@ static int capture_decode_stack(phx_moe_ctx* c, int first, int n_layers, int T)
     for (int i = 0; i < n_layers; i++) {
         const Layer& L = c->layers[first + i];
         DecLayerH h = dec_layer(c, L, T, xs[i % 2], nullptr, out, nullptr);
+        h.seq = i;
         {
             ProfScope p(c, PHX_K_ROUTER);
             if (i == 0) launch_dec_route(st, h);

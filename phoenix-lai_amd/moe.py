@@ -98,7 +98,8 @@ class LayerDesc(C.Structure):
 
 
 def lib_path() -> Path:
-    return _HERE / "libphxmoe.so"
+    """libphxmoe.so in the package directory, or the file PHX_MOE_LIB names (an instrumented build)."""
+    return Path(os.environ["PHX_MOE_LIB"]) if os.environ.get("PHX_MOE_LIB") else _HERE / "libphxmoe.so"
 
 
 _LIB = None
