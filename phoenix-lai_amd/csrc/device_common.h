@@ -301,6 +301,18 @@ __device__ __forceinline__ double wave_max_d(double v)
     return v;
 }
 
+// The two float ends of (S -/+ B) / n, the interval of means a certified sum of squares S (error bound
+// B, S >= 0) allows, formed with the reciprocal rn = 1 / n instead of a double division: the bound is
+// widened by S * 2^-49, above the relative error of rn and of the product (under 2^-51), so the ends
+// still bracket the reference's (double)(sum / n) for every sum in [S - B, S + B]; equal ends are the
+// reference's (float)(sum / n) (division and both roundings are monotone).
+__device__ __forceinline__ void mean_ends(double S, double B, double rn, float* lo, float* hi)
+{
+    const double Bw = B + S * 0x1p-49;
+    *lo = (float)((S - Bw) * rn);
+    *hi = (float)((S + Bw) * rn);
+}
+
 // Mean of squares of one row as CpuRef.RmsNorm rounds it: (float)(sum / n) with sum the double sum of
 // x_i^2 in index order (src/CpuRef.cs:186-188).  A parallel double sum differs from the sequential
 // one by at most (n + per + depth) * 2^-53 * sum (all terms are non-negative); when both ends of
@@ -323,7 +335,8 @@ __device__ float mean_sq_cert(const float* x, int n, double* red, int* fallbacks
     for (int w = 0; w < NW; w++) S += red[w];
     const int per = (n + NT - 1) / NT;
     const double B = ((double)n + per + 64.0) * 0x1p-53 * S * 2.0;
-    const float lo = (float)((S - B) / (double)n), hi = (float)((S + B) / (double)n);
+    float lo, hi;
+    mean_ends(S, B, 1.0 / (double)n, &lo, &hi);
     float mean = lo;
     if (lo != hi) {
         __syncthreads();
@@ -352,7 +365,8 @@ __device__ __forceinline__ float mean_sq_cert_wave(const float* x, int n, int* f
     }
     const double S = wave_sum_dpp(s);
     const double B = ((double)n + per + 64.0) * 0x1p-53 * S * 2.0;
-    const float lo = (float)((S - B) / (double)n), hi = (float)((S + B) / (double)n);
+    float lo, hi;
+    mean_ends(S, B, 1.0 / (double)n, &lo, &hi);
     if (lo == hi) return lo;
     double q = 0.0;
     if (lane == 0) {

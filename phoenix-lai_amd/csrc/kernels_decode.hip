@@ -142,7 +142,8 @@ __device__ float wg_mean_sq(double s, const float* xr, int n, double* red, int* 
     __syncthreads();
     const double S = wave_sum_dpp(lane < nw ? red[lane] : 0.0);  // the wave totals in a fixed tree order
     const double B = ((double)n + 64.0) * 0x1p-52 * S;
-    const float lo = (float)((S - B) / (double)n), hi = (float)((S + B) / (double)n);
+    float lo, hi;
+    mean_ends(S, B, 1.0 / (double)n, &lo, &hi);
     float mean = lo;
     if (lo != hi) {  // uniform: every thread formed the same S
         if (tid == 0) {
@@ -175,8 +176,10 @@ __device__ void wg_mean_sq2(double s0, double s1, const float* x0, const float* 
     const double S0 = wave_sum_dpp(lane < nw ? red[lane] : 0.0);
     const double S1 = wave_sum_dpp(lane < nw ? red1[lane] : 0.0);
     const double B0 = ((double)n + 64.0) * 0x1p-52 * S0, B1 = ((double)n + 64.0) * 0x1p-52 * S1;
-    float lo0 = (float)((S0 - B0) / (double)n), hi0 = (float)((S0 + B0) / (double)n);
-    float lo1 = (float)((S1 - B1) / (double)n), hi1 = (float)((S1 + B1) / (double)n);
+    const double rn = 1.0 / (double)n;
+    float lo0, hi0, lo1, hi1;
+    mean_ends(S0, B0, rn, &lo0, &hi0);
+    mean_ends(S1, B1, rn, &lo1, &hi1);
     if (lo0 != hi0 || lo1 != hi1) {  // uniform: every thread formed the same sums
         if (tid == 0) {
             if (lo0 != hi0) {
@@ -433,7 +436,7 @@ __device__ __forceinline__ void gu_epilogue(float S, int rgi, int split, int64_t
 // also go to p.out and p.xres (x read from p.xin).  sacc and so: LDS [d] each.
 // What the combine of a layer reads and writes (a small kernel argument of the fused router)
 struct CombArgs {
-    int d, k;
+    int d, k, seq;
     float eps;
     const float *w, *yd, *shout, *post1, *post2, *post_ffw, *xin;
     float *out, *xres;
@@ -491,6 +494,7 @@ __device__ __forceinline__ void combine_into(const CombArgs& p, int t, float* sx
                     acc[q].w += yv[q][jj].w * wj[jj];
                 }
     }
+    TL_STAMP(p.seq, 3, 4);
     double s2 = 0.0, s1 = 0.0;
 #pragma unroll
     for (int q = 0; q < CQ; q++)
@@ -506,6 +510,7 @@ __device__ __forceinline__ void combine_into(const CombArgs& p, int t, float* sx
     wg_mean_sq2(s2, s1, sacc, sh4 ? (const float*)sh4 : nullptr, d, red, leader ? p.flags : nullptr, &m2, &m1);
     const float sc2 = rms_scale_from_mean(m2, p.eps);
     const float sc1 = sh4 ? rms_scale_from_mean(m1, p.eps) : 0.0f;
+    TL_STAMP(p.seq, 3, 5);
     // pass 2: out = rmsnorm(shared) * post1 + rmsnorm(acc) * post2 and its sum of squares
     float4 ov[CQ];
     double s3 = 0.0;
@@ -525,6 +530,7 @@ __device__ __forceinline__ void combine_into(const CombArgs& p, int t, float* sx
     }
     __syncthreads();
     const float sc3 = rms_scale_from_mean(wg_mean_sq(s3, so, d, red, leader ? p.flags : nullptr), p.eps);
+    TL_STAMP(p.seq, 3, 6);
     // pass 3: x_new = x + rmsnorm(out) * post_ffw_norm
 #pragma unroll
     for (int q = 0; q < CQ; q++) {
@@ -617,8 +623,9 @@ __device__ __forceinline__ void route_wg(const DecArgs& a, int t, int e, float* 
     __syncthreads();
     const double S = (red[0] + red[1]) + (red[2] + red[3]);
     const double Bs = ((double)d + 64.0) * 0x1p-52 * S;
-    float mean = (float)((S - Bs) / (double)d);
-    if (mean != (float)((S + Bs) / (double)d)) {  // uniform: S is the same in every thread
+    float mean, mhi;
+    mean_ends(S, Bs, 1.0 / (double)d, &mean, &mhi);
+    if (mean != mhi) {  // uniform: S is the same in every thread
         if (tid == 0) {
             double q = 0.0;
             for (int i = 0; i < d; i++) q += (double)sx[i] * (double)sx[i];
@@ -1653,6 +1660,7 @@ void launch_dec_route_fused(hipStream_t st, const DecLayerH& prev, const DecLaye
     CombArgs cb;
     cb.d = prev.d;
     cb.k = prev.k;
+    cb.seq = h.seq;
     cb.eps = prev.eps;
     cb.w = prev.w;
     cb.yd = prev.yd;
