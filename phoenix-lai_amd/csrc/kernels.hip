@@ -1444,6 +1444,47 @@ void launch_planar_act_k(hipStream_t st, int rows, int n, const int8_t* qs, cons
     launch(k_planar_act_k, dim3((unsigned)((nblk + 3) / 4)), dim3(256), 0, st, nblk, n / 256, qs, d, a);
 }
 
+// Copy of a small buffer (bytes a multiple of 16) by a few workgroups: the host-buffer path's staging
+// between pinned host rows and the device rows, as graph nodes rather than DMA copies.
+__global__ __launch_bounds__(256) void k_copy16(uint4* __restrict__ dst, const uint4* __restrict__ src, int64_t n16)
+{
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += stride) dst[i] = src[i];
+}
+
+void launch_copy_small(hipStream_t st, void* dst, const void* src, int64_t bytes)
+{
+    const int64_t n16 = bytes / 16;
+    launch(k_copy16, dim3((unsigned)std::min<int64_t>(64, (n16 + 255) / 256)), dim3(256), 0, st, (uint4*)dst,
+           (const uint4*)src, n16);
+}
+
+// The last copies of a host-buffer call, by one workgroup: out (and x with the residual) to the pinned
+// rows, then the call's completion word: the next count (never zero, the word's initial value), stored
+// after a system-scope fence so the host, which polls the word, reads whole rows once it changes.
+__global__ __launch_bounds__(1024) void k_copy_done(uint4* __restrict__ d0, const uint4* __restrict__ s0,
+                                                    uint4* __restrict__ d1, const uint4* __restrict__ s1, int64_t n16,
+                                                    uint32_t* __restrict__ ctr, uint32_t* done)
+{
+    for (int64_t i = threadIdx.x; i < n16; i += 1024) d0[i] = s0[i];
+    if (d1)
+        for (int64_t i = threadIdx.x; i < n16; i += 1024) d1[i] = s1[i];
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t v = ctr[0] == 0xFFFFFFFFu ? 1u : ctr[0] + 1u;
+        ctr[0] = v;
+        __threadfence_system();
+        __hip_atomic_store(done, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+}
+
+void launch_copy_done(hipStream_t st, void* d0, const void* s0, void* d1, const void* s1, int64_t bytes, uint32_t* ctr,
+                      uint32_t* done)
+{
+    launch(k_copy_done, dim3(1), dim3(1024), 0, st, (uint4*)d0, (const uint4*)s0, (uint4*)d1, (const uint4*)s1,
+           bytes / 16, ctr, done);
+}
+
 // Fill n 32-bit words with v: clears workspace that must start at zero with a kernel rather than a
 // memset node, so the enqueued work stays a plain kernel when a caller captures it into a graph.
 __global__ __launch_bounds__(256) void k_fill_u32(uint32_t* __restrict__ p, int64_t n, uint32_t v)

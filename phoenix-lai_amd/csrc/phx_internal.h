@@ -201,6 +201,12 @@ void launch_dec_combine(hipStream_t st, const DecLayerH& h);
 void launch_stream_read(hipStream_t st, const void* src, int64_t bytes, uint32_t* sink);
 void launch_stream_copy(hipStream_t st, void* dst, const void* src, int64_t bytes);
 void launch_fill_u32(hipStream_t st, uint32_t* p, int64_t n, uint32_t v);
+// a small copy (bytes a multiple of 16, either side may be pinned host memory) as one kernel
+void launch_copy_small(hipStream_t st, void* dst, const void* src, int64_t bytes);
+// the last copies of a host-buffer call (d1 / s1 may be null), then *done = ++*ctr (ctr device memory,
+// done pinned host memory) after a system-scope fence; one workgroup
+void launch_copy_done(hipStream_t st, void* d0, const void* s0, void* d1, const void* s1, int64_t bytes, uint32_t* ctr,
+                      uint32_t* done);
 void launch_planar_act(hipStream_t st, int rows, int n, const int8_t* qs, const uint16_t* d, Act a);
 // planar Q8_K rows (qs [rows][n], d [rows][n/256]) into a's K-quant orders (ACT_K4 / ACT_K6, qh / bh when set)
 void launch_planar_act_k(hipStream_t st, int rows, int n, const int8_t* qs, const float* d, Act a);

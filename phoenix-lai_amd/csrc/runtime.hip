@@ -9,6 +9,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <chrono>
 #include <mutex>
 #include <string>
 #include <thread>
@@ -265,6 +266,7 @@ struct Layer {
     float *wt4 = nullptr, *wrow = nullptr, *gis = nullptr, *ds = nullptr, *pre2 = nullptr, *post1 = nullptr, *post2 = nullptr;
     float *ffn_norm = nullptr, *post_ffw = nullptr;
     QMat gu, dn, sgu, sdn;
+    uint64_t gen = 0;  // upload generation: graphs captured over an earlier upload are stale
 };
 
 struct Buf {
@@ -282,7 +284,7 @@ struct phx_moe_ctx {
     float* gelu_tab = nullptr;
     std::vector<Layer> layers;
     std::vector<Buf> ws;
-    int* flags = nullptr;  // [0] count of certified-sum fallbacks
+    int* flags = nullptr;  // [0] count of certified-sum fallbacks, [1] router fallbacks, [15] host-call completions
     int last_T = 0, last_layer = -1;
     // profiling
     bool profiling = false;
@@ -308,6 +310,19 @@ struct phx_moe_ctx {
     unsigned char* bump_base = nullptr;
     size_t bump_off = 0, bump_cap = 0;
     FaultPlan fault;  // PHX_FAULT, see phx_internal.h
+    // phx_moe_ffn on host buffers: pinned staging rows ([3][pin_bytes]: x, shared, out) and each
+    // (layer, T, flags, shared given) call captured once as a graph over the workspace it was captured on
+    float* pin = nullptr;    // ... then the completion word (small calls)
+    size_t pin_bytes = 0;
+    struct FfnGraph {
+        int layer, T;
+        unsigned key;
+        uint64_t gen;
+        std::vector<void*> ws;
+        hipGraphExec_t exec;
+    };
+    std::vector<FfnGraph> ffn_graphs;
+    uint64_t upload_gen = 0;
 };
 
 namespace {
@@ -350,7 +365,23 @@ hipError_t dev_malloc(phx_moe_ctx* c, void** p, size_t n)
         *p = nullptr;
         return hipErrorOutOfMemory;
     }
-    return hipMalloc(p, n);  // the one allocation site
+    return hipMalloc(p, n);  // the one device allocation site
+}
+
+// pinned host memory, under the same fault plan
+hipError_t host_malloc(phx_moe_ctx* c, void** p, size_t n)
+{
+    if (c && c->fault.fire(FaultPlan::MALLOC)) {
+        *p = nullptr;
+        return hipErrorOutOfMemory;
+    }
+    return hipHostMalloc(p, n, hipHostMallocCoherent);
+}
+
+void drop_ffn_graphs(phx_moe_ctx* c)
+{
+    for (auto& g : c->ffn_graphs) (void)hipGraphExecDestroy(g.exec);
+    c->ffn_graphs.clear();
 }
 
 // the launches' status: an injected launch fault, else the runtime's last error
@@ -1084,6 +1115,8 @@ void phx_moe_destroy(phx_moe_ctx* c)
     if (c->stream) (void)hipStreamSynchronize(c->stream);
     if (c->graph_exec) (void)hipGraphExecDestroy(c->graph_exec);
     if (c->graph) (void)hipGraphDestroy(c->graph);
+    drop_ffn_graphs(c);
+    if (c->pin) (void)hipHostFree(c->pin);
     for (auto& L : c->layers) free_layer(L);
     for (auto& b : c->ws)
         if (b.p) (void)hipFree(b.p);
@@ -1113,6 +1146,7 @@ int phx_moe_layer_upload(phx_moe_ctx* c, int layer, const phx_moe_layer_desc* D)
     if ((int)c->layers.size() <= layer) c->layers.resize(layer + 1);
     Layer& L = c->layers[layer];
     free_layer(L);
+    L.gen = ++c->upload_gen;
     L.desc = *D;
     const int d = D->d, E = D->n_expert, nf = D->n_ff;
     // router transposed to [d/4][E][4] (consecutive experts are consecutive lanes)
@@ -1144,6 +1178,105 @@ int phx_moe_layer_upload(phx_moe_ctx* c, int layer, const phx_moe_layer_desc* D)
     return PHX_OK;
 }
 
+namespace {
+
+// phx_moe_ffn on host buffers: the caller's rows pass through pinned staging rows, and the layer call,
+// with the copies between the staging rows and the device rows as small kernels, is captured as a graph
+// the first time a (layer, T, flags, shared given) call comes and replayed after: one graph launch and one
+// wait per call (the reference records the layer once and replays the command buffer per token,
+// src/GemmaGpu.cs:544-554).  A graph is kept while the layer's upload and the workspace it was captured
+// over are unchanged.
+int ffn_host(phx_moe_ctx* c, int layer, int T, float* x, const float* shared, float* out, unsigned flags)
+{
+    const Layer& L = c->layers[layer];
+    const size_t bytes = (size_t)T * L.desc.d * 4;
+    hipStream_t st = c->stream;
+    if (c->pin_bytes < bytes) {
+        HIPCHK(c, hipStreamSynchronize(st));
+        drop_ffn_graphs(c);
+        if (c->pin) (void)hipHostFree(c->pin);
+        c->pin = nullptr;
+        c->pin_bytes = 0;
+        HIPCHK(c, host_malloc(c, (void**)&c->pin, 3 * bytes + 256));
+        c->pin_bytes = bytes;
+        // the completion word starts at zero, which the device's count never writes (pinned memory comes
+        // back from the allocator with an earlier owner's bytes)
+        *(volatile uint32_t*)(c->pin + 3 * (bytes / 4)) = 0u;
+    }
+    float *px = c->pin, *psh = c->pin + c->pin_bytes / 4, *pout = c->pin + 2 * (c->pin_bytes / 4);
+    volatile uint32_t* done = (volatile uint32_t*)(c->pin + 3 * (c->pin_bytes / 4));
+    const bool res = flags & PHX_FLAG_RESIDUAL;
+    // a decode-sized call ends with one workgroup copying the rows out and writing the completion word,
+    // which the host polls (a stream wait costs more than the copies); larger calls copy with several
+    // workgroups and wait on the stream
+    const bool small = bytes * (res ? 2 : 1) <= (256u << 10);
+    const unsigned key = (flags & (PHX_FLAG_RESIDUAL | PHX_FLAG_EXACT_ROUTER)) | (shared ? 0x80000000u : 0u);
+    std::vector<void*> sig(c->ws.size());
+    for (size_t i = 0; i < c->ws.size(); i++) sig[i] = c->ws[i].p;
+    hipGraphExec_t exec = nullptr;
+    for (auto& g : c->ffn_graphs)
+        if (g.layer == layer && g.T == T && g.key == key && g.gen == L.gen && g.ws == sig) exec = g.exec;
+    if (!exec) {
+        HIPCHK(c, hipStreamSynchronize(st));
+        HIPCHK(c, hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+        float *xd = wp<float>(c, W_X), *od = wp<float>(c, W_OUT), *sd = shared ? wp<float>(c, W_SHARED) : nullptr;
+        launch_copy_small(st, xd, px, (int64_t)bytes);
+        if (shared) launch_copy_small(st, sd, psh, (int64_t)bytes);
+        int rc = run_layer(c, L, T, xd, sd, od, res ? xd : nullptr, flags & ~PHX_FLAG_ASYNC);
+        if (small) {
+            launch_copy_done(st, pout, od, res ? px : nullptr, res ? xd : nullptr, (int64_t)bytes,
+                             (uint32_t*)(c->flags + 15), (uint32_t*)done);
+        } else {
+            launch_copy_small(st, pout, od, (int64_t)bytes);
+            if (res) launch_copy_small(st, px, xd, (int64_t)bytes);
+        }
+        const hipError_t le = launch_status(c);
+        hipGraph_t g = nullptr;
+        const hipError_t ce = hipStreamEndCapture(st, &g);
+        if (!rc && le != hipSuccess) rc = set_err(c, hip_code(le), "%s", hipGetErrorString(le));
+        if (!rc && ce != hipSuccess) rc = set_err(c, hip_code(ce), "stream capture failed: %s", hipGetErrorString(ce));
+        if (!rc) {
+            const hipError_t ie = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+            if (ie != hipSuccess) rc = set_err(c, hip_code(ie), "graph instantiate: %s", hipGetErrorString(ie));
+        }
+        if (g) (void)hipGraphDestroy(g);
+        if (rc) return rc;
+        if (c->ffn_graphs.size() >= 64) {  // the oldest goes
+            (void)hipGraphExecDestroy(c->ffn_graphs.front().exec);
+            c->ffn_graphs.erase(c->ffn_graphs.begin());
+        }
+        c->ffn_graphs.push_back(phx_moe_ctx::FfnGraph{layer, T, key, L.gen, sig, exec});
+    }
+    memcpy(px, x, bytes);
+    if (shared) memcpy(psh, shared, bytes);
+    const uint32_t before = *done;
+    HIPCHK(c, hipGraphLaunch(exec, st));
+    if (small) {
+        // the word changes once the rows are out; a call that never ends it (a fault) is left to the stream
+        // wait after two seconds, which reports the error
+        const auto t0 = std::chrono::steady_clock::now();
+        while (*done == before)
+            if (std::chrono::steady_clock::now() - t0 > std::chrono::seconds(2)) {
+                HIPCHK(c, hipStreamSynchronize(st));
+                if (*done == before) {
+                    uint32_t ctr = 0;
+                    (void)hipMemcpy(&ctr, c->flags + 15, 4, hipMemcpyDeviceToHost);
+                    return set_err(c, PHX_ERR_HIP, "host-buffer call: no completion (word %u, device count %u)",
+                                   (unsigned)*done, (unsigned)ctr);
+                }
+            }
+    } else {
+        HIPCHK(c, hipStreamSynchronize(st));
+    }
+    memcpy(out, pout, bytes);
+    if (res) memcpy(x, px, bytes);
+    c->last_T = T;
+    c->last_layer = layer;
+    return PHX_OK;
+}
+
+}  // namespace
+
 int phx_moe_ffn(phx_moe_ctx* c, int layer, int T, float* x, const float* shared, float* out, unsigned flags)
 {
     if (!c) return PHX_ERR_ARG;
@@ -1156,6 +1289,7 @@ int phx_moe_ffn(phx_moe_ctx* c, int layer, int T, float* x, const float* shared,
     c->last_scratch = false;
     const size_t bytes = (size_t)T * L.desc.d * 4;
     const bool dev = flags & PHX_FLAG_DEVICE_PTRS;
+    if (!dev && !c->profiling && bytes % 16 == 0) return ffn_host(c, layer, T, x, shared, out, flags);
     float* xin = x;
     const float* shin = shared;
     float* o = out;

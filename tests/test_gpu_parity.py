@@ -579,3 +579,51 @@ def test_iq_layers_bit_exact(ctx, pkg, orc, case):
     x = pkg.synth.make_input(cfg, T=T)
     ctx.upload(0, L)
     check_layer(ctx, orc, L, x, tag=f"iq {case}", exact=True)
+
+
+def test_host_buffer_calls_replay_graphs(ctx, pkg, orc):
+    """phx_moe_ffn on host buffers replays one captured graph per (layer, T, flags, shared given): repeated
+    calls equal the device-pointer call bit for bit (decode-sized calls end on the completion word, large
+    ones on a stream wait); a layer uploaded again, another T, the residual and a given shared branch each
+    take their own graph and the oracle's results."""
+    S = pkg.synth
+    La = layer(pkg, "c1_tiny")
+    Lb = layer(pkg, "c1_tiny", norms="noisy")
+    ctx.upload(0, La)
+    d = La["d"]
+    for T in (1, 3, 64, 1):
+        x = S.make_input("c1_tiny", T=T)
+        say(f"host graphs: T={T}")
+        outs = [ctx.ffn(0, x) for _ in range(3)]
+        xb, ob = ctx.alloc(x.nbytes), ctx.alloc(x.nbytes)
+        xb.upload(x)
+        ctx.ffn_device(0, T, xb.ptr, None, ob.ptr)
+        ctx.sync()
+        dev = ob.download((T, d))
+        xb.free()
+        ob.free()
+        for o in outs:
+            np.testing.assert_array_equal(o, dev)
+        assert within(outs[0], orc.moe_block(La, x)[0])[0]
+    # the same slot uploaded with other weights: a fresh capture
+    x = S.make_input("c1_tiny", T=3)
+    before = ctx.ffn(0, x)
+    ctx.upload(0, Lb)
+    after = ctx.ffn(0, x)
+    assert within(after, orc.moe_block(Lb, x)[0])[0] and not np.array_equal(before, after)
+    # residual (x updated in place through the pinned rows) and a given shared branch
+    Lc = layer(pkg, "c5_stack", norms="noisy")
+    ctx.upload(1, Lc)
+    x = S.make_input("c5_stack", T=2)
+    ro = orc.moe_block(Lc, x)[0]
+    for _ in range(2):
+        out, xn = ctx.ffn(1, x, residual=True)
+        assert within(out, ro)[0]
+        assert within(xn, orc.residual(Lc, x, ro))[0]
+    sh = S.normal(99, "host.shared", (3, d))
+    xs = S.make_input("c1_tiny", T=3)
+    ctx.upload(0, La)
+    o1 = ctx.ffn(0, xs, sh)
+    o2 = ctx.ffn(0, xs, sh)
+    np.testing.assert_array_equal(o1, o2)
+    assert within(o1, orc.moe_block(La, xs, sh)[0])[0]
