@@ -9,6 +9,24 @@
 
 namespace phx {
 
+// Clock stamps of kernel phases, compiled only into an instrumented build (-DPHX_TIMELINE; one table
+// per source file): thread 0 of
+// workgroup b (< TL_WG) writes the 100 MHz wall clock at phase `slot` of launch kind `kind` of stack
+// layer `seq` (modulo TL_SEQ); phxdbg_timeline copies the table to the host.  Without the macro the
+// stamps compile to nothing.
+#ifdef PHX_TIMELINE
+constexpr int TL_SEQ = 64, TL_KIND = 4, TL_SLOT = 8, TL_WG = 512;
+static __device__ unsigned long long phx_tl[TL_SEQ * TL_KIND * TL_SLOT * TL_WG];
+#define TL_STAMP(seq, kind, slot)                                                                   \
+    do {                                                                                            \
+        if (threadIdx.x == 0 && blockIdx.x < TL_WG)                                                 \
+            phx_tl[((((seq) % TL_SEQ) * TL_KIND + (kind)) * TL_SLOT + (slot)) * TL_WG + blockIdx.x] = \
+                wall_clock64();                                                                     \
+    } while (0)
+#else
+#define TL_STAMP(seq, kind, slot) ((void)0)
+#endif
+
 // ------------------------------------------------------------------------------ scalar helpers
 
 // fp16 bits -> float (exact: every binary16 value is a binary32 value; f16 denormals are kept)

@@ -148,8 +148,10 @@ __global__ __launch_bounds__(NT) void k_prologue(int d, float eps, const float* 
     extern __shared__ __align__(16) float sbuf[];
     __shared__ double red[NT];
     const int t = blockIdx.x, tid = threadIdx.x;
+    TL_STAMP(0, 0, 0);
     const float* xr = x + (int64_t)t * d;
     float scale = rms_scale_from_mean(mean_sq_cert<NT>(xr, d, red, flags), eps);
+    TL_STAMP(0, 0, 1);
     float sc = 1.0f / (float)__dsqrt_rn((double)d);
     float* ri = router_in + (int64_t)t * d;
     // four values per thread and round (d and the activation widths are multiples of 32)
@@ -171,7 +173,9 @@ __global__ __launch_bounds__(NT) void k_prologue(int d, float eps, const float* 
     }
     fill(pre2, act_gu.cols);
     __syncthreads();
+    TL_STAMP(0, 0, 2);
     quantize_row<NT>(sbuf, act_gu, t);
+    TL_STAMP(0, 0, 3);
     if (ffn_norm) {
         __syncthreads();
         fill(ffn_norm, act_sh.cols);
@@ -179,6 +183,7 @@ __global__ __launch_bounds__(NT) void k_prologue(int d, float eps, const float* 
         quantize_row<NT>(sbuf, act_sh, t);
     }
     if (tid == 0) xscale[t] = scale;
+    TL_STAMP(0, 0, 4);
 }
 
 void launch_prologue(hipStream_t st, int T, int d, float eps, const float* x, const float* gis, const float* pre2,
@@ -426,9 +431,8 @@ __global__ __launch_bounds__(64) void k_topk(int E, int k, int rule, const float
                                              const float* __restrict__ ds, int* __restrict__ ids, float* __restrict__ wout)
 {
     const int t = blockIdx.x, lane = threadIdx.x;
-    __shared__ float sel[PHX_MAX_USED_DEV];
-    __shared__ int sid[PHX_MAX_USED_DEV];
-    float v[4];
+    float my_sel = 0.0f, v[4];
+    int my_id = 0;
     bool avail[4];
 #pragma unroll
     for (int q = 0; q < 4; q++) {
@@ -458,23 +462,22 @@ __global__ __launch_bounds__(64) void k_topk(int E, int k, int rule, const float
             }
         }
         if (bi >= 0 && lane == (bi & 63)) avail[bi >> 6] = false;
-        if (lane == 0) { sel[j] = bv; sid[j] = bi < 0 ? 0 : bi; }
+        if (lane == j) {  // the round's result is wave-uniform: lane j keeps rank j
+            my_sel = bv;
+            my_id = bi < 0 ? 0 : bi;
+        }
     }
-    __syncthreads();
-    if (lane == 0) {
-        float p[PHX_MAX_USED_DEV];
-        double sum = 0.0;
-        float top = sel[0];
-        for (int j = 0; j < k; j++) {
-            float pj = (float)exp((double)(sel[j] - top));
-            if (rule == 1 && j == 0) top = pj;  // GemmaCpu.cs:407 overwrites sel[0] before later terms read it
-            p[j] = pj;
-            sum += (double)pj;
-        }
-        for (int j = 0; j < k; j++) {
-            ids[(int64_t)t * k + j] = sid[j];
-            wout[(int64_t)t * k + j] = (float)((double)p[j] / sum) * ds[sid[j]];
-        }
+    // weights (src/GemmaCpu.cs:406-407,417), lane j for rank j: p_j = (float)exp((double)(l_j - top)),
+    // the double sum in rank order, w_j = (float)(p_j / sum) * down_scale; GemmaCpu.cs:407 overwrites
+    // sel[0] with p_0 = exp(0) = 1 before the later terms read it (rule 1)
+    const float sel0 = __shfl(my_sel, 0, 64);
+    const float top = (rule == 1 && lane > 0) ? 1.0f : sel0;
+    const float pj = lane < k ? (float)exp((double)(my_sel - top)) : 0.0f;
+    double sum = 0.0;
+    for (int q = 0; q < k; q++) sum += (double)__shfl(pj, q, 64);
+    if (lane < k) {
+        ids[(int64_t)t * k + lane] = my_id;
+        wout[(int64_t)t * k + lane] = (float)((double)pj / sum) * ds[my_id];
     }
 }
 
@@ -485,18 +488,17 @@ void launch_topk(hipStream_t st, int T, int E, int k, int rule, const float* log
 
 // ------------------------------------------------------------------------------ dispatch
 // Per-expert ascending assignment lists (the lists of KernelsMoe.Bucket, src/KernelsMoe.cs:281-330)
-// as one stable counting sort in a single workgroup: per-chunk histograms, per-expert prefix over
-// chunks, expert offsets, then every chunk places its assignments in order.  Also the work list of
-// (expert, first list position, count <= A) tiles for the grouped kernels.
-// chunks of the stable counting sort: at most 256 (one per thread) and at most 16,384 / E so the
-// u16 histogram stays within 32 KB of LDS
-// One workgroup of 16 waves; wave w owns the contiguous segment w of the assignments and walks it 64
-// at a time.  In a batch, eight ballots over the expert-id bits give each lane the mask of the lanes
-// holding the same expert: its rank among them (a popcount of the lower lanes) and their count, so no
-// lane waits on another.  Pass 1 counts each segment's experts, a prefix over (expert, segment) gives
-// the list offsets and every segment's start in every list, pass 2 places the assignments: the lists
-// come out in ascending assignment order (a stable counting sort, the lists of KernelsMoe.Bucket).
-constexpr int DSP_NT = 1024, DSP_SEG = DSP_NT / 64;
+// as one stable counting sort, and the work list of (expert, first list position, count <= A) tiles
+// for the grouped kernels.
+// Workgroups of 16 waves, one per chunk of 2048 assignments; wave w owns the contiguous segment w of
+// the chunk and walks it 64 at a time.  In a batch, eight ballots over the expert-id bits give each
+// lane the mask of the lanes holding the same expert: its rank among them (a popcount of the lower
+// lanes) and their count, so no lane waits on another.  Every workgroup counts each expert over the
+// whole list and before its chunk, and each segment's experts; a prefix over the experts gives the
+// list offsets, the counts before the chunk and over the earlier segments each segment's start in
+// every list, and a last pass places the chunk's assignments: the lists come out in ascending
+// assignment order (a stable counting sort, the lists of KernelsMoe.Bucket).
+constexpr int DSP_NT = 1024, DSP_SEG = DSP_NT / 64, DSP_CH = 2048;
 
 __device__ __forceinline__ uint64_t same_expert_mask(int e, bool valid, int nbits)
 {
@@ -509,19 +511,31 @@ __device__ __forceinline__ uint64_t same_expert_mask(int e, bool valid, int nbit
     return valid ? m : 0ull;
 }
 
+// Workgroup g places the assignments of chunk g, [g CH, (g + 1) CH).  Every workgroup reads the whole id
+// list (the previous launch wrote it: one cold read, L2 hits after) and counts, per expert, the
+// assignments of the list and those before its chunk, so the placements of the chunks need no exchange
+// between workgroups: assignment a of expert e lands at offsets[e] + (e's assignments before the chunk) +
+// (e's assignments before a in the chunk), ascending a within each expert.  Workgroup 0 also writes the
+// offsets, the tile count and the tiles.
 __global__ __launch_bounds__(DSP_NT) void k_dispatch(int n, int E, int A, const int* __restrict__ ids,
                                                      int* __restrict__ offsets, int* __restrict__ perm,
                                                      Tile* __restrict__ tiles, int* __restrict__ ntiles)
 {
     __shared__ int cnt[DSP_SEG][PHX_MAX_EXPERTS_DEV];
+    __shared__ int pre[PHX_MAX_EXPERTS_DEV], tot[PHX_MAX_EXPERTS_DEV];
     __shared__ int toff[PHX_MAX_EXPERTS_DEV + 1], tb[PHX_MAX_EXPERTS_DEV + 1];
-    __shared__ int wsum[2][DSP_SEG];
+    __shared__ int wsum[2][DSP_SEG], tsum[5][DSP_SEG];
     extern __shared__ uint8_t sid[];  // the expert ids as bytes [n]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int c0 = blockIdx.x * DSP_CH, c1 = min(n, c0 + DSP_CH);  // this workgroup's chunk (c0 % 64 == 0)
     int nbits = 0;
     while ((1 << nbits) < E) nbits++;
     for (int i = tid; i < DSP_SEG * PHX_MAX_EXPERTS_DEV; i += DSP_NT) (&cnt[0][0])[i] = 0;
-    // the ids (written by the previous launch: cold reads) in batches of 16 loads per thread
+    for (int i = tid; i < PHX_MAX_EXPERTS_DEV; i += DSP_NT) {
+        pre[i] = 0;
+        tot[i] = 0;
+    }
+    // the ids in batches of 16 loads per thread
     for (int i0 = tid; i0 < n; i0 += DSP_NT * 16) {
         int v[16];
 #pragma unroll
@@ -530,10 +544,21 @@ __global__ __launch_bounds__(DSP_NT) void k_dispatch(int n, int E, int A, const 
         for (int u = 0; u < 16; u++)
             if (i0 + DSP_NT * u < n) sid[i0 + DSP_NT * u] = (uint8_t)clamp_id(v[u], E);
     }
-    const int seg = (n + DSP_SEG - 1) / DSP_SEG, s0 = min(n, wave * seg), s1 = min(n, s0 + seg);
+    const int seg = (c1 - c0 + DSP_SEG - 1) / DSP_SEG, s0 = min(c1, c0 + wave * seg), s1 = min(c1, s0 + seg);
     const uint64_t lower = (1ull << lane) - 1ull;
     __syncthreads();
-    // pass 1: per segment and expert, the count (the lowest lane of each expert adds its batch count)
+    // counts over the list, 64 assignments per batch (the lowest lane of each expert adds its count; one
+    // workgroup: its segments cover the list), and per segment of the chunk
+    for (int a0 = 64 * wave; gridDim.x > 1 && a0 < n; a0 += 64 * DSP_SEG) {
+        const int a = a0 + lane;
+        const bool valid = a < n;
+        const int e = valid ? sid[a] : 0;
+        const uint64_t m = same_expert_mask(e, valid, nbits);
+        if (valid && (m & lower) == 0) {
+            atomicAdd(&tot[e], __popcll(m));
+            if (a0 < c0) atomicAdd(&pre[e], __popcll(m));  // whole batches lie before the chunk or not
+        }
+    }
     for (int a0 = s0; a0 < s1; a0 += 64) {
         const int a = a0 + lane;
         const bool valid = a < s1;
@@ -542,14 +567,16 @@ __global__ __launch_bounds__(DSP_NT) void k_dispatch(int n, int E, int A, const 
         if (valid && (m & lower) == 0) cnt[wave][e] += __popcll(m);
     }
     __syncthreads();
-    // per expert: total, tile count, and each segment's start within the expert's list
+    // per expert: each segment's start within the chunk's share, the total and the tile count
     int c = 0, tcount = 0;
     if (tid < E) {
+        int run = pre[tid];
         for (int w = 0; w < DSP_SEG; w++) {
             const int h = cnt[w][tid];
-            cnt[w][tid] = c;
-            c += h;
+            cnt[w][tid] = run;
+            run += h;
         }
+        c = gridDim.x > 1 ? tot[tid] : run;
         tcount = (c + A - 1) / A;
     }
     // exclusive scans of c and tcount over the experts (E <= 256: threads 0-255)
@@ -579,11 +606,53 @@ __global__ __launch_bounds__(DSP_NT) void k_dispatch(int n, int E, int A, const 
     if (tid == PHX_MAX_EXPERTS_DEV - 1) {  // the scans' totals: experts past E hold zeros
         toff[E] = b1 + v1;
         tb[E] = b2 + v2;
-        *ntiles = b2 + v2;
+        if (blockIdx.x == 0) *ntiles = b2 + v2;
     }
     __syncthreads();
-    for (int e = tid; e <= E; e += DSP_NT) offsets[e] = toff[e];
-    // pass 2: placement in assignment order
+    if (blockIdx.x == 0) {
+        for (int e = tid; e <= E; e += DSP_NT) offsets[e] = toff[e];
+        // the tiles, longest first (a grid runs its workgroups in tile order, so the short ones fill the
+        // end): every full tile in expert order, then the partial ones in four size classes from the
+        // largest, each in expert order
+        const int nfull = tid < E ? c / A : 0, rem = tid < E ? c - nfull * A : 0;
+        const int cls = rem ? min(4, (4 * rem + A - 1) / A) : 0;  // 1..4, 0: no partial tile
+        int v[5] = {nfull, cls == 1, cls == 2, cls == 3, cls == 4};
+        int inc[5];
+#pragma unroll
+        for (int q = 0; q < 5; q++) {
+            int x = v[q];
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const int y = __shfl_up(x, o, 64);
+                if (lane >= o) x += y;
+            }
+            inc[q] = x;
+            if (lane == 63) tsum[q][wave] = x;
+        }
+        __syncthreads();
+        int tot5[5], pre5[5];
+#pragma unroll
+        for (int q = 0; q < 5; q++) {
+            tot5[q] = 0;
+            pre5[q] = 0;
+            for (int w = 0; w < DSP_SEG; w++) {
+                tot5[q] += tsum[q][w];
+                if (w < wave) pre5[q] += tsum[q][w];
+            }
+        }
+        if (tid < E) {
+            const int fb = pre5[0] + inc[0] - v[0];  // this expert's first full tile
+            for (int q = 0; q < nfull; q++) tiles[fb + q] = Tile{tid, toff[tid] + q * A, A};
+            if (cls) {
+                int pos = tot5[0];
+                for (int b = 4; b > cls; b--) pos += tot5[b];
+                pos += cls == 1 ? pre5[1] + inc[1] - 1 : cls == 2 ? pre5[2] + inc[2] - 1
+                       : cls == 3 ? pre5[3] + inc[3] - 1 : pre5[4] + inc[4] - 1;
+                tiles[pos] = Tile{tid, toff[tid] + nfull * A, rem};
+            }
+        }
+    }
+    // placement of the chunk in assignment order
     for (int a0 = s0; a0 < s1; a0 += 64) {
         const int a = a0 + lane;
         const bool valid = a < s1;
@@ -594,23 +663,14 @@ __global__ __launch_bounds__(DSP_NT) void k_dispatch(int n, int E, int A, const 
         __builtin_amdgcn_wave_barrier();  // every lane has read cnt before the batch's leaders advance it
         if (valid && (m & lower) == 0) cnt[wave][e] += __popcll(m);
     }
-    if (tid < E) {
-        const int base = tb[tid];
-        for (int q = 0; q * A < c; q++) {
-            Tile tl;
-            tl.e = tid;
-            tl.start = toff[tid] + q * A;
-            tl.cnt = min(A, c - q * A);
-            tiles[base + q] = tl;
-        }
-    }
 }
 
 void launch_dispatch(hipStream_t st, int n, int E, int A, const int* ids, int* offsets, int* perm, Tile* tiles,
                      int* ntiles)
 {
     (void)hipFuncSetAttribute((const void*)k_dispatch, hipFuncAttributeMaxDynamicSharedMemorySize, n);
-    launch(k_dispatch, dim3(1), dim3(DSP_NT), (uint32_t)n, st, n, E, A, ids, offsets, perm, tiles, ntiles);
+    launch(k_dispatch, dim3((unsigned)((n + DSP_CH - 1) / DSP_CH)), dim3(DSP_NT), (uint32_t)n, st, n, E, A, ids, offsets,
+           perm, tiles, ntiles);
 }
 
 // ------------------------------------------------------------------------------ grouped row products
@@ -1284,8 +1344,9 @@ void launch_matvec(hipStream_t st, int type, int rows, int nb, int T, const uint
 // ------------------------------------------------------------------------------ combine, norms, residual
 // Per token: acc = sum_j yd[t*k+j] * w_j in rank order (src/GemmaCpu.cs:418, each term rounded then
 // added), out = rmsnorm(shared) * post1 + rmsnorm(acc) * post2 (src/GemmaCpu.cs:384,420-421), and
-// optionally x += rmsnorm(out) * post_ffw_norm (src/GemmaCpu.cs:355-356).
-__global__ __launch_bounds__(256) void k_combine(int d, int k, float eps, const float* __restrict__ yd,
+// optionally x += rmsnorm(out) * post_ffw_norm (src/GemmaCpu.cs:355-356).  For rows wider than the
+// one-round combine's 4096 columns (kernels_decode.hip: launch_combine): 256 threads over the row.
+__global__ __launch_bounds__(256) void k_combine_wide(int d, int k, float eps, const float* __restrict__ yd,
                                                  const float* __restrict__ w, const float* __restrict__ shared,
                                                  const float* __restrict__ post1, const float* __restrict__ post2,
                                                  float* __restrict__ out, float* __restrict__ xres,
@@ -1341,11 +1402,12 @@ __global__ __launch_bounds__(256) void k_combine(int d, int k, float eps, const 
     }
 }
 
-void launch_combine(hipStream_t st, int T, int d, int k, float eps, const float* yd, const float* w, const float* shared,
-                    const float* post1, const float* post2, float* out, float* xres, const float* post_ffw, int* flags)
+void launch_combine_wide(hipStream_t st, int T, int d, int k, float eps, const float* yd, const float* w,
+                         const float* shared, const float* post1, const float* post2, float* out, float* xres,
+                         const float* post_ffw, int* flags)
 {
-    launch(k_combine, dim3(T), dim3(256), (size_t)2 * d * sizeof(float), st, d, k, eps, yd, w, shared, post1,
-                       post2, out, xres, post_ffw, flags);
+    launch(k_combine_wide, dim3(T), dim3(256), (size_t)2 * d * sizeof(float), st, d, k, eps, yd, w, shared, post1,
+           post2, out, xres, post_ffw, flags);
 }
 
 // ------------------------------------------------------------------------------ streaming read
@@ -1525,3 +1587,19 @@ void launch_selftest(hipStream_t st, int op, int n, const float* a, const float*
 }
 
 }  // namespace phx
+
+#ifdef PHX_TIMELINE
+// the instrumented build's clock-stamp table of this file's kernels (as phxdbg_timeline)
+extern "C" __attribute__((visibility("default"))) int phxdbg_timeline_general(unsigned long long* host, size_t n, int clear)
+{
+    const size_t all = sizeof(phx::phx_tl) / sizeof(phx::phx_tl[0]);
+    if (host && hipMemcpyFromSymbol(host, HIP_SYMBOL(phx::phx_tl), std::min(n, all) * 8, 0, hipMemcpyDeviceToHost) != hipSuccess)
+        return -1;
+    if (clear) {
+        static unsigned long long* zero = nullptr;
+        if (!zero) zero = (unsigned long long*)calloc(all, 8);
+        if (hipMemcpyToSymbol(HIP_SYMBOL(phx::phx_tl), zero, all * 8, 0, hipMemcpyHostToDevice) != hipSuccess) return -1;
+    }
+    return (int)all;
+}
+#endif

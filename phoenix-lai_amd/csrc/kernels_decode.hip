@@ -30,22 +30,6 @@
 
 namespace phx {
 
-// Clock stamps of kernel phases, compiled only into an instrumented build (-DPHX_TIMELINE): thread 0 of
-// workgroup b (< TL_WG) writes the 100 MHz wall clock at phase `slot` of launch kind `kind` of stack
-// layer `seq` (modulo TL_SEQ); phxdbg_timeline copies the table to the host.  Without the macro the
-// stamps compile to nothing.
-#ifdef PHX_TIMELINE
-constexpr int TL_SEQ = 64, TL_KIND = 4, TL_SLOT = 8, TL_WG = 512;
-__device__ unsigned long long phx_tl[TL_SEQ * TL_KIND * TL_SLOT * TL_WG];
-#define TL_STAMP(seq, kind, slot)                                                                   \
-    do {                                                                                            \
-        if (threadIdx.x == 0 && blockIdx.x < TL_WG)                                                 \
-            phx_tl[((((seq) % TL_SEQ) * TL_KIND + (kind)) * TL_SLOT + (slot)) * TL_WG + blockIdx.x] = \
-                wall_clock64();                                                                     \
-    } while (0)
-#else
-#define TL_STAMP(seq, kind, slot) ((void)0)
-#endif
 
 constexpr int DMAXNB = 128;  // blocks of 32 per row: K <= 4096
 constexpr int DROWS = 2;     // assignments (expert tiles) or tokens (shared FFN) per workgroup
@@ -1426,87 +1410,82 @@ __global__ __launch_bounds__(1024) void k_dec_down(DecArgs a)
 // rounded then added), out = rmsnorm(shared) * post1 + rmsnorm(acc) * post2 (src/GemmaCpu.cs:384,
 // 420-421), and with a residual x += rmsnorm(out) * post_ffw_norm (src/GemmaCpu.cs:355-356).  Every
 // load of the token, the residual row included, is issued in one round before the first use (d <= 4096:
-// four elements per thread; ranks in groups of 8), and the two branch norms share one reduction.
+// one float4 of four consecutive columns per thread; ranks in groups of 8), and the two branch norms
+// share one reduction.
 constexpr int CB_NT = 1024, CB_E = 4;
 
 __global__ __launch_bounds__(CB_NT) void k_dec_combine(DecArgs a)
 {
     extern __shared__ __align__(16) float cb[];  // acc [d], out [d]
     __shared__ double red[2 * (CB_NT / 64 + 1)];
-    const int t = blockIdx.x, tid = threadIdx.x, d = a.d, k = a.k;
-    float* sacc = cb;
-    float* so = cb + d;
-    const float* sh = a.shout ? a.shout + (int64_t)t * d : nullptr;
-    float* xr = a.xres ? a.xres + (int64_t)t * d : nullptr;
-    const float* xi = a.xin ? a.xin + (int64_t)t * d : xr;  // the residual's source row
-    int ix[CB_E];
-    float accv[CB_E], shv[CB_E], p1[CB_E], p2[CB_E], xv[CB_E], pf[CB_E];
-#pragma unroll
-    for (int q = 0; q < CB_E; q++) {
-        ix[q] = min(tid + q * CB_NT, d - 1);
-        accv[q] = 0.0f;
-    }
+    const int t = blockIdx.x, tid = threadIdx.x, d = a.d, k = a.k, n4 = d / 4;
+    float4* sacc = (float4*)cb;
+    float4* so = (float4*)(cb + d);
+    const float4* sh = a.shout ? (const float4*)(a.shout + (int64_t)t * d) : nullptr;
+    float4* xr = a.xres ? (float4*)(a.xres + (int64_t)t * d) : nullptr;
+    const float4* xi = a.xin ? (const float4*)(a.xin + (int64_t)t * d) : xr;  // the residual's source row
+    const float4* yd = (const float4*)a.yd + (int64_t)t * k * n4;
+    const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const int ix = min(tid, n4 - 1);  // thread tid: columns 4 tid .. 4 tid + 3 (d <= 4 CB_NT)
+    const bool own = tid < n4;
+    float4 acc = z4, shv = z4, p1, p2, xv = z4, pf = z4;
     // ranks in groups of 8, every load of a group issued before its first use
     for (int j0 = 0; j0 < k; j0 += 8) {
-        float yv[CB_E][8], wj[8];
+        float4 yv[8];
+        float wj[8];
 #pragma unroll
         for (int jj = 0; jj < 8; jj++) wj[jj] = a.w[(int64_t)t * k + min(j0 + jj, k - 1)];
 #pragma unroll
-        for (int q = 0; q < CB_E; q++)
-#pragma unroll
-            for (int jj = 0; jj < 8; jj++) yv[q][jj] = a.yd[((int64_t)t * k + min(j0 + jj, k - 1)) * d + ix[q]];
+        for (int jj = 0; jj < 8; jj++) yv[jj] = yd[(int64_t)min(j0 + jj, k - 1) * n4 + ix];
         if (j0 == 0) {
-#pragma unroll
-            for (int q = 0; q < CB_E; q++) {
-                shv[q] = sh ? sh[ix[q]] : 0.0f;
-                p1[q] = a.post1[ix[q]];
-                p2[q] = a.post2[ix[q]];
-                xv[q] = xr ? xi[ix[q]] : 0.0f;
-                pf[q] = xr ? a.post_ffw[ix[q]] : 0.0f;
+            if (sh) shv = sh[ix];
+            p1 = ((const float4*)a.post1)[ix];
+            p2 = ((const float4*)a.post2)[ix];
+            if (xr) {
+                xv = xi[ix];
+                pf = ((const float4*)a.post_ffw)[ix];
             }
         }
 #pragma unroll
-        for (int q = 0; q < CB_E; q++)
-#pragma unroll
-            for (int jj = 0; jj < 8; jj++)
-                if (j0 + jj < k) accv[q] += yv[q][jj] * wj[jj];
+        for (int jj = 0; jj < 8; jj++)
+            if (j0 + jj < k) {
+                acc.x += yv[jj].x * wj[jj];
+                acc.y += yv[jj].y * wj[jj];
+                acc.z += yv[jj].z * wj[jj];
+                acc.w += yv[jj].w * wj[jj];
+            }
     }
     double s2 = 0.0, s1 = 0.0;
-#pragma unroll
-    for (int q = 0; q < CB_E; q++) {
-        const int i = tid + q * CB_NT;
-        if (i < d) {
-            sacc[i] = accv[q];
-            s2 += (double)accv[q] * (double)accv[q];
-            s1 += (double)shv[q] * (double)shv[q];
-        }
+    if (own) {
+        sacc[tid] = acc;
+        s2 = ((double)acc.x * (double)acc.x + (double)acc.y * (double)acc.y) +
+             ((double)acc.z * (double)acc.z + (double)acc.w * (double)acc.w);
+        s1 = ((double)shv.x * (double)shv.x + (double)shv.y * (double)shv.y) +
+             ((double)shv.z * (double)shv.z + (double)shv.w * (double)shv.w);
     }
     __syncthreads();
     float m2, m1;
-    wg_mean_sq2(s2, s1, sacc, sh, d, red, a.flags, &m2, &m1);
+    wg_mean_sq2(s2, s1, cb, sh ? (const float*)sh : nullptr, d, red, a.flags, &m2, &m1);
     const float sc2 = rms_scale_from_mean(m2, a.eps);
     const float sc1 = sh ? rms_scale_from_mean(m1, a.eps) : 0.0f;
-    float ov[CB_E];
+    float4 ov;
+    ov.x = (sh ? shv.x * sc1 * p1.x : 0.0f) + acc.x * sc2 * p2.x;
+    ov.y = (sh ? shv.y * sc1 * p1.y : 0.0f) + acc.y * sc2 * p2.y;
+    ov.z = (sh ? shv.z * sc1 * p1.z : 0.0f) + acc.z * sc2 * p2.z;
+    ov.w = (sh ? shv.w * sc1 * p1.w : 0.0f) + acc.w * sc2 * p2.w;
     double s3 = 0.0;
-#pragma unroll
-    for (int q = 0; q < CB_E; q++) {
-        const int i = tid + q * CB_NT;
-        const float mlp = sh ? shv[q] * sc1 * p1[q] : 0.0f;
-        ov[q] = mlp + accv[q] * sc2 * p2[q];
-        if (i < d) {
-            a.out[(int64_t)t * d + i] = ov[q];
-            so[i] = ov[q];
-            s3 += (double)ov[q] * (double)ov[q];
-        }
+    if (own) {
+        ((float4*)(a.out + (int64_t)t * d))[tid] = ov;
+        so[tid] = ov;
+        s3 = ((double)ov.x * (double)ov.x + (double)ov.y * (double)ov.y) +
+             ((double)ov.z * (double)ov.z + (double)ov.w * (double)ov.w);
     }
     if (xr) {
         __syncthreads();
-        const float sc3 = rms_scale_from_mean(wg_mean_sq(s3, so, d, red, a.flags), a.eps);
-#pragma unroll
-        for (int q = 0; q < CB_E; q++) {
-            const int i = tid + q * CB_NT;
-            if (i < d) xr[i] = xv[q] + ov[q] * sc3 * pf[q];
-        }
+        const float sc3 = rms_scale_from_mean(wg_mean_sq(s3, cb + d, d, red, a.flags), a.eps);
+        if (own)
+            xr[tid] = make_float4(xv.x + ov.x * sc3 * pf.x, xv.y + ov.y * sc3 * pf.y, xv.z + ov.z * sc3 * pf.z,
+                                  xv.w + ov.w * sc3 * pf.w);
     }
 }
 
@@ -1689,6 +1668,34 @@ void launch_dec_down(hipStream_t st, const DecLayerH& h)
     const int rpw = rpw_down(h), nrgb = (h.dn->rg + rpw - 1) / rpw;
     const int nsh = h.sdn ? (h.T + DROWS - 1) / DROWS * h.sdn->rg : 0;
     launch_typed<KDown>(h, dim3(h.max_tiles * nrgb + nsh), dim3(64 * nw_down(h)), down_lds(h), st, dec_args(h));
+}
+
+// The general path's combine (any T): the same kernel over the general path's rows; per token acc =
+// sum_j yd[t*k+j] * w_j in rank order (src/GemmaCpu.cs:418, each term rounded then added),
+// out = rmsnorm(shared) * post1 + rmsnorm(acc) * post2 (src/GemmaCpu.cs:384,420-421), and with xres
+// x += rmsnorm(out) * post_ffw_norm in place (src/GemmaCpu.cs:355-356).
+void launch_combine(hipStream_t st, int T, int d, int k, float eps, const float* yd, const float* w, const float* shared,
+                    const float* post1, const float* post2, float* out, float* xres, const float* post_ffw, int* flags)
+{
+    if (d > CB_E * CB_NT) {
+        launch_combine_wide(st, T, d, k, eps, yd, w, shared, post1, post2, out, xres, post_ffw, flags);
+        return;
+    }
+    DecArgs a{};
+    a.T = T;
+    a.d = d;
+    a.k = k;
+    a.eps = eps;
+    a.yd = const_cast<float*>(yd);
+    a.w = const_cast<float*>(w);
+    a.shout = const_cast<float*>(shared);
+    a.post1 = post1;
+    a.post2 = post2;
+    a.out = out;
+    a.xres = xres;
+    a.post_ffw = post_ffw;
+    a.flags = flags;
+    launch(k_dec_combine, dim3(T), dim3(CB_NT), (uint32_t)((size_t)2 * d * 4), st, a);
 }
 
 void launch_dec_combine(hipStream_t st, const DecLayerH& h)

@@ -371,12 +371,21 @@ __global__ __launch_bounds__(256, 3) void k_grouped_mfma(MmaArgs g)
     if (tile >= *g.ntiles) return;  // uniform over the workgroup
     const Tile tl = g.tiles[tile];
     const int cnt = min(tl.cnt, MMA_TOK);
+#ifdef PHX_TIMELINE
+    // start and end of each workgroup: entries 2 f, 2 f + 1 of the flat workgroup index f (down products:
+    // from entry 16384)
+    const int wgf = blockIdx.y * gridDim.x + blockIdx.x, tbase = g.paired ? 0 : 16384;
+    if (threadIdx.x == 0 && wgf < 8192) phx_tl[tbase + 2 * wgf] = wall_clock64();
+#endif
     switch ((cnt + 31) / 32) {  // active 32-token column tiles
     case 1: mma_tile<TYPE, 1>(g, tl, cnt, ring); break;
     case 2: mma_tile<TYPE, 2>(g, tl, cnt, ring); break;
     case 3: mma_tile<TYPE, 3>(g, tl, cnt, ring); break;
     default: mma_tile<TYPE, 4>(g, tl, cnt, ring); break;
     }
+#ifdef PHX_TIMELINE
+    if (threadIdx.x == 0 && wgf < 8192) phx_tl[tbase + 2 * wgf + 1] = wall_clock64();
+#endif
 }
 
 void launch_grouped_mfma(hipStream_t st, const QMat& w, Act act, const Tile* tiles, const int* ntiles, int max_tiles,
@@ -831,3 +840,19 @@ void launch_grouped_kmma(hipStream_t st, const QMat& w, Act act, const Tile* til
 }
 
 }  // namespace phx
+
+#ifdef PHX_TIMELINE
+// the instrumented build's clock-stamp table of this file's kernels (as phxdbg_timeline)
+extern "C" __attribute__((visibility("default"))) int phxdbg_timeline_prefill(unsigned long long* host, size_t n, int clear)
+{
+    const size_t all = sizeof(phx::phx_tl) / sizeof(phx::phx_tl[0]);
+    if (host && hipMemcpyFromSymbol(host, HIP_SYMBOL(phx::phx_tl), std::min(n, all) * 8, 0, hipMemcpyDeviceToHost) != hipSuccess)
+        return -1;
+    if (clear) {
+        static unsigned long long* zero = nullptr;
+        if (!zero) zero = (unsigned long long*)calloc(all, 8);
+        if (hipMemcpyToSymbol(HIP_SYMBOL(phx::phx_tl), zero, all * 8, 0, hipMemcpyHostToDevice) != hipSuccess) return -1;
+    }
+    return (int)all;
+}
+#endif

@@ -172,6 +172,9 @@ void launch_grouped_kmma(hipStream_t st, const QMat& w, Act act, const Tile* til
 void launch_combine(hipStream_t st, int T, int d, int k, float eps, const float* yd, const float* w,
                     const float* shared, const float* post1, const float* post2, float* out, float* x_resid,
                     const float* post_ffw, int* flags);
+void launch_combine_wide(hipStream_t st, int T, int d, int k, float eps, const float* yd, const float* w,
+                    const float* shared, const float* post1, const float* post2, float* out, float* x_resid,
+                    const float* post_ffw, int* flags);
 // decode path (kernels_decode.hip): four launches per layer for T <= 16 tokens, Q4_0 / Q8_0
 struct DecLayerH {
     int T, d, E, k, nf, nff, rule, max_tiles;
