@@ -191,8 +191,16 @@ void launch_prologue(hipStream_t st, int T, int d, float eps, const float* x, co
 {
     int cols = act_gu.cols > act_sh.cols ? act_gu.cols : act_sh.cols;
     if (cols < d) cols = d;
-    launch(k_prologue<256>, dim3(T), dim3(256), (size_t)cols * sizeof(float), st, d, eps, x, gis, pre2,
-                       ffn_norm, router_in, xscale, act_gu, act_sh, flags);
+    // rows of more than 3072 columns: a thread per four columns (one load round per phase, the Q8_K
+    // super-blocks one per wave; measured faster at C4's 4096, slower at C3's 2816 where the launch is
+    // bound by HBM with 256)
+    const size_t lds = (size_t)cols * sizeof(float);
+    if (cols / 4 > 768)
+        launch(k_prologue<1024>, dim3(T), dim3(1024), lds, st, d, eps, x, gis, pre2, ffn_norm, router_in, xscale, act_gu,
+               act_sh, flags);
+    else
+        launch(k_prologue<256>, dim3(T), dim3(256), lds, st, d, eps, x, gis, pre2, ffn_norm, router_in, xscale, act_gu,
+               act_sh, flags);
 }
 
 // ------------------------------------------------------------------------------ router logits
@@ -317,29 +325,34 @@ __global__ __launch_bounds__(256, 2) void k_router_exact_wide(int T, int d, int 
     }
 }
 
-// Fewer tokens (latency-bound: too few chains to hide the loads): the same four-wave workgroup of 64
-// experts and four tokens (one per wave), with the router columns streamed through a ring of RR_RING
+// Fewer tokens (latency-bound: too few chains to hide the loads): a workgroup of NWV waves takes 64
+// experts and NWV tokens (one per wave), with the router columns streamed through a ring of RR_RING
 // LDS slots by direct global -> LDS loads, RR_RING - 1 chunks of 64 elements ahead: a wave issues
-// four 1-KB column loads (the 64 experts of one float4 column are contiguous) and its token's 16
-// float4 of m per chunk, so its own count of outstanding loads tells when a chunk has landed.
-constexpr int RR_CH4 = 16, RR_RING = 4, RR_DMA = 5;
-__global__ __launch_bounds__(256) void k_router_ring(int T, int d, int E, const float4* __restrict__ wt4,
-                                                     const float* __restrict__ rin, float* __restrict__ logits)
+// 16 / NWV 1-KB column loads (the 64 experts of one float4 column are contiguous) and its token's 16
+// float4 of m per chunk, so its own count of outstanding loads tells when a chunk has landed.  One wave
+// alone issues a VALU instruction about every 8.7 cycles and two or more waves share a SIMD at about 3
+// (measured on MI355X), so with 32 or more token groups eight waves per workgroup (two per SIMD) run
+// the chains faster than four.
+constexpr int RR_CH4 = 16, RR_RING = 4;
+template <int NWV>
+__global__ __launch_bounds__(64 * NWV) void k_router_ring(int T, int d, int E, const float4* __restrict__ wt4,
+                                                          const float* __restrict__ rin, float* __restrict__ logits)
 {
+    constexpr int CPW = RR_CH4 / NWV, DMA = CPW + 1;  // columns and direct loads per wave and chunk
     __shared__ float4 wring[RR_RING][RR_CH4][64];
-    __shared__ float4 mring[RR_RING][4][RR_CH4];
+    __shared__ float4 mring[RR_RING][NWV][RR_CH4];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int e = blockIdx.x * 64 + lane, t = blockIdx.y * 4 + wave;
+    const int e = blockIdx.x * 64 + lane, t = blockIdx.y * NWV + wave;
     const int n4 = d / 4, nch = (n4 + RR_CH4 - 1) / RR_CH4;  // d % 64 == 0: whole chunks
     const float4* wsrc = wt4 + min(e, E - 1);                      // column c: + c * E
     const float4* msrc = (const float4*)(rin + (int64_t)min(t, T - 1) * d) + min(lane, RR_CH4 - 1);
     auto issue = [&](int c) {  // chunk c (clamped: past the end a harmless reload) into its slot
         const int cc = min(c, nch - 1), slot = c % RR_RING;
 #pragma unroll
-        for (int j = 0; j < 4; j++)
-            __builtin_amdgcn_global_load_lds((glb_void_t)(wsrc + (int64_t)(cc * RR_CH4 + 4 * wave + j) * E),
-                                             (lds_void_t)&wring[slot][4 * wave + j][0], 16, 0, 0);
+        for (int j = 0; j < CPW; j++)
+            __builtin_amdgcn_global_load_lds((glb_void_t)(wsrc + (int64_t)(cc * RR_CH4 + CPW * wave + j) * E),
+                                             (lds_void_t)&wring[slot][CPW * wave + j][0], 16, 0, 0);
         if (lane < RR_CH4)
             __builtin_amdgcn_global_load_lds((glb_void_t)(msrc + cc * RR_CH4), (lds_void_t)&mring[slot][wave][0], 16, 0, 0);
     };
@@ -351,13 +364,13 @@ __global__ __launch_bounds__(256) void k_router_ring(int T, int d, int E, const 
     for (int c = 0; c < nch; c++) {
         // chunk c has landed once at most the two later chunks' loads are outstanding; the barrier then
         // publishes it and ends every wave's reads of the slot that issue(c + RING - 1) refills
-        __builtin_amdgcn_s_waitcnt((RR_DMA * (RR_RING - 2)) | (0x7 << 4) | (0xF << 8));
+        __builtin_amdgcn_s_waitcnt((DMA * (RR_RING - 2)) | (0x7 << 4) | (0xF << 8));
         __builtin_amdgcn_s_barrier();
         issue(c + RR_RING - 1);
         const int slot = c % RR_RING;
         // explicit reads (see device_common.h), four columns per batch, the next batch's reads issued
         // before this batch's adds
-        const uint32_t wa = w0 + slot * (RR_CH4 * 64 * 16), ma = m0 + slot * (4 * RR_CH4 * 16);
+        const uint32_t wa = w0 + slot * (RR_CH4 * 64 * 16), ma = m0 + slot * (NWV * RR_CH4 * 16);
         u32x4 W[2][4], M[2][4];
         auto reads = [&](auto GC) {
             constexpr int g = decltype(GC)::value, b = g & 1;
@@ -414,8 +427,10 @@ void launch_router_exact(hipStream_t st, int T, int d, int E, const float* wt4, 
     const float4* w = (const float4*)wt4;
     if (T * gx >= 1024)
         launch(k_router_exact_wide<2>, dim3(gx, (T + 7) / 8), dim3(256), 0, st, T, d, E, w, rin, logits);
+    else if (d % 64 == 0 && (T + 7) / 8 * gx >= 32)
+        launch(k_router_ring<8>, dim3(gx, (T + 7) / 8), dim3(512), 0, st, T, d, E, w, rin, logits);
     else if (d % 64 == 0)
-        launch(k_router_ring, dim3(gx, (T + 3) / 4), dim3(256), 0, st, T, d, E, w, rin, logits);
+        launch(k_router_ring<4>, dim3(gx, (T + 3) / 4), dim3(256), 0, st, T, d, E, w, rin, logits);
     else
         launch(k_router_exact<1>, dim3(gx, T), dim3(64), (uint32_t)(d * 4), st, T, d, E, w, rin, logits);
 }
@@ -1048,8 +1063,9 @@ void launch_grouped(hipStream_t st, const QMat& w, Act act, const Tile* tiles, c
 // ------------------------------------------------------------------------------ GELU-gated requant
 // Per assignment row: e = gelu(g) * u (src/GemmaCpu.cs:415), zero padding up to act.cols, then the
 // activation quantizer of the down weights (Q8_0 or Q8_K on entry to the down MatVec).
-__global__ __launch_bounds__(256) void k_requant(int nf, const float* __restrict__ g, const float* __restrict__ u,
-                                                 const float* __restrict__ tab, Act act)
+template <int NT>
+__global__ __launch_bounds__(NT) void k_requant(int nf, const float* __restrict__ g, const float* __restrict__ u,
+                                                const float* __restrict__ tab, Act act)
 {
     extern __shared__ __align__(16) float sbuf[];
     const int64_t r = blockIdx.x;
@@ -1057,7 +1073,7 @@ __global__ __launch_bounds__(256) void k_requant(int nf, const float* __restrict
     // four values per thread and round (nf and cols are multiples of 32)
     const float4* g4 = (const float4*)(g + r * nf);
     const float4* u4 = (const float4*)(u + r * nf);
-    for (int i4 = tid; i4 < act.cols / 4; i4 += 256) {
+    for (int i4 = tid; i4 < act.cols / 4; i4 += NT) {
         float4 e = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         if (4 * i4 < nf) {
             const float4 gv = g4[i4], uv = u4[i4];
@@ -1067,12 +1083,19 @@ __global__ __launch_bounds__(256) void k_requant(int nf, const float* __restrict
         ((float4*)sbuf)[i4] = e;
     }
     __syncthreads();
-    quantize_row<256>(sbuf, act, r);
+    quantize_row<NT>(sbuf, act, r);
 }
 
+// Q8_K rows: one wave per super-block, all of a row's super-blocks at once up to 1024 threads (a row's
+// values then need one load round); Q8_0 rows: 256 threads
 void launch_requant(hipStream_t st, int rows, int nf, const float* g, const float* u, const float* tab, Act act)
 {
-    launch(k_requant, dim3(rows), dim3(256), (size_t)act.cols * sizeof(float), st, nf, g, u, tab, act);
+    const size_t lds = (size_t)act.cols * sizeof(float);
+    const int nsb = act.fmt == ACT_Q8_0 ? 0 : act.cols / 256;
+    if (nsb >= 12) launch(k_requant<1024>, dim3(rows), dim3(1024), lds, st, nf, g, u, tab, act);
+    else if (nsb >= 7) launch(k_requant<768>, dim3(rows), dim3(768), lds, st, nf, g, u, tab, act);
+    else if (nsb >= 5) launch(k_requant<384>, dim3(rows), dim3(384), lds, st, nf, g, u, tab, act);
+    else launch(k_requant<256>, dim3(rows), dim3(256), lds, st, nf, g, u, tab, act);
 }
 
 // ------------------------------------------------------------------------------ standalone quantizers
