@@ -425,11 +425,21 @@ __device__ __forceinline__ uint32_t ds_r32(uint32_t a)
     asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v) : "v"(a), "i"(OFF));
     return v;
 }
+template <int OFF = 0>
 __device__ __forceinline__ uint32_t ds_ru16(uint32_t a)
 {
     uint32_t v;
-    asm volatile("ds_read_u16 %0, %1" : "=v"(v) : "v"(a));
+    asm volatile("ds_read_u16 %0, %1 offset:%2" : "=v"(v) : "v"(a), "i"(OFF));
     return v;
+}
+
+// A raw buffer resource (gfx9 descriptor, stride 0) over the 4 GB from p: a direct buffer -> LDS load
+// through it takes its lane offset from a VGPR and a uniform offset from an SGPR, so a loop that walks
+// a row advances a scalar instead of each lane's 64-bit address.  The range covers every 32-bit
+// offset; no access relies on the range check.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* p)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, -1, 0x00020000);
 }
 // waits for every LDS read of the wave; the registers passed are the reads' results, tied to the wait
 // so that no use of them is scheduled above it.  A read's result must have no other use before its
@@ -450,6 +460,15 @@ __device__ __forceinline__ void lds_wait(u32x4& a, u32x4& b, uint32_t& c, u32x2&
 }
 // compile-time index for unrolled steps with immediate offsets
 template <int N> using ic = std::integral_constant<int, N>;
+// f(ic<0>), f(ic<1>), ..., f(ic<N - 1>) in order
+template <int N, int I = 0, class F>
+__device__ __forceinline__ void static_for(F&& f)
+{
+    if constexpr (I < N) {
+        f(ic<I>{});
+        static_for<N, I + 1>(f);
+    }
+}
 // after an explicit `s_waitcnt lgkmcnt(0)`: the read's result is defined here (no use moves above it)
 __device__ __forceinline__ void tie(u32x4& v) { asm volatile("" : "+v"(v)); }
 __device__ __forceinline__ void tie(u32x2& v) { asm volatile("" : "+v"(v)); }
