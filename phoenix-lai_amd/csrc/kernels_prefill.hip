@@ -483,16 +483,20 @@ constexpr int KM_NW = 8;    // waves per workgroup
 constexpr int KM_DMA = 9;   // direct loads per wave per super-block
 constexpr int KM_RING = 3;  // ring slots
 
+// LDS ring, region-major: each region holds its KM_RING slots one after another, so a lane's read
+// address in a region is one VGPR and the slot an immediate offset
 template <int TYPE>
-struct KmSlot {
+struct KmRing {
     static constexpr bool Q4K = TYPE == PHX_Q4_K_DEV;
     static constexpr int PAY = Q4K ? 144 : 208;
-    static constexpr int ACT = 0;                                // [32 chunks][48 assignments][16 B]
-    static constexpr int BSM = ACT + 32 * KM_TOK * 16;           // Q4_K: [4 quarters][48][4 fp16 bsums]
-    static constexpr int YD = BSM + (Q4K ? 4 * KM_TOK * 8 : 0);  // [48] token scales
-    static constexpr int W = YD + KM_TOK * 4;                    // [8 waves][16 rows][PAY]
-    static constexpr int WS = W + KM_NW * 16 * PAY;              // [8 waves][16 rows] 4-byte slots
-    static constexpr int BYTES = WS + KM_NW * 16 * 4;
+    static constexpr int ACT_N = 32 * KM_TOK * 16;          // [32 chunks][48 assignments][16 B]
+    static constexpr int BSM_N = Q4K ? 4 * KM_TOK * 8 : 0;  // Q4_K: [4 quarters][48][4 fp16 bsums]
+    static constexpr int YD_N = KM_TOK * 4;                 // [48] token scales
+    static constexpr int W_N = KM_NW * 16 * PAY;            // [8 waves][16 rows][PAY]
+    static constexpr int WS_N = KM_NW * 16 * 4;             // [8 waves][16 rows] 4-byte slots
+    static constexpr int ACT = 0, BSM = ACT + KM_RING * ACT_N, YD = BSM + KM_RING * BSM_N;
+    static constexpr int W = YD + KM_RING * YD_N, WS = W + KM_RING * W_N, BYTES = WS + KM_RING * WS_N;
+    static_assert(W % 16 == 0 && WS % 16 == 0, "16-byte direct loads land aligned");
 };
 
 typedef _Float16 mh4 __attribute__((ext_vector_type(4)));
@@ -516,9 +520,9 @@ constexpr int vm_wait(int n) { return (n & 15) | ((n >> 4) << 14) | (0x7 << 4) |
 template <int TYPE, int NJ>
 __device__ __forceinline__ void kmma_tile(const MmaArgs& g, const Tile& tl, int cnt, unsigned char* ring, int bx)
 {
-    using SL = KmSlot<TYPE>;
-    constexpr bool Q4K = SL::Q4K;
-    constexpr int PAY = SL::PAY, RING = KM_RING, SBY = Q4K ? 4 : 2;
+    using RG = KmRing<TYPE>;
+    constexpr bool Q4K = RG::Q4K;
+    constexpr int PAY = RG::PAY, RING = KM_RING, SBY = Q4K ? 4 : 2;
     const int tid = threadIdx.x, lane = tid & 63, r16 = lane & 15, q = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int gI = bx * 2 + (wave >> 2), ws = wave & 3;
@@ -526,63 +530,69 @@ __device__ __forceinline__ void kmma_tile(const MmaArgs& g, const Tile& tl, int 
     const int nb = g.nb;
     const uint32_t ring0 = (uint32_t)(uintptr_t)(lds_void_t)ring;
 
-    // the direct loads' lane sources at super-block 0 (assignments past cnt: a valid row, never stored)
+    // the direct loads' lane sources (assignments past cnt: a valid row, never stored), as buffer -> LDS
+    // loads: each lane's byte offset (a VGPR, the same for every super-block) and the super-block's
+    // uniform offset (an SGPR)
     auto arow = [&](int t) -> int64_t { return g.perm[tl.start + min(t, cnt - 1)] / g.act_div; };
     // (1)-(3) activation chunks: load i of wave w fills positions 64 (3 w + i) + lane of the
     // [chunk][assignment] array: chunk p / 48 of assignment p % 48
-    const uint16_t* xs[3];
+    uint32_t vx[3];
 #pragma unroll
     for (int i = 0; i < 3; i++) {
         const int p = 64 * (3 * wave + i) + lane;
-        xs[i] = g.act.qh + arow(p % KM_TOK) * g.act.qhstride + 8 * (p / KM_TOK);
+        vx[i] = (uint32_t)(2 * (arow(p % KM_TOK) * g.act.qhstride + 8 * (p / KM_TOK)));
     }
     // (4) Q4_K: dword 48 w + lane (lanes 0-47) of the block sums' [quarter][assignment][2 dwords]
-    const uint16_t* bsrc = nullptr;
+    uint32_t vb = 0;
     if (Q4K) {
         const int dw = 48 * wave + min(lane, 47);
-        bsrc = g.act.bh + arow((dw % 96) >> 1) * g.act.bhstride + 4 * (dw / 96) + 2 * (dw & 1);
+        vb = (uint32_t)(2 * (arow((dw % 96) >> 1) * g.act.bhstride + 4 * (dw / 96) + 2 * (dw & 1)));
     }
     // (5) token scales of assignments 6 w + lane (lanes 0-5)
-    const float* ysrc = g.act.d + arow(6 * wave + min(lane, 5)) * g.act.dstride;
+    const uint32_t vy = (uint32_t)(4 * arow(6 * wave + min(lane, 5)) * g.act.dstride);
     // (6)-(8) the wave's 16 weight rows, 1 KB per load; (9) their scales (lanes 0-15)
     const int gIc = min(gI, g.rg - 1);
-    const uint8_t* wsrc = g.payload + tl.e * g.mat_pay + gIc * g.rg_pay + 16 * ws * PAY + 16 * lane;
-    const uint8_t* ssrc = g.scale + tl.e * g.mat_sc + ((int64_t)gIc * nb * 64 + 16 * ws + r16) * SBY;
+    const __amdgpu_buffer_rsrc_t r_act = buf_rsrc(g.act.qh), r_yd = buf_rsrc(g.act.d);
+    const __amdgpu_buffer_rsrc_t r_bh = buf_rsrc(Q4K ? (const void*)g.act.bh : (const void*)g.act.d);
+    const __amdgpu_buffer_rsrc_t r_w = buf_rsrc(g.payload + tl.e * g.mat_pay + gIc * g.rg_pay);
+    const __amdgpu_buffer_rsrc_t r_s = buf_rsrc(g.scale + tl.e * g.mat_sc + (int64_t)gIc * nb * 64 * SBY);
+    const uint32_t vw = 16 * ws * PAY + 16 * lane, vs = (16 * ws + r16) * SBY;
 
-#define KM_DMA_LOAD(src, lds_off, size) \
-    __builtin_amdgcn_global_load_lds((glb_void_t)(src), (lds_void_t)(ring + (lds_off)), size, 0, 0)
-    auto issue = [&](int b) {  // super-block b (clamped: past the end a harmless reload) into its slot
-        const int bc = min(b, nb - 1);
-        const uint32_t slot = (uint32_t)(b % RING) * SL::BYTES;
-        const uint8_t* wb = wsrc + (int64_t)bc * 64 * PAY;
-        const uint32_t wl = slot + SL::W + wave * 16 * PAY;
+#define KM_LOAD(rsrc, lds_off, size, voff, soff) \
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t)(ring + (lds_off)), size, voff, soff, 0, 0)
+    auto issue = [&](auto SC, int b) {  // super-block b (clamped: past the end a harmless reload) into slot S
+        constexpr int S = decltype(SC)::value;
+        const uint32_t bc = (uint32_t)min(b, nb - 1);
+        const uint32_t sw = bc * 64 * PAY;
+        const int wl = RG::W + S * RG::W_N + wave * 16 * PAY;
 #pragma unroll
-        for (int i = 0; i < 3; i++) KM_DMA_LOAD(xs[i] + (int64_t)bc * 256, slot + SL::ACT + (3 * wave + i) * 1024, 16);
+        for (int i = 0; i < 3; i++) KM_LOAD(r_act, RG::ACT + S * RG::ACT_N + (3 * wave + i) * 1024, 16, vx[i], bc * 512);
         if (Q4K) {
-            if (lane < 48) KM_DMA_LOAD(bsrc + (int64_t)bc * 16, slot + SL::BSM + 192 * wave, 4);
+            if (lane < 48) KM_LOAD(r_bh, RG::BSM + S * RG::BSM_N + 192 * wave, 4, vb, bc * 32);
         } else {
-            if (lane < 16) KM_DMA_LOAD(wb + 3072, wl + 3072, 16);  // Q6_K rows: 3328 bytes
+            if (lane < 16) KM_LOAD(r_w, wl + 3072, 16, vw, sw + 3072);  // Q6_K rows: 3328 bytes
         }
-        if (lane < 6) KM_DMA_LOAD(ysrc + bc, slot + SL::YD + 24 * wave, 4);
-        KM_DMA_LOAD(wb, wl, 16);
-        KM_DMA_LOAD(wb + 1024, wl + 1024, 16);
+        if (lane < 6) KM_LOAD(r_yd, RG::YD + S * RG::YD_N + 24 * wave, 4, vy, bc * 4);
+        KM_LOAD(r_w, wl, 16, vw, sw);
+        KM_LOAD(r_w, wl + 1024, 16, vw, sw + 1024);
         if (Q4K) {
-            if (lane < 16) KM_DMA_LOAD(wb + 2048, wl + 2048, 16);  // Q4_K rows: 2304 bytes
+            if (lane < 16) KM_LOAD(r_w, wl + 2048, 16, vw, sw + 2048);  // Q4_K rows: 2304 bytes
         } else {
-            KM_DMA_LOAD(wb + 2048, wl + 2048, 16);
+            KM_LOAD(r_w, wl + 2048, 16, vw, sw + 2048);
         }
         if (lane < 16) {
-            if (Q4K) KM_DMA_LOAD(ssrc + (int64_t)bc * 64 * SBY, slot + SL::WS + 64 * wave, 4);
-            else KM_DMA_LOAD(ssrc + (int64_t)bc * 64 * SBY, slot + SL::WS + 64 * wave, 2);
+            if (Q4K) KM_LOAD(r_s, RG::WS + S * RG::WS_N + 64 * wave, 4, vs, bc * 64 * SBY);
+            else KM_LOAD(r_s, RG::WS + S * RG::WS_N + 64 * wave, 2, vs, bc * 64 * SBY);
         }
     };
-#undef KM_DMA_LOAD
-    // super-block b has landed once at most the later ones' loads are outstanding; the barrier then
-    // publishes it and ends every wave's reads of the slot that issue(b + RING - 1) refills
-    auto land = [&](int b) {
+#undef KM_LOAD
+    // super-block b (slot S) has landed once at most the later ones' loads are outstanding; the barrier
+    // then publishes it and ends every wave's reads of the slot that issue(b + RING - 1) refills
+    auto land = [&](auto SC, int b) {
+        constexpr int S = decltype(SC)::value;
         __builtin_amdgcn_s_waitcnt(vm_wait(KM_DMA * (RING - 2)));
         __builtin_amdgcn_s_barrier();
-        issue(b + RING - 1);
+        issue(ic<(S + RING - 1) % RING>{}, b + RING - 1);
     };
 
     float sums[8][NJ][4], sumf[NJ][4];
@@ -595,48 +605,56 @@ __device__ __forceinline__ void kmma_tile(const MmaArgs& g, const Tile& tl, int 
             for (int l = 0; l < 8; l++) sums[l][c][v] = 0.0f;
         }
     const mf4 zero4 = {};
-    // the lane's LDS read offsets within a slot
-    const uint32_t o_act = SL::ACT + q * (KM_TOK * 16) + r16 * 16;
-    const uint32_t o_bs = SL::BSM + q * (KM_TOK * 8) + r16 * 8;
-    const uint32_t o_yd = SL::YD + r16 * 4;
-    const uint32_t o_row = SL::W + (wave * 16 + r16) * PAY + 32 * q;
-    const uint32_t o_sc = SL::W + (wave * 16 + r16) * PAY + (Q4K ? 128 + 4 * (q >> 1) : 128 + 16 * q);
-    const uint32_t o_y = Q4K ? o_sc + 8 : SL::W + (wave * 16 + r16) * PAY + 192 + 4 * q;
-    const uint32_t o_ws = SL::WS + (wave * 16 + 4 * q) * 4;
+    // the lane's LDS read addresses in slot 0 of each region (slot S: + S * region slot bytes in the
+    // immediate; the third activation slot from a second address, past the immediate's 64 KB)
+    const uint32_t a_act = ring0 + RG::ACT + q * (KM_TOK * 16) + r16 * 16, a_act2 = a_act + 2 * RG::ACT_N;
+    const uint32_t a_bs = ring0 + RG::BSM + q * (KM_TOK * 8) + r16 * 8;
+    const uint32_t a_yd = ring0 + RG::YD + r16 * 4;
+    const uint32_t a_row = ring0 + RG::W + (wave * 16 + r16) * PAY + 32 * q;
+    const uint32_t a_sc = ring0 + RG::W + (wave * 16 + r16) * PAY + (Q4K ? 128 + 4 * (q >> 1) : 128 + 16 * q);
+    const uint32_t a_y = Q4K ? a_sc + 8 : ring0 + RG::W + (wave * 16 + r16) * PAY + 192 + 4 * q;
+    const uint32_t a_ws = ring0 + RG::WS + (wave * 16 + 4 * q) * 4;
+    static_assert((RING - 1) * RG::W_N + 192 + 16 * 3 + 16 < 65536, "weight slots within the LDS immediate");
+    static_assert(RG::ACT_N + 8 * KM_TOK * 64 < 65536, "two activation slots within the LDS immediate");
+    // activation chunk reads of slot S at inner offset O
+    auto act_rd = [&](auto SC, auto OC) -> u32x4 {
+        constexpr int S = decltype(SC)::value, O = decltype(OC)::value;
+        if constexpr (S < 2) return ds_r128<S * RG::ACT_N + O>(a_act);
+        else return ds_r128<(S - 2) * RG::ACT_N + O>(a_act2);
+    };
 
-#pragma unroll
-    for (int b = 0; b < RING - 1; b++) issue(b);
-    for (int b = 0; b < nb; b++) {
-        land(b);
-        const uint32_t sb = ring0 + (uint32_t)(b % RING) * SL::BYTES;
+    // super-block b in slot S
+    auto sblock = [&](auto SC, int b) {
+        constexpr int S = decltype(SC)::value;
+        land(SC, b);
         // the super-block's weights, row scales, token scales, block sums and the first operands (a read's
         // result is used only after its wait, never first composed into another value)
-        const uint32_t a_row = sb + o_row, a_sc = sb + o_sc, a_act = sb + o_act, a_yd = sb + o_yd;
-        u32x4 D0 = ds_r128(a_row), D1 = ds_r128<16>(a_row);
+        constexpr int OW = S * RG::W_N;
+        u32x4 D0 = ds_r128<OW>(a_row), D1 = ds_r128<OW + 16>(a_row);
         // Q4_K: X0 the dword of sc[2 q], sc[2 q + 1], Y that of mins[2 q], mins[2 q + 1];
         // Q6_K: X the high-bit dwords (s = 2 q: lq 0, 1; s = 2 q + 1: lq 0, 1), Y sc[4 q .. 4 q + 3]
         u32x4 X;
         uint32_t X0;
-        if (Q4K) X0 = ds_r32(a_sc);
-        else X = ds_r128(a_sc);
-        uint32_t Y = ds_r32(sb + o_y);
-        u32x4 WSV = ds_r128(sb + o_ws);
+        if (Q4K) X0 = ds_r32<OW>(a_sc);
+        else X = ds_r128<OW>(a_sc);
+        uint32_t Y = ds_r32<OW>(a_y);
+        u32x4 WSV = ds_r128<S * RG::WS_N>(a_ws);
         uint32_t YD[NJ];
         u32x2 BS[NJ];
         u32x4 B[2][NJ];
-        const uint32_t a_bs = sb + o_bs;
-        YD[0] = ds_r32(a_yd);
-        if (Q4K) BS[0] = ds_r64(a_bs);
-        B[0][0] = ds_r128(a_act);
+        constexpr int OY = S * RG::YD_N, OB = S * RG::BSM_N;
+        YD[0] = ds_r32<OY>(a_yd);
+        if (Q4K) BS[0] = ds_r64<OB>(a_bs);
+        B[0][0] = act_rd(SC, ic<0>{});
         if (NJ > 1) {
-            YD[1 % NJ] = ds_r32<64>(a_yd);
-            if (Q4K) BS[1 % NJ] = ds_r64<128>(a_bs);
-            B[0][1 % NJ] = ds_r128<256>(a_act);
+            YD[1 % NJ] = ds_r32<OY + 64>(a_yd);
+            if (Q4K) BS[1 % NJ] = ds_r64<OB + 128>(a_bs);
+            B[0][1 % NJ] = act_rd(SC, ic<256>{});
         }
         if (NJ > 2) {
-            YD[2 % NJ] = ds_r32<128>(a_yd);
-            if (Q4K) BS[2 % NJ] = ds_r64<256>(a_bs);
-            B[0][2 % NJ] = ds_r128<512>(a_act);
+            YD[2 % NJ] = ds_r32<OY + 128>(a_yd);
+            if (Q4K) BS[2 % NJ] = ds_r64<OB + 256>(a_bs);
+            B[0][2 % NJ] = act_rd(SC, ic<512>{});
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         tie(D0);
@@ -735,9 +753,9 @@ __device__ __forceinline__ void kmma_tile(const MmaArgs& g, const Tile& tl, int 
         auto step = [&](auto LC) {
             constexpr int l = decltype(LC)::value, cur = l & 1;
             if (l + 1 < 8) {
-                B[cur ^ 1][0] = ds_r128<(l + 1) * KM_TOK * 64>(a_act);
-                if (NJ > 1) B[cur ^ 1][1 % NJ] = ds_r128<(l + 1) * KM_TOK * 64 + 256>(a_act);
-                if (NJ > 2) B[cur ^ 1][2 % NJ] = ds_r128<(l + 1) * KM_TOK * 64 + 512>(a_act);
+                B[cur ^ 1][0] = act_rd(SC, ic<(l + 1) * KM_TOK * 64>{});
+                if (NJ > 1) B[cur ^ 1][1 % NJ] = act_rd(SC, ic<(l + 1) * KM_TOK * 64 + 256>{});
+                if (NJ > 2) B[cur ^ 1][2 % NJ] = act_rd(SC, ic<(l + 1) * KM_TOK * 64 + 512>{});
             }
             mh8 A, A2;
             a_op(l, A, A2);
@@ -774,6 +792,16 @@ __device__ __forceinline__ void kmma_tile(const MmaArgs& g, const Tile& tl, int 
                 for (int v = 0; v < 4; v++) sumf[c][v] = sumf[c][v] - dm[c][v] * Cm[v];
             }
         }
+    };
+
+    issue(ic<0>{}, 0);
+    issue(ic<1>{}, 1);
+    // the ring's slots by unrolling: every LDS offset is an immediate
+    static_assert(RING == 3, "the super-block loop is unrolled by the ring size");
+    for (int b = 0; b < nb; b += 3) {
+        sblock(ic<0>{}, b);
+        if (b + 1 < nb) sblock(ic<1>{}, b + 1);
+        if (b + 2 < nb) sblock(ic<2>{}, b + 2);
     }
     // the loads issued past the last super-block land in this workgroup's LDS: let them finish
     __builtin_amdgcn_s_waitcnt(0);
@@ -857,11 +885,11 @@ void launch_grouped_kmma(hipStream_t st, const QMat& w, Act act, const Tile* til
     g.paired = w.paired;
     const dim3 grid((w.rg + 1) / 2, max_tiles);
     if (w.type == PHX_Q4_K_DEV) {
-        constexpr size_t lds = (size_t)KM_RING * KmSlot<PHX_Q4_K_DEV>::BYTES;
+        constexpr size_t lds = (size_t)KmRing<PHX_Q4_K_DEV>::BYTES;
         (void)hipFuncSetAttribute((const void*)k_grouped_kmma<PHX_Q4_K_DEV>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         launch(k_grouped_kmma<PHX_Q4_K_DEV>, grid, dim3(KM_NW * 64), (uint32_t)lds, st, g);
     } else {
-        constexpr size_t lds = (size_t)KM_RING * KmSlot<PHX_Q6_K_DEV>::BYTES;
+        constexpr size_t lds = (size_t)KmRing<PHX_Q6_K_DEV>::BYTES;
         (void)hipFuncSetAttribute((const void*)k_grouped_kmma<PHX_Q6_K_DEV>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         launch(k_grouped_kmma<PHX_Q6_K_DEV>, grid, dim3(KM_NW * 64), (uint32_t)lds, st, g);
     }

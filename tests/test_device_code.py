@@ -1,6 +1,7 @@
 """Static checks of the generated gfx950 code (CPU only: hipcc cross-compiles the kernels to assembly).
 
-The kernels fed by direct global -> LDS loads (the matrix-core kernels, the ring-fed router) read their
+The kernels fed by direct global -> LDS loads (global_load_lds, or buffer_load ... lds: the matrix-core
+kernels, the ring-fed router) read their
 LDS operands with explicit ds_read instructions and wait for
 them themselves (phoenix-lai_amd/csrc/device_common.h).  The compiler takes an inline-asm result as
 ready at once, so any instruction it places between such a read and its wait (a register copy at a
@@ -51,11 +52,13 @@ def early_uses(asm_text):
         if inasm and op == "s_waitcnt" and "lgkmcnt(0)" in s:
             pending = set()
             continue
-        srcs = parts[1:] if op.startswith(stores) else parts[2:]
+        # direct loads into LDS (global_load_lds, buffer_load ... lds) write no VGPR: every operand is a source
+        nodst = op.startswith(stores) or (op.startswith("buffer_load") and parts[-1] == "lds")
+        srcs = parts[1:] if nodst else parts[2:]
         for t in srcs:
             for r in _regs(t) & pending:
                 out.append((i + 1, s, r))
-        if len(parts) > 1 and not op.startswith(stores) and not op.startswith("s_"):
+        if len(parts) > 1 and not nodst and not op.startswith("s_"):
             pending -= _regs(parts[1])
     return out
 
@@ -79,6 +82,7 @@ def test_kernels_wait_before_using_lds_reads(tmp_path, src):
            f"-I{ROOT / 'include'}", "--cuda-device-only", "-S", str(CSRC / src), "-o", str(out)]
     subprocess.run(cmd, check=True, capture_output=True, timeout=600)
     text = out.read_text()
-    assert "ds_read_b128" in text and "global_load_lds_dwordx4" in text
+    assert "ds_read_b128" in text
+    assert "global_load_lds_dwordx4" in text or re.search(r"buffer_load_dwordx4 .* lds$", text, re.M)
     bad = early_uses(text)
     assert not bad, f"{len(bad)} early uses, first: {bad[:3]}"
