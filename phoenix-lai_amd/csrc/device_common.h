@@ -269,6 +269,27 @@ __device__ __forceinline__ unsigned wave_max_u32(unsigned v)
     return (unsigned)__builtin_amdgcn_readlane((int)v, 63);
 }
 
+// Maximum over the 64 lanes of the 64-bit key (hi, lo), returned to every lane.
+template <int CTRL, int ROWMASK = 0xf>
+__device__ __forceinline__ void key_max_step(unsigned& hi, unsigned& lo)
+{
+    const unsigned oh = (unsigned)dpp_i<CTRL, ROWMASK>((int)hi, (int)hi), ol = (unsigned)dpp_i<CTRL, ROWMASK>((int)lo, (int)lo);
+    const bool gt = oh > hi || (oh == hi && ol > lo);
+    hi = gt ? oh : hi;
+    lo = gt ? ol : lo;
+}
+__device__ __forceinline__ void wave_max_key(unsigned& hi, unsigned& lo)
+{
+    key_max_step<0xb1>(hi, lo);
+    key_max_step<0x4e>(hi, lo);
+    key_max_step<0x141>(hi, lo);
+    key_max_step<0x140>(hi, lo);
+    key_max_step<0x142, 0xa>(hi, lo);
+    key_max_step<0x143, 0xc>(hi, lo);
+    hi = (unsigned)__builtin_amdgcn_readlane((int)hi, 63);
+    lo = (unsigned)__builtin_amdgcn_readlane((int)lo, 63);
+}
+
 // Maximum over the 64 lanes of a double (NaN-free inputs), returned to every lane.
 __device__ __forceinline__ double wave_max_dpp(double v)
 {

@@ -25,11 +25,11 @@ __device__ __forceinline__ void store_q8k_block(const Act& act, int64_t row, int
     sm += __shfl_xor(sm, 1, 64);
     sm += __shfl_xor(sm, 2, 64);
     if ((lane & 3) == 0) {
-        if (act.fmt == ACT_K4) act.s[row * act.sstride + b * 16 + (lane >> 2)] = sm;
+        if (act.fmt == ACT_K4 && act.s) act.s[row * act.sstride + b * 16 + (lane >> 2)] = sm;
         if (act.bh) act.bh[row * act.bhstride + b * 16 + (lane >> 2)] = (uint16_t)f2h_bits((float)sm);  // exact
     }
     if (act.fmt == ACT_Q8K) {
-        ((uint32_t*)(act.q + row * act.qstride + (int64_t)b * 256))[lane] = pk;
+        if (act.q) ((uint32_t*)(act.q + row * act.qstride + (int64_t)b * 256))[lane] = pk;
         if (!act.qh) return;  // uniform
     }
     const uint8_t* qb = (const uint8_t*)qrow;
@@ -38,7 +38,8 @@ __device__ __forceinline__ void store_q8k_block(const Act& act, int64_t row, int
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     auto qv = [&](int e) { return (int)(int8_t)qb[e]; };
-    if (act.fmt == ACT_K4) {  // dword (s, l) = x[32 s + l + 8 m], m = 0..3: lane = 8 s + l
+    if (!act.q) {  // uniform: only the matrix cores' copy is wanted
+    } else if (act.fmt == ACT_K4) {  // dword (s, l) = x[32 s + l + 8 m], m = 0..3: lane = 8 s + l
         const int s8 = lane >> 3, l = lane & 7, e = 32 * s8 + l;
         ((uint32_t*)(act.q + row * act.qstride + (int64_t)b * 256))[lane] =
             (uint32_t)qb[e] | ((uint32_t)qb[e + 8] << 8) | ((uint32_t)qb[e + 16] << 16) | ((uint32_t)qb[e + 24] << 24);
@@ -82,7 +83,7 @@ __device__ void quantize_row(const float* v, Act act, int64_t row)
             int sum;
             const int qw = q8_0_oct(xv, &dval, &sum);
             if (b < nb) {
-                ((int*)(act.q + row * act.qstride))[8 * b + l8] = qw;
+                if (act.q) ((int*)(act.q + row * act.qstride))[8 * b + l8] = qw;
                 if (act.qh) {  // the four integers as exact fp16 (signed bytes through the 1152 bias)
                     const uint32_t u = (uint32_t)qw ^ 0x80808080u;
                     *(uint2*)(act.qh + row * act.qhstride + 32 * b + 4 * l8) =
@@ -90,7 +91,7 @@ __device__ void quantize_row(const float* v, Act act, int64_t row)
                 }
                 if (l8 == 0) {
                     act.d[row * act.dstride + b] = dval;
-                    act.s[row * act.sstride + b] = sum;
+                    if (act.s) act.s[row * act.sstride + b] = sum;
                 }
             }
         }
@@ -153,7 +154,6 @@ __global__ __launch_bounds__(NT) void k_prologue(int d, float eps, const float* 
     float scale = rms_scale_from_mean(mean_sq_cert<NT>(xr, d, red, flags), eps);
     TL_STAMP(0, 0, 1);
     float sc = 1.0f / (float)__dsqrt_rn((double)d);
-    float* ri = router_in + (int64_t)t * d;
     // four values per thread and round (d and the activation widths are multiples of 32)
     const float4* x4 = (const float4*)xr;
     auto fill = [&](const float* nw, int cols) {
@@ -166,10 +166,13 @@ __global__ __launch_bounds__(NT) void k_prologue(int d, float eps, const float* 
             ((float4*)sbuf)[i4] = v;
         }
     };
-    for (int i4 = tid; i4 < d / 4; i4 += NT) {
-        const float4 xv = x4[i4], gv = ((const float4*)gis)[i4];
-        ((float4*)ri)[i4] = make_float4(xv.x * scale * sc * gv.x, xv.y * scale * sc * gv.y, xv.z * scale * sc * gv.z,
-                                        xv.w * scale * sc * gv.w);
+    if (router_in) {  // uniform; null where the router forms m from x and the scale itself
+        float* ri = router_in + (int64_t)t * d;
+        for (int i4 = tid; i4 < d / 4; i4 += NT) {
+            const float4 xv = x4[i4], gv = ((const float4*)gis)[i4];
+            ((float4*)ri)[i4] = make_float4(xv.x * scale * sc * gv.x, xv.y * scale * sc * gv.y,
+                                            xv.z * scale * sc * gv.z, xv.w * scale * sc * gv.w);
+        }
     }
     fill(pre2, act_gu.cols);
     __syncthreads();
@@ -203,13 +206,96 @@ void launch_prologue(hipStream_t st, int T, int d, float eps, const float* x, co
                act_sh, flags);
 }
 
+// ------------------------------------------------------------------------------ top-k and weights
+// One wave per token (topk_wave: lane e + 64 q holds expert e + 64 q's logit in v[q], avail[q] whether
+// the expert exists; lanes j < k write rank j's id and weight to ids[j], wout[j]), in k_topk or, where
+// one router workgroup holds every expert (E <= 64), at the end of the router kernel.  k rounds of the
+// reference's scan (GemmaCpu.cs:400-405, see scan_start): the
+// lowest-index untaken expert when its logit is NaN, else the argmax of the untaken non-NaN logits
+// with the lower expert index winning ties (the rank rule of KernelsMoe.RouterSelect,
+// src/KernelsMoe.cs:64-78, for NaN-free logits).
+// Weights as GemmaCpu.cs:406-407,417: p_j = (float)exp((double)(l_j - l_0)), sum in double,
+// w_j = (float)(p_j / sum) * down_scale[e_j]; rule 1 keeps the CPU's in-place sel[0] update.
+__device__ __forceinline__ void topk_wave(const float (&v)[4], bool (&avail)[4], int k, int rule,
+                                          const float* __restrict__ ds, int* __restrict__ ids,
+                                          float* __restrict__ wout)
+{
+    const int lane = threadIdx.x & 63;
+    float my_sel = 0.0f;
+    int my_id = 0;
+    float dsv[4];  // the down scales, loaded now: their latency hides behind the rounds
+#pragma unroll
+    for (int q = 0; q < 4; q++) dsv[q] = avail[q] ? ds[lane + 64 * q] : 0.0f;
+    for (int j = 0; j < k; j++) {
+        bool e0_nan;
+        const int e0 = scan_start(avail, v, &e0_nan);
+        int bi;
+        if (e0_nan) {  // uniform: the scan keeps e0
+            bi = e0;
+        } else {
+            // the round's maximum as one 64-bit key per lane: the logit's order-preserving bits above
+            // (both zeros as +0, which compare equal), the complemented index below (ties to the lower
+            // index); a NaN or taken expert's key is 0, below every number's
+            unsigned bh = 0u, bl = 0u;
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                if (avail[q] && v[q] == v[q]) {
+                    const unsigned kh = sortable_f32(v[q] == 0.0f ? 0.0f : v[q]), kl = ~(unsigned)(lane + 64 * q);
+                    if (kh > bh || (kh == bh && kl > bl)) {
+                        bh = kh;
+                        bl = kl;
+                    }
+                }
+            wave_max_key(bh, bl);
+            bi = bh ? (int)~bl : -1;  // -1: no expert left (every lane agrees)
+        }
+        if (bi >= 0 && lane == (bi & 63)) avail[bi >> 6] = false;
+        // the round's logit, from the lane that holds it (bi is wave-uniform)
+        const int q0 = bi < 0 ? 0 : bi >> 6;
+        const float vq = q0 == 0 ? v[0] : q0 == 1 ? v[1] : q0 == 2 ? v[2] : v[3];
+        const float bv = bi < 0 ? 0.0f : __int_as_float(__builtin_amdgcn_readlane(__float_as_int(vq), bi & 63));
+        if (lane == j) {  // lane j keeps rank j
+            my_sel = bv;
+            my_id = bi < 0 ? 0 : bi;
+        }
+    }
+    // weights (src/GemmaCpu.cs:406-407,417), lane j for rank j: p_j = (float)exp((double)(l_j - top)),
+    // the double sum in rank order, w_j = (float)(p_j / sum) * down_scale; GemmaCpu.cs:407 overwrites
+    // sel[0] with p_0 = exp(0) = 1 before the later terms read it (rule 1)
+    const float sel0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_sel), 0));
+    const float top = (rule == 1 && lane > 0) ? 1.0f : sel0;
+    const float pj = lane < k ? (float)exp((double)(my_sel - top)) : 0.0f;
+    double sum = 0.0;
+    for (int q = 0; q < k; q++) sum += (double)__int_as_float(__builtin_amdgcn_readlane(__float_as_int(pj), q));
+    // ds[my_id] from the lane that loaded it (every lane takes part in the exchanges)
+    float dj = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const float t = __shfl(dsv[q], my_id & 63, 64);
+        if ((my_id >> 6) == q) dj = t;
+    }
+    if (lane < k) {
+        ids[lane] = my_id;
+        wout[lane] = (float)((double)pj / sum) * dj;
+    }
+}
+
+// the top-k of token t in a router wave whose lane e holds expert e's logit s (E <= 64)
+__device__ __forceinline__ void topk_row(const TopkOut& to, int t, float s, bool valid)
+{
+    const float v[4] = {s, 0.0f, 0.0f, 0.0f};
+    bool avail[4] = {valid, false, false, false};
+    topk_wave(v, avail, to.k, to.rule, to.ds, to.ids + (int64_t)t * to.k, to.w + (int64_t)t * to.k);
+}
+
 // ------------------------------------------------------------------------------ router logits
 // logits[t][e] = sum_i W[e][i] * m[t][i] as the sequential float sum of GemmaCpu.cs:393-394: one lane
 // per (t, e), the products rounded, then added in index order.  W is stored [d/4][E][4] so the 64
 // lanes (experts) of a wave read 1 KB contiguous; m is wave-uniform.
 template <int TB>
 __global__ __launch_bounds__(64) void k_router_exact(int T, int d, int E, const float4* __restrict__ wt4,
-                                                     const float* __restrict__ rin, float* __restrict__ logits)
+                                                     const float* __restrict__ rin, float* __restrict__ logits,
+                                                     TopkOut to)
 {
     extern __shared__ float4 srin[];  // [TB][d / 4]: the wave's token rows of m
     const int lane = threadIdx.x, e = blockIdx.x * 64 + lane, t0 = blockIdx.y * TB;
@@ -250,6 +336,11 @@ __global__ __launch_bounds__(64) void k_router_exact(int T, int d, int E, const 
         for (int j = 0; j < TB; j++)
             if (t0 + j < T) logits[(int64_t)(t0 + j) * E + e] = s[j];
     }
+    if (to.ids) {  // uniform: every expert is in this wave (E <= 64)
+#pragma unroll
+        for (int j = 0; j < TB; j++)
+            if (t0 + j < T) topk_row(to, t0 + j, s[j], e < E);
+    }
 }
 
 // Many tokens: a workgroup of four waves takes 64 experts and 4 TPW tokens; wave w carries tokens
@@ -264,7 +355,7 @@ constexpr int RXW_CH4 = 32;  // float4 columns per chunk
 template <int TPW>
 __global__ __launch_bounds__(256, 2) void k_router_exact_wide(int T, int d, int E, const float4* __restrict__ wt4,
                                                               const float* __restrict__ rin,
-                                                              float* __restrict__ logits)
+                                                              float* __restrict__ logits, TopkOut to, RouterX rx)
 {
     constexpr int TOK = 4 * TPW;
     __shared__ float4 wbuf[2][RXW_CH4][64];
@@ -278,14 +369,26 @@ __global__ __launch_bounds__(256, 2) void k_router_exact_wide(int T, int d, int 
     // (threads below 32 TOK) column tid % 32 of token row tid / 32
     const int er = min(e, E - 1), cr = tid >> 6, mt = min(tid >> 5, TOK - 1), mc = tid & 31;
     const bool mld = tid < 32 * TOK;
-    const float4* mrow = (const float4*)(rin + (int64_t)min(tb + mt, T - 1) * d);
-    float4 st[8], sm;
+    const int mtok = min(tb + mt, T - 1);
+    const float4* mrow = (const float4*)(rin + (int64_t)mtok * d);
+    // rx.xscale set: rin is x and m = ((x * rinv) * (1/sqrt(d))) * s is formed here as the prologue would
+    // (src/GemmaCpu.cs:388-389), the row's rms scale rinv from the prologue
+    const float rinv = rx.xscale ? rx.xscale[mtok] : 0.0f, sc = 1.0f / (float)__dsqrt_rn((double)d);
+    const float4* gis4 = (const float4*)(rx.xscale ? rx.gis : rin);
+    // the loads go out with the chunk's others; m is formed where it is stored, after the chunk's adds
+    auto mval = [&](const float4& v, const float4& gv) {
+        return rx.xscale ? make_float4(v.x * rinv * sc * gv.x, v.y * rinv * sc * gv.y, v.z * rinv * sc * gv.z,
+                                       v.w * rinv * sc * gv.w)
+                         : v;
+    };
+    float4 st[8], sm, sg;
 #pragma unroll
     for (int k = 0; k < 8; k++) st[k] = wt4[(int64_t)min(cr + 4 * k, n4 - 1) * E + er];
     sm = mrow[min(mc, n4 - 1)];
+    sg = gis4[min(mc, n4 - 1)];
 #pragma unroll
     for (int k = 0; k < 8; k++) wbuf[0][cr + 4 * k][lane] = st[k];
-    if (mld) mbuf[0][mt][mc] = sm;
+    if (mld) mbuf[0][mt][mc] = mval(sm, sg);
     __syncthreads();
     float s[TPW];
 #pragma unroll
@@ -297,6 +400,7 @@ __global__ __launch_bounds__(256, 2) void k_router_exact_wide(int T, int d, int 
 #pragma unroll
         for (int k = 0; k < 8; k++) st[k] = wt4[(int64_t)min(cn + cr + 4 * k, n4 - 1) * E + er];
         sm = mrow[min(cn + mc, n4 - 1)];
+        sg = gis4[min(cn + mc, n4 - 1)];
         const int ni = min(RXW_CH4, n4 - c * RXW_CH4);  // d % 32 == 0: ni % 8 == 0
 #pragma unroll 8
         for (int i = 0; i < ni; i++) {
@@ -315,13 +419,18 @@ __global__ __launch_bounds__(256, 2) void k_router_exact_wide(int T, int d, int 
         }
 #pragma unroll
         for (int k = 0; k < 8; k++) wbuf[buf ^ 1][cr + 4 * k][lane] = st[k];  // read before the last barrier
-        if (mld) mbuf[buf ^ 1][mt][mc] = sm;
+        if (mld) mbuf[buf ^ 1][mt][mc] = mval(sm, sg);
         __syncthreads();
     }
     if (e < E) {
 #pragma unroll
         for (int j = 0; j < TPW; j++)
             if (t0 + j < T) logits[(int64_t)(t0 + j) * E + e] = s[j];
+    }
+    if (to.ids) {  // uniform: every expert is in this workgroup (E <= 64), the wave's tokens are its own
+#pragma unroll
+        for (int j = 0; j < TPW; j++)
+            if (t0 + j < T) topk_row(to, t0 + j, s[j], e < E);
     }
 }
 
@@ -336,7 +445,8 @@ __global__ __launch_bounds__(256, 2) void k_router_exact_wide(int T, int d, int 
 constexpr int RR_CH4 = 16, RR_RING = 4;
 template <int NWV>
 __global__ __launch_bounds__(64 * NWV) void k_router_ring(int T, int d, int E, const float4* __restrict__ wt4,
-                                                          const float* __restrict__ rin, float* __restrict__ logits)
+                                                          const float* __restrict__ rin, float* __restrict__ logits,
+                                                          TopkOut to)
 {
     constexpr int CPW = RR_CH4 / NWV, DMA = CPW + 1;  // columns and direct loads per wave and chunk
     __shared__ float4 wring[RR_RING][RR_CH4][64];
@@ -416,38 +526,35 @@ __global__ __launch_bounds__(64 * NWV) void k_router_ring(int T, int d, int E, c
     }
     __builtin_amdgcn_s_waitcnt(0);  // the reloads past the last chunk land before the workgroup ends
     if (e < E && t < T) logits[(int64_t)t * E + e] = s;
+    if (to.ids && t < T) topk_row(to, t, s, e < E);  // uniform: every expert is in this wave (E <= 64)
 }
 
 // Eight tokens per workgroup where that still makes 1024 workgroups (enough chains to keep the SIMDs
 // busy: compute-bound), else four with the deeper load ring (d % 64 == 0), else one wave per (64
 // experts, token) with the token's row of m in LDS.
-void launch_router_exact(hipStream_t st, int T, int d, int E, const float* wt4, const float* rin, float* logits)
+bool router_reads_x(int T, int d, int E) { return T * ((E + 63) / 64) >= 1024; }
+
+void launch_router_exact(hipStream_t st, int T, int d, int E, const float* wt4, const float* rin, float* logits,
+                         TopkOut to, RouterX rx)
 {
     const int gx = (E + 63) / 64;
+    if (gx > 1) to.ids = nullptr;  // the top-k needs every expert of a token in one wave
     const float4* w = (const float4*)wt4;
     if (T * gx >= 1024)
-        launch(k_router_exact_wide<2>, dim3(gx, (T + 7) / 8), dim3(256), 0, st, T, d, E, w, rin, logits);
+        launch(k_router_exact_wide<2>, dim3(gx, (T + 7) / 8), dim3(256), 0, st, T, d, E, w, rin, logits, to, rx);
     else if (d % 64 == 0 && (T + 7) / 8 * gx >= 32)
-        launch(k_router_ring<8>, dim3(gx, (T + 7) / 8), dim3(512), 0, st, T, d, E, w, rin, logits);
+        launch(k_router_ring<8>, dim3(gx, (T + 7) / 8), dim3(512), 0, st, T, d, E, w, rin, logits, to);
     else if (d % 64 == 0)
-        launch(k_router_ring<4>, dim3(gx, (T + 3) / 4), dim3(256), 0, st, T, d, E, w, rin, logits);
+        launch(k_router_ring<4>, dim3(gx, (T + 3) / 4), dim3(256), 0, st, T, d, E, w, rin, logits, to);
     else
-        launch(k_router_exact<1>, dim3(gx, T), dim3(64), (uint32_t)(d * 4), st, T, d, E, w, rin, logits);
+        launch(k_router_exact<1>, dim3(gx, T), dim3(64), (uint32_t)(d * 4), st, T, d, E, w, rin, logits, to);
 }
 
-// ------------------------------------------------------------------------------ top-k and weights
-// One wave per token.  k rounds of the reference's scan (GemmaCpu.cs:400-405, see scan_start): the
-// lowest-index untaken expert when its logit is NaN, else the argmax of the untaken non-NaN logits
-// with the lower expert index winning ties (the rank rule of KernelsMoe.RouterSelect,
-// src/KernelsMoe.cs:64-78, for NaN-free logits).
-// Weights as GemmaCpu.cs:406-407,417: p_j = (float)exp((double)(l_j - l_0)), sum in double,
-// w_j = (float)(p_j / sum) * down_scale[e_j]; rule 1 keeps the CPU's in-place sel[0] update.
 __global__ __launch_bounds__(64) void k_topk(int E, int k, int rule, const float* __restrict__ logits,
                                              const float* __restrict__ ds, int* __restrict__ ids, float* __restrict__ wout)
 {
     const int t = blockIdx.x, lane = threadIdx.x;
-    float my_sel = 0.0f, v[4];
-    int my_id = 0;
+    float v[4];
     bool avail[4];
 #pragma unroll
     for (int q = 0; q < 4; q++) {
@@ -455,45 +562,7 @@ __global__ __launch_bounds__(64) void k_topk(int E, int k, int rule, const float
         avail[q] = e < E;
         v[q] = avail[q] ? logits[(int64_t)t * E + e] : 0.0f;
     }
-    for (int j = 0; j < k; j++) {
-        bool e0_nan;
-        const int e0 = scan_start(avail, v, &e0_nan);
-        float bv = 0.0f;
-        int bi = -1;
-        if (e0_nan) {  // uniform: the scan keeps e0
-            bi = e0;
-            const int q0 = e0 >> 6;
-            const float vq = q0 == 0 ? v[0] : q0 == 1 ? v[1] : q0 == 2 ? v[2] : v[3];
-            bv = __shfl(vq, e0 & 63, 64);
-        } else {
-#pragma unroll
-            for (int q = 0; q < 4; q++)
-                if (avail[q] && v[q] == v[q] && sel_beats(v[q], lane + 64 * q, bv, bi)) { bv = v[q]; bi = lane + 64 * q; }
-#pragma unroll
-            for (int off = 32; off > 0; off >>= 1) {
-                float ov = __shfl_xor(bv, off, 64);
-                int oi = __shfl_xor(bi, off, 64);
-                if (sel_beats(ov, oi, bv, bi)) { bv = ov; bi = oi; }
-            }
-        }
-        if (bi >= 0 && lane == (bi & 63)) avail[bi >> 6] = false;
-        if (lane == j) {  // the round's result is wave-uniform: lane j keeps rank j
-            my_sel = bv;
-            my_id = bi < 0 ? 0 : bi;
-        }
-    }
-    // weights (src/GemmaCpu.cs:406-407,417), lane j for rank j: p_j = (float)exp((double)(l_j - top)),
-    // the double sum in rank order, w_j = (float)(p_j / sum) * down_scale; GemmaCpu.cs:407 overwrites
-    // sel[0] with p_0 = exp(0) = 1 before the later terms read it (rule 1)
-    const float sel0 = __shfl(my_sel, 0, 64);
-    const float top = (rule == 1 && lane > 0) ? 1.0f : sel0;
-    const float pj = lane < k ? (float)exp((double)(my_sel - top)) : 0.0f;
-    double sum = 0.0;
-    for (int q = 0; q < k; q++) sum += (double)__shfl(pj, q, 64);
-    if (lane < k) {
-        ids[(int64_t)t * k + lane] = my_id;
-        wout[(int64_t)t * k + lane] = (float)((double)pj / sum) * ds[my_id];
-    }
+    topk_wave(v, avail, k, rule, ds, ids + (int64_t)t * k, wout + (int64_t)t * k);
 }
 
 void launch_topk(hipStream_t st, int T, int E, int k, int rule, const float* logits, const float* ds, int* ids, float* w)

@@ -135,7 +135,23 @@ struct DecTile { int e, cnt, row[2]; };
 void launch_prologue(hipStream_t st, int T, int d, float eps, const float* x, const float* gate_inp_scale,
                      const float* pre2, const float* ffn_norm, float* router_in, float* xscale, Act act_gu,
                      Act act_sh, int* flags);
-void launch_router_exact(hipStream_t st, int T, int d, int E, const float* wt4, const float* router_in, float* logits);
+// the router kernels' top-k outputs (ids set: ids [T][k] and weights, written by the router itself when one
+// workgroup holds every expert, E <= 64; else ignored, k_topk runs)
+struct TopkOut {
+    int k = 0, rule = 0;
+    const float* ds = nullptr;
+    int* ids = nullptr;
+    float* w = nullptr;
+};
+// xscale set: the router forms m from the layer input x (router_in = x), the prologue's row scales and the
+// router input scale gis, where router_reads_x(T, d, E) (its many-token variant); otherwise router_in is m
+struct RouterX {
+    const float* xscale = nullptr;
+    const float* gis = nullptr;
+};
+bool router_reads_x(int T, int d, int E);
+void launch_router_exact(hipStream_t st, int T, int d, int E, const float* wt4, const float* router_in, float* logits,
+                         TopkOut to = TopkOut{}, RouterX rx = RouterX{});
 void launch_topk(hipStream_t st, int T, int E, int k, int rule, const float* logits, const float* down_scale,
                  int* ids, float* w);
 void launch_dispatch(hipStream_t st, int n_assign, int E, int A, const int* ids, int* offsets, int* perm,

@@ -781,16 +781,27 @@ int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, con
             launch_cert_select(st, h);
         }
     } else {
+        // the many-token router forms its input m from x and the row scales itself (no m rows written)
+        const bool rx = router_reads_x(T, d, E);
+        // the matrix-core products read only the fp16 copies of their inputs: no int8 rows or sums
+        Act pgu = agu, psh = ash;
+        if (mma || kmma) pgu.q = nullptr, pgu.s = nullptr;
+        if (smma) psh.q = nullptr, psh.s = nullptr;
         {
             ProfScope p(c, PHX_K_PROLOGUE);
-            launch_prologue(st, T, d, D.eps, x, L.gis, L.pre2, shared_ffn ? L.ffn_norm : nullptr, wp<float>(c, W_RIN),
-                            wp<float>(c, W_XSCALE), agu, ash, c->flags);
+            launch_prologue(st, T, d, D.eps, x, L.gis, L.pre2, shared_ffn ? L.ffn_norm : nullptr,
+                            rx ? nullptr : wp<float>(c, W_RIN), wp<float>(c, W_XSCALE), pgu, psh, c->flags);
         }
+        // up to 64 experts the router's waves hold all of a token's logits and take its top-k themselves
+        const bool fused_topk = E <= 64;
         {
             ProfScope p(c, PHX_K_ROUTER);
-            launch_router_exact(st, T, d, E, L.wt4, wp<float>(c, W_RIN), wp<float>(c, W_LOGITS));
+            TopkOut to;
+            if (fused_topk) to = TopkOut{k, D.weight_rule, L.ds, wp<int>(c, W_IDS), wp<float>(c, W_W)};
+            launch_router_exact(st, T, d, E, L.wt4, rx ? x : wp<float>(c, W_RIN), wp<float>(c, W_LOGITS), to,
+                                rx ? RouterX{wp<float>(c, W_XSCALE), L.gis} : RouterX{});
         }
-        {
+        if (!fused_topk) {
             ProfScope p(c, PHX_K_TOPK);
             launch_topk(st, T, E, k, D.weight_rule, wp<float>(c, W_LOGITS), L.ds, wp<int>(c, W_IDS), wp<float>(c, W_W));
         }
