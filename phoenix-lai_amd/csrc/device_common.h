@@ -15,7 +15,7 @@ namespace phx {
 // layer `seq` (modulo TL_SEQ); phxdbg_timeline copies the table to the host.  Without the macro the
 // stamps compile to nothing.
 #ifdef PHX_TIMELINE
-constexpr int TL_SEQ = 64, TL_KIND = 4, TL_SLOT = 8, TL_WG = 512;
+constexpr int TL_SEQ = 64, TL_KIND = 4, TL_SLOT = 12, TL_WG = 512;
 static __device__ unsigned long long phx_tl[TL_SEQ * TL_KIND * TL_SLOT * TL_WG];
 #define TL_STAMP(seq, kind, slot)                                                                   \
     do {                                                                                            \
@@ -23,8 +23,15 @@ static __device__ unsigned long long phx_tl[TL_SEQ * TL_KIND * TL_SLOT * TL_WG];
             phx_tl[((((seq) % TL_SEQ) * TL_KIND + (kind)) * TL_SLOT + (slot)) * TL_WG + blockIdx.x] = \
                 wall_clock64();                                                                     \
     } while (0)
+// the stamp once the wave's outstanding loads have landed (the wait itself only in the instrumented build)
+#define TL_STAMP_LANDED(seq, kind, slot)  \
+    do {                                  \
+        __builtin_amdgcn_s_waitcnt(0);    \
+        TL_STAMP(seq, kind, slot);        \
+    } while (0)
 #else
 #define TL_STAMP(seq, kind, slot) ((void)0)
+#define TL_STAMP_LANDED(seq, kind, slot) ((void)0)
 #endif
 
 // ------------------------------------------------------------------------------ scalar helpers

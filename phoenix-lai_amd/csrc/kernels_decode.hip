@@ -77,6 +77,7 @@ struct DecArgs {
     int rpw;              // k_dec_down: expert row groups per workgroup
     double* Lb;           // [T][E] certified logits (double sums)
     double* Bb;           // [T][E] their error bounds
+    uint4* kb;            // [T][E] selection keys: rank key, lower end, upper end, finite (route_wg)
     int* ids;             // [T][k]
     float* w;             // [T][k]
     float* logits;        // [T][E]
@@ -529,6 +530,32 @@ __device__ __forceinline__ void combine_into(const CombArgs& p, int t, float* sx
     __syncthreads();
 }
 
+__device__ __forceinline__ float f32_down(double v)  // the largest float <= v
+{
+    const float f = (float)v;
+    if (!((double)f > v)) return f;
+    if (f == 0.0f) return -__uint_as_float(1u);  // below zero: minus the smallest subnormal
+    const unsigned b = __float_as_uint(f);
+    return __uint_as_float(f > 0.0f ? b - 1u : b + 1u);
+}
+
+__device__ __forceinline__ float f32_up(double v)  // the smallest float >= v
+{
+    const float f = (float)v;
+    if (!((double)f < v)) return f;
+    if (f == 0.0f) return __uint_as_float(1u);
+    const unsigned b = __float_as_uint(f);
+    return __uint_as_float(f > 0.0f ? b + 1u : b - 1u);
+}
+
+// expert e's selection key and interval ends for the gate|up launch's ranking (see wave_topk)
+__device__ __forceinline__ uint4 sel_key(double L, double B, int e)
+{
+    const bool f = isfinite(L) && isfinite(B);
+    return make_uint4((sortable_f32((float)L) & ~0xFFu) | (unsigned)(255 - e), f ? sortable_f32(f32_down(L - B)) : 0u,
+                      f ? sortable_f32(f32_up(L + B)) : 0xFFFFFFFFu, f ? 1u : 0u);
+}
+
 // ------------------------------------------------------------------------------ k_dec_route
 // One workgroup of 256 threads per (token t, expert e); thread i holds the PER = d / 256 consecutive
 // elements PER*i..PER*i+PER-1 (x_t, the router scale and W[e] staged in LDS by direct global -> LDS
@@ -650,6 +677,7 @@ __device__ __forceinline__ void route_wg(const DecArgs& a, int t, int e, float* 
         wA[wave] = Af;
         wP[wave] = Pf;
     }
+    TL_STAMP(a.seq, 0, 4);
     // the expert and shared-FFN input blocks of this workgroup
     if (b < nb) {
         const float4 xq = *(const float4*)(sx + 32 * b + 4 * l8);
@@ -676,13 +704,16 @@ __device__ __forceinline__ void route_wg(const DecArgs& a, int t, int e, float* 
             }
         }
     }
+    TL_STAMP(a.seq, 0, 5);
     __syncthreads();
     if (tid == 0) {
         const double L = ((wsum[0] + wsum[1]) + wsum[2]) + wsum[3];
         const double As = (double)((wA[0] + wA[1]) + (wA[2] + wA[3])) * (1.0 + 0x1p-10);
         const double Ps = (double)((wP[0] + wP[1]) + (wP[2] + wP[3])) * (1.0 + 0x1p-10);
+        const double B = 0x1p-24 * As * 1.001 + 0x1p-45 * Ps;
         a.Lb[(int64_t)t * a.E + e] = L;
-        a.Bb[(int64_t)t * a.E + e] = 0x1p-24 * As * 1.001 + 0x1p-45 * Ps;
+        a.Bb[(int64_t)t * a.E + e] = B;
+        a.kb[(int64_t)t * a.E + e] = sel_key(L, B, e);
     }
     TL_STAMP(a.seq, 0, 3);
 }
@@ -769,74 +800,44 @@ __device__ void shared_dn_wg(const DecArgs& a, int tile, int rgi, unsigned char*
 // ------------------------------------------------------------------------------ k_dec_gu
 // Selection, in every expert workgroup and in the routing workgroup.  Fast path, one wave per token:
 // the experts' 32-bit keys (the order-preserving bits of (float)L with the low 8 bits replaced by
-// 255 - expert, so keys are distinct and ties go to the lower index) and k rounds of a wave maximum
-// give the top-k.  The order is certified if each chosen expert's lower end L - B lies above the
-// upper ends L + B of every expert ranked after it, compared as floats rounded outward (so a float
-// comparison that holds implies the exact one); an order the key gets wrong (logits within 256 float
-// ulps) is never certified, since certification compares the intervals themselves.  When a token is
-// not certified, the whole workgroup takes select_exact.
-__device__ __forceinline__ float f32_down(double v)  // the largest float <= v
-{
-    const float f = (float)v;
-    if (!((double)f > v)) return f;
-    if (f == 0.0f) return -__uint_as_float(1u);  // below zero: minus the smallest subnormal
-    const unsigned b = __float_as_uint(f);
-    return __uint_as_float(f > 0.0f ? b - 1u : b + 1u);
-}
-
-__device__ __forceinline__ float f32_up(double v)  // the smallest float >= v
-{
-    const float f = (float)v;
-    if (!((double)f < v)) return f;
-    if (f == 0.0f) return __uint_as_float(1u);
-    const unsigned b = __float_as_uint(f);
-    return __uint_as_float(f > 0.0f ? b + 1u : b - 1u);
-}
-
+// 255 - expert, so keys are distinct and ties go to the lower index) give the top-k.  The order is
+// certified if each chosen expert's lower end L - B lies above the upper ends L + B of every expert
+// ranked after it, compared as floats rounded outward (so a float comparison that holds implies the
+// exact one); an order the key gets wrong (logits within 256 float ulps) is never certified, since
+// certification compares the intervals themselves.  The router workgroup of (t, e) forms the key and
+// both ends once (sel_key).  When a token is not certified, the whole workgroup takes select_exact.
 // The router's logits and bounds of token t for one wave (lane + 64 q in slot q): cold reads (the router
 // launch wrote them), issued at workgroup start so they travel beside the shared units' weights.
 struct SelIn {
-    double L[4], B[4];
+    uint4 kb[4];
 };
 
 __device__ __forceinline__ void sel_issue(const DecArgs& a, int t, SelIn& in)
 {
     const int lane = threadIdx.x & 63;
-    const double* Lr = a.Lb + (int64_t)t * a.E;
-    const double* Br = a.Bb + (int64_t)t * a.E;
+    const uint4* kr = a.kb + (int64_t)t * a.E;
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
-        const int ex = min(lane + 64 * q, a.E - 1);
-        in.L[q] = Lr[ex];
-        in.B[q] = Br[ex];
-    }
+    for (int q = 0; q < 4; q++) in.kb[q] = kr[min(lane + 64 * q, a.E - 1)];
 }
 
+// The certified top-k of token t (one wave): k rounds of a wave maximum of the keys rank the experts;
+// the order is accepted if every chosen expert's lower end lies above every later expert's upper end
+// (ends rounded outward to floats); false when it cannot be (or a sum is not finite): the exact chains
+// decide then.
 __device__ bool wave_topk(const DecArgs& a, int t, const SelIn& in, int* s_ids, unsigned* s_klo, unsigned* s_khi)
 {
-    const int lane = threadIdx.x & 63;
-    double L[4], B[4];
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-        L[q] = in.L[q];
-        B[q] = in.B[q];
-    }
-    unsigned key[4], klo[4], khi[4];
+    const int lane = threadIdx.x & 63, nq = (a.E + 63) / 64, k = a.k;
+    unsigned key[4];
     int rank[4];
     bool fin = true;
 #pragma unroll
     for (int q = 0; q < 4; q++) {
-        const int ex = lane + 64 * q;
-        const bool valid = ex < a.E;
-        const bool f = isfinite(L[q]) && isfinite(B[q]);
-        if (valid && !f) fin = false;
-        key[q] = valid ? (sortable_f32((float)L[q]) & ~0xFFu) | (unsigned)(255 - ex) : 0u;
-        klo[q] = f ? sortable_f32(f32_down(L[q] - B[q])) : 0u;
-        khi[q] = f ? sortable_f32(f32_up(L[q] + B[q])) : 0xFFFFFFFFu;
+        const bool valid = q < nq && lane + 64 * q < a.E;
+        key[q] = valid ? in.kb[q].x : 0u;
+        if (valid && !in.kb[q].w) fin = false;
         rank[q] = 64;
     }
-    const int nq = (a.E + 63) / 64;
-    for (int j = 0; j < a.k; j++) {
+    for (int j = 0; j < k; j++) {
         unsigned m = key[0];
         if (nq > 1) m = max(m, key[1]);
         if (nq > 2) m = max(m, max(key[2], key[3]));
@@ -853,11 +854,11 @@ __device__ bool wave_topk(const DecArgs& a, int t, const SelIn& in, int* s_ids, 
     for (int q = 0; q < 4; q++) {
         const int ex = lane + 64 * q;
         if (rank[q] < 64) {
-            s_klo[rank[q]] = klo[q];
-            s_khi[rank[q]] = khi[q];
-            s_ids[t * a.k + rank[q]] = ex;
-        } else if (ex < a.E) {
-            hun = max(hun, khi[q]);
+            s_klo[rank[q]] = in.kb[q].y;
+            s_khi[rank[q]] = in.kb[q].z;
+            s_ids[t * k + rank[q]] = ex;
+        } else if (q < nq && ex < a.E) {
+            hun = max(hun, in.kb[q].z);
         }
     }
     hun = wave_max_u32(hun);
@@ -865,13 +866,15 @@ __device__ bool wave_topk(const DecArgs& a, int t, const SelIn& in, int* s_ids, 
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     // lane j < k: its lower end must lie above every later rank's upper end and the unchosen ones'
+    // (every read issued before the first use)
+    unsigned hk[PHX_MAX_USED_DEV];
+#pragma unroll
+    for (int r = 0; r < PHX_MAX_USED_DEV; r++) hk[r] = s_khi[r];
+    const unsigned lo = s_klo[min(lane, PHX_MAX_USED_DEV - 1)];
     unsigned later = hun;
 #pragma unroll
-    for (int r = 0; r < PHX_MAX_USED_DEV; r++) {
-        const unsigned h = s_khi[r];
-        if (r > lane && r < a.k) later = max(later, h);
-    }
-    const bool ok = lane >= a.k || s_klo[lane] > later;
+    for (int r = 0; r < PHX_MAX_USED_DEV; r++) later = (r > lane && r < k) ? max(later, hk[r]) : later;
+    const bool ok = lane >= k || lo > later;
     return __all(fin && ok);
 }
 
@@ -1211,6 +1214,7 @@ __global__ __launch_bounds__(CS_NT) void k_cert_select(DecArgs a)
     b.x = a.x + (int64_t)t * a.d;
     b.Lb = a.Lb + (int64_t)t * a.E;
     b.Bb = a.Bb + (int64_t)t * a.E;
+    b.kb = a.kb + (int64_t)t * a.E;
     if (wave == 0) {
         SelIn in;
         sel_issue(b, 0, in);
@@ -1284,6 +1288,7 @@ __device__ void gu_wg(const DecArgs& a, unsigned char* smem)
     if (pre) act_issue(ain, a.agu, 0, 0, 1, nb);
     if (tid == 0) s_misc[1] = 0;
     __syncthreads();
+    TL_STAMP_LANDED(a.seq, 1, 10);
     for (int t = wave; t < a.T; t += NWV) {
         if (!PRESEL || t != wave) sel_issue(a, t, sin);
         const bool cert = wave_topk(a, t, sin, s_ids, s_kb + wave * 32, s_kb + wave * 32 + 16);
@@ -1292,7 +1297,9 @@ __device__ void gu_wg(const DecArgs& a, unsigned char* smem)
             if (!cert) s_misc[1] = 1;
         }
     }
+    TL_STAMP(a.seq, 1, 8);
     __syncthreads();
+    TL_STAMP(a.seq, 1, 9);
     const bool exact = s_misc[1] != 0;
     double* sL = (double*)un;
     if (exact) select_exact(a, un, s_ids, s_misc + 2, red, routing);
@@ -1552,6 +1559,7 @@ static DecArgs dec_args(const DecLayerH& h)
     a.rpw = rpw_down(h);
     a.Lb = h.Lb;
     a.Bb = h.Bb;
+    a.kb = (uint4*)h.kb;
     a.ids = h.ids;
     a.w = h.w;
     a.logits = h.logits;

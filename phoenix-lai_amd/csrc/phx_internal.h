@@ -200,6 +200,7 @@ struct DecLayerH {
     const float *x, *W, *gis, *ds, *pre2, *post1, *post2, *fnorm, *post_ffw, *shared_in;
     const QMat *gu, *dn, *sgu, *sdn;  // sgu / sdn null: no shared FFN computed in the call
     double *Lb, *Bb;
+    uint32_t* kb;  // [T][E][4] selection keys of the certified router (see k_dec_route)
     int *ids, *offsets, *perm, *flags;
     float *w, *logits, *g, *u, *yd, *shg, *shu, *shout, *out, *xres;
     const float* xin = nullptr;  // the residual's source rows when not xres itself

@@ -414,7 +414,7 @@ enum WsId {
     W_X, W_SHARED, W_OUT, W_RIN, W_XSCALE, W_AGU_Q, W_AGU_D, W_AGU_S, W_ASH_Q, W_ASH_D, W_ASH_S, W_LOGITS, W_IDS, W_W,
     W_OFF, W_PERM, W_TILES, W_NTILES, W_G, W_U, W_ADN_Q, W_ADN_D, W_ADN_S, W_YD, W_SHG, W_SHU, W_ASD_Q, W_ASD_D,
     W_ASD_S, W_SHOUT, W_ZERO, W_STILES, W_SNTILES, W_SOFF, W_SPERM, W_LB, W_BB, W_ADEC, W_SDEC, W_AGUP, W_ASHP, W_AGU_H, W_ADN_H, W_ASH_H, W_ASD_H, W_X2,
-    W_MM_IDS, W_MM_OFF, W_MM_PERM, W_MM_TILES, W_MM_NT, W_MM_D, W_MM_S, W_MM_H, W_AGU_BH, W_ADN_BH, W_MK_Q, W_MK_BH,
+    W_MM_IDS, W_MM_OFF, W_MM_PERM, W_MM_TILES, W_MM_NT, W_MM_D, W_MM_S, W_MM_H, W_AGU_BH, W_ADN_BH, W_MK_Q, W_MK_BH, W_KB,
     W_COUNT
 };
 
@@ -523,6 +523,7 @@ int ensure_workspace(phx_moe_ctx* c, const Layer& L, int T)
     ENS(W_G, n * D.n_ff * 4);
     ENS(W_LB, (size_t)T * D.n_expert * 8);
     ENS(W_BB, (size_t)T * D.n_expert * 8);
+    ENS(W_KB, (size_t)T * D.n_expert * 16);
     ENS(W_U, n * D.n_ff * 4);
     ENS(W_YD, n * D.d * 4);
     if ((rc = ensure_act(c, act_fmt(D.gate_up_type), T, D.d, W_AGU_Q, W_AGU_D, W_AGU_S))) return rc;
@@ -666,6 +667,7 @@ DecLayerH dec_layer(phx_moe_ctx* c, const Layer& L, int T, const float* x, const
     if (c->ws.size() >= (size_t)W_COUNT && c->ws[W_LB].p) {
         h.Lb = wp<double>(c, W_LB);
         h.Bb = wp<double>(c, W_BB);
+        h.kb = wp<uint32_t>(c, W_KB);
         h.ids = wp<int>(c, W_IDS);
         h.offsets = wp<int>(c, W_OFF);
         h.perm = wp<int>(c, W_PERM);
