@@ -190,6 +190,7 @@ def run_layer(args, pkg):
     for r in range(wreps):
         ctx.stack_run_device(xbuf.ptr + (r % NX) * xstride, T)
     ctx.sync()
+    fb0 = ctx.fallback_counts()
     t0 = time.perf_counter()
     for r in range(reps):
         ctx.stack_run_device(xbuf.ptr + (r % NX) * xstride, T)
@@ -197,6 +198,9 @@ def run_layer(args, pkg):
         ctx.ffn_device(s, T, xbuf.ptr + ((reps + s) % NX) * xstride, None, obuf.ptr, RES_ASYNC)
     ctx.sync()
     dt = time.perf_counter() - t0
+    # tokens whose routing the certified router could not certify (their ambiguous experts' exact chains
+    # ran) in the timed steps
+    fb_tokens = ctx.fallback_counts()[1] - fb0[1]
     ms_per_step = dt * 1e3 / steps
     tokens_s = T * steps / dt
 
@@ -318,6 +322,7 @@ def run_layer(args, pkg):
             **down_rate,
             "kernels": kernels,
             "kernel_timing": f"{prof_steps} eager layer calls, each kernel's execution interval",
+            "router_fallback_token_frac": round(fb_tokens / (T * steps), 4),
             "stream_read_gbs_measured": round(stream_gbs, 1),
             "pcie_inclusive": pcie,
         },

@@ -722,38 +722,60 @@ __device__ __forceinline__ void route_wg(const DecArgs& a, int t, int e, float* 
 // clamped last loads land in the padding)
 __host__ __device__ inline int route_row_floats(int d) { return (d / 4 + RT_NT - 1) / RT_NT * RT_NT * 4; }
 
-template <bool FUSED>
-__device__ __forceinline__ void route_dispatch(const DecArgs& a, const CombArgs& prev, float* rsm)
+// one kernel per row width PER = d / RT_NT (each compiled with its own register budget; the host picks it)
+template <int PER, bool FUSED>
+__device__ __forceinline__ void route_at(const DecArgs& a, const CombArgs& prev, float* rsm)
 {
-    const int t = blockIdx.x / a.E, e = blockIdx.x % a.E, d = a.d, dp = route_row_floats(d);
+    const int t = blockIdx.x / a.E, e = blockIdx.x % a.E, dp = route_row_floats(a.d);
     float* sx = rsm;
     float* sg = sx + dp;
     float* sw = sg + dp;
     float* scb = sw + dp;  // fused: the combine's two rows
-#define RT_CASE(n) \
-    case n: route_wg<n, FUSED>(a, t, e, sx, sg, sw, prev, scb); break;
-    switch (d / RT_NT) {
-        RT_CASE(1) RT_CASE(2) RT_CASE(3) RT_CASE(4) RT_CASE(5) RT_CASE(6) RT_CASE(7) RT_CASE(8) RT_CASE(9)
-        RT_CASE(10) RT_CASE(11) RT_CASE(12) RT_CASE(13) RT_CASE(14) RT_CASE(15)
-    default: route_wg<16, FUSED>(a, t, e, sx, sg, sw, prev, scb); break;
-    }
-#undef RT_CASE
+    route_wg<PER, FUSED>(a, t, e, sx, sg, sw, prev, scb);
 }
 
+template <int PER>
 __global__ __launch_bounds__(RT_NT) void k_dec_route(DecArgs a)
 {
     extern __shared__ __align__(16) float rsm[];  // x, router scale, W row: route_row_floats(d) each
-    route_dispatch<false>(a, CombArgs{}, rsm);
+    route_at<PER, false>(a, CombArgs{}, rsm);
 }
 
 // A layer of a stack whose previous layer's combine is folded in: every (token, expert) workgroup forms
 // the token's x from the previous layer's outputs (combine_into, identical in every workgroup), the
 // expert-0 workgroup of each token also writes that layer's out and the new x, then the router as
 // k_dec_route.  One launch fewer per layer than route + combine.
+template <int PER>
 __global__ __launch_bounds__(RT_NT) void k_dec_route_fused(CombArgs prev, DecArgs a)
 {
     extern __shared__ __align__(16) float rsm[];  // x, router scale, W row, then the combine's two rows
-    route_dispatch<true>(a, prev, rsm);
+    route_at<PER, true>(a, prev, rsm);
+}
+
+template <int P> struct KRoute { static constexpr auto fn = k_dec_route<P>; };
+template <int P> struct KRouteF { static constexpr auto fn = k_dec_route_fused<P>; };
+// the instantiation for row width d (PER = d / RT_NT, 1..15; wider rows 16)
+template <template <int> class K>
+static auto route_kernel(int d)
+{
+    switch (d / RT_NT) {
+    case 1: return K<1>::fn;
+    case 2: return K<2>::fn;
+    case 3: return K<3>::fn;
+    case 4: return K<4>::fn;
+    case 5: return K<5>::fn;
+    case 6: return K<6>::fn;
+    case 7: return K<7>::fn;
+    case 8: return K<8>::fn;
+    case 9: return K<9>::fn;
+    case 10: return K<10>::fn;
+    case 11: return K<11>::fn;
+    case 12: return K<12>::fn;
+    case 13: return K<13>::fn;
+    case 14: return K<14>::fn;
+    case 15: return K<15>::fn;
+    default: return K<16>::fn;
+    }
 }
 
 // ------------------------------------------------------------------------------ shared FFN workgroups
@@ -1629,8 +1651,8 @@ template <int T> struct KDown { static constexpr auto fn = k_dec_down<T>; };
 
 void launch_dec_route(hipStream_t st, const DecLayerH& h)
 {
-    launch(k_dec_route, dim3(h.T * h.E), dim3(RT_NT), (uint32_t)((size_t)3 * route_row_floats(h.d) * 4), st,
-           dec_args(h));
+    launch(route_kernel<KRoute>(h.d), dim3(h.T * h.E), dim3(RT_NT), (uint32_t)((size_t)3 * route_row_floats(h.d) * 4),
+           st, dec_args(h));
 }
 
 void launch_cert_select(hipStream_t st, const DecLayerH& h)
@@ -1643,7 +1665,8 @@ void launch_cert_select(hipStream_t st, const DecLayerH& h)
 void launch_dec_route_fused(hipStream_t st, const DecLayerH& prev, const DecLayerH& h)
 {
     const size_t lds = ((size_t)3 * route_row_floats(h.d) + 2 * (h.d + 4)) * 4;
-    raise_lds(k_dec_route_fused, lds);
+    const auto kf = route_kernel<KRouteF>(h.d);
+    raise_lds(kf, lds);
     CombArgs cb;
     cb.d = prev.d;
     cb.k = prev.k;
@@ -1659,7 +1682,7 @@ void launch_dec_route_fused(hipStream_t st, const DecLayerH& prev, const DecLaye
     cb.out = prev.out;
     cb.xres = prev.xres;
     cb.flags = prev.flags;
-    launch(k_dec_route_fused, dim3(h.T * h.E), dim3(RT_NT), (uint32_t)lds, st, cb, dec_args(h));
+    launch(kf, dim3(h.T * h.E), dim3(RT_NT), (uint32_t)lds, st, cb, dec_args(h));
 }
 
 void launch_dec_gu(hipStream_t st, const DecLayerH& h)
