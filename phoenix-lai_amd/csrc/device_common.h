@@ -264,15 +264,27 @@ __device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v)
     return ((unsigned long long)hi << 32) | lo;
 }
 
-// Maximum over the 64 lanes of an unsigned 32-bit value, returned to every lane.
+// Maximum over the 64 lanes of an unsigned 32-bit value, returned to every lane: six in-place maxima
+// with a DPP operand (quad swaps, half mirror, mirror, then the row broadcasts into rows 1, 3 and
+// 2, 3); the compiler would copy the value through a separate DPP move at every step.  Each step reads
+// the previous step's result through DPP, two wait states after it is written.
 __device__ __forceinline__ unsigned wave_max_u32(unsigned v)
 {
-    v = max(v, (unsigned)dpp_i<0xb1>((int)v, (int)v));
-    v = max(v, (unsigned)dpp_i<0x4e>((int)v, (int)v));
-    v = max(v, (unsigned)dpp_i<0x141>((int)v, (int)v));
-    v = max(v, (unsigned)dpp_i<0x140>((int)v, (int)v));
-    v = max(v, (unsigned)dpp_i<0x142, 0xa>((int)v, (int)v));
-    v = max(v, (unsigned)dpp_i<0x143, 0xc>((int)v, (int)v));
+    asm volatile(
+        "s_nop 1\n\t"
+        "v_max_u32_dpp %0, %0, %0 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
+        "s_nop 1\n\t"
+        "v_max_u32_dpp %0, %0, %0 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf\n\t"
+        "s_nop 1\n\t"
+        "v_max_u32_dpp %0, %0, %0 row_half_mirror row_mask:0xf bank_mask:0xf\n\t"
+        "s_nop 1\n\t"
+        "v_max_u32_dpp %0, %0, %0 row_mirror row_mask:0xf bank_mask:0xf\n\t"
+        "s_nop 1\n\t"
+        "v_max_u32_dpp %0, %0, %0 row_bcast:15 row_mask:0xa bank_mask:0xf\n\t"
+        "s_nop 1\n\t"
+        "v_max_u32_dpp %0, %0, %0 row_bcast:31 row_mask:0xc bank_mask:0xf\n\t"
+        "s_nop 1"
+        : "+v"(v));
     return (unsigned)__builtin_amdgcn_readlane((int)v, 63);
 }
 

@@ -860,16 +860,24 @@ __device__ bool wave_topk(const DecArgs& a, int t, const SelIn& in, int* s_ids, 
         rank[q] = 64;
     }
     for (int j = 0; j < k; j++) {
-        unsigned m = key[0];
-        if (nq > 1) m = max(m, key[1]);
-        if (nq > 2) m = max(m, max(key[2], key[3]));
+        unsigned m = max(key[0], key[1]);  // key[1] is 0 where nq == 1
+        if (nq > 2) m = max(m, max(key[2], key[3]));  // uniform
         m = wave_max_u32(m);
+        // the keys are distinct and nonzero: one slot of one lane matches
 #pragma unroll
-        for (int q = 0; q < 4; q++)
-            if (key[q] == m) {  // the keys are distinct and nonzero: one slot of one lane
+        for (int q = 0; q < 2; q++)
+            if (key[q] == m) {
                 key[q] = 0u;
                 rank[q] = j;
             }
+        if (nq > 2) {
+#pragma unroll
+            for (int q = 2; q < 4; q++)
+                if (key[q] == m) {
+                    key[q] = 0u;
+                    rank[q] = j;
+                }
+        }
     }
     unsigned hun = 0u;  // the unchosen experts' highest upper end
 #pragma unroll
