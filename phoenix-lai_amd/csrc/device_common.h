@@ -23,6 +23,14 @@ static __device__ unsigned long long phx_tl[TL_SEQ * TL_KIND * TL_SLOT * TL_WG];
             phx_tl[((((seq) % TL_SEQ) * TL_KIND + (kind)) * TL_SLOT + (slot)) * TL_WG + blockIdx.x] = \
                 wall_clock64();                                                                     \
     } while (0)
+// the workgroup's compute unit instead of a time: XCC_ID << 16 | HW_ID bits 8-15 (CU, SH, SE)
+#define TL_HWID(seq, kind, slot)                                                                          \
+    do {                                                                                                  \
+        if (threadIdx.x == 0 && blockIdx.x < TL_WG)                                                       \
+            phx_tl[((((seq) % TL_SEQ) * TL_KIND + (kind)) * TL_SLOT + (slot)) * TL_WG + blockIdx.x] =       \
+                ((unsigned long long)(__builtin_amdgcn_s_getreg((31 << 11) | 20) & 0xF) << 16) |           \
+                ((__builtin_amdgcn_s_getreg((31 << 11) | 4) >> 8) & 0xFF) | (1ull << 62);                  \
+    } while (0)
 // the stamp once the wave's outstanding loads have landed (the wait itself only in the instrumented build)
 #define TL_STAMP_LANDED(seq, kind, slot)  \
     do {                                  \
@@ -32,6 +40,7 @@ static __device__ unsigned long long phx_tl[TL_SEQ * TL_KIND * TL_SLOT * TL_WG];
 #else
 #define TL_STAMP(seq, kind, slot) ((void)0)
 #define TL_STAMP_LANDED(seq, kind, slot) ((void)0)
+#define TL_HWID(seq, kind, slot) ((void)0)
 #endif
 
 // ------------------------------------------------------------------------------ scalar helpers

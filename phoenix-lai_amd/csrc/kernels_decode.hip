@@ -1302,6 +1302,7 @@ __device__ void gu_wg(const DecArgs& a, unsigned char* smem)
     const int total = nsh + a.max_tiles * a.gu.rg;
     int u = routing ? total : (int)blockIdx.x;
     TL_STAMP(a.seq, 1, 0);
+    TL_HWID(a.seq, 1, 11);
     // this wave's token's selection inputs (tokens past the waves load theirs at the selection)
     SelIn sin;
     if (PRESEL && wave < a.T) sel_issue(a, wave, sin);

@@ -7,7 +7,7 @@ layer and prints, per phase, the earliest / median / latest workgroup stamp.
       stored, 3: end), gate|up (0: start, 1: shared unit done, 10: the selection's inputs landed (the
       instrumented build waits for them there), 8: the wave's token ranked, 9: every
       token ranked, 2: selection done, 6: weight loads issued, 7: input in LDS, 3: after the barrier,
-      4: chain done, 5: end), down (0: start, 1: input in LDS, 2: chain done, 3: end) and the folded
+      4: chain done, 5: end, 11: the compute unit of each workgroup), down (0: start, 1: input in LDS, 2: chain done, 3: end) and the folded
       combine's phases
       (comb 4: loads in, 5: branch norms, 6: residual norm), µs from the layer's first router workgroup
   python3 phoenix-lai_amd/timeline.py prologue [CONFIG]   the general path's prologue phases (0: start,
@@ -43,15 +43,35 @@ def _reader(lib, name):
     return f
 
 
+HWID = 1 << 62  # entries holding a workgroup's compute unit (TL_HWID) instead of a time
+
+
 def _phases(tab, base, kinds, names):
     for k in kinds:
         for sl in range(TL_SLOT):
             v = tab[k, sl]
+            if (v & HWID).any():
+                _units(tab, k, sl, names[k])
+                continue
             v = v[v > 0]
             if v.size:
                 v = (v - base) / 100.0
                 print(f"   {names[k]:5s} slot {sl}: n={v.size:3d} min {v.min():7.2f} med {np.median(v):7.2f} "
                       f"max {v.max():7.2f}")
+
+
+def _units(tab, k, sl, name):
+    """Workgroups per compute unit from a TL_HWID slot, and the end stamps (slot 5) of those sharing one."""
+    ids = tab[k, sl]
+    wgs = np.nonzero(ids & HWID)[0]
+    cu = ids[wgs] & 0xFFFFF
+    uniq, cnt = np.unique(cu, return_counts=True)
+    shared = uniq[cnt > 1]
+    print(f"   {name:5s} units: {wgs.size} workgroups on {uniq.size} compute units, {shared.size} units with more "
+          f"than one")
+    for u in shared[:8]:
+        w = wgs[cu == u]
+        print(f"      unit {int(u):#07x}: workgroups {w.tolist()}")
 
 
 def decode(cfg="c2_decode", T=1, noshared=False, layers=8):
