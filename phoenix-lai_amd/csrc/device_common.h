@@ -229,18 +229,20 @@ __device__ __forceinline__ uint32_t bias_pair(uint32_t w, int p, float bias)
 // LDS activation layout); *dval and *sum (the block's q sum) are valid in all 8 lanes.
 __device__ __forceinline__ int q8_0_oct(float4 v, float* dval, int* sum)
 {
+    // the 8-lane maximum and sum by DPP (quad swaps, then the other quad through the half-row mirror);
+    // both are exact in any order
     float am = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-    am = fmaxf(am, __shfl_xor(am, 1, 64));
-    am = fmaxf(am, __shfl_xor(am, 2, 64));
-    am = fmaxf(am, __shfl_xor(am, 4, 64));
+    am = fmaxf(am, dpp_f<0xb1>(am, am));
+    am = fmaxf(am, dpp_f<0x4e>(am, am));
+    am = fmaxf(am, dpp_f<0x141>(am, am));
     const float dd = am / 127.0f;
     const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
     const int q0 = (int)roundf(v.x * id), q1 = (int)roundf(v.y * id), q2 = (int)roundf(v.z * id),
               q3 = (int)roundf(v.w * id);
     int sm = q0 + q1 + q2 + q3;
-    sm += __shfl_xor(sm, 1, 64);
-    sm += __shfl_xor(sm, 2, 64);
-    sm += __shfl_xor(sm, 4, 64);
+    sm += dpp_i<0xb1>(sm, sm);
+    sm += dpp_i<0x4e>(sm, sm);
+    sm += dpp_i<0x141>(sm, sm);
     *dval = h2f(f2h_bits(dd));
     *sum = sm;
     return (q0 & 0xFF) | ((q1 & 0xFF) << 8) | ((q2 & 0xFF) << 16) | (int)((unsigned)q3 << 24);
@@ -386,21 +388,32 @@ __device__ __forceinline__ void mean_ends(double S, double B, double rn, float* 
 // that interval give the same float the result is certain, otherwise one thread re-sums
 // sequentially (rare; counted in fallbacks[0]).  Block-level: NT threads, red >= NT/64 + 1 doubles.
 template <int NT>
+__device__ float mean_sq_cert_from(double s, int per, const float* x, int n, double* red, int* fallbacks);
+
+template <int NT>
 __device__ float mean_sq_cert(const float* x, int n, double* red, int* fallbacks)
 {
-    constexpr int NW = NT / 64;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x;
     double s = 0.0;
     for (int i = tid; i < n; i += NT) {
         double v = (double)x[i];
         s += v * v;
     }
+    return mean_sq_cert_from<NT>(s, (n + NT - 1) / NT, x, n, red, fallbacks);
+}
+
+// The same from each thread's own double sum s of at most `per` squares (any partition of the row):
+// the wave and workgroup sums, the bound and, if it cannot certify the rounding, the sequential sum.
+template <int NT>
+__device__ float mean_sq_cert_from(double s, int per, const float* x, int n, double* red, int* fallbacks)
+{
+    constexpr int NW = NT / 64;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     s = wave_sum_dpp(s);
     if (lane == 0) red[wave] = s;
     __syncthreads();
     double S = 0.0;
     for (int w = 0; w < NW; w++) S += red[w];
-    const int per = (n + NT - 1) / NT;
     const double B = ((double)n + per + 64.0) * 0x1p-53 * S * 2.0;
     float lo, hi;
     mean_ends(S, B, 1.0 / (double)n, &lo, &hi);

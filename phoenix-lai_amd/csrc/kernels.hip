@@ -22,8 +22,8 @@ __device__ __forceinline__ void store_q8k_block(const Act& act, int64_t row, int
     int sm = (int)(int8_t)(pk & 0xFF) + (int)(int8_t)((pk >> 8) & 0xFF) + (int)(int8_t)((pk >> 16) & 0xFF) +
              (int)(int8_t)(pk >> 24);
     // block sums of 16: lanes 4j .. 4j + 3
-    sm += __shfl_xor(sm, 1, 64);
-    sm += __shfl_xor(sm, 2, 64);
+    sm += dpp_i<0xb1>(sm, sm);  // 4-lane sum: quad swaps
+    sm += dpp_i<0x4e>(sm, sm);
     if ((lane & 3) == 0) {
         if (act.fmt == ACT_K4 && act.s) act.s[row * act.sstride + b * 16 + (lane >> 2)] = sm;
         if (act.bh) act.bh[row * act.bhstride + b * 16 + (lane >> 2)] = (uint16_t)f2h_bits((float)sm);  // exact
@@ -114,16 +114,26 @@ __device__ void quantize_row(const float* v, Act act, int64_t row)
                 vmax = x[j];
                 imax = 4 * lane + j;
             }
-#pragma unroll
-        for (int m = 1; m < 64; m <<= 1) {
-            const float oa = __shfl_xor(amax, m, 64), ov = __shfl_xor(vmax, m, 64);
-            const int oi = __shfl_xor(imax, m, 64);
+        // the wave's first largest |x| by DPP steps (lanes outside a step's rows keep their own triple),
+        // lane 63 ending with the result
+        auto step = [&](auto C, auto RM) {
+            constexpr int CTRL = decltype(C)::value, ROWMASK = decltype(RM)::value;
+            const float oa = dpp_f<CTRL, ROWMASK>(amax, amax), ov = dpp_f<CTRL, ROWMASK>(vmax, vmax);
+            const int oi = dpp_i<CTRL, ROWMASK>(imax, imax);
             if (oa > amax || (oa == amax && oi < imax)) {
                 amax = oa;
                 vmax = ov;
                 imax = oi;
             }
-        }
+        };
+        step(ic<0xb1>{}, ic<0xf>{});
+        step(ic<0x4e>{}, ic<0xf>{});
+        step(ic<0x141>{}, ic<0xf>{});
+        step(ic<0x140>{}, ic<0xf>{});
+        step(ic<0x142>{}, ic<0xa>{});
+        step(ic<0x143>{}, ic<0xc>{});
+        amax = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(amax), 63));
+        vmax = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(vmax), 63));
         const float iscale = amax == 0.0f ? 0.0f : -127.0f / vmax;
         int q[4];
 #pragma unroll
@@ -189,6 +199,80 @@ __global__ __launch_bounds__(NT) void k_prologue(int d, float eps, const float* 
     TL_STAMP(0, 0, 4);
 }
 
+// The same with the row held in registers (Q float4 per thread, rows up to 4 Q NT columns): x is read
+// from memory once, for the mean of squares and for every normed copy.
+template <int NT, int Q>
+__global__ __launch_bounds__(NT) void k_prologue_r(int d, float eps, const float* __restrict__ x,
+                                                   const float* __restrict__ gis, const float* __restrict__ pre2,
+                                                   const float* __restrict__ ffn_norm, float* __restrict__ router_in,
+                                                   float* __restrict__ xscale, Act act_gu, Act act_sh, int* flags)
+{
+    extern __shared__ __align__(16) float sbuf[];
+    __shared__ double red[NT / 64 + 1];
+    const int t = blockIdx.x, tid = threadIdx.x, n4 = d / 4;
+    TL_STAMP(0, 0, 0);
+    const float* xr = x + (int64_t)t * d;
+    const float4* x4 = (const float4*)xr;
+    const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float4 xv[Q], pv[Q];  // the row and the pre_ffw_norm_2 weights, both loaded at once
+#pragma unroll
+    for (int q = 0; q < Q; q++) {
+        const int i4 = tid + q * NT;
+        xv[q] = i4 < n4 ? x4[i4] : z4;
+        pv[q] = i4 < n4 ? ((const float4*)pre2)[i4] : z4;
+    }
+    double s2 = 0.0;  // this thread's squares (at most 4 Q of them), any order: the bound covers it
+#pragma unroll
+    for (int q = 0; q < Q; q++) {
+        s2 += (double)xv[q].x * (double)xv[q].x;
+        s2 += (double)xv[q].y * (double)xv[q].y;
+        s2 += (double)xv[q].z * (double)xv[q].z;
+        s2 += (double)xv[q].w * (double)xv[q].w;
+    }
+    const float scale = rms_scale_from_mean(mean_sq_cert_from<NT>(s2, 4 * Q, xr, d, red, flags), eps);
+    TL_STAMP(0, 0, 1);
+    const float sc = 1.0f / (float)__dsqrt_rn((double)d);
+    if (router_in) {  // uniform; null where the router forms m from x and the scale itself
+        float4* ri = (float4*)(router_in + (int64_t)t * d);
+#pragma unroll
+        for (int q = 0; q < Q; q++) {
+            const int i4 = tid + q * NT;
+            if (i4 < n4) {
+                const float4 xq = xv[q], gv = ((const float4*)gis)[i4];
+                ri[i4] = make_float4(xq.x * scale * sc * gv.x, xq.y * scale * sc * gv.y, xq.z * scale * sc * gv.z,
+                                     xq.w * scale * sc * gv.w);
+            }
+        }
+    }
+    auto fill = [&](const float* nw, int cols) {  // nw null: pre_ffw_norm_2 from registers
+#pragma unroll
+        for (int q = 0; q < Q; q++) {
+            const int i4 = tid + q * NT;
+            if (i4 < cols / 4) {
+                float4 v = z4;
+                if (i4 < n4) {
+                    const float4 xq = xv[q], nv = nw ? ((const float4*)nw)[i4] : pv[q];
+                    v = make_float4(xq.x * scale * nv.x, xq.y * scale * nv.y, xq.z * scale * nv.z, xq.w * scale * nv.w);
+                }
+                ((float4*)sbuf)[i4] = v;
+            }
+        }
+    };
+    fill(nullptr, act_gu.cols);
+    __syncthreads();
+    TL_STAMP(0, 0, 2);
+    quantize_row<NT>(sbuf, act_gu, t);
+    TL_STAMP(0, 0, 3);
+    if (ffn_norm) {
+        __syncthreads();
+        fill(ffn_norm, act_sh.cols);
+        __syncthreads();
+        quantize_row<NT>(sbuf, act_sh, t);
+    }
+    if (tid == 0) xscale[t] = scale;
+    TL_STAMP(0, 0, 4);
+}
+
 void launch_prologue(hipStream_t st, int T, int d, float eps, const float* x, const float* gis, const float* pre2,
                      const float* ffn_norm, float* router_in, float* xscale, Act act_gu, Act act_sh, int* flags)
 {
@@ -198,6 +282,26 @@ void launch_prologue(hipStream_t st, int T, int d, float eps, const float* x, co
     // super-blocks one per wave; measured faster at C4's 4096, slower at C3's 2816 where the launch is
     // bound by HBM with 256)
     const size_t lds = (size_t)cols * sizeof(float);
+#define PRO_R(NT, Q) \
+    launch(k_prologue_r<NT, Q>, dim3(T), dim3(NT), lds, st, d, eps, x, gis, pre2, ffn_norm, router_in, xscale, act_gu, \
+           act_sh, flags)
+    const int c4 = cols / 4;
+    if (c4 > 768) {
+        switch ((c4 + 1023) / 1024) {
+        case 1: PRO_R(1024, 1); return;
+        case 2: PRO_R(1024, 2); return;
+        case 3: PRO_R(1024, 3); return;
+        case 4: PRO_R(1024, 4); return;
+        default: break;  // wider rows: the kernel that reads them twice
+        }
+    } else {
+        switch ((c4 + 255) / 256) {
+        case 1: PRO_R(256, 1); return;
+        case 2: PRO_R(256, 2); return;
+        default: PRO_R(256, 3); return;
+        }
+    }
+#undef PRO_R
     if (cols / 4 > 768)
         launch(k_prologue<1024>, dim3(T), dim3(1024), lds, st, d, eps, x, gis, pre2, ffn_norm, router_in, xscale, act_gu,
                act_sh, flags);
@@ -1241,16 +1345,26 @@ __global__ __launch_bounds__(QZ_NT) void k_quant(int n, int ch, float eps, const
                 vmax = v[j];
                 imax = 4 * lane + j;
             }
-#pragma unroll
-        for (int m = 1; m < 64; m <<= 1) {
-            const float oa = __shfl_xor(amax, m, 64), ov = __shfl_xor(vmax, m, 64);
-            const int oi = __shfl_xor(imax, m, 64);
+        // the wave's first largest |x| by DPP steps (lanes outside a step's rows keep their own triple),
+        // lane 63 ending with the result
+        auto step = [&](auto C, auto RM) {
+            constexpr int CTRL = decltype(C)::value, ROWMASK = decltype(RM)::value;
+            const float oa = dpp_f<CTRL, ROWMASK>(amax, amax), ov = dpp_f<CTRL, ROWMASK>(vmax, vmax);
+            const int oi = dpp_i<CTRL, ROWMASK>(imax, imax);
             if (oa > amax || (oa == amax && oi < imax)) {
                 amax = oa;
                 vmax = ov;
                 imax = oi;
             }
-        }
+        };
+        step(ic<0xb1>{}, ic<0xf>{});
+        step(ic<0x4e>{}, ic<0xf>{});
+        step(ic<0x141>{}, ic<0xf>{});
+        step(ic<0x140>{}, ic<0xf>{});
+        step(ic<0x142>{}, ic<0xa>{});
+        step(ic<0x143>{}, ic<0xc>{});
+        amax = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(amax), 63));
+        vmax = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(vmax), 63));
         const float iscale = amax == 0.0f ? 0.0f : -127.0f / vmax;
         int q[4], sm = 0;
 #pragma unroll
@@ -1260,8 +1374,8 @@ __global__ __launch_bounds__(QZ_NT) void k_quant(int n, int ch, float eps, const
         }
         *(int*)(qs + row * n + b * 256 + 4 * lane) =
             (q[0] & 0xFF) | ((q[1] & 0xFF) << 8) | ((q[2] & 0xFF) << 16) | (int)((unsigned)q[3] << 24);
-        sm += __shfl_xor(sm, 1, 64);
-        sm += __shfl_xor(sm, 2, 64);
+        sm += dpp_i<0xb1>(sm, sm);  // 4-lane sum: quad swaps
+        sm += dpp_i<0x4e>(sm, sm);
         if (bsums && (lane & 3) == 0) bsums[row * (n / 16) + b * 16 + (lane >> 2)] = (int16_t)sm;
         if (lane == 0) dk[row * (n / 256) + b] = amax == 0.0f ? 0.0f : 1.0f / iscale;
     }
@@ -1550,9 +1664,9 @@ __global__ __launch_bounds__(256) void k_planar_act(int64_t nblk, int nb, const 
     const int q0 = (int8_t)(w & 0xFF), q1 = (int8_t)((w >> 8) & 0xFF), q2 = (int8_t)((w >> 16) & 0xFF),
               q3 = (int8_t)(w >> 24);
     int sm = q0 + q1 + q2 + q3;
-    sm += __shfl_xor(sm, 1, 64);
-    sm += __shfl_xor(sm, 2, 64);
-    sm += __shfl_xor(sm, 4, 64);
+    sm += dpp_i<0xb1>(sm, sm);  // 8-lane sum: quad swaps, then the other quad (half-row mirror)
+    sm += dpp_i<0x4e>(sm, sm);
+    sm += dpp_i<0x141>(sm, sm);
     if (!ok) return;
     const int64_t t = g / nb;
     const int b = (int)(g - t * nb);
