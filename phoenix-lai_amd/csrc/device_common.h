@@ -334,6 +334,18 @@ __device__ __forceinline__ double wave_max_dpp(double v)
     return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
 }
 
+// Inclusive prefix sum of an int over the 64 lanes (the same steps as the double one below).
+__device__ __forceinline__ int wave_incl_scan_i(int v)
+{
+    v += dpp_i<0x111>(0, v);  // row_shr:1
+    v += dpp_i<0x112>(0, v);  // row_shr:2
+    v += dpp_i<0x114>(0, v);  // row_shr:4
+    v += dpp_i<0x118>(0, v);  // row_shr:8
+    v += dpp_i<0x142, 0xa>(0, v);  // row_bcast:15 into rows 1 and 3
+    v += dpp_i<0x143, 0xc>(0, v);  // row_bcast:31 into rows 2 and 3
+    return v;
+}
+
 // Inclusive prefix sum over the 64 lanes (row shifts within 16-lane rows, then row broadcasts).
 __device__ __forceinline__ double wave_incl_scan_dpp(double v)
 {

@@ -768,15 +768,7 @@ __global__ __launch_bounds__(DSP_NT) void k_dispatch(int n, int E, int A, const 
         tcount = (c + A - 1) / A;
     }
     // exclusive scans of c and tcount over the experts (E <= 256: threads 0-255)
-    int v1 = c, v2 = tcount;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const int y1 = __shfl_up(v1, o, 64), y2 = __shfl_up(v2, o, 64);
-        if (lane >= o) {
-            v1 += y1;
-            v2 += y2;
-        }
-    }
+    const int v1 = wave_incl_scan_i(c), v2 = wave_incl_scan_i(tcount);
     if (lane == 63) {
         wsum[0][wave] = v1;
         wsum[1][wave] = v2;
@@ -808,12 +800,7 @@ __global__ __launch_bounds__(DSP_NT) void k_dispatch(int n, int E, int A, const 
         int inc[5];
 #pragma unroll
         for (int q = 0; q < 5; q++) {
-            int x = v[q];
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) {
-                const int y = __shfl_up(x, o, 64);
-                if (lane >= o) x += y;
-            }
+            const int x = wave_incl_scan_i(v[q]);
             inc[q] = x;
             if (lane == 63) tsum[q][wave] = x;
         }

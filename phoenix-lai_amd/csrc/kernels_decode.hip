@@ -1150,15 +1150,7 @@ __device__ void build_tiles(const DecArgs& a, const int* s_ids, int* s_cnt, int*
     {
         const int c = tid < a.E ? s_cnt[tid] : 0;
         const int tcount = (c + DROWS - 1) / DROWS;
-        int v1 = c, v2 = tcount;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int y1 = __shfl_up(v1, o, 64), y2 = __shfl_up(v2, o, 64);
-            if (lane >= o) {
-                v1 += y1;
-                v2 += y2;
-            }
-        }
+        const int v1 = wave_incl_scan_i(c), v2 = wave_incl_scan_i(tcount);
         if (lane == 63) {
             wtot[wave] = v1;
             wtot[16 + wave] = v2;
@@ -1214,12 +1206,13 @@ __device__ void write_routing(const DecArgs& a, LF Lr, const int* s_ids, const i
         const bool act = j < a.k;
         const int id = act ? s_ids[tt * a.k + j] : 0;
         const float selj = act ? (float)Lr(tt, id) : 0.0f;
-        const float sel0 = __shfl(selj, 0, 64);
+        const float sel0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(selj), 0));
         // p_0 = exp(0) = 1 exactly, so the CPU's in-place rule uses 1 for every later term
         const float top = (a.rule == 1 && j > 0) ? 1.0f : sel0;
         const float pj = act ? (float)exp((double)(selj - top)) : 0.0f;
         double sum = 0.0;
-        for (int q = 0; q < a.k; q++) sum += (double)__shfl(pj, q, 64);  // in rank order
+        for (int q = 0; q < a.k; q++)  // in rank order
+            sum += (double)__int_as_float(__builtin_amdgcn_readlane(__float_as_int(pj), q));
         if (act) {
             a.ids[(int64_t)tt * a.k + j] = id;
             a.w[(int64_t)tt * a.k + j] = (float)((double)pj / sum) * a.ds[id];
@@ -1261,11 +1254,12 @@ __global__ __launch_bounds__(CS_NT) void k_cert_select(DecArgs a)
         const bool act = j < a.k;
         const int id = act ? s_ids[j] : 0;
         const float selj = act ? (float)(exact ? sL[id] : b.Lb[id]) : 0.0f;
-        const float sel0 = __shfl(selj, 0, 64);
+        const float sel0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(selj), 0));
         const float top = (a.rule == 1 && j > 0) ? 1.0f : sel0;
         const float pj = act ? (float)exp((double)(selj - top)) : 0.0f;
         double sum = 0.0;
-        for (int q = 0; q < a.k; q++) sum += (double)__shfl(pj, q, 64);  // in rank order
+        for (int q = 0; q < a.k; q++)  // in rank order
+            sum += (double)__int_as_float(__builtin_amdgcn_readlane(__float_as_int(pj), q));
         if (act) {
             a.ids[(int64_t)t * a.k + j] = id;
             a.w[(int64_t)t * a.k + j] = (float)((double)pj / sum) * a.ds[id];
