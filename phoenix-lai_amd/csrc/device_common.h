@@ -367,21 +367,6 @@ __device__ __forceinline__ unsigned sortable_f32(float f)
     return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
-// sum over the 64 lanes of a wave (butterfly: every lane ends with the same value)
-__device__ __forceinline__ double wave_sum_d(double v)
-{
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
-
-__device__ __forceinline__ double wave_max_d(double v)
-{
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmax(v, __shfl_xor(v, o, 64));
-    return v;
-}
-
 // The two float ends of (S -/+ B) / n, the interval of means a certified sum of squares S (error bound
 // B, S >= 0) allows, formed with the reciprocal rn = 1 / n instead of a double division: the bound is
 // widened by S * 2^-49, above the relative error of rn and of the product (under 2^-51), so the ends
