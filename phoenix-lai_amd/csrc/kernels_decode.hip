@@ -118,7 +118,9 @@ __device__ __forceinline__ int q8_0_half(float x, float* dval, int* sum)
 // summing n non-negative terms is within (n + 64) * 2^-52 * sum of the sequential sum (the summation
 // depth here is far below 64); when both ends of that interval give the same float the result is the
 // reference's, otherwise thread 0 re-sums sequentially (rare; counted in *fallbacks when non-null).
-// Workgroup-level: every thread calls it; red holds blockDim.x / 64 + 1 doubles.
+// Workgroup-level: every thread calls it; red holds blockDim.x / 64 + 1 doubles.  TRAIL: a closing
+// barrier, for callers that reuse red right after.
+template <bool TRAIL = true>
 __device__ float wg_mean_sq(double s, const float* xr, int n, double* red, int* fallbacks)
 {
     const int tid = threadIdx.x, lane = tid & 63, nw = blockDim.x >> 6;
@@ -140,12 +142,13 @@ __device__ float wg_mean_sq(double s, const float* xr, int n, double* red, int* 
         __syncthreads();
         mean = (float)(red[nw] / (double)n);
     }
-    __syncthreads();  // red is reused by the next call
+    if (TRAIL) __syncthreads();  // red is reused by the next call
     return mean;
 }
 
 // The means of squares of two rows in one reduction pass, each by the rule of wg_mean_sq (x1 may be
 // null when s1 is zero everywhere).  red holds 2 * (blockDim.x / 64 + 1) doubles.
+template <bool TRAIL = true>
 __device__ void wg_mean_sq2(double s0, double s1, const float* x0, const float* x1, int n, double* red,
                             int* fallbacks, float* m0, float* m1)
 {
@@ -186,7 +189,7 @@ __device__ void wg_mean_sq2(double s0, double s1, const float* x0, const float* 
     }
     *m0 = lo0;
     *m1 = lo1;
-    __syncthreads();  // red is reused by the next call
+    if (TRAIL) __syncthreads();  // red is reused by the next call
 }
 
 // The Q8_0 input rows of a gate|up workgroup: n_i = (x_i * rinv) * nw_i (src/GemmaCpu.cs:409 with
@@ -417,8 +420,10 @@ __device__ __forceinline__ void gu_epilogue(float S, int rgi, int split, int64_t
 // term rounded then added), out = rmsnorm(shared) * post1 + rmsnorm(acc) * post2 (src/GemmaCpu.cs:384,
 // 420-421), x_new = x + rmsnorm(out) * post_ffw_norm (src/GemmaCpu.cs:355-356), the same expressions
 // as k_dec_combine.  Every load is issued in one round into registers (the caller's occupancy is set
-// by its LDS, so the registers are free); x_new lands in sx (LDS, [d]); with leader, out and x_new
-// also go to p.out and p.xres (x read from p.xin).  sacc and so: LDS [d] each.
+// by its LDS, so the registers are free); x_new lands in sx (LDS, [d]) and this thread's float4s of it
+// in xkeep; with leader, out and x_new also go to p.out and p.xres (x read from p.xin).  sacc and so:
+// LDS [d] each; red: 3 * (blockDim.x / 64 + 1) doubles.  No barrier after the last pass: the caller's
+// next barrier publishes sx.
 // What the combine of a layer reads and writes (a small kernel argument of the fused router)
 struct CombArgs {
     int d, k, seq;
@@ -430,7 +435,7 @@ struct CombArgs {
 
 template <int CQ, class F>
 __device__ __forceinline__ void combine_into(const CombArgs& p, int t, float* sx, float* sacc, float* so, double* red,
-                                             bool leader, F&& after_issue)
+                                             bool leader, F&& after_issue, float4* xkeep)
 {
     constexpr int RG = CQ <= 3 ? 8 : 4;  // ranks per load round (register budget)
     const int tid = threadIdx.x, NT = blockDim.x, d = p.d, k = p.k, n4 = d / 4;
@@ -490,9 +495,10 @@ __device__ __forceinline__ void combine_into(const CombArgs& p, int t, float* sx
             s1 += (double)shv[q].x * (double)shv[q].x + (double)shv[q].y * (double)shv[q].y;
             s1 += (double)shv[q].z * (double)shv[q].z + (double)shv[q].w * (double)shv[q].w;
         }
-    __syncthreads();
+    // (the reductions' own barriers publish sacc and so to their sequential fallbacks; the two use
+    // separate parts of red, so neither needs a closing barrier)
     float m2, m1;
-    wg_mean_sq2(s2, s1, sacc, sh4 ? (const float*)sh4 : nullptr, d, red, leader ? p.flags : nullptr, &m2, &m1);
+    wg_mean_sq2<false>(s2, s1, sacc, sh4 ? (const float*)sh4 : nullptr, d, red, leader ? p.flags : nullptr, &m2, &m1);
     const float sc2 = rms_scale_from_mean(m2, p.eps);
     const float sc1 = sh4 ? rms_scale_from_mean(m1, p.eps) : 0.0f;
     TL_STAMP(p.seq, 3, 5);
@@ -513,8 +519,8 @@ __device__ __forceinline__ void combine_into(const CombArgs& p, int t, float* sx
             s3 += (double)ov[q].z * (double)ov[q].z + (double)ov[q].w * (double)ov[q].w;
         }
     }
-    __syncthreads();
-    const float sc3 = rms_scale_from_mean(wg_mean_sq(s3, so, d, red, leader ? p.flags : nullptr), p.eps);
+    const float sc3 =
+        rms_scale_from_mean(wg_mean_sq<false>(s3, so, d, red + 2 * (NT / 64 + 1), leader ? p.flags : nullptr), p.eps);
     TL_STAMP(p.seq, 3, 6);
     // pass 3: x_new = x + rmsnorm(out) * post_ffw_norm
 #pragma unroll
@@ -522,12 +528,12 @@ __device__ __forceinline__ void combine_into(const CombArgs& p, int t, float* sx
         const int i4 = tid + q * NT;
         const float4 xn = make_float4(xv[q].x + ov[q].x * sc3 * pf[q].x, xv[q].y + ov[q].y * sc3 * pf[q].y,
                                       xv[q].z + ov[q].z * sc3 * pf[q].z, xv[q].w + ov[q].w * sc3 * pf[q].w);
+        xkeep[q] = xn;
         if (i4 < n4) {
             ((float4*)sx)[i4] = xn;
             if (leader) ((float4*)(p.xres + (int64_t)t * d))[i4] = xn;
         }
     }
-    __syncthreads();
 }
 
 __device__ __forceinline__ float f32_down(double v)  // the largest float <= v
@@ -557,9 +563,10 @@ __device__ __forceinline__ uint4 sel_key(double L, double B, int e)
 }
 
 // ------------------------------------------------------------------------------ k_dec_route
-// One workgroup of 256 threads per (token t, expert e); thread i holds the PER = d / 256 consecutive
-// elements PER*i..PER*i+PER-1 (x_t, the router scale and W[e] staged in LDS by direct global -> LDS
-// loads; an odd PER reads LDS without bank conflicts).  The reference logit is the sequential float sum
+// One workgroup of d / 4 threads per (token t, expert e) (d % 256 == 0, d <= 4096: whole waves, at most
+// 16); thread i holds the four consecutive elements 4i..4i+3 (x_t, the router scale and W[e] staged in
+// LDS by one direct global -> LDS load per thread and row).  Many short per-thread chains rather than
+// four waves of long ones: a SIMD with one wave issues an instruction only every ~8.7 cycles.  The reference logit is the sequential float sum
 // of the rounded products p_i = fl(W[e][i] * m_i), m_i = ((x_i * rinv) * sc) * s_i
 // (src/GemmaCpu.cs:389-395).  The workgroup forms the same p_i, sums them in double (L, from a scan of
 // the chunk sums), and bounds the reference's accumulated rounding by
@@ -569,7 +576,8 @@ __device__ __forceinline__ uint4 sel_key(double L, double B, int e)
 // certifies the order from these intervals.  The workgroup also writes the Q8_0 expert input
 // n = (x * rinv) * pre_ffw_norm_2 (src/GemmaCpu.cs:409) and the shared-FFN input (x * rinv) * ffn_norm
 // (:349) of the 32-blocks b with b % E == e, one 8-lane group per block.
-constexpr int RT_NT = 256;
+constexpr int RT_PER = 4, RT_MAXW = 16;  // elements per thread, waves per workgroup at most
+__host__ __device__ inline int route_threads(int d) { return d / RT_PER; }
 
 // the matrix-core kernels' copy of a Q8_0 activation dword (four integers as exact fp16, signed bytes
 // through the 1152 bias), for the general path's rows when it routes through this kernel
@@ -584,55 +592,60 @@ template <int PER, bool FUSED>
 __device__ __forceinline__ void route_wg(const DecArgs& a, int t, int e, float* sx, float* sg, float* sw,
                                          const CombArgs& prev, float* scb)
 {
-    __shared__ double red[5], wsum[4], red5[2 * (RT_NT / 64 + 1)];
-    __shared__ float wA[4], wP[4];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, d = a.d;
+    static_assert(!FUSED || PER == 4, "the folded combine hands over one float4 of x per thread");
+    __shared__ double red[RT_MAXW + 1], wsum[RT_MAXW], red5[3 * (RT_MAXW + 1)];
+    __shared__ float wA[RT_MAXW], wP[RT_MAXW];
+    const int tid = threadIdx.x, NT = blockDim.x, lane = tid & 63, wave = tid >> 6, nw = NT >> 6, d = a.d;
     TL_STAMP(a.seq, 0, 0);
-    const float* xr = a.x + (int64_t)t * d;
-    // the input blocks of this workgroup (8 threads per block): their norm weights, loaded now
-    const int nb = d / 32, g = tid >> 3, l8 = tid & 7, b = e + g * a.E, bc = min(b, nb - 1);
+    // the input blocks b = e + g E of this workgroup, 8 threads per block counted from the last thread (the
+    // last wave, while wave 0 forms the sum, bound and key): their norm weights, loaded now
+    const int nb = d / 32, g = (NT - 1 - tid) >> 3, l8 = tid & 7, b = e + g * a.E, bc = min(b, nb - 1);
     const float4 nv = ((const float4*)a.pre2)[8 * bc + l8];
     const float4 fv = a.ash.q ? ((const float4*)a.fnorm)[8 * bc + l8] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    {
+    // rows staged into LDS by direct loads, one float4 per thread and round (every lane issues every load,
+    // the last ones clamped to the row's end and landing in the padding of the LDS row)
+    auto stage = [&](const float* src, float* dst) {
         const int n4 = d / 4;
-        // every lane issues every load (the last ones clamped to the row's end, landing in the padding of
-        // the LDS row), so no branch makes the compiler's wait counts conservative
-        auto stage = [&](const float* src, float* dst) {
-            for (int q = 0; q * RT_NT < n4; q++) {
-                const int i = min(q * RT_NT + tid, n4 - 1);
-                __builtin_amdgcn_global_load_lds((glb_void_t)((const float4*)src + i),
-                                                 (lds_void_t)((float4*)dst + q * RT_NT + wave * 64), 16, 0, 0);
-            }
-        };
-        if (FUSED) {
-            // this token's x is the previous layer's combine, formed here (scb: its two LDS rows); its loads
-            // go out first, the router scale and W row behind them
-            combine_into<(PER + 3) / 4>(prev, t, sx, scb, scb + d, red5, e == 0, [&] {
-                stage(a.gis, sg);
-                stage(a.W + (int64_t)e * d, sw);
-            });
-        } else {
-            stage(xr, sx);
+        for (int q = 0; q * NT < n4; q++) {
+            const int i = min(q * NT + tid, n4 - 1);
+            __builtin_amdgcn_global_load_lds((glb_void_t)((const float4*)src + i),
+                                             (lds_void_t)((float4*)dst + q * NT + wave * 64), 16, 0, 0);
+        }
+    };
+    const int c0 = tid * PER;
+    float xv[PER];
+    double s2 = 0.0;
+    if constexpr (FUSED) {
+        // this token's x is the previous layer's combine, formed here (scb: its two LDS rows; x_new in sx
+        // and in this thread's registers); its loads go out first, the router scale and W row behind them
+        float4 xk;
+        combine_into<1>(prev, t, sx, scb, scb + d, red5, e == 0, [&] {
             stage(a.gis, sg);
             stage(a.W + (int64_t)e * d, sw);
-        }
+        }, &xk);
+        xv[0] = xk.x;
+        xv[1] = xk.y;
+        xv[2] = xk.z;
+        xv[3] = xk.w;
+    } else {
+        stage(a.x + (int64_t)t * d, sx);
+        stage(a.gis, sg);
+        stage(a.W + (int64_t)e * d, sw);
         __builtin_amdgcn_s_waitcnt(0);
-    }
-    __syncthreads();
-    TL_STAMP(a.seq, 0, 1);
-    const int c0 = tid * PER;
-    float xv[PER], pv[PER];
-    double s2 = 0.0;
+        __syncthreads();
 #pragma unroll
-    for (int j = 0; j < PER; j++) {
-        xv[j] = sx[c0 + j];
-        s2 += (double)xv[j] * (double)xv[j];
+        for (int j = 0; j < PER; j++) xv[j] = sx[c0 + j];
     }
-    // the RmsNorm scale: wave sums, then the four wave totals in a fixed order
+    // the RmsNorm scale: wave sums, then the wave totals in a fixed tree order (folded: the one barrier
+    // also publishes the staged router scale and W row)
+#pragma unroll
+    for (int j = 0; j < PER; j++) s2 += (double)xv[j] * (double)xv[j];
     s2 = wave_sum_dpp(s2);
     if (lane == 0) red[wave] = s2;
+    if constexpr (FUSED) __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    const double S = (red[0] + red[1]) + (red[2] + red[3]);
+    TL_STAMP(a.seq, 0, 1);
+    const double S = wave_sum_dpp(lane < nw ? red[lane] : 0.0);
     const double Bs = ((double)d + 64.0) * 0x1p-52 * S;
     float mean, mhi;
     mean_ends(S, Bs, 1.0 / (double)d, &mean, &mhi);
@@ -640,15 +653,16 @@ __device__ __forceinline__ void route_wg(const DecArgs& a, int t, int e, float* 
         if (tid == 0) {
             double q = 0.0;
             for (int i = 0; i < d; i++) q += (double)sx[i] * (double)sx[i];
-            red[4] = q;
+            red[RT_MAXW] = q;
             if (e == 0) atomicAdd(&a.flags[0], 1);
         }
         __syncthreads();
-        mean = (float)(red[4] / (double)d);
+        mean = (float)(red[RT_MAXW] / (double)d);
     }
     const float rinv = rms_scale_from_mean(mean, a.eps);
     TL_STAMP(a.seq, 0, 2);
     const float sc = 1.0f / (float)__dsqrt_rn((double)d);
+    float pv[PER];
     double loc = 0.0;
     float Pf = 0.0f;
 #pragma unroll
@@ -660,11 +674,8 @@ __device__ __forceinline__ void route_wg(const DecArgs& a, int t, int e, float* 
     const double inc = wave_incl_scan_dpp(loc);
     if (lane == 63) wsum[wave] = inc;
     __syncthreads();
-    double base = 0.0;
-    if (wave > 0) base += wsum[0];
-    if (wave > 1) base += wsum[1];
-    if (wave > 2) base += wsum[2];
-    double acc = base + (inc - loc);  // exclusive prefix (within the double slack of the bound)
+    // exclusive prefix (within the double slack of the bound): the earlier waves' totals, then this wave's
+    double acc = wave_sum_dpp(lane < wave ? wsum[lane] : 0.0) + (inc - loc);
     float Af = 0.0f;
 #pragma unroll
     for (int j = 0; j < PER; j++) {
@@ -678,8 +689,23 @@ __device__ __forceinline__ void route_wg(const DecArgs& a, int t, int e, float* 
         wP[wave] = Pf;
     }
     TL_STAMP(a.seq, 0, 4);
-    // the expert and shared-FFN input blocks of this workgroup
-    if (b < nb) {
+    __syncthreads();
+    TL_STAMP(a.seq, 0, 5);
+    // wave 0: the sum, bound and selection key; beside it, the input blocks
+    if (wave == 0) {
+        const double L = wave_sum_dpp(lane < nw ? wsum[lane] : 0.0);
+        const float Aw = wave_sum_f(lane < nw ? wA[lane] : 0.0f);
+        const float Pw = wave_sum_f(lane < nw ? wP[lane] : 0.0f);
+        if (lane == 0) {
+            const double As = (double)Aw * (1.0 + 0x1p-10);
+            const double Ps = (double)Pw * (1.0 + 0x1p-10);
+            const double B = 0x1p-24 * As * 1.001 + 0x1p-45 * Ps;
+            a.Lb[(int64_t)t * a.E + e] = L;
+            a.Bb[(int64_t)t * a.E + e] = B;
+            a.kb[(int64_t)t * a.E + e] = sel_key(L, B, e);
+        }
+    }
+    if (b < nb) {  // 8-lane groups: whole groups take a block or none
         const float4 xq = *(const float4*)(sx + 32 * b + 4 * l8);
         float dval;
         int sum;
@@ -704,29 +730,17 @@ __device__ __forceinline__ void route_wg(const DecArgs& a, int t, int e, float* 
             }
         }
     }
-    TL_STAMP(a.seq, 0, 5);
-    __syncthreads();
-    if (tid == 0) {
-        const double L = ((wsum[0] + wsum[1]) + wsum[2]) + wsum[3];
-        const double As = (double)((wA[0] + wA[1]) + (wA[2] + wA[3])) * (1.0 + 0x1p-10);
-        const double Ps = (double)((wP[0] + wP[1]) + (wP[2] + wP[3])) * (1.0 + 0x1p-10);
-        const double B = 0x1p-24 * As * 1.001 + 0x1p-45 * Ps;
-        a.Lb[(int64_t)t * a.E + e] = L;
-        a.Bb[(int64_t)t * a.E + e] = B;
-        a.kb[(int64_t)t * a.E + e] = sel_key(L, B, e);
-    }
     TL_STAMP(a.seq, 0, 3);
 }
 
-// floats of one staged router row in LDS: d rounded up to whole rounds of RT_NT float4 (the staging's
-// clamped last loads land in the padding)
-__host__ __device__ inline int route_row_floats(int d) { return (d / 4 + RT_NT - 1) / RT_NT * RT_NT * 4; }
+// floats of one staged router row in LDS: d rounded up to whole rounds of blockDim.x float4 (the
+// staging's clamped last loads land in the padding)
+__host__ __device__ inline int route_row_floats(int d, int nt) { return (d / 4 + nt - 1) / nt * nt * 4; }
 
-// one kernel per row width PER = d / RT_NT (each compiled with its own register budget; the host picks it)
 template <int PER, bool FUSED>
 __device__ __forceinline__ void route_at(const DecArgs& a, const CombArgs& prev, float* rsm)
 {
-    const int t = blockIdx.x / a.E, e = blockIdx.x % a.E, dp = route_row_floats(a.d);
+    const int t = blockIdx.x / a.E, e = blockIdx.x % a.E, dp = route_row_floats(a.d, blockDim.x);
     float* sx = rsm;
     float* sg = sx + dp;
     float* sw = sg + dp;
@@ -735,9 +749,9 @@ __device__ __forceinline__ void route_at(const DecArgs& a, const CombArgs& prev,
 }
 
 template <int PER>
-__global__ __launch_bounds__(RT_NT) void k_dec_route(DecArgs a)
+__global__ __launch_bounds__(64 * RT_MAXW) void k_dec_route(DecArgs a)
 {
-    extern __shared__ __align__(16) float rsm[];  // x, router scale, W row: route_row_floats(d) each
+    extern __shared__ __align__(16) float rsm[];  // x, router scale, W row: route_row_floats(d, NT) each
     route_at<PER, false>(a, CombArgs{}, rsm);
 }
 
@@ -745,36 +759,36 @@ __global__ __launch_bounds__(RT_NT) void k_dec_route(DecArgs a)
 // the token's x from the previous layer's outputs (combine_into, identical in every workgroup), the
 // expert-0 workgroup of each token also writes that layer's out and the new x, then the router as
 // k_dec_route.  One launch fewer per layer than route + combine.
-template <int PER>
-__global__ __launch_bounds__(RT_NT) void k_dec_route_fused(CombArgs prev, DecArgs a)
+__global__ __launch_bounds__(64 * RT_MAXW) void k_dec_route_fused(CombArgs prev, DecArgs a)
 {
     extern __shared__ __align__(16) float rsm[];  // x, router scale, W row, then the combine's two rows
-    route_at<PER, true>(a, prev, rsm);
+    route_at<4, true>(a, prev, rsm);
 }
 
+// Elements per thread: 4 (d / 4 threads) for a stack's few tokens, where the router's chain of
+// reductions is the layer's latency; d / 256 (256 threads) for many tokens, where more workgroups per CU
+// hide each other's barriers.  Each width is its own instantiation (its own register budget).
 template <int P> struct KRoute { static constexpr auto fn = k_dec_route<P>; };
-template <int P> struct KRouteF { static constexpr auto fn = k_dec_route_fused<P>; };
-// the instantiation for row width d (PER = d / RT_NT, 1..15; wider rows 16)
-template <template <int> class K>
-static auto route_kernel(int d)
+static int route_per(int T, int E, int d) { return (int64_t)T * E > 1024 ? d / 256 : 4; }
+static auto route_kernel(int per)
 {
-    switch (d / RT_NT) {
-    case 1: return K<1>::fn;
-    case 2: return K<2>::fn;
-    case 3: return K<3>::fn;
-    case 4: return K<4>::fn;
-    case 5: return K<5>::fn;
-    case 6: return K<6>::fn;
-    case 7: return K<7>::fn;
-    case 8: return K<8>::fn;
-    case 9: return K<9>::fn;
-    case 10: return K<10>::fn;
-    case 11: return K<11>::fn;
-    case 12: return K<12>::fn;
-    case 13: return K<13>::fn;
-    case 14: return K<14>::fn;
-    case 15: return K<15>::fn;
-    default: return K<16>::fn;
+    switch (per) {
+    case 1: return KRoute<1>::fn;
+    case 2: return KRoute<2>::fn;
+    case 3: return KRoute<3>::fn;
+    case 4: return KRoute<4>::fn;
+    case 5: return KRoute<5>::fn;
+    case 6: return KRoute<6>::fn;
+    case 7: return KRoute<7>::fn;
+    case 8: return KRoute<8>::fn;
+    case 9: return KRoute<9>::fn;
+    case 10: return KRoute<10>::fn;
+    case 11: return KRoute<11>::fn;
+    case 12: return KRoute<12>::fn;
+    case 13: return KRoute<13>::fn;
+    case 14: return KRoute<14>::fn;
+    case 15: return KRoute<15>::fn;
+    default: return KRoute<16>::fn;
     }
 }
 
@@ -1654,8 +1668,11 @@ template <int T> struct KDown { static constexpr auto fn = k_dec_down<T>; };
 
 void launch_dec_route(hipStream_t st, const DecLayerH& h)
 {
-    launch(route_kernel<KRoute>(h.d), dim3(h.T * h.E), dim3(RT_NT), (uint32_t)((size_t)3 * route_row_floats(h.d) * 4),
-           st, dec_args(h));
+    const int per = route_per(h.T, h.E, h.d), nt = h.d / per;
+    const size_t lds = (size_t)3 * route_row_floats(h.d, nt) * 4;
+    const auto kr = route_kernel(per);
+    raise_lds(kr, lds);
+    launch(kr, dim3(h.T * h.E), dim3(nt), (uint32_t)lds, st, dec_args(h));
 }
 
 void launch_cert_select(hipStream_t st, const DecLayerH& h)
@@ -1667,8 +1684,8 @@ void launch_cert_select(hipStream_t st, const DecLayerH& h)
 
 void launch_dec_route_fused(hipStream_t st, const DecLayerH& prev, const DecLayerH& h)
 {
-    const size_t lds = ((size_t)3 * route_row_floats(h.d) + 2 * (h.d + 4)) * 4;
-    const auto kf = route_kernel<KRouteF>(h.d);
+    const size_t lds = ((size_t)3 * route_row_floats(h.d, route_threads(h.d)) + 2 * (h.d + 4)) * 4;
+    const auto kf = k_dec_route_fused;
     raise_lds(kf, lds);
     CombArgs cb;
     cb.d = prev.d;
@@ -1685,7 +1702,7 @@ void launch_dec_route_fused(hipStream_t st, const DecLayerH& prev, const DecLaye
     cb.out = prev.out;
     cb.xres = prev.xres;
     cb.flags = prev.flags;
-    launch(kf, dim3(h.T * h.E), dim3(RT_NT), (uint32_t)lds, st, cb, dec_args(h));
+    launch(kf, dim3(h.T * h.E), dim3(route_threads(h.d)), (uint32_t)lds, st, cb, dec_args(h));
 }
 
 void launch_dec_gu(hipStream_t st, const DecLayerH& h)
