@@ -47,7 +47,7 @@ METRIC = "MoE layer tokens/s; decode HBM GB/s vs peak; prefill MFMA util"
 # (config, T, kernel); re-measured whenever that kernel changes.
 PMC_TRAFFIC = {
     # FETCH_SIZE 12,377.4 KiB x 2.000 + WRITE_SIZE 86.6 KiB x 1.000 per launch of phx::k_dec_gu<2>
-    ("c2_decode", 1, "gate_up"): (25_416_909, "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, 392 launches each"),
+    ("c2_decode", 1, "gate_up"): (25_432_268, "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, 392 launches each"),
 }
 
 
