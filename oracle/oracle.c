@@ -587,6 +587,15 @@ void orc_router(const orc_layer* L, const float* x, float* logits, int32_t* ids,
 
 static int64_t exp_rows_bytes(int type, int rows, int cols) { return (int64_t)rows * orc_row_bytes(type, cols); }
 
+/* GemmaCpu.cs:410 clears _moeAcc; :417-418 add each expert's down output times its weight, rank by rank:
+ * _moeAcc[i] += _ed[i] * we for j = 0..k-1. */
+void orc_combine(int k, int d, const float* yd, const float* w, float* acc)
+{
+    for (int i = 0; i < d; i++) acc[i] = 0;
+    for (int j = 0; j < k; j++)
+        for (int i = 0; i < d; i++) acc[i] += yd[(int64_t)j * d + i] * w[j];
+}
+
 /* GemmaCpu.MoeFfn (GemmaCpu.cs:376-422) for one token. */
 void orc_moe_token(const orc_layer* L, const float* x, const float* shared, float* out, int32_t* ids,
                    float* wout, float* gdbg, float* udbg, float* yddbg, int nthreads)
@@ -595,10 +604,10 @@ void orc_moe_token(const orc_layer* L, const float* x, const float* shared, floa
     float* mlp = (float*)calloc((size_t)d, sizeof(float));
     float* logits = (float*)malloc(sizeof(float) * L->n_expert);
     float* moe_in = (float*)malloc(sizeof(float) * d);
-    float* acc = (float*)calloc((size_t)d, sizeof(float));
+    float* acc = (float*)malloc(sizeof(float) * d);
     float* gu = (float*)malloc(sizeof(float) * 2 * nf);
     float* eg = (float*)calloc((size_t)dc, sizeof(float));
-    float* ed = (float*)malloc(sizeof(float) * d);
+    float* ed = (float*)malloc(sizeof(float) * (size_t)k * d);   /* every rank's down output */
     float* acc2 = (float*)malloc(sizeof(float) * d);
     float w[64];
     int32_t id[64];
@@ -612,12 +621,12 @@ void orc_moe_token(const orc_layer* L, const float* x, const float* shared, floa
         int e = id[j];
         orc_matvec(L->gate_up_type, L->gate_up_exps + (int64_t)e * gu_bytes, 2 * nf, d, moe_in, gu, nthreads);
         for (int i = 0; i < nf; i++) eg[i] = orc_gelu(gu[i]) * gu[nf + i];
-        orc_matvec(L->down_type, L->down_exps + (int64_t)e * dn_bytes, d, dc, eg, ed, nthreads);
-        for (int i = 0; i < d; i++) acc[i] += ed[i] * w[j];
+        orc_matvec(L->down_type, L->down_exps + (int64_t)e * dn_bytes, d, dc, eg, ed + (int64_t)j * d, nthreads);
         if (gdbg) memcpy(gdbg + (int64_t)j * nf, gu, sizeof(float) * nf);
         if (udbg) memcpy(udbg + (int64_t)j * nf, gu + nf, sizeof(float) * nf);
-        if (yddbg) memcpy(yddbg + (int64_t)j * d, ed, sizeof(float) * d);
     }
+    if (yddbg) memcpy(yddbg, ed, sizeof(float) * (size_t)k * d);
+    orc_combine(k, d, ed, w, acc);                                    /* GemmaCpu.cs:417-418 */
     orc_rmsnorm(acc, d, L->post_ffw_norm_2, L->eps, acc2);           /* GemmaCpu.cs:420 */
     for (int i = 0; i < d; i++) out[i] = mlp[i] + acc2[i];            /* GemmaCpu.cs:421 */
     if (ids) memcpy(ids, id, sizeof(int32_t) * k);

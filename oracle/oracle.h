@@ -90,6 +90,10 @@ typedef struct orc_layer {
  * combine weight including ffn_down_exps.scale */
 void orc_router(const orc_layer* L, const float* x, float* logits, int32_t* ids, float* w);
 
+/* the weighted combine of one token (GemmaCpu.cs:410, 417-418): acc = 0, then for ranks j = 0..k-1 in
+ * order acc[i] += yd[j][i] * w[j] (float products and sums).  yd [k][d], w [k], acc [d]. */
+void orc_combine(int k, int d, const float* yd, const float* w, float* acc);
+
 /* routed experts of one token (GemmaCpu.cs:376-422): out = rmsnorm(shared)*post1 +
  * rmsnorm(sum_j w_j down_e(gelu(gate_e(n)) * up_e(n)))*post2, n = rmsnorm(x)*pre2.  Debug outputs
  * (nullable): g/u [k][nf] are the expert gate/up products, yd [k][d] the expert down products. */

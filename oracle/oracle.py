@@ -80,6 +80,7 @@ def lib():
         L.orc_rms_scale.argtypes = [vp, i32, f32]
         L.orc_rms_scale.restype = f32
         L.orc_router.argtypes = [C.POINTER(OrcLayer), vp, vp, vp, vp]
+        L.orc_combine.argtypes = [i32, i32, vp, vp, vp]
         L.orc_moe_token.argtypes = [C.POINTER(OrcLayer), vp, vp, vp, vp, vp, vp, vp, vp, i32]
         L.orc_shared_ffn_token.argtypes = [C.POINTER(OrcLayer), vp, vp, i32]
         L.orc_moe_block.argtypes = [C.POINTER(OrcLayer), i32, vp, vp, vp, vp, vp, i32]
@@ -205,6 +206,15 @@ def router(Ld, x):
     w = np.empty(Ld["n_used"], np.float32)
     lib().orc_router(C.byref(s), x.ctypes.data, logits.ctypes.data, ids.ctypes.data, w.ctypes.data)
     return logits, ids, w
+
+
+def combine(yd, w):
+    """acc[d] = sum over ranks j = 0..k-1, in order, of yd[j] * w[j] (GemmaCpu.cs:417-418)."""
+    yd, w = f32(yd), f32(w)
+    k, d = yd.shape
+    acc = np.empty(d, np.float32)
+    lib().orc_combine(k, d, yd.ctypes.data, w.ctypes.data, acc.ctypes.data)
+    return acc
 
 
 def moe_token(Ld, x, shared=None, nthreads=0):

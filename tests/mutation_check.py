@@ -2,7 +2,8 @@
 
 Each mutation plants one plausible mistake into a copy of oracle/oracle.c, builds it into a temporary
 library with the oracle's own flags, and runs the pin tests (tests/test_oracle_numerics.py,
-test_oracle_layer.py, test_oracle_chain_order.py) against it through PHX_ORACLE_LIB.  A mutation that
+test_oracle_layer.py, test_oracle_chain_order.py, test_oracle_iq.py, test_oracle_rounding_order.py)
+against it through PHX_ORACLE_LIB.  A mutation that
 every pin test passes means the pins miss that mistake; the script reports it and exits nonzero.  The
 golden fixtures are left out on purpose: they were written by the oracle, so they would flag every
 change without pinning anything.
@@ -18,7 +19,7 @@ from pathlib import Path
 ROOT = Path(__file__).resolve().parent.parent
 ORACLE = ROOT / "oracle"
 PINS = ["tests/test_oracle_numerics.py", "tests/test_oracle_layer.py", "tests/test_oracle_chain_order.py",
-        "tests/test_oracle_iq.py"]
+        "tests/test_oracle_iq.py", "tests/test_oracle_rounding_order.py"]
 CFLAGS = ["-O2", "-std=c11", "-fPIC", "-ffp-contract=off", "-fno-fast-math", "-fexcess-precision=standard",
           "-fopenmp", "-shared"]
 
@@ -70,6 +71,22 @@ MUTATIONS = {
                            ("sumf -= dm * (float)sumi;", "summin += dm * (float)sumi;"),
                            ("for (int l = 0; l < 8; l++) sumf += sums[l];\n    return sumf;",
                             "for (int l = 0; l < 8; l++) sumf += sums[l];\n    sumf -= summin;\n    return sumf;")],
+    # single-step roundings
+    "router input (x * (rinv * sc)) * s": [("in[i] = x[i] * rinv * sc * L->gate_inp_scale[i];",
+                                            "in[i] = x[i] * (rinv * sc) * L->gate_inp_scale[i];")],
+    "router input x * rinv * (sc * s)": [("in[i] = x[i] * rinv * sc * L->gate_inp_scale[i];",
+                                          "in[i] = x[i] * rinv * (sc * L->gate_inp_scale[i]);")],
+    "router mean left in double": [("float rinv = 1.0f / (float)sqrt((double)((float)(ss / d) + L->eps));",
+                                    "float rinv = 1.0f / (float)sqrt(ss / d + L->eps);")],
+    "rmsnorm x * (scale * w)": [("y[i] = x[i] * scale * w[i];", "y[i] = x[i] * (scale * w[i]);")],
+    "rmsnorm (x * w) * scale": [("y[i] = x[i] * scale * w[i];", "y[i] = x[i] * w[i] * scale;")],
+    "rmsnorm mean left in double": [("    float mean = (float)(sum / n);\n    return 1.0f / (float)sqrt((double)(mean + eps));",
+                                     "    double mean = sum / n;\n    return 1.0f / (float)sqrt(mean + eps);")],
+    "combine ranks summed k-1..0": [("    for (int j = 0; j < k; j++)\n        for (int i = 0; i < d; i++) acc[i] +=",
+                                     "    for (int j = k - 1; j >= 0; j--)\n        for (int i = 0; i < d; i++) acc[i] +=")],
+    "weight cast after the down scale": [("w[j] = (float)(sel[j] / sum) * L->down_scale[ids[j]];",
+                                          "w[j] = (float)(sel[j] / sum * L->down_scale[ids[j]]);")],
+    "q8_0 id = 127 / amax": [("float id = d != 0 ? 1.0f / d : 0.0f;", "float id = amax != 0 ? 127.0f / amax : 0.0f;")],
     # IQ formats
     "iq2_xxs super-blocks reversed": [("    for (int i = 0; i < nb; i++) {\n        const uint8_t* blk = row + (int64_t)i * 66;",
                                        "    for (int i = nb - 1; i >= 0; i--) {\n        const uint8_t* blk = row + (int64_t)i * 66;")],
