@@ -13,9 +13,14 @@ Prints one JSON line: value = tokens/s through the layer (inputs resident in HBM
 object for the dominant kernel (the grouped gate|up product: algorithmic bytes per launch over its
 average duration, each launch's execution interval stamped by HIP events on the library's stream,
 the interval a kernel-trace profiler reports), the CPU baseline (the C restatement of the reference
-CPU path timed on this host's cores over a bounded sample), and a `prefill` object for configs[2]
-(T=2048, Zipf routing) measured in the same run: tokens/s and the matrix-core utilisation of the
-grouped gate|up and down products.
+CPU path timed on this host's cores over a bounded sample), and three objects measured in the same
+run: `prefill` for configs[2] (T=2048, Zipf routing: tokens/s and the matrix-core utilisation of the
+grouped gate|up and down products), `kquant` for configs[3] (T=512, Q4_K gate|up and Q6_K down:
+tokens/s, weight GB/s and matrix-core rates) and `stack` for configs[4] (30 Q8_0 layers at T=32 with a
+hot expert, captured as one HIP graph: the step's latency and GB/s over the distinct experts read).
+
+Kernel durations come from a fixed sample of eager layer calls (--prof-steps, 200 by default, after 20
+unprofiled calls), independent of --steps, each launch's execution interval stamped by HIP events.
 
 `--config quant` measures the ops either side of the layer instead (the activation quantizers, the
 residual norm-add with the quantized next input and the dense matvec): one JSON line of the same form
@@ -205,8 +210,11 @@ def run_layer(args, pkg):
     tokens_s = T * steps / dt
 
     # ---- per-kernel durations: eager layer calls over the slots and inputs, every launch stamped with
-    # its own execution interval (hipExtLaunchKernel events on the library's stream)
-    prof_steps = max(1, min(steps, args.prof_steps))
+    # its own execution interval (hipExtLaunchKernel events on the library's stream); a fixed sample after
+    # unprofiled warm-up calls, whatever --steps is
+    prof_steps = max(1, args.prof_steps)
+    for s in range(20):
+        ctx.ffn_device(s % n_slots, T, xbuf.ptr + (s % NX) * xstride, None, obuf.ptr, RES_ASYNC)
 
     def prof_calls():
         for s in range(prof_steps):
@@ -321,7 +329,8 @@ def run_layer(args, pkg):
             "down_avg_us": round(dn_ms * 1e3, 3),
             **down_rate,
             "kernels": kernels,
-            "kernel_timing": f"{prof_steps} eager layer calls, each kernel's execution interval",
+            "kernel_timing": f"{prof_steps} eager layer calls after 20 unprofiled ones, each kernel's execution "
+                             f"interval",
             "router_fallback_token_frac": round(fb_tokens / (T * steps), 4),
             "stream_read_gbs_measured": round(stream_gbs, 1),
             "pcie_inclusive": pcie,
@@ -337,12 +346,19 @@ def run_layer(args, pkg):
     if cfg_name == "c2_decode" and not args.no_prefill:
         log("[bench] prefill (configs[2], T=2048) ...")
         line["prefill"] = run_prefill(args, pkg)
+    if cfg_name == "c2_decode" and not args.no_kquant:
+        log("[bench] K-quant layer (configs[3], T=512) ...")
+        line["kquant"] = run_prefill(args, pkg, "c4_kquant", args.kquant_steps)
+    if cfg_name == "c2_decode" and not args.no_stack:
+        log("[bench] 30-layer stack (configs[4], T=32) ...")
+        line["stack"] = run_stack(args, pkg)
     return line
 
 
-def run_prefill(args, pkg, cfg_name="c3_prefill"):
-    """configs[2] in the same run: T = 2048 tokens with Zipf(1.1) expert popularity through one layer,
-    eager (one call per step, inputs resident in HBM), the grouped products on the matrix cores."""
+def run_prefill(args, pkg, cfg_name="c3_prefill", steps=None):
+    """A many-token config in the same run, one eager layer call per step (inputs resident in HBM), the
+    grouped products on the matrix cores: configs[2] (T = 2048 tokens with Zipf(1.1) expert popularity,
+    Q4_0) or configs[3] (T = 512, Q4_K gate|up and Q6_K down, uniform router)."""
     S = pkg.synth
     cfg = S.CONFIGS[cfg_name]
     T = cfg["T"]
@@ -351,12 +367,13 @@ def run_prefill(args, pkg, cfg_name="c3_prefill"):
     ctx.upload(0, L)
     NX = 4
     xs = S.normal(cfg["idx"] + 7000, "bench.x", (NX, T, L["d"]))
-    xs[:, :, -1] = S.BIAS_X
+    if L.get("biased"):
+        xs[:, :, -1] = S.BIAS_X
     xbuf = ctx.alloc(xs.nbytes)
     xbuf.upload(xs)
     obuf = ctx.alloc(T * L["d"] * 4)
     xstride = T * L["d"] * 4
-    steps = args.prefill_steps
+    steps = steps or args.prefill_steps
     for s in range(3):
         ctx.ffn_device(0, T, xbuf.ptr + (s % NX) * xstride, None, obuf.ptr, pkg.PHX.FLAG_ASYNC)
     ctx.sync()
@@ -374,16 +391,106 @@ def run_prefill(args, pkg, cfg_name="c3_prefill"):
     ids = ctx.routing()[0]
     cnt = np.bincount(ids.ravel(), minlength=L["n_expert"])
     ctx.close()
+    gu_b, dn_b = expert_bytes(L)
+    touched = int((cnt > 0).sum())
+    gu_ms, dn_ms = prof["gate_up"][0], prof["down"][0]
+    layer_s = dt / steps
     out = {"workload": f"{cfg_name}: T={T}, d={L['d']}, E={L['n_expert']}, top-{L['n_used']}, expert ffn {L['n_ff']}, "
-                       f"Q4_0, Zipf(1.1) router bias; {steps} eager layer calls, inputs in HBM",
+                       f"{qname(L['gate_up_type'])}/{qname(L['down_type'])}"
+                       + (", Zipf(1.1) router bias" if cfg.get("zipf") else ", uniform router")
+                       + (f" (down K padded {L['n_ff']} -> {L['down_cols']})" if L["down_cols"] != L["n_ff"] else "")
+                       + f"; {steps} eager layer calls, inputs in HBM",
            "tokens_s": round(T * steps / dt, 1), "ms_per_step": round(dt * 1e3 / steps, 4), "steps": steps,
-           **mfma_rates(L, T, prof["gate_up"][0], prof["down"][0]),
+           **mfma_rates(L, T, gu_ms, dn_ms),
+           "hbm": {"expert_bytes_per_step": touched * (gu_b + dn_b),
+                   "layer_gbs": round(touched * (gu_b + dn_b) / layer_s / 1e9, 1),
+                   "gate_up_gbs": round(touched * gu_b / (gu_ms * 1e-3) / 1e9, 1),
+                   "gate_up_frac": round(touched * gu_b / (gu_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                   "down_gbs": round(touched * dn_b / (dn_ms * 1e-3) / 1e9, 1),
+                   "floor_us": round(touched * (gu_b + dn_b) / (HBM_PEAK_GBS * 1e9) * 1e6, 1),
+                   "note": "unpadded GGUF bytes of the experts with at least one assignment"},
            "kernels": {k_: {"avg_us": round(v[0] * 1e3, 2), "launches": v[1]} for k_, v in prof.items()},
            "kernel_timing": f"{steps} eager layer calls, each kernel's execution interval",
            "assignments_per_expert": {"max": int(cnt.max()), "empty_experts": int((cnt == 0).sum())}}
     if not args.no_cpu:
-        log("[bench] prefill CPU baseline ...")
-        out["cpu_baseline"] = cpu_baseline(pkg, L, cfg_name, min(args.cpu_seconds, 6.0))
+        log(f"[bench] {cfg_name} CPU baseline ...")
+        out["cpu_baseline"] = cpu_baseline(pkg, L, cfg_name, min(args.cpu_seconds, 6.0 if cfg_name == "c3_prefill" else 3.0))
+    return out
+
+
+def run_stack(args, pkg, cfg_name="c5_stack"):
+    """configs[4] in the same run: 30 consecutive Q8_0 MoE layers, each with its RmsNorm and residual
+    (GemmaCpu.cs:355-356), over T = 32 independent tokens with one hot expert, captured as ONE HIP graph
+    of the 30-layer step and replayed (inputs resident in HBM, x varied per replay).  Layers have their own
+    routers and norms; the expert weights are one generated set uploaded into 30 distinct device copies
+    (synth.make_stack), so every step reads 30 layers' experts from HBM."""
+    S = pkg.synth
+    cfg = S.CONFIGS[cfg_name]
+    T, n_layers = cfg["T"], cfg["layers"]
+    layers = S.make_stack(cfg_name, n_layers)
+    ctx = pkg.MoeContext(0)
+    for i, L in enumerate(layers):
+        ctx.upload(i, L)
+    L0 = layers[0]
+    d = L0["d"]
+    NX = 8
+    xs = S.normal(cfg["idx"] + 7000, "bench.x", (NX, T, d))
+    xs[:, :, -1] = S.BIAS_X
+    xbuf = ctx.alloc(xs.nbytes)
+    xbuf.upload(xs)
+    xstride = T * d * 4
+    ctx.stack_capture(0, n_layers, T)
+    for r in range(3):
+        ctx.stack_run_device(xbuf.ptr + (r % NX) * xstride, T)
+    ctx.sync()
+    xbuf.upload(xs)
+    steps = args.stack_steps
+    fb0 = ctx.fallback_counts()
+    t0 = time.perf_counter()
+    for r in range(steps):
+        ctx.stack_run_device(xbuf.ptr + (r % NX) * xstride, T)
+    ctx.sync()
+    dt = time.perf_counter() - t0
+    fb_tokens = ctx.fallback_counts()[1] - fb0[1]
+    # one step replayed layer by layer (the same calls the graph holds) for the experts each layer touches
+    # and the per-kernel durations
+    xbuf.upload(xs)
+    obuf = ctx.alloc(T * d * 4)
+    res = pkg.PHX.FLAG_RESIDUAL | pkg.PHX.FLAG_ASYNC
+    touched = []
+    for i in range(n_layers):
+        ctx.ffn_device(i, T, xbuf.ptr, None, obuf.ptr, res)
+        touched.append(len(np.unique(ctx.routing()[0])))
+
+    def calls():
+        for r in range(2):
+            for i in range(n_layers):
+                ctx.ffn_device(i, T, xbuf.ptr + (r % NX) * xstride, None, obuf.ptr, res)
+
+    prof = kernel_times(ctx, calls)
+    ctx.close()
+    gu_b, dn_b = expert_bytes(L0)
+    step_bytes = sum(touched) * (gu_b + dn_b)
+    step_s = dt / steps
+    out = {"workload": f"{cfg_name}: {n_layers} MoE layers (RmsNorm + residual each), T={T}, d={d}, "
+                       f"E={L0['n_expert']}, top-{L0['n_used']}, expert ffn {L0['n_ff']}, "
+                       f"{qname(L0['gate_up_type'])}, hot expert {cfg['hot']:.0%} of tokens; the {n_layers}-layer "
+                       f"step captured as one HIP graph, {steps} replays, x varied per replay",
+           "ms_per_step": round(step_s * 1e3, 4), "tokens_s": round(T / step_s, 1),
+           "layer_us": round(step_s * 1e6 / n_layers, 2), "steps": steps,
+           "distinct_experts_per_layer": round(sum(touched) / n_layers, 2),
+           "expert_bytes_per_step": step_bytes,
+           "expert_gbs": round(step_bytes / step_s / 1e9, 1),
+           "expert_gbs_frac_of_peak": round(step_bytes / step_s / 1e9 / HBM_PEAK_GBS, 4),
+           "hbm_floor_ms": round(step_bytes / (HBM_PEAK_GBS * 1e9) * 1e3, 3),
+           "router_fallback_token_frac": round(fb_tokens / (T * n_layers * steps), 4),
+           "kernels": {k_: {"avg_us": round(v[0] * 1e3, 2), "launches": v[1]} for k_, v in prof.items()},
+           "kernel_timing": f"{2 * n_layers} eager layer calls, each kernel's execution interval"}
+    if not args.no_cpu:
+        log("[bench] stack CPU baseline ...")
+        cb = cpu_baseline(pkg, L0, cfg_name, min(args.cpu_seconds, 3.0))
+        cb["note"] = "tokens/s through one layer; a 30-layer step is 30 such layer-tokens per token"
+        out["cpu_baseline"] = cb
     return out
 
 
@@ -570,6 +677,10 @@ def main():
     ap.add_argument("--calibrate", action="store_true", help="also run the PMC calibration kernels")
     ap.add_argument("--no-prefill", action="store_true", help="leave out the prefill object of the default run")
     ap.add_argument("--prefill-steps", type=int, default=40, help="timed C3 layer calls of the prefill object")
+    ap.add_argument("--no-kquant", action="store_true", help="leave out the K-quant object of the default run")
+    ap.add_argument("--kquant-steps", type=int, default=40, help="timed C4 layer calls of the kquant object")
+    ap.add_argument("--no-stack", action="store_true", help="leave out the 30-layer stack object of the default run")
+    ap.add_argument("--stack-steps", type=int, default=20, help="timed replays of the 30-layer C5 step")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(f"bench.py: this build runs on one GPU only (the MoE path shards by experts across GPUs by design, "

@@ -130,9 +130,11 @@ int phx_moe_layer_upload(phx_moe_ctx* ctx, int layer, const phx_moe_layer_desc* 
 int phx_moe_ffn(phx_moe_ctx* ctx, int layer, int T, float* x, const float* shared, float* out, unsigned flags);
 
 /* phx_moe_ffn without allocating: no counterpart in the reference.  For callers that cannot allocate
- * device memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
- * The same computation and kernels as phx_moe_ffn with PHX_FLAG_DEVICE_PTRS (x, shared, out are device
- * pointers; PHX_FLAG_RESIDUAL, PHX_FLAG_EXACT_ROUTER and PHX_FLAG_ASYNC apply), but the call's workspace
+ * device memory (tight serving loops, harnesses that forbid hipMalloc).  The work runs on the context's
+ * own stream, so a graph capture on a caller's stream does not record it.
+ * The same computation and kernels as phx_moe_ffn with PHX_FLAG_DEVICE_PTRS (x, shared, out must be
+ * device-accessible memory: hipMalloc'd, managed or pinned host; a pageable host pointer returns
+ * PHX_ERR_ARG; PHX_FLAG_RESIDUAL, PHX_FLAG_EXACT_ROUTER and PHX_FLAG_ASYNC apply), but the call's workspace
  * (activations, routing, lists, intermediates) lives in a fixed array of PHX_NOALLOC_SCRATCH_BYTES per
  * device instead of the context's arena, and the call makes no hipMalloc / hipFree.  A call whose
  * workspace would not fit returns PHX_ERR_ARG (at C2's shapes every T up to 64 fits).  Every noalloc
@@ -157,9 +159,18 @@ int phx_moe_get_intermediates(phx_moe_ctx* ctx, float* g, float* u, float* yd);
 int phx_moe_stack_capture(phx_moe_ctx* ctx, int first_layer, int n_layers, int T);
 /* The same with phx_moe_ffn flags applied to every layer (PHX_FLAG_EXACT_ROUTER). */
 int phx_moe_stack_capture2(phx_moe_ctx* ctx, int first_layer, int n_layers, int T, unsigned flags);
+/* Replays the captured stack.  Returns PHX_ERR_ARG when a layer of the stack was uploaded again or the
+ * workspace grew (a larger phx_moe_ffn call) since the capture: the graph would name freed memory, so
+ * the caller captures again. */
 int phx_moe_stack_run(phx_moe_ctx* ctx, float* x_inout, int T, unsigned flags);
 
 int phx_moe_sync(phx_moe_ctx* ctx);
+
+/* Host-buffer calls of phx_moe_ffn replay a graph captured per (layer, T, flags, shared given); this
+ * returns how many calls found their graph and how many captured one (no counterpart in the reference:
+ * the graph cache is this library's).  The cache keeps the least recently used graphs out first, with
+ * room for four shapes per uploaded layer (at least 64). */
+int phx_moe_graph_stats(phx_moe_ctx* ctx, int64_t* hits, int64_t* misses);
 
 /* Device memory for callers without their own allocator (test harness, benchmark). */
 int phx_moe_dev_alloc(phx_moe_ctx* ctx, uint64_t bytes, void** ptr);

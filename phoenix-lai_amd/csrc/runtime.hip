@@ -299,6 +299,11 @@ struct phx_moe_ctx {
     hipGraphExec_t graph_exec = nullptr;
     hipGraph_t graph = nullptr;
     int graph_T = 0, graph_first = 0, graph_n = 0;
+    // what the stack graph was captured over: each layer's upload generation and the workspace
+    // pointers (a later upload or a workspace regrowth frees memory the graph still names)
+    std::vector<uint64_t> graph_gens;
+    std::vector<void*> graph_ws;
+    int64_t ffn_graph_hits = 0, ffn_graph_misses = 0;  // host-buffer call graphs (ffn_host)
     // phx_moe_ffn_noalloc: this device's address of the scratch array, the workspace table laid out
     // inside it (sized at creation, swapped with ws during a call), whether the last call used it, and
     // the bump allocation ensure() does while it lays the table out
@@ -730,11 +735,15 @@ int run_layer_decode(phx_moe_ctx* c, const Layer& L, int T, const float* x, cons
 // router launch has few enough workgroups (T * E of them, each reading a router row) and the expert
 // input is Q8_0 (k_dec_route writes it, with the matrix cores' fp16 copy where the rows carry one);
 // otherwise, and always under PHX_FLAG_EXACT_ROUTER, through the exact float chains.
+// The router workgroups also quantize the expert (and shared) input: workgroup (t, e) takes blocks
+// e + g E for each of its eight-thread groups g, so the groups of a token's E workgroups must cover its
+// d / 32 blocks.  With T * E > 1024 a workgroup has 256 threads (32 groups): d / 32 <= 32 E.
 constexpr int CERT_MAX_TE = 8192;
 bool cert_route(const Layer& L, int T, bool shared_ffn)
 {
     const phx_moe_layer_desc& D = L.desc;
     if ((int64_t)T * D.n_expert > CERT_MAX_TE || D.d > 4096 || D.d % 256 != 0 || D.n_expert > 256) return false;
+    if (D.d / 32 > 32 * D.n_expert) return false;
     if (!dec_type(D.gate_up_type) || (shared_ffn && !dec_type(D.shared_type))) return false;
     return true;
 }
@@ -1039,6 +1048,27 @@ int check_ffn_args(phx_moe_ctx* c, int layer, int T, const float* x, float* out,
     return PHX_OK;
 }
 
+// A device-pointer call's rows must be memory the GPU can address: hipMalloc'd, managed or pinned host.
+// A pageable host pointer would fault the device, so it is refused here.
+bool device_accessible(const void* p)
+{
+    hipPointerAttribute_t at{};
+    if (hipPointerGetAttributes(&at, p) != hipSuccess) {
+        (void)hipGetLastError();  // the query's error is not the caller's
+        return false;
+    }
+    return at.type == hipMemoryTypeDevice || at.type == hipMemoryTypeManaged || at.type == hipMemoryTypeHost ||
+           at.type == hipMemoryTypeUnified;
+}
+
+int check_device_rows(phx_moe_ctx* c, const float* x, const float* shared, const float* out)
+{
+    if (!device_accessible(x)) return set_err(c, PHX_ERR_ARG, "x is not device-accessible memory");
+    if (shared && !device_accessible(shared)) return set_err(c, PHX_ERR_ARG, "shared is not device-accessible memory");
+    if (!device_accessible(out)) return set_err(c, PHX_ERR_ARG, "out is not device-accessible memory");
+    return PHX_OK;
+}
+
 // the workspace table the last call used (routing and intermediates are read from it)
 const std::vector<Buf>& last_ws(const phx_moe_ctx* c) { return c->last_scratch ? c->ws_scratch : c->ws; }
 
@@ -1047,30 +1077,6 @@ const std::vector<Buf>& last_ws(const phx_moe_ctx* c) { return c->last_scratch ?
 // ================================================================================ C ABI
 
 extern "C" {
-
-int phx_moe_check_desc(const phx_moe_layer_desc* D)
-{
-    if (!D) return PHX_ERR_ARG;
-    if (D->d <= 0 || D->n_expert <= 0 || D->n_used <= 0 || D->n_ff <= 0) return PHX_ERR_ARG;
-    if (D->n_expert > PHX_MAX_EXPERTS || D->n_used > PHX_MAX_USED || D->n_used > D->n_expert) return PHX_ERR_UNSUPPORTED;
-    if (D->n_ff % 32 != 0 || D->d % 32 != 0) return PHX_ERR_UNSUPPORTED;
-    if (!quant_type(D->gate_up_type) || !quant_type(D->down_type)) return PHX_ERR_UNSUPPORTED;
-    if (D->d % block_elems(D->gate_up_type) != 0) return PHX_ERR_UNSUPPORTED;
-    if (D->down_cols != round_up(D->n_ff, block_elems(D->down_type))) return PHX_ERR_ARG;
-    if (D->weight_rule != PHX_WEIGHTS_SOFTMAX && D->weight_rule != PHX_WEIGHTS_CPUREF) return PHX_ERR_ARG;
-    if (!D->gate_inp || !D->gate_inp_scale || !D->down_scale || !D->pre_ffw_norm_2 || !D->post_ffw_norm_1 ||
-        !D->post_ffw_norm_2 || !D->gate_up_exps || !D->down_exps)
-        return PHX_ERR_ARG;
-    if (!(D->eps >= 0.0f)) return PHX_ERR_ARG;
-    if (D->n_ff_shared < 0) return PHX_ERR_ARG;
-    if (D->n_ff_shared > 0) {
-        if (!quant_type(D->shared_type)) return PHX_ERR_UNSUPPORTED;
-        if (D->d % block_elems(D->shared_type) != 0 || D->n_ff_shared % 32 != 0) return PHX_ERR_UNSUPPORTED;
-        if (block_elems(D->shared_type) == 256 && D->n_ff_shared % 256 != 0) return PHX_ERR_UNSUPPORTED;
-        if (!D->ffn_norm || !D->ffn_gate || !D->ffn_up || !D->ffn_down) return PHX_ERR_ARG;
-    }
-    return PHX_OK;
-}
 
 int phx_moe_create(int hip_device, phx_moe_ctx** out)
 {
@@ -1214,10 +1220,10 @@ int ffn_host(phx_moe_ctx* c, int layer, int T, float* x, const float* shared, fl
         c->pin_bytes = bytes;
         // the completion word starts at zero, which the device's count never writes (pinned memory comes
         // back from the allocator with an earlier owner's bytes)
-        *(volatile uint32_t*)(c->pin + 3 * (bytes / 4)) = 0u;
+        __atomic_store_n((uint32_t*)(c->pin + 3 * (bytes / 4)), 0u, __ATOMIC_RELEASE);
     }
     float *px = c->pin, *psh = c->pin + c->pin_bytes / 4, *pout = c->pin + 2 * (c->pin_bytes / 4);
-    volatile uint32_t* done = (volatile uint32_t*)(c->pin + 3 * (c->pin_bytes / 4));
+    uint32_t* done = (uint32_t*)(c->pin + 3 * (c->pin_bytes / 4));
     const bool res = flags & PHX_FLAG_RESIDUAL;
     // a decode-sized call ends with one workgroup copying the rows out and writing the completion word,
     // which the host polls (a stream wait costs more than the copies); larger calls copy with several
@@ -1227,8 +1233,17 @@ int ffn_host(phx_moe_ctx* c, int layer, int T, float* x, const float* shared, fl
     std::vector<void*> sig(c->ws.size());
     for (size_t i = 0; i < c->ws.size(); i++) sig[i] = c->ws[i].p;
     hipGraphExec_t exec = nullptr;
-    for (auto& g : c->ffn_graphs)
-        if (g.layer == layer && g.T == T && g.key == key && g.gen == L.gen && g.ws == sig) exec = g.exec;
+    for (size_t i = 0; i < c->ffn_graphs.size(); i++) {
+        const auto& g = c->ffn_graphs[i];
+        if (g.layer == layer && g.T == T && g.key == key && g.gen == L.gen && g.ws == sig) {
+            exec = g.exec;
+            // least recently used last out: the hit moves to the back
+            std::rotate(c->ffn_graphs.begin() + i, c->ffn_graphs.begin() + i + 1, c->ffn_graphs.end());
+            break;
+        }
+    }
+    if (exec) c->ffn_graph_hits++;
+    else c->ffn_graph_misses++;
     if (!exec) {
         HIPCHK(c, hipStreamSynchronize(st));
         HIPCHK(c, hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
@@ -1254,7 +1269,12 @@ int ffn_host(phx_moe_ctx* c, int layer, int T, float* x, const float* shared, fl
         }
         if (g) (void)hipGraphDestroy(g);
         if (rc) return rc;
-        if (c->ffn_graphs.size() >= 64) {  // the oldest goes
+        // room for a few shapes per uploaded layer (prefill chunks, a partial chunk, decode); the least
+        // recently used graph goes
+        size_t layers_up = 0;
+        for (const Layer& l : c->layers) layers_up += l.present;
+        const size_t cap = std::max<size_t>(64, 4 * layers_up);
+        while (c->ffn_graphs.size() >= cap) {
             (void)hipGraphExecDestroy(c->ffn_graphs.front().exec);
             c->ffn_graphs.erase(c->ffn_graphs.begin());
         }
@@ -1262,20 +1282,21 @@ int ffn_host(phx_moe_ctx* c, int layer, int T, float* x, const float* shared, fl
     }
     memcpy(px, x, bytes);
     if (shared) memcpy(psh, shared, bytes);
-    const uint32_t before = *done;
+    const uint32_t before = __atomic_load_n(done, __ATOMIC_ACQUIRE);
     HIPCHK(c, hipGraphLaunch(exec, st));
     if (small) {
         // the word changes once the rows are out; a call that never ends it (a fault) is left to the stream
         // wait after two seconds, which reports the error
         const auto t0 = std::chrono::steady_clock::now();
-        while (*done == before)
+        // the acquire load orders the reads of the output rows after the word's change
+        while (__atomic_load_n(done, __ATOMIC_ACQUIRE) == before)
             if (std::chrono::steady_clock::now() - t0 > std::chrono::seconds(2)) {
                 HIPCHK(c, hipStreamSynchronize(st));
-                if (*done == before) {
+                if (__atomic_load_n(done, __ATOMIC_ACQUIRE) == before) {
                     uint32_t ctr = 0;
                     (void)hipMemcpy(&ctr, c->flags + 15, 4, hipMemcpyDeviceToHost);
                     return set_err(c, PHX_ERR_HIP, "host-buffer call: no completion (word %u, device count %u)",
-                                   (unsigned)*done, (unsigned)ctr);
+                                   (unsigned)__atomic_load_n(done, __ATOMIC_ACQUIRE), (unsigned)ctr);
                 }
             }
     } else {
@@ -1302,6 +1323,7 @@ int phx_moe_ffn(phx_moe_ctx* c, int layer, int T, float* x, const float* shared,
     c->last_scratch = false;
     const size_t bytes = (size_t)T * L.desc.d * 4;
     const bool dev = flags & PHX_FLAG_DEVICE_PTRS;
+    if (dev && (rc = check_device_rows(c, x, shared, out))) return rc;
     if (!dev && !c->profiling && bytes % 16 == 0) return ffn_host(c, layer, T, x, shared, out, flags);
     float* xin = x;
     const float* shin = shared;
@@ -1335,6 +1357,7 @@ int phx_moe_ffn_noalloc(phx_moe_ctx* c, int layer, int T, float* x, const float*
     if (!c->scratch || (int)c->ws_scratch.size() != W_COUNT) return set_err(c, PHX_ERR_HIP, "no scratch array");
     const Layer& L = c->layers[layer];
     ENTER(c);
+    if ((rc = check_device_rows(c, x, shared, out))) return rc;
     // this call's workspace table, laid out afresh inside the scratch array (no allocation: the table
     // was sized at creation and the vectors only swap)
     std::swap(c->ws, c->ws_scratch);
@@ -1480,13 +1503,35 @@ int phx_moe_stack_capture2(phx_moe_ctx* c, int first, int n_layers, int T, unsig
     c->graph_T = T;
     c->graph_first = first;
     c->graph_n = n_layers;
+    c->graph_gens.clear();
+    for (int l = first; l < first + n_layers; l++) c->graph_gens.push_back(c->layers[l].gen);
+    c->graph_ws.clear();
+    for (const Buf& b : c->ws) c->graph_ws.push_back(b.p);
     return PHX_OK;
 }
+
+namespace {
+// the captured stack still names live memory: no layer of it uploaded again, no workspace buffer regrown
+bool stack_graph_current(const phx_moe_ctx* c)
+{
+    if ((int)c->graph_gens.size() != c->graph_n || c->graph_ws.size() != c->ws.size()) return false;
+    for (int i = 0; i < c->graph_n; i++) {
+        const int l = c->graph_first + i;
+        if (l >= (int)c->layers.size() || !c->layers[l].present || c->layers[l].gen != c->graph_gens[i]) return false;
+    }
+    for (size_t i = 0; i < c->ws.size(); i++)
+        if (c->ws[i].p != c->graph_ws[i]) return false;
+    return true;
+}
+}  // namespace
 
 int phx_moe_stack_run(phx_moe_ctx* c, float* x, int T, unsigned flags)
 {
     if (!c || !c->graph_exec) return set_err(c, PHX_ERR_ARG, "no captured stack");
     if (T != c->graph_T || !x) return set_err(c, PHX_ERR_ARG, "T=%d differs from the captured %d", T, c->graph_T);
+    if (!stack_graph_current(c))
+        return set_err(c, PHX_ERR_ARG, "the captured stack is stale (a layer was uploaded again or the workspace "
+                                       "grew since the capture): capture it again");
     ENTER(c);
     const size_t bytes = (size_t)T * c->layers[c->graph_first].desc.d * 4;
     const bool dev = flags & PHX_FLAG_DEVICE_PTRS;
@@ -1507,6 +1552,14 @@ int phx_moe_stack_run(phx_moe_ctx* c, float* x, int T, unsigned flags)
         }
     }
     if (!(flags & PHX_FLAG_ASYNC) || !dev) HIPCHK(c, hipStreamSynchronize(c->stream));
+    return PHX_OK;
+}
+
+int phx_moe_graph_stats(phx_moe_ctx* c, int64_t* hits, int64_t* misses)
+{
+    if (!c) return PHX_ERR_ARG;
+    if (hits) *hits = c->ffn_graph_hits;
+    if (misses) *misses = c->ffn_graph_misses;
     return PHX_OK;
 }
 

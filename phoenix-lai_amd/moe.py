@@ -129,6 +129,7 @@ def load_lib():
         "phx_moe_stack_capture2": (i32, [vp, i32, i32, i32, u32]),
         "phx_moe_stack_run": (i32, [vp, vp, i32, u32]),
         "phx_moe_sync": (i32, [vp]),
+        "phx_moe_graph_stats": (i32, [vp, C.POINTER(C.c_int64), C.POINTER(C.c_int64)]),
         "phx_moe_dev_alloc": (i32, [vp, C.c_uint64, C.POINTER(vp)]),
         "phx_moe_dev_free": (i32, [vp, vp]),
         "phx_moe_memcpy_h2d": (i32, [vp, vp, vp, C.c_uint64]),
@@ -501,6 +502,12 @@ class MoeContext:
     def stack_run_device(self, x_ptr: int, T: int):
         """Replay the captured stack on a device-resident x (async; sync() waits)."""
         self._check(self.lib.phx_moe_stack_run(self.h, x_ptr, T, PHX.FLAG_DEVICE_PTRS | PHX.FLAG_ASYNC))
+
+    def graph_stats(self) -> tuple[int, int]:
+        """(host-buffer calls that replayed a cached graph, calls that captured one)"""
+        h, m = C.c_int64(), C.c_int64()
+        self._check(self.lib.phx_moe_graph_stats(self.h, C.byref(h), C.byref(m)))
+        return h.value, m.value
 
     def fallback_counts(self) -> tuple[int, int]:
         """(norm sums re-summed sequentially, decode tokens routed through the exact router)"""

@@ -203,6 +203,26 @@ def make_layer(cfg: dict | str, layer: int = 0, weight_rule: int = 0, norms: str
     return L
 
 
+def make_stack(cfg: dict | str, n_layers: int | None = None) -> list[dict]:
+    """The layers of a decode stack: layer i has its own router, router scale, norms and down
+    scales (the blk.i. tensors, hot-expert bias included); the expert weights are generated once and
+    shared in value by every layer.  Each upload still places its own copy in device memory, so one step
+    through the stack reads n_layers distinct weight sets from HBM."""
+    if isinstance(cfg, str):
+        cfg = CONFIGS[cfg]
+    n_layers = n_layers or cfg.get("layers", 1)
+    base = make_layer(cfg, layer=0)
+    layers = [base]
+    for i in range(1, n_layers):
+        L = make_layer(cfg, layer=i, experts=False)
+        for key in ("gate_up_exps", "down_exps", "n_ff_shared", "shared_type", "ffn_norm", "ffn_gate", "ffn_up",
+                    "ffn_down"):
+            if key in base:
+                L[key] = base[key]
+        layers.append(L)
+    return layers
+
+
 def make_input(cfg: dict | str, T: int | None = None, seed: int | None = None, name: str = "x", biased=None) -> np.ndarray:
     """Activations x[T][d] ~ N(0, 1); with a biased router the last channel carries BIAS_X."""
     if isinstance(cfg, str):

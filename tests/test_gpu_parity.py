@@ -165,6 +165,29 @@ def test_c2_decode(ctx, pkg, orc, T, exact):
     check_layer(ctx, orc, L, x, tag=f"c2 T={T} exact={exact}", exact=exact)
 
 
+@pytest.mark.parametrize("exact", [False, True])
+@pytest.mark.parametrize("T", [1, 8])
+def test_c2_decode_cpuref_weights(ctx, pkg, orc, T, exact):
+    """The reference CPU's own weight rule (sel[0] replaced by 1 before the later terms read it,
+    src/GemmaCpu.cs:406-407) on the decode path, certified and exact."""
+    say(f"c2_decode CPUREF weights T={T} exact={exact}")
+    L = layer(pkg, "c2_decode", weight_rule=1)
+    x = pkg.synth.make_input("c2_decode", T=T)
+    ctx.upload(0, L)
+    check_layer(ctx, orc, L, x, tag=f"c2 cpuref T={T} exact={exact}", exact=exact)
+
+
+@pytest.mark.parametrize("cfg,T", [("c3_prefill", 256), ("c4_kquant", 64), ("c5_stack", 32)])
+def test_general_path_cpuref_weights(ctx, pkg, orc, cfg, T):
+    """The CPUREF weight rule on the general path: the matrix-core products at C3, the K-quant
+    products at C4, the certified many-token router at C5."""
+    say(f"{cfg} CPUREF weights T={T}")
+    L = layer(pkg, cfg, weight_rule=1)
+    x = pkg.synth.make_input(cfg, T=T)
+    ctx.upload(0, L)
+    check_layer(ctx, orc, L, x, tag=f"{cfg} cpuref T={T}")
+
+
 def test_router_tie_forces_fallback(ctx, pkg, orc):
     """Two experts with identical router rows tie exactly: the certified order cannot separate
     them, the exact fallback must pick the lower index first (src/GemmaCpu.cs:400-405)."""
