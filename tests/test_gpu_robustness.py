@@ -29,27 +29,30 @@ def test_general_router_covers_every_input_block(ctx, pkg, orc, E, k, d, T):
     check_layer(ctx, orc, L, x, tag=f"E{E} d{d} T{T}")
 
 
-def test_stack_refuses_a_stale_capture(ctx, pkg):
+def test_stack_refuses_a_stale_capture(pkg):
+    """A context of its own, so the workspace starts at the stack's size (T = 4) and the larger call
+    (T = 1024) regrows it."""
     say("stack: capture at T=4, then a larger call and a new upload make it stale")
     L0 = pkg.synth.make_layer("c1_tiny", layer=0, norms="noisy")
     L1 = pkg.synth.make_layer("c1_tiny", layer=1, norms="noisy")
-    ctx.upload(0, L0)
-    ctx.upload(1, L1)
-    x = pkg.synth.normal(910, "robust.stack", (4, L0["d"]))
-    ctx.stack_capture(0, 2, 4)
-    ref = ctx.stack_run(x.copy())
-    # a call with more tokens regrows the workspace the graph was captured over
-    ctx.ffn(0, pkg.synth.normal(911, "robust.big", (64, L0["d"])))
-    with pytest.raises(pkg.moe.ArgumentError, match="stale"):
-        ctx.stack_run(x.copy())
-    ctx.stack_capture(0, 2, 4)
-    np.testing.assert_array_equal(ctx.stack_run(x.copy()), ref)
-    # uploading a layer of the stack again frees the weights the graph names
-    ctx.upload(1, L1)
-    with pytest.raises(pkg.moe.ArgumentError, match="stale"):
-        ctx.stack_run(x.copy())
-    ctx.stack_capture(0, 2, 4)
-    np.testing.assert_array_equal(ctx.stack_run(x.copy()), ref)
+    with pkg.MoeContext(0) as ctx:
+        ctx.upload(0, L0)
+        ctx.upload(1, L1)
+        x = pkg.synth.normal(910, "robust.stack", (4, L0["d"]))
+        ctx.stack_capture(0, 2, 4)
+        ref = ctx.stack_run(x.copy())
+        # a call with more tokens regrows the workspace the graph was captured over
+        ctx.ffn(0, pkg.synth.normal(911, "robust.big", (1024, L0["d"])))
+        with pytest.raises(pkg.moe.ArgumentError, match="stale"):
+            ctx.stack_run(x.copy())
+        ctx.stack_capture(0, 2, 4)
+        np.testing.assert_array_equal(ctx.stack_run(x.copy()), ref)
+        # uploading a layer of the stack again frees the weights the graph names
+        ctx.upload(1, L1)
+        with pytest.raises(pkg.moe.ArgumentError, match="stale"):
+            ctx.stack_run(x.copy())
+        ctx.stack_capture(0, 2, 4)
+        np.testing.assert_array_equal(ctx.stack_run(x.copy()), ref)
     say("  refused twice, equal after each recapture")
 
 
