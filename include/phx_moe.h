@@ -64,6 +64,13 @@ extern "C" {
                                    and out must not be x */
 #define PHX_FLAG_EXACT_ROUTER 8u /* replay the reference's float router sums for every token (outputs bit-exact
                                     to the CPU reference) instead of the certified decode router */
+#define PHX_FLAG_FAST_MATH 16u /* tolerance mode of the prefill-sized Q4_0 / Q8_0 expert products (the role of
+                                  the reference's f16 cooperative-matrix path, src/KernelsCoop.cs:1-10,
+                                  src/GemmaGpu.cs:893): block scales folded into fp16 operands and whole rows
+                                  accumulated on the matrix cores.  Routing, ids and lists are unchanged (bit-
+                                  exact); the products differ from the CPU reference's chains by the operands'
+                                  fp16 rounding, and the GELU-gated requant amplifies that where a value sits
+                                  near a rounding boundary.  Decode-sized calls ignore it. */
 
 typedef struct phx_moe_ctx phx_moe_ctx;
 

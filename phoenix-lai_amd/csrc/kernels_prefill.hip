@@ -98,7 +98,12 @@ __device__ __forceinline__ uint32_t act_off(int t, int q)
 }
 
 // One workgroup's tile: NJ active 32-token column tiles (1..4).  ring: the workgroup's LDS ring.
-template <int TYPE, int NJ>
+// FOLD (the tolerance mode, PHX_FLAG_FAST_MATH): the block scales are folded into the operands as fp16
+// products, (q_w - 8) * d_w and q_x * d_x, each rounded once to fp16, and the whole row accumulates on the
+// matrix cores in fp32: two MFMAs per block and column tile, no scale MFMA and no per-block VALU chain.
+// The results then differ from the reference chain by the operands' fp16 rounding (about 2^-12 of each
+// term), not bit for bit.
+template <int TYPE, int NJ, bool FOLD>
 __device__ __forceinline__ void mma_tile(const MmaArgs& g, const Tile& tl, int cnt, unsigned char* ring, int bx)
 {
     using SL = MmaSlot<TYPE>;
@@ -252,19 +257,78 @@ __device__ __forceinline__ void mma_tile(const MmaArgs& g, const Tile& tl, int c
         });
     };
 
+    // the tolerance mode's block: land it, read the row scale, the weights and every column tile's
+    // operands, wait once, fold the scales into fp16 operands and accumulate on the matrix cores
+    auto fold_block = [&](auto SC, int b) {
+        constexpr int O = decltype(SC)::value * SL::BYTES;
+        land(SC, b);
+        u32x2 fq0 = ds_r64<O>(A_WQ), fq1 = {0u, 0u};
+        if constexpr (PAY == 32) fq1 = ds_r64<O + 16>(A_WQ);
+        uint32_t fwd = ds_ru16<O>(A_WD);
+        u32x4 fb0[NJ], fb1[NJ];
+        uint32_t fdx[NJ];
+        static_for<NJ>([&](auto JC) {
+            constexpr int j = decltype(JC)::value;
+            fb0[j] = ds_r128<O + 2048 * j>(A_B0);
+            fb1[j] = ds_r128<O + 2048 * j>(A_B1);
+            fdx[j] = ds_r32<O + 128 * j>(A_DX);
+        });
+        if constexpr (PAY == 32) asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(fq0), "+v"(fq1), "+v"(fwd)::"memory");
+        else asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(fq0), "+v"(fwd)::"memory");
+        static_for<NJ>([&](auto JC) {
+            constexpr int j = decltype(JC)::value;
+            lds_wait(fb0[j], fb1[j], fdx[j]);
+        });
+        const _Float16 dw = __builtin_bit_cast(_Float16, (uint16_t)fwd);
+        const mh8 dw8 = {dw, dw, dw, dw, dw, dw, dw, dw};
+        mh8 A0, A1;
+        if (TYPE == PHX_Q4_0_DEV) {
+            A0 = bias8(fq0.x & 0x0F0F0F0Fu, fq0.y & 0x0F0F0F0Fu, 1032.0f) * dw8;
+            A1 = bias8((fq0.x >> 4) & 0x0F0F0F0Fu, (fq0.y >> 4) & 0x0F0F0F0Fu, 1032.0f) * dw8;
+        } else {
+            A0 = bias8(fq0.x ^ 0x80808080u, fq0.y ^ 0x80808080u, 1152.0f) * dw8;
+            A1 = bias8(fq1.x ^ 0x80808080u, fq1.y ^ 0x80808080u, 1152.0f) * dw8;
+        }
+        mh8 X[NJ];
+        static_for<NJ>([&](auto JC) {  // the token scales are fp16 values: the conversions are exact
+            constexpr int j = decltype(JC)::value;
+            const _Float16 xs = (_Float16)__uint_as_float(fdx[j]);
+            X[j] = mh8{xs, xs, xs, xs, xs, xs, xs, xs};
+        });
+        // the low halves of every column tile, then the high halves: a column's two products are NJ
+        // MFMAs apart
+        static_for<NJ>([&](auto JC) {
+            constexpr int j = decltype(JC)::value;
+            S[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A0, __builtin_bit_cast(mh8, fb0[j]) * X[j], S[j], 0, 0, 0);
+        });
+        static_for<NJ>([&](auto JC) {
+            constexpr int j = decltype(JC)::value;
+            S[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A1, __builtin_bit_cast(mh8, fb1[j]) * X[j], S[j], 0, 0, 0);
+        });
+    };
+
     issue(ic<0>{}, 0);
     issue(ic<1>{}, 1);
     issue(ic<2>{}, 2);
-    land(ic<0>{}, 0);
-    start_reads(ic<0>{});
-    start_wait();
     // the ring's slots by unrolling: every LDS offset is an immediate
     static_assert(MMA_RING == 4, "the block loop is unrolled by the ring size");
-    for (int b = 0; b < nb; b += 4) {
-        block(ic<0>{}, b);
-        if (b + 1 < nb) block(ic<1>{}, b + 1);
-        if (b + 2 < nb) block(ic<2>{}, b + 2);
-        if (b + 3 < nb) block(ic<3>{}, b + 3);
+    if constexpr (FOLD) {
+        for (int b = 0; b < nb; b += 4) {
+            fold_block(ic<0>{}, b);
+            if (b + 1 < nb) fold_block(ic<1>{}, b + 1);
+            if (b + 2 < nb) fold_block(ic<2>{}, b + 2);
+            if (b + 3 < nb) fold_block(ic<3>{}, b + 3);
+        }
+    } else {
+        land(ic<0>{}, 0);
+        start_reads(ic<0>{});
+        start_wait();
+        for (int b = 0; b < nb; b += 4) {
+            block(ic<0>{}, b);
+            if (b + 1 < nb) block(ic<1>{}, b + 1);
+            if (b + 2 < nb) block(ic<2>{}, b + 2);
+            if (b + 3 < nb) block(ic<3>{}, b + 3);
+        }
     }
     // the loads issued past the last block land in this workgroup's LDS: let them finish before it ends
     __builtin_amdgcn_s_waitcnt(0);
@@ -388,7 +452,7 @@ __device__ __forceinline__ int xcd_tile(int* bx)
 }
 inline int xcd_tile_slots(int max_tiles) { return (max_tiles + 7) / 8 * 8; }
 
-template <int TYPE>
+template <int TYPE, bool FOLD>
 __global__ __launch_bounds__(256, 3) void k_grouped_mfma(MmaArgs g)
 {
     __shared__ __align__(16) unsigned char ring[MMA_RING * MmaSlot<TYPE>::BYTES];
@@ -404,10 +468,10 @@ __global__ __launch_bounds__(256, 3) void k_grouped_mfma(MmaArgs g)
     if (threadIdx.x == 0 && wgf < 8192) phx_tl[tbase + 2 * wgf] = wall_clock64();
 #endif
     switch ((cnt + 31) / 32) {  // active 32-token column tiles
-    case 1: mma_tile<TYPE, 1>(g, tl, cnt, ring, bx); break;
-    case 2: mma_tile<TYPE, 2>(g, tl, cnt, ring, bx); break;
-    case 3: mma_tile<TYPE, 3>(g, tl, cnt, ring, bx); break;
-    default: mma_tile<TYPE, 4>(g, tl, cnt, ring, bx); break;
+    case 1: mma_tile<TYPE, 1, FOLD>(g, tl, cnt, ring, bx); break;
+    case 2: mma_tile<TYPE, 2, FOLD>(g, tl, cnt, ring, bx); break;
+    case 3: mma_tile<TYPE, 3, FOLD>(g, tl, cnt, ring, bx); break;
+    default: mma_tile<TYPE, 4, FOLD>(g, tl, cnt, ring, bx); break;
     }
 #ifdef PHX_TIMELINE
     if (threadIdx.x == 0 && wgf < 8192) phx_tl[tbase + 2 * wgf + 1] = wall_clock64();
@@ -416,7 +480,7 @@ __global__ __launch_bounds__(256, 3) void k_grouped_mfma(MmaArgs g)
 
 void launch_grouped_mfma(hipStream_t st, const QMat& w, Act act, const Tile* tiles, const int* ntiles, int max_tiles,
                          const int* perm, int act_div, float* out0, float* out1, int split, int out_stride,
-                         int64_t npos, const Act* qout, int64_t qnpos, const float* gelu_tab)
+                         int64_t npos, const Act* qout, int64_t qnpos, const float* gelu_tab, bool fold)
 {
     MmaArgs g;
     g.payload = w.payload;
@@ -443,8 +507,10 @@ void launch_grouped_mfma(hipStream_t st, const QMat& w, Act act, const Tile* til
     g.qnpos = qnpos;
     g.gelu_tab = gelu_tab;
     const dim3 grid((w.rg + 1) / 2, xcd_tile_slots(max_tiles));
-    if (w.type == PHX_Q4_0_DEV) launch(k_grouped_mfma<PHX_Q4_0_DEV>, grid, dim3(256), 0, st, g);
-    else launch(k_grouped_mfma<PHX_Q8_0_DEV>, grid, dim3(256), 0, st, g);
+    if (w.type == PHX_Q4_0_DEV)
+        launch(fold ? k_grouped_mfma<PHX_Q4_0_DEV, true> : k_grouped_mfma<PHX_Q4_0_DEV, false>, grid, dim3(256), 0, st, g);
+    else
+        launch(fold ? k_grouped_mfma<PHX_Q8_0_DEV, true> : k_grouped_mfma<PHX_Q8_0_DEV, false>, grid, dim3(256), 0, st, g);
 }
 
 // ============================================================================ K-quant products

@@ -173,12 +173,13 @@ void launch_matvec(hipStream_t st, int type, int rows, int nb, int T, const uint
 // assignments; same arguments and outputs as launch_grouped.  npos > 0 reads the activations in
 // expert-list order, block-major (fp16 integers of block b, list position p at qh + (b * npos + p) * 32,
 // scales at d[b * npos + p]).  For a paired gate|up matrix with qout set, the kernel also does the
-// GELU-gated requant into qout in that layout over qnpos positions (its qh and d only).
+// GELU-gated requant into qout in that layout over qnpos positions (its qh and d only).  fold: the
+// tolerance mode (scales folded into fp16 operands, the row accumulated on the matrix cores).
 constexpr int kMmaTile = 128;
 void launch_grouped_mfma(hipStream_t st, const QMat& w, Act act, const Tile* tiles, const int* ntiles, int max_tiles,
                          const int* perm, int act_div, float* out0, float* out1, int split, int out_stride,
                          int64_t npos = 0, const Act* qout = nullptr, int64_t qnpos = 0,
-                         const float* gelu_tab = nullptr);
+                         const float* gelu_tab = nullptr, bool fold = false);
 // K-quant prefill path (kernels_prefill.hip): Q4_K / Q6_K grouped products on MFMA, tiles of up to
 // kKmmaTile assignments, activations' fp16 copies (qh; Q4_K also bh) in row order; arguments and outputs
 // as launch_grouped

@@ -749,7 +749,7 @@ bool cert_route(const Layer& L, int T, bool shared_ffn)
 }
 
 int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, const float* shared, float* out, float* xres,
-                      bool exact)
+                      bool exact, bool fast)
 {
     const phx_moe_layer_desc& D = L.desc;
     hipStream_t st = c->stream;
@@ -839,7 +839,7 @@ int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, con
         ProfScope p(c, PHX_K_GATE_UP);
         if (mma)  // the matrix-core gate|up also writes the down input (GELU-gated Q8_0, list order)
             launch_grouped_mfma(st, L.gu, agu, wp<Tile>(c, W_TILES), wp<int>(c, W_NTILES), max_tiles, wp<int>(c, W_PERM), k,
-                                wp<float>(c, W_G), wp<float>(c, W_U), nf, nf, 0, &adn, n, c->gelu_tab);
+                                wp<float>(c, W_G), wp<float>(c, W_U), nf, nf, 0, &adn, n, c->gelu_tab, fast);
         else if (kmma)
             launch_grouped_kmma(st, L.gu, agu, wp<Tile>(c, W_TILES), wp<int>(c, W_NTILES), max_tiles, wp<int>(c, W_PERM), k,
                                 wp<float>(c, W_G), wp<float>(c, W_U), nf, nf);
@@ -855,7 +855,7 @@ int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, con
         ProfScope p(c, PHX_K_DOWN);
         if (mma)
             launch_grouped_mfma(st, L.dn, adn, wp<Tile>(c, W_TILES), wp<int>(c, W_NTILES), max_tiles, wp<int>(c, W_PERM), 1,
-                                wp<float>(c, W_YD), wp<float>(c, W_YD), d, d, n);
+                                wp<float>(c, W_YD), wp<float>(c, W_YD), d, d, n, nullptr, 0, nullptr, fast);
         else if (kmma)
             launch_grouped_kmma(st, L.dn, adn, wp<Tile>(c, W_TILES), wp<int>(c, W_NTILES), max_tiles, wp<int>(c, W_PERM), 1,
                                 wp<float>(c, W_YD), wp<float>(c, W_YD), d, d);
@@ -879,14 +879,14 @@ int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, con
         }
         if (smma)
             launch_grouped_mfma(st, L.sgu, ash, wp<Tile>(c, W_STILES), wp<int>(c, W_SNTILES), smax, wp<int>(c, W_SPERM), 1,
-                                wp<float>(c, W_SHG), wp<float>(c, W_SHU), nff, nff, 0, &asd, T, c->gelu_tab);
+                                wp<float>(c, W_SHG), wp<float>(c, W_SHU), nff, nff, 0, &asd, T, c->gelu_tab, fast);
         else
             launch_grouped(st, L.sgu, ash, wp<Tile>(c, W_STILES), wp<int>(c, W_SNTILES), smax, kTileA, wp<int>(c, W_SPERM),
                            1, wp<float>(c, W_SHG), wp<float>(c, W_SHU), nff, nff);
         if (!smma) launch_requant(st, T, nff, wp<float>(c, W_SHG), wp<float>(c, W_SHU), c->gelu_tab, asd);
         if (smma)
             launch_grouped_mfma(st, L.sdn, asd, wp<Tile>(c, W_STILES), wp<int>(c, W_SNTILES), smax, wp<int>(c, W_SPERM), 1,
-                                wp<float>(c, W_SHOUT), wp<float>(c, W_SHOUT), d, d, T);
+                                wp<float>(c, W_SHOUT), wp<float>(c, W_SHOUT), d, d, T, nullptr, 0, nullptr, fast);
         else
             launch_grouped(st, L.sdn, asd, wp<Tile>(c, W_STILES), wp<int>(c, W_SNTILES), smax, kTileA, wp<int>(c, W_SPERM),
                            1, wp<float>(c, W_SHOUT), wp<float>(c, W_SHOUT), d, d);
@@ -905,7 +905,8 @@ int run_layer(phx_moe_ctx* c, const Layer& L, int T, const float* x, const float
               unsigned flags)
 {
     if (use_decode(c, L, T, flags)) return run_layer_decode(c, L, T, x, shared, out, xres);
-    return run_layer_general(c, L, T, x, shared, out, xres, (flags & PHX_FLAG_EXACT_ROUTER) != 0);
+    return run_layer_general(c, L, T, x, shared, out, xres, (flags & PHX_FLAG_EXACT_ROUTER) != 0,
+                             (flags & PHX_FLAG_FAST_MATH) != 0);
 }
 
 int upload_f32(phx_moe_ctx* c, const float* src, size_t n, float** dst)
@@ -1229,7 +1230,8 @@ int ffn_host(phx_moe_ctx* c, int layer, int T, float* x, const float* shared, fl
     // which the host polls (a stream wait costs more than the copies); larger calls copy with several
     // workgroups and wait on the stream
     const bool small = bytes * (res ? 2 : 1) <= (256u << 10);
-    const unsigned key = (flags & (PHX_FLAG_RESIDUAL | PHX_FLAG_EXACT_ROUTER)) | (shared ? 0x80000000u : 0u);
+    const unsigned key =
+        (flags & (PHX_FLAG_RESIDUAL | PHX_FLAG_EXACT_ROUTER | PHX_FLAG_FAST_MATH)) | (shared ? 0x80000000u : 0u);
     std::vector<void*> sig(c->ws.size());
     for (size_t i = 0; i < c->ws.size(); i++) sig[i] = c->ws[i].p;
     hipGraphExec_t exec = nullptr;
