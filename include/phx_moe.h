@@ -37,7 +37,9 @@ extern "C" {
 #define PHX_F32 0
 #define PHX_Q4_0 2
 #define PHX_Q8_0 8
+#define PHX_Q3_K 11 /* 110 B / 256: hmask, 2-bit q, 16 six-bit scales, d (src/CpuRefIQuants.cs:9, 19-43) */
 #define PHX_Q4_K 12
+#define PHX_Q5_K 13 /* 176 B / 256: Q4_K with a fifth bit per value from qh[32] (src/CpuRefKQuants.cs:13, 134-146) */
 #define PHX_Q6_K 14
 /* IQ expert formats (CpuRefIQuants.cs:9-12: 256-element super-blocks of 66, 82 and 110 bytes), dotted
  * against Q8_K activations by the reference's DotIQ2XXS / DotIQ2S / DotIQ3S (src/CpuRefIQuants.cs:45-167)
@@ -273,7 +275,7 @@ int phx_matvec(phx_moe_ctx* ctx, int type, const void* w, int rows, int cols, in
 /* Prefill matmul of a dense quantized matrix over T token rows: KernelsPrefill.MatMulQ4Q8Tile as
  * GemmaGpu.Mm records it (src/KernelsPrefill.cs:143-260, src/GemmaGpu.cs:907-923) for the shared FFN
  * and every other dense projection of a prompt chunk.  phx_weight_upload repacks `rows` GGUF rows of
- * `cols` (PHX_Q4_0 or PHX_Q8_0; PHX_Q4_K or PHX_Q6_K for phx_matmul_k, cols a multiple of 256; host
+ * `cols` (PHX_Q4_0 or PHX_Q8_0; PHX_Q3_K, PHX_Q4_K, PHX_Q5_K or PHX_Q6_K for phx_matmul_k, cols a multiple of 256; host
  * memory, as the file holds them) into the device's row groups once (GemmaGpu.UploadW / UploadK,
  * src/GemmaGpu.cs:344-352, 402-436); phx_weight_free releases them.  phx_matmul: xq / xd are
  * T Q8_0 rows in the layout of phx_quant_q8_0 (device pointers, xq 4-byte aligned) and
@@ -285,10 +287,11 @@ int phx_weight_upload(phx_moe_ctx* ctx, int type, int rows, int cols, const void
 void phx_weight_free(phx_moe_ctx* ctx, phx_weight* w);
 int phx_matmul(phx_moe_ctx* ctx, const phx_weight* w, int T, const int8_t* xq, const uint16_t* xd, float* y);
 
-/* Dense K-quant matvec over T token rows: KernelsK.MatVec for Q4_K / Q6_K weights as GemmaGpu.MatVec
- * records it (src/KernelsKQuants.cs:65-108, src/GemmaGpu.cs:471-473, bindings w, kq, kd, y), for any
- * K-quant dense projection (the shared FFN and attention of a K-quant model).  w: a phx_weight_upload
- * handle of type PHX_Q4_K or PHX_Q6_K (cols a multiple of 256; Q4_0 / Q8_0 handles return
+/* Dense K-quant matvec over T token rows: KernelsK.MatVec for Q4_K / Q5_K / Q6_K weights as GemmaGpu.MatVec
+ * records it (src/KernelsKQuants.cs:65-108, src/GemmaGpu.cs:471-473, bindings w, kq, kd, y), and Q3_K
+ * rows as CpuRef.MatVec computes them (src/CpuRef.cs:79-85), for any K-quant dense projection (the shared
+ * FFN and attention of a K-quant model).  w: a phx_weight_upload handle of a K-quant type (cols a
+ * multiple of 256; Q4_0 / Q8_0 handles return
  * PHX_ERR_UNSUPPORTED).  xq / xd: T Q8_K input rows in the layout of phx_quant_q8_k (qs int8 [T][cols],
  * d float [T][cols/256]; device pointers, 4-byte aligned); the block sums are formed from xq.
  * y[t][r] = CpuRefKQuants.MatVecK's value for token t (src/CpuRefKQuants.cs:176-232: DotK's integer lane

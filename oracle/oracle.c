@@ -155,7 +155,9 @@ int64_t orc_row_bytes(int type, int cols)
     case ORC_F32: return (int64_t)cols * 4;
     case ORC_Q4_0: return (int64_t)(cols / 32) * 18;
     case ORC_Q8_0: return (int64_t)(cols / 32) * 34;
+    case ORC_Q3_K: return (int64_t)(cols / 256) * 110;
     case ORC_Q4_K: return (int64_t)(cols / 256) * 144;
+    case ORC_Q5_K: return (int64_t)(cols / 256) * 176;
     case ORC_Q6_K: return (int64_t)(cols / 256) * 210;
     case ORC_IQ2_XXS: return (int64_t)(cols / 256) * 66;
     case ORC_IQ2_S: return (int64_t)(cols / 256) * 82;
@@ -177,9 +179,38 @@ static void scale_min_k4(int j, const uint8_t* q, int* sc, int* m)
     }
 }
 
-/* UnpackK (CpuRefKQuants.cs:90-147), Q4_K and Q6_K: 256 small integers, scales, mins. */
+/* ScaleQ3K (CpuRefIQuants.cs:19-25): 6-bit Q3_K scale j before its -32 offset */
+static int scale_q3k(const uint8_t* s, int j)
+{
+    int low = j < 8 ? s[j] & 0xF : s[j - 8] >> 4;
+    int high = (s[8 + (j & 3)] >> (2 * (j >> 2))) & 3;
+    return low | (high << 4);
+}
+
+/* UnpackK (CpuRefKQuants.cs:90-147), Q3_K through UnpackQ3K (CpuRefIQuants.cs:28-43): 256 small
+ * integers, scales, mins. */
+static int k_block_bytes(int t)
+{
+    return t == ORC_Q3_K ? 110 : t == ORC_Q4_K ? 144 : t == ORC_Q5_K ? 176 : 210;
+}
+
 static void unpack_k(int t, const uint8_t* blk, int8_t* a, int* scales, int* mins, float* d, float* dmin)
 {
+    if (t == ORC_Q3_K) {
+        const uint8_t* hm = blk; const uint8_t* q3 = blk + 32;
+        int m = 1;
+        for (int j = 0; j < QK_K; j += 128) {
+            for (int shift = 0; shift < 8; shift += 2) {
+                for (int l = 0; l < 32; l++) a[l] = (int8_t)(((q3[l] >> shift) & 3) - ((hm[l] & m) != 0 ? 0 : 4));
+                a += 32; m <<= 1;
+            }
+            q3 += 32;
+        }
+        for (int j = 0; j < 16; j++) scales[j] = scale_q3k(blk + 96, j) - 32;
+        *d = orc_half_to_float(rd16(blk + 108));
+        *dmin = 0;
+        return;
+    }
     if (t == ORC_Q6_K) {
         const uint8_t* ql = blk; const uint8_t* qh = blk + 128; const int8_t* sc = (const int8_t*)(blk + 192);
         for (int n = 0; n < QK_K / 128; n++) {
@@ -196,17 +227,29 @@ static void unpack_k(int t, const uint8_t* blk, int8_t* a, int* scales, int* min
         *dmin = 0;
         return;
     }
-    /* Q4_K */
+    /* Q4_K, Q5_K */
     *d = orc_half_to_float(rd16(blk));
     *dmin = orc_half_to_float(rd16(blk + 2));
     const uint8_t* sc8 = blk + 4;
     for (int j = 0; j < 8; j++) scale_min_k4(j, sc8, &scales[j], &mins[j]);
-    const uint8_t* q4 = blk + 16;
-    for (int j = 0; j < QK_K / 64; j++) {
-        for (int l = 0; l < 32; l++) a[l] = (int8_t)(q4[l] & 0xF);
-        a += 32;
-        for (int l = 0; l < 32; l++) a[l] = (int8_t)(q4[l] >> 4);
-        a += 32; q4 += 32;
+    if (t == ORC_Q4_K) {
+        const uint8_t* q4 = blk + 16;
+        for (int j = 0; j < QK_K / 64; j++) {
+            for (int l = 0; l < 32; l++) a[l] = (int8_t)(q4[l] & 0xF);
+            a += 32;
+            for (int l = 0; l < 32; l++) a[l] = (int8_t)(q4[l] >> 4);
+            a += 32; q4 += 32;
+        }
+    } else {
+        const uint8_t* hm = blk + 16; const uint8_t* q4 = blk + 48;
+        int m = 1;
+        for (int j = 0; j < QK_K / 64; j++) {
+            for (int l = 0; l < 32; l++) a[l] = (int8_t)((q4[l] & 0xF) + ((hm[l] & m) != 0 ? 16 : 0));
+            a += 32; m <<= 1;
+            for (int l = 0; l < 32; l++) a[l] = (int8_t)((q4[l] >> 4) + ((hm[l] & m) != 0 ? 16 : 0));
+            a += 32; m <<= 1;
+            q4 += 32;
+        }
     }
 }
 
@@ -236,14 +279,14 @@ int orc_dequantize_row(int type, const uint8_t* row, int cols, float* dst)
         }
         return 0;
     }
-    if (type == ORC_Q4_K || type == ORC_Q6_K) {
-        int nb = cols / QK_K, bytes = type == ORC_Q4_K ? 144 : 210;
+    if (type == ORC_Q3_K || type == ORC_Q4_K || type == ORC_Q5_K || type == ORC_Q6_K) {
+        int nb = cols / QK_K, bytes = k_block_bytes(type);
         int8_t a[QK_K]; int scales[16]; int mins[8];
         for (int b = 0; b < nb; b++) {
             float d, dmin;
             unpack_k(type, row + (int64_t)b * bytes, a, scales, mins, &d, &dmin);
             int o = b * QK_K;
-            if (type == ORC_Q6_K) {
+            if (type == ORC_Q6_K || type == ORC_Q3_K) {
                 for (int e = 0; e < QK_K; e++) dst[o + e] = d * scales[e / 16] * a[e];
             } else {
                 for (int e = 0; e < QK_K; e++) { int sb = e / 32; dst[o + e] = d * scales[sb] * a[e] - dmin * mins[sb]; }
@@ -295,9 +338,9 @@ float orc_dot_k(int t, const uint8_t* row, int nb, const float* kd, const int8_t
     int8_t a[QK_K]; int scales[16]; int mins[8];
     for (int l = 0; l < 8; l++) sums[l] = 0;
     float sumf = 0;
-    int sixteen = t == ORC_Q6_K;
+    int sixteen = t == ORC_Q6_K || t == ORC_Q3_K;
     int sub = sixteen ? 16 : 32;
-    int bytes = t == ORC_Q4_K ? 144 : 210;
+    int bytes = k_block_bytes(t);
     for (int i = 0; i < nb; i++) {
         float d, dmin;
         unpack_k(t, row + (int64_t)i * bytes, a, scales, mins, &d, &dmin);
@@ -449,7 +492,7 @@ static int set_threads(int nthreads)
 #endif
 }
 
-/* CpuRef.MatVec (CpuRef.cs:70-89) for F32/Q4_0/Q8_0/Q4_K/Q6_K: the activation quantization, then
+/* CpuRef.MatVec (CpuRef.cs:70-89) for F32/Q4_0/Q8_0 and the K and IQ types: the activation quantization, then
  * one independent dot per row (Parallel.For in the reference; rows never interact).  F32 follows
  * MatVecF32 (CpuRef.cs:121-132): a double sum cast to float. */
 int orc_matvec(int type, const uint8_t* w, int rows, int cols, const float* x, float* y, int nthreads)

@@ -20,7 +20,7 @@ extern "C" {
 #endif
 
 /* GgmlType codes (src/Gguf.cs:18-24). */
-enum { ORC_F32 = 0, ORC_Q4_0 = 2, ORC_Q8_0 = 8, ORC_Q4_K = 12, ORC_Q6_K = 14, ORC_IQ2_XXS = 16, ORC_IQ3_S = 21,
+enum { ORC_F32 = 0, ORC_Q4_0 = 2, ORC_Q8_0 = 8, ORC_Q3_K = 11, ORC_Q4_K = 12, ORC_Q5_K = 13, ORC_Q6_K = 14, ORC_IQ2_XXS = 16, ORC_IQ3_S = 21,
        ORC_IQ2_S = 22 };
 
 /* Router weight rule.  ORC_W_SOFTMAX: renormalised softmax over the selected logits, exp and sum in

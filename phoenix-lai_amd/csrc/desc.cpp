@@ -4,7 +4,11 @@
 
 namespace {
 bool iq_desc_type(int t) { return t == PHX_IQ2_XXS || t == PHX_IQ2_S || t == PHX_IQ3_S; }
-bool quant_type(int t) { return t == PHX_Q4_0 || t == PHX_Q8_0 || t == PHX_Q4_K || t == PHX_Q6_K || iq_desc_type(t); }
+bool quant_type(int t)
+{
+    return t == PHX_Q4_0 || t == PHX_Q8_0 || t == PHX_Q3_K || t == PHX_Q4_K || t == PHX_Q5_K || t == PHX_Q6_K ||
+           iq_desc_type(t);
+}
 int block_elems(int t) { return (t == PHX_Q4_0 || t == PHX_Q8_0) ? 32 : 256; }
 int round_up(int v, int m) { return (v + m - 1) / m * m; }
 }  // namespace

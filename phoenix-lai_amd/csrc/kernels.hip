@@ -946,7 +946,7 @@ __global__ __launch_bounds__(256) void k_grouped_q(GroupArgs g)
 
 // K-quant rows: DotK (src/CpuRefKQuants.cs:177-212) per (row, assignment): per super-block the eight
 // integer lanes aux32[l] (element e contributes to lane e % 8), float lanes
-// sums[l] += (d * yd) * aux32[l], the Q4_K min term sumf -= (dmin * yd) * sumi, finally sumf += sums[l].
+// sums[l] += (d * yd) * aux32[l], the Q4_K / Q5_K min term sumf -= (dmin * yd) * sumi, finally sumf += sums[l].
 template <int TYPE, int A>
 __global__ __launch_bounds__(256) void k_grouped_k(GroupArgs g)
 {
@@ -956,10 +956,11 @@ __global__ __launch_bounds__(256) void k_grouped_k(GroupArgs g)
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int rgi = blockIdx.y * 4 + wave;
     if (rgi >= g.rg) return;
-    constexpr bool Q4K = TYPE == PHX_Q4_K_DEV;
-    constexpr int PAY = Q4K ? 144 : 208;
+    constexpr bool Q4K = TYPE == PHX_Q4_K_DEV, Q5K = TYPE == PHX_Q5_K_DEV;
+    constexpr bool AFF = Q4K || Q5K;  // scales and mins per 32 (the min term); else 16 signed scales per 16
+    constexpr int PAY = Q4K ? 144 : Q5K ? 176 : 208;
     const uint8_t* wp = g.payload + tl.e * g.mat_pay + rgi * g.rg_pay + lane * PAY;
-    const uint8_t* wsb = g.scale + tl.e * g.mat_sc + ((int64_t)rgi * g.nb * 64 + lane) * (Q4K ? 4 : 2);
+    const uint8_t* wsb = g.scale + tl.e * g.mat_sc + ((int64_t)rgi * g.nb * 64 + lane) * (AFF ? 4 : 2);
     int arow[A];
     float sums[A][8], sumf[A];
 #pragma unroll
@@ -980,7 +981,7 @@ __global__ __launch_bounds__(256) void k_grouped_k(GroupArgs g)
             }
         }
         float d, dmin = 0.0f;
-        if (Q4K) {
+        if (AFF) {
             uint32_t dm = *(const uint32_t*)(wsb + (int64_t)b * 64 * 4);
             d = h2f(dm & 0xFFFF);
             dmin = h2f(dm >> 16);
@@ -990,12 +991,15 @@ __global__ __launch_bounds__(256) void k_grouped_k(GroupArgs g)
         // unpacked weight dwords
         uint32_t v[64];
         int sc[16], mn[8];
-        if (Q4K) {
+        if (AFF) {
 #pragma unroll
             for (int w = 0; w < 32; w++) {
                 v[2 * w] = wv[w] & 0x0F0F0F0Fu;
                 v[2 * w + 1] = (wv[w] >> 4) & 0x0F0F0F0Fu;
             }
+            if (Q5K)  // the fifth bits: bit l of byte mm of dword s belongs to value dword 8 s + l, byte mm
+#pragma unroll
+                for (int x = 0; x < 64; x++) v[x] |= ((wv[36 + x / 8] >> (x % 8)) & 0x01010101u) << 4;
 #pragma unroll
             for (int s = 0; s < 8; s++) {
                 sc[s] = (wv[32 + s / 4] >> (8 * (s % 4))) & 0xFF;
@@ -1021,7 +1025,7 @@ __global__ __launch_bounds__(256) void k_grouped_k(GroupArgs g)
                 int aux[8];
 #pragma unroll
                 for (int l = 0; l < 8; l++) aux[l] = 0;
-                if (Q4K) {
+                if (AFF) {
                     const uint32_t* xq = (const uint32_t*)(g.act.q + r * g.act.qstride + b * 256);
 #pragma unroll
                     for (int s = 0; s < 8; s++)
@@ -1046,7 +1050,7 @@ __global__ __launch_bounds__(256) void k_grouped_k(GroupArgs g)
                 const float dd = d * yd;
 #pragma unroll
                 for (int l = 0; l < 8; l++) sums[i][l] += dd * (float)aux[l];
-                if (Q4K) {
+                if (AFF) {
                     const int* bs = g.act.s + r * g.act.sstride + b * 16;
                     int sumi = 0;
 #pragma unroll
@@ -1213,6 +1217,7 @@ void launch_grouped(hipStream_t st, const QMat& w, Act act, const Tile* tiles, c
     case PHX_Q4_0_DEV: launch((k_grouped_q<PHX_Q4_0_DEV, 4>), grid, dim3(256), 0, st, g); break;
     case PHX_Q8_0_DEV: launch((k_grouped_q<PHX_Q8_0_DEV, 4>), grid, dim3(256), 0, st, g); break;
     case PHX_Q4_K_DEV: launch((k_grouped_k<PHX_Q4_K_DEV, 4>), grid, dim3(256), 0, st, g); break;
+    case PHX_Q5_K_DEV: launch((k_grouped_k<PHX_Q5_K_DEV, 4>), grid, dim3(256), 0, st, g); break;
     case PHX_Q6_K_DEV: launch((k_grouped_k<PHX_Q6_K_DEV, 4>), grid, dim3(256), 0, st, g); break;
     case PHX_IQ2_XXS_DEV: launch((k_grouped_iq<PHX_IQ2_XXS_DEV, 4>), grid, dim3(256), 0, st, g); break;
     case PHX_IQ2_S_DEV: launch((k_grouped_iq<PHX_IQ2_S_DEV, 4>), grid, dim3(256), 0, st, g); break;

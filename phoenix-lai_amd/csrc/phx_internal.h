@@ -9,6 +9,7 @@
 #define PHX_Q4_0_DEV 2
 #define PHX_Q8_0_DEV 8
 #define PHX_Q4_K_DEV 12
+#define PHX_Q5_K_DEV 13
 #define PHX_Q6_K_DEV 14
 #define PHX_IQ2_XXS_DEV 16
 #define PHX_IQ3_S_DEV 21

@@ -93,7 +93,9 @@ int64_t row_bytes(int type, int cols)
     case PHX_F32: return (int64_t)cols * 4;
     case PHX_Q4_0: return (int64_t)(cols / 32) * 18;
     case PHX_Q8_0: return (int64_t)(cols / 32) * 34;
+    case PHX_Q3_K: return (int64_t)(cols / 256) * 110;
     case PHX_Q4_K: return (int64_t)(cols / 256) * 144;
+    case PHX_Q5_K: return (int64_t)(cols / 256) * 176;
     case PHX_Q6_K: return (int64_t)(cols / 256) * 210;
     case PHX_IQ2_XXS: return (int64_t)(cols / 256) * 66;
     case PHX_IQ2_S: return (int64_t)(cols / 256) * 82;
@@ -103,9 +105,19 @@ int64_t row_bytes(int type, int cols)
 }
 
 bool iq_type(int t) { return t == PHX_IQ2_XXS || t == PHX_IQ2_S || t == PHX_IQ3_S; }
-bool quant_type(int t) { return t == PHX_Q4_0 || t == PHX_Q8_0 || t == PHX_Q4_K || t == PHX_Q6_K || iq_type(t); }
+bool k_type(int t) { return t == PHX_Q3_K || t == PHX_Q4_K || t == PHX_Q5_K || t == PHX_Q6_K; }
+bool quant_type(int t) { return t == PHX_Q4_0 || t == PHX_Q8_0 || k_type(t) || iq_type(t); }
 int block_elems(int t) { return (t == PHX_Q4_0 || t == PHX_Q8_0) ? 32 : 256; }
-int act_fmt(int t) { return t == PHX_Q4_K ? ACT_K4 : t == PHX_Q6_K ? ACT_K6 : iq_type(t) ? ACT_Q8K : ACT_Q8_0; }
+// Q3_K rows live on the device as Q6_K blocks: DotK's integer lanes, float lanes and fold are the same
+// for both (src/CpuRefKQuants.cs:183-211: sixteen scales of 16 elements, no min term), and every Q3_K
+// value (q - 4 in -4..3, scale - 32 in -32..31, the same fp16 d) is a Q6_K one, so the Q6_K kernels give
+// the reference's Q3_K results bit for bit
+int dev_type(int t) { return t == PHX_Q3_K ? PHX_Q6_K : t; }
+int act_fmt(int t)
+{
+    t = dev_type(t);
+    return (t == PHX_Q4_K || t == PHX_Q5_K) ? ACT_K4 : t == PHX_Q6_K ? ACT_K6 : iq_type(t) ? ACT_Q8K : ACT_Q8_0;
+}
 int iq_pay(int t) { return t == PHX_IQ2_XXS ? 64 : t == PHX_IQ2_S ? 80 : 112; }
 int round_up(int v, int m) { return (v + m - 1) / m * m; }
 
@@ -115,20 +127,74 @@ struct HostQ {
     std::vector<uint8_t> payload, scale;
 };
 
-void decode_q4k_natural(const uint8_t* blk, uint8_t* q, int* sc, int* mn)
+// the eight 6-bit scales and mins of a Q4_K / Q5_K block (ScaleMinK4, src/CpuRefKQuants.cs:32-43)
+void decode_k4_scales(const uint8_t* blk, int* sc, int* mn)
 {
-    // UnpackK's element order for Q4_K (src/CpuRefKQuants.cs:118-133)
     const uint8_t* s8 = blk + 4;
     for (int j = 0; j < 8; j++) {
         if (j < 4) { sc[j] = s8[j] & 63; mn[j] = s8[j + 4] & 63; }
         else { sc[j] = (s8[j + 4] & 0xF) | ((s8[j - 4] >> 6) << 4); mn[j] = (s8[j + 4] >> 4) | ((s8[j] >> 6) << 4); }
     }
+}
+
+void decode_q4k_natural(const uint8_t* blk, uint8_t* q, int* sc, int* mn)
+{
+    // UnpackK's element order for Q4_K (src/CpuRefKQuants.cs:118-133)
+    decode_k4_scales(blk, sc, mn);
     const uint8_t* q4 = blk + 16;
     for (int c = 0; c < 4; c++)
         for (int l = 0; l < 32; l++) {
             q[64 * c + l] = q4[32 * c + l] & 0xF;
             q[64 * c + 32 + l] = q4[32 * c + l] >> 4;
         }
+}
+
+void decode_q5k_natural(const uint8_t* blk, uint8_t* q, int* sc, int* mn)
+{
+    // UnpackK's element order for Q5_K (src/CpuRefKQuants.cs:134-146): Q4_K's nibbles plus bit j of qh[l]
+    // as the fifth bit of element l of sub-block j
+    decode_k4_scales(blk, sc, mn);
+    const uint8_t* qh = blk + 16;
+    const uint8_t* q4 = blk + 48;
+    for (int c = 0; c < 4; c++)
+        for (int l = 0; l < 32; l++) {
+            q[64 * c + l] = (uint8_t)((q4[32 * c + l] & 0xF) | (((qh[l] >> (2 * c)) & 1) << 4));
+            q[64 * c + 32 + l] = (uint8_t)((q4[32 * c + l] >> 4) | (((qh[l] >> (2 * c + 1)) & 1) << 4));
+        }
+}
+
+// One Q3_K block (110 B) as the Q6_K block (210 B) of the same values: q6 = q3 + 32, scale = scale - 32,
+// d unchanged (UnpackQ3K, src/CpuRefIQuants.cs:28-43; ScaleQ3K :19-25)
+void q3k_as_q6k(const uint8_t* blk, uint8_t* out)
+{
+    const uint8_t* hm = blk;
+    const uint8_t* q3 = blk + 32;
+    const uint8_t* s8 = blk + 96;
+    uint8_t v[256];
+    for (int h = 0; h < 2; h++)
+        for (int j = 0; j < 4; j++)
+            for (int l = 0; l < 32; l++) {
+                const int a = ((q3[32 * h + l] >> (2 * j)) & 3) - ((hm[l] >> (4 * h + j)) & 1 ? 0 : 4);
+                v[128 * h + 32 * j + l] = (uint8_t)(a + 32);
+            }
+    memset(out, 0, 210);
+    for (int n = 0; n < 2; n++) {
+        const uint8_t* a = v + 128 * n;
+        uint8_t* L = out + 64 * n;
+        uint8_t* H = out + 128 + 32 * n;
+        for (int l = 0; l < 32; l++) {
+            L[l] = (uint8_t)((a[l] & 0xF) | ((a[l + 64] & 0xF) << 4));
+            L[l + 32] = (uint8_t)((a[l + 32] & 0xF) | ((a[l + 96] & 0xF) << 4));
+            H[l] = (uint8_t)((a[l] >> 4) | ((a[l + 32] >> 4) << 2) | ((a[l + 64] >> 4) << 4) | ((a[l + 96] >> 4) << 6));
+        }
+    }
+    for (int j = 0; j < 16; j++) {
+        const int lo = j < 8 ? s8[j] & 0xF : s8[j - 8] >> 4;
+        const int hi = (s8[8 + (j & 3)] >> (2 * (j >> 2))) & 3;
+        out[192 + j] = (uint8_t)(int8_t)((lo | (hi << 4)) - 32);
+    }
+    out[208] = blk[108];
+    out[209] = blk[109];
 }
 
 void decode_q6k_natural(const uint8_t* blk, uint8_t* v)
@@ -160,17 +226,36 @@ void repack_block(int type, const uint8_t* blk, uint8_t* pay, uint8_t* sc)
         memcpy(sc, blk, 2);
         memcpy(pay, blk + 2, 32);
         break;
-    case PHX_Q4_K: {
+    case PHX_Q4_K:
+    case PHX_Q5_K: {
+        // 128 nibble bytes: dword w = 2 value dwords (s, l = 2 (w % 4), +1), byte mm of each the element
+        // 32 s + l + 8 mm; then 8 scales and 8 mins; Q5_K then 8 dwords of fifth bits: bit l of byte mm of
+        // dword s is element 32 s + l + 8 mm's
         uint8_t q[256];
         int s[8], m[8];
-        decode_q4k_natural(blk, q, s, m);
+        if (type == PHX_Q4_K) decode_q4k_natural(blk, q, s, m);
+        else decode_q5k_natural(blk, q, s, m);
         for (int w = 0; w < 32; w++) {
             int sb = w / 4, p = w % 4;
             for (int mm = 0; mm < 4; mm++)
-                pay[4 * w + mm] = (uint8_t)(q[32 * sb + 2 * p + 8 * mm] | (q[32 * sb + 2 * p + 1 + 8 * mm] << 4));
+                pay[4 * w + mm] = (uint8_t)((q[32 * sb + 2 * p + 8 * mm] & 0xF) | ((q[32 * sb + 2 * p + 1 + 8 * mm] & 0xF) << 4));
         }
         for (int j = 0; j < 8; j++) { pay[128 + j] = (uint8_t)s[j]; pay[136 + j] = (uint8_t)m[j]; }
+        if (type == PHX_Q5_K) {
+            for (int sb = 0; sb < 8; sb++)
+                for (int mm = 0; mm < 4; mm++) {
+                    uint8_t b = 0;
+                    for (int l = 0; l < 8; l++) b |= (uint8_t)(((q[32 * sb + l + 8 * mm] >> 4) & 1) << l);
+                    pay[144 + 4 * sb + mm] = b;
+                }
+        }
         memcpy(sc, blk, 4);  // d | dmin << 16
+        break;
+    }
+    case PHX_Q3_K: {
+        uint8_t q6[210];
+        q3k_as_q6k(blk, q6);
+        repack_block(PHX_Q6_K, q6, pay, sc);
         break;
     }
     case PHX_Q6_K: {
@@ -210,15 +295,16 @@ void repack_block(int type, const uint8_t* blk, uint8_t* pay, uint8_t* sc)
 // and up rows rows/2 + 32g.. in lanes 32-63.
 void repack(int type, const uint8_t* src, int n_mat, int rows, int cols, QMat& q, HostQ& h, bool paired = false)
 {
-    q.type = type;
+    q.type = dev_type(type);
     q.n_mat = n_mat;
     q.rows = rows;
     q.cols = cols;
     q.paired = paired;
     q.rg = paired ? (rows / 2 + 31) / 32 : (rows + kRowGroup - 1) / kRowGroup;
     q.nb = cols / block_elems(type);
-    q.pay = type == PHX_Q4_0 ? 16 : type == PHX_Q8_0 ? 32 : type == PHX_Q4_K ? 144 : iq_type(type) ? iq_pay(type) : 208;
-    q.sbytes = type == PHX_Q4_K ? 4 : 2;
+    q.pay = type == PHX_Q4_0 ? 16 : type == PHX_Q8_0 ? 32 : type == PHX_Q4_K ? 144 : type == PHX_Q5_K ? 176
+          : iq_type(type) ? iq_pay(type) : 208;
+    q.sbytes = (type == PHX_Q4_K || type == PHX_Q5_K) ? 4 : 2;
     const int64_t rb = row_bytes(type, cols), bb = rb / q.nb;
     const int nb8 = (q.nb + 7) / 8;
     q.rg_pay = (int64_t)q.nb * kRowGroup * q.pay + (q.has_sc8() ? (int64_t)nb8 * kRowGroup * 16 : 0);
@@ -503,7 +589,8 @@ int ensure_act(phx_moe_ctx* c, int fmt, int64_t rows, int cols, int qid, int did
 constexpr int kTileA = 4;  // assignments per grouped tile
 
 bool mfma_type(int t);
-bool kmma_type(int t) { return t == PHX_Q4_K || t == PHX_Q6_K; }
+// the K-quant matrix-core kernel takes Q4_K and Q6_K device rows (so Q3_K too); Q5_K runs the VALU rows
+bool kmma_type(int t) { return dev_type(t) == PHX_Q4_K || dev_type(t) == PHX_Q6_K; }
 
 int ensure_workspace(phx_moe_ctx* c, const Layer& L, int T)
 {
@@ -1757,8 +1844,9 @@ int phx_weight_upload(phx_moe_ctx* c, int type, int rows, int cols, const void* 
 {
     if (!c || !out) return PHX_ERR_ARG;
     *out = nullptr;
-    if (type != PHX_Q4_0 && type != PHX_Q8_0 && type != PHX_Q4_K && type != PHX_Q6_K)
-        return set_err(c, PHX_ERR_UNSUPPORTED, "weight upload: type %d (Q4_0, Q8_0, Q4_K and Q6_K only)", type);
+    if (type != PHX_Q4_0 && type != PHX_Q8_0 && !k_type(type))
+        return set_err(c, PHX_ERR_UNSUPPORTED, "weight upload: type %d (Q4_0, Q8_0, Q3_K, Q4_K, Q5_K and Q6_K only)",
+                       type);
     const int be = block_elems(type);
     if (rows <= 0 || cols <= 0 || cols % be || cols > 16384 || !src)
         return set_err(c, PHX_ERR_ARG, "weight upload: shape %d x %d (cols a multiple of %d, <= 16384)", rows, cols, be);
@@ -1850,15 +1938,15 @@ int phx_matmul_k(phx_moe_ctx* c, const phx_weight* w, int T, const int8_t* xq, c
     if (!c) return PHX_ERR_ARG;
     if (!w || !xq || !xd || !y) return set_err(c, PHX_ERR_ARG, "matmul_k: null argument");
     if (T <= 0 || T > 65535) return set_err(c, PHX_ERR_ARG, "matmul_k: T=%d out of range", T);
-    if (w->type != PHX_Q4_K && w->type != PHX_Q6_K)
-        return set_err(c, PHX_ERR_UNSUPPORTED, "matmul_k: weight type %d (Q4_K and Q6_K only)", w->type);
+    if (!k_type(w->type))
+        return set_err(c, PHX_ERR_UNSUPPORTED, "matmul_k: weight type %d (Q3_K, Q4_K, Q5_K and Q6_K only)", w->type);
     if ((uintptr_t)xq % 4 || (uintptr_t)xd % 4 || (uintptr_t)y % 4)
         return set_err(c, PHX_ERR_ARG, "matmul_k: xq, xd and y need 4-byte alignment");
     ENTER(c);
     const int fmt = act_fmt(w->type), cols = w->cols;
     // the general path's rule with one matrix (at least 8 rows per matrix): the matrix cores, else the
     // VALU row walk
-    const bool kmma = T >= 8;
+    const bool kmma = T >= 8 && kmma_type(w->type);
     const int A = kmma ? kKmmaTile : kTileA;
     const int max_tiles = (T + A - 1) / A;
     size_t qb, db, sb;

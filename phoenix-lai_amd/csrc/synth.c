@@ -215,13 +215,101 @@ static void q6_k_block(const float* x, uint8_t* blk)
     wr16(blk + 208, dh);
 }
 
+/* Q5_K (176 B / 256): Q4_K's affine sub-blocks with 5-bit q (0..31): d, dmin, the 12 packed scale/min
+ * bytes, qh[32] (bit s of qh[l]: the high bit of element 32 s + l), qs[128] (the low nibbles as Q4_K). */
+static void q5_k_block(const float* x, uint8_t* blk)
+{
+    float scl[8], mn[8], maxs = 0, maxm = 0;
+    for (int s = 0; s < 8; s++) {
+        float lo = x[32 * s], hi = x[32 * s];
+        for (int j = 1; j < 32; j++) { float v = x[32 * s + j]; if (v < lo) lo = v; if (v > hi) hi = v; }
+        if (lo > 0) lo = 0;
+        scl[s] = (hi - lo) / 31.0f;
+        mn[s] = -lo;
+        if (scl[s] > maxs) maxs = scl[s];
+        if (mn[s] > maxm) maxm = mn[s];
+    }
+    uint16_t dh = half_from_float(maxs / 63.0f), mh = half_from_float(maxm / 63.0f);
+    float d = half_to_float(dh), dmin = half_to_float(mh);
+    int sc[8], m[8];
+    for (int s = 0; s < 8; s++) {
+        int a = d > 0 ? (int)lrintf(scl[s] / d) : 0, b = dmin > 0 ? (int)lrintf(mn[s] / dmin) : 0;
+        sc[s] = a < 0 ? 0 : a > 63 ? 63 : a;
+        m[s] = b < 0 ? 0 : b > 63 ? 63 : b;
+    }
+    memset(blk, 0, 176);
+    wr16(blk, dh);
+    wr16(blk + 2, mh);
+    uint8_t* q = blk + 4;
+    for (int j = 0; j < 4; j++) {
+        q[j] = (uint8_t)(sc[j] | ((sc[j + 4] >> 4) << 6));
+        q[j + 4] = (uint8_t)(m[j] | ((m[j + 4] >> 4) << 6));
+        q[j + 8] = (uint8_t)((sc[j + 4] & 0xF) | ((m[j + 4] & 0xF) << 4));
+    }
+    uint8_t* qh = blk + 16;
+    uint8_t* qs = blk + 48;
+    for (int s = 0; s < 8; s++) {
+        float ds = d * sc[s], off = dmin * m[s];
+        for (int l = 0; l < 32; l++) {
+            int qq = ds > 0 ? (int)lrintf((x[32 * s + l] + off) / ds) : 0;
+            qq = qq < 0 ? 0 : qq > 31 ? 31 : qq;
+            qs[32 * (s / 2) + l] |= (uint8_t)((qq & 15) << (4 * (s & 1)));
+            qh[l] |= (uint8_t)((qq >> 4) << s);
+        }
+    }
+}
+
+/* Q3_K (110 B / 256): per 16-element sub-block a 6-bit signed scale (stored + 32) under an fp16 d:
+ * value = d*sc*q, q in -4..3 as q + 4 = (2 low bits in qs) | (hmask bit << 2).  hmask[32] @0, qs[64] @32
+ * (element 128 h + 32 j + l: bits 2j of qs[32 h + l]; its hmask bit is bit 4 h + j of hmask[l]),
+ * scales[12] @96 (sub-block i: low nibble of byte i (i < 8) or high nibble of byte i - 8, high 2 bits
+ * at bits 2 (i / 4) of byte 8 + i % 4), d @108. */
+static void q3_k_block(const float* x, uint8_t* blk)
+{
+    float scl[16], maxs = 0;
+    for (int s = 0; s < 16; s++) {
+        float amax = 0, max = 0;
+        for (int j = 0; j < 16; j++) { float a = fabsf(x[16 * s + j]); if (a > amax) { amax = a; max = x[16 * s + j]; } }
+        scl[s] = max / -4.0f;
+        if (fabsf(scl[s]) > maxs) maxs = fabsf(scl[s]);
+    }
+    uint16_t dh = half_from_float(maxs / 31.0f);
+    float d = half_to_float(dh);
+    int sc[16];
+    for (int s = 0; s < 16; s++) {
+        int a = d > 0 ? (int)lrintf(scl[s] / d) : 0;
+        sc[s] = a < -32 ? -32 : a > 31 ? 31 : a;
+    }
+    memset(blk, 0, 110);
+    uint8_t* hm = blk;
+    uint8_t* qs = blk + 32;
+    uint8_t* s8 = blk + 96;
+    for (int e = 0; e < 256; e++) {
+        float ds = d * sc[e / 16];
+        int v = ds != 0 ? (int)lrintf(x[e] / ds) : 0;
+        v = (v < -4 ? -4 : v > 3 ? 3 : v) + 4;
+        int h = e / 128, j = (e % 128) / 32, l = e % 32;
+        qs[32 * h + l] |= (uint8_t)((v & 3) << (2 * j));
+        hm[l] |= (uint8_t)((v >> 2) << (4 * h + j));
+    }
+    for (int i = 0; i < 16; i++) {
+        int u = sc[i] + 32;
+        if (i < 8) s8[i] |= (uint8_t)(u & 15);
+        else s8[i - 8] |= (uint8_t)((u & 15) << 4);
+        s8[8 + (i % 4)] |= (uint8_t)((u >> 4) << (2 * (i / 4)));
+    }
+    wr16(blk + 108, dh);
+}
+
 int64_t phx_synth_row_bytes(int type, int cols)
 {
     switch (type) {
     case 0: return (int64_t)cols * 4;
     case 2: return (int64_t)(cols / 32) * 18;
     case 8: return (int64_t)(cols / 32) * 34;
+    case 11: return (int64_t)(cols / 256) * 110;
     case 12: return (int64_t)(cols / 256) * 144;
+    case 13: return (int64_t)(cols / 256) * 176;
     case 14: return (int64_t)(cols / 256) * 210;
     }
     return -1;
@@ -232,7 +320,7 @@ int phx_synth_quantize(int type, const float* x, int64_t rows, int cols, uint8_t
 {
     int64_t rb = phx_synth_row_bytes(type, cols);
     if (rb < 0) return -3;
-    int bs = type == 0 ? 1 : (type == 12 || type == 14) ? 256 : 32;
+    int bs = type == 0 ? 1 : (type >= 11 && type <= 14) ? 256 : 32;
     if (cols % bs) return -1;
 #pragma omp parallel for schedule(static)
     for (int64_t r = 0; r < rows; r++) {
@@ -242,7 +330,9 @@ int phx_synth_quantize(int type, const float* x, int64_t rows, int cols, uint8_t
         for (int b = 0; b < cols / bs; b++) {
             if (type == 2) q4_0_block(xr + 32 * b, o + 18 * b);
             else if (type == 8) q8_0_block(xr + 32 * b, o + 34 * b);
+            else if (type == 11) q3_k_block(xr + 256 * b, o + 110 * b);
             else if (type == 12) q4_k_block(xr + 256 * b, o + 144 * b);
+            else if (type == 13) q5_k_block(xr + 256 * b, o + 176 * b);
             else q6_k_block(xr + 256 * b, o + 210 * b);
         }
     }

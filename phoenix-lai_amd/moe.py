@@ -17,7 +17,7 @@ _HERE = Path(__file__).resolve().parent
 
 class PHX:
     OK, ERR_ARG, ERR_OOM, ERR_UNSUPPORTED, ERR_DEVICE_LOST, ERR_HIP, ERR_FORMAT = 0, -1, -2, -3, -4, -5, -6
-    F32, Q4_0, Q8_0, Q4_K, Q6_K, IQ2_XXS, IQ3_S, IQ2_S = 0, 2, 8, 12, 14, 16, 21, 22
+    F32, Q4_0, Q8_0, Q3_K, Q4_K, Q5_K, Q6_K, IQ2_XXS, IQ3_S, IQ2_S = 0, 2, 8, 11, 12, 13, 14, 16, 21, 22
     WEIGHTS_SOFTMAX, WEIGHTS_CPUREF = 0, 1
     FLAG_DEVICE_PTRS, FLAG_ASYNC, FLAG_RESIDUAL, FLAG_EXACT_ROUTER, FLAG_FAST_MATH = 1, 2, 4, 8, 16
     KINDS = ["prologue", "router", "topk", "dispatch", "gate_up", "requant", "down", "combine", "shared"]
@@ -445,7 +445,8 @@ class MoeContext:
         """phx_weight_upload (GemmaGpu.UploadW): GGUF rows from host memory, repacked on the device once;
         returns the handle for matmul_device / weight_free."""
         w = np.ascontiguousarray(w, dtype=np.uint8)
-        be, bb = {PHX.Q4_0: (32, 18), PHX.Q8_0: (32, 34), PHX.Q4_K: (256, 144), PHX.Q6_K: (256, 210)}.get(wtype, (32, 0))
+        be, bb = {PHX.Q4_0: (32, 18), PHX.Q8_0: (32, 34), PHX.Q3_K: (256, 110), PHX.Q4_K: (256, 144), PHX.Q5_K: (256, 176),
+                  PHX.Q6_K: (256, 210)}.get(wtype, (32, 0))
         if cols <= 0 or cols % be or w.size != rows * (cols // be) * bb:
             raise ArgumentError(PHX.ERR_ARG, f"weight bytes {w.size} != {rows} rows x {cols // be} blocks x {bb}")
         h = C.c_void_p()

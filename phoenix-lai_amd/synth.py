@@ -70,7 +70,7 @@ def row_bytes(t: int, cols: int) -> int:
 
 
 def block_elems(t: int) -> int:
-    return 256 if t in (PHX.Q4_K, PHX.Q6_K) or t in _IQ_BYTES else (1 if t == PHX.F32 else 32)
+    return 256 if t in (PHX.Q3_K, PHX.Q4_K, PHX.Q5_K, PHX.Q6_K) or t in _IQ_BYTES else (1 if t == PHX.F32 else 32)
 
 
 def normal(seed: int, name: str, shape, mean=0.0, std=1.0, offset=0) -> np.ndarray:

@@ -1,5 +1,5 @@
 """Independent numpy decoders of the GGUF block layouts (the layout table of src/Gguf.cs:29-59 and
-the ggml block structs): Q4_0, Q8_0, Q4_K, Q6_K.  Written from the format, not from the oracle's
+the ggml block structs): Q4_0, Q8_0, Q3_K, Q4_K, Q5_K, Q6_K.  Written from the format, not from the oracle's
 code, so the oracle's bit-level decoding is checked against a second reading of the spec."""
 import numpy as np
 
@@ -71,6 +71,63 @@ def q6_k_parts(blk: np.ndarray):
     return d, sc, q - 32
 
 
+def q5_k_parts(blk: np.ndarray):
+    """(d, dmin, sc[8], m[8], q[256] in 0..31) of one 176-byte Q5_K super-block: fp16 d, fp16 dmin, the 12
+    scale/min bytes packed as Q4_K's, qh[32], qs[128].  The low four bits of q are Q4_K's nibbles (chunk c
+    of 32 qs bytes: sub-block 2c low nibbles, 2c+1 high nibbles); element l of sub-block j takes bit j of
+    qh[l] as its fifth bit (value 16)."""
+    d, dmin, sc, m, _ = q4_k_parts(np.concatenate([blk[:16], blk[48:176]]))
+    qh = blk[16:48].astype(np.int32)
+    qs = blk[48:176].reshape(4, 32).astype(np.int32)
+    q = np.empty(256, np.int32)
+    for j in range(8):
+        nib = (qs[j // 2] >> (4 * (j % 2))) & 15
+        q[32 * j:32 * j + 32] = nib + 16 * ((qh >> j) & 1)
+    return d, dmin, sc, m, q
+
+
+def q3_k_parts(blk: np.ndarray):
+    """(d, sc[16] in -32..31, q[256] in -4..3) of one 110-byte Q3_K super-block: hmask[32], qs[64],
+    scales[12], fp16 d.  Element 128 h + 32 j + l has two low bits at bits 2j..2j+1 of qs[32 h + l] and
+    a high bit at bit 4h + j of hmask[l]; q = low + 4 * high - 4.  Scale i is six bits: the low four
+    are the low nibble of scales[i] (i < 8) or the high nibble of scales[i - 8], the high two are bits
+    2 (i / 4) of scales[8 + i % 4]; the stored value is offset by 32."""
+    hm = blk[0:32].astype(np.int32)
+    qs = blk[32:96].astype(np.int32)
+    s = blk[96:108].astype(np.int32)
+    d = f16(int(blk[108]) | (int(blk[109]) << 8))
+    q = np.empty(256, np.int32)
+    for h in range(2):
+        for j in range(4):
+            low = (qs[32 * h:32 * h + 32] >> (2 * j)) & 3
+            high = (hm >> (4 * h + j)) & 1
+            q[128 * h + 32 * j:128 * h + 32 * j + 32] = low + 4 * high - 4
+    sc = np.empty(16, np.int32)
+    for i in range(16):
+        lo = (s[i] & 15) if i < 8 else (s[i - 8] >> 4)
+        hi = (s[8 + i % 4] >> (2 * (i // 4))) & 3
+        sc[i] = (lo | (hi << 4)) - 32
+    return d, sc, q
+
+
+def dequant_q5_k(row: np.ndarray, cols: int) -> np.ndarray:
+    out = np.empty(cols, np.float32)
+    for b in range(cols // QK):
+        d, dmin, sc, m, q = q5_k_parts(row[176 * b:176 * b + 176])
+        sb = np.arange(256) // 32
+        out[QK * b:QK * b + QK] = (np.float32(d) * sc[sb].astype(np.float32) * q.astype(np.float32)
+                                   - np.float32(dmin) * m[sb].astype(np.float32))
+    return out
+
+
+def dequant_q3_k(row: np.ndarray, cols: int) -> np.ndarray:
+    out = np.empty(cols, np.float32)
+    for b in range(cols // QK):
+        d, sc, q = q3_k_parts(row[110 * b:110 * b + 110])
+        out[QK * b:QK * b + QK] = np.float32(d) * sc[np.arange(256) // 16].astype(np.float32) * q.astype(np.float32)
+    return out
+
+
 def dequant_q4_k(row: np.ndarray, cols: int) -> np.ndarray:
     out = np.empty(cols, np.float32)
     for b in range(cols // QK):
@@ -89,8 +146,8 @@ def dequant_q6_k(row: np.ndarray, cols: int) -> np.ndarray:
     return out
 
 
-DEQUANT = {2: dequant_q4_0, 8: dequant_q8_0, 12: dequant_q4_k, 14: dequant_q6_k}
-BLOCK = {2: (32, 18), 8: (32, 34), 12: (256, 144), 14: (256, 210)}
+DEQUANT = {2: dequant_q4_0, 8: dequant_q8_0, 11: dequant_q3_k, 12: dequant_q4_k, 13: dequant_q5_k, 14: dequant_q6_k}
+BLOCK = {2: (32, 18), 8: (32, 34), 11: (256, 110), 12: (256, 144), 13: (256, 176), 14: (256, 210)}
 
 
 def random_blocks(rng: np.random.Generator, t: int, nblocks: int) -> np.ndarray:
@@ -106,15 +163,16 @@ def random_blocks(rng: np.random.Generator, t: int, nblocks: int) -> np.ndarray:
         d = h16(nblocks)
         b[:, 0] = d & 0xFF
         b[:, 1] = d >> 8
-    elif t == 12:
+    elif t in (12, 13):
         for off in (0, 2):
             d = h16(nblocks)
             b[:, off] = d & 0xFF
             b[:, off + 1] = d >> 8
     else:
+        off = 108 if t == 11 else 208
         d = h16(nblocks)
-        b[:, 208] = d & 0xFF
-        b[:, 209] = d >> 8
+        b[:, off] = d & 0xFF
+        b[:, off + 1] = d >> 8
     return b.reshape(-1)
 
 

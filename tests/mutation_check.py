@@ -87,6 +87,12 @@ MUTATIONS = {
     "weight cast after the down scale": [("w[j] = (float)(sel[j] / sum) * L->down_scale[ids[j]];",
                                           "w[j] = (float)(sel[j] / sum * L->down_scale[ids[j]]);")],
     "q8_0 id = 127 / amax": [("float id = d != 0 ? 1.0f / d : 0.0f;", "float id = amax != 0 ? 127.0f / amax : 0.0f;")],
+    # Q3_K and Q5_K decoding
+    "q5_k high nibble takes the low bit": [("a[l] = (int8_t)((q4[l] >> 4) + ((hm[l] & m) != 0 ? 16 : 0));",
+                                            "a[l] = (int8_t)((q4[l] >> 4) + ((hm[l] & (m >> 1)) != 0 ? 16 : 0));")],
+    "q3_k hmask sense inverted": [("- ((hm[l] & m) != 0 ? 0 : 4));", "- ((hm[l] & m) != 0 ? 4 : 0));")],
+    "q3_k scale high bits transposed": [("int high = (s[8 + (j & 3)] >> (2 * (j >> 2))) & 3;",
+                                         "int high = (s[8 + (j >> 2)] >> (2 * (j & 3))) & 3;")],
     # IQ formats
     "iq2_xxs super-blocks reversed": [("    for (int i = 0; i < nb; i++) {\n        const uint8_t* blk = row + (int64_t)i * 66;",
                                        "    for (int i = nb - 1; i >= 0; i--) {\n        const uint8_t* blk = row + (int64_t)i * 66;")],

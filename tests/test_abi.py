@@ -100,8 +100,8 @@ def test_constants_match_python_mirror(pkg):
     assert (d["PHX_OK"], d["PHX_ERR_ARG"], d["PHX_ERR_OOM"], d["PHX_ERR_UNSUPPORTED"], d["PHX_ERR_DEVICE_LOST"],
             d["PHX_ERR_HIP"], d["PHX_ERR_FORMAT"]) == (P.OK, P.ERR_ARG, P.ERR_OOM, P.ERR_UNSUPPORTED, P.ERR_DEVICE_LOST,
                                                    P.ERR_HIP, P.ERR_FORMAT)
-    assert (d["PHX_F32"], d["PHX_Q4_0"], d["PHX_Q8_0"], d["PHX_Q4_K"], d["PHX_Q6_K"]) == (P.F32, P.Q4_0, P.Q8_0,
-                                                                                       P.Q4_K, P.Q6_K)
+    assert (d["PHX_F32"], d["PHX_Q4_0"], d["PHX_Q8_0"], d["PHX_Q3_K"], d["PHX_Q4_K"], d["PHX_Q5_K"], d["PHX_Q6_K"]) == (
+        P.F32, P.Q4_0, P.Q8_0, P.Q3_K, P.Q4_K, P.Q5_K, P.Q6_K)
     assert (d["PHX_MAX_EXPERTS"], d["PHX_MAX_USED"]) == (P.MAX_EXPERTS, P.MAX_USED)
     assert (d["PHX_WEIGHTS_SOFTMAX"], d["PHX_WEIGHTS_CPUREF"]) == (P.WEIGHTS_SOFTMAX, P.WEIGHTS_CPUREF)
     assert (d["PHX_FLAG_DEVICE_PTRS"], d["PHX_FLAG_ASYNC"], d["PHX_FLAG_RESIDUAL"], d["PHX_FLAG_EXACT_ROUTER"],
@@ -153,6 +153,9 @@ def test_check_desc_k_quant_alignment(pkg, tiny_layer):
     assert _check(pkg, tiny_layer, gate_up_type=P.Q4_K, d=288) == P.ERR_UNSUPPORTED
     assert _check(pkg, tiny_layer, down_type=P.Q6_K) == P.ERR_ARG  # down_cols 128 is not 256-aligned
     assert _check(pkg, tiny_layer, down_type=P.Q6_K, down_cols=256) == P.OK
+    # Q3_K and Q5_K (GGUF types 11 and 13) on either product
+    assert _check(pkg, tiny_layer, gate_up_type=P.Q5_K, down_type=P.Q3_K, down_cols=256) == P.OK
+    assert _check(pkg, tiny_layer, gate_up_type=P.Q3_K, d=288) == P.ERR_UNSUPPORTED
 
 
 def test_check_desc_null(pkg):

@@ -18,6 +18,7 @@ def _layers(pkg, cfg, n, **kw):
 SMALL = dict(idx=21, T=4, d=512, E=8, k=2, nf=256, gu=2, dn=2, nff=384, sh=2)
 SMALL_Q8 = dict(idx=22, T=4, d=512, E=8, k=2, nf=256, gu=8, dn=8, nff=256, sh=8)
 SMALL_K = dict(idx=23, T=4, d=512, E=4, k=2, nf=512, gu=12, dn=14)  # K-quant rows: nf a multiple of 256
+SMALL_K35 = dict(idx=24, T=4, d=512, E=4, k=2, nf=512, gu=13, dn=11, nff=512, sh=13)  # Q5_K and Q3_K (types 13, 11)
 
 
 @pytest.fixture(scope="module")
@@ -57,7 +58,7 @@ def test_parse_round_trip(pkg, small_file):
                                   "n_ff_exp": 256, "eps": np.float32(1e-6)}
 
 
-@pytest.mark.parametrize("cfg", [SMALL, SMALL_Q8, SMALL_K])
+@pytest.mark.parametrize("cfg", [SMALL, SMALL_Q8, SMALL_K, SMALL_K35])
 def test_layer_descriptor_points_at_the_tensors(pkg, tmp_path, cfg):
     layers = _layers(pkg, cfg, 2)
     path = GW.moe_model(layers).write(tmp_path / "m.gguf")

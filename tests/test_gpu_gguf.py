@@ -22,6 +22,8 @@ CASES = {
     "c2_q4_0": ("c2_decode", 2, [(1, False), (8, False), (40, False), (4, True)]),
     # K-quants with whole-block down rows (n_ff = 512)
     "kquant": (dict(idx=24, T=8, d=1024, E=16, k=4, nf=512, gu=12, dn=14), 1, [(12, False), (3, True)]),
+    # a Q5_K_M-like layer: Q5_K gate|up, Q3_K down (GGUF types 13 and 11), the dense FFN in Q5_K
+    "q5k_q3k": (dict(idx=25, T=8, d=512, E=8, k=2, nf=512, gu=13, dn=11, nff=512, sh=13), 1, [(6, False), (40, True)]),
 }
 
 

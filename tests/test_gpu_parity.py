@@ -583,6 +583,29 @@ def test_kmma_grouped_products_bit_exact(ctx, pkg, orc, case):
     check_layer(ctx, orc, L, x, tag=f"kmma {case}", exact=True)
 
 
+# Q5_K (the VALU row walk at any T: five-bit values with the min term) and Q3_K (held on the device as
+# the Q6_K blocks of the same values, so the Q6_K kernels run it, on the matrix cores from 8 assignments
+# per expert); either type on either product, a shared FFN in Q5_K, padded down rows
+Q35_CASES = {
+    "q5k_gu_q3k_dn_T8": (dict(idx=61, T=8, d=512, E=8, k=2, nf=512, gu=13, dn=11), 8),
+    "q3k_gu_q5k_dn_T12_shared": (dict(idx=62, T=12, d=768, E=8, k=2, nf=512, gu=11, dn=13, nff=512, sh=13), 12),
+    "q5k_both_T64_full_tiles": (dict(idx=63, T=64, d=512, E=4, k=2, nf=512, gu=13, dn=13), 64),
+    "q3k_both_T96_kmma": (dict(idx=64, T=96, d=1024, E=8, k=2, nf=384, gu=11, dn=11), 96),
+}
+
+
+@pytest.mark.parametrize("case", list(Q35_CASES))
+def test_q3k_q5k_layers_bit_exact(ctx, pkg, orc, case):
+    """Q3_K and Q5_K experts (src/CpuRefKQuants.cs:92-147 through DotK :177-212): gate, up and down
+    products and outputs equal the oracle bit for bit (exact router)."""
+    cfg, T = Q35_CASES[case]
+    say(f"q3k/q5k {case}: T={T}")
+    L = pkg.synth.make_layer(cfg, norms="noisy")
+    x = pkg.synth.make_input(cfg, T=T)
+    ctx.upload(0, L)
+    check_layer(ctx, orc, L, x, tag=f"q3k/q5k {case}", exact=True)
+
+
 # ---------------------------------------------------------------------------------------- IQ formats
 IQ_CASES = {
     # gate|up, down (and the shared FFN) in the IQ formats (CpuRefIQuants.cs); n_ff 384 pads the down rows

@@ -186,22 +186,23 @@ def test_matmul_matches_oracle(ctx, orc, wtype, T, rows, cols):
 
 
 def gguf_k_rows(rng, wtype, rows, cols):
-    """Random GGUF rows of Q4_K (144-byte super-blocks) or Q6_K (210-byte): every quant, 6-bit scale and
-    min, and int8 sub-block scale value, with finite fp16 super-block scales (d, dmin)."""
-    bb = 144 if wtype == 12 else 210
+    """Random GGUF rows of Q3_K (110-byte super-blocks), Q4_K (144), Q5_K (176) or Q6_K (210): every quant,
+    high bit, 6-bit scale and min, and int8 sub-block scale value, with finite fp16 super-block scales."""
+    bb = {11: 110, 12: 144, 13: 176, 14: 210}[wtype]
     n = rows * cols // 256
     blocks = rng.integers(0, 256, (n, bb), dtype=np.uint8)
     d = (rng.standard_normal(n) * 0.002).astype(np.float16)
-    if wtype == 12:
+    if wtype in (12, 13):
         blocks[:, 0:2] = d.view(np.uint8).reshape(-1, 2)
         dmin = (np.abs(rng.standard_normal(n)) * 0.001).astype(np.float16)
         blocks[:, 2:4] = dmin.view(np.uint8).reshape(-1, 2)
     else:
-        blocks[:, 208:210] = d.view(np.uint8).reshape(-1, 2)
+        off = 108 if wtype == 11 else 208
+        blocks[:, off:off + 2] = d.view(np.uint8).reshape(-1, 2)
     return blocks.reshape(-1)
 
 
-@pytest.mark.parametrize("wtype", [12, 14])
+@pytest.mark.parametrize("wtype", [11, 12, 13, 14])
 @pytest.mark.parametrize("T,rows,cols", [(1, 1408, 4096), (3, 301, 2816), (7, 64, 12288), (8, 301, 2816),
                                          (48, 4096, 1536), (200, 2112, 4096), (512, 4096, 1536)])
 def test_matmul_k_matches_oracle(ctx, orc, wtype, T, rows, cols):

@@ -9,7 +9,7 @@ import pytest
 import gguf_spec as G
 import textbook as TB
 
-TYPES = [2, 8, 12, 14]
+TYPES = [2, 8, 11, 12, 13, 14]
 
 
 # ---------------------------------------------------------------------------------------- fp16
@@ -176,7 +176,7 @@ def _pow2_scales(blocks, t, exp2=-8):
     h = np.float16(2.0 ** exp2).view(np.uint16)
     size = G.BLOCK[t][1]
     b = blocks.reshape(-1, size)
-    offs = {2: [0], 8: [0], 12: [0, 2], 14: [208]}[t]
+    offs = {2: [0], 8: [0], 11: [108], 12: [0, 2], 13: [0, 2], 14: [208]}[t]
     for o in offs:
         b[:, o] = h & 0xFF
         b[:, o + 1] = h >> 8
