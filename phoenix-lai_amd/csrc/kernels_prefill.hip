@@ -76,18 +76,26 @@ __device__ __forceinline__ mh8 bias8(uint32_t w0, uint32_t w1, float bias)
 }
 
 constexpr int MMA_RING = 4;  // LDS ring slots: blocks in flight ahead of the one being multiplied
-constexpr int MMA_DMA = 5;   // direct loads per wave per block
 
 // LDS ring slot layout (bytes).  A direct load of 1, 2 or 4 bytes writes lane l's value at 4 l from
 // the wave's LDS base (16 l for 16-byte loads).
+// Weight scales: Q4_0 rows take their fp16 scales from the row group's scale groups (16 bytes = 8 blocks
+// per row) into a two-slot scale ring beside the block ring, one load per wave every 8 blocks (SG); Q8_0
+// rows (whose larger payload leaves no LDS for that ring at three workgroups per CU) one 2-byte load per
+// block into the slot (WD).  The direct loads' address processing bounds the kernel, so every load
+// instruction saved counts.
 template <int TYPE>
 struct MmaSlot {
     static constexpr int PAY = TYPE == PHX_Q4_0_DEV ? 16 : 32;
+    static constexpr bool SG = TYPE == PHX_Q4_0_DEV;
+    static constexpr int DMA = SG ? 4 : 5;           // direct loads per wave per block (scale groups aside)
     static constexpr int ACT = 0;                    // 128 tokens x 64 B, swizzled 16-token groups
     static constexpr int ADX = ACT + MMA_TOK * 64;   // 128 token scales (float)
     static constexpr int WQ = ADX + MMA_TOK * 4;     // 128 weight rows x PAY
-    static constexpr int WD = WQ + 128 * PAY;        // 128 weight scales (fp16 in the low half of a dword)
-    static constexpr int BYTES = WD + 128 * 4;
+    static constexpr int WD = WQ + 128 * PAY;        // (Q8_0) 128 weight scales (fp16 in the low half of a dword)
+    static constexpr int BYTES = WD + (SG ? 0 : 128 * 4);
+    static constexpr int SR = MMA_RING * BYTES;      // (Q4_0) scale ring: [2 groups][4 waves][32 rows][8 fp16]
+    static constexpr int LDS = SR + (SG ? 2 * 4 * 512 : 0);
 };
 
 // byte offset of (token t, 16-byte part q) in a slot's activation rows
@@ -139,19 +147,28 @@ __device__ __forceinline__ void mma_tile(const MmaArgs& g, const Tile& tl, int c
     const uint32_t vwq = PAY == 16 ? (32 * half + r32) * 16 : (32 * half + (lane >> 1)) * 32 + 16 * (lane & 1);
     const uint32_t vwd = (uint32_t)g.sc_off + (32 * half + r32) * 16;
 
-    // block b (clamped: past the end a harmless reload) into ring slot S = b % MMA_RING
+    // block b (clamped: past the end a harmless reload) into ring slot S = b % MMA_RING; with SG, at the
+    // first block of each group of 8 (before the block's own loads, so it lands first) the group's weight
+    // scales into scale slot (b / 8) % 2, whose previous group ended eight blocks earlier
     auto issue = [&](auto SC, int b) {
         constexpr int S = decltype(SC)::value;
         const uint32_t bc = (uint32_t)min(b, nb - 1);
         unsigned char* slot = ring + S * SL::BYTES;
         const uint32_t sx = bc * xstep;
+        if constexpr (SL::SG) {
+            if ((b & 7) == 0 && h == 0)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    r_w, (lds_void_t)(ring + SL::SR + ((b >> 3) & 1) * 2048 + 512 * wave), 16, vwd,
+                    (uint32_t)min(b >> 3, (nb - 1) >> 3) * 1024, 0, 0);
+        }
         __builtin_amdgcn_raw_ptr_buffer_load_lds(r_act, (lds_void_t)(slot + SL::ACT + (2 * wave) * 1024), 16, vx[0], sx, 0, 0);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(r_act, (lds_void_t)(slot + SL::ACT + (2 * wave + 1) * 1024), 16, vx[1], sx,
                                                  0, 0);
         if (h == 0) {
             __builtin_amdgcn_raw_ptr_buffer_load_lds(r_ds, (lds_void_t)(slot + SL::ADX + 128 * wave), 4, vds, bc * dstep, 0, 0);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(r_w, (lds_void_t)(slot + SL::WD + 128 * wave), 2, vwd,
-                                                     (bc >> 3) * 1024 + (bc & 7) * 2, 0, 0);
+            if constexpr (!SL::SG)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(r_w, (lds_void_t)(slot + SL::WD + 128 * wave), 2, vwd,
+                                                         (bc >> 3) * 1024 + (bc & 7) * 2, 0, 0);
         }
         if (PAY == 32 || h == 0)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(r_w, (lds_void_t)(slot + SL::WQ + 32 * PAY * wave), 16, vwq,
@@ -168,17 +185,24 @@ __device__ __forceinline__ void mma_tile(const MmaArgs& g, const Tile& tl, int c
 
     // the lane's LDS read addresses in slot 0 (slot S: + S * BYTES in the immediate offset)
     static_assert(3 * SL::BYTES + SL::WD + 128 * 4 < 65536, "ring offsets fit the LDS immediate");
+    // the weight scale of block b: the ring slot's (Q8_0) or the scale ring's (Q4_0: a VGPR offset per block)
+    const uint32_t A_SG = ring0 + SL::SR + 512 * wave + 16 * r32;
+    auto wd_read = [&](auto SC, int b) -> uint32_t {
+        if constexpr (SL::SG) return ds_ru16<0>(A_SG + (uint32_t)(((b >> 3) & 1) * 2048 + (b & 7) * 2));
+        else return ds_ru16<decltype(SC)::value * SL::BYTES>(ring0 + SL::WD + 128 * wave + 4 * r32);
+    };
     const uint32_t A_B0 = ring0 + SL::ACT + act_off(r32, h), A_B1 = ring0 + SL::ACT + act_off(r32, 2 + h);
     const uint32_t A_DX = ring0 + SL::ADX + 4 * r32;
     const uint32_t A_WQ = ring0 + SL::WQ + 32 * PAY * wave + PAY * r32 + 8 * h;
-    const uint32_t A_WD = ring0 + SL::WD + 128 * wave + 4 * r32;
 
     // block b has landed once at most the two later blocks' loads are outstanding; the barrier then
     // publishes it to every wave, and ends every wave's reads of the slot that issue(b + RING - 1)
     // refills (the slot of block b - 1)
     auto land = [&](auto SC, int b) {  // S = b % MMA_RING
         constexpr int S = decltype(SC)::value;
-        __builtin_amdgcn_s_waitcnt((MMA_DMA * (MMA_RING - 2)) | (0x7 << 4) | (0xF << 8));
+        // at most the two later blocks' loads outstanding (a scale-group load among them only makes the
+        // wait a little longer: it is older than its block's loads)
+        __builtin_amdgcn_s_waitcnt((SL::DMA * (MMA_RING - 2)) | (0x7 << 4) | (0xF << 8));
         __builtin_amdgcn_s_barrier();
         issue(ic<(S + MMA_RING - 1) % MMA_RING>{}, b + MMA_RING - 1);
     };
@@ -186,12 +210,12 @@ __device__ __forceinline__ void mma_tile(const MmaArgs& g, const Tile& tl, int c
     uint32_t wdv;
     u32x4 B0[2], B1[2];
     uint32_t dx[2];
-    // the block's first reads: weights, weight scale and tile 0's operands
-    auto start_reads = [&](auto SC) {
+    // block b's first reads: weights, weight scale and tile 0's operands
+    auto start_reads = [&](auto SC, int b) {
         constexpr int O = decltype(SC)::value * SL::BYTES;
         wq0 = ds_r64<O>(A_WQ);
         if (PAY == 32) wq1 = ds_r64<O + 16>(A_WQ);
-        wdv = ds_ru16<O>(A_WD);
+        wdv = wd_read(SC, b);
         B0[0] = ds_r128<O>(A_B0);
         B1[0] = ds_r128<O>(A_B1);
         dx[0] = ds_r32<O>(A_DX);
@@ -244,7 +268,7 @@ __device__ __forceinline__ void mma_tile(const MmaArgs& g, const Tile& tl, int c
                 // the next block lands and its first reads go out behind this block's last chain (after
                 // the last block: a harmless extra barrier and reads of a slot nobody uses)
                 land(ic<S1>{}, b + 1);
-                start_reads(ic<S1>{});
+                start_reads(ic<S1>{}, b + 1);
             }
             // keep the program order: the reads ahead of the chain, the chain before the next column
             __builtin_amdgcn_sched_barrier(0);
@@ -264,7 +288,7 @@ __device__ __forceinline__ void mma_tile(const MmaArgs& g, const Tile& tl, int c
         land(SC, b);
         u32x2 fq0 = ds_r64<O>(A_WQ), fq1 = {0u, 0u};
         if constexpr (PAY == 32) fq1 = ds_r64<O + 16>(A_WQ);
-        uint32_t fwd = ds_ru16<O>(A_WD);
+        uint32_t fwd = wd_read(SC, b);
         u32x4 fb0[NJ], fb1[NJ];
         uint32_t fdx[NJ];
         static_for<NJ>([&](auto JC) {
@@ -321,7 +345,7 @@ __device__ __forceinline__ void mma_tile(const MmaArgs& g, const Tile& tl, int c
         }
     } else {
         land(ic<0>{}, 0);
-        start_reads(ic<0>{});
+        start_reads(ic<0>{}, 0);
         start_wait();
         for (int b = 0; b < nb; b += 4) {
             block(ic<0>{}, b);
@@ -455,7 +479,7 @@ inline int xcd_tile_slots(int max_tiles) { return (max_tiles + 7) / 8 * 8; }
 template <int TYPE, bool FOLD>
 __global__ __launch_bounds__(256, 3) void k_grouped_mfma(MmaArgs g)
 {
-    __shared__ __align__(16) unsigned char ring[MMA_RING * MmaSlot<TYPE>::BYTES];
+    __shared__ __align__(16) unsigned char ring[MmaSlot<TYPE>::LDS];
     int bx;
     const int tile = xcd_tile(&bx);
     if (tile >= *g.ntiles) return;  // uniform over the workgroup
