@@ -73,6 +73,10 @@ extern "C" {
                                   exact); the products differ from the CPU reference's chains by the operands'
                                   fp16 rounding, and the GELU-gated requant amplifies that where a value sits
                                   near a rounding boundary.  Decode-sized calls ignore it. */
+#define PHX_FLAG_KEEP_INTERMEDIATES 32u /* also store the gate and up products for phx_moe_get_intermediates
+                                           (debug; no counterpart in the reference).  The prefill-sized Q4_0 /
+                                           Q8_0 expert products feed their GELU-gated requant straight into the
+                                           down product and skip those stores without it. */
 
 typedef struct phx_moe_ctx phx_moe_ctx;
 
@@ -160,7 +164,9 @@ int phx_moe_ffn_noalloc(phx_moe_ctx* ctx, int layer, int T, float* x, const floa
 int phx_moe_get_routing(phx_moe_ctx* ctx, int32_t* ids, float* weights, int32_t* offsets, int32_t* perm, float* logits);
 
 /* Expert intermediates of the last call (debug; NULL skips): g, u [T*k][n_ff] gate/up products
- * and yd [T*k][d] the down products, in assignment order a = t*k + j. */
+ * and yd [T*k][d] the down products, in assignment order a = t*k + j.  g and u of a prefill-sized
+ * Q4_0 / Q8_0 call are kept only with PHX_FLAG_KEEP_INTERMEDIATES: asking for them after a call that
+ * skipped them returns PHX_ERR_ARG. */
 int phx_moe_get_intermediates(phx_moe_ctx* ctx, float* g, float* u, float* yd);
 
 /* Consecutive layers as one HIP graph (batched decode): each layer does phx_moe_ffn with

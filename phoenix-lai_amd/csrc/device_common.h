@@ -223,6 +223,25 @@ __device__ __forceinline__ uint32_t bias_pair(uint32_t w, int p, float bias)
     return __builtin_bit_cast(uint32_t, v);
 }
 
+// Four Q8_0 integers (bytes of qw) as fp16 halves: exact (signed bytes through the 1152 bias), or, for
+// the tolerance mode's operands, times the block scale d (an fp16 value: q * d is exact in float) and
+// rounded once to fp16.
+__device__ __forceinline__ uint2 int_q4(int qw)
+{
+    const uint32_t u = (uint32_t)qw ^ 0x80808080u;
+    return make_uint2(bias_pair(u, 0, 1152.0f), bias_pair(u, 1, 1152.0f));
+}
+__device__ __forceinline__ uint32_t fold_pair(int q0, int q1, float d)
+{
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)((float)q0 * d)) |
+           ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)((float)q1 * d)) << 16);
+}
+__device__ __forceinline__ uint2 fold_q4(int qw, float d)
+{
+    return make_uint2(fold_pair((int8_t)(qw & 0xFF), (int8_t)((qw >> 8) & 0xFF), d),
+                      fold_pair((int8_t)((qw >> 16) & 0xFF), (int8_t)(qw >> 24), d));
+}
+
 // Q8_0 of one 32-block held as 4 consecutive values per lane by an 8-lane group (lane l of the group:
 // elements 4l..4l+3), CpuRef.QuantizeQ8_0 (src/CpuRef.cs:49-62): amax, d = amax / 127, id = 1 / d,
 // q = roundf(x * id) (half away from zero), fp16 d.  Returns the lane's 4 q bytes as one dword (the

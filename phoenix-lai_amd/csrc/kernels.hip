@@ -84,11 +84,8 @@ __device__ void quantize_row(const float* v, Act act, int64_t row)
             const int qw = q8_0_oct(xv, &dval, &sum);
             if (b < nb) {
                 if (act.q) ((int*)(act.q + row * act.qstride))[8 * b + l8] = qw;
-                if (act.qh) {  // the four integers as exact fp16 (signed bytes through the 1152 bias)
-                    const uint32_t u = (uint32_t)qw ^ 0x80808080u;
-                    *(uint2*)(act.qh + row * act.qhstride + 32 * b + 4 * l8) =
-                        make_uint2(bias_pair(u, 0, 1152.0f), bias_pair(u, 1, 1152.0f));
-                }
+                if (act.qh)  // the four integers as exact fp16, or folded with the block scale
+                    *(uint2*)(act.qh + row * act.qhstride + 32 * b + 4 * l8) = act.fold ? fold_q4(qw, dval) : int_q4(qw);
                 if (l8 == 0) {
                     act.d[row * act.dstride + b] = dval;
                     if (act.s) act.s[row * act.sstride + b] = sum;

@@ -579,13 +579,12 @@ __device__ __forceinline__ uint4 sel_key(double L, double B, int e)
 constexpr int RT_PER = 4, RT_MAXW = 16;  // elements per thread, waves per workgroup at most
 __host__ __device__ inline int route_threads(int d) { return d / RT_PER; }
 
-// the matrix-core kernels' copy of a Q8_0 activation dword (four integers as exact fp16, signed bytes
-// through the 1152 bias), for the general path's rows when it routes through this kernel
-__device__ __forceinline__ void store_qh(const Act& act, int t, int b, int l8, int qw)
+// the matrix-core kernels' copy of a Q8_0 activation dword (four integers as exact fp16, or folded with
+// the block scale dval for the tolerance mode), for the general path's rows when it routes through this
+// kernel
+__device__ __forceinline__ void store_qh(const Act& act, int t, int b, int l8, int qw, float dval)
 {
-    const uint32_t u = (uint32_t)qw ^ 0x80808080u;
-    *(uint2*)(act.qh + (int64_t)t * act.qhstride + 32 * b + 4 * l8) =
-        make_uint2(bias_pair(u, 0, 1152.0f), bias_pair(u, 1, 1152.0f));
+    *(uint2*)(act.qh + (int64_t)t * act.qhstride + 32 * b + 4 * l8) = act.fold ? fold_q4(qw, dval) : int_q4(qw);
 }
 
 template <int PER, bool FUSED>
@@ -713,7 +712,7 @@ __device__ __forceinline__ void route_wg(const DecArgs& a, int t, int e, float* 
                                             (xq.w * rinv) * nv.w),
                                 &dval, &sum);
         ((int*)(a.agu.q + (int64_t)t * a.agu.qstride))[8 * b + l8] = qw;
-        if (a.agu.qh) store_qh(a.agu, t, b, l8, qw);
+        if (a.agu.qh) store_qh(a.agu, t, b, l8, qw, dval);
         if (l8 == 0) {
             a.agu.d[(int64_t)t * a.agu.dstride + b] = dval;
             a.agu.s[(int64_t)t * a.agu.sstride + b] = sum;
@@ -723,7 +722,7 @@ __device__ __forceinline__ void route_wg(const DecArgs& a, int t, int e, float* 
                                                 (xq.w * rinv) * fv.w),
                                     &dval, &sum);
             ((int*)(a.ash.q + (int64_t)t * a.ash.qstride))[8 * b + l8] = qs;
-            if (a.ash.qh) store_qh(a.ash, t, b, l8, qs);
+            if (a.ash.qh) store_qh(a.ash, t, b, l8, qs, dval);
             if (l8 == 0) {
                 a.ash.d[(int64_t)t * a.ash.dstride + b] = dval;
                 a.ash.s[(int64_t)t * a.ash.sstride + b] = sum;

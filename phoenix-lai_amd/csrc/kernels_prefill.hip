@@ -106,12 +106,7 @@ __device__ __forceinline__ uint32_t act_off(int t, int q)
 }
 
 // One workgroup's tile: NJ active 32-token column tiles (1..4).  ring: the workgroup's LDS ring.
-// FOLD (the tolerance mode, PHX_FLAG_FAST_MATH): the block scales are folded into the operands as fp16
-// products, (q_w - 8) * d_w and q_x * d_x, each rounded once to fp16, and the whole row accumulates on the
-// matrix cores in fp32: two MFMAs per block and column tile, no scale MFMA and no per-block VALU chain.
-// The results then differ from the reference chain by the operands' fp16 rounding (about 2^-12 of each
-// term), not bit for bit.
-template <int TYPE, int NJ, bool FOLD>
+template <int TYPE, int NJ>
 __device__ __forceinline__ void mma_tile(const MmaArgs& g, const Tile& tl, int cnt, unsigned char* ring, int bx)
 {
     using SL = MmaSlot<TYPE>;
@@ -281,78 +276,19 @@ __device__ __forceinline__ void mma_tile(const MmaArgs& g, const Tile& tl, int c
         });
     };
 
-    // the tolerance mode's block: land it, read the row scale, the weights and every column tile's
-    // operands, wait once, fold the scales into fp16 operands and accumulate on the matrix cores
-    auto fold_block = [&](auto SC, int b) {
-        constexpr int O = decltype(SC)::value * SL::BYTES;
-        land(SC, b);
-        u32x2 fq0 = ds_r64<O>(A_WQ), fq1 = {0u, 0u};
-        if constexpr (PAY == 32) fq1 = ds_r64<O + 16>(A_WQ);
-        uint32_t fwd = wd_read(SC, b);
-        u32x4 fb0[NJ], fb1[NJ];
-        uint32_t fdx[NJ];
-        static_for<NJ>([&](auto JC) {
-            constexpr int j = decltype(JC)::value;
-            fb0[j] = ds_r128<O + 2048 * j>(A_B0);
-            fb1[j] = ds_r128<O + 2048 * j>(A_B1);
-            fdx[j] = ds_r32<O + 128 * j>(A_DX);
-        });
-        if constexpr (PAY == 32) asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(fq0), "+v"(fq1), "+v"(fwd)::"memory");
-        else asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(fq0), "+v"(fwd)::"memory");
-        static_for<NJ>([&](auto JC) {
-            constexpr int j = decltype(JC)::value;
-            lds_wait(fb0[j], fb1[j], fdx[j]);
-        });
-        const _Float16 dw = __builtin_bit_cast(_Float16, (uint16_t)fwd);
-        const mh8 dw8 = {dw, dw, dw, dw, dw, dw, dw, dw};
-        mh8 A0, A1;
-        if (TYPE == PHX_Q4_0_DEV) {
-            A0 = bias8(fq0.x & 0x0F0F0F0Fu, fq0.y & 0x0F0F0F0Fu, 1032.0f) * dw8;
-            A1 = bias8((fq0.x >> 4) & 0x0F0F0F0Fu, (fq0.y >> 4) & 0x0F0F0F0Fu, 1032.0f) * dw8;
-        } else {
-            A0 = bias8(fq0.x ^ 0x80808080u, fq0.y ^ 0x80808080u, 1152.0f) * dw8;
-            A1 = bias8(fq1.x ^ 0x80808080u, fq1.y ^ 0x80808080u, 1152.0f) * dw8;
-        }
-        mh8 X[NJ];
-        static_for<NJ>([&](auto JC) {  // the token scales are fp16 values: the conversions are exact
-            constexpr int j = decltype(JC)::value;
-            const _Float16 xs = (_Float16)__uint_as_float(fdx[j]);
-            X[j] = mh8{xs, xs, xs, xs, xs, xs, xs, xs};
-        });
-        // the low halves of every column tile, then the high halves: a column's two products are NJ
-        // MFMAs apart
-        static_for<NJ>([&](auto JC) {
-            constexpr int j = decltype(JC)::value;
-            S[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A0, __builtin_bit_cast(mh8, fb0[j]) * X[j], S[j], 0, 0, 0);
-        });
-        static_for<NJ>([&](auto JC) {
-            constexpr int j = decltype(JC)::value;
-            S[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A1, __builtin_bit_cast(mh8, fb1[j]) * X[j], S[j], 0, 0, 0);
-        });
-    };
-
     issue(ic<0>{}, 0);
     issue(ic<1>{}, 1);
     issue(ic<2>{}, 2);
     // the ring's slots by unrolling: every LDS offset is an immediate
     static_assert(MMA_RING == 4, "the block loop is unrolled by the ring size");
-    if constexpr (FOLD) {
-        for (int b = 0; b < nb; b += 4) {
-            fold_block(ic<0>{}, b);
-            if (b + 1 < nb) fold_block(ic<1>{}, b + 1);
-            if (b + 2 < nb) fold_block(ic<2>{}, b + 2);
-            if (b + 3 < nb) fold_block(ic<3>{}, b + 3);
-        }
-    } else {
-        land(ic<0>{}, 0);
-        start_reads(ic<0>{}, 0);
-        start_wait();
-        for (int b = 0; b < nb; b += 4) {
-            block(ic<0>{}, b);
-            if (b + 1 < nb) block(ic<1>{}, b + 1);
-            if (b + 2 < nb) block(ic<2>{}, b + 2);
-            if (b + 3 < nb) block(ic<3>{}, b + 3);
-        }
+    land(ic<0>{}, 0);
+    start_reads(ic<0>{}, 0);
+    start_wait();
+    for (int b = 0; b < nb; b += 4) {
+        block(ic<0>{}, b);
+        if (b + 1 < nb) block(ic<1>{}, b + 1);
+        if (b + 2 < nb) block(ic<2>{}, b + 2);
+        if (b + 3 < nb) block(ic<3>{}, b + 3);
     }
     // the loads issued past the last block land in this workgroup's LDS: let them finish before it ends
     __builtin_amdgcn_s_waitcnt(0);
@@ -423,8 +359,9 @@ __device__ __forceinline__ void mma_tile(const MmaArgs& g, const Tile& tl, int c
         }
     }
 
-    // results: lane holds rows i_q = 8 (q / 4) + 4 h + (q % 4) of the wave's 32, token column r32
-    if (!live) return;
+    // results: lane holds rows i_q = 8 (q / 4) + 4 h + (q % 4) of the wave's 32, token column r32 (a
+    // paired launch without g and u outputs ends with its requant)
+    if (!live || (g.paired && !g.out0)) return;
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
         const int sidx = 32 * j + r32;
@@ -476,7 +413,7 @@ __device__ __forceinline__ int xcd_tile(int* bx)
 }
 inline int xcd_tile_slots(int max_tiles) { return (max_tiles + 7) / 8 * 8; }
 
-template <int TYPE, bool FOLD>
+template <int TYPE>
 __global__ __launch_bounds__(256, 3) void k_grouped_mfma(MmaArgs g)
 {
     __shared__ __align__(16) unsigned char ring[MmaSlot<TYPE>::LDS];
@@ -492,10 +429,333 @@ __global__ __launch_bounds__(256, 3) void k_grouped_mfma(MmaArgs g)
     if (threadIdx.x == 0 && wgf < 8192) phx_tl[tbase + 2 * wgf] = wall_clock64();
 #endif
     switch ((cnt + 31) / 32) {  // active 32-token column tiles
-    case 1: mma_tile<TYPE, 1, FOLD>(g, tl, cnt, ring, bx); break;
-    case 2: mma_tile<TYPE, 2, FOLD>(g, tl, cnt, ring, bx); break;
-    case 3: mma_tile<TYPE, 3, FOLD>(g, tl, cnt, ring, bx); break;
-    default: mma_tile<TYPE, 4, FOLD>(g, tl, cnt, ring, bx); break;
+    case 1: mma_tile<TYPE, 1>(g, tl, cnt, ring, bx); break;
+    case 2: mma_tile<TYPE, 2>(g, tl, cnt, ring, bx); break;
+    case 3: mma_tile<TYPE, 3>(g, tl, cnt, ring, bx); break;
+    default: mma_tile<TYPE, 4>(g, tl, cnt, ring, bx); break;
+    }
+#ifdef PHX_TIMELINE
+    if (threadIdx.x == 0 && wgf < 8192) phx_tl[tbase + 2 * wgf + 1] = wall_clock64();
+#endif
+}
+
+// ---------------------------------------------------------------------------- tolerance mode
+// The products of PHX_FLAG_FAST_MATH, after the reference's own GPU prefill (src/KernelsCoop.cs:1-11:
+// weights dequantized to f16, f16 activations, f32 accumulation over the whole row on the matrix
+// units): the block scales are folded into the operands, (q_w - 8) * d_w (Q4_0) or q_w * d_w (Q8_0) and
+// q_x * d_x, each rounded once to fp16, and every row accumulates in fp32 across all its blocks: two
+// v_mfma_f32_32x32x16_f16 per block and (32-row, 32-token) tile, no per-block VALU chain.  Results then
+// differ from the CPU reference by the operands' fp16 rounding (about 2^-12 of each term).
+//
+// Work layout: a workgroup of four waves covers four row groups (256 rows; wave w: row group 4 x + w,
+// both of its 32-row halves: gate and up of a paired row group) and one tile of up to 128 assignments,
+// so each block of the tile's activations leaves L2 once per 256 rows.  Per block every wave issues the
+// same direct loads into a ring slot (its share of the activations and their scales, its row group's
+// payload and, for Q8_0, its scales; Q4_0 scales come once per 8 blocks into a two-slot scale ring),
+// MMA_RING - 1 blocks ahead; after one barrier per block a wave reads its two weight tiles and the
+// tile's activation operands, folds the scales (fp16 products) and issues 4 NJ MFMAs, each column
+// tile's two k-halves 2 NJ MFMAs apart.  Two workgroups per CU (two waves per SIMD: 128 accumulator
+// registers per wave) take turns between the matrix cores and the reads and folds.  A paired launch's
+// wave holds gate and up of the same 32 columns, so the GELU-gated Q8_0 requant of the down input runs
+// in its registers.
+template <int TYPE>
+struct CoopSlot {
+    static constexpr int PAY = TYPE == PHX_Q4_0_DEV ? 16 : 32;
+    static constexpr bool SG = TYPE == PHX_Q4_0_DEV;
+    static constexpr int WL = PAY / 16;                // payload loads per wave and block (1 KB each)
+    static constexpr int DMA = 2 + WL + (SG ? 0 : 1);  // activations 2, payload, Q8_0 scales
+    static constexpr int ACT = 0;                      // 128 tokens x 64 B (folded fp16), swizzled 16-token groups
+    static constexpr int WQ = ACT + MMA_TOK * 64;      // [wave][64 rows][PAY]
+    static constexpr int WD = WQ + 4 * 64 * PAY;       // (Q8_0) [wave][64 rows] fp16 in the low half of a dword
+    static constexpr int BYTES = WD + (SG ? 0 : 4 * 64 * 4);
+    static constexpr int SR = MMA_RING * BYTES;        // (Q4_0) scale ring [2 groups][4 waves][64 rows][8 fp16]
+    static constexpr int LDS = SR + (SG ? 2 * 4 * 1024 : 0);
+};
+
+template <int TYPE, int NJ>
+__device__ __forceinline__ void coop_tile(const MmaArgs& g, const Tile& tl, int cnt, unsigned char* ring, int bx)
+{
+    using SL = CoopSlot<TYPE>;
+    constexpr int PAY = SL::PAY;
+    const int tid = threadIdx.x, lane = tid & 63, r32 = lane & 31, h = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int gI = bx * 4 + wave;
+    const bool live = gI < g.rg;  // a wave past the last row group loads its share and multiplies nothing
+    const int nb = g.nb;
+    const uint32_t ring0 = (uint32_t)(uintptr_t)(lds_void_t)ring;
+
+    const bool lst = g.npos > 0;
+    const uint32_t xstep = lst ? (uint32_t)g.npos * 64u : 64u;  // bytes per block
+    // activation rows of tokens 32 w + 16 i + lane / 4, part (lane % 4) ^ (lane / 16)
+    uint32_t vx[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int t = min(32 * wave + 16 * i + (lane >> 2), cnt - 1);  // past cnt: a valid row, never stored
+        const int q = (lane & 3) ^ ((lane >> 4) & 3);
+        const int64_t row = lst ? (int64_t)(tl.start + t) * 32 : (int64_t)(g.perm[tl.start + t] / g.act_div) * g.act.qhstride;
+        vx[i] = (uint32_t)(2 * (row + 8 * q));
+    }
+    const int gIc = min(gI, g.rg - 1);
+    const __amdgpu_buffer_rsrc_t r_act = buf_rsrc(g.act.qh);
+    const __amdgpu_buffer_rsrc_t r_w = buf_rsrc(g.payload + tl.e * g.mat_pay + gIc * g.rg_pay);
+    const uint32_t vwq = 16 * lane;                           // payload: the row group's block, 1 KB per load
+    const uint32_t vwd = (uint32_t)g.sc_off + 16 * lane;      // scales of row `lane`: (b / 8, row) * 16 + (b % 8) * 2
+
+    auto issue = [&](auto SC, int b) {
+        constexpr int S = decltype(SC)::value;
+        const uint32_t bc = (uint32_t)min(b, nb - 1);
+        unsigned char* slot = ring + S * SL::BYTES;
+        const uint32_t sx = bc * xstep;
+        if constexpr (SL::SG) {
+            if ((b & 7) == 0)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(r_w, (lds_void_t)(ring + SL::SR + ((b >> 3) & 1) * 4096 + 1024 * wave),
+                                                         16, vwd, (uint32_t)min(b >> 3, (nb - 1) >> 3) * 1024, 0, 0);
+        }
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r_act, (lds_void_t)(slot + SL::ACT + (2 * wave) * 1024), 16, vx[0], sx, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r_act, (lds_void_t)(slot + SL::ACT + (2 * wave + 1) * 1024), 16, vx[1], sx,
+                                                 0, 0);
+        if constexpr (!SL::SG)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(r_w, (lds_void_t)(slot + SL::WD + 256 * wave), 2, vwd,
+                                                     (bc >> 3) * 1024 + (bc & 7) * 2, 0, 0);
+#pragma unroll
+        for (int i = 0; i < SL::WL; i++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(r_w, (lds_void_t)(slot + SL::WQ + 64 * PAY * wave + 1024 * i), 16, vwq,
+                                                     bc * 64 * PAY + 1024 * i, 0, 0);
+    };
+    auto land = [&](auto SC, int b) {  // S = b % MMA_RING (see mma_tile)
+        constexpr int S = decltype(SC)::value;
+        __builtin_amdgcn_s_waitcnt((SL::DMA * (MMA_RING - 2)) | (0x7 << 4) | (0xF << 8));
+        __builtin_amdgcn_s_barrier();
+        issue(ic<(S + MMA_RING - 1) % MMA_RING>{}, b + MMA_RING - 1);
+    };
+
+    mf16 C[2][NJ];
+#pragma unroll
+    for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+#pragma unroll
+            for (int q = 0; q < 16; q++) C[t][j][q] = 0.0f;
+
+    static_assert(3 * SL::BYTES + 3 * 2048 + 1024 + 64 < 65536, "ring offsets fit the LDS immediate");
+    // lane (r32, h) of tile t: row 32 t + r32 of the wave's row group, k values 8 h .. 8 h + 7 (A0) and
+    // 16 + 8 h .. (A1); the activations as in mma_tile
+    const uint32_t A_WQ = ring0 + SL::WQ + 64 * PAY * wave + PAY * r32 + 8 * h;
+    const uint32_t A_SG = ring0 + SL::SR + 1024 * wave + 16 * r32;
+    const uint32_t A_WD = ring0 + SL::WD + 256 * wave + 4 * r32;
+    const uint32_t A_B0 = ring0 + SL::ACT + act_off(r32, h), A_B1 = ring0 + SL::ACT + act_off(r32, 2 + h);
+
+    // a block's operands as read from LDS (valid after `landed`, in the reads' basic block)
+    u32x2 q[2][SL::WL];
+    uint32_t wd[2];
+    u32x4 fb0[NJ], fb1[NJ];
+    auto reads = [&](auto SC, int b) {  // block b in slot S
+        constexpr int O = decltype(SC)::value * SL::BYTES;
+        q[0][0] = ds_r64<O>(A_WQ);
+        q[1][0] = ds_r64<O + 32 * PAY>(A_WQ);
+        if constexpr (PAY == 32) {
+            q[0][SL::WL - 1] = ds_r64<O + 16>(A_WQ);
+            q[1][SL::WL - 1] = ds_r64<O + 32 * PAY + 16>(A_WQ);
+        }
+        if constexpr (SL::SG) {
+            const uint32_t a = A_SG + (uint32_t)(((b >> 3) & 1) * 4096 + (b & 7) * 2);
+            wd[0] = ds_ru16<0>(a);
+            wd[1] = ds_ru16<512>(a);
+        } else {
+            wd[0] = ds_ru16<O>(A_WD);
+            wd[1] = ds_ru16<O + 128>(A_WD);
+        }
+        static_for<NJ>([&](auto JC) {
+            constexpr int j = decltype(JC)::value;
+            fb0[j] = ds_r128<O + 2048 * j>(A_B0);
+            fb1[j] = ds_r128<O + 2048 * j>(A_B1);
+        });
+    };
+    auto landed = [&]() {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+#pragma unroll
+            for (int i = 0; i < SL::WL; i++) tie(q[t][i]);
+            tie(wd[t]);
+        }
+        static_for<NJ>([&](auto JC) {
+            constexpr int j = decltype(JC)::value;
+            tie(fb0[j]);
+            tie(fb1[j]);
+        });
+    };
+
+    // block b (slot S, its operands read and landed): fold them, then land block b + 1 and issue its
+    // reads, then this block's MFMAs, which cover the reads' latency, then wait for the reads (after the
+    // last block: a harmless extra barrier and reads of a slot nobody uses)
+    auto block = [&](auto SC, int b) {
+        constexpr int S1 = (decltype(SC)::value + 1) % MMA_RING;
+        mh8 A0[2], A1[2], X0[NJ], X1[NJ];
+        if (live) {  // uniform
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                const _Float16 dw = __builtin_bit_cast(_Float16, (uint16_t)wd[t]);
+                const mh8 dw8 = {dw, dw, dw, dw, dw, dw, dw, dw};
+                if (TYPE == PHX_Q4_0_DEV) {
+                    A0[t] = bias8(q[t][0].x & 0x0F0F0F0Fu, q[t][0].y & 0x0F0F0F0Fu, 1032.0f) * dw8;
+                    A1[t] = bias8((q[t][0].x >> 4) & 0x0F0F0F0Fu, (q[t][0].y >> 4) & 0x0F0F0F0Fu, 1032.0f) * dw8;
+                } else {
+                    A0[t] = bias8(q[t][0].x ^ 0x80808080u, q[t][0].y ^ 0x80808080u, 1152.0f) * dw8;
+                    A1[t] = bias8(q[t][SL::WL - 1].x ^ 0x80808080u, q[t][SL::WL - 1].y ^ 0x80808080u, 1152.0f) * dw8;
+                }
+            }
+            static_for<NJ>([&](auto JC) {  // the activations arrive folded
+                constexpr int j = decltype(JC)::value;
+                X0[j] = __builtin_bit_cast(mh8, fb0[j]);
+                X1[j] = __builtin_bit_cast(mh8, fb1[j]);
+            });
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        land(ic<S1>{}, b + 1);
+        if (live) {
+            reads(ic<S1>{}, b + 1);
+            __builtin_amdgcn_sched_barrier(0);
+            static_for<NJ>([&](auto JC) {
+                constexpr int j = decltype(JC)::value;
+                C[0][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A0[0], X0[j], C[0][j], 0, 0, 0);
+                C[1][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A0[1], X0[j], C[1][j], 0, 0, 0);
+            });
+            static_for<NJ>([&](auto JC) {
+                constexpr int j = decltype(JC)::value;
+                C[0][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A1[0], X1[j], C[0][j], 0, 0, 0);
+                C[1][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A1[1], X1[j], C[1][j], 0, 0, 0);
+            });
+            __builtin_amdgcn_sched_barrier(0);
+            landed();  // in the reads' basic block: the loop carries landed values
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    issue(ic<0>{}, 0);
+    issue(ic<1>{}, 1);
+    issue(ic<2>{}, 2);
+    static_assert(MMA_RING == 4, "the block loop is unrolled by the ring size");
+    land(ic<0>{}, 0);
+    if (live) {
+        reads(ic<0>{}, 0);
+        landed();
+    }
+    for (int b = 0; b < nb; b += 4) {
+        block(ic<0>{}, b);
+        if (b + 1 < nb) block(ic<1>{}, b + 1);
+        if (b + 2 < nb) block(ic<2>{}, b + 2);
+        if (b + 3 < nb) block(ic<3>{}, b + 3);
+    }
+    // the loads issued past the last block land in this workgroup's LDS: let them finish before it ends
+    __builtin_amdgcn_s_waitcnt(0);
+    if (!live) return;
+
+    // lane (r32, h) holds, for token column r32 of tile j, rows 8 (q / 4) + 4 h + q % 4 of each half
+    if (g.qout.qh) {  // uniform: the GELU-gated Q8_0 requant of the down input (src/GemmaCpu.cs:415, src/CpuRef.cs:49-62)
+        float tv[NJ][16];
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+#pragma unroll
+            for (int q = 0; q < 16; q++) tv[j][q] = g.gelu_tab[f2h_bits(C[0][j][q])];
+        const Act& o = g.qout;
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            float e[16], am = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 16; q++) {
+                const float v = C[0][j][q];
+                const float gl = v <= -10.0f ? 0.0f : (v >= 10.0f ? v : tv[j][q]);
+                const int col = gI * 32 + 8 * (q >> 2) + 4 * h + (q & 3);
+                e[q] = col < g.split ? gl * C[1][j][q] : 0.0f;
+                am = fmaxf(am, fabsf(e[q]));
+            }
+            am = fmaxf(am, __shfl_xor(am, 32, 64));  // the other 16 columns: lane r32 + 32 (1 - 2 h)
+            const float dd = am / 127.0f;
+            const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
+            const float dv = h2f(f2h_bits(dd));  // the block's fp16 scale
+            uint32_t w[4][2];
+#pragma unroll
+            for (int g4 = 0; g4 < 4; g4++) {
+                const int q0 = (int)roundf(e[4 * g4] * id), q1 = (int)roundf(e[4 * g4 + 1] * id),
+                          q2 = (int)roundf(e[4 * g4 + 2] * id), q3 = (int)roundf(e[4 * g4 + 3] * id);
+                w[g4][0] = fold_pair(q0, q1, dv);  // the down product's operands, folded
+                w[g4][1] = fold_pair(q2, q3, dv);
+            }
+            const uint32_t s0 = h ? w[0][0] : w[2][0], s1 = h ? w[0][1] : w[2][1];
+            const uint32_t s2 = h ? w[1][0] : w[3][0], s3 = h ? w[1][1] : w[3][1];
+            const uint32_t p0 = (uint32_t)__shfl_xor((int)s0, 32, 64), p1 = (uint32_t)__shfl_xor((int)s1, 32, 64);
+            const uint32_t p2 = (uint32_t)__shfl_xor((int)s2, 32, 64), p3 = (uint32_t)__shfl_xor((int)s3, 32, 64);
+            const uint4 lo = h ? make_uint4(p0, p1, w[2][0], w[2][1]) : make_uint4(w[0][0], w[0][1], p0, p1);
+            const uint4 hi = h ? make_uint4(p2, p3, w[3][0], w[3][1]) : make_uint4(w[1][0], w[1][1], p2, p3);
+            const int sidx = 32 * j + r32;
+            if (sidx < cnt) {
+                const int64_t pos = (int64_t)gI * g.qnpos + tl.start + sidx;
+                uint16_t* hq = o.qh + pos * 32 + 16 * h;
+                *(uint4*)hq = lo;
+                *(uint4*)(hq + 8) = hi;
+                if (h == 0) o.d[pos] = h2f(f2h_bits(dd));
+            }
+        }
+    }
+
+    if (g.paired && !g.out0) return;  // no g and u outputs: the requant above was the product's output
+    const bool vec = (g.out_stride & 3) == 0;
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const int sidx = 32 * j + r32;
+        if (sidx >= cnt) continue;
+        const int64_t a = g.perm[tl.start + sidx];
+#pragma unroll
+        for (int half = 0; half < 2; half++)
+#pragma unroll
+            for (int q4 = 0; q4 < 4; q4++) {
+                const int lg0 = half * 32 + 8 * q4 + 4 * h;  // lane within the row group of the first of four
+                const float4 v = make_float4(C[half][j][4 * q4], C[half][j][4 * q4 + 1], C[half][j][4 * q4 + 2],
+                                             C[half][j][4 * q4 + 3]);
+                if (g.paired) {
+                    const int col = gI * 32 + (lg0 & 31);
+                    float* dst = (half ? g.out1 : g.out0) + a * g.out_stride + col;
+                    if (vec && col + 3 < g.split) *(float4*)dst = v;
+                    else
+#pragma unroll
+                        for (int i = 0; i < 4; i++)
+                            if (col + i < g.split) dst[i] = C[half][j][4 * q4 + i];
+                } else {
+                    const int row = gI * 64 + lg0;
+                    if (vec && row + 3 < min(g.rows, g.split)) *(float4*)(g.out0 + a * g.out_stride + row) = v;
+                    else
+#pragma unroll
+                        for (int i = 0; i < 4; i++) {
+                            const int r = row + i;
+                            if (r < g.rows) {
+                                if (r < g.split) g.out0[a * g.out_stride + r] = C[half][j][4 * q4 + i];
+                                else g.out1[a * g.out_stride + r - g.split] = C[half][j][4 * q4 + i];
+                            }
+                        }
+                }
+            }
+    }
+}
+
+template <int TYPE>
+__global__ __launch_bounds__(256, 2) void k_grouped_coop(MmaArgs g)
+{
+    __shared__ __align__(16) unsigned char ring[CoopSlot<TYPE>::LDS];
+    int bx;
+    const int tile = xcd_tile(&bx);
+    if (tile >= *g.ntiles) return;  // uniform over the workgroup
+    const Tile tl = g.tiles[tile];
+    const int cnt = min(tl.cnt, MMA_TOK);
+#ifdef PHX_TIMELINE
+    const int wgf = tile * gridDim.x + bx, tbase = g.paired ? 0 : 16384;  // as in k_grouped_mfma
+    if (threadIdx.x == 0 && wgf < 8192) phx_tl[tbase + 2 * wgf] = wall_clock64();
+#endif
+    switch ((cnt + 31) / 32) {  // active 32-token column tiles
+    case 1: coop_tile<TYPE, 1>(g, tl, cnt, ring, bx); break;
+    case 2: coop_tile<TYPE, 2>(g, tl, cnt, ring, bx); break;
+    case 3: coop_tile<TYPE, 3>(g, tl, cnt, ring, bx); break;
+    default: coop_tile<TYPE, 4>(g, tl, cnt, ring, bx); break;
     }
 #ifdef PHX_TIMELINE
     if (threadIdx.x == 0 && wgf < 8192) phx_tl[tbase + 2 * wgf + 1] = wall_clock64();
@@ -504,7 +764,7 @@ __global__ __launch_bounds__(256, 3) void k_grouped_mfma(MmaArgs g)
 
 void launch_grouped_mfma(hipStream_t st, const QMat& w, Act act, const Tile* tiles, const int* ntiles, int max_tiles,
                          const int* perm, int act_div, float* out0, float* out1, int split, int out_stride,
-                         int64_t npos, const Act* qout, int64_t qnpos, const float* gelu_tab, bool fold)
+                         int64_t npos, const Act* qout, int64_t qnpos, const float* gelu_tab)
 {
     MmaArgs g;
     g.payload = w.payload;
@@ -530,11 +790,15 @@ void launch_grouped_mfma(hipStream_t st, const QMat& w, Act act, const Tile* til
     g.qout = qout && w.paired ? *qout : Act{};
     g.qnpos = qnpos;
     g.gelu_tab = gelu_tab;
+    if (act.fold) {  // the tolerance mode's folded operands (its gate|up writes the down input folded too)
+        const dim3 grid((w.rg + 3) / 4, xcd_tile_slots(max_tiles));
+        if (w.type == PHX_Q4_0_DEV) launch(k_grouped_coop<PHX_Q4_0_DEV>, grid, dim3(256), 0, st, g);
+        else launch(k_grouped_coop<PHX_Q8_0_DEV>, grid, dim3(256), 0, st, g);
+        return;
+    }
     const dim3 grid((w.rg + 1) / 2, xcd_tile_slots(max_tiles));
-    if (w.type == PHX_Q4_0_DEV)
-        launch(fold ? k_grouped_mfma<PHX_Q4_0_DEV, true> : k_grouped_mfma<PHX_Q4_0_DEV, false>, grid, dim3(256), 0, st, g);
-    else
-        launch(fold ? k_grouped_mfma<PHX_Q8_0_DEV, true> : k_grouped_mfma<PHX_Q8_0_DEV, false>, grid, dim3(256), 0, st, g);
+    if (w.type == PHX_Q4_0_DEV) launch(k_grouped_mfma<PHX_Q4_0_DEV>, grid, dim3(256), 0, st, g);
+    else launch(k_grouped_mfma<PHX_Q8_0_DEV>, grid, dim3(256), 0, st, g);
 }
 
 // ============================================================================ K-quant products

@@ -124,6 +124,8 @@ struct Act {
                              // element order, the K formats per super-block in the order [l][s][mm']:
                              // x(32 s + l + 8 {0, 2, 1, 3}[mm'])
     int64_t qhstride = 0;    // halves per row
+    bool fold = false;       // ACT_Q8_0 with qh: qh holds fp16(q * d), the block scale folded in (the
+                             // tolerance mode's operands), instead of the integers
     uint16_t* bh = nullptr;  // optional, K formats: the Q8_K block sums as fp16 [row][cols / 16]
     int64_t bhstride = 0;    // halves per row
 };
@@ -180,7 +182,7 @@ constexpr int kMmaTile = 128;
 void launch_grouped_mfma(hipStream_t st, const QMat& w, Act act, const Tile* tiles, const int* ntiles, int max_tiles,
                          const int* perm, int act_div, float* out0, float* out1, int split, int out_stride,
                          int64_t npos = 0, const Act* qout = nullptr, int64_t qnpos = 0,
-                         const float* gelu_tab = nullptr, bool fold = false);
+                         const float* gelu_tab = nullptr);
 // K-quant prefill path (kernels_prefill.hip): Q4_K / Q6_K grouped products on MFMA, tiles of up to
 // kKmmaTile assignments, activations' fp16 copies (qh; Q4_K also bh) in row order; arguments and outputs
 // as launch_grouped

@@ -385,6 +385,7 @@ struct phx_moe_ctx {
     hipGraphExec_t graph_exec = nullptr;
     hipGraph_t graph = nullptr;
     int graph_T = 0, graph_first = 0, graph_n = 0;
+    bool graph_gu_kept = true;  // the captured stack's last layer stores g and u
     // what the stack graph was captured over: each layer's upload generation and the workspace
     // pointers (a later upload or a workspace regrowth frees memory the graph still names)
     std::vector<uint64_t> graph_gens;
@@ -398,6 +399,7 @@ struct phx_moe_ctx {
     // the IQ codebooks expanded (iq_grids.h): IQ2_XXS 256 and IQ2_S 1024 64-bit words, IQ3_S 512 32-bit
     uint8_t* iq_grid = nullptr;
     bool last_scratch = false;
+    bool last_gu_kept = true;  // the last call stored the gate and up products (see keeps_gu)
     unsigned char* bump_base = nullptr;
     size_t bump_off = 0, bump_cap = 0;
     FaultPlan fault;  // PHX_FAULT, see phx_internal.h
@@ -835,17 +837,29 @@ bool cert_route(const Layer& L, int T, bool shared_ffn)
     return true;
 }
 
+// prefill-sized expert work (several assignments per expert on average) runs on the matrix cores, whose
+// kernels read the activations' fp16 copies
+static bool mma_path(const phx_moe_layer_desc& D, int T)
+{
+    return mfma_type(D.gate_up_type) && mfma_type(D.down_type) && T * D.n_used >= 8 * D.n_expert;
+}
+
+// whether a call stores the gate and up products for phx_moe_get_intermediates: the matrix-core Q4_0 /
+// Q8_0 products requantize gelu(g) * u in registers and store g and u only when asked to
+bool keeps_gu(phx_moe_ctx* c, const Layer& L, int T, unsigned flags)
+{
+    return (flags & PHX_FLAG_KEEP_INTERMEDIATES) || use_decode(c, L, T, flags) || !mma_path(L.desc, T);
+}
+
 int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, const float* shared, float* out, float* xres,
-                      bool exact, bool fast)
+                      bool exact, bool fast, bool keep)
 {
     const phx_moe_layer_desc& D = L.desc;
     hipStream_t st = c->stream;
     const int d = D.d, E = D.n_expert, k = D.n_used, nf = D.n_ff;
     const int n = T * k;
     const bool shared_ffn = shared == nullptr && D.n_ff_shared > 0;
-    // prefill-sized expert work (several assignments per expert on average) runs on the matrix cores,
-    // whose kernels read the activations' fp16 copies
-    const bool mma = mfma_type(D.gate_up_type) && mfma_type(D.down_type) && n >= 8 * E;
+    const bool mma = mma_path(D, T);
     const bool kmma = kmma_type(D.gate_up_type) && kmma_type(D.down_type) && n >= 8 * E;
     const bool smma = shared_ffn && mfma_type(D.shared_type) && T >= 32;
     Act agu = make_act(c, act_fmt(D.gate_up_type), d, W_AGU_Q, W_AGU_D, W_AGU_S);
@@ -853,6 +867,9 @@ int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, con
         agu.qh = wp<uint16_t>(c, W_AGU_H);
         agu.qhstride = d;
     }
+    // the tolerance mode (Q4_0 / Q8_0 on the matrix cores): every fp16 activation copy carries its block
+    // scale folded in, which selects the tolerance-mode products
+    agu.fold = fast && mma;
     if (kmma && D.gate_up_type == PHX_Q4_K) {
         agu.bh = wp<uint16_t>(c, W_AGU_BH);
         agu.bhstride = d / 16;
@@ -863,6 +880,7 @@ int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, con
     if (smma) {
         ash.qh = wp<uint16_t>(c, W_ASH_H);
         ash.qhstride = d;
+        ash.fold = fast;
     }
     if (!exact && cert_route(L, T, shared_ffn)) {
         // the router's certified sums with the expert (and shared) inputs quantized beside them, then
@@ -918,6 +936,7 @@ int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, con
         adn.qh = wp<uint16_t>(c, W_ADN_H);
         adn.qhstride = D.down_cols;
     }
+    adn.fold = fast && mma;
     if (kmma && D.down_type == PHX_Q4_K) {
         adn.bh = wp<uint16_t>(c, W_ADN_BH);
         adn.bhstride = D.down_cols / 16;
@@ -926,7 +945,8 @@ int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, con
         ProfScope p(c, PHX_K_GATE_UP);
         if (mma)  // the matrix-core gate|up also writes the down input (GELU-gated Q8_0, list order)
             launch_grouped_mfma(st, L.gu, agu, wp<Tile>(c, W_TILES), wp<int>(c, W_NTILES), max_tiles, wp<int>(c, W_PERM), k,
-                                wp<float>(c, W_G), wp<float>(c, W_U), nf, nf, 0, &adn, n, c->gelu_tab, fast);
+                                keep ? wp<float>(c, W_G) : nullptr, keep ? wp<float>(c, W_U) : nullptr, nf, nf, 0, &adn,
+                                n, c->gelu_tab);
         else if (kmma)
             launch_grouped_kmma(st, L.gu, agu, wp<Tile>(c, W_TILES), wp<int>(c, W_NTILES), max_tiles, wp<int>(c, W_PERM), k,
                                 wp<float>(c, W_G), wp<float>(c, W_U), nf, nf);
@@ -942,7 +962,7 @@ int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, con
         ProfScope p(c, PHX_K_DOWN);
         if (mma)
             launch_grouped_mfma(st, L.dn, adn, wp<Tile>(c, W_TILES), wp<int>(c, W_NTILES), max_tiles, wp<int>(c, W_PERM), 1,
-                                wp<float>(c, W_YD), wp<float>(c, W_YD), d, d, n, nullptr, 0, nullptr, fast);
+                                wp<float>(c, W_YD), wp<float>(c, W_YD), d, d, n);
         else if (kmma)
             launch_grouped_kmma(st, L.dn, adn, wp<Tile>(c, W_TILES), wp<int>(c, W_NTILES), max_tiles, wp<int>(c, W_PERM), 1,
                                 wp<float>(c, W_YD), wp<float>(c, W_YD), d, d);
@@ -963,17 +983,18 @@ int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, con
         if (smma) {
             asd.qh = wp<uint16_t>(c, W_ASD_H);
             asd.qhstride = asd.cols;
+            asd.fold = fast;
         }
         if (smma)
             launch_grouped_mfma(st, L.sgu, ash, wp<Tile>(c, W_STILES), wp<int>(c, W_SNTILES), smax, wp<int>(c, W_SPERM), 1,
-                                wp<float>(c, W_SHG), wp<float>(c, W_SHU), nff, nff, 0, &asd, T, c->gelu_tab, fast);
+                                nullptr, nullptr, nff, nff, 0, &asd, T, c->gelu_tab);  // (no reader of g, u)
         else
             launch_grouped(st, L.sgu, ash, wp<Tile>(c, W_STILES), wp<int>(c, W_SNTILES), smax, kTileA, wp<int>(c, W_SPERM),
                            1, wp<float>(c, W_SHG), wp<float>(c, W_SHU), nff, nff);
         if (!smma) launch_requant(st, T, nff, wp<float>(c, W_SHG), wp<float>(c, W_SHU), c->gelu_tab, asd);
         if (smma)
             launch_grouped_mfma(st, L.sdn, asd, wp<Tile>(c, W_STILES), wp<int>(c, W_SNTILES), smax, wp<int>(c, W_SPERM), 1,
-                                wp<float>(c, W_SHOUT), wp<float>(c, W_SHOUT), d, d, T, nullptr, 0, nullptr, fast);
+                                wp<float>(c, W_SHOUT), wp<float>(c, W_SHOUT), d, d, T);
         else
             launch_grouped(st, L.sdn, asd, wp<Tile>(c, W_STILES), wp<int>(c, W_SNTILES), smax, kTileA, wp<int>(c, W_SPERM),
                            1, wp<float>(c, W_SHOUT), wp<float>(c, W_SHOUT), d, d);
@@ -993,7 +1014,7 @@ int run_layer(phx_moe_ctx* c, const Layer& L, int T, const float* x, const float
 {
     if (use_decode(c, L, T, flags)) return run_layer_decode(c, L, T, x, shared, out, xres);
     return run_layer_general(c, L, T, x, shared, out, xres, (flags & PHX_FLAG_EXACT_ROUTER) != 0,
-                             (flags & PHX_FLAG_FAST_MATH) != 0);
+                             (flags & PHX_FLAG_FAST_MATH) != 0, (flags & PHX_FLAG_KEEP_INTERMEDIATES) != 0);
 }
 
 int upload_f32(phx_moe_ctx* c, const float* src, size_t n, float** dst)
@@ -1318,7 +1339,8 @@ int ffn_host(phx_moe_ctx* c, int layer, int T, float* x, const float* shared, fl
     // workgroups and wait on the stream
     const bool small = bytes * (res ? 2 : 1) <= (256u << 10);
     const unsigned key =
-        (flags & (PHX_FLAG_RESIDUAL | PHX_FLAG_EXACT_ROUTER | PHX_FLAG_FAST_MATH)) | (shared ? 0x80000000u : 0u);
+        (flags & (PHX_FLAG_RESIDUAL | PHX_FLAG_EXACT_ROUTER | PHX_FLAG_FAST_MATH | PHX_FLAG_KEEP_INTERMEDIATES)) |
+        (shared ? 0x80000000u : 0u);
     std::vector<void*> sig(c->ws.size());
     for (size_t i = 0; i < c->ws.size(); i++) sig[i] = c->ws[i].p;
     hipGraphExec_t exec = nullptr;
@@ -1395,6 +1417,7 @@ int ffn_host(phx_moe_ctx* c, int layer, int T, float* x, const float* shared, fl
     if (res) memcpy(x, px, bytes);
     c->last_T = T;
     c->last_layer = layer;
+    c->last_gu_kept = keeps_gu(c, c->layers[layer], T, flags);
     return PHX_OK;
 }
 
@@ -1430,6 +1453,7 @@ int phx_moe_ffn(phx_moe_ctx* c, int layer, int T, float* x, const float* shared,
     if (rc) return rc;
     c->last_T = T;
     c->last_layer = layer;
+    c->last_gu_kept = keeps_gu(c, c->layers[layer], T, flags);
     if (!dev) {
         HIPCHK(c, hipMemcpyAsync(out, o, bytes, hipMemcpyDeviceToHost, c->stream));
         if (flags & PHX_FLAG_RESIDUAL) HIPCHK(c, hipMemcpyAsync(x, xin, bytes, hipMemcpyDeviceToHost, c->stream));
@@ -1469,6 +1493,7 @@ int phx_moe_ffn_noalloc(phx_moe_ctx* c, int layer, int T, float* x, const float*
     HIPCHK(c, launch_status(c));
     c->last_T = T;
     c->last_layer = layer;
+    c->last_gu_kept = keeps_gu(c, c->layers[layer], T, flags);
     c->last_scratch = true;
     if (!(flags & PHX_FLAG_ASYNC)) HIPCHK(c, hipStreamSynchronize(c->stream));
     return PHX_OK;
@@ -1492,6 +1517,8 @@ int phx_moe_get_routing(phx_moe_ctx* c, int32_t* ids, float* weights, int32_t* o
 int phx_moe_get_intermediates(phx_moe_ctx* c, float* g, float* u, float* yd)
 {
     if (!c || c->last_layer < 0) return PHX_ERR_ARG;
+    if ((g || u) && !c->last_gu_kept)
+        return set_err(c, PHX_ERR_ARG, "the last call skipped the gate and up stores: pass PHX_FLAG_KEEP_INTERMEDIATES");
     const phx_moe_layer_desc& D = c->layers[c->last_layer].desc;
     const size_t n = (size_t)c->last_T * D.n_used;
     HIPCHK(c, hipStreamSynchronize(c->stream));
@@ -1592,6 +1619,7 @@ int phx_moe_stack_capture2(phx_moe_ctx* c, int first, int n_layers, int T, unsig
     c->graph_T = T;
     c->graph_first = first;
     c->graph_n = n_layers;
+    c->graph_gu_kept = keeps_gu(c, c->layers[first + n_layers - 1], T, flags);
     c->graph_gens.clear();
     for (int l = first; l < first + n_layers; l++) c->graph_gens.push_back(c->layers[l].gen);
     c->graph_ws.clear();
@@ -1630,6 +1658,7 @@ int phx_moe_stack_run(phx_moe_ctx* c, float* x, int T, unsigned flags)
     HIPCHK(c, hipMemcpyAsync(x, xs, bytes, dev ? hipMemcpyDeviceToDevice : hipMemcpyDeviceToHost, c->stream));
     c->last_T = T;
     c->last_layer = c->graph_first + c->graph_n - 1;
+    c->last_gu_kept = c->graph_gu_kept;
     c->last_scratch = false;
     if (c->profiling && !c->graph_timing.empty()) {
         // a stack captured while profiling: this replay's kernel intervals, read before the next one

@@ -20,6 +20,7 @@ class PHX:
     F32, Q4_0, Q8_0, Q3_K, Q4_K, Q5_K, Q6_K, IQ2_XXS, IQ3_S, IQ2_S = 0, 2, 8, 11, 12, 13, 14, 16, 21, 22
     WEIGHTS_SOFTMAX, WEIGHTS_CPUREF = 0, 1
     FLAG_DEVICE_PTRS, FLAG_ASYNC, FLAG_RESIDUAL, FLAG_EXACT_ROUTER, FLAG_FAST_MATH = 1, 2, 4, 8, 16
+    FLAG_KEEP_INTERMEDIATES = 32
     KINDS = ["prologue", "router", "topk", "dispatch", "gate_up", "requant", "down", "combine", "shared"]
     MAX_EXPERTS, MAX_USED = 256, 16
     # activation quantizer modes (KernelsQuant.Mode, src/KernelsQuant.cs:13)
@@ -222,9 +223,11 @@ class MoeContext:
         self.layers[layer] = {k: L[k] for k in ("d", "n_expert", "n_used", "n_ff")}
 
     def ffn(self, layer: int, x: np.ndarray, shared: np.ndarray | None = None, residual: bool = False,
-            exact_router: bool = False, fast_math: bool = False) -> np.ndarray:
+            exact_router: bool = False, fast_math: bool = False, keep_intermediates: bool = False) -> np.ndarray:
         """out[T][d] of one MoE FFN block on host arrays; with residual, returns (out, x + rmsnorm(out) * post).
-        fast_math: the tolerance mode of the prefill-sized expert products (PHX_FLAG_FAST_MATH)."""
+        fast_math: the tolerance mode of the prefill-sized expert products (PHX_FLAG_FAST_MATH).
+        keep_intermediates: store g and u for intermediates() (PHX_FLAG_KEEP_INTERMEDIATES; the
+        prefill-sized Q4_0 / Q8_0 products skip those stores without it)."""
         x = _f32(x)
         if residual:
             x = x.copy()
@@ -232,7 +235,7 @@ class MoeContext:
         out = np.empty_like(x)
         sh = None if shared is None else _f32(shared)
         flags = (PHX.FLAG_RESIDUAL if residual else 0) | (PHX.FLAG_EXACT_ROUTER if exact_router else 0) | \
-            (PHX.FLAG_FAST_MATH if fast_math else 0)
+            (PHX.FLAG_FAST_MATH if fast_math else 0) | (PHX.FLAG_KEEP_INTERMEDIATES if keep_intermediates else 0)
         self._last_layer, self._last_T = layer, T
         self._check(self.lib.phx_moe_ffn(self.h, layer, T, x.ctypes.data, None if sh is None else sh.ctypes.data,
                                          out.ctypes.data, flags))

@@ -12,8 +12,9 @@ layer and prints, per phase, the earliest / median / latest workgroup stamp.
       (comb 4: loads in, 5: branch norms, 6: residual norm), µs from the layer's first router workgroup
   python3 phoenix-lai_amd/timeline.py prologue [CONFIG]   the general path's prologue phases (0: start,
       1: mean of squares, 2: router input and normed row in LDS, 3: quantized, 4: end)
-  python3 phoenix-lai_amd/timeline.py mfma [CONFIG]   start and end of every workgroup of the prefill
-      matrix-core products, by the tile's active 32-token columns, and the count running over time
+  python3 phoenix-lai_amd/timeline.py mfma [CONFIG [fast]]   start and end of every workgroup of the
+      prefill matrix-core products (fast: the tolerance mode's), by the tile's active 32-token columns,
+      and the count running over time
 """
 from __future__ import annotations
 
@@ -132,7 +133,7 @@ def prologue(cfg="c3_prefill"):
     ctx.close()
 
 
-def mfma(cfg="c3_prefill"):
+def mfma(cfg="c3_prefill", fast=False):
     pkg = _package()
     S = pkg.synth
     L = S.make_layer(cfg)
@@ -142,9 +143,9 @@ def mfma(cfg="c3_prefill"):
     rd = _reader(ctx.lib, "phxdbg_timeline_prefill")
     buf = np.zeros(N, np.uint64)
     for _ in range(3):
-        ctx.ffn(0, x)
+        ctx.ffn(0, x, fast_math=fast)
     rd(None, 0, 1)
-    ctx.ffn(0, x)
+    ctx.ffn(0, x, fast_math=fast)
     rd(buf.ctypes.data, N, 0)
     _, _, off, _, _ = ctx.routing()
     A = 128
@@ -154,7 +155,8 @@ def mfma(cfg="c3_prefill"):
         if c % A:
             parts[min(4, (4 * (c % A) + A - 1) // A)].append(c % A)
     tiles = full + parts[4] + parts[3] + parts[2] + parts[1]
-    for name, base, gx in (("gate_up", 0, (L["n_ff"] // 32 + 1) // 2), ("down", 16384, (L["d"] // 64 + 1) // 2)):
+    per = 4 if fast else 2  # row groups per workgroup
+    for name, base, gx in (("gate_up", 0, (L["n_ff"] // 32 + per - 1) // per), ("down", 16384, (L["d"] // 64 + per - 1) // per)):
         st = buf[base:base + 16384].astype(np.int64).reshape(-1, 2)
         ok = np.nonzero(st[:, 0] > 0)[0]
         s0, s1 = st[ok, 0], st[ok, 1]
@@ -181,6 +183,6 @@ if __name__ == "__main__":
     elif a[0] == "prologue":
         prologue(*a[1:2])
     elif a[0] == "mfma":
-        mfma(*a[1:2])
+        mfma(a[1] if len(a) > 1 else "c3_prefill", len(a) > 2 and a[2] == "fast")
     else:
         sys.exit(__doc__)

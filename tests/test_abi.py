@@ -105,8 +105,9 @@ def test_constants_match_python_mirror(pkg):
     assert (d["PHX_MAX_EXPERTS"], d["PHX_MAX_USED"]) == (P.MAX_EXPERTS, P.MAX_USED)
     assert (d["PHX_WEIGHTS_SOFTMAX"], d["PHX_WEIGHTS_CPUREF"]) == (P.WEIGHTS_SOFTMAX, P.WEIGHTS_CPUREF)
     assert (d["PHX_FLAG_DEVICE_PTRS"], d["PHX_FLAG_ASYNC"], d["PHX_FLAG_RESIDUAL"], d["PHX_FLAG_EXACT_ROUTER"],
-            d["PHX_FLAG_FAST_MATH"]) == (P.FLAG_DEVICE_PTRS, P.FLAG_ASYNC, P.FLAG_RESIDUAL, P.FLAG_EXACT_ROUTER,
-                                         P.FLAG_FAST_MATH)
+            d["PHX_FLAG_FAST_MATH"], d["PHX_FLAG_KEEP_INTERMEDIATES"]) == (
+        P.FLAG_DEVICE_PTRS, P.FLAG_ASYNC, P.FLAG_RESIDUAL, P.FLAG_EXACT_ROUTER, P.FLAG_FAST_MATH,
+        P.FLAG_KEEP_INTERMEDIATES)
     assert (d["PHX_QUANT_PLAIN"], d["PHX_QUANT_SILU_MUL"], d["PHX_QUANT_RMS_NORM"], d["PHX_QUANT_GELU_MUL"]) == (
         P.QUANT_PLAIN, P.QUANT_SILU_MUL, P.QUANT_RMS_NORM, P.QUANT_GELU_MUL)
 

@@ -75,7 +75,7 @@ def test_fast_math_products_and_error(ctx, pkg, orc, cfg, T):
     L = pkg.synth.make_layer(cfg)
     x = pkg.synth.make_input(cfg, T=T)
     ctx.upload(0, L)
-    out = ctx.ffn(0, x, fast_math=True)
+    out = ctx.ffn(0, x, fast_math=True, keep_intermediates=True)
     ids, w, off, perm, logits = ctx.routing()
     g, u, yd = ctx.intermediates()
     k, nf, d = L["n_used"], L["n_ff"], L["d"]

@@ -24,7 +24,7 @@ def say(*a):
 def _check_layer_exact(ctx, orc, L, x, tag):
     T = x.shape[0]
     t0 = time.time()
-    out = ctx.ffn(0, x)
+    out = ctx.ffn(0, x, keep_intermediates=True)
     ids, w, off, perm, logits = ctx.routing()
     g, u, yd = ctx.intermediates()
     say(f"{tag}: GPU done ({time.time() - t0:.1f} s); oracle on {T} tokens ...")

@@ -47,7 +47,7 @@ def check_layer(ctx, orc, L, x, shared=None, tag="", exact=False, layer=0):
     ids and lists are bit-exact, logits agree within the router's error bound and weights/outputs
     within the tolerance; gate/up/down products are bit-exact on both paths."""
     T = x.shape[0]
-    out = ctx.ffn(layer, x, shared, exact_router=exact)
+    out = ctx.ffn(layer, x, shared, exact_router=exact, keep_intermediates=True)
     ids, w, off, perm, logits = ctx.routing()
     g, u, yd = ctx.intermediates()
     k = L["n_used"]

@@ -1,7 +1,8 @@
 """GPU checks of the library's guards: the certified general-path router only where its workgroups
 cover every input block (small expert counts with wide rows take the exact router), a captured stack
 refused once a layer is uploaded again or the workspace grows (the graph would name freed memory),
-device-pointer calls refused on pageable host memory, and the host-buffer call graph cache's counts."""
+device-pointer calls refused on pageable host memory, the host-buffer call graph cache's counts, and
+gate/up intermediates refused after a call that skipped their stores."""
 import sys
 
 import numpy as np
@@ -96,3 +97,30 @@ def test_host_call_graphs_are_counted(ctx, pkg):
     np.testing.assert_array_equal(ctx.ffn(0, x3), b)
     h1, m1 = ctx.graph_stats()
     assert (h1 - h0, m1 - m0) == (2, 2)
+
+
+@pytest.mark.parametrize("fast", [False, True])
+def test_skipped_gate_up_stores_are_refused(ctx, pkg, orc, fast):
+    """A prefill-sized Q4_0 call skips the g and u stores unless PHX_FLAG_KEEP_INTERMEDIATES is given:
+    asking for them afterwards is an error (not the previous call's rows), yd stays available, the output
+    is the same with and without the stores, and the kept g and u are the oracle's (exact mode)."""
+    say(f"skipped g/u stores (fast={fast}): refused without the flag, kept with it")
+    L = pkg.synth.make_layer("c3_prefill")
+    ctx.upload(0, L)
+    T = 256  # T * k = 2048 >= 8 E: the matrix-core path
+    x = pkg.synth.make_input("c3_prefill", T=T)
+    out0 = ctx.ffn(0, x, fast_math=fast)
+    with pytest.raises(Exception, match="KEEP_INTERMEDIATES"):
+        ctx.intermediates()
+    n, d = T * L["n_used"], L["d"]
+    yd = np.empty((n, d), np.float32)
+    assert ctx.lib.phx_moe_get_intermediates(ctx.h, None, None, yd.ctypes.data) == 0
+    out1 = ctx.ffn(0, x, fast_math=fast, keep_intermediates=True)
+    np.testing.assert_array_equal(out0, out1)
+    g, u, yd1 = ctx.intermediates()
+    np.testing.assert_array_equal(yd, yd1)
+    if not fast:
+        for t in (0, T - 1):
+            _, _, _, rg, ru, _ = orc.moe_token(L, x[t], None)
+            np.testing.assert_array_equal(g[t * L["n_used"]:(t + 1) * L["n_used"]], rg)
+            np.testing.assert_array_equal(u[t * L["n_used"]:(t + 1) * L["n_used"]], ru)

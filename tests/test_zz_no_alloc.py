@@ -25,7 +25,7 @@ def _call(ctx, fn, layer, x, shared, flags):
         xb.upload(x)
         if sb:
             sb.upload(shared)
-        fn(layer, T, xb.ptr, sb.ptr if sb else None, ob.ptr, flags)
+        fn(layer, T, xb.ptr, sb.ptr if sb else None, ob.ptr, flags | 32)  # | PHX_FLAG_KEEP_INTERMEDIATES: g, u compared
         ctx.sync()
         res = {"out": ob.download((T, d)), "x": xb.download((T, d))}
     finally:
