@@ -470,6 +470,7 @@ struct CoopSlot {
     static constexpr int BYTES = WD + (SG ? 0 : 4 * 64 * 4);
     static constexpr int SR = MMA_RING * BYTES;        // (Q4_0) scale ring [2 groups][4 waves][64 rows][8 fp16]
     static constexpr int LDS = SR + (SG ? 2 * 4 * 1024 : 0);
+    static_assert(LDS >= 4 * 32 * 68 * 4, "the epilogue's transpose fits the ring");
 };
 
 template <int TYPE, int NJ>
@@ -545,89 +546,96 @@ __device__ __forceinline__ void coop_tile(const MmaArgs& g, const Tile& tl, int 
     const uint32_t A_WD = ring0 + SL::WD + 256 * wave + 4 * r32;
     const uint32_t A_B0 = ring0 + SL::ACT + act_off(r32, h), A_B1 = ring0 + SL::ACT + act_off(r32, 2 + h);
 
-    // a block's operands as read from LDS (valid after `landed`, in the reads' basic block)
-    u32x2 q[2][SL::WL];
-    uint32_t wd[2];
-    u32x4 fb0[NJ], fb1[NJ];
-    auto reads = [&](auto SC, int b) {  // block b in slot S
-        constexpr int O = decltype(SC)::value * SL::BYTES;
-        q[0][0] = ds_r64<O>(A_WQ);
-        q[1][0] = ds_r64<O + 32 * PAY>(A_WQ);
+    // a block's operands as read from LDS, in two register sets (block b in set b % 2, so the next block's
+    // reads land beside the operands being multiplied); valid after `landed`, in the reads' basic block
+    u32x2 q[2][2][SL::WL];
+    uint32_t wd[2][2];
+    u32x4 fb0[2][NJ], fb1[2][NJ];
+    auto reads = [&](auto SC, int b) {  // block b in slot S, into set S % 2
+        constexpr int S = decltype(SC)::value, O = S * SL::BYTES, s = S & 1;
+        q[s][0][0] = ds_r64<O>(A_WQ);
+        q[s][1][0] = ds_r64<O + 32 * PAY>(A_WQ);
         if constexpr (PAY == 32) {
-            q[0][SL::WL - 1] = ds_r64<O + 16>(A_WQ);
-            q[1][SL::WL - 1] = ds_r64<O + 32 * PAY + 16>(A_WQ);
+            q[s][0][SL::WL - 1] = ds_r64<O + 16>(A_WQ);
+            q[s][1][SL::WL - 1] = ds_r64<O + 32 * PAY + 16>(A_WQ);
         }
         if constexpr (SL::SG) {
             const uint32_t a = A_SG + (uint32_t)(((b >> 3) & 1) * 4096 + (b & 7) * 2);
-            wd[0] = ds_ru16<0>(a);
-            wd[1] = ds_ru16<512>(a);
+            wd[s][0] = ds_ru16<0>(a);
+            wd[s][1] = ds_ru16<512>(a);
         } else {
-            wd[0] = ds_ru16<O>(A_WD);
-            wd[1] = ds_ru16<O + 128>(A_WD);
+            wd[s][0] = ds_ru16<O>(A_WD);
+            wd[s][1] = ds_ru16<O + 128>(A_WD);
         }
         static_for<NJ>([&](auto JC) {
             constexpr int j = decltype(JC)::value;
-            fb0[j] = ds_r128<O + 2048 * j>(A_B0);
-            fb1[j] = ds_r128<O + 2048 * j>(A_B1);
+            fb0[s][j] = ds_r128<O + 2048 * j>(A_B0);
+            fb1[s][j] = ds_r128<O + 2048 * j>(A_B1);
         });
     };
-    auto landed = [&]() {
+    auto landed = [&](auto SC) {  // set S % 2
+        constexpr int s = decltype(SC)::value & 1;
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
         for (int t = 0; t < 2; t++) {
 #pragma unroll
-            for (int i = 0; i < SL::WL; i++) tie(q[t][i]);
-            tie(wd[t]);
+            for (int i = 0; i < SL::WL; i++) tie(q[s][t][i]);
+            tie(wd[s][t]);
         }
         static_for<NJ>([&](auto JC) {
             constexpr int j = decltype(JC)::value;
-            tie(fb0[j]);
-            tie(fb1[j]);
+            tie(fb0[s][j]);
+            tie(fb1[s][j]);
         });
     };
-
-    // block b (slot S, its operands read and landed): fold them, then land block b + 1 and issue its
-    // reads, then this block's MFMAs, which cover the reads' latency, then wait for the reads (after the
-    // last block: a harmless extra barrier and reads of a slot nobody uses)
-    auto block = [&](auto SC, int b) {
-        constexpr int S1 = (decltype(SC)::value + 1) % MMA_RING;
-        mh8 A0[2], A1[2], X0[NJ], X1[NJ];
-        if (live) {  // uniform
-#pragma unroll
-            for (int t = 0; t < 2; t++) {
-                const _Float16 dw = __builtin_bit_cast(_Float16, (uint16_t)wd[t]);
-                const mh8 dw8 = {dw, dw, dw, dw, dw, dw, dw, dw};
-                if (TYPE == PHX_Q4_0_DEV) {
-                    A0[t] = bias8(q[t][0].x & 0x0F0F0F0Fu, q[t][0].y & 0x0F0F0F0Fu, 1032.0f) * dw8;
-                    A1[t] = bias8((q[t][0].x >> 4) & 0x0F0F0F0Fu, (q[t][0].y >> 4) & 0x0F0F0F0Fu, 1032.0f) * dw8;
-                } else {
-                    A0[t] = bias8(q[t][0].x ^ 0x80808080u, q[t][0].y ^ 0x80808080u, 1152.0f) * dw8;
-                    A1[t] = bias8(q[t][SL::WL - 1].x ^ 0x80808080u, q[t][SL::WL - 1].y ^ 0x80808080u, 1152.0f) * dw8;
-                }
-            }
-            static_for<NJ>([&](auto JC) {  // the activations arrive folded
-                constexpr int j = decltype(JC)::value;
-                X0[j] = __builtin_bit_cast(mh8, fb0[j]);
-                X1[j] = __builtin_bit_cast(mh8, fb1[j]);
-            });
+    // weight operand (tile t, k-half kh) of the block in set s: (q - 8) * d_w (Q4_0) or q * d_w (Q8_0) in fp16
+    auto fold_w = [&](int s, int t, int kh) -> mh8 {
+        const _Float16 dw = __builtin_bit_cast(_Float16, (uint16_t)wd[s][t]);
+        const mh8 dw8 = {dw, dw, dw, dw, dw, dw, dw, dw};
+        if (TYPE == PHX_Q4_0_DEV) {
+            const u32x2 w = q[s][t][0];
+            return kh ? bias8((w.x >> 4) & 0x0F0F0F0Fu, (w.y >> 4) & 0x0F0F0F0Fu, 1032.0f) * dw8
+                      : bias8(w.x & 0x0F0F0F0Fu, w.y & 0x0F0F0F0Fu, 1032.0f) * dw8;
+        } else {
+            const u32x2 w = q[s][t][kh ? SL::WL - 1 : 0];
+            return bias8(w.x ^ 0x80808080u, w.y ^ 0x80808080u, 1152.0f) * dw8;
         }
-        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    // block b (slot S, its operands landed in set S % 2): land block b + 1 and issue its reads into the
+    // other set, then this block's products: each weight operand is folded just before the NJ MFMAs that
+    // take it, the next operand's fold interleaved with them, so the wave's VALU runs beside its own
+    // matrix-core work; the reads' wait closes the block (after the last block: a harmless extra barrier
+    // and reads of a slot nobody uses)
+    auto block = [&](auto SC, int b) {
+        constexpr int S = decltype(SC)::value, s = S & 1, S1 = (S + 1) % MMA_RING;
         land(ic<S1>{}, b + 1);
-        if (live) {
+        if (live) {  // uniform
             reads(ic<S1>{}, b + 1);
             __builtin_amdgcn_sched_barrier(0);
-            static_for<NJ>([&](auto JC) {
-                constexpr int j = decltype(JC)::value;
-                C[0][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A0[0], X0[j], C[0][j], 0, 0, 0);
-                C[1][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A0[1], X0[j], C[1][j], 0, 0, 0);
-            });
-            static_for<NJ>([&](auto JC) {
-                constexpr int j = decltype(JC)::value;
-                C[0][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A1[0], X1[j], C[0][j], 0, 0, 0);
-                C[1][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A1[1], X1[j], C[1][j], 0, 0, 0);
+            // operand order (t, kh) = (0, 0), (1, 0), (0, 1), (1, 1): an accumulator's two products are
+            // 2 NJ MFMAs apart
+            mh8 A = fold_w(s, 0, 0);
+            static_for<4>([&](auto UC) {
+                constexpr int u = decltype(UC)::value, t = u & 1, kh = u >> 1;
+                mh8 An = A;
+                if constexpr (u < 3) An = fold_w(s, (u + 1) & 1, (u + 1) >> 1);
+                static_for<NJ>([&](auto JC) {
+                    constexpr int j = decltype(JC)::value;
+                    C[t][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A, __builtin_bit_cast(mh8, kh ? fb1[s][j] : fb0[s][j]),
+                                                                     C[t][j], 0, 0, 0);
+                });
+                if constexpr (u < 3) {
+                    // the next operand's fold beside these MFMAs: one MFMA, then a few VALU, in turn
+                    static_for<NJ>([&](auto) {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, u);
+                        __builtin_amdgcn_sched_group_barrier(0x002, 4, u);
+                    });
+                }
+                A = An;
             });
             __builtin_amdgcn_sched_barrier(0);
-            landed();  // in the reads' basic block: the loop carries landed values
+            landed(ic<S1>{});  // in the reads' basic block: the loop carries landed values
         }
         __builtin_amdgcn_sched_barrier(0);
     };
@@ -639,7 +647,7 @@ __device__ __forceinline__ void coop_tile(const MmaArgs& g, const Tile& tl, int 
     land(ic<0>{}, 0);
     if (live) {
         reads(ic<0>{}, 0);
-        landed();
+        landed(ic<0>{});
     }
     for (int b = 0; b < nb; b += 4) {
         block(ic<0>{}, b);
@@ -647,8 +655,10 @@ __device__ __forceinline__ void coop_tile(const MmaArgs& g, const Tile& tl, int 
         if (b + 2 < nb) block(ic<2>{}, b + 2);
         if (b + 3 < nb) block(ic<3>{}, b + 3);
     }
-    // the loads issued past the last block land in this workgroup's LDS: let them finish before it ends
+    // the loads issued past the last block land in this workgroup's LDS: let them finish, and every wave
+    // be done with the ring, before the epilogue reuses it
     __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
     if (!live) return;
 
     // lane (r32, h) holds, for token column r32 of tile j, rows 8 (q / 4) + 4 h + q % 4 of each half
@@ -701,6 +711,50 @@ __device__ __forceinline__ void coop_tile(const MmaArgs& g, const Tile& tl, int 
 
     if (g.paired && !g.out0) return;  // no g and u outputs: the requant above was the product's output
     const bool vec = (g.out_stride & 3) == 0;
+    if (!g.paired) {
+        // rows of a token through LDS: each 16-lane group then stores 256 contiguous bytes of one output
+        // row (whole cache lines) instead of 32 lanes storing 32-byte pieces of 32 rows
+        float* tb = (float*)ring + wave * (32 * 68);  // [32 tokens][64 rows + 4 pad]
+        const int c16 = lane & 15, row0 = gI * 64 + 4 * c16;
+        const bool full = vec && row0 + 3 < min(g.rows, g.split);
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+#pragma unroll
+            for (int t = 0; t < 2; t++)
+#pragma unroll
+                for (int q4 = 0; q4 < 4; q4++)
+                    *(float4*)(tb + r32 * 68 + 32 * t + 8 * q4 + 4 * h) =
+                        make_float4(C[t][j][4 * q4], C[t][j][4 * q4 + 1], C[t][j][4 * q4 + 2], C[t][j][4 * q4 + 3]);
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+            for (int rd = 0; rd < 8; rd++) {
+                const int tok = 4 * rd + (lane >> 4), sidx = 32 * j + tok;
+                const float4 v = *(const float4*)(tb + tok * 68 + 4 * c16);
+                if (sidx < cnt) {
+                    const int64_t a = g.perm[tl.start + sidx];
+                    if (full) *(float4*)(g.out0 + a * g.out_stride + row0) = v;
+                    else {
+                        const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                        for (int i = 0; i < 4; i++) {
+                            const int r = row0 + i;
+                            if (r < g.rows) {
+                                if (r < g.split) g.out0[a * g.out_stride + r] = vv[i];
+                                else g.out1[a * g.out_stride + r - g.split] = vv[i];
+                            }
+                        }
+                    }
+                }
+            }
+            // every lane's reads of this tile end before the next tile's writes
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
         const int sidx = 32 * j + r32;
