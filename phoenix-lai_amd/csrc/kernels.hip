@@ -884,6 +884,9 @@ __device__ __forceinline__ void store_row(const GroupArgs& g, int rgi, int lane,
     }
 }
 
+// Q4_0 / Q8_0 rows of up to QG_SHORT blocks: each lane walks its row's blocks in order, loading each
+// block's payload and scale as it goes (a short row's many workgroups, no LDS, run in one round at
+// several per CU and hide each other's loads).
 template <int TYPE, int A>
 __global__ __launch_bounds__(256) void k_grouped_q(GroupArgs g)
 {
@@ -939,6 +942,139 @@ __global__ __launch_bounds__(256) void k_grouped_q(GroupArgs g)
 #pragma unroll
     for (int i = 0; i < A; i++)
         if (i < tl.cnt) store_row(g, rgi, lane, g.perm[tl.start + i], acc[i]);
+}
+
+// Q4_0 / Q8_0 rows of more than QG_SHORT blocks.  The tile's activation rows (integers, scales and, for
+// Q4_0, block sums) are staged in LDS, QG_CHB blocks at a time, and read back as wave-wide broadcasts.
+// Each wave streams its row group's blocks (payload and scales) into a ring of QG_R slots of its own by
+// direct global -> LDS loads, QG_R - 1 blocks ahead, and waits for a block by its own count of
+// outstanding loads: no barrier, as no wave reads another's ring.  Every LDS read is explicit (a read the compiler emitted would first wait
+// for all outstanding direct loads).  The launch gives each workgroup at least QG_LDS_MIN bytes of LDS:
+// three workgroups per CU, which ran a layer's gate|up tiles (C5: ~720 workgroups) in one even round,
+// 88 µs against 101 at four per CU and 106 for the row walk above.
+constexpr int QG_R = 3, QG_CHB = 128;
+template <int TYPE, int A>
+__global__ __launch_bounds__(256) void k_grouped_q_ring(GroupArgs g)
+{
+    const int tile = blockIdx.x;
+    if (tile >= *g.ntiles) return;  // uniform over the workgroup
+    const Tile tl = g.tiles[tile];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int rgi = blockIdx.y * 4 + wave;
+    const bool live = rgi < g.rg;  // a wave past the last row group streams a clamped one, stores nothing
+    constexpr int PAY = TYPE == PHX_Q4_0_DEV ? 16 : 32, NC = PAY / 16, NL = NC + 1;  // direct loads per block
+    constexpr bool Q4 = TYPE == PHX_Q4_0_DEV;
+    constexpr int SLOT = 64 * PAY + 256;  // a block's payload [64 rows][PAY], then its scales (4 B per lane)
+    // LDS (sized by the launch for CH = min(nb, QG_CHB) blocks): the waves' rings [4][QG_R][SLOT], then the
+    // activation chunk: integers [A][CH][32 B], scales [A][CH] and (Q4_0) block sums [A][CH]
+    extern __shared__ __align__(16) unsigned char qg_lds[];
+    const int nb = g.nb, rgc = min(rgi, g.rg - 1), CH = min(nb, QG_CHB);
+    unsigned char* ringb = qg_lds;
+    uint32_t* sq = (uint32_t*)(qg_lds + 4 * QG_R * SLOT);
+    float* sd = (float*)(sq + A * CH * 8);
+    int* ss = (int*)(sd + A * CH);
+    const __amdgpu_buffer_rsrc_t r_w = buf_rsrc(g.payload + tl.e * g.mat_pay + rgc * g.rg_pay);
+    const __amdgpu_buffer_rsrc_t r_s = buf_rsrc(g.scale + tl.e * g.mat_sc + (int64_t)rgc * nb * 64 * 2);
+    const int cnt = min(tl.cnt, A);
+    int arow[A];
+    float acc[A];
+#pragma unroll
+    for (int i = 0; i < A; i++) {
+        arow[i] = g.perm[tl.start + min(i, cnt - 1)] / g.act_div;
+        acc[i] = 0.0f;
+    }
+    unsigned char* myring = ringb + wave * (QG_R * SLOT);
+    auto issue = [&](int slot, int b) {  // block b (clamped: past the end a harmless reload)
+        const uint32_t bc = (uint32_t)min(b, nb - 1);
+        unsigned char* sl = myring + slot * SLOT;
+#pragma unroll
+        for (int c = 0; c < NC; c++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(r_w, (lds_void_t)(sl + 1024 * c), 16, 16 * lane, bc * 64 * PAY + 1024 * c,
+                                                     0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r_s, (lds_void_t)(sl + 64 * PAY), 2, 2 * lane, bc * 128, 0, 0);
+    };
+    const uint32_t a_w = (uint32_t)(uintptr_t)(lds_void_t)myring + PAY * lane;
+    const uint32_t a_s = (uint32_t)(uintptr_t)(lds_void_t)myring + 64 * PAY + 4 * lane;
+    const uint32_t a_q = (uint32_t)(uintptr_t)(lds_void_t)sq, a_d = (uint32_t)(uintptr_t)(lds_void_t)sd;
+    const uint32_t a_ss = (uint32_t)(uintptr_t)(lds_void_t)ss;
+    for (int c0 = 0; c0 < nb; c0 += QG_CHB) {
+        // a chunk of activations into LDS (the loads' wait also lands the previous chunk's trailing ring
+        // loads, so the ring restarts with nothing outstanding)
+        const int nbc = min(QG_CHB, nb - c0);
+        __syncthreads();  // the previous chunk's reads are done
+        for (int x = tid; x < A * nbc * 2; x += 256) {
+            const int i = x / (nbc * 2), y = x - i * nbc * 2;
+            ((uint4*)(sq + i * CH * 8))[y] =
+                ((const uint4*)(g.act.q + (int64_t)arow[i] * g.act.qstride + (int64_t)c0 * 32))[y];
+        }
+        for (int x = tid; x < A * nbc; x += 256) {
+            const int i = x / nbc, y = x - i * nbc;
+            sd[i * CH + y] = g.act.d[(int64_t)arow[i] * g.act.dstride + c0 + y];
+            if (Q4) ss[i * CH + y] = g.act.s[(int64_t)arow[i] * g.act.sstride + c0 + y];
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < QG_R - 1; r++) issue(r, c0 + r);
+        for (int bl = 0; bl < nbc; bl++) {
+            const int b = c0 + bl, slot = bl % QG_R;
+            // block b has landed once at most the QG_R - 2 later blocks' loads are outstanding; then the
+            // slot read in the previous step (its reads waited for) takes block b + QG_R - 1
+            __builtin_amdgcn_s_waitcnt((NL * (QG_R - 2)) | (0x7 << 4) | (0xF << 8));
+            issue((bl + QG_R - 1) % QG_R, b + QG_R - 1);
+            const uint32_t so = (uint32_t)(slot * SLOT);
+            u32x4 w0 = ds_r128<0>(a_w + so), w1 = {0u, 0u, 0u, 0u};
+            if constexpr (NC == 2) w1 = ds_r128<16>(a_w + so);
+            uint32_t sv = ds_ru16<0>(a_s + so);
+            u32x4 X0[A], X1[A];
+            uint32_t XD[A], XS[A];
+#pragma unroll
+            for (int i = 0; i < A; i++) {
+                X0[i] = ds_r128<0>(a_q + i * (CH * 32) + 32 * bl);
+                X1[i] = ds_r128<16>(a_q + i * (CH * 32) + 32 * bl);
+                XD[i] = ds_r32<0>(a_d + i * (CH * 4) + 4 * bl);
+                XS[i] = Q4 ? ds_r32<0>(a_ss + i * (CH * 4) + 4 * bl) : 0u;
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            tie(w0);
+            tie(w1);
+            tie(sv);
+#pragma unroll
+            for (int i = 0; i < A; i++) {
+                tie(X0[i]);
+                tie(X1[i]);
+                tie(XD[i]);
+                tie(XS[i]);
+            }
+            const float dw = h2f(sv);
+            const uint32_t w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+            for (int i = 0; i < A; i++) {
+                if (i < cnt) {  // uniform
+                    const uint32_t xq[8] = {X0[i].x, X0[i].y, X0[i].z, X0[i].w, X1[i].x, X1[i].y, X1[i].z, X1[i].w};
+                    int isum = 0;
+                    if constexpr (Q4) {
+#pragma unroll
+                        for (int k = 0; k < 4; k++) {
+                            isum = __builtin_amdgcn_sdot4((int)(w[k] & 0x0F0F0F0Fu), (int)xq[k], isum, false);
+                            isum = __builtin_amdgcn_sdot4((int)((w[k] >> 4) & 0x0F0F0F0Fu), (int)xq[4 + k], isum, false);
+                        }
+                        isum -= 8 * (int)XS[i];
+                    } else {
+#pragma unroll
+                        for (int k = 0; k < 8; k++) isum = __builtin_amdgcn_sdot4((int)w[k], (int)xq[k], isum, false);
+                    }
+                    const float dd = dw * __uint_as_float(XD[i]);
+                    acc[i] += (float)isum * dd;
+                }
+            }
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // the trailing ring loads land in this workgroup's LDS before it ends
+    if (!live) return;
+#pragma unroll
+    for (int i = 0; i < A; i++)
+        if (i < cnt) store_row(g, rgi, lane, g.perm[tl.start + i], acc[i]);
 }
 
 // K-quant rows: DotK (src/CpuRefKQuants.cs:177-212) per (row, assignment): per super-block the eight
@@ -1185,6 +1321,15 @@ __global__ __launch_bounds__(256) void k_grouped_iq(GroupArgs g)
         if (i < tl.cnt) store_row(g, rgi, lane, g.perm[tl.start + i], IQ3 ? sumf[i] : 0.125f * sumf[i]);
 }
 
+// dynamic LDS of k_grouped_q_ring<type, 4>: the rings and one activation chunk, at least QG_LDS_MIN
+constexpr int QG_SHORT = 32, QG_LDS_MIN = 163840 / 4 + 1024;
+static uint32_t grouped_q_lds(int type, int nb)
+{
+    const int pay = type == PHX_Q4_0_DEV ? 16 : 32, ch = std::min(nb, QG_CHB);
+    const int need = 4 * QG_R * (64 * pay + 256) + 4 * ch * (32 + 4 + (type == PHX_Q4_0_DEV ? 4 : 0));
+    return (uint32_t)std::max(need, QG_LDS_MIN);
+}
+
 void launch_grouped(hipStream_t st, const QMat& w, Act act, const Tile* tiles, const int* ntiles, int max_tiles, int A,
                     const int* perm, int act_div, float* out0, float* out1, int split, int out_stride)
 {
@@ -1211,8 +1356,14 @@ void launch_grouped(hipStream_t st, const QMat& w, Act act, const Tile* tiles, c
     dim3 grid(max_tiles, (w.rg + 3) / 4);
     (void)A;  // the tile size the dispatch used: 4, the one instantiation
     switch (w.type) {
-    case PHX_Q4_0_DEV: launch((k_grouped_q<PHX_Q4_0_DEV, 4>), grid, dim3(256), 0, st, g); break;
-    case PHX_Q8_0_DEV: launch((k_grouped_q<PHX_Q8_0_DEV, 4>), grid, dim3(256), 0, st, g); break;
+    case PHX_Q4_0_DEV:
+        if (w.nb > QG_SHORT) launch((k_grouped_q_ring<PHX_Q4_0_DEV, 4>), grid, dim3(256), grouped_q_lds(w.type, w.nb), st, g);
+        else launch((k_grouped_q<PHX_Q4_0_DEV, 4>), grid, dim3(256), 0, st, g);
+        break;
+    case PHX_Q8_0_DEV:
+        if (w.nb > QG_SHORT) launch((k_grouped_q_ring<PHX_Q8_0_DEV, 4>), grid, dim3(256), grouped_q_lds(w.type, w.nb), st, g);
+        else launch((k_grouped_q<PHX_Q8_0_DEV, 4>), grid, dim3(256), 0, st, g);
+        break;
     case PHX_Q4_K_DEV: launch((k_grouped_k<PHX_Q4_K_DEV, 4>), grid, dim3(256), 0, st, g); break;
     case PHX_Q5_K_DEV: launch((k_grouped_k<PHX_Q5_K_DEV, 4>), grid, dim3(256), 0, st, g); break;
     case PHX_Q6_K_DEV: launch((k_grouped_k<PHX_Q6_K_DEV, 4>), grid, dim3(256), 0, st, g); break;
