@@ -401,7 +401,7 @@ def run_prefill(args, pkg, cfg_name="c3_prefill", steps=None):
     ids = ctx.routing()[0]
     cnt = np.bincount(ids.ravel(), minlength=L["n_expert"])
     fast = None
-    if L["gate_up_type"] in (pkg.PHX.Q4_0, pkg.PHX.Q8_0) and not args.no_fast_math:
+    if L["gate_up_type"] in (pkg.PHX.Q4_0, pkg.PHX.Q8_0, pkg.PHX.Q4_K, pkg.PHX.Q6_K) and not args.no_fast_math:
         fast = fast_math_object(args, pkg, ctx, L, xbuf, obuf, xs, steps)
     ctx.close()
     gu_b, dn_b = expert_bytes(L)

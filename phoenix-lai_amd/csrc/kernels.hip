@@ -17,7 +17,7 @@ namespace phx {
 // set, the matrix cores' fp16 copies; the block's scale is the caller's.  qrow is the wave's 64-dword
 // LDS row through which the integers reach the packed orders.  Wave-level: all 64 lanes call it.
 __device__ __forceinline__ void store_q8k_block(const Act& act, int64_t row, int b, int lane, uint32_t pk,
-                                                uint32_t* qrow)
+                                                uint32_t* qrow, float dval)
 {
     int sm = (int)(int8_t)(pk & 0xFF) + (int)(int8_t)((pk >> 8) & 0xFF) + (int)(int8_t)((pk >> 16) & 0xFF) +
              (int)(int8_t)(pk >> 24);
@@ -52,11 +52,13 @@ __device__ __forceinline__ void store_q8k_block(const Act& act, int64_t row, int
         c[(2 * P) * 8 + l] = -32 * (qv(e) + qv(e + 8));
         c[(2 * P + 1) * 8 + l] = -32 * (qv(e + 16) + qv(e + 24));
     }
-    if (act.qh) {  // the matrix cores' copy: exact fp16 integers, halves [l][s][mm']: lane = 8 l + s
+    if (act.qh) {  // the matrix cores' copy: exact fp16 integers (or, folded, fp16 of q * dval), halves
+                   // [l][s][mm']: lane = 8 l + s
         const int l = lane >> 3, s8 = lane & 7, e = 32 * s8 + l;
         uint32_t* hq = (uint32_t*)(act.qh + row * act.qhstride + (int64_t)b * 256) + l * 16 + s8 * 2;
-        hq[0] = f2h_bits((float)qv(e)) | (f2h_bits((float)qv(e + 16)) << 16);
-        hq[1] = f2h_bits((float)qv(e + 8)) | (f2h_bits((float)qv(e + 24)) << 16);
+        const float f = act.fold ? dval : 1.0f;
+        hq[0] = f2h_bits((float)qv(e) * f) | (f2h_bits((float)qv(e + 16) * f) << 16);
+        hq[1] = f2h_bits((float)qv(e + 8) * f) | (f2h_bits((float)qv(e + 24) * f) << 16);
     }
     // the row is rewritten by the wave's next block only after every lane's reads above
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -137,8 +139,9 @@ __device__ void quantize_row(const float* v, Act act, int64_t row)
         for (int j = 0; j < 4; j++) q[j] = amax == 0.0f ? 0 : min(nearest_int(iscale * x[j]), 127);
         const uint32_t pk = (uint32_t)(q[0] & 0xFF) | ((uint32_t)(q[1] & 0xFF) << 8) | ((uint32_t)(q[2] & 0xFF) << 16) |
                             ((uint32_t)q[3] << 24);
-        if (lane == 0) act.d[row * act.dstride + b] = amax == 0.0f ? 0.0f : 1.0f / iscale;
-        store_q8k_block(act, row, b, lane, pk, qsm[wave]);
+        const float dval = amax == 0.0f ? 0.0f : 1.0f / iscale;
+        if (lane == 0) act.d[row * act.dstride + b] = dval;
+        store_q8k_block(act, row, b, lane, pk, qsm[wave], dval);
     }
 }
 
@@ -1842,8 +1845,9 @@ __global__ __launch_bounds__(256) void k_planar_act_k(int64_t nblk, int nb, cons
     const int64_t t = g / nb;
     const int b = (int)(g - t * nb);
     const uint32_t pk = ((const uint32_t*)qs)[g * 64 + lane];
-    if (lane == 0) a.d[t * a.dstride + b] = d[g];
-    store_q8k_block(a, t, b, lane, pk, qsm[wave]);
+    const float dval = d[g];
+    if (lane == 0) a.d[t * a.dstride + b] = dval;
+    store_q8k_block(a, t, b, lane, pk, qsm[wave], dval);
 }
 
 void launch_planar_act_k(hipStream_t st, int rows, int n, const int8_t* qs, const float* d, Act a)

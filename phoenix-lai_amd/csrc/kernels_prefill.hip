@@ -925,7 +925,12 @@ __device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t c)
 // s_waitcnt vmcnt(n) alone (gfx9 encoding: vmcnt bits 3:0 and 15:14)
 constexpr int vm_wait(int n) { return (n & 15) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
 
-template <int TYPE, int NJ>
+// FOLD (the tolerance mode, PHX_FLAG_FAST_MATH): the activations arrive folded (fp16(q * d) of their
+// Q8_K scale), each weight operand is folded per super-block, fp16(sc * q * d - dmin * m) for Q4_K (one
+// rounding, dmin * m first rounded to fp16) and fp16(lo * q * d), fp16(32 hi * q * d) for Q6_K's two
+// parts, and every row accumulates over all its super-blocks in fp32 on the matrix cores: no per-lane
+// float chain, no min term, no scale products.
+template <int TYPE, int NJ, bool FOLD>
 __device__ __forceinline__ void kmma_tile(const MmaArgs& g, const Tile& tl, int cnt, unsigned char* ring, int bx)
 {
     using RG = KmRing<TYPE>;
@@ -1013,6 +1018,9 @@ __device__ __forceinline__ void kmma_tile(const MmaArgs& g, const Tile& tl, int 
             for (int l = 0; l < 8; l++) sums[l][c][v] = 0.0f;
         }
     const mf4 zero4 = {};
+    mf4 acc[NJ];  // FOLD: the tiles' fp32 sums over all super-blocks
+#pragma unroll
+    for (int c = 0; c < NJ; c++) acc[c] = zero4;
     // the lane's LDS read addresses in slot 0 of each region (slot S: + S * region slot bytes in the
     // immediate; the third activation slot from a second address, past the immediate's 64 KB)
     const uint32_t a_act = ring0 + RG::ACT + q * (KM_TOK * 16) + r16 * 16, a_act2 = a_act + 2 * RG::ACT_N;
@@ -1022,6 +1030,7 @@ __device__ __forceinline__ void kmma_tile(const MmaArgs& g, const Tile& tl, int 
     const uint32_t a_sc = ring0 + RG::W + (wave * 16 + r16) * PAY + (Q4K ? 128 + 4 * (q >> 1) : 128 + 16 * q);
     const uint32_t a_y = Q4K ? a_sc + 8 : ring0 + RG::W + (wave * 16 + r16) * PAY + 192 + 4 * q;
     const uint32_t a_ws = ring0 + RG::WS + (wave * 16 + 4 * q) * 4;
+    const uint32_t a_wr = ring0 + RG::WS + (wave * 16 + r16) * 4;  // FOLD: d (and dmin) of the A operand's row
     static_assert((RING - 1) * RG::W_N + 192 + 16 * 3 + 16 < 65536, "weight slots within the LDS immediate");
     static_assert(RG::ACT_N + 8 * KM_TOK * 64 < 65536, "two activation slots within the LDS immediate");
     // activation chunk reads of slot S at inner offset O
@@ -1046,22 +1055,25 @@ __device__ __forceinline__ void kmma_tile(const MmaArgs& g, const Tile& tl, int 
         if (Q4K) X0 = ds_r32<OW>(a_sc);
         else X = ds_r128<OW>(a_sc);
         uint32_t Y = ds_r32<OW>(a_y);
-        u32x4 WSV = ds_r128<S * RG::WS_N>(a_ws);
+        u32x4 WSV = {0u, 0u, 0u, 0u};
+        uint32_t WR = 0;
+        if constexpr (FOLD) WR = ds_r32<S * RG::WS_N>(a_wr);
+        else WSV = ds_r128<S * RG::WS_N>(a_ws);
         uint32_t YD[NJ];
         u32x2 BS[NJ];
         u32x4 B[2][NJ];
         constexpr int OY = S * RG::YD_N, OB = S * RG::BSM_N;
-        YD[0] = ds_r32<OY>(a_yd);
-        if (Q4K) BS[0] = ds_r64<OB>(a_bs);
+        if (!FOLD) YD[0] = ds_r32<OY>(a_yd);
+        if (Q4K && !FOLD) BS[0] = ds_r64<OB>(a_bs);
         B[0][0] = act_rd(SC, ic<0>{});
         if (NJ > 1) {
-            YD[1 % NJ] = ds_r32<OY + 64>(a_yd);
-            if (Q4K) BS[1 % NJ] = ds_r64<OB + 128>(a_bs);
+            if (!FOLD) YD[1 % NJ] = ds_r32<OY + 64>(a_yd);
+            if (Q4K && !FOLD) BS[1 % NJ] = ds_r64<OB + 128>(a_bs);
             B[0][1 % NJ] = act_rd(SC, ic<256>{});
         }
         if (NJ > 2) {
-            YD[2 % NJ] = ds_r32<OY + 128>(a_yd);
-            if (Q4K) BS[2 % NJ] = ds_r64<OB + 256>(a_bs);
+            if (!FOLD) YD[2 % NJ] = ds_r32<OY + 128>(a_yd);
+            if (Q4K && !FOLD) BS[2 % NJ] = ds_r64<OB + 256>(a_bs);
             B[0][2 % NJ] = act_rd(SC, ic<512>{});
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -1070,23 +1082,39 @@ __device__ __forceinline__ void kmma_tile(const MmaArgs& g, const Tile& tl, int 
         if (Q4K) tie(X0);
         else tie(X);
         tie(Y);
-        tie(WSV);
+        if constexpr (FOLD) tie(WR);
+        else tie(WSV);
 #pragma unroll
         for (int c = 0; c < NJ; c++) {
-            tie(YD[c]);
-            if (Q4K) tie(BS[c]);
+            if (!FOLD) tie(YD[c]);
+            if (Q4K && !FOLD) tie(BS[c]);
             tie(B[0][c]);
         }
         // d * yd (and dmin * yd) per (row 4 q + v, assignment)
         float dd[NJ][4], dm[NJ][4];
+        if constexpr (!FOLD) {
 #pragma unroll
-        for (int c = 0; c < NJ; c++)
+            for (int c = 0; c < NJ; c++)
 #pragma unroll
-            for (int v = 0; v < 4; v++) {
-                const float yd = __uint_as_float(YD[c]);
-                dd[c][v] = h2f(WSV[v] & 0xFFFFu) * yd;
-                if (Q4K) dm[c][v] = h2f(WSV[v] >> 16) * yd;
+                for (int v = 0; v < 4; v++) {
+                    const float yd = __uint_as_float(YD[c]);
+                    dd[c][v] = h2f(WSV[v] & 0xFFFFu) * yd;
+                    if (Q4K) dm[c][v] = h2f(WSV[v] >> 16) * yd;
+                }
+        }
+        // FOLD: the row's d as an fp16 pair and, for Q4_K, -fp16(dmin * m) of sub-blocks 2 q, 2 q + 1
+        const _Float16 dwh = __builtin_bit_cast(_Float16, (uint16_t)(WR & 0xFFFFu));
+        const mh2 D2 = hpair(dwh, dwh);
+        mh2 MT[2];
+        if (FOLD && Q4K) {
+            const uint32_t mw = Y >> (16 * (q & 1));  // mins[2 q], mins[2 q + 1]
+            const float dmin = h2f(WR >> 16);
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const _Float16 mt = (_Float16)(dmin * (float)(int)((mw >> (8 * j)) & 0xFFu));  // exact, then rounded once
+                MT[j] = hpair(-mt, -mt);
             }
+        }
         // per-s constants of the A operands (s = 2 q, 2 q + 1).  Q4_K: the nibble n enters as the half
         // 1024 + n (l even) or 1024 + 16 n (l odd), so sc * n = fma(., sc, -1024 sc) or
         // fma(., sc / 16, -64 sc).  Q6_K: the 6-bit value v enters as 1024 + 4 v, q = v - 32, and with
@@ -1128,6 +1156,10 @@ __device__ __forceinline__ void kmma_tile(const MmaArgs& g, const Tile& tl, int 
                 w[1] = pk_fma(and_or(x0 >> 8, m, 0x64006400u), k0, c0);
                 w[2] = pk_fma(and_or(x1, m, 0x64006400u), k1, c1);
                 w[3] = pk_fma(and_or(x1 >> 8, m, 0x64006400u), k1, c1);
+                if constexpr (FOLD) {  // sc * q (exact) * d - fp16(dmin * m), one rounding
+#pragma unroll
+                    for (int i = 0; i < 4; i++) w[i] = pk_fma(w[i], D2, MT[i >> 1]);
+                }
                 A = __builtin_bit_cast(mh8, make_uint4(w[0], w[1], w[2], w[3]));
             } else {
                 // the low nibble to bits 2-5 of each half, the two high bits (bits 2 i of the byte,
@@ -1152,6 +1184,10 @@ __device__ __forceinline__ void kmma_tile(const MmaArgs& g, const Tile& tl, int 
                 for (int j = 0; j < 4; j++) {
                     w[j] = pk_fma(v[j], K0[j >> 1], M0[j >> 1]);  // lo * (v - 32)
                     u[j] = pk_fma(v[j], K1[j >> 1], M1[j >> 1]);  // 32 hi * (v - 32)
+                    if constexpr (FOLD) {  // each part times d, one rounding each
+                        w[j] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(mh2, w[j]) * D2);
+                        u[j] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(mh2, u[j]) * D2);
+                    }
                 }
                 A = __builtin_bit_cast(mh8, make_uint4(w[0], w[1], w[2], w[3]));
                 A2 = __builtin_bit_cast(mh8, make_uint4(u[0], u[1], u[2], u[3]));
@@ -1169,11 +1205,17 @@ __device__ __forceinline__ void kmma_tile(const MmaArgs& g, const Tile& tl, int 
             a_op(l, A, A2);
 #pragma unroll
             for (int c = 0; c < NJ; c++) {
-                mf4 C = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, __builtin_bit_cast(mh8, B[cur][c]), zero4, 0, 0, 0);
-                if (!Q4K) C = __builtin_amdgcn_mfma_f32_16x16x32_f16(A2, __builtin_bit_cast(mh8, B[cur][c]), C, 0, 0, 0);
-                // the reference chain: sums[l] += (d * yd) * aux32[l]
+                if constexpr (FOLD) {
+                    acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, __builtin_bit_cast(mh8, B[cur][c]), acc[c], 0, 0, 0);
+                    if (!Q4K)
+                        acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A2, __builtin_bit_cast(mh8, B[cur][c]), acc[c], 0, 0, 0);
+                } else {
+                    mf4 C = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, __builtin_bit_cast(mh8, B[cur][c]), zero4, 0, 0, 0);
+                    if (!Q4K) C = __builtin_amdgcn_mfma_f32_16x16x32_f16(A2, __builtin_bit_cast(mh8, B[cur][c]), C, 0, 0, 0);
+                    // the reference chain: sums[l] += (d * yd) * aux32[l]
 #pragma unroll
-                for (int v = 0; v < 4; v++) sums[l][c][v] = sums[l][c][v] + dd[c][v] * C[v];
+                    for (int v = 0; v < 4; v++) sums[l][c][v] = sums[l][c][v] + dd[c][v] * C[v];
+                }
             }
             if (l + 1 < 8) {
                 asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -1189,7 +1231,7 @@ __device__ __forceinline__ void kmma_tile(const MmaArgs& g, const Tile& tl, int 
         step(ic<5>{});
         step(ic<6>{});
         step(ic<7>{});
-        if (Q4K) {  // the min term: sumf -= (dmin * yd) * sumi
+        if (Q4K && !FOLD) {  // the min term: sumf -= (dmin * yd) * sumi
             const uint32_t mw = Y >> (16 * (q & 1));  // mins[2 q], mins[2 q + 1]
             const _Float16 m0 = (_Float16)(int)(mw & 0xFFu), m1 = (_Float16)(int)((mw >> 8) & 0xFFu);
             const mh4 Am = {m0, m0, m1, m1};
@@ -1225,7 +1267,7 @@ __device__ __forceinline__ void kmma_tile(const MmaArgs& g, const Tile& tl, int 
             float s = sumf[c][v];
 #pragma unroll
             for (int l = 0; l < 8; l++) s += sums[l][c][v];
-            o[v] = s;
+            o[v] = FOLD ? acc[c][v] : s;
         }
         const int64_t a = g.perm[tl.start + t];
         const int lg0 = 16 * ws + 4 * q;  // lane within the row group of the first of four
@@ -1254,7 +1296,7 @@ __device__ __forceinline__ void kmma_tile(const MmaArgs& g, const Tile& tl, int 
     }
 }
 
-template <int TYPE>
+template <int TYPE, bool FOLD>
 __global__ __launch_bounds__(KM_NW * 64, 1) void k_grouped_kmma(MmaArgs g)
 {
     extern __shared__ __align__(16) unsigned char kring[];
@@ -1264,9 +1306,9 @@ __global__ __launch_bounds__(KM_NW * 64, 1) void k_grouped_kmma(MmaArgs g)
     if (tile >= *g.ntiles) return;  // uniform over the workgroup
     const Tile tl = g.tiles[tile];
     const int cnt = min(tl.cnt, KM_TOK);
-    if (cnt > 32) kmma_tile<TYPE, 3>(g, tl, cnt, kring, bx);
-    else if (cnt > 16) kmma_tile<TYPE, 2>(g, tl, cnt, kring, bx);
-    else kmma_tile<TYPE, 1>(g, tl, cnt, kring, bx);
+    if (cnt > 32) kmma_tile<TYPE, 3, FOLD>(g, tl, cnt, kring, bx);
+    else if (cnt > 16) kmma_tile<TYPE, 2, FOLD>(g, tl, cnt, kring, bx);
+    else kmma_tile<TYPE, 1, FOLD>(g, tl, cnt, kring, bx);
 }
 
 void launch_grouped_kmma(hipStream_t st, const QMat& w, Act act, const Tile* tiles, const int* ntiles, int max_tiles,
@@ -1292,14 +1334,19 @@ void launch_grouped_kmma(hipStream_t st, const QMat& w, Act act, const Tile* til
     g.out_stride = out_stride;
     g.paired = w.paired;
     const dim3 grid((w.rg + 1) / 2, max_tiles);
+    // the activations' format picks the arithmetic: folded fp16 copies take the tolerance mode
+    auto go = [&](auto kern, size_t lds) {
+        (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        launch(kern, grid, dim3(KM_NW * 64), (uint32_t)lds, st, g);
+    };
     if (w.type == PHX_Q4_K_DEV) {
         constexpr size_t lds = (size_t)KmRing<PHX_Q4_K_DEV>::BYTES;
-        (void)hipFuncSetAttribute((const void*)k_grouped_kmma<PHX_Q4_K_DEV>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        launch(k_grouped_kmma<PHX_Q4_K_DEV>, grid, dim3(KM_NW * 64), (uint32_t)lds, st, g);
+        if (act.fold) go(k_grouped_kmma<PHX_Q4_K_DEV, true>, lds);
+        else go(k_grouped_kmma<PHX_Q4_K_DEV, false>, lds);
     } else {
         constexpr size_t lds = (size_t)KmRing<PHX_Q6_K_DEV>::BYTES;
-        (void)hipFuncSetAttribute((const void*)k_grouped_kmma<PHX_Q6_K_DEV>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        launch(k_grouped_kmma<PHX_Q6_K_DEV>, grid, dim3(KM_NW * 64), (uint32_t)lds, st, g);
+        if (act.fold) go(k_grouped_kmma<PHX_Q6_K_DEV, true>, lds);
+        else go(k_grouped_kmma<PHX_Q6_K_DEV, false>, lds);
     }
 }
 

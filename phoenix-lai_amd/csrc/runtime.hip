@@ -867,9 +867,9 @@ int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, con
         agu.qh = wp<uint16_t>(c, W_AGU_H);
         agu.qhstride = d;
     }
-    // the tolerance mode (Q4_0 / Q8_0 on the matrix cores): every fp16 activation copy carries its block
-    // scale folded in, which selects the tolerance-mode products
-    agu.fold = fast && mma;
+    // the tolerance mode (the matrix-core products): every fp16 activation copy carries its block scale
+    // folded in, which selects the tolerance-mode products
+    agu.fold = fast && (mma || kmma);
     if (kmma && D.gate_up_type == PHX_Q4_K) {
         agu.bh = wp<uint16_t>(c, W_AGU_BH);
         agu.bhstride = d / 16;
@@ -936,7 +936,7 @@ int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, con
         adn.qh = wp<uint16_t>(c, W_ADN_H);
         adn.qhstride = D.down_cols;
     }
-    adn.fold = fast && mma;
+    adn.fold = fast && (mma || kmma);
     if (kmma && D.down_type == PHX_Q4_K) {
         adn.bh = wp<uint16_t>(c, W_ADN_BH);
         adn.bhstride = D.down_cols / 16;

@@ -122,3 +122,154 @@ def test_fast_math_products_and_error(ctx, pkg, orc, cfg, T):
         f"(output rms {rms:.3g}), {100 * bar.mean():.2f}% of elements within the 2e-3 bar")
     assert float(np.sqrt(np.mean(err ** 2))) <= 2e-2 * rms
     assert float(err.max()) <= 0.25 * rms
+
+
+# ---------------------------------------------------------------------------------------- K-quants
+def _q4_k_blocks(B):
+    """(d, dmin, sc [n][8], m [n][8], q [n][256]) of Q4_K super-blocks B [n][144] (the layout
+    gguf_spec.q4_k_parts decodes one block at a time)."""
+    d = B[:, 0:2].copy().view(F16)[:, 0].astype(np.float64)
+    dmin = B[:, 2:4].copy().view(F16)[:, 0].astype(np.float64)
+    s = B[:, 4:16].astype(np.int32)
+    sc = np.empty((len(B), 8), np.int32)
+    m = np.empty((len(B), 8), np.int32)
+    sc[:, :4], m[:, :4] = s[:, 0:4] & 63, s[:, 4:8] & 63
+    sc[:, 4:] = (s[:, 8:12] & 15) | ((s[:, 0:4] >> 6) << 4)
+    m[:, 4:] = (s[:, 8:12] >> 4) | ((s[:, 4:8] >> 6) << 4)
+    qs = B[:, 16:144].reshape(-1, 4, 1, 32).astype(np.int32)
+    q = np.concatenate([qs & 15, qs >> 4], axis=2).reshape(-1, 256)
+    return d, dmin, sc, m, q
+
+
+def _q6_k_blocks(B):
+    """(d, sc [n][16] signed, q [n][256] in -32..31) of Q6_K super-blocks B [n][210]."""
+    ql = B[:, 0:128].astype(np.int32)
+    qh = B[:, 128:192].astype(np.int32)
+    sc = B[:, 192:208].copy().view(np.int8).astype(np.int32)
+    d = B[:, 208:210].copy().view(F16)[:, 0].astype(np.float64)
+    q = np.empty((len(B), 256), np.int32)
+    for h in range(2):
+        L, H = ql[:, 64 * h:64 * h + 64], qh[:, 32 * h:32 * h + 32]
+        q[:, 128 * h + 0:128 * h + 32] = (L[:, :32] & 15) | ((H & 3) << 4)
+        q[:, 128 * h + 32:128 * h + 64] = (L[:, 32:] & 15) | (((H >> 2) & 3) << 4)
+        q[:, 128 * h + 64:128 * h + 96] = (L[:, :32] >> 4) | (((H >> 4) & 3) << 4)
+        q[:, 128 * h + 96:128 * h + 128] = (L[:, 32:] >> 4) | (((H >> 6) & 3) << 4)
+    return d, sc, q - 32
+
+
+def folded_k_rows(pkg, L, which, e, rows):
+    """The tolerance mode's weight operands of the given rows, as float64 [parts][rows][cols]:
+    Q4_K one part, fp16(sc q d - fp16(dmin m)) (one rounding of the exact sc q d - fp16(dmin m));
+    Q6_K two parts, fp16(lo q d) and fp16(32 hi q d) with sc = 32 hi + lo, lo = sc & 31."""
+    S = pkg.synth
+    if which == "gu":
+        t, cols, nrows, buf = L["gate_up_type"], L["d"], 2 * L["n_ff"], L["gate_up_exps"]
+    else:
+        t, cols, nrows, buf = L["down_type"], L["down_cols"], L["d"], L["down_exps"]
+    rb = S.row_bytes(t, cols)
+    base = e * nrows * rb
+    raw = np.stack([np.frombuffer(buf[base + r * rb: base + (r + 1) * rb].tobytes(), np.uint8) for r in rows])
+    nb = cols // 256
+    if t == pkg.moe.PHX.Q4_K:
+        d, dmin, sc, m, q = _q4_k_blocks(raw.reshape(-1, 144))
+        mt = (dmin[:, None] * m).astype(F16).astype(np.float64)  # [blk][8]
+        sub = np.arange(256) // 32
+        w = (sc[:, sub] * q * d[:, None] - mt[:, sub]).astype(F16).astype(np.float64)
+        return w.reshape(1, len(rows), nb * 256)
+    d, sc, q = _q6_k_blocks(raw.reshape(-1, 210))
+    sub = np.arange(256) // 16
+    lo, hi = sc & 31, sc >> 5
+    wl = (lo[:, sub] * q * d[:, None]).astype(F16).astype(np.float64)
+    wh = (32 * hi[:, sub] * q * d[:, None]).astype(F16).astype(np.float64)
+    return np.stack([wl.reshape(len(rows), -1), wh.reshape(len(rows), -1)])
+
+
+def folded_k_act(orc, v):
+    """fp16(fp32(q_x d_x)) of the oracle's Q8_K of v (the kernels' quantizers are bit-exact to it)."""
+    d, q, _ = orc.quantize_q8_k(v)
+    f = q.reshape(-1, 256).astype(np.float32) * d[:, None].astype(np.float32)
+    return f.astype(F16).reshape(-1).astype(np.float64)
+
+
+def kmma_bound(P, b):
+    """|fp32 matrix-core sum - exact sum| over the parts P [parts][rows][K]: each 32-deep MFMA adds to the
+    fp32 accumulator once (K / 32 additions per part) after at most 32 roundings inside it."""
+    n = P.shape[0] * P.shape[2] / 32 + 32
+    return n * 2.0 ** -24 * sum(np.abs(p) @ np.abs(b) for p in P) + 1e-30
+
+
+def test_kquant_block_decoders_match_the_spec(pkg):
+    """The vectorized decoders above against gguf_spec's one-block decoders on random super-blocks."""
+    import gguf_spec as gs
+    rng = np.random.default_rng(11)
+    PHX = pkg.moe.PHX
+    B4 = gs.random_blocks(rng, PHX.Q4_K, 6).reshape(6, 144)
+    d, dmin, sc, m, q = _q4_k_blocks(B4)
+    for i in range(6):
+        rd, rdm, rsc, rm, rq = gs.q4_k_parts(B4[i])
+        assert (d[i], dmin[i]) == (rd, rdm)
+        np.testing.assert_array_equal(sc[i], rsc)
+        np.testing.assert_array_equal(m[i], rm)
+        np.testing.assert_array_equal(q[i], rq)
+    B6 = gs.random_blocks(rng, PHX.Q6_K, 6).reshape(6, 210)
+    d, sc, q = _q6_k_blocks(B6)
+    for i in range(6):
+        rd, rsc, rq = gs.q6_k_parts(B6[i])
+        assert d[i] == rd
+        np.testing.assert_array_equal(sc[i], rsc)
+        np.testing.assert_array_equal(q[i], rq)
+
+
+def test_fast_math_kquant_products_and_error(ctx, pkg, orc):
+    """C4 (Q4_K gate|up, Q6_K down) in the tolerance mode: routing bit-exact, gate|up and down on sampled
+    assignments and rows equal to the float64 textbook of the folded operands within the fp32 bound, the
+    outputs' distance from the CPU reference bounded as for Q4_0."""
+    cfg, T = "c4_kquant", 512
+    say(f"fast math {cfg} T={T}")
+    L = pkg.synth.make_layer(cfg)
+    x = pkg.synth.make_input(cfg, T=T)
+    ctx.upload(0, L)
+    out = ctx.ffn(0, x, fast_math=True, keep_intermediates=True)
+    ids, w, off, perm, logits = ctx.routing()
+    g, u, yd = ctx.intermediates()
+    k, nf, d = L["n_used"], L["n_ff"], L["d"]
+    rids = np.stack([orc.router(L, x[t])[1] for t in range(T)])
+    np.testing.assert_array_equal(ids, rids)
+    roff, rperm = orc.bucket(ids, L["n_expert"])
+    np.testing.assert_array_equal(off, roff)
+    np.testing.assert_array_equal(perm, rperm)
+    rng = np.random.default_rng(7)
+    sample = sorted(rng.choice(T * k, size=8, replace=False))
+    rows_gu = np.sort(rng.choice(2 * nf, size=192, replace=False))
+    rows_dn = np.sort(rng.choice(d, size=192, replace=False))
+    worst = {"g": 0.0, "yd": 0.0}
+    for a in sample:
+        t, e = a // k, int(ids.reshape(-1)[a])
+        n_in = orc.rmsnorm(x[t], L["pre_ffw_norm_2"], L["eps"])
+        P = folded_k_rows(pkg, L, "gu", e, rows_gu)
+        bx = folded_k_act(orc, n_in)
+        want = sum(p @ bx for p in P)
+        bound = kmma_bound(P, bx)
+        got = np.concatenate([g[a], u[a]])[rows_gu].astype(np.float64)
+        assert np.all(np.abs(got - want) <= bound), f"gate|up of assignment {a} beyond the fp32 bound"
+        worst["g"] = max(worst["g"], float(np.max(np.abs(got - want) / bound)))
+        h = (orc.gelu(g[a]) * u[a]).astype(np.float32)
+        hp = np.zeros(L["down_cols"], np.float32)
+        hp[:nf] = h
+        P = folded_k_rows(pkg, L, "dn", e, rows_dn)
+        bh = folded_k_act(orc, hp)
+        want = sum(p @ bh for p in P)
+        bound = kmma_bound(P, bh)
+        got = yd[a][rows_dn].astype(np.float64)
+        assert np.all(np.abs(got - want) <= bound), f"down of assignment {a} beyond the fp32 bound"
+        worst["yd"] = max(worst["yd"], float(np.max(np.abs(got - want) / bound)))
+    toks = np.arange(0, T, max(1, T // 32))
+    ref, _, _ = orc.moe_block(L, x[toks])
+    err = np.abs(out[toks].astype(np.float64) - ref)
+    rms = float(np.sqrt(np.mean(ref.astype(np.float64) ** 2)))
+    bar = err <= np.maximum(2e-3 * np.abs(ref), 1e-4)
+    say(f"  products within the fp32 bound (worst fraction of the bound: g/u {worst['g']:.3f}, "
+        f"down {worst['yd']:.3f}); outputs vs CPU reference: max abs {err.max():.3g}, rms {np.sqrt(np.mean(err**2)):.3g} "
+        f"(output rms {rms:.3g}), {100 * bar.mean():.2f}% of elements within the 2e-3 bar")
+    assert float(np.sqrt(np.mean(err ** 2))) <= 2e-2 * rms
+    assert float(err.max()) <= 0.25 * rms
