@@ -216,8 +216,11 @@ int phx_moe_profile_read(phx_moe_ctx* ctx, double* total_ms, int64_t* launches);
 /* Arithmetic self-test: runs the library's device primitives on n host inputs so a test can check
  * them bit for bit against IEEE results.  op: 0 f32 division a/b, 1 rms scale 1/(float)sqrt(a+b)
  * as the reference writes it, 2 double->float of (double)a/(double)b, 3 roundf(a), 4 fp16 bits of a
- * (round to nearest even), 5 nearest-even int of a (1.5*2^23 trick), 6 GELU(a).  out is float
- * (int results as their value). */
+ * (round to nearest even), 5 nearest-even int of a (1.5*2^23 trick), 6 GELU(a), 7 the float of
+ * fp16 bits a; 8 and 9 one fp32 matrix-core product (v_mfma_f32_16x16x4_f32) per 64 inputs (n a
+ * multiple of 64): lane l of a group supplies A[l % 16][l / 16] = a and B[l / 16][l % 16] = b, the
+ * accumulator starts at 0 (8) or 1 (9), and out holds D[4 (l / 16)][l % 16] (the numerics the
+ * many-token router's error bound assumes).  out is float (int results as their value). */
 int phx_moe_selftest(phx_moe_ctx* ctx, int op, int n, const float* a, const float* b, float* out);
 
 /* Average time (ms) of `iters` coalesced streaming reads of a device buffer: the achievable HBM

@@ -536,6 +536,8 @@ __device__ __forceinline__ void lds_wait(u32x4& a, u32x4& b, uint32_t& c, u32x2&
 {
     asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d), "+v"(e), "+v"(f)::"memory");
 }
+// s_waitcnt vmcnt(n) alone (gfx9 encoding: vmcnt bits 3:0 and 15:14)
+constexpr int vm_wait(int n) { return (n & 15) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
 // compile-time index for unrolled steps with immediate offsets
 template <int N> using ic = std::integral_constant<int, N>;
 // f(ic<0>), f(ic<1>), ..., f(ic<N - 1>) in order

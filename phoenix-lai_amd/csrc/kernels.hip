@@ -1912,10 +1912,18 @@ void launch_fill_u32(hipStream_t st, uint32_t* p, int64_t n, uint32_t v)
 }
 
 // ------------------------------------------------------------------------------ arithmetic self-test
+typedef float st_f4 __attribute__((ext_vector_type(4)));
 __global__ void k_selftest(int op, int n, const float* __restrict__ a, const float* __restrict__ b, float* __restrict__ out,
                            const float* __restrict__ tab)
 {
     int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (op >= 8) {  // one 16 x 16 x 4 fp32 matrix-core product per 64 elements (n a multiple of 64)
+        if (i - (i & 63) >= n) return;  // whole waves
+        const float c = op == 9 ? 1.0f : 0.0f;
+        const st_f4 d = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], b[i], st_f4{c, c, c, c}, 0, 0, 0);
+        out[i] = d[0];
+        return;
+    }
     if (i >= n) return;
     float x = a[i], y = b[i], r = 0.0f;
     switch (op) {

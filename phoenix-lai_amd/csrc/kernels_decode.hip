@@ -63,6 +63,7 @@ struct DecArgs {
     int seq;              // position in a captured stack (clock-stamp slot of the instrumented build)
     float eps;
     const float* x;       // [T][d]
+    const float* xscale;  // [T] the rows' rms scales when the prologue formed them (else null)
     const float* W;       // [E][d] router (ffn_gate_inp.weight)
     const float* gis;     // ffn_gate_inp.scale
     const float* ds;      // ffn_down_exps.scale
@@ -78,6 +79,7 @@ struct DecArgs {
     double* Lb;           // [T][E] certified logits (double sums)
     double* Bb;           // [T][E] their error bounds
     uint4* kb;            // [T][E] selection keys: rank key, lower end, upper end, finite (route_wg)
+    int* cbad;            // [1 + T]: the count, then the tokens k_cert_select leaves to the exact chains
     int* ids;             // [T][k]
     float* w;             // [T][k]
     float* logits;        // [T][E]
@@ -596,6 +598,7 @@ __device__ __forceinline__ void route_wg(const DecArgs& a, int t, int e, float* 
     __shared__ float wA[RT_MAXW], wP[RT_MAXW];
     const int tid = threadIdx.x, NT = blockDim.x, lane = tid & 63, wave = tid >> 6, nw = NT >> 6, d = a.d;
     TL_STAMP(a.seq, 0, 0);
+    if (!FUSED && a.cbad && blockIdx.x == 0 && tid == 0) a.cbad[0] = 0;  // k_cert_select's list count
     // the input blocks b = e + g E of this workgroup, 8 threads per block counted from the last thread (the
     // last wave, while wave 0 forms the sum, bound and key): their norm weights, loaded now
     const int nb = d / 32, g = (NT - 1 - tid) >> 3, l8 = tid & 7, b = e + g * a.E, bc = min(b, nb - 1);
@@ -926,13 +929,13 @@ __device__ bool wave_topk(const DecArgs& a, int t, const SelIn& in, int* s_ids, 
 // four wave counts, the chosen experts' lower ends [16] and the ambiguous experts' exact keys [E]
 // (doubles), and two product buffers of sel_buf_floats(NT) floats.  The host sizes the region with
 // the same function.
-__host__ __device__ inline size_t sel_buf_floats(int NT) { return (size_t)4 * (NT - 64) + 256; }
+__host__ __device__ inline size_t sel_buf_floats(int NT, int P = 1) { return (size_t)4 * P * (NT - 64) + 256; }
 
 struct SelLds {
     size_t m, list, lo, key, buf, total;
 };
 
-__host__ __device__ inline SelLds sel_lds(int T, int E, int d, int NT)
+__host__ __device__ inline SelLds sel_lds(int T, int E, int d, int NT, int P = 1)
 {
     SelLds o;
     const size_t TE = (size_t)T * E;
@@ -941,7 +944,7 @@ __host__ __device__ inline SelLds sel_lds(int T, int E, int d, int NT)
     o.lo = (o.list + (size_t)(E + 4) * 4 + 7) & ~(size_t)7;
     o.key = o.lo + PHX_MAX_USED_DEV * 8;
     o.buf = (o.key + (size_t)E * 8 + 15) & ~(size_t)15;
-    o.total = o.buf + 2 * sel_buf_floats(NT) * 4;
+    o.total = o.buf + 2 * sel_buf_floats(NT, P) * 4;
     return o;
 }
 
@@ -994,8 +997,8 @@ __device__ void exact_chains(const float* W, int d, const float* sm, const int* 
                 const float4* b4 = (const float4*)(sbuf + (sp & 1) * bufn + tid * stride);
                 // batches of sixteen float4: the batch's reads go out together and the adds of its first
                 // float4 wait for one LDS round trip, the rest arrive while the earlier ones are added
-                const int c8 = c4 & ~15;
-                for (int c = 0; c < c8; c += 16) {
+                const int c16 = c4 & ~15;
+                for (int c = 0; c < c16; c += 16) {
                     float4 v[16];
 #pragma unroll
                     for (int u = 0; u < 16; u++) v[u] = b4[c + u];
@@ -1007,7 +1010,7 @@ __device__ void exact_chains(const float* W, int d, const float* sm, const int* 
                         s += v[u].w;
                     }
                 }
-                for (int c = c8; c < c4; c++) {
+                for (int c = c16; c < c4; c++) {
                     const float4 t = b4[c];
                     s += t.x;
                     s += t.y;
@@ -1022,6 +1025,89 @@ __device__ void exact_chains(const float* W, int d, const float* sm, const int* 
     __syncthreads();
 }
 
+// The fallback kernel's chains (exact_chains' arithmetic and order): each producer forms CF_P float4 of
+// products per step, so a chain's segment per step is CF_P times longer (fewer barriers), the W loads
+// for the next step issued right after the current step's products; the adding lane reads its segment
+// with explicit LDS reads, 32 float4 per round trip.
+constexpr int CF_P = 2;
+__device__ void exact_chains_wide(const float* W, int d, const float* sm, const int* list, int ng, float* sbuf,
+                                  size_t bufn, double* out)
+{
+    ng = __builtin_amdgcn_readfirstlane(ng);
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), NPT = blockDim.x - 64;
+    const int sq = CF_P * NPT / ng, segq = min(sq >= 32 ? sq & ~31 : sq, d / 4), seg = 4 * segq, stride = seg + 4;
+    const int nseg = (d + seg - 1) / seg, n4 = d / 4;
+    const float4* sm4 = (const float4*)sm;
+    // producer q = tid - 64: slots q + p NPT of the step (chain j, float4 o), idle past ng * segq
+    const int q = tid >= 64 ? tid - 64 : 0;
+    int jq[CF_P], oq[CF_P];
+    bool act[CF_P];
+    const float4* wr[CF_P];
+    float4 r[CF_P];
+#pragma unroll
+    for (int p = 0; p < CF_P; p++) {
+        const int sl = q + p * NPT;
+        jq[p] = sl / segq;
+        oq[p] = sl - jq[p] * segq;
+        act[p] = wave > 0 && jq[p] < ng;
+        wr[p] = (const float4*)(W + (int64_t)list[min(jq[p], ng - 1)] * d);
+        r[p] = wr[p][min(oq[p], n4 - 1)];
+    }
+    float s = 0.0f;
+    const uint32_t abase = (uint32_t)(uintptr_t)(lds_void_t)(sbuf + tid * stride);
+    for (int st = 0; st <= nseg; st++) {
+        if (st < nseg) {
+#pragma unroll
+            for (int p = 0; p < CF_P; p++) {
+                const int i4 = st * segq + oq[p];
+                if (act[p] && i4 < n4) {
+                    const float4 m = sm4[i4];
+                    float4 v;
+                    v.x = r[p].x * m.x;
+                    v.y = r[p].y * m.y;
+                    v.z = r[p].z * m.z;
+                    v.w = r[p].w * m.w;
+                    *(float4*)(sbuf + (st & 1) * bufn + jq[p] * stride + 4 * oq[p]) = v;
+                }
+            }
+#pragma unroll
+            for (int p = 0; p < CF_P; p++) r[p] = wr[p][min((st + 1) * segq + oq[p], n4 - 1)];  // the next step's
+        }
+        if (wave == 0 && st >= 1 && tid < ng) {
+            const int sp = st - 1, c4 = min(segq, n4 - sp * segq), c32 = c4 & ~31;
+            const uint32_t a0 = abase + (uint32_t)((sp & 1) * bufn * 4);
+            for (int c = 0; c < c32; c += 32) {
+                u32x4 v[32];
+                static_for<32>([&](auto U) { v[decltype(U)::value] = ds_r128<16 * decltype(U)::value>(a0 + 16 * c); });
+                static_for<32>([&](auto U) {
+                    constexpr int u = decltype(U)::value;
+                    // two waits per batch (a wait per float4 would cost an issue slot per four adds): at
+                    // most 15 LDS reads are outstanding (the counter's width), so the first 17 have landed
+                    // once 15 remain; the rest long before the first 17 are added
+                    if constexpr (u == 0) asm volatile("s_waitcnt lgkmcnt(15)" ::: "memory");
+                    if constexpr (u == 17) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                    tie(v[u]);
+                    s += __uint_as_float(v[u].x);
+                    s += __uint_as_float(v[u].y);
+                    s += __uint_as_float(v[u].z);
+                    s += __uint_as_float(v[u].w);
+                });
+            }
+            const float4* b4 = (const float4*)(sbuf + (sp & 1) * bufn + tid * stride);
+            for (int c = c32; c < c4; c++) {
+                const float4 t = b4[c];
+                s += t.x;
+                s += t.y;
+                s += t.z;
+                s += t.w;
+            }
+        }
+        __syncthreads();
+    }
+    if (wave == 0 && tid < ng) out[list[tid]] = (double)s;
+    __syncthreads();
+}
+
 // Exact selection for the tokens marked in s_bad (rare): the experts that can reach the chosen ones
 // (the ambiguous ones) are recomputed as the reference's float chains (src/GemmaCpu.cs:389-395) and
 // ranked exactly by the strict '>' scan of GemmaCpu.cs:400-405 (ties to the lower index; a NaN
@@ -1029,11 +1115,13 @@ __device__ void exact_chains(const float* W, int d, const float* sm, const int* 
 // chosen expert's lower end, so the top-k lies among the ambiguous ones, unless a chain ends
 // non-finite: then every expert of the token is recomputed and ranked.  un: the LDS of sel_lds; sL (at un) ends holding the logits
 // the routing reports for those tokens.
+// PIPE: the fallback kernel's variant (the prologue's rms scales when given)
+template <bool PIPE = false>
 __device__ void select_exact(const DecArgs& a, unsigned char* un, int* s_ids, const int* s_bad, double* red,
                              bool count)
 {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, NT = blockDim.x;
-    const SelLds lds = sel_lds(a.T, a.E, a.d, NT);
+    const SelLds lds = sel_lds(a.T, a.E, a.d, NT, PIPE ? CF_P : 1);
     double* sL = (double*)un;
     float* sm = (float*)(un + lds.m);
     int* slist = (int*)(un + lds.list);
@@ -1059,9 +1147,14 @@ __device__ void select_exact(const DecArgs& a, unsigned char* un, int* s_ids, co
             const int ex = s_ids[tt * k + tid];
             slo[tid] = Lr[ex] - Br[ex];
         }
-        double s = 0.0;
-        for (int i = tid; i < a.d; i += NT) s += (double)xr[i] * (double)xr[i];
-        const float rinv_t = rms_scale_from_mean(wg_mean_sq(s, xr, a.d, red, nullptr), a.eps);
+        float rinv_t;
+        if (PIPE && a.xscale) {  // the prologue's (the same certified mean and expression)
+            rinv_t = a.xscale[tt];
+        } else {
+            double s = 0.0;
+            for (int i = tid; i < a.d; i += NT) s += (double)xr[i] * (double)xr[i];
+            rinv_t = rms_scale_from_mean(wg_mean_sq(s, xr, a.d, red, nullptr), a.eps);
+        }
         for (int i = tid; i < a.d; i += NT) sm[i] = ((xr[i] * rinv_t) * sc) * a.gis[i];
         const bool nonfinite = __syncthreads_or(tid < E && !(isfinite(lb) && isfinite(bb)));  // publishes sm, slo
         // the lowest lower end among the fast path's chosen experts: an expert whose upper end does not
@@ -1092,7 +1185,11 @@ __device__ void select_exact(const DecArgs& a, unsigned char* un, int* s_ids, co
             if (amb) slist[off + __popcll(m & ((1ull << lane) - 1))] = tid;
             __syncthreads();
             for (int g0 = 0; g0 < na; g0 += 64)
-                exact_chains(a.W, a.d, sm, slist + g0, min(64, na - g0), sbuf, sel_buf_floats(NT), sL + tt * E);
+                if constexpr (PIPE)
+                    exact_chains_wide(a.W, a.d, sm, slist + g0, min(64, na - g0), sbuf, sel_buf_floats(NT, CF_P),
+                                      sL + tt * E);
+                else
+                    exact_chains(a.W, a.d, sm, slist + g0, min(64, na - g0), sbuf, sel_buf_floats(NT), sL + tt * E);
             if (all) break;
             // a non-finite chain (overflow) voids the bounds' argument: recompute every expert
             const bool nfc = tid < na && !isfinite(sL[tt * E + slist[tid]]);
@@ -1233,24 +1330,100 @@ __device__ void write_routing(const DecArgs& a, LF Lr, const int* s_ids, const i
     }
 }
 
-// The general path's selection from the certified router (k_dec_route's sums and bounds), one
-// workgroup of CS_NT threads per token: the fast path of wave_topk, else select_exact (counted as a
-// router fallback); then the token's ids and weights (as write_routing) and the logits it used.
-constexpr int CS_NT = 256;
-__global__ __launch_bounds__(CS_NT) void k_cert_select(DecArgs a)
+// One token's routing outputs from one wave: its logits (Lr: the exact chains' values where the
+// selection ran them, the certified sums elsewhere), ids and weights (src/GemmaCpu.cs:406-407,417, as
+// write_routing).
+__device__ void token_routing_out(const DecArgs& a, int t, const double* Lr, const int* s_ids)
 {
-    extern __shared__ __align__(16) unsigned char csm[];  // sel_lds(1, E, d, CS_NT)
-    __shared__ int s_ids[PHX_MAX_USED_DEV];
-    __shared__ unsigned s_kb[2 * PHX_MAX_USED_DEV];
-    __shared__ double red[CS_NT / 64 + 1];
-    __shared__ int s_bad;
-    const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    DecArgs b = a;  // the token's own view: one token
+    const int lane = threadIdx.x & 63;
+    for (int e = lane; e < a.E; e += 64) a.logits[(int64_t)t * a.E + e] = (float)Lr[e];
+    const int j = lane;
+    const bool act = j < a.k;
+    const int id = act ? s_ids[j] : 0;
+    const float selj = act ? (float)Lr[id] : 0.0f;
+    const float sel0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(selj), 0));
+    const float top = (a.rule == 1 && j > 0) ? 1.0f : sel0;
+    const float pj = act ? (float)exp((double)(selj - top)) : 0.0f;
+    double sum = 0.0;
+    for (int q = 0; q < a.k; q++)  // in rank order
+        sum += (double)__int_as_float(__builtin_amdgcn_readlane(__float_as_int(pj), q));
+    if (act) {
+        a.ids[(int64_t)t * a.k + j] = id;
+        a.w[(int64_t)t * a.k + j] = (float)((double)pj / sum) * a.ds[id];
+    }
+}
+
+// The token's own view of the certified sums (one token)
+__device__ __forceinline__ DecArgs token_view(const DecArgs& a, int t)
+{
+    DecArgs b = a;
     b.T = 1;
     b.x = a.x + (int64_t)t * a.d;
+    b.xscale = a.xscale ? a.xscale + t : nullptr;
     b.Lb = a.Lb + (int64_t)t * a.E;
     b.Bb = a.Bb + (int64_t)t * a.E;
     b.kb = a.kb + (int64_t)t * a.E;
+    return b;
+}
+
+// The general path's selection from the certified routers (k_dec_route's or k_router_mm's sums and
+// bounds), one wave per token: the fast path of wave_topk and the token's ids, weights and logits; a
+// token whose order the bounds leave open is marked in bad[] for k_cert_fallback.
+constexpr int CS_TPW = 4;  // tokens (waves) per workgroup
+__global__ __launch_bounds__(64 * CS_TPW) void k_cert_select(DecArgs a)
+{
+    __shared__ int s_ids[CS_TPW][PHX_MAX_USED_DEV];
+    __shared__ unsigned s_kb[CS_TPW][2 * PHX_MAX_USED_DEV];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int t = blockIdx.x * CS_TPW + wave;
+    if (t >= a.T) return;  // wave-uniform; no workgroup barrier follows
+    const DecArgs b = token_view(a, t);
+    SelIn in;
+    sel_issue(b, 0, in);
+    const bool cert = wave_topk(b, 0, in, s_ids[wave], s_kb[wave], s_kb[wave] + PHX_MAX_USED_DEV);
+    if (cert) {
+        token_routing_out(a, t, b.Lb, s_ids[wave]);
+    } else {
+        if (lane < a.k) a.ids[(int64_t)t * a.k + lane] = s_ids[wave][lane];  // provisional: their lower ends
+        if (lane == 0) a.cbad[1 + atomicAdd(&a.cbad[0], 1)] = t;  // (the router cleared the count)
+    }
+}
+
+// The tokens k_cert_select listed: the exact selection (select_exact, counted as router fallbacks)
+// with a workgroup of CF_NT threads per token, so that each chain's segment per step is long; workgroup
+// g takes the listed tokens g, g + G, ... (G workgroups).
+constexpr int CF_NT = 512;
+__global__ __launch_bounds__(CF_NT) void k_cert_fallback(DecArgs a)
+{
+    extern __shared__ __align__(16) unsigned char csm[];  // sel_lds(1, E, d, CF_NT)
+    __shared__ int s_ids[PHX_MAX_USED_DEV];
+    __shared__ double red[CF_NT / 64 + 1];
+    __shared__ int s_one;
+    const int tid = threadIdx.x, wave = tid >> 6, G = gridDim.x;
+    if (tid == 0) s_one = 1;
+    const int n = a.cbad[0];
+    for (int q = blockIdx.x; q < n; q += G) {  // uniform
+        const int tt = a.cbad[1 + q];
+        const DecArgs b = token_view(a, tt);
+        if (tid < a.k) s_ids[tid] = a.ids[(int64_t)tt * a.k + tid];  // k_cert_select's provisional top-k
+        __syncthreads();
+        select_exact<true>(b, csm, s_ids, &s_one, red, true);
+        if (wave == 0) token_routing_out(a, tt, (const double*)csm, s_ids);
+        __syncthreads();
+    }
+}
+
+// Few tokens (at most one workgroup per compute unit): one workgroup of CF_NT threads per token, the
+// fast path in wave 0 and, for a token the bounds leave open, the exact selection in the same launch.
+__global__ __launch_bounds__(CF_NT) void k_cert_select_one(DecArgs a)
+{
+    extern __shared__ __align__(16) unsigned char csm[];  // sel_lds(1, E, d, CF_NT, CF_P)
+    __shared__ int s_ids[PHX_MAX_USED_DEV];
+    __shared__ unsigned s_kb[2 * PHX_MAX_USED_DEV];
+    __shared__ double red[CF_NT / 64 + 1];
+    __shared__ int s_bad;
+    const int t = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const DecArgs b = token_view(a, t);
     if (wave == 0) {
         SelIn in;
         sel_issue(b, 0, in);
@@ -1259,25 +1432,233 @@ __global__ __launch_bounds__(CS_NT) void k_cert_select(DecArgs a)
     }
     __syncthreads();
     const bool exact = s_bad != 0;  // uniform
-    if (exact) select_exact(b, csm, s_ids, &s_bad, red, true);
-    const double* sL = (const double*)csm;
-    for (int e = tid; e < a.E; e += CS_NT) a.logits[(int64_t)t * a.E + e] = (float)(exact ? sL[e] : b.Lb[e]);
-    if (wave == 0) {  // weights (src/GemmaCpu.cs:406-407,417), as write_routing
-        const int j = lane;
-        const bool act = j < a.k;
-        const int id = act ? s_ids[j] : 0;
-        const float selj = act ? (float)(exact ? sL[id] : b.Lb[id]) : 0.0f;
-        const float sel0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(selj), 0));
-        const float top = (a.rule == 1 && j > 0) ? 1.0f : sel0;
-        const float pj = act ? (float)exp((double)(selj - top)) : 0.0f;
-        double sum = 0.0;
-        for (int q = 0; q < a.k; q++)  // in rank order
-            sum += (double)__int_as_float(__builtin_amdgcn_readlane(__float_as_int(pj), q));
-        if (act) {
-            a.ids[(int64_t)t * a.k + j] = id;
-            a.w[(int64_t)t * a.k + j] = (float)((double)pj / sum) * a.ds[id];
+    if (exact) select_exact<true>(b, csm, s_ids, &s_bad, red, true);
+    if (wave == 0) token_routing_out(a, t, exact ? (const double*)csm : b.Lb, s_ids);
+}
+
+// ------------------------------------------------------------------------------ k_router_mm
+// The certified router for many tokens, where a workgroup per (token, expert) no longer pays: the
+// logits of a tile of TM tokens x TN experts as fp32 matrix-core sums, with the bound k_cert_select
+// certifies the top-k order from (the decode router's L, B, keys; the reference chain is
+// src/GemmaCpu.cs:389-395, its input m_i = ((x_i * rinv) * sc) * s_i, :388-389).
+//
+// Split over the reduction: wave w of the RM_NW waves sums the chunks [c0, c0 + cnt) of 16 elements
+// of every logit of the tile (v_mfma_f32_16x16x4_f32; lane group g of a 16 x 16 product holds the
+// elements 4 g .. 4 g + 3 of the chunk, so the four products of a chunk cover it whole), and adds
+// |C_j|, its accumulator after each chunk j, to a sum.  Each wave streams its own operands through an
+// LDS ring of RM_RING chunks (one direct global -> LDS load per 16 rows: x, W, the router scale), so
+// no barrier is needed inside the loop.
+//
+// The bound.  With p_i = fl(m_i w_i), S_k = sum_{i <= k} p_i and u = 2^-24, the reference's chain
+// ends within 1.004 u sum_k |S_k| of S_n (n <= 65536).  Range r (n_r elements, exact prefix O_r at its
+// start) gives sum_{k in r} |S_k| <= n_r |O_r| + 16 sum_j |Q_rj| + 15 sum_r |p| (Q_rj the range's own
+// prefix at the end of chunk j: within a chunk each prefix differs from the chunk end's by at most
+// the chunk's |p|).  A 4-deep fp32 product rounds at most five times, each to nearest, so the matrix
+// cores' sum differs from the exact one of the exact products by at most 5 u (|C_in| + sum |a b|) per
+// instruction, summed: 20 u (sum_j |C_j| + sum |m w|) over a range (every instruction's C_in lies
+// within the chunk's |m w| of the chunk's start).  Products rounded: u sum |m w|.  Together, with the
+// second-order terms (the n_r-fold ranges' errors, the float sums of |C_j| and of the squares) inside
+// the 1.03 factor:
+//   |S_ref - L| <= 1.03 u (sum_r n_r |O_r| + 36 sum_rj |C_rj| + 37 sum_r |m_r| |w_r|) + 2^-50 sum_r |C_r|
+//                  + 2^-90 n,
+// sum |m w| bounded per range by Cauchy-Schwarz, O_r from the waves' totals, L their double sum; the
+// last terms cover L's double rounding and products or sums the matrix cores flush below 2^-126.  A
+// bound of 2^100 or more (or a non-finite one) is made infinite: the token then takes the exact
+// chains for every expert, as for a non-finite logit.
+constexpr int RM_NW = 8, RM_RING = 3;
+template <int TM16, int TN16>
+struct RmLds {
+    static constexpr int TM = 16 * TM16, TN = 16 * TN16;
+    static constexpr int SLOT = (TM + TN) * 64 + 64;  // [TM x rows][TN W rows] of 16 floats, the scales' 16
+    static constexpr int DMA = TM16 + TN16 + 1;       // direct loads per chunk and wave
+    static constexpr int RINGS = RM_NW * RM_RING * SLOT;
+    static constexpr int FIN = RM_NW * (2 * TM * TN + TM + TN) * 4;  // per wave: C, sum |C_j|, |m|^2, |w|^2
+    static constexpr int BYTES = RINGS > FIN ? RINGS : FIN;
+};
+typedef float mf4v __attribute__((ext_vector_type(4)));
+
+struct RmArgs {
+    int T, d, E;
+    const float *x, *xscale, *gis, *W;  // x [T][d], rinv [T], router scale [d], W [E][d]
+    double *Lb, *Bb;
+    uint4* kb;
+    int* cbad;  // the selection's list of uncertified tokens: its count is cleared here
+};
+
+// (a device function: the direct loads' builtin inside a kernel's own lambdas leaves the host side
+// without the kernel's launch stub)
+template <int TM16, int TN16>
+__device__ __forceinline__ void router_mm_tile(const RmArgs& a, unsigned char* rmsm)
+{
+    using RG = RmLds<TM16, TN16>;
+    constexpr int TM = RG::TM, TN = RG::TN;
+    const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, r = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int t0 = blockIdx.x * TM, e0 = blockIdx.y * TN;
+    const int nch = a.d / 16, base = nch / RM_NW, extra = nch % RM_NW;
+    const int c0 = wave * base + min(wave, extra), cnt = base + (wave < extra);
+    unsigned char* ring = rmsm + wave * (RM_RING * RG::SLOT);
+    const uint32_t ring0 = (uint32_t)(uintptr_t)(lds_void_t)ring;
+    if (tid == 0 && blockIdx.x == 0 && blockIdx.y == 0) a.cbad[0] = 0;
+
+    // direct-load sources: row 16 s + lane / 4 of the tile, 16 bytes (lane % 4) of the chunk; rows past
+    // the end load the last one (never stored)
+    uint32_t vx[TM16], vw[TN16];
+#pragma unroll
+    for (int s = 0; s < TM16; s++) vx[s] = (uint32_t)((min(t0 + 16 * s + (lane >> 2), a.T - 1) * a.d + 4 * (lane & 3)) * 4);
+#pragma unroll
+    for (int s = 0; s < TN16; s++) vw[s] = (uint32_t)((min(e0 + 16 * s + (lane >> 2), a.E - 1) * a.d + 4 * (lane & 3)) * 4);
+    const uint32_t vg = 16 * lane;
+    const __amdgpu_buffer_rsrc_t r_x = buf_rsrc(a.x), r_w = buf_rsrc(a.W), r_g = buf_rsrc(a.gis);
+#define RM_LOAD(rsrc, off, voff, soff) \
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t)(ring + (off)), 16, voff, soff, 0, 0)
+    auto issue = [&](auto SC, int j) {  // chunk j of the wave's range into slot S (past the end: the last again)
+        constexpr int S = decltype(SC)::value;
+        const uint32_t so = (uint32_t)((c0 + min(j, cnt - 1)) * 64);
+#pragma unroll
+        for (int s = 0; s < TM16; s++) RM_LOAD(r_x, S * RG::SLOT + 1024 * s, vx[s], so);
+#pragma unroll
+        for (int s = 0; s < TN16; s++) RM_LOAD(r_w, S * RG::SLOT + TM * 64 + 1024 * s, vw[s], so);
+        if (lane < 4) RM_LOAD(r_g, S * RG::SLOT + (TM + TN) * 64, vg, so);
+    };
+#undef RM_LOAD
+
+    float rinv[TM16];
+#pragma unroll
+    for (int i = 0; i < TM16; i++) rinv[i] = a.xscale[min(t0 + 16 * i + r, a.T - 1)];
+    const float sc = 1.0f / (float)__dsqrt_rn((double)a.d);
+    mf4v acc[TM16][TN16], sab[TM16][TN16];
+    float mm[TM16], ww[TN16];
+#pragma unroll
+    for (int i = 0; i < TM16; i++) {
+        mm[i] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < TN16; j++) acc[i][j] = sab[i][j] = mf4v{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+#pragma unroll
+    for (int j = 0; j < TN16; j++) ww[j] = 0.0f;
+    // the lane's LDS read addresses: x row 16 i + r, W row 16 j + r, 16 bytes g; the scales' 16 bytes g
+    const uint32_t a_x = ring0 + r * 64 + 16 * g, a_w = a_x + TM * 64, a_g = ring0 + (TM + TN) * 64 + 16 * g;
+
+    auto step = [&](auto SC, int j) {
+        constexpr int S = decltype(SC)::value;
+        __builtin_amdgcn_s_waitcnt(vm_wait(RG::DMA * (RM_RING - 1)));  // chunk j landed (j + 1, j + 2 may not)
+        u32x4 X[TM16], Wv[TN16], G;
+        static_for<TM16>([&](auto I) { X[I] = ds_r128<S * RG::SLOT + 1024 * decltype(I)::value>(a_x); });
+        static_for<TN16>([&](auto J) { Wv[J] = ds_r128<S * RG::SLOT + 1024 * decltype(J)::value>(a_w); });
+        G = ds_r128<S * RG::SLOT>(a_g);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int i = 0; i < TM16; i++) tie(X[i]);
+#pragma unroll
+        for (int jj = 0; jj < TN16; jj++) tie(Wv[jj]);
+        tie(G);
+        float m[TM16][4], w[TN16][4];
+#pragma unroll
+        for (int i = 0; i < TM16; i++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                m[i][q] = ((__uint_as_float(X[i][q]) * rinv[i]) * sc) * __uint_as_float(G[q]);
+                mm[i] = fmaf(m[i][q], m[i][q], mm[i]);
+            }
+#pragma unroll
+        for (int jj = 0; jj < TN16; jj++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                w[jj][q] = __uint_as_float(Wv[jj][q]);
+                ww[jj] = fmaf(w[jj][q], w[jj][q], ww[jj]);
+            }
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+#pragma unroll
+            for (int i = 0; i < TM16; i++)
+#pragma unroll
+                for (int jj = 0; jj < TN16; jj++)
+                    acc[i][jj] = __builtin_amdgcn_mfma_f32_16x16x4f32(m[i][q], w[jj][q], acc[i][jj], 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < TM16; i++)
+#pragma unroll
+            for (int jj = 0; jj < TN16; jj++)
+#pragma unroll
+                for (int v = 0; v < 4; v++) sab[i][jj][v] += fabsf(acc[i][jj][v]);
+    };
+    // chunk j + 2 goes into the slot chunk j - 1 left (its reads ended in step j - 1) before step j
+    issue(ic<0>{}, 0);
+    issue(ic<1>{}, 1);
+    for (int j = 0; j < cnt; j += RM_RING) {
+        issue(ic<2>{}, j + 2);
+        step(ic<0>{}, j);
+        if (j + 1 < cnt) {
+            issue(ic<0>{}, j + 3);
+            step(ic<1>{}, j + 1);
+        }
+        if (j + 2 < cnt) {
+            issue(ic<1>{}, j + 4);
+            step(ic<2>{}, j + 2);
         }
     }
+    static_assert(RM_RING == 3, "the loop above steps through three slots");
+    __builtin_amdgcn_s_waitcnt(vm_wait(0));  // the clamped reloads past the end (into this wave's ring)
+
+    // the squares' sums over the four lane groups (each lane: its group's elements of row r)
+#pragma unroll
+    for (int i = 0; i < TM16; i++) {
+        mm[i] += __shfl_xor(mm[i], 16);
+        mm[i] += __shfl_xor(mm[i], 32);
+    }
+#pragma unroll
+    for (int jj = 0; jj < TN16; jj++) {
+        ww[jj] += __shfl_xor(ww[jj], 16);
+        ww[jj] += __shfl_xor(ww[jj], 32);
+    }
+    __syncthreads();  // every wave is done with its ring
+    float* fC = (float*)rmsm;          // [wave][TM][TN] the range's sum
+    float* fS = fC + RM_NW * TM * TN;  // [wave][TM][TN] its sum of |C_j|
+    float* fM = fS + RM_NW * TM * TN;  // [wave][TM] |m|^2 over the range
+    float* fW = fM + RM_NW * TM;       // [wave][TN] |w|^2
+#pragma unroll
+    for (int i = 0; i < TM16; i++)
+#pragma unroll
+        for (int jj = 0; jj < TN16; jj++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) {  // lane: token 16 i + 4 g + v, expert 16 jj + r
+                const int o = (wave * TM + 16 * i + 4 * g + v) * TN + 16 * jj + r;
+                fC[o] = acc[i][jj][v];
+                fS[o] = sab[i][jj][v];
+            }
+    if (g == 0) {
+#pragma unroll
+        for (int i = 0; i < TM16; i++) fM[wave * TM + 16 * i + r] = mm[i];
+#pragma unroll
+        for (int jj = 0; jj < TN16; jj++) fW[wave * TN + 16 * jj + r] = ww[jj];
+    }
+    __syncthreads();
+    for (int o = tid; o < TM * TN; o += RM_NW * 64) {
+        const int tl = o / TN, el = o % TN, t = t0 + tl, e = e0 + el;
+        if (t >= a.T || e >= a.E) continue;
+        double O = 0.0, mainb = 0.0, cs = 0.0, absC = 0.0;
+        for (int w = 0; w < RM_NW; w++) {
+            const double nw = 16.0 * (base + (w < extra));
+            const double C = fC[(w * TM + tl) * TN + el], Sj = fS[(w * TM + tl) * TN + el];
+            mainb += nw * fabs(O) + 36.0 * Sj;
+            O += C;
+            absC += fabs(C);
+            cs += sqrt((double)fM[w * TM + tl] * (double)fW[w * TN + el]);
+        }
+        double B = 0x1.08p-24 * (mainb + 37.0 * cs) + 0x1p-50 * absC + 0x1p-90 * a.d;
+        if (!(B < 0x1p100)) B = INFINITY;  // also NaN
+        const int64_t te = (int64_t)t * a.E + e;
+        a.Lb[te] = O;
+        a.Bb[te] = B;
+        a.kb[te] = sel_key(O, B, e);
+    }
+}
+
+template <int TM16, int TN16>
+__global__ __launch_bounds__(RM_NW * 64, 1) void k_router_mm(RmArgs a)
+{
+    extern __shared__ __align__(16) unsigned char rmsm[];  // RmLds<TM16, TN16>::BYTES
+    router_mm_tile<TM16, TN16>(a, rmsm);
 }
 
 // PRESEL: the selection's inputs are loaded at entry and held in registers through the shared units
@@ -1580,6 +1961,7 @@ static DecArgs dec_args(const DecLayerH& h)
     a.seq = h.seq;
     a.eps = h.eps;
     a.x = h.x;
+    a.xscale = h.xscale;
     a.W = h.W;
     a.gis = h.gis;
     a.ds = h.ds;
@@ -1598,6 +1980,7 @@ static DecArgs dec_args(const DecLayerH& h)
     a.Lb = h.Lb;
     a.Bb = h.Bb;
     a.kb = (uint4*)h.kb;
+    a.cbad = h.bad;
     a.ids = h.ids;
     a.w = h.w;
     a.logits = h.logits;
@@ -1676,9 +2059,42 @@ void launch_dec_route(hipStream_t st, const DecLayerH& h)
 
 void launch_cert_select(hipStream_t st, const DecLayerH& h)
 {
-    const size_t lds = sel_lds(1, h.E, h.d, CS_NT).total;
-    raise_lds(k_cert_select, lds);
-    launch(k_cert_select, dim3(h.T), dim3(CS_NT), (uint32_t)lds, st, dec_args(h));
+    const DecArgs a = dec_args(h);
+    if (h.T <= std::max(h.ncu, 1)) {  // a workgroup per token fits the chip: one launch
+        const size_t lds1 = sel_lds(1, h.E, h.d, CF_NT, CF_P).total;
+        raise_lds(k_cert_select_one, lds1);
+        launch(k_cert_select_one, dim3(h.T), dim3(CF_NT), (uint32_t)lds1, st, a);
+        return;
+    }
+    launch(k_cert_select, dim3((h.T + CS_TPW - 1) / CS_TPW), dim3(64 * CS_TPW), 0, st, a);
+    // the marked tokens: at most one per compute unit at a time
+    const size_t lds = sel_lds(1, h.E, h.d, CF_NT, CF_P).total;
+    raise_lds(k_cert_fallback, lds);
+    launch(k_cert_fallback, dim3(std::min(h.T, std::max(h.ncu, 1))), dim3(CF_NT), (uint32_t)lds, st, a);
+}
+
+template <int A, int B> struct KRm { static constexpr auto fn = k_router_mm<A, B>; };
+
+bool router_mm_supported(int T, int d, int E)
+{
+    return d % 16 == 0 && d / 16 >= RM_NW && E <= 256 && (int64_t)T * d * 4 < ((int64_t)1 << 31) &&
+           (int64_t)E * d * 4 < ((int64_t)1 << 31);
+}
+
+void launch_router_mm(hipStream_t st, int T, int d, int E, const float* x, const float* xscale, const float* gis,
+                      const float* W, double* Lb, double* Bb, uint32_t* kb, int* cbad)
+{
+    const RmArgs a{T, d, E, x, xscale, gis, W, Lb, Bb, (uint4*)kb, cbad};
+    // 32 x 32 tiles where they still give a workgroup per compute unit, 16 x 16 below
+    if ((int64_t)((T + 31) / 32) * ((E + 31) / 32) >= 256) {
+        using RG = RmLds<2, 2>;
+        raise_lds(KRm<2, 2>::fn, RG::BYTES);
+        launch(KRm<2, 2>::fn, dim3((T + 31) / 32, (E + 31) / 32), dim3(RM_NW * 64), (uint32_t)RG::BYTES, st, a);
+    } else {
+        using RG = RmLds<1, 1>;
+        raise_lds(KRm<1, 1>::fn, RG::BYTES);
+        launch(KRm<1, 1>::fn, dim3((T + 15) / 16, (E + 15) / 16), dim3(RM_NW * 64), (uint32_t)RG::BYTES, st, a);
+    }
 }
 
 void launch_dec_route_fused(hipStream_t st, const DecLayerH& prev, const DecLayerH& h)

@@ -922,8 +922,6 @@ __device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t c)
     asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "s"(m), "v"(c));  // one SGPR operand (gfx9)
     return r;
 }
-// s_waitcnt vmcnt(n) alone (gfx9 encoding: vmcnt bits 3:0 and 15:14)
-constexpr int vm_wait(int n) { return (n & 15) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
 
 // FOLD (the tolerance mode, PHX_FLAG_FAST_MATH): the activations arrive folded (fp16(q * d) of their
 // Q8_K scale), each weight operand is folded per super-block, fp16(sc * q * d - dmin * m) for Q4_K (one

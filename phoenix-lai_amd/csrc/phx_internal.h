@@ -202,9 +202,11 @@ struct DecLayerH {
     int ncu;  // compute units: the gate|up launch has at most one unit workgroup per CU
     float eps;
     const float *x, *W, *gis, *ds, *pre2, *post1, *post2, *fnorm, *post_ffw, *shared_in;
+    const float* xscale = nullptr;  // [T] the prologue's rms scales, where it ran (the exact selection reuses them)
     const QMat *gu, *dn, *sgu, *sdn;  // sgu / sdn null: no shared FFN computed in the call
     double *Lb, *Bb;
     uint32_t* kb;  // [T][E][4] selection keys of the certified router (see k_dec_route)
+    int* bad = nullptr;  // [1 + T] the count and the tokens the certified selection leaves to the exact chains
     int *ids, *offsets, *perm, *flags;
     float *w, *logits, *g, *u, *yd, *shg, *shu, *shout, *out, *xres;
     const float* xin = nullptr;  // the residual's source rows when not xres itself
@@ -216,6 +218,11 @@ bool dec_supported(const DecLayerH& h);
 void launch_dec_route(hipStream_t st, const DecLayerH& h);
 // the general path's selection from k_dec_route's certified sums: ids, weights and logits per token
 void launch_cert_select(hipStream_t st, const DecLayerH& h);
+// the certified router for many tokens: matrix-core logits with bounds (Lb, Bb) and selection keys kb
+// [T][E][4] for launch_cert_select, from x, the prologue's rms scales and the router scale
+bool router_mm_supported(int T, int d, int E);
+void launch_router_mm(hipStream_t st, int T, int d, int E, const float* x, const float* xscale, const float* gis,
+                      const float* W, double* Lb, double* Bb, uint32_t* kb, int* cbad);
 // a stack layer's router with the previous layer's combine folded in (prev: that layer, its xin the
 // rows it reads, its xres where the new x goes; h.x must be prev.xres)
 void launch_dec_route_fused(hipStream_t st, const DecLayerH& prev, const DecLayerH& h);

@@ -508,7 +508,7 @@ enum WsId {
     W_OFF, W_PERM, W_TILES, W_NTILES, W_G, W_U, W_ADN_Q, W_ADN_D, W_ADN_S, W_YD, W_SHG, W_SHU, W_ASD_Q, W_ASD_D,
     W_ASD_S, W_SHOUT, W_ZERO, W_STILES, W_SNTILES, W_SOFF, W_SPERM, W_LB, W_BB, W_ADEC, W_SDEC, W_AGUP, W_ASHP, W_AGU_H, W_ADN_H, W_ASH_H, W_ASD_H, W_X2,
     W_MM_IDS, W_MM_OFF, W_MM_PERM, W_MM_TILES, W_MM_NT, W_MM_D, W_MM_S, W_MM_H, W_AGU_BH, W_ADN_BH, W_MK_Q, W_MK_BH, W_KB,
-    W_COUNT
+    W_CBAD, W_COUNT
 };
 
 int ensure(phx_moe_ctx* c, int id, size_t bytes)
@@ -618,6 +618,7 @@ int ensure_workspace(phx_moe_ctx* c, const Layer& L, int T)
     ENS(W_LB, (size_t)T * D.n_expert * 8);
     ENS(W_BB, (size_t)T * D.n_expert * 8);
     ENS(W_KB, (size_t)T * D.n_expert * 16);
+    ENS(W_CBAD, (size_t)(T + 1) * 4);
     ENS(W_U, n * D.n_ff * 4);
     ENS(W_YD, n * D.d * 4);
     if ((rc = ensure_act(c, act_fmt(D.gate_up_type), T, D.d, W_AGU_Q, W_AGU_D, W_AGU_S))) return rc;
@@ -762,6 +763,7 @@ DecLayerH dec_layer(phx_moe_ctx* c, const Layer& L, int T, const float* x, const
         h.Lb = wp<double>(c, W_LB);
         h.Bb = wp<double>(c, W_BB);
         h.kb = wp<uint32_t>(c, W_KB);
+        h.bad = wp<int>(c, W_CBAD);
         h.ids = wp<int>(c, W_IDS);
         h.offsets = wp<int>(c, W_OFF);
         h.perm = wp<int>(c, W_PERM);
@@ -882,7 +884,11 @@ int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, con
         ash.qhstride = d;
         ash.fold = fast;
     }
-    if (!exact && cert_route(L, T, shared_ffn)) {
+    // the certified routers (decode-style workgroups per pair up to CERT_MAX_TE pairs, the matrix-core
+    // one beyond), else the exact chains
+    const bool cert = !exact && cert_route(L, T, shared_ffn);
+    const bool mmr = !exact && !cert && (int64_t)T * E > CERT_MAX_TE && router_mm_supported(T, d, E);
+    if (cert) {
         // the router's certified sums with the expert (and shared) inputs quantized beside them, then
         // the selection
         DecLayerH h = dec_layer(c, L, T, x, shared, out, xres);
@@ -897,8 +903,8 @@ int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, con
             launch_cert_select(st, h);
         }
     } else {
-        // the many-token router forms its input m from x and the row scales itself (no m rows written)
-        const bool rx = router_reads_x(T, d, E);
+        // the many-token routers form their input m from x and the row scales themselves (no m rows written)
+        const bool rx = mmr || router_reads_x(T, d, E);
         // the matrix-core products read only the fp16 copies of their inputs: no int8 rows or sums
         Act pgu = agu, psh = ash;
         if (mma || kmma) pgu.q = nullptr, pgu.s = nullptr;
@@ -910,16 +916,30 @@ int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, con
         }
         // up to 64 experts the router's waves hold all of a token's logits and take its top-k themselves
         const bool fused_topk = E <= 64;
-        {
-            ProfScope p(c, PHX_K_ROUTER);
-            TopkOut to;
-            if (fused_topk) to = TopkOut{k, D.weight_rule, L.ds, wp<int>(c, W_IDS), wp<float>(c, W_W)};
-            launch_router_exact(st, T, d, E, L.wt4, rx ? x : wp<float>(c, W_RIN), wp<float>(c, W_LOGITS), to,
-                                rx ? RouterX{wp<float>(c, W_XSCALE), L.gis} : RouterX{});
-        }
-        if (!fused_topk) {
+        if (mmr) {
+            // matrix-core sums with bounds, then the certified selection (exact chains for the tokens
+            // whose order the bounds leave open)
+            DecLayerH h = dec_layer(c, L, T, x, shared, out, xres);
+            h.xscale = wp<float>(c, W_XSCALE);
+            {
+                ProfScope p(c, PHX_K_ROUTER);
+                launch_router_mm(st, T, d, E, x, wp<float>(c, W_XSCALE), L.gis, L.wrow, h.Lb, h.Bb, h.kb, h.bad);
+            }
             ProfScope p(c, PHX_K_TOPK);
-            launch_topk(st, T, E, k, D.weight_rule, wp<float>(c, W_LOGITS), L.ds, wp<int>(c, W_IDS), wp<float>(c, W_W));
+            launch_cert_select(st, h);
+        } else {
+            {
+                ProfScope p(c, PHX_K_ROUTER);
+                TopkOut to;
+                if (fused_topk) to = TopkOut{k, D.weight_rule, L.ds, wp<int>(c, W_IDS), wp<float>(c, W_W)};
+                launch_router_exact(st, T, d, E, L.wt4, rx ? x : wp<float>(c, W_RIN), wp<float>(c, W_LOGITS), to,
+                                    rx ? RouterX{wp<float>(c, W_XSCALE), L.gis} : RouterX{});
+            }
+            if (!fused_topk) {
+                ProfScope p(c, PHX_K_TOPK);
+                launch_topk(st, T, E, k, D.weight_rule, wp<float>(c, W_LOGITS), L.ds, wp<int>(c, W_IDS),
+                            wp<float>(c, W_W));
+            }
         }
     }
     // tile sizes: the MFMA kernels' 128 (Q4_0 / Q8_0) and 32 (K-quants), the VALU kernels' 4 (their row
@@ -1746,7 +1766,7 @@ int phx_moe_profile_read(phx_moe_ctx* c, double* total_ms, int64_t* launches)
 
 int phx_moe_selftest(phx_moe_ctx* c, int op, int n, const float* a, const float* b, float* out)
 {
-    if (!c || n <= 0 || !a || !b || !out || op < 0 || op > 7) return PHX_ERR_ARG;
+    if (!c || n <= 0 || !a || !b || !out || op < 0 || op > 9 || (op >= 8 && n % 64)) return PHX_ERR_ARG;
     ENTER(c);
     float *da = nullptr, *db = nullptr, *dout = nullptr;
     size_t bytes = (size_t)n * 4;
