@@ -387,11 +387,13 @@ def run_prefill(args, pkg, cfg_name="c3_prefill", steps=None):
     for s in range(3):
         ctx.ffn_device(0, T, xbuf.ptr + (s % NX) * xstride, None, obuf.ptr, pkg.PHX.FLAG_ASYNC)
     ctx.sync()
+    fb0 = ctx.fallback_counts()[1]
     t0 = time.perf_counter()
     for s in range(steps):
         ctx.ffn_device(0, T, xbuf.ptr + (s % NX) * xstride, None, obuf.ptr, pkg.PHX.FLAG_ASYNC)
     ctx.sync()
     dt = time.perf_counter() - t0
+    fb_tokens = ctx.fallback_counts()[1] - fb0
 
     def calls():
         for s in range(steps):
@@ -423,7 +425,10 @@ def run_prefill(args, pkg, cfg_name="c3_prefill", steps=None):
                    "floor_us": round(touched * (gu_b + dn_b) / (HBM_PEAK_GBS * 1e9) * 1e6, 1),
                    "note": "unpadded GGUF bytes of the experts with at least one assignment"},
            "kernels": {k_: {"avg_us": round(v[0] * 1e3, 2), "launches": v[1]} for k_, v in prof.items()},
-           "kernel_timing": f"{steps} eager layer calls, each kernel's execution interval",
+           "kernel_timing": f"{steps} eager layer calls, each kernel's execution interval; 'router' is the "
+                            f"certified router's matrix-core sums, 'topk' its selection (exact chains for the "
+                            f"tokens the bounds leave open)",
+           "router_fallback_token_frac": round(fb_tokens / (T * steps), 4),
            "assignments_per_expert": {"max": int(cnt.max()), "empty_experts": int((cnt == 0).sum())}}
     if fast:
         out["fast_math"] = fast

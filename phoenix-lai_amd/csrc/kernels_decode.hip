@@ -1465,7 +1465,7 @@ __global__ __launch_bounds__(CF_NT) void k_cert_select_one(DecArgs a)
 // last terms cover L's double rounding and products or sums the matrix cores flush below 2^-126.  A
 // bound of 2^100 or more (or a non-finite one) is made infinite: the token then takes the exact
 // chains for every expert, as for a non-finite logit.
-constexpr int RM_NW = 8, RM_RING = 3;
+constexpr int RM_NW = 8, RM_RING = 4;
 template <int TM16, int TN16>
 struct RmLds {
     static constexpr int TM = 16 * TM16, TN = 16 * TN16;
@@ -1542,7 +1542,7 @@ __device__ __forceinline__ void router_mm_tile(const RmArgs& a, unsigned char* r
 
     auto step = [&](auto SC, int j) {
         constexpr int S = decltype(SC)::value;
-        __builtin_amdgcn_s_waitcnt(vm_wait(RG::DMA * (RM_RING - 1)));  // chunk j landed (j + 1, j + 2 may not)
+        __builtin_amdgcn_s_waitcnt(vm_wait(RG::DMA * (RM_RING - 1)));  // chunk j landed (the later ones may not)
         u32x4 X[TM16], Wv[TN16], G;
         static_for<TM16>([&](auto I) { X[I] = ds_r128<S * RG::SLOT + 1024 * decltype(I)::value>(a_x); });
         static_for<TN16>([&](auto J) { Wv[J] = ds_r128<S * RG::SLOT + 1024 * decltype(J)::value>(a_w); });
@@ -1582,22 +1582,18 @@ __device__ __forceinline__ void router_mm_tile(const RmArgs& a, unsigned char* r
 #pragma unroll
                 for (int v = 0; v < 4; v++) sab[i][jj][v] += fabsf(acc[i][jj][v]);
     };
-    // chunk j + 2 goes into the slot chunk j - 1 left (its reads ended in step j - 1) before step j
-    issue(ic<0>{}, 0);
-    issue(ic<1>{}, 1);
+    // chunk j + RM_RING - 1 goes into the slot chunk j - 1 left (its reads ended in step j - 1) before
+    // step j
+    static_for<RM_RING - 1>([&](auto S) { issue(S, decltype(S)::value); });
     for (int j = 0; j < cnt; j += RM_RING) {
-        issue(ic<2>{}, j + 2);
-        step(ic<0>{}, j);
-        if (j + 1 < cnt) {
-            issue(ic<0>{}, j + 3);
-            step(ic<1>{}, j + 1);
-        }
-        if (j + 2 < cnt) {
-            issue(ic<1>{}, j + 4);
-            step(ic<2>{}, j + 2);
-        }
+        static_for<RM_RING>([&](auto S) {
+            constexpr int sl = decltype(S)::value;
+            if (j + sl < cnt) {
+                issue(ic<(sl + RM_RING - 1) % RM_RING>{}, j + sl + RM_RING - 1);
+                step(S, j + sl);
+            }
+        });
     }
-    static_assert(RM_RING == 3, "the loop above steps through three slots");
     __builtin_amdgcn_s_waitcnt(vm_wait(0));  // the clamped reloads past the end (into this wave's ring)
 
     // the squares' sums over the four lane groups (each lane: its group's elements of row r)
@@ -1643,7 +1639,7 @@ __device__ __forceinline__ void router_mm_tile(const RmArgs& a, unsigned char* r
             mainb += nw * fabs(O) + 36.0 * Sj;
             O += C;
             absC += fabs(C);
-            cs += sqrt((double)fM[w * TM + tl] * (double)fW[w * TN + el]);
+            cs += (double)sqrtf(fM[w * TM + tl] * fW[w * TN + el]);  // (its float roundings: inside the 1.03)
         }
         double B = 0x1.08p-24 * (mainb + 37.0 * cs) + 0x1p-50 * absC + 0x1p-90 * a.d;
         if (!(B < 0x1p100)) B = INFINITY;  // also NaN
