@@ -735,17 +735,24 @@ __global__ __launch_bounds__(DSP_NT) void k_dispatch(int n, int E, int A, const 
     const int seg = (c1 - c0 + DSP_SEG - 1) / DSP_SEG, s0 = min(c1, c0 + wave * seg), s1 = min(c1, s0 + seg);
     const uint64_t lower = (1ull << lane) - 1ull;
     __syncthreads();
-    // counts over the list, 64 assignments per batch (the lowest lane of each expert adds its count; one
-    // workgroup: its segments cover the list), and per segment of the chunk
-    for (int a0 = 64 * wave; gridDim.x > 1 && a0 < n; a0 += 64 * DSP_SEG) {
-        const int a = a0 + lane;
-        const bool valid = a < n;
-        const int e = valid ? sid[a] : 0;
-        const uint64_t m = same_expert_mask(e, valid, nbits);
-        if (valid && (m & lower) == 0) {
-            atomicAdd(&tot[e], __popcll(m));
-            if (a0 < c0) atomicAdd(&pre[e], __popcll(m));  // whole batches lie before the chunk or not
+    // counts over the list: every lane adds its assignment into its wave's own row by an LDS atomic (the
+    // list total in the low 16 bits, the count before the chunk in the high 16, n <= 65535), summed per
+    // expert (one workgroup: its segments cover the list); then per segment of the chunk.  (A rank-free
+    // count needs no same-expert mask: its eight ballots per batch made this pass VALU-bound, 256
+    // batches of ~100 instructions in every workgroup.)
+    if (gridDim.x > 1) {  // uniform
+        for (int a = tid; a < n; a += DSP_NT) atomicAdd(&cnt[wave][sid[a]], a < c0 ? 0x10001 : 1);
+        __syncthreads();
+        if (tid < E) {
+            unsigned sum = 0;
+            for (int w = 0; w < DSP_SEG; w++) {
+                sum += (unsigned)cnt[w][tid];
+                cnt[w][tid] = 0;
+            }
+            tot[tid] = (int)(sum & 0xFFFFu);
+            pre[tid] = (int)(sum >> 16);
         }
+        __syncthreads();
     }
     for (int a0 = s0; a0 < s1; a0 += 64) {
         const int a = a0 + lane;
