@@ -210,6 +210,19 @@ __device__ __forceinline__ float half_max_f(float v)
     return (threadIdx.x & 32) ? b : a;
 }
 
+// Q8_0 of 32 values held one per lane of a 32-lane half (CpuRef.QuantizeQ8_0, src/CpuRef.cs:49-62):
+// returns q; *dval the block scale as its fp16 value, *sum the block's integer sum.
+__device__ __forceinline__ int q8_0_half(float x, float* dval, int* sum)
+{
+    const float amax = half_max_f(fabsf(x));
+    const float dd = amax / 127.0f;
+    const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
+    const int q = (int)roundf(x * id);
+    *dval = h2f(f2h_bits(dd));
+    *sum = half_sum_i(q);
+    return q;
+}
+
 typedef _Float16 mh2 __attribute__((ext_vector_type(2)));
 
 // Bytes to exact fp16 pairs by the 1024-bias: the half with bits 0x64XX is 1024 + XX.  Returns the

@@ -876,6 +876,8 @@ struct GroupArgs {
     int split, out_stride;
     bool paired;
     const void* grid;  // IQ types: the expanded codebook (64-bit words for IQ2_XXS / IQ2_S, 32-bit for IQ3_S)
+    Act req;                       // req.q set: the paired gate|up kernel also writes gelu(g) * u as Q8_0 rows
+    const float* gelu_tab = nullptr;
 };
 
 // Output of lane `lane` of row group rgi for assignment row a: natural row order, or for a paired
@@ -890,6 +892,26 @@ __device__ __forceinline__ void store_row(const GroupArgs& g, int rgi, int lane,
         if (row < g.rows) {
             if (row < g.split) g.out0[a * g.out_stride + row] = v;
             else g.out1[a * g.out_stride + row - g.split] = v;
+        }
+    }
+}
+
+// The down input block rgi of assignment a from a paired row group's results (lanes 0-31 gate rows
+// 32 rgi + l, lanes 32-63 the matching up rows): e = gelu(g) * u (src/GemmaCpu.cs:415) as a Q8_0 block
+// (src/CpuRef.cs:49-62), what k_requant writes for it.  Wave-level.
+__device__ __forceinline__ void requant_block(const GroupArgs& g, int rgi, int64_t a, float S)
+{
+    const int lane = threadIdx.x & 63, jj = rgi * 32 + (lane & 31);
+    const float uv = __shfl_down(S, 32, 64);
+    const float ev = lane < 32 ? gelu_ref(S, g.gelu_tab) * uv : 0.0f;
+    float dval;
+    int sum;
+    const int q = q8_0_half(ev, &dval, &sum);
+    if (lane < 32) {
+        g.req.q[a * g.req.qstride + jj] = (int8_t)q;
+        if (lane == 0) {
+            g.req.d[a * g.req.dstride + rgi] = dval;
+            g.req.s[a * g.req.sstride + rgi] = sum;
         }
     }
 }
@@ -1081,10 +1103,14 @@ __global__ __launch_bounds__(256) void k_grouped_q_ring(GroupArgs g)
         }
     }
     __builtin_amdgcn_s_waitcnt(0);  // the trailing ring loads land in this workgroup's LDS before it ends
-    if (!live) return;
+    if (!live) return;  // wave-uniform
 #pragma unroll
     for (int i = 0; i < A; i++)
-        if (i < cnt) store_row(g, rgi, lane, g.perm[tl.start + i], acc[i]);
+        if (i < cnt) {  // uniform
+            const int64_t a = g.perm[tl.start + i];
+            store_row(g, rgi, lane, a, acc[i]);
+            if (g.req.q) requant_block(g, rgi, a, acc[i]);
+        }
 }
 
 // K-quant rows: DotK (src/CpuRefKQuants.cs:177-212) per (row, assignment): per super-block the eight
@@ -1341,7 +1367,8 @@ static uint32_t grouped_q_lds(int type, int nb)
 }
 
 void launch_grouped(hipStream_t st, const QMat& w, Act act, const Tile* tiles, const int* ntiles, int max_tiles, int A,
-                    const int* perm, int act_div, float* out0, float* out1, int split, int out_stride)
+                    const int* perm, int act_div, float* out0, float* out1, int split, int out_stride,
+                    const Act* req, const float* gelu_tab, int req_rows)
 {
     GroupArgs g;
     g.payload = w.payload;
@@ -1363,6 +1390,14 @@ void launch_grouped(hipStream_t st, const QMat& w, Act act, const Tile* tiles, c
     g.out_stride = out_stride;
     g.paired = w.paired;
     g.grid = w.grid;
+    // the down input in the ring kernel's epilogue where it covers every block of the row (paired Q4_0 /
+    // Q8_0 rows past QG_SHORT blocks into Q8_0 rows with no padding blocks); else k_requant after it
+    const bool fuse = req && w.paired && w.nb > QG_SHORT && (w.type == PHX_Q4_0_DEV || w.type == PHX_Q8_0_DEV) &&
+                      req->fmt == ACT_Q8_0 && req->cols == 32 * w.rg && split == 32 * w.rg && !req->qh;
+    if (fuse) {
+        g.req = *req;
+        g.gelu_tab = gelu_tab;
+    }
     dim3 grid(max_tiles, (w.rg + 3) / 4);
     (void)A;  // the tile size the dispatch used: 4, the one instantiation
     switch (w.type) {
@@ -1381,6 +1416,7 @@ void launch_grouped(hipStream_t st, const QMat& w, Act act, const Tile* tiles, c
     case PHX_IQ2_S_DEV: launch((k_grouped_iq<PHX_IQ2_S_DEV, 4>), grid, dim3(256), 0, st, g); break;
     case PHX_IQ3_S_DEV: launch((k_grouped_iq<PHX_IQ3_S_DEV, 4>), grid, dim3(256), 0, st, g); break;
     }
+    if (req && !fuse) launch_requant(st, req_rows, split, out0, out1, gelu_tab, *req);
 }
 
 // ------------------------------------------------------------------------------ GELU-gated requant

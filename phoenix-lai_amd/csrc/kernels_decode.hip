@@ -103,17 +103,6 @@ struct DecArgs {
 
 // ------------------------------------------------------------------------------ helpers
 
-// The same for 32 values held one per lane of a 32-lane half; returns q.
-__device__ __forceinline__ int q8_0_half(float x, float* dval, int* sum)
-{
-    const float amax = half_max_f(fabsf(x));
-    const float dd = amax / 127.0f;
-    const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
-    const int q = (int)roundf(x * id);
-    *dval = h2f(f2h_bits(dd));
-    *sum = half_sum_i(q);
-    return q;
-}
 
 // Mean of squares of a row (RmsNorm's (float)(sum / n), sum the sequential double sum of x_i^2,
 // src/CpuRef.cs:186-188) from per-thread partial double sums `s` over disjoint elements.  Any order of

@@ -159,8 +159,11 @@ void launch_topk(hipStream_t st, int T, int E, int k, int rule, const float* log
                  int* ids, float* w);
 void launch_dispatch(hipStream_t st, int n_assign, int E, int A, const int* ids, int* offsets, int* perm,
                      Tile* tiles, int* ntiles);
+// req: the paired gate|up product's down input (gelu(g) * u as Q8_0 rows, req_rows of them), formed in
+// the product's epilogue where it can be, else by k_requant after it
 void launch_grouped(hipStream_t st, const QMat& w, Act act, const Tile* tiles, const int* ntiles, int max_tiles,
-                    int A, const int* perm, int act_div, float* out0, float* out1, int split, int out_stride);
+                    int A, const int* perm, int act_div, float* out0, float* out1, int split, int out_stride,
+                    const Act* req = nullptr, const float* gelu_tab = nullptr, int req_rows = 0);
 void launch_requant(hipStream_t st, int rows, int nf, const float* g, const float* u, const float* gelu_tab, Act act);
 // standalone Q8_0 (fmt_k 0) / Q8_K (fmt_k 1) quantizer of rows x n inputs; mode as PHX_QUANT_*; -1 on a bad mode
 int launch_quant(hipStream_t st, int fmt_k, int mode, int rows, int n, float eps, const float* x, const float* aux,

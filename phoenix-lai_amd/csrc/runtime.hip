@@ -970,11 +970,11 @@ int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, con
         else if (kmma)
             launch_grouped_kmma(st, L.gu, agu, wp<Tile>(c, W_TILES), wp<int>(c, W_NTILES), max_tiles, wp<int>(c, W_PERM), k,
                                 wp<float>(c, W_G), wp<float>(c, W_U), nf, nf);
-        else
+        else  // the down input from the product's epilogue (or k_requant right after it)
             launch_grouped(st, L.gu, agu, wp<Tile>(c, W_TILES), wp<int>(c, W_NTILES), max_tiles, tileA, wp<int>(c, W_PERM),
-                           k, wp<float>(c, W_G), wp<float>(c, W_U), nf, nf);
+                           k, wp<float>(c, W_G), wp<float>(c, W_U), nf, nf, &adn, c->gelu_tab, n);
     }
-    if (!mma) {
+    if (kmma) {
         ProfScope p(c, PHX_K_REQUANT);
         launch_requant(st, n, nf, wp<float>(c, W_G), wp<float>(c, W_U), c->gelu_tab, adn);
     }
@@ -1010,8 +1010,7 @@ int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, con
                                 nullptr, nullptr, nff, nff, 0, &asd, T, c->gelu_tab);  // (no reader of g, u)
         else
             launch_grouped(st, L.sgu, ash, wp<Tile>(c, W_STILES), wp<int>(c, W_SNTILES), smax, kTileA, wp<int>(c, W_SPERM),
-                           1, wp<float>(c, W_SHG), wp<float>(c, W_SHU), nff, nff);
-        if (!smma) launch_requant(st, T, nff, wp<float>(c, W_SHG), wp<float>(c, W_SHU), c->gelu_tab, asd);
+                           1, wp<float>(c, W_SHG), wp<float>(c, W_SHU), nff, nff, &asd, c->gelu_tab, T);
         if (smma)
             launch_grouped_mfma(st, L.sdn, asd, wp<Tile>(c, W_STILES), wp<int>(c, W_SNTILES), smax, wp<int>(c, W_SPERM), 1,
                                 wp<float>(c, W_SHOUT), wp<float>(c, W_SHOUT), d, d, T);
