@@ -64,15 +64,19 @@ extern "C" {
 #define PHX_FLAG_ASYNC 2u       /* return after enqueueing; phx_moe_sync waits */
 #define PHX_FLAG_RESIDUAL 4u    /* also x += rmsnorm(out) * post_ffw_norm (src/GemmaCpu.cs:355-356); x is updated in place
                                    and out must not be x */
-#define PHX_FLAG_EXACT_ROUTER 8u /* replay the reference's float router sums for every token (outputs bit-exact
-                                    to the CPU reference) instead of the certified decode router */
-#define PHX_FLAG_FAST_MATH 16u /* tolerance mode of the prefill-sized Q4_0 / Q8_0 expert products (the role of
-                                  the reference's f16 cooperative-matrix path, src/KernelsCoop.cs:1-10,
-                                  src/GemmaGpu.cs:893): block scales folded into fp16 operands and whole rows
-                                  accumulated on the matrix cores.  Routing, ids and lists are unchanged (bit-
-                                  exact); the products differ from the CPU reference's chains by the operands'
-                                  fp16 rounding, and the GELU-gated requant amplifies that where a value sits
-                                  near a rounding boundary.  Decode-sized calls ignore it. */
+#define PHX_FLAG_EXACT_ROUTER 8u /* replay the reference's float router sums for every token (logits, weights and
+                                    outputs bit-exact to the CPU reference) instead of the certified routers
+                                    (the default: sums with error bounds, the reference's float chains only for
+                                    the tokens whose top-k order the bounds leave open; ids and lists are the
+                                    reference's either way, logits and weights then within ~1e-6 of them) */
+#define PHX_FLAG_FAST_MATH 16u /* tolerance mode of the prefill-sized expert products on the matrix cores
+                                  (Q4_0 / Q8_0 and Q4_K / Q6_K; the role of the reference's f16 cooperative-
+                                  matrix path, src/KernelsCoop.cs:1-10, src/GemmaGpu.cs:893): block scales folded
+                                  into fp16 operands and whole rows accumulated on the matrix cores.  Routing,
+                                  ids and lists are unchanged (bit-exact); the products differ from the CPU
+                                  reference's chains by the operands' fp16 rounding, and the GELU-gated requant
+                                  amplifies that where a value sits near a rounding boundary.  Decode-sized
+                                  calls ignore it. */
 #define PHX_FLAG_KEEP_INTERMEDIATES 32u /* also store the gate and up products for phx_moe_get_intermediates
                                            (debug; no counterpart in the reference).  The prefill-sized Q4_0 /
                                            Q8_0 expert products feed their GELU-gated requant straight into the
