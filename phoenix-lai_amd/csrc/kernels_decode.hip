@@ -1429,7 +1429,8 @@ __global__ __launch_bounds__(CF_NT) void k_cert_select_one(DecArgs a)
 // The certified router for many tokens, where a workgroup per (token, expert) no longer pays: the
 // logits of a tile of TM tokens x TN experts as fp32 matrix-core sums, with the bound k_cert_select
 // certifies the top-k order from (the decode router's L, B, keys; the reference chain is
-// src/GemmaCpu.cs:389-395, its input m_i = ((x_i * rinv) * sc) * s_i, :388-389).
+// src/GemmaCpu.cs:389-395, its input m_i = ((x_i * rinv) * sc) * s_i, :388-389, rinv the row's rms scale,
+// CpuRef.cs:183-191).
 //
 // Split over the reduction: wave w of the RM_NW waves sums the chunks [c0, c0 + cnt) of 16 elements
 // of every logit of the tile (v_mfma_f32_16x16x4_f32; lane group g of a 16 x 16 product holds the
@@ -1439,21 +1440,25 @@ __global__ __launch_bounds__(CF_NT) void k_cert_select_one(DecArgs a)
 // no barrier is needed inside the loop.
 //
 // The bound.  With p_i = fl(m_i w_i), S_k = sum_{i <= k} p_i and u = 2^-24, the reference's chain
-// ends within 1.004 u sum_k |S_k| of S_n (n <= 65536).  Range r (n_r elements, exact prefix O_r at its
-// start) gives sum_{k in r} |S_k| <= n_r |O_r| + 16 sum_j |Q_rj| + 15 sum_r |p| (Q_rj the range's own
-// prefix at the end of chunk j: within a chunk each prefix differs from the chunk end's by at most
-// the chunk's |p|).  A 4-deep fp32 product rounds at most five times, each to nearest, so the matrix
-// cores' sum differs from the exact one of the exact products by at most 5 u (|C_in| + sum |a b|) per
-// instruction, summed: 20 u (sum_j |C_j| + sum |m w|) over a range (every instruction's C_in lies
-// within the chunk's |m w| of the chunk's start).  Products rounded: u sum |m w|.  Together, with the
+// ends within 1.004 u sum_k |S_k| of S_n (n <= 65536).  The matrix cores sum a_i w_i with a_i = fl(x_i s_i)
+// and the row's factor f = rinv / sqrt(d) (exact in double) scales the sums: m_i lies within 4u of
+// f a_i (three roundings against one), so f a_i w_i stands in for p_i within 5u |f a_i w_i|.  Range r
+// (n_r elements, exact prefix O_r at its start) gives sum_{k in r} |S_k| <= n_r |O_r| + 16 sum_j |Q_rj|
+// + 15 sum_r |p| (Q_rj the range's own prefix at the end of chunk j: within a chunk each prefix differs
+// from the chunk end's by at most the chunk's |p|).  A 4-deep fp32 product rounds at most five times,
+// each to nearest, so the matrix cores' sum differs from the exact one of the exact products by at
+// most 5 u (|C_in| + sum |a b|) per instruction, summed: 20 u (sum_j |C_j| + sum |a w|) over a range
+// (every instruction's C_in lies within the chunk's |a w| of the chunk's start).  Together, with the
 // second-order terms (the n_r-fold ranges' errors, the float sums of |C_j| and of the squares) inside
-// the 1.03 factor:
-//   |S_ref - L| <= 1.03 u (sum_r n_r |O_r| + 36 sum_rj |C_rj| + 37 sum_r |m_r| |w_r|) + 2^-50 sum_r |C_r|
-//                  + 2^-90 n,
-// sum |m w| bounded per range by Cauchy-Schwarz, O_r from the waves' totals, L their double sum; the
-// last terms cover L's double rounding and products or sums the matrix cores flush below 2^-126.  A
-// bound of 2^100 or more (or a non-finite one) is made infinite: the token then takes the exact
-// chains for every expert, as for a non-finite logit.
+// the 1.03 factor and the coefficient of the last sum:
+//   |S_ref - L| <= 1.03 u f (sum_r n_r |O_r| + 36 sum_rj |C_rj| + 44 sum_r |a_r| |w_r|)
+//                  + 2^-50 f sum_r |C_r| + 2^-90 n (1 + f),
+// sum |a w| bounded per range by Cauchy-Schwarz, O_r from the waves' unscaled totals, L = f times their
+// double sum; the last terms cover L's double roundings and products or sums the matrix cores flush
+// below 2^-126.  A bound of 2^100 or more (or a non-finite one) is made infinite: the token then takes
+// the exact chains for every expert, as for a non-finite logit.  The rows' rms scales come from the
+// waves' double sums of squares, certified as the prologue certifies them, so this kernel needs no
+// input from the prologue.
 constexpr int RM_NW = 8, RM_RING = 4;
 template <int TM16, int TN16>
 struct RmLds {
@@ -1461,17 +1466,21 @@ struct RmLds {
     static constexpr int SLOT = (TM + TN) * 64 + 64;  // [TM x rows][TN W rows] of 16 floats, the scales' 16
     static constexpr int DMA = TM16 + TN16 + 1;       // direct loads per chunk and wave
     static constexpr int RINGS = RM_NW * RM_RING * SLOT;
-    static constexpr int FIN = RM_NW * (2 * TM * TN + TM + TN) * 4;  // per wave: C, sum |C_j|, |m|^2, |w|^2
+    // per wave: C, sum |C_j|, |m|^2, |w|^2 (floats), the tokens' sums of squares (doubles); the tokens' scales
+    static constexpr int FIN = RM_NW * (2 * TM * TN + TM + TN) * 4 + RM_NW * TM * 8 + TM * 4;
     static constexpr int BYTES = RINGS > FIN ? RINGS : FIN;
 };
 typedef float mf4v __attribute__((ext_vector_type(4)));
 
 struct RmArgs {
     int T, d, E;
-    const float *x, *xscale, *gis, *W;  // x [T][d], rinv [T], router scale [d], W [E][d]
+    float eps;
+    const float *x, *gis, *W;  // x [T][d], router scale [d], W [E][d]
+    float* xscale;             // [T] out: the rows' rms scales (the exact selection's)
     double *Lb, *Bb;
     uint4* kb;
-    int* cbad;  // the selection's list of uncertified tokens: its count is cleared here
+    int* cbad;   // the selection's list of uncertified tokens: its count is cleared here
+    int* flags;  // [0] the rows whose certified mean fell back to the sequential sum
 };
 
 // (a device function: the direct loads' builtin inside a kernel's own lambdas leaves the host side
@@ -1512,15 +1521,13 @@ __device__ __forceinline__ void router_mm_tile(const RmArgs& a, unsigned char* r
     };
 #undef RM_LOAD
 
-    float rinv[TM16];
-#pragma unroll
-    for (int i = 0; i < TM16; i++) rinv[i] = a.xscale[min(t0 + 16 * i + r, a.T - 1)];
-    const float sc = 1.0f / (float)__dsqrt_rn((double)a.d);
     mf4v acc[TM16][TN16], sab[TM16][TN16];
     float mm[TM16], ww[TN16];
+    double s2[TM16];  // the rows' sums of squares (this lane's elements)
 #pragma unroll
     for (int i = 0; i < TM16; i++) {
         mm[i] = 0.0f;
+        s2[i] = 0.0;
 #pragma unroll
         for (int j = 0; j < TN16; j++) acc[i][j] = sab[i][j] = mf4v{0.0f, 0.0f, 0.0f, 0.0f};
     }
@@ -1547,8 +1554,10 @@ __device__ __forceinline__ void router_mm_tile(const RmArgs& a, unsigned char* r
         for (int i = 0; i < TM16; i++)
 #pragma unroll
             for (int q = 0; q < 4; q++) {
-                m[i][q] = ((__uint_as_float(X[i][q]) * rinv[i]) * sc) * __uint_as_float(G[q]);
+                const float xv = __uint_as_float(X[i][q]);
+                m[i][q] = xv * __uint_as_float(G[q]);  // x s: the row's scale rinv / sqrt(d) is applied to the sums
                 mm[i] = fmaf(m[i][q], m[i][q], mm[i]);
+                s2[i] += (double)xv * (double)xv;
             }
 #pragma unroll
         for (int jj = 0; jj < TN16; jj++)
@@ -1590,6 +1599,8 @@ __device__ __forceinline__ void router_mm_tile(const RmArgs& a, unsigned char* r
     for (int i = 0; i < TM16; i++) {
         mm[i] += __shfl_xor(mm[i], 16);
         mm[i] += __shfl_xor(mm[i], 32);
+        s2[i] += __shfl_xor(s2[i], 16);
+        s2[i] += __shfl_xor(s2[i], 32);
     }
 #pragma unroll
     for (int jj = 0; jj < TN16; jj++) {
@@ -1601,6 +1612,8 @@ __device__ __forceinline__ void router_mm_tile(const RmArgs& a, unsigned char* r
     float* fS = fC + RM_NW * TM * TN;  // [wave][TM][TN] its sum of |C_j|
     float* fM = fS + RM_NW * TM * TN;  // [wave][TM] |m|^2 over the range
     float* fW = fM + RM_NW * TM;       // [wave][TN] |w|^2
+    double* fQ = (double*)(fW + RM_NW * TN);  // [wave][TM] the rows' sums of squares
+    float* fR = (float*)(fQ + RM_NW * TM);    // [TM] the rows' rms scales
 #pragma unroll
     for (int i = 0; i < TM16; i++)
 #pragma unroll
@@ -1613,14 +1626,40 @@ __device__ __forceinline__ void router_mm_tile(const RmArgs& a, unsigned char* r
             }
     if (g == 0) {
 #pragma unroll
-        for (int i = 0; i < TM16; i++) fM[wave * TM + 16 * i + r] = mm[i];
+        for (int i = 0; i < TM16; i++) {
+            fM[wave * TM + 16 * i + r] = mm[i];
+            fQ[wave * TM + 16 * i + r] = s2[i];
+        }
 #pragma unroll
         for (int jj = 0; jj < TN16; jj++) fW[wave * TN + 16 * jj + r] = ww[jj];
     }
     __syncthreads();
+    // each row's scale as CpuRef.RmsNorm forms it (src/CpuRef.cs:183-191): the waves' double sums in a
+    // fixed order, certified against the sequential sum (any order of the d non-negative terms lies within
+    // (d + 64) 2^-52 of it), else re-summed in index order by this thread (rare; counted)
+    if (tid < TM) {
+        const int t = min(t0 + tid, a.T - 1);
+        double S = 0.0;
+        for (int w = 0; w < RM_NW; w++) S += fQ[w * TM + tid];
+        float mean, mhi;
+        mean_ends(S, ((double)a.d + 64.0) * 0x1p-52 * S, 1.0 / (double)a.d, &mean, &mhi);
+        if (mean != mhi) {
+            const float* xr = a.x + (int64_t)t * a.d;
+            double q = 0.0;
+            for (int i = 0; i < a.d; i++) q += (double)xr[i] * (double)xr[i];
+            mean = (float)(q / (double)a.d);
+            if (blockIdx.y == 0 && t0 + tid < a.T && a.flags) atomicAdd(&a.flags[0], 1);
+        }
+        const float rinv = rms_scale_from_mean(mean, a.eps);
+        fR[tid] = rinv;
+        if (blockIdx.y == 0 && t0 + tid < a.T) a.xscale[t] = rinv;
+    }
+    __syncthreads();
+    const double sc = (double)(1.0f / (float)__dsqrt_rn((double)a.d));
     for (int o = tid; o < TM * TN; o += RM_NW * 64) {
         const int tl = o / TN, el = o % TN, t = t0 + tl, e = e0 + el;
         if (t >= a.T || e >= a.E) continue;
+        const double f = (double)fR[tl] * sc;  // rinv / sqrt(d): exact in double
         double O = 0.0, mainb = 0.0, cs = 0.0, absC = 0.0;
         for (int w = 0; w < RM_NW; w++) {
             const double nw = 16.0 * (base + (w < extra));
@@ -1630,12 +1669,13 @@ __device__ __forceinline__ void router_mm_tile(const RmArgs& a, unsigned char* r
             absC += fabs(C);
             cs += (double)sqrtf(fM[w * TM + tl] * fW[w * TN + el]);  // (its float roundings: inside the 1.03)
         }
-        double B = 0x1.08p-24 * (mainb + 37.0 * cs) + 0x1p-50 * absC + 0x1p-90 * a.d;
+        double B = 0x1.08p-24 * f * (mainb + 44.0 * cs) + 0x1p-50 * f * absC + 0x1p-90 * a.d * (1.0 + f);
         if (!(B < 0x1p100)) B = INFINITY;  // also NaN
+        const double L = f * O;
         const int64_t te = (int64_t)t * a.E + e;
-        a.Lb[te] = O;
+        a.Lb[te] = L;
         a.Bb[te] = B;
-        a.kb[te] = sel_key(O, B, e);
+        a.kb[te] = sel_key(L, B, e);
     }
 }
 
@@ -2066,10 +2106,10 @@ bool router_mm_supported(int T, int d, int E)
            (int64_t)E * d * 4 < ((int64_t)1 << 31);
 }
 
-void launch_router_mm(hipStream_t st, int T, int d, int E, const float* x, const float* xscale, const float* gis,
-                      const float* W, double* Lb, double* Bb, uint32_t* kb, int* cbad)
+void launch_router_mm(hipStream_t st, int T, int d, int E, float eps, const float* x, const float* gis, const float* W,
+                      float* xscale, double* Lb, double* Bb, uint32_t* kb, int* cbad, int* flags)
 {
-    const RmArgs a{T, d, E, x, xscale, gis, W, Lb, Bb, (uint4*)kb, cbad};
+    const RmArgs a{T, d, E, eps, x, gis, W, xscale, Lb, Bb, (uint4*)kb, cbad, flags};
     // 32 x 32 tiles where they still give a workgroup per compute unit, 16 x 16 below
     if ((int64_t)((T + 31) / 32) * ((E + 31) / 32) >= 256) {
         using RG = RmLds<2, 2>;

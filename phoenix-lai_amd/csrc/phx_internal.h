@@ -222,10 +222,11 @@ void launch_dec_route(hipStream_t st, const DecLayerH& h);
 // the general path's selection from k_dec_route's certified sums: ids, weights and logits per token
 void launch_cert_select(hipStream_t st, const DecLayerH& h);
 // the certified router for many tokens: matrix-core logits with bounds (Lb, Bb) and selection keys kb
-// [T][E][4] for launch_cert_select, from x, the prologue's rms scales and the router scale
+// [T][E][4] for launch_cert_select, from x and the router scale; it forms the rows' rms scales itself
+// (xscale out), so it needs nothing from the prologue
 bool router_mm_supported(int T, int d, int E);
-void launch_router_mm(hipStream_t st, int T, int d, int E, const float* x, const float* xscale, const float* gis,
-                      const float* W, double* Lb, double* Bb, uint32_t* kb, int* cbad);
+void launch_router_mm(hipStream_t st, int T, int d, int E, float eps, const float* x, const float* gis, const float* W,
+                      float* xscale, double* Lb, double* Bb, uint32_t* kb, int* cbad, int* flags);
 // a stack layer's router with the previous layer's combine folded in (prev: that layer, its xin the
 // rows it reads, its xres where the new x goes; h.x must be prev.xres)
 void launch_dec_route_fused(hipStream_t st, const DecLayerH& prev, const DecLayerH& h);

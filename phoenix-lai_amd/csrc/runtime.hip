@@ -366,6 +366,9 @@ struct phx_moe_ctx {
     int device = 0;
     int ncu = 256;  // compute units of the device
     hipStream_t stream = nullptr;
+    // the general path's prologue runs on side beside the matrix-core router (fork and join events)
+    hipStream_t side = nullptr;
+    hipEvent_t ev_fork = nullptr, ev_join = nullptr;
     std::string err;
     float* gelu_tab = nullptr;
     std::vector<Layer> layers;
@@ -508,7 +511,7 @@ enum WsId {
     W_OFF, W_PERM, W_TILES, W_NTILES, W_G, W_U, W_ADN_Q, W_ADN_D, W_ADN_S, W_YD, W_SHG, W_SHU, W_ASD_Q, W_ASD_D,
     W_ASD_S, W_SHOUT, W_ZERO, W_STILES, W_SNTILES, W_SOFF, W_SPERM, W_LB, W_BB, W_ADEC, W_SDEC, W_AGUP, W_ASHP, W_AGU_H, W_ADN_H, W_ASH_H, W_ASD_H, W_X2,
     W_MM_IDS, W_MM_OFF, W_MM_PERM, W_MM_TILES, W_MM_NT, W_MM_D, W_MM_S, W_MM_H, W_AGU_BH, W_ADN_BH, W_MK_Q, W_MK_BH, W_KB,
-    W_CBAD, W_COUNT
+    W_CBAD, W_RSCALE, W_COUNT
 };
 
 int ensure(phx_moe_ctx* c, int id, size_t bytes)
@@ -619,6 +622,7 @@ int ensure_workspace(phx_moe_ctx* c, const Layer& L, int T)
     ENS(W_BB, (size_t)T * D.n_expert * 8);
     ENS(W_KB, (size_t)T * D.n_expert * 16);
     ENS(W_CBAD, (size_t)(T + 1) * 4);
+    ENS(W_RSCALE, (size_t)T * 4);
     ENS(W_U, n * D.n_ff * 4);
     ENS(W_YD, n * D.d * 4);
     if ((rc = ensure_act(c, act_fmt(D.gate_up_type), T, D.d, W_AGU_Q, W_AGU_D, W_AGU_S))) return rc;
@@ -888,6 +892,7 @@ int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, con
     // one beyond), else the exact chains
     const bool cert = !exact && cert_route(L, T, shared_ffn);
     const bool mmr = !exact && !cert && (int64_t)T * E > CERT_MAX_TE && router_mm_supported(T, d, E);
+    bool joined = false;  // the side stream's prologue still to be joined
     if (cert) {
         // the router's certified sums with the expert (and shared) inputs quantized beside them, then
         // the selection
@@ -909,10 +914,22 @@ int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, con
         Act pgu = agu, psh = ash;
         if (mma || kmma) pgu.q = nullptr, pgu.s = nullptr;
         if (smma) psh.q = nullptr, psh.s = nullptr;
+        // the matrix-core router needs nothing from the prologue: the prologue runs on the side stream
+        // beside the router and the selection, joined before the products read its rows
+        hipStream_t sp = st;
+        if (mmr) {
+            HIPCHK(c, hipEventRecord(c->ev_fork, st));
+            HIPCHK(c, hipStreamWaitEvent(c->side, c->ev_fork, 0));
+            sp = c->side;
+        }
         {
             ProfScope p(c, PHX_K_PROLOGUE);
-            launch_prologue(st, T, d, D.eps, x, L.gis, L.pre2, shared_ffn ? L.ffn_norm : nullptr,
+            launch_prologue(sp, T, d, D.eps, x, L.gis, L.pre2, shared_ffn ? L.ffn_norm : nullptr,
                             rx ? nullptr : wp<float>(c, W_RIN), wp<float>(c, W_XSCALE), pgu, psh, c->flags);
+        }
+        if (mmr) {
+            HIPCHK(c, hipEventRecord(c->ev_join, c->side));
+            joined = true;
         }
         // up to 64 experts the router's waves hold all of a token's logits and take its top-k themselves
         const bool fused_topk = E <= 64;
@@ -920,10 +937,11 @@ int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, con
             // matrix-core sums with bounds, then the certified selection (exact chains for the tokens
             // whose order the bounds leave open)
             DecLayerH h = dec_layer(c, L, T, x, shared, out, xres);
-            h.xscale = wp<float>(c, W_XSCALE);
+            h.xscale = wp<float>(c, W_RSCALE);
             {
                 ProfScope p(c, PHX_K_ROUTER);
-                launch_router_mm(st, T, d, E, x, wp<float>(c, W_XSCALE), L.gis, L.wrow, h.Lb, h.Bb, h.kb, h.bad);
+                launch_router_mm(st, T, d, E, D.eps, x, L.gis, L.wrow, wp<float>(c, W_RSCALE), h.Lb, h.Bb, h.kb, h.bad,
+                                 c->flags);
             }
             ProfScope p(c, PHX_K_TOPK);
             launch_cert_select(st, h);
@@ -951,6 +969,7 @@ int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, con
         launch_dispatch(st, n, E, tileA, wp<int>(c, W_IDS), wp<int>(c, W_OFF), wp<int>(c, W_PERM), wp<Tile>(c, W_TILES),
                         wp<int>(c, W_NTILES));
     }
+    if (joined) HIPCHK(c, hipStreamWaitEvent(st, c->ev_join, 0));  // the prologue's rows, before the products
     Act adn = make_act(c, act_fmt(D.down_type), D.down_cols, W_ADN_Q, W_ADN_D, W_ADN_S);
     if (mma || kmma) {
         adn.qh = wp<uint16_t>(c, W_ADN_H);
@@ -1230,7 +1249,10 @@ int phx_moe_create(int hip_device, phx_moe_ctx** out)
             rc = set_err(c, hip_code(h), "hipDeviceGetAttribute failed");
             break;
         }
-        if ((h = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking)) != hipSuccess) {
+        if ((h = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking)) != hipSuccess ||
+            (h = hipStreamCreateWithFlags(&c->side, hipStreamNonBlocking)) != hipSuccess ||
+            (h = hipEventCreateWithFlags(&c->ev_fork, hipEventDisableTiming)) != hipSuccess ||
+            (h = hipEventCreateWithFlags(&c->ev_join, hipEventDisableTiming)) != hipSuccess) {
             rc = set_err(c, hip_code(h), "hipStreamCreate failed");
             break;
         }
@@ -1276,6 +1298,9 @@ void phx_moe_destroy(phx_moe_ctx* c)
     if (c->gelu_tab) (void)hipFree(c->gelu_tab);
     if (c->flags) (void)hipFree(c->flags);
     if (c->iq_grid) (void)hipFree(c->iq_grid);
+    if (c->ev_fork) (void)hipEventDestroy(c->ev_fork);
+    if (c->ev_join) (void)hipEventDestroy(c->ev_join);
+    if (c->side) (void)hipStreamDestroy(c->side);
     if (c->stream) (void)hipStreamDestroy(c->stream);
     delete c;
 }
