@@ -427,7 +427,8 @@ def run_prefill(args, pkg, cfg_name="c3_prefill", steps=None):
            "kernels": {k_: {"avg_us": round(v[0] * 1e3, 2), "launches": v[1]} for k_, v in prof.items()},
            "kernel_timing": f"{steps} eager layer calls, each kernel's execution interval; 'router' is the "
                             f"certified router's matrix-core sums, 'topk' its selection (exact chains for the "
-                            f"tokens the bounds leave open)",
+                            f"tokens the bounds leave open); the prologue runs on a side stream beside them, so "
+                            f"its interval overlaps theirs",
            "router_fallback_token_frac": round(fb_tokens / (T * steps), 4),
            "assignments_per_expert": {"max": int(cnt.max()), "empty_experts": int((cnt == 0).sum())}}
     if fast:

@@ -915,22 +915,14 @@ int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, con
         if (mma || kmma) pgu.q = nullptr, pgu.s = nullptr;
         if (smma) psh.q = nullptr, psh.s = nullptr;
         // the matrix-core router needs nothing from the prologue: the prologue runs on the side stream
-        // beside the router and the selection, joined before the products read its rows
-        hipStream_t sp = st;
-        if (mmr) {
-            HIPCHK(c, hipEventRecord(c->ev_fork, st));
-            HIPCHK(c, hipStreamWaitEvent(c->side, c->ev_fork, 0));
-            sp = c->side;
-        }
-        {
+        // beside the router and the selection (launched after the router, whose workgroups need more LDS
+        // than a prologue-filled compute unit leaves), joined before the products read its rows
+        auto prologue = [&](hipStream_t sp) {
             ProfScope p(c, PHX_K_PROLOGUE);
             launch_prologue(sp, T, d, D.eps, x, L.gis, L.pre2, shared_ffn ? L.ffn_norm : nullptr,
                             rx ? nullptr : wp<float>(c, W_RIN), wp<float>(c, W_XSCALE), pgu, psh, c->flags);
-        }
-        if (mmr) {
-            HIPCHK(c, hipEventRecord(c->ev_join, c->side));
-            joined = true;
-        }
+        };
+        if (!mmr) prologue(st);
         // up to 64 experts the router's waves hold all of a token's logits and take its top-k themselves
         const bool fused_topk = E <= 64;
         if (mmr) {
@@ -938,11 +930,16 @@ int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, con
             // whose order the bounds leave open)
             DecLayerH h = dec_layer(c, L, T, x, shared, out, xres);
             h.xscale = wp<float>(c, W_RSCALE);
+            HIPCHK(c, hipEventRecord(c->ev_fork, st));
             {
                 ProfScope p(c, PHX_K_ROUTER);
                 launch_router_mm(st, T, d, E, D.eps, x, L.gis, L.wrow, wp<float>(c, W_RSCALE), h.Lb, h.Bb, h.kb, h.bad,
                                  c->flags);
             }
+            HIPCHK(c, hipStreamWaitEvent(c->side, c->ev_fork, 0));
+            prologue(c->side);
+            HIPCHK(c, hipEventRecord(c->ev_join, c->side));
+            joined = true;
             ProfScope p(c, PHX_K_TOPK);
             launch_cert_select(st, h);
         } else {
