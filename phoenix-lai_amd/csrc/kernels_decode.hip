@@ -1433,16 +1433,17 @@ __global__ __launch_bounds__(CF_NT) void k_cert_select_one(DecArgs a)
 // CpuRef.cs:183-191).
 //
 // Split over the reduction: wave w of the RM_NW waves sums the chunks [c0, c0 + cnt) of 16 elements
-// of every logit of the tile (v_mfma_f32_16x16x4_f32; lane group g of a 16 x 16 product holds the
-// elements 4 g .. 4 g + 3 of the chunk, so the four products of a chunk cover it whole), and adds
-// |C_j|, its accumulator after each chunk j, to a sum.  Each wave streams its own operands through an
-// LDS ring of RM_RING chunks (one direct global -> LDS load per 16 rows: x, W, the router scale), so
-// no barrier is needed inside the loop.
+// of every logit of the tile (router_range; v_mfma_f32_16x16x4_f32; lane group g of a 16 x 16 product
+// holds the elements 4 g .. 4 g + 3 of the chunk, so the four products of a chunk cover it whole), and
+// adds |C_j|, its accumulator after each chunk j, to a sum.  Each wave streams its own operands through
+// an LDS ring of RING chunks (one direct global -> LDS load per 16 rows: x and the prescaled router
+// rows), so no barrier is needed inside the loop.
 //
 // The bound.  With p_i = fl(m_i w_i), S_k = sum_{i <= k} p_i and u = 2^-24, the reference's chain
-// ends within 1.004 u sum_k |S_k| of S_n (n <= 65536).  The matrix cores sum a_i w_i with a_i = fl(x_i s_i)
-// and the row's factor f = rinv / sqrt(d) (exact in double) scales the sums: m_i lies within 4u of
-// f a_i (three roundings against one), so f a_i w_i stands in for p_i within 5u |f a_i w_i|.  Range r
+// ends within 1.004 u sum_k |S_k| of S_n (n <= 65536).  The matrix cores sum a_i w'_i with a_i = x_i
+// and w'_i = fl(s_i w_i) (the rows prescaled at upload), and the row's factor f = rinv / sqrt(d) (exact
+// in double) scales the sums: p_i carries four roundings (three in m_i, one in the product) and
+// f a_i w'_i one, so f a_i w'_i stands in for p_i within 5u |f a_i w'_i|.  Range r
 // (n_r elements, exact prefix O_r at its start) gives sum_{k in r} |S_k| <= n_r |O_r| + 16 sum_j |Q_rj|
 // + 15 sum_r |p| (Q_rj the range's own prefix at the end of chunk j: within a chunk each prefix differs
 // from the chunk end's by at most the chunk's |p|).  A 4-deep fp32 product rounds at most five times,
@@ -1453,21 +1454,26 @@ __global__ __launch_bounds__(CF_NT) void k_cert_select_one(DecArgs a)
 // the 1.03 factor and the coefficient of the last sum:
 //   |S_ref - L| <= 1.03 u f (sum_r n_r |O_r| + 36 sum_rj |C_rj| + 44 sum_r |a_r| |w_r|)
 //                  + 2^-50 f sum_r |C_r| + 2^-90 n (1 + f),
-// sum |a w| bounded per range by Cauchy-Schwarz, O_r from the waves' unscaled totals, L = f times their
+// sum |a w'| bounded per range by Cauchy-Schwarz (|a_r|^2 the range's double sum of squares of x, |w'_r|^2
+// formed at upload and rounded up), O_r from the waves' unscaled totals, L = f times their
 // double sum; the last terms cover L's double roundings and products or sums the matrix cores flush
 // below 2^-126.  A bound of 2^100 or more (or a non-finite one) is made infinite: the token then takes
 // the exact chains for every expert, as for a non-finite logit.  The rows' rms scales come from the
 // waves' double sums of squares, certified as the prologue certifies them, so this kernel needs no
 // input from the prologue.
-constexpr int RM_NW = 8, RM_RING = 4;
+constexpr int RM_NW = kRouterRanges;
 template <int TM16, int TN16>
 struct RmLds {
     static constexpr int TM = 16 * TM16, TN = 16 * TN16;
-    static constexpr int SLOT = (TM + TN) * 64 + 64;  // [TM x rows][TN W rows] of 16 floats, the scales' 16
-    static constexpr int DMA = TM16 + TN16 + 1;       // direct loads per chunk and wave
-    static constexpr int RINGS = RM_NW * RM_RING * SLOT;
-    // per wave: C, sum |C_j|, |m|^2, |w|^2 (floats), the tokens' sums of squares (doubles); the tokens' scales
-    static constexpr int FIN = RM_NW * (2 * TM * TN + TM + TN) * 4 + RM_NW * TM * 8 + TM * 4;
+    static constexpr int SLOT = (TM + TN) * 64;  // [TM x rows][TN W' rows] of 16 floats
+    static constexpr int DMA = TM16 + TN16;      // direct loads per chunk and wave
+    // ring depth: the chunks a wave keeps in flight (deeper rings, 160 KB of LDS at 32 x 32 and 128 KB at
+    // 16 x 16, measured no faster: C3 30.3 -> 27.7 us but the side stream's prologue then finds no room
+    // beside it and the layer got slower; C4 18.2 -> 18.8 us)
+    static constexpr int RING = 4;
+    static constexpr int RINGS = RM_NW * RING * SLOT;
+    // per wave: C, sum |C_j| (floats), |w'|^2 (floats), the tokens' sums of squares (doubles); the tokens' scales
+    static constexpr int FIN = RM_NW * (2 * TM * TN + TN) * 4 + RM_NW * TM * 8 + TM * 4;
     static constexpr int BYTES = RINGS > FIN ? RINGS : FIN;
 };
 typedef float mf4v __attribute__((ext_vector_type(4)));
@@ -1475,7 +1481,7 @@ typedef float mf4v __attribute__((ext_vector_type(4)));
 struct RmArgs {
     int T, d, E;
     float eps;
-    const float *x, *gis, *W;  // x [T][d], router scale [d], W [E][d]
+    const float *x, *W, *Wn;   // x [T][d], W [E][d] the prescaled router rows, Wn [E][RM_NW] their range norms^2
     float* xscale;             // [T] out: the rows' rms scales (the exact selection's)
     double *Lb, *Bb;
     uint4* kb;
@@ -1493,8 +1499,9 @@ __device__ __forceinline__ void router_mm_tile(const RmArgs& a, unsigned char* r
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, r = lane & 15;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int t0 = blockIdx.x * TM, e0 = blockIdx.y * TN;
-    const int nch = a.d / 16, base = nch / RM_NW, extra = nch % RM_NW;
-    const int c0 = wave * base + min(wave, extra), cnt = base + (wave < extra);
+    int c0, cnt;
+    router_range(a.d, wave, &c0, &cnt);
+    constexpr int RM_RING = RG::RING;
     unsigned char* ring = rmsm + wave * (RM_RING * RG::SLOT);
     const uint32_t ring0 = (uint32_t)(uintptr_t)(lds_void_t)ring;
     if (tid == 0 && blockIdx.x == 0 && blockIdx.y == 0) a.cbad[0] = 0;
@@ -1506,8 +1513,7 @@ __device__ __forceinline__ void router_mm_tile(const RmArgs& a, unsigned char* r
     for (int s = 0; s < TM16; s++) vx[s] = (uint32_t)((min(t0 + 16 * s + (lane >> 2), a.T - 1) * a.d + 4 * (lane & 3)) * 4);
 #pragma unroll
     for (int s = 0; s < TN16; s++) vw[s] = (uint32_t)((min(e0 + 16 * s + (lane >> 2), a.E - 1) * a.d + 4 * (lane & 3)) * 4);
-    const uint32_t vg = 16 * lane;
-    const __amdgpu_buffer_rsrc_t r_x = buf_rsrc(a.x), r_w = buf_rsrc(a.W), r_g = buf_rsrc(a.gis);
+    const __amdgpu_buffer_rsrc_t r_x = buf_rsrc(a.x), r_w = buf_rsrc(a.W);
 #define RM_LOAD(rsrc, off, voff, soff) \
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void_t)(ring + (off)), 16, voff, soff, 0, 0)
     auto issue = [&](auto SC, int j) {  // chunk j of the wave's range into slot S (past the end: the last again)
@@ -1517,55 +1523,44 @@ __device__ __forceinline__ void router_mm_tile(const RmArgs& a, unsigned char* r
         for (int s = 0; s < TM16; s++) RM_LOAD(r_x, S * RG::SLOT + 1024 * s, vx[s], so);
 #pragma unroll
         for (int s = 0; s < TN16; s++) RM_LOAD(r_w, S * RG::SLOT + TM * 64 + 1024 * s, vw[s], so);
-        if (lane < 4) RM_LOAD(r_g, S * RG::SLOT + (TM + TN) * 64, vg, so);
     };
 #undef RM_LOAD
 
     mf4v acc[TM16][TN16], sab[TM16][TN16];
-    float mm[TM16], ww[TN16];
     double s2[TM16];  // the rows' sums of squares (this lane's elements)
 #pragma unroll
     for (int i = 0; i < TM16; i++) {
-        mm[i] = 0.0f;
         s2[i] = 0.0;
 #pragma unroll
         for (int j = 0; j < TN16; j++) acc[i][j] = sab[i][j] = mf4v{0.0f, 0.0f, 0.0f, 0.0f};
     }
-#pragma unroll
-    for (int j = 0; j < TN16; j++) ww[j] = 0.0f;
-    // the lane's LDS read addresses: x row 16 i + r, W row 16 j + r, 16 bytes g; the scales' 16 bytes g
-    const uint32_t a_x = ring0 + r * 64 + 16 * g, a_w = a_x + TM * 64, a_g = ring0 + (TM + TN) * 64 + 16 * g;
+    // the lane's LDS read addresses: x row 16 i + r, W' row 16 j + r, 16 bytes g
+    const uint32_t a_x = ring0 + r * 64 + 16 * g, a_w = a_x + TM * 64;
 
     auto step = [&](auto SC, int j) {
         constexpr int S = decltype(SC)::value;
         __builtin_amdgcn_s_waitcnt(vm_wait(RG::DMA * (RM_RING - 1)));  // chunk j landed (the later ones may not)
-        u32x4 X[TM16], Wv[TN16], G;
+        u32x4 X[TM16], Wv[TN16];
         static_for<TM16>([&](auto I) { X[I] = ds_r128<S * RG::SLOT + 1024 * decltype(I)::value>(a_x); });
         static_for<TN16>([&](auto J) { Wv[J] = ds_r128<S * RG::SLOT + 1024 * decltype(J)::value>(a_w); });
-        G = ds_r128<S * RG::SLOT>(a_g);
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
         for (int i = 0; i < TM16; i++) tie(X[i]);
 #pragma unroll
         for (int jj = 0; jj < TN16; jj++) tie(Wv[jj]);
-        tie(G);
+        // x as it is (the row's scale rinv / sqrt(d) is applied to the sums), W' prescaled at upload
         float m[TM16][4], w[TN16][4];
 #pragma unroll
         for (int i = 0; i < TM16; i++)
 #pragma unroll
             for (int q = 0; q < 4; q++) {
-                const float xv = __uint_as_float(X[i][q]);
-                m[i][q] = xv * __uint_as_float(G[q]);  // x s: the row's scale rinv / sqrt(d) is applied to the sums
-                mm[i] = fmaf(m[i][q], m[i][q], mm[i]);
-                s2[i] += (double)xv * (double)xv;
+                m[i][q] = __uint_as_float(X[i][q]);
+                s2[i] = fma((double)m[i][q], (double)m[i][q], s2[i]);  // x^2 exact in double: one rounding either way
             }
 #pragma unroll
         for (int jj = 0; jj < TN16; jj++)
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-                w[jj][q] = __uint_as_float(Wv[jj][q]);
-                ww[jj] = fmaf(w[jj][q], w[jj][q], ww[jj]);
-            }
+            for (int q = 0; q < 4; q++) w[jj][q] = __uint_as_float(Wv[jj][q]);
 #pragma unroll
         for (int q = 0; q < 4; q++)
 #pragma unroll
@@ -1597,22 +1592,14 @@ __device__ __forceinline__ void router_mm_tile(const RmArgs& a, unsigned char* r
     // the squares' sums over the four lane groups (each lane: its group's elements of row r)
 #pragma unroll
     for (int i = 0; i < TM16; i++) {
-        mm[i] += __shfl_xor(mm[i], 16);
-        mm[i] += __shfl_xor(mm[i], 32);
         s2[i] += __shfl_xor(s2[i], 16);
         s2[i] += __shfl_xor(s2[i], 32);
-    }
-#pragma unroll
-    for (int jj = 0; jj < TN16; jj++) {
-        ww[jj] += __shfl_xor(ww[jj], 16);
-        ww[jj] += __shfl_xor(ww[jj], 32);
     }
     __syncthreads();  // every wave is done with its ring
     float* fC = (float*)rmsm;          // [wave][TM][TN] the range's sum
     float* fS = fC + RM_NW * TM * TN;  // [wave][TM][TN] its sum of |C_j|
-    float* fM = fS + RM_NW * TM * TN;  // [wave][TM] |m|^2 over the range
-    float* fW = fM + RM_NW * TM;       // [wave][TN] |w|^2
-    double* fQ = (double*)(fW + RM_NW * TN);  // [wave][TM] the rows' sums of squares
+    float* fW = fS + RM_NW * TM * TN;  // [wave][TN] |w'|^2 over the range (from upload)
+    double* fQ = (double*)(fW + RM_NW * TN);  // [wave][TM] the rows' sums of squares over the range
     float* fR = (float*)(fQ + RM_NW * TM);    // [TM] the rows' rms scales
 #pragma unroll
     for (int i = 0; i < TM16; i++)
@@ -1626,13 +1613,9 @@ __device__ __forceinline__ void router_mm_tile(const RmArgs& a, unsigned char* r
             }
     if (g == 0) {
 #pragma unroll
-        for (int i = 0; i < TM16; i++) {
-            fM[wave * TM + 16 * i + r] = mm[i];
-            fQ[wave * TM + 16 * i + r] = s2[i];
-        }
-#pragma unroll
-        for (int jj = 0; jj < TN16; jj++) fW[wave * TN + 16 * jj + r] = ww[jj];
+        for (int i = 0; i < TM16; i++) fQ[wave * TM + 16 * i + r] = s2[i];
     }
+    if (lane < TN) fW[wave * TN + lane] = a.Wn[(int64_t)min(e0 + lane, a.E - 1) * RM_NW + wave];
     __syncthreads();
     // each row's scale as CpuRef.RmsNorm forms it (src/CpuRef.cs:183-191): the waves' double sums in a
     // fixed order, certified against the sequential sum (any order of the d non-negative terms lies within
@@ -1662,12 +1645,14 @@ __device__ __forceinline__ void router_mm_tile(const RmArgs& a, unsigned char* r
         const double f = (double)fR[tl] * sc;  // rinv / sqrt(d): exact in double
         double O = 0.0, mainb = 0.0, cs = 0.0, absC = 0.0;
         for (int w = 0; w < RM_NW; w++) {
-            const double nw = 16.0 * (base + (w < extra));
+            int wc0, wcnt;
+            router_range(a.d, w, &wc0, &wcnt);
+            const double nw = 16.0 * wcnt;
             const double C = fC[(w * TM + tl) * TN + el], Sj = fS[(w * TM + tl) * TN + el];
             mainb += nw * fabs(O) + 36.0 * Sj;
             O += C;
             absC += fabs(C);
-            cs += (double)sqrtf(fM[w * TM + tl] * fW[w * TN + el]);  // (its float roundings: inside the 1.03)
+            cs += sqrt(fQ[w * TM + tl] * (double)fW[w * TN + el]);  // (its roundings: inside the 1.03)
         }
         double B = 0x1.08p-24 * f * (mainb + 44.0 * cs) + 0x1p-50 * f * absC + 0x1p-90 * a.d * (1.0 + f);
         if (!(B < 0x1p100)) B = INFINITY;  // also NaN
@@ -2106,10 +2091,10 @@ bool router_mm_supported(int T, int d, int E)
            (int64_t)E * d * 4 < ((int64_t)1 << 31);
 }
 
-void launch_router_mm(hipStream_t st, int T, int d, int E, float eps, const float* x, const float* gis, const float* W,
+void launch_router_mm(hipStream_t st, int T, int d, int E, float eps, const float* x, const float* Ws, const float* Wn,
                       float* xscale, double* Lb, double* Bb, uint32_t* kb, int* cbad, int* flags)
 {
-    const RmArgs a{T, d, E, eps, x, gis, W, xscale, Lb, Bb, (uint4*)kb, cbad, flags};
+    const RmArgs a{T, d, E, eps, x, Ws, Wn, xscale, Lb, Bb, (uint4*)kb, cbad, flags};
     // 32 x 32 tiles where they still give a workgroup per compute unit, 16 x 16 below
     if ((int64_t)((T + 31) / 32) * ((E + 31) / 32) >= 256) {
         using RG = RmLds<2, 2>;

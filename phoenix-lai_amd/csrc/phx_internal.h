@@ -222,10 +222,20 @@ void launch_dec_route(hipStream_t st, const DecLayerH& h);
 // the general path's selection from k_dec_route's certified sums: ids, weights and logits per token
 void launch_cert_select(hipStream_t st, const DecLayerH& h);
 // the certified router for many tokens: matrix-core logits with bounds (Lb, Bb) and selection keys kb
-// [T][E][4] for launch_cert_select, from x and the router scale; it forms the rows' rms scales itself
-// (xscale out), so it needs nothing from the prologue
+// [T][E][4] for launch_cert_select, from x and the router rows prescaled at upload (Ws[e][i] =
+// fl(s_i W[e][i]), s the router scale) with their squared norms over the kernel's kRouterRanges
+// reduction ranges (Wn[e][r], rounded up); it forms the rows' rms scales itself (xscale out), so it
+// needs nothing from the prologue
+constexpr int kRouterRanges = 8;
+// reduction range r of a row of d elements (d % 16 == 0): chunks of 16 elements [c0, c0 + cnt)
+__host__ __device__ inline void router_range(int d, int r, int* c0, int* cnt)
+{
+    const int nch = d / 16, base = nch / kRouterRanges, extra = nch % kRouterRanges;
+    *c0 = r * base + (r < extra ? r : extra);
+    *cnt = base + (r < extra);
+}
 bool router_mm_supported(int T, int d, int E);
-void launch_router_mm(hipStream_t st, int T, int d, int E, float eps, const float* x, const float* gis, const float* W,
+void launch_router_mm(hipStream_t st, int T, int d, int E, float eps, const float* x, const float* Ws, const float* Wn,
                       float* xscale, double* Lb, double* Bb, uint32_t* kb, int* cbad, int* flags);
 // a stack layer's router with the previous layer's combine folded in (prev: that layer, its xin the
 // rows it reads, its xres where the new x goes; h.x must be prev.xres)

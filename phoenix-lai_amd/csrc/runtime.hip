@@ -350,6 +350,7 @@ struct Layer {
     bool present = false;
     phx_moe_layer_desc desc{};
     float *wt4 = nullptr, *wrow = nullptr, *gis = nullptr, *ds = nullptr, *pre2 = nullptr, *post1 = nullptr, *post2 = nullptr;
+    float *wsc = nullptr, *wnr = nullptr;  // the many-token router's prescaled rows and their range norms^2
     float *ffn_norm = nullptr, *post_ffw = nullptr;
     QMat gu, dn, sgu, sdn;
     uint64_t gen = 0;  // upload generation: graphs captured over an earlier upload are stale
@@ -933,7 +934,7 @@ int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, con
             HIPCHK(c, hipEventRecord(c->ev_fork, st));
             {
                 ProfScope p(c, PHX_K_ROUTER);
-                launch_router_mm(st, T, d, E, D.eps, x, L.gis, L.wrow, wp<float>(c, W_RSCALE), h.Lb, h.Bb, h.kb, h.bad,
+                launch_router_mm(st, T, d, E, D.eps, x, L.wsc, L.wnr, wp<float>(c, W_RSCALE), h.Lb, h.Bb, h.kb, h.bad,
                                  c->flags);
             }
             HIPCHK(c, hipStreamWaitEvent(c->side, c->ev_fork, 0));
@@ -1106,7 +1107,7 @@ int upload_q(phx_moe_ctx* c, int type, const void* src, int n_mat, int rows, int
 
 void free_layer(Layer& L)
 {
-    float** fs[] = {&L.wt4, &L.wrow, &L.gis, &L.ds, &L.pre2, &L.post1, &L.post2, &L.ffn_norm, &L.post_ffw};
+    float** fs[] = {&L.wt4, &L.wrow, &L.gis, &L.ds, &L.pre2, &L.post1, &L.post2, &L.ffn_norm, &L.post_ffw, &L.wsc, &L.wnr};
     for (float** f : fs) {
         if (*f) (void)hipFree(*f);
         *f = nullptr;
@@ -1325,6 +1326,28 @@ int phx_moe_layer_upload(phx_moe_ctx* c, int layer, const phx_moe_layer_desc* D)
     if ((rc = upload_f32(c, wt.data(), wt.size(), &L.wt4))) return rc;
     if ((rc = upload_f32(c, D->gate_inp, (size_t)d * E, &L.wrow))) return rc;
     if ((rc = upload_f32(c, D->gate_inp_scale, d, &L.gis))) return rc;
+    if (d % 16 == 0 && d / 16 >= kRouterRanges) {
+        // the matrix-core router's operands: w'_i = fl(s_i w_i) (one float product, as the kernel would
+        // form it) and |w'_r|^2 over each reduction range, a double sum rounded up to a float
+        std::vector<float> ws((size_t)d * E), wn((size_t)E * kRouterRanges);
+        for (int e = 0; e < E; e++) {
+            const float* w = D->gate_inp + (size_t)e * d;
+            float* o = ws.data() + (size_t)e * d;
+            for (int i = 0; i < d; i++) o[i] = D->gate_inp_scale[i] * w[i];
+            for (int r = 0; r < kRouterRanges; r++) {
+                int c0, cnt;
+                router_range(d, r, &c0, &cnt);
+                double q = 0.0;
+                for (int i = 16 * c0; i < 16 * (c0 + cnt); i++) q += (double)o[i] * (double)o[i];
+                q *= 1.0 + 0x1p-40;  // above the double sum's relative error (n * 2^-53, n <= 4096)
+                float f = (float)q;
+                if ((double)f < q) f = nextafterf(f, INFINITY);
+                wn[(size_t)e * kRouterRanges + r] = (q == q) ? f : NAN;
+            }
+        }
+        if ((rc = upload_f32(c, ws.data(), ws.size(), &L.wsc))) return rc;
+        if ((rc = upload_f32(c, wn.data(), wn.size(), &L.wnr))) return rc;
+    }
     if ((rc = upload_f32(c, D->down_scale, E, &L.ds))) return rc;
     if ((rc = upload_f32(c, D->pre_ffw_norm_2, d, &L.pre2))) return rc;
     if ((rc = upload_f32(c, D->post_ffw_norm_1, d, &L.post1))) return rc;
