@@ -224,7 +224,10 @@ int phx_moe_profile_read(phx_moe_ctx* ctx, double* total_ms, int64_t* launches);
  * fp16 bits a; 8 and 9 one fp32 matrix-core product (v_mfma_f32_16x16x4_f32) per 64 inputs (n a
  * multiple of 64): lane l of a group supplies A[l % 16][l / 16] = a and B[l / 16][l % 16] = b, the
  * accumulator starts at 0 (8) or 1 (9), and out holds D[4 (l / 16)][l % 16] (the numerics the
- * many-token router's error bound assumes).  out is float (int results as their value). */
+ * many-token router's error bound assumes); 10 the sequential double sum of squares of each row of
+ * m = b[0] floats of a (n a multiple of m, 2 <= m <= 65536), the sum RmsNorm's certified means fall back
+ * to, formed by one wave as the kernels form it: out[2 r] and out[2 r + 1] hold the low and high 32
+ * bits of row r's double.  out is float (int results as their value). */
 int phx_moe_selftest(phx_moe_ctx* ctx, int op, int n, const float* a, const float* b, float* out);
 
 /* Average time (ms) of `iters` coalesced streaming reads of a device buffer: the achievable HBM

@@ -411,6 +411,106 @@ __device__ __forceinline__ void mean_ends(double S, double B, double rn, float* 
     *hi = (float)((S + Bw) * rn);
 }
 
+// ------------------------------------------------------------------------------ sequential sum of squares
+// The reference's sum of squares q = ((0 + x_0^2) + x_1^2) + ... + x_{n-1}^2 in double, in index order
+// (CpuRef.RmsNorm, src/CpuRef.cs:186-187), bit for bit, by one wave (all 64 lanes, uniform control flow)
+// with far fewer than n dependent additions.  Every x_i^2 is exact in double and every partial sum is
+// >= 0, so the chain only climbs.  While it stays in one binade [2^e, 2^(e+1)) its values are multiples
+// of g = 2^(e-52) and each step adds x_i^2 rounded to a multiple of g: to nearest, and at an exact half
+// to the even multiple of the sum, so the step count of g is fixed by x_i and the parity of the sum
+// before it (and the sum is even right after such a step).  Lane c takes the chunk [c C, (c + 1) C),
+// C = ceil(n / 64), and counts its steps for either starting parity when the chunk lies in one binade:
+// the chain stays within (n + 128) 2^-51 of the exact prefix sums, and the wave's scan of the chunk sums
+// within that of them too, so the chunk's ends bound it.  A walk over the 64 chunks then adds each such
+// chunk's count for the parity the sum has at its start and replays the others (the first chunk, those
+// where the sum crosses a power of two: about 7 of 64 for rows of like terms, non-finite ones) term by
+// term.  Short rows are summed term by term.
+__device__ __forceinline__ double seq_sum_sq_serial(const float* x, int b, int e, double q)
+{
+    int i = b;
+    for (; i + 8 <= e; i += 8) {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) v[j] = x[i + j];
+#pragma unroll
+        for (int j = 0; j < 8; j++) q = fma((double)v[j], (double)v[j], q);  // x^2 exact: one rounding
+    }
+    for (; i < e; i++) q = fma((double)x[i], (double)x[i], q);
+    return q;
+}
+
+// a wave-uniform double from lane c (c uniform)
+__device__ __forceinline__ double readlane_d(double v, int c)
+{
+    const long long t = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_readlane((int)t, c), hi = __builtin_amdgcn_readlane((int)(t >> 32), c);
+    return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
+
+// whether the integer-valued double v (0 <= v < 2^53) is odd
+__device__ __forceinline__ bool odd_d(double v) { return floor(v * 0.5) != v * 0.5; }
+
+__device__ __noinline__ double seq_sum_sq_wave(const float* x, int n)
+{
+    if (n < 512) return seq_sum_sq_serial(x, 0, n, 0.0);
+    const int lane = threadIdx.x & 63, C = (n + 63) / 64;
+    const int b = min(n, lane * C), e = min(n, b + C);
+    double Q = 0.0;
+    for (int i = b; i < e; i++) Q = fma((double)x[i], (double)x[i], Q);
+    double inc = Q;  // inclusive scan of the chunk sums, then the exclusive one: A = the chunks before
+#pragma unroll
+    for (int k = 1; k < 64; k *= 2) {
+        const double y = __shfl_up(inc, k, 64);
+        if (lane >= k) inc += y;
+    }
+    double A = __shfl_up(inc, 1, 64);
+    if (lane == 0) A = 0.0;
+    const double eps = ((double)n + 128.0) * 0x1p-50;  // twice the chain's and the scan's relative error
+    const double lo = A * (1.0 - eps), hi = (A + Q) * (1.0 + eps);
+    int el = 0, eh = 1;
+    if (lo > 0.0 && hi < INFINITY) {
+        frexp(lo, &el);
+        frexp(hi, &eh);
+    }
+    const int ex = el - 1;  // lo in [2^ex, 2^(ex + 1))
+    // the chunk's count of g = 2^(ex - 52) for a start of even parity (d0), and the odd start's difference
+    // at its first half-way term (after it both sums are even and agree)
+    double d0 = 0.0;
+    int diff = 0, ties = 0;
+    const bool clean = b < e && el == eh;
+    if (clean) {
+        for (int i = b; i < e; i++) {
+            const double t = (double)x[i] * (double)x[i];
+            const double v = ldexp(t, 52 - ex), fl = floor(v), f = v - fl;
+            double step = f > 0.5 ? fl + 1.0 : fl;
+            if (f == 0.5) {  // to the even multiple: (start + d0 + fl) even keeps fl, else fl + 1
+                const bool up = odd_d(d0) != odd_d(fl);  // even start
+                step = up ? fl + 1.0 : fl;
+                if (ties++ == 0) diff = up ? -1 : 1;  // the odd start rounds the other way
+            }
+            d0 += step;
+        }
+    }
+    // the walk: each clean chunk's count for the parity of the sum at its start, the others term by term
+    const int info = clean ? ((ex + 2048) << 2 | (ties ? 2 : 0) | 1) : 0;
+    double q = 0.0;
+    for (int c = 0; c < 64; c++) {  // uniform
+        const int cb = min(n, c * C), ce = min(n, cb + C);
+        if (cb >= ce) break;
+        const int ci = __builtin_amdgcn_readlane(info, c);
+        if (ci & 1) {
+            const int cx = (ci >> 2) - 2048;
+            double D = readlane_d(d0, c);
+            // q lies in [2^cx, 2^(cx + 1)): its last significand bit is its parity in g
+            if ((ci & 2) && (__double_as_longlong(q) & 1)) D += (double)__builtin_amdgcn_readlane(diff, c);
+            q += ldexp(D, cx - 52);  // exact: the result is the chain's value
+        } else {
+            q = seq_sum_sq_serial(x, cb, ce, q);
+        }
+    }
+    return q;
+}
+
 // Mean of squares of one row as CpuRef.RmsNorm rounds it: (float)(sum / n) with sum the double sum of
 // x_i^2 in index order (src/CpuRef.cs:186-188).  A parallel double sum differs from the sequential
 // one by at most (n + per + depth) * 2^-53 * sum (all terms are non-negative); when both ends of
@@ -449,11 +549,12 @@ __device__ float mean_sq_cert_from(double s, int per, const float* x, int n, dou
     float mean = lo;
     if (lo != hi) {
         __syncthreads();
-        if (tid == 0) {
-            double q = 0.0;
-            for (int i = 0; i < n; i++) q += (double)x[i] * (double)x[i];
-            red[NW] = q;
-            if (fallbacks) atomicAdd(fallbacks, 1);
+        if (tid < 64) {
+            const double q = seq_sum_sq_wave(x, n);
+            if (tid == 0) {
+                red[NW] = q;
+                if (fallbacks) atomicAdd(fallbacks, 1);
+            }
         }
         __syncthreads();
         mean = (float)(red[NW] / (double)n);
@@ -477,12 +578,8 @@ __device__ __forceinline__ float mean_sq_cert_wave(const float* x, int n, int* f
     float lo, hi;
     mean_ends(S, B, 1.0 / (double)n, &lo, &hi);
     if (lo == hi) return lo;
-    double q = 0.0;
-    if (lane == 0) {
-        for (int i = 0; i < n; i++) q += (double)x[i] * (double)x[i];
-        if (fallbacks) atomicAdd(fallbacks, 1);
-    }
-    q = __shfl(q, 0, 64);
+    const double q = seq_sum_sq_wave(x, n);
+    if (lane == 0 && fallbacks) atomicAdd(fallbacks, 1);
     return (float)(q / (double)n);
 }
 

@@ -1987,6 +1987,24 @@ void launch_selftest(hipStream_t st, int op, int n, const float* a, const float*
     launch(k_selftest, dim3((n + 255) / 256), dim3(256), 0, st, op, n, a, b, out, tab);
 }
 
+// one wave per row of m floats: the row's sequential double sum of squares (seq_sum_sq_wave), its two
+// 32-bit halves in out[2 r] (low) and out[2 r + 1] (high)
+__global__ __launch_bounds__(64) void k_selftest_seq(int m, const float* __restrict__ a, float* __restrict__ out)
+{
+    const int r = blockIdx.x;
+    const double q = seq_sum_sq_wave(a + (int64_t)r * m, m);
+    if (threadIdx.x == 0) {
+        const unsigned long long u = (unsigned long long)__double_as_longlong(q);
+        out[2 * r] = __uint_as_float((unsigned)u);
+        out[2 * r + 1] = __uint_as_float((unsigned)(u >> 32));
+    }
+}
+
+void launch_selftest_seq(hipStream_t st, int m, int rows, const float* a, float* out)
+{
+    launch(k_selftest_seq, dim3(rows), dim3(64), 0, st, m, a, out);
+}
+
 }  // namespace phx
 
 #ifdef PHX_TIMELINE

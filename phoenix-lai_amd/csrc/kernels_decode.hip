@@ -110,8 +110,9 @@ struct DecArgs {
 // depth here is far below 64); when both ends of that interval give the same float the result is the
 // reference's, otherwise thread 0 re-sums sequentially (rare; counted in *fallbacks when non-null).
 // Workgroup-level: every thread calls it; red holds blockDim.x / 64 + 1 doubles.  TRAIL: a closing
-// barrier, for callers that reuse red right after.
-template <bool TRAIL = true>
+// barrier, for callers that reuse red right after.  WAVE: the sequential sum by wave 0
+// (seq_sum_sq_wave), else by thread 0 alone (for kernels whose registers are tight).
+template <bool TRAIL = true, bool WAVE = true>
 __device__ float wg_mean_sq(double s, const float* xr, int n, double* red, int* fallbacks)
 {
     const int tid = threadIdx.x, lane = tid & 63, nw = blockDim.x >> 6;
@@ -124,11 +125,15 @@ __device__ float wg_mean_sq(double s, const float* xr, int n, double* red, int* 
     mean_ends(S, B, 1.0 / (double)n, &lo, &hi);
     float mean = lo;
     if (lo != hi) {  // uniform: every thread formed the same S
-        if (tid == 0) {
+        if (WAVE ? tid < 64 : tid == 0) {
             double q = 0.0;
-            for (int i = 0; i < n; i++) q += (double)xr[i] * (double)xr[i];
-            red[nw] = q;
-            if (fallbacks) atomicAdd(fallbacks, 1);
+            if (WAVE) q = seq_sum_sq_wave(xr, n);
+            else
+                for (int i = 0; i < n; i++) q += (double)xr[i] * (double)xr[i];
+            if (tid == 0) {
+                red[nw] = q;
+                if (fallbacks) atomicAdd(fallbacks, 1);
+            }
         }
         __syncthreads();
         mean = (float)(red[nw] / (double)n);
@@ -160,18 +165,20 @@ __device__ void wg_mean_sq2(double s0, double s1, const float* x0, const float* 
     mean_ends(S0, B0, rn, &lo0, &hi0);
     mean_ends(S1, B1, rn, &lo1, &hi1);
     if (lo0 != hi0 || lo1 != hi1) {  // uniform: every thread formed the same sums
-        if (tid == 0) {
+        if (tid < 64) {
             if (lo0 != hi0) {
-                double q = 0.0;
-                for (int i = 0; i < n; i++) q += (double)x0[i] * (double)x0[i];
-                red[nw] = q;
-                if (fallbacks) atomicAdd(fallbacks, 1);
+                const double q = seq_sum_sq_wave(x0, n);
+                if (tid == 0) {
+                    red[nw] = q;
+                    if (fallbacks) atomicAdd(fallbacks, 1);
+                }
             }
             if (lo1 != hi1 && x1) {
-                double q = 0.0;
-                for (int i = 0; i < n; i++) q += (double)x1[i] * (double)x1[i];
-                red1[nw] = q;
-                if (fallbacks) atomicAdd(fallbacks, 1);
+                const double q = seq_sum_sq_wave(x1, n);
+                if (tid == 0) {
+                    red1[nw] = q;
+                    if (fallbacks) atomicAdd(fallbacks, 1);
+                }
             }
         }
         __syncthreads();
@@ -641,7 +648,7 @@ __device__ __forceinline__ void route_wg(const DecArgs& a, int t, int e, float* 
     float mean, mhi;
     mean_ends(S, Bs, 1.0 / (double)d, &mean, &mhi);
     if (mean != mhi) {  // uniform: S is the same in every thread
-        if (tid == 0) {
+        if (tid == 0) {  // (one thread: the wave routine would cost this kernel registers)
             double q = 0.0;
             for (int i = 0; i < d; i++) q += (double)sx[i] * (double)sx[i];
             red[RT_MAXW] = q;
@@ -1142,7 +1149,7 @@ __device__ void select_exact(const DecArgs& a, unsigned char* un, int* s_ids, co
         } else {
             double s = 0.0;
             for (int i = tid; i < a.d; i += NT) s += (double)xr[i] * (double)xr[i];
-            rinv_t = rms_scale_from_mean(wg_mean_sq(s, xr, a.d, red, nullptr), a.eps);
+            rinv_t = rms_scale_from_mean(wg_mean_sq<true, PIPE>(s, xr, a.d, red, nullptr), a.eps);
         }
         for (int i = tid; i < a.d; i += NT) sm[i] = ((xr[i] * rinv_t) * sc) * a.gis[i];
         const bool nonfinite = __syncthreads_or(tid < E && !(isfinite(lb) && isfinite(bb)));  // publishes sm, slo
@@ -1620,22 +1627,27 @@ __device__ __forceinline__ void router_mm_tile(const RmArgs& a, unsigned char* r
     // each row's scale as CpuRef.RmsNorm forms it (src/CpuRef.cs:183-191): the waves' double sums in a
     // fixed order, certified against the sequential sum (any order of the d non-negative terms lies within
     // (d + 64) 2^-52 of it), else re-summed in index order by this thread (rare; counted)
-    if (tid < TM) {
-        const int t = min(t0 + tid, a.T - 1);
-        double S = 0.0;
-        for (int w = 0; w < RM_NW; w++) S += fQ[w * TM + tid];
-        float mean, mhi;
-        mean_ends(S, ((double)a.d + 64.0) * 0x1p-52 * S, 1.0 / (double)a.d, &mean, &mhi);
-        if (mean != mhi) {
-            const float* xr = a.x + (int64_t)t * a.d;
-            double q = 0.0;
-            for (int i = 0; i < a.d; i++) q += (double)xr[i] * (double)xr[i];
-            mean = (float)(q / (double)a.d);
-            if (blockIdx.y == 0 && t0 + tid < a.T && a.flags) atomicAdd(&a.flags[0], 1);
+    static_assert(TM <= 64, "one lane of wave 0 per row");
+    if (wave == 0) {
+        const int t = min(t0 + lane, a.T - 1);
+        float mean = 0.0f, mhi = 0.0f;
+        if (lane < TM) {
+            double S = 0.0;
+            for (int w = 0; w < RM_NW; w++) S += fQ[w * TM + lane];
+            mean_ends(S, ((double)a.d + 64.0) * 0x1p-52 * S, 1.0 / (double)a.d, &mean, &mhi);
         }
-        const float rinv = rms_scale_from_mean(mean, a.eps);
-        fR[tid] = rinv;
-        if (blockIdx.y == 0 && t0 + tid < a.T) a.xscale[t] = rinv;
+        // rows the bound leaves open: the sequential sum by the whole wave, one row after another
+        for (unsigned long long open = __ballot(lane < TM && mean != mhi); open; open &= open - 1) {
+            const int rr = __builtin_ctzll(open), tr = min(t0 + rr, a.T - 1);
+            const double q = seq_sum_sq_wave(a.x + (int64_t)tr * a.d, a.d);
+            if (lane == rr) mean = (float)(q / (double)a.d);
+            if (lane == 0 && blockIdx.y == 0 && t0 + rr < a.T && a.flags) atomicAdd(&a.flags[0], 1);
+        }
+        if (lane < TM) {
+            const float rinv = rms_scale_from_mean(mean, a.eps);
+            fR[lane] = rinv;
+            if (blockIdx.y == 0 && t0 + lane < a.T) a.xscale[t] = rinv;
+        }
     }
     __syncthreads();
     const double sc = (double)(1.0f / (float)__dsqrt_rn((double)a.d));
@@ -1904,6 +1916,7 @@ __global__ __launch_bounds__(CB_NT) void k_dec_combine(DecArgs a)
     wg_mean_sq2(s2, s1, cb, sh ? (const float*)sh : nullptr, d, red, a.flags, &m2, &m1);
     const float sc2 = rms_scale_from_mean(m2, a.eps);
     const float sc1 = sh ? rms_scale_from_mean(m1, a.eps) : 0.0f;
+    acc = sacc[ix];  // from LDS: not held in registers across the means' fallback
     float4 ov;
     ov.x = (sh ? shv.x * sc1 * p1.x : 0.0f) + acc.x * sc2 * p2.x;
     ov.y = (sh ? shv.y * sc1 * p1.y : 0.0f) + acc.y * sc2 * p2.y;

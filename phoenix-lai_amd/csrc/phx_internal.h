@@ -256,5 +256,6 @@ void launch_planar_act(hipStream_t st, int rows, int n, const int8_t* qs, const 
 // planar Q8_K rows (qs [rows][n], d [rows][n/256]) into a's K-quant orders (ACT_K4 / ACT_K6, qh / bh when set)
 void launch_planar_act_k(hipStream_t st, int rows, int n, const int8_t* qs, const float* d, Act a);
 void launch_selftest(hipStream_t st, int op, int n, const float* a, const float* b, float* out, const float* gelu_tab);
+void launch_selftest_seq(hipStream_t st, int m, int rows, const float* a, float* out);
 
 }  // namespace phx

@@ -1810,7 +1810,13 @@ int phx_moe_profile_read(phx_moe_ctx* c, double* total_ms, int64_t* launches)
 
 int phx_moe_selftest(phx_moe_ctx* c, int op, int n, const float* a, const float* b, float* out)
 {
-    if (!c || n <= 0 || !a || !b || !out || op < 0 || op > 9 || (op >= 8 && n % 64)) return PHX_ERR_ARG;
+    if (!c || n <= 0 || !a || !b || !out || op < 0 || op > 10 || ((op == 8 || op == 9) && n % 64)) return PHX_ERR_ARG;
+    int m = 0;  // op 10: the row length
+    if (op == 10) {
+        if (!(b[0] >= 2.0f && b[0] <= 65536.0f)) return PHX_ERR_ARG;
+        m = (int)b[0];
+        if ((float)m != b[0] || n % m) return PHX_ERR_ARG;
+    }
     ENTER(c);
     float *da = nullptr, *db = nullptr, *dout = nullptr;
     size_t bytes = (size_t)n * 4;
@@ -1819,7 +1825,8 @@ int phx_moe_selftest(phx_moe_ctx* c, int op, int n, const float* a, const float*
     HIPCHK(c, dev_malloc(c, (void**)&dout, bytes));
     HIPCHK(c, hipMemcpy(da, a, bytes, hipMemcpyHostToDevice));
     HIPCHK(c, hipMemcpy(db, b, bytes, hipMemcpyHostToDevice));
-    launch_selftest(c->stream, op, n, da, db, dout, c->gelu_tab);
+    if (op == 10) launch_selftest_seq(c->stream, m, n / m, da, dout);
+    else launch_selftest(c->stream, op, n, da, db, dout, c->gelu_tab);
     HIPCHK(c, hipStreamSynchronize(c->stream));
     HIPCHK(c, hipMemcpy(out, dout, bytes, hipMemcpyDeviceToHost));
     (void)hipFree(da);
