@@ -1651,20 +1651,20 @@ __device__ __forceinline__ void router_mm_tile(const RmArgs& a, unsigned char* r
     }
     __syncthreads();
     const double sc = (double)(1.0f / (float)__dsqrt_rn((double)a.d));
+    const int nbase = a.d / 16 / RM_NW, nextra = a.d / 16 % RM_NW;  // router_range's split
     for (int o = tid; o < TM * TN; o += RM_NW * 64) {
         const int tl = o / TN, el = o % TN, t = t0 + tl, e = e0 + el;
         if (t >= a.T || e >= a.E) continue;
         const double f = (double)fR[tl] * sc;  // rinv / sqrt(d): exact in double
-        double O = 0.0, mainb = 0.0, cs = 0.0, absC = 0.0;
+        double O = 0.0, mainb = 0.0, absC = 0.0;
+        float cs = 0.0f;
         for (int w = 0; w < RM_NW; w++) {
-            int wc0, wcnt;
-            router_range(a.d, w, &wc0, &wcnt);
-            const double nw = 16.0 * wcnt;
+            const double nw = 16.0 * (nbase + (w < nextra));
             const double C = fC[(w * TM + tl) * TN + el], Sj = fS[(w * TM + tl) * TN + el];
             mainb += nw * fabs(O) + 36.0 * Sj;
             O += C;
             absC += fabs(C);
-            cs += sqrt(fQ[w * TM + tl] * (double)fW[w * TN + el]);  // (its roundings: inside the 1.03)
+            cs += sqrtf((float)fQ[w * TM + tl]) * sqrtf(fW[w * TN + el]);  // (its float roundings: inside the 1.03)
         }
         double B = 0x1.08p-24 * f * (mainb + 44.0 * cs) + 0x1p-50 * f * absC + 0x1p-90 * a.d * (1.0 + f);
         if (!(B < 0x1p100)) B = INFINITY;  // also NaN
