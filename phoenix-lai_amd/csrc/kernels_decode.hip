@@ -1111,7 +1111,7 @@ __device__ void exact_chains_wide(const float* W, int d, const float* sm, const 
 // chosen expert's lower end, so the top-k lies among the ambiguous ones, unless a chain ends
 // non-finite: then every expert of the token is recomputed and ranked.  un: the LDS of sel_lds; sL (at un) ends holding the logits
 // the routing reports for those tokens.
-// PIPE: the fallback kernel's variant (the prologue's rms scales when given)
+// PIPE: the fallback kernel's variant (the rms scales the many-token router formed, when given)
 template <bool PIPE = false>
 __device__ void select_exact(const DecArgs& a, unsigned char* un, int* s_ids, const int* s_bad, double* red,
                              bool count)
@@ -1144,7 +1144,7 @@ __device__ void select_exact(const DecArgs& a, unsigned char* un, int* s_ids, co
             slo[tid] = Lr[ex] - Br[ex];
         }
         float rinv_t;
-        if (PIPE && a.xscale) {  // the prologue's (the same certified mean and expression)
+        if (PIPE && a.xscale) {  // the router's (the same certified mean and expression)
             rinv_t = a.xscale[tt];
         } else {
             double s = 0.0;

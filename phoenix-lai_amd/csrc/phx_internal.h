@@ -205,7 +205,7 @@ struct DecLayerH {
     int ncu;  // compute units: the gate|up launch has at most one unit workgroup per CU
     float eps;
     const float *x, *W, *gis, *ds, *pre2, *post1, *post2, *fnorm, *post_ffw, *shared_in;
-    const float* xscale = nullptr;  // [T] the prologue's rms scales, where it ran (the exact selection reuses them)
+    const float* xscale = nullptr;  // [T] rms scales formed earlier in the call (the exact selection reuses them)
     const QMat *gu, *dn, *sgu, *sdn;  // sgu / sdn null: no shared FFN computed in the call
     double *Lb, *Bb;
     uint32_t* kb;  // [T][E][4] selection keys of the certified router (see k_dec_route)
