@@ -763,6 +763,150 @@ __global__ __launch_bounds__(64 * RT_MAXW) void k_dec_route_fused(CombArgs prev,
     route_at<4, true>(a, prev, rsm);
 }
 
+// Many (token, expert) pairs (T * E > 1024, E a multiple of RT_RX): one workgroup of d / PER threads per
+// token t and RT_RX consecutive experts.  The token's x row and the router scale are staged and the
+// RmsNorm scale formed once for its RT_RX experts, and each expert's sum, scan and bound (route_wg's) run
+// side by side; wave r finalizes expert e0 + r.  The input blocks b = g + G j (G = E / RT_RX workgroups
+// per token, g this one's index) are quantized here, as route_wg quantizes b = e + E j.  (Two experts
+// per workgroup measured no faster at C5: 15.6 against 15.4 us.)
+constexpr int RT_RX = 4;
+template <int PER>
+__global__ __launch_bounds__(256) void k_dec_route_mx(DecArgs a)
+{
+    extern __shared__ __align__(16) float rsm[];  // x, router scale, RT_RX W rows: route_row_floats(d, NT) each
+    __shared__ double red[RT_MAXW + 1], wsum[RT_RX][RT_MAXW];
+    __shared__ float wA[RT_RX][RT_MAXW], wP[RT_RX][RT_MAXW];
+    const int tid = threadIdx.x, NT = blockDim.x, lane = tid & 63, wave = tid >> 6, nw = NT >> 6, d = a.d;
+    const int G = a.E / RT_RX, t = blockIdx.x / G, eg = blockIdx.x % G, e0 = eg * RT_RX;
+    const int dp = route_row_floats(d, NT);
+    float* sx = rsm;
+    float* sg = sx + dp;
+    float* sw = sg + dp;  // RT_RX rows of dp floats
+    if (a.cbad && blockIdx.x == 0 && tid == 0) a.cbad[0] = 0;  // k_cert_select's list count
+    const int nb = d / 32, g = (NT - 1 - tid) >> 3, l8 = tid & 7, b = eg + g * G, bc = min(b, nb - 1);
+    const float4 nv = ((const float4*)a.pre2)[8 * bc + l8];
+    const float4 fv = a.ash.q ? ((const float4*)a.fnorm)[8 * bc + l8] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    auto stage = [&](const float* src, float* dst) {
+        const int n4 = d / 4;
+        for (int q = 0; q * NT < n4; q++) {
+            const int i = min(q * NT + tid, n4 - 1);
+            __builtin_amdgcn_global_load_lds((glb_void_t)((const float4*)src + i),
+                                             (lds_void_t)((float4*)dst + q * NT + wave * 64), 16, 0, 0);
+        }
+    };
+    stage(a.x + (int64_t)t * d, sx);
+    stage(a.gis, sg);
+#pragma unroll
+    for (int r = 0; r < RT_RX; r++) stage(a.W + (int64_t)(e0 + r) * d, sw + r * dp);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    const int c0 = tid * PER;
+    float xv[PER];
+    double s2 = 0.0;
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        xv[j] = sx[c0 + j];
+        s2 += (double)xv[j] * (double)xv[j];
+    }
+    // the RmsNorm scale as route_wg forms it
+    s2 = wave_sum_dpp(s2);
+    if (lane == 0) red[wave] = s2;
+    __syncthreads();
+    const double S = wave_sum_dpp(lane < nw ? red[lane] : 0.0);
+    float mean, mhi;
+    mean_ends(S, ((double)d + 64.0) * 0x1p-52 * S, 1.0 / (double)d, &mean, &mhi);
+    if (mean != mhi) {  // uniform
+        if (tid == 0) {
+            double q = 0.0;
+            for (int i = 0; i < d; i++) q += (double)sx[i] * (double)sx[i];
+            red[RT_MAXW] = q;
+            if (eg == 0) atomicAdd(&a.flags[0], 1);
+        }
+        __syncthreads();
+        mean = (float)(red[RT_MAXW] / (double)d);
+    }
+    const float rinv = rms_scale_from_mean(mean, a.eps);
+    const float sc = 1.0f / (float)__dsqrt_rn((double)d);
+    // m_i = ((x_i * rinv) * sc) * s_i, p_i = fl(W[e][i] * m_i) (route_wg's expression)
+    float m[PER];
+#pragma unroll
+    for (int j = 0; j < PER; j++) m[j] = xv[j] * rinv * sc * sg[c0 + j];
+    double loc[RT_RX], inc[RT_RX];
+    float Pf[RT_RX];
+#pragma unroll
+    for (int r = 0; r < RT_RX; r++) {
+        loc[r] = 0.0;
+        Pf[r] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < PER; j++) {
+            const float p = sw[r * dp + c0 + j] * m[j];
+            loc[r] += (double)p;
+            Pf[r] += fabsf(p);
+        }
+        inc[r] = wave_incl_scan_dpp(loc[r]);
+        if (lane == 63) wsum[r][wave] = inc[r];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < RT_RX; r++) {
+        // exclusive prefix: the earlier waves' totals, then this wave's
+        double acc = wave_sum_dpp(lane < wave ? wsum[r][lane] : 0.0) + (inc[r] - loc[r]);
+        float Af = 0.0f;
+#pragma unroll
+        for (int j = 0; j < PER; j++) {
+            acc += (double)(sw[r * dp + c0 + j] * m[j]);
+            Af += fabsf((float)acc);
+        }
+        Af = wave_sum_f(Af);
+        const float P = wave_sum_f(Pf[r]);
+        if (lane == 0) {
+            wA[r][wave] = Af;
+            wP[r][wave] = P;
+        }
+    }
+    __syncthreads();
+    for (int r = wave; r < RT_RX; r += nw) {  // wave r: expert e0 + r's sum, bound and selection key (route_wg's)
+        const int e = e0 + r;
+        const double L = wave_sum_dpp(lane < nw ? wsum[r][lane] : 0.0);
+        const float Aw = wave_sum_f(lane < nw ? wA[r][lane] : 0.0f);
+        const float Pw = wave_sum_f(lane < nw ? wP[r][lane] : 0.0f);
+        if (lane == 0) {
+            const double As = (double)Aw * (1.0 + 0x1p-10);
+            const double Ps = (double)Pw * (1.0 + 0x1p-10);
+            const double B = 0x1p-24 * As * 1.001 + 0x1p-45 * Ps;
+            a.Lb[(int64_t)t * a.E + e] = L;
+            a.Bb[(int64_t)t * a.E + e] = B;
+            a.kb[(int64_t)t * a.E + e] = sel_key(L, B, e);
+        }
+    }
+    if (b < nb) {  // 8-lane groups: whole groups take a block or none
+        const float4 xq = *(const float4*)(sx + 32 * b + 4 * l8);
+        float dval;
+        int sum;
+        const int qw = q8_0_oct(make_float4((xq.x * rinv) * nv.x, (xq.y * rinv) * nv.y, (xq.z * rinv) * nv.z,
+                                            (xq.w * rinv) * nv.w),
+                                &dval, &sum);
+        ((int*)(a.agu.q + (int64_t)t * a.agu.qstride))[8 * b + l8] = qw;
+        if (a.agu.qh) store_qh(a.agu, t, b, l8, qw, dval);
+        if (l8 == 0) {
+            a.agu.d[(int64_t)t * a.agu.dstride + b] = dval;
+            a.agu.s[(int64_t)t * a.agu.sstride + b] = sum;
+        }
+        if (a.ash.q) {
+            const int qs = q8_0_oct(make_float4((xq.x * rinv) * fv.x, (xq.y * rinv) * fv.y, (xq.z * rinv) * fv.z,
+                                                (xq.w * rinv) * fv.w),
+                                    &dval, &sum);
+            ((int*)(a.ash.q + (int64_t)t * a.ash.qstride))[8 * b + l8] = qs;
+            if (a.ash.qh) store_qh(a.ash, t, b, l8, qs, dval);
+            if (l8 == 0) {
+                a.ash.d[(int64_t)t * a.ash.dstride + b] = dval;
+                a.ash.s[(int64_t)t * a.ash.sstride + b] = sum;
+            }
+        }
+    }
+}
+template <int P> struct KRouteMx { static constexpr auto fn = k_dec_route_mx<P>; };
+
 // Elements per thread: 4 (d / 4 threads) for a stack's few tokens, where the router's chain of
 // reductions is the layer's latency; d / 256 (256 threads) for many tokens, where more workgroups per CU
 // hide each other's barriers.  Each width is its own instantiation (its own register budget).
@@ -2071,9 +2215,39 @@ template <int T> struct KGu { static constexpr auto fn = k_dec_gu<T, 768>; };
 template <int T> struct KGuW { static constexpr auto fn = k_dec_gu<T, 1024>; };
 template <int T> struct KDown { static constexpr auto fn = k_dec_down<T>; };
 
+static auto route_mx_kernel(int per)
+{
+    switch (per) {
+    case 1: return KRouteMx<1>::fn;
+    case 2: return KRouteMx<2>::fn;
+    case 3: return KRouteMx<3>::fn;
+    case 4: return KRouteMx<4>::fn;
+    case 5: return KRouteMx<5>::fn;
+    case 6: return KRouteMx<6>::fn;
+    case 7: return KRouteMx<7>::fn;
+    case 8: return KRouteMx<8>::fn;
+    case 9: return KRouteMx<9>::fn;
+    case 10: return KRouteMx<10>::fn;
+    case 11: return KRouteMx<11>::fn;
+    case 12: return KRouteMx<12>::fn;
+    case 13: return KRouteMx<13>::fn;
+    case 14: return KRouteMx<14>::fn;
+    case 15: return KRouteMx<15>::fn;
+    default: return KRouteMx<16>::fn;
+    }
+}
+
 void launch_dec_route(hipStream_t st, const DecLayerH& h)
 {
     const int per = route_per(h.T, h.E, h.d), nt = h.d / per;
+    // a workgroup per token and RT_RX experts, where its 8-lane groups cover the token's input blocks
+    if ((int64_t)h.T * h.E > 1024 && h.E % RT_RX == 0 && h.d / 32 <= nt / 8 * (h.E / RT_RX)) {
+        const size_t lds = (size_t)(2 + RT_RX) * route_row_floats(h.d, nt) * 4;
+        const auto kr = route_mx_kernel(per);
+        raise_lds(kr, lds);
+        launch(kr, dim3(h.T * (h.E / RT_RX)), dim3(nt), (uint32_t)lds, st, dec_args(h));
+        return;
+    }
     const size_t lds = (size_t)3 * route_row_floats(h.d, nt) * 4;
     const auto kr = route_kernel(per);
     raise_lds(kr, lds);
