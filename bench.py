@@ -402,9 +402,9 @@ def run_prefill(args, pkg, cfg_name="c3_prefill", steps=None):
     prof = kernel_times(ctx, calls)
     ids = ctx.routing()[0]
     cnt = np.bincount(ids.ravel(), minlength=L["n_expert"])
-    fast = None
+    fast, fast_sample = None, None
     if L["gate_up_type"] in (pkg.PHX.Q4_0, pkg.PHX.Q8_0, pkg.PHX.Q4_K, pkg.PHX.Q6_K) and not args.no_fast_math:
-        fast = fast_math_object(args, pkg, ctx, L, xbuf, obuf, xs, steps)
+        fast, fast_sample = fast_math_object(args, pkg, ctx, L, xbuf, obuf, xs, steps)
     ctx.close()
     gu_b, dn_b = expert_bytes(L)
     touched = int((cnt > 0).sum())
@@ -436,13 +436,15 @@ def run_prefill(args, pkg, cfg_name="c3_prefill", steps=None):
     if not args.no_cpu:
         log(f"[bench] {cfg_name} CPU baseline ...")
         out["cpu_baseline"] = cpu_baseline(pkg, L, cfg_name, min(args.cpu_seconds, 6.0 if cfg_name == "c3_prefill" else 3.0))
+        if fast:
+            fast["error_vs_cpu_reference"] = fast_math_error(L, fast_sample)
     return out
 
 
 def fast_math_object(args, pkg, ctx, L, xbuf, obuf, xs, steps):
     """The same layer in the tolerance mode (PHX_FLAG_FAST_MATH: block scales folded into fp16 operands,
-    rows accumulated on the matrix cores), timed the same way, with its measured distance from the CPU
-    reference on a sample of tokens (the mode is not bit-exact; routing still is)."""
+    rows accumulated on the matrix cores), timed the same way; returns the object and a token sample of
+    its outputs (inputs, outputs), which the CPU leg compares with the CPU reference."""
     T, d = xs.shape[1], L["d"]
     xstride = T * d * 4
     FM = pkg.PHX.FLAG_FAST_MATH | pkg.PHX.FLAG_ASYNC
@@ -463,23 +465,26 @@ def fast_math_object(args, pkg, ctx, L, xbuf, obuf, xs, steps):
     out = {"tokens_s": round(T * steps / dt, 1), "ms_per_step": round(dt * 1e3 / steps, 4),
            **mfma_rates(L, T, prof["gate_up"][0], prof["down"][0]),
            "kernels": {k_: {"avg_us": round(v[0] * 1e3, 2), "launches": v[1]} for k_, v in prof.items()}}
-    if not args.no_cpu:
-        from oracle import oracle as orc
-        # one more call on the first input (the calls leave their inputs unchanged), a token sample compared
-        x = xs[0]
-        ctx.ffn_device(0, T, xbuf.ptr, None, obuf.ptr, FM)
-        ctx.sync()
-        got = obuf.download((T, d))
-        toks = np.arange(0, T, max(1, T // 32))
-        threads, _ = host_cpu()
-        ref, _, _ = orc.moe_block(L, x[toks], nthreads=threads)
-        err = np.abs(got[toks].astype(np.float64) - ref)
-        rms = float(np.sqrt(np.mean(ref.astype(np.float64) ** 2)))
-        out["error_vs_cpu_reference"] = {
-            "tokens": int(len(toks)), "max_abs": round(float(err.max()), 6),
+    # one more call on the first input (the calls leave their inputs unchanged): a token sample of its
+    # outputs, compared with the CPU reference in the CPU leg (fast_math_error)
+    ctx.ffn_device(0, T, xbuf.ptr, None, obuf.ptr, FM)
+    ctx.sync()
+    toks = np.arange(0, T, max(1, T // 32))
+    return out, (xs[0][toks], obuf.download((T, d))[toks])
+
+
+def fast_math_error(L, sample):
+    """The CPU leg's check of the tolerance mode: the oracle's outputs for the sampled tokens against the
+    GPU's (the mode is not bit-exact; routing still is)."""
+    from oracle import oracle as orc
+    x, got = sample
+    threads, _ = host_cpu()
+    ref, _, _ = orc.moe_block(L, x, nthreads=threads)
+    err = np.abs(got.astype(np.float64) - ref)
+    rms = float(np.sqrt(np.mean(ref.astype(np.float64) ** 2)))
+    return {"tokens": int(len(x)), "max_abs": round(float(err.max()), 6),
             "rms": round(float(np.sqrt(np.mean(err ** 2))), 6), "output_rms": round(rms, 4),
             "within_2e-3_bar_frac": round(float((err <= np.maximum(2e-3 * np.abs(ref), 1e-4)).mean()), 4)}
-    return out
 
 
 def run_stack(args, pkg, cfg_name="c5_stack"):
