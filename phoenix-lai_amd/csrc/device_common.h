@@ -563,26 +563,6 @@ __device__ float mean_sq_cert_from(double s, int per, const float* x, int n, dou
     return mean;
 }
 
-// The same for one wave over contiguous per-lane chunks (no barriers).
-__device__ __forceinline__ float mean_sq_cert_wave(const float* x, int n, int* fallbacks)
-{
-    const int lane = threadIdx.x & 63;
-    const int per = (n + 63) / 64, c0 = min(n, lane * per), c1 = min(n, c0 + per);
-    double s = 0.0;
-    for (int i = c0; i < c1; i++) {
-        double v = (double)x[i];
-        s += v * v;
-    }
-    const double S = wave_sum_dpp(s);
-    const double B = ((double)n + per + 64.0) * 0x1p-53 * S * 2.0;
-    float lo, hi;
-    mean_ends(S, B, 1.0 / (double)n, &lo, &hi);
-    if (lo == hi) return lo;
-    const double q = seq_sum_sq_wave(x, n);
-    if (lane == 0 && fallbacks) atomicAdd(fallbacks, 1);
-    return (float)(q / (double)n);
-}
-
 // ------------------------------------------------------------------------------ explicit LDS reads
 // Kernels that fill LDS with direct global -> LDS loads read it back with these: the compiler would
 // otherwise wait for every outstanding direct load before any LDS read it emits.
