@@ -19,8 +19,11 @@ def say(*a):
 
 
 # (E, k, d, T): E = 2 at d = 4096 has 128 input blocks against 32 E = 64 covered by the 256-thread router
-# workgroups, so it must take the exact router; E = 4 covers exactly 128 and stays certified
-@pytest.mark.parametrize("E,k,d,T", [(2, 1, 4096, 600), (4, 2, 4096, 300), (2, 2, 2048, 1100)])
+# workgroups, so it must take the exact router; E = 4 covers exactly 128 and stays certified (a workgroup
+# per (token, expert): the four-expert workgroups would cover 32 E / 4); E = 8 likewise; E = 16 covers
+# exactly 128 with four experts per workgroup
+@pytest.mark.parametrize("E,k,d,T", [(2, 1, 4096, 600), (4, 2, 4096, 300), (2, 2, 2048, 1100), (8, 2, 4096, 300),
+                                     (16, 2, 4096, 300)])
 def test_general_router_covers_every_input_block(ctx, pkg, orc, E, k, d, T):
     say(f"general path, E={E} k={k} d={d} T={T}: vs oracle")
     cfg = dict(idx=31, T=T, d=d, E=E, k=k, nf=128, gu=2, dn=2)
