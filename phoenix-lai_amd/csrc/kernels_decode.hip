@@ -1553,7 +1553,7 @@ __global__ __launch_bounds__(CF_NT) void k_cert_fallback(DecArgs a)
     }
 }
 
-// Few tokens (at most one workgroup per compute unit): one workgroup of CF_NT threads per token, the
+// Few tokens (at most two workgroups per compute unit): one workgroup of CF_NT threads per token, the
 // fast path in wave 0 and, for a token the bounds leave open, the exact selection in the same launch.
 __global__ __launch_bounds__(CF_NT) void k_cert_select_one(DecArgs a)
 {
@@ -2257,7 +2257,7 @@ void launch_dec_route(hipStream_t st, const DecLayerH& h)
 void launch_cert_select(hipStream_t st, const DecLayerH& h)
 {
     const DecArgs a = dec_args(h);
-    if (h.T <= std::max(h.ncu, 1)) {  // a workgroup per token fits the chip: one launch
+    if (h.T <= 2 * std::max(h.ncu, 1)) {  // a workgroup per token in at most two rounds: one launch
         const size_t lds1 = sel_lds(1, h.E, h.d, CF_NT, CF_P).total;
         raise_lds(k_cert_select_one, lds1);
         launch(k_cert_select_one, dim3(h.T), dim3(CF_NT), (uint32_t)lds1, st, a);
