@@ -1034,20 +1034,48 @@ __global__ __launch_bounds__(256) void k_grouped_q_ring(GroupArgs g)
         // loads, so the ring restarts with nothing outstanding)
         const int nbc = min(QG_CHB, nb - c0);
         __syncthreads();  // the previous chunk's reads are done
-        for (int x = tid; x < A * nbc * 2; x += 256) {
-            const int i = x / (nbc * 2), y = x - i * nbc * 2;
-            ((uint4*)(sq + i * CH * 8))[y] =
-                ((const uint4*)(g.act.q + (int64_t)arow[i] * g.act.qstride + (int64_t)c0 * 32))[y];
+        // the first chunk's first ring blocks go out before its activation loads (nothing is outstanding
+        // yet), so the two cold reads overlap
+        if (c0 == 0) {
+#pragma unroll
+            for (int r = 0; r < QG_R - 1; r++) issue(r, r);
         }
-        for (int x = tid; x < A * nbc; x += 256) {
-            const int i = x / nbc, y = x - i * nbc;
-            sd[i * CH + y] = g.act.d[(int64_t)arow[i] * g.act.dstride + c0 + y];
-            if (Q4) ss[i * CH + y] = g.act.s[(int64_t)arow[i] * g.act.sstride + c0 + y];
+        // the tile's rows of the chunk (rows past cnt are never read): every load, then the stores
+        constexpr int NQ = (A * QG_CHB * 2 + 255) / 256, ND = (A * QG_CHB + 255) / 256;
+        uint4 qv[NQ];
+        float dv[ND];
+        int sv[ND];
+#pragma unroll
+        for (int u = 0; u < NQ; u++) {
+            const int x = tid + 256 * u, i = x / (nbc * 2), y = x - i * nbc * 2;
+            qv[u] = i < cnt ? ((const uint4*)(g.act.q + (int64_t)arow[i] * g.act.qstride + (int64_t)c0 * 32))[y]
+                            : make_uint4(0u, 0u, 0u, 0u);
+        }
+#pragma unroll
+        for (int u = 0; u < ND; u++) {
+            const int x = tid + 256 * u, i = x / nbc, y = x - i * nbc;
+            dv[u] = i < cnt ? g.act.d[(int64_t)arow[i] * g.act.dstride + c0 + y] : 0.0f;
+            sv[u] = Q4 && i < cnt ? g.act.s[(int64_t)arow[i] * g.act.sstride + c0 + y] : 0;
+        }
+#pragma unroll
+        for (int u = 0; u < NQ; u++) {
+            const int x = tid + 256 * u, i = x / (nbc * 2), y = x - i * nbc * 2;
+            if (i < cnt) ((uint4*)(sq + i * CH * 8))[y] = qv[u];
+        }
+#pragma unroll
+        for (int u = 0; u < ND; u++) {
+            const int x = tid + 256 * u, i = x / nbc, y = x - i * nbc;
+            if (i < cnt) {
+                sd[i * CH + y] = dv[u];
+                if (Q4) ss[i * CH + y] = sv[u];
+            }
         }
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
+        if (c0 != 0) {
 #pragma unroll
-        for (int r = 0; r < QG_R - 1; r++) issue(r, c0 + r);
+            for (int r = 0; r < QG_R - 1; r++) issue(r, c0 + r);
+        }
         for (int bl = 0; bl < nbc; bl++) {
             const int b = c0 + bl, slot = bl % QG_R;
             // block b has landed once at most the QG_R - 2 later blocks' loads are outstanding; then the
