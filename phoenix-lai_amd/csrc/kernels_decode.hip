@@ -1271,6 +1271,9 @@ __device__ void select_exact(const DecArgs& a, unsigned char* un, int* s_ids, co
     float* sbuf = (float*)(un + lds.buf);
     const float sc = 1.0f / (float)__dsqrt_rn((double)a.d);
     const int E = a.E, k = a.k, nwe = (E + 63) / 64;
+    // elements per thread per load round of the token's row (the decode kernel's variant keeps one: its
+    // registers are the roofline kernel's)
+    constexpr int RB = PIPE ? 8 : 1;
     for (int tt = 0; tt < a.T; tt++) {
         if (!s_bad[tt]) continue;  // uniform: an LDS value read after a barrier
         if (count && tid == 0) atomicAdd(&a.flags[1], 1);
@@ -1292,10 +1295,28 @@ __device__ void select_exact(const DecArgs& a, unsigned char* un, int* s_ids, co
             rinv_t = a.xscale[tt];
         } else {
             double s = 0.0;
-            for (int i = tid; i < a.d; i += NT) s += (double)xr[i] * (double)xr[i];
+            for (int i0 = tid; i0 < a.d; i0 += RB * NT) {  // RB loads per round, then the terms in order
+                float xv[RB];
+#pragma unroll
+                for (int u = 0; u < RB; u++) xv[u] = xr[min(i0 + u * NT, a.d - 1)];
+#pragma unroll
+                for (int u = 0; u < RB; u++)
+                    if (i0 + u * NT < a.d) s += (double)xv[u] * (double)xv[u];
+            }
             rinv_t = rms_scale_from_mean(wg_mean_sq<true, PIPE>(s, xr, a.d, red, nullptr), a.eps);
         }
-        for (int i = tid; i < a.d; i += NT) sm[i] = ((xr[i] * rinv_t) * sc) * a.gis[i];
+        for (int i0 = tid; i0 < a.d; i0 += RB * NT) {  // RB elements per round: every load, then the stores
+            float xv[RB], gv[RB];
+#pragma unroll
+            for (int u = 0; u < RB; u++) {
+                const int i = min(i0 + u * NT, a.d - 1);
+                xv[u] = xr[i];
+                gv[u] = a.gis[i];
+            }
+#pragma unroll
+            for (int u = 0; u < RB; u++)
+                if (i0 + u * NT < a.d) sm[i0 + u * NT] = ((xv[u] * rinv_t) * sc) * gv[u];
+        }
         const bool nonfinite = __syncthreads_or(tid < E && !(isfinite(lb) && isfinite(bb)));  // publishes sm, slo
         // the lowest lower end among the fast path's chosen experts: an expert whose upper end does not
         // reach it ranks below every chosen one in exact arithmetic too
