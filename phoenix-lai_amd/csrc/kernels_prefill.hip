@@ -362,11 +362,16 @@ __device__ __forceinline__ void mma_tile(const MmaArgs& g, const Tile& tl, int c
     // results: lane holds rows i_q = 8 (q / 4) + 4 h + (q % 4) of the wave's 32, token column r32 (a
     // paired launch without g and u outputs ends with its requant)
     if (!live || (g.paired && !g.out0)) return;
+    // the lane's assignment indices, every load before the first store (a store's wait would otherwise
+    // hold the next index's load back)
+    int pa[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) pa[j] = g.perm[tl.start + min(32 * j + r32, cnt - 1)];
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
         const int sidx = 32 * j + r32;
         if (sidx >= cnt) continue;
-        const int64_t a = g.perm[tl.start + sidx];
+        const int64_t a = pa[j];
         // four consecutive rows (columns of the output row a) per q4: one 16-byte store where the four
         // lie inside the output and the row stride keeps them aligned, else element by element
         const bool vec = (g.out_stride & 3) == 0;
@@ -717,6 +722,11 @@ __device__ __forceinline__ void coop_tile(const MmaArgs& g, const Tile& tl, int 
         float* tb = (float*)ring + wave * (32 * 68);  // [32 tokens][64 rows + 4 pad]
         const int c16 = lane & 15, row0 = gI * 64 + 4 * c16;
         const bool full = vec && row0 + 3 < min(g.rows, g.split);
+        // the tile's assignment indices (32 NJ <= 128): lane l loads positions l and 64 + l before any
+        // store, a store round takes its own by a lane shuffle (a load per round would wait behind the
+        // previous round's stores)
+        static_assert(NJ <= 4, "two indices per lane cover the tile");
+        const int pa0 = g.perm[tl.start + min(lane, cnt - 1)], pa1 = g.perm[tl.start + min(64 + lane, cnt - 1)];
 #pragma unroll
         for (int j = 0; j < NJ; j++) {
 #pragma unroll
@@ -732,8 +742,9 @@ __device__ __forceinline__ void coop_tile(const MmaArgs& g, const Tile& tl, int 
             for (int rd = 0; rd < 8; rd++) {
                 const int tok = 4 * rd + (lane >> 4), sidx = 32 * j + tok;
                 const float4 v = *(const float4*)(tb + tok * 68 + 4 * c16);
+                const int av = __shfl(j < 2 ? pa0 : pa1, 32 * (j & 1) + tok, 64);
                 if (sidx < cnt) {
-                    const int64_t a = g.perm[tl.start + sidx];
+                    const int64_t a = av;
                     if (full) *(float4*)(g.out0 + a * g.out_stride + row0) = v;
                     else {
                         const float vv[4] = {v.x, v.y, v.z, v.w};
@@ -755,11 +766,14 @@ __device__ __forceinline__ void coop_tile(const MmaArgs& g, const Tile& tl, int 
         }
         return;
     }
+    int pa[NJ];  // every index load before the first store
+#pragma unroll
+    for (int j = 0; j < NJ; j++) pa[j] = g.perm[tl.start + min(32 * j + r32, cnt - 1)];
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
         const int sidx = 32 * j + r32;
         if (sidx >= cnt) continue;
-        const int64_t a = g.perm[tl.start + sidx];
+        const int64_t a = pa[j];
 #pragma unroll
         for (int half = 0; half < 2; half++)
 #pragma unroll
@@ -1254,7 +1268,11 @@ __device__ __forceinline__ void kmma_tile(const MmaArgs& g, const Tile& tl, int 
     // the loads issued past the last super-block land in this workgroup's LDS: let them finish
     __builtin_amdgcn_s_waitcnt(0);
     if (!live) return;
-    // lane (r16, q): assignment 16 c + r16, rows 4 q .. 4 q + 3 of the wave's 16
+    // lane (r16, q): assignment 16 c + r16, rows 4 q .. 4 q + 3 of the wave's 16; every index load
+    // before the first store
+    int pa[NJ];
+#pragma unroll
+    for (int c = 0; c < NJ; c++) pa[c] = g.perm[tl.start + min(16 * c + r16, cnt - 1)];
 #pragma unroll
     for (int c = 0; c < NJ; c++) {
         const int t = 16 * c + r16;
@@ -1267,7 +1285,7 @@ __device__ __forceinline__ void kmma_tile(const MmaArgs& g, const Tile& tl, int 
             for (int l = 0; l < 8; l++) s += sums[l][c][v];
             o[v] = FOLD ? acc[c][v] : s;
         }
-        const int64_t a = g.perm[tl.start + t];
+        const int64_t a = pa[c];
         const int lg0 = 16 * ws + 4 * q;  // lane within the row group of the first of four
         const bool vec = (g.out_stride & 3) == 0;
         if (g.paired) {
