@@ -718,31 +718,42 @@ __global__ __launch_bounds__(DSP_NT) void k_dispatch(int n, int E, int A, const 
     const int c0 = blockIdx.x * DSP_CH, c1 = min(n, c0 + DSP_CH);  // this workgroup's chunk (c0 % 64 == 0)
     int nbits = 0;
     while ((1 << nbits) < E) nbits++;
+    // the ids in batches of 16 loads per thread (the first batch goes out before the counters are cleared)
+    int v[16];
+    auto load = [&](int i0) {
+#pragma unroll
+        for (int u = 0; u < 16; u++) v[u] = ids[min(i0 + DSP_NT * u, n - 1)];
+    };
+    load(tid);
     for (int i = tid; i < DSP_SEG * PHX_MAX_EXPERTS_DEV; i += DSP_NT) (&cnt[0][0])[i] = 0;
     for (int i = tid; i < PHX_MAX_EXPERTS_DEV; i += DSP_NT) {
         pre[i] = 0;
         tot[i] = 0;
     }
-    // the ids in batches of 16 loads per thread
+    const bool multi = gridDim.x > 1;  // uniform
+    const int nwe = (E + 63) >> 6;     // the waves whose threads hold experts (one per thread below)
+    __syncthreads();
+    // with several chunks, counts over the list as the ids arrive: every lane adds its assignment into its
+    // wave's own row by an LDS atomic (the list total in the low 16 bits, the count before the chunk in
+    // the high 16, n <= 65535), summed per expert below (one workgroup: its segments cover the list); then
+    // per segment of the chunk.  (A rank-free count needs no same-expert mask: its eight ballots per
+    // batch made this pass VALU-bound, 256 batches of ~100 instructions in every workgroup.)
     for (int i0 = tid; i0 < n; i0 += DSP_NT * 16) {
-        int v[16];
+        if (i0 != tid) load(i0);
 #pragma unroll
-        for (int u = 0; u < 16; u++) v[u] = ids[min(i0 + DSP_NT * u, n - 1)];
-#pragma unroll
-        for (int u = 0; u < 16; u++)
-            if (i0 + DSP_NT * u < n) sid[i0 + DSP_NT * u] = (uint8_t)clamp_id(v[u], E);
+        for (int u = 0; u < 16; u++) {
+            const int a = i0 + DSP_NT * u;
+            if (a < n) {
+                const int e = clamp_id(v[u], E);
+                sid[a] = (uint8_t)e;
+                if (multi) atomicAdd(&cnt[wave][e], a < c0 ? 0x10001 : 1);
+            }
+        }
     }
     const int seg = (c1 - c0 + DSP_SEG - 1) / DSP_SEG, s0 = min(c1, c0 + wave * seg), s1 = min(c1, s0 + seg);
     const uint64_t lower = (1ull << lane) - 1ull;
     __syncthreads();
-    // counts over the list: every lane adds its assignment into its wave's own row by an LDS atomic (the
-    // list total in the low 16 bits, the count before the chunk in the high 16, n <= 65535), summed per
-    // expert (one workgroup: its segments cover the list); then per segment of the chunk.  (A rank-free
-    // count needs no same-expert mask: its eight ballots per batch made this pass VALU-bound, 256
-    // batches of ~100 instructions in every workgroup.)
-    if (gridDim.x > 1) {  // uniform
-        for (int a = tid; a < n; a += DSP_NT) atomicAdd(&cnt[wave][sid[a]], a < c0 ? 0x10001 : 1);
-        __syncthreads();
+    if (multi) {
         if (tid < E) {
             unsigned sum = 0;
             for (int w = 0; w < DSP_SEG; w++) {
@@ -782,7 +793,7 @@ __global__ __launch_bounds__(DSP_NT) void k_dispatch(int n, int E, int A, const 
     }
     __syncthreads();
     int b1 = 0, b2 = 0;
-    for (int w = 0; w < wave; w++) {
+    for (int w = 0; w < min(wave, nwe); w++) {  // the later waves' sums are zero
         b1 += wsum[0][w];
         b2 += wsum[1][w];
     }
@@ -817,7 +828,7 @@ __global__ __launch_bounds__(DSP_NT) void k_dispatch(int n, int E, int A, const 
         for (int q = 0; q < 5; q++) {
             tot5[q] = 0;
             pre5[q] = 0;
-            for (int w = 0; w < DSP_SEG; w++) {
+            for (int w = 0; w < nwe; w++) {  // the later waves' sums are zero
                 tot5[q] += tsum[q][w];
                 if (w < wave) pre5[q] += tsum[q][w];
             }
