@@ -2278,7 +2278,7 @@ void launch_dec_route(hipStream_t st, const DecLayerH& h)
 void launch_cert_select(hipStream_t st, const DecLayerH& h)
 {
     const DecArgs a = dec_args(h);
-    if (h.T <= 2 * std::max(h.ncu, 1)) {  // a workgroup per token in at most two rounds: one launch
+    if (cert_select_one_launch(h)) {  // a workgroup per token in at most two rounds: one launch
         const size_t lds1 = sel_lds(1, h.E, h.d, CF_NT, CF_P).total;
         raise_lds(k_cert_select_one, lds1);
         launch(k_cert_select_one, dim3(h.T), dim3(CF_NT), (uint32_t)lds1, st, a);

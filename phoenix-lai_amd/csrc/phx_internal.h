@@ -221,6 +221,9 @@ bool dec_supported(const DecLayerH& h);
 void launch_dec_route(hipStream_t st, const DecLayerH& h);
 // the general path's selection from k_dec_route's certified sums: ids, weights and logits per token
 void launch_cert_select(hipStream_t st, const DecLayerH& h);
+// whether launch_cert_select runs as one launch (a workgroup per token in at most two rounds over the
+// compute units) rather than a wave per token and a fallback launch for the uncertified tokens
+inline bool cert_select_one_launch(const DecLayerH& h) { return h.T <= 2 * std::max(h.ncu, 1); }
 // the certified router for many tokens: matrix-core logits with bounds (Lb, Bb) and selection keys kb
 // [T][E][4] for launch_cert_select, from x and the router rows prescaled at upload (Ws[e][i] =
 // fl(s_i W[e][i]), s the router scale) with their squared norms over the kernel's kRouterRanges

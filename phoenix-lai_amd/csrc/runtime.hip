@@ -916,8 +916,12 @@ int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, con
         if (mma || kmma) pgu.q = nullptr, pgu.s = nullptr;
         if (smma) psh.q = nullptr, psh.s = nullptr;
         // the matrix-core router needs nothing from the prologue: the prologue runs on the side stream
-        // beside the router and the selection (launched after the router, whose workgroups need more LDS
-        // than a prologue-filled compute unit leaves), joined before the products read its rows
+        // (launched after the router, whose workgroups need more LDS than a prologue-filled compute unit
+        // leaves), joined before the products read its rows.  Beside a one-launch selection it starts
+        // once the router is done: the router alone is faster (C4 18.6 -> 16.1 us) and the prologue
+        // takes the compute units the selection's rounds leave (layer 0.493 -> 0.485 ms).  Beside the
+        // two-kernel selection it starts with the router: after it, it slowed the fallback's exact
+        // chains more than it sped the router (C3 router 31.4 -> 26.8 us, selection 24.8 -> 32.1 us).
         auto prologue = [&](hipStream_t sp) {
             ProfScope p(c, PHX_K_PROLOGUE);
             launch_prologue(sp, T, d, D.eps, x, L.gis, L.pre2, shared_ffn ? L.ffn_norm : nullptr,
@@ -931,12 +935,14 @@ int run_layer_general(phx_moe_ctx* c, const Layer& L, int T, const float* x, con
             // whose order the bounds leave open)
             DecLayerH h = dec_layer(c, L, T, x, shared, out, xres);
             h.xscale = wp<float>(c, W_RSCALE);
-            HIPCHK(c, hipEventRecord(c->ev_fork, st));
+            const bool late = cert_select_one_launch(h);
+            if (!late) HIPCHK(c, hipEventRecord(c->ev_fork, st));
             {
                 ProfScope p(c, PHX_K_ROUTER);
                 launch_router_mm(st, T, d, E, D.eps, x, L.wsc, L.wnr, wp<float>(c, W_RSCALE), h.Lb, h.Bb, h.kb, h.bad,
                                  c->flags);
             }
+            if (late) HIPCHK(c, hipEventRecord(c->ev_fork, st));
             HIPCHK(c, hipStreamWaitEvent(c->side, c->ev_fork, 0));
             prologue(c->side);
             HIPCHK(c, hipEventRecord(c->ev_join, c->side));
